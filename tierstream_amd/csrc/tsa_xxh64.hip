@@ -1,0 +1,219 @@
+// Device XXH64 (seed 0) for units already resident in HBM, two kernels:
+//
+//  * digest: one lane-quad per unit, lane q owns accumulator q and streams the unit's 32-byte stripes in order. XXH64
+//    keeps four dependent 64-bit chains per input, each chain a sequence of rotl(v + w*P2, 31)*P1 steps: there is no
+//    associative combine, so a unit's digest is chain-latency bound (one quad) and the kernel reaches HBM speed only
+//    with thousands of units in one launch.
+//  * verify: checkpoint-parallel. The host hashes every unit once while it fills the pinned tier / the arena and keeps
+//    the four accumulators at the start of every segment (a fixed byte count inside each extent). On the device each
+//    (unit, segment) pair is an independent quad: start from the segment's checkpoint, run the segment's stripes over
+//    the device bytes, and require the next checkpoint (or, for the unit's last segment, the finalized digest equal to
+//    the descriptor's hash). All segments of all units run in parallel, so one launch is HBM-bound even for one unit.
+//    If every segment agrees, the device bytes' XXH64 equals the descriptor hash exactly (the transitions compose).
+//
+// Byte order and the algorithm follow the published XXH64 description (reference src/xxh64.cpp:39-112 restates it).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tsa_device.hpp"
+
+namespace tsa {
+namespace dev {
+
+constexpr uint64_t P1 = 0x9E3779B185EBCA87ull;
+constexpr uint64_t P2 = 0xC2B2AE3D27D4EB4Full;
+constexpr uint64_t P3 = 0x165667B19E3779F9ull;
+constexpr uint64_t P4 = 0x85EBCA77C2B2AE63ull;
+constexpr uint64_t P5 = 0x27D4EB2F165667C5ull;
+
+__device__ __forceinline__ uint64_t rotl64(uint64_t x, int r) { return (x << r) | (x >> (64 - r)); }
+__device__ __forceinline__ uint64_t xround(uint64_t acc, uint64_t w) { return rotl64(acc + w * P2, 31) * P1; }
+__device__ __forceinline__ uint64_t xmerge(uint64_t h, uint64_t v) { return (h ^ xround(0, v)) * P1 + P4; }
+
+// Digest of the four accumulators, the total length and the (< 32 byte) tail. Runs on one lane.
+__device__ uint64_t xfinal(const uint64_t v[4], uint64_t total, const unsigned char* tail, uint32_t tail_len) {
+  uint64_t h;
+  if (total >= 32) {
+    h = rotl64(v[0], 1) + rotl64(v[1], 7) + rotl64(v[2], 12) + rotl64(v[3], 18);
+    for (int k = 0; k < 4; ++k) h = xmerge(h, v[k]);
+  } else {
+    h = P5;  // seed 0
+  }
+  h += total;
+  uint32_t i = 0;
+  for (; i + 8 <= tail_len; i += 8) {
+    uint64_t w = 0;
+    for (int b = 7; b >= 0; --b) w = (w << 8) | tail[i + b];
+    h ^= xround(0, w);
+    h = rotl64(h, 27) * P1 + P4;
+  }
+  if (i + 4 <= tail_len) {
+    const uint32_t w = uint32_t(tail[i]) | uint32_t(tail[i + 1]) << 8 | uint32_t(tail[i + 2]) << 16 |
+                       uint32_t(tail[i + 3]) << 24;
+    h ^= uint64_t(w) * P1;
+    h = rotl64(h, 23) * P2 + P3;
+    i += 4;
+  }
+  for (; i < tail_len; ++i) {
+    h ^= uint64_t(tail[i]) * P5;
+    h = rotl64(h, 11) * P1;
+  }
+  h ^= h >> 33;
+  h *= P2;
+  h ^= h >> 29;
+  h *= P3;
+  h ^= h >> 32;
+  return h;
+}
+
+// One chain (lane q of the quad) over n stripes starting at p (p is 8-byte aligned: extents start 256-byte aligned
+// in every caller, and every extent but the last is a multiple of 32 bytes). Loads run kAhead stripes ahead of the
+// rounds so each lane keeps kAhead independent 8-byte loads in flight.
+constexpr int kAhead = 8;
+__device__ __forceinline__ uint64_t chain(uint64_t v, const unsigned char* p, uint64_t n, uint32_t q) {
+  const uint64_t* w = reinterpret_cast<const uint64_t*>(p) + q;
+  uint64_t s = 0;
+  for (; s + kAhead <= n; s += kAhead) {
+    uint64_t buf[kAhead];
+#pragma unroll
+    for (int k = 0; k < kAhead; ++k) buf[k] = __builtin_nontemporal_load(w + 4 * (s + k));
+#pragma unroll
+    for (int k = 0; k < kAhead; ++k) v = xround(v, buf[k]);
+  }
+  for (; s < n; ++s) v = xround(v, __builtin_nontemporal_load(w + 4 * s));
+  return v;
+}
+
+__device__ __forceinline__ void init_acc(uint64_t v[4]) {
+  v[0] = P1 + P2;
+  v[1] = P2;
+  v[2] = 0;
+  v[3] = 0 - P1;
+}
+
+__global__ __launch_bounds__(256) void digest_kernel(const TsaUnit* __restrict__ units, uint32_t n,
+                                                     uint64_t* __restrict__ out) {
+  const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t u = gid >> 2, q = gid & 3u;
+  const bool live = u < n;
+  uint64_t acc[4];
+  init_acc(acc);
+  uint64_t v = acc[q];
+  uint64_t total = 0;
+  const unsigned char* tail = nullptr;
+  uint32_t tail_len = 0;
+  if (live) {
+    const TsaUnit un = units[u];
+    for (uint32_t e = 0; e < un.n_ext; ++e) {
+      const unsigned char* p = static_cast<const unsigned char*>(un.ext[e].ptr);
+      const uint64_t b = un.ext[e].bytes;
+      const uint64_t stripes = b / 32;
+      v = chain(v, p, stripes, q);
+      total += b;
+      if (e + 1 == un.n_ext) {
+        tail = p + stripes * 32;
+        tail_len = uint32_t(b - stripes * 32);
+      }
+    }
+  }
+  // the quad's accumulators to its lane 0 (all lanes of the wave take part in the shuffles)
+  uint64_t all[4];
+  const uint32_t base = threadIdx.x & ~3u;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) all[k] = __shfl(v, int(base + k), 64);
+  if (live && q == 0) out[u] = xfinal(all, total, tail, tail_len);
+}
+
+// One (unit, segment) per quad. seg_first is the prefix sum of segments over the launch's units (ascending).
+__global__ __launch_bounds__(256) void verify_kernel(const TsaVerifyUnit* __restrict__ units, uint32_t n_units,
+                                                     uint64_t n_segments, uint64_t seg_bytes,
+                                                     uint32_t* __restrict__ fail) {
+  const uint64_t gid = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const uint64_t s = gid >> 2;
+  const uint32_t q = uint32_t(gid & 3u);
+  const bool live = s < n_segments;
+  uint32_t ui = 0;
+  if (live) {  // the unit holding global segment s (units sorted by seg_first)
+    uint32_t lo = 0, hi = n_units;
+    while (hi - lo > 1) {
+      const uint32_t mid = (lo + hi) / 2;
+      if (units[mid].seg_first <= s) lo = mid;
+      else hi = mid;
+    }
+    ui = lo;
+  }
+  uint64_t v = 0;
+  bool last = false, check_state = false;
+  uint64_t local = 0, total = 0;
+  const unsigned char* tail = nullptr;
+  uint32_t tail_len = 0;
+  const TsaVerifyUnit* un = units + ui;
+  if (live) {
+    local = s - un->seg_first;  // the unit's segment index (its checkpoint index)
+    // the extent and the segment inside it
+    uint64_t k = local;
+    uint32_t e = 0;
+    uint64_t off = 0, stripes = 0;
+    for (; e < un->n_ext; ++e) {
+      const uint64_t b = un->ext[e].bytes;
+      const bool last_ext = e + 1 == un->n_ext;
+      const uint64_t span = last_ext ? b / 32 * 32 : b;
+      uint64_t nseg = (span + seg_bytes - 1) / seg_bytes;
+      if (last_ext && nseg == 0) nseg = 1;
+      if (k < nseg) {
+        off = k * seg_bytes;
+        const uint64_t end = off + seg_bytes < span ? off + seg_bytes : span;
+        stripes = (end - off) / 32;
+        last = last_ext && k + 1 == nseg;
+        if (last) {
+          tail = static_cast<const unsigned char*>(un->ext[e].ptr) + span;
+          tail_len = uint32_t(b - span);
+        }
+        break;
+      }
+      k -= nseg;
+    }
+    if (e == un->n_ext) {  // the launch's prefix sums disagree with the extents: reported, nothing read
+      if (q == 0) atomicOr(fail + ui, 2u);
+      return;  // (the whole quad: its lanes share s)
+    }
+    v = un->states[4 * local + q];
+    v = chain(v, static_cast<const unsigned char*>(un->ext[e].ptr) + off, stripes, q);
+    total = un->total;
+    check_state = !last;
+  }
+  uint64_t all[4];
+  const uint32_t base = threadIdx.x & ~3u;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) all[k] = __shfl(v, int(base + k), 64);
+  if (!live) return;
+  if (check_state) {
+    if (v != un->states[4 * (local + 1) + q]) atomicOr(fail + ui, 1u);
+  } else if (q == 0) {
+    if (xfinal(all, total, tail, tail_len) != un->digest) atomicOr(fail + ui, 1u);
+  }
+}
+
+}  // namespace dev
+
+int launch_digest(const TsaUnit* units_dev, uint32_t n, uint64_t* out_dev, hipStream_t stream) {
+  if (n == 0) return 0;
+  const uint32_t threads = 256;
+  const uint64_t lanes = uint64_t(n) * 4;
+  const uint32_t blocks = uint32_t((lanes + threads - 1) / threads);
+  hipLaunchKernelGGL(dev::digest_kernel, dim3(blocks), dim3(threads), 0, stream, units_dev, n, out_dev);
+  return int(hipGetLastError());
+}
+
+int launch_verify(const TsaVerifyUnit* units_dev, uint32_t n_units, uint64_t n_segments, uint64_t seg_bytes,
+                  uint32_t* fail_dev, hipStream_t stream) {
+  if (n_units == 0 || n_segments == 0) return 0;
+  const uint32_t threads = 256;
+  const uint64_t blocks = (n_segments * 4 + threads - 1) / threads;
+  if (blocks > 0x7fffffffull) return int(hipErrorInvalidValue);
+  hipLaunchKernelGGL(dev::verify_kernel, dim3(uint32_t(blocks)), dim3(threads), 0, stream, units_dev, n_units,
+                     n_segments, seg_bytes, fail_dev);
+  return int(hipGetLastError());
+}
+
+}  // namespace tsa
