@@ -43,6 +43,9 @@ typedef struct tsa_unit {
 /* XXH64 (seed 0) of each unit's bytes into digests_dev[i]. units_dev: n entries in device memory. */
 SS_API ss_status tsa_xxh64_digest(const tsa_unit* units_dev, uint32_t n, uint64_t* digests_dev, void* stream);
 
+/* Host XXH64 (seed 0) of host bytes: the same function the library checks descriptor hashes with. */
+SS_API uint64_t tsa_xxh64_host(const void* data, uint64_t bytes);
+
 /* Checkpoint layout of a unit: for each extent e, its segments are [k*seg, min((k+1)*seg, span_e)) with span_e =
  * bytes_e (the last extent: bytes rounded down to 32, and at least one segment); the checkpoint of a segment is the
  * four accumulators before its first stripe. tsa_checkpoint_count gives the count for extent byte sizes. */

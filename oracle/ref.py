@@ -1,0 +1,204 @@
+"""ORACLE (test infrastructure only): the reference's own CPU library (oracle/_ref/libtsref_harness.so, compiled from its
+sources by oracle/Makefile) driven through its C ABI, and its DgCore on an immediate transport. The library is loaded
+privately (RTLD_LOCAL) so its ss_* symbols never meet the product's."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from . import HERE
+
+HARNESS = HERE / "_ref" / "libtsref_harness.so"
+u32, u64, i32, vp = C.c_uint32, C.c_uint64, C.c_int32, C.c_void_p
+
+_lib = None
+
+
+def available() -> bool:
+    return HARNESS.exists()
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not HARNESS.exists():
+            raise RuntimeError(f"{HARNESS} is not built (make -C oracle ref, where the reference sources exist)")
+        from tierstream_amd.ss import SsBudget, SsLayerStats, SsLayerView, SsOptions
+        L = C.CDLL(str(HARNESS), mode=os.RTLD_NOW | os.RTLD_LOCAL)
+        st = C.c_int
+        sigs = {
+            "ss_last_error": (C.c_char_p, []),
+            "ss_desc_from_json": (st, [C.c_char_p, C.c_size_t, C.POINTER(vp)]),
+            "ss_desc_free": (None, [vp]),
+            "ss_desc_n_layers": (C.c_int, [vp]),
+            "ss_desc_layer_units": (C.c_int, [vp, C.c_int]),
+            "ss_desc_unit_bytes": (u64, [vp, C.c_int]),
+            "ss_budget_defaults_sized": (None, [C.POINTER(SsBudget), u32]),
+            "ss_options_defaults_sized": (None, [C.POINTER(SsOptions), u32]),
+            "ss_plan_make": (st, [vp, C.POINTER(SsBudget), C.POINTER(C.c_double), C.c_size_t, C.POINTER(vp)]),
+            "ss_plan_free": (None, [vp]),
+            "ss_plan_unit_tier": (C.c_int, [vp, C.c_int, C.c_int]),
+            "ss_plan_to_json": (st, [vp, C.POINTER(C.c_char_p), C.POINTER(C.c_size_t)]),
+            "ss_free": (None, [vp]),
+            "ss_open": (st, [vp, C.POINTER(SsBudget), vp, C.POINTER(SsOptions), C.POINTER(vp)]),
+            "ss_close": (None, [vp]),
+            "ss_begin": (st, [vp, vp, C.c_int]),
+            "ss_layer_routes": (st, [vp, C.c_int, C.POINTER(i32), C.c_int]),
+            "ss_layer_all": (st, [vp, C.c_int]),
+            "ss_acquire": (st, [vp, C.c_int, vp, C.POINTER(SsLayerView)]),
+            "ss_acquire_groups": (st, [vp, C.c_int, vp, C.POINTER(SsLayerView)]),
+            "ss_group_wait": (st, [vp, C.c_int, C.c_int, vp]),
+            "ss_release": (st, [vp, C.c_int, vp]),
+            "ss_end": (st, [vp]),
+            "ss_stats_total": (st, [vp, C.POINTER(SsLayerStats)]),
+            "ref_region_of": (C.c_int, [vp, u64, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(u64)]),
+            "refdg_open": (vp, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, u32, u32, u32, u32,
+                                C.POINTER(u64), u32, C.POINTER(u32), u32]),
+            "refdg_token": (C.c_int, [vp, C.POINTER(u32), u32, C.POINTER(u32), u32, C.POINTER(i32), C.POINTER(u64)]),
+            "refdg_counter_names": (C.c_char_p, []),
+            "refdg_residency": (u32, [vp, C.POINTER(u32), u32]),
+            "refdg_close": (None, [vp]),
+        }
+        for name, (res, args) in sigs.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _ck(st):
+    if st != 0:
+        raise RuntimeError(f"reference status {st}: {lib().ss_last_error().decode()}")
+
+
+def plan_json(desc_json: str, budget) -> dict:
+    import json
+    L = lib()
+    d, p = vp(), vp()
+    b = desc_json.encode()
+    _ck(L.ss_desc_from_json(b, len(b), C.byref(d)))
+    try:
+        _ck(L.ss_plan_make(d, C.byref(budget), None, 0, C.byref(p)))
+        s, n = C.c_char_p(), C.c_size_t()
+        _ck(L.ss_plan_to_json(p, C.byref(s), C.byref(n)))
+        out = json.loads(C.string_at(s, n.value).decode())
+        L.ss_free(s)
+        L.ss_plan_free(p)
+        return out
+    finally:
+        L.ss_desc_free(d)
+
+
+def host_run(desc_json: str, budget, options, routes: np.ndarray, mode: int = 0):
+    """The reference CPU backend over `routes` ([steps][layers][max_ids], -1 padded), the engine loop of the product's
+    tse_host_run. Per step: {"stats": ..., "tables": [[(kind, index, offset) per unit] per layer], "groups": [...],
+    "checksums": [[...]]}; checksums are of the bytes the reference's table entries point at (host memory)."""
+    from tierstream_amd.ss import SsLayerStats, SsLayerView
+    from .fixtures import engine_checksum
+    L = lib()
+    d, ctx = vp(), vp()
+    b = desc_json.encode()
+    _ck(L.ss_desc_from_json(b, len(b), C.byref(d)))
+    options.backend = 0  # SS_BACKEND_CPU
+    out = []
+    try:
+        _ck(L.ss_open(d, C.byref(budget), None, C.byref(options), C.byref(ctx)))
+        nl = L.ss_desc_n_layers(d)
+        steps, _, max_ids = routes.shape
+        for s in range(steps):
+            before = SsLayerStats()
+            _ck(L.ss_stats_total(ctx, C.byref(before)))
+            _ck(L.ss_begin(ctx, None, 0))
+            step = {"tables": [], "groups": [], "checksums": []}
+            for l in range(nl):
+                nu = L.ss_desc_layer_units(d, l)
+                if nu <= 0:
+                    step["tables"].append([])
+                    step["groups"].append([])
+                    step["checksums"].append([])
+                    continue
+                r = np.ascontiguousarray(routes[s, l], dtype=np.int32)
+                n = int(np.sum(r >= 0)) if mode != 1 else 0
+                if mode == 1:
+                    _ck(L.ss_layer_all(ctx, l))
+                else:
+                    _ck(L.ss_layer_routes(ctx, l, r.ctypes.data_as(C.POINTER(i32)), n))
+                v = SsLayerView()
+                _ck((L.ss_acquire_groups if mode == 2 else L.ss_acquire)(ctx, l, None, C.byref(v)))
+                if mode == 2:
+                    for gi in range(1, v.n_groups):
+                        _ck(L.ss_group_wait(ctx, l, gi, None))
+                tab = []
+                for u in range(nu):
+                    a = int(v.table_host[u])
+                    k, i, off = C.c_int(), C.c_int(), u64()
+                    L.ref_region_of(ctx, a, C.byref(k), C.byref(i), C.byref(off))
+                    tab.append((k.value, i.value, int(off.value)) if a else (0, -1, 0))
+                step["tables"].append(tab)
+                step["groups"].append([[v.groups[gi].units[j] for j in range(v.groups[gi].n_units)]
+                                       for gi in range(v.n_groups)])
+                ub = int(L.ss_desc_unit_bytes(d, l))
+                ids = list(range(nu)) if mode == 1 else [int(x) for x in r[:n]]
+                cks = []
+                for u in ids:
+                    a = int(v.table_host[u])
+                    cks.append(engine_checksum(np.frombuffer(C.string_at(a, ub), dtype=np.uint8)) if a else 0)
+                step["checksums"].append(cks)
+                _ck(L.ss_release(ctx, l, None))
+            _ck(L.ss_end(ctx))
+            after = SsLayerStats()
+            _ck(L.ss_stats_total(ctx, C.byref(after)))
+            step["stats"] = {k: after.as_dict()[k] - before.as_dict()[k] for k in after.as_dict()}
+            out.append(step)
+    finally:
+        if ctx:
+            L.ss_close(ctx)
+        L.ss_desc_free(d)
+    return out
+
+
+class RefDg:
+    """The reference DgCore on an immediate transport (its canonical schedule)."""
+
+    def __init__(self, n_units, persistent, bank, blocks, spare_target, part_bytes, order, prefetch_reserve=0xFFFFFFFF,
+                 pf_layer=4, pf_token=48, wb_defer=1, wb_on_d2h=1, inclusive=0):
+        L = lib()
+        nu = (u32 * len(n_units))(*n_units)
+        pb = (u64 * len(part_bytes))(*part_bytes)
+        od = (u32 * len(order))(*order)
+        self.h = L.refdg_open(nu, len(n_units), persistent, bank, blocks, spare_target, prefetch_reserve, pf_layer,
+                              pf_token, wb_defer, wb_on_d2h, inclusive, pb, len(part_bytes), od, len(order))
+        if not self.h:
+            raise RuntimeError("refdg_open failed")
+        self.keys = sum(n_units)
+        self.G = len(n_units)
+        self.names = L.refdg_counter_names().decode().split()
+
+    def token(self, ids: np.ndarray, pred: np.ndarray | None = None):
+        """ids uint32 [G][n]; returns (table int32 [keys], counters dict)."""
+        L = lib()
+        x = np.ascontiguousarray(ids, dtype=np.uint32)
+        n = x.shape[1]
+        p = np.ascontiguousarray(pred, dtype=np.uint32) if pred is not None else np.zeros((1, 1), np.uint32)
+        n_pred = p.shape[1] if pred is not None else 0
+        table = np.zeros(self.keys, dtype=np.int32)
+        counts = np.zeros(len(self.names), dtype=np.uint64)
+        st = L.refdg_token(self.h, x.ctypes.data_as(C.POINTER(u32)), n, p.ctypes.data_as(C.POINTER(u32)), n_pred,
+                           table.ctypes.data_as(C.POINTER(i32)), counts.ctypes.data_as(C.POINTER(u64)))
+        if st != 0:
+            raise RuntimeError("refdg_token failed")
+        return table, {k: int(v) for k, v in zip(self.names, counts)}
+
+    def residency(self):
+        L = lib()
+        out = np.zeros(self.keys, dtype=np.uint32)
+        n = L.refdg_residency(self.h, out.ctypes.data_as(C.POINTER(u32)), self.keys)
+        return [int(x) for x in out[:n]]
+
+    def close(self):
+        if self.h:
+            lib().refdg_close(self.h)
+            self.h = None

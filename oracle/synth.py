@@ -25,6 +25,7 @@ def mix64_scalar(z: int) -> int:
 
 
 def key(seed: int, sid: int) -> int:
+    seed, sid = int(seed), int(sid)
     return mix64_scalar((seed ^ ((sid * SID_ODD) & M64)) & M64)
 
 

@@ -1,0 +1,129 @@
+"""Device-gated decode on the MI355X against the reference DgCore (bit-exact placement): the same plan and token route
+stream through the product (HIP kernels in a captured hipGraph, the service thread, SDMA copies, stream value-writes)
+and through the reference's own cache state machine on an immediate transport (its canonical schedule). After every
+token the slot table and the cache counters must be identical, and every routed unit the engine read through
+ss_dg_slot must checksum to the oracle's value of the file bytes. Device verify (verify_hash = 2) re-hashes every
+landed unit in HBM. Shapes: the mixtral workload at test size (reference tests/test_dg_cuda.cu:297-323 drives the
+same protocol)."""
+import numpy as np
+import pytest
+
+from oracle import fixtures, ref
+from tierstream_amd import ss
+
+pytestmark = pytest.mark.gpu
+
+KiB = 1024
+COUNTERS = ["lookups", "misses", "covered", "fetched", "resurrected", "bank_serves", "evicted", "evict_short",
+            "wb_deferred", "wb_cancelled", "wb_boundary_flushed", "inclusive_kept", "inclusive_drops"]
+
+
+def _setup(tmp_path, layers, units, parts, n_res, dyn, spares, n_ids, inclusive=0, seed=21, wb_defer=1, zipf=True):
+    m = fixtures.write_model(tmp_path, layers, units, parts, top_k=n_ids, seed=seed)
+    st = (m.unit_bytes + 255) // 256 * 256
+    hs = (m.unit_bytes + 4095) // 4096 * 4096
+    ring = 2 * n_ids + 1
+    dev = n_res * st + ring * st + dyn * layers * st + st // 2
+    host = (layers * units - n_res + spares) * hs + hs // 2 + (1 << 20)
+    bkw = dict(device_bytes=dev, host_pinned_bytes=host, dynamic_slots_per_layer=dyn, ring_slots=ring, tier_mode=1,
+               host_spare_units=spares)
+    okw = dict(forward_mode=1, dg_max_ids=n_ids, pin_planned=0, verify_hash=2, dg_inclusive_blocks=inclusive,
+               dg_wb_defer=wb_defer, dg_wait_timeout_ms=5000)
+    return m, bkw, okw
+
+
+def _routes(layers, units, n_ids, tokens, seed, zipf):
+    rng = np.random.default_rng(seed)
+    if zipf:
+        p = 1.0 / np.arange(1, units + 1) ** 1.1
+        p /= p.sum()
+    else:
+        p = np.full(units, 1.0 / units)
+    perms = [np.random.default_rng(seed + L).permutation(units) for L in range(layers)]
+    out = np.zeros((tokens, layers, n_ids), dtype=np.int32)
+    for t in range(tokens):
+        for L in range(layers):
+            out[t, L] = perms[L][rng.choice(units, size=n_ids, replace=False, p=p)]
+    return out
+
+
+CASES = {
+    "mixtral-shape": dict(layers=4, units=8, parts=[64 * KiB] * 3, n_res=12, dyn=1, spares=6, n_ids=2, tokens=24),
+    "clean-copies": dict(layers=4, units=8, parts=[64 * KiB] * 3, n_res=12, dyn=1, spares=8, n_ids=2, tokens=24,
+                         inclusive=5),
+    "boundary-writebacks": dict(layers=3, units=16, parts=[32 * KiB, 32 * KiB, 64 * KiB], n_res=12, dyn=2, spares=10,
+                                n_ids=4, tokens=20, wb_defer=0, zipf=False),
+    "batch-union": dict(layers=4, units=16, parts=[64 * KiB] * 3, n_res=20, dyn=2, spares=12, n_ids=8, tokens=16),
+    # kernels launched one by one on the engine's stream (no graph): the library's copy and publication streams must
+    # not queue behind the spinning wait kernel
+    "direct-launch": dict(layers=4, units=8, parts=[64 * KiB] * 3, n_res=12, dyn=1, spares=6, n_ids=2, tokens=12,
+                          graph=False),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_dg_matches_reference(name, tmp_path, gpu):
+    c = dict(CASES[name])
+    tokens = c.pop("tokens")
+    zipf = c.pop("zipf", True)
+    use_graph = c.pop("graph", True)
+    m, bkw, okw = _setup(tmp_path, c["layers"], c["units"], c["parts"], c["n_res"], c["dyn"], c["spares"], c["n_ids"],
+                         inclusive=c.get("inclusive", 0), wb_defer=c.get("wb_defer", 1))
+    routes = _routes(c["layers"], c["units"], c["n_ids"], tokens, seed=5, zipf=zipf)
+    d = ss.Desc(m.desc_json())
+    plan = ss.Plan(d, ss.budget(**bkw))
+    pj = plan.json()
+    tiers = plan.tiers()
+    residents = [L * c["units"] + u for L in range(c["layers"]) for u in range(c["units"]) if tiers[L][u] == 0]
+    P = sum(1 for L in range(c["layers"]) for u in range(c["units"]) if tiers[L][u] == 1)
+    Q = [s["blocks"] for s in pj["spare_blocks"]][0]
+    # spare slots: each gated layer contributes min(dynamic_slots_per_layer, its non-resident units)
+    # (reference src/dg_layout.cpp:284)
+    R = len(residents)
+    D = sum(min(c["dyn"], sum(1 for u in range(c["units"]) if tiers[L][u] != 0)) for L in range(c["layers"]))
+    keys = c["layers"] * c["units"]
+    refdg = ref.RefDg([c["units"]] * c["layers"], R + D, c["n_ids"], P + Q, D, c["parts"],
+                      residents + list(range(keys)), wb_defer=c.get("wb_defer", 1), inclusive=c.get("inclusive", 0))
+    ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(**okw))
+    eng = ss.DgEngine(ctx, c["n_ids"], use_graph=use_graph)
+    expect = {(L, u): fixtures.engine_checksum(m.unit_data(L, u)) for L in range(c["layers"]) for u in range(c["units"])}
+    try:
+        for t in range(tokens):
+            cks, _ = eng.token(routes[t])
+            want_table, want = refdg.token(routes[t].astype(np.uint32))
+            got = ctx.dg_stats()
+            assert np.array_equal(ctx.dg_table(), want_table), (name, t)
+            for k in COUNTERS:
+                assert got[k] == want[k], (name, t, k, got[k], want[k])
+            for L in range(c["layers"]):
+                for i, u in enumerate(routes[t, L]):
+                    assert int(cks[L, i]) == expect[(L, int(u))], (name, t, L, i)
+        assert got["tokens"] == tokens and got["misses"] > 0
+    finally:
+        eng.close()
+        ctx.close()
+        refdg.close()
+
+
+def test_zero_miss_token_needs_no_copy(tmp_path, gpu):
+    """A token whose every routed unit is resident: no miss, no copy, the wait kernels return at once."""
+    m, bkw, okw = _setup(tmp_path, 2, 16, [64 * KiB] * 3, 24, 1, 4, 2)
+    d = ss.Desc(m.desc_json())
+    plan = ss.Plan(d, ss.budget(**bkw))
+    tiers = plan.tiers()
+    res = [[u for u in range(16) if tiers[L][u] == 0] for L in range(2)]
+    assert len(res[1]) >= 2 and any(t != 0 for t in tiers[1]), tiers  # layer 1 streams, two of its units are resident
+    routes = np.array([res[0][:2], res[1][:2]], dtype=np.int32)
+    ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(**okw))
+    eng = ss.DgEngine(ctx, 2, use_graph=True)
+    try:
+        for t in range(4):
+            cks, _ = eng.token(routes)
+            for L in range(2):
+                for i, u in enumerate(routes[L]):
+                    assert int(cks[L, i]) == fixtures.engine_checksum(m.unit_data(L, int(u)))
+        s = ctx.dg_stats()
+        assert s["misses"] == 0 and s["fetched"] == 0 and s["tokens"] == 4 and s["lookups"] == 16
+    finally:
+        eng.close()
+        ctx.close()

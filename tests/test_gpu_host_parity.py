@@ -1,0 +1,100 @@
+"""Host contract on the MI355X against the reference CPU backend (bit-exact): the same descriptor, budget, options and
+route stream through both; per step the stats, every layer's table (region + offset: identical up to base), and the
+checksum of every routed unit's bytes as the engine reads them through table_dev on the device. The reference's
+checksums are of the bytes its own table entries point at, and both must equal the oracle's checksum of the file.
+Shapes follow the BASELINE workloads at test size (reference tests/test_runtime.cpp:58-83 check the same things:
+table bytes == file bytes, stats balance)."""
+import numpy as np
+import pytest
+
+from oracle import fixtures, ref
+from tierstream_amd import ss
+
+pytestmark = pytest.mark.gpu
+
+KiB = 1024
+
+
+def _budget(m, n_res, ring_slots, dyn=0, **kw):
+    st = (m.unit_bytes + 255) // 256 * 256
+    ring = ring_slots * st
+    dev = n_res * st + ring + dyn * m.layers * st + st // 2
+    host = (m.layers * m.units) * ((m.unit_bytes + 4095) // 4096 * 4096) + (64 << 20)
+    return dict(device_bytes=dev, host_pinned_bytes=host, dynamic_slots_per_layer=dyn, ring_slots=ring_slots, **kw)
+
+
+CASES = {
+    # moe-small shape: ranked, half resident, inclusive, planned residents pinned (no eviction)
+    "moe-small": dict(layers=4, units=8, parts=[64 * KiB] * 3, n_res=16, ring=8, steps=16, top_k=2, mode=0,
+                      opts={}),
+    # decode with a dynamic LRU set: residents are a warm start, 2 spare slots per layer, evictions every step
+    "decode-lru": dict(layers=4, units=8, parts=[32 * KiB, 32 * KiB, 16 * KiB], n_res=8, ring=16, dyn=2, steps=24,
+                       top_k=2, mode=0, opts=dict(pin_planned=0)),
+    # dense-prefix shape: blob layers, prefix order, a 2-slot blob ring, ss_layer_all on every layer
+    "dense-prefix": dict(layers=8, units=1, parts=[256 * KiB], kind="blob", order="prefix", n_res=3, ring=2, steps=4,
+                         top_k=1, mode=1, opts={}),
+    # qwen3-moe shape: a union of 4 tokens x top-4, exclusive with write-backs, hits-first groups
+    "qwen-exclusive": dict(layers=6, units=16, parts=[32 * KiB] * 3, n_res=24, ring=32, dyn=2, steps=20, top_k=4,
+                           tokens=4, mode=2, opts=dict(pin_planned=0, group_units=2),
+                           budget=dict(tier_mode=1, host_spare_units=6)),
+}
+
+
+def _run_case(name, tmp_path, gpu):
+    c = CASES[name]
+    m = fixtures.write_model(tmp_path, c["layers"], c["units"], c["parts"], kind=c.get("kind", "moe"),
+                             top_k=c["top_k"], order=c.get("order", "ranked"), seed=7)
+    routes = fixtures.uniform_routes(c["layers"], c["units"], c["top_k"], c["steps"], seed=11,
+                                     tokens=c.get("tokens", 1))
+    bkw = _budget(m, c["n_res"], c["ring"], c.get("dyn", 0), **c.get("budget", {}))
+    desc_json = m.desc_json()
+    # the reference (CPU backend)
+    want = ref.host_run(desc_json, ss.budget(**bkw), ss.options(**c["opts"]), routes, c["mode"])
+    # the product (MI355X)
+    d = ss.Desc(desc_json)
+    ctx = ss.Ctx(d, ss.budget(**bkw), None, ss.options(**c["opts"]))
+    try:
+        cks, tabs, stats, _ = ctx.host_run(routes, c["mode"])
+        for s in range(c["steps"]):
+            w = want[s]
+            got_stats = {k: v for k, v in stats[s].items() if k != "wait_ns"}
+            want_stats = {k: v for k, v in w["stats"].items() if k != "wait_ns"}
+            assert got_stats == want_stats, (name, s)
+            for l in range(c["layers"]):
+                got_tab = [ctx.region_of(int(a)) if a else (0, -1, 0) for a in tabs[s, l, :c["units"]]]
+                assert got_tab == w["tables"][l], (name, s, l)
+                ids = list(range(c["units"])) if c["mode"] == 1 else [int(x) for x in routes[s, l] if x >= 0]
+                exp = [fixtures.engine_checksum(m.unit_data(l, u)) for u in ids]
+                assert [int(x) for x in cks[s, l, :len(ids)]] == exp == w["checksums"][l], (name, s, l)
+        return ctx, want
+    except Exception:
+        ctx.close()
+        raise
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_host_contract_matches_reference(name, tmp_path, gpu):
+    ctx, _ = _run_case(name, tmp_path, gpu)
+    tot = ctx.stats_total()
+    # the stats balance of reference tests/test_runtime.cpp:78-83
+    assert tot["hits"] + tot["admitted"] + tot["transient"] + tot["prefetched"] + tot["spec_used"] == tot["routed"]
+    if name == "qwen-exclusive":
+        x = ctx.exclusive_stats()
+        assert x["writebacks"] > 0  # the shape exercises write-backs
+    ctx.close()
+
+
+def test_device_verify_of_landed_units(tmp_path, gpu):
+    """verify_hash = 2: every landed unit re-hashed in HBM (checkpoint-parallel) against the descriptor; none fails."""
+    c = CASES["decode-lru"]
+    m = fixtures.write_model(tmp_path, c["layers"], c["units"], c["parts"], top_k=2, seed=3)
+    routes = fixtures.uniform_routes(c["layers"], c["units"], 2, 12, seed=5)
+    bkw = _budget(m, c["n_res"], c["ring"], c["dyn"])
+    d = ss.Desc(m.desc_json())
+    ctx = ss.Ctx(d, ss.budget(**bkw), None, ss.options(pin_planned=0, verify_hash=2))
+    try:
+        ctx.host_run(routes, 0)
+        import tierstream_amd as tsa
+        assert tsa.ss._declare().tsa_test_verify_failures(ctx.h) == 0
+    finally:
+        ctx.close()

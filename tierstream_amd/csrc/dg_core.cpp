@@ -1,0 +1,679 @@
+#include "dg_core.hpp"
+
+#include <algorithm>
+#include <string>
+
+#include "common.hpp"
+
+namespace tsa {
+namespace {
+[[noreturn]] void broken(const std::string& what) { fail(SS_E_BACKEND, "device-gated cache invariant: " + what); }
+}  // namespace
+
+DgCore::DgCore(const DgConfig& cfg, DgTransport* t) : c_(cfg), t_(t) {
+  base_.assign(1, 0);
+  uint64_t n = 0;
+  for (uint32_t u : c_.n_units) {
+    n += u;
+    require(n < 0x7fffffffull, SS_E_INVALID, "device-gated: more than 2^31 - 1 gated units");
+    base_.push_back(uint32_t(n));
+  }
+  keys_ = uint32_t(n);
+  require(c_.persistent_slots >= 1 && c_.spare_target <= c_.persistent_slots, SS_E_INVALID,
+          "device-gated: spare target above the persistent slots");
+  const uint64_t slots = uint64_t(c_.persistent_slots) + 2ull * c_.bank_slots;
+  require(slots < 0x7fffffffull, SS_E_INVALID, "device-gated: more than 2^31 - 1 slots");
+  slots_ = uint32_t(slots);
+  bank_first_ = c_.persistent_slots;
+  e_.assign(keys_, Entry{});
+  table_.assign(keys_, -1);
+  bank_key_.assign(2u * size_t(c_.bank_slots), kNone);
+  pf_layer_.assign(gated(), 0);
+  layer_missed_.assign(gated(), 0);
+  lc_.assign(gated(), DgLayerCounts{});
+  slot_ev_.assign(slots_, nullptr);
+  block_ev_.assign(c_.blocks, nullptr);
+  if (c_.prefetch_reserve_auto) c_.prefetch_reserve = std::min<uint32_t>(24, c_.spare_target / 4);
+  require(t_->parts() >= 1, SS_E_INVALID, "device-gated: a unit without parts");
+  for (uint32_t p = 0; p < t_->parts(); ++p) unit_bytes_ += t_->part_bytes(p);
+  require(c_.inclusive < c_.blocks || c_.inclusive == 0, SS_E_INVALID,
+          "device-gated: the inclusive share must leave a block for write-backs");
+  if (c_.wb_defer) {
+    wb_stream_ = c_.wb_on_d2h ? DgTransport::kD2h : DgTransport::kDem;
+    layer_bytes_ = c_.wb_layer_bytes ? c_.wb_layer_bytes : t_->part_bytes(0);
+    max_outstanding_ = c_.wb_max_outstanding ? c_.wb_max_outstanding : 2 * unit_bytes_;
+    if (c_.wb_on_d2h) post_ready_ev_ = event();
+  }
+  victims_.reserve(c_.persistent_slots);
+}
+
+DgCore::~DgCore() {
+  for (void* ev : all_events_) t_->event_destroy(ev);
+}
+
+uint32_t DgCore::gated_of(uint32_t k) const {
+  return uint32_t(std::upper_bound(base_.begin(), base_.end(), k) - base_.begin()) - 1;
+}
+
+void* DgCore::event() {
+  if (!event_pool_.empty()) {
+    void* ev = event_pool_.back();
+    event_pool_.pop_back();
+    return ev;
+  }
+  void* ev = t_->event_create();
+  all_events_.push_back(ev);
+  return ev;
+}
+
+// ---- write-back events attached to slots and blocks ----
+// A write-back is collected in bookkeeping when the canonical schedule says so (see the header); until its D2H has
+// really finished, its event stays attached to the slot it reads and the block it writes, and any copy into that slot
+// or out of that block first makes its stream wait for it (device side).
+void DgCore::attach(std::vector<void*>& where, int32_t i, void* ev) {
+  if (where[size_t(i)]) detach(where, i);
+  where[size_t(i)] = ev;
+  ++ev_refs_[ev];
+}
+
+void DgCore::detach(std::vector<void*>& where, int32_t i) {
+  void* ev = where[size_t(i)];
+  if (!ev) return;
+  where[size_t(i)] = nullptr;
+  auto it = ev_refs_.find(ev);
+  if (it == ev_refs_.end()) broken("a write-back event without references");
+  if (--it->second == 0) {
+    ev_refs_.erase(it);
+    event_pool_.push_back(ev);
+  }
+}
+
+void DgCore::sweep_events() {
+  for (uint32_t s = 0; s < slots_; ++s)
+    if (slot_ev_[s] && t_->query(slot_ev_[s])) detach(slot_ev_, int32_t(s));
+  for (uint32_t b = 0; b < c_.blocks; ++b)
+    if (block_ev_[b] && t_->query(block_ev_[b])) detach(block_ev_, int32_t(b));
+}
+
+void DgCore::place(const std::vector<uint32_t>& priority) {
+  const uint32_t dev_max = c_.persistent_slots - c_.spare_target;
+  std::vector<uint8_t> placed(keys_, 0);
+  std::vector<uint32_t> order;
+  for (uint32_t k : priority) {
+    require(k < keys_, SS_E_INVALID, "device-gated: resident key out of range");
+    if (!placed[k] && order.size() < dev_max) {
+      placed[k] = 1;
+      order.push_back(k);
+    }
+  }
+  const uint32_t dev0 = uint32_t(order.size());
+  require(uint64_t(keys_) - dev0 <= c_.blocks, SS_E_CAPACITY, "device-gated: fewer host blocks than non-resident units");
+  int32_t next_block = 0;
+  on_host_ = backed_ = 0;
+  for (uint32_t k = 0; k < keys_; ++k) {
+    Entry& x = e_[k];
+    x = Entry{};
+    if (!placed[k]) {
+      x.home = Home::Host;
+      x.block = next_block++;
+      ++on_host_;
+    }
+  }
+  for (uint32_t i = 0; i < dev0; ++i) {
+    Entry& x = e_[order[i]];
+    x.home = Home::Device;
+    x.slot = int32_t(i);
+    table_[order[i]] = x.slot;
+  }
+  head_ = tail_ = kNone;
+  for (uint32_t i = dev0; i-- > 0;) push_front(order[i]);  // the first of the priority list is the most recent
+  on_device_ = dev0;
+  free_slots_.clear();
+  free_blocks_.clear();
+  for (uint32_t s = c_.persistent_slots; s-- > dev0;) free_slots_.push_back(int32_t(s));  // lowest on top
+  for (int32_t b = int32_t(c_.blocks); b-- > next_block;) free_blocks_.push_back(b);
+}
+
+void DgCore::unlink(uint32_t k) {
+  Entry& x = e_[k];
+  if (!x.in_list) return;
+  if (x.prev != kNone) e_[x.prev].next = x.next;
+  else head_ = x.next;
+  if (x.next != kNone) e_[x.next].prev = x.prev;
+  else tail_ = x.prev;
+  x.prev = x.next = kNone;
+  x.in_list = false;
+}
+
+void DgCore::push_front(uint32_t k) {
+  Entry& x = e_[k];
+  x.prev = kNone;
+  x.next = head_;
+  if (head_ != kNone) e_[head_].prev = k;
+  else tail_ = k;
+  head_ = k;
+  x.in_list = true;
+}
+
+std::vector<uint32_t> DgCore::residency() const {
+  std::vector<uint32_t> out;
+  for (uint32_t k = head_; k != kNone; k = e_[k].next)
+    if (e_[k].home == Home::Device) out.push_back(k);
+  return out;
+}
+
+void DgCore::write_entry(DgTransport::Stream s, uint32_t k, int32_t v) {
+  table_[k] = v;
+  t_->write_entry(s, k, v);
+}
+
+// Every recorded write-back is complete in bookkeeping: the key's block is its home and its slot is free (a discarded
+// one - the key was resurrected - only returns its block). The events stay attached until the copies really ended.
+uint32_t DgCore::collect() {
+  uint32_t n = 0;
+  while (!wbs_.empty()) {
+    Writeback& w = wbs_.front();
+    Entry& x = e_[w.key];
+    x.wb_pending = false;
+    if (w.discard) {
+      free_blocks_.push_back(w.block);
+      attach(block_ev_, w.block, w.done);
+    } else {
+      x.home = Home::Host;
+      x.block = w.block;
+      x.slot = -1;
+      ++on_host_;
+      free_slots_.push_back(w.slot);
+      attach(slot_ev_, w.slot, w.done);
+      attach(block_ev_, w.block, w.done);
+    }
+    ++n;
+    outstanding_ -= w.bytes;
+    st_.wb_completed_bytes += w.bytes;
+    auto it = ev_refs_.find(w.done);
+    if (it == ev_refs_.end()) event_pool_.push_back(w.done);  // (attached to nothing: a discard of a zero-part record)
+    wbs_.pop_front();
+  }
+  st_.writebacks_done += n;
+  return n;
+}
+
+void DgCore::submit_part(Deferred& d) {
+  const uint32_t p = d.parts_done;
+  t_->d2h_part(wb_stream_, d.slot, d.block, p);
+  ++d.parts_done;
+  const uint64_t b = t_->part_bytes(p);
+  d.bytes += b;
+  outstanding_ += b;
+  st_.wb_issued_bytes += b;
+}
+
+void* DgCore::record_deferred_front(bool discard) {
+  Deferred& d = deferred_.front();
+  void* ev = event();
+  t_->record(ev, wb_stream_);
+  wbs_.push_back({d.key, d.slot, d.block, ev, discard, d.bytes});
+  deferred_.pop_front();
+  return ev;
+}
+
+void* DgCore::finish_deferred_front() {
+  Deferred& d = deferred_.front();
+  while (d.parts_done < t_->parts()) submit_part(d);
+  return record_deferred_front(false);
+}
+
+void DgCore::issue_writebacks(uint32_t g) {
+  if (deferred_.empty()) {
+    credit_ = 0;
+    return;
+  }
+  if (g + 1 >= gated()) return;  // nothing after the last gated layer
+  const int64_t grant = int64_t(layer_bytes_);
+  credit_ = std::min(credit_ + grant, grant);  // a debt carries over, unused credit does not
+  st_.collected_mid += collect();
+  bool after_ready = false;
+  while (credit_ > 0 && !deferred_.empty() && outstanding_ < max_outstanding_) {
+    if (wb_stream_ == DgTransport::kD2h && !after_ready) {  // behind the ready already on the demand stream
+      t_->record(post_ready_ev_, DgTransport::kDem);
+      t_->wait(DgTransport::kD2h, post_ready_ev_);
+      after_ready = true;
+    }
+    Deferred& d = deferred_.front();
+    credit_ -= int64_t(t_->part_bytes(d.parts_done));
+    if (d.parts_done + 1 == t_->parts()) finish_deferred_front();
+    else submit_part(d);
+  }
+}
+
+// A demand without a free slot while victims are deferred: finish the deferred front (its remaining parts), collect,
+// until a persistent slot is free.
+void DgCore::force_free_slot() {
+  while (free_slots_.empty() && !deferred_.empty()) {
+    bool live = false;
+    for (const Writeback& w : wbs_) live = live || !w.discard;
+    if (!live) finish_deferred_front();
+    ++st_.wb_forced;
+    st_.collected_mid += collect();
+  }
+}
+
+// A demand bank slot of gated layer g: bank g & 1, reused two gated layers later; its previous alias is unpublished.
+int32_t DgCore::take_bank_slot(uint32_t g) {
+  const uint32_t b = g & 1u;
+  if (bank_seq_[b] != seq_ || bank_layer_[b] != g) {
+    bank_seq_[b] = seq_;
+    bank_layer_[b] = g;
+    bank_next_[b] = 0;
+  }
+  if (bank_next_[b] >= c_.bank_slots) return -1;
+  const uint32_t idx = b * c_.bank_slots + bank_next_[b]++;
+  const int32_t slot = int32_t(bank_first_ + idx);
+  const uint32_t old = bank_key_[idx];
+  if (old != kNone && e_[old].home == Home::Bank && e_[old].slot == slot) {
+    to_block(old);
+    write_entry(DgTransport::kDem, old, -1);
+  }
+  bank_key_[idx] = kNone;
+  return slot;
+}
+
+void DgCore::to_block(uint32_t k) {
+  Entry& x = e_[k];
+  x.slot = -1;
+  if (x.backed) {
+    x.backed = false;
+    --backed_;
+  }
+  if (x.block < 0) broken("a key without a block left the device without a write-back");
+  x.home = Home::Host;
+  ++on_host_;
+}
+
+void DgCore::begin_token(uint32_t seq) {
+  seq_ = seq;
+  pf_token_ = 0;
+  std::fill(pf_layer_.begin(), pf_layer_.end(), 0u);
+  std::fill(layer_missed_.begin(), layer_missed_.end(), uint8_t(0));
+  pred_.clear();
+  pred_layer_ = kNone;
+}
+
+bool DgCore::fetch(uint32_t g, uint32_t unit, bool prefetch) {
+  const uint32_t k = key(g, unit);
+  Entry& x = e_[k];
+  if (prefetch && (pf_layer_[g] >= c_.prefetch_per_layer || pf_token_ >= c_.prefetch_per_token)) return false;
+  switch (x.home) {
+    case Home::Coming:
+    case Home::Device:
+    case Home::Bank:
+      return false;
+    case Home::Evicting: {  // resurrection: the slot still holds the bytes (the write-back only reads them)
+      bool done = false;
+      for (auto it = deferred_.begin(); it != deferred_.end() && !done; ++it) {
+        if (it->key != k) continue;
+        done = true;
+        if (it->parts_done == 0) {  // nothing submitted: the record goes, its block returns unread
+          const int32_t b = it->block;
+          deferred_.erase(it);
+          free_blocks_.push_back(b);
+          x.wb_pending = false;
+          ++st_.wb_cancelled;
+          st_.wb_cancelled_bytes += unit_bytes_;
+        } else {  // partly submitted (only the front): its event after the sent parts, discarded
+          if (it != deferred_.begin()) broken("parts submitted behind the deferred front");
+          st_.wb_cancelled_bytes += unit_bytes_ - it->bytes;
+          record_deferred_front(true);
+        }
+        break;
+      }
+      if (!done)
+        for (Writeback& w : wbs_)
+          if (w.key == k && !w.discard) {
+            w.discard = true;
+            break;
+          }
+      x.home = Home::Device;
+      x.block = -1;
+      write_entry(DgTransport::kDem, k, x.slot);
+      push_front(k);
+      ++on_device_;
+      ++st_.resurrected;
+      return true;
+    }
+    case Home::Host:
+      break;
+  }
+  int32_t slot = -1;
+  bool bank = false;
+  const size_t reserve = prefetch ? c_.prefetch_reserve : 0u;
+  if (free_slots_.size() <= reserve) st_.collected_mid += collect();
+  if (!prefetch && free_slots_.empty()) force_free_slot();
+  if (free_slots_.size() > reserve) {
+    slot = free_slots_.back();
+    free_slots_.pop_back();
+  } else if (prefetch) {
+    return false;
+  } else {
+    slot = take_bank_slot(g);
+    if (slot >= 0) {
+      bank = true;
+    } else {  // a layer has at most bank_slots distinct misses: only an internal error reaches here
+      force_free_slot();
+      while (free_slots_.empty() && !wbs_.empty()) {
+        collect();
+        ++st_.stalled;
+      }
+      if (free_slots_.empty()) fail(SS_E_BACKEND, "device-gated: no free slot, no bank slot, no write-back to wait for");
+      slot = free_slots_.back();
+      free_slots_.pop_back();
+    }
+  }
+  const DgTransport::Stream s = prefetch ? DgTransport::kPf : DgTransport::kDem;
+  // the slot's last write-back and the block's incoming write-back (if still copying) come first
+  if (slot_ev_[size_t(slot)]) {
+    t_->wait(s, slot_ev_[size_t(slot)]);
+    detach(slot_ev_, slot);
+  }
+  if (block_ev_[size_t(x.block)]) {
+    t_->wait(s, block_ev_[size_t(x.block)]);
+    detach(block_ev_, x.block);
+  }
+  t_->h2d(s, slot, x.block);
+  write_entry(s, k, slot);
+  --on_host_;
+  x.slot = slot;
+  x.via_prefetch = prefetch;
+  x.used = false;
+  if (prefetch) {
+    x.pf_done = event();
+    t_->record(x.pf_done, s);
+  }
+  if (bank) {
+    x.home = Home::Bank;
+    bank_key_[size_t(slot) - bank_first_] = k;
+    banked_.push_back(k);
+    ++st_.bank_serves;
+    ++lc_[g].bank_serves;
+  } else {
+    x.home = Home::Coming;
+    coming_.push_back(k);
+    push_front(k);
+    ++on_device_;
+  }
+  if (prefetch) {
+    ++st_.prefetched;
+    ++lc_[g].prefetched;
+    ++pf_layer_[g];
+    ++pf_token_;
+    t_->landed(s, g, &k, &slot, 1);
+  } else {
+    ++st_.fetched;
+    ++lc_[g].fetched;
+    landed_keys_.push_back(k);
+    landed_slots_.push_back(slot);
+  }
+  return true;
+}
+
+void DgCore::cover(uint32_t g, uint32_t unit) {
+  Entry& x = e_[key(g, unit)];
+  if (x.home == Home::Coming && x.via_prefetch && x.pf_done) {  // the layer's readers wait for the prefetch's copies
+    t_->wait(DgTransport::kDem, x.pf_done);
+    ++st_.covered_waits;
+  }
+}
+
+void DgCore::use(uint32_t g, uint32_t unit, bool was_miss) {
+  const uint32_t k = key(g, unit);
+  Entry& x = e_[k];
+  ++st_.lookups;
+  ++lc_[g].lookups;
+  if (was_miss) {
+    ++st_.misses;
+    ++lc_[g].misses;
+    if (!layer_missed_[g]) {
+      layer_missed_[g] = 1;
+      ++st_.miss_layers;
+    }
+  }
+  if (x.via_prefetch && !x.used) {
+    x.used = true;
+    ++st_.prefetch_used;
+    ++lc_[g].prefetch_used;
+  }
+  if (x.in_list) {
+    unlink(k);
+    push_front(k);
+  }
+}
+
+void DgCore::serve_demand(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask) {
+  const uint32_t nu = units(g);
+  for (uint32_t i = 0; i < n; ++i)
+    require(ids[i] < nu, SS_E_INVALID,
+            "device-gated: layer " + std::to_string(g) + " exported id " + std::to_string(ids[i]) + " of " +
+                std::to_string(nu));
+  landed_keys_.clear();
+  landed_slots_.clear();
+  // per masked occurrence in export order: a repeated id is fetched at its first occurrence, covered at the others
+  for (uint32_t i = 0; i < n; ++i) {
+    if (!(mask >> i & 1u)) continue;
+    if (on_device_or_coming(g, ids[i])) {
+      cover(g, ids[i]);
+      ++st_.covered;
+    } else {
+      fetch(g, ids[i], false);
+    }
+  }
+  if (mask) t_->signal_ready(g, seq_);
+  if (!landed_keys_.empty())
+    t_->landed(DgTransport::kDem, g, landed_keys_.data(), landed_slots_.data(), uint32_t(landed_keys_.size()));
+}
+
+void DgCore::serve_use(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask) {
+  const bool have_pred = pred_layer_ == g;
+  uniq_.assign(ids, ids + n);
+  std::sort(uniq_.begin(), uniq_.end());
+  uniq_.erase(std::unique(uniq_.begin(), uniq_.end()), uniq_.end());
+  for (uint32_t id : uniq_) {
+    bool miss = false;
+    for (uint32_t i = 0; i < n; ++i)
+      if (ids[i] == id && (mask >> i & 1u)) miss = true;
+    use(g, id, miss);
+    if (have_pred && std::find(pred_.begin(), pred_.end(), id) != pred_.end()) ++st_.predicted_true;
+  }
+  pred_.clear();
+  pred_layer_ = kNone;
+}
+
+void DgCore::serve_prediction(uint32_t g_next, const uint32_t* pred, uint32_t n) {
+  if (g_next >= gated()) return;
+  const uint32_t nu = units(g_next);
+  uniq_.clear();
+  for (uint32_t i = 0; i < n; ++i) {  // order kept: the budget keeps the head of the list
+    if (pred[i] >= nu) {
+      ++st_.pred_invalid;
+      continue;
+    }
+    if (std::find(uniq_.begin(), uniq_.end(), pred[i]) == uniq_.end()) uniq_.push_back(pred[i]);
+  }
+  st_.predicted += uniq_.size();
+  pred_.assign(uniq_.begin(), uniq_.end());
+  pred_layer_ = g_next;
+  for (uint32_t id : pred_) fetch(g_next, id, true);
+}
+
+void DgCore::end_token() {
+  // every copy and entry write of the token has landed before anything changes home
+  t_->sync(DgTransport::kDem);
+  t_->sync(DgTransport::kPf);
+  for (uint32_t k : coming_) {  // admitted: device homes now; their source blocks are free (or kept clean)
+    Entry& x = e_[k];
+    if (x.home != Home::Coming) continue;
+    x.home = Home::Device;
+    x.via_prefetch = false;
+    if (x.pf_done) {
+      event_pool_.push_back(x.pf_done);
+      x.pf_done = nullptr;
+    }
+    if (x.block >= 0) {
+      if (backed_ < c_.inclusive) {
+        x.backed = true;
+        ++backed_;
+        ++st_.inclusive_kept;
+      } else {
+        free_blocks_.push_back(x.block);
+        x.block = -1;
+      }
+    }
+  }
+  coming_.clear();
+  for (uint32_t k : banked_) {  // bank units: back to their blocks
+    Entry& x = e_[k];
+    if (x.home == Home::Bank) {
+      to_block(k);
+      table_[k] = -1;
+    }
+    if (x.pf_done) {
+      event_pool_.push_back(x.pf_done);
+      x.pf_done = nullptr;
+    }
+    x.via_prefetch = false;
+  }
+  banked_.clear();
+  std::fill(bank_key_.begin(), bank_key_.end(), kNone);
+  bank_seq_[0] = bank_seq_[1] = 0;
+  bank_layer_[0] = bank_layer_[1] = kNone;
+  collect();
+  // victims from the recency tail until free + pending + accepted = the spare target; the first victim without a
+  // free block stops the walk (it stays on the device)
+  size_t pending = deferred_.size();
+  for (const Writeback& w : wbs_) pending += w.discard ? 0u : 1u;
+  const size_t base = free_slots_.size() + pending;
+  victims_.clear();
+  size_t got = 0;
+  for (uint32_t k = tail_; k != kNone && base + got < c_.spare_target;) {
+    const uint32_t prev = e_[k].prev;
+    Entry& x = e_[k];
+    if (x.home == Home::Device && !x.wb_pending) {
+      if (x.backed) {  // a clean copy: its block is its home again, no copy
+        ++st_.inclusive_drops;
+        unlink(k);
+        --on_device_;
+        free_slots_.push_back(x.slot);
+        to_block(k);
+        table_[k] = -1;
+        ++st_.evicted;
+        ++lc_[gated_of(k)].evicted;
+        ++got;
+      } else if (free_blocks_.empty()) {
+        ++st_.evict_short;
+        break;
+      } else {
+        const int32_t b = free_blocks_.back();
+        free_blocks_.pop_back();
+        unlink(k);
+        --on_device_;
+        x.home = Home::Evicting;
+        x.block = b;
+        x.wb_pending = true;
+        table_[k] = -1;
+        victims_.push_back(k);
+        ++got;
+      }
+    }
+    k = prev;
+  }
+  const size_t n_evict = victims_.size();
+  t_->upload_table(table_.data(), keys_);  // the device table = the mirror, before any write-back is enqueued
+  const size_t n_old = deferred_.size(), carry = std::max(n_evict, prev_evict_);
+  const size_t n_flush = n_old > carry ? n_old - carry : 0;
+  prev_evict_ = n_evict;
+  credit_ = 0;
+  for (size_t i = 0; c_.wb_defer && i < n_evict; ++i) {
+    const uint32_t k = victims_[i];
+    deferred_.push_back({k, e_[k].slot, e_[k].block, 0, 0});
+    ++st_.wb_deferred;
+    ++st_.evicted;
+    ++lc_[gated_of(k)].evicted;
+  }
+  const uint64_t issued0 = st_.wb_issued_bytes;
+  size_t n_issued = 0;
+  for (; n_issued < n_flush; ++n_issued) finish_deferred_front();
+  st_.wb_boundary_flushed += n_issued;
+  st_.wb_boundary_flushed_bytes += st_.wb_issued_bytes - issued0;
+  for (size_t i = 0; !c_.wb_defer && i < n_evict; ++i) {
+    const uint32_t k = victims_[i];
+    const Entry& x = e_[k];
+    t_->d2h(x.slot, x.block);
+    void* ev = event();
+    t_->record(ev, DgTransport::kD2h);
+    wbs_.push_back({k, x.slot, x.block, ev, false, unit_bytes_});
+    outstanding_ += unit_bytes_;
+    st_.wb_issued_bytes += unit_bytes_;
+    ++st_.evicted;
+    ++lc_[gated_of(k)].evicted;
+  }
+  sweep_events();
+  ++st_.tokens;
+}
+
+void DgCore::drain() {
+  while (!deferred_.empty()) finish_deferred_front();
+  t_->sync(DgTransport::kDem);
+  t_->sync(DgTransport::kPf);
+  t_->sync(DgTransport::kD2h);
+  sweep_events();
+}
+
+void DgCore::set_spare_target(uint32_t n) {
+  require(n <= c_.persistent_slots, SS_E_INVALID, "device-gated: spare target above the persistent slots");
+  c_.spare_target = n;
+  if (c_.prefetch_reserve_auto) c_.prefetch_reserve = std::min<uint32_t>(24, n / 4);
+}
+
+void DgCore::set_prefetch_budget(uint32_t per_layer, uint32_t per_token) {
+  c_.prefetch_per_layer = per_layer;
+  c_.prefetch_per_token = per_token;
+}
+
+void DgCore::check() const {
+  std::vector<uint8_t> slot_used(slots_, 0), block_used(c_.blocks, 0);
+  uint32_t dev = 0, host = 0;
+  for (uint32_t k = 0; k < keys_; ++k) {
+    const Entry& x = e_[k];
+    switch (x.home) {
+      case Home::Device:
+      case Home::Coming:
+        ++dev;
+        [[fallthrough]];
+      case Home::Bank:
+      case Home::Evicting:
+        if (x.slot < 0 || uint32_t(x.slot) >= slots_ || slot_used[size_t(x.slot)]++)
+          broken("slot of key " + std::to_string(k) + " missing or shared");
+        break;
+      case Home::Host:
+        ++host;
+        if (x.slot != -1) broken("a pinned home with a slot");
+        break;
+    }
+    if (x.block >= 0 && (uint32_t(x.block) >= c_.blocks || block_used[size_t(x.block)]++))
+      broken("block of key " + std::to_string(k) + " shared");
+    if ((x.home == Home::Host || x.home == Home::Evicting || x.home == Home::Bank) && x.block < 0)
+      broken("key " + std::to_string(k) + " has no block in a home that needs one");
+    if (x.home == Home::Device && table_[k] != x.slot) broken("device key " + std::to_string(k) + " unpublished");
+    if ((x.home == Home::Host || x.home == Home::Evicting) && table_[k] >= 0)
+      broken("key " + std::to_string(k) + " published while off the device");
+  }
+  for (int32_t s : free_slots_)
+    if (slot_used[size_t(s)]++) broken("free slot " + std::to_string(s) + " also owned");
+  for (int32_t b : free_blocks_)
+    if (block_used[size_t(b)]++) broken("free block " + std::to_string(b) + " also owned");
+  for (const Writeback& w : wbs_)
+    if (w.discard && block_used[size_t(w.block)]++) broken("a discarded write-back's block also owned");
+  if (dev != on_device_) broken("device count");
+  if (host != on_host_) broken("pinned count");
+}
+
+}  // namespace tsa

@@ -1,0 +1,194 @@
+// Device-gated decode: the cache state machine, free of any device API (a transport does the copies, publications and
+// events). The decisions - homes (Host / Device / Coming / Bank / Evicting), free-slot and bank-slot choice, cover,
+// resurrection, recency, the boundary's admissions, victims from the recency tail to the spare target, deferred
+// write-backs with a per-layer credit, the inclusive share of clean copies - are those of reference src/dg_core.cpp
+// (place :769-858, fetch_impl :1146-1368, serve_demand / serve_use / serve_prediction :1415-1634, end_token
+// :1636-1927, collect / write-back scheduling :961-1097) for its two-tier LRU configuration.
+//
+// Schedule: this core asks its transport for completion (collect) only through done(), which the MI355X transport
+// answers after waiting for the event, and it never asks whether the device "ran ahead". Every decision is therefore
+// the one the reference makes under its canonical (eager) schedule: placement is a function of the route stream alone,
+// which is what makes slot tables comparable bit for bit with the CPU oracle.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <deque>
+#include <unordered_map>
+#include <vector>
+
+namespace tsa {
+
+class DgTransport {
+ public:
+  enum Stream { kDem = 0, kPf = 1, kD2h = 2 };
+  virtual ~DgTransport() = default;
+  virtual void h2d(Stream s, int32_t slot, int32_t block) = 0;  // every part, host block -> slot
+  virtual void d2h(int32_t slot, int32_t block) = 0;            // every part, slot -> block, on kD2h
+  virtual void d2h_part(Stream s, int32_t slot, int32_t block, uint32_t part) = 0;
+  virtual uint32_t parts() const = 0;
+  virtual uint64_t part_bytes(uint32_t part) const = 0;
+  virtual void write_entry(Stream s, uint32_t key, int32_t v) = 0;  // slot_of[key] = v after s's earlier work
+  virtual void signal_ready(uint32_t g, uint32_t seq) = 0;          // ready[g] = seq on kDem, after its copies
+  virtual void* event_create() = 0;
+  virtual void event_destroy(void* ev) = 0;
+  virtual void record(void* ev, Stream s) = 0;
+  virtual void wait(Stream s, void* ev) = 0;
+  virtual bool done(void* ev) = 0;
+  virtual void event_sync(void* ev) = 0;
+  virtual void sync(Stream s) = 0;
+  virtual bool query(void* ev) = 0;  // non-blocking: the event's last record has completed
+  virtual void upload_table(const int32_t* table, uint32_t n) = 0;  // the whole table on kDem, then sync
+  // Units just copied in (key, slot) on stream s (a layer's demand copies after its ready, or one prefetch): a
+  // transport that verifies landed bytes enqueues the check here (default: nothing).
+  virtual void landed(Stream s, uint32_t g, const uint32_t* keys, const int32_t* slots, uint32_t n) {
+    (void)s, (void)g, (void)keys, (void)slots, (void)n;
+  }
+};
+
+struct DgConfig {
+  std::vector<uint32_t> n_units;  // per gated layer
+  uint32_t persistent_slots = 0;  // R + D
+  uint32_t bank_slots = 0;        // per bank (dg_max_ids)
+  uint32_t blocks = 0;            // P + Q
+  uint32_t spare_target = 0;
+  uint32_t prefetch_reserve = 0;
+  bool prefetch_reserve_auto = false;
+  uint32_t prefetch_per_layer = 4, prefetch_per_token = 48;
+  bool wb_defer = true, wb_on_d2h = true;
+  uint64_t wb_layer_bytes = 0, wb_max_outstanding = 0;
+  uint32_t inclusive = 0;  // device units that may keep their block as a clean copy
+};
+
+struct DgCounts {  // the subset of ss_dg_stats this core counts
+  uint64_t tokens = 0, lookups = 0, misses = 0, covered = 0, fetched = 0, prefetched = 0, prefetch_used = 0;
+  uint64_t pred_invalid = 0, resurrected = 0, bank_serves = 0, collected_mid = 0, evicted = 0, evict_short = 0;
+  uint64_t writebacks_done = 0, stalled = 0, predicted = 0, predicted_true = 0, miss_layers = 0, covered_waits = 0;
+  uint64_t wb_deferred = 0, wb_cancelled = 0, wb_forced = 0, wb_boundary_flushed = 0;
+  uint64_t wb_issued_bytes = 0, wb_completed_bytes = 0, wb_cancelled_bytes = 0, wb_boundary_flushed_bytes = 0;
+  uint64_t wb_forced_wait_ns = 0, inclusive_kept = 0, inclusive_drops = 0;
+};
+struct DgLayerCounts {
+  uint64_t lookups = 0, misses = 0, fetched = 0, bank_serves = 0, prefetched = 0, prefetch_used = 0, evicted = 0;
+};
+
+class DgCore {
+ public:
+  enum class Home : uint8_t { Host, Device, Coming, Bank, Evicting };
+
+  DgCore(const DgConfig& cfg, DgTransport* t);
+  ~DgCore();
+  DgCore(const DgCore&) = delete;
+  DgCore& operator=(const DgCore&) = delete;
+
+  // Open: the first persistent_slots - spare_target distinct keys of `priority` take slots 0.. (the first one most
+  // recent); every other key takes a block, in key order; free slots are a stack with the lowest on top.
+  void place(const std::vector<uint32_t>& priority);
+  uint32_t keys() const { return keys_; }
+  uint32_t gated() const { return uint32_t(base_.size() - 1); }
+  uint32_t units(uint32_t g) const { return base_[g + 1] - base_[g]; }
+  uint32_t key(uint32_t g, uint32_t u) const { return base_[g] + u; }
+  uint32_t gated_of(uint32_t k) const;
+  const std::vector<uint32_t>& unit_base() const { return base_; }
+  const std::vector<int32_t>& table() const { return table_; }
+  Home home(uint32_t k) const { return e_[k].home; }
+  int32_t slot_of(uint32_t k) const { return e_[k].slot; }
+  int32_t block_of(uint32_t k) const { return e_[k].block; }
+  uint32_t free_slots() const { return uint32_t(free_slots_.size()); }
+  uint32_t free_blocks() const { return uint32_t(free_blocks_.size()); }
+  uint32_t on_device() const { return on_device_; }
+  uint32_t backed_units() const { return backed_; }
+  uint64_t outstanding_bytes() const { return outstanding_; }
+  uint32_t deferred() const { return uint32_t(deferred_.size()); }
+  const DgCounts& counts() const { return st_; }
+  const std::vector<DgLayerCounts>& layer_counts() const { return lc_; }
+  std::vector<uint32_t> residency() const;  // device keys, most recent first
+
+  void begin_token(uint32_t seq);
+  void serve_demand(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask);
+  void serve_use(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask);
+  void serve_prediction(uint32_t g_next, const uint32_t* pred, uint32_t n);
+  void issue_writebacks(uint32_t g);  // the deferred write-back slice after layer g's service
+  void end_token();
+  void drain();  // between tokens: every deferred write-back submitted, every stream synchronized
+  void set_spare_target(uint32_t n);
+  void set_prefetch_budget(uint32_t per_layer, uint32_t per_token);
+  uint32_t spare_target() const { return c_.spare_target; }
+  void check() const;  // ownership invariants (tests); throws SS_E_BACKEND naming the first broken rule
+
+ private:
+  static constexpr uint32_t kNone = 0xffffffffu;
+  struct Entry {
+    Home home = Home::Host;
+    int32_t slot = -1, block = -1;
+    uint32_t prev = kNone, next = kNone;
+    bool in_list = false, wb_pending = false, via_prefetch = false, used = false, backed = false;
+    void* pf_done = nullptr;
+  };
+  struct Writeback {
+    uint32_t key;
+    int32_t slot, block;
+    void* done;
+    bool discard;
+    uint64_t bytes;
+  };
+  struct Deferred {
+    uint32_t key;
+    int32_t slot, block;
+    uint32_t parts_done;
+    uint64_t bytes;
+  };
+
+  void unlink(uint32_t k);
+  void push_front(uint32_t k);
+  void* event();
+  uint32_t collect();
+  void submit_part(Deferred& d);
+  void* record_deferred_front(bool discard);
+  void* finish_deferred_front();
+  void force_free_slot();
+  int32_t take_bank_slot(uint32_t g);
+  void write_entry(DgTransport::Stream s, uint32_t k, int32_t v);
+  bool fetch(uint32_t g, uint32_t unit, bool prefetch);
+  void cover(uint32_t g, uint32_t unit);
+  void use(uint32_t g, uint32_t unit, bool was_miss);
+  void to_block(uint32_t k);  // leaves the device (or a bank) without a write-back: its block is its home again
+  void attach(std::vector<void*>& where, int32_t i, void* ev);
+  void detach(std::vector<void*>& where, int32_t i);
+  void sweep_events();
+  bool on_device_or_coming(uint32_t g, uint32_t unit) const {
+    const Home h = e_[key(g, unit)].home;
+    return h == Home::Device || h == Home::Coming || h == Home::Bank;
+  }
+
+  DgConfig c_;
+  DgTransport* t_;
+  std::vector<uint32_t> base_;
+  uint32_t keys_ = 0, slots_ = 0, bank_first_ = 0;
+  std::vector<Entry> e_;
+  std::vector<int32_t> table_;
+  std::vector<int32_t> free_slots_, free_blocks_;
+  uint32_t head_ = kNone, tail_ = kNone, on_device_ = 0, on_host_ = 0, backed_ = 0;
+  std::vector<uint32_t> coming_, banked_, bank_key_;
+  uint32_t bank_seq_[2] = {0, 0}, bank_layer_[2] = {kNone, kNone}, bank_next_[2] = {0, 0};
+  std::deque<Writeback> wbs_;
+  std::deque<Deferred> deferred_;
+  uint64_t unit_bytes_ = 0, outstanding_ = 0, layer_bytes_ = 0, max_outstanding_ = 0;
+  int64_t credit_ = 0;
+  size_t prev_evict_ = 0;
+  DgTransport::Stream wb_stream_ = DgTransport::kDem;
+  void* post_ready_ev_ = nullptr;
+  std::vector<uint32_t> pf_layer_;
+  uint32_t pf_token_ = 0, seq_ = 0, pred_layer_ = kNone;
+  std::vector<uint8_t> layer_missed_;
+  std::vector<uint32_t> pred_, uniq_, victims_;
+  std::vector<uint32_t> landed_keys_;
+  std::vector<int32_t> landed_slots_;
+  std::vector<void*> event_pool_, all_events_;
+  std::vector<void*> slot_ev_, block_ev_;        // a write-back still copying out of the slot / into the block
+  std::unordered_map<void*, int> ev_refs_;      // attachments of each such event
+  DgCounts st_;
+  std::vector<DgLayerCounts> lc_;
+};
+
+}  // namespace tsa

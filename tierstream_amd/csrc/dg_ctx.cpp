@@ -1,0 +1,1094 @@
+#include "dg_ctx.hpp"
+
+#include <hip/hip_runtime_api.h>
+#include <immintrin.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cstring>
+#include <mutex>
+#include <thread>
+#include <vector>
+
+#include "dg_core.hpp"
+#include "dg_proto.hpp"
+#include "hip_rt.hpp"
+#include "source.hpp"
+#include "tsa_device.hpp"
+
+namespace tsa {
+namespace {
+
+using Clock = std::chrono::steady_clock;
+constexpr uint64_t kSegBytes = 64 * 1024;          // device-verify checkpoint spacing
+constexpr uint64_t kScatterBelow = 8ull << 20;     // parts smaller than this land staged + scattered
+
+uint64_t align64(uint64_t v) { return (v + 63) / 64 * 64; }
+
+// ---- layout: refusals and geometry (reference src/dg_layout.cpp:182-446, the two-tier subset) ---------------------
+struct Layout {
+  std::vector<int> gated, ordinal;
+  std::vector<uint32_t> unit_base;
+  std::vector<uint64_t> part_bytes, part_offset;
+  uint64_t unit_bytes = 0, host_stride = 0;
+  uint32_t keys = 0, R = 0, D = 0, B = 0, P = 0, Q = 0, I = 0;
+  uint32_t persistent_slots = 0, slots = 0, guard_slot = 0, blocks = 0;
+  std::vector<uint32_t> residents;
+};
+
+Layout make_layout(const Desc& d, const Plan& p, const ss_options& o) {
+  auto refuse = [](ss_status st, const std::string& why) { fail(st, "device-gated: " + why); };
+  const ss_budget& b = p.budget;
+  if (b.tier_mode != SS_TIER_MODE_EXCLUSIVE) refuse(SS_E_INVALID, "needs tier_mode EXCLUSIVE");
+  if (b.pinned_backing) refuse(SS_E_INVALID, "pinned_backing is refused (each unit has one home)");
+  if (o.policy == SS_POLICY_SCORED || o.policy == SS_POLICY_SCORED_AUTO)
+    refuse(SS_E_UNSUPPORTED, "scored eviction is not part of this library's serve path (policy LRU)");
+  if (o.policy != SS_POLICY_LRU) refuse(SS_E_INVALID, "policy must be LRU or SCORED or SCORED_AUTO");
+  if (o.pin_planned) refuse(SS_E_INVALID, "needs pin_planned = 0 (planned residents are a warm start)");
+  if (!o.fill_residents) refuse(SS_E_INVALID, "needs fill_residents = 1 (a resident's slot is its only copy)");
+  if (o.readahead_units) refuse(SS_E_INVALID, "readahead_units must be 0 (no gated unit is read from its file)");
+  if (o.spec_persistent) refuse(SS_E_INVALID, "spec_persistent is refused (prediction is the service's)");
+  if (o.dg_max_ids < 1 || o.dg_max_ids > kDgMaxIds) refuse(SS_E_INVALID, "dg_max_ids must be 1..64 (rows x top_k)");
+  if (o.dg_wait_timeout_ms < 1) refuse(SS_E_INVALID, "dg_wait_timeout_ms must be >= 1");
+  if (o.dg_wb_defer > 1) refuse(SS_E_INVALID, "dg_wb_defer must be 0 or 1");
+  if (o.dg_wb_stream > 1) refuse(SS_E_INVALID, "dg_wb_stream must be 0 or 1");
+  if (o.dg_disk_tier || o.dg_disk_prefetch || o.dg_disk_staging || (o.dg_disk_queue && o.dg_disk_queue != 0xFFFFFFFFu) ||
+      o.dg_landing_blocks || o.dg_landing_max_queued || o.dg_landing_ttl || o.dg_landing_chunk || o.dg_bank_keep ||
+      o.dg_disk_queue_adapt)
+    refuse(SS_E_UNSUPPORTED, "the three-tier file path (dg_disk_tier and its options) is not in this build yet");
+  if (o.dg_no_admit || o.dg_pf_revert_unused || o.dg_pf_strict_admit || o.dg_prior_len || o.dg_prior ||
+      o.dg_score_profile_len || o.dg_score_profile)
+    refuse(SS_E_UNSUPPORTED, "dg_no_admit / dg_pf_revert_unused / dg_pf_strict_admit / priors / score profiles are "
+                             "not part of this library's serve path");
+  if (o.dg_clean_evict > 1) refuse(SS_E_INVALID, "dg_clean_evict must be 0 or 1");
+
+  Layout x;
+  x.B = o.dg_max_ids;
+  x.ordinal.assign(d.layers.size(), -1);
+  const Layer* shape = nullptr;
+  for (size_t L = 0; L < d.layers.size(); ++L) {
+    const Layer& l = d.layers[L];
+    if (l.n_units == 0) continue;
+    if (!l.streamable)
+      refuse(SS_E_UNSUPPORTED, "layer " + std::to_string(l.index) + " has non-streamable units (every unit is gated)");
+    if (!shape) {
+      shape = &l;
+      if (l.parts.size() > SS_DG_MAX_PARTS) refuse(SS_E_UNSUPPORTED, "more than 4 parts per unit");
+      uint64_t off = 0;
+      for (const Part& part : l.parts) {
+        if (part.bytes % 256 != 0)
+          refuse(SS_E_UNSUPPORTED, "part " + part.name + " is " + std::to_string(part.bytes) +
+                                       " bytes, not a multiple of 256 (the arena stride equals the part bytes)");
+        x.part_bytes.push_back(part.bytes);
+        x.part_offset.push_back(off);
+        off += part.bytes;
+      }
+      x.unit_bytes = l.unit_bytes;
+    } else {
+      bool same = l.parts.size() == shape->parts.size();
+      for (size_t i = 0; same && i < l.parts.size(); ++i) same = l.parts[i].bytes == shape->parts[i].bytes;
+      if (!same) refuse(SS_E_UNSUPPORTED, "layer " + std::to_string(l.index) + " has another part shape (one arena)");
+    }
+    x.ordinal[L] = int(x.gated.size());
+    x.gated.push_back(int(L));
+  }
+  if (x.gated.empty()) refuse(SS_E_INVALID, "the descriptor has no streamable units");
+  x.host_stride = host_stride(x.unit_bytes);
+  x.unit_base.assign(1, 0);
+  uint64_t keys = 0;
+  for (int L : x.gated) {
+    const Layer& l = d.layers[size_t(L)];
+    uint32_t planned = 0;
+    for (int u = 0; u < l.n_units; ++u) {
+      const uint8_t t = p.tier[size_t(d.unit_base[size_t(L)] + u)];
+      if (t == SS_TIER_RESIDENT) {
+        x.residents.push_back(uint32_t(keys + uint64_t(u)));
+        ++planned;
+      } else if (t == SS_TIER_PINNED) {
+        ++x.P;
+      } else {
+        refuse(SS_E_CAPACITY, "unit (" + std::to_string(l.index) + ", " + std::to_string(u) +
+                                  ") is not resident or pinned (no gated unit is read from its file)");
+      }
+    }
+    x.D += std::min<uint32_t>(b.dynamic_slots_per_layer, uint32_t(l.n_units) - planned);
+    keys += uint64_t(l.n_units);
+    require(keys < 0x7fffffffull, SS_E_INVALID, "device-gated: more than 2^31 - 1 gated units");
+    x.unit_base.push_back(uint32_t(keys));
+  }
+  x.keys = uint32_t(keys);
+  x.R = uint32_t(x.residents.size());
+  if (o.dg_spare_slots) {
+    if (o.dg_spare_slots > x.P)
+      refuse(SS_E_INVALID, "dg_spare_slots " + std::to_string(o.dg_spare_slots) + " above the non-resident units (" +
+                               std::to_string(x.P) + ")");
+    x.D = o.dg_spare_slots;
+  }
+  if (x.D < 1)
+    refuse(SS_E_INVALID, "needs dynamic_slots_per_layer > 0 or dg_spare_slots > 0 (the spare slots; the boundary keeps "
+                         "them free)");
+  const uint64_t stride = d.unit_stride(x.gated[0]);
+  uint32_t ring_slots = 0;
+  for (const RingClass& rc : p.rings)
+    if (rc.stride == stride) ring_slots = rc.slots;
+  if (uint64_t(ring_slots) < 2ull * x.B + 1)
+    refuse(SS_E_CAPACITY, "the plan bills " + std::to_string(ring_slots) + " ring slots, the banks and the guard need " +
+                              std::to_string(2 * x.B + 1) + " (set ring_slots = 2 x dg_max_ids + 1)");
+  for (const SpareClass& sc : p.spares)
+    if (sc.block_bytes == x.host_stride) x.Q = sc.blocks;
+  if (x.Q < 1)
+    refuse(SS_E_CAPACITY, "the plan granted no spare blocks (host_spare_units asked " +
+                              std::to_string(b.host_spare_units) + "): a write-back needs a free block");
+  x.blocks = x.P + x.Q;
+  x.I = o.dg_inclusive_blocks;
+  if (x.I && x.I >= x.Q)
+    refuse(SS_E_CAPACITY, "dg_inclusive_blocks " + std::to_string(x.I) + " must stay below the spare blocks (" +
+                              std::to_string(x.Q) + "): raise host_spare_units by the inclusive share");
+  x.persistent_slots = x.R + x.D;
+  const uint64_t S = uint64_t(x.persistent_slots) + 2ull * x.B + 1;
+  require(S < 0x7fffffffull, SS_E_INVALID, "device-gated: more than 2^31 - 1 slots");
+  x.slots = uint32_t(S);
+  x.guard_slot = x.slots - 1;
+  // device admission: the arena, the slot table and the control words instead of what the plan billed for the slots
+  uint64_t need = S * x.unit_bytes + uint64_t(keys) * 4 + 4096;
+  const uint64_t billed = p.resident + p.dynamic + p.ring;
+  const uint64_t limit = p.cap > p.margin ? p.cap - p.margin : 0;
+  const uint64_t other = p.peak >= billed ? p.peak - billed : 0;
+  if (other + need > limit)
+    refuse(SS_E_CAPACITY, "the arena needs " + std::to_string(need) + " bytes where the plan billed " +
+                              std::to_string(billed) + "; with the rest of the plan that is above the cap - margin");
+  return x;
+}
+
+// ---- fine-grained control area layout ----
+struct MappedLayout {
+  uint64_t rec, prec, flag, pflag, words, total;
+};
+MappedLayout mapped_layout(uint32_t G) {
+  MappedLayout m;
+  m.rec = 0;
+  m.prec = align64(m.rec + uint64_t(G) * sizeof(DgRecord));
+  m.flag = align64(m.prec + uint64_t(G) * sizeof(DgPredRecord));
+  m.pflag = align64(m.flag + uint64_t(G) * 4);
+  m.words = align64(m.pflag + uint64_t(G) * 4);
+  m.total = align64(m.words + 8 * 4);
+  return m;
+}
+
+// ---- the HIP transport ----------------------------------------------------------------------------------------------
+class HipTransport final : public DgTransport {
+ public:
+  // max_copies: the most unit copies one stream can enqueue between two boundaries (the boundary synchronizes the
+  // copy streams, so a scatter job entry is never rewritten while its upload may still be pending)
+  HipTransport(HipDevice* dev, const Layout& x, std::vector<void*> arena, int32_t* slot_of_dev, uint32_t* ready_dev,
+               std::vector<void*> block_chunks, uint64_t blocks_per_chunk, uint32_t max_copies)
+      : dev_(dev), x_(x), arena_(std::move(arena)), slot_of_(slot_of_dev), ready_(ready_dev),
+        chunks_(std::move(block_chunks)), per_chunk_(blocks_per_chunk), kJobRing(max_copies + 8) {
+    for (auto& s : s_) s = dev_->stream_create_dedicated();
+    stage_host_ = static_cast<int32_t*>(dev_->alloc_pinned(4ull * x_.keys, "slot table upload stage"));
+    bool small = false;
+    for (uint64_t pb : x_.part_bytes) small = small || pb < kScatterBelow;
+    scatter_ = small && x_.part_bytes.size() > 1;
+    if (scatter_) {
+      for (int k = 0; k < 2; ++k) {
+        stage_dev_[k] = dev_->alloc_device(x_.unit_bytes, "scatter staging");
+        jobs_host_[k] = static_cast<tsa_scatter_job*>(dev_->alloc_pinned(sizeof(tsa_scatter_job) * kJobRing, "jobs"));
+        jobs_dev_[k] = static_cast<tsa_scatter_job*>(dev_->alloc_device(sizeof(tsa_scatter_job) * kJobRing, "jobs"));
+      }
+      scatter_blocks_ = tsa_scatter_blocks(x_.part_bytes.data(), uint32_t(x_.part_bytes.size()));
+    }
+  }
+  ~HipTransport() override {
+    for (auto& s : s_) {
+      (void)hipStreamSynchronize(s);
+      dev_->stream_destroy(s);
+    }
+    dev_->free_pinned(stage_host_);
+    for (int k = 0; k < 2; ++k) {
+      dev_->free_device(stage_dev_[k]);
+      dev_->free_pinned(jobs_host_[k]);
+      dev_->free_device(jobs_dev_[k]);
+    }
+    dev_->free_pinned(vtab_host_);
+    dev_->free_device(vtab_dev_);
+    dev_->free_pinned(vfail_host_);
+    dev_->free_device(vfail_dev_);
+  }
+
+  hipStream_t stream(Stream s) const { return s_[s]; }
+  char* block_ptr(int32_t b) const {
+    return static_cast<char*>(chunks_[size_t(uint64_t(b) / per_chunk_)]) + (uint64_t(b) % per_chunk_) * x_.host_stride;
+  }
+  char* slot_ptr(uint32_t p, int32_t slot) const {
+    return static_cast<char*>(arena_[p]) + uint64_t(slot) * x_.part_bytes[p];
+  }
+
+  void h2d(Stream s, int32_t slot, int32_t block) override {
+    const char* src = block_ptr(block);
+    if (!scatter_) {  // one SDMA copy per part straight into its arena slot
+      for (uint32_t p = 0; p < x_.part_bytes.size(); ++p)
+        copy_h2d(slot_ptr(p, slot), src + x_.part_offset[p], x_.part_bytes[p], s_[s]);
+      return;
+    }
+    // small parts: the whole unit in one SDMA copy to the stream's HBM staging, then one kernel writes every part
+    const int k = s == kPf ? 1 : 0;
+    copy_h2d(stage_dev_[k], src, x_.unit_bytes, s_[s]);
+    const uint32_t j = job_next_[k]++ % kJobRing;
+    tsa_scatter_job& job = jobs_host_[k][j];
+    std::memset(&job, 0, sizeof job);
+    job.src = stage_dev_[k];
+    for (uint32_t p = 0; p < x_.part_bytes.size(); ++p) {
+      job.dst[p] = slot_ptr(p, slot);
+      job.bytes[p] = x_.part_bytes[p];
+    }
+    job.n_parts = uint32_t(x_.part_bytes.size());
+    job.block_first = 0;
+    copy_h2d(jobs_dev_[k] + j, &job, sizeof job, s_[s]);
+    hip_check(hipError_t(launch_scatter(jobs_dev_[k] + j, 1, scatter_blocks_, s_[s])), "scatter launch");
+  }
+  void d2h(int32_t slot, int32_t block) override {
+    char* dst = block_ptr(block);
+    for (uint32_t p = 0; p < x_.part_bytes.size(); ++p)
+      copy_d2h(dst + x_.part_offset[p], slot_ptr(p, slot), x_.part_bytes[p], s_[kD2h]);
+  }
+  void d2h_part(Stream s, int32_t slot, int32_t block, uint32_t p) override {
+    copy_d2h(block_ptr(block) + x_.part_offset[p], slot_ptr(p, slot), x_.part_bytes[p], s_[s]);
+  }
+  uint32_t parts() const override { return uint32_t(x_.part_bytes.size()); }
+  uint64_t part_bytes(uint32_t p) const override { return x_.part_bytes[p]; }
+  void write_entry(Stream s, uint32_t key, int32_t v) override {
+    hip_check(hipStreamWriteValue32(s_[s], slot_of_ + key, uint32_t(v), 0), "hipStreamWriteValue32 (slot entry)");
+  }
+  void signal_ready(uint32_t g, uint32_t seq) override {
+    hip_check(hipStreamWriteValue32(s_[kDem], ready_ + g, seq, 0), "hipStreamWriteValue32 (ready)");
+  }
+  void* event_create() override { return dev_->event_create(); }
+  void event_destroy(void* ev) override { dev_->event_destroy(static_cast<hipEvent_t>(ev)); }
+  void record(void* ev, Stream s) override { ev_record(static_cast<hipEvent_t>(ev), s_[s]); }
+  void wait(Stream s, void* ev) override { stream_wait(s_[s], static_cast<hipEvent_t>(ev)); }
+  bool done(void* ev) override {  // the canonical schedule: a completion query waits for the completion
+    ev_sync(static_cast<hipEvent_t>(ev));
+    return true;
+  }
+  bool query(void* ev) override { return ev_done(static_cast<hipEvent_t>(ev)); }
+  void event_sync(void* ev) override { ev_sync(static_cast<hipEvent_t>(ev)); }
+  void sync(Stream s) override { stream_sync(s_[s]); }
+  void upload_table(const int32_t* table, uint32_t n) override {
+    std::memcpy(stage_host_, table, 4ull * n);
+    copy_h2d(slot_of_, stage_host_, 4ull * n, s_[kDem]);
+    stream_sync(s_[kDem]);
+  }
+
+  // ---- device verify of landed units (verify_hash = 2) ----
+  void enable_verify(const std::vector<uint64_t>& digests, uint64_t* ckpt_dev, uint64_t n_ckpt, uint32_t max_per_token) {
+    verify_ = true;
+    digests_ = digests;
+    ckpt_dev_ = ckpt_dev;
+    n_ckpt_ = n_ckpt;
+    vcap_ = max_per_token;
+    vtab_host_ = static_cast<tsa_verify_unit*>(dev_->alloc_pinned(sizeof(tsa_verify_unit) * vcap_, "verify table"));
+    vtab_dev_ = static_cast<tsa_verify_unit*>(dev_->alloc_device(sizeof(tsa_verify_unit) * vcap_, "verify table"));
+    vfail_host_ = static_cast<uint32_t*>(dev_->alloc_pinned(4ull * vcap_, "verify results"));
+    vfail_dev_ = static_cast<uint32_t*>(dev_->alloc_device(4ull * vcap_, "verify results"));
+    hip_check(hipMemset(vfail_dev_, 0, 4ull * vcap_), "hipMemset");
+  }
+  void landed(Stream s, uint32_t g, const uint32_t* keys, const int32_t* slots, uint32_t n) override {
+    (void)g;
+    if (!verify_ || n == 0) return;
+    require(vused_ + n <= vcap_, SS_E_BACKEND, "device verify: more landed units in a token than the table holds");
+    const uint32_t first = vused_;
+    for (uint32_t i = 0; i < n; ++i) {
+      tsa_verify_unit& v = vtab_host_[first + i];
+      std::memset(&v, 0, sizeof v);
+      for (uint32_t p = 0; p < x_.part_bytes.size(); ++p) {
+        v.ext[p].ptr = slot_ptr(p, slots[i]);
+        v.ext[p].bytes = x_.part_bytes[p];
+      }
+      v.n_ext = uint32_t(x_.part_bytes.size());
+      v.seg_first = uint64_t(i) * n_ckpt_;
+      v.states = ckpt_dev_ + uint64_t(keys[i]) * n_ckpt_ * 4;
+      v.digest = digests_[keys[i]];
+      v.total = x_.unit_bytes;
+      vkeys_.push_back(keys[i]);
+    }
+    vused_ += n;
+    copy_h2d(vtab_dev_ + first, vtab_host_ + first, sizeof(tsa_verify_unit) * n, s_[s]);
+    hip_check(hipError_t(launch_verify(vtab_dev_ + first, n, uint64_t(n) * n_ckpt_, kSegBytes, vfail_dev_ + first,
+                                       s_[s])),
+              "device verify launch");
+  }
+  // At the boundary (kDem / kPf synchronized): the keys whose landed bytes differ from their descriptor hash.
+  std::vector<uint32_t> collect_verify() {
+    std::vector<uint32_t> bad;
+    if (!verify_ || vused_ == 0) return bad;
+    hip_check(hipMemcpy(vfail_host_, vfail_dev_, 4ull * vused_, hipMemcpyDeviceToHost), "hipMemcpy (verify)");
+    for (uint32_t i = 0; i < vused_; ++i)
+      if (vfail_host_[i]) bad.push_back(vkeys_[i]);
+    hip_check(hipMemset(vfail_dev_, 0, 4ull * vused_), "hipMemset");
+    verified_ += vused_;
+    vused_ = 0;
+    vkeys_.clear();
+    return bad;
+  }
+  uint64_t verified() const { return verified_; }
+
+ private:
+  HipDevice* dev_;
+  const Layout& x_;
+  std::vector<void*> arena_;
+  int32_t* slot_of_;
+  uint32_t* ready_;
+  std::vector<void*> chunks_;
+  uint64_t per_chunk_;
+  uint32_t kJobRing;
+  hipStream_t s_[3] = {nullptr, nullptr, nullptr};
+  int32_t* stage_host_ = nullptr;
+  bool scatter_ = false;
+  void* stage_dev_[2] = {nullptr, nullptr};
+  tsa_scatter_job* jobs_host_[2] = {nullptr, nullptr};
+  tsa_scatter_job* jobs_dev_[2] = {nullptr, nullptr};
+  uint32_t job_next_[2] = {0, 0};
+  uint64_t scatter_blocks_ = 0;
+  bool verify_ = false;
+  std::vector<uint64_t> digests_;
+  uint64_t* ckpt_dev_ = nullptr;
+  uint64_t n_ckpt_ = 0;
+  uint32_t vcap_ = 0, vused_ = 0;
+  tsa_verify_unit* vtab_host_ = nullptr;
+  tsa_verify_unit* vtab_dev_ = nullptr;
+  uint32_t* vfail_host_ = nullptr;
+  uint32_t* vfail_dev_ = nullptr;
+  std::vector<uint32_t> vkeys_;
+  uint64_t verified_ = 0;
+};
+
+// ---- the service thread ----------------------------------------------------------------------------------------------
+struct ServiceStop {};
+
+class Service {
+ public:
+  enum State : uint32_t { kIdle = 0, kServed = 1, kFailed = 2, kStopped = 3 };
+  Service(DgCore* core, const DgMappedHost& m, uint32_t max_ids, uint32_t timeout_ms, int device)
+      : core_(core), m_(m), max_ids_(max_ids), timeout_(std::chrono::milliseconds(timeout_ms)), device_(device) {
+    run_.assign(core_->gated(), 1);
+    run_next_.assign(core_->gated(), 1);
+    last_flag_.assign(core_->gated(), 0);
+    ids_.reserve(kDgMaxIds);
+    pred_.reserve(kDgMaxIds);
+  }
+  ~Service() { stop_join(); }
+  void start() {
+    const uint32_t seen = host_seq_.load(std::memory_order_acquire);
+    th_ = std::thread([this, seen] { run(seen); });
+  }
+  void begin(uint32_t seq, const std::vector<uint8_t>& run) {
+    std::copy(run.begin(), run.end(), run_next_.begin());
+    host_seq_.store(seq, std::memory_order_release);
+  }
+  State wait_terminal(uint32_t seq, Clock::time_point deadline) {
+    for (uint32_t spins = 0;; ++spins) {
+      const uint64_t t = term_.load(std::memory_order_acquire);
+      const State s = State(t >> 32);
+      if (s == kFailed || s == kStopped) return s;
+      if (s == kServed && uint32_t(t) == seq) return kServed;
+      if ((spins & 1023u) == 0 && Clock::now() > deadline) return kIdle;
+      _mm_pause();
+    }
+  }
+  void stop_join() {
+    stop_.store(true, std::memory_order_release);
+    if (m_.host_abort) store_release(m_.host_abort, 1);
+    if (th_.joinable()) th_.join();
+  }
+  std::string error() const {
+    std::lock_guard<std::mutex> lk(mu_);
+    return err_;
+  }
+
+ private:
+  void publish(State s, uint32_t seq) { term_.store(uint64_t(s) << 32 | seq, std::memory_order_release); }
+  void fail_with(const std::string& msg) {
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      if (err_.empty()) err_ = msg;
+    }
+    if (m_.host_abort) store_release(m_.host_abort, 1);  // every later wait of the token sees it
+  }
+  void wait_word(const uint32_t* w, uint32_t seq, const char* what, uint32_t g, bool strict, uint32_t last) {
+    const auto start = Clock::now();
+    for (uint32_t spins = 0;; ++spins) {
+      const uint32_t v = load_acquire(w);
+      if (v == seq) return;
+      if (strict && v != last)
+        fail(SS_E_BACKEND, std::string("device-gated: sequence desync: ") + what + " of gated layer " +
+                               std::to_string(g) + " holds " + std::to_string(v) + " while serving token " +
+                               std::to_string(seq));
+      if ((spins & 4095u) == 0) {
+        if (stop_.load(std::memory_order_acquire)) throw ServiceStop{};
+        if (Clock::now() - start > timeout_)
+          fail(SS_E_BACKEND, std::string("device-gated: ") + what + " of gated layer " + std::to_string(g) +
+                                 " never came (token " + std::to_string(seq) + ")");
+      }
+      _mm_pause();
+    }
+  }
+  void wait_began(uint32_t seq) {
+    for (uint32_t spins = 0;; ++spins) {
+      const uint32_t v = load_acquire(m_.began);
+      if (v == seq) return;
+      if (int32_t(v - seq) > 0)
+        fail(SS_E_BACKEND, "device-gated: sequence desync: a gated step began with seq " + std::to_string(v) +
+                               " while serving token " + std::to_string(seq) + " (a step ran outside ss_begin / ss_end)");
+      if ((spins & 1023u) == 0) {
+        if (stop_.load(std::memory_order_acquire)) throw ServiceStop{};
+        if (load_acquire(m_.host_abort)) throw ServiceStop{};
+      }
+      if (spins < 20000) _mm_pause();
+      else std::this_thread::yield();
+    }
+  }
+  void run(uint32_t seen) {
+    try {
+      hip_check(hipSetDevice(device_), "hipSetDevice (service)");
+    } catch (const std::exception& e) {
+      fail_with(e.what());
+      publish(kFailed, 0);
+      return;
+    }
+    for (;;) {
+      uint32_t seq = 0;
+      for (uint32_t spins = 0;; ++spins) {
+        seq = host_seq_.load(std::memory_order_acquire);
+        if (seq != seen) break;
+        if (stop_.load(std::memory_order_acquire)) {
+          publish(kStopped, seen);
+          return;
+        }
+        if (spins < 20000) _mm_pause();
+        else std::this_thread::yield();
+      }
+      seen = seq;
+      try {
+        serve_token(seq);
+      } catch (const ServiceStop&) {
+        publish(kStopped, seq);
+        return;
+      } catch (const std::exception& e) {
+        fail_with(e.what());
+        publish(kFailed, seq);
+        return;
+      }
+      publish(kServed, seq);
+    }
+  }
+  void serve_token(uint32_t seq) {
+    const uint32_t G = core_->gated();
+    std::copy(run_next_.begin(), run_next_.end(), run_.begin());
+    core_->begin_token(seq);
+    wait_began(seq);
+    auto next_run = [&](uint32_t g) {
+      uint32_t h = g + 1;
+      while (h < G && !run_[h]) ++h;
+      return h;
+    };
+    for (uint32_t g = 0; g < G; ++g) {
+      if (!run_[g]) continue;
+      const uint32_t nx = next_run(g);
+      wait_word(&m_.flag[g], seq, "export flag", g, true, last_flag_[g]);
+      last_flag_[g] = seq;
+      const DgRecord& r = m_.rec[g];
+      require(r.seq == seq, SS_E_BACKEND,
+              "device-gated: sequence desync: the record of gated layer " + std::to_string(g) + " is for token " +
+                  std::to_string(r.seq) + ", serving " + std::to_string(seq));
+      const uint32_t n = r.n_ids, n_pred = r.n_pred_promised;
+      require(n >= 1 && n <= max_ids_, SS_E_BACKEND,
+              "device-gated: gated layer " + std::to_string(g) + " exported " + std::to_string(n) + " ids");
+      require(n_pred <= kDgMaxIds && (n_pred == 0 || g + 1 < G), SS_E_BACKEND,
+              "device-gated: gated layer " + std::to_string(g) + " promised " + std::to_string(n_pred) +
+                  " predicted ids");
+      const uint64_t mask = uint64_t(r.mask_lo) | uint64_t(r.mask_hi) << 32;
+      ids_.assign(r.ids, r.ids + n);
+      core_->serve_demand(g, ids_.data(), n, mask);
+      core_->serve_use(g, ids_.data(), n, mask);
+      if (n_pred > 0 && run_[g + 1]) {
+        wait_word(&m_.pflag[g], seq, "prediction flag", g, false, 0);
+        const DgPredRecord& pr = m_.prec[g];
+        require(pr.n_pred == n_pred, SS_E_BACKEND,
+                "device-gated: gated layer " + std::to_string(g) + " predicted " + std::to_string(pr.n_pred) +
+                    " ids, its export promised " + std::to_string(n_pred));
+        pred_.assign(pr.pred, pr.pred + n_pred);
+        core_->serve_prediction(g + 1, pred_.data(), n_pred);
+      }
+      if (core_->deferred() && nx < G) core_->issue_writebacks(g);
+    }
+  }
+
+  DgCore* core_;
+  DgMappedHost m_;
+  uint32_t max_ids_;
+  std::chrono::milliseconds timeout_;
+  int device_;
+  std::vector<uint8_t> run_, run_next_;
+  std::vector<uint32_t> last_flag_;
+  std::vector<uint32_t> ids_, pred_;
+  std::atomic<uint32_t> host_seq_{0};
+  std::atomic<uint64_t> term_{0};
+  std::atomic<bool> stop_{false};
+  mutable std::mutex mu_;
+  std::string err_;
+  std::thread th_;
+};
+
+// ---- the context ------------------------------------------------------------------------------------------------------
+class HipDgCtx final : public DgCtx {
+ public:
+  HipDgCtx(const Desc& d, const Plan& p, const ss_options& o) : d_(d), o_(o), x_(make_layout(d, p, o)) {
+    try {
+      init();
+    } catch (...) {
+      release();
+      throw;
+    }
+  }
+  ~HipDgCtx() override { release(); }
+
+  bool poisoned() const override { return poisoned_; }
+  void poison() override { poisoned_ = true; }
+  int n_sources() const override { return int(files_.size()); }
+  bool source_direct(int i) const override { return files_[size_t(i)]->direct(); }
+
+  void begin(const uint32_t* rows, int n_layers) override {
+    require(!in_token_, SS_E_INVALID, "ss_begin: a gated token is already open (call ss_end)");
+    if (rows)
+      require(n_layers == int(d_.layers.size()), SS_E_INVALID, "ss_begin: rows_per_layer must cover every layer");
+    for (size_t g = 0; g < x_.gated.size(); ++g) run_[g] = !rows || rows[size_t(x_.gated[g])] != 0;
+    // no step ran outside a pair: every word still holds the last token's sequence
+    bool clean = load_acquire(m_.done) == seq_ && load_acquire(m_.began) == seq_;
+    for (size_t g = 0; clean && g < x_.gated.size(); ++g)
+      clean = int32_t(load_acquire(m_.flag + g) - seq_) <= 0 && int32_t(load_acquire(m_.pflag + g) - seq_) <= 0;
+    if (!clean) {
+      store_release(m_.host_abort, 1);
+      svc_->stop_join();
+      poisoned_ = true;
+      fail(SS_E_BACKEND, "device-gated: sequence desync at ss_begin: a gated step ran outside ss_begin / ss_end (done " +
+                             std::to_string(load_acquire(m_.done)) + ", began " +
+                             std::to_string(load_acquire(m_.began)) + ", last token " + std::to_string(seq_) +
+                             "; the context is poisoned)");
+    }
+    ++seq_;
+    in_token_ = true;
+    store_release(m_.host_seq, seq_);  // the begin kernel authorizes exactly this sequence
+    svc_->begin(seq_, run_);
+  }
+
+  void end() override {
+    require(in_token_, SS_E_INVALID, "ss_end: no gated token is open");
+    in_token_ = false;
+    const auto deadline = Clock::now() + std::chrono::milliseconds(uint64_t(o_.dg_wait_timeout_ms) + 5000);
+    // 1. the completion edge: the end kernel ran after every reader of the token
+    bool at = false;
+    for (uint32_t spins = 0;; ++spins) {
+      const uint32_t v = load_acquire(m_.done);
+      if (v == seq_) {
+        at = true;
+        break;
+      }
+      if (int32_t(v - seq_) > 0) break;
+      if ((spins & 1023u) == 0 && Clock::now() > deadline) break;
+      if (spins < 100000) _mm_pause();
+      else std::this_thread::yield();
+    }
+    const uint32_t began = load_acquire(m_.began);
+    if (!at || began != seq_) {
+      const std::string dev = device_error();
+      store_release(m_.host_abort, 1);
+      svc_->stop_join();
+      poisoned_ = true;
+      fail(SS_E_BACKEND, token_failure(dev, at ? "sequence desync at ss_end: another gated step ran in it"
+                                               : "the device did not finish it (no end kernel)"));
+    }
+    // 2. the service's terminal word for this token
+    if (svc_->wait_terminal(seq_, deadline) != Service::kServed) {
+      const std::string dev = device_error();
+      store_release(m_.host_abort, 1);
+      svc_->stop_join();
+      poisoned_ = true;
+      const std::string why = svc_->error();
+      fail(SS_E_BACKEND, token_failure(dev, "the service: " + (why.empty() ? std::string("it did not finish") : why)));
+    }
+    // 3. the device's error word
+    const std::string dev = device_error();
+    if (!dev.empty()) {
+      poisoned_ = true;
+      fail(SS_E_BACKEND, token_failure(dev, ""));
+    }
+    // 4. the boundary, then the device check of this token's landed units
+    core_->end_token();
+    const std::vector<uint32_t> bad = tr_->collect_verify();
+    if (!bad.empty()) {
+      verify_failures_ += bad.size();
+      poisoned_ = true;
+      const uint32_t g = core_->gated_of(bad[0]);
+      fail(SS_E_HASH, token_failure("", std::to_string(bad.size()) + " landed unit(s) differ from the descriptor hash "
+                                        "in HBM, first gated (" + std::to_string(g) + ", " +
+                                        std::to_string(bad[0] - core_->unit_base()[g]) + ")"));
+    }
+  }
+
+  ss_dg_device_view device_view() const override {
+    ss_dg_device_view v{};
+    v.struct_size = uint32_t(sizeof v);
+    v.protocol = SS_DG_PROTOCOL;
+    v.n_gated = uint32_t(x_.gated.size());
+    v.n_parts = uint32_t(x_.part_bytes.size());
+    v.guard_slot = x_.guard_slot;
+    v.slots = x_.slots;
+    v.slot_of = dw_.slot_of;
+    v.unit_base = dw_.unit_base;
+    v.abort = dw_.abort;
+    for (size_t p = 0; p < x_.part_bytes.size(); ++p) v.parts[p] = {arena_[p], x_.part_bytes[p], x_.part_bytes[p]};
+    v.absent_err = dw_.absent_err;
+    return v;
+  }
+  int gated_index(int layer) const override {
+    return layer < 0 || size_t(layer) >= x_.ordinal.size() ? -1 : x_.ordinal[size_t(layer)];
+  }
+  void check_g(int g, const char* fn) const {
+    require(g >= 0 && size_t(g) < x_.gated.size(), SS_E_INVALID, std::string(fn) + ": gated layer out of range");
+  }
+  void enqueue_begin(void* stream) override { launch_ck(dg_launch_begin(dw_, stream), "ss_dg_enqueue_begin"); }
+  void enqueue_export(int g, const int32_t* ids_dev, int n, int n_pred, void* stream) override {
+    check_g(g, "ss_dg_enqueue_export");
+    require(ids_dev && n >= 1 && uint32_t(n) <= x_.B, SS_E_INVALID, "ss_dg_enqueue_export: 1..dg_max_ids ids");
+    require(n_pred >= 0 && n_pred <= int(kDgMaxIds), SS_E_INVALID, "ss_dg_enqueue_export: n_pred 0..64");
+    launch_ck(dg_launch_export(dw_, uint32_t(g), ids_dev, uint32_t(n), uint32_t(n_pred), stream),
+              "ss_dg_enqueue_export");
+  }
+  void enqueue_predict(int g, const int32_t* ids_dev, int n, void* stream) override {
+    check_g(g, "ss_dg_enqueue_predict");
+    require(ids_dev && n >= 1 && n <= int(kDgMaxIds), SS_E_INVALID, "ss_dg_enqueue_predict: 1..64 ids");
+    launch_ck(dg_launch_predict(dw_, uint32_t(g), ids_dev, uint32_t(n), stream), "ss_dg_enqueue_predict");
+  }
+  void enqueue_wait(int g, void* stream) override {
+    check_g(g, "ss_dg_enqueue_wait");
+    launch_ck(dg_launch_wait(dw_, uint32_t(g), stream), "ss_dg_enqueue_wait");
+  }
+  void enqueue_end(void* stream) override { launch_ck(dg_launch_end(dw_, stream), "ss_dg_enqueue_end"); }
+
+  uint32_t residency(ss_dg_unit* out, uint32_t cap) override {
+    require(!in_token_, SS_E_INVALID, "ss_dg_residency: between tokens only");
+    const std::vector<uint32_t> r = core_->residency();
+    for (uint32_t i = 0; i < cap && i < r.size(); ++i) {
+      const uint32_t g = core_->gated_of(r[i]);
+      out[i] = {int32_t(g), int32_t(r[i] - core_->unit_base()[g])};
+    }
+    return uint32_t(r.size());
+  }
+  void set_budgets(uint32_t spare_target, uint32_t per_layer, uint32_t per_token) override {
+    require(!in_token_, SS_E_INVALID, "ss_dg_set_budgets: between tokens only");
+    require(spare_target <= x_.D, SS_E_INVALID, "ss_dg_set_budgets: spare target above the billed spares");
+    core_->set_spare_target(spare_target);
+    core_->set_prefetch_budget(per_layer, per_token);
+  }
+
+  ss_dg_stats stats() const override {
+    const DgCounts a = core_->counts();
+    const DgCounts& b = base_;
+    ss_dg_stats s{};
+    s.struct_size = uint32_t(sizeof s);
+#define TSA_D(f) s.f = a.f - b.f
+    TSA_D(tokens);
+    TSA_D(lookups);
+    TSA_D(misses);
+    TSA_D(covered);
+    TSA_D(fetched);
+    TSA_D(prefetched);
+    TSA_D(prefetch_used);
+    TSA_D(pred_invalid);
+    TSA_D(resurrected);
+    TSA_D(bank_serves);
+    TSA_D(collected_mid);
+    TSA_D(evicted);
+    TSA_D(evict_short);
+    TSA_D(writebacks_done);
+    TSA_D(stalled);
+    TSA_D(predicted);
+    TSA_D(predicted_true);
+    TSA_D(miss_layers);
+    TSA_D(covered_waits);
+    TSA_D(wb_deferred);
+    TSA_D(wb_cancelled);
+    TSA_D(wb_forced);
+    TSA_D(wb_boundary_flushed);
+    TSA_D(wb_issued_bytes);
+    TSA_D(wb_completed_bytes);
+    TSA_D(wb_cancelled_bytes);
+    TSA_D(wb_boundary_flushed_bytes);
+    TSA_D(wb_forced_wait_ns);
+    TSA_D(inclusive_kept);
+    TSA_D(inclusive_drops);
+#undef TSA_D
+    s.free_slots = core_->free_slots();
+    s.blocks = x_.blocks;
+    s.slots = x_.slots;
+    s.device_timeouts = load_acquire(m_.err_count);
+    s.wb_outstanding_bytes = core_->outstanding_bytes();
+    s.backed_units = core_->backed_units();
+    return s;
+  }
+  ss_layer_stats layer_stats(int layer) const override {
+    require(layer >= 0 && size_t(layer) < d_.layers.size(), SS_E_INVALID, "ss_stats_layer: layer out of range");
+    const int g = x_.ordinal[size_t(layer)];
+    if (g < 0) return ss_layer_stats{};
+    return to_layer(core_->layer_counts()[size_t(g)], base_l_[size_t(g)]);
+  }
+  ss_layer_stats total_stats() const override {
+    ss_layer_stats t{};
+    for (size_t g = 0; g < x_.gated.size(); ++g) {
+      const ss_layer_stats l = to_layer(core_->layer_counts()[g], base_l_[g]);
+      t.routed += l.routed;
+      t.hits += l.hits;
+      t.admitted += l.admitted;
+      t.transient += l.transient;
+      t.evicted += l.evicted;
+      t.spec_issued += l.spec_issued;
+      t.spec_used += l.spec_used;
+      t.spec_dropped += l.spec_dropped;
+      t.bytes_pinned += l.bytes_pinned;
+    }
+    return t;
+  }
+  ss_exclusive_stats exclusive_stats() const override {
+    const DgCounts& a = core_->counts();
+    ss_exclusive_stats x{};
+    x.struct_size = uint32_t(sizeof x);
+    x.writebacks = a.evicted - a.wb_cancelled - a.inclusive_drops;
+    x.writeback_bytes = x.writebacks * x_.unit_bytes;
+    x.promoted = a.fetched + a.prefetched;
+    x.free_blocks = core_->free_blocks();
+    return x;
+  }
+  void stats_reset() override {
+    if (in_token_) return;
+    base_ = core_->counts();
+    base_l_ = core_->layer_counts();
+  }
+  uint32_t host_table(int32_t* out, uint32_t cap) const override {
+    const std::vector<int32_t>& t = core_->table();
+    for (uint32_t i = 0; i < cap && i < t.size(); ++i) out[i] = t[i];
+    return uint32_t(t.size());
+  }
+  uint64_t verify_failures() const override { return verify_failures_; }
+
+ private:
+  static void launch_ck(int e, const char* what) { hip_check(hipError_t(e), what); }
+  ss_layer_stats to_layer(const DgLayerCounts& a, const DgLayerCounts& b) const {
+    ss_layer_stats l{};
+    l.routed = a.lookups - b.lookups;
+    l.hits = l.routed - (a.misses - b.misses);
+    l.transient = a.bank_serves - b.bank_serves;
+    l.admitted = (a.fetched - b.fetched) - l.transient;
+    l.evicted = a.evicted - b.evicted;
+    l.spec_issued = a.prefetched - b.prefetched;
+    l.spec_used = a.prefetch_used - b.prefetch_used;
+    l.spec_dropped = l.spec_issued >= l.spec_used ? l.spec_issued - l.spec_used : 0;
+    l.bytes_pinned = ((a.fetched - b.fetched) + (a.prefetched - b.prefetched)) * x_.unit_bytes;
+    return l;
+  }
+  std::string device_error() const {
+    const uint32_t code = load_acquire(m_.err_code), aux = load_acquire(m_.err_aux);
+    if (code == kDgOk) return std::string();
+    const char* what = code == kDgTimeout ? "a wait timed out" : code == kDgBadId ? "an exported id was out of range"
+                       : code == kDgHostAbort ? "the host aborted the token"
+                       : code == kDgDesync ? "a step the host did not authorize"
+                       : code == kDgAbsent ? "a slot lookup met an absent entry" : "unknown device error";
+    return std::string(what) + (code == kDgDesync ? " (seq " : code == kDgAbsent ? "" : " (gated layer ") +
+           (code == kDgAbsent ? std::string() : std::to_string(aux) + ")");
+  }
+  std::string token_failure(const std::string& device, const std::string& host) const {
+    std::string m = "device-gated: token " + std::to_string(seq_) + ": ";
+    if (!device.empty()) m += "the device: " + device + (host.empty() ? "" : "; ");
+    return m + host + " (the context is poisoned, the token's outputs must be discarded)";
+  }
+
+  void init();
+  void fill();
+  void release() noexcept;
+
+  Desc d_;
+  ss_options o_;
+  Layout x_;
+  std::unique_ptr<HipDevice> dev_;
+  std::vector<std::unique_ptr<SourceFile>> files_;
+  std::vector<void*> arena_;
+  int32_t* slot_of_dev_ = nullptr;
+  char* ctl_dev_ = nullptr;
+  void* mapped_host_ = nullptr;
+  void* mapped_dev_ = nullptr;
+  std::vector<void*> block_chunks_;
+  uint64_t per_chunk_ = 1;
+  uint64_t* ckpt_dev_ = nullptr;
+  DgDevWords dw_;
+  DgMappedHost m_;
+  std::unique_ptr<HipTransport> tr_;
+  std::unique_ptr<DgCore> core_;
+  std::unique_ptr<Service> svc_;
+  std::vector<uint8_t> run_;
+  uint32_t seq_ = 0;
+  bool in_token_ = false, poisoned_ = false;
+  DgCounts base_;
+  std::vector<DgLayerCounts> base_l_;
+  uint64_t verify_failures_ = 0;
+};
+
+void HipDgCtx::init() {
+  dev_ = std::make_unique<HipDevice>(o_.device);
+  for (const auto& s : d_.sources) files_.push_back(std::make_unique<SourceFile>(s.path, o_.direct_io != 0));
+  const uint32_t G = uint32_t(x_.gated.size());
+  // the arena: one HBM array per part, the guard slot zeroed
+  for (uint64_t pb : x_.part_bytes) {
+    arena_.push_back(dev_->alloc_device(uint64_t(x_.slots) * pb, "device-gated arena"));
+    hip_check(hipMemset(static_cast<char*>(arena_.back()) + uint64_t(x_.guard_slot) * pb, 0, pb), "hipMemset (guard)");
+  }
+  slot_of_dev_ = static_cast<int32_t*>(dev_->alloc_device(4ull * x_.keys, "slot table"));
+  // HBM control words: seq, abort, err_count, err_code, err_aux, absent_err | any_miss[G] | ready[G] | unit_base[G+1]
+  // | stamps[4G]
+  const uint64_t o_any = 64, o_ready = align64(o_any + 4ull * G), o_base = align64(o_ready + 4ull * G),
+                 o_stamps = align64(o_base + 4ull * (G + 1)), ctl_bytes = align64(o_stamps + 32ull * G);
+  ctl_dev_ = static_cast<char*>(dev_->alloc_device(ctl_bytes, "device-gated control words"));
+  hip_check(hipMemset(ctl_dev_, 0, ctl_bytes), "hipMemset (control words)");
+  hip_check(hipMemcpy(ctl_dev_ + o_base, x_.unit_base.data(), 4ull * (G + 1), hipMemcpyHostToDevice),
+            "hipMemcpy (unit_base)");
+  uint32_t* w = reinterpret_cast<uint32_t*>(ctl_dev_);
+  dw_.seq = w + 0;
+  dw_.abort = w + 1;
+  dw_.err_count = w + 2;
+  dw_.err_code = w + 3;
+  dw_.err_aux = w + 4;
+  dw_.absent_err = w + 5;
+  dw_.any_miss = reinterpret_cast<uint32_t*>(ctl_dev_ + o_any);
+  dw_.ready = reinterpret_cast<uint32_t*>(ctl_dev_ + o_ready);
+  dw_.unit_base = reinterpret_cast<const uint32_t*>(ctl_dev_ + o_base);
+  dw_.stamps = reinterpret_cast<uint64_t*>(ctl_dev_ + o_stamps);
+  dw_.slot_of = slot_of_dev_;
+  dw_.timeout_ticks = uint64_t(o_.dg_wait_timeout_ms) * 100000ull;  // wall clock: 100 MHz
+  // the fine-grained control area (device writes, host polls; host writes, device reads)
+  const MappedLayout ml = mapped_layout(G);
+  mapped_host_ = dev_->alloc_mapped(ml.total, &mapped_dev_, "device-gated control area");
+  char* h = static_cast<char*>(mapped_host_);
+  char* dv = static_cast<char*>(mapped_dev_);
+  m_.rec = reinterpret_cast<DgRecord*>(h + ml.rec);
+  m_.prec = reinterpret_cast<DgPredRecord*>(h + ml.prec);
+  m_.flag = reinterpret_cast<uint32_t*>(h + ml.flag);
+  m_.pflag = reinterpret_cast<uint32_t*>(h + ml.pflag);
+  uint32_t* hw = reinterpret_cast<uint32_t*>(h + ml.words);
+  m_.done = hw + 0;
+  m_.err_code = hw + 1;
+  m_.err_aux = hw + 2;
+  m_.err_count = hw + 3;
+  m_.host_abort = hw + 4;
+  m_.host_seq = hw + 5;
+  m_.began = hw + 6;
+  dw_.rec = reinterpret_cast<DgRecord*>(dv + ml.rec);
+  dw_.prec = reinterpret_cast<DgPredRecord*>(dv + ml.prec);
+  dw_.flag = reinterpret_cast<uint32_t*>(dv + ml.flag);
+  dw_.pflag = reinterpret_cast<uint32_t*>(dv + ml.pflag);
+  uint32_t* dvw = reinterpret_cast<uint32_t*>(dv + ml.words);
+  dw_.done = dvw + 0;
+  dw_.m_err_code = dvw + 1;
+  dw_.m_err_aux = dvw + 2;
+  dw_.m_err_count = dvw + 3;
+  dw_.host_abort = dvw + 4;
+  dw_.host_seq = dvw + 5;
+  dw_.began = dvw + 6;
+  // pinned blocks: P + Q of one host stride each, in chunks of at most 1 GiB (a larger block alone)
+  per_chunk_ = std::max<uint64_t>(1, kPinnedChunk / x_.host_stride);
+  for (uint64_t left = x_.blocks; left > 0;) {
+    const uint64_t n = std::min(per_chunk_, left);
+    block_chunks_.push_back(dev_->alloc_pinned(n * x_.host_stride, "pinned blocks"));
+    left -= n;
+  }
+  tr_ = std::make_unique<HipTransport>(dev_.get(), x_, arena_, slot_of_dev_, dw_.ready, block_chunks_, per_chunk_,
+                                       G * x_.B + o_.dg_prefetch_per_token + x_.D);
+  DgConfig c;
+  for (int L : x_.gated) c.n_units.push_back(uint32_t(d_.layers[size_t(L)].n_units));
+  c.persistent_slots = x_.persistent_slots;
+  c.bank_slots = x_.B;
+  c.blocks = x_.blocks;
+  const uint32_t T = o_.dg_spare_target == 0xFFFFFFFFu ? x_.D : o_.dg_spare_target;
+  require(T <= x_.D, SS_E_INVALID,
+          "device-gated: dg_spare_target " + std::to_string(T) + " above the billed spares (" + std::to_string(x_.D) + ")");
+  c.spare_target = T;
+  c.prefetch_reserve_auto = o_.dg_prefetch_reserve == 0xFFFFFFFFu;
+  c.prefetch_reserve = c.prefetch_reserve_auto ? std::min<uint32_t>(24, T / 4) : o_.dg_prefetch_reserve;
+  c.prefetch_per_layer = o_.dg_prefetch_per_layer;
+  c.prefetch_per_token = o_.dg_prefetch_per_token;
+  c.wb_defer = o_.dg_wb_defer != 0;
+  c.wb_on_d2h = o_.dg_wb_stream == 1;
+  c.wb_layer_bytes = o_.dg_wb_layer_bytes;
+  c.wb_max_outstanding = o_.dg_wb_max_outstanding;
+  c.inclusive = x_.I;
+  core_ = std::make_unique<DgCore>(c, tr_.get());
+  // priority: the seed (validated), the plan's residents, then key order
+  std::vector<uint32_t> order;
+  for (uint32_t i = 0; i < o_.dg_seed_n; ++i) {
+    require(o_.dg_seed != nullptr, SS_E_INVALID, "device-gated: dg_seed_n > 0 with a null dg_seed");
+    const ss_dg_unit& e = o_.dg_seed[i];
+    require(e.gated >= 0 && uint32_t(e.gated) < G && e.unit >= 0 &&
+                uint32_t(e.unit) < core_->units(uint32_t(e.gated)),
+            SS_E_INVALID, "device-gated: dg_seed entry " + std::to_string(i) + " is out of range");
+    order.push_back(core_->key(uint32_t(e.gated), uint32_t(e.unit)));
+  }
+  o_.dg_seed = nullptr;
+  o_.dg_seed_n = 0;
+  order.insert(order.end(), x_.residents.begin(), x_.residents.end());
+  for (uint32_t k = 0; k < x_.keys; ++k) order.push_back(k);
+  core_->place(order);
+  fill();
+  tr_->upload_table(core_->table().data(), x_.keys);
+  core_->check();
+  run_.assign(G, 1);
+  base_l_.assign(G, DgLayerCounts{});
+  svc_ = std::make_unique<Service>(core_.get(), m_, x_.B, o_.dg_wait_timeout_ms, o_.device);
+  svc_->start();
+}
+
+// Open-time fill, in parallel: every key from its file into its home (a pinned block, or through a per-thread pinned
+// staging buffer into its arena slot). With verify_hash the unit's XXH64 is checked against the descriptor; with
+// verify_hash = 2 its checkpoints are kept in HBM for the device check of every later landing.
+void HipDgCtx::fill() {
+  const uint32_t G = uint32_t(x_.gated.size());
+  std::vector<uint64_t> digests(x_.keys, 0);
+  bool have_hash = true;
+  for (int L : x_.gated) have_hash = have_hash && !d_.layers[size_t(L)].hash.empty();
+  const bool dverify = o_.verify_hash == 2 && have_hash;
+  uint64_t n_ckpt = 0;
+  std::vector<uint64_t> ckpt_host;
+  if (dverify) {
+    n_ckpt = tsa_checkpoint_count(x_.part_bytes.data(), uint32_t(x_.part_bytes.size()), kSegBytes);
+    ckpt_dev_ = static_cast<uint64_t*>(dev_->alloc_device(uint64_t(x_.keys) * n_ckpt * 32, "verify checkpoints"));
+    ckpt_host.assign(size_t(uint64_t(x_.keys) * n_ckpt * 4), 0);
+  }
+  const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+  const unsigned nthreads = std::min<unsigned>(16, std::max<unsigned>(1, std::min<unsigned>(hw, x_.keys)));
+  std::atomic<uint32_t> next{0};
+  std::mutex err_mu;
+  std::string err;
+  ss_status err_st = SS_OK;
+  auto work = [&]() {
+    void* stage = nullptr;
+    hipStream_t st = nullptr;
+    try {
+      dev_->bind();
+      stage = dev_->alloc_pinned(x_.host_stride, "fill staging");
+      st = dev_->stream_create();
+      for (;;) {
+        const uint32_t k = next.fetch_add(1);
+        if (k >= x_.keys) break;
+        {
+          std::lock_guard<std::mutex> lk(err_mu);
+          if (err_st != SS_OK) break;
+        }
+        const uint32_t g = core_->gated_of(k);
+        const int L = x_.gated[g];
+        const int u = int(k - x_.unit_base[g]);
+        const Layer& l = d_.layers[size_t(L)];
+        const bool on_dev = core_->home(k) == DgCore::Home::Device;
+        char* dst = on_dev ? static_cast<char*>(stage) : tr_->block_ptr(core_->block_of(k));
+        for (size_t p = 0; p < l.parts.size(); ++p) {
+          const Part& part = l.parts[p];
+          const SourceFile& f = *files_[size_t(part.source)];
+          const uint64_t F = part.offset + uint64_t(u) * part.stride;
+          require(F + part.bytes <= f.size(), SS_E_IO,
+                  "unit (" + std::to_string(L) + ", " + std::to_string(u) + ") is past the end of its source");
+          const uint64_t al = std::max<uint64_t>(d_.sources[size_t(part.source)].align, 512);
+          if (!f.direct() || (F % al == 0 && part.bytes % al == 0 && x_.part_offset[p] % al == 0)) {
+            f.pread_all(dst + x_.part_offset[p], part.bytes, F);
+          } else {  // a buffered read of an unaligned range
+            SourceFile bf(f.path(), false);
+            bf.pread_all(dst + x_.part_offset[p], part.bytes, F);
+          }
+        }
+        if (o_.verify_hash && !l.hash.empty()) {
+          tsa_unit hu{};
+          for (size_t p = 0; p < x_.part_bytes.size(); ++p) {
+            hu.ext[p].ptr = dst + x_.part_offset[p];
+            hu.ext[p].bytes = x_.part_bytes[p];
+          }
+          hu.n_ext = uint32_t(x_.part_bytes.size());
+          uint64_t dig = 0;
+          if (dverify) {
+            const ss_status s = tsa_xxh64_checkpoints(&hu, kSegBytes, ckpt_host.data() + uint64_t(k) * n_ckpt * 4,
+                                                      n_ckpt, &dig);
+            require(s == SS_OK, s, "device-gated: checkpoints of a unit");
+          } else {
+            dig = xxh64(dst, size_t(x_.unit_bytes));
+          }
+          digests[k] = l.hash[size_t(u)];
+          require(dig == l.hash[size_t(u)], SS_E_HASH,
+                  "unit (" + std::to_string(L) + ", " + std::to_string(u) + ") bytes differ from the descriptor hash");
+        }
+        if (on_dev) {
+          const int32_t slot = core_->slot_of(k);
+          for (size_t p = 0; p < x_.part_bytes.size(); ++p)
+            copy_h2d(static_cast<char*>(arena_[p]) + uint64_t(slot) * x_.part_bytes[p], dst + x_.part_offset[p],
+                     x_.part_bytes[p], st);
+          stream_sync(st);
+        }
+      }
+    } catch (const Error& e) {
+      std::lock_guard<std::mutex> lk(err_mu);
+      if (err_st == SS_OK) {
+        err_st = e.status();
+        err = e.what();
+      }
+    } catch (const std::exception& e) {
+      std::lock_guard<std::mutex> lk(err_mu);
+      if (err_st == SS_OK) {
+        err_st = SS_E_BACKEND;
+        err = e.what();
+      }
+    }
+    if (st) dev_->stream_destroy(st);
+    dev_->free_pinned(stage);
+  };
+  std::vector<std::thread> th;
+  for (unsigned i = 0; i < nthreads; ++i) th.emplace_back(work);
+  for (auto& t : th) t.join();
+  if (err_st != SS_OK) fail(err_st, err);
+  if (dverify) {
+    hip_check(hipMemcpy(ckpt_dev_, ckpt_host.data(), ckpt_host.size() * 8, hipMemcpyHostToDevice),
+              "hipMemcpy (checkpoints)");
+    tr_->enable_verify(digests, ckpt_dev_, n_ckpt, G * x_.B + o_.dg_prefetch_per_token + 64);
+  }
+  (void)G;
+}
+
+void HipDgCtx::release() noexcept {
+  if (svc_) svc_->stop_join();
+  if (dev_) (void)hipDeviceSynchronize();
+  svc_.reset();
+  core_.reset();
+  tr_.reset();
+  if (!dev_) return;
+  for (void* a : arena_) dev_->free_device(a);
+  dev_->free_device(slot_of_dev_);
+  dev_->free_device(ctl_dev_);
+  dev_->free_device(ckpt_dev_);
+  dev_->free_pinned(mapped_host_);
+  for (void* c : block_chunks_) dev_->free_pinned(c);
+  arena_.clear();
+  block_chunks_.clear();
+  dev_.reset();
+}
+
+}  // namespace
+
+std::unique_ptr<DgCtx> open_dg_ctx(const Desc& d, const Plan& p, const ss_options& o) {
+  require(o.forward_mode == SS_FORWARD_DEVICE_GATED, SS_E_INVALID,
+          "device-gated: forward_mode is not SS_FORWARD_DEVICE_GATED");
+  return std::make_unique<HipDgCtx>(d, p, o);
+}
+
+}  // namespace tsa

@@ -1,0 +1,42 @@
+// The device-gated decode context (SS_FORWARD_DEVICE_GATED) on one MI355X: the open-time layout and refusals
+// (reference src/dg_layout.cpp:182-446, two-tier subset), the HBM arena (one array per part, slots = R + D + 2B + 1,
+// the last one the zeroed guard), the fine-grained control area, the HIP transport, the service thread
+// (reference src/dg_service.cpp:269-365) and the begin / end protocol (reference src/dg_ctx.cpp:429-567).
+#pragma once
+
+#include <memory>
+
+#include "model.hpp"
+
+namespace tsa {
+
+class DgCtx {
+ public:
+  virtual ~DgCtx() = default;
+  virtual bool poisoned() const = 0;
+  virtual void poison() = 0;
+  virtual int n_sources() const = 0;
+  virtual bool source_direct(int i) const = 0;
+  virtual void begin(const uint32_t* rows, int n_layers) = 0;
+  virtual void end() = 0;
+  virtual ss_dg_device_view device_view() const = 0;
+  virtual int gated_index(int layer) const = 0;
+  virtual void enqueue_begin(void* stream) = 0;
+  virtual void enqueue_export(int g, const int32_t* ids_dev, int n, int n_pred, void* stream) = 0;
+  virtual void enqueue_predict(int g, const int32_t* ids_dev, int n, void* stream) = 0;
+  virtual void enqueue_wait(int g, void* stream) = 0;
+  virtual void enqueue_end(void* stream) = 0;
+  virtual uint32_t residency(ss_dg_unit* out, uint32_t cap) = 0;
+  virtual void set_budgets(uint32_t spare_target, uint32_t per_layer, uint32_t per_token) = 0;
+  virtual ss_dg_stats stats() const = 0;
+  virtual ss_layer_stats layer_stats(int layer) const = 0;
+  virtual ss_layer_stats total_stats() const = 0;
+  virtual ss_exclusive_stats exclusive_stats() const = 0;
+  virtual void stats_reset() = 0;
+  virtual uint32_t host_table(int32_t* out, uint32_t cap) const = 0;
+  virtual uint64_t verify_failures() const = 0;
+};
+
+std::unique_ptr<DgCtx> open_dg_ctx(const Desc& d, const Plan& p, const ss_options& o);
+
+}  // namespace tsa

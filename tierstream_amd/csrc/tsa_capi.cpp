@@ -70,6 +70,11 @@ ss_status tsa_xxh64_digest(const tsa_unit* units_dev, uint32_t n, uint64_t* dige
   });
 }
 
+uint64_t tsa_xxh64_host(const void* data, uint64_t bytes) {
+  if (!data && bytes) return 0;
+  return xxh64(data, size_t(bytes));
+}
+
 uint64_t tsa_checkpoint_count(const uint64_t* extent_bytes, uint32_t n_ext, uint64_t seg_bytes) {
   if (!extent_bytes || n_ext == 0 || n_ext > TSA_MAX_EXTENTS || seg_bytes == 0 || seg_bytes % 32) return 0;
   return count_checkpoints(extent_bytes, n_ext, seg_bytes);

@@ -1,0 +1,293 @@
+// The synthetic engine the tests and the benchmark drive libtierstream_amd with (not part of the product): what an
+// inference engine does around the serve path, with the model math replaced by a checksum of every routed unit's
+// bytes read through the library's tables. The checksum kernels read HBM like a batch-1 MoE layer reads its experts
+// (every byte of every routed unit once), so in the benchmark they stand in for the expert compute.
+//
+// Checksum of a unit: sum over its little-endian 32-bit words w_j of w_j * ((j mod 251) + 1), mod 2^64 (words counted
+// from the unit's first byte, across its parts; a unit's bytes are a multiple of 4 in every workload here).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "strix_stream/ss.h"
+#include "tierstream_amd/tsa_test.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr uint64_t kChunk = 256 * 1024;  // bytes per workgroup
+
+__device__ __forceinline__ uint64_t sum_words(const uint32_t* p, uint64_t first_word, uint64_t n_words) {
+  uint64_t s = 0;
+  for (uint64_t j = threadIdx.x; j < n_words; j += kThreads) {
+    const uint64_t w = __builtin_nontemporal_load(p + j);
+    s += w * ((first_word + j) % 251 + 1);
+  }
+  return s;
+}
+
+__device__ __forceinline__ void block_add(uint64_t s, unsigned long long* out) {
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
+  __shared__ uint64_t part[kThreads / 64];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t t = 0;
+    for (int w = 0; w < kThreads / 64; ++w) t += part[w];
+    atomicAdd(out, (unsigned long long)t);
+  }
+}
+
+// Host contract: blockIdx.y = routed unit i (its table entry table_dev[ids[i]]); blockIdx.x = a chunk of its bytes.
+__global__ __launch_bounds__(kThreads) void checksum_table(const uint64_t* table_dev, const int32_t* ids, uint64_t bytes,
+                                                           unsigned long long* out) {
+  const int32_t u = ids[blockIdx.y];
+  const uint64_t a = table_dev[u];
+  const uint64_t off = uint64_t(blockIdx.x) * kChunk;
+  if (a == 0 || off >= bytes) return;
+  const uint64_t n = (bytes - off < kChunk ? bytes - off : kChunk) / 4;
+  block_add(sum_words(reinterpret_cast<const uint32_t*>(a + off), off / 4, n), out + blockIdx.y);
+}
+
+// Device-gated: the slot from ss_dg_slot, then each part at base + slot * stride.
+__global__ __launch_bounds__(kThreads) void checksum_dg(ss_dg_device_view v, uint32_t g, const int32_t* ids,
+                                                        unsigned long long* out) {
+  __shared__ int32_t slot_s;
+  if (threadIdx.x == 0) slot_s = ss_dg_slot(&v, g, ids[blockIdx.y]);
+  __syncthreads();
+  const int32_t slot = slot_s;
+  uint64_t b = blockIdx.x, word0 = 0;
+  for (uint32_t p = 0; p < v.n_parts; ++p) {  // chunk b of the unit: each part has its own whole chunks
+    const uint64_t pb = v.parts[p].bytes, nb = (pb + kChunk - 1) / kChunk;
+    if (b < nb) {
+      const uint64_t off = b * kChunk;
+      const uint64_t n = (pb - off < kChunk ? pb - off : kChunk) / 4;
+      const uint32_t* base = reinterpret_cast<const uint32_t*>(static_cast<const char*>(v.parts[p].base) +
+                                                               uint64_t(slot) * v.parts[p].stride + off);
+      block_add(sum_words(base, word0 + off / 4, n), out + blockIdx.y);
+      return;
+    }
+    b -= nb;
+    word0 += pb / 4;
+  }
+}
+
+ss_status ck(hipError_t e) { return e == hipSuccess ? SS_OK : SS_E_BACKEND; }
+#define TSE_CK(x)                                          \
+  do {                                                     \
+    const ss_status s_ = (x);                              \
+    if (s_ != SS_OK) return s_;                            \
+  } while (0)
+#define TSE_HIP(x) TSE_CK(ck(x))
+
+uint32_t chunks_of(uint64_t bytes) { return uint32_t((bytes + kChunk - 1) / kChunk); }
+
+double ms_since(std::chrono::steady_clock::time_point t) {
+  return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t).count();
+}
+
+}  // namespace
+
+extern "C" {
+
+// Host contract: `steps` forwards over every layer with units. routes[step][layer][max_ids] (-1 = none);
+// mode 0 = ss_layer_routes + ss_acquire, 1 = ss_layer_all + ss_acquire, 2 = ss_layer_routes + ss_acquire_groups with
+// one ss_group_wait per group. Outputs (may be NULL): checksums[step][layer][max_ids] of the routed ids (0 for -1),
+// tables[step][layer][max_units] = the layer's table_host, stats[step] = the forward's totals, step_ms[step].
+__attribute__((visibility("default"))) ss_status tse_host_run(ss_ctx* c, const ss_desc* d, int steps,
+                                                              const int32_t* routes, int max_ids, int max_units,
+                                                              int mode, uint64_t* checksums, uint64_t* tables,
+                                                              ss_layer_stats* stats, double* step_ms) {
+  const int L = ss_desc_n_layers(d);
+  hipStream_t s = nullptr;
+  TSE_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  int32_t* ids_dev = nullptr;
+  unsigned long long* out_dev = nullptr;
+  std::vector<unsigned long long> out_host(size_t(max_ids));
+  ss_status st = SS_OK;
+  if (hipMalloc(&ids_dev, 4ull * max_ids * L) != hipSuccess || hipMalloc(&out_dev, 8ull * max_ids * L) != hipSuccess)
+    st = SS_E_NOMEM;
+  for (int step = 0; st == SS_OK && step < steps; ++step) {
+    const auto t0 = std::chrono::steady_clock::now();
+    ss_layer_stats before{};
+    ss_stats_total(c, &before);
+    if ((st = ss_begin(c, nullptr, 0)) != SS_OK) break;
+    if ((st = ck(hipMemsetAsync(out_dev, 0, 8ull * max_ids * L, s))) != SS_OK) break;
+    for (int l = 0; st == SS_OK && l < L; ++l) {
+      const int nu = ss_desc_layer_units(d, l);
+      if (nu <= 0) continue;
+      const int32_t* r = routes + (size_t(step) * L + l) * max_ids;
+      int n = 0;
+      while (n < max_ids && r[n] >= 0) ++n;
+      if (mode == 1) st = ss_layer_all(c, l);
+      else st = ss_layer_routes(c, l, r, n);
+      if (st != SS_OK) break;
+      ss_layer_view v{};
+      st = mode == 2 ? ss_acquire_groups(c, l, s, &v) : ss_acquire(c, l, s, &v);
+      if (st != SS_OK) break;
+      if (mode == 2)
+        for (int gi = 1; st == SS_OK && gi < v.n_groups; ++gi) st = ss_group_wait(c, l, gi, s);
+      if (st != SS_OK) break;
+      const int n_read = mode == 1 ? nu : n;
+      std::vector<int32_t> rid(size_t(std::max(n_read, 1)));
+      for (int i = 0; i < n_read; ++i) rid[size_t(i)] = mode == 1 ? i : r[i];
+      if (n_read > 0) {
+        st = ck(hipMemcpyAsync(ids_dev + size_t(l) * max_ids, rid.data(), 4ull * n_read, hipMemcpyHostToDevice, s));
+        if (st == SS_OK) {
+          hipLaunchKernelGGL(checksum_table, dim3(chunks_of(ss_desc_unit_bytes(d, l)), n_read), dim3(kThreads), 0, s,
+                             v.table_dev, ids_dev + size_t(l) * max_ids, ss_desc_unit_bytes(d, l),
+                             out_dev + size_t(l) * max_ids);
+          st = ck(hipGetLastError());
+        }
+        if (st == SS_OK) st = ck(hipStreamSynchronize(s));  // (the rid buffer is pageable: the copy must finish)
+      }
+      if (st == SS_OK && tables)
+        std::memcpy(tables + (size_t(step) * L + l) * max_units, v.table_host, 8ull * std::min(nu, max_units));
+      if (st == SS_OK) st = ss_release(c, l, s);
+    }
+    if (st == SS_OK) st = ck(hipStreamSynchronize(s));
+    const ss_status end_st = ss_end(c);
+    if (st == SS_OK) st = end_st;
+    if (st != SS_OK) break;
+    if (step_ms) step_ms[step] = ms_since(t0);
+    if (stats) {
+      ss_layer_stats after{};
+      ss_stats_total(c, &after);
+      ss_layer_stats& o = stats[step];
+      o = after;
+      o.routed -= before.routed, o.hits -= before.hits, o.admitted -= before.admitted;
+      o.transient -= before.transient, o.evicted -= before.evicted, o.prefetched -= before.prefetched;
+      o.spec_issued -= before.spec_issued, o.spec_used -= before.spec_used, o.spec_dropped -= before.spec_dropped;
+      o.bytes_pinned -= before.bytes_pinned, o.bytes_disk -= before.bytes_disk, o.wait_ns -= before.wait_ns;
+    }
+    if (checksums) {
+      std::vector<unsigned long long> all(size_t(max_ids) * L);
+      if ((st = ck(hipMemcpy(all.data(), out_dev, 8ull * max_ids * L, hipMemcpyDeviceToHost))) != SS_OK) break;
+      std::memcpy(checksums + size_t(step) * L * max_ids, all.data(), 8ull * max_ids * L);
+    }
+  }
+  (void)hipStreamSynchronize(s);
+  (void)hipFree(ids_dev);
+  (void)hipFree(out_dev);
+  (void)hipStreamDestroy(s);
+  return st;
+}
+
+// ---- device-gated ----
+struct TseDg {
+  ss_ctx* c = nullptr;
+  uint32_t G = 0, n_ids = 0, max_chunks = 0;
+  bool checksum = true, dg = true;
+  hipStream_t s = nullptr;
+  int32_t* ids_dev = nullptr;               // [G][64]
+  unsigned long long* out_dev = nullptr;    // [G][64]
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  ss_dg_device_view view{};
+};
+
+static ss_status tse_enqueue_token(TseDg* e) {
+  if (e->dg) TSE_CK(ss_dg_enqueue_begin(e->c, e->s));
+  for (uint32_t g = 0; g < e->G; ++g) {
+    if (e->dg) TSE_CK(ss_dg_enqueue_export(e->c, int(g), e->ids_dev + 64 * g, int(e->n_ids), 0, e->s));
+    if (e->dg) TSE_CK(ss_dg_enqueue_wait(e->c, int(g), e->s));
+    if (e->checksum) {
+      hipLaunchKernelGGL(checksum_dg, dim3(e->max_chunks, e->n_ids), dim3(kThreads), 0, e->s, e->view, g,
+                         e->ids_dev + 64 * g, e->out_dev + 64 * g);
+      TSE_HIP(hipGetLastError());
+    }
+  }
+  if (e->dg) TSE_CK(ss_dg_enqueue_end(e->c, e->s));
+  return SS_OK;
+}
+
+// A device-gated engine: n_ids routed ids per gated layer per token, captured once into a hipGraph (use_graph = 1) or
+// enqueued per token. checksum = 0 leaves out the checksum kernels; dg = 0 leaves out the gating kernels (a baseline
+// graph for the wait overhead: the same checksum kernels, nothing gated).
+__attribute__((visibility("default"))) ss_status tse_dg_create(ss_ctx* c, uint32_t n_ids, int use_graph, int checksum,
+                                                               int dg, void** out) {
+  auto* e = new TseDg;
+  e->c = c;
+  e->n_ids = n_ids;
+  e->checksum = checksum != 0;
+  e->dg = dg != 0;
+  ss_status st = ss_dg_get_device_view(c, &e->view);
+  if (st != SS_OK) {
+    delete e;
+    return st;
+  }
+  e->G = e->view.n_gated;
+  uint64_t unit = 0;
+  for (uint32_t p = 0; p < e->view.n_parts; ++p) unit += e->view.parts[p].bytes;
+  uint32_t chunks = 0;
+  for (uint32_t p = 0; p < e->view.n_parts; ++p) chunks += chunks_of(e->view.parts[p].bytes);
+  e->max_chunks = chunks;
+  if (hipStreamCreateWithFlags(&e->s, hipStreamNonBlocking) != hipSuccess ||
+      hipMalloc(&e->ids_dev, 4ull * 64 * e->G) != hipSuccess || hipMalloc(&e->out_dev, 8ull * 64 * e->G) != hipSuccess) {
+    delete e;
+    return SS_E_NOMEM;
+  }
+  (void)hipMemset(e->out_dev, 0, 8ull * 64 * e->G);
+  (void)hipMemset(e->ids_dev, 0, 4ull * 64 * e->G);
+  if (use_graph) {
+    st = ck(hipStreamBeginCapture(e->s, hipStreamCaptureModeThreadLocal));
+    if (st == SS_OK) {
+      const ss_status qs = tse_enqueue_token(e);
+      const ss_status es = ck(hipStreamEndCapture(e->s, &e->graph));
+      st = qs != SS_OK ? qs : es;
+    }
+    if (st == SS_OK) st = ck(hipGraphInstantiate(&e->exec, e->graph, nullptr, nullptr, 0));
+    if (st != SS_OK) {
+      delete e;
+      return st;
+    }
+  }
+  *out = e;
+  return SS_OK;
+}
+
+// One token: routes (host, [G][n_ids]) uploaded, ss_begin, the graph (or the kernels), ss_end. checksums
+// ([G][n_ids]) and token_ms (begin -> end) may be NULL.
+__attribute__((visibility("default"))) ss_status tse_dg_token(void* h, const int32_t* routes, uint64_t* checksums,
+                                                              double* token_ms) {
+  TseDg* e = static_cast<TseDg*>(h);
+  std::vector<int32_t> ids(size_t(64) * e->G, 0);
+  for (uint32_t g = 0; g < e->G; ++g)
+    for (uint32_t i = 0; i < e->n_ids; ++i) ids[64 * g + i] = routes[size_t(g) * e->n_ids + i];
+  TSE_HIP(hipMemcpyAsync(e->ids_dev, ids.data(), 4ull * ids.size(), hipMemcpyHostToDevice, e->s));
+  if (e->checksum) TSE_HIP(hipMemsetAsync(e->out_dev, 0, 8ull * 64 * e->G, e->s));
+  TSE_HIP(hipStreamSynchronize(e->s));
+  const auto t0 = std::chrono::steady_clock::now();
+  if (e->dg) TSE_CK(ss_begin(e->c, nullptr, 0));
+  ss_status st = e->exec ? ck(hipGraphLaunch(e->exec, e->s)) : tse_enqueue_token(e);
+  const ss_status end_st = e->dg ? ss_end(e->c) : ck(hipStreamSynchronize(e->s));
+  if (token_ms) *token_ms = ms_since(t0);
+  (void)hipStreamSynchronize(e->s);
+  if (st == SS_OK) st = end_st;
+  if (st != SS_OK) return st;
+  if (checksums) {
+    std::vector<unsigned long long> out(size_t(64) * e->G);
+    TSE_HIP(hipMemcpy(out.data(), e->out_dev, 8ull * out.size(), hipMemcpyDeviceToHost));
+    for (uint32_t g = 0; g < e->G; ++g)
+      for (uint32_t i = 0; i < e->n_ids; ++i) checksums[size_t(g) * e->n_ids + i] = out[64 * g + i];
+  }
+  return SS_OK;
+}
+
+__attribute__((visibility("default"))) void tse_dg_destroy(void* h) {
+  TseDg* e = static_cast<TseDg*>(h);
+  if (!e) return;
+  (void)hipStreamSynchronize(e->s);
+  if (e->exec) (void)hipGraphExecDestroy(e->exec);
+  if (e->graph) (void)hipGraphDestroy(e->graph);
+  (void)hipFree(e->ids_dev);
+  (void)hipFree(e->out_dev);
+  (void)hipStreamDestroy(e->s);
+  delete e;
+}
+
+}  // extern "C"

@@ -1,0 +1,382 @@
+"""ctypes mirror of the strix-stream C ABI the library serves (include/strix_stream/ss.h), plus the synthetic engine
+(libtsa_engine.so) the tests and the benchmark drive it with. Struct layouts are declared field for field; a CPU test
+checks them against the C compiler's sizeof / offsetof."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from . import ENGINE_PATH, SsError, check, lib
+
+u32, u64, i32, vp = C.c_uint32, C.c_uint64, C.c_int32, C.c_void_p
+
+
+class SsBudget(C.Structure):
+    _fields_ = [("struct_size", u32), ("device_bytes", u64), ("host_pinned_bytes", u64), ("workspace_bytes", u64),
+                ("margin_gib", C.c_double), ("margin_fraction", C.c_double), ("dynamic_slots_per_layer", u32),
+                ("ring_slots", u32), ("pinned_backing", C.c_int), ("reserved0", u32), ("tier_mode", C.c_int),
+                ("host_spare_units", u32)]
+
+
+_OPT = [("struct_size", u32), ("backend", C.c_int), ("device", C.c_int), ("policy", C.c_int),
+        ("lookahead_budget", u32), ("reader_threads", u32), ("staging_buffers", u32), ("staging_bytes", u64),
+        ("copy_piece_bytes", u64), ("verify_hash", C.c_int), ("fill_residents", C.c_int), ("score_window", u32),
+        ("pin_planned", C.c_int), ("direct_io", C.c_int), ("group_units", u32), ("spec_persistent", C.c_int),
+        ("reserved0", u32), ("readahead_units", u32), ("reserved1", u32), ("forward_mode", C.c_int),
+        ("dg_max_ids", u32), ("dg_prefetch_reserve", u32), ("dg_prefetch_per_layer", u32),
+        ("dg_prefetch_per_token", u32), ("dg_wait_timeout_ms", u32), ("dg_service_boost", u32), ("dg_diag", u32),
+        ("dg_test_hooks", u32), ("dg_spare_target", u32), ("dg_seed_n", u32), ("dg_seed", vp),
+        ("dg_spare_slots", u32), ("dg_flush_ready", u32), ("dg_wb_defer", u32), ("dg_wb_stream", u32),
+        ("dg_wb_layer_bytes", u32), ("dg_wb_max_outstanding", u32), ("dg_prior_len", u64), ("dg_prior", vp),
+        ("exclusive_discard", u32), ("reserved2", u32), ("dg_score_w_trans", u32), ("dg_score_w_freq", u32),
+        ("dg_score_w_recency", u32), ("reserved3", u32), ("dg_score_profile_len", u64), ("dg_score_profile", vp),
+        ("weight_dirs", vp), ("drive_readers", u32), ("weight_verify", C.c_int), ("dg_disk_tier", u32),
+        ("dg_disk_prefetch", u32), ("dg_disk_staging", u32), ("dg_inclusive_blocks", u32), ("dg_disk_queue", u32),
+        ("reserved4", u32), ("source_identity_n", u32), ("reserved5", u32), ("source_identities", vp),
+        ("budget", vp), ("dg_no_admit", u32), ("reserved6", u32), ("dg_clean_evict", u32), ("reserved7", u32),
+        ("dg_pf_revert_unused", u32), ("reserved8", u32), ("dg_pf_strict_admit", u32), ("reserved9", u32),
+        ("dg_landing_blocks", u32), ("dg_landing_max_queued", u32), ("dg_landing_ttl", u32), ("reserved10", u32),
+        ("dg_landing_chunk", u32), ("reserved11", u32), ("dg_bank_keep", u32), ("reserved12", u32),
+        ("dg_disk_queue_adapt", u32), ("reserved13", u32)]
+
+
+class SsOptions(C.Structure):
+    _fields_ = _OPT
+
+
+class SsGroup(C.Structure):
+    _fields_ = [("units", C.POINTER(i32)), ("n_units", C.c_int)]
+
+
+class SsLayerView(C.Structure):
+    _fields_ = [("table_dev", vp), ("table_host", C.POINTER(u64)), ("n_units", C.c_int),
+                ("groups", C.POINTER(SsGroup)), ("n_groups", C.c_int)]
+
+
+STAT_FIELDS = ["routed", "hits", "admitted", "transient", "evicted", "prefetched", "spec_issued", "spec_used",
+               "spec_dropped", "bytes_pinned", "bytes_disk", "wait_ns"]
+
+
+class SsLayerStats(C.Structure):
+    _fields_ = [(n, u64) for n in STAT_FIELDS]
+
+    def as_dict(self):
+        return {n: int(getattr(self, n)) for n in STAT_FIELDS}
+
+
+class SsExclusiveStats(C.Structure):
+    _fields_ = [("struct_size", u32), ("writebacks", u64), ("writeback_bytes", u64), ("deferred", u64),
+                ("promoted", u64), ("free_blocks", u64), ("min_free_blocks", u64), ("rereads", u64),
+                ("discards", u64)]
+
+
+class SsPlanTotals(C.Structure):
+    _fields_ = [(n, u64) for n in ["fixed_bytes", "margin_bytes", "resident_bytes", "dynamic_bytes", "ring_bytes",
+                                   "peak_device_bytes", "pinned_bytes", "disk_bytes", "n_resident", "n_pinned",
+                                   "n_disk"]]
+
+
+class SsDgPart(C.Structure):
+    _fields_ = [("base", vp), ("stride", u64), ("bytes", u64)]
+
+
+class SsDgDeviceView(C.Structure):
+    _fields_ = [("struct_size", u32), ("protocol", u32), ("n_gated", u32), ("n_parts", u32), ("guard_slot", u32),
+                ("slots", u32), ("slot_of", vp), ("unit_base", vp), ("abort", vp), ("parts", SsDgPart * 4),
+                ("absent_err", vp)]
+
+
+DG_STAT_U64 = ("tokens lookups misses covered fetched prefetched prefetch_used pred_invalid resurrected bank_serves "
+               "collected_mid evicted evict_short writebacks_done stalled free_slots blocks slots predicted "
+               "predicted_true miss_layers device_timeouts covered_waits wb_deferred wb_cancelled wb_forced "
+               "wb_boundary_flushed wb_issued_bytes wb_completed_bytes wb_cancelled_bytes wb_boundary_flushed_bytes "
+               "wb_outstanding_bytes wb_forced_wait_ns winpf_hints winpf_hint_rows prior_issued prior_used prior_late "
+               "prior_reverted l1_candidates l1_issued l1_used l1_late l1_reverted l1_priced_out l1_skipped_ahead "
+               "prior_budget_stops score_fallbacks scored_victims score_layers score_candidates score_saturated "
+               "score_ns score_deferred score_last_ns disk_reads disk_read_bytes disk_read_ns disk_stage_waits "
+               "disk_drops disk_discards inclusive_kept inclusive_drops disk_units backed_units disk_wait_ns "
+               "disk_overlapped disk_max_in_flight disk_carried disk_carried_bytes resident_units resident_evicted "
+               "resident_bytes resident_ns round_count round_units round_bytes round_ns round_cancelled").split()
+DG_STAT_TAIL = [("cuda_module_loading", u32), ("reserved1", u32)] + [(n, u64) for n in (
+    "clean_drops clean_drop_bytes mkres_file_reads mkres_file_bytes mkres_read_ns mkres_h2d_bytes mkres_wb_bytes "
+    "lm_tokens lm_parts lm_mid_evictions lm_early_admits pf_reverted pf_revert_bytes pred_skipped_ahead "
+    "pf_strict_refused pred_shadow_file_predicted pred_shadow_file_demanded pred_shadow_file_hit "
+    "pred_shadow_file_predicted_bytes pred_shadow_file_demanded_bytes pred_shadow_file_hit_bytes").split()] + \
+    [("disk_queue_resolved", u32), ("disk_locations", u32)] + [(n, u64) for n in (
+        "landing_issued landing_promoted landing_late landing_wait_ns landing_expired landing_dropped_full "
+        "landing_read_bytes landing_cancelled landing_expired_layer landing_skipped_passed landing_yields "
+        "landing_aborted_bytes bank_kept").split()] + \
+    [("disk_depth_active", u32), ("disk_depth_adapt", u32), ("disk_depth_changes", u64),
+     ("disk_depth_calibrations", u64)]
+
+
+class SsDgStats(C.Structure):
+    _fields_ = [("struct_size", u32), ("reserved0", u32)] + [(n, u64) for n in DG_STAT_U64] + DG_STAT_TAIL
+
+    def as_dict(self):
+        return {n: int(getattr(self, n)) for n, _ in self._fields_ if not n.startswith("reserved")}
+
+
+_declared = False
+
+
+def _declare() -> C.CDLL:
+    global _declared
+    L = lib()
+    if _declared:
+        return L
+    st = C.c_int
+    sigs = {
+        "ss_desc_from_json": (st, [C.c_char_p, C.c_size_t, C.POINTER(vp)]),
+        "ss_desc_from_file": (st, [C.c_char_p, C.POINTER(vp)]),
+        "ss_desc_free": (None, [vp]),
+        "ss_desc_n_layers": (C.c_int, [vp]),
+        "ss_desc_layer_units": (C.c_int, [vp, C.c_int]),
+        "ss_desc_unit_bytes": (u64, [vp, C.c_int]),
+        "ss_desc_total_units": (C.c_int64, [vp]),
+        "ss_desc_to_json": (st, [vp, C.POINTER(C.c_char_p), C.POINTER(C.c_size_t)]),
+        "ss_free": (None, [vp]),
+        "ss_budget_defaults_sized": (None, [C.POINTER(SsBudget), u32]),
+        "ss_options_defaults_sized": (None, [C.POINTER(SsOptions), u32]),
+        "ss_plan_make": (st, [vp, C.POINTER(SsBudget), C.POINTER(C.c_double), C.c_size_t, C.POINTER(vp)]),
+        "ss_plan_from_tiers": (st, [vp, C.POINTER(SsBudget), C.POINTER(C.c_uint8), C.c_size_t, C.POINTER(vp)]),
+        "ss_plan_free": (None, [vp]),
+        "ss_plan_unit_tier": (C.c_int, [vp, C.c_int, C.c_int]),
+        "ss_plan_get_totals": (None, [vp, C.POINTER(SsPlanTotals)]),
+        "ss_plan_to_json": (st, [vp, C.POINTER(C.c_char_p), C.POINTER(C.c_size_t)]),
+        "ss_open": (st, [vp, C.POINTER(SsBudget), vp, C.POINTER(SsOptions), C.POINTER(vp)]),
+        "ss_close": (None, [vp]),
+        "ss_begin": (st, [vp, vp, C.c_int]),
+        "ss_layer_routes": (st, [vp, C.c_int, C.POINTER(i32), C.c_int]),
+        "ss_layer_all": (st, [vp, C.c_int]),
+        "ss_acquire": (st, [vp, C.c_int, vp, C.POINTER(SsLayerView)]),
+        "ss_acquire_groups": (st, [vp, C.c_int, vp, C.POINTER(SsLayerView)]),
+        "ss_group_wait": (st, [vp, C.c_int, C.c_int, vp]),
+        "ss_release": (st, [vp, C.c_int, vp]),
+        "ss_end": (st, [vp]),
+        "ss_check_unit": (st, [vp, C.c_int, C.c_int]),
+        "ss_stats_layer": (st, [vp, C.c_int, C.POINTER(SsLayerStats)]),
+        "ss_stats_total": (st, [vp, C.POINTER(SsLayerStats)]),
+        "ss_stats_exclusive_sized": (st, [vp, C.POINTER(SsExclusiveStats), u32]),
+        "ss_stats_dg_sized": (st, [vp, C.POINTER(SsDgStats), u32]),
+        "ss_dg_get_device_view_sized": (st, [vp, C.POINTER(SsDgDeviceView), u32]),
+        "ss_dg_gated_index": (C.c_int, [vp, C.c_int]),
+        "ss_dg_residency": (st, [vp, vp, u32, C.POINTER(u32)]),
+        "tsa_test_region_of": (st, [vp, u64, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(u64)]),
+        "tsa_test_dg_table": (st, [vp, C.POINTER(i32), u32, C.POINTER(u32)]),
+        "tsa_test_verify_failures": (u64, [vp]),
+        "tsa_xxh64_host": (u64, [vp, u64]),
+    }
+    for name, (res, args) in sigs.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    _declared = True
+    return L
+
+
+_engine = None
+
+
+def engine() -> C.CDLL:
+    global _engine
+    if _engine is None:
+        if not ENGINE_PATH.exists():
+            raise RuntimeError(f"{ENGINE_PATH} is not built: run python -m tierstream_amd.build")
+        _declare()
+        _engine = C.CDLL(str(ENGINE_PATH), mode=os.RTLD_NOW | os.RTLD_LOCAL)
+        E = _engine
+        E.tse_host_run.restype = C.c_int
+        E.tse_host_run.argtypes = [vp, vp, C.c_int, C.POINTER(i32), C.c_int, C.c_int, C.c_int, C.POINTER(u64),
+                                   C.POINTER(u64), C.POINTER(SsLayerStats), C.POINTER(C.c_double)]
+        E.tse_dg_create.restype = C.c_int
+        E.tse_dg_create.argtypes = [vp, u32, C.c_int, C.c_int, C.c_int, C.POINTER(vp)]
+        E.tse_dg_token.restype = C.c_int
+        E.tse_dg_token.argtypes = [vp, C.POINTER(i32), C.POINTER(u64), C.POINTER(C.c_double)]
+        E.tse_dg_destroy.restype = None
+        E.tse_dg_destroy.argtypes = [vp]
+    return _engine
+
+
+def budget(device_bytes: int, host_pinned_bytes: int, **kw) -> SsBudget:
+    L = _declare()
+    b = SsBudget()
+    L.ss_budget_defaults_sized(C.byref(b), C.sizeof(b))
+    b.device_bytes = device_bytes
+    b.host_pinned_bytes = host_pinned_bytes
+    b.margin_gib = 0.0
+    b.margin_fraction = 0.0
+    for k, v in kw.items():
+        setattr(b, k, v)
+    return b
+
+
+def options(**kw) -> SsOptions:
+    L = _declare()
+    o = SsOptions()
+    L.ss_options_defaults_sized(C.byref(o), C.sizeof(o))
+    for k, v in kw.items():
+        setattr(o, k, v)
+    return o
+
+
+class Desc:
+    def __init__(self, json_text: str):
+        L = _declare()
+        self.h = vp()
+        b = json_text.encode()
+        check(L.ss_desc_from_json(b, len(b), C.byref(self.h)))
+        self.n_layers = L.ss_desc_n_layers(self.h)
+
+    def units(self, layer):
+        return _declare().ss_desc_layer_units(self.h, layer)
+
+    def unit_bytes(self, layer):
+        return int(_declare().ss_desc_unit_bytes(self.h, layer))
+
+    def close(self):
+        if self.h:
+            _declare().ss_desc_free(self.h)
+            self.h = None
+
+
+class Plan:
+    def __init__(self, desc: Desc, b: SsBudget):
+        L = _declare()
+        self.h = vp()
+        check(L.ss_plan_make(desc.h, C.byref(b), None, 0, C.byref(self.h)))
+        self.desc = desc
+
+    def tiers(self):
+        L = _declare()
+        return [[L.ss_plan_unit_tier(self.h, l, u) for u in range(self.desc.units(l))]
+                for l in range(self.desc.n_layers)]
+
+    def totals(self) -> SsPlanTotals:
+        t = SsPlanTotals()
+        _declare().ss_plan_get_totals(self.h, C.byref(t))
+        return t
+
+    def json(self) -> dict:
+        import json as _json
+        L = _declare()
+        s, n = C.c_char_p(), C.c_size_t()
+        check(L.ss_plan_to_json(self.h, C.byref(s), C.byref(n)))
+        out = _json.loads(C.string_at(s, n.value).decode())
+        L.ss_free(s)
+        return out
+
+    def close(self):
+        if self.h:
+            _declare().ss_plan_free(self.h)
+            self.h = None
+
+
+class Ctx:
+    def __init__(self, desc: Desc, b: SsBudget, plan: Plan | None, o: SsOptions):
+        L = _declare()
+        self.h = vp()
+        self.desc = desc
+        check(L.ss_open(desc.h, C.byref(b), plan.h if plan else None, C.byref(o), C.byref(self.h)))
+
+    def close(self):
+        if self.h:
+            _declare().ss_close(self.h)
+            self.h = None
+
+    def stats_total(self) -> dict:
+        s = SsLayerStats()
+        check(_declare().ss_stats_total(self.h, C.byref(s)))
+        return s.as_dict()
+
+    def stats_layer(self, layer) -> dict:
+        s = SsLayerStats()
+        check(_declare().ss_stats_layer(self.h, layer, C.byref(s)))
+        return s.as_dict()
+
+    def exclusive_stats(self) -> dict:
+        x = SsExclusiveStats()
+        check(_declare().ss_stats_exclusive_sized(self.h, C.byref(x), C.sizeof(x)))
+        return {n: int(getattr(x, n)) for n, _ in x._fields_ if n != "struct_size"}
+
+    def dg_stats(self) -> dict:
+        s = SsDgStats()
+        check(_declare().ss_stats_dg_sized(self.h, C.byref(s), C.sizeof(s)))
+        return s.as_dict()
+
+    def dg_table(self) -> np.ndarray:
+        L = _declare()
+        n = u32(0)
+        check(L.tsa_test_dg_table(self.h, None, 0, C.byref(n)))
+        out = np.zeros(max(n.value, 1), dtype=np.int32)
+        check(L.tsa_test_dg_table(self.h, out.ctypes.data_as(C.POINTER(i32)), n.value, C.byref(n)))
+        return out[:n.value]
+
+    def dg_view(self) -> SsDgDeviceView:
+        v = SsDgDeviceView()
+        check(_declare().ss_dg_get_device_view_sized(self.h, C.byref(v), C.sizeof(v)))
+        return v
+
+    def region_of(self, addr: int):
+        k, i, off = C.c_int(), C.c_int(), u64()
+        check(_declare().tsa_test_region_of(self.h, addr, C.byref(k), C.byref(i), C.byref(off)))
+        return k.value, i.value, int(off.value)
+
+    # ---- engine drivers ----
+    def host_run(self, routes: np.ndarray, mode: int = 0, want_tables=True):
+        """routes int32 [steps][layers][max_ids]; returns checksums, tables, per-step stats, step ms."""
+        E = engine()
+        steps, L, max_ids = routes.shape
+        max_units = max(self.desc.units(l) for l in range(L))
+        r = np.ascontiguousarray(routes, dtype=np.int32)
+        cks = np.zeros((steps, L, max_ids), dtype=np.uint64)
+        tabs = np.zeros((steps, L, max_units), dtype=np.uint64) if want_tables else None
+        stats = (SsLayerStats * steps)()
+        ms = np.zeros(steps, dtype=np.float64)
+        st = E.tse_host_run(self.h, self.desc.h, steps, r.ctypes.data_as(C.POINTER(i32)), max_ids, max_units, mode,
+                            cks.ctypes.data_as(C.POINTER(u64)),
+                            tabs.ctypes.data_as(C.POINTER(u64)) if want_tables else None, stats,
+                            ms.ctypes.data_as(C.POINTER(C.c_double)))
+        check(st)
+        return cks, tabs, [s.as_dict() for s in stats], ms
+
+
+class DgEngine:
+    """A graph-captured device-gated engine over a context (tse_dg_*)."""
+
+    def __init__(self, ctx: Ctx, n_ids: int, use_graph=True, checksum=True, gated=True):
+        E = engine()
+        self.h = vp()
+        self.G = ctx.dg_view().n_gated
+        self.n_ids = n_ids
+        check(E.tse_dg_create(ctx.h, n_ids, int(use_graph), int(checksum), int(gated), C.byref(self.h)))
+
+    def token(self, routes: np.ndarray, want_checksums=True):
+        """routes int32 [G][n_ids]; returns (checksums [G][n_ids] or None, ms)."""
+        E = engine()
+        r = np.ascontiguousarray(routes, dtype=np.int32)
+        assert r.shape == (self.G, self.n_ids)
+        cks = np.zeros((self.G, self.n_ids), dtype=np.uint64) if want_checksums else None
+        ms = C.c_double(0)
+        check(E.tse_dg_token(self.h, r.ctypes.data_as(C.POINTER(i32)),
+                             cks.ctypes.data_as(C.POINTER(u64)) if want_checksums else None, C.byref(ms)))
+        return cks, ms.value
+
+    def close(self):
+        if self.h:
+            engine().tse_dg_destroy(self.h)
+            self.h = None
+
+
+def word_checksum(b: np.ndarray) -> int:
+    """The engine's checksum of a unit's bytes: sum of little-endian u32 words x ((j mod 251) + 1), mod 2^64."""
+    w = np.frombuffer(np.ascontiguousarray(b).tobytes(), dtype="<u4").astype(np.uint64)
+    mult = (np.arange(w.size, dtype=np.uint64) % np.uint64(251)) + np.uint64(1)
+    with np.errstate(over="ignore"):
+        return int(np.sum(w * mult, dtype=np.uint64))
+
+
+__all__ = ["SsBudget", "SsOptions", "SsLayerStats", "SsDgStats", "Desc", "Plan", "Ctx", "DgEngine", "budget",
+           "options", "word_checksum", "SsError"]

@@ -1,0 +1,228 @@
+"""The serve-path workloads (synthetic models and route streams) at their full sizes and scaled down for tests.
+
+A workload is a desc-v1 model written to one source file (unit-major: every unit's parts back to back at a 4 KiB unit
+stride, the layers one after the other), a budget, options and a seeded route stream:
+
+  moe-small    4 layers x 8 experts, 3 parts of 1 MiB uniform bytes, top-2 uniform ids; ranked, VRAM for 50 % of the
+               units, the rest pinned (inclusive); 64 decode steps. (host contract)
+  dense-prefix 32 blob layers of 4096 x 4096 x 7 bf16 N(0, 0.02); prefix order, 12 of 32 layers resident, the rest
+               pinned through the blob ring; ss_layer_all on every layer; 32 forwards. (host contract)
+  mixtral      32 layers x 8 experts, parts 4096 x 14336 x 2 (gate, up, down: 112 MiB each) bf16 N(0, 0.02); Zipf(1.1)
+               top-2 over a per-layer seeded permutation, batch 1; 40 % of the units resident, the rest pinned;
+               device-gated, a hipGraph-captured token; 256 steps. Device-gated mode requires the exclusive tier mode:
+               the inclusive intent is kept with dg_inclusive_blocks clean copies.
+  qwen3-moe    48 layers x 128 experts, parts 2048 x 768 x 2 (3 MiB each) bf16; 32 tokens x top-8 per step (the route
+               union per layer); exclusive with write-backs, ss_acquire_groups hits first; 25 % resident; 128 steps.
+  deepseek-q4  58 layers x 256 experts, parts 7168 x 2048 in 18-byte Q4 blocks (8,257,536 bytes each); three tiers
+               (not served by this build: the file tier is next).
+
+Bytes come from the counter-based generator (tsa_synth on the GPU, the same words for uniform bytes as
+oracle/synth.py); each unit's XXH64 is computed on the host by the library (tsa_xxh64_host).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import json
+import math
+import os
+from concurrent.futures import ThreadPoolExecutor
+from dataclasses import dataclass, field, replace
+from pathlib import Path
+
+import numpy as np
+
+MiB = 1 << 20
+GiB = 1 << 30
+UNIT_ALIGN_FILE = 4096
+
+
+@dataclass
+class Workload:
+    name: str
+    layers: int
+    units: int                 # per layer
+    parts: list                # part bytes
+    kind: str = "moe"          # moe | blob
+    top_k: int = 2
+    tokens: int = 1            # rows per step (the route union per layer)
+    routes: str = "uniform"    # uniform | zipf
+    zipf_s: float = 1.1
+    gen: int = 0               # tsa_synth kind: 0 uniform bytes, 1 bf16 N(0, sigma)
+    sigma: float = 0.02
+    resident_fraction: float = 0.5
+    order: str = "ranked"
+    tier_mode: int = 0         # 0 inclusive, 1 exclusive
+    forward: int = 0           # 0 host contract, 1 device-gated
+    steps: int = 64
+    layer_all: bool = False
+    groups: bool = False
+    dynamic_slots: int = 0
+    ring_slots: int = 0
+    spare_units: int = 0
+    inclusive_blocks: int = 0
+    seed: int = 1234
+    notes: dict = field(default_factory=dict)
+
+    @property
+    def unit_bytes(self) -> int:
+        return int(sum(self.parts))
+
+    @property
+    def n_units(self) -> int:
+        return self.layers * self.units
+
+    @property
+    def unit_stride_file(self) -> int:
+        return (self.unit_bytes + UNIT_ALIGN_FILE - 1) // UNIT_ALIGN_FILE * UNIT_ALIGN_FILE
+
+    @property
+    def max_ids(self) -> int:
+        return self.units if self.layer_all else min(64, self.tokens * self.top_k) if self.forward else \
+            self.tokens * self.top_k
+
+
+BF16 = 2
+WORKLOADS = {
+    "moe-small": Workload("moe-small", 4, 8, [MiB] * 3, top_k=2, routes="uniform", gen=0, resident_fraction=0.5,
+                          steps=64, ring_slots=0),
+    "dense-prefix": Workload("dense-prefix", 32, 1, [4096 * 4096 * 7 * BF16], kind="blob", top_k=1, gen=1,
+                             order="prefix", resident_fraction=12 / 32, layer_all=True, steps=32),
+    "mixtral": Workload("mixtral", 32, 8, [4096 * 14336 * BF16] * 3, top_k=2, routes="zipf", zipf_s=1.1, gen=1,
+                        resident_fraction=0.4, tier_mode=1, forward=1, steps=256),
+    "qwen3-moe": Workload("qwen3-moe", 48, 128, [2048 * 768 * BF16] * 3, top_k=8, tokens=32, routes="zipf",
+                          zipf_s=1.1, gen=1, resident_fraction=0.25, tier_mode=1, groups=True, steps=128,
+                          dynamic_slots=8),
+}
+
+
+def scaled(w: Workload, part_bytes: int | None = None, layers: int | None = None, units: int | None = None,
+           steps: int | None = None, **kw) -> Workload:
+    """The same shape at a size tests run in seconds."""
+    parts = [part_bytes] * len(w.parts) if part_bytes else list(w.parts)
+    return replace(w, parts=parts, layers=layers or w.layers, units=units or w.units, steps=steps or w.steps, **kw)
+
+
+# ---- routes --------------------------------------------------------------------------------------------------------
+def route_stream(w: Workload, steps: int | None = None) -> np.ndarray:
+    """int32 [steps][layers][max_ids], -1 padded: per step and layer the ids of `tokens` rows x top_k (rows drawn
+    without replacement inside a row; for device-gated workloads the flat row-major list, duplicates kept)."""
+    steps = w.steps if steps is None else steps
+    rng = np.random.default_rng(w.seed)
+    perms = [np.random.default_rng(w.seed * 1000 + L).permutation(w.units) for L in range(w.layers)]
+    k = min(w.top_k, w.units)
+    width = w.tokens * k
+    out = np.full((steps, w.layers, max(width, 1)), -1, dtype=np.int32)
+    if w.routes == "zipf":
+        p = 1.0 / np.power(np.arange(1, w.units + 1, dtype=np.float64), w.zipf_s)
+        p /= p.sum()
+    else:
+        p = np.full(w.units, 1.0 / w.units)
+    for s in range(steps):
+        for L in range(w.layers):
+            rows = []
+            for _ in range(w.tokens):
+                ranks = rng.choice(w.units, size=k, replace=False, p=p)
+                rows.extend(int(perms[L][r]) for r in ranks)
+            out[s, L, :len(rows)] = rows
+    return out
+
+
+# ---- sources, descriptor, budget -------------------------------------------------------------------------------------
+def unit_offset(w: Workload, L: int, u: int) -> int:
+    return (L * w.units + u) * w.unit_stride_file
+
+
+def source_bytes(w: Workload) -> int:
+    return w.n_units * w.unit_stride_file
+
+
+def write_sources_gpu(w: Workload, path: str | os.PathLike, threads: int = 16) -> list:
+    """Writes the source file from bytes the GPU generates (tsa_synth); returns the per-unit XXH64 list (global order),
+    computed on the host by the library. Each unit's parts are stream ids 4 g + p."""
+    import tierstream_amd as tsa
+    L = tsa.lib()
+    path = str(path)
+    total = source_bytes(w)
+    fd = os.open(path, os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o644)
+    try:
+        os.ftruncate(fd, total)
+    finally:
+        os.close(fd)
+    ub = w.unit_bytes
+    batch = max(1, min(w.n_units, (2 * GiB) // max(ub, 1)))  # units per GPU batch
+    dev = tsa.DeviceBuffer(batch * w.unit_stride_file)
+    host = C.c_void_p()
+    tsa.check(L.tsa_host_alloc(C.byref(host), batch * w.unit_stride_file))
+    hashes = [0] * w.n_units
+    try:
+        fd = os.open(path, os.O_WRONLY)
+        with ThreadPoolExecutor(threads) as ex:
+            for g0 in range(0, w.n_units, batch):
+                n = min(batch, w.n_units - g0)
+                for i in range(n):
+                    off = 0
+                    for p, pb in enumerate(w.parts):
+                        tsa.check(L.tsa_synth(C.c_void_p(dev.ptr + i * w.unit_stride_file + off), pb, w.seed,
+                                              4 * (g0 + i) + p, 0, w.gen, C.c_float(w.sigma), None))
+                        off += pb
+                tsa.check(L.tsa_memcpy(host, C.c_void_p(dev.ptr), n * w.unit_stride_file, 1, None))
+                tsa.check(L.tsa_stream_sync(None))
+                base = host.value
+
+                def one(i):
+                    p = base + i * w.unit_stride_file
+                    hashes[g0 + i] = int(L.tsa_xxh64_host(C.c_void_p(p), ub))
+                    mv = (C.c_char * ub).from_address(p)
+                    os.pwrite(fd, mv, unit_offset(w, 0, 0) + (g0 + i) * w.unit_stride_file)
+
+                list(ex.map(one, range(n)))
+        os.close(fd)
+    finally:
+        L.tsa_host_free(host)
+        dev.close()
+    return hashes
+
+
+def desc_json(w: Workload, path: str, hashes: list) -> str:
+    layers = []
+    for L in range(w.layers):
+        off = 0
+        parts = []
+        names = ["gate", "up", "down"] if len(w.parts) == 3 else [f"p{i}" for i in range(len(w.parts))]
+        for p, pb in enumerate(w.parts):
+            parts.append({"name": names[p], "format": "BF16" if w.gen == 1 else "U8", "source": 0,
+                          "offset": unit_offset(w, L, 0) + off, "stride": w.unit_stride_file, "bytes": pb})
+            off += pb
+        lay = {"index": L, "kind": w.kind, "n_units": w.units, "unit_bytes": w.unit_bytes, "parts": parts,
+               "hash": [f"{h:016x}" for h in hashes[L * w.units:(L + 1) * w.units]]}
+        if w.kind == "moe":
+            lay["top_k"] = min(w.top_k, w.units)
+        layers.append(lay)
+    d = {"schema": "strix-stream/desc-v1", "model": w.name, "engine": "tsa-synthetic", "unit_align": 256,
+         "order": w.order, "tiers": "pinned", "sources": [{"name": "weights", "path": str(path), "align": 4096}],
+         "layers": layers}
+    return json.dumps(d)
+
+
+def unit_stride_dev(w: Workload) -> int:
+    return (w.unit_bytes + 255) // 256 * 256
+
+
+def budget_numbers(w: Workload) -> dict:
+    """device_bytes / host_pinned_bytes that give the workload's resident fraction under the planner's rule."""
+    st = unit_stride_dev(w)
+    n_res = int(round(w.resident_fraction * w.n_units))
+    margin = 2 * GiB
+    if w.forward == 1:
+        # device-gated: residents + spare slots + banks + guard (ring_slots = 2 B + 1), billed as resident + ring
+        ring = 2 * w.max_ids + 1
+        dyn = w.dynamic_slots or 1
+        dev = n_res * st + ring * st + dyn * w.layers * st + margin + 64 * MiB
+    else:
+        ring_slots = w.ring_slots or (2 * w.units)
+        dyn = w.dynamic_slots
+        dev = n_res * st + ring_slots * st + dyn * w.layers * st + margin + 64 * MiB
+    hs = (w.unit_bytes + 4095) // 4096 * 4096
+    spares = w.spare_units or (min(64, w.n_units) if w.tier_mode == 1 else 0)
+    host = (w.n_units - n_res) * hs + spares * hs + 512 * MiB
+    return {"device_bytes": int(dev), "host_pinned_bytes": int(host), "n_resident": n_res}
