@@ -1,0 +1,317 @@
+#!/usr/bin/env python3
+"""Decode-step serve benchmark of libtierstream_amd on one MI355X.
+
+Workload (default): the Mixtral-shape MoE decode. 32 layers x 8 experts, each expert a unit of three bf16 parts
+(gate and up 4096 x 14336, down 14336 x 4096: 112 MiB each, 336 MiB per unit), values N(0, 0.02) from the
+counter-based generator. Routes are Zipf(1.1) top-2 over a per-layer seeded permutation, batch 1. 40 % of the units
+(102) are planned residents in HBM and the other 154 live in hipHostMalloc pinned memory. The context runs
+SS_FORWARD_DEVICE_GATED: each token is a hipGraph of begin, then per layer export, wait and the engine's expert
+stand-in, then end. The stand-in is a checksum that reads every byte of both routed units through ss_dg_slot.
+Every landed unit is re-hashed in HBM by the device XXH64 verify (verify_hash = 2).
+
+A step is one token: ss_begin -> graph launch -> ss_end on the engine thread (the reference's decode-step serve
+latency). The timed region is exactly --steps tokens after --warmup untimed ones, bracketed by device
+synchronizations. The JSON line's value is the p50 step latency in ms.
+
+Beside it:
+  h2d        miss bytes over the copy engines' busy time (timed events around every unit copy), against the pinned
+             host-to-device peak measured in the same run (2 GiB hipMemcpyAsync from hipHostMalloc memory)
+  roofline   the device XXH64 verify kernel (the dominant kernel of the library): unit bytes hashed per launch over
+             its mean launch time (timed events on the stream it runs on), against the 8 TB/s HBM peak
+  wait       the zero-miss layer wait on the device timeline: from the export kernel's end to the layer's compute
+             start when the layer had no miss (wall-clock stamps, 10 ns), and the miss layers' wait for their copies
+  cpu_baseline  the reference DgCore (compiled from the reference sources) on a synchronous memcpy transport over host
+             memory with a host XXH64 of every landed unit, one thread, over a bounded sample of the same tokens
+Checks at full size: no unit fails its device hash check, and every routed unit's checksum is the same each time it
+is routed (a stale or partial copy would change it).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import shutil
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+METRIC = "decode-step serve latency p50/p99; miss H2D GB/s and HBM GB/s vs roofline"
+HBM_PEAK_GBPS = 8000.0
+TICK_NS = 10.0  # wall_clock64 runs at 100 MHz on gfx950
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--workload", default="mixtral")
+    ap.add_argument("--part-bytes", type=int, default=0, help="scale every part to this size (0 = full size)")
+    ap.add_argument("--probe-tokens", type=int, default=32, help="tokens after the timed ones that read the stamps")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="target CPU time of the baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--workdir", default="", help="where the source file is written (default /dev/shm)")
+    return ap.parse_args()
+
+
+def pct(a, q):
+    return float(np.percentile(np.asarray(a, dtype=np.float64), q)) if len(a) else None
+
+
+# ---- peaks measured in the same run ---------------------------------------------------------------------------------
+def measure_peaks(tsa, L, C):
+    """Pinned H2D peak (2 GiB from hipHostMalloc memory) and an HBM copy (4 GiB device to device: 2 x bytes moved)."""
+    out = {}
+    n = 2 << 30
+    host, dev, dev2, s = C.c_void_p(), C.c_void_p(), C.c_void_p(), C.c_void_p()
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    tsa.check(L.tsa_host_alloc(C.byref(host), n))
+    tsa.check(L.tsa_malloc(C.byref(dev), 2 * n))
+    tsa.check(L.tsa_malloc(C.byref(dev2), 2 * n))
+    tsa.check(L.tsa_stream_create(C.byref(s)))
+    tsa.check(L.tsa_event_create(C.byref(e0)))
+    tsa.check(L.tsa_event_create(C.byref(e1)))
+    try:
+        C.memset(host, 1, n)
+
+        def timed(fn):
+            tsa.check(L.tsa_event_record(e0, s))
+            fn()
+            tsa.check(L.tsa_event_record(e1, s))
+            tsa.check(L.tsa_event_sync(e1))
+            ms = C.c_float()
+            tsa.check(L.tsa_event_elapsed_ms(e0, e1, C.byref(ms)))
+            return ms.value / 1e3
+
+        h2d = [n / timed(lambda: tsa.check(L.tsa_memcpy(dev, host, n, 0, s))) / 1e9 for _ in range(6)]
+        d2h = [n / timed(lambda: tsa.check(L.tsa_memcpy(host, dev, n, 1, s))) / 1e9 for _ in range(4)]
+        d2d = [2 * (2 * n) / timed(lambda: tsa.check(L.tsa_memcpy(dev2, dev, 2 * n, 2, s))) / 1e9 for _ in range(6)]
+        out = {"h2d_pinned_GBps": max(h2d[1:]), "h2d_pinned_GBps_median": float(np.median(h2d[1:])),
+               "d2h_pinned_GBps": max(d2h[1:]), "hbm_copy_GBps": max(d2d[1:]),
+               "pcie_gen5_x16_GBps": 64.0, "hbm_peak_GBps": HBM_PEAK_GBPS}
+    finally:
+        L.tsa_event_destroy(e0)
+        L.tsa_event_destroy(e1)
+        L.tsa_stream_destroy(s)
+        L.tsa_free(dev)
+        L.tsa_free(dev2)
+        L.tsa_host_free(host)
+    return out
+
+
+# ---- the CPU baseline -----------------------------------------------------------------------------------------------
+def cpu_baseline(w, shape, path, hashes, routes, start, est_token_s, seconds):
+    """The reference DgCore on a memcpy transport (oracle/_ref), over tokens start.. of the same route stream."""
+    try:
+        from oracle import ref
+    except Exception as e:  # noqa: BLE001
+        return None, f"oracle unavailable: {e}"
+    if not ref.available():
+        return None, "oracle/_ref is not built"
+    from tierstream_amd import workloads as W
+    n_tok = int(max(3, min(64, seconds / max(est_token_s, 1e-3))))
+    n_tok = min(n_tok, routes.shape[0] - start)
+    keys = w.n_units
+    residents = list(range(shape.R))
+    order = residents + list(range(keys))
+    offsets = [W.unit_offset(w, 0, 0) + g * w.unit_stride_file for g in range(keys)]
+    ids = routes[start:start + n_tok].astype(np.uint32)
+    hs = (w.unit_bytes + 4095) // 4096 * 4096
+    t0 = time.time()
+    ms, c = ref.cpu_baseline([w.units] * w.layers, shape.R + shape.D, shape.B, shape.P + shape.Q, shape.D, w.parts,
+                             hs, order, path, offsets, hashes, ids, wb_defer=1, inclusive=shape.I, setup_threads=16)
+    log(f"cpu baseline: {n_tok} tokens in {time.time() - t0:.1f} s (setup included), counters {c}")
+    return (ms, c, n_tok), None
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py: --gpus {a.gpus}: this benchmark runs on one GPU only (the serve path has no cross-GPU "
+              f"exchange; each GPU would open its own context over its share of units)", file=sys.stderr)
+        sys.exit(2)
+    import ctypes as C
+
+    import tierstream_amd as tsa
+    from tierstream_amd import ss
+    from tierstream_amd import workloads as W
+
+    L = tsa.lib()
+    if tsa.gpu_count() < 1:
+        raise SystemExit("bench.py: no HIP device")
+    w = W.WORKLOADS[a.workload]
+    if w.forward != 1:
+        raise SystemExit(f"bench.py: workload {a.workload} is not device-gated")
+    if a.part_bytes:
+        w = W.scaled(w, part_bytes=a.part_bytes)
+    shape = W.dg_shape(w)
+    base = a.workdir or ("/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir())
+    work = tempfile.mkdtemp(prefix="tsa_bench_", dir=base)
+    path = os.path.join(work, "weights.bin")
+    result = {}
+    try:
+        t0 = time.time()
+        log(f"workload {w.name}: {w.layers} x {w.units} units of {w.unit_bytes / 2**20:.0f} MiB, writing "
+            f"{W.source_bytes(w) / 1e9:.1f} GB to {path}")
+        hashes = W.write_sources_gpu(w, path)
+        log(f"sources written in {time.time() - t0:.1f} s")
+        d = ss.Desc(W.desc_json(w, path, hashes))
+        b = ss.budget(**shape.budget)
+        plan = ss.Plan(d, b)
+        tiers = plan.tiers()
+        n_res = sum(1 for r in tiers for t in r if t == 0)
+        log(f"plan: {n_res} resident units (target {shape.R}), D {shape.D}, Q {shape.Q}, inclusive {shape.I}, "
+            f"device budget {shape.budget['device_bytes'] / 1e9:.1f} GB, pinned {shape.budget['host_pinned_bytes'] / 1e9:.1f} GB")
+        t0 = time.time()
+        ctx = ss.Ctx(d, b, plan, ss.options(**shape.options, verify_hash=2, dg_wait_timeout_ms=20000))
+        log(f"context open (fill + hash check) in {time.time() - t0:.1f} s")
+        eng = ss.DgEngine(ctx, shape.B, use_graph=True)
+        G = eng.G
+        steps, warm, probe = a.steps, a.warmup, a.probe_tokens
+        routes = W.route_stream(w, warm + steps + probe)[:, :, :shape.B]
+        ck_seen, ck_bad = {}, 0
+
+        def check_cks(t, cks):
+            nonlocal ck_bad
+            for g in range(G):
+                for j in range(shape.B):
+                    k = (g, int(routes[t, g, j]))
+                    v = int(cks[g, j])
+                    if ck_seen.setdefault(k, v) != v:
+                        ck_bad += 1
+
+        for t in range(warm):
+            cks, _ = eng.token(routes[t])
+            check_cks(t, cks)
+        ctx.profile_enable(True)
+        s0 = ctx.dg_stats()
+        tsa.check(L.tsa_device_sync())
+        lat = np.zeros(steps)
+        t_start = time.perf_counter()
+        for i in range(steps):
+            cks, lat[i] = eng.token(routes[warm + i])
+            check_cks(warm + i, cks)
+        tsa.check(L.tsa_device_sync())
+        wall = time.perf_counter() - t_start
+        s1 = ctx.dg_stats()
+        prof = ctx.profile_read(wait=True)
+        log(f"timed {steps} tokens in {wall:.2f} s: p50 {pct(lat, 50):.2f} ms p99 {pct(lat, 99):.2f} ms; {prof}")
+        # the probe tokens: device stamps per layer
+        zero_gap, miss_wait, zero_wait_kernel = [], [], []
+        ctx.profile_enable(False)
+        for i in range(probe):
+            t = warm + steps + i
+            cks, _ = eng.token(routes[t])
+            check_cks(t, cks)
+            st = ctx.dg_stamps().astype(np.int64)
+            start = eng.stamps().astype(np.int64)
+            for g in range(G):
+                if st[g, 1] == 0:
+                    zero_gap.append((start[g] - st[g, 0]) * TICK_NS / 1e3)
+                else:
+                    miss_wait.append((st[g, 2] - st[g, 1]) * TICK_NS / 1e6)
+        dstat = {k: s1[k] - s0[k] for k in ("tokens", "lookups", "misses", "fetched", "evicted", "bank_serves",
+                                             "writebacks_done", "inclusive_kept", "inclusive_drops", "miss_layers")}
+        failures = ctx.verify_failures()
+        eng.close()
+        ctx.close()
+        plan.close()
+        d.close()
+        peaks = measure_peaks(tsa, L, C)
+        log(f"peaks {peaks}")
+
+        copy_gbps = prof["copy_bytes"] / prof["copy_ns"] if prof["copy_ns"] else None
+        ver_gbps = prof["verify_bytes"] / prof["verify_ns"] if prof["verify_ns"] else None
+        miss_bytes = dstat["fetched"] * w.unit_bytes
+        result = {
+            "metric": METRIC,
+            "value": round(pct(lat, 50), 3),
+            "unit": "ms",
+            "n_gpus": 1,
+            "steps": steps,
+            "warmup": warm,
+            "ms_per_step": round(wall * 1e3 / steps, 3),
+            "higher_is_better": False,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "u8",
+            "data": "synthetic (bf16 N(0, 0.02) expert bytes from the counter-based generator; Zipf(1.1) routes)",
+            "config": {"workload": f"{w.name}: {w.layers} layers x {w.units} experts, top-{w.top_k}, units "
+                                   f"{w.unit_bytes} B (3 parts), {n_res} resident / {w.n_units - n_res} pinned, "
+                                   f"device-gated hipGraph token, verify_hash 2",
+                       "layers": w.layers, "experts": w.units, "top_k": w.top_k, "unit_bytes": w.unit_bytes,
+                       "resident_units": n_res, "spare_slots": shape.D, "inclusive_blocks": shape.I,
+                       "device_budget_bytes": shape.budget["device_bytes"],
+                       "pinned_budget_bytes": shape.budget["host_pinned_bytes"]},
+            "p50_ms": round(pct(lat, 50), 3),
+            "p99_ms": round(pct(lat, 99), 3),
+            "tokens_per_s": round(steps / wall, 3),
+            "misses_per_token": round(dstat["misses"] / steps, 3),
+            "h2d": {"miss_bytes": miss_bytes, "copies": prof["copies"],
+                    "busy_GBps": round(copy_gbps, 2) if copy_gbps else None,
+                    "wall_GBps": round(miss_bytes / wall / 1e9, 2),
+                    "pinned_peak_GBps": round(peaks["h2d_pinned_GBps"], 2),
+                    "frac_of_pinned_peak": round(copy_gbps / peaks["h2d_pinned_GBps"], 3) if copy_gbps else None,
+                    "frac_of_pcie_gen5_x16": round(copy_gbps / 64.0, 3) if copy_gbps else None},
+            "roofline": {"bound": "hbm", "kernel": "verify_kernel (device XXH64 of every landed unit)",
+                         "achieved": round(ver_gbps, 1) if ver_gbps else None, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(ver_gbps / HBM_PEAK_GBPS, 4) if ver_gbps else None, "traffic": None,
+                         "launches": prof["verifies"], "units": prof["verify_units"],
+                         "bytes_per_launch": prof["verify_bytes"] // max(prof["verifies"], 1),
+                         "mean_launch_us": round(prof["verify_ns"] / max(prof["verifies"], 1) / 1e3, 2)},
+            "hbm_copy_GBps": round(peaks["hbm_copy_GBps"], 1),
+            "wait": {"zero_miss_layer_us_p50": round(pct(zero_gap, 50), 2) if zero_gap else None,
+                     "zero_miss_layer_us_p99": round(pct(zero_gap, 99), 2) if zero_gap else None,
+                     "zero_miss_samples": len(zero_gap),
+                     "miss_layer_wait_ms_p50": round(pct(miss_wait, 50), 3) if miss_wait else None,
+                     "miss_samples": len(miss_wait)},
+            "writeback": {"units": prof["writebacks"], "bytes": prof["writeback_bytes"],
+                          "busy_GBps": round(prof["writeback_bytes"] / prof["writeback_ns"], 2)
+                          if prof["writeback_ns"] else None},
+            "stats": dstat,
+            "checks": {"verify_failures": failures, "checksum_mismatches": ck_bad,
+                       "units_seen": len(ck_seen)},
+            "cpu_baseline": None,
+        }
+        if not a.no_cpu:
+            est = float(np.median(lat)) / 1e3 * 20  # a first guess of the CPU's time per token
+            got, why = cpu_baseline(w, shape, path, hashes, routes, warm, est, a.cpu_seconds)
+            if got:
+                ms, c, n_tok = got
+                result["cpu_baseline"] = {
+                    "value": round(pct(ms, 50), 3), "unit": "ms", "cores": 1, "kind": "reference",
+                    "p99_ms": round(pct(ms, 99), 3), "mean_ms": round(float(np.mean(ms)), 3),
+                    "copy_GBps": round(c["copied_bytes"] / (float(np.sum(ms)) / 1e3) / 1e9, 2),
+                    "sample": f"tokens {warm}..{warm + n_tok - 1} of the same route stream from the open-time "
+                              f"placement: reference DgCore + memcpy transport + host XXH64 of each landed unit, "
+                              f"1 thread; misses {c['misses']}, hash mismatches {c['hash_mismatches']}",
+                    "cpu": cpu_model(), "nproc": os.cpu_count()}
+            else:
+                log(f"cpu baseline skipped: {why}")
+    finally:
+        shutil.rmtree(work, ignore_errors=True)
+    print(json.dumps(result), flush=True)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    main()

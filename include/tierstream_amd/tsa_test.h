@@ -1,6 +1,6 @@
 /*
  * Test hooks of libtierstream_amd (the counterpart of reference include/strix_stream/ss_test.h: calls tests link by
- * name that an engine never needs). None changes state.
+ * name that an engine never needs). None changes the cache state.
  */
 #ifndef TIERSTREAM_AMD_TSA_TEST_H
 #define TIERSTREAM_AMD_TSA_TEST_H
@@ -20,6 +20,29 @@ SS_API ss_status tsa_test_region_of(const ss_ctx* c, uint64_t addr, int* kind, i
 SS_API ss_status tsa_test_dg_table(const ss_ctx* c, int32_t* out, uint32_t cap, uint32_t* n);
 /* verify_hash = 2: landed units whose device check failed, since open. */
 SS_API uint64_t tsa_test_verify_failures(const ss_ctx* c);
+
+/* Device-gated timing (measurement only; the cache state is untouched). While enabled the library brackets every unit
+ * copy host -> HBM, every write-back HBM -> host and every device verify launch with timed events on the stream that
+ * runs it; durations are summed once the events completed. Enabling (or disabling) resets the totals. */
+typedef struct tsa_test_profile {
+  uint64_t copies;          /* unit copies into HBM (demand and prefetch) */
+  uint64_t copy_bytes;
+  uint64_t copy_ns;         /* summed durations: the copy engines' busy time */
+  uint64_t writebacks;      /* unit (or part) copies out of HBM */
+  uint64_t writeback_bytes;
+  uint64_t writeback_ns;
+  uint64_t verifies;        /* verify kernel launches (verify_hash = 2) */
+  uint64_t verify_units;
+  uint64_t verify_bytes;    /* bytes hashed: the units' bytes */
+  uint64_t verify_ns;
+  uint64_t pending;         /* bracketed operations whose events had not completed at the read */
+} tsa_test_profile;
+SS_API ss_status tsa_test_profile_enable(ss_ctx* c, int on);
+/* Between tokens; wait = 1 first waits for every bracketed operation (write-backs may still run after ss_end). */
+SS_API ss_status tsa_test_profile_read(ss_ctx* c, int wait, tsa_test_profile* out);
+/* Between tokens: the device-gated kernels' wall-clock stamps of the last token (100 MHz ticks), 4 per gated layer:
+ * export end, wait entry (0: the layer had no miss, the wait returned at once), ready seen, unused. *n = 4 G. */
+SS_API ss_status tsa_test_dg_stamps(const ss_ctx* c, uint64_t* out, uint32_t cap, uint32_t* n);
 
 #ifdef __cplusplus
 }

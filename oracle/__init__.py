@@ -1,7 +1,7 @@
 """ORACLE: test infrastructure, never the product.
 
 CPU restatements of the reference's algorithms on the serve path, each function citing the reference file:line it
-follows, used as the checker by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg only. The product path
+follows, used for comparison by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg only. The product path
 (tierstream_amd) never imports, links or calls anything here.
 
 Contents:

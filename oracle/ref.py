@@ -60,6 +60,10 @@ def lib() -> C.CDLL:
             "refdg_counter_names": (C.c_char_p, []),
             "refdg_residency": (u32, [vp, C.POINTER(u32), u32]),
             "refdg_close": (None, [vp]),
+            "refdg_cpu_baseline": (C.c_int, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, C.POINTER(u64), u32,
+                                              u64, C.POINTER(u32), u32, C.c_char_p, C.POINTER(u64), C.POINTER(u64),
+                                              C.POINTER(u32), u32, u32, C.c_int, C.POINTER(C.c_double),
+                                              C.POINTER(u64)]),
         }
         for name, (res, args) in sigs.items():
             f = getattr(L, name)
@@ -202,3 +206,28 @@ class RefDg:
         if self.h:
             lib().refdg_close(self.h)
             self.h = None
+
+
+def cpu_baseline(n_units, persistent, bank, blocks, spare_target, part_bytes, host_stride, order, path, unit_offsets,
+                 hashes, ids: np.ndarray, wb_defer=1, inclusive=0, setup_threads=16):
+    """The reference DgCore on a synchronous memcpy transport over host memory (refdg_cpu_baseline), timed per token
+    on the calling thread. ids uint32 [tokens][G][n]. Returns (token_ms [tokens], counters dict)."""
+    L = lib()
+    x = np.ascontiguousarray(ids, dtype=np.uint32)
+    tokens, G, n = x.shape
+    nu = (u32 * G)(*n_units)
+    pb = (u64 * len(part_bytes))(*part_bytes)
+    od = (u32 * len(order))(*order)
+    offs = np.ascontiguousarray(unit_offsets, dtype=np.uint64)
+    hs = np.ascontiguousarray(hashes, dtype=np.uint64)
+    ms = np.zeros(tokens, dtype=np.float64)
+    out = np.zeros(6, dtype=np.uint64)
+    st = L.refdg_cpu_baseline(nu, G, persistent, bank, blocks, spare_target, wb_defer, inclusive, pb, len(part_bytes),
+                              host_stride, od, len(order), str(path).encode(), offs.ctypes.data_as(C.POINTER(u64)),
+                              hs.ctypes.data_as(C.POINTER(u64)), x.ctypes.data_as(C.POINTER(u32)), n, tokens,
+                              setup_threads, ms.ctypes.data_as(C.POINTER(C.c_double)),
+                              out.ctypes.data_as(C.POINTER(u64)))
+    if st != 0:
+        raise RuntimeError("refdg_cpu_baseline failed")
+    names = ["misses", "fetched", "evicted", "writebacks_done", "hash_mismatches", "copied_bytes"]
+    return ms, {k: int(v) for k, v in zip(names, out)}

@@ -7,6 +7,8 @@
 //    (tests/test_dg.cpp:201): a transport whose copies, entries and events complete at once (done() is always true)
 //    and a service loop that never sees the device "ahead". Each token: begin_token, per gated layer the export mask
 //    from the table as the device would read it, serve_demand, serve_use, issue_writebacks, then end_token.
+//  * refdg_cpu_baseline: the same core on a synchronous memcpy transport over host memory, timed per token: the CPU
+//    baseline the benchmark reports beside the device numbers (device-gated decode has no CPU backend in the reference).
 // every standard header the reference headers pull in, first (the access override below must not reach them)
 #include <algorithm>
 #include <atomic>
@@ -37,10 +39,15 @@
 #include <utility>
 #include <vector>
 
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <unistd.h>
+
 #define private public
 #define protected public
 #include "dg_core.hpp"
 #include "stream_ctx.hpp"
+#include "xxh64.hpp"
 #undef private
 #undef protected
 
@@ -206,5 +213,205 @@ uint32_t refdg_residency(void* h, uint32_t* out, uint32_t cap) {
 }
 
 void refdg_close(void* h) { delete static_cast<RefDg*>(h); }
+
+}  // extern "C"
+
+// ---- the CPU baseline -----------------------------------------------------------------------------------------------
+// The reference DgCore on a transport shaped like the reference CPU backend (src/backend_cpu.cpp:20-59: host memory
+// stands in for the device, copies are synchronous memcpy), plus a host XXH64 of every landed unit (src/xxh64.cpp), the
+// CPU counterpart of the device verify. The "device" is one anonymous array per part (slots x part bytes); every host
+// block is anonymous memory of one unit stride, filled from the source file before timing.
+namespace {
+
+void* map_anon(uint64_t bytes) {
+  void* p = ::mmap(nullptr, size_t(bytes), PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS | MAP_NORESERVE, -1, 0);
+  if (p == MAP_FAILED) throw std::runtime_error("mmap of " + std::to_string(bytes) + " bytes failed");
+  return p;
+}
+
+class Memcpy final : public ts::DgTransport {
+ public:
+  Memcpy(std::vector<uint64_t> parts, uint64_t host_stride, uint32_t slots, uint32_t blocks)
+      : parts_(std::move(parts)), stride_(host_stride), slots_(slots), blk_(size_t(blocks) + 1, nullptr) {
+    uint64_t off = 0;
+    for (uint64_t pb : parts_) {
+      off_.push_back(off);
+      off += pb;
+      arena_.push_back(static_cast<char*>(map_anon(pb * slots)));
+    }
+    unit_ = off;
+    for (auto& b : blk_) b = static_cast<char*>(map_anon(stride_));
+  }
+  ~Memcpy() override {
+    for (size_t p = 0; p < parts_.size(); ++p) ::munmap(arena_[p], size_t(parts_[p] * slots_));
+    for (char* b : blk_) ::munmap(b, size_t(stride_));
+  }
+  char* slot(uint32_t p, int32_t s) const { return arena_[p] + uint64_t(s) * parts_[p]; }
+  char* block(int32_t b) const { return blk_[size_t(b + 1)]; }  // block -1: the one-unit staging buffer
+  uint64_t part_offset(uint32_t p) const { return off_[p]; }
+
+  void h2d(Stream, int32_t s, int32_t b) override {
+    for (uint32_t p = 0; p < parts_.size(); ++p) std::memcpy(slot(p, s), block(b) + off_[p], parts_[p]);
+  }
+  void d2h(int32_t s, int32_t b) override {
+    for (uint32_t p = 0; p < parts_.size(); ++p) std::memcpy(block(b) + off_[p], slot(p, s), parts_[p]);
+  }
+  void d2d(int32_t a, int32_t b) override {
+    for (uint32_t p = 0; p < parts_.size(); ++p) std::memcpy(slot(p, b), slot(p, a), parts_[p]);
+  }
+  void h2h(int32_t a, int32_t b) override { std::memcpy(block(b), block(a), unit_); }
+  void d2h_part(Stream, int32_t s, int32_t b, uint32_t p) override {
+    std::memcpy(block(b) + off_[p], slot(p, s), parts_[p]);
+  }
+  uint32_t parts() const override { return uint32_t(parts_.size()); }
+  uint64_t part_bytes(uint32_t p) const override { return parts_[p]; }
+  void write_entry(Stream, uint32_t, int32_t) override {}
+  void signal_ready(uint32_t, uint32_t) override {}
+  void* event_create() override { return new int(0); }
+  void event_destroy(void* ev) override { delete static_cast<int*>(ev); }
+  void record(void*, Stream) override {}
+  void wait(Stream, void*) override {}
+  bool done(void*) override { return true; }
+  void event_sync(void*) override {}
+  void sync(Stream) override {}
+  void upload_table(const int32_t*, uint32_t) override {}
+  void upload_table_ranges(const int32_t*, const uint32_t*, uint32_t) override {}
+
+ private:
+  std::vector<uint64_t> parts_, off_;
+  uint64_t stride_, unit_ = 0;
+  uint32_t slots_;
+  std::vector<char*> arena_, blk_;
+};
+
+// Runs `work(i)` for i in [0, n) on `threads` threads.
+template <class F>
+void parallel_for(uint32_t n, int threads, F work) {
+  std::atomic<uint32_t> next{0};
+  std::vector<std::thread> th;
+  for (int t = 0; t < std::max(1, threads); ++t)
+    th.emplace_back([&] {
+      for (uint32_t i; (i = next.fetch_add(1)) < n;) work(i);
+    });
+  for (auto& t : th) t.join();
+}
+
+}  // namespace
+
+extern "C" {
+
+// The CPU baseline over `n_tokens` tokens of ids [n_tokens][G][n]: the same placement as refdg_open, then per token
+// begin_token, per gated layer the export mask, serve_demand (synchronous memcpy of every miss), a host XXH64 of every
+// landed unit against hashes[key], serve_use, issue_writebacks, and end_token, on the calling thread. The source file
+// holds unit `key` at unit_offset[key] (unit bytes contiguous). token_ms[t] = the token's wall time; out[] = misses,
+// fetched, evicted, writebacks_done, hash mismatches, bytes copied into slots (sums over the timed tokens).
+int refdg_cpu_baseline(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
+                       uint32_t spare_target, uint32_t wb_defer, uint32_t inclusive, const uint64_t* part_bytes,
+                       uint32_t n_parts, uint64_t host_stride, const uint32_t* order, uint32_t n_order,
+                       const char* path, const uint64_t* unit_offset, const uint64_t* hashes, const uint32_t* ids,
+                       uint32_t n, uint32_t n_tokens, int setup_threads, double* token_ms, uint64_t* out) {
+  try {
+    const std::vector<uint64_t> parts(part_bytes, part_bytes + n_parts);
+    uint64_t unit = 0;
+    for (uint64_t pb : parts) unit += pb;
+    const uint32_t slots = persistent + 2 * bank + 1;
+    Memcpy t(parts, host_stride, slots, blocks);
+    ts::DgConfig c;
+    c.n_units.assign(n_units, n_units + G);
+    c.persistent_slots = persistent;
+    c.bank_slots = bank;
+    c.blocks = blocks;
+    c.spare_target = spare_target;
+    c.prefetch_reserve = std::min<uint32_t>(24, spare_target / 4);
+    c.prefetch_per_layer = 4;
+    c.prefetch_per_token = 48;
+    c.wb_defer = wb_defer != 0;
+    c.inclusive = inclusive;
+    c.max_ids = bank;
+    c.pf_legacy = true;
+    ts::DgCore core(c, &t);
+    core.place(std::vector<uint32_t>(order, order + n_order));
+    // fill: every key's bytes into its home (a slot or a block), from the file; spare blocks and free slots touched
+    const int fd = ::open(path, O_RDONLY | O_CLOEXEC);
+    if (fd < 0) throw std::runtime_error(std::string("open ") + path);
+    const uint32_t keys = core.keys();
+    std::atomic<int> io_err{0};
+    parallel_for(keys, setup_threads, [&](uint32_t k) {
+      std::vector<char> buf;
+      const int32_t s = core.table()[k];
+      const int32_t b = core.block_of(k);
+      char* dst = b >= 0 ? t.block(b) : nullptr;
+      if (s >= 0) {
+        buf.resize(size_t(unit));
+        dst = buf.data();
+      }
+      if (!dst) return;
+      uint64_t got = 0;
+      while (got < unit) {
+        const ssize_t r = ::pread(fd, dst + got, size_t(unit - got), off_t(unit_offset[k] + got));
+        if (r <= 0) {
+          io_err = 1;
+          return;
+        }
+        got += uint64_t(r);
+      }
+      if (s >= 0)
+        for (uint32_t p = 0; p < n_parts; ++p) std::memcpy(t.slot(p, s), dst + t.part_offset(p), parts[p]);
+    });
+    ::close(fd);
+    if (io_err) throw std::runtime_error(std::string("short read of ") + path);
+    std::vector<uint8_t> used_slot(slots, 0);
+    for (uint32_t k = 0; k < keys; ++k)
+      if (core.table()[k] >= 0) used_slot[size_t(core.table()[k])] = 1;
+    std::vector<int32_t> used_block(size_t(blocks) + 1, 0);
+    for (uint32_t k = 0; k < keys; ++k)
+      if (core.block_of(k) >= 0) used_block[size_t(core.block_of(k)) + 1] = 1;
+    parallel_for(slots, setup_threads, [&](uint32_t s) {
+      if (!used_slot[s])
+        for (uint32_t p = 0; p < n_parts; ++p) std::memset(t.slot(p, int32_t(s)), 0, parts[p]);
+    });
+    parallel_for(blocks + 1, setup_threads, [&](uint32_t b) {
+      if (!used_block[b]) std::memset(t.block(int32_t(b) - 1), 0, host_stride);
+    });
+    // the timed tokens
+    const ts::DgStats s0 = core.stats();
+    uint64_t bad = 0, copied = 0;
+    for (uint32_t tok = 0; tok < n_tokens; ++tok) {
+      const auto t0 = std::chrono::steady_clock::now();
+      core.begin_token(tok + 1);
+      for (uint32_t g = 0; g < G; ++g) {
+        const uint32_t* x = ids + (size_t(tok) * G + g) * n;
+        uint64_t mask = 0;
+        for (uint32_t i = 0; i < n; ++i)
+          if (x[i] < core.units(g) && core.table()[core.key(g, x[i])] < 0) mask |= uint64_t(1) << i;
+        core.serve_demand(g, x, n, mask);
+        for (uint32_t i = 0; i < n; ++i) {
+          if (!(mask >> i & 1u)) continue;
+          const uint32_t k = core.key(g, x[i]);
+          const int32_t s = core.table()[k];
+          ts::Xxh64 h;
+          for (uint32_t p = 0; p < n_parts; ++p) h.update(t.slot(p, s), size_t(parts[p]));
+          bad += h.digest() != hashes[k];
+          copied += unit;
+        }
+        core.serve_use(g, x, n, mask);
+        if (core.deferred() && g + 1 < G) core.issue_writebacks(g, nullptr);
+      }
+      core.end_token({}, 1);
+      token_ms[tok] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    }
+    const ts::DgStats& s1 = core.stats();
+    out[0] = s1.misses - s0.misses;
+    out[1] = s1.fetched - s0.fetched;
+    out[2] = s1.evicted - s0.evicted;
+    out[3] = s1.writebacks_done - s0.writebacks_done;
+    out[4] = bad;
+    out[5] = copied;
+    return 0;
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "refdg_cpu_baseline: %s\n", e.what());
+    return 1;
+  }
+}
 
 }  // extern "C"

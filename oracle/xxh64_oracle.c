@@ -1,7 +1,7 @@
 /*
  * ORACLE (test infrastructure only): a CPU restatement of the reference's XXH64 and of the checkpoint layout the device
- * verifier uses. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and only as the
- * checker; the product never links or calls it.
+ * verifier uses. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and only to compare
+ * against; the product never links or calls it.
  *
  * xxh64: reference src/xxh64.cpp:39-112 (XXH64, seed 0, little-endian 64-bit lanes, 32-byte stripes into four
  * accumulators v = rotl(v + lane * P2, 31) * P1, merge of the four, length, tail by 8 / 4 / 1 bytes, avalanche).

@@ -2,7 +2,7 @@
 route stream through both; per step the stats, every layer's table (region + offset: identical up to base), and the
 checksum of every routed unit's bytes as the engine reads them through table_dev on the device. The reference's
 checksums are of the bytes its own table entries point at, and both must equal the oracle's checksum of the file.
-Shapes follow the BASELINE workloads at test size (reference tests/test_runtime.cpp:58-83 check the same things:
+Shapes follow the benchmark workloads at test size (reference tests/test_runtime.cpp:58-83 check the same things:
 table bytes == file bytes, stats balance)."""
 import numpy as np
 import pytest

@@ -75,6 +75,7 @@ def _declare(L: C.CDLL) -> None:
         "ss_last_error": (C.c_char_p, []),
         "ss_abi_version": (C.c_int, []),
         "tsa_xxh64_digest": (st, [vp, u32, vp, vp]),
+        "tsa_xxh64_host": (u64, [vp, u64]),
         "tsa_checkpoint_count": (u64, [C.POINTER(u64), u32, u64]),
         "tsa_xxh64_checkpoints": (st, [C.POINTER(TsaUnit), u64, C.POINTER(u64), u64, C.POINTER(u64)]),
         "tsa_xxh64_verify": (st, [vp, u32, u64, u64, vp, vp]),

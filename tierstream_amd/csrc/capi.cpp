@@ -64,7 +64,7 @@ void clear_reserved(ss_options& o) {
   o.reserved0 = o.reserved1 = o.reserved2 = o.reserved3 = o.reserved4 = o.reserved5 = o.reserved6 = o.reserved7 = 0;
 }
 
-// An input struct: this build's defaults, then min(struct_size, sizeof) bytes of the caller's.
+// An input struct: the library's defaults, then min(struct_size, sizeof) bytes of the caller's.
 template <class T>
 T versioned(const T* in, void (*defaults)(T*), const char* what) {
   T v;
@@ -410,6 +410,24 @@ ss_status tsa_test_dg_table(const ss_ctx* c, int32_t* out, uint32_t cap, uint32_
 uint64_t tsa_test_verify_failures(const ss_ctx* c) {
   if (!c) return 0;
   return c->dg ? c->dg->verify_failures() : c->host->verify_failures();
+}
+ss_status tsa_test_profile_enable(ss_ctx* c, int on) {
+  return guard([&] {
+    need(c != nullptr, "tsa_test_profile_enable: null context");
+    dg_of(c, "tsa_test_profile_enable").profile_enable(on != 0);
+  });
+}
+ss_status tsa_test_profile_read(ss_ctx* c, int wait, tsa_test_profile* out) {
+  return guard([&] {
+    need(c && out, "tsa_test_profile_read: null argument");
+    *out = dg_of(c, "tsa_test_profile_read").profile_read(wait != 0);
+  });
+}
+ss_status tsa_test_dg_stamps(const ss_ctx* c, uint64_t* out, uint32_t cap, uint32_t* n) {
+  return guard([&] {
+    need(c && n && (out || cap == 0), "tsa_test_dg_stamps: null argument");
+    *n = dg_of(c, "tsa_test_dg_stamps").stamps(out, cap);
+  });
 }
 
 }  // extern "C"

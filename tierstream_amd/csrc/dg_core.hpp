@@ -96,6 +96,7 @@ class DgCore {
   int32_t block_of(uint32_t k) const { return e_[k].block; }
   uint32_t free_slots() const { return uint32_t(free_slots_.size()); }
   uint32_t free_blocks() const { return uint32_t(free_blocks_.size()); }
+  const std::vector<int32_t>& free_block_ids() const { return free_blocks_; }  // the free stack, top last
   uint32_t on_device() const { return on_device_; }
   uint32_t backed_units() const { return backed_; }
   uint64_t outstanding_bytes() const { return outstanding_; }

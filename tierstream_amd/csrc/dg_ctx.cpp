@@ -16,12 +16,16 @@
 #include "hip_rt.hpp"
 #include "source.hpp"
 #include "tsa_device.hpp"
+#include "tierstream_amd/tsa_test.h"
 
 namespace tsa {
 namespace {
 
 using Clock = std::chrono::steady_clock;
-constexpr uint64_t kSegBytes = 64 * 1024;          // device-verify checkpoint spacing
+// device-verify checkpoint spacing: 8 KiB gives one 336 MiB unit 43,008 independent segments, one lane-quad each
+// (2,688 wavefronts), enough to keep every SIMD of the chip busy in one launch; the checkpoints cost 32 bytes per
+// segment (0.4 % of the unit) in HBM
+constexpr uint64_t kSegBytes = 8 * 1024;
 constexpr uint64_t kScatterBelow = 8ull << 20;     // parts smaller than this land staged + scattered
 
 uint64_t align64(uint64_t v) { return (v + 63) / 64 * 64; }
@@ -56,7 +60,7 @@ Layout make_layout(const Desc& d, const Plan& p, const ss_options& o) {
   if (o.dg_disk_tier || o.dg_disk_prefetch || o.dg_disk_staging || (o.dg_disk_queue && o.dg_disk_queue != 0xFFFFFFFFu) ||
       o.dg_landing_blocks || o.dg_landing_max_queued || o.dg_landing_ttl || o.dg_landing_chunk || o.dg_bank_keep ||
       o.dg_disk_queue_adapt)
-    refuse(SS_E_UNSUPPORTED, "the three-tier file path (dg_disk_tier and its options) is not in this build yet");
+    refuse(SS_E_UNSUPPORTED, "the three-tier file path (dg_disk_tier and its options) is not supported by this library yet");
   if (o.dg_no_admit || o.dg_pf_revert_unused || o.dg_pf_strict_admit || o.dg_prior_len || o.dg_prior ||
       o.dg_score_profile_len || o.dg_score_profile)
     refuse(SS_E_UNSUPPORTED, "dg_no_admit / dg_pf_revert_unused / dg_pf_strict_admit / priors / score profiles are "
@@ -200,6 +204,7 @@ class HipTransport final : public DgTransport {
     }
   }
   ~HipTransport() override {
+    if (vs_) (void)hipStreamSynchronize(vs_);
     for (auto& s : s_) {
       (void)hipStreamSynchronize(s);
       dev_->stream_destroy(s);
@@ -212,8 +217,11 @@ class HipTransport final : public DgTransport {
     }
     dev_->free_pinned(vtab_host_);
     dev_->free_device(vtab_dev_);
+    dev_->stream_destroy(vs_);
+    for (hipEvent_t e : vev_) dev_->event_destroy(e);
     dev_->free_pinned(vfail_host_);
     dev_->free_device(vfail_dev_);
+    for (hipEvent_t e : prof_events_) dev_->event_destroy(e);
   }
 
   hipStream_t stream(Stream s) const { return s_[s]; }
@@ -225,6 +233,11 @@ class HipTransport final : public DgTransport {
   }
 
   void h2d(Stream s, int32_t slot, int32_t block) override {
+    Timed t = prof_start(kProfCopy, x_.unit_bytes, 1, s_[s]);
+    h2d_unit(s, slot, block);
+    prof_end(t, s_[s]);
+  }
+  void h2d_unit(Stream s, int32_t slot, int32_t block) {
     const char* src = block_ptr(block);
     if (!scatter_) {  // one SDMA copy per part straight into its arena slot
       for (uint32_t p = 0; p < x_.part_bytes.size(); ++p)
@@ -248,12 +261,16 @@ class HipTransport final : public DgTransport {
     hip_check(hipError_t(launch_scatter(jobs_dev_[k] + j, 1, scatter_blocks_, s_[s])), "scatter launch");
   }
   void d2h(int32_t slot, int32_t block) override {
+    Timed t = prof_start(kProfWb, x_.unit_bytes, 1, s_[kD2h]);
     char* dst = block_ptr(block);
     for (uint32_t p = 0; p < x_.part_bytes.size(); ++p)
       copy_d2h(dst + x_.part_offset[p], slot_ptr(p, slot), x_.part_bytes[p], s_[kD2h]);
+    prof_end(t, s_[kD2h]);
   }
   void d2h_part(Stream s, int32_t slot, int32_t block, uint32_t p) override {
+    Timed t = prof_start(kProfWb, x_.part_bytes[p], 1, s_[s]);
     copy_d2h(block_ptr(block) + x_.part_offset[p], slot_ptr(p, slot), x_.part_bytes[p], s_[s]);
+    prof_end(t, s_[s]);
   }
   uint32_t parts() const override { return uint32_t(x_.part_bytes.size()); }
   uint64_t part_bytes(uint32_t p) const override { return x_.part_bytes[p]; }
@@ -292,6 +309,7 @@ class HipTransport final : public DgTransport {
     vfail_host_ = static_cast<uint32_t*>(dev_->alloc_pinned(4ull * vcap_, "verify results"));
     vfail_dev_ = static_cast<uint32_t*>(dev_->alloc_device(4ull * vcap_, "verify results"));
     hip_check(hipMemset(vfail_dev_, 0, 4ull * vcap_), "hipMemset");
+    vs_ = dev_->stream_create_dedicated();
   }
   void landed(Stream s, uint32_t g, const uint32_t* keys, const int32_t* slots, uint32_t n) override {
     (void)g;
@@ -313,14 +331,27 @@ class HipTransport final : public DgTransport {
       vkeys_.push_back(keys[i]);
     }
     vused_ += n;
-    copy_h2d(vtab_dev_ + first, vtab_host_ + first, sizeof(tsa_verify_unit) * n, s_[s]);
+    // the verify stream waits for these copies, so the check never holds up the next layer's copies on s
+    if (vev_used_ == vev_.size()) vev_.push_back(dev_->event_create());
+    hipEvent_t landed_ev = vev_[vev_used_++];
+    ev_record(landed_ev, s_[s]);
+    stream_wait(vs_, landed_ev);
+    copy_h2d(vtab_dev_ + first, vtab_host_ + first, sizeof(tsa_verify_unit) * n, vs_);
+    Timed t = prof_start(kProfVerify, uint64_t(n) * x_.unit_bytes, n, vs_);
     hip_check(hipError_t(launch_verify(vtab_dev_ + first, n, uint64_t(n) * n_ckpt_, kSegBytes, vfail_dev_ + first,
-                                       s_[s])),
+                                       vs_)),
               "device verify launch");
+    prof_end(t, vs_);
   }
-  // At the boundary (kDem / kPf synchronized): the keys whose landed bytes differ from their descriptor hash.
+  // Before the boundary may reuse a slot: every check of this token has read its bytes.
+  void verify_sync() {
+    if (vs_) stream_sync(vs_);
+  }
+  // At the boundary: the keys whose landed bytes differ from their descriptor hash.
   std::vector<uint32_t> collect_verify() {
     std::vector<uint32_t> bad;
+    verify_sync();
+    vev_used_ = 0;
     if (!verify_ || vused_ == 0) return bad;
     hip_check(hipMemcpy(vfail_host_, vfail_dev_, 4ull * vused_, hipMemcpyDeviceToHost), "hipMemcpy (verify)");
     for (uint32_t i = 0; i < vused_; ++i)
@@ -333,7 +364,101 @@ class HipTransport final : public DgTransport {
   }
   uint64_t verified() const { return verified_; }
 
+  // ---- timing (a test hook): timed events around unit copies, write-backs and verify launches ----
+  void profile_enable(bool on) {
+    std::lock_guard<std::mutex> lk(prof_mu_);
+    drain_locked(true);
+    prof_on_ = on;
+    prof_tot_ = tsa_test_profile{};
+  }
+  tsa_test_profile profile_read(bool wait) {
+    std::lock_guard<std::mutex> lk(prof_mu_);
+    drain_locked(wait);
+    tsa_test_profile out = prof_tot_;
+    out.pending = pending_.size();
+    return out;
+  }
+  void profile_collect() {  // completed brackets only; recycles their events
+    std::lock_guard<std::mutex> lk(prof_mu_);
+    drain_locked(false);
+  }
+
  private:
+  enum ProfKind : uint32_t { kProfCopy, kProfWb, kProfVerify };
+  struct Timed {
+    hipEvent_t a = nullptr, b = nullptr;
+    ProfKind kind = kProfCopy;
+    uint64_t bytes = 0;
+    uint32_t units = 0;
+  };
+  hipEvent_t take_event_locked() {
+    if (prof_free_.empty()) {
+      prof_events_.push_back(dev_->event_create_timed());
+      return prof_events_.back();
+    }
+    hipEvent_t e = prof_free_.back();
+    prof_free_.pop_back();
+    return e;
+  }
+  Timed prof_start(ProfKind k, uint64_t bytes, uint32_t units, hipStream_t s) {
+    Timed t;
+    std::lock_guard<std::mutex> lk(prof_mu_);
+    if (!prof_on_) return t;
+    t.a = take_event_locked();
+    t.b = take_event_locked();
+    t.kind = k;
+    t.bytes = bytes;
+    t.units = units;
+    ev_record(t.a, s);
+    return t;
+  }
+  void prof_end(const Timed& t, hipStream_t s) {
+    if (!t.a) return;
+    std::lock_guard<std::mutex> lk(prof_mu_);
+    ev_record(t.b, s);
+    pending_.push_back(t);
+  }
+  void drain_locked(bool wait) {
+    size_t keep = 0;
+    for (const Timed& t : pending_) {
+      if (wait) ev_sync(t.b);
+      else if (!ev_done(t.b)) {
+        pending_[keep++] = t;
+        continue;
+      }
+      float ms = 0.0f;
+      hip_check(hipEventElapsedTime(&ms, t.a, t.b), "hipEventElapsedTime");
+      const uint64_t ns = uint64_t(double(ms) * 1e6 + 0.5);
+      switch (t.kind) {
+        case kProfCopy:
+          ++prof_tot_.copies;
+          prof_tot_.copy_bytes += t.bytes;
+          prof_tot_.copy_ns += ns;
+          break;
+        case kProfWb:
+          ++prof_tot_.writebacks;
+          prof_tot_.writeback_bytes += t.bytes;
+          prof_tot_.writeback_ns += ns;
+          break;
+        case kProfVerify:
+          ++prof_tot_.verifies;
+          prof_tot_.verify_units += t.units;
+          prof_tot_.verify_bytes += t.bytes;
+          prof_tot_.verify_ns += ns;
+          break;
+      }
+      prof_free_.push_back(t.a);
+      prof_free_.push_back(t.b);
+    }
+    pending_.resize(keep);
+  }
+
+  std::mutex prof_mu_;  // the service thread brackets demand copies, the engine thread reads and the boundary's copies
+  bool prof_on_ = false;
+  tsa_test_profile prof_tot_{};
+  std::vector<Timed> pending_;
+  std::vector<hipEvent_t> prof_events_, prof_free_;
+
   HipDevice* dev_;
   const Layout& x_;
   std::vector<void*> arena_;
@@ -361,6 +486,9 @@ class HipTransport final : public DgTransport {
   uint32_t* vfail_dev_ = nullptr;
   std::vector<uint32_t> vkeys_;
   uint64_t verified_ = 0;
+  hipStream_t vs_ = nullptr;        // the verify stream (a hardware queue of its own)
+  std::vector<hipEvent_t> vev_;     // per landed batch of the token: its copies completed
+  size_t vev_used_ = 0;
 };
 
 // ---- the service thread ----------------------------------------------------------------------------------------------
@@ -624,8 +752,10 @@ class HipDgCtx final : public DgCtx {
       fail(SS_E_BACKEND, token_failure(dev, ""));
     }
     // 4. the boundary, then the device check of this token's landed units
+    tr_->verify_sync();  // the boundary may hand a landed slot to a write-back or a new copy
     core_->end_token();
     const std::vector<uint32_t> bad = tr_->collect_verify();
+    tr_->profile_collect();
     if (!bad.empty()) {
       verify_failures_ += bad.size();
       poisoned_ = true;
@@ -780,6 +910,22 @@ class HipDgCtx final : public DgCtx {
     return uint32_t(t.size());
   }
   uint64_t verify_failures() const override { return verify_failures_; }
+
+  void profile_enable(bool on) override {
+    require(!in_token_, SS_E_INVALID, "tsa_test_profile_enable: between tokens only");
+    tr_->profile_enable(on);
+  }
+  tsa_test_profile profile_read(bool wait) override {
+    require(!in_token_, SS_E_INVALID, "tsa_test_profile_read: between tokens only");
+    return tr_->profile_read(wait);
+  }
+  uint32_t stamps(uint64_t* out, uint32_t cap) const override {
+    require(!in_token_, SS_E_INVALID, "tsa_test_dg_stamps: between tokens only");
+    const uint32_t n = 4u * uint32_t(x_.gated.size());
+    if (out && cap)
+      hip_check(hipMemcpy(out, dw_.stamps, 8ull * std::min(n, cap), hipMemcpyDeviceToHost), "hipMemcpy (stamps)");
+    return n;
+  }
 
  private:
   static void launch_ck(int e, const char* what) { hip_check(hipError_t(e), what); }
@@ -954,8 +1100,10 @@ void HipDgCtx::init() {
   svc_->start();
 }
 
-// Open-time fill, in parallel: every key from its file into its home (a pinned block, or through a per-thread pinned
-// staging buffer into its arena slot). With verify_hash the unit's XXH64 is checked against the descriptor; with
+// Open-time fill, in parallel: every key from its file into its home. Units homed on the device are read into a free
+// spare block (the spare blocks hold nothing before the first write-back, so they serve as the fill's staging and
+// the fill pins no memory of its own; one per worker), then copied into their arena slot; the other units are read
+// straight into their pinned block. With verify_hash the unit's XXH64 is checked against the descriptor; with
 // verify_hash = 2 its checkpoints are kept in HBM for the device check of every later landing.
 void HipDgCtx::fill() {
   const uint32_t G = uint32_t(x_.gated.size());
@@ -971,31 +1119,36 @@ void HipDgCtx::fill() {
     ckpt_host.assign(size_t(uint64_t(x_.keys) * n_ckpt * 4), 0);
   }
   const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
-  const unsigned nthreads = std::min<unsigned>(16, std::max<unsigned>(1, std::min<unsigned>(hw, x_.keys)));
+  const unsigned max_threads = std::min<unsigned>(16, hw);
+  std::vector<uint32_t> dev_keys, host_keys;
+  for (uint32_t k = 0; k < x_.keys; ++k)
+    (core_->home(k) == DgCore::Home::Device ? dev_keys : host_keys).push_back(k);
+  const std::vector<int32_t> spare = core_->free_block_ids();
+  require(dev_keys.empty() || !spare.empty(), SS_E_CAPACITY, "device-gated: no free block to stage the fill through");
+  const std::vector<uint32_t>* keys = nullptr;
   std::atomic<uint32_t> next{0};
   std::mutex err_mu;
   std::string err;
   ss_status err_st = SS_OK;
-  auto work = [&]() {
-    void* stage = nullptr;
+  auto work = [&](char* stage) {
     hipStream_t st = nullptr;
     try {
       dev_->bind();
-      stage = dev_->alloc_pinned(x_.host_stride, "fill staging");
-      st = dev_->stream_create();
+      if (stage) st = dev_->stream_create();
       for (;;) {
-        const uint32_t k = next.fetch_add(1);
-        if (k >= x_.keys) break;
+        const uint32_t i = next.fetch_add(1);
+        if (i >= keys->size()) break;
         {
           std::lock_guard<std::mutex> lk(err_mu);
           if (err_st != SS_OK) break;
         }
+        const uint32_t k = (*keys)[i];
         const uint32_t g = core_->gated_of(k);
         const int L = x_.gated[g];
         const int u = int(k - x_.unit_base[g]);
         const Layer& l = d_.layers[size_t(L)];
         const bool on_dev = core_->home(k) == DgCore::Home::Device;
-        char* dst = on_dev ? static_cast<char*>(stage) : tr_->block_ptr(core_->block_of(k));
+        char* dst = on_dev ? stage : tr_->block_ptr(core_->block_of(k));
         for (size_t p = 0; p < l.parts.size(); ++p) {
           const Part& part = l.parts[p];
           const SourceFile& f = *files_[size_t(part.source)];
@@ -1051,11 +1204,17 @@ void HipDgCtx::fill() {
       }
     }
     if (st) dev_->stream_destroy(st);
-    dev_->free_pinned(stage);
   };
-  std::vector<std::thread> th;
-  for (unsigned i = 0; i < nthreads; ++i) th.emplace_back(work);
-  for (auto& t : th) t.join();
+  // phase 1: the device homes, one spare block per worker; phase 2: the block homes
+  for (int phase = 0; phase < 2 && err_st == SS_OK; ++phase) {
+    keys = phase == 0 ? &dev_keys : &host_keys;
+    next = 0;
+    const size_t cap = phase == 0 ? spare.size() : size_t(max_threads);
+    const unsigned n = unsigned(std::min<size_t>({size_t(max_threads), cap, keys->size()}));
+    std::vector<std::thread> th;
+    for (unsigned i = 0; i < n; ++i) th.emplace_back(work, phase == 0 ? tr_->block_ptr(spare[i]) : nullptr);
+    for (auto& t : th) t.join();
+  }
   if (err_st != SS_OK) fail(err_st, err);
   if (dverify) {
     hip_check(hipMemcpy(ckpt_dev_, ckpt_host.data(), ckpt_host.size() * 8, hipMemcpyHostToDevice),

@@ -7,6 +7,7 @@
 #include <memory>
 
 #include "model.hpp"
+#include "tierstream_amd/tsa_test.h"
 
 namespace tsa {
 
@@ -35,6 +36,10 @@ class DgCtx {
   virtual void stats_reset() = 0;
   virtual uint32_t host_table(int32_t* out, uint32_t cap) const = 0;
   virtual uint64_t verify_failures() const = 0;
+  // measurement hooks (tsa_test.h)
+  virtual void profile_enable(bool on) = 0;
+  virtual tsa_test_profile profile_read(bool wait) = 0;
+  virtual uint32_t stamps(uint64_t* out, uint32_t cap) const = 0;
 };
 
 std::unique_ptr<DgCtx> open_dg_ctx(const Desc& d, const Plan& p, const ss_options& o);

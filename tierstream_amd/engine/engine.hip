@@ -55,8 +55,9 @@ __global__ __launch_bounds__(kThreads) void checksum_table(const uint64_t* table
 
 // Device-gated: the slot from ss_dg_slot, then each part at base + slot * stride.
 __global__ __launch_bounds__(kThreads) void checksum_dg(ss_dg_device_view v, uint32_t g, const int32_t* ids,
-                                                        unsigned long long* out) {
+                                                        unsigned long long* out, unsigned long long* start) {
   __shared__ int32_t slot_s;
+  if (threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0) start[g] = wall_clock64();  // the layer's compute began
   if (threadIdx.x == 0) slot_s = ss_dg_slot(&v, g, ids[blockIdx.y]);
   __syncthreads();
   const int32_t slot = slot_s;
@@ -185,9 +186,20 @@ struct TseDg {
   hipStream_t s = nullptr;
   int32_t* ids_dev = nullptr;               // [G][64]
   unsigned long long* out_dev = nullptr;    // [G][64]
+  unsigned long long* start_dev = nullptr;  // [G]: wall clock at each layer's first checksum workgroup
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   ss_dg_device_view view{};
+
+  ~TseDg() {
+    if (s) (void)hipStreamSynchronize(s);
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    (void)hipFree(ids_dev);
+    (void)hipFree(out_dev);
+    (void)hipFree(start_dev);
+    if (s) (void)hipStreamDestroy(s);
+  }
 };
 
 static ss_status tse_enqueue_token(TseDg* e) {
@@ -197,7 +209,7 @@ static ss_status tse_enqueue_token(TseDg* e) {
     if (e->dg) TSE_CK(ss_dg_enqueue_wait(e->c, int(g), e->s));
     if (e->checksum) {
       hipLaunchKernelGGL(checksum_dg, dim3(e->max_chunks, e->n_ids), dim3(kThreads), 0, e->s, e->view, g,
-                         e->ids_dev + 64 * g, e->out_dev + 64 * g);
+                         e->ids_dev + 64 * g, e->out_dev + 64 * g, e->start_dev);
       TSE_HIP(hipGetLastError());
     }
   }
@@ -221,18 +233,18 @@ __attribute__((visibility("default"))) ss_status tse_dg_create(ss_ctx* c, uint32
     return st;
   }
   e->G = e->view.n_gated;
-  uint64_t unit = 0;
-  for (uint32_t p = 0; p < e->view.n_parts; ++p) unit += e->view.parts[p].bytes;
   uint32_t chunks = 0;
   for (uint32_t p = 0; p < e->view.n_parts; ++p) chunks += chunks_of(e->view.parts[p].bytes);
   e->max_chunks = chunks;
   if (hipStreamCreateWithFlags(&e->s, hipStreamNonBlocking) != hipSuccess ||
-      hipMalloc(&e->ids_dev, 4ull * 64 * e->G) != hipSuccess || hipMalloc(&e->out_dev, 8ull * 64 * e->G) != hipSuccess) {
+      hipMalloc(&e->ids_dev, 4ull * 64 * e->G) != hipSuccess || hipMalloc(&e->out_dev, 8ull * 64 * e->G) != hipSuccess ||
+      hipMalloc(&e->start_dev, 8ull * e->G) != hipSuccess) {
     delete e;
     return SS_E_NOMEM;
   }
   (void)hipMemset(e->out_dev, 0, 8ull * 64 * e->G);
   (void)hipMemset(e->ids_dev, 0, 4ull * 64 * e->G);
+  (void)hipMemset(e->start_dev, 0, 8ull * e->G);
   if (use_graph) {
     st = ck(hipStreamBeginCapture(e->s, hipStreamCaptureModeThreadLocal));
     if (st == SS_OK) {
@@ -278,16 +290,16 @@ __attribute__((visibility("default"))) ss_status tse_dg_token(void* h, const int
   return SS_OK;
 }
 
-__attribute__((visibility("default"))) void tse_dg_destroy(void* h) {
+// The last token's per-layer compute-start stamps (wall clock, 100 MHz ticks), [G].
+__attribute__((visibility("default"))) ss_status tse_dg_stamps(void* h, uint64_t* out) {
   TseDg* e = static_cast<TseDg*>(h);
-  if (!e) return;
-  (void)hipStreamSynchronize(e->s);
-  if (e->exec) (void)hipGraphExecDestroy(e->exec);
-  if (e->graph) (void)hipGraphDestroy(e->graph);
-  (void)hipFree(e->ids_dev);
-  (void)hipFree(e->out_dev);
-  (void)hipStreamDestroy(e->s);
-  delete e;
+  TSE_HIP(hipStreamSynchronize(e->s));
+  TSE_HIP(hipMemcpy(out, e->start_dev, 8ull * e->G, hipMemcpyDeviceToHost));
+  return SS_OK;
+}
+
+__attribute__((visibility("default"))) void tse_dg_destroy(void* h) {
+  delete static_cast<TseDg*>(h);
 }
 
 }  // extern "C"

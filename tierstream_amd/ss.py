@@ -112,6 +112,14 @@ DG_STAT_TAIL = [("cuda_module_loading", u32), ("reserved1", u32)] + [(n, u64) fo
      ("disk_depth_calibrations", u64)]
 
 
+class TsaTestProfile(C.Structure):
+    _fields_ = [(n, u64) for n in ("copies copy_bytes copy_ns writebacks writeback_bytes writeback_ns verifies "
+                                   "verify_units verify_bytes verify_ns pending").split()]
+
+    def as_dict(self):
+        return {n: int(getattr(self, n)) for n, _ in self._fields_}
+
+
 class SsDgStats(C.Structure):
     _fields_ = [("struct_size", u32), ("reserved0", u32)] + [(n, u64) for n in DG_STAT_U64] + DG_STAT_TAIL
 
@@ -167,6 +175,9 @@ def _declare() -> C.CDLL:
         "tsa_test_region_of": (st, [vp, u64, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(u64)]),
         "tsa_test_dg_table": (st, [vp, C.POINTER(i32), u32, C.POINTER(u32)]),
         "tsa_test_verify_failures": (u64, [vp]),
+        "tsa_test_profile_enable": (st, [vp, C.c_int]),
+        "tsa_test_profile_read": (st, [vp, C.c_int, C.POINTER(TsaTestProfile)]),
+        "tsa_test_dg_stamps": (st, [vp, C.POINTER(u64), u32, C.POINTER(u32)]),
         "tsa_xxh64_host": (u64, [vp, u64]),
     }
     for name, (res, args) in sigs.items():
@@ -195,6 +206,8 @@ def engine() -> C.CDLL:
         E.tse_dg_create.argtypes = [vp, u32, C.c_int, C.c_int, C.c_int, C.POINTER(vp)]
         E.tse_dg_token.restype = C.c_int
         E.tse_dg_token.argtypes = [vp, C.POINTER(i32), C.POINTER(u64), C.POINTER(C.c_double)]
+        E.tse_dg_stamps.restype = C.c_int
+        E.tse_dg_stamps.argtypes = [vp, C.POINTER(u64)]
         E.tse_dg_destroy.restype = None
         E.tse_dg_destroy.argtypes = [vp]
     return _engine
@@ -319,6 +332,26 @@ class Ctx:
         check(_declare().ss_dg_get_device_view_sized(self.h, C.byref(v), C.sizeof(v)))
         return v
 
+    def verify_failures(self) -> int:
+        return int(_declare().tsa_test_verify_failures(self.h))
+
+    def profile_enable(self, on: bool = True):
+        check(_declare().tsa_test_profile_enable(self.h, int(on)))
+
+    def profile_read(self, wait: bool = True) -> dict:
+        p = TsaTestProfile()
+        check(_declare().tsa_test_profile_read(self.h, int(wait), C.byref(p)))
+        return p.as_dict()
+
+    def dg_stamps(self) -> np.ndarray:
+        """uint64 [G][4] wall-clock ticks of the last token: export end, wait entry, ready seen, unused."""
+        L = _declare()
+        n = u32(0)
+        check(L.tsa_test_dg_stamps(self.h, None, 0, C.byref(n)))
+        out = np.zeros(n.value, dtype=np.uint64)
+        check(L.tsa_test_dg_stamps(self.h, out.ctypes.data_as(C.POINTER(u64)), n.value, C.byref(n)))
+        return out.reshape(-1, 4)
+
     def region_of(self, addr: int):
         k, i, off = C.c_int(), C.c_int(), u64()
         check(_declare().tsa_test_region_of(self.h, addr, C.byref(k), C.byref(i), C.byref(off)))
@@ -364,19 +397,17 @@ class DgEngine:
                              cks.ctypes.data_as(C.POINTER(u64)) if want_checksums else None, C.byref(ms)))
         return cks, ms.value
 
+    def stamps(self) -> np.ndarray:
+        """uint64 [G]: the last token's per-layer compute-start wall-clock ticks."""
+        out = np.zeros(self.G, dtype=np.uint64)
+        check(engine().tse_dg_stamps(self.h, out.ctypes.data_as(C.POINTER(u64))))
+        return out
+
     def close(self):
         if self.h:
             engine().tse_dg_destroy(self.h)
             self.h = None
 
 
-def word_checksum(b: np.ndarray) -> int:
-    """The engine's checksum of a unit's bytes: sum of little-endian u32 words x ((j mod 251) + 1), mod 2^64."""
-    w = np.frombuffer(np.ascontiguousarray(b).tobytes(), dtype="<u4").astype(np.uint64)
-    mult = (np.arange(w.size, dtype=np.uint64) % np.uint64(251)) + np.uint64(1)
-    with np.errstate(over="ignore"):
-        return int(np.sum(w * mult, dtype=np.uint64))
-
-
 __all__ = ["SsBudget", "SsOptions", "SsLayerStats", "SsDgStats", "Desc", "Plan", "Ctx", "DgEngine", "budget",
-           "options", "word_checksum", "SsError"]
+           "options", "SsError", "TsaTestProfile"]

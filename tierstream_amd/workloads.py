@@ -14,7 +14,7 @@ stride, the layers one after the other), a budget, options and a seeded route st
   qwen3-moe    48 layers x 128 experts, parts 2048 x 768 x 2 (3 MiB each) bf16; 32 tokens x top-8 per step (the route
                union per layer); exclusive with write-backs, ss_acquire_groups hits first; 25 % resident; 128 steps.
   deepseek-q4  58 layers x 256 experts, parts 7168 x 2048 in 18-byte Q4 blocks (8,257,536 bytes each); three tiers
-               (not served by this build: the file tier is next).
+               (not served yet: it needs the three-tier file path).
 
 Bytes come from the counter-based generator (tsa_synth on the GPU, the same words for uniform bytes as
 oracle/synth.py); each unit's XXH64 is computed on the host by the library (tsa_xxh64_host).
@@ -208,21 +208,42 @@ def unit_stride_dev(w: Workload) -> int:
     return (w.unit_bytes + 255) // 256 * 256
 
 
-def budget_numbers(w: Workload) -> dict:
-    """device_bytes / host_pinned_bytes that give the workload's resident fraction under the planner's rule."""
+@dataclass
+class DgShape:
+    """A device-gated workload's cache shape: R planned residents (the first units in model order: equal benefit), D
+    spare slots, B ids per layer (2 B + 1 bank and guard slots), P pinned homes, Q spare blocks, I clean copies."""
+    R: int
+    D: int
+    B: int
+    P: int
+    Q: int
+    I: int
+    budget: dict
+    options: dict
+
+
+def dg_shape(w: Workload) -> DgShape:
+    """The budget and options that give a device-gated workload its resident fraction. Units are ranked with equal
+    benefit, so the residents are the first R units in model order. Each layer contributes min(dynamic slots, its
+    non-resident units) spare slots; the ring is the 2 B + 1 bank and guard slots. dg_inclusive_blocks covers every unit
+    that can be on the device beyond the planned residents (D + 2 B), so evicting one is a drop (the inclusive intent;
+    device-gated mode runs the exclusive tier mode), and Q keeps 4 blocks beyond them for write-backs of evicted planned
+    residents."""
     st = unit_stride_dev(w)
-    n_res = int(round(w.resident_fraction * w.n_units))
-    margin = 2 * GiB
-    if w.forward == 1:
-        # device-gated: residents + spare slots + banks + guard (ring_slots = 2 B + 1), billed as resident + ring
-        ring = 2 * w.max_ids + 1
-        dyn = w.dynamic_slots or 1
-        dev = n_res * st + ring * st + dyn * w.layers * st + margin + 64 * MiB
-    else:
-        ring_slots = w.ring_slots or (2 * w.units)
-        dyn = w.dynamic_slots
-        dev = n_res * st + ring_slots * st + dyn * w.layers * st + margin + 64 * MiB
     hs = (w.unit_bytes + 4095) // 4096 * 4096
-    spares = w.spare_units or (min(64, w.n_units) if w.tier_mode == 1 else 0)
-    host = (w.n_units - n_res) * hs + spares * hs + 512 * MiB
-    return {"device_bytes": int(dev), "host_pinned_bytes": int(host), "n_resident": n_res}
+    R = int(round(w.resident_fraction * w.n_units))
+    B = w.max_ids
+    dyn = w.dynamic_slots or 1
+    res_in = [min(w.units, max(0, R - L * w.units)) for L in range(w.layers)]
+    D = sum(min(dyn, w.units - r) for r in res_in)
+    ring = 2 * B + 1
+    P = w.n_units - R
+    I = w.inclusive_blocks or (D + 2 * B)
+    Q = w.spare_units or (I + 4)
+    # the planner reserves min(dynamic slots, units) for every layer before it places residents (reference
+    # src/plan.cpp:60-64); the spare slots it bills afterwards (D) are what the residents leave
+    reserve = w.layers * min(dyn, w.units)
+    budget = dict(device_bytes=(R + reserve + ring) * st + st // 2, host_pinned_bytes=(P + Q) * hs + hs // 2,
+                  dynamic_slots_per_layer=dyn, ring_slots=ring, tier_mode=1, host_spare_units=Q)
+    options = dict(forward_mode=1, dg_max_ids=B, pin_planned=0, dg_inclusive_blocks=I, dg_wb_defer=1)
+    return DgShape(R, D, B, P, Q, I, budget, options)
