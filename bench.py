@@ -43,6 +43,10 @@ sys.path.insert(0, HERE)
 METRIC = "decode-step serve latency p50/p99; miss H2D GB/s and HBM GB/s vs roofline"
 HBM_PEAK_GBPS = 8000.0
 TICK_NS = 10.0  # wall_clock64 runs at 100 MHz on gfx950
+# HBM bytes one verify launch moves per unit it checks, keyed by unit bytes: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
+# on a launch of one unit of this shape, each scaled by the counter's reading for a copy kernel of known size (FETCH
+# 2.0, WRITE 1.0): 346,966 KiB fetched, nothing written (profiles/verify_kernel_mixtral_unit_pmc.md).
+VERIFY_TRAFFIC_PER_UNIT = {352321536: 346966 * 1024}
 
 
 def log(*a):
@@ -60,6 +64,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="target CPU time of the baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--workdir", default="", help="where the source file is written (default /dev/shm)")
+    ap.add_argument("--inclusive", type=int, default=0,
+                    help="dg_inclusive_blocks (clean copies; 0 = spare slots + banks); spare blocks = this + 4")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="only the copy peaks and the library's HBM kernels alone (no serve loop: for counter runs)")
     return ap.parse_args()
 
 
@@ -95,9 +103,37 @@ def measure_peaks(tsa, L, C):
         h2d = [n / timed(lambda: tsa.check(L.tsa_memcpy(dev, host, n, 0, s))) / 1e9 for _ in range(6)]
         d2h = [n / timed(lambda: tsa.check(L.tsa_memcpy(host, dev, n, 1, s))) / 1e9 for _ in range(4)]
         d2d = [2 * (2 * n) / timed(lambda: tsa.check(L.tsa_memcpy(dev2, dev, 2 * n, 2, s))) / 1e9 for _ in range(6)]
+        # both directions at once (a write-back beside a miss copy): host -> dev on s, dev2 -> host2 on s2
+        host2, s2, e2, e3 = C.c_void_p(), C.c_void_p(), C.c_void_p(), C.c_void_p()
+        tsa.check(L.tsa_host_alloc(C.byref(host2), n))
+        tsa.check(L.tsa_stream_create(C.byref(s2)))
+        tsa.check(L.tsa_event_create(C.byref(e2)))
+        tsa.check(L.tsa_event_create(C.byref(e3)))
+        bidir = []
+        try:
+            for _ in range(4):
+                tsa.check(L.tsa_device_sync())
+                tsa.check(L.tsa_event_record(e0, s))
+                tsa.check(L.tsa_event_record(e2, s2))
+                tsa.check(L.tsa_memcpy(dev, host, n, 0, s))
+                tsa.check(L.tsa_memcpy(host2, dev2, n, 1, s2))
+                tsa.check(L.tsa_event_record(e1, s))
+                tsa.check(L.tsa_event_record(e3, s2))
+                tsa.check(L.tsa_event_sync(e1))
+                tsa.check(L.tsa_event_sync(e3))
+                a, b = C.c_float(), C.c_float()
+                tsa.check(L.tsa_event_elapsed_ms(e0, e1, C.byref(a)))
+                tsa.check(L.tsa_event_elapsed_ms(e2, e3, C.byref(b)))
+                bidir.append((n / (a.value / 1e3) / 1e9, n / (b.value / 1e3) / 1e9))
+        finally:
+            L.tsa_event_destroy(e2)
+            L.tsa_event_destroy(e3)
+            L.tsa_stream_destroy(s2)
+            L.tsa_host_free(host2)
+        bi = max(bidir[1:], key=lambda x: x[0] + x[1])
         out = {"h2d_pinned_GBps": max(h2d[1:]), "h2d_pinned_GBps_median": float(np.median(h2d[1:])),
-               "d2h_pinned_GBps": max(d2h[1:]), "hbm_copy_GBps": max(d2d[1:]),
-               "pcie_gen5_x16_GBps": 64.0, "hbm_peak_GBps": HBM_PEAK_GBPS}
+               "d2h_pinned_GBps": max(d2h[1:]), "bidir_h2d_GBps": bi[0], "bidir_d2h_GBps": bi[1],
+               "hbm_copy_GBps": max(d2d[1:]), "pcie_gen5_x16_GBps": 64.0, "hbm_peak_GBps": HBM_PEAK_GBPS}
     finally:
         L.tsa_event_destroy(e0)
         L.tsa_event_destroy(e1)
@@ -105,6 +141,87 @@ def measure_peaks(tsa, L, C):
         L.tsa_free(dev)
         L.tsa_free(dev2)
         L.tsa_host_free(host)
+    return out
+
+
+def measure_kernels(tsa, L, C, w, seg=8192, reps=10):
+    """The library's HBM kernels alone at the workload's unit shape: the device XXH64 verify of one unit (checkpoints
+    every `seg` bytes, computed on the host) and the unit scatter used as a plain copy of known size (one part of
+    256 MiB: read 256 MiB, write 256 MiB), whose counters calibrate the traffic counters of the others."""
+    parts = w.parts
+    ub = w.unit_bytes
+    bufs = []
+    out = {}
+    s, e0, e1 = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    tsa.check(L.tsa_stream_create(C.byref(s)))
+    tsa.check(L.tsa_event_create(C.byref(e0)))
+    tsa.check(L.tsa_event_create(C.byref(e1)))
+
+    def dev_alloc(n):
+        b = tsa.DeviceBuffer(n)
+        bufs.append(b)
+        return b
+
+    def timed(fn, n=reps):
+        ms = []
+        fn()
+        tsa.check(L.tsa_stream_sync(s))
+        for _ in range(n):
+            tsa.check(L.tsa_event_record(e0, s))
+            fn()
+            tsa.check(L.tsa_event_record(e1, s))
+            tsa.check(L.tsa_event_sync(e1))
+            t = C.c_float()
+            tsa.check(L.tsa_event_elapsed_ms(e0, e1, C.byref(t)))
+            ms.append(t.value)
+        return float(np.median(ms)) / 1e3
+
+    try:
+        # verify: one unit, its parts in separate HBM arrays as in the arena
+        pbufs = [dev_alloc(pb) for pb in parts]
+        for p, (b, pb) in enumerate(zip(pbufs, parts)):
+            tsa.check(L.tsa_synth(C.c_void_p(b.ptr), pb, 77, p, 0, 1, C.c_float(0.02), None))
+        tsa.check(L.tsa_device_sync())
+        states, digest = tsa.host_checkpoints([b.download(pb) for b, pb in zip(pbufs, parts)], seg)
+        n_ck = states.size // 4
+        st_dev = dev_alloc(states.nbytes)
+        st_dev.upload(states)
+        vu = tsa.TsaVerifyUnit()
+        for p, (b, pb) in enumerate(zip(pbufs, parts)):
+            vu.ext[p].ptr = b.ptr
+            vu.ext[p].bytes = pb
+        vu.n_ext, vu.seg_first, vu.states, vu.digest, vu.total = len(parts), 0, st_dev.ptr, digest, ub
+        tab = dev_alloc(C.sizeof(vu))
+        tab.upload(np.frombuffer(bytes(vu), dtype=np.uint8))
+        fail = dev_alloc(64)
+        fail.upload(np.zeros(16, dtype=np.uint32))
+        t = timed(lambda: tsa.check(L.tsa_xxh64_verify(C.c_void_p(tab.ptr), 1, n_ck, seg, C.c_void_p(fail.ptr), s)))
+        bad = int(fail.download(4, dtype=np.uint32)[0])
+        out["verify"] = {"unit_bytes": ub, "seg_bytes": seg, "segments": n_ck, "us": round(t * 1e6, 1),
+                         "GBps": round(ub / t / 1e9, 1), "frac_of_hbm_peak": round(ub / t / 1e9 / HBM_PEAK_GBPS, 4),
+                         "fail_word": bad}
+        # the scatter kernel as a plain copy: one part of 256 MiB
+        n = 256 << 20
+        src, dst = dev_alloc(n), dev_alloc(n)
+        job = tsa.TsaScatterJob()
+        job.src = src.ptr
+        job.dst[0] = dst.ptr
+        job.bytes[0] = n
+        job.n_parts = 1
+        job.block_first = 0
+        pb_arr = (C.c_uint64 * 1)(n)
+        nblk = int(L.tsa_scatter_blocks(pb_arr, 1))
+        jdev = dev_alloc(C.sizeof(job))
+        jdev.upload(np.frombuffer(bytes(job), dtype=np.uint8))
+        t = timed(lambda: tsa.check(L.tsa_scatter(C.c_void_p(jdev.ptr), 1, nblk, s)))
+        out["copy_kernel"] = {"kernel": "scatter_kernel (one 256 MiB part)", "bytes_read": n, "bytes_written": n,
+                              "us": round(t * 1e6, 1), "GBps": round(2 * n / t / 1e9, 1)}
+    finally:
+        for b in bufs:
+            b.close()
+        L.tsa_event_destroy(e0)
+        L.tsa_event_destroy(e1)
+        L.tsa_stream_destroy(s)
     return out
 
 
@@ -153,7 +270,15 @@ def main():
         raise SystemExit(f"bench.py: workload {a.workload} is not device-gated")
     if a.part_bytes:
         w = W.scaled(w, part_bytes=a.part_bytes)
+    if a.inclusive:
+        w = W.scaled(w, inclusive_blocks=a.inclusive, spare_units=a.inclusive + 4)
     shape = W.dg_shape(w)
+    if a.kernels_only:
+        kern = measure_kernels(tsa, L, C, w)
+        log(f"kernels {kern}")
+        peaks = measure_peaks(tsa, L, C)
+        print(json.dumps({"kernels_only": True, "workload": w.name, "kernels": kern, "peaks": peaks}), flush=True)
+        return
     base = a.workdir or ("/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir())
     work = tempfile.mkdtemp(prefix="tsa_bench_", dir=base)
     path = os.path.join(work, "weights.bin")
@@ -228,6 +353,8 @@ def main():
         d.close()
         peaks = measure_peaks(tsa, L, C)
         log(f"peaks {peaks}")
+        kern = measure_kernels(tsa, L, C, w)
+        log(f"kernels {kern}")
 
         copy_gbps = prof["copy_bytes"] / prof["copy_ns"] if prof["copy_ns"] else None
         ver_gbps = prof["verify_bytes"] / prof["verify_ns"] if prof["verify_ns"] else None
@@ -264,10 +391,17 @@ def main():
                     "frac_of_pcie_gen5_x16": round(copy_gbps / 64.0, 3) if copy_gbps else None},
             "roofline": {"bound": "hbm", "kernel": "verify_kernel (device XXH64 of every landed unit)",
                          "achieved": round(ver_gbps, 1) if ver_gbps else None, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                         "frac": round(ver_gbps / HBM_PEAK_GBPS, 4) if ver_gbps else None, "traffic": None,
+                         "frac": round(ver_gbps / HBM_PEAK_GBPS, 4) if ver_gbps else None,
+                         "traffic": int(VERIFY_TRAFFIC_PER_UNIT[w.unit_bytes] * prof["verify_units"] /
+                                        max(prof["verifies"], 1)) if w.unit_bytes in VERIFY_TRAFFIC_PER_UNIT else None,
                          "launches": prof["verifies"], "units": prof["verify_units"],
                          "bytes_per_launch": prof["verify_bytes"] // max(prof["verifies"], 1),
-                         "mean_launch_us": round(prof["verify_ns"] / max(prof["verifies"], 1) / 1e3, 2)},
+                         "mean_launch_us": round(prof["verify_ns"] / max(prof["verifies"], 1) / 1e3, 2),
+                         "note": "live: each launch checks a layer's landed units while the layer's compute reads "
+                                 "HBM beside it; standalone figure under kernels.verify"},
+            "kernels": kern,
+            "pcie": {k: round(peaks[k], 2) for k in ("h2d_pinned_GBps", "d2h_pinned_GBps", "bidir_h2d_GBps",
+                                                    "bidir_d2h_GBps")},
             "hbm_copy_GBps": round(peaks["hbm_copy_GBps"], 1),
             "wait": {"zero_miss_layer_us_p50": round(pct(zero_gap, 50), 2) if zero_gap else None,
                      "zero_miss_layer_us_p99": round(pct(zero_gap, 99), 2) if zero_gap else None,

@@ -32,6 +32,7 @@ def lib() -> C.CDLL:
             "ss_last_error": (C.c_char_p, []),
             "ss_desc_from_json": (st, [C.c_char_p, C.c_size_t, C.POINTER(vp)]),
             "ss_desc_free": (None, [vp]),
+            "ss_desc_to_json": (st, [vp, C.POINTER(C.c_char_p), C.POINTER(C.c_size_t)]),
             "ss_desc_n_layers": (C.c_int, [vp]),
             "ss_desc_layer_units": (C.c_int, [vp, C.c_int]),
             "ss_desc_unit_bytes": (u64, [vp, C.c_int]),
@@ -78,14 +79,48 @@ def _ck(st):
         raise RuntimeError(f"reference status {st}: {lib().ss_last_error().decode()}")
 
 
-def plan_json(desc_json: str, budget) -> dict:
+def desc_roundtrip(desc_json: str) -> dict:
+    """The reference's canonical JSON of a descriptor (ss_desc_from_json, then ss_desc_to_json)."""
+    import json
+    L = lib()
+    d = vp()
+    b = desc_json.encode()
+    _ck(L.ss_desc_from_json(b, len(b), C.byref(d)))
+    try:
+        s, n = C.c_char_p(), C.c_size_t()
+        _ck(L.ss_desc_to_json(d, C.byref(s), C.byref(n)))
+        out = json.loads(C.string_at(s, n.value).decode())
+        L.ss_free(s)
+        return out
+    finally:
+        L.ss_desc_free(d)
+
+
+def plan_status(desc_json: str, budget, benefit=None) -> int:
+    """The reference's status for planning (0 = a plan was made)."""
+    L = lib()
+    d, p = vp(), vp()
+    b = desc_json.encode()
+    _ck(L.ss_desc_from_json(b, len(b), C.byref(d)))
+    try:
+        ben = (C.c_double * len(benefit))(*benefit) if benefit is not None else None
+        st = L.ss_plan_make(d, C.byref(budget), ben, len(benefit) if benefit is not None else 0, C.byref(p))
+        if st == 0:
+            L.ss_plan_free(p)
+        return st
+    finally:
+        L.ss_desc_free(d)
+
+
+def plan_json(desc_json: str, budget, benefit=None) -> dict:
     import json
     L = lib()
     d, p = vp(), vp()
     b = desc_json.encode()
     _ck(L.ss_desc_from_json(b, len(b), C.byref(d)))
     try:
-        _ck(L.ss_plan_make(d, C.byref(budget), None, 0, C.byref(p)))
+        ben = (C.c_double * len(benefit))(*benefit) if benefit is not None else None
+        _ck(L.ss_plan_make(d, C.byref(budget), ben, len(benefit) if benefit is not None else 0, C.byref(p)))
         s, n = C.c_char_p(), C.c_size_t()
         _ck(L.ss_plan_to_json(p, C.byref(s), C.byref(n)))
         out = json.loads(C.string_at(s, n.value).decode())

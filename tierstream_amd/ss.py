@@ -243,6 +243,16 @@ class Desc:
         check(L.ss_desc_from_json(b, len(b), C.byref(self.h)))
         self.n_layers = L.ss_desc_n_layers(self.h)
 
+    def json(self) -> dict:
+        """The canonical descriptor JSON (ss_desc_to_json)."""
+        import json as _json
+        L = _declare()
+        s, n = C.c_char_p(), C.c_size_t()
+        check(L.ss_desc_to_json(self.h, C.byref(s), C.byref(n)))
+        out = _json.loads(C.string_at(s, n.value).decode())
+        L.ss_free(s)
+        return out
+
     def units(self, layer):
         return _declare().ss_desc_layer_units(self.h, layer)
 
@@ -256,10 +266,11 @@ class Desc:
 
 
 class Plan:
-    def __init__(self, desc: Desc, b: SsBudget):
+    def __init__(self, desc: Desc, b: SsBudget, benefit=None):
         L = _declare()
         self.h = vp()
-        check(L.ss_plan_make(desc.h, C.byref(b), None, 0, C.byref(self.h)))
+        ben = (C.c_double * len(benefit))(*benefit) if benefit is not None else None
+        check(L.ss_plan_make(desc.h, C.byref(b), ben, len(benefit) if benefit is not None else 0, C.byref(self.h)))
         self.desc = desc
 
     def tiers(self):

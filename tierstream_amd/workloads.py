@@ -87,8 +87,11 @@ WORKLOADS = {
                           steps=64, ring_slots=0),
     "dense-prefix": Workload("dense-prefix", 32, 1, [4096 * 4096 * 7 * BF16], kind="blob", top_k=1, gen=1,
                              order="prefix", resident_fraction=12 / 32, layer_all=True, steps=32),
+    # 36 clean copies in 40 spare blocks: 154 + 40 pinned blocks of 336 MiB (63.7 GiB) stay under the 65 GiB of
+    # hipHostMalloc memory one process can hold on the measured MI355X host
     "mixtral": Workload("mixtral", 32, 8, [4096 * 14336 * BF16] * 3, top_k=2, routes="zipf", zipf_s=1.1, gen=1,
-                        resident_fraction=0.4, tier_mode=1, forward=1, steps=256),
+                        resident_fraction=0.4, tier_mode=1, forward=1, steps=256, inclusive_blocks=36,
+                        spare_units=40),
     "qwen3-moe": Workload("qwen3-moe", 48, 128, [2048 * 768 * BF16] * 3, top_k=8, tokens=32, routes="zipf",
                           zipf_s=1.1, gen=1, resident_fraction=0.25, tier_mode=1, groups=True, steps=128,
                           dynamic_slots=8),
