@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "strix_stream/ss.h"
+#include "tierstream/ts.h"
 #include "tierstream_amd/tsa_test.h"
 
 namespace {
@@ -288,6 +289,73 @@ __attribute__((visibility("default"))) ss_status tse_dg_token(void* h, const int
       for (uint32_t i = 0; i < e->n_ids; ++i) checksums[size_t(g) * e->n_ids + i] = out[64 * g + i];
   }
   return SS_OK;
+}
+
+// ss_dg_slot / ts_dg_slot on the device over a synthetic view (no context): slot_of[n_keys], unit_base[n_gated + 1],
+// the guard slot, an abort word and an absent_err word (with_absent = 0: the view has no absent_err). Query i resolves
+// id[i] of gated layer g[i] (every g[i] < n_gated); out_ss / out_ts get both results, *absent the absent_err word.
+__global__ void slot_probe(ss_dg_device_view v, const uint32_t* g, const int32_t* id, uint32_t n, int32_t* out_ss,
+                           int32_t* out_ts) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out_ss[i] = ss_dg_slot(&v, g[i], id[i]);
+  out_ts[i] = ts_dg_slot(&v, g[i], id[i]);
+}
+
+__attribute__((visibility("default"))) ss_status tse_slot_probe(const int32_t* slot_of, uint32_t n_keys,
+                                                                const uint32_t* unit_base, uint32_t n_gated,
+                                                                uint32_t guard, uint32_t aborted, int with_absent,
+                                                                const uint32_t* g, const int32_t* id, uint32_t n,
+                                                                int32_t* out_ss, int32_t* out_ts, uint32_t* absent) {
+  for (uint32_t i = 0; i < n; ++i)
+    if (g[i] >= n_gated) return SS_E_INVALID;
+  for (uint32_t k = 0; k <= n_gated; ++k)
+    if (unit_base[k] > n_keys || (k && unit_base[k] < unit_base[k - 1])) return SS_E_INVALID;
+  int32_t *d_slot = nullptr, *d_id = nullptr, *d_ss = nullptr, *d_ts = nullptr;
+  uint32_t *d_base = nullptr, *d_g = nullptr, *d_words = nullptr;
+  ss_status st = SS_OK;
+  if (hipMalloc(&d_slot, 4ull * (n_keys ? n_keys : 1)) != hipSuccess || hipMalloc(&d_base, 4ull * (n_gated + 1)) != hipSuccess ||
+      hipMalloc(&d_g, 4ull * n) != hipSuccess || hipMalloc(&d_id, 4ull * n) != hipSuccess ||
+      hipMalloc(&d_ss, 4ull * n) != hipSuccess || hipMalloc(&d_ts, 4ull * n) != hipSuccess ||
+      hipMalloc(&d_words, 8) != hipSuccess)
+    st = SS_E_NOMEM;
+  const uint32_t words[2] = {aborted, 0};
+  if (st == SS_OK) {
+    st = ck(hipMemcpy(d_slot, slot_of, 4ull * n_keys, hipMemcpyHostToDevice));
+    if (st == SS_OK) st = ck(hipMemcpy(d_base, unit_base, 4ull * (n_gated + 1), hipMemcpyHostToDevice));
+    if (st == SS_OK) st = ck(hipMemcpy(d_g, g, 4ull * n, hipMemcpyHostToDevice));
+    if (st == SS_OK) st = ck(hipMemcpy(d_id, id, 4ull * n, hipMemcpyHostToDevice));
+    if (st == SS_OK) st = ck(hipMemcpy(d_words, words, 8, hipMemcpyHostToDevice));
+  }
+  if (st == SS_OK) {
+    ss_dg_device_view v;
+    std::memset(&v, 0, sizeof v);
+    v.struct_size = uint32_t(sizeof v);
+    v.protocol = SS_DG_PROTOCOL;
+    v.n_gated = n_gated;
+    v.guard_slot = guard;
+    v.slots = guard + 1;
+    v.slot_of = d_slot;
+    v.unit_base = d_base;
+    v.abort = d_words;
+    v.absent_err = with_absent ? d_words + 1 : nullptr;
+    hipLaunchKernelGGL(slot_probe, dim3((n + 63) / 64), dim3(64), 0, nullptr, v, d_g, d_id, n, d_ss, d_ts);
+    st = ck(hipGetLastError());
+    if (st == SS_OK) st = ck(hipDeviceSynchronize());
+    if (st == SS_OK) st = ck(hipMemcpy(out_ss, d_ss, 4ull * n, hipMemcpyDeviceToHost));
+    if (st == SS_OK) st = ck(hipMemcpy(out_ts, d_ts, 4ull * n, hipMemcpyDeviceToHost));
+    uint32_t back[2] = {0, 0};
+    if (st == SS_OK) st = ck(hipMemcpy(back, d_words, 8, hipMemcpyDeviceToHost));
+    if (absent) *absent = back[1];
+  }
+  (void)hipFree(d_slot);
+  (void)hipFree(d_base);
+  (void)hipFree(d_g);
+  (void)hipFree(d_id);
+  (void)hipFree(d_ss);
+  (void)hipFree(d_ts);
+  (void)hipFree(d_words);
+  return st;
 }
 
 // The last token's per-layer compute-start stamps (wall clock, 100 MHz ticks), [G].
