@@ -371,14 +371,9 @@ bool DgCore::fetch(uint32_t g, uint32_t unit, bool prefetch) {
   }
   const DgTransport::Stream s = prefetch ? DgTransport::kPf : DgTransport::kDem;
   // the slot's last write-back and the block's incoming write-back (if still copying) come first
-  if (slot_ev_[size_t(slot)]) {
-    t_->wait(s, slot_ev_[size_t(slot)]);
-    detach(slot_ev_, slot);
-  }
-  if (block_ev_[size_t(x.block)]) {
-    t_->wait(s, block_ev_[size_t(x.block)]);
-    detach(block_ev_, x.block);
-  }
+  t_->wait_copy_in(s, slot, x.block, slot_ev_[size_t(slot)], block_ev_[size_t(x.block)]);
+  detach(slot_ev_, slot);
+  detach(block_ev_, x.block);
   t_->h2d(s, slot, x.block);
   write_entry(s, k, slot);
   --on_host_;

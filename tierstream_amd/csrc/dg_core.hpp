@@ -39,6 +39,14 @@ class DgTransport {
   virtual void sync(Stream s) = 0;
   virtual bool query(void* ev) = 0;  // non-blocking: the event's last record has completed
   virtual void upload_table(const int32_t* table, uint32_t n) = 0;  // the whole table on kDem, then sync
+  // Before h2d(s, slot, block): slot_ev / block_ev (either may be null) are the write-backs that may still read the
+  // slot or write the block. The default makes s wait for both; a transport that tracks its copies per part may let
+  // each part of the next h2d wait only for the same part of those write-backs.
+  virtual void wait_copy_in(Stream s, int32_t slot, int32_t block, void* slot_ev, void* block_ev) {
+    (void)slot, (void)block;
+    if (slot_ev) wait(s, slot_ev);
+    if (block_ev) wait(s, block_ev);
+  }
   // Units just copied in (key, slot) on stream s (a layer's demand copies after its ready, or one prefetch): a
   // transport that verifies landed bytes enqueues the check here (default: nothing).
   virtual void landed(Stream s, uint32_t g, const uint32_t* keys, const int32_t* slots, uint32_t n) {

@@ -190,6 +190,7 @@ class HipTransport final : public DgTransport {
       : dev_(dev), x_(x), arena_(std::move(arena)), slot_of_(slot_of_dev), ready_(ready_dev),
         chunks_(std::move(block_chunks)), per_chunk_(blocks_per_chunk), kJobRing(max_copies + 8) {
     for (auto& s : s_) s = dev_->stream_create_dedicated();
+    part_ev_.assign((size_t(x_.slots) + size_t(x_.blocks)) * x_.part_bytes.size(), nullptr);
     stage_host_ = static_cast<int32_t*>(dev_->alloc_pinned(4ull * x_.keys, "slot table upload stage"));
     bool small = false;
     for (uint64_t pb : x_.part_bytes) small = small || pb < kScatterBelow;
@@ -219,6 +220,7 @@ class HipTransport final : public DgTransport {
     dev_->free_device(vtab_dev_);
     dev_->stream_destroy(vs_);
     for (hipEvent_t e : vev_) dev_->event_destroy(e);
+    for (hipEvent_t e : part_ev_) dev_->event_destroy(e);
     dev_->free_pinned(vfail_host_);
     dev_->free_device(vfail_dev_);
     for (hipEvent_t e : prof_events_) dev_->event_destroy(e);
@@ -232,21 +234,40 @@ class HipTransport final : public DgTransport {
     return static_cast<char*>(arena_[p]) + uint64_t(slot) * x_.part_bytes[p];
   }
 
+  // A write-back's parts are separate copies (one arena per part), so each part's copy records its own events on
+  // the slot it read and the block it wrote; the next copy into that slot waits part by part: part p of the new unit
+  // starts once part p of the old one is out, instead of once the whole unit is.
+  void wait_copy_in(Stream s, int32_t slot, int32_t block, void* slot_ev, void* block_ev) override {
+    (void)s;
+    wait_slot_ = slot_ev ? slot : -1;
+    wait_block_ = block_ev ? block : -1;
+  }
   void h2d(Stream s, int32_t slot, int32_t block) override {
-    Timed t = prof_start(kProfCopy, x_.unit_bytes, 1, s_[s]);
     h2d_unit(s, slot, block);
-    prof_end(t, s_[s]);
+    wait_slot_ = wait_block_ = -1;
+  }
+  void part_wait(Stream s, int32_t slot, int32_t block, uint32_t p) {
+    if (slot >= 0 && slot == wait_slot_) stream_wait(s_[s], part_ev_[part_ev_index(false, slot, p)]);
+    if (block >= 0 && block == wait_block_) stream_wait(s_[s], part_ev_[part_ev_index(true, block, p)]);
   }
   void h2d_unit(Stream s, int32_t slot, int32_t block) {
     const char* src = block_ptr(block);
-    if (!scatter_) {  // one SDMA copy per part straight into its arena slot
-      for (uint32_t p = 0; p < x_.part_bytes.size(); ++p)
+    const uint32_t P = uint32_t(x_.part_bytes.size());
+    if (!scatter_) {  // one SDMA copy per part straight into its arena slot (timed after its wait: engine busy time)
+      for (uint32_t p = 0; p < P; ++p) {
+        part_wait(s, slot, block, p);
+        Timed t = prof_start(kProfCopy, x_.part_bytes[p], p == 0 ? 1 : 0, s_[s]);
         copy_h2d(slot_ptr(p, slot), src + x_.part_offset[p], x_.part_bytes[p], s_[s]);
+        prof_end(t, s_[s]);
+      }
       return;
     }
     // small parts: the whole unit in one SDMA copy to the stream's HBM staging, then one kernel writes every part
     const int k = s == kPf ? 1 : 0;
+    for (uint32_t p = 0; p < P; ++p) part_wait(s, -1, block, p);  // the staging copy reads every part of the block
+    Timed t = prof_start(kProfCopy, x_.unit_bytes, 1, s_[s]);
     copy_h2d(stage_dev_[k], src, x_.unit_bytes, s_[s]);
+    for (uint32_t p = 0; p < P; ++p) part_wait(s, slot, -1, p);   // the scatter writes every part of the slot
     const uint32_t j = job_next_[k]++ % kJobRing;
     tsa_scatter_job& job = jobs_host_[k][j];
     std::memset(&job, 0, sizeof job);
@@ -259,18 +280,33 @@ class HipTransport final : public DgTransport {
     job.block_first = 0;
     copy_h2d(jobs_dev_[k] + j, &job, sizeof job, s_[s]);
     hip_check(hipError_t(launch_scatter(jobs_dev_[k] + j, 1, scatter_blocks_, s_[s])), "scatter launch");
+    prof_end(t, s_[s]);
   }
   void d2h(int32_t slot, int32_t block) override {
     Timed t = prof_start(kProfWb, x_.unit_bytes, 1, s_[kD2h]);
     char* dst = block_ptr(block);
-    for (uint32_t p = 0; p < x_.part_bytes.size(); ++p)
+    for (uint32_t p = 0; p < x_.part_bytes.size(); ++p) {
       copy_d2h(dst + x_.part_offset[p], slot_ptr(p, slot), x_.part_bytes[p], s_[kD2h]);
+      mark_part(kD2h, slot, block, p);
+    }
     prof_end(t, s_[kD2h]);
   }
   void d2h_part(Stream s, int32_t slot, int32_t block, uint32_t p) override {
     Timed t = prof_start(kProfWb, x_.part_bytes[p], 1, s_[s]);
     copy_d2h(block_ptr(block) + x_.part_offset[p], slot_ptr(p, slot), x_.part_bytes[p], s_[s]);
+    mark_part(s, slot, block, p);
     prof_end(t, s_[s]);
+  }
+  // events of the last write-back copy of (slot, part) and into (block, part)
+  size_t part_ev_index(bool block, int32_t i, uint32_t p) const {
+    const size_t P = x_.part_bytes.size();
+    return (block ? size_t(x_.slots) * P : 0) + size_t(i) * P + p;
+  }
+  void mark_part(Stream s, int32_t slot, int32_t block, uint32_t p) {
+    for (size_t i : {part_ev_index(false, slot, p), part_ev_index(true, block, p)}) {
+      if (!part_ev_[i]) part_ev_[i] = dev_->event_create();
+      ev_record(part_ev_[i], s_[s]);
+    }
   }
   uint32_t parts() const override { return uint32_t(x_.part_bytes.size()); }
   uint64_t part_bytes(uint32_t p) const override { return x_.part_bytes[p]; }
@@ -431,7 +467,7 @@ class HipTransport final : public DgTransport {
       const uint64_t ns = uint64_t(double(ms) * 1e6 + 0.5);
       switch (t.kind) {
         case kProfCopy:
-          ++prof_tot_.copies;
+          prof_tot_.copies += t.units;  // a unit's first part counts the unit
           prof_tot_.copy_bytes += t.bytes;
           prof_tot_.copy_ns += ns;
           break;
@@ -486,6 +522,8 @@ class HipTransport final : public DgTransport {
   uint32_t* vfail_dev_ = nullptr;
   std::vector<uint32_t> vkeys_;
   uint64_t verified_ = 0;
+  std::vector<hipEvent_t> part_ev_;  // [slots + blocks][parts]: the last write-back copy of each part (lazily made)
+  int32_t wait_slot_ = -1, wait_block_ = -1;  // the next h2d waits per part on these (wait_copy_in)
   hipStream_t vs_ = nullptr;        // the verify stream (a hardware queue of its own)
   std::vector<hipEvent_t> vev_;     // per landed batch of the token: its copies completed
   size_t vev_used_ = 0;
