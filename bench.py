@@ -18,8 +18,9 @@ Beside it:
              host-to-device peak measured in the same run (2 GiB hipMemcpyAsync from hipHostMalloc memory)
   roofline   the device XXH64 verify kernel (the dominant kernel of the library): unit bytes hashed per launch over
              its mean launch time (timed events on the stream it runs on), against the 8 TB/s HBM peak
-  wait       the zero-miss layer wait on the device timeline: from the export kernel's end to the layer's compute
-             start when the layer had no miss (wall-clock stamps, 10 ns), and the miss layers' wait for their copies
+  wait       the zero-miss layer wait on the device timeline (wall-clock stamps, 10 ns): the wait kernel's own entry
+             to exit, and from the export kernel's end to the layer's compute start with the two kernel dispatch gaps
+             either side of the wait; and the miss layers' wait for their copies
   cpu_baseline  the reference DgCore (compiled from the reference sources) on a synchronous memcpy transport over host
              memory with a host XXH64 of every landed unit, one thread, over a bounded sample of the same tokens
 Checks at full size: no unit fails its device hash check, and every routed unit's checksum is the same each time it
@@ -177,7 +178,8 @@ def measure_kernels(tsa, L, C, w, seg=8192, reps=10):
         return float(np.median(ms)) / 1e3
 
     try:
-        # verify: one unit, its parts in separate HBM arrays as in the arena
+        # verify: one unit in slot 0 of a one-slot arena (its parts in separate HBM arrays, as in the context), checked
+        # by the same kernel the serve loop runs (tsa_xxh64_verify_slots)
         pbufs = [dev_alloc(pb) for pb in parts]
         for p, (b, pb) in enumerate(zip(pbufs, parts)):
             tsa.check(L.tsa_synth(C.c_void_p(b.ptr), pb, 77, p, 0, 1, C.c_float(0.02), None))
@@ -186,20 +188,21 @@ def measure_kernels(tsa, L, C, w, seg=8192, reps=10):
         n_ck = states.size // 4
         st_dev = dev_alloc(states.nbytes)
         st_dev.upload(states)
-        vu = tsa.TsaVerifyUnit()
+        dg_dev = dev_alloc(8)
+        dg_dev.upload(np.array([digest], dtype=np.uint64))
+        av = tsa.TsaArenaVerify()
         for p, (b, pb) in enumerate(zip(pbufs, parts)):
-            vu.ext[p].ptr = b.ptr
-            vu.ext[p].bytes = pb
-        vu.n_ext, vu.seg_first, vu.states, vu.digest, vu.total = len(parts), 0, st_dev.ptr, digest, ub
-        tab = dev_alloc(C.sizeof(vu))
-        tab.upload(np.frombuffer(bytes(vu), dtype=np.uint8))
+            av.arena[p] = b.ptr
+            av.part_bytes[p] = pb
+        av.n_parts, av.seg_bytes, av.states_dev, av.digests_dev = len(parts), seg, st_dev.ptr, dg_dev.ptr
+        keys, slots = (C.c_uint32 * 1)(0), (C.c_int32 * 1)(0)
         fail = dev_alloc(64)
         fail.upload(np.zeros(16, dtype=np.uint32))
-        t = timed(lambda: tsa.check(L.tsa_xxh64_verify(C.c_void_p(tab.ptr), 1, n_ck, seg, C.c_void_p(fail.ptr), s)))
+        t = timed(lambda: tsa.check(L.tsa_xxh64_verify_slots(C.byref(av), keys, slots, 1, C.c_void_p(fail.ptr), s)))
         bad = int(fail.download(4, dtype=np.uint32)[0])
-        out["verify"] = {"unit_bytes": ub, "seg_bytes": seg, "segments": n_ck, "us": round(t * 1e6, 1),
-                         "GBps": round(ub / t / 1e9, 1), "frac_of_hbm_peak": round(ub / t / 1e9 / HBM_PEAK_GBPS, 4),
-                         "fail_word": bad}
+        out["verify"] = {"kernel": "dg_verify_kernel", "unit_bytes": ub, "seg_bytes": seg, "segments": n_ck,
+                         "us": round(t * 1e6, 1), "GBps": round(ub / t / 1e9, 1),
+                         "frac_of_hbm_peak": round(ub / t / 1e9 / HBM_PEAK_GBPS, 4), "fail_word": bad}
         # the scatter kernel as a plain copy: one part of 256 MiB
         n = 256 << 20
         src, dst = dev_alloc(n), dev_alloc(n)
@@ -331,7 +334,10 @@ def main():
         prof = ctx.profile_read(wait=True)
         log(f"timed {steps} tokens in {wall:.2f} s: p50 {pct(lat, 50):.2f} ms p99 {pct(lat, 99):.2f} ms; {prof}")
         # the probe tokens: device stamps per layer
-        zero_gap, miss_wait, zero_wait_kernel = [], [], []
+        # stamps per gated layer: export end, wait entry, ready seen (0: no miss), wait exit; and the engine's compute
+        # start. A zero-miss layer: the wait kernel's own time (entry -> exit), the dispatch gaps either side of it,
+        # and export end -> compute start (what the engine sees).
+        zero_gap, zero_wait_kernel, gap_in, gap_out, miss_wait = [], [], [], [], []
         ctx.profile_enable(False)
         for i in range(probe):
             t = warm + steps + i
@@ -339,9 +345,13 @@ def main():
             check_cks(t, cks)
             st = ctx.dg_stamps().astype(np.int64)
             start = eng.stamps().astype(np.int64)
+            us = TICK_NS / 1e3
             for g in range(G):
-                if st[g, 1] == 0:
-                    zero_gap.append((start[g] - st[g, 0]) * TICK_NS / 1e3)
+                if st[g, 2] == 0:
+                    zero_gap.append((start[g] - st[g, 0]) * us)
+                    zero_wait_kernel.append((st[g, 3] - st[g, 1]) * us)
+                    gap_in.append((st[g, 1] - st[g, 0]) * us)
+                    gap_out.append((start[g] - st[g, 3]) * us)
                 else:
                     miss_wait.append((st[g, 2] - st[g, 1]) * TICK_NS / 1e6)
         dstat = {k: s1[k] - s0[k] for k in ("tokens", "lookups", "misses", "fetched", "evicted", "bank_serves",
@@ -389,7 +399,7 @@ def main():
                     "pinned_peak_GBps": round(peaks["h2d_pinned_GBps"], 2),
                     "frac_of_pinned_peak": round(copy_gbps / peaks["h2d_pinned_GBps"], 3) if copy_gbps else None,
                     "frac_of_pcie_gen5_x16": round(copy_gbps / 64.0, 3) if copy_gbps else None},
-            "roofline": {"bound": "hbm", "kernel": "verify_kernel (device XXH64 of every landed unit)",
+            "roofline": {"bound": "hbm", "kernel": "dg_verify_kernel (device XXH64 of every landed unit)",
                          "achieved": round(ver_gbps, 1) if ver_gbps else None, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(ver_gbps / HBM_PEAK_GBPS, 4) if ver_gbps else None,
                          "traffic": int(VERIFY_TRAFFIC_PER_UNIT[w.unit_bytes] * prof["verify_units"] /
@@ -397,14 +407,19 @@ def main():
                          "launches": prof["verifies"], "units": prof["verify_units"],
                          "bytes_per_launch": prof["verify_bytes"] // max(prof["verifies"], 1),
                          "mean_launch_us": round(prof["verify_ns"] / max(prof["verifies"], 1) / 1e3, 2),
-                         "note": "live: each launch checks a layer's landed units while the layer's compute reads "
-                                 "HBM beside it; standalone figure under kernels.verify"},
+                         "note": "live: each launch checks the units a layer's copies landed, before the layer's ready word "
+                                 "(the engine's compute of the layer waits for it); standalone figure under "
+                                 "kernels.verify"},
             "kernels": kern,
             "pcie": {k: round(peaks[k], 2) for k in ("h2d_pinned_GBps", "d2h_pinned_GBps", "bidir_h2d_GBps",
                                                     "bidir_d2h_GBps")},
             "hbm_copy_GBps": round(peaks["hbm_copy_GBps"], 1),
-            "wait": {"zero_miss_layer_us_p50": round(pct(zero_gap, 50), 2) if zero_gap else None,
+            "wait": {"zero_miss_wait_kernel_us_p50": round(pct(zero_wait_kernel, 50), 2) if zero_gap else None,
+                     "zero_miss_wait_kernel_us_p99": round(pct(zero_wait_kernel, 99), 2) if zero_gap else None,
+                     "zero_miss_layer_us_p50": round(pct(zero_gap, 50), 2) if zero_gap else None,
                      "zero_miss_layer_us_p99": round(pct(zero_gap, 99), 2) if zero_gap else None,
+                     "zero_miss_dispatch_gaps_us_p50": [round(pct(gap_in, 50), 2), round(pct(gap_out, 50), 2)]
+                     if zero_gap else None,
                      "zero_miss_samples": len(zero_gap),
                      "miss_layer_wait_ms_p50": round(pct(miss_wait, 50), 3) if miss_wait else None,
                      "miss_samples": len(miss_wait)},

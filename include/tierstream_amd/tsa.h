@@ -9,6 +9,8 @@
  *  - tsa_scatter: the per-part copies of a device-gated miss into each part's arena slot (reference
  *    src/dg_ctx.cpp:163-168) as one staged copy plus a kernel that writes every part with 128-bit stores.
  *  - tsa_xxh64_checkpoints: the host side of tsa_xxh64_verify (the four XXH64 accumulators at segment starts).
+ *  - tsa_xxh64_verify_slots: the same check for units landed in a device-gated arena, addressed by (key, slot) with
+ *    the arguments passed by value (the check a device-gated context runs before each layer's ready word).
  *
  * Every pointer named *_dev is device memory; every launch is asynchronous on `stream` (a hipStream_t, NULL = the
  * null stream) and allocates nothing. Return: SS_OK, SS_E_INVALID (argument checks, done on the host before any
@@ -67,6 +69,24 @@ typedef struct tsa_verify_unit {
  * n_segments = the units' checkpoint counts summed; seg_bytes as for the checkpoints. The caller zeroes fail_dev. */
 SS_API ss_status tsa_xxh64_verify(const tsa_verify_unit* units_dev, uint32_t n_units, uint64_t n_segments,
                                   uint64_t seg_bytes, uint32_t* fail_dev, void* stream);
+
+/* Units laid out as a device-gated arena: part p of the unit in slot s at arena[p] + s x part_bytes[p] (every arena
+ * pointer 8-byte aligned, every part_bytes a multiple of 8, every part but the last a multiple of 32); key k's
+ * checkpoints (its parts as the extents, tsa_xxh64_checkpoints) at states_dev + k x count x 4, its digest at
+ * digests_dev[k]. */
+typedef struct tsa_arena_verify {
+  const void* arena[TSA_MAX_EXTENTS];
+  uint64_t part_bytes[TSA_MAX_EXTENTS];
+  uint32_t n_parts;
+  uint32_t reserved;
+  uint64_t seg_bytes;
+  const uint64_t* states_dev;
+  const uint64_t* digests_dev;
+} tsa_arena_verify;
+/* fail_dev[i] |= 1 when unit (keys[i], slots[i]) differs from its checkpoints and digest. keys and slots are host
+ * arrays of n entries (any n: launches of up to 64 units each). The caller zeroes fail_dev. */
+SS_API ss_status tsa_xxh64_verify_slots(const tsa_arena_verify* a, const uint32_t* keys, const int32_t* slots, uint32_t n,
+                                        uint32_t* fail_dev, void* stream);
 
 /* One staged unit: src_dev holds the unit's bytes back to back; part p goes to dst[p] (parts[p] bytes). Every pointer
  * 16-byte aligned, every part a multiple of 16 bytes. block_first: prefix sum of the jobs' 16 KiB blocks. */

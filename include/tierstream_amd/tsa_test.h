@@ -41,8 +41,11 @@ SS_API ss_status tsa_test_profile_enable(ss_ctx* c, int on);
 /* Between tokens; wait = 1 first waits for every bracketed operation (write-backs may still run after ss_end). */
 SS_API ss_status tsa_test_profile_read(ss_ctx* c, int wait, tsa_test_profile* out);
 /* Between tokens: the device-gated kernels' wall-clock stamps of the last token (100 MHz ticks), 4 per gated layer:
- * export end, wait entry (0: the layer had no miss, the wait returned at once), ready seen, unused. *n = 4 G. */
+ * export end, wait entry, ready seen (0: the layer had no miss and the wait returned at once), wait exit. *n = 4 G. */
 SS_API ss_status tsa_test_dg_stamps(const ss_ctx* c, uint64_t* out, uint32_t cap, uint32_t* n);
+/* Between tokens: flips byte `offset` of unit (gated, unit)'s copy in its pinned block (the unit must live in its block,
+ * off the device), so that its next landing fails the device check (verify_hash = 2). SS_E_INVALID otherwise. */
+SS_API ss_status tsa_test_dg_corrupt_block(ss_ctx* c, int gated, int unit, uint64_t offset);
 
 #ifdef __cplusplus
 }

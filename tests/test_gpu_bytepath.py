@@ -90,7 +90,7 @@ def _verify(gpu, ext_groups, states_list, digests, seg):
     return fail.download(4 * len(units)).view(np.uint32)
 
 
-@pytest.mark.parametrize("seg", [1024, 65536])
+@pytest.mark.parametrize("seg", [1024, 1536, 8192, 65536])
 def test_verify_checkpoint_parallel(gpu, oracle, seg):
     rng = np.random.default_rng(seg)
     shapes = [[1 << 20] * 3, [(1 << 18) + 32 * 5, 4096, 1000], [31], [0], [32 * 3 + 5], [1 << 16, 1 << 16]]
@@ -120,6 +120,55 @@ def test_verify_checkpoint_parallel(gpu, oracle, seg):
     gpu.check(gpu.lib().tsa_stream_sync(None))
     res = _verify(gpu, ext_groups, states, digests, seg)
     assert [int(x != 0) for x in res] == [1, 1, 0, 0, 0, 0]
+
+
+@pytest.mark.parametrize("parts,seg", [([64 * 1024] * 3, 8192), ([2048, 4096 + 32, 1000], 1024), ([96], 1024)])
+def test_verify_slots_arena(gpu, oracle, parts, seg):
+    """tsa_xxh64_verify_slots (the device-gated check): keys in arena slots, by value; against the oracle's
+    checkpoints and XXH64; then one flipped byte fails only its unit."""
+    rng = np.random.default_rng(len(parts) * seg + parts[0])
+    slots_n, keys_n = 6, 5
+    arena = [gpu.DeviceBuffer(slots_n * pb) for pb in parts]
+    data = {k: [rng.integers(0, 256, pb, dtype=np.uint8) for pb in parts] for k in range(keys_n)}
+    placed = {0: 3, 2: 0, 4: 5, 1: 1}  # key -> slot
+    for k, sl in placed.items():
+        for p, (buf, pb) in enumerate(zip(arena, parts)):
+            buf.upload(data[k][p], sl * pb)
+    n_ck = len(oracle.checkpoints(data[0], seg)[0]) // 4
+    states = np.zeros((keys_n, n_ck, 4), dtype=np.uint64)
+    digests = np.zeros(keys_n, dtype=np.uint64)
+    for k in range(keys_n):
+        st, dg = oracle.checkpoints(data[k], seg)
+        states[k] = st.reshape(n_ck, 4)
+        digests[k] = dg
+        assert dg == xxhash.xxh64_intdigest(b"".join(a.tobytes() for a in data[k]))
+    st_dev = gpu.DeviceBuffer(states.nbytes)
+    st_dev.upload(states)
+    dg_dev = gpu.DeviceBuffer(digests.nbytes)
+    dg_dev.upload(digests)
+    a = gpu.TsaArenaVerify()
+    for p, (buf, pb) in enumerate(zip(arena, parts)):
+        a.arena[p] = buf.ptr
+        a.part_bytes[p] = pb
+    a.n_parts, a.seg_bytes, a.states_dev, a.digests_dev = len(parts), seg, st_dev.ptr, dg_dev.ptr
+    keys = (C.c_uint32 * len(placed))(*placed.keys())
+    slots = (C.c_int32 * len(placed))(*placed.values())
+    fail = gpu.DeviceBuffer(4 * len(placed))
+
+    def run():
+        fail.upload(np.zeros(len(placed), dtype=np.uint32))
+        gpu.check(gpu.lib().tsa_xxh64_verify_slots(C.byref(a), keys, slots, len(placed), C.c_void_p(fail.ptr), None))
+        gpu.check(gpu.lib().tsa_stream_sync(None))
+        return list(fail.download(4 * len(placed)).view(np.uint32))
+
+    assert run() == [0] * len(placed)
+    # key 4 (slot 5): flip a byte of its last part's last byte; key 2 (slot 0): its first part's first byte
+    last = len(parts) - 1
+    one = np.array([255 - data[4][last][-1]], dtype=np.uint8)
+    arena[last].upload(one, 5 * parts[last] + parts[last] - 1)
+    assert run() == [0, 0, 1, 0]
+    arena[0].upload(np.array([255 - data[2][0][0]], dtype=np.uint8), 0)
+    assert run() == [0, 1, 1, 0]
 
 
 def test_scatter_parts(gpu):

@@ -127,3 +127,38 @@ def test_zero_miss_token_needs_no_copy(tmp_path, gpu):
     finally:
         eng.close()
         ctx.close()
+
+
+def test_device_check_gates_a_corrupted_unit(tmp_path, gpu):
+    """verify_hash = 2 gates what the engine reads: a unit whose pinned copy was corrupted lands, its device check
+    fails, and the check raises the token's abort before the layer's ready word. Every read of the token from then on
+    resolves to the zeroed guard slot (checksum 0), the layers before it read their true bytes, the token fails with
+    SS_E_HASH naming the unit, and the context is poisoned."""
+    m, bkw, okw = _setup(tmp_path, 4, 8, [64 * KiB] * 3, 12, 1, 6, 2)
+    d = ss.Desc(m.desc_json())
+    plan = ss.Plan(d, ss.budget(**bkw))
+    ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(**okw))
+    eng = ss.DgEngine(ctx, 2, use_graph=True)
+    try:
+        table = ctx.dg_table().reshape(4, 8)
+        on_dev = [[u for u in range(8) if table[L, u] >= 0] for L in range(4)]
+        off_dev = [u for u in range(8) if table[2, u] < 0]
+        assert all(len(r) >= 2 for r in on_dev[:2]) and off_dev, table
+        bad = off_dev[0]
+        ctx.dg_corrupt_block(2, bad, 4097)
+        routes = np.array([on_dev[0][:2], on_dev[1][:2], [bad, (bad + 1) % 8], [0, 1]], dtype=np.int32)
+        st, cks, _ = eng.token_status(routes)
+        assert st == 7, st  # SS_E_HASH
+        import tierstream_amd as tsa
+        msg = tsa.lib().ss_last_error().decode()
+        assert "differ from the descriptor hash" in msg and f"first gated (2, {bad})" in msg, msg
+        for L in range(2):
+            for i, u in enumerate(routes[L]):
+                assert int(cks[L, i]) == fixtures.engine_checksum(m.unit_data(L, int(u))), (L, i)
+        assert not cks[2:].any(), cks  # the guard slot from the failed check on
+        assert ctx.verify_failures() == 1
+        with pytest.raises(ss.SsError):
+            eng.token(routes)  # poisoned
+    finally:
+        eng.close()
+        ctx.close()

@@ -49,6 +49,12 @@ class TsaVerifyUnit(C.Structure):
                 ("seg_first", C.c_uint64), ("states", C.c_void_p), ("digest", C.c_uint64), ("total", C.c_uint64)]
 
 
+class TsaArenaVerify(C.Structure):
+    _fields_ = [("arena", C.c_void_p * TSA_MAX_EXTENTS), ("part_bytes", C.c_uint64 * TSA_MAX_EXTENTS),
+                ("n_parts", C.c_uint32), ("reserved", C.c_uint32), ("seg_bytes", C.c_uint64),
+                ("states_dev", C.c_void_p), ("digests_dev", C.c_void_p)]
+
+
 class TsaScatterJob(C.Structure):
     _fields_ = [("src", C.c_void_p), ("dst", C.c_void_p * TSA_MAX_EXTENTS), ("bytes", C.c_uint64 * TSA_MAX_EXTENTS),
                 ("n_parts", C.c_uint32), ("reserved", C.c_uint32), ("block_first", C.c_uint64)]
@@ -79,6 +85,7 @@ def _declare(L: C.CDLL) -> None:
         "tsa_checkpoint_count": (u64, [C.POINTER(u64), u32, u64]),
         "tsa_xxh64_checkpoints": (st, [C.POINTER(TsaUnit), u64, C.POINTER(u64), u64, C.POINTER(u64)]),
         "tsa_xxh64_verify": (st, [vp, u32, u64, u64, vp, vp]),
+        "tsa_xxh64_verify_slots": (st, [vp, C.POINTER(u32), C.POINTER(i32), u32, vp, vp]),
         "tsa_scatter_blocks": (u64, [C.POINTER(u64), u32]),
         "tsa_scatter": (st, [vp, u32, u64, vp]),
         "tsa_synth": (st, [vp, u64, u64, u64, u64, u32, C.c_float, vp]),

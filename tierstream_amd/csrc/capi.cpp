@@ -429,5 +429,11 @@ ss_status tsa_test_dg_stamps(const ss_ctx* c, uint64_t* out, uint32_t cap, uint3
     *n = dg_of(c, "tsa_test_dg_stamps").stamps(out, cap);
   });
 }
+ss_status tsa_test_dg_corrupt_block(ss_ctx* c, int gated, int unit, uint64_t offset) {
+  return guard([&] {
+    need(c != nullptr, "tsa_test_dg_corrupt_block: null context");
+    dg_of(c, "tsa_test_dg_corrupt_block").corrupt_block(gated, unit, offset);
+  });
+}
 
 }  // extern "C"

@@ -401,13 +401,13 @@ bool DgCore::fetch(uint32_t g, uint32_t unit, bool prefetch) {
     ++lc_[g].prefetched;
     ++pf_layer_[g];
     ++pf_token_;
-    t_->landed(s, g, &k, &slot, 1);
   } else {
     ++st_.fetched;
     ++lc_[g].fetched;
-    landed_keys_.push_back(k);
-    landed_slots_.push_back(slot);
   }
+  // each unit as soon as its copies are issued: a transport that checks landed bytes checks this unit while the
+  // layer's next miss is still copying
+  t_->landed(s, g, &k, &slot, 1);
   return true;
 }
 
@@ -449,8 +449,6 @@ void DgCore::serve_demand(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t 
     require(ids[i] < nu, SS_E_INVALID,
             "device-gated: layer " + std::to_string(g) + " exported id " + std::to_string(ids[i]) + " of " +
                 std::to_string(nu));
-  landed_keys_.clear();
-  landed_slots_.clear();
   // per masked occurrence in export order: a repeated id is fetched at its first occurrence, covered at the others
   for (uint32_t i = 0; i < n; ++i) {
     if (!(mask >> i & 1u)) continue;
@@ -461,9 +459,8 @@ void DgCore::serve_demand(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t 
       fetch(g, ids[i], false);
     }
   }
+  // after every fetch's landed(): a transport that checks landed units orders the ready word behind the checks
   if (mask) t_->signal_ready(g, seq_);
-  if (!landed_keys_.empty())
-    t_->landed(DgTransport::kDem, g, landed_keys_.data(), landed_slots_.data(), uint32_t(landed_keys_.size()));
 }
 
 void DgCore::serve_use(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask) {

@@ -29,7 +29,7 @@ class DgTransport {
   virtual uint32_t parts() const = 0;
   virtual uint64_t part_bytes(uint32_t part) const = 0;
   virtual void write_entry(Stream s, uint32_t key, int32_t v) = 0;  // slot_of[key] = v after s's earlier work
-  virtual void signal_ready(uint32_t g, uint32_t seq) = 0;          // ready[g] = seq on kDem, after its copies
+  virtual void signal_ready(uint32_t g, uint32_t seq) = 0;  // ready[g] = seq after the layer's copies (and landed())
   virtual void* event_create() = 0;
   virtual void event_destroy(void* ev) = 0;
   virtual void record(void* ev, Stream s) = 0;
@@ -47,8 +47,8 @@ class DgTransport {
     if (slot_ev) wait(s, slot_ev);
     if (block_ev) wait(s, block_ev);
   }
-  // Units just copied in (key, slot) on stream s (a layer's demand copies after its ready, or one prefetch): a
-  // transport that verifies landed bytes enqueues the check here (default: nothing).
+  // Units just copied in (key, slot) on stream s: one call per fetch, right after its copies (a demand's before the
+  // layer's signal_ready). A transport that verifies landed bytes enqueues the check here (default: nothing).
   virtual void landed(Stream s, uint32_t g, const uint32_t* keys, const int32_t* slots, uint32_t n) {
     (void)s, (void)g, (void)keys, (void)slots, (void)n;
   }
@@ -191,8 +191,6 @@ class DgCore {
   uint32_t pf_token_ = 0, seq_ = 0, pred_layer_ = kNone;
   std::vector<uint8_t> layer_missed_;
   std::vector<uint32_t> pred_, uniq_, victims_;
-  std::vector<uint32_t> landed_keys_;
-  std::vector<int32_t> landed_slots_;
   std::vector<void*> event_pool_, all_events_;
   std::vector<void*> slot_ev_, block_ev_;        // a write-back still copying out of the slot / into the block
   std::unordered_map<void*, int> ev_refs_;      // attachments of each such event

@@ -216,8 +216,7 @@ class HipTransport final : public DgTransport {
       dev_->free_pinned(jobs_host_[k]);
       dev_->free_device(jobs_dev_[k]);
     }
-    dev_->free_pinned(vtab_host_);
-    dev_->free_device(vtab_dev_);
+    dev_->free_device(digests_dev_);
     dev_->stream_destroy(vs_);
     for (hipEvent_t e : vev_) dev_->event_destroy(e);
     for (hipEvent_t e : part_ev_) dev_->event_destroy(e);
@@ -313,8 +312,17 @@ class HipTransport final : public DgTransport {
   void write_entry(Stream s, uint32_t key, int32_t v) override {
     hip_check(hipStreamWriteValue32(s_[s], slot_of_ + key, uint32_t(v), 0), "hipStreamWriteValue32 (slot entry)");
   }
+  // ready[g] = seq after the layer's demand copies (and cover waits) on kDem; with device verify on the verify stream,
+  // behind the checks of every unit landed so far in the token (its stream order).
   void signal_ready(uint32_t g, uint32_t seq) override {
-    hip_check(hipStreamWriteValue32(s_[kDem], ready_ + g, seq, 0), "hipStreamWriteValue32 (ready)");
+    hipStream_t on = s_[kDem];
+    if (verify_) {
+      hipEvent_t ev = next_vev();
+      ev_record(ev, s_[kDem]);
+      stream_wait(vs_, ev);
+      on = vs_;
+    }
+    hip_check(hipStreamWriteValue32(on, ready_ + g, seq, 0), "hipStreamWriteValue32 (ready)");
   }
   void* event_create() override { return dev_->event_create(); }
   void event_destroy(void* ev) override { dev_->event_destroy(static_cast<hipEvent_t>(ev)); }
@@ -334,50 +342,59 @@ class HipTransport final : public DgTransport {
   }
 
   // ---- device verify of landed units (verify_hash = 2) ----
-  void enable_verify(const std::vector<uint64_t>& digests, uint64_t* ckpt_dev, uint64_t n_ckpt, uint32_t max_per_token) {
+  // Every landed unit is re-hashed in HBM on the verify stream once its copies are done, and the layer's ready word
+  // is written behind those checks on the same stream: an engine reads a landed unit only after its bytes reproduced
+  // the descriptor hash. A mismatch raises the token's sticky abort (kDgHash) before the ready word, so every later
+  // ss_dg_slot of the token gives the guard slot and the token fails.
+  void enable_verify(const std::vector<uint64_t>& digests, uint64_t* ckpt_dev, uint64_t n_ckpt, uint32_t max_per_token,
+                     const DgDevWords& dw) {
     verify_ = true;
-    digests_ = digests;
-    ckpt_dev_ = ckpt_dev;
-    n_ckpt_ = n_ckpt;
     vcap_ = max_per_token;
-    vtab_host_ = static_cast<tsa_verify_unit*>(dev_->alloc_pinned(sizeof(tsa_verify_unit) * vcap_, "verify table"));
-    vtab_dev_ = static_cast<tsa_verify_unit*>(dev_->alloc_device(sizeof(tsa_verify_unit) * vcap_, "verify table"));
+    digests_dev_ = static_cast<uint64_t*>(dev_->alloc_device(8ull * digests.size(), "verify digests"));
+    hip_check(hipMemcpy(digests_dev_, digests.data(), 8ull * digests.size(), hipMemcpyHostToDevice),
+              "hipMemcpy (digests)");
     vfail_host_ = static_cast<uint32_t*>(dev_->alloc_pinned(4ull * vcap_, "verify results"));
     vfail_dev_ = static_cast<uint32_t*>(dev_->alloc_device(4ull * vcap_, "verify results"));
     hip_check(hipMemset(vfail_dev_, 0, 4ull * vcap_), "hipMemset");
     vs_ = dev_->stream_create_dedicated();
+    DgVerifyLaunch& a = vlaunch_;
+    require(set_dg_verify_shape(a, arena_.data(), x_.part_bytes.data(), uint32_t(x_.part_bytes.size()), kSegBytes) &&
+                a.unit_segs == n_ckpt && a.unit_bytes == x_.unit_bytes,
+            SS_E_BACKEND, "device verify: the parts' segments disagree with the checkpoint count");
+    a.ckpt = ckpt_dev;
+    a.digests = digests_dev_;
+    a.abort = dw.abort;
+    a.err_code = dw.err_code;
+    a.err_aux = dw.err_aux;
+    a.err = kDgHash;
+  }
+  hipEvent_t next_vev() {
+    if (vev_used_ == vev_.size()) vev_.push_back(dev_->event_create());
+    return vev_[vev_used_++];
   }
   void landed(Stream s, uint32_t g, const uint32_t* keys, const int32_t* slots, uint32_t n) override {
-    (void)g;
     if (!verify_ || n == 0) return;
     require(vused_ + n <= vcap_, SS_E_BACKEND, "device verify: more landed units in a token than the table holds");
-    const uint32_t first = vused_;
-    for (uint32_t i = 0; i < n; ++i) {
-      tsa_verify_unit& v = vtab_host_[first + i];
-      std::memset(&v, 0, sizeof v);
-      for (uint32_t p = 0; p < x_.part_bytes.size(); ++p) {
-        v.ext[p].ptr = slot_ptr(p, slots[i]);
-        v.ext[p].bytes = x_.part_bytes[p];
-      }
-      v.n_ext = uint32_t(x_.part_bytes.size());
-      v.seg_first = uint64_t(i) * n_ckpt_;
-      v.states = ckpt_dev_ + uint64_t(keys[i]) * n_ckpt_ * 4;
-      v.digest = digests_[keys[i]];
-      v.total = x_.unit_bytes;
-      vkeys_.push_back(keys[i]);
-    }
-    vused_ += n;
-    // the verify stream waits for these copies, so the check never holds up the next layer's copies on s
-    if (vev_used_ == vev_.size()) vev_.push_back(dev_->event_create());
-    hipEvent_t landed_ev = vev_[vev_used_++];
+    // the verify stream waits for these copies (the next layer's copies on s never wait for the check)
+    hipEvent_t landed_ev = next_vev();
     ev_record(landed_ev, s_[s]);
     stream_wait(vs_, landed_ev);
-    copy_h2d(vtab_dev_ + first, vtab_host_ + first, sizeof(tsa_verify_unit) * n, vs_);
-    Timed t = prof_start(kProfVerify, uint64_t(n) * x_.unit_bytes, n, vs_);
-    hip_check(hipError_t(launch_verify(vtab_dev_ + first, n, uint64_t(n) * n_ckpt_, kSegBytes, vfail_dev_ + first,
-                                       vs_)),
-              "device verify launch");
-    prof_end(t, vs_);
+    for (uint32_t i0 = 0; i0 < n; i0 += kDgVerifyMax) {
+      DgVerifyLaunch& a = vlaunch_;
+      a.n = std::min(kDgVerifyMax, n - i0);
+      a.fail = vfail_dev_ + vused_;
+      a.aux = g;
+      for (uint32_t i = 0; i < a.n; ++i) {
+        a.keys[i] = keys[i0 + i];
+        a.slots[i] = slots[i0 + i];
+        vkeys_.push_back(keys[i0 + i]);
+      }
+      // timed by the launch's own start / stop events (the kernel's begin and end, not the queue around it)
+      Timed t = prof_take(kProfVerify, uint64_t(a.n) * x_.unit_bytes, a.n);
+      hip_check(hipError_t(launch_dg_verify(a, vs_, t.a, t.b)), "device verify launch");
+      prof_put(t);
+      vused_ += a.n;
+    }
   }
   // Before the boundary may reuse a slot: every check of this token has read its bytes.
   void verify_sync() {
@@ -454,6 +471,23 @@ class HipTransport final : public DgTransport {
     ev_record(t.b, s);
     pending_.push_back(t);
   }
+  // A pair of timing events for a launch that records them itself (prof_take, launch with them, prof_put).
+  Timed prof_take(ProfKind k, uint64_t bytes, uint32_t units) {
+    Timed t;
+    std::lock_guard<std::mutex> lk(prof_mu_);
+    if (!prof_on_) return t;
+    t.a = take_event_locked();
+    t.b = take_event_locked();
+    t.kind = k;
+    t.bytes = bytes;
+    t.units = units;
+    return t;
+  }
+  void prof_put(const Timed& t) {
+    if (!t.a) return;
+    std::lock_guard<std::mutex> lk(prof_mu_);
+    pending_.push_back(t);
+  }
   void drain_locked(bool wait) {
     size_t keep = 0;
     for (const Timed& t : pending_) {
@@ -512,12 +546,9 @@ class HipTransport final : public DgTransport {
   uint32_t job_next_[2] = {0, 0};
   uint64_t scatter_blocks_ = 0;
   bool verify_ = false;
-  std::vector<uint64_t> digests_;
-  uint64_t* ckpt_dev_ = nullptr;
-  uint64_t n_ckpt_ = 0;
+  DgVerifyLaunch vlaunch_;            // the launch arguments that stay fixed (arena, shape, checkpoints, gate)
+  uint64_t* digests_dev_ = nullptr;   // [keys]: the descriptor hashes
   uint32_t vcap_ = 0, vused_ = 0;
-  tsa_verify_unit* vtab_host_ = nullptr;
-  tsa_verify_unit* vtab_dev_ = nullptr;
   uint32_t* vfail_host_ = nullptr;
   uint32_t* vfail_dev_ = nullptr;
   std::vector<uint32_t> vkeys_;
@@ -525,7 +556,7 @@ class HipTransport final : public DgTransport {
   std::vector<hipEvent_t> part_ev_;  // [slots + blocks][parts]: the last write-back copy of each part (lazily made)
   int32_t wait_slot_ = -1, wait_block_ = -1;  // the next h2d waits per part on these (wait_copy_in)
   hipStream_t vs_ = nullptr;        // the verify stream (a hardware queue of its own)
-  std::vector<hipEvent_t> vev_;     // per landed batch of the token: its copies completed
+  std::vector<hipEvent_t> vev_;     // per landed batch and ready write of the token: the copies before it
   size_t vev_used_ = 0;
 };
 
@@ -783,13 +814,15 @@ class HipDgCtx final : public DgCtx {
       const std::string why = svc_->error();
       fail(SS_E_BACKEND, token_failure(dev, "the service: " + (why.empty() ? std::string("it did not finish") : why)));
     }
-    // 3. the device's error word
+    // 3. the device's error word (a failed device check is reported with its units below)
     const std::string dev = device_error();
-    if (!dev.empty()) {
+    const bool hash_abort = load_acquire(m_.err_code) == kDgHash;
+    if (!dev.empty() && !hash_abort) {
       poisoned_ = true;
       fail(SS_E_BACKEND, token_failure(dev, ""));
     }
-    // 4. the boundary, then the device check of this token's landed units
+    // 4. the boundary, then the device check of this token's landed units (a check of a prefetch may end after the
+    // end kernel: its failure is only in the check's result words)
     tr_->verify_sync();  // the boundary may hand a landed slot to a write-back or a new copy
     core_->end_token();
     const std::vector<uint32_t> bad = tr_->collect_verify();
@@ -798,9 +831,13 @@ class HipDgCtx final : public DgCtx {
       verify_failures_ += bad.size();
       poisoned_ = true;
       const uint32_t g = core_->gated_of(bad[0]);
-      fail(SS_E_HASH, token_failure("", std::to_string(bad.size()) + " landed unit(s) differ from the descriptor hash "
-                                        "in HBM, first gated (" + std::to_string(g) + ", " +
-                                        std::to_string(bad[0] - core_->unit_base()[g]) + ")"));
+      fail(SS_E_HASH, token_failure(dev, std::to_string(bad.size()) + " landed unit(s) differ from the descriptor hash "
+                                         "in HBM, first gated (" + std::to_string(g) + ", " +
+                                         std::to_string(bad[0] - core_->unit_base()[g]) + ")"));
+    }
+    if (hash_abort) {
+      poisoned_ = true;
+      fail(SS_E_BACKEND, token_failure(dev, "no device check result names the unit"));
     }
   }
 
@@ -965,6 +1002,18 @@ class HipDgCtx final : public DgCtx {
     return n;
   }
 
+  void corrupt_block(int g, int unit, uint64_t offset) override {
+    require(!in_token_, SS_E_INVALID, "tsa_test_dg_corrupt_block: between tokens only");
+    check_g(g, "tsa_test_dg_corrupt_block");
+    require(unit >= 0 && uint32_t(unit) < core_->units(uint32_t(g)), SS_E_INVALID,
+            "tsa_test_dg_corrupt_block: unit out of range");
+    const uint32_t k = core_->key(uint32_t(g), uint32_t(unit));
+    require(core_->home(k) == DgCore::Home::Host && core_->block_of(k) >= 0, SS_E_INVALID,
+            "tsa_test_dg_corrupt_block: the unit is not in its pinned block");
+    require(offset < x_.unit_bytes, SS_E_INVALID, "tsa_test_dg_corrupt_block: offset past the unit");
+    tr_->block_ptr(core_->block_of(k))[offset] ^= char(0xff);
+  }
+
  private:
   static void launch_ck(int e, const char* what) { hip_check(hipError_t(e), what); }
   ss_layer_stats to_layer(const DgLayerCounts& a, const DgLayerCounts& b) const {
@@ -986,7 +1035,8 @@ class HipDgCtx final : public DgCtx {
     const char* what = code == kDgTimeout ? "a wait timed out" : code == kDgBadId ? "an exported id was out of range"
                        : code == kDgHostAbort ? "the host aborted the token"
                        : code == kDgDesync ? "a step the host did not authorize"
-                       : code == kDgAbsent ? "a slot lookup met an absent entry" : "unknown device error";
+                       : code == kDgAbsent ? "a slot lookup met an absent entry"
+                       : code == kDgHash ? "a landed unit differs from its descriptor hash" : "unknown device error";
     return std::string(what) + (code == kDgDesync ? " (seq " : code == kDgAbsent ? "" : " (gated layer ") +
            (code == kDgAbsent ? std::string() : std::to_string(aux) + ")");
   }
@@ -1257,7 +1307,7 @@ void HipDgCtx::fill() {
   if (dverify) {
     hip_check(hipMemcpy(ckpt_dev_, ckpt_host.data(), ckpt_host.size() * 8, hipMemcpyHostToDevice),
               "hipMemcpy (checkpoints)");
-    tr_->enable_verify(digests, ckpt_dev_, n_ckpt, G * x_.B + o_.dg_prefetch_per_token + 64);
+    tr_->enable_verify(digests, ckpt_dev_, n_ckpt, G * x_.B + o_.dg_prefetch_per_token + 64, dw_);
   }
   (void)G;
 }

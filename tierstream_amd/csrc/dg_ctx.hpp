@@ -40,6 +40,7 @@ class DgCtx {
   virtual void profile_enable(bool on) = 0;
   virtual tsa_test_profile profile_read(bool wait) = 0;
   virtual uint32_t stamps(uint64_t* out, uint32_t cap) const = 0;
+  virtual void corrupt_block(int g, int unit, uint64_t offset) = 0;
 };
 
 std::unique_ptr<DgCtx> open_dg_ctx(const Desc& d, const Plan& p, const ss_options& o);

@@ -65,6 +65,7 @@ __global__ __launch_bounds__(64) void export_kernel(DgDevWords d, uint32_t g, co
     if (d.stamps) {
       d.stamps[4u * g + 1u] = 0ull;
       d.stamps[4u * g + 2u] = 0ull;
+      d.stamps[4u * g + 3u] = 0ull;
       d.stamps[4u * g] = wall_clock64();
     }
   }
@@ -83,13 +84,12 @@ __global__ __launch_bounds__(64) void predict_kernel(DgDevWords d, uint32_t g, c
 // One wavefront; lane 0 polls. Zero-miss layers return at once on the HBM any_miss word. A miss waits for ready[g] to
 // reach the token's sequence (a system-scope acquire that pairs with the service's value-write behind the copies),
 // polling with an s_sleep backoff; the host's abort word and the wall-clock deadline end it with an error.
-__global__ __launch_bounds__(64) void wait_kernel(DgDevWords d, uint32_t g) {
-  if (threadIdx.x != 0) return;
+// Stamps (wall clock): [1] entry and [3] exit on every path, [2] the poll that saw ready (left 0 by the export when
+// the layer had no miss).
+__device__ __forceinline__ void wait_poll(const DgDevWords& d, uint32_t g, uint64_t t0) {
   if (__hip_atomic_load(d.abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
   if (!__hip_atomic_load(d.any_miss + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
   const uint32_t seq = __hip_atomic_load(d.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const uint64_t t0 = wall_clock64();
-  if (d.stamps) d.stamps[4u * g + 1u] = t0;
   for (uint32_t polls = 0;; ++polls) {
     if (int32_t(ld_acq_sys(d.ready + g) - seq) >= 0) {
       if (d.stamps) d.stamps[4u * g + 2u] = wall_clock64();
@@ -106,6 +106,15 @@ __global__ __launch_bounds__(64) void wait_kernel(DgDevWords d, uint32_t g) {
       }
     }
     __builtin_amdgcn_s_sleep(2);
+  }
+}
+__global__ __launch_bounds__(64) void wait_kernel(DgDevWords d, uint32_t g) {
+  if (threadIdx.x != 0) return;
+  const uint64_t t0 = wall_clock64();
+  wait_poll(d, g, t0);
+  if (d.stamps) {
+    d.stamps[4u * g + 1u] = t0;
+    d.stamps[4u * g + 3u] = wall_clock64();
   }
 }
 

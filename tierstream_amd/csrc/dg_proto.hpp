@@ -23,7 +23,11 @@ struct DgPredRecord {
 static_assert(sizeof(DgRecord) == 288 && sizeof(DgPredRecord) == 272, "record layout");
 
 // Device error codes (err_aux = the gated layer, or the step's sequence for kDgDesync).
-enum DgErrCode : uint32_t { kDgOk = 0, kDgTimeout = 1, kDgBadId = 2, kDgHostAbort = 3, kDgDesync = 4, kDgAbsent = 5 };
+// kDgHash (this library's device verify, no reference counterpart): a landed unit's bytes in HBM differ from its
+// descriptor hash (err_aux = the gated layer whose copies landed it).
+enum DgErrCode : uint32_t {
+  kDgOk = 0, kDgTimeout = 1, kDgBadId = 2, kDgHostAbort = 3, kDgDesync = 4, kDgAbsent = 5, kDgHash = 6
+};
 
 // Every address the control kernels use, fixed at open (a captured graph replays for the context's life).
 struct DgDevWords {
@@ -38,7 +42,7 @@ struct DgDevWords {
   uint32_t* absent_err = nullptr;
   const int32_t* slot_of = nullptr;
   const uint32_t* unit_base = nullptr;  // [G + 1]
-  uint64_t* stamps = nullptr;      // [4 G]: export, wait entry, ready seen (wall clock ticks), unused
+  uint64_t* stamps = nullptr;      // [4 G]: export end, wait entry, ready seen (0: no miss), wait exit (wall clock)
   // fine-grained host memory, device addresses
   DgRecord* rec = nullptr;          // [G]
   DgPredRecord* prec = nullptr;     // [G]

@@ -178,6 +178,7 @@ def _declare() -> C.CDLL:
         "tsa_test_profile_enable": (st, [vp, C.c_int]),
         "tsa_test_profile_read": (st, [vp, C.c_int, C.POINTER(TsaTestProfile)]),
         "tsa_test_dg_stamps": (st, [vp, C.POINTER(u64), u32, C.POINTER(u32)]),
+        "tsa_test_dg_corrupt_block": (st, [vp, C.c_int, C.c_int, u64]),
         "tsa_xxh64_host": (u64, [vp, u64]),
     }
     for name, (res, args) in sigs.items():
@@ -355,13 +356,19 @@ class Ctx:
         return p.as_dict()
 
     def dg_stamps(self) -> np.ndarray:
-        """uint64 [G][4] wall-clock ticks of the last token: export end, wait entry, ready seen, unused."""
+        """uint64 [G][4] wall-clock ticks of the last token: export end, wait entry, ready seen (0: the layer had no
+        miss), wait exit."""
         L = _declare()
         n = u32(0)
         check(L.tsa_test_dg_stamps(self.h, None, 0, C.byref(n)))
         out = np.zeros(n.value, dtype=np.uint64)
         check(L.tsa_test_dg_stamps(self.h, out.ctypes.data_as(C.POINTER(u64)), n.value, C.byref(n)))
         return out.reshape(-1, 4)
+
+    def dg_corrupt_block(self, gated: int, unit: int, offset: int = 0):
+        """Flip one byte of a unit's pinned copy (the unit must be off the device): its next landing fails the device
+        check."""
+        check(_declare().tsa_test_dg_corrupt_block(self.h, gated, unit, offset))
 
     def region_of(self, addr: int):
         k, i, off = C.c_int(), C.c_int(), u64()
@@ -399,14 +406,20 @@ class DgEngine:
 
     def token(self, routes: np.ndarray, want_checksums=True):
         """routes int32 [G][n_ids]; returns (checksums [G][n_ids] or None, ms)."""
+        st, cks, ms = self.token_status(routes, want_checksums)
+        check(st)
+        return cks, ms
+
+    def token_status(self, routes: np.ndarray, want_checksums=True):
+        """As token(), without raising: (status, checksums, ms); a failed token's checksums are still read back."""
         E = engine()
         r = np.ascontiguousarray(routes, dtype=np.int32)
         assert r.shape == (self.G, self.n_ids)
         cks = np.zeros((self.G, self.n_ids), dtype=np.uint64) if want_checksums else None
         ms = C.c_double(0)
-        check(E.tse_dg_token(self.h, r.ctypes.data_as(C.POINTER(i32)),
-                             cks.ctypes.data_as(C.POINTER(u64)) if want_checksums else None, C.byref(ms)))
-        return cks, ms.value
+        st = E.tse_dg_token(self.h, r.ctypes.data_as(C.POINTER(i32)),
+                            cks.ctypes.data_as(C.POINTER(u64)) if want_checksums else None, C.byref(ms))
+        return int(st), cks, ms.value
 
     def stamps(self) -> np.ndarray:
         """uint64 [G]: the last token's per-layer compute-start wall-clock ticks."""
