@@ -586,6 +586,8 @@ void DgCore::end_token() {
   for (size_t i = 0; c_.wb_defer && i < n_evict; ++i) {
     const uint32_t k = victims_[i];
     deferred_.push_back({k, e_[k].slot, e_[k].block, 0, 0});
+    // (only on the D2H stream: the write-back events this core records on wb_stream_ then follow the copies)
+    if (wb_stream_ == DgTransport::kD2h) t_->prestage(e_[k].slot, e_[k].block);
     ++st_.wb_deferred;
     ++st_.evicted;
     ++lc_[gated_of(k)].evicted;

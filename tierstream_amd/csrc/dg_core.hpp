@@ -47,6 +47,11 @@ class DgTransport {
     if (slot_ev) wait(s, slot_ev);
     if (block_ev) wait(s, block_ev);
   }
+  // A deferred write-back (slot -> block, every part) the core has just recorded at the boundary, with write-backs on
+  // kD2h. It will submit it later, part by part (d2h_part on kD2h), by its credit or when it needs the slot; meanwhile
+  // neither the slot nor the block is written by anything else. A transport may copy it now on kD2h and make the
+  // later d2h_part calls of the same (slot, block, part) no-ops (default: nothing).
+  virtual void prestage(int32_t slot, int32_t block) { (void)slot, (void)block; }
   // Units just copied in (key, slot) on stream s: one call per fetch, right after its copies (a demand's before the
   // layer's signal_ready). A transport that verifies landed bytes enqueues the check here (default: nothing).
   virtual void landed(Stream s, uint32_t g, const uint32_t* keys, const int32_t* slots, uint32_t n) {

@@ -9,6 +9,7 @@
 #include <cstring>
 #include <mutex>
 #include <thread>
+#include <unordered_map>
 #include <vector>
 
 #include "dg_core.hpp"
@@ -290,7 +291,28 @@ class HipTransport final : public DgTransport {
     }
     prof_end(t, s_[kD2h]);
   }
+  // Deferred write-backs are copied at the boundary that chose them (prestage), in the core's order, on the D2H
+  // stream: the copy engine of that direction is otherwise idle, and PCIe is full duplex, so a miss copy later into
+  // the slot finds its write-back done instead of queued behind the token's other write-backs. The core still submits
+  // each one part by part when its credit or a needed slot says so (its bookkeeping, hence placement, is unchanged);
+  // those submissions find the part copied and only the part's events matter (recorded at the copy).
+  void prestage(int32_t slot, int32_t block) override {
+    const uint32_t P = uint32_t(x_.part_bytes.size());
+    for (uint32_t p = 0; p < P; ++p) {
+      Timed t = prof_start(kProfWb, x_.part_bytes[p], 1, s_[kD2h]);
+      copy_d2h(block_ptr(block) + x_.part_offset[p], slot_ptr(p, slot), x_.part_bytes[p], s_[kD2h]);
+      mark_part(kD2h, slot, block, p);
+      prof_end(t, s_[kD2h]);
+    }
+    prestaged_[slot] = {block, (1u << P) - 1u};
+  }
   void d2h_part(Stream s, int32_t slot, int32_t block, uint32_t p) override {
+    auto it = prestaged_.find(slot);
+    if (it != prestaged_.end() && it->second.block == block && (it->second.parts >> p & 1u)) {
+      it->second.parts &= ~(1u << p);
+      if (!it->second.parts) prestaged_.erase(it);
+      return;
+    }
     Timed t = prof_start(kProfWb, x_.part_bytes[p], 1, s_[s]);
     copy_d2h(block_ptr(block) + x_.part_offset[p], slot_ptr(p, slot), x_.part_bytes[p], s_[s]);
     mark_part(s, slot, block, p);
@@ -396,6 +418,11 @@ class HipTransport final : public DgTransport {
       vused_ += a.n;
     }
   }
+  // A small device-to-host read on the demand stream (between tokens), not on the null stream.
+  void read_device(void* dst, const void* src, uint64_t bytes) {
+    copy_d2h(dst, src, bytes, s_[kDem]);
+    stream_sync(s_[kDem]);
+  }
   // Before the boundary may reuse a slot: every check of this token has read its bytes.
   void verify_sync() {
     if (vs_) stream_sync(vs_);
@@ -406,10 +433,13 @@ class HipTransport final : public DgTransport {
     verify_sync();
     vev_used_ = 0;
     if (!verify_ || vused_ == 0) return bad;
-    hip_check(hipMemcpy(vfail_host_, vfail_dev_, 4ull * vused_, hipMemcpyDeviceToHost), "hipMemcpy (verify)");
+    // on the verify stream, never the null stream: the library's streams (CU-masked, hence blocking) would all be
+    // waited for, the write-backs on the D2H stream included
+    copy_d2h(vfail_host_, vfail_dev_, 4ull * vused_, vs_);
+    stream_sync(vs_);
     for (uint32_t i = 0; i < vused_; ++i)
       if (vfail_host_[i]) bad.push_back(vkeys_[i]);
-    hip_check(hipMemset(vfail_dev_, 0, 4ull * vused_), "hipMemset");
+    hip_check(hipMemsetAsync(vfail_dev_, 0, 4ull * vused_, vs_), "hipMemsetAsync");
     verified_ += vused_;
     vused_ = 0;
     vkeys_.clear();
@@ -555,6 +585,11 @@ class HipTransport final : public DgTransport {
   uint64_t verified_ = 0;
   std::vector<hipEvent_t> part_ev_;  // [slots + blocks][parts]: the last write-back copy of each part (lazily made)
   int32_t wait_slot_ = -1, wait_block_ = -1;  // the next h2d waits per part on these (wait_copy_in)
+  struct Prestaged {
+    int32_t block;
+    uint32_t parts;  // the parts copied at the boundary whose submission has not come yet
+  };
+  std::unordered_map<int32_t, Prestaged> prestaged_;  // by slot
   hipStream_t vs_ = nullptr;        // the verify stream (a hardware queue of its own)
   std::vector<hipEvent_t> vev_;     // per landed batch and ready write of the token: the copies before it
   size_t vev_used_ = 0;
@@ -998,7 +1033,7 @@ class HipDgCtx final : public DgCtx {
     require(!in_token_, SS_E_INVALID, "tsa_test_dg_stamps: between tokens only");
     const uint32_t n = 4u * uint32_t(x_.gated.size());
     if (out && cap)
-      hip_check(hipMemcpy(out, dw_.stamps, 8ull * std::min(n, cap), hipMemcpyDeviceToHost), "hipMemcpy (stamps)");
+      tr_->read_device(out, dw_.stamps, 8ull * std::min(n, cap));
     return n;
   }
 

@@ -194,7 +194,9 @@ __attribute__((visibility("default"))) ss_status tse_host_run(ss_ctx* c, const s
     }
     if (checksums) {
       std::vector<unsigned long long> all(size_t(max_ids) * L);
-      if ((st = ck(hipMemcpy(all.data(), out_dev, 8ull * max_ids * L, hipMemcpyDeviceToHost))) != SS_OK) break;
+      if ((st = ck(hipMemcpyAsync(all.data(), out_dev, 8ull * max_ids * L, hipMemcpyDeviceToHost, s))) != SS_OK ||
+          (st = ck(hipStreamSynchronize(s))) != SS_OK)
+        break;
       std::memcpy(checksums + size_t(step) * L * max_ids, all.data(), 8ull * max_ids * L);
     }
   }
@@ -310,7 +312,9 @@ __attribute__((visibility("default"))) ss_status tse_dg_token(void* h, const int
   // the checksums also when the token failed (a failed token's reads after its abort are the guard slot's zeros)
   if (checksums) {
     std::vector<unsigned long long> out(size_t(64) * e->G);
-    TSE_HIP(hipMemcpy(out.data(), e->out_dev, 8ull * out.size(), hipMemcpyDeviceToHost));
+    // on the engine's stream (the null stream would wait for the library's blocking copy streams)
+    TSE_HIP(hipMemcpyAsync(out.data(), e->out_dev, 8ull * out.size(), hipMemcpyDeviceToHost, e->s));
+    TSE_HIP(hipStreamSynchronize(e->s));
     for (uint32_t g = 0; g < e->G; ++g)
       for (uint32_t i = 0; i < e->n_ids; ++i) checksums[size_t(g) * e->n_ids + i] = out[64 * g + i];
   }
