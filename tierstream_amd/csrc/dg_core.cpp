@@ -162,9 +162,9 @@ std::vector<uint32_t> DgCore::residency() const {
   return out;
 }
 
-void DgCore::write_entry(DgTransport::Stream s, uint32_t k, int32_t v) {
+void DgCore::write_entry(DgTransport::Stream s, uint32_t k, int32_t v, bool landing) {
   table_[k] = v;
-  t_->write_entry(s, k, v);
+  if (!(landing && t_->publishes_landed())) t_->write_entry(s, k, v);
 }
 
 // Every recorded write-back is complete in bookkeeping: the key's block is its home and its slot is free (a discarded
@@ -375,7 +375,7 @@ bool DgCore::fetch(uint32_t g, uint32_t unit, bool prefetch) {
   detach(slot_ev_, slot);
   detach(block_ev_, x.block);
   t_->h2d(s, slot, x.block);
-  write_entry(s, k, slot);
+  write_entry(s, k, slot, true);
   --on_host_;
   x.slot = slot;
   x.via_prefetch = prefetch;

@@ -29,6 +29,9 @@ class DgTransport {
   virtual uint32_t parts() const = 0;
   virtual uint64_t part_bytes(uint32_t part) const = 0;
   virtual void write_entry(Stream s, uint32_t key, int32_t v) = 0;  // slot_of[key] = v after s's earlier work
+  // True: the entry of a fetched unit (key -> its slot) is published by the transport with its landed() call, after
+  // the unit's copies (the core then never calls write_entry for it).
+  virtual bool publishes_landed() const { return false; }
   virtual void signal_ready(uint32_t g, uint32_t seq) = 0;  // ready[g] = seq after the layer's copies (and landed())
   virtual void* event_create() = 0;
   virtual void event_destroy(void* ev) = 0;
@@ -162,7 +165,7 @@ class DgCore {
   void* finish_deferred_front();
   void force_free_slot();
   int32_t take_bank_slot(uint32_t g);
-  void write_entry(DgTransport::Stream s, uint32_t k, int32_t v);
+  void write_entry(DgTransport::Stream s, uint32_t k, int32_t v, bool landing = false);
   bool fetch(uint32_t g, uint32_t unit, bool prefetch);
   void cover(uint32_t g, uint32_t unit);
   void use(uint32_t g, uint32_t unit, bool was_miss);

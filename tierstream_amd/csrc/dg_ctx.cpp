@@ -218,6 +218,7 @@ class HipTransport final : public DgTransport {
       dev_->free_device(jobs_dev_[k]);
     }
     dev_->free_device(digests_dev_);
+    dev_->free_device(vcount_dev_);
     dev_->stream_destroy(vs_);
     for (hipEvent_t e : vev_) dev_->event_destroy(e);
     for (hipEvent_t e : part_ev_) dev_->event_destroy(e);
@@ -337,14 +338,22 @@ class HipTransport final : public DgTransport {
   // ready[g] = seq after the layer's demand copies (and cover waits) on kDem; with device verify on the verify stream,
   // behind the checks of every unit landed so far in the token (its stream order).
   void signal_ready(uint32_t g, uint32_t seq) override {
-    hipStream_t on = s_[kDem];
-    if (verify_) {
-      hipEvent_t ev = next_vev();
-      ev_record(ev, s_[kDem]);
-      stream_wait(vs_, ev);
-      on = vs_;
+    if (!verify_) {
+      hip_check(hipStreamWriteValue32(s_[kDem], ready_ + g, seq, 0), "hipStreamWriteValue32 (ready)");
+      return;
     }
-    hip_check(hipStreamWriteValue32(on, ready_ + g, seq, 0), "hipStreamWriteValue32 (ready)");
+    hipEvent_t ev = next_vev();  // the layer's cover waits and copies, all on kDem
+    ev_record(ev, s_[kDem]);
+    stream_wait(vs_, ev);
+    if (vpending_) {  // the layer's last check writes the ready word when it has published its units
+      vlaunch_.ready = ready_;
+      vlaunch_.ready_g = g;
+      vlaunch_.seq = seq;
+      flush_verify();
+      vlaunch_.ready = nullptr;
+    } else {
+      hip_check(hipStreamWriteValue32(vs_, ready_ + g, seq, 0), "hipStreamWriteValue32 (ready)");
+    }
   }
   void* event_create() override { return dev_->event_create(); }
   void event_destroy(void* ev) override { dev_->event_destroy(static_cast<hipEvent_t>(ev)); }
@@ -389,34 +398,50 @@ class HipTransport final : public DgTransport {
     a.err_code = dw.err_code;
     a.err_aux = dw.err_aux;
     a.err = kDgHash;
+    vcount_dev_ = static_cast<uint32_t*>(dev_->alloc_device(64, "verify publication counter"));
+    hip_check(hipMemset(vcount_dev_, 0, 64), "hipMemset");
+    a.done_count = vcount_dev_;
+    a.slot_of = slot_of_;
   }
+  bool publishes_landed() const override { return verify_; }
   hipEvent_t next_vev() {
     if (vev_used_ == vev_.size()) vev_.push_back(dev_->event_create());
     return vev_[vev_used_++];
   }
+  // A landed unit's check is launched once the next landed() or the layer's signal_ready() comes (the service issues
+  // them back to back), so the layer's last check can carry the ready word; each waits for its own unit's copies.
   void landed(Stream s, uint32_t g, const uint32_t* keys, const int32_t* slots, uint32_t n) override {
     if (!verify_ || n == 0) return;
     require(vused_ + n <= vcap_, SS_E_BACKEND, "device verify: more landed units in a token than the table holds");
-    // the verify stream waits for these copies (the next layer's copies on s never wait for the check)
+    flush_verify();
     hipEvent_t landed_ev = next_vev();
     ev_record(landed_ev, s_[s]);
     stream_wait(vs_, landed_ev);
     for (uint32_t i0 = 0; i0 < n; i0 += kDgVerifyMax) {
+      if (i0) flush_verify();
       DgVerifyLaunch& a = vlaunch_;
       a.n = std::min(kDgVerifyMax, n - i0);
       a.fail = vfail_dev_ + vused_;
       a.aux = g;
+      a.ready = nullptr;
       for (uint32_t i = 0; i < a.n; ++i) {
         a.keys[i] = keys[i0 + i];
         a.slots[i] = slots[i0 + i];
         vkeys_.push_back(keys[i0 + i]);
       }
-      // timed by the launch's own start / stop events (the kernel's begin and end, not the queue around it)
-      Timed t = prof_take(kProfVerify, uint64_t(a.n) * x_.unit_bytes, a.n);
-      hip_check(hipError_t(launch_dg_verify(a, vs_, t.a, t.b)), "device verify launch");
-      prof_put(t);
       vused_ += a.n;
+      vpending_ = true;
     }
+    if (s != kDem) flush_verify();  // a prefetch's check carries no ready word
+  }
+  void flush_verify() {
+    if (!vpending_) return;
+    vpending_ = false;
+    const DgVerifyLaunch& a = vlaunch_;
+    // timed by the launch's own start / stop events (the kernel's begin and end, not the queue around it)
+    Timed t = prof_take(kProfVerify, uint64_t(a.n) * x_.unit_bytes, a.n);
+    hip_check(hipError_t(launch_dg_verify(a, vs_, t.a, t.b)), "device verify launch");
+    prof_put(t);
   }
   // A small device-to-host read on the demand stream (between tokens), not on the null stream.
   void read_device(void* dst, const void* src, uint64_t bytes) {
@@ -425,6 +450,7 @@ class HipTransport final : public DgTransport {
   }
   // Before the boundary may reuse a slot: every check of this token has read its bytes.
   void verify_sync() {
+    flush_verify();  // (every demand landing is followed by its layer's signal_ready: nothing should be pending)
     if (vs_) stream_sync(vs_);
   }
   // At the boundary: the keys whose landed bytes differ from their descriptor hash.
@@ -576,7 +602,9 @@ class HipTransport final : public DgTransport {
   uint32_t job_next_[2] = {0, 0};
   uint64_t scatter_blocks_ = 0;
   bool verify_ = false;
-  DgVerifyLaunch vlaunch_;            // the launch arguments that stay fixed (arena, shape, checkpoints, gate)
+  DgVerifyLaunch vlaunch_;            // the next launch (arena, shape, checkpoints, gate and publication words fixed)
+  bool vpending_ = false;             // vlaunch_ holds units whose check is not launched yet
+  uint32_t* vcount_dev_ = nullptr;    // the launches' publication counter
   uint64_t* digests_dev_ = nullptr;   // [keys]: the descriptor hashes
   uint32_t vcap_ = 0, vused_ = 0;
   uint32_t* vfail_host_ = nullptr;

@@ -2,7 +2,9 @@
 // (src/dg_proto.hpp:14-25: DgRecord 288 bytes, DgPredRecord 272 bytes) so a record dump reads the same; the placement
 // is this library's: records, export flags and the completion words live in fine-grained coherent host memory (the
 // service thread polls them), while ready words, the sequence, the sticky abort and the error words live in HBM (only
-// the GPU polls ready; the service writes it with stream value-writes ordered after the layer's copies).
+// the GPU polls ready). The service publishes a layer's ready word with a stream value-write ordered after its copies,
+// or, with the device check of landed units on, the layer's last check kernel writes it (and the landed units' slot
+// entries) when it ends.
 #pragma once
 
 #include <cstdint>

@@ -46,6 +46,13 @@ struct DgVerifyLaunch {
   uint32_t* err_code = nullptr;
   uint32_t* err_aux = nullptr;
   uint32_t err = 0, aux = 0;
+  // Publication by the launch's last workgroup (done_count null: none): every unit's entry slot_of[key] = slot (when
+  // slot_of is set), then ready[ready_g] = seq (when ready is set). done_count is a zeroed device word the launches of
+  // one stream share (the last workgroup zeroes it again).
+  uint32_t* done_count = nullptr;
+  int32_t* slot_of = nullptr;
+  uint32_t* ready = nullptr;
+  uint32_t ready_g = 0, seq = 0;
   uint32_t keys[kDgVerifyMax] = {};
   int32_t slots[kDgVerifyMax] = {};
 };

@@ -245,16 +245,32 @@ __global__ __launch_bounds__(256) void dg_verify_kernel(const DgVerifyLaunch a) 
   const uint32_t base4 = threadIdx.x & ~3u;
 #pragma unroll
   for (int k = 0; k < 4; ++k) all[k] = __shfl(v, int(base4 + k), 64);
-  if (!live) return;
   bool bad = false;
-  if (!last) bad = v != a.ckpt[(key * a.unit_segs + local + 1) * 4 + q];
-  else if (q == 0) bad = xfinal(all, a.unit_bytes, tail, tail_len) != a.digests[key];
+  if (live) {
+    if (!last) bad = v != a.ckpt[(key * a.unit_segs + local + 1) * 4 + q];
+    else if (q == 0) bad = xfinal(all, a.unit_bytes, tail, tail_len) != a.digests[key];
+  }
   if (bad) {
     atomicOr(a.fail + u, 1u);
-    if (a.abort) {  // the gate: the token fails before the layer's ready word is written behind this kernel
+    if (a.abort) {  // the gate: the token fails before the layer's ready word is written
       if (atomicCAS(a.err_code, 0u, a.err) == 0u) atomicExch(a.err_aux, a.aux);
       atomicExch(a.abort, 1u);
     }
+    __threadfence();  // performed before this thread reaches the barrier below (and so before its group counts)
+  }
+  if (!a.done_count) return;
+  // publication by the last workgroup to finish. Only a failing thread has words to release, and it did so above;
+  // the count itself is relaxed (a release fence per workgroup is an L2 write-back each on this chip).
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  if (__hip_atomic_fetch_add(a.done_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != gridDim.x - 1u) return;
+  if (a.slot_of)
+    for (uint32_t i = 0; i < a.n; ++i)
+      __hip_atomic_store(a.slot_of + a.keys[i], a.slots[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(a.done_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (a.ready) {
+    __threadfence_system();
+    __hip_atomic_store(a.ready + a.ready_g, a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 
