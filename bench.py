@@ -14,8 +14,10 @@ latency). The timed region is exactly --steps tokens after --warmup untimed ones
 synchronizations. The JSON line's value is the p50 step latency in ms.
 
 Beside it:
-  h2d        miss bytes over the copy engines' busy time (timed events around every unit copy), against the pinned
-             host-to-device peak measured in the same run (2 GiB hipMemcpyAsync from hipHostMalloc memory)
+  h2d        miss bytes over the wall clock of the timed region, and over the copy engine's busy time (timed events
+             around every part copy of the probe tokens after the timed ones: brackets are left out of the timed
+             region, whose copies they would delay), against the pinned host-to-device peak measured in the same run
+             (2 GiB hipMemcpyAsync from hipHostMalloc memory)
   roofline   the device XXH64 verify kernel (the dominant kernel of the library): unit bytes hashed per launch over
              its mean launch time (timed events on the stream it runs on), against the 8 TB/s HBM peak
   wait       the zero-miss layer wait on the device timeline (wall-clock stamps, 10 ns): the wait kernel's own entry
@@ -45,9 +47,10 @@ METRIC = "decode-step serve latency p50/p99; miss H2D GB/s and HBM GB/s vs roofl
 HBM_PEAK_GBPS = 8000.0
 TICK_NS = 10.0  # wall_clock64 runs at 100 MHz on gfx950
 # HBM bytes one verify launch moves per unit it checks, keyed by unit bytes: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
-# on a launch of one unit of this shape, each scaled by the counter's reading for a copy kernel of known size (FETCH
-# 2.0, WRITE 1.0): 346,966 KiB fetched, nothing written (profiles/verify_kernel_mixtral_unit_pmc.md).
-VERIFY_TRAFFIC_PER_UNIT = {352321536: 346966 * 1024}
+# on a launch of one unit of this shape (dg_verify_kernel through tsa_xxh64_verify_slots), each scaled by the
+# counter's reading for a copy kernel of known size (FETCH 2.0, WRITE 1.0): 347,205 KiB fetched, nothing written
+# (profiles/dg_verify_kernel_mixtral_unit_pmc.md).
+VERIFY_TRAFFIC_PER_UNIT = {352321536: 347205 * 1024}
 
 
 def log(*a):
@@ -320,7 +323,9 @@ def main():
         for t in range(warm):
             cks, _ = eng.token(routes[t])
             check_cks(t, cks)
-        ctx.profile_enable(True)
+        # the timed region brackets only the verify launches (their own dispatch stamps: no extra stream work); the
+        # copies and write-backs are bracketed in the probe tokens after it
+        ctx.profile_enable(ctx.PROF_VERIFY)
         s0 = ctx.dg_stats()
         tsa.check(L.tsa_device_sync())
         lat = np.zeros(steps)
@@ -338,7 +343,7 @@ def main():
         # start. A zero-miss layer: the wait kernel's own time (entry -> exit), the dispatch gaps either side of it,
         # and export end -> compute start (what the engine sees).
         zero_gap, zero_wait_kernel, gap_in, gap_out, miss_wait = [], [], [], [], []
-        ctx.profile_enable(False)
+        ctx.profile_enable(ctx.PROF_COPY | ctx.PROF_WRITEBACK)
         for i in range(probe):
             t = warm + steps + i
             cks, _ = eng.token(routes[t])
@@ -354,8 +359,11 @@ def main():
                     gap_out.append((start[g] - st[g, 3]) * us)
                 else:
                     miss_wait.append((st[g, 2] - st[g, 1]) * TICK_NS / 1e6)
+        pprof = ctx.profile_read(wait=True)  # the probe tokens' copy and write-back brackets
+        log(f"probe tokens: {pprof}")
         dstat = {k: s1[k] - s0[k] for k in ("tokens", "lookups", "misses", "fetched", "evicted", "bank_serves",
-                                             "writebacks_done", "inclusive_kept", "inclusive_drops", "miss_layers")}
+                                             "writebacks_done", "inclusive_kept", "inclusive_drops", "miss_layers",
+                                             "wb_forced", "collected_mid", "stalled")}
         failures = ctx.verify_failures()
         eng.close()
         ctx.close()
@@ -366,7 +374,7 @@ def main():
         kern = measure_kernels(tsa, L, C, w)
         log(f"kernels {kern}")
 
-        copy_gbps = prof["copy_bytes"] / prof["copy_ns"] if prof["copy_ns"] else None
+        copy_gbps = pprof["copy_bytes"] / pprof["copy_ns"] if pprof["copy_ns"] else None
         ver_gbps = prof["verify_bytes"] / prof["verify_ns"] if prof["verify_ns"] else None
         miss_bytes = dstat["fetched"] * w.unit_bytes
         result = {
@@ -393,8 +401,10 @@ def main():
             "p99_ms": round(pct(lat, 99), 3),
             "tokens_per_s": round(steps / wall, 3),
             "misses_per_token": round(dstat["misses"] / steps, 3),
-            "h2d": {"miss_bytes": miss_bytes, "copies": prof["copies"],
+            "h2d": {"miss_bytes": miss_bytes,
                     "busy_GBps": round(copy_gbps, 2) if copy_gbps else None,
+                    "busy_sample": f"{pprof['copies']} unit copies of the {probe} probe tokens after the timed ones, "
+                                   f"each part bracketed by timed events",
                     "wall_GBps": round(miss_bytes / wall / 1e9, 2),
                     "pinned_peak_GBps": round(peaks["h2d_pinned_GBps"], 2),
                     "frac_of_pinned_peak": round(copy_gbps / peaks["h2d_pinned_GBps"], 3) if copy_gbps else None,
@@ -423,9 +433,10 @@ def main():
                      "zero_miss_samples": len(zero_gap),
                      "miss_layer_wait_ms_p50": round(pct(miss_wait, 50), 3) if miss_wait else None,
                      "miss_samples": len(miss_wait)},
-            "writeback": {"units": prof["writebacks"], "bytes": prof["writeback_bytes"],
-                          "busy_GBps": round(prof["writeback_bytes"] / prof["writeback_ns"], 2)
-                          if prof["writeback_ns"] else None},
+            "writeback": {"parts": pprof["writebacks"], "bytes": pprof["writeback_bytes"],
+                          "busy_GBps": round(pprof["writeback_bytes"] / pprof["writeback_ns"], 2)
+                          if pprof["writeback_ns"] else None,
+                          "sample": f"the {probe} probe tokens (part copies to host, issued at each boundary)"},
             "stats": dstat,
             "checks": {"verify_failures": failures, "checksum_mismatches": ck_bad,
                        "units_seen": len(ck_seen)},

@@ -37,6 +37,12 @@ typedef struct tsa_test_profile {
   uint64_t verify_ns;
   uint64_t pending;         /* bracketed operations whose events had not completed at the read */
 } tsa_test_profile;
+/* on: a mask of what is bracketed, TSA_TEST_PROF_COPY | _WRITEBACK | _VERIFY (0: nothing); 1 keeps its older meaning
+ * of everything. The verify launches take the dispatch's own begin and end stamps (no extra stream work); a copy
+ * bracket records two events on the copy's stream. */
+#define TSA_TEST_PROF_COPY 0x2
+#define TSA_TEST_PROF_WRITEBACK 0x4
+#define TSA_TEST_PROF_VERIFY 0x8
 SS_API ss_status tsa_test_profile_enable(ss_ctx* c, int on);
 /* Between tokens; wait = 1 first waits for every bracketed operation (write-backs may still run after ss_end). */
 SS_API ss_status tsa_test_profile_read(ss_ctx* c, int wait, tsa_test_profile* out);

@@ -414,7 +414,9 @@ uint64_t tsa_test_verify_failures(const ss_ctx* c) {
 ss_status tsa_test_profile_enable(ss_ctx* c, int on) {
   return guard([&] {
     need(c != nullptr, "tsa_test_profile_enable: null context");
-    dg_of(c, "tsa_test_profile_enable").profile_enable(on != 0);
+    need(on >= 0 && on <= (TSA_TEST_PROF_COPY | TSA_TEST_PROF_WRITEBACK | TSA_TEST_PROF_VERIFY),
+         "tsa_test_profile_enable: on is 0, 1 or a mask of TSA_TEST_PROF_*");
+    dg_of(c, "tsa_test_profile_enable").profile_enable(on);
   });
 }
 ss_status tsa_test_profile_read(ss_ctx* c, int wait, tsa_test_profile* out) {

@@ -474,10 +474,10 @@ class HipTransport final : public DgTransport {
   uint64_t verified() const { return verified_; }
 
   // ---- timing (a test hook): timed events around unit copies, write-backs and verify launches ----
-  void profile_enable(bool on) {
+  void profile_enable(int on) {
     std::lock_guard<std::mutex> lk(prof_mu_);
     drain_locked(true);
-    prof_on_ = on;
+    prof_mask_ = on == 1 ? (TSA_TEST_PROF_COPY | TSA_TEST_PROF_WRITEBACK | TSA_TEST_PROF_VERIFY) : uint32_t(on);
     prof_tot_ = tsa_test_profile{};
   }
   tsa_test_profile profile_read(bool wait) {
@@ -509,10 +509,13 @@ class HipTransport final : public DgTransport {
     prof_free_.pop_back();
     return e;
   }
+  static uint32_t prof_bit(ProfKind k) {
+    return k == kProfCopy ? TSA_TEST_PROF_COPY : k == kProfWb ? TSA_TEST_PROF_WRITEBACK : TSA_TEST_PROF_VERIFY;
+  }
   Timed prof_start(ProfKind k, uint64_t bytes, uint32_t units, hipStream_t s) {
     Timed t;
     std::lock_guard<std::mutex> lk(prof_mu_);
-    if (!prof_on_) return t;
+    if (!(prof_mask_ & prof_bit(k))) return t;
     t.a = take_event_locked();
     t.b = take_event_locked();
     t.kind = k;
@@ -531,7 +534,7 @@ class HipTransport final : public DgTransport {
   Timed prof_take(ProfKind k, uint64_t bytes, uint32_t units) {
     Timed t;
     std::lock_guard<std::mutex> lk(prof_mu_);
-    if (!prof_on_) return t;
+    if (!(prof_mask_ & prof_bit(k))) return t;
     t.a = take_event_locked();
     t.b = take_event_locked();
     t.kind = k;
@@ -580,7 +583,7 @@ class HipTransport final : public DgTransport {
   }
 
   std::mutex prof_mu_;  // the service thread brackets demand copies, the engine thread reads and the boundary's copies
-  bool prof_on_ = false;
+  uint32_t prof_mask_ = 0;  // TSA_TEST_PROF_* kinds bracketed
   tsa_test_profile prof_tot_{};
   std::vector<Timed> pending_;
   std::vector<hipEvent_t> prof_events_, prof_free_;
@@ -1049,7 +1052,7 @@ class HipDgCtx final : public DgCtx {
   }
   uint64_t verify_failures() const override { return verify_failures_; }
 
-  void profile_enable(bool on) override {
+  void profile_enable(int on) override {
     require(!in_token_, SS_E_INVALID, "tsa_test_profile_enable: between tokens only");
     tr_->profile_enable(on);
   }

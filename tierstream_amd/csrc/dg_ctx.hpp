@@ -37,7 +37,7 @@ class DgCtx {
   virtual uint32_t host_table(int32_t* out, uint32_t cap) const = 0;
   virtual uint64_t verify_failures() const = 0;
   // measurement hooks (tsa_test.h)
-  virtual void profile_enable(bool on) = 0;
+  virtual void profile_enable(int on) = 0;
   virtual tsa_test_profile profile_read(bool wait) = 0;
   virtual uint32_t stamps(uint64_t* out, uint32_t cap) const = 0;
   virtual void corrupt_block(int g, int unit, uint64_t offset) = 0;

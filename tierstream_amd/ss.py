@@ -347,7 +347,10 @@ class Ctx:
     def verify_failures(self) -> int:
         return int(_declare().tsa_test_verify_failures(self.h))
 
-    def profile_enable(self, on: bool = True):
+    PROF_COPY, PROF_WRITEBACK, PROF_VERIFY = 0x2, 0x4, 0x8
+
+    def profile_enable(self, on=True):
+        """on: True / False (every kind / none), or a mask of PROF_COPY | PROF_WRITEBACK | PROF_VERIFY."""
         check(_declare().tsa_test_profile_enable(self.h, int(on)))
 
     def profile_read(self, wait: bool = True) -> dict:
