@@ -53,6 +53,33 @@ SS_API ss_status tsa_test_dg_stamps(const ss_ctx* c, uint64_t* out, uint32_t cap
  * off the device), so that its next landing fails the device check (verify_hash = 2). SS_E_INVALID otherwise. */
 SS_API ss_status tsa_test_dg_corrupt_block(ss_ctx* c, int gated, int unit, uint64_t offset);
 
+/* The device-gated cache state machine alone (no device, no context): this library's DgCore driven on an eager
+ * transport whose copies, entries, events and file reads complete at once - the reference's canonical schedule
+ * (reference tests/test_dg.cpp:201) - so its placement can be compared with the reference core's on the CPU. Each
+ * token: per gated layer the export mask from the table as the device would read it, serve_demand, serve_use, the
+ * deferred write-back slice, then the boundary and the ownership check. */
+typedef struct tsa_test_dgcore_config {
+  const uint32_t* n_units; /* per gated layer */
+  uint32_t n_gated;
+  uint32_t persistent_slots, bank_slots, blocks, spare_target;
+  uint32_t prefetch_reserve; /* 0xFFFFFFFF: automatic (min(24, spare_target / 4)) */
+  uint32_t prefetch_per_layer, prefetch_per_token;
+  uint32_t wb_defer, wb_on_d2h, inclusive;
+  const uint64_t* part_bytes;
+  uint32_t n_parts;
+  uint32_t disk_tier, home_blocks, disk_staging, clean_evict, disk_prefetch;
+  const uint8_t* disk; /* three-tier: 1 per key for the plan's file tier (key order) */
+} tsa_test_dgcore_config;
+SS_API ss_status tsa_test_dgcore_open(const tsa_test_dgcore_config* cfg, const uint32_t* order, uint32_t n_order,
+                                      void** out);
+/* ids [n_gated][n]; table_out [keys]; counts [n_counts] in the order of tsa_test_dgcore_counter_names. */
+SS_API ss_status tsa_test_dgcore_token(void* h, const uint32_t* ids, uint32_t n, int32_t* table_out, uint64_t* counts,
+                                       uint32_t n_counts);
+SS_API const char* tsa_test_dgcore_counter_names(void);
+/* Three-tier: the pinned homes, most recently homed first; the return is the count. */
+SS_API uint32_t tsa_test_dgcore_host_order(void* h, uint32_t* out, uint32_t cap);
+SS_API void tsa_test_dgcore_close(void* h);
+
 #ifdef __cplusplus
 }
 #endif

@@ -60,6 +60,9 @@ def lib() -> C.CDLL:
             "refdg_token": (C.c_int, [vp, C.POINTER(u32), u32, C.POINTER(u32), u32, C.POINTER(i32), C.POINTER(u64)]),
             "refdg_counter_names": (C.c_char_p, []),
             "refdg_residency": (u32, [vp, C.POINTER(u32), u32]),
+            "refdg_open_disk": (vp, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, C.POINTER(u64), u32,
+                                     C.POINTER(u32), u32, u32, u32, u32, u32, C.POINTER(C.c_uint8)]),
+            "refdg_host_order": (u32, [vp, C.POINTER(u32), u32]),
             "refdg_close": (None, [vp]),
             "refdg_cpu_baseline": (C.c_int, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, C.POINTER(u64), u32,
                                               u64, C.POINTER(u32), u32, C.c_char_p, C.POINTER(u64), C.POINTER(u64),
@@ -203,13 +206,21 @@ class RefDg:
     """The reference DgCore on an immediate transport (its canonical schedule)."""
 
     def __init__(self, n_units, persistent, bank, blocks, spare_target, part_bytes, order, prefetch_reserve=0xFFFFFFFF,
-                 pf_layer=4, pf_token=48, wb_defer=1, wb_on_d2h=1, inclusive=0):
+                 pf_layer=4, pf_token=48, wb_defer=1, wb_on_d2h=1, inclusive=0, disk=None):
+        """disk (three-tier): dict(flags=[keys] 0/1 file-tier, home_blocks=P, disk_staging=S, clean_evict=0,
+        disk_prefetch=0); the prefetch budgets then take their defaults."""
         L = lib()
         nu = (u32 * len(n_units))(*n_units)
         pb = (u64 * len(part_bytes))(*part_bytes)
         od = (u32 * len(order))(*order)
-        self.h = L.refdg_open(nu, len(n_units), persistent, bank, blocks, spare_target, prefetch_reserve, pf_layer,
-                              pf_token, wb_defer, wb_on_d2h, inclusive, pb, len(part_bytes), od, len(order))
+        if disk is None:
+            self.h = L.refdg_open(nu, len(n_units), persistent, bank, blocks, spare_target, prefetch_reserve, pf_layer,
+                                  pf_token, wb_defer, wb_on_d2h, inclusive, pb, len(part_bytes), od, len(order))
+        else:
+            fl = (C.c_uint8 * sum(n_units))(*disk["flags"])
+            self.h = L.refdg_open_disk(nu, len(n_units), persistent, bank, blocks, spare_target, wb_defer, inclusive,
+                                       pb, len(part_bytes), od, len(order), disk["home_blocks"], disk["disk_staging"],
+                                       disk.get("clean_evict", 0), disk.get("disk_prefetch", 0), fl)
         if not self.h:
             raise RuntimeError("refdg_open failed")
         self.keys = sum(n_units)
@@ -235,6 +246,12 @@ class RefDg:
         L = lib()
         out = np.zeros(self.keys, dtype=np.uint32)
         n = L.refdg_residency(self.h, out.ctypes.data_as(C.POINTER(u32)), self.keys)
+        return [int(x) for x in out[:n]]
+
+    def host_order(self):
+        """Three-tier: the pinned homes, most recently homed first."""
+        out = np.zeros(self.keys, dtype=np.uint32)
+        n = lib().refdg_host_order(self.h, out.ctypes.data_as(C.POINTER(u32)), self.keys)
         return [int(x) for x in out[:n]]
 
     def close(self):

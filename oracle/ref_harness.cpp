@@ -112,6 +112,7 @@ class Eager final : public ts::DgTransport {
   void sync(Stream) override {}
   void upload_table(const int32_t*, uint32_t) override {}
   void upload_table_ranges(const int32_t*, const uint32_t*, uint32_t) override {}
+  void read_unit(uint32_t, int32_t) override {}  // three-tier: the file read completes at once too
 
  private:
   std::vector<uint64_t> parts_;
@@ -127,10 +128,44 @@ struct RefDg {
 
 extern "C" {
 
+// Three-tier options of refdg_open (disk_tier 0: none of the others is read): home_blocks = the plan's pinned units,
+// disk_staging buffers, the file-tier flags of the keys (keys entries, key order), clean_evict, disk_prefetch.
+struct RefDiskOpts {
+  uint32_t disk_tier = 0, home_blocks = 0, disk_staging = 0, clean_evict = 0, disk_prefetch = 0;
+  const uint8_t* disk = nullptr;
+};
+void* refdg_open_impl(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
+                      uint32_t spare_target, uint32_t prefetch_reserve, uint32_t pf_layer, uint32_t pf_token,
+                      uint32_t wb_defer, uint32_t wb_on_d2h, uint32_t inclusive, const uint64_t* part_bytes,
+                      uint32_t n_parts, const uint32_t* order, uint32_t n_order, const RefDiskOpts& dk);
+
 void* refdg_open(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
                  uint32_t spare_target, uint32_t prefetch_reserve, uint32_t pf_layer, uint32_t pf_token,
                  uint32_t wb_defer, uint32_t wb_on_d2h, uint32_t inclusive, const uint64_t* part_bytes,
                  uint32_t n_parts, const uint32_t* order, uint32_t n_order) {
+  return refdg_open_impl(n_units, G, persistent, bank, blocks, spare_target, prefetch_reserve, pf_layer, pf_token,
+                         wb_defer, wb_on_d2h, inclusive, part_bytes, n_parts, order, n_order, RefDiskOpts{});
+}
+
+void* refdg_open_disk(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
+                      uint32_t spare_target, uint32_t wb_defer, uint32_t inclusive, const uint64_t* part_bytes,
+                      uint32_t n_parts, const uint32_t* order, uint32_t n_order, uint32_t home_blocks,
+                      uint32_t disk_staging, uint32_t clean_evict, uint32_t disk_prefetch, const uint8_t* disk) {
+  RefDiskOpts dk;
+  dk.disk_tier = 1;
+  dk.home_blocks = home_blocks;
+  dk.disk_staging = disk_staging;
+  dk.clean_evict = clean_evict;
+  dk.disk_prefetch = disk_prefetch;
+  dk.disk = disk;
+  return refdg_open_impl(n_units, G, persistent, bank, blocks, spare_target, 0xFFFFFFFFu, 4, 48, wb_defer, 1, inclusive,
+                         part_bytes, n_parts, order, n_order, dk);
+}
+
+void* refdg_open_impl(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
+                      uint32_t spare_target, uint32_t prefetch_reserve, uint32_t pf_layer, uint32_t pf_token,
+                      uint32_t wb_defer, uint32_t wb_on_d2h, uint32_t inclusive, const uint64_t* part_bytes,
+                      uint32_t n_parts, const uint32_t* order, uint32_t n_order, const RefDiskOpts& dk) {
   try {
     auto* r = new RefDg;
     r->t = std::make_unique<Eager>(std::vector<uint64_t>(part_bytes, part_bytes + n_parts));
@@ -149,8 +184,20 @@ void* refdg_open(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint3
     c.inclusive = inclusive;
     c.max_ids = bank;
     c.pf_legacy = true;
+    std::vector<uint8_t> disk;
+    if (dk.disk_tier) {
+      c.disk_tier = true;
+      c.disk_prefetch = dk.disk_prefetch != 0;
+      c.home_blocks = dk.home_blocks;
+      c.disk_staging = dk.disk_staging;
+      c.disk_queue = 1;
+      c.clean_evict = dk.clean_evict != 0;
+      uint32_t keys = 0;
+      for (uint32_t g = 0; g < G; ++g) keys += n_units[g];
+      disk.assign(dk.disk, dk.disk + keys);
+    }
     r->core = std::make_unique<ts::DgCore>(c, r->t.get());
-    r->core->place(std::vector<uint32_t>(order, order + n_order));
+    r->core->place(std::vector<uint32_t>(order, order + n_order), dk.disk_tier ? &disk : nullptr);
     return r;
   } catch (const std::exception& e) {
     std::fprintf(stderr, "refdg_open: %s\n", e.what());
@@ -188,7 +235,8 @@ int refdg_token(void* h, const uint32_t* ids, uint32_t n, const uint32_t* pred, 
                           s.miss_layers,   s.covered_waits, s.wb_deferred,    s.wb_cancelled, s.wb_forced,
                           s.wb_boundary_flushed, s.wb_issued_bytes, s.wb_cancelled_bytes, s.inclusive_kept,
                           s.inclusive_drops, uint64_t(c.free_slots()), uint64_t(c.free_blocks()),
-                          uint64_t(c.on_device()), uint64_t(c.backed_units())};
+                          uint64_t(c.on_device()), uint64_t(c.backed_units()), s.disk_reads, s.disk_drops,
+                          s.disk_discards, s.clean_drops, uint64_t(c.file_units())};
     std::memcpy(counts, v, sizeof v);
     return 0;
   } catch (const std::exception& e) {
@@ -201,13 +249,21 @@ const char* refdg_counter_names() {
   return "tokens lookups misses covered fetched prefetched prefetch_used pred_invalid resurrected bank_serves evicted "
          "evict_short writebacks_done predicted predicted_true miss_layers covered_waits wb_deferred wb_cancelled "
          "wb_forced wb_boundary_flushed wb_issued_bytes wb_cancelled_bytes inclusive_kept inclusive_drops free_slots "
-         "free_blocks on_device backed_units";
+         "free_blocks on_device backed_units disk_reads disk_drops disk_discards clean_drops file_units";
 }
 
 // The device keys in recency order, most recent first.
 uint32_t refdg_residency(void* h, uint32_t* out, uint32_t cap) {
   auto* r = static_cast<RefDg*>(h);
   const std::vector<uint32_t> v = r->core->residency();
+  for (uint32_t i = 0; i < cap && i < v.size(); ++i) out[i] = v[i];
+  return uint32_t(v.size());
+}
+
+// Three-tier: the pinned homes in recency order, most recently homed first.
+uint32_t refdg_host_order(void* h, uint32_t* out, uint32_t cap) {
+  auto* r = static_cast<RefDg*>(h);
+  const std::vector<uint32_t> v = r->core->host_order();
   for (uint32_t i = 0; i < cap && i < v.size(); ++i) out[i] = v[i];
   return uint32_t(v.size());
 }

@@ -1,0 +1,191 @@
+"""The device-gated cache state machine against the reference's own, on the CPU (no GPU): this library's DgCore
+(tsa_test_dgcore_*: the product's core on an eager transport) and the reference DgCore compiled from its sources
+(oracle/_ref, refdg_*), on the same configuration, open-time priority and token route stream. After every token the
+slot table, the counters and (three-tier) the pinned homes' recency order must be identical.
+
+Configurations are drawn at random per seed: 2-6 gated layers of 4-16 units, 1-4 ids per layer (sometimes repeated,
+the batch-union case), residents, spare slots and spare blocks, clean copies (dg_inclusive_blocks), deferred or
+boundary write-backs; three-tier adds a file tier (a random share of the non-resident units), clean_evict and
+disk prefetch off. Routes are skewed (Zipf-like over a per-layer permutation) so that hits, misses, bank serves,
+resurrections and write-backs all occur. The reference's own CPU tests drive its core the same way
+(tests/test_dg.cpp:201)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import ref
+
+u32, u64 = C.c_uint32, C.c_uint64
+
+
+class DgCoreConfig(C.Structure):
+    _fields_ = [("n_units", C.POINTER(u32)), ("n_gated", u32), ("persistent_slots", u32), ("bank_slots", u32),
+                ("blocks", u32), ("spare_target", u32), ("prefetch_reserve", u32), ("prefetch_per_layer", u32),
+                ("prefetch_per_token", u32), ("wb_defer", u32), ("wb_on_d2h", u32), ("inclusive", u32),
+                ("part_bytes", C.POINTER(u64)), ("n_parts", u32), ("disk_tier", u32), ("home_blocks", u32),
+                ("disk_staging", u32), ("clean_evict", u32), ("disk_prefetch", u32),
+                ("disk", C.POINTER(C.c_uint8))]
+
+
+def _lib():
+    import tierstream_amd as tsa
+    L = tsa.lib()
+    L.tsa_test_dgcore_open.argtypes = [C.POINTER(DgCoreConfig), C.POINTER(u32), u32, C.POINTER(C.c_void_p)]
+    L.tsa_test_dgcore_open.restype = C.c_int
+    L.tsa_test_dgcore_token.argtypes = [C.c_void_p, C.POINTER(u32), u32, C.POINTER(C.c_int32), C.POINTER(u64), u32]
+    L.tsa_test_dgcore_token.restype = C.c_int
+    L.tsa_test_dgcore_counter_names.restype = C.c_char_p
+    L.tsa_test_dgcore_host_order.argtypes = [C.c_void_p, C.POINTER(u32), u32]
+    L.tsa_test_dgcore_host_order.restype = u32
+    L.tsa_test_dgcore_close.argtypes = [C.c_void_p]
+    L.tsa_test_dgcore_close.restype = None
+    return tsa, L
+
+
+class OurCore:
+    def __init__(self, n_units, persistent, bank, blocks, spare_target, part_bytes, order, wb_defer, inclusive,
+                 disk=None):
+        self.tsa, self.L = _lib()
+        self._keep = []
+        nu = (u32 * len(n_units))(*n_units)
+        pb = (u64 * len(part_bytes))(*part_bytes)
+        od = (u32 * len(order))(*order)
+        c = DgCoreConfig()
+        c.n_units, c.n_gated = nu, len(n_units)
+        c.persistent_slots, c.bank_slots, c.blocks, c.spare_target = persistent, bank, blocks, spare_target
+        c.prefetch_reserve, c.prefetch_per_layer, c.prefetch_per_token = 0xFFFFFFFF, 4, 48
+        c.wb_defer, c.wb_on_d2h, c.inclusive = wb_defer, 1, inclusive
+        c.part_bytes, c.n_parts = pb, len(part_bytes)
+        if disk:
+            fl = (C.c_uint8 * sum(n_units))(*disk["flags"])
+            c.disk_tier, c.home_blocks, c.disk_staging = 1, disk["home_blocks"], disk["disk_staging"]
+            c.clean_evict, c.disk_prefetch, c.disk = disk.get("clean_evict", 0), 0, fl
+            self._keep.append(fl)
+        self._keep += [nu, pb, od, c]
+        self.h = C.c_void_p()
+        self.tsa.check(self.L.tsa_test_dgcore_open(C.byref(c), od, len(order), C.byref(self.h)))
+        self.keys = sum(n_units)
+        self.names = self.L.tsa_test_dgcore_counter_names().decode().split()
+
+    def token(self, ids):
+        x = np.ascontiguousarray(ids, dtype=np.uint32)
+        table = np.zeros(self.keys, dtype=np.int32)
+        counts = np.zeros(len(self.names), dtype=np.uint64)
+        self.tsa.check(self.L.tsa_test_dgcore_token(self.h, x.ctypes.data_as(C.POINTER(u32)), x.shape[1],
+                                                    table.ctypes.data_as(C.POINTER(C.c_int32)),
+                                                    counts.ctypes.data_as(C.POINTER(u64)), len(self.names)))
+        return table, {k: int(v) for k, v in zip(self.names, counts)}
+
+    def host_order(self):
+        out = np.zeros(self.keys, dtype=np.uint32)
+        n = self.L.tsa_test_dgcore_host_order(self.h, out.ctypes.data_as(C.POINTER(u32)), self.keys)
+        return [int(v) for v in out[:n]]
+
+    def close(self):
+        if self.h:
+            self.L.tsa_test_dgcore_close(self.h)
+            self.h = None
+
+
+def _case(seed, three):
+    rng = np.random.default_rng(seed)
+    G = int(rng.integers(2, 7))
+    n_units = [int(rng.integers(4, 17)) for _ in range(G)]
+    keys = sum(n_units)
+    B = int(rng.integers(1, 5))
+    repeats = bool(rng.integers(0, 4) == 0)
+    prio = [int(k) for k in rng.permutation(keys)]
+    R = int(rng.integers(0, keys // 2 + 1))
+    D = int(rng.integers(1, 5))
+    non_res = keys - R
+    D = min(D, max(non_res, 1))
+    persistent = R + D
+    spare_target = int(rng.integers(max(0, D - 1), D + 1))
+    order = prio[:R] + list(range(keys))  # the residents by priority, then key order (as the context builds it)
+    residents = set(prio[:R])
+    Q = int(rng.integers(1, 7))
+    inclusive = int(rng.integers(0, Q)) if rng.integers(0, 2) else 0
+    wb_defer = int(rng.integers(0, 2))
+    parts = [int(p) for p in rng.choice([256, 512, 1024], size=int(rng.integers(1, 4)))]
+    disk = None
+    if three:
+        cand = [k for k in range(keys) if k not in residents]
+        f = int(rng.integers(1, max(2, len(cand))))
+        file_keys = set(int(k) for k in rng.choice(cand, size=min(f, len(cand)), replace=False))
+        flags = [1 if k in file_keys else 0 for k in range(keys)]
+        P = non_res - len(file_keys)
+        blocks = P + Q
+        disk = dict(flags=flags, home_blocks=P, disk_staging=int(rng.integers(1, 9)),
+                    clean_evict=int(rng.integers(0, 2)))
+    else:
+        blocks = non_res + Q
+    tokens = int(rng.integers(16, 33))
+    routes = np.zeros((tokens, G, B), dtype=np.uint32)
+    perms = [rng.permutation(n) for n in n_units]
+    for t in range(tokens):
+        for g in range(G):
+            w = 1.0 / np.arange(1, n_units[g] + 1) ** 1.1
+            w /= w.sum()
+            if repeats:
+                ids = rng.choice(n_units[g], size=B, replace=True, p=w)
+            else:
+                ids = rng.choice(n_units[g], size=min(B, n_units[g]), replace=False, p=w)
+                ids = np.resize(ids, B)
+            routes[t, g] = perms[g][ids]
+    return dict(n_units=n_units, persistent=persistent, bank=B, blocks=blocks, spare_target=spare_target,
+                parts=parts, order=order, wb_defer=wb_defer, inclusive=inclusive, disk=disk, routes=routes)
+
+
+def _run(seed, three):
+    if not ref.available():
+        pytest.skip("oracle/_ref (the reference core) is not built")
+    c = _case(seed, three)
+    kw = dict(wb_defer=c["wb_defer"], inclusive=c["inclusive"])
+    ours = OurCore(c["n_units"], c["persistent"], c["bank"], c["blocks"], c["spare_target"], c["parts"], c["order"],
+                   disk=c["disk"], **kw)
+    theirs = ref.RefDg(c["n_units"], c["persistent"], c["bank"], c["blocks"], c["spare_target"], c["parts"],
+                       c["order"], disk=c["disk"], **kw)
+    seen = {}
+    try:
+        for t, ids in enumerate(c["routes"]):
+            got_t, got = ours.token(ids)
+            want_t, want = theirs.token(ids)
+            assert np.array_equal(got_t, want_t), (seed, t, "table")
+            for k, v in got.items():
+                assert v == want[k], (seed, t, k, v, want[k])
+            if three:
+                assert ours.host_order() == theirs.host_order(), (seed, t, "pinned recency order")
+            for k in got:
+                seen[k] = seen.get(k, 0) + got[k]
+        return seen
+    finally:
+        ours.close()
+        theirs.close()
+
+
+@pytest.mark.parametrize("seed", range(150))
+def test_two_tier_placement_matches_reference(seed):
+    _run(seed, False)
+
+
+@pytest.mark.parametrize("seed", range(150))
+def test_three_tier_placement_matches_reference(seed):
+    _run(1000 + seed, True)
+
+
+def test_cases_exercise_the_paths():
+    """The random cases together reach every path the parity relies on (a case generator that stopped producing
+    misses, write-backs or file reads would pass vacuously)."""
+    if not ref.available():
+        pytest.skip("oracle/_ref (the reference core) is not built")
+    tot2, tot3 = {}, {}
+    for s in range(40):
+        for k, v in _run(s, False).items():
+            tot2[k] = tot2.get(k, 0) + v
+        for k, v in _run(1000 + s, True).items():
+            tot3[k] = tot3.get(k, 0) + v
+    for k in ("misses", "bank_serves", "evicted", "writebacks_done", "resurrected", "inclusive_drops", "wb_forced"):
+        assert tot2[k] > 0, k
+    for k in ("disk_reads", "disk_drops", "disk_discards", "clean_drops", "writebacks_done", "bank_serves"):
+        assert tot3[k] > 0, k

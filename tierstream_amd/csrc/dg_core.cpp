@@ -38,6 +38,10 @@ DgCore::DgCore(const DgConfig& cfg, DgTransport* t) : c_(cfg), t_(t) {
   for (uint32_t p = 0; p < t_->parts(); ++p) unit_bytes_ += t_->part_bytes(p);
   require(c_.inclusive < c_.blocks || c_.inclusive == 0, SS_E_INVALID,
           "device-gated: the inclusive share must leave a block for write-backs");
+  require(!c_.disk_tier || c_.disk_staging >= 1, SS_E_INVALID, "device-gated: the disk tier needs staging buffers");
+  require(c_.disk_tier || (!c_.disk_prefetch && !c_.disk_staging && !c_.home_blocks && !c_.clean_evict), SS_E_INVALID,
+          "device-gated: disk options without the disk tier");
+  if (c_.disk_tier) stage_ev_.assign(c_.disk_staging, nullptr);
   if (c_.wb_defer) {
     wb_stream_ = c_.wb_on_d2h ? DgTransport::kD2h : DgTransport::kDem;
     layer_bytes_ = c_.wb_layer_bytes ? c_.wb_layer_bytes : t_->part_bytes(0);
@@ -95,7 +99,11 @@ void DgCore::sweep_events() {
     if (block_ev_[b] && t_->query(block_ev_[b])) detach(block_ev_, int32_t(b));
 }
 
-void DgCore::place(const std::vector<uint32_t>& priority) {
+void DgTransport::read_unit(uint32_t, int32_t) {
+  fail(SS_E_UNSUPPORTED, "device-gated: this transport cannot read a unit from its file");
+}
+
+void DgCore::place(const std::vector<uint32_t>& priority, const std::vector<uint8_t>* disk) {
   const uint32_t dev_max = c_.persistent_slots - c_.spare_target;
   std::vector<uint8_t> placed(keys_, 0);
   std::vector<uint32_t> order;
@@ -107,18 +115,51 @@ void DgCore::place(const std::vector<uint32_t>& priority) {
     }
   }
   const uint32_t dev0 = uint32_t(order.size());
-  require(uint64_t(keys_) - dev0 <= c_.blocks, SS_E_CAPACITY, "device-gated: fewer host blocks than non-resident units");
+  const bool three = c_.disk_tier;
+  const std::vector<uint8_t> none(three && !disk ? keys_ : 0, 0);
+  if (three && !disk) disk = &none;
+  require(!three || disk->size() == keys_, SS_E_INVALID, "device-gated: the disk flags do not cover the keys");
+  // three-tier: the keys off the device that get a pinned home, plan-pinned first, then file-tier, each in priority
+  // order (the priority list, duplicates dropped, then any key it missed), up to home_blocks
+  std::vector<uint8_t> blocked(keys_, 0);
+  std::vector<uint32_t> host_rank;
+  if (three) {
+    std::vector<uint8_t> seen(keys_, 0);
+    std::vector<uint32_t> prio;
+    for (uint32_t k : priority)
+      if (!seen[k]) {
+        seen[k] = 1;
+        prio.push_back(k);
+      }
+    for (uint32_t k = 0; k < keys_; ++k)
+      if (!seen[k]) prio.push_back(k);
+    const uint32_t cap = std::min(c_.home_blocks, c_.blocks);
+    for (int pass = 0; pass < 2; ++pass)
+      for (uint32_t k : prio)
+        if (!placed[k] && (*disk)[k] == uint8_t(pass) && host_rank.size() < cap) {
+          blocked[k] = 1;
+          host_rank.push_back(k);
+        }
+  } else {
+    require(uint64_t(keys_) - dev0 <= c_.blocks, SS_E_CAPACITY,
+            "device-gated: fewer host blocks than non-resident units");
+  }
   int32_t next_block = 0;
-  on_host_ = backed_ = 0;
+  on_host_ = on_file_ = backed_ = 0;
+  hhead_ = htail_ = kNone;
   for (uint32_t k = 0; k < keys_; ++k) {
     Entry& x = e_[k];
     x = Entry{};
-    if (!placed[k]) {
+    if (!placed[k] && (!three || blocked[k])) {
       x.home = Home::Host;
       x.block = next_block++;
-      ++on_host_;
+      if (!three) ++on_host_;
+    } else if (!placed[k]) {
+      x.home = Home::File;
+      ++on_file_;
     }
   }
+  for (size_t i = host_rank.size(); i-- > 0;) hpush(host_rank[i]);  // the first by priority most recent
   for (uint32_t i = 0; i < dev0; ++i) {
     Entry& x = e_[order[i]];
     x.home = Home::Device;
@@ -182,7 +223,7 @@ uint32_t DgCore::collect() {
       x.home = Home::Host;
       x.block = w.block;
       x.slot = -1;
-      ++on_host_;
+      hpush(w.key);
       free_slots_.push_back(w.slot);
       attach(slot_ev_, w.slot, w.done);
       attach(block_ev_, w.block, w.done);
@@ -271,23 +312,86 @@ int32_t DgCore::take_bank_slot(uint32_t g) {
   const int32_t slot = int32_t(bank_first_ + idx);
   const uint32_t old = bank_key_[idx];
   if (old != kNone && e_[old].home == Home::Bank && e_[old].slot == slot) {
-    to_block(old);
+    to_lower(old);  // its block, or (read from its file) its file
     write_entry(DgTransport::kDem, old, -1);
   }
   bank_key_[idx] = kNone;
   return slot;
 }
 
-void DgCore::to_block(uint32_t k) {
+void DgCore::to_lower(uint32_t k) {
   Entry& x = e_[k];
   x.slot = -1;
   if (x.backed) {
     x.backed = false;
     --backed_;
   }
-  if (x.block < 0) broken("a key without a block left the device without a write-back");
-  x.home = Home::Host;
+  if (x.block >= 0) {
+    x.home = Home::Host;
+    hpush(k);
+  } else {
+    if (!c_.disk_tier) broken("a key without a block left the device without a write-back");
+    x.home = Home::File;
+    ++on_file_;
+  }
+}
+
+// ---- three-tier: the pinned homes' recency list (most recently homed at the head) ----
+void DgCore::hpush(uint32_t k) {
   ++on_host_;
+  if (!c_.disk_tier) return;
+  Entry& x = e_[k];
+  x.hprev = kNone;
+  x.hnext = hhead_;
+  if (hhead_ != kNone) e_[hhead_].hprev = k;
+  else htail_ = k;
+  hhead_ = k;
+  x.in_hlist = true;
+}
+
+void DgCore::hunlink(uint32_t k) {
+  --on_host_;
+  if (!c_.disk_tier) return;
+  Entry& x = e_[k];
+  if (!x.in_hlist) broken("a pinned home outside the recency list");
+  if (x.hprev != kNone) e_[x.hprev].hnext = x.hnext;
+  else hhead_ = x.hnext;
+  if (x.hnext != kNone) e_[x.hnext].hprev = x.hprev;
+  else htail_ = x.hprev;
+  x.hprev = x.hnext = kNone;
+  x.in_hlist = false;
+}
+
+std::vector<uint32_t> DgCore::host_order() const {
+  std::vector<uint32_t> out;
+  for (uint32_t k = hhead_; k != kNone; k = e_[k].hnext) out.push_back(k);
+  return out;
+}
+
+// The least recently homed pinned unit goes to its file (no copy: the file holds its bytes) and its block is free at
+// once (a pinned home's block is quiescent: nothing copies into or out of it).
+bool DgCore::drop_host_lru() {
+  if (!c_.disk_tier || htail_ == kNone) return false;
+  const uint32_t k = htail_;
+  Entry& x = e_[k];
+  hunlink(k);
+  free_blocks_.push_back(x.block);
+  x.block = -1;
+  x.home = Home::File;
+  ++on_file_;
+  ++st_.disk_drops;
+  return true;
+}
+
+// The next staging buffer (round robin); the copy that last read it must have landed before a read overwrites it.
+int32_t DgCore::take_stage() {
+  const uint32_t i = stage_next_;
+  stage_next_ = (i + 1) % c_.disk_staging;
+  if (stage_ev_[i] && !t_->query(stage_ev_[i])) {
+    t_->event_sync(stage_ev_[i]);
+    ++st_.disk_stage_waits;
+  }
+  return int32_t(c_.blocks + i);
 }
 
 void DgCore::begin_token(uint32_t seq) {
@@ -343,6 +447,9 @@ bool DgCore::fetch(uint32_t g, uint32_t unit, bool prefetch) {
     }
     case Home::Host:
       break;
+    case Home::File:  // three-tier: read from its file below; a prefetch only with disk_prefetch
+      if (prefetch && !c_.disk_prefetch) return false;
+      break;
   }
   int32_t slot = -1;
   bool bank = false;
@@ -370,13 +477,27 @@ bool DgCore::fetch(uint32_t g, uint32_t unit, bool prefetch) {
     }
   }
   const DgTransport::Stream s = prefetch ? DgTransport::kPf : DgTransport::kDem;
-  // the slot's last write-back and the block's incoming write-back (if still copying) come first
-  t_->wait_copy_in(s, slot, x.block, slot_ev_[size_t(slot)], block_ev_[size_t(x.block)]);
-  detach(slot_ev_, slot);
-  detach(block_ev_, x.block);
-  t_->h2d(s, slot, x.block);
+  if (x.home == Home::File) {  // its bytes from its file into a staging buffer, then the same copy from there
+    const int32_t stage = take_stage();
+    t_->read_unit(k, stage);
+    ++st_.disk_reads;
+    st_.disk_read_bytes += unit_bytes_;
+    t_->wait_copy_in(s, slot, stage, slot_ev_[size_t(slot)], nullptr);  // (no write-back touches a staging buffer)
+    detach(slot_ev_, slot);
+    t_->h2d(s, slot, stage);
+    void*& ev = stage_ev_[uint32_t(stage) - c_.blocks];  // the buffer is reusable once this copy landed
+    if (!ev) ev = event();
+    t_->record(ev, s);
+    --on_file_;
+  } else {
+    // the slot's last write-back and the block's incoming write-back (if still copying) come first
+    t_->wait_copy_in(s, slot, x.block, slot_ev_[size_t(slot)], block_ev_[size_t(x.block)]);
+    detach(slot_ev_, slot);
+    detach(block_ev_, x.block);
+    t_->h2d(s, slot, x.block);
+    hunlink(k);
+  }
   write_entry(s, k, slot, true);
-  --on_host_;
   x.slot = slot;
   x.via_prefetch = prefetch;
   x.used = false;
@@ -521,10 +642,10 @@ void DgCore::end_token() {
     }
   }
   coming_.clear();
-  for (uint32_t k : banked_) {  // bank units: back to their blocks
+  for (uint32_t k : banked_) {  // bank units: back to their blocks (three-tier: read from their file, to it)
     Entry& x = e_[k];
     if (x.home == Home::Bank) {
-      to_block(k);
+      to_lower(k);
       table_[k] = -1;
     }
     if (x.pf_done) {
@@ -549,12 +670,20 @@ void DgCore::end_token() {
     const uint32_t prev = e_[k].prev;
     Entry& x = e_[k];
     if (x.home == Home::Device && !x.wb_pending) {
-      if (x.backed) {  // a clean copy: its block is its home again, no copy
-        ++st_.inclusive_drops;
+      // a clean copy (its block is its home again), or three-tier with no block to write into after the least
+      // recently homed pinned unit was offered (clean_evict: not even that): its file. No copy either way.
+      const bool clean = !x.backed && clean_now();
+      if (x.backed || clean || (free_blocks_.empty() && !drop_host_lru() && c_.disk_tier)) {
+        if (x.backed) ++st_.inclusive_drops;
+        else ++st_.disk_discards;
+        if (clean) {
+          ++st_.clean_drops;
+          st_.clean_drop_bytes += unit_bytes_;
+        }
         unlink(k);
         --on_device_;
         free_slots_.push_back(x.slot);
-        to_block(k);
+        to_lower(k);
         table_[k] = -1;
         ++st_.evicted;
         ++lc_[gated_of(k)].evicted;
@@ -634,7 +763,7 @@ void DgCore::set_prefetch_budget(uint32_t per_layer, uint32_t per_token) {
 
 void DgCore::check() const {
   std::vector<uint8_t> slot_used(slots_, 0), block_used(c_.blocks, 0);
-  uint32_t dev = 0, host = 0;
+  uint32_t dev = 0, host = 0, file = 0;
   for (uint32_t k = 0; k < keys_; ++k) {
     const Entry& x = e_[k];
     switch (x.home) {
@@ -650,11 +779,18 @@ void DgCore::check() const {
       case Home::Host:
         ++host;
         if (x.slot != -1) broken("a pinned home with a slot");
+        if (c_.disk_tier && !x.in_hlist) broken("a pinned home outside the recency list");
+        break;
+      case Home::File:
+        ++file;
+        if (!c_.disk_tier || x.slot != -1 || x.block != -1 || table_[k] >= 0)
+          broken("file home of key " + std::to_string(k) + " with a slot, a block or an entry");
         break;
     }
+    if (x.home != Home::Host && x.in_hlist) broken("key " + std::to_string(k) + " in the recency list off its block");
     if (x.block >= 0 && (uint32_t(x.block) >= c_.blocks || block_used[size_t(x.block)]++))
       broken("block of key " + std::to_string(k) + " shared");
-    if ((x.home == Home::Host || x.home == Home::Evicting || x.home == Home::Bank) && x.block < 0)
+    if ((x.home == Home::Host || x.home == Home::Evicting || (x.home == Home::Bank && !c_.disk_tier)) && x.block < 0)
       broken("key " + std::to_string(k) + " has no block in a home that needs one");
     if (x.home == Home::Device && table_[k] != x.slot) broken("device key " + std::to_string(k) + " unpublished");
     if ((x.home == Home::Host || x.home == Home::Evicting) && table_[k] >= 0)
@@ -668,6 +804,13 @@ void DgCore::check() const {
     if (w.discard && block_used[size_t(w.block)]++) broken("a discarded write-back's block also owned");
   if (dev != on_device_) broken("device count");
   if (host != on_host_) broken("pinned count");
+  if (file != on_file_) broken("file count");
+  if (c_.disk_tier) {
+    uint32_t n = 0;
+    for (uint32_t k = hhead_; k != kNone; k = e_[k].hnext)
+      if (++n > keys_ || e_[k].home != Home::Host) broken("the pinned recency list");
+    if (n != on_host_) broken("the pinned recency list's length");
+  }
 }
 
 }  // namespace tsa

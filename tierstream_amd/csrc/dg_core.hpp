@@ -42,6 +42,9 @@ class DgTransport {
   virtual void sync(Stream s) = 0;
   virtual bool query(void* ev) = 0;  // non-blocking: the event's last record has completed
   virtual void upload_table(const int32_t* table, uint32_t n) = 0;  // the whole table on kDem, then sync
+  // Three-tier: the unit's bytes from its file into staging block `block` (blocks .. blocks + disk_staging - 1: the
+  // host layout of a unit), synchronously; the core then copies it in from that block as from a pinned home.
+  virtual void read_unit(uint32_t key, int32_t block);
   // Before h2d(s, slot, block): slot_ev / block_ev (either may be null) are the write-backs that may still read the
   // slot or write the block. The default makes s wait for both; a transport that tracks its copies per part may let
   // each part of the next h2d wait only for the same part of those write-backs.
@@ -74,6 +77,15 @@ struct DgConfig {
   bool wb_defer = true, wb_on_d2h = true;
   uint64_t wb_layer_bytes = 0, wb_max_outstanding = 0;
   uint32_t inclusive = 0;  // device units that may keep their block as a clean copy
+  // Three-tier (SS_DG_DISK_TIER): keys off the device and without a pinned home live in their file (Home::File) and
+  // a miss reads them through one of disk_staging staging buffers (round robin). home_blocks: the blocks that are
+  // pinned homes at open (the plan's pinned units; the rest of `blocks` are spares). Pinned homes keep a recency list
+  // (most recently homed first); a victim that needs a block while none is free takes the least recently homed pinned
+  // unit's (that unit goes to its file, disk_drops), or with no pinned unit left goes to its file itself
+  // (disk_discards). clean_evict: such a victim goes to its file at once, no pinned unit displaced. disk_prefetch:
+  // a prefetch may read a file-homed unit.
+  bool disk_tier = false, disk_prefetch = false, clean_evict = false;
+  uint32_t home_blocks = 0, disk_staging = 0;
 };
 
 struct DgCounts {  // the subset of ss_dg_stats this core counts
@@ -83,6 +95,8 @@ struct DgCounts {  // the subset of ss_dg_stats this core counts
   uint64_t wb_deferred = 0, wb_cancelled = 0, wb_forced = 0, wb_boundary_flushed = 0;
   uint64_t wb_issued_bytes = 0, wb_completed_bytes = 0, wb_cancelled_bytes = 0, wb_boundary_flushed_bytes = 0;
   uint64_t wb_forced_wait_ns = 0, inclusive_kept = 0, inclusive_drops = 0;
+  uint64_t disk_reads = 0, disk_read_bytes = 0, disk_stage_waits = 0, disk_drops = 0, disk_discards = 0;
+  uint64_t clean_drops = 0, clean_drop_bytes = 0;
 };
 struct DgLayerCounts {
   uint64_t lookups = 0, misses = 0, fetched = 0, bank_serves = 0, prefetched = 0, prefetch_used = 0, evicted = 0;
@@ -90,7 +104,7 @@ struct DgLayerCounts {
 
 class DgCore {
  public:
-  enum class Home : uint8_t { Host, Device, Coming, Bank, Evicting };
+  enum class Home : uint8_t { Host, Device, Coming, Bank, Evicting, File };
 
   DgCore(const DgConfig& cfg, DgTransport* t);
   ~DgCore();
@@ -98,8 +112,11 @@ class DgCore {
   DgCore& operator=(const DgCore&) = delete;
 
   // Open: the first persistent_slots - spare_target distinct keys of `priority` take slots 0.. (the first one most
-  // recent); every other key takes a block, in key order; free slots are a stack with the lowest on top.
-  void place(const std::vector<uint32_t>& priority);
+  // recent); every other key takes a block, in key order; free slots are a stack with the lowest on top. Three-tier:
+  // `disk` flags the plan's file-tier keys; of the keys off the device, the plan-pinned ones and then the file-tier
+  // ones, each in `priority` order, take pinned homes up to home_blocks (blocks in key order; the recency list in
+  // priority order, the first most recent), every other key lives in its file.
+  void place(const std::vector<uint32_t>& priority, const std::vector<uint8_t>* disk = nullptr);
   uint32_t keys() const { return keys_; }
   uint32_t gated() const { return uint32_t(base_.size() - 1); }
   uint32_t units(uint32_t g) const { return base_[g + 1] - base_[g]; }
@@ -114,6 +131,8 @@ class DgCore {
   uint32_t free_blocks() const { return uint32_t(free_blocks_.size()); }
   const std::vector<int32_t>& free_block_ids() const { return free_blocks_; }  // the free stack, top last
   uint32_t on_device() const { return on_device_; }
+  uint32_t file_units() const { return on_file_; }
+  std::vector<uint32_t> host_order() const;  // three-tier: the pinned homes, most recently homed first
   uint32_t backed_units() const { return backed_; }
   uint64_t outstanding_bytes() const { return outstanding_; }
   uint32_t deferred() const { return uint32_t(deferred_.size()); }
@@ -141,6 +160,8 @@ class DgCore {
     uint32_t prev = kNone, next = kNone;
     bool in_list = false, wb_pending = false, via_prefetch = false, used = false, backed = false;
     void* pf_done = nullptr;
+    uint32_t hprev = kNone, hnext = kNone;  // three-tier: the pinned homes' recency list
+    bool in_hlist = false;
   };
   struct Writeback {
     uint32_t key;
@@ -169,7 +190,14 @@ class DgCore {
   bool fetch(uint32_t g, uint32_t unit, bool prefetch);
   void cover(uint32_t g, uint32_t unit);
   void use(uint32_t g, uint32_t unit, bool was_miss);
-  void to_block(uint32_t k);  // leaves the device (or a bank) without a write-back: its block is its home again
+  // Leaves the device (or a bank) without a write-back: its block is its home again (the recency head), else
+  // (three-tier, no block) its file.
+  void to_lower(uint32_t k);
+  void hpush(uint32_t k);    // a pinned home now (three-tier: at the recency head)
+  void hunlink(uint32_t k);  // no longer a pinned home
+  bool drop_host_lru();      // three-tier: the least recently homed pinned unit to its file, its block free
+  int32_t take_stage();      // three-tier: the next staging buffer, its last copy out of it landed
+  bool clean_now() const { return c_.clean_evict && c_.disk_tier && free_blocks_.empty(); }
   void attach(std::vector<void*>& where, int32_t i, void* ev);
   void detach(std::vector<void*>& where, int32_t i);
   void sweep_events();
@@ -186,6 +214,8 @@ class DgCore {
   std::vector<int32_t> table_;
   std::vector<int32_t> free_slots_, free_blocks_;
   uint32_t head_ = kNone, tail_ = kNone, on_device_ = 0, on_host_ = 0, backed_ = 0;
+  uint32_t hhead_ = kNone, htail_ = kNone, on_file_ = 0, stage_next_ = 0;
+  std::vector<void*> stage_ev_;  // [disk_staging]: the last copy out of each staging buffer
   std::vector<uint32_t> coming_, banked_, bank_key_;
   uint32_t bank_seq_[2] = {0, 0}, bank_layer_[2] = {kNone, kNone}, bank_next_[2] = {0, 0};
   std::deque<Writeback> wbs_;

@@ -1,0 +1,145 @@
+// Test hooks over the device-gated cache state machine alone (include/tierstream_amd/tsa_test.h, tsa_test_dgcore_*):
+// this library's DgCore on an eager transport, the schedule the reference's CPU tests run its core on
+// (reference tests/test_dg.cpp:201), so placement compares with the reference core's token by token without a GPU.
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "dg_core.hpp"
+#include "tierstream_amd/tsa_test.h"
+
+namespace tsa {
+namespace {
+
+// Every copy, entry write, event and file read completes when issued.
+class EagerTransport final : public DgTransport {
+ public:
+  explicit EagerTransport(std::vector<uint64_t> parts) : parts_(std::move(parts)) {}
+  ~EagerTransport() override = default;
+  void h2d(Stream, int32_t, int32_t) override {}
+  void d2h(int32_t, int32_t) override {}
+  void d2h_part(Stream, int32_t, int32_t, uint32_t) override {}
+  uint32_t parts() const override { return uint32_t(parts_.size()); }
+  uint64_t part_bytes(uint32_t p) const override { return parts_[p]; }
+  void write_entry(Stream, uint32_t, int32_t) override {}
+  void signal_ready(uint32_t, uint32_t) override {}
+  void* event_create() override { return new int(0); }
+  void event_destroy(void* ev) override { delete static_cast<int*>(ev); }
+  void record(void*, Stream) override {}
+  void wait(Stream, void*) override {}
+  bool done(void*) override { return true; }
+  bool query(void*) override { return true; }
+  void event_sync(void*) override {}
+  void sync(Stream) override {}
+  void upload_table(const int32_t*, uint32_t) override {}
+  void read_unit(uint32_t, int32_t) override {}
+
+ private:
+  std::vector<uint64_t> parts_;
+};
+
+struct TestCore {
+  std::unique_ptr<EagerTransport> t;
+  std::unique_ptr<DgCore> core;
+  uint32_t seq = 0;
+};
+
+constexpr const char* kNames =
+    "tokens lookups misses covered fetched prefetched prefetch_used resurrected bank_serves evicted evict_short "
+    "writebacks_done miss_layers covered_waits wb_deferred wb_cancelled wb_forced wb_boundary_flushed wb_issued_bytes "
+    "wb_cancelled_bytes inclusive_kept inclusive_drops free_slots free_blocks on_device backed_units disk_reads "
+    "disk_drops disk_discards clean_drops file_units";
+
+}  // namespace
+}  // namespace tsa
+
+extern "C" {
+
+ss_status tsa_test_dgcore_open(const tsa_test_dgcore_config* cfg, const uint32_t* order, uint32_t n_order,
+                               void** out) {
+  return tsa::guard([&] {
+    using namespace tsa;
+    require(cfg && out && cfg->n_units && cfg->part_bytes && (order || n_order == 0), SS_E_INVALID,
+            "tsa_test_dgcore_open: null argument");
+    auto r = std::make_unique<TestCore>();
+    r->t = std::make_unique<EagerTransport>(std::vector<uint64_t>(cfg->part_bytes, cfg->part_bytes + cfg->n_parts));
+    DgConfig c;
+    c.n_units.assign(cfg->n_units, cfg->n_units + cfg->n_gated);
+    c.persistent_slots = cfg->persistent_slots;
+    c.bank_slots = cfg->bank_slots;
+    c.blocks = cfg->blocks;
+    c.spare_target = cfg->spare_target;
+    c.prefetch_reserve_auto = cfg->prefetch_reserve == 0xFFFFFFFFu;
+    c.prefetch_reserve = c.prefetch_reserve_auto ? 0 : cfg->prefetch_reserve;
+    c.prefetch_per_layer = cfg->prefetch_per_layer;
+    c.prefetch_per_token = cfg->prefetch_per_token;
+    c.wb_defer = cfg->wb_defer != 0;
+    c.wb_on_d2h = cfg->wb_on_d2h != 0;
+    c.inclusive = cfg->inclusive;
+    c.disk_tier = cfg->disk_tier != 0;
+    c.disk_prefetch = cfg->disk_prefetch != 0;
+    c.home_blocks = cfg->home_blocks;
+    c.disk_staging = cfg->disk_staging;
+    c.clean_evict = cfg->clean_evict != 0;
+    r->core = std::make_unique<DgCore>(c, r->t.get());
+    std::vector<uint8_t> disk;
+    if (c.disk_tier) {
+      require(cfg->disk != nullptr, SS_E_INVALID, "tsa_test_dgcore_open: the disk tier needs its flags");
+      disk.assign(cfg->disk, cfg->disk + r->core->keys());
+    }
+    r->core->place(std::vector<uint32_t>(order, order + n_order), c.disk_tier ? &disk : nullptr);
+    r->core->check();
+    *out = r.release();
+  });
+}
+
+ss_status tsa_test_dgcore_token(void* h, const uint32_t* ids, uint32_t n, int32_t* table_out, uint64_t* counts,
+                                uint32_t n_counts) {
+  return tsa::guard([&] {
+    using namespace tsa;
+    require(h && ids && n >= 1 && n <= 64, SS_E_INVALID, "tsa_test_dgcore_token: bad argument");
+    auto* r = static_cast<TestCore*>(h);
+    DgCore& c = *r->core;
+    const uint32_t G = c.gated();
+    c.begin_token(++r->seq);
+    for (uint32_t g = 0; g < G; ++g) {
+      const uint32_t* x = ids + size_t(g) * n;
+      uint64_t mask = 0;
+      for (uint32_t i = 0; i < n; ++i)  // the export kernel: slot_of[unit_base[g] + id] < 0 at export time
+        if (x[i] < c.units(g) && c.table()[c.key(g, x[i])] < 0) mask |= uint64_t(1) << i;
+      c.serve_demand(g, x, n, mask);
+      c.serve_use(g, x, n, mask);
+      if (c.deferred() && g + 1 < G) c.issue_writebacks(g);
+    }
+    c.end_token();
+    c.check();
+    if (table_out) std::memcpy(table_out, c.table().data(), 4ull * c.keys());
+    if (counts) {
+      const DgCounts& s = c.counts();
+      const uint64_t v[] = {s.tokens, s.lookups, s.misses, s.covered, s.fetched, s.prefetched, s.prefetch_used,
+                            s.resurrected, s.bank_serves, s.evicted, s.evict_short, s.writebacks_done, s.miss_layers,
+                            s.covered_waits, s.wb_deferred, s.wb_cancelled, s.wb_forced, s.wb_boundary_flushed,
+                            s.wb_issued_bytes, s.wb_cancelled_bytes, s.inclusive_kept, s.inclusive_drops,
+                            uint64_t(c.free_slots()), uint64_t(c.free_blocks()), uint64_t(c.on_device()),
+                            uint64_t(c.backed_units()), s.disk_reads, s.disk_drops, s.disk_discards, s.clean_drops,
+                            uint64_t(c.file_units())};
+      const uint32_t m = uint32_t(sizeof v / sizeof v[0]);
+      std::memcpy(counts, v, 8ull * (n_counts < m ? n_counts : m));
+    }
+  });
+}
+
+const char* tsa_test_dgcore_counter_names(void) { return tsa::kNames; }
+
+uint32_t tsa_test_dgcore_host_order(void* h, uint32_t* out, uint32_t cap) {
+  if (!h) return 0;
+  const std::vector<uint32_t> v = static_cast<tsa::TestCore*>(h)->core->host_order();
+  for (uint32_t i = 0; out && i < cap && i < v.size(); ++i) out[i] = v[i];
+  return uint32_t(v.size());
+}
+
+void tsa_test_dgcore_close(void* h) { delete static_cast<tsa::TestCore*>(h); }
+
+}  // extern "C"

@@ -7,6 +7,7 @@
 #include <atomic>
 #include <chrono>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <thread>
 #include <unordered_map>
@@ -40,6 +41,10 @@ struct Layout {
   uint32_t keys = 0, R = 0, D = 0, B = 0, P = 0, Q = 0, I = 0;
   uint32_t persistent_slots = 0, slots = 0, guard_slot = 0, blocks = 0;
   std::vector<uint32_t> residents;
+  // three-tier: F file-tier units (plan tier DISK), their flags in key order, S staging buffers
+  bool disk_tier = false, disk_prefetch = false;
+  uint32_t F = 0, S = 0;
+  std::vector<uint8_t> disk;
 };
 
 Layout make_layout(const Desc& d, const Plan& p, const ss_options& o) {
@@ -58,10 +63,18 @@ Layout make_layout(const Desc& d, const Plan& p, const ss_options& o) {
   if (o.dg_wait_timeout_ms < 1) refuse(SS_E_INVALID, "dg_wait_timeout_ms must be >= 1");
   if (o.dg_wb_defer > 1) refuse(SS_E_INVALID, "dg_wb_defer must be 0 or 1");
   if (o.dg_wb_stream > 1) refuse(SS_E_INVALID, "dg_wb_stream must be 0 or 1");
-  if (o.dg_disk_tier || o.dg_disk_prefetch || o.dg_disk_staging || (o.dg_disk_queue && o.dg_disk_queue != 0xFFFFFFFFu) ||
-      o.dg_landing_blocks || o.dg_landing_max_queued || o.dg_landing_ttl || o.dg_landing_chunk || o.dg_bank_keep ||
+  // the three-tier file path (reference src/dg_layout.cpp:200-225): landings, the adaptive depth and kept bank reads
+  // are not part of this library's serve path
+  if (o.dg_disk_tier > 1 || o.dg_disk_prefetch > 1) refuse(SS_E_INVALID, "dg_disk_tier / dg_disk_prefetch must be 0 or 1");
+  const bool queue_auto = o.dg_disk_queue == 0xFFFFFFFFu;
+  if (!o.dg_disk_tier && (o.dg_disk_prefetch || o.dg_disk_staging || (o.dg_disk_queue && !queue_auto)))
+    refuse(SS_E_INVALID, "dg_disk_prefetch / dg_disk_staging / dg_disk_queue need dg_disk_tier = 1");
+  if (o.dg_disk_staging > 256) refuse(SS_E_INVALID, "dg_disk_staging must be 0..256");
+  if (o.dg_disk_queue > 64 && !queue_auto) refuse(SS_E_INVALID, "dg_disk_queue must be 0..64 or SS_DG_DISK_QUEUE_AUTO");
+  if (o.dg_landing_blocks || o.dg_landing_max_queued || o.dg_landing_ttl || o.dg_landing_chunk || o.dg_bank_keep ||
       o.dg_disk_queue_adapt)
-    refuse(SS_E_UNSUPPORTED, "the three-tier file path (dg_disk_tier and its options) is not supported by this library yet");
+    refuse(SS_E_UNSUPPORTED, "landings (dg_landing_*), dg_bank_keep and dg_disk_queue_adapt are not part of this "
+                             "library's serve path");
   if (o.dg_no_admit || o.dg_pf_revert_unused || o.dg_pf_strict_admit || o.dg_prior_len || o.dg_prior ||
       o.dg_score_profile_len || o.dg_score_profile)
     refuse(SS_E_UNSUPPORTED, "dg_no_admit / dg_pf_revert_unused / dg_pf_strict_admit / priors / score profiles are "
@@ -112,22 +125,30 @@ Layout make_layout(const Desc& d, const Plan& p, const ss_options& o) {
         ++planned;
       } else if (t == SS_TIER_PINNED) {
         ++x.P;
+      } else if (t == SS_TIER_DISK && o.dg_disk_tier) {
+        ++x.F;
       } else {
         refuse(SS_E_CAPACITY, "unit (" + std::to_string(l.index) + ", " + std::to_string(u) +
                                   ") is not resident or pinned (no gated unit is read from its file)");
       }
     }
     x.D += std::min<uint32_t>(b.dynamic_slots_per_layer, uint32_t(l.n_units) - planned);
+    if (o.dg_disk_tier)
+      for (int u = 0; u < l.n_units; ++u)
+        x.disk.push_back(p.tier[size_t(d.unit_base[size_t(L)] + u)] == SS_TIER_DISK ? 1 : 0);
     keys += uint64_t(l.n_units);
     require(keys < 0x7fffffffull, SS_E_INVALID, "device-gated: more than 2^31 - 1 gated units");
     x.unit_base.push_back(uint32_t(keys));
   }
   x.keys = uint32_t(keys);
   x.R = uint32_t(x.residents.size());
+  x.disk_tier = o.dg_disk_tier != 0;
+  x.disk_prefetch = o.dg_disk_prefetch != 0;
+  x.S = x.disk_tier ? (o.dg_disk_staging ? o.dg_disk_staging : 8u) : 0u;
   if (o.dg_spare_slots) {
-    if (o.dg_spare_slots > x.P)
+    if (o.dg_spare_slots > x.P + x.F)
       refuse(SS_E_INVALID, "dg_spare_slots " + std::to_string(o.dg_spare_slots) + " above the non-resident units (" +
-                               std::to_string(x.P) + ")");
+                               std::to_string(x.P + x.F) + ")");
     x.D = o.dg_spare_slots;
   }
   if (x.D < 1)
@@ -225,11 +246,24 @@ class HipTransport final : public DgTransport {
     dev_->free_pinned(vfail_host_);
     dev_->free_device(vfail_dev_);
     for (hipEvent_t e : prof_events_) dev_->event_destroy(e);
+    for (char* b : stage_) dev_->free_pinned(b);
   }
 
   hipStream_t stream(Stream s) const { return s_[s]; }
+  // blocks 0 .. blocks - 1: the pinned homes and spares (in chunks); blocks .. blocks + S - 1: the staging buffers
   char* block_ptr(int32_t b) const {
+    if (uint32_t(b) >= x_.blocks) return stage_[size_t(uint32_t(b) - x_.blocks)];
     return static_cast<char*>(chunks_[size_t(uint64_t(b) / per_chunk_)]) + (uint64_t(b) % per_chunk_) * x_.host_stride;
+  }
+  // Three-tier: the staging buffers (pinned, one host stride each) and the context's reader of a key's file bytes.
+  void enable_disk(std::function<void(uint32_t, char*)> reader) {
+    reader_ = std::move(reader);
+    for (uint32_t i = 0; i < x_.S; ++i)
+      stage_.push_back(static_cast<char*>(dev_->alloc_pinned(x_.host_stride, "disk staging buffer")));
+  }
+  void read_unit(uint32_t key, int32_t block) override {
+    require(reader_ && uint32_t(block) >= x_.blocks, SS_E_BACKEND, "device-gated: a file read outside the staging buffers");
+    reader_(key, block_ptr(block));
   }
   char* slot_ptr(uint32_t p, int32_t slot) const {
     return static_cast<char*>(arena_[p]) + uint64_t(slot) * x_.part_bytes[p];
@@ -621,6 +655,8 @@ class HipTransport final : public DgTransport {
     uint32_t parts;  // the parts copied at the boundary whose submission has not come yet
   };
   std::unordered_map<int32_t, Prestaged> prestaged_;  // by slot
+  std::vector<char*> stage_;                          // three-tier staging buffers
+  std::function<void(uint32_t, char*)> reader_;       // three-tier: a key's bytes from its file, host block layout
   hipStream_t vs_ = nullptr;        // the verify stream (a hardware queue of its own)
   std::vector<hipEvent_t> vev_;     // per landed batch and ready write of the token: the copies before it
   size_t vev_used_ = 0;
@@ -1115,6 +1151,10 @@ class HipDgCtx final : public DgCtx {
   void init();
   void fill();
   void release() noexcept;
+  // Every part of key k from its source file into dst, laid out as a host block (part p at part_offset[p]).
+  void read_key(uint32_t k, char* dst) const;
+  // The XXH64 of key k's bytes at dst against its descriptor hash (SS_E_HASH on a mismatch).
+  void check_key(uint32_t k, const char* dst) const;
 
   Desc d_;
   ss_options o_;
@@ -1229,7 +1269,17 @@ void HipDgCtx::init() {
   c.wb_layer_bytes = o_.dg_wb_layer_bytes;
   c.wb_max_outstanding = o_.dg_wb_max_outstanding;
   c.inclusive = x_.I;
+  c.disk_tier = x_.disk_tier;
+  c.disk_prefetch = x_.disk_prefetch;
+  c.home_blocks = x_.disk_tier ? x_.P : 0;
+  c.disk_staging = x_.S;
+  c.clean_evict = o_.dg_clean_evict != 0;
   core_ = std::make_unique<DgCore>(c, tr_.get());
+  if (x_.disk_tier)
+    tr_->enable_disk([this](uint32_t k, char* dst) {
+      read_key(k, dst);
+      if (o_.verify_hash == 1) check_key(k, dst);  // (verify_hash 2: the device checks the landed bytes)
+    });
   // priority: the seed (validated), the plan's residents, then key order
   std::vector<uint32_t> order;
   for (uint32_t i = 0; i < o_.dg_seed_n; ++i) {
@@ -1244,7 +1294,7 @@ void HipDgCtx::init() {
   o_.dg_seed_n = 0;
   order.insert(order.end(), x_.residents.begin(), x_.residents.end());
   for (uint32_t k = 0; k < x_.keys; ++k) order.push_back(k);
-  core_->place(order);
+  core_->place(order, x_.disk_tier ? &x_.disk : nullptr);
   fill();
   tr_->upload_table(core_->table().data(), x_.keys);
   core_->check();
@@ -1252,6 +1302,37 @@ void HipDgCtx::init() {
   base_l_.assign(G, DgLayerCounts{});
   svc_ = std::make_unique<Service>(core_.get(), m_, x_.B, o_.dg_wait_timeout_ms, o_.device);
   svc_->start();
+}
+
+void HipDgCtx::read_key(uint32_t k, char* dst) const {
+  const uint32_t g = core_->gated_of(k);
+  const int L = x_.gated[g];
+  const int u = int(k - x_.unit_base[g]);
+  const Layer& l = d_.layers[size_t(L)];
+  for (size_t p = 0; p < l.parts.size(); ++p) {
+    const Part& part = l.parts[p];
+    const SourceFile& f = *files_[size_t(part.source)];
+    const uint64_t F = part.offset + uint64_t(u) * part.stride;
+    require(F + part.bytes <= f.size(), SS_E_IO,
+            "unit (" + std::to_string(L) + ", " + std::to_string(u) + ") is past the end of its source");
+    const uint64_t al = std::max<uint64_t>(d_.sources[size_t(part.source)].align, 512);
+    if (!f.direct() || (F % al == 0 && part.bytes % al == 0 && x_.part_offset[p] % al == 0)) {
+      f.pread_all(dst + x_.part_offset[p], part.bytes, F);
+    } else {  // a buffered read of an unaligned range
+      SourceFile bf(f.path(), false);
+      bf.pread_all(dst + x_.part_offset[p], part.bytes, F);
+    }
+  }
+}
+
+void HipDgCtx::check_key(uint32_t k, const char* dst) const {
+  const uint32_t g = core_->gated_of(k);
+  const Layer& l = d_.layers[size_t(x_.gated[g])];
+  const uint32_t u = k - x_.unit_base[g];
+  if (l.hash.empty()) return;
+  require(xxh64(dst, size_t(x_.unit_bytes)) == l.hash[size_t(u)], SS_E_HASH,
+          "unit (" + std::to_string(l.index) + ", " + std::to_string(u) + ") bytes read from its file differ from the "
+          "descriptor hash");
 }
 
 // Open-time fill, in parallel: every key from its file into its home. Units homed on the device are read into a free
@@ -1274,9 +1355,14 @@ void HipDgCtx::fill() {
   }
   const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
   const unsigned max_threads = std::min<unsigned>(16, hw);
-  std::vector<uint32_t> dev_keys, host_keys;
-  for (uint32_t k = 0; k < x_.keys; ++k)
-    (core_->home(k) == DgCore::Home::Device ? dev_keys : host_keys).push_back(k);
+  std::vector<uint32_t> dev_keys, host_keys, file_keys;
+  for (uint32_t k = 0; k < x_.keys; ++k) {
+    const DgCore::Home h = core_->home(k);
+    (h == DgCore::Home::Device ? dev_keys : h == DgCore::Home::File ? file_keys : host_keys).push_back(k);
+  }
+  // three-tier: the file homes stay in their files; with a hash check each is read once here, through a staging
+  // buffer per worker, for its hash (and its checkpoints), never kept
+  if (!o_.verify_hash || !have_hash) file_keys.clear();
   const std::vector<int32_t> spare = core_->free_block_ids();
   require(dev_keys.empty() || !spare.empty(), SS_E_CAPACITY, "device-gated: no free block to stage the fill through");
   const std::vector<uint32_t>* keys = nullptr;
@@ -1301,22 +1387,10 @@ void HipDgCtx::fill() {
         const int L = x_.gated[g];
         const int u = int(k - x_.unit_base[g]);
         const Layer& l = d_.layers[size_t(L)];
-        const bool on_dev = core_->home(k) == DgCore::Home::Device;
-        char* dst = on_dev ? stage : tr_->block_ptr(core_->block_of(k));
-        for (size_t p = 0; p < l.parts.size(); ++p) {
-          const Part& part = l.parts[p];
-          const SourceFile& f = *files_[size_t(part.source)];
-          const uint64_t F = part.offset + uint64_t(u) * part.stride;
-          require(F + part.bytes <= f.size(), SS_E_IO,
-                  "unit (" + std::to_string(L) + ", " + std::to_string(u) + ") is past the end of its source");
-          const uint64_t al = std::max<uint64_t>(d_.sources[size_t(part.source)].align, 512);
-          if (!f.direct() || (F % al == 0 && part.bytes % al == 0 && x_.part_offset[p] % al == 0)) {
-            f.pread_all(dst + x_.part_offset[p], part.bytes, F);
-          } else {  // a buffered read of an unaligned range
-            SourceFile bf(f.path(), false);
-            bf.pread_all(dst + x_.part_offset[p], part.bytes, F);
-          }
-        }
+        const DgCore::Home home = core_->home(k);
+        const bool on_dev = home == DgCore::Home::Device;
+        char* dst = home == DgCore::Home::Host ? tr_->block_ptr(core_->block_of(k)) : stage;
+        read_key(k, dst);
         if (o_.verify_hash && !l.hash.empty()) {
           tsa_unit hu{};
           for (size_t p = 0; p < x_.part_bytes.size(); ++p) {
@@ -1359,14 +1433,17 @@ void HipDgCtx::fill() {
     }
     if (st) dev_->stream_destroy(st);
   };
-  // phase 1: the device homes, one spare block per worker; phase 2: the block homes
-  for (int phase = 0; phase < 2 && err_st == SS_OK; ++phase) {
-    keys = phase == 0 ? &dev_keys : &host_keys;
+  // phase 1: the device homes, one spare block per worker; phase 2: the block homes; phase 3: the file homes, one
+  // staging buffer per worker
+  for (int phase = 0; phase < 3 && err_st == SS_OK; ++phase) {
+    keys = phase == 0 ? &dev_keys : phase == 1 ? &host_keys : &file_keys;
     next = 0;
-    const size_t cap = phase == 0 ? spare.size() : size_t(max_threads);
+    const size_t cap = phase == 0 ? spare.size() : phase == 1 ? size_t(max_threads) : size_t(x_.S);
     const unsigned n = unsigned(std::min<size_t>({size_t(max_threads), cap, keys->size()}));
     std::vector<std::thread> th;
-    for (unsigned i = 0; i < n; ++i) th.emplace_back(work, phase == 0 ? tr_->block_ptr(spare[i]) : nullptr);
+    for (unsigned i = 0; i < n; ++i)
+      th.emplace_back(work, phase == 0 ? tr_->block_ptr(spare[i])
+                            : phase == 2 ? tr_->block_ptr(int32_t(x_.blocks + i)) : nullptr);
     for (auto& t : th) t.join();
   }
   if (err_st != SS_OK) fail(err_st, err);
