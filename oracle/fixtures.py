@@ -29,6 +29,7 @@ class Model:
     order: str = "ranked"
     seed: int = 99
     hashes: list = field(default_factory=list)
+    tiers: str = "pinned"  # the descriptor's tier list ("pinned|disk": the planner spills to the file tier)
 
     @property
     def unit_bytes(self):
@@ -57,12 +58,14 @@ class Model:
                 lay["top_k"] = self.top_k
             layers.append(lay)
         return json.dumps({"schema": "strix-stream/desc-v1", "model": "oracle-fixture", "engine": "oracle",
-                           "unit_align": 256, "order": self.order, "tiers": "pinned",
+                           "unit_align": 256, "order": self.order, "tiers": self.tiers,
                            "sources": [{"name": "w", "path": self.path, "align": 4096}], "layers": layers})
 
 
-def write_model(directory, layers, units, parts, kind="moe", top_k=2, order="ranked", seed=99) -> Model:
-    m = Model(os.path.join(str(directory), f"weights-{seed}.bin"), layers, units, list(parts), kind, top_k, order, seed)
+def write_model(directory, layers, units, parts, kind="moe", top_k=2, order="ranked", seed=99,
+                tiers="pinned") -> Model:
+    m = Model(os.path.join(str(directory), f"weights-{seed}.bin"), layers, units, list(parts), kind, top_k, order, seed,
+              tiers=tiers)
     assert all(pb % 8 == 0 for pb in parts)
     with open(m.path, "wb") as f:
         for L in range(layers):

@@ -162,3 +162,56 @@ def test_device_check_gates_a_corrupted_unit(tmp_path, gpu):
     finally:
         eng.close()
         ctx.close()
+
+
+@pytest.mark.parametrize("clean_evict", [0, 1])
+def test_three_tier_matches_reference(tmp_path, gpu, clean_evict):
+    """Three tiers (dg_disk_tier): 12 of 32 units resident, 10 pinned, 10 read from the file on a miss through staging
+    buffers. The plan's tiers are given explicitly (a planner spill to the file tier leaves no room for spare blocks,
+    as in the reference). Every token the slot table and the counters (file reads, drops of the pinned LRU to the
+    file, discards) must equal the reference core's, and every routed unit the engine read must checksum to the
+    file's bytes; every landed unit is re-hashed in HBM (verify_hash 2)."""
+    layers, units, parts, n_ids, staging = 4, 8, [64 * KiB] * 3, 2, 4
+    m = fixtures.write_model(tmp_path, layers, units, parts, top_k=n_ids, seed=31, tiers="pinned|disk")
+    keys = layers * units
+    tiers = [0] * 12 + [1] * 10 + [2] * 10
+    st = (m.unit_bytes + 255) // 256 * 256
+    hs = (m.unit_bytes + 4095) // 4096 * 4096
+    ring, dyn, spares = 2 * n_ids + 1, 1, 6
+    bkw = dict(device_bytes=12 * st + ring * st + dyn * layers * st + st // 2,
+               host_pinned_bytes=(10 + spares) * hs + hs // 2, dynamic_slots_per_layer=dyn, ring_slots=ring,
+               tier_mode=1, host_spare_units=spares)
+    d = ss.Desc(m.desc_json())
+    plan = ss.Plan(d, ss.budget(**bkw), tiers=tiers)
+    Q = plan.json()["spare_blocks"][0]["blocks"]
+    assert Q == spares
+    residents = list(range(12))
+    # spare slots: dyn per layer, capped by the layer's non-resident units (layer 0 is all resident here)
+    D = sum(min(dyn, sum(1 for u in range(units) if tiers[L * units + u] != 0)) for L in range(layers))
+    flags = [1 if t == 2 else 0 for t in tiers]
+    refdg = ref.RefDg([units] * layers, 12 + D, n_ids, 10 + Q, D, parts, residents + list(range(keys)),
+                      disk=dict(flags=flags, home_blocks=10, disk_staging=staging, clean_evict=clean_evict))
+    ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(forward_mode=1, dg_max_ids=n_ids, pin_planned=0, verify_hash=2,
+                                                      dg_disk_tier=1, dg_disk_staging=staging,
+                                                      dg_clean_evict=clean_evict, dg_wait_timeout_ms=5000))
+    eng = ss.DgEngine(ctx, n_ids, use_graph=True)
+    routes = _routes(layers, units, n_ids, 24, seed=9, zipf=True)
+    expect = {(L, u): fixtures.engine_checksum(m.unit_data(L, u)) for L in range(layers) for u in range(units)}
+    counters = COUNTERS + ["disk_reads", "disk_drops", "disk_discards", "clean_drops"]
+    try:
+        for t in range(routes.shape[0]):
+            cks, _ = eng.token(routes[t])
+            want_table, want = refdg.token(routes[t].astype(np.uint32))
+            got = ctx.dg_stats()
+            assert np.array_equal(ctx.dg_table(), want_table), (t, "table")
+            for k in counters:
+                assert got[k] == want[k], (t, k, got[k], want[k])
+            for L in range(layers):
+                for i, u in enumerate(routes[t, L]):
+                    assert int(cks[L, i]) == expect[(L, int(u))], (t, L, i)
+        assert got["disk_reads"] > 0 and (got["disk_drops"] + got["disk_discards"]) > 0, got
+        assert ctx.verify_failures() == 0
+    finally:
+        eng.close()
+        ctx.close()
+        refdg.close()

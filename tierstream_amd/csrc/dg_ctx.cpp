@@ -1035,7 +1035,15 @@ class HipDgCtx final : public DgCtx {
     TSA_D(wb_forced_wait_ns);
     TSA_D(inclusive_kept);
     TSA_D(inclusive_drops);
+    TSA_D(disk_reads);
+    TSA_D(disk_read_bytes);
+    TSA_D(disk_stage_waits);
+    TSA_D(disk_drops);
+    TSA_D(disk_discards);
+    TSA_D(clean_drops);
+    TSA_D(clean_drop_bytes);
 #undef TSA_D
+    s.disk_units = core_->file_units();
     s.free_slots = core_->free_slots();
     s.blocks = x_.blocks;
     s.slots = x_.slots;

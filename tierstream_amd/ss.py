@@ -267,11 +267,17 @@ class Desc:
 
 
 class Plan:
-    def __init__(self, desc: Desc, b: SsBudget, benefit=None):
+    def __init__(self, desc: Desc, b: SsBudget, benefit=None, tiers=None):
+        """ss_plan_make, or with `tiers` (one SS_TIER_* per unit in descriptor order) ss_plan_from_tiers."""
         L = _declare()
         self.h = vp()
-        ben = (C.c_double * len(benefit))(*benefit) if benefit is not None else None
-        check(L.ss_plan_make(desc.h, C.byref(b), ben, len(benefit) if benefit is not None else 0, C.byref(self.h)))
+        if tiers is not None:
+            t = (C.c_uint8 * len(tiers))(*tiers)
+            check(L.ss_plan_from_tiers(desc.h, C.byref(b), t, len(tiers), C.byref(self.h)))
+        else:
+            ben = (C.c_double * len(benefit))(*benefit) if benefit is not None else None
+            check(L.ss_plan_make(desc.h, C.byref(b), ben, len(benefit) if benefit is not None else 0,
+                                 C.byref(self.h)))
         self.desc = desc
 
     def tiers(self):
