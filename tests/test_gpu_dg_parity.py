@@ -5,6 +5,8 @@ token the slot table and the cache counters must be identical, and every routed 
 ss_dg_slot must checksum to the oracle's value of the file bytes. Device verify (verify_hash = 2) re-hashes every
 landed unit in HBM. Shapes: the mixtral workload at test size (reference tests/test_dg_cuda.cu:297-323 drives the
 same protocol)."""
+import os
+
 import numpy as np
 import pytest
 
@@ -164,16 +166,9 @@ def test_device_check_gates_a_corrupted_unit(tmp_path, gpu):
         ctx.close()
 
 
-@pytest.mark.parametrize("clean_evict", [0, 1])
-def test_three_tier_matches_reference(tmp_path, gpu, clean_evict):
-    """Three tiers (dg_disk_tier): 12 of 32 units resident, 10 pinned, 10 read from the file on a miss through staging
-    buffers. The plan's tiers are given explicitly (a planner spill to the file tier leaves no room for spare blocks,
-    as in the reference). Every token the slot table and the counters (file reads, drops of the pinned LRU to the
-    file, discards) must equal the reference core's, and every routed unit the engine read must checksum to the
-    file's bytes; every landed unit is re-hashed in HBM (verify_hash 2)."""
-    layers, units, parts, n_ids, staging = 4, 8, [64 * KiB] * 3, 2, 4
+def _three_tier(tmp_path):
+    layers, units, parts, n_ids = 4, 8, [64 * KiB] * 3, 2
     m = fixtures.write_model(tmp_path, layers, units, parts, top_k=n_ids, seed=31, tiers="pinned|disk")
-    keys = layers * units
     tiers = [0] * 12 + [1] * 10 + [2] * 10
     st = (m.unit_bytes + 255) // 256 * 256
     hs = (m.unit_bytes + 4095) // 4096 * 4096
@@ -181,6 +176,53 @@ def test_three_tier_matches_reference(tmp_path, gpu, clean_evict):
     bkw = dict(device_bytes=12 * st + ring * st + dyn * layers * st + st // 2,
                host_pinned_bytes=(10 + spares) * hs + hs // 2, dynamic_slots_per_layer=dyn, ring_slots=ring,
                tier_mode=1, host_spare_units=spares)
+    return m, tiers, bkw
+
+
+@pytest.mark.parametrize("queue", [0, 4])
+def test_three_tier_read_failure_fails_the_token(tmp_path, gpu, queue):
+    """A file read that fails (the source truncated after the open) fails its token with the read's error before the
+    layer is signalled ready, and poisons the context; with reads in flight the copy's await still ends (the reader
+    stores its word on the failure path), so every kernel of the token exits and the context closes."""
+    m, tiers, bkw = _three_tier(tmp_path)
+    d = ss.Desc(m.desc_json())
+    plan = ss.Plan(d, ss.budget(**bkw), tiers=tiers)
+    ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(forward_mode=1, dg_max_ids=2, pin_planned=0, verify_hash=2,
+                                                      dg_disk_tier=1, dg_disk_staging=4, dg_disk_queue=queue,
+                                                      dg_wait_timeout_ms=5000))
+    eng = ss.DgEngine(ctx, 2, use_graph=True)
+    routes = _routes(4, 8, 2, 24, seed=9, zipf=True)
+    os.truncate(m.path, 0)
+    try:
+        failed = None
+        for t in range(routes.shape[0]):
+            before = ctx.dg_stats()["disk_reads"]
+            try:
+                eng.token(routes[t])
+            except ss.SsError as e:
+                failed = (t, str(e))
+                break
+            assert ctx.dg_stats()["disk_reads"] == before, (t, "a file read succeeded from an empty file")
+        assert failed is not None, "no token read the file tier"
+        assert "short read" in failed[1], failed
+        with pytest.raises(ss.SsError):
+            eng.token(routes[0])  # poisoned
+    finally:
+        eng.close()
+        ctx.close()
+
+
+@pytest.mark.parametrize("clean_evict,queue", [(0, 0), (1, 0), (0, 4), (1, 4)])
+def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue):
+    """Three tiers (dg_disk_tier): 12 of 32 units resident, 10 pinned, 10 read from the file on a miss through staging
+    buffers. The plan's tiers are given explicitly (a planner spill to the file tier leaves no room for spare blocks,
+    as in the reference). Every token the slot table and the counters (file reads, drops of the pinned LRU to the
+    file, discards) must equal the reference core's, and every routed unit the engine read must checksum to the
+    file's bytes; every landed unit is re-hashed in HBM (verify_hash 2). dg_disk_queue 4: the reads run on reader
+    threads and each copy out of a staging buffer awaits its read on the device; the placement is the same."""
+    layers, units, parts, n_ids, staging, dyn, spares = 4, 8, [64 * KiB] * 3, 2, 4, 1, 6
+    m, tiers, bkw = _three_tier(tmp_path)
+    keys = layers * units
     d = ss.Desc(m.desc_json())
     plan = ss.Plan(d, ss.budget(**bkw), tiers=tiers)
     Q = plan.json()["spare_blocks"][0]["blocks"]
@@ -193,7 +235,8 @@ def test_three_tier_matches_reference(tmp_path, gpu, clean_evict):
                       disk=dict(flags=flags, home_blocks=10, disk_staging=staging, clean_evict=clean_evict))
     ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(forward_mode=1, dg_max_ids=n_ids, pin_planned=0, verify_hash=2,
                                                       dg_disk_tier=1, dg_disk_staging=staging,
-                                                      dg_clean_evict=clean_evict, dg_wait_timeout_ms=5000))
+                                                      dg_clean_evict=clean_evict, dg_disk_queue=queue,
+                                                      dg_wait_timeout_ms=5000))
     eng = ss.DgEngine(ctx, n_ids, use_graph=True)
     routes = _routes(layers, units, n_ids, 24, seed=9, zipf=True)
     expect = {(L, u): fixtures.engine_checksum(m.unit_data(L, u)) for L in range(layers) for u in range(units)}
@@ -210,6 +253,8 @@ def test_three_tier_matches_reference(tmp_path, gpu, clean_evict):
                 for i, u in enumerate(routes[t, L]):
                     assert int(cks[L, i]) == expect[(L, int(u))], (t, L, i)
         assert got["disk_reads"] > 0 and (got["disk_drops"] + got["disk_discards"]) > 0, got
+        assert got["disk_queue_resolved"] == max(queue, 1) and 1 <= got["disk_max_in_flight"] <= max(queue, 1), got
+        assert got["disk_read_ns"] > 0 and got["disk_wait_ns"] > 0, got
         assert ctx.verify_failures() == 0
     finally:
         eng.close()

@@ -6,7 +6,10 @@
 #include <algorithm>
 #include <atomic>
 #include <chrono>
+#include <condition_variable>
 #include <cstring>
+#include <deque>
+#include <exception>
 #include <functional>
 #include <mutex>
 #include <thread>
@@ -41,9 +44,9 @@ struct Layout {
   uint32_t keys = 0, R = 0, D = 0, B = 0, P = 0, Q = 0, I = 0;
   uint32_t persistent_slots = 0, slots = 0, guard_slot = 0, blocks = 0;
   std::vector<uint32_t> residents;
-  // three-tier: F file-tier units (plan tier DISK), their flags in key order, S staging buffers
+  // three-tier: F file-tier units (plan tier DISK), their flags in key order, S staging buffers, reads in flight
   bool disk_tier = false, disk_prefetch = false;
-  uint32_t F = 0, S = 0;
+  uint32_t F = 0, S = 0, disk_queue = 0;
   std::vector<uint8_t> disk;
 };
 
@@ -144,7 +147,14 @@ Layout make_layout(const Desc& d, const Plan& p, const ss_options& o) {
   x.R = uint32_t(x.residents.size());
   x.disk_tier = o.dg_disk_tier != 0;
   x.disk_prefetch = o.dg_disk_prefetch != 0;
-  x.S = x.disk_tier ? (o.dg_disk_staging ? o.dg_disk_staging : 8u) : 0u;
+  // reads in flight (reference include/strix_stream/ss.h:318-334): 0 and 1 = one read inside its fetch; 2..64 = that
+  // many reader threads; AUTO = 4 (one read location: this library reads each source from its own file only), raised
+  // staging when dg_disk_staging is left at 0, cut to an explicit dg_disk_staging
+  if (x.disk_tier) {
+    const uint32_t q = queue_auto ? 4u : std::max<uint32_t>(o.dg_disk_queue, 1u);
+    x.S = o.dg_disk_staging ? o.dg_disk_staging : std::max<uint32_t>(8u, q);
+    x.disk_queue = std::min(q, x.S);
+  }
   if (o.dg_spare_slots) {
     if (o.dg_spare_slots > x.P + x.F)
       refuse(SS_E_INVALID, "dg_spare_slots " + std::to_string(o.dg_spare_slots) + " above the non-resident units (" +
@@ -202,6 +212,103 @@ MappedLayout mapped_layout(uint32_t G) {
   return m;
 }
 
+// ---- three-tier reads in flight ------------------------------------------------------------------------------------
+// dg_disk_queue > 1: reader threads take (key, staging buffer, word, generation) jobs in submission order, read the
+// key's file bytes into the buffer, then store the generation into the buffer's word in fine-grained host memory. The
+// stream that copies out of the buffer polls that word first (an await kernel), so the service thread only decides and
+// enqueues; the reads of a layer's misses overlap one another and the copies of the units read before them. The word
+// is stored on every path (a failed read records its error first), so every await ends.
+class ReadPool {
+ public:
+  using Reader = std::function<void(uint32_t, char*)>;
+  ReadPool(uint32_t threads, Reader reader) : reader_(std::move(reader)) {
+    for (uint32_t i = 0; i < threads; ++i) th_.emplace_back([this] { run(); });
+  }
+  ~ReadPool() { stop(); }
+  // The queued reads finish first; no job is dropped.
+  void stop() {
+    {
+      std::lock_guard<std::mutex> l(m_);
+      stop_ = true;
+    }
+    cv_.notify_all();
+    for (auto& t : th_)
+      if (t.joinable()) t.join();
+  }
+  void submit(uint32_t key, char* dst, uint32_t* word, uint32_t gen) {
+    {
+      std::lock_guard<std::mutex> l(m_);
+      q_.push_back(Job{key, dst, word, gen});
+      ++inflight_;
+      max_inflight_ = std::max<uint64_t>(max_inflight_, inflight_);
+    }
+    cv_.notify_one();
+  }
+  // Waits for every submitted read (returns the wait in ns); rethrows the first read failure not yet reported.
+  uint64_t drain() {
+    std::unique_lock<std::mutex> l(m_);
+    uint64_t ns = 0;
+    if (inflight_) {
+      const auto t0 = Clock::now();
+      idle_.wait(l, [this] { return inflight_ == 0; });
+      ns = uint64_t(std::chrono::duration_cast<std::chrono::nanoseconds>(Clock::now() - t0).count());
+    }
+    if (err_) {
+      std::exception_ptr e = err_;
+      err_ = nullptr;
+      std::rethrow_exception(e);
+    }
+    return ns;
+  }
+  uint64_t read_ns() const { return read_ns_.load(std::memory_order_relaxed); }
+  uint64_t max_inflight() {
+    std::lock_guard<std::mutex> l(m_);
+    return max_inflight_;
+  }
+
+ private:
+  struct Job {
+    uint32_t key;
+    char* dst;
+    uint32_t* word;
+    uint32_t gen;
+  };
+  void run() {
+    for (;;) {
+      Job j;
+      {
+        std::unique_lock<std::mutex> l(m_);
+        cv_.wait(l, [this] { return stop_ || !q_.empty(); });
+        if (q_.empty()) return;  // stopping, nothing queued
+        j = q_.front();
+        q_.pop_front();
+      }
+      std::exception_ptr e;
+      const auto t0 = Clock::now();
+      try {
+        reader_(j.key, j.dst);
+      } catch (...) {
+        e = std::current_exception();
+      }
+      read_ns_.fetch_add(uint64_t(std::chrono::duration_cast<std::chrono::nanoseconds>(Clock::now() - t0).count()),
+                         std::memory_order_relaxed);
+      std::lock_guard<std::mutex> l(m_);
+      if (e && !err_) err_ = e;
+      __atomic_store_n(j.word, j.gen, __ATOMIC_RELEASE);  // the buffer's bytes (or the failure) before the word
+      if (--inflight_ == 0) idle_.notify_all();
+    }
+  }
+  Reader reader_;
+  std::mutex m_;
+  std::condition_variable cv_, idle_;
+  std::deque<Job> q_;
+  std::vector<std::thread> th_;
+  uint64_t inflight_ = 0, max_inflight_ = 0;
+  std::atomic<uint64_t> read_ns_{0};
+  std::exception_ptr err_;
+  bool stop_ = false;
+};
+
 // ---- the HIP transport ----------------------------------------------------------------------------------------------
 class HipTransport final : public DgTransport {
  public:
@@ -227,6 +334,7 @@ class HipTransport final : public DgTransport {
     }
   }
   ~HipTransport() override {
+    if (pool_) pool_->stop();  // every read's word stored: no await left waiting on the streams below
     if (vs_) (void)hipStreamSynchronize(vs_);
     for (auto& s : s_) {
       (void)hipStreamSynchronize(s);
@@ -247,6 +355,7 @@ class HipTransport final : public DgTransport {
     dev_->free_device(vfail_dev_);
     for (hipEvent_t e : prof_events_) dev_->event_destroy(e);
     for (char* b : stage_) dev_->free_pinned(b);
+    dev_->free_pinned(rword_host_);
   }
 
   hipStream_t stream(Stream s) const { return s_[s]; }
@@ -255,16 +364,50 @@ class HipTransport final : public DgTransport {
     if (uint32_t(b) >= x_.blocks) return stage_[size_t(uint32_t(b) - x_.blocks)];
     return static_cast<char*>(chunks_[size_t(uint64_t(b) / per_chunk_)]) + (uint64_t(b) % per_chunk_) * x_.host_stride;
   }
-  // Three-tier: the staging buffers (pinned, one host stride each) and the context's reader of a key's file bytes.
-  void enable_disk(std::function<void(uint32_t, char*)> reader) {
+  // Three-tier: the staging buffers (pinned, one host stride each) and the context's reader of a key's file bytes;
+  // with x_.disk_queue > 1 a read pool and one word per staging buffer in fine-grained host memory.
+  void enable_disk(std::function<void(uint32_t, char*)> reader, const DgDevWords& dw) {
     reader_ = std::move(reader);
     for (uint32_t i = 0; i < x_.S; ++i)
       stage_.push_back(static_cast<char*>(dev_->alloc_pinned(x_.host_stride, "disk staging buffer")));
+    if (x_.disk_queue > 1) {
+      rword_host_ = static_cast<uint32_t*>(dev_->alloc_mapped(4ull * x_.S, &rword_dev_, "read words"));
+      std::memset(rword_host_, 0, 4ull * x_.S);
+      rgen_.assign(x_.S, 0);
+      rpending_.assign(x_.S, 0);
+      raux_.assign(x_.S, 0);
+      dw_ = dw;
+      pool_ = std::make_unique<ReadPool>(x_.disk_queue, reader_);
+    }
   }
+  // A file read into staging buffer `block`: synchronous, or queued to the pool (its copies then await its word).
   void read_unit(uint32_t key, int32_t block) override {
     require(reader_ && uint32_t(block) >= x_.blocks, SS_E_BACKEND, "device-gated: a file read outside the staging buffers");
-    reader_(key, block_ptr(block));
+    if (!pool_) {
+      const auto t0 = Clock::now();
+      reader_(key, block_ptr(block));
+      const uint64_t ns = uint64_t(std::chrono::duration_cast<std::chrono::nanoseconds>(Clock::now() - t0).count());
+      read_ns_ += ns;
+      read_wait_ns_ += ns;
+      return;
+    }
+    const uint32_t i = uint32_t(block) - x_.blocks;
+    if (++rgen_[i] == 0) rgen_[i] = 1;  // (0 is the word's initial value)
+    rpending_[i] = rgen_[i];
+    raux_[i] = uint32_t(std::upper_bound(x_.unit_base.begin(), x_.unit_base.end(), key) - x_.unit_base.begin()) - 1;
+    pool_->submit(key, stage_[i], rword_host_ + i, rgen_[i]);
   }
+  // Every read submitted so far has returned; rethrows the first failed read (the token fails before the layer whose
+  // copies read it is signalled ready, so its bytes never reach an engine).
+  void drain_reads() {
+    if (pool_) read_wait_ns_ += pool_->drain();
+  }
+  void stop_reads() {
+    if (pool_) pool_->stop();
+  }
+  uint64_t read_ns() const { return pool_ ? pool_->read_ns() : read_ns_; }
+  uint64_t read_wait_ns() const { return read_wait_ns_; }
+  uint64_t max_reads_in_flight() const { return pool_ ? pool_->max_inflight() : (read_ns_ ? 1 : 0); }
   char* slot_ptr(uint32_t p, int32_t slot) const {
     return static_cast<char*>(arena_[p]) + uint64_t(slot) * x_.part_bytes[p];
   }
@@ -287,6 +430,14 @@ class HipTransport final : public DgTransport {
   }
   void h2d_unit(Stream s, int32_t slot, int32_t block) {
     const char* src = block_ptr(block);
+    if (pool_ && uint32_t(block) >= x_.blocks) {  // its read may still run: the stream waits for the read's word
+      const uint32_t i = uint32_t(block) - x_.blocks;
+      if (rpending_[i]) {
+        const uint32_t* w = static_cast<const uint32_t*>(rword_dev_) + i;
+        hip_check(hipError_t(dg_launch_await(dw_, w, rpending_[i], raux_[i], s_[s])), "await of a file read");
+        rpending_[i] = 0;
+      }
+    }
     const uint32_t P = uint32_t(x_.part_bytes.size());
     if (!scatter_) {  // one SDMA copy per part straight into its arena slot (timed after its wait: engine busy time)
       for (uint32_t p = 0; p < P; ++p) {
@@ -372,6 +523,7 @@ class HipTransport final : public DgTransport {
   // ready[g] = seq after the layer's demand copies (and cover waits) on kDem; with device verify on the verify stream,
   // behind the checks of every unit landed so far in the token (its stream order).
   void signal_ready(uint32_t g, uint32_t seq) override {
+    drain_reads();
     if (!verify_) {
       hip_check(hipStreamWriteValue32(s_[kDem], ready_ + g, seq, 0), "hipStreamWriteValue32 (ready)");
       return;
@@ -656,6 +808,12 @@ class HipTransport final : public DgTransport {
   };
   std::unordered_map<int32_t, Prestaged> prestaged_;  // by slot
   std::vector<char*> stage_;                          // three-tier staging buffers
+  std::unique_ptr<ReadPool> pool_;                    // reads in flight (dg_disk_queue > 1)
+  uint32_t* rword_host_ = nullptr;                    // per staging buffer: the generation of its last finished read
+  void* rword_dev_ = nullptr;
+  std::vector<uint32_t> rgen_, rpending_, raux_;      // per staging buffer: last generation, one to await, its layer
+  DgDevWords dw_;                                     // the await kernel's abort words and deadline
+  uint64_t read_ns_ = 0, read_wait_ns_ = 0;
   std::function<void(uint32_t, char*)> reader_;       // three-tier: a key's bytes from its file, host block layout
   hipStream_t vs_ = nullptr;        // the verify stream (a hardware queue of its own)
   std::vector<hipEvent_t> vev_;     // per landed batch and ready write of the token: the copies before it
@@ -926,6 +1084,12 @@ class HipDgCtx final : public DgCtx {
     // 4. the boundary, then the device check of this token's landed units (a check of a prefetch may end after the
     // end kernel: its failure is only in the check's result words)
     tr_->verify_sync();  // the boundary may hand a landed slot to a write-back or a new copy
+    try {
+      tr_->drain_reads();  // (a prefetch's read may still run: the boundary may reuse its staging buffer)
+    } catch (...) {
+      poisoned_ = true;
+      throw;
+    }
     core_->end_token();
     const std::vector<uint32_t> bad = tr_->collect_verify();
     tr_->profile_collect();
@@ -1044,6 +1208,11 @@ class HipDgCtx final : public DgCtx {
     TSA_D(clean_drop_bytes);
 #undef TSA_D
     s.disk_units = core_->file_units();
+    s.disk_queue_resolved = x_.disk_tier ? x_.disk_queue : 0;
+    s.disk_locations = x_.disk_tier ? 1 : 0;
+    s.disk_read_ns = tr_->read_ns();
+    s.disk_wait_ns = tr_->read_wait_ns();
+    s.disk_max_in_flight = tr_->max_reads_in_flight();
     s.free_slots = core_->free_slots();
     s.blocks = x_.blocks;
     s.slots = x_.slots;
@@ -1284,10 +1453,12 @@ void HipDgCtx::init() {
   c.clean_evict = o_.dg_clean_evict != 0;
   core_ = std::make_unique<DgCore>(c, tr_.get());
   if (x_.disk_tier)
-    tr_->enable_disk([this](uint32_t k, char* dst) {
-      read_key(k, dst);
-      if (o_.verify_hash == 1) check_key(k, dst);  // (verify_hash 2: the device checks the landed bytes)
-    });
+    tr_->enable_disk(
+        [this](uint32_t k, char* dst) {  // (reader threads too: the sources' positional reads are thread-safe)
+          read_key(k, dst);
+          if (o_.verify_hash == 1) check_key(k, dst);  // (verify_hash 2: the device checks the landed bytes)
+        },
+        dw_);
   // priority: the seed (validated), the plan's residents, then key order
   std::vector<uint32_t> order;
   for (uint32_t i = 0; i < o_.dg_seed_n; ++i) {
@@ -1465,6 +1636,7 @@ void HipDgCtx::fill() {
 
 void HipDgCtx::release() noexcept {
   if (svc_) svc_->stop_join();
+  if (tr_) tr_->stop_reads();  // the readers use this context's sources and layout
   if (dev_) (void)hipDeviceSynchronize();
   svc_.reset();
   core_.reset();

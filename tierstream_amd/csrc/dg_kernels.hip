@@ -1,8 +1,9 @@
-// Device-gated control kernels for CDNA4 (gfx950): begin, export, predict, wait, end. Each is one wavefront or one
-// lane; none touches weight bytes. The protocol (sequence authorization, sticky abort, first error wins, the export
-// record then its flag, the ready wait with a deadline, the completion word) is the reference's (src/dg_kernels.cu:
-// 31-135); the implementation is wave64-native: the export's miss mask is one ballot, the wait is one wavefront that
-// polls a system-scope acquire load and sleeps between polls, and time is the constant-rate wall clock.
+// Device-gated control kernels for CDNA4 (gfx950): begin, export, predict, wait, end, and the await of a file read.
+// Each is one wavefront or one lane; none touches weight bytes. The protocol (sequence authorization, sticky abort,
+// first error wins, the export record then its flag, the ready wait with a deadline, the completion word) is the
+// reference's (src/dg_kernels.cu:31-135); the implementation is wave64-native: the export's miss mask is one ballot,
+// the wait is one wavefront that polls a system-scope acquire load and sleeps between polls, and time is the
+// constant-rate wall clock.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -130,6 +131,29 @@ __global__ __launch_bounds__(64) void end_kernel(DgDevWords d) {
   st_sys(d.done, __hip_atomic_load(d.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
+// A staging buffer's file read, awaited on the stream that copies out of it: lane 0 polls the reader's word (a
+// system-scope acquire: the reader stores the read's generation after the read returned) with the wait kernel's
+// exits: the token's device abort (it fails already), the host's abort, and the deadline.
+__global__ __launch_bounds__(64) void await_kernel(DgDevWords d, const uint32_t* word, uint32_t gen, uint32_t aux) {
+  if (threadIdx.x != 0) return;
+  const uint64_t t0 = wall_clock64();
+  for (uint32_t polls = 0;; ++polls) {
+    if (ld_acq_sys(word) == gen) return;
+    if (__hip_atomic_load(d.abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
+    if ((polls & 15u) == 15u) {
+      if (ld_acq_sys(d.host_abort)) {
+        set_error(d, kDgHostAbort, aux);
+        return;
+      }
+      if (wall_clock64() - t0 > d.timeout_ticks) {
+        set_error(d, kDgTimeout, aux);
+        return;
+      }
+    }
+    __builtin_amdgcn_s_sleep(8);
+  }
+}
+
 __global__ __launch_bounds__(64) void store_kernel(uint32_t* word, uint32_t v) {
   if (threadIdx.x != 0) return;
   __threadfence_system();
@@ -156,6 +180,10 @@ int dg_launch_wait(const DgDevWords& d, uint32_t g, void* s) {
 }
 int dg_launch_end(const DgDevWords& d, void* s) {
   hipLaunchKernelGGL(dgk::end_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(s), d);
+  return int(hipGetLastError());
+}
+int dg_launch_await(const DgDevWords& d, const uint32_t* word, uint32_t gen, uint32_t aux, void* s) {
+  hipLaunchKernelGGL(dgk::await_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(s), d, word, gen, aux);
   return int(hipGetLastError());
 }
 int dg_launch_store(uint32_t* word, uint32_t v, void* s) {

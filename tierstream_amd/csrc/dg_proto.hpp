@@ -86,5 +86,9 @@ int dg_launch_wait(const DgDevWords& d, uint32_t g, void* stream);
 int dg_launch_end(const DgDevWords& d, void* stream);
 // A one-lane store of v into a device word on the stream (the ready / entry publication when value-writes are off).
 int dg_launch_store(uint32_t* word, uint32_t v, void* stream);
+// Three-tier reads in flight: one lane polls a reader's word in fine-grained host memory until it holds gen, so the
+// copies enqueued behind it on the stream start once the staging buffer's file read returned. The token's abort words
+// and the wait deadline end it too (a deadline sets kDgTimeout with err_aux = aux, the gated layer of the read).
+int dg_launch_await(const DgDevWords& d, const uint32_t* word, uint32_t gen, uint32_t aux, void* stream);
 
 }  // namespace tsa
