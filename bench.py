@@ -60,7 +60,7 @@ def log(*a):
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--steps", type=int, default=None, help="timed tokens (default: the workload's: mixtral 256)")
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="mixtral")
     ap.add_argument("--part-bytes", type=int, default=0, help="scale every part to this size (0 = full size)")
@@ -68,6 +68,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="target CPU time of the baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--workdir", default="", help="where the source file is written (default /dev/shm)")
+    ap.add_argument("--layers", type=int, default=0, help="run the workload with this many layers (0 = all)")
+    ap.add_argument("--disk-dir", default="",
+                    help="three tiers: where the file tier's source file is written (default: the temp directory, "
+                         "a drive that takes direct I/O; the other layers' file stays in --workdir)")
     ap.add_argument("--inclusive", type=int, default=0,
                     help="dg_inclusive_blocks (clean copies; 0 = spare slots + banks); spare blocks = this + 4")
     ap.add_argument("--kernels-only", action="store_true",
@@ -145,6 +149,55 @@ def measure_peaks(tsa, L, C):
         L.tsa_free(dev)
         L.tsa_free(dev2)
         L.tsa_host_free(host)
+    return out
+
+
+def measure_disk(path, w, n_layers, threads=4, seconds=4.0):
+    """Direct-I/O read rate of the file tier's drive: `threads` readers, each reading whole units (every part of a
+    unit, one positional read at the unit's 4 KiB-aligned offset) of the file-tier source into its own page-aligned
+    buffer, units in a seeded random order, for about `seconds`; and one reader alone (the read depth of
+    dg_disk_queue 1). Bytes over wall time."""
+    import mmap
+    import threading
+    n_units = n_layers * w.units
+    ub = w.unit_bytes
+    out = {}
+    try:
+        fd = os.open(path, os.O_RDONLY | getattr(os, "O_DIRECT", 0))
+    except OSError as e:
+        return {"error": f"direct open: {e}"}
+    try:
+        for nth in sorted({1, threads}):
+            order = np.random.default_rng(7 + nth).permutation(n_units)
+            nxt = [0]
+            lock = threading.Lock()
+            done = [0]
+            t_end = time.perf_counter() + seconds / 2
+
+            def reader():
+                buf = mmap.mmap(-1, ub)
+                try:
+                    while time.perf_counter() < t_end:
+                        with lock:
+                            i = nxt[0]
+                            nxt[0] += 1
+                        if i >= n_units:
+                            return
+                        got = os.preadv(fd, [buf], int(order[i]) * w.unit_stride_file)
+                        with lock:
+                            done[0] += got
+                finally:
+                    buf.close()
+
+            t0 = time.perf_counter()
+            th = [threading.Thread(target=reader) for _ in range(nth)]
+            for t in th:
+                t.start()
+            for t in th:
+                t.join()
+            out[f"readers_{nth}_GBps"] = round(done[0] / (time.perf_counter() - t0) / 1e9, 2)
+    finally:
+        os.close(fd)
     return out
 
 
@@ -232,8 +285,9 @@ def measure_kernels(tsa, L, C, w, seg=8192, reps=10):
 
 
 # ---- the CPU baseline -----------------------------------------------------------------------------------------------
-def cpu_baseline(w, shape, path, hashes, routes, start, est_token_s, seconds):
-    """The reference DgCore on a memcpy transport (oracle/_ref), over tokens start.. of the same route stream."""
+def cpu_baseline(w, shape, files, hashes, routes, start, est_token_s, seconds):
+    """The reference DgCore on a memcpy transport (oracle/_ref), over tokens start.. of the same route stream. files:
+    [(path, first layer, layers)] as the descriptor's sources."""
     try:
         from oracle import ref
     except Exception as e:  # noqa: BLE001
@@ -246,12 +300,24 @@ def cpu_baseline(w, shape, path, hashes, routes, start, est_token_s, seconds):
     keys = w.n_units
     residents = list(range(shape.R))
     order = residents + list(range(keys))
-    offsets = [W.unit_offset(w, 0, 0) + g * w.unit_stride_file for g in range(keys)]
+    path_of, offsets = [], []
+    for i, (_, first, n) in enumerate(files):
+        for L in range(first, first + n):
+            for u in range(w.units):
+                path_of.append(i)
+                offsets.append(W.unit_offset(w, L, u, first))
     ids = routes[start:start + n_tok].astype(np.uint32)
     hs = (w.unit_bytes + 4095) // 4096 * 4096
     t0 = time.time()
-    ms, c = ref.cpu_baseline([w.units] * w.layers, shape.R + shape.D, shape.B, shape.P + shape.Q, shape.D, w.parts,
-                             hs, order, path, offsets, hashes, ids, wb_defer=1, inclusive=shape.I, setup_threads=16)
+    if shape.F:
+        flags = [1 if t == 2 else 0 for t in shape.tiers]
+        ms, c = ref.cpu_baseline_disk([w.units] * w.layers, shape.R + shape.D, shape.B, shape.P + shape.Q, shape.D,
+                                      w.parts, hs, order, [f[0] for f in files], path_of, offsets, hashes, ids, flags,
+                                      shape.P, 8, clean_evict=w.clean_evict, setup_threads=16)
+    else:
+        ms, c = ref.cpu_baseline([w.units] * w.layers, shape.R + shape.D, shape.B, shape.P + shape.Q, shape.D, w.parts,
+                                 hs, order, files[0][0], offsets, hashes, ids, wb_defer=1, inclusive=shape.I,
+                                 setup_threads=16)
     log(f"cpu baseline: {n_tok} tokens in {time.time() - t0:.1f} s (setup included), counters {c}")
     return (ms, c, n_tok), None
 
@@ -276,6 +342,10 @@ def main():
         raise SystemExit(f"bench.py: workload {a.workload} is not device-gated")
     if a.part_bytes:
         w = W.scaled(w, part_bytes=a.part_bytes)
+    if a.layers:
+        w = W.scaled(w, layers=a.layers)
+    if a.steps is None:
+        a.steps = w.steps
     if a.inclusive:
         w = W.scaled(w, inclusive_blocks=a.inclusive, spare_units=a.inclusive + 4)
     shape = W.dg_shape(w)
@@ -288,20 +358,37 @@ def main():
     base = a.workdir or ("/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir())
     work = tempfile.mkdtemp(prefix="tsa_bench_", dir=base)
     path = os.path.join(work, "weights.bin")
+    three = shape.F > 0
+    cold = shape.cold_first_layer(w)
+    cold_work = tempfile.mkdtemp(prefix="tsa_bench_", dir=a.disk_dir or tempfile.gettempdir()) if three else None
+    cold_path = os.path.join(cold_work, "weights-file-tier.bin") if three else None
     result = {}
     try:
         t0 = time.time()
-        log(f"workload {w.name}: {w.layers} x {w.units} units of {w.unit_bytes / 2**20:.0f} MiB, writing "
-            f"{W.source_bytes(w) / 1e9:.1f} GB to {path}")
-        hashes = W.write_sources_gpu(w, path)
+        log(f"workload {w.name}: {w.layers} x {w.units} units of {w.unit_bytes / 2**20:.1f} MiB, writing "
+            f"{W.source_bytes(w, cold) / 1e9:.1f} GB to {path}")
+        hashes = W.write_sources_gpu(w, path, n_layers=cold) if cold else []
+        files = [(path, 0, cold)] if cold else []
+        if three:
+            log(f"three tiers: layers {cold}..{w.layers - 1} ({W.source_bytes(w, w.layers - cold) / 1e9:.1f} GB) to "
+                f"{cold_path}")
+            hashes += W.write_sources_gpu(w, cold_path, first_layer=cold, drop_cache=True)
+            files.append((cold_path, cold, w.layers - cold))
         log(f"sources written in {time.time() - t0:.1f} s")
-        d = ss.Desc(W.desc_json(w, path, hashes))
+        d = ss.Desc(W.desc_json(w, files, hashes))
         b = ss.budget(**shape.budget)
-        plan = ss.Plan(d, b)
+        plan = ss.Plan(d, b, tiers=shape.tiers) if three else ss.Plan(d, b)
         tiers = plan.tiers()
         n_res = sum(1 for r in tiers for t in r if t == 0)
-        log(f"plan: {n_res} resident units (target {shape.R}), D {shape.D}, Q {shape.Q}, inclusive {shape.I}, "
-            f"device budget {shape.budget['device_bytes'] / 1e9:.1f} GB, pinned {shape.budget['host_pinned_bytes'] / 1e9:.1f} GB")
+        n_pin = sum(1 for r in tiers for t in r if t == 1)
+        n_file = sum(1 for r in tiers for t in r if t == 2)
+        log(f"plan: {n_res} resident units (target {shape.R}), {n_pin} pinned, {n_file} file, D {shape.D}, Q {shape.Q}, "
+            f"inclusive {shape.I}, device budget {shape.budget['device_bytes'] / 1e9:.1f} GB, pinned "
+            f"{shape.budget['host_pinned_bytes'] / 1e9:.1f} GB")
+        disk_peak = measure_disk(cold_path, w, w.layers - cold, threads=max(shape.options.get("dg_disk_queue") or 1, 1)) \
+            if three else None
+        if disk_peak:
+            log(f"file tier drive: {disk_peak}")
         t0 = time.time()
         ctx = ss.Ctx(d, b, plan, ss.options(**shape.options, verify_hash=2, dg_wait_timeout_ms=20000))
         log(f"context open (fill + hash check) in {time.time() - t0:.1f} s")
@@ -361,9 +448,15 @@ def main():
                     miss_wait.append((st[g, 2] - st[g, 1]) * TICK_NS / 1e6)
         pprof = ctx.profile_read(wait=True)  # the probe tokens' copy and write-back brackets
         log(f"probe tokens: {pprof}")
-        dstat = {k: s1[k] - s0[k] for k in ("tokens", "lookups", "misses", "fetched", "evicted", "bank_serves",
-                                             "writebacks_done", "inclusive_kept", "inclusive_drops", "miss_layers",
-                                             "wb_forced", "collected_mid", "stalled")}
+        dkeys = ["tokens", "lookups", "misses", "fetched", "evicted", "bank_serves", "writebacks_done",
+                 "inclusive_kept", "inclusive_drops", "miss_layers", "wb_forced", "collected_mid", "stalled"]
+        if three:
+            dkeys += ["disk_reads", "disk_read_bytes", "disk_read_ns", "disk_wait_ns", "disk_stage_waits",
+                      "disk_drops", "disk_discards", "clean_drops"]
+        dstat = {k: s1[k] - s0[k] for k in dkeys}
+        if three:
+            dstat["disk_max_in_flight"] = s1["disk_max_in_flight"]
+            dstat["disk_queue_resolved"] = s1["disk_queue_resolved"]
         failures = ctx.verify_failures()
         eng.close()
         ctx.close()
@@ -389,12 +482,18 @@ def main():
             "scaling": "weak",
             "vs_baseline": None,
             "dtype": "u8",
-            "data": "synthetic (bf16 N(0, 0.02) expert bytes from the counter-based generator; Zipf(1.1) routes)",
+            "data": (f"synthetic ({'Q4 blocks (fp16 scale + 16 bytes of 4-bit values per 18 bytes)' if w.gen == 2 else 'bf16 N(0, 0.02)'}"
+                     f" expert bytes from the counter-based generator; Zipf({w.zipf_s}) routes)"),
             "config": {"workload": f"{w.name}: {w.layers} layers x {w.units} experts, top-{w.top_k}, units "
-                                   f"{w.unit_bytes} B (3 parts), {n_res} resident / {w.n_units - n_res} pinned, "
-                                   f"device-gated hipGraph token, verify_hash 2",
+                                   f"{w.unit_bytes} B (3 parts), {n_res} resident / {n_pin} pinned"
+                                   + (f" / {n_file} read from the file tier (direct I/O, "
+                                      f"{dstat.get('disk_queue_resolved', 1)} reads in flight)" if three else "")
+                                   + ", device-gated hipGraph token, verify_hash 2"
+                                   + (f"; {w.layers} of the full model's {W.WORKLOADS[w.name].layers} layers"
+                                      if w.layers != W.WORKLOADS[w.name].layers else ""),
                        "layers": w.layers, "experts": w.units, "top_k": w.top_k, "unit_bytes": w.unit_bytes,
-                       "resident_units": n_res, "spare_slots": shape.D, "inclusive_blocks": shape.I,
+                       "resident_units": n_res, "pinned_units": n_pin, "file_units": n_file,
+                       "spare_slots": shape.D, "spare_blocks": shape.Q, "inclusive_blocks": shape.I,
                        "device_budget_bytes": shape.budget["device_bytes"],
                        "pinned_budget_bytes": shape.budget["host_pinned_bytes"]},
             "p50_ms": round(pct(lat, 50), 3),
@@ -442,9 +541,22 @@ def main():
                        "units_seen": len(ck_seen)},
             "cpu_baseline": None,
         }
+        if three:
+            rb = dstat["disk_read_bytes"]
+            result["file_tier"] = {
+                "reads_per_token": round(dstat["disk_reads"] / steps, 3),
+                "read_GBps_wall": round(rb / wall / 1e9, 2),
+                "read_ms_mean": round(dstat["disk_read_ns"] / max(dstat["disk_reads"], 1) / 1e6, 3),
+                "read_GBps_per_reader": round(rb / dstat["disk_read_ns"], 2) if dstat["disk_read_ns"] else None,
+                "service_wait_ms_per_token": round(dstat["disk_wait_ns"] / steps / 1e6, 3),
+                "reads_in_flight_max": dstat["disk_max_in_flight"],
+                "drive_direct_read_GBps": disk_peak,
+                "note": "read_GBps_wall: file-tier bytes read over the timed region's wall clock; the reads run on "
+                        "reader threads while earlier copies and layers proceed (the service waits only before a "
+                        "layer's ready word)"}
         if not a.no_cpu:
             est = float(np.median(lat)) / 1e3 * 20  # a first guess of the CPU's time per token
-            got, why = cpu_baseline(w, shape, path, hashes, routes, warm, est, a.cpu_seconds)
+            got, why = cpu_baseline(w, shape, files, hashes, routes, warm, est, a.cpu_seconds)
             if got:
                 ms, c, n_tok = got
                 result["cpu_baseline"] = {
@@ -452,13 +564,18 @@ def main():
                     "p99_ms": round(pct(ms, 99), 3), "mean_ms": round(float(np.mean(ms)), 3),
                     "copy_GBps": round(c["copied_bytes"] / (float(np.sum(ms)) / 1e3) / 1e9, 2),
                     "sample": f"tokens {warm}..{warm + n_tok - 1} of the same route stream from the open-time "
-                              f"placement: reference DgCore + memcpy transport + host XXH64 of each landed unit, "
-                              f"1 thread; misses {c['misses']}, hash mismatches {c['hash_mismatches']}",
+                              f"placement: reference DgCore + memcpy transport + host XXH64 of each landed unit"
+                              + (", file-tier units read synchronously with direct I/O into staging buffers"
+                                 if three else "")
+                              + f", 1 thread; misses {c['misses']}, hash mismatches {c['hash_mismatches']}"
+                              + (f", file reads {c['disk_reads']}" if three else ""),
                     "cpu": cpu_model(), "nproc": os.cpu_count()}
             else:
                 log(f"cpu baseline skipped: {why}")
     finally:
         shutil.rmtree(work, ignore_errors=True)
+        if cold_work:
+            shutil.rmtree(cold_work, ignore_errors=True)
     print(json.dumps(result), flush=True)
 
 

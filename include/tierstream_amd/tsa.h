@@ -104,8 +104,9 @@ SS_API uint64_t tsa_scatter_blocks(const uint64_t* part_bytes, uint32_t n_parts)
 SS_API ss_status tsa_scatter(const tsa_scatter_job* jobs_dev, uint32_t n_jobs, uint64_t n_blocks, void* stream);
 
 /* Synthetic bytes, counter-based: kind 0 = uniform bytes (word i of the stream = a splitmix64 of (seed, stream_id,
- * i)), kind 1 = bfloat16 N(0, sigma) by Box-Muller over the same words. offset: the stream's first byte written
- * (a multiple of 8); bytes: a multiple of 8. */
+ * i)), kind 1 = bfloat16 N(0, sigma) by Box-Muller over the same words, kind 2 = Q4 blocks of 18 bytes (an fp16
+ * scale, then 16 bytes of packed 4-bit values; sigma unused). offset: the stream's first byte written (a multiple of
+ * 8); bytes: a multiple of 8. */
 SS_API ss_status tsa_synth(void* dst_dev, uint64_t bytes, uint64_t seed, uint64_t stream_id, uint64_t offset,
                            uint32_t kind, float sigma, void* stream);
 

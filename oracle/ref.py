@@ -68,6 +68,11 @@ def lib() -> C.CDLL:
                                               u64, C.POINTER(u32), u32, C.c_char_p, C.POINTER(u64), C.POINTER(u64),
                                               C.POINTER(u32), u32, u32, C.c_int, C.POINTER(C.c_double),
                                               C.POINTER(u64)]),
+            "refdg_cpu_baseline_disk": (C.c_int, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, C.POINTER(u64),
+                                                   u32, u64, C.POINTER(u32), u32, C.POINTER(C.c_char_p), u32,
+                                                   C.POINTER(u32), C.POINTER(u64), C.POINTER(u64), C.POINTER(u32), u32,
+                                                   u32, C.c_int, C.POINTER(C.c_uint8), u32, u32, u32,
+                                                   C.POINTER(C.c_double), C.POINTER(u64)]),
         }
         for name, (res, args) in sigs.items():
             f = getattr(L, name)
@@ -282,4 +287,36 @@ def cpu_baseline(n_units, persistent, bank, blocks, spare_target, part_bytes, ho
     if st != 0:
         raise RuntimeError("refdg_cpu_baseline failed")
     names = ["misses", "fetched", "evicted", "writebacks_done", "hash_mismatches", "copied_bytes"]
+    return ms, {k: int(v) for k, v in zip(names, out)}
+
+
+def cpu_baseline_disk(n_units, persistent, bank, blocks, spare_target, part_bytes, host_stride, order, paths, path_of,
+                      unit_offsets, hashes, ids: np.ndarray, disk_flags, home_blocks, disk_staging, clean_evict=0,
+                      wb_defer=1, setup_threads=16):
+    """Three tiers (refdg_cpu_baseline_disk): key k's bytes in paths[path_of[k]] at unit_offsets[k]; the file-tier keys
+    (disk_flags) are read synchronously into a staging buffer on a miss (direct I/O where the file system allows it).
+    Returns (token_ms [tokens], counters dict)."""
+    L = lib()
+    x = np.ascontiguousarray(ids, dtype=np.uint32)
+    tokens, G, n = x.shape
+    nu = (u32 * G)(*n_units)
+    pb = (u64 * len(part_bytes))(*part_bytes)
+    od = (u32 * len(order))(*order)
+    pa = (C.c_char_p * len(paths))(*[str(p).encode() for p in paths])
+    po = np.ascontiguousarray(path_of, dtype=np.uint32)
+    offs = np.ascontiguousarray(unit_offsets, dtype=np.uint64)
+    hs = np.ascontiguousarray(hashes, dtype=np.uint64)
+    fl = np.ascontiguousarray(disk_flags, dtype=np.uint8)
+    ms = np.zeros(tokens, dtype=np.float64)
+    out = np.zeros(8, dtype=np.uint64)
+    st = L.refdg_cpu_baseline_disk(nu, G, persistent, bank, blocks, spare_target, wb_defer, 0, pb, len(part_bytes),
+                                   host_stride, od, len(order), pa, len(paths), po.ctypes.data_as(C.POINTER(u32)),
+                                   offs.ctypes.data_as(C.POINTER(u64)), hs.ctypes.data_as(C.POINTER(u64)),
+                                   x.ctypes.data_as(C.POINTER(u32)), n, tokens, setup_threads,
+                                   fl.ctypes.data_as(C.POINTER(C.c_uint8)), home_blocks, disk_staging, clean_evict,
+                                   ms.ctypes.data_as(C.POINTER(C.c_double)), out.ctypes.data_as(C.POINTER(u64)))
+    if st != 0:
+        raise RuntimeError("refdg_cpu_baseline_disk failed")
+    names = ["misses", "fetched", "evicted", "writebacks_done", "hash_mismatches", "copied_bytes", "disk_reads",
+             "disk_drops"]
     return ms, {k: int(v) for k, v in zip(names, out)}

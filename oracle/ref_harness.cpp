@@ -287,6 +287,7 @@ void* map_anon(uint64_t bytes) {
 
 class Memcpy final : public ts::DgTransport {
  public:
+  // blocks: the pinned homes and spares, then (three tiers) the staging buffers; block -1 is a one-unit buffer
   Memcpy(std::vector<uint64_t> parts, uint64_t host_stride, uint32_t slots, uint32_t blocks)
       : parts_(std::move(parts)), stride_(host_stride), slots_(slots), blk_(size_t(blocks) + 1, nullptr) {
     uint64_t off = 0;
@@ -332,6 +333,10 @@ class Memcpy final : public ts::DgTransport {
   void sync(Stream) override {}
   void upload_table(const int32_t*, uint32_t) override {}
   void upload_table_ranges(const int32_t*, const uint32_t*, uint32_t) override {}
+  // three tiers: a file-tier unit's bytes from its file into a staging buffer (as the reference reads them: one
+  // positional read of the unit, direct I/O where the file system allows it)
+  std::function<void(uint32_t, char*)> reader;
+  void read_unit(uint32_t key, int32_t b) override { reader(key, block(b)); }
 
  private:
   std::vector<uint64_t> parts_, off_;
@@ -361,17 +366,71 @@ extern "C" {
 // landed unit against hashes[key], serve_use, issue_writebacks, and end_token, on the calling thread. The source file
 // holds unit `key` at unit_offset[key] (unit bytes contiguous). token_ms[t] = the token's wall time; out[] = misses,
 // fetched, evicted, writebacks_done, hash mismatches, bytes copied into slots (sums over the timed tokens).
+// Three-tier variant: n_paths source files, key k in paths[path_of[k]] at unit_offset[k]; disk[k] = 1 for the
+// file-tier keys, home_blocks = the pinned homes, disk_staging buffers; reads are synchronous (one at a time inside
+// their fetch: dg_disk_queue 1). out[6] = file reads, out[7] = drops of pinned units to their file.
+int refdg_cpu_baseline_disk(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
+                            uint32_t spare_target, uint32_t wb_defer, uint32_t inclusive, const uint64_t* part_bytes,
+                            uint32_t n_parts, uint64_t host_stride, const uint32_t* order, uint32_t n_order,
+                            const char* const* paths, uint32_t n_paths, const uint32_t* path_of,
+                            const uint64_t* unit_offset, const uint64_t* hashes, const uint32_t* ids, uint32_t n,
+                            uint32_t n_tokens, int setup_threads, const uint8_t* disk, uint32_t home_blocks,
+                            uint32_t disk_staging, uint32_t clean_evict, double* token_ms, uint64_t* out);
+
 int refdg_cpu_baseline(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
                        uint32_t spare_target, uint32_t wb_defer, uint32_t inclusive, const uint64_t* part_bytes,
                        uint32_t n_parts, uint64_t host_stride, const uint32_t* order, uint32_t n_order,
                        const char* path, const uint64_t* unit_offset, const uint64_t* hashes, const uint32_t* ids,
                        uint32_t n, uint32_t n_tokens, int setup_threads, double* token_ms, uint64_t* out) {
+  uint32_t keys = 0;
+  for (uint32_t g = 0; g < G; ++g) keys += n_units[g];
+  const std::vector<uint32_t> path_of(keys, 0);
+  return refdg_cpu_baseline_disk(n_units, G, persistent, bank, blocks, spare_target, wb_defer, inclusive, part_bytes,
+                                 n_parts, host_stride, order, n_order, &path, 1, path_of.data(), unit_offset, hashes,
+                                 ids, n, n_tokens, setup_threads, nullptr, 0, 0, 0, token_ms, out);
+}
+
+int refdg_cpu_baseline_disk(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
+                            uint32_t spare_target, uint32_t wb_defer, uint32_t inclusive, const uint64_t* part_bytes,
+                            uint32_t n_parts, uint64_t host_stride, const uint32_t* order, uint32_t n_order,
+                            const char* const* paths, uint32_t n_paths, const uint32_t* path_of,
+                            const uint64_t* unit_offset, const uint64_t* hashes, const uint32_t* ids, uint32_t n,
+                            uint32_t n_tokens, int setup_threads, const uint8_t* disk, uint32_t home_blocks,
+                            uint32_t disk_staging, uint32_t clean_evict, double* token_ms, uint64_t* out) {
+  std::vector<int> fds, dfds;
+  auto close_all = [&] {
+    for (int f : fds) ::close(f);
+    for (int f : dfds)
+      if (f >= 0) ::close(f);
+  };
   try {
     const std::vector<uint64_t> parts(part_bytes, part_bytes + n_parts);
     uint64_t unit = 0;
     for (uint64_t pb : parts) unit += pb;
     const uint32_t slots = persistent + 2 * bank + 1;
-    Memcpy t(parts, host_stride, slots, blocks);
+    Memcpy t(parts, host_stride, slots, blocks + (disk ? disk_staging : 0));
+    for (uint32_t i = 0; i < n_paths; ++i) {
+      const int fd = ::open(paths[i], O_RDONLY | O_CLOEXEC);
+      if (fd < 0) throw std::runtime_error(std::string("open ") + paths[i]);
+      fds.push_back(fd);
+      dfds.push_back(::open(paths[i], O_RDONLY | O_CLOEXEC | O_DIRECT));  // -1: buffered reads
+    }
+    auto pread_all = [](int fd, char* dst, uint64_t bytes, uint64_t off) {
+      uint64_t got = 0;
+      while (got < bytes) {
+        const ssize_t r = ::pread(fd, dst + got, size_t(bytes - got), off_t(off + got));
+        if (r <= 0) return false;
+        got += uint64_t(r);
+      }
+      return true;
+    };
+    const bool aligned = unit % 4096 == 0;
+    t.reader = [&](uint32_t k, char* dst) {
+      const int dfd = dfds[path_of[k]];
+      const bool direct = dfd >= 0 && aligned && unit_offset[k] % 4096 == 0;
+      if (!pread_all(direct ? dfd : fds[path_of[k]], dst, unit, unit_offset[k]))
+        throw std::runtime_error("short read of a file-tier unit");
+    };
     ts::DgConfig c;
     c.n_units.assign(n_units, n_units + G);
     c.persistent_slots = persistent;
@@ -385,11 +444,20 @@ int refdg_cpu_baseline(const uint32_t* n_units, uint32_t G, uint32_t persistent,
     c.inclusive = inclusive;
     c.max_ids = bank;
     c.pf_legacy = true;
+    uint32_t n_keys = 0;
+    for (uint32_t g = 0; g < G; ++g) n_keys += n_units[g];
+    std::vector<uint8_t> dflags;
+    if (disk) {
+      c.disk_tier = true;
+      c.home_blocks = home_blocks;
+      c.disk_staging = disk_staging;
+      c.disk_queue = 1;
+      c.clean_evict = clean_evict != 0;
+      dflags.assign(disk, disk + n_keys);
+    }
     ts::DgCore core(c, &t);
-    core.place(std::vector<uint32_t>(order, order + n_order));
+    core.place(std::vector<uint32_t>(order, order + n_order), disk ? &dflags : nullptr);
     // fill: every key's bytes into its home (a slot or a block), from the file; spare blocks and free slots touched
-    const int fd = ::open(path, O_RDONLY | O_CLOEXEC);
-    if (fd < 0) throw std::runtime_error(std::string("open ") + path);
     const uint32_t keys = core.keys();
     std::atomic<int> io_err{0};
     parallel_for(keys, setup_threads, [&](uint32_t k) {
@@ -402,31 +470,26 @@ int refdg_cpu_baseline(const uint32_t* n_units, uint32_t G, uint32_t persistent,
         dst = buf.data();
       }
       if (!dst) return;
-      uint64_t got = 0;
-      while (got < unit) {
-        const ssize_t r = ::pread(fd, dst + got, size_t(unit - got), off_t(unit_offset[k] + got));
-        if (r <= 0) {
-          io_err = 1;
-          return;
-        }
-        got += uint64_t(r);
+      if (!pread_all(fds[path_of[k]], dst, unit, unit_offset[k])) {
+        io_err = 1;
+        return;
       }
       if (s >= 0)
         for (uint32_t p = 0; p < n_parts; ++p) std::memcpy(t.slot(p, s), dst + t.part_offset(p), parts[p]);
     });
-    ::close(fd);
-    if (io_err) throw std::runtime_error(std::string("short read of ") + path);
+    if (io_err) throw std::runtime_error("short read of a source file at the fill");
     std::vector<uint8_t> used_slot(slots, 0);
     for (uint32_t k = 0; k < keys; ++k)
       if (core.table()[k] >= 0) used_slot[size_t(core.table()[k])] = 1;
-    std::vector<int32_t> used_block(size_t(blocks) + 1, 0);
+    const uint32_t all_blocks = blocks + (disk ? disk_staging : 0);
+    std::vector<int32_t> used_block(size_t(all_blocks) + 1, 0);
     for (uint32_t k = 0; k < keys; ++k)
       if (core.block_of(k) >= 0) used_block[size_t(core.block_of(k)) + 1] = 1;
     parallel_for(slots, setup_threads, [&](uint32_t s) {
       if (!used_slot[s])
         for (uint32_t p = 0; p < n_parts; ++p) std::memset(t.slot(p, int32_t(s)), 0, parts[p]);
     });
-    parallel_for(blocks + 1, setup_threads, [&](uint32_t b) {
+    parallel_for(all_blocks + 1, setup_threads, [&](uint32_t b) {
       if (!used_block[b]) std::memset(t.block(int32_t(b) - 1), 0, host_stride);
     });
     // the timed tokens
@@ -463,8 +526,14 @@ int refdg_cpu_baseline(const uint32_t* n_units, uint32_t G, uint32_t persistent,
     out[3] = s1.writebacks_done - s0.writebacks_done;
     out[4] = bad;
     out[5] = copied;
+    if (disk) {
+      out[6] = s1.disk_reads - s0.disk_reads;
+      out[7] = s1.disk_drops - s0.disk_drops;
+    }
+    close_all();
     return 0;
   } catch (const std::exception& e) {
+    close_all();
     std::fprintf(stderr, "refdg_cpu_baseline: %s\n", e.what());
     return 1;
   }

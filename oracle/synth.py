@@ -4,7 +4,8 @@ Word i of stream `sid` under `seed` is mix64(key + (i + 1) * 0x9E3779B97F4A7C15)
 0xD1B54A32D192ED03) and mix64 the splitmix64 finalizer; kind 0 stores each word little-endian (uniform bytes). The
 product's device generator (tsa_synth) must give the same bytes for kind 0 (integer arithmetic, bit-exact). Kind 1
 (bf16 N(0, sigma), Box-Muller in float32) is restated for distribution checks only: the device's logf / sincosf may
-differ from numpy's in the last ulp, so its bytes are not compared bit for bit.
+differ from numpy's in the last ulp, so its bytes are not compared bit for bit. Kind 2 (Q4 blocks: an fp16 scale and
+16 bytes of 4-bit values per 18 bytes) is integer arithmetic and compared bit for bit.
 
 Byte-level fixture helpers (the closed form the reference's own tests use, tests/fixture.hpp:16-22) live here too.
 """
@@ -61,6 +62,20 @@ def bf16_normal(seed: int, sid: int, offset: int, nbytes: int, sigma: float) -> 
     x = z.view(np.uint32)
     rne = ((x + np.uint32(0x7FFF) + ((x >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
     return rne.view(np.uint8)
+
+
+def q4_blocks(seed: int, sid: int, offset: int, nbytes: int) -> np.ndarray:
+    """kind 2: Q4 blocks of 18 bytes from the stream's byte 0: block b = the fp16 scale 0x2000 | (word 3b & 0x3FF)
+    little-endian, then the 16 bytes of words 3b + 1 and 3b + 2 little-endian. Integer arithmetic: bit-exact."""
+    j = np.arange(offset, offset + nbytes, dtype=np.uint64)
+    b = j // np.uint64(18)
+    o = (j - b * np.uint64(18)).astype(np.int64)
+    b0 = int(b[0]) if nbytes else 0
+    nb = (int(b[-1]) - b0 + 1) if nbytes else 0
+    w = words(seed, sid, 3 * b0, 3 * nb).reshape(nb, 3) if nb else np.zeros((0, 3), np.uint64)
+    scale = (np.uint64(0x2000) | (w[:, 0] & np.uint64(0x3FF))).astype("<u2").view(np.uint8).reshape(nb, 2)
+    block = np.concatenate([scale, w[:, 1:].astype("<u8").view(np.uint8).reshape(nb, 16)], axis=1)  # [nb][18]
+    return block[(b - np.uint64(b0)).astype(np.int64), o]
 
 
 def fixture_byte_at(L: int, u: int, part: int, i: np.ndarray) -> np.ndarray:

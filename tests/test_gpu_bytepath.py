@@ -212,6 +212,15 @@ def test_synth_uniform_matches_oracle(gpu):
     assert np.array_equal(buf.download(), synth.uniform_bytes(1234, 77, 4096, n))
 
 
+def test_synth_q4_blocks_match_oracle(gpu):
+    """Q4 blocks are integer arithmetic: bit-exact, including a start inside a block (offset 4096 = block 227 + 10)."""
+    n = (1 << 20) + 8
+    buf = gpu.DeviceBuffer(n)
+    gpu.check(gpu.lib().tsa_synth(C.c_void_p(buf.ptr), n, 99, 5, 4096, 2, C.c_float(0.0), None))
+    gpu.check(gpu.lib().tsa_stream_sync(None))
+    assert np.array_equal(buf.download(), synth.q4_blocks(99, 5, 4096, n))
+
+
 def test_synth_bf16_normal(gpu):
     n = 1 << 22
     buf = gpu.DeviceBuffer(n)

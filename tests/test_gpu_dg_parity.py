@@ -166,8 +166,8 @@ def test_device_check_gates_a_corrupted_unit(tmp_path, gpu):
         ctx.close()
 
 
-def _three_tier(tmp_path):
-    layers, units, parts, n_ids = 4, 8, [64 * KiB] * 3, 2
+def _three_tier(tmp_path, parts=(64 * KiB,) * 3):
+    layers, units, parts, n_ids = 4, 8, list(parts), 2
     m = fixtures.write_model(tmp_path, layers, units, parts, top_k=n_ids, seed=31, tiers="pinned|disk")
     tiers = [0] * 12 + [1] * 10 + [2] * 10
     st = (m.unit_bytes + 255) // 256 * 256
@@ -212,16 +212,22 @@ def test_three_tier_read_failure_fails_the_token(tmp_path, gpu, queue):
         ctx.close()
 
 
-@pytest.mark.parametrize("clean_evict,queue", [(0, 0), (1, 0), (0, 4), (1, 4)])
-def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue):
+# parts above the 8 MiB read piece: one unit's read is several pieces on several readers
+BIG_PARTS = (8 * 1024 * KiB + 64 * KiB, 64 * KiB, 4 * 1024 * KiB)
+
+
+@pytest.mark.parametrize("clean_evict,queue,parts", [(0, 0, None), (1, 0, None), (0, 4, None), (1, 4, None),
+                                                     (0, 3, BIG_PARTS)])
+def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts):
     """Three tiers (dg_disk_tier): 12 of 32 units resident, 10 pinned, 10 read from the file on a miss through staging
     buffers. The plan's tiers are given explicitly (a planner spill to the file tier leaves no room for spare blocks,
     as in the reference). Every token the slot table and the counters (file reads, drops of the pinned LRU to the
     file, discards) must equal the reference core's, and every routed unit the engine read must checksum to the
     file's bytes; every landed unit is re-hashed in HBM (verify_hash 2). dg_disk_queue 4: the reads run on reader
     threads and each copy out of a staging buffer awaits its read on the device; the placement is the same."""
-    layers, units, parts, n_ids, staging, dyn, spares = 4, 8, [64 * KiB] * 3, 2, 4, 1, 6
-    m, tiers, bkw = _three_tier(tmp_path)
+    parts = list(parts or (64 * KiB,) * 3)
+    layers, units, n_ids, staging, dyn, spares = 4, 8, 2, 4, 1, 6
+    m, tiers, bkw = _three_tier(tmp_path, parts)
     keys = layers * units
     d = ss.Desc(m.desc_json())
     plan = ss.Plan(d, ss.budget(**bkw), tiers=tiers)

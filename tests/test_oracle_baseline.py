@@ -42,3 +42,45 @@ def test_cpu_baseline_moves_the_right_bytes(tmp_path, wb_defer, inclusive):
         assert got[k] == want[k], k
     if inclusive == 0:
         assert got["writebacks_done"] > 0                # exclusive: evictions write units back, and they re-land intact
+
+
+@pytest.mark.parametrize("clean_evict", [0, 1])
+def test_cpu_baseline_three_tier(tmp_path, clean_evict):
+    """Three tiers: the file-tier units are read from the source file into staging buffers on a miss (two source
+    files: the first two layers in one, the rest in the other) and every landed unit hashes right; the counters equal
+    the immediate-transport core's."""
+    layers, units, parts, n_ids = 4, 8, [16 * KiB, 16 * KiB, 32 * KiB], 2
+    m = fixtures.write_model(tmp_path, layers, units, parts, top_k=n_ids, seed=7)
+    keys = layers * units
+    residents = list(range(10))
+    tiers = [0] * 10 + [1] * 12 + [2] * 10
+    flags = [1 if t == 2 else 0 for t in tiers]
+    D, P, Q = 3, 12, 4
+    order = residents + list(range(keys))
+    # the same bytes split over two files (layers 0-1, layers 2-3)
+    with open(m.path, "rb") as f:
+        raw = f.read()
+    half = 2 * units * m.stride
+    paths = [tmp_path / "a.bin", tmp_path / "b.bin"]
+    paths[0].write_bytes(raw[:half])
+    paths[1].write_bytes(raw[half:])
+    path_of = [0 if g < 2 * units else 1 for g in range(keys)]
+    offsets = [(g if g < 2 * units else g - 2 * units) * m.stride for g in range(keys)]
+    rng = np.random.default_rng(5)
+    tokens = 24
+    ids = np.stack([np.stack([rng.choice(units, size=n_ids, replace=False) for _ in range(layers)])
+                    for _ in range(tokens)]).astype(np.uint32)
+    ms, got = ref.cpu_baseline_disk([units] * layers, len(residents) + D, n_ids, P + Q, D, parts, m.stride, order,
+                                    paths, path_of, offsets, m.hashes, ids, flags, P, 3, clean_evict=clean_evict,
+                                    setup_threads=2)
+    assert ms.shape == (tokens,) and got["hash_mismatches"] == 0
+    assert got["disk_reads"] > 0 and got["copied_bytes"] == got["misses"] * m.unit_bytes
+    eager = ref.RefDg([units] * layers, len(residents) + D, n_ids, P + Q, D, parts, order,
+                      disk=dict(flags=flags, home_blocks=P, disk_staging=3, clean_evict=clean_evict))
+    try:
+        for t in range(tokens):
+            _, want = eager.token(ids[t])
+    finally:
+        eager.close()
+    for k in ("misses", "fetched", "evicted", "writebacks_done", "disk_reads", "disk_drops"):
+        assert got[k] == want[k], k

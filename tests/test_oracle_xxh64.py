@@ -68,3 +68,18 @@ def test_bf16_normal_distribution():
     b = synth.bf16_normal(5, 1, 0, 1 << 20, 0.02).view(np.uint16).astype(np.uint32) << 16
     x = b.view(np.float32)
     assert abs(float(x.mean())) < 1e-3 and abs(float(x.std()) - 0.02) < 1e-3
+
+
+def test_q4_blocks_layout():
+    """Q4 block b of a stream, by the scalar formula: the fp16 scale 0x2000 | (word 3b & 0x3FF) little-endian (a
+    positive fp16 with exponent field 8: [2^-7, 2^-6)), then words 3b + 1 and 3b + 2 little-endian; an offset inside
+    a block continues the same stream."""
+    k = synth.key(7, 3)
+    word = [synth.mix64_scalar(k + (i + 1) * synth.GOLDEN) for i in range(9)]
+    got = synth.q4_blocks(7, 3, 0, 54).reshape(3, 18)
+    for b in range(3):
+        scale = int(got[b, 0]) | int(got[b, 1]) << 8
+        assert scale == 0x2000 | (word[3 * b] & 0x3FF)
+        assert 2.0 ** -7 <= float(np.array([scale], dtype="<u2").view(np.float16)[0]) < 2.0 ** -6
+        assert bytes(got[b, 2:]) == word[3 * b + 1].to_bytes(8, "little") + word[3 * b + 2].to_bytes(8, "little")
+    assert np.array_equal(synth.q4_blocks(7, 3, 13, 40), synth.q4_blocks(7, 3, 0, 54)[13:53])

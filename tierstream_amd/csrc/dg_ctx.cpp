@@ -32,6 +32,7 @@ using Clock = std::chrono::steady_clock;
 // segment (0.4 % of the unit) in HBM
 constexpr uint64_t kSegBytes = 8 * 1024;
 constexpr uint64_t kScatterBelow = 8ull << 20;     // parts smaller than this land staged + scattered
+constexpr uint64_t kReadPiece = 8ull << 20;        // three-tier reads in flight: the largest piece one reader reads
 
 uint64_t align64(uint64_t v) { return (v + 63) / 64 * 64; }
 
@@ -213,19 +214,27 @@ MappedLayout mapped_layout(uint32_t G) {
 }
 
 // ---- three-tier reads in flight ------------------------------------------------------------------------------------
-// dg_disk_queue > 1: reader threads take (key, staging buffer, word, generation) jobs in submission order, read the
-// key's file bytes into the buffer, then store the generation into the buffer's word in fine-grained host memory. The
-// stream that copies out of the buffer polls that word first (an await kernel), so the service thread only decides and
-// enqueues; the reads of a layer's misses overlap one another and the copies of the units read before them. The word
-// is stored on every path (a failed read records its error first), so every await ends.
+// dg_disk_queue > 1: reader threads read file-tier units into staging buffers in pieces of at most 8 MiB (a part, or a
+// 4 KiB-aligned slice of one), so one unit's read runs on every reader at once. The piece that completes a unit runs
+// the unit's finisher (the host hash check with verify_hash 1), then stores the read's generation into the staging
+// buffer's word in fine-grained host memory, which the stream that copies out of the buffer polls first (an await
+// kernel): the service thread only decides and enqueues, and the reads of a layer's misses overlap one another and
+// the copies of the units read before them. The word is stored on every path (a failed piece records its error
+// first), so every await ends.
 class ReadPool {
  public:
-  using Reader = std::function<void(uint32_t, char*)>;
-  ReadPool(uint32_t threads, Reader reader) : reader_(std::move(reader)) {
+  struct Piece {
+    uint32_t part;
+    uint64_t off, bytes, dst_off;  // offset inside the part, bytes, offset inside the host block
+  };
+  using PieceReader = std::function<void(uint32_t key, uint32_t part, uint64_t off, uint64_t bytes, char* dst)>;
+  using Finisher = std::function<void(uint32_t key, const char* block)>;
+  ReadPool(uint32_t threads, std::vector<Piece> pieces, PieceReader read, Finisher finish)
+      : pieces_(std::move(pieces)), read_(std::move(read)), finish_(std::move(finish)) {
     for (uint32_t i = 0; i < threads; ++i) th_.emplace_back([this] { run(); });
   }
   ~ReadPool() { stop(); }
-  // The queued reads finish first; no job is dropped.
+  // The queued reads finish first; no piece is dropped.
   void stop() {
     {
       std::lock_guard<std::mutex> l(m_);
@@ -235,14 +244,15 @@ class ReadPool {
     for (auto& t : th_)
       if (t.joinable()) t.join();
   }
-  void submit(uint32_t key, char* dst, uint32_t* word, uint32_t gen) {
+  void submit(uint32_t key, char* block, uint32_t* word, uint32_t gen) {
     {
       std::lock_guard<std::mutex> l(m_);
-      q_.push_back(Job{key, dst, word, gen});
+      units_.push_back(Unit{key, block, word, gen, uint32_t(pieces_.size())});
+      Unit* u = &units_.back();
+      for (const Piece& pc : pieces_) q_.push_back(Job{u, &pc});
       ++inflight_;
-      max_inflight_ = std::max<uint64_t>(max_inflight_, inflight_);
     }
-    cv_.notify_one();
+    cv_.notify_all();
   }
   // Waits for every submitted read (returns the wait in ns); rethrows the first read failure not yet reported.
   uint64_t drain() {
@@ -253,6 +263,7 @@ class ReadPool {
       idle_.wait(l, [this] { return inflight_ == 0; });
       ns = uint64_t(std::chrono::duration_cast<std::chrono::nanoseconds>(Clock::now() - t0).count());
     }
+    units_.clear();  // (every unit finished: no job points into the list)
     if (err_) {
       std::exception_ptr e = err_;
       err_ = nullptr;
@@ -261,17 +272,21 @@ class ReadPool {
     return ns;
   }
   uint64_t read_ns() const { return read_ns_.load(std::memory_order_relaxed); }
-  uint64_t max_inflight() {
+  uint64_t max_running() {
     std::lock_guard<std::mutex> l(m_);
-    return max_inflight_;
+    return max_running_;
   }
 
  private:
-  struct Job {
+  struct Unit {
     uint32_t key;
-    char* dst;
+    char* block;
     uint32_t* word;
-    uint32_t gen;
+    uint32_t gen, left;  // pieces not yet read
+  };
+  struct Job {
+    Unit* unit;
+    const Piece* piece;
   };
   void run() {
     for (;;) {
@@ -282,28 +297,46 @@ class ReadPool {
         if (q_.empty()) return;  // stopping, nothing queued
         j = q_.front();
         q_.pop_front();
+        max_running_ = std::max<uint64_t>(max_running_, ++running_);
       }
+      Unit& u = *j.unit;
       std::exception_ptr e;
       const auto t0 = Clock::now();
       try {
-        reader_(j.key, j.dst);
+        read_(u.key, j.piece->part, j.piece->off, j.piece->bytes, u.block + j.piece->dst_off);
       } catch (...) {
         e = std::current_exception();
       }
       read_ns_.fetch_add(uint64_t(std::chrono::duration_cast<std::chrono::nanoseconds>(Clock::now() - t0).count()),
                          std::memory_order_relaxed);
+      bool last;
+      {
+        std::lock_guard<std::mutex> l(m_);
+        --running_;
+        if (e && !err_) err_ = e;
+        last = --u.left == 0;
+      }
+      if (!last) continue;
+      try {  // every piece of the unit landed (or failed): the finisher, then the word
+        finish_(u.key, u.block);
+      } catch (...) {
+        std::lock_guard<std::mutex> l(m_);
+        if (!err_) err_ = std::current_exception();
+      }
       std::lock_guard<std::mutex> l(m_);
-      if (e && !err_) err_ = e;
-      __atomic_store_n(j.word, j.gen, __ATOMIC_RELEASE);  // the buffer's bytes (or the failure) before the word
+      __atomic_store_n(u.word, u.gen, __ATOMIC_RELEASE);  // the buffer's bytes (or the failure) before the word
       if (--inflight_ == 0) idle_.notify_all();
     }
   }
-  Reader reader_;
+  std::vector<Piece> pieces_;
+  PieceReader read_;
+  Finisher finish_;
   std::mutex m_;
   std::condition_variable cv_, idle_;
   std::deque<Job> q_;
+  std::deque<Unit> units_;  // (stable addresses: jobs point at their unit)
   std::vector<std::thread> th_;
-  uint64_t inflight_ = 0, max_inflight_ = 0;
+  uint64_t inflight_ = 0, running_ = 0, max_running_ = 0;
   std::atomic<uint64_t> read_ns_{0};
   std::exception_ptr err_;
   bool stop_ = false;
@@ -364,9 +397,11 @@ class HipTransport final : public DgTransport {
     if (uint32_t(b) >= x_.blocks) return stage_[size_t(uint32_t(b) - x_.blocks)];
     return static_cast<char*>(chunks_[size_t(uint64_t(b) / per_chunk_)]) + (uint64_t(b) % per_chunk_) * x_.host_stride;
   }
-  // Three-tier: the staging buffers (pinned, one host stride each) and the context's reader of a key's file bytes;
-  // with x_.disk_queue > 1 a read pool and one word per staging buffer in fine-grained host memory.
-  void enable_disk(std::function<void(uint32_t, char*)> reader, const DgDevWords& dw) {
+  // Three-tier: the staging buffers (pinned, one host stride each) and the context's readers of a key's file bytes
+  // (the whole unit; a piece of a part) and its finisher; with x_.disk_queue > 1 a read pool and one word per
+  // staging buffer in fine-grained host memory.
+  void enable_disk(std::function<void(uint32_t, char*)> reader, ReadPool::PieceReader piece_reader,
+                   ReadPool::Finisher finisher, const DgDevWords& dw) {
     reader_ = std::move(reader);
     for (uint32_t i = 0; i < x_.S; ++i)
       stage_.push_back(static_cast<char*>(dev_->alloc_pinned(x_.host_stride, "disk staging buffer")));
@@ -377,7 +412,12 @@ class HipTransport final : public DgTransport {
       rpending_.assign(x_.S, 0);
       raux_.assign(x_.S, 0);
       dw_ = dw;
-      pool_ = std::make_unique<ReadPool>(x_.disk_queue, reader_);
+      std::vector<ReadPool::Piece> pieces;  // 8 MiB slices of each part (4 KiB-aligned; the last one the rest)
+      for (uint32_t p = 0; p < x_.part_bytes.size(); ++p)
+        for (uint64_t o = 0; o < x_.part_bytes[p]; o += kReadPiece)
+          pieces.push_back(ReadPool::Piece{p, o, std::min(kReadPiece, x_.part_bytes[p] - o), x_.part_offset[p] + o});
+      pool_ = std::make_unique<ReadPool>(x_.disk_queue, std::move(pieces), std::move(piece_reader),
+                                         std::move(finisher));
     }
   }
   // A file read into staging buffer `block`: synchronous, or queued to the pool (its copies then await its word).
@@ -407,7 +447,7 @@ class HipTransport final : public DgTransport {
   }
   uint64_t read_ns() const { return pool_ ? pool_->read_ns() : read_ns_; }
   uint64_t read_wait_ns() const { return read_wait_ns_; }
-  uint64_t max_reads_in_flight() const { return pool_ ? pool_->max_inflight() : (read_ns_ ? 1 : 0); }
+  uint64_t max_reads_in_flight() const { return pool_ ? pool_->max_running() : (read_ns_ ? 1 : 0); }
   char* slot_ptr(uint32_t p, int32_t slot) const {
     return static_cast<char*>(arena_[p]) + uint64_t(slot) * x_.part_bytes[p];
   }
@@ -1330,6 +1370,8 @@ class HipDgCtx final : public DgCtx {
   void release() noexcept;
   // Every part of key k from its source file into dst, laid out as a host block (part p at part_offset[p]).
   void read_key(uint32_t k, char* dst) const;
+  // Bytes off .. off + bytes - 1 of part p of key k from its source file into dst.
+  void read_part(uint32_t k, uint32_t p, uint64_t off, uint64_t bytes, char* dst) const;
   // The XXH64 of key k's bytes at dst against its descriptor hash (SS_E_HASH on a mismatch).
   void check_key(uint32_t k, const char* dst) const;
 
@@ -1454,9 +1496,15 @@ void HipDgCtx::init() {
   core_ = std::make_unique<DgCore>(c, tr_.get());
   if (x_.disk_tier)
     tr_->enable_disk(
-        [this](uint32_t k, char* dst) {  // (reader threads too: the sources' positional reads are thread-safe)
+        [this](uint32_t k, char* dst) {
           read_key(k, dst);
           if (o_.verify_hash == 1) check_key(k, dst);  // (verify_hash 2: the device checks the landed bytes)
+        },
+        [this](uint32_t k, uint32_t p, uint64_t off, uint64_t bytes, char* dst) {  // (reader threads: the sources'
+          read_part(k, p, off, bytes, dst);                                         // positional reads are thread-safe)
+        },
+        [this](uint32_t k, const char* block) {
+          if (o_.verify_hash == 1) check_key(k, block);
         },
         dw_);
   // priority: the seed (validated), the plan's residents, then key order
@@ -1484,23 +1532,24 @@ void HipDgCtx::init() {
 }
 
 void HipDgCtx::read_key(uint32_t k, char* dst) const {
+  for (uint32_t p = 0; p < x_.part_bytes.size(); ++p) read_part(k, p, 0, x_.part_bytes[p], dst + x_.part_offset[p]);
+}
+
+void HipDgCtx::read_part(uint32_t k, uint32_t p, uint64_t off, uint64_t bytes, char* dst) const {
   const uint32_t g = core_->gated_of(k);
   const int L = x_.gated[g];
   const int u = int(k - x_.unit_base[g]);
-  const Layer& l = d_.layers[size_t(L)];
-  for (size_t p = 0; p < l.parts.size(); ++p) {
-    const Part& part = l.parts[p];
-    const SourceFile& f = *files_[size_t(part.source)];
-    const uint64_t F = part.offset + uint64_t(u) * part.stride;
-    require(F + part.bytes <= f.size(), SS_E_IO,
-            "unit (" + std::to_string(L) + ", " + std::to_string(u) + ") is past the end of its source");
-    const uint64_t al = std::max<uint64_t>(d_.sources[size_t(part.source)].align, 512);
-    if (!f.direct() || (F % al == 0 && part.bytes % al == 0 && x_.part_offset[p] % al == 0)) {
-      f.pread_all(dst + x_.part_offset[p], part.bytes, F);
-    } else {  // a buffered read of an unaligned range
-      SourceFile bf(f.path(), false);
-      bf.pread_all(dst + x_.part_offset[p], part.bytes, F);
-    }
+  const Part& part = d_.layers[size_t(L)].parts[p];
+  const SourceFile& f = *files_[size_t(part.source)];
+  const uint64_t F = part.offset + uint64_t(u) * part.stride + off;
+  require(F + bytes <= f.size(), SS_E_IO,
+          "unit (" + std::to_string(L) + ", " + std::to_string(u) + ") is past the end of its source");
+  const uint64_t al = std::max<uint64_t>(d_.sources[size_t(part.source)].align, 512);
+  if (!f.direct() || (F % al == 0 && bytes % al == 0 && reinterpret_cast<uintptr_t>(dst) % al == 0)) {
+    f.pread_all(dst, bytes, F);
+  } else {  // a buffered read of an unaligned range
+    SourceFile bf(f.path(), false);
+    bf.pread_all(dst, bytes, F);
   }
 }
 

@@ -170,7 +170,7 @@ ss_status tsa_synth(void* dst_dev, uint64_t bytes, uint64_t seed, uint64_t strea
                     float sigma, void* stream) {
   return guard([&] {
     require(bytes % 8 == 0 && offset % 8 == 0, SS_E_INVALID, "tsa_synth: bytes and offset must be multiples of 8");
-    require(kind <= 1, SS_E_INVALID, "tsa_synth: kind 0 (uniform bytes) or 1 (bf16 normal)");
+    require(kind <= 2, SS_E_INVALID, "tsa_synth: kind 0 (uniform bytes), 1 (bf16 normal) or 2 (Q4 blocks)");
     require(bytes == 0 || dst_dev, SS_E_INVALID, "tsa_synth: null destination");
     launch_ck(launch_synth(dst_dev, bytes, seed, stream_id, offset, kind, sigma, static_cast<hipStream_t>(stream)),
               "tsa_synth");

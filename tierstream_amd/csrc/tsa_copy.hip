@@ -74,9 +74,24 @@ __device__ __forceinline__ uint16_t bf16_rne(float f) {
   return uint16_t(x >> 16);
 }
 
+// Q4 blocks of 18 bytes (kind 2): block b is a little-endian fp16 scale, then 16 bytes of packed 4-bit values. The
+// scale is 0x2000 | (low 10 bits of word 3b): exponent field 8, so 2^-7 x (1 + m / 1024), a positive scale in
+// [0.0078, 0.0156); the 16 value bytes are words 3b + 1 and 3b + 2, little-endian. Byte j of the stream is byte j % 18
+// of block j / 18 (the blocks start at the stream's byte 0).
+__device__ __forceinline__ uint32_t q4_byte(uint64_t key, uint64_t j) {
+  const uint64_t b = j / 18u;
+  const uint32_t o = uint32_t(j - b * 18u);
+  if (o < 2u) {
+    const uint32_t scale = 0x2000u | uint32_t(word_at(key, 3u * b) & 0x3FFu);
+    return (scale >> (8u * o)) & 0xFFu;
+  }
+  const uint32_t q = o - 2u;
+  return uint32_t(word_at(key, 3u * b + 1u + (q >> 3)) >> (8u * (q & 7u))) & 0xFFu;
+}
+
 // kind 0: every 8-byte word is word_at(i). kind 1: word i gives two bf16 values (elements 2i, 2i + 1) by Box-Muller:
 // u1 = (hi32 + 0.5) / 2^32, u2 = (lo32 + 0.5) / 2^32, r = sigma sqrt(-2 ln u1), (r cos 2 pi u2, r sin 2 pi u2); a
-// 64-bit output word then holds elements 4w .. 4w + 3, i.e. source words 2w and 2w + 1.
+// 64-bit output word then holds elements 4w .. 4w + 3, i.e. source words 2w and 2w + 1. kind 2: Q4 blocks (above).
 __global__ __launch_bounds__(256) void synth_kernel(uint64_t* __restrict__ dst, uint64_t n_words, uint64_t key,
                                                     uint64_t first_word, uint32_t kind, float sigma) {
   const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
@@ -85,6 +100,9 @@ __global__ __launch_bounds__(256) void synth_kernel(uint64_t* __restrict__ dst, 
     uint64_t out;
     if (kind == 0) {
       out = word_at(key, gw);
+    } else if (kind == 2) {
+      out = 0;
+      for (uint32_t k = 0; k < 8u; ++k) out |= uint64_t(q4_byte(key, 8u * gw + k)) << (8u * k);
     } else {
       out = 0;
       for (int h = 0; h < 2; ++h) {

@@ -13,8 +13,13 @@ stride, the layers one after the other), a budget, options and a seeded route st
                the inclusive intent is kept with dg_inclusive_blocks clean copies.
   qwen3-moe    48 layers x 128 experts, parts 2048 x 768 x 2 (3 MiB each) bf16; 32 tokens x top-8 per step (the route
                union per layer); exclusive with write-backs, ss_acquire_groups hits first; 25 % resident; 128 steps.
-  deepseek-q4  58 layers x 256 experts, parts 7168 x 2048 in 18-byte Q4 blocks (8,257,536 bytes each); three tiers
-               (not served yet: it needs the three-tier file path).
+  deepseek-q4  58 layers x 256 experts, parts 7168 x 2048 in 18-byte Q4 blocks (8,257,536 bytes each, 24.8 MB per
+               unit, 367.8 GB in all); Zipf(1.2) top-8, batch 1; three tiers: VRAM for 54.4 % of the units (200 GB:
+               51.2 % residents, 8 spare slots per layer, the banks and the guard), pinned RAM for 17.4 % (64 GB: the
+               pinned homes and 24 spare blocks), the rest read from the source file with direct I/O on a miss
+               (dg_disk_tier, 4 reads in flight); device-gated, a hipGraph-captured token; 64 steps. The whole model
+               needs more host memory than one measurement host holds with its page cache, so the benchmark runs it
+               with fewer layers (the same per-layer shape, tier shares and routes).
 
 Bytes come from the counter-based generator (tsa_synth on the GPU, the same words for uniform bytes as
 oracle/synth.py); each unit's XXH64 is computed on the host by the library (tsa_xxh64_host).
@@ -60,6 +65,9 @@ class Workload:
     ring_slots: int = 0
     spare_units: int = 0
     inclusive_blocks: int = 0
+    pinned_fraction: float = 0.0  # three tiers: pinned homes + spare blocks as a share of the units (0: two tiers)
+    disk_queue: int = 0        # three tiers: file reads in flight (dg_disk_queue)
+    clean_evict: int = 0       # three tiers: dg_clean_evict
     seed: int = 1234
     notes: dict = field(default_factory=dict)
 
@@ -95,6 +103,9 @@ WORKLOADS = {
     "qwen3-moe": Workload("qwen3-moe", 48, 128, [2048 * 768 * BF16] * 3, top_k=8, tokens=32, routes="zipf",
                           zipf_s=1.1, gen=1, resident_fraction=0.25, tier_mode=1, groups=True, steps=128,
                           dynamic_slots=8),
+    "deepseek-q4": Workload("deepseek-q4", 58, 256, [7168 * 2048 // 32 * 18] * 3, top_k=8, routes="zipf", zipf_s=1.2,
+                            gen=2, resident_fraction=0.512, pinned_fraction=0.174, tier_mode=1, forward=1, steps=64,
+                            dynamic_slots=8, spare_units=24, disk_queue=4),
 }
 
 
@@ -131,42 +142,48 @@ def route_stream(w: Workload, steps: int | None = None) -> np.ndarray:
 
 
 # ---- sources, descriptor, budget -------------------------------------------------------------------------------------
-def unit_offset(w: Workload, L: int, u: int) -> int:
-    return (L * w.units + u) * w.unit_stride_file
+def unit_offset(w: Workload, L: int, u: int, first_layer: int = 0) -> int:
+    """Byte offset of unit (L, u) in the source file that holds layers first_layer.. (unit-major, 4 KiB stride)."""
+    return ((L - first_layer) * w.units + u) * w.unit_stride_file
 
 
-def source_bytes(w: Workload) -> int:
-    return w.n_units * w.unit_stride_file
+def source_bytes(w: Workload, n_layers: int | None = None) -> int:
+    return (w.layers if n_layers is None else n_layers) * w.units * w.unit_stride_file
 
 
-def write_sources_gpu(w: Workload, path: str | os.PathLike, threads: int = 16) -> list:
-    """Writes the source file from bytes the GPU generates (tsa_synth); returns the per-unit XXH64 list (global order),
-    computed on the host by the library. Each unit's parts are stream ids 4 g + p."""
+def write_sources_gpu(w: Workload, path: str | os.PathLike, threads: int = 16, first_layer: int = 0,
+                      n_layers: int | None = None, drop_cache: bool = False) -> list:
+    """Writes a source file holding layers first_layer .. first_layer + n_layers - 1 (default: every layer) from
+    bytes the GPU generates (tsa_synth); returns those units' XXH64 list (model order), computed on the host by the
+    library. Each unit's parts are stream ids 4 g + p (g = its global unit index). drop_cache: the file is synced and
+    its pages dropped from the page cache afterwards (a direct-I/O reader then reads the device)."""
     import tierstream_amd as tsa
     L = tsa.lib()
     path = str(path)
-    total = source_bytes(w)
+    n_layers = w.layers - first_layer if n_layers is None else n_layers
+    n_units = n_layers * w.units
+    g_first = first_layer * w.units
     fd = os.open(path, os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o644)
     try:
-        os.ftruncate(fd, total)
+        os.ftruncate(fd, source_bytes(w, n_layers))
     finally:
         os.close(fd)
     ub = w.unit_bytes
-    batch = max(1, min(w.n_units, (2 * GiB) // max(ub, 1)))  # units per GPU batch
+    batch = max(1, min(n_units, (2 * GiB) // max(ub, 1)))  # units per GPU batch
     dev = tsa.DeviceBuffer(batch * w.unit_stride_file)
     host = C.c_void_p()
     tsa.check(L.tsa_host_alloc(C.byref(host), batch * w.unit_stride_file))
-    hashes = [0] * w.n_units
+    hashes = [0] * n_units
     try:
         fd = os.open(path, os.O_WRONLY)
         with ThreadPoolExecutor(threads) as ex:
-            for g0 in range(0, w.n_units, batch):
-                n = min(batch, w.n_units - g0)
+            for i0 in range(0, n_units, batch):
+                n = min(batch, n_units - i0)
                 for i in range(n):
                     off = 0
                     for p, pb in enumerate(w.parts):
                         tsa.check(L.tsa_synth(C.c_void_p(dev.ptr + i * w.unit_stride_file + off), pb, w.seed,
-                                              4 * (g0 + i) + p, 0, w.gen, C.c_float(w.sigma), None))
+                                              4 * (g_first + i0 + i) + p, 0, w.gen, C.c_float(w.sigma), None))
                         off += pb
                 tsa.check(L.tsa_memcpy(host, C.c_void_p(dev.ptr), n * w.unit_stride_file, 1, None))
                 tsa.check(L.tsa_stream_sync(None))
@@ -174,11 +191,14 @@ def write_sources_gpu(w: Workload, path: str | os.PathLike, threads: int = 16) -
 
                 def one(i):
                     p = base + i * w.unit_stride_file
-                    hashes[g0 + i] = int(L.tsa_xxh64_host(C.c_void_p(p), ub))
+                    hashes[i0 + i] = int(L.tsa_xxh64_host(C.c_void_p(p), ub))
                     mv = (C.c_char * ub).from_address(p)
-                    os.pwrite(fd, mv, unit_offset(w, 0, 0) + (g0 + i) * w.unit_stride_file)
+                    os.pwrite(fd, mv, (i0 + i) * w.unit_stride_file)
 
                 list(ex.map(one, range(n)))
+        if drop_cache:
+            os.fsync(fd)
+            os.posix_fadvise(fd, 0, 0, os.POSIX_FADV_DONTNEED)
         os.close(fd)
     finally:
         L.tsa_host_free(host)
@@ -186,15 +206,27 @@ def write_sources_gpu(w: Workload, path: str | os.PathLike, threads: int = 16) -
     return hashes
 
 
-def desc_json(w: Workload, path: str, hashes: list) -> str:
+PART_FORMAT = {0: "U8", 1: "BF16", 2: "Q4_0"}
+
+
+def desc_json(w: Workload, path, hashes: list) -> str:
+    """The desc-v1 descriptor. path: one source file holding every layer, or a list of (path, first_layer, n_layers)
+    covering the layers in order (each layer's parts read the file that holds it)."""
+    files = [(str(path), 0, w.layers)] if isinstance(path, (str, os.PathLike)) else [(str(p), a, n) for p, a, n in path]
+    src_of = {}
+    for i, (_, a, n) in enumerate(files):
+        for L in range(a, a + n):
+            src_of[L] = (i, a)
+    assert sorted(src_of) == list(range(w.layers)), "the source files must cover every layer once"
     layers = []
     for L in range(w.layers):
         off = 0
         parts = []
         names = ["gate", "up", "down"] if len(w.parts) == 3 else [f"p{i}" for i in range(len(w.parts))]
+        src, first = src_of[L]
         for p, pb in enumerate(w.parts):
-            parts.append({"name": names[p], "format": "BF16" if w.gen == 1 else "U8", "source": 0,
-                          "offset": unit_offset(w, L, 0) + off, "stride": w.unit_stride_file, "bytes": pb})
+            parts.append({"name": names[p], "format": PART_FORMAT[w.gen], "source": src,
+                          "offset": unit_offset(w, L, 0, first) + off, "stride": w.unit_stride_file, "bytes": pb})
             off += pb
         lay = {"index": L, "kind": w.kind, "n_units": w.units, "unit_bytes": w.unit_bytes, "parts": parts,
                "hash": [f"{h:016x}" for h in hashes[L * w.units:(L + 1) * w.units]]}
@@ -202,7 +234,9 @@ def desc_json(w: Workload, path: str, hashes: list) -> str:
             lay["top_k"] = min(w.top_k, w.units)
         layers.append(lay)
     d = {"schema": "strix-stream/desc-v1", "model": w.name, "engine": "tsa-synthetic", "unit_align": 256,
-         "order": w.order, "tiers": "pinned", "sources": [{"name": "weights", "path": str(path), "align": 4096}],
+         "order": w.order, "tiers": "pinned|disk" if w.pinned_fraction else "pinned",
+         "sources": [{"name": f"weights{i}" if i else "weights", "path": p, "align": 4096}
+                     for i, (p, _, _) in enumerate(files)],
          "layers": layers}
     return json.dumps(d)
 
@@ -214,7 +248,9 @@ def unit_stride_dev(w: Workload) -> int:
 @dataclass
 class DgShape:
     """A device-gated workload's cache shape: R planned residents (the first units in model order: equal benefit), D
-    spare slots, B ids per layer (2 B + 1 bank and guard slots), P pinned homes, Q spare blocks, I clean copies."""
+    spare slots, B ids per layer (2 B + 1 bank and guard slots), P pinned homes, Q spare blocks, I clean copies; three
+    tiers: F file-tier units (the last in model order) and the explicit plan tiers (0 resident, 1 pinned, 2 file) in
+    model order."""
     R: int
     D: int
     B: int
@@ -223,6 +259,12 @@ class DgShape:
     I: int
     budget: dict
     options: dict
+    F: int = 0
+    tiers: list | None = None
+
+    def cold_first_layer(self, w: Workload) -> int:
+        """The first layer holding a file-tier unit (w.layers with none)."""
+        return (self.R + self.P) // w.units if self.F else w.layers
 
 
 def dg_shape(w: Workload) -> DgShape:
@@ -236,6 +278,8 @@ def dg_shape(w: Workload) -> DgShape:
     hs = (w.unit_bytes + 4095) // 4096 * 4096
     R = int(round(w.resident_fraction * w.n_units))
     B = w.max_ids
+    if w.pinned_fraction:
+        return _dg_shape_three_tier(w, R, B, st, hs)
     dyn = w.dynamic_slots or 1
     res_in = [min(w.units, max(0, R - L * w.units)) for L in range(w.layers)]
     D = sum(min(dyn, w.units - r) for r in res_in)
@@ -250,3 +294,26 @@ def dg_shape(w: Workload) -> DgShape:
                   dynamic_slots_per_layer=dyn, ring_slots=ring, tier_mode=1, host_spare_units=Q)
     options = dict(forward_mode=1, dg_max_ids=B, pin_planned=0, dg_inclusive_blocks=I, dg_wb_defer=1)
     return DgShape(R, D, B, P, Q, I, budget, options)
+
+
+def _dg_shape_three_tier(w: Workload, R: int, B: int, st: int, hs: int) -> DgShape:
+    """Three tiers from explicit plan tiers (a planner spill to the file tier fills the pinned budget and leaves no
+    spare block, which device-gated decode needs): the first R units resident, the next P pinned, the last F read from
+    their file. Pinned memory holds P homes and Q spare blocks (round(pinned_fraction x units) in all); a device victim
+    with no free block drops the least recently homed pinned unit to its file for its block, so Q only absorbs the
+    write-backs in flight. No clean copies (inclusive blocks) in three-tier mode."""
+    dyn = w.dynamic_slots or 1
+    res_in = [min(w.units, max(0, R - L * w.units)) for L in range(w.layers)]
+    D = sum(min(dyn, w.units - r) for r in res_in)
+    ring = 2 * B + 1
+    Q = w.spare_units or (2 * B + 8)
+    P = int(round(w.pinned_fraction * w.n_units)) - Q
+    F = w.n_units - R - P
+    if P < 1 or F < 1:
+        raise ValueError(f"{w.name}: three tiers need pinned and file units (R {R}, P {P}, F {F})")
+    reserve = w.layers * min(dyn, w.units)
+    budget = dict(device_bytes=(R + reserve + ring) * st + st // 2, host_pinned_bytes=(P + Q) * hs + hs // 2,
+                  dynamic_slots_per_layer=dyn, ring_slots=ring, tier_mode=1, host_spare_units=Q)
+    options = dict(forward_mode=1, dg_max_ids=B, pin_planned=0, dg_wb_defer=1, dg_disk_tier=1,
+                   dg_disk_queue=w.disk_queue, dg_clean_evict=w.clean_evict)
+    return DgShape(R, D, B, P, Q, 0, budget, options, F=F, tiers=[0] * R + [1] * P + [2] * F)
