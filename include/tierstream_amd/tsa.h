@@ -124,7 +124,7 @@ SS_API ss_status tsa_stream_create(void** stream);
 SS_API ss_status tsa_stream_destroy(void* stream);
 SS_API ss_status tsa_stream_sync(void* stream);
 SS_API ss_status tsa_device_sync(void);
-SS_API ss_status tsa_event_create(void** ev);              /* timing event */
+SS_API ss_status tsa_event_create(void** ev);              /* timing event (no system-scope fence when recorded) */
 SS_API ss_status tsa_event_destroy(void* ev);
 SS_API ss_status tsa_event_record(void* ev, void* stream);
 SS_API ss_status tsa_event_sync(void* ev);

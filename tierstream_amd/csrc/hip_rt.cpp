@@ -88,9 +88,11 @@ hipEvent_t HipDevice::event_create() {
   return e;
 }
 
+// Timing brackets carry only timestamps: recorded without a system-scope fence (no L2 write-back and invalidate at a
+// bracket, which would also touch the work it measures).
 hipEvent_t HipDevice::event_create_timed() {
   hipEvent_t e = nullptr;
-  hip_check(hipEventCreate(&e), "hipEventCreate");
+  hip_check(hipEventCreateWithFlags(&e, hipEventDisableSystemFence), "hipEventCreateWithFlags (timing)");
   return e;
 }
 

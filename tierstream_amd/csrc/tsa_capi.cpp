@@ -232,7 +232,7 @@ ss_status tsa_event_create(void** ev) {
   return guard([&] {
     require(ev != nullptr, SS_E_INVALID, "tsa_event_create: null");
     hipEvent_t e = nullptr;
-    hip_ck(hipEventCreate(&e), "hipEventCreate");
+    hip_ck(hipEventCreateWithFlags(&e, hipEventDisableSystemFence), "hipEventCreateWithFlags");
     *ev = e;
   });
 }
