@@ -338,14 +338,14 @@ def main():
     if tsa.gpu_count() < 1:
         raise SystemExit("bench.py: no HIP device")
     w = W.WORKLOADS[a.workload]
-    if w.forward != 1:
-        raise SystemExit(f"bench.py: workload {a.workload} is not device-gated")
     if a.part_bytes:
         w = W.scaled(w, part_bytes=a.part_bytes)
     if a.layers:
         w = W.scaled(w, layers=a.layers)
     if a.steps is None:
         a.steps = w.steps
+    if w.forward != 1:
+        return run_host(a, w, tsa, ss, W, L, C)
     if a.inclusive:
         w = W.scaled(w, inclusive_blocks=a.inclusive, spare_units=a.inclusive + 4)
     shape = W.dg_shape(w)
@@ -576,6 +576,106 @@ def main():
         shutil.rmtree(work, ignore_errors=True)
         if cold_work:
             shutil.rmtree(cold_work, ignore_errors=True)
+    print(json.dumps(result), flush=True)
+
+
+def run_host(a, w, tsa, ss, W, L, C):
+    """The host contract (ss_begin, per layer ss_layer_routes or ss_layer_all, ss_acquire or ss_acquire_groups with
+    every group waited for, the engine's read of the routed units through the table, ss_release; ss_end), one step per
+    forward, timed on the engine thread (tse_host_run); every landed unit re-hashed in HBM (verify_hash 2)."""
+    shape = W.host_shape(w)
+    base = a.workdir or ("/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir())
+    work = tempfile.mkdtemp(prefix="tsa_bench_", dir=base)
+    path = os.path.join(work, "weights.bin")
+    result = {}
+    try:
+        t0 = time.time()
+        log(f"workload {w.name}: {w.layers} x {w.units} units of {w.unit_bytes / 2**20:.1f} MiB, writing "
+            f"{W.source_bytes(w) / 1e9:.1f} GB to {path}")
+        hashes = W.write_sources_gpu(w, path)
+        log(f"sources written in {time.time() - t0:.1f} s")
+        desc_json = W.desc_json(w, path, hashes)
+        d = ss.Desc(desc_json)
+        b = ss.budget(**shape.budget)
+        plan = ss.Plan(d, b)
+        tiers = plan.tiers()
+        n_res = sum(1 for r in tiers for t in r if t == 0)
+        t0 = time.time()
+        ctx = ss.Ctx(d, b, plan, ss.options(**shape.options))
+        log(f"context open in {time.time() - t0:.1f} s: {n_res} resident units, mode {shape.mode}, budget {shape.budget}")
+        steps, warm = a.steps, a.warmup
+        routes = W.route_stream(w, warm + steps)
+        if shape.mode == 1:
+            routes = np.tile(np.arange(w.units, dtype=np.int32), (warm + steps, w.layers, 1))
+        ctx.host_run(routes[:warm], shape.mode, want_tables=False)
+        s0 = ctx.stats_total()
+        x0 = ctx.exclusive_stats() if w.tier_mode == 1 else None
+        tsa.check(L.tsa_device_sync())
+        t_start = time.perf_counter()
+        cks, _, stats, lat = ctx.host_run(routes[warm:warm + steps], shape.mode, want_tables=False)
+        tsa.check(L.tsa_device_sync())
+        wall = time.perf_counter() - t_start
+        s1 = ctx.stats_total()
+        x1 = ctx.exclusive_stats() if w.tier_mode == 1 else None
+        seen, bad = {}, 0
+        for t in range(steps):
+            for l in range(w.layers):
+                for i, u in enumerate(routes[warm + t, l]):
+                    if u < 0:
+                        continue
+                    v = int(cks[t, l, i])
+                    if seen.setdefault((l, int(u)), v) != v:
+                        bad += 1
+        failures = int(ss._declare().tsa_test_verify_failures(ctx.h))
+        ctx.close()
+        plan.close()
+        d.close()
+        log(f"timed {steps} steps in {wall:.2f} s: p50 {pct(lat, 50):.2f} ms p99 {pct(lat, 99):.2f} ms")
+        peaks = measure_peaks(tsa, L, C)
+        kern = measure_kernels(tsa, L, C, w)
+        dst = {k: s1[k] - s0[k] for k in s1 if k != "wait_ns"}
+        h2d_bytes = dst["bytes_pinned"]
+        result = {
+            "metric": METRIC, "value": round(pct(lat, 50), 3), "unit": "ms", "n_gpus": 1, "steps": steps,
+            "warmup": warm, "ms_per_step": round(wall * 1e3 / steps, 3), "higher_is_better": False, "scaling": "weak",
+            "vs_baseline": None, "dtype": "u8",
+            "data": f"synthetic ({'bf16 N(0, 0.02)' if w.gen == 1 else 'uniform'} bytes from the counter-based "
+                    f"generator; {w.routes} routes)",
+            "config": {"workload": f"{w.name}: {w.layers} layers x {w.units} units of {w.unit_bytes} B, "
+                                   f"{w.tokens} x top-{w.top_k} per step, {n_res} resident, host contract mode "
+                                   f"{shape.mode} ({['ss_acquire', 'ss_layer_all', 'ss_acquire_groups'][shape.mode]}), "
+                                   f"{'exclusive' if w.tier_mode == 1 else 'inclusive'}, verify_hash 2",
+                       "budget": shape.budget, "options": shape.options},
+            "p50_ms": round(pct(lat, 50), 3), "p99_ms": round(pct(lat, 99), 3),
+            "h2d": {"bytes_per_step": h2d_bytes // steps, "wall_GBps": round(h2d_bytes / wall / 1e9, 2),
+                    "pinned_peak_GBps": round(peaks["h2d_pinned_GBps"], 2),
+                    "frac_of_pinned_peak_wall": round(h2d_bytes / wall / 1e9 / peaks["h2d_pinned_GBps"], 3)},
+            "roofline": None,
+            "kernels": kern,
+            "stats": dst,
+            "exclusive": {k: x1[k] - x0[k] for k in x1} if x1 else None,
+            "checks": {"verify_failures": failures, "checksum_mismatches": bad, "units_seen": len(seen)},
+            "cpu_baseline": None,
+        }
+        if not a.no_cpu:
+            try:
+                from oracle import ref
+                if ref.available():
+                    n_tok = int(max(3, min(steps, a.cpu_seconds / max(float(np.median(lat)) / 1e3 * 10, 1e-3))))
+                    o = ss.options(**{k: v for k, v in shape.options.items() if k != "verify_hash"}, verify_hash=1)
+                    ms, open_s = ref.host_time(desc_json, ss.budget(**shape.budget), o,
+                                               routes[warm:warm + n_tok], shape.mode)
+                    result["cpu_baseline"] = {
+                        "value": round(pct(ms, 50), 3), "unit": "ms", "cores": 3, "kind": "reference",
+                        "p99_ms": round(pct(ms, 99), 3),
+                        "sample": f"steps {warm}..{warm + n_tok - 1} of the same route stream: the reference CPU "
+                                  f"backend (memcpy copies, host XXH64 of what it reads) after its open "
+                                  f"({open_s:.1f} s), the engine thread plus its 2 reader threads",
+                        "cpu": cpu_model(), "nproc": os.cpu_count()}
+            except Exception as e:  # noqa: BLE001
+                log(f"cpu baseline skipped: {e}")
+    finally:
+        shutil.rmtree(work, ignore_errors=True)
     print(json.dumps(result), flush=True)
 
 

@@ -320,3 +320,48 @@ def cpu_baseline_disk(n_units, persistent, bank, blocks, spare_target, part_byte
     names = ["misses", "fetched", "evicted", "writebacks_done", "hash_mismatches", "copied_bytes", "disk_reads",
              "disk_drops"]
     return ms, {k: int(v) for k, v in zip(names, out)}
+
+
+def host_time(desc_json: str, budget, options, routes: np.ndarray, mode: int = 0):
+    """The reference CPU backend's step time over `routes` (the contract calls of tse_host_run's loop: begin, per
+    layer routes or layer_all, acquire or acquire_groups with every group waited for, release; end), no tables or
+    checksums. Returns (step_ms [steps], open_s)."""
+    import time
+    from tierstream_amd.ss import SsLayerView
+    L = lib()
+    d, ctx = vp(), vp()
+    b = desc_json.encode()
+    _ck(L.ss_desc_from_json(b, len(b), C.byref(d)))
+    options.backend = 0  # SS_BACKEND_CPU
+    steps, nl, max_ids = routes.shape
+    ms = np.zeros(steps)
+    try:
+        t0 = time.perf_counter()
+        _ck(L.ss_open(d, C.byref(budget), None, C.byref(options), C.byref(ctx)))
+        open_s = time.perf_counter() - t0
+        units = [L.ss_desc_layer_units(d, l) for l in range(nl)]
+        rr = [[np.ascontiguousarray(routes[s, l], dtype=np.int32) for l in range(nl)] for s in range(steps)]
+        v = SsLayerView()
+        for s in range(steps):
+            t = time.perf_counter()
+            _ck(L.ss_begin(ctx, None, 0))
+            for l in range(nl):
+                if units[l] <= 0:
+                    continue
+                r = rr[s][l]
+                if mode == 1:
+                    _ck(L.ss_layer_all(ctx, l))
+                else:
+                    _ck(L.ss_layer_routes(ctx, l, r.ctypes.data_as(C.POINTER(i32)), int(np.sum(r >= 0))))
+                _ck((L.ss_acquire_groups if mode == 2 else L.ss_acquire)(ctx, l, None, C.byref(v)))
+                if mode == 2:
+                    for gi in range(1, v.n_groups):
+                        _ck(L.ss_group_wait(ctx, l, gi, None))
+                _ck(L.ss_release(ctx, l, None))
+            _ck(L.ss_end(ctx))
+            ms[s] = (time.perf_counter() - t) * 1e3
+    finally:
+        if ctx:
+            L.ss_close(ctx)
+        L.ss_desc_free(d)
+    return ms, open_s

@@ -11,7 +11,8 @@ namespace tsa {
 namespace {
 
 constexpr uint64_t kHostAlign = 4096;
-constexpr uint64_t kDefaultSegBytes = 64 * 1024;
+constexpr uint64_t kDefaultSegBytes = 8 * 1024;  // device verify checkpoints: 32 B per segment (0.4 % of a unit)
+constexpr size_t kVerifyBatch = 32;                // landed units per device verify launch
 
 bool resident_tier(uint8_t t) { return t == SS_TIER_RESIDENT || t == SS_TIER_RESIDENT_BACKED; }
 
@@ -229,6 +230,9 @@ void HostCtx::init() {
     vfail_dev_ = static_cast<uint32_t*>(dev_->alloc_device(vcap_ * 4, "verify results"));
     hip_check(hipMemsetAsync(vfail_dev_, 0, vcap_ * 4, copy_), "hipMemsetAsync");
     vdone_ev_ = dev_->event_create();
+    vready_ev_ = dev_->event_create();
+    vstream_ = dev_->stream_create_dedicated();
+    stream_sync(copy_);  // (the zeroed results before any check on the verify stream)
   }
 
   for (uint32_t i = 0; i < o_.reader_threads; ++i) workers_.emplace_back([this] { worker(); });
@@ -309,6 +313,8 @@ void HostCtx::cleanup() noexcept {
   dev_->free_device(vtable_dev_);
   dev_->free_device(vfail_dev_);
   dev_->event_destroy(vdone_ev_);
+  dev_->event_destroy(vready_ev_);
+  if (vstream_) dev_->stream_destroy(vstream_);
   dev_->stream_destroy(copy_);
   dev_->stream_destroy(wb_);
   L_.clear();
@@ -595,8 +601,10 @@ void HostCtx::read_unit_device(HostJob& j) {
   if (dverify_) verify_landed(j);
 }
 
-// verify_hash = 2: enqueue the checkpoint-parallel check of the unit just landed at j.dst, behind its copies on the
-// copy stream (copy_mu_ held by the caller). Collected at ss_end.
+// verify_hash = 2: the checkpoint-parallel check of the unit just landed at j.dst joins the pending batch (copy_mu_
+// held by the caller: its copies are on the copy stream already). A batch of kVerifyBatch units is launched at once on
+// the verify stream, behind the copy stream's work so far; the rest at ss_end, where the results are collected. One
+// launch per unit on the copy stream made every next copy wait for the check (a 9 MiB unit: 1,152 quads, 134 us).
 void HostCtx::verify_landed(const HostJob& j) {
   const Layer& l = d_.layers[size_t(j.layer)];
   const UnitCheck& c = checks_[size_t(gidx(j.layer, j.unit))];
@@ -608,14 +616,30 @@ void HostCtx::verify_landed(const HostJob& j) {
   v.ext[0].ptr = j.dst;
   v.ext[0].bytes = l.unit_bytes;
   v.n_ext = 1;
-  v.seg_first = 0;
+  v.seg_first = c.n_states;  // (its checkpoint count until the flush turns it into the launch's prefix sum)
   v.states = c.states_dev;
   v.digest = l.hash[size_t(j.unit)];
   v.total = l.unit_bytes;
   vunits_.push_back({j.layer, j.unit});
-  tsa_verify_unit* vd = static_cast<tsa_verify_unit*>(vtable_dev_) + i;
-  copy_h2d(vd, &v, sizeof v, copy_);
-  hip_check(hipError_t(launch_verify(vd, 1, c.n_states, seg_bytes_, vfail_dev_ + i, copy_)), "device verify launch");
+  if (vused_ - vflushed_ >= kVerifyBatch) flush_verify();
+}
+
+void HostCtx::flush_verify() {
+  const size_t n = vused_ - vflushed_;
+  if (!n) return;
+  uint64_t segs = 0;
+  for (size_t i = vflushed_; i < vused_; ++i) {
+    const uint64_t count = vtable_host_[i].seg_first;
+    vtable_host_[i].seg_first = segs;
+    segs += count;
+  }
+  ev_record(vready_ev_, copy_);
+  stream_wait(vstream_, vready_ev_);
+  tsa_verify_unit* vd = static_cast<tsa_verify_unit*>(vtable_dev_) + vflushed_;
+  copy_h2d(vd, vtable_host_ + vflushed_, n * sizeof(tsa_verify_unit), vstream_);
+  hip_check(hipError_t(launch_verify(vd, uint32_t(n), segs, seg_bytes_, vfail_dev_ + vflushed_, vstream_)),
+            "device verify launch");
+  vflushed_ = vused_;
 }
 
 void HostCtx::collect_verify() {
@@ -624,9 +648,10 @@ void HostCtx::collect_verify() {
     std::lock_guard<std::mutex> lk(copy_mu_);
     n = vused_;
     if (!n) return;
-    copy_d2h(vfail_host_, vfail_dev_, 4 * n, copy_);
-    hip_check(hipMemsetAsync(vfail_dev_, 0, 4 * n, copy_), "hipMemsetAsync");
-    ev_record(vdone_ev_, copy_);
+    flush_verify();
+    copy_d2h(vfail_host_, vfail_dev_, 4 * n, vstream_);
+    hip_check(hipMemsetAsync(vfail_dev_, 0, 4 * n, vstream_), "hipMemsetAsync");
+    ev_record(vdone_ev_, vstream_);
   }
   ev_sync(vdone_ev_);
   std::string bad;
@@ -635,7 +660,7 @@ void HostCtx::collect_verify() {
   {
     std::lock_guard<std::mutex> lk(copy_mu_);
     units.swap(vunits_);
-    vused_ = 0;
+    vused_ = vflushed_ = 0;
   }
   for (size_t i = 0; i < n; ++i)
     if (vfail_host_[i]) {

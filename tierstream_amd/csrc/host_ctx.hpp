@@ -158,7 +158,8 @@ class HostCtx {
   int block_class(int layer) const { return excl_ ? layer_class_[size_t(layer)] : -1; }
   hipEvent_t pooled_event();
   int64_t gidx(int layer, int unit) const { return d_.unit_base[size_t(layer)] + unit; }
-  void verify_landed(const HostJob& j);  // verify_hash = 2, on the copy stream behind the unit's copies
+  void verify_landed(const HostJob& j);  // verify_hash = 2: the unit joins the pending check batch (copy_mu_ held)
+  void flush_verify();                   // the pending batch: one launch on the verify stream behind its copies
   void collect_verify();
 
   Desc d_;
@@ -209,7 +210,9 @@ class HostCtx {
   uint32_t* vfail_dev_ = nullptr;
   tsa_verify_unit* vtable_host_ = nullptr;
   uint32_t* vfail_host_ = nullptr;
-  size_t vcap_ = 0, vused_ = 0;
+  size_t vcap_ = 0, vused_ = 0, vflushed_ = 0;  // table slots used this forward; the ones already launched
+  hipStream_t vstream_ = nullptr;                 // the checks (copies never queue behind them)
+  hipEvent_t vready_ev_ = nullptr;                // the copy stream at a flush: the batch's copies are done
   std::vector<std::pair<int, int>> vunits_;  // (layer, unit) of each verify slot this forward
   hipEvent_t vdone_ev_ = nullptr;
   uint64_t verify_fail_total_ = 0;

@@ -134,10 +134,11 @@ __attribute__((visibility("default"))) ss_status tse_host_run(ss_ctx* c, const s
   hipStream_t s = nullptr;
   TSE_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
   int32_t* ids_dev = nullptr;
+  int32_t* ids_host = nullptr;  // pinned: a layer's id copy needs no host wait (the step's end waits for them all)
   unsigned long long* out_dev = nullptr;
-  std::vector<unsigned long long> out_host(size_t(max_ids));
   ss_status st = SS_OK;
-  if (hipMalloc(&ids_dev, 4ull * max_ids * L) != hipSuccess || hipMalloc(&out_dev, 8ull * max_ids * L) != hipSuccess)
+  if (hipMalloc(&ids_dev, 4ull * max_ids * L) != hipSuccess || hipMalloc(&out_dev, 8ull * max_ids * L) != hipSuccess ||
+      hipHostMalloc(&ids_host, 4ull * max_ids * L, hipHostMallocDefault) != hipSuccess)
     st = SS_E_NOMEM;
   for (int step = 0; st == SS_OK && step < steps; ++step) {
     const auto t0 = std::chrono::steady_clock::now();
@@ -160,18 +161,17 @@ __attribute__((visibility("default"))) ss_status tse_host_run(ss_ctx* c, const s
       if (mode == 2)
         for (int gi = 1; st == SS_OK && gi < v.n_groups; ++gi) st = ss_group_wait(c, l, gi, s);
       if (st != SS_OK) break;
-      const int n_read = mode == 1 ? nu : n;
-      std::vector<int32_t> rid(size_t(std::max(n_read, 1)));
-      for (int i = 0; i < n_read; ++i) rid[size_t(i)] = mode == 1 ? i : r[i];
+      const int n_read = mode == 1 ? std::min(nu, max_ids) : n;
+      int32_t* rid = ids_host + size_t(l) * max_ids;
+      for (int i = 0; i < n_read; ++i) rid[i] = mode == 1 ? i : r[i];
       if (n_read > 0) {
-        st = ck(hipMemcpyAsync(ids_dev + size_t(l) * max_ids, rid.data(), 4ull * n_read, hipMemcpyHostToDevice, s));
+        st = ck(hipMemcpyAsync(ids_dev + size_t(l) * max_ids, rid, 4ull * n_read, hipMemcpyHostToDevice, s));
         if (st == SS_OK) {
           hipLaunchKernelGGL(checksum_table, dim3(chunks_of(ss_desc_unit_bytes(d, l)), n_read), dim3(kThreads), 0, s,
                              v.table_dev, ids_dev + size_t(l) * max_ids, ss_desc_unit_bytes(d, l),
                              out_dev + size_t(l) * max_ids);
           st = ck(hipGetLastError());
         }
-        if (st == SS_OK) st = ck(hipStreamSynchronize(s));  // (the rid buffer is pageable: the copy must finish)
       }
       if (st == SS_OK && tables)
         std::memcpy(tables + (size_t(step) * L + l) * max_units, v.table_host, 8ull * std::min(nu, max_units));
@@ -203,6 +203,7 @@ __attribute__((visibility("default"))) ss_status tse_host_run(ss_ctx* c, const s
   (void)hipStreamSynchronize(s);
   (void)hipFree(ids_dev);
   (void)hipFree(out_dev);
+  (void)hipHostFree(ids_host);
   (void)hipStreamDestroy(s);
   return st;
 }

@@ -68,6 +68,7 @@ class Workload:
     pinned_fraction: float = 0.0  # three tiers: pinned homes + spare blocks as a share of the units (0: two tiers)
     disk_queue: int = 0        # three tiers: file reads in flight (dg_disk_queue)
     clean_evict: int = 0       # three tiers: dg_clean_evict
+    group_units: int = 16      # host contract with groups: units per group (ss_options.group_units)
     seed: int = 1234
     notes: dict = field(default_factory=dict)
 
@@ -317,3 +318,34 @@ def _dg_shape_three_tier(w: Workload, R: int, B: int, st: int, hs: int) -> DgSha
     options = dict(forward_mode=1, dg_max_ids=B, pin_planned=0, dg_wb_defer=1, dg_disk_tier=1,
                    dg_disk_queue=w.disk_queue, dg_clean_evict=w.clean_evict)
     return DgShape(R, D, B, P, Q, 0, budget, options, F=F, tiers=[0] * R + [1] * P + [2] * F)
+
+
+@dataclass
+class HostShape:
+    """A host-contract workload's budget, options and engine mode (0 ss_layer_routes + ss_acquire, 1 ss_layer_all +
+    ss_acquire, 2 ss_layer_routes + ss_acquire_groups)."""
+    R: int
+    budget: dict
+    options: dict
+    mode: int
+
+
+def host_shape(w: Workload) -> HostShape:
+    """The budget that gives a host-contract workload its resident share. Units are ranked with equal benefit (or in
+    prefix order), so the residents are the first R units in model order; the planner reserves the dynamic slots and
+    the ring before it places residents (reference src/plan.cpp:60-83), so they are billed on top. Exclusive mode
+    bills spare blocks (host_spare_units) for the write-backs of evicted units."""
+    st = unit_stride_dev(w)
+    hs = (w.unit_bytes + 4095) // 4096 * 4096
+    R = int(round(w.resident_fraction * w.n_units))
+    dyn = w.dynamic_slots
+    ring = w.ring_slots or (2 if w.kind == "blob" else 2 * min(w.units, max(8, w.max_ids // 4)))
+    Q = w.spare_units or (dyn * w.layers if w.tier_mode == 1 else 0)
+    budget = dict(device_bytes=(R + dyn * w.layers + ring) * st + st // 2,
+                  host_pinned_bytes=(w.n_units - R + Q) * hs + hs // 2 + (64 << 20),
+                  dynamic_slots_per_layer=dyn, ring_slots=ring, tier_mode=w.tier_mode, host_spare_units=Q)
+    options = dict(pin_planned=0 if dyn else 1, verify_hash=2)
+    if w.groups:
+        options["group_units"] = w.group_units
+    mode = 1 if w.layer_all else (2 if w.groups else 0)
+    return HostShape(R, budget, options, mode)
