@@ -37,6 +37,12 @@ CASES = {
     "qwen-exclusive": dict(layers=6, units=16, parts=[32 * KiB] * 3, n_res=24, ring=32, dyn=2, steps=20, top_k=4,
                            tokens=4, mode=2, opts=dict(pin_planned=0, group_units=2),
                            budget=dict(tier_mode=1, host_spare_units=6)),
+    # the SCORED policy (reference src/resident_set.cpp:52-68: 0.7 transition + 0.2 window frequency + 0.1 recency)
+    "decode-scored": dict(layers=4, units=8, parts=[32 * KiB, 32 * KiB, 16 * KiB], n_res=8, ring=16, dyn=2, steps=24,
+                          top_k=2, mode=0, opts=dict(pin_planned=0, policy=1, score_window=6)),
+    "qwen-exclusive-scored": dict(layers=6, units=16, parts=[32 * KiB] * 3, n_res=24, ring=32, dyn=2, steps=20,
+                                  top_k=4, tokens=4, mode=2, opts=dict(pin_planned=0, group_units=2, policy=1),
+                                  budget=dict(tier_mode=1, host_spare_units=6)),
 }
 
 

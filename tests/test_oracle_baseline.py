@@ -84,3 +84,4 @@ def test_cpu_baseline_three_tier(tmp_path, clean_evict):
         eager.close()
     for k in ("misses", "fetched", "evicted", "writebacks_done", "disk_reads", "disk_drops"):
         assert got[k] == want[k], k
+
