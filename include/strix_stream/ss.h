@@ -292,6 +292,10 @@ SS_API void ss_stats_reset(ss_ctx* c);
 typedef void (*ss_stats_hook)(void* user, const ss_layer_stats* forward_total, const ss_layer_stats* per_layer,
                               int n_layers);
 SS_API void ss_set_stats_hook(ss_ctx* c, ss_stats_hook hook, void* user);
+/* The strix-stream/stats-v1 document of the counters now (reference include/strix_stream/ss.h:552): the backend,
+ * forwards, sources_direct, total, layers, and the exclusive (EXCLUSIVE tier mode) and device_gated objects. Freed
+ * with ss_free. */
+SS_API ss_status ss_stats_to_json(const ss_ctx* c, char** out_json, size_t* out_len);
 
 typedef struct ss_exclusive_stats {
   uint32_t struct_size;
@@ -308,6 +312,32 @@ SS_API ss_status ss_stats_exclusive_sized(const ss_ctx* c, ss_exclusive_stats* o
 static inline ss_status ss_stats_exclusive(const ss_ctx* c, ss_exclusive_stats* out) {
   return ss_stats_exclusive_sized(c, out, (uint32_t)sizeof *out);
 }
+
+/* Stats snapshot (reference include/strix_stream/ss.h:573-615): callable from any thread (not concurrently with or
+ * after ss_close), also on a poisoned context. The first call arms the context and returns SS_E_INVALID; from then on
+ * each ss_end that folds a forward (or token) and each ss_stats_reset between forwards publishes an immutable copy of
+ * the counters, which the calls return. The read-ahead fields stay 0 (read-ahead is not served by this library). */
+#define SS_HAVE_STATS_SNAPSHOT 1
+#define SS_SNAPSHOT_READAHEAD 1u
+#define SS_SNAPSHOT_EXCLUSIVE 2u
+typedef struct ss_snapshot_info {
+  uint32_t struct_size;
+  uint32_t flags;
+  uint64_t sequence;
+  uint64_t forwards;
+  uint64_t readahead_buffers, readahead_buffer_bytes, readahead_requested, readahead_read, readahead_landed;
+  uint64_t readahead_unused, readahead_failed, readahead_fallback, readahead_bytes;
+  uint64_t exclusive_writebacks, exclusive_writeback_bytes, exclusive_deferred, exclusive_promoted;
+  uint64_t exclusive_free_blocks, exclusive_min_free_blocks, exclusive_rereads, exclusive_blocks;
+  uint64_t exclusive_discards;
+} ss_snapshot_info;
+SS_API ss_status ss_stats_snapshot_sized(const ss_ctx* c, ss_layer_stats* total_out, ss_snapshot_info* info_out,
+                                         uint32_t info_size);
+static inline ss_status ss_stats_snapshot(const ss_ctx* c, ss_layer_stats* total_out, ss_snapshot_info* info_out) {
+  return ss_stats_snapshot_sized(c, total_out, info_out, (uint32_t)sizeof *info_out);
+}
+/* The stats-v1 document of the last publication, byte for byte what ss_stats_to_json gave then. Freed with ss_free. */
+SS_API ss_status ss_stats_snapshot_json(const ss_ctx* c, char** out_json, size_t* out_len);
 
 /* ---- device-gated decode ---------------------------------------------------------------------------------------- */
 #define SS_DG_MAX_PARTS 4

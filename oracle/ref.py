@@ -54,6 +54,7 @@ def lib() -> C.CDLL:
             "ss_release": (st, [vp, C.c_int, vp]),
             "ss_end": (st, [vp]),
             "ss_stats_total": (st, [vp, C.POINTER(SsLayerStats)]),
+            "ss_stats_to_json": (st, [vp, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]),
             "ref_region_of": (C.c_int, [vp, u64, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(u64)]),
             "refdg_open": (vp, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, u32, u32, u32, u32,
                                 C.POINTER(u64), u32, C.POINTER(u32), u32]),
@@ -199,6 +200,11 @@ def host_run(desc_json: str, budget, options, routes: np.ndarray, mode: int = 0)
             after = SsLayerStats()
             _ck(L.ss_stats_total(ctx, C.byref(after)))
             step["stats"] = {k: after.as_dict()[k] - before.as_dict()[k] for k in after.as_dict()}
+            if s == steps - 1:  # the stats-v1 document after the last step
+                txt, n = C.c_void_p(), C.c_size_t()
+                _ck(L.ss_stats_to_json(ctx, C.byref(txt), C.byref(n)))
+                step["stats_json"] = C.string_at(txt, n.value).decode()
+                L.ss_free(txt)
             out.append(step)
     finally:
         if ctx:

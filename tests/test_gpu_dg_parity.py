@@ -5,6 +5,7 @@ token the slot table and the cache counters must be identical, and every routed 
 ss_dg_slot must checksum to the oracle's value of the file bytes. Device verify (verify_hash = 2) re-hashes every
 landed unit in HBM. Shapes: the mixtral workload at test size (reference tests/test_dg_cuda.cu:297-323 drives the
 same protocol)."""
+import json
 import os
 
 import numpy as np
@@ -89,6 +90,8 @@ def test_dg_matches_reference(name, tmp_path, gpu):
     ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(**okw))
     eng = ss.DgEngine(ctx, c["n_ids"], use_graph=use_graph)
     expect = {(L, u): fixtures.engine_checksum(m.unit_data(L, u)) for L in range(c["layers"]) for u in range(c["units"])}
+    with pytest.raises(ss.SsError):  # arms the stats snapshot: each token's boundary publishes from now on
+        ctx.snapshot()
     try:
         for t in range(tokens):
             cks, _ = eng.token(routes[t])
@@ -101,10 +104,41 @@ def test_dg_matches_reference(name, tmp_path, gpu):
                 for i, u in enumerate(routes[t, L]):
                     assert int(cks[L, i]) == expect[(L, int(u))], (name, t, L, i)
         assert got["tokens"] == tokens and got["misses"] > 0
+        _check_stats_doc(ctx, want, tokens)
     finally:
         eng.close()
         ctx.close()
         refdg.close()
+
+
+def _check_stats_doc(ctx, want, tokens):
+    """The exclusive counters (reference src/dg_ctx.cpp:1081-1091, since open) from the reference core's counters, the
+    stats-v1 document (reference src/dg_ctx.cpp:1359-1545) and the snapshot published at the last boundary."""
+    x = ctx.exclusive_stats()
+    assert x["writebacks"] == want["evicted"] - want["wb_cancelled"] - want["inclusive_drops"] - want["disk_discards"]
+    assert x["writeback_bytes"] == want["wb_issued_bytes"]
+    assert x["promoted"] == want["fetched"] - want["bank_serves"] + want["prefetched"]
+    assert x["free_blocks"] == want["free_blocks"] and x["min_free_blocks"] <= x["free_blocks"]
+    text = ctx.stats_json()
+    doc = json.loads(text)
+    assert text == json.dumps(doc, sort_keys=True, separators=(",", ":"))
+    assert doc["schema"] == "strix-stream/stats-v1" and doc["backend"] == "hip" and doc["forwards"] == tokens
+    g, st = doc["device_gated"], ctx.dg_stats()
+    for k in COUNTERS + ["tokens", "writebacks_done", "wb_issued_bytes", "free_slots", "slots", "blocks"]:
+        if k.startswith("inclusive_"):  # (in the three_tier object, present with clean copies or a file tier)
+            assert "three_tier" not in g or g["three_tier"][k] == st[k], k
+        else:
+            assert g[k] == st[k], k
+    assert g["policy"] == "lru" and g["landing_issued"] == 0 and g["pf_legacy"] == 1
+    for k in ("writebacks", "writeback_bytes", "promoted", "free_blocks", "min_free_blocks"):
+        assert doc["exclusive"][k] == x[k], k
+    tot = ctx.stats_total()
+    assert {k: v for k, v in doc["total"].items()} == tot
+    assert sum(1 for _ in doc["layers"]) == len(doc["layers"]) and doc["layers"][0].keys() == tot.keys()
+    stot, info = ctx.snapshot()
+    assert stot == tot and info["sequence"] == tokens and info["forwards"] == tokens and info["flags"] == 2
+    assert info["exclusive_writebacks"] == x["writebacks"] and info["exclusive_blocks"] == doc["exclusive"]["blocks"]
+    assert ctx.snapshot_json() == text
 
 
 def test_zero_miss_token_needs_no_copy(tmp_path, gpu):
@@ -247,6 +281,8 @@ def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts):
     routes = _routes(layers, units, n_ids, 24, seed=9, zipf=True)
     expect = {(L, u): fixtures.engine_checksum(m.unit_data(L, u)) for L in range(layers) for u in range(units)}
     counters = COUNTERS + ["disk_reads", "disk_drops", "disk_discards", "clean_drops"]
+    with pytest.raises(ss.SsError):
+        ctx.snapshot()
     try:
         for t in range(routes.shape[0]):
             cks, _ = eng.token(routes[t])
@@ -262,6 +298,11 @@ def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts):
         assert got["disk_queue_resolved"] == max(queue, 1) and 1 <= got["disk_max_in_flight"] <= max(queue, 1), got
         assert got["disk_read_ns"] > 0 and got["disk_wait_ns"] > 0, got
         assert ctx.verify_failures() == 0
+        _check_stats_doc(ctx, want, routes.shape[0])
+        tt = json.loads(ctx.stats_json())["device_gated"]["three_tier"]
+        for k in ("disk_reads", "disk_drops", "disk_discards", "clean_drops"):
+            assert tt[k] == got[k], k
+        assert tt["disk_queue_resolved"] == max(queue, 1) and tt["staging"] == staging
     finally:
         eng.close()
         ctx.close()

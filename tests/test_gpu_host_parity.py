@@ -4,6 +4,8 @@ checksum of every routed unit's bytes as the engine reads them through table_dev
 checksums are of the bytes its own table entries point at, and both must equal the oracle's checksum of the file.
 Shapes follow the benchmark workloads at test size (reference tests/test_runtime.cpp:58-83 check the same things:
 table bytes == file bytes, stats balance)."""
+import json
+
 import numpy as np
 import pytest
 
@@ -78,9 +80,23 @@ def _run_case(name, tmp_path, gpu):
         raise
 
 
+def _stats_doc(text):
+    """A stats-v1 document with what legitimately differs between the two backends taken out: the backend name and
+    the host wait times. The text itself must be canonical (sorted keys, no whitespace), as the reference writes it."""
+    doc = json.loads(text)
+    assert text == json.dumps(doc, sort_keys=True, separators=(",", ":"))
+    doc["backend"] = None
+    for st in [doc["total"]] + doc["layers"]:
+        st["wait_ns"] = 0
+    return doc
+
+
 @pytest.mark.parametrize("name", list(CASES))
 def test_host_contract_matches_reference(name, tmp_path, gpu):
-    ctx, _ = _run_case(name, tmp_path, gpu)
+    ctx, want = _run_case(name, tmp_path, gpu)
+    # the stats-v1 document (reference src/stream_ctx.cpp:1827-1885) after the same forwards
+    assert _stats_doc(ctx.stats_json()) == _stats_doc(want[-1]["stats_json"]), name
+    assert json.loads(ctx.stats_json())["backend"] == "hip"
     tot = ctx.stats_total()
     # the stats balance of reference tests/test_runtime.cpp:78-83
     assert tot["hits"] + tot["admitted"] + tot["transient"] + tot["prefetched"] + tot["spec_used"] == tot["routed"]
@@ -102,5 +118,40 @@ def test_device_verify_of_landed_units(tmp_path, gpu):
         ctx.host_run(routes, 0)
         import tierstream_amd as tsa
         assert tsa.ss._declare().tsa_test_verify_failures(ctx.h) == 0
+    finally:
+        ctx.close()
+
+
+@pytest.mark.parametrize("name", ["moe-small", "qwen-exclusive"])
+def test_stats_snapshot(name, tmp_path, gpu):
+    """ss_stats_snapshot (reference include/strix_stream/ss.h:573-615): the first call arms and fails; each ss_end
+    then publishes the counters as ss_stats_total / ss_stats_exclusive / ss_stats_to_json gave them, and so does a
+    reset between forwards."""
+    c = CASES[name]
+    m = fixtures.write_model(tmp_path, c["layers"], c["units"], c["parts"], top_k=c["top_k"], seed=7)
+    routes = fixtures.uniform_routes(c["layers"], c["units"], c["top_k"], 3, seed=11, tokens=c.get("tokens", 1))
+    bkw = _budget(m, c["n_res"], c["ring"], c.get("dyn", 0), **c.get("budget", {}))
+    d = ss.Desc(m.desc_json())
+    ctx = ss.Ctx(d, ss.budget(**bkw), None, ss.options(**c["opts"]))
+    try:
+        with pytest.raises(ss.SsError):
+            ctx.snapshot()
+        with pytest.raises(ss.SsError):
+            ctx.snapshot_json()
+        ctx.host_run(routes[:2], c["mode"])
+        tot, info = ctx.snapshot()
+        assert tot == ctx.stats_total() and info["sequence"] == 2 and info["forwards"] == 2
+        assert ctx.snapshot_json() == ctx.stats_json()
+        excl = bkw.get("tier_mode", 0) == 1
+        assert info["flags"] == (2 if excl else 0)
+        if excl:
+            x = ctx.exclusive_stats()
+            for k in ("writebacks", "writeback_bytes", "deferred", "promoted", "free_blocks", "min_free_blocks",
+                      "rereads", "discards"):
+                assert info["exclusive_" + k] == x[k], k
+            assert info["exclusive_blocks"] == json.loads(ctx.stats_json())["exclusive"]["blocks"] > 0
+        ctx.stats_reset()
+        tot, info = ctx.snapshot()
+        assert info["sequence"] == 3 and tot["routed"] == 0 and ctx.snapshot_json() == ctx.stats_json()
     finally:
         ctx.close()

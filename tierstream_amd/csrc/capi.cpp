@@ -334,7 +334,48 @@ void ss_stats_reset(ss_ctx* c) {
   else c->host->stats_reset();
 }
 void ss_set_stats_hook(ss_ctx* c, ss_stats_hook hook, void* user) {
-  if (c && c->host) c->host->set_hook(hook, user);
+  if (!c) return;
+  if (c->dg) c->dg->set_hook(hook, user);
+  else if (c->host) c->host->set_hook(hook, user);
+}
+ss_status ss_stats_to_json(const ss_ctx* c, char** out_json, size_t* out_len) {
+  std::string s;
+  const ss_status st = guard([&] {
+    need(c != nullptr, "ss_stats_to_json: null context");
+    s = json_dump(c->dg ? c->dg->stats_json() : c->host->stats_json());
+  });
+  return st != SS_OK ? st : give_text(s, out_json, out_len);
+}
+// Any thread (reference include/strix_stream/ss.h:573-615): the first call arms the publication.
+ss_status ss_stats_snapshot_sized(const ss_ctx* c, ss_layer_stats* total_out, ss_snapshot_info* info_out,
+                                  uint32_t info_size) {
+  return guard([&] {
+    need(c != nullptr, "ss_stats_snapshot: null context");
+    need(total_out || info_out, "ss_stats_snapshot: no output");
+    need(!info_out || info_size >= sizeof(uint32_t), "ss_stats_snapshot: info_size below struct_size");
+    ss_layer_stats t{};
+    ss_snapshot_info i{};
+    need(c->dg ? c->dg->snapshot(&t, &i) : c->host->snapshot(&t, &i),
+         "no stats snapshot published yet (armed now: published at the next completed ss_end or reset between "
+         "forwards)");
+    if (total_out) *total_out = t;
+    if (info_out) {
+      i.struct_size = std::min<uint32_t>(info_size, uint32_t(sizeof i));
+      std::memcpy(static_cast<void*>(info_out), &i, i.struct_size);
+    }
+  });
+}
+ss_status ss_stats_snapshot_json(const ss_ctx* c, char** out_json, size_t* out_len) {
+  std::string s;
+  const ss_status st = guard([&] {
+    need(c != nullptr, "ss_stats_snapshot_json: null context");
+    Json j;
+    need(c->dg ? c->dg->snapshot_json(&j) : c->host->snapshot_json(&j),
+         "no stats snapshot published yet (armed now: published at the next completed ss_end or reset between "
+         "forwards)");
+    s = json_dump(j);
+  });
+  return st != SS_OK ? st : give_text(s, out_json, out_len);
 }
 ss_status ss_stats_exclusive_sized(const ss_ctx* c, ss_exclusive_stats* out, uint32_t size) {
   return guard([&] {

@@ -20,6 +20,7 @@
 #include "dg_proto.hpp"
 #include "hip_rt.hpp"
 #include "source.hpp"
+#include "stats_json.hpp"
 #include "tsa_device.hpp"
 #include "tierstream_amd/tsa_test.h"
 
@@ -1145,6 +1146,7 @@ class HipDgCtx final : public DgCtx {
       poisoned_ = true;
       fail(SS_E_BACKEND, token_failure(dev, "no device check result names the unit"));
     }
+    fold(true);
   }
 
   ss_dg_device_view device_view() const override {
@@ -1203,8 +1205,10 @@ class HipDgCtx final : public DgCtx {
     core_->set_prefetch_budget(per_layer, per_token);
   }
 
+  // Counters as folded at the last successful boundary (and at open): a token whose ss_end failed never shows, and a
+  // call between tokens never reads the service's live counters (reference src/dg_ctx.cpp:1547-1577).
   ss_dg_stats stats() const override {
-    const DgCounts a = core_->counts();
+    const DgCounts& a = fold_;
     const DgCounts& b = base_;
     ss_dg_stats s{};
     s.struct_size = uint32_t(sizeof s);
@@ -1247,30 +1251,30 @@ class HipDgCtx final : public DgCtx {
     TSA_D(clean_drops);
     TSA_D(clean_drop_bytes);
 #undef TSA_D
-    s.disk_units = core_->file_units();
+    s.disk_units = fold_file_units_;
     s.disk_queue_resolved = x_.disk_tier ? x_.disk_queue : 0;
     s.disk_locations = x_.disk_tier ? 1 : 0;
-    s.disk_read_ns = tr_->read_ns();
-    s.disk_wait_ns = tr_->read_wait_ns();
-    s.disk_max_in_flight = tr_->max_reads_in_flight();
-    s.free_slots = core_->free_slots();
+    s.disk_read_ns = fold_read_ns_ - base_read_ns_;
+    s.disk_wait_ns = fold_wait_ns_ - base_wait_ns_;
+    s.disk_max_in_flight = fold_max_in_flight_;
+    s.free_slots = fold_free_slots_;
     s.blocks = x_.blocks;
     s.slots = x_.slots;
     s.device_timeouts = load_acquire(m_.err_count);
-    s.wb_outstanding_bytes = core_->outstanding_bytes();
-    s.backed_units = core_->backed_units();
+    s.wb_outstanding_bytes = fold_outstanding_;
+    s.backed_units = fold_backed_;
     return s;
   }
   ss_layer_stats layer_stats(int layer) const override {
     require(layer >= 0 && size_t(layer) < d_.layers.size(), SS_E_INVALID, "ss_stats_layer: layer out of range");
     const int g = x_.ordinal[size_t(layer)];
     if (g < 0) return ss_layer_stats{};
-    return to_layer(core_->layer_counts()[size_t(g)], base_l_[size_t(g)]);
+    return to_layer(fold_l_[size_t(g)], base_l_[size_t(g)]);
   }
   ss_layer_stats total_stats() const override {
     ss_layer_stats t{};
     for (size_t g = 0; g < x_.gated.size(); ++g) {
-      const ss_layer_stats l = to_layer(core_->layer_counts()[g], base_l_[g]);
+      const ss_layer_stats l = to_layer(fold_l_[g], base_l_[g]);
       t.routed += l.routed;
       t.hits += l.hits;
       t.admitted += l.admitted;
@@ -1283,20 +1287,92 @@ class HipDgCtx final : public DgCtx {
     }
     return t;
   }
+  // Since open, never reset (reference src/dg_ctx.cpp:1081-1091): evictions that copied (not cancelled, not dropped
+  // as a clean copy, not discarded to their file), the bytes copied, the copies into persistent slots.
   ss_exclusive_stats exclusive_stats() const override {
-    const DgCounts& a = core_->counts();
+    const DgCounts& a = fold_;
     ss_exclusive_stats x{};
     x.struct_size = uint32_t(sizeof x);
-    x.writebacks = a.evicted - a.wb_cancelled - a.inclusive_drops;
-    x.writeback_bytes = x.writebacks * x_.unit_bytes;
-    x.promoted = a.fetched + a.prefetched;
-    x.free_blocks = core_->free_blocks();
+    x.writebacks = a.evicted - a.wb_cancelled - a.inclusive_drops - a.disk_discards;
+    x.writeback_bytes = a.wb_issued_bytes;
+    x.deferred = a.evict_short;
+    x.promoted = a.fetched - a.bank_serves + a.prefetched;
+    x.free_blocks = fold_free_blocks_;
+    x.min_free_blocks = min_free_blocks_;
     return x;
   }
   void stats_reset() override {
-    if (in_token_) return;
-    base_ = core_->counts();
-    base_l_ = core_->layer_counts();
+    if (in_token_) return;  // (nothing changes inside a gated token)
+    base_ = fold_;
+    base_l_ = fold_l_;
+    base_read_ns_ = fold_read_ns_;
+    base_wait_ns_ = fold_wait_ns_;
+    publish();
+  }
+  void set_hook(ss_stats_hook h, void* user) override {
+    hook_ = h;
+    hook_user_ = user;
+  }
+  Json stats_json() const override { return format_stats(stats(), exclusive_stats(), layers_now()); }
+  bool snapshot(ss_layer_stats* total, ss_snapshot_info* info) const override {
+    snap_armed_.store(true, std::memory_order_relaxed);
+    std::lock_guard<std::mutex> lk(snap_mu_);
+    if (snap_.seq == 0) return false;
+    ss_layer_stats t{};
+    for (const ss_layer_stats& l : snap_.layers) add_stats(t, l);
+    if (total) *total = t;
+    if (info) {
+      *info = ss_snapshot_info{};
+      info->struct_size = uint32_t(sizeof *info);
+      info->flags = SS_SNAPSHOT_EXCLUSIVE;
+      info->sequence = snap_.seq;
+      info->forwards = snap_.s.tokens;
+      info->exclusive_writebacks = snap_.x.writebacks;
+      info->exclusive_writeback_bytes = snap_.x.writeback_bytes;
+      info->exclusive_deferred = snap_.x.deferred;
+      info->exclusive_promoted = snap_.x.promoted;
+      info->exclusive_free_blocks = snap_.x.free_blocks;
+      info->exclusive_min_free_blocks = snap_.x.min_free_blocks;
+      info->exclusive_blocks = x_.blocks;
+    }
+    return true;
+  }
+  bool snapshot_json(Json* out) const override {
+    snap_armed_.store(true, std::memory_order_relaxed);
+    Published p;
+    {
+      std::lock_guard<std::mutex> lk(snap_mu_);
+      if (snap_.seq == 0) return false;
+      p = snap_;
+    }
+    *out = format_stats(p.s, p.x, p.layers);
+    return true;
+  }
+  // After a successful boundary (and at open): the core's counters as the stats show them, the hook with this
+  // token's per-layer numbers, the snapshot when armed (reference src/dg_ctx.cpp:1547-1577).
+  void fold(bool call_hook) {
+    prev_l_ = fold_l_;
+    fold_ = core_->counts();
+    fold_l_ = core_->layer_counts();
+    fold_free_slots_ = core_->free_slots();
+    fold_free_blocks_ = core_->free_blocks();
+    fold_outstanding_ = core_->outstanding_bytes();
+    fold_backed_ = core_->backed_units();
+    fold_file_units_ = core_->file_units();
+    fold_read_ns_ = tr_->read_ns();
+    fold_wait_ns_ = tr_->read_wait_ns();
+    fold_max_in_flight_ = tr_->max_reads_in_flight();
+    min_free_blocks_ = std::min(min_free_blocks_, fold_free_blocks_);
+    if (hook_ && call_hook) {
+      std::vector<ss_layer_stats> fwd(d_.layers.size());
+      ss_layer_stats tot{};
+      for (size_t g = 0; g < fold_l_.size(); ++g) {
+        fwd[size_t(x_.gated[g])] = to_layer(fold_l_[g], prev_l_[g]);
+        add_stats(tot, fwd[size_t(x_.gated[g])]);
+      }
+      hook_(hook_user_, &tot, fwd.data(), int(fwd.size()));
+    }
+    publish();
   }
   uint32_t host_table(int32_t* out, uint32_t cap) const override {
     const std::vector<int32_t>& t = core_->table();
@@ -1396,9 +1472,56 @@ class HipDgCtx final : public DgCtx {
   std::vector<uint8_t> run_;
   uint32_t seq_ = 0;
   bool in_token_ = false, poisoned_ = false;
-  DgCounts base_;
-  std::vector<DgLayerCounts> base_l_;
+  DgCounts base_, fold_;
+  std::vector<DgLayerCounts> base_l_, fold_l_, prev_l_;
+  uint32_t fold_free_slots_ = 0, fold_free_blocks_ = 0, min_free_blocks_ = UINT32_MAX;
+  uint64_t fold_outstanding_ = 0, fold_backed_ = 0, fold_file_units_ = 0;
+  uint64_t fold_read_ns_ = 0, fold_wait_ns_ = 0, fold_max_in_flight_ = 0, base_read_ns_ = 0, base_wait_ns_ = 0;
+  ss_stats_hook hook_ = nullptr;
+  void* hook_user_ = nullptr;
+  struct Published {
+    uint64_t seq = 0;
+    ss_dg_stats s{};
+    ss_exclusive_stats x{};
+    std::vector<ss_layer_stats> layers;
+  };
+  mutable std::atomic<bool> snap_armed_{false};
+  mutable std::mutex snap_mu_;
+  Published snap_;
   uint64_t verify_failures_ = 0;
+
+  static void add_stats(ss_layer_stats& a, const ss_layer_stats& b) {
+    a.routed += b.routed;
+    a.hits += b.hits;
+    a.admitted += b.admitted;
+    a.transient += b.transient;
+    a.evicted += b.evicted;
+    a.prefetched += b.prefetched;
+    a.spec_issued += b.spec_issued;
+    a.spec_used += b.spec_used;
+    a.spec_dropped += b.spec_dropped;
+    a.bytes_pinned += b.bytes_pinned;
+    a.bytes_disk += b.bytes_disk;
+    a.wait_ns += b.wait_ns;
+  }
+  // per descriptor layer (0 for a layer with no gated units)
+  std::vector<ss_layer_stats> layers_now() const {
+    std::vector<ss_layer_stats> v(d_.layers.size());
+    for (size_t L = 0; L < v.size(); ++L) v[L] = layer_stats(int(L));
+    return v;
+  }
+  // A poisoned context publishes no more: the last successful publication stays.
+  void publish() {
+    if (!snap_armed_.load(std::memory_order_relaxed) || poisoned_) return;
+    Published p;
+    p.s = stats();
+    p.x = exclusive_stats();
+    p.layers = layers_now();
+    std::lock_guard<std::mutex> lk(snap_mu_);
+    p.seq = snap_.seq + 1;
+    std::swap(snap_, p);
+  }
+  Json format_stats(const ss_dg_stats& s, const ss_exclusive_stats& x, const std::vector<ss_layer_stats>& layers) const;
 };
 
 void HipDgCtx::init() {
@@ -1527,8 +1650,137 @@ void HipDgCtx::init() {
   core_->check();
   run_.assign(G, 1);
   base_l_.assign(G, DgLayerCounts{});
+  fold(false);
   svc_ = std::make_unique<Service>(core_.get(), m_, x_.B, o_.dg_wait_timeout_ms, o_.device);
   svc_->start();
+}
+
+// The stats-v1 document of a device-gated context (reference src/dg_ctx.cpp:1359-1545): the host contract's keys, the
+// exclusive object and the device_gated object. Counters of what this library does not serve (priors, window
+// prefetches, landings, scored victims, placement rounds, make-resident, bank keeping) are 0, as the reference writes
+// them when those are off; backend is "hip".
+Json HipDgCtx::format_stats(const ss_dg_stats& s, const ss_exclusive_stats& x,
+                            const std::vector<ss_layer_stats>& layers) const {
+  static const std::pair<const char*, uint64_t ss_dg_stats::*> kFields[] = {
+      {"tokens", &ss_dg_stats::tokens}, {"lookups", &ss_dg_stats::lookups}, {"misses", &ss_dg_stats::misses},
+      {"covered", &ss_dg_stats::covered}, {"fetched", &ss_dg_stats::fetched},
+      {"prefetched", &ss_dg_stats::prefetched}, {"prefetch_used", &ss_dg_stats::prefetch_used},
+      {"pred_invalid", &ss_dg_stats::pred_invalid}, {"resurrected", &ss_dg_stats::resurrected},
+      {"bank_serves", &ss_dg_stats::bank_serves}, {"collected_mid", &ss_dg_stats::collected_mid},
+      {"evicted", &ss_dg_stats::evicted}, {"evict_short", &ss_dg_stats::evict_short},
+      {"writebacks_done", &ss_dg_stats::writebacks_done}, {"stalled", &ss_dg_stats::stalled},
+      {"wb_deferred", &ss_dg_stats::wb_deferred}, {"wb_cancelled", &ss_dg_stats::wb_cancelled},
+      {"wb_forced", &ss_dg_stats::wb_forced}, {"wb_boundary_flushed", &ss_dg_stats::wb_boundary_flushed},
+      {"wb_issued_bytes", &ss_dg_stats::wb_issued_bytes}, {"wb_completed_bytes", &ss_dg_stats::wb_completed_bytes},
+      {"wb_cancelled_bytes", &ss_dg_stats::wb_cancelled_bytes},
+      {"wb_boundary_flushed_bytes", &ss_dg_stats::wb_boundary_flushed_bytes},
+      {"wb_forced_wait_ns", &ss_dg_stats::wb_forced_wait_ns}, {"winpf_hints", &ss_dg_stats::winpf_hints},
+      {"winpf_hint_rows", &ss_dg_stats::winpf_hint_rows}, {"prior_issued", &ss_dg_stats::prior_issued},
+      {"prior_used", &ss_dg_stats::prior_used}, {"prior_late", &ss_dg_stats::prior_late},
+      {"prior_reverted", &ss_dg_stats::prior_reverted}, {"l1_candidates", &ss_dg_stats::l1_candidates},
+      {"l1_issued", &ss_dg_stats::l1_issued}, {"l1_used", &ss_dg_stats::l1_used}, {"l1_late", &ss_dg_stats::l1_late},
+      {"l1_reverted", &ss_dg_stats::l1_reverted}, {"l1_priced_out", &ss_dg_stats::l1_priced_out},
+      {"l1_skipped_ahead", &ss_dg_stats::l1_skipped_ahead}, {"prior_budget_stops", &ss_dg_stats::prior_budget_stops},
+      {"pf_reverted", &ss_dg_stats::pf_reverted}, {"pf_revert_bytes", &ss_dg_stats::pf_revert_bytes},
+      {"pred_skipped_ahead", &ss_dg_stats::pred_skipped_ahead},
+      {"pred_shadow_file_predicted", &ss_dg_stats::pred_shadow_file_predicted},
+      {"pred_shadow_file_demanded", &ss_dg_stats::pred_shadow_file_demanded},
+      {"pred_shadow_file_hit", &ss_dg_stats::pred_shadow_file_hit},
+      {"pred_shadow_file_predicted_bytes", &ss_dg_stats::pred_shadow_file_predicted_bytes},
+      {"pred_shadow_file_demanded_bytes", &ss_dg_stats::pred_shadow_file_demanded_bytes},
+      {"pred_shadow_file_hit_bytes", &ss_dg_stats::pred_shadow_file_hit_bytes},
+      {"pf_strict_refused", &ss_dg_stats::pf_strict_refused}, {"landing_issued", &ss_dg_stats::landing_issued},
+      {"landing_promoted", &ss_dg_stats::landing_promoted}, {"landing_late", &ss_dg_stats::landing_late},
+      {"landing_wait_ns", &ss_dg_stats::landing_wait_ns}, {"landing_expired", &ss_dg_stats::landing_expired},
+      {"landing_dropped_full", &ss_dg_stats::landing_dropped_full},
+      {"landing_read_bytes", &ss_dg_stats::landing_read_bytes},
+      {"landing_cancelled", &ss_dg_stats::landing_cancelled},
+      {"landing_expired_layer", &ss_dg_stats::landing_expired_layer},
+      {"landing_skipped_passed", &ss_dg_stats::landing_skipped_passed},
+      {"landing_yields", &ss_dg_stats::landing_yields},
+      {"landing_aborted_bytes", &ss_dg_stats::landing_aborted_bytes},
+      {"score_fallbacks", &ss_dg_stats::score_fallbacks}, {"scored_victims", &ss_dg_stats::scored_victims},
+      {"score_layers", &ss_dg_stats::score_layers}, {"score_candidates", &ss_dg_stats::score_candidates},
+      {"score_saturated", &ss_dg_stats::score_saturated}, {"score_ns", &ss_dg_stats::score_ns},
+      {"score_deferred", &ss_dg_stats::score_deferred}, {"score_last_ns", &ss_dg_stats::score_last_ns},
+      {"resident_units", &ss_dg_stats::resident_units}, {"resident_evicted", &ss_dg_stats::resident_evicted},
+      {"resident_bytes", &ss_dg_stats::resident_bytes}, {"resident_ns", &ss_dg_stats::resident_ns},
+      {"mkres_file_reads", &ss_dg_stats::mkres_file_reads}, {"mkres_file_bytes", &ss_dg_stats::mkres_file_bytes},
+      {"mkres_read_ns", &ss_dg_stats::mkres_read_ns}, {"mkres_h2d_bytes", &ss_dg_stats::mkres_h2d_bytes},
+      {"mkres_wb_bytes", &ss_dg_stats::mkres_wb_bytes}, {"round_count", &ss_dg_stats::round_count},
+      {"round_units", &ss_dg_stats::round_units}, {"round_bytes", &ss_dg_stats::round_bytes},
+      {"round_ns", &ss_dg_stats::round_ns}, {"round_cancelled", &ss_dg_stats::round_cancelled},
+      {"lm_tokens", &ss_dg_stats::lm_tokens}, {"lm_parts", &ss_dg_stats::lm_parts},
+      {"lm_mid_evictions", &ss_dg_stats::lm_mid_evictions}, {"lm_early_admits", &ss_dg_stats::lm_early_admits}};
+  static const std::pair<const char*, uint64_t ss_dg_stats::*> kDiskFields[] = {
+      {"disk_reads", &ss_dg_stats::disk_reads}, {"disk_read_bytes", &ss_dg_stats::disk_read_bytes},
+      {"disk_read_ns", &ss_dg_stats::disk_read_ns}, {"disk_stage_waits", &ss_dg_stats::disk_stage_waits},
+      {"disk_drops", &ss_dg_stats::disk_drops}, {"disk_discards", &ss_dg_stats::disk_discards},
+      {"inclusive_kept", &ss_dg_stats::inclusive_kept}, {"inclusive_drops", &ss_dg_stats::inclusive_drops},
+      {"disk_wait_ns", &ss_dg_stats::disk_wait_ns}, {"disk_overlapped", &ss_dg_stats::disk_overlapped},
+      {"disk_carried", &ss_dg_stats::disk_carried}, {"disk_carried_bytes", &ss_dg_stats::disk_carried_bytes},
+      {"disk_max_in_flight", &ss_dg_stats::disk_max_in_flight}, {"clean_drops", &ss_dg_stats::clean_drops},
+      {"clean_drop_bytes", &ss_dg_stats::clean_drop_bytes}, {"bank_kept", &ss_dg_stats::bank_kept}};
+  Json j = Json::object();
+  j["schema"] = Json::string("strix-stream/stats-v1");
+  j["backend"] = Json::string("hip");
+  j["forwards"] = Json::number(s.tokens);
+  Json direct = Json::array();
+  for (const auto& f : files_) direct.push(Json::boolean(f->direct()));
+  j["sources_direct"] = direct;
+  ss_layer_stats t{};
+  Json ls = Json::array();
+  for (const ss_layer_stats& l : layers) {
+    add_stats(t, l);
+    ls.push(stats_object(l));
+  }
+  j["total"] = stats_object(t);
+  j["layers"] = ls;
+  Json e = Json::object();
+  e["writebacks"] = Json::number(x.writebacks);
+  e["writeback_bytes"] = Json::number(x.writeback_bytes);
+  e["deferred"] = Json::number(x.deferred);
+  e["wb_deferred"] = Json::number(fold_.wb_deferred);  // since open, as the other exclusive counters
+  e["rereads"] = Json::number(uint64_t(0));
+  e["promoted"] = Json::number(x.promoted);
+  e["free_blocks"] = Json::number(x.free_blocks);
+  e["min_free_blocks"] = Json::number(x.min_free_blocks);
+  e["blocks"] = Json::number(uint64_t(x_.blocks));
+  j["exclusive"] = e;
+  Json g = Json::object();
+  for (const auto& f : kFields) g[f.first] = Json::number(s.*f.second);
+    g["free_slots"] = Json::number(uint64_t(uint64_t(s.free_slots)));
+  g["blocks"] = Json::number(uint64_t(uint64_t(x_.blocks)));
+  g["slots"] = Json::number(uint64_t(uint64_t(x_.slots)));
+  g["pf_revert_unused"] = Json::number(uint64_t(0));
+  g["pf_strict_admit"] = Json::number(uint64_t(0));
+  g["pf_legacy"] = Json::number(uint64_t(1));
+  g["landing_blocks"] = Json::number(uint64_t(0));
+  g["landing_max_queued"] = Json::number(uint64_t(0));
+  g["landing_ttl"] = Json::number(uint64_t(0));
+  g["landing_failed"] = Json::number(uint64_t(0));
+  g["policy"] = Json::string("lru");
+  g["cuda_module_loading"] = Json::string("unknown");  // (a CUDA setting; HIP has no such mode)
+  g["landing_chunk"] = Json::number(uint64_t(0));
+  if (x_.disk_tier || x_.I) {  // three tiers or clean copies: only then, so the two-tier document is unchanged
+    Json tt = Json::object();
+    for (const auto& f : kDiskFields) tt[f.first] = Json::number(s.*f.second);
+    tt["unit_subread_bytes"] = Json::number(uint64_t(0));
+    tt["clean_evict"] = Json::number(uint64_t(uint64_t(o_.dg_clean_evict != 0)));
+    tt["bank_keep"] = Json::number(uint64_t(0));
+    tt["bank_keep_drops"] = Json::number(uint64_t(0));
+    tt["bank_keep_rereads"] = Json::number(uint64_t(0));
+    tt["disk_queue"] = Json::number(uint64_t(uint64_t(x_.disk_queue)));
+    tt["disk_queue_resolved"] = Json::number(uint64_t(uint64_t(x_.disk_queue)));
+    tt["disk_locations"] = Json::number(uint64_t(uint64_t(x_.disk_tier ? 1 : 0)));
+    tt["disk_units_open"] = Json::number(uint64_t(uint64_t(x_.F)));
+    tt["staging"] = Json::number(uint64_t(uint64_t(x_.S)));
+    tt["inclusive_blocks"] = Json::number(uint64_t(uint64_t(x_.I)));
+    tt["disk_queue_adapt"] = Json::string("off");
+    g["three_tier"] = tt;
+  }
+  j["device_gated"] = g;
+  return j;
 }
 
 void HipDgCtx::read_key(uint32_t k, char* dst) const {

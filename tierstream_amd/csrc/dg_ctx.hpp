@@ -6,6 +6,7 @@
 
 #include <memory>
 
+#include "json.hpp"
 #include "model.hpp"
 #include "tierstream_amd/tsa_test.h"
 
@@ -34,6 +35,11 @@ class DgCtx {
   virtual ss_layer_stats total_stats() const = 0;
   virtual ss_exclusive_stats exclusive_stats() const = 0;
   virtual void stats_reset() = 0;
+  virtual void set_hook(ss_stats_hook h, void* user) = 0;
+  // The stats-v1 document of the counters now; the snapshot publication (as the host contract's)
+  virtual Json stats_json() const = 0;
+  virtual bool snapshot(ss_layer_stats* total, ss_snapshot_info* info) const = 0;
+  virtual bool snapshot_json(Json* out) const = 0;
   virtual uint32_t host_table(int32_t* out, uint32_t cap) const = 0;
   virtual uint64_t verify_failures() const = 0;
   // measurement hooks (tsa_test.h)

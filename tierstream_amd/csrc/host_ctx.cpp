@@ -5,6 +5,7 @@
 #include <cstdio>
 #include <cstring>
 
+#include "stats_json.hpp"
 #include "tsa_device.hpp"
 
 namespace tsa {
@@ -172,6 +173,7 @@ void HostCtx::init() {
       for (size_t i = blocks.size(); i-- > 0;) free_blocks_[k].push_back(blocks[i]);  // lowest address on top
       spares_of_.push_back(plan_.spares[k].blocks);
       free_total += plan_.spares[k].blocks;
+      n_blocks_ += class_total[k];
     }
     xst_.free_blocks = xst_.min_free_blocks = free_total;
     wb_units_.reserve(size_t(d_.total_units));
@@ -1286,6 +1288,7 @@ void HostCtx::end() {
   in_forward_ = false;
   fwd_open_ = false;
   ++forward_;
+  publish();  // (also a forward whose read failed: its numbers are folded)
   if (dverify_ && failed == SS_OK) collect_verify();  // throws SS_E_HASH naming the first unit that differs
   if (failed != SS_OK) fail(failed, err);
 }
@@ -1323,7 +1326,102 @@ ss_layer_stats HostCtx::total() const {
   return t;
 }
 
-void HostCtx::stats_reset() { std::fill(stats_.begin(), stats_.end(), ss_layer_stats{}); }
+void HostCtx::stats_reset() {
+  std::fill(stats_.begin(), stats_.end(), ss_layer_stats{});
+  if (!in_forward_) publish();
+}
+
+// ---- stats-v1 and the snapshot (reference src/stream_ctx.cpp:1762-1885) ------------------------------------------
+
+void HostCtx::publish() {
+  if (!snap_armed_.load(std::memory_order_relaxed)) return;
+  std::lock_guard<std::mutex> lk(snap_mu_);
+  if (snap_.layers.size() != stats_.size()) snap_.layers.resize(stats_.size());
+  std::copy(stats_.begin(), stats_.end(), snap_.layers.begin());
+  snap_.x = xst_;
+  snap_.forwards = forward_;
+  ++snap_.seq;
+}
+
+bool HostCtx::snapshot(ss_layer_stats* total, ss_snapshot_info* info) const {
+  snap_armed_.store(true, std::memory_order_relaxed);
+  ss_layer_stats t{};
+  ss_snapshot_info i{};
+  {
+    std::lock_guard<std::mutex> lk(snap_mu_);
+    if (snap_.seq == 0) return false;
+    for (const ss_layer_stats& l : snap_.layers) add(t, l);
+    i.sequence = snap_.seq;
+    i.forwards = snap_.forwards;
+    if (excl_) {
+      i.exclusive_writebacks = snap_.x.writebacks;
+      i.exclusive_writeback_bytes = snap_.x.writeback_bytes;
+      i.exclusive_deferred = snap_.x.deferred;
+      i.exclusive_promoted = snap_.x.promoted;
+      i.exclusive_free_blocks = snap_.x.free_blocks;
+      i.exclusive_min_free_blocks = snap_.x.min_free_blocks;
+      i.exclusive_rereads = snap_.x.rereads;
+      i.exclusive_discards = snap_.x.discards;
+    }
+  }
+  if (excl_) {
+    i.flags |= SS_SNAPSHOT_EXCLUSIVE;
+    i.exclusive_blocks = n_blocks_;
+  }
+  i.struct_size = uint32_t(sizeof i);
+  if (total) *total = t;
+  if (info) *info = i;
+  return true;
+}
+
+bool HostCtx::snapshot_json(Json* out) const {
+  snap_armed_.store(true, std::memory_order_relaxed);
+  Published p;
+  p.layers.resize(stats_.size());
+  {
+    std::lock_guard<std::mutex> lk(snap_mu_);
+    if (snap_.seq == 0) return false;
+    std::copy(snap_.layers.begin(), snap_.layers.end(), p.layers.begin());
+    p.x = snap_.x;
+    p.forwards = snap_.forwards;
+  }
+  *out = format_stats(p.forwards, p.layers.data(), p.x);
+  return true;
+}
+
+Json HostCtx::stats_json() const { return format_stats(forward_, stats_.data(), xst_); }
+
+Json HostCtx::format_stats(uint64_t forwards, const ss_layer_stats* layers, const ss_exclusive_stats& x) const {
+  Json j = Json::object();
+  j["schema"] = Json::string("strix-stream/stats-v1");
+  j["backend"] = Json::string("hip");
+  j["forwards"] = Json::number(forwards);
+  Json direct = Json::array();
+  for (const auto& f : files_) direct.push(Json::boolean(f->direct()));
+  j["sources_direct"] = direct;
+  ss_layer_stats t{};
+  Json ls = Json::array();
+  for (size_t L = 0; L < stats_.size(); ++L) {
+    add(t, layers[L]);
+    ls.push(stats_object(layers[L]));
+  }
+  j["total"] = stats_object(t);
+  j["layers"] = ls;
+  if (excl_) {
+    Json e = Json::object();
+    e["writebacks"] = Json::number(x.writebacks);
+    e["writeback_bytes"] = Json::number(x.writeback_bytes);
+    e["discards"] = Json::number(x.discards);
+    e["deferred"] = Json::number(x.deferred);
+    e["rereads"] = Json::number(x.rereads);
+    e["promoted"] = Json::number(x.promoted);
+    e["free_blocks"] = Json::number(x.free_blocks);
+    e["min_free_blocks"] = Json::number(x.min_free_blocks);
+    e["blocks"] = Json::number(n_blocks_);
+    j["exclusive"] = e;
+  }
+  return j;
+}
 
 ss_exclusive_stats HostCtx::exclusive_stats() const {
   ss_exclusive_stats x = xst_;

@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "hip_rt.hpp"
+#include "json.hpp"
 #include "model.hpp"
 #include "residency.hpp"
 #include "source.hpp"
@@ -82,6 +83,11 @@ class HostCtx {
   bool poisoned() const { return poisoned_; }
   Region region_of(uint64_t addr) const;
   uint64_t verify_failures() const { return verify_fail_total_; }
+  // The stats-v1 document of the counters now; the snapshot publication (armed by the first snapshot call, published
+  // at each ss_end that folds a forward and each reset between forwards; any thread).
+  Json stats_json() const;
+  bool snapshot(ss_layer_stats* total, ss_snapshot_info* info) const;
+  bool snapshot_json(Json* out) const;
 
  private:
   enum Loc : int8_t { None = 0, Persistent = 1, Ring = 2 };
@@ -221,6 +227,17 @@ class HostCtx {
   bool fwd_stream_set_ = false;
   bool poisoned_ = false, in_forward_ = false, fwd_open_ = false;
   uint64_t forward_ = 0;
+  uint64_t n_blocks_ = 0;  // EXCLUSIVE: the pinned blocks (the homes of the pinned units and the spares)
+  struct Published {
+    uint64_t seq = 0, forwards = 0;
+    std::vector<ss_layer_stats> layers;
+    ss_exclusive_stats x{};
+  };
+  mutable std::atomic<bool> snap_armed_{false};
+  mutable std::mutex snap_mu_;
+  Published snap_;
+  void publish();
+  Json format_stats(uint64_t forwards, const ss_layer_stats* layers, const ss_exclusive_stats& x) const;
   std::vector<HostJobPtr> fwd_jobs_;
   std::vector<ss_layer_stats> stats_, fwd_stats_;
   ss_stats_hook hook_ = nullptr;

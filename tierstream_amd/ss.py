@@ -66,6 +66,15 @@ class SsLayerStats(C.Structure):
         return {n: int(getattr(self, n)) for n in STAT_FIELDS}
 
 
+class SsSnapshotInfo(C.Structure):
+    _fields_ = [("struct_size", u32), ("flags", u32), ("sequence", u64), ("forwards", u64)] + [
+        (n, u64) for n in ("readahead_buffers readahead_buffer_bytes readahead_requested readahead_read "
+                           "readahead_landed readahead_unused readahead_failed readahead_fallback readahead_bytes "
+                           "exclusive_writebacks exclusive_writeback_bytes exclusive_deferred exclusive_promoted "
+                           "exclusive_free_blocks exclusive_min_free_blocks exclusive_rereads exclusive_blocks "
+                           "exclusive_discards").split()]
+
+
 class SsExclusiveStats(C.Structure):
     _fields_ = [("struct_size", u32), ("writebacks", u64), ("writeback_bytes", u64), ("deferred", u64),
                 ("promoted", u64), ("free_blocks", u64), ("min_free_blocks", u64), ("rereads", u64),
@@ -168,6 +177,10 @@ def _declare() -> C.CDLL:
         "ss_stats_layer": (st, [vp, C.c_int, C.POINTER(SsLayerStats)]),
         "ss_stats_total": (st, [vp, C.POINTER(SsLayerStats)]),
         "ss_stats_exclusive_sized": (st, [vp, C.POINTER(SsExclusiveStats), u32]),
+        "ss_stats_to_json": (st, [vp, C.POINTER(vp), C.POINTER(C.c_size_t)]),
+        "ss_stats_snapshot_sized": (st, [vp, C.POINTER(SsLayerStats), C.POINTER(SsSnapshotInfo), u32]),
+        "ss_stats_snapshot_json": (st, [vp, C.POINTER(vp), C.POINTER(C.c_size_t)]),
+        "ss_stats_reset": (None, [vp]),
         "ss_stats_dg_sized": (st, [vp, C.POINTER(SsDgStats), u32]),
         "ss_dg_get_device_view_sized": (st, [vp, C.POINTER(SsDgDeviceView), u32]),
         "ss_dg_gated_index": (C.c_int, [vp, C.c_int]),
@@ -326,6 +339,31 @@ class Ctx:
         s = SsLayerStats()
         check(_declare().ss_stats_layer(self.h, layer, C.byref(s)))
         return s.as_dict()
+
+    def _text(self, fn) -> str:
+        L = _declare()
+        p, n = vp(), C.c_size_t()
+        check(fn(self.h, C.byref(p), C.byref(n)))
+        try:
+            return C.string_at(p, n.value).decode()
+        finally:
+            L.ss_free(p)
+
+    def stats_json(self) -> str:
+        """ss_stats_to_json: the stats-v1 document of the counters now."""
+        return self._text(_declare().ss_stats_to_json)
+
+    def snapshot(self):
+        """ss_stats_snapshot: (total dict, info dict); raises SsError (SS_E_INVALID) until something is published."""
+        t, i = SsLayerStats(), SsSnapshotInfo()
+        check(_declare().ss_stats_snapshot_sized(self.h, C.byref(t), C.byref(i), C.sizeof(i)))
+        return t.as_dict(), {n: int(getattr(i, n)) for n, _ in i._fields_}
+
+    def snapshot_json(self) -> str:
+        return self._text(_declare().ss_stats_snapshot_json)
+
+    def stats_reset(self):
+        _declare().ss_stats_reset(self.h)
 
     def exclusive_stats(self) -> dict:
         x = SsExclusiveStats()
