@@ -375,6 +375,23 @@ SS_API ss_status ss_dg_enqueue_end(ss_ctx* c, void* stream);
 SS_API ss_status ss_dg_residency(ss_ctx* c, ss_dg_unit* out, uint32_t cap, uint32_t* total);
 SS_API ss_status ss_dg_set_budgets(ss_ctx* c, uint32_t spare_target, uint32_t prefetch_per_layer,
                                    uint32_t prefetch_per_token);
+/* Scored eviction (policy SS_POLICY_SCORED or SS_POLICY_SCORED_AUTO; reference include/strix_stream/ss.h:730-746).
+ * Only the boundary's choice of victims changes: the eligible units (on the device, no write-back in flight) are taken
+ * lowest score first, score = w_t P + w_f F + w_r Rec in integers (P: the transition estimate from this token's union
+ * of the layer's routed ids; F: how many of the layer's last 16 unions hold the unit; Rec: 1 / (1 + tokens since its
+ * last routed use)); ties go to the older use, then to the less recent unit. The history lives as long as the context
+ * (ss_stats_reset keeps it). dg_score_w_* (thousandths, summing to 1000; all 0 = 700 / 200 / 100) and an optional
+ * TSSCPRF1 dg_score_profile of starting counts, bound to the descriptor's per-unit hashes, are read at ss_open. Host
+ * memory: 4 x units^2 bytes per gated layer (twice that with a profile), pageable. */
+#define SS_DG_SCORED 1
+/* ss_end for a token that closed `rows` verify rows (rows >= 1; ss_end is one row): SCORED_AUTO ranks by score only
+ * when rows > 1, else it takes the recency tail (its history still learns). */
+SS_API ss_status ss_dg_end_rows(ss_ctx* c, uint32_t rows);
+/* Between tokens: drains the write-backs, switches LRU / SCORED / SCORED_AUTO and resets the learning to the open
+ * profile's counts (or zero) and every demand epoch, keeping placement and recency. Switching to scoring needs a
+ * context opened with SCORED or SCORED_AUTO (SS_E_INVALID otherwise). */
+#define SS_DG_SET_POLICY 1
+SS_API ss_status ss_dg_set_policy(ss_ctx* c, ss_policy policy);
 
 /* The reference layout in full (fields this library does not count stay 0). */
 typedef struct ss_dg_stats {

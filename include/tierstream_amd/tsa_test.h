@@ -69,6 +69,11 @@ typedef struct tsa_test_dgcore_config {
   uint32_t n_parts;
   uint32_t disk_tier, home_blocks, disk_staging, clean_evict, disk_prefetch;
   const uint8_t* disk; /* three-tier: 1 per key for the plan's file tier (key order) */
+  /* appended, scored eviction: policy 0 LRU / 1 SCORED / 2 SCORED_AUTO, the score weights (thousandths, sum 1000), the
+   * verify rows each token's boundary closes (0 = 1), starting transition counts (per gated layer units^2 uint32
+   * row-major [previous unit][unit], layers concatenated; null = an empty table). The union width is bank_slots. */
+  uint32_t policy, w_trans, w_freq, w_rec, rows;
+  const uint32_t* score_cells;
 } tsa_test_dgcore_config;
 SS_API ss_status tsa_test_dgcore_open(const tsa_test_dgcore_config* cfg, const uint32_t* order, uint32_t n_order,
                                       void** out);
@@ -76,6 +81,17 @@ SS_API ss_status tsa_test_dgcore_open(const tsa_test_dgcore_config* cfg, const u
 SS_API ss_status tsa_test_dgcore_token(void* h, const uint32_t* ids, uint32_t n, int32_t* table_out, uint64_t* counts,
                                        uint32_t n_counts);
 SS_API const char* tsa_test_dgcore_counter_names(void);
+/* As tsa_test_dgcore_token with run [n_gated] (null: all): the gated layers the token exports (ss_begin's rows). */
+SS_API ss_status tsa_test_dgcore_token_run(void* h, const uint32_t* ids, uint32_t n, const uint8_t* run,
+                                           int32_t* table_out, uint64_t* counts, uint32_t n_counts);
+/* Between tokens: the policy switch of ss_dg_set_policy on the core alone. */
+SS_API ss_status tsa_test_dgcore_set_policy(void* h, uint32_t policy);
+/* Scored eviction's profile rules without a context: the SHA-256 of data[0..n) (32 raw bytes into out), and the
+ * TSSCPRF1 checks of a profile against the gated layers' units and a 32-byte identity (SS_E_INVALID naming the first
+ * broken rule; the provenance into prov, NUL-terminated, when it passes). */
+SS_API ss_status tsa_test_sha256(const void* data, uint64_t n, unsigned char* out);
+SS_API ss_status tsa_test_score_profile_check(const void* data, uint64_t len, const uint32_t* units, uint32_t n_gated,
+                                              const unsigned char* identity, char* prov, uint32_t prov_cap);
 /* Three-tier: the pinned homes, most recently homed first; the return is the count. */
 SS_API uint32_t tsa_test_dgcore_host_order(void* h, uint32_t* out, uint32_t cap);
 SS_API void tsa_test_dgcore_close(void* h);

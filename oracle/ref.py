@@ -59,10 +59,19 @@ def lib() -> C.CDLL:
             "refdg_open": (vp, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, u32, u32, u32, u32,
                                 C.POINTER(u64), u32, C.POINTER(u32), u32]),
             "refdg_token": (C.c_int, [vp, C.POINTER(u32), u32, C.POINTER(u32), u32, C.POINTER(i32), C.POINTER(u64)]),
+            "refdg_token_run": (C.c_int, [vp, C.POINTER(u32), u32, C.POINTER(u32), u32, C.POINTER(C.c_uint8),
+                                          C.POINTER(i32), C.POINTER(u64)]),
             "refdg_counter_names": (C.c_char_p, []),
             "refdg_residency": (u32, [vp, C.POINTER(u32), u32]),
             "refdg_open_disk": (vp, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, C.POINTER(u64), u32,
                                      C.POINTER(u32), u32, u32, u32, u32, u32, C.POINTER(C.c_uint8)]),
+            "refdg_open_scored": (vp, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, C.POINTER(u64), u32,
+                                       C.POINTER(u32), u32, u32, u32, u32, u32, u32, C.POINTER(u32), u32, u32, u32,
+                                       C.POINTER(C.c_uint8)]),
+            "refdg_set_policy": (C.c_int, [vp, u32]),
+            "refdg_profile_check": (C.c_int, [C.c_char_p, u64, C.POINTER(u32), u32, C.c_char_p]),
+            "refdg_score_identity": (C.c_int, [u32, C.POINTER(u32), C.POINTER(u32), C.POINTER(u64), C.POINTER(u64),
+                                               C.c_char_p]),
             "refdg_host_order": (u32, [vp, C.POINTER(u32), u32]),
             "refdg_close": (None, [vp]),
             "refdg_cpu_baseline": (C.c_int, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, C.POINTER(u64), u32,
@@ -217,14 +226,27 @@ class RefDg:
     """The reference DgCore on an immediate transport (its canonical schedule)."""
 
     def __init__(self, n_units, persistent, bank, blocks, spare_target, part_bytes, order, prefetch_reserve=0xFFFFFFFF,
-                 pf_layer=4, pf_token=48, wb_defer=1, wb_on_d2h=1, inclusive=0, disk=None):
+                 pf_layer=4, pf_token=48, wb_defer=1, wb_on_d2h=1, inclusive=0, disk=None, score=None):
         """disk (three-tier): dict(flags=[keys] 0/1 file-tier, home_blocks=P, disk_staging=S, clean_evict=0,
-        disk_prefetch=0); the prefetch budgets then take their defaults."""
+        disk_prefetch=0); the prefetch budgets then take their defaults. score (scored eviction): dict(policy=1 SCORED
+        or 2 SCORED_AUTO, w=(w_trans, w_freq, w_rec), rows=verify rows per boundary, cells=None or the starting
+        transition counts, per gated layer units^2 row-major, concatenated); the prefetch budgets take their defaults
+        and disk prefetch stays off."""
         L = lib()
         nu = (u32 * len(n_units))(*n_units)
         pb = (u64 * len(part_bytes))(*part_bytes)
         od = (u32 * len(order))(*order)
-        if disk is None:
+        if score is not None:
+            w = score.get("w", (700, 200, 100))
+            cells = score.get("cells")
+            cp = (u32 * len(cells))(*cells) if cells is not None else None
+            fl = (C.c_uint8 * sum(n_units))(*disk["flags"]) if disk else None
+            dk = disk or {}
+            self.h = L.refdg_open_scored(nu, len(n_units), persistent, bank, blocks, spare_target, wb_defer, inclusive,
+                                         pb, len(part_bytes), od, len(order), score["policy"], w[0], w[1], w[2],
+                                         score.get("rows", 1), cp, dk.get("home_blocks", 0), dk.get("disk_staging", 0),
+                                         dk.get("clean_evict", 0), fl)
+        elif disk is None:
             self.h = L.refdg_open(nu, len(n_units), persistent, bank, blocks, spare_target, prefetch_reserve, pf_layer,
                                   pf_token, wb_defer, wb_on_d2h, inclusive, pb, len(part_bytes), od, len(order))
         else:
@@ -238,8 +260,9 @@ class RefDg:
         self.G = len(n_units)
         self.names = L.refdg_counter_names().decode().split()
 
-    def token(self, ids: np.ndarray, pred: np.ndarray | None = None):
-        """ids uint32 [G][n]; returns (table int32 [keys], counters dict)."""
+    def token(self, ids: np.ndarray, pred: np.ndarray | None = None, run=None):
+        """ids uint32 [G][n]; run: the gated layers the token exports (None: all); returns (table int32 [keys],
+        counters dict)."""
         L = lib()
         x = np.ascontiguousarray(ids, dtype=np.uint32)
         n = x.shape[1]
@@ -247,11 +270,16 @@ class RefDg:
         n_pred = p.shape[1] if pred is not None else 0
         table = np.zeros(self.keys, dtype=np.int32)
         counts = np.zeros(len(self.names), dtype=np.uint64)
-        st = L.refdg_token(self.h, x.ctypes.data_as(C.POINTER(u32)), n, p.ctypes.data_as(C.POINTER(u32)), n_pred,
-                           table.ctypes.data_as(C.POINTER(i32)), counts.ctypes.data_as(C.POINTER(u64)))
+        rv = (C.c_uint8 * self.G)(*run) if run is not None else None
+        st = L.refdg_token_run(self.h, x.ctypes.data_as(C.POINTER(u32)), n, p.ctypes.data_as(C.POINTER(u32)), n_pred,
+                               rv, table.ctypes.data_as(C.POINTER(i32)), counts.ctypes.data_as(C.POINTER(u64)))
         if st != 0:
             raise RuntimeError("refdg_token failed")
         return table, {k: int(v) for k, v in zip(self.names, counts)}
+
+    def set_policy(self, policy):
+        if lib().refdg_set_policy(self.h, policy) != 0:
+            raise RuntimeError("refdg_set_policy failed")
 
     def residency(self):
         L = lib()

@@ -46,6 +46,7 @@
 #define private public
 #define protected public
 #include "dg_core.hpp"
+#include "dg_score.hpp"
 #include "stream_ctx.hpp"
 #include "xxh64.hpp"
 #undef private
@@ -122,6 +123,7 @@ struct RefDg {
   std::unique_ptr<Eager> t;
   std::unique_ptr<ts::DgCore> core;
   uint32_t seq = 0;
+  uint32_t rows = 1;  // the verify rows each token's boundary closes (scored auto ranks only above one)
 };
 
 }  // namespace
@@ -134,10 +136,19 @@ struct RefDiskOpts {
   uint32_t disk_tier = 0, home_blocks = 0, disk_staging = 0, clean_evict = 0, disk_prefetch = 0;
   const uint8_t* disk = nullptr;
 };
+// Scored eviction options of refdg_open (policy 0 = LRU: none of the others is read): policy 1 SCORED / 2 SCORED_AUTO,
+// the weights, the verify rows each boundary closes, and optional starting counts (per gated layer units^2 uint32
+// row-major, layers concatenated; null: an empty table), loaded as the reference loads a TSSCPRF1 profile (written by
+// its own dg_profile_write under a fixed identity).
+struct RefScoreOpts {
+  uint32_t policy = 0, w_trans = 700, w_freq = 200, w_rec = 100, rows = 1;
+  const uint32_t* cells = nullptr;
+};
 void* refdg_open_impl(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
                       uint32_t spare_target, uint32_t prefetch_reserve, uint32_t pf_layer, uint32_t pf_token,
                       uint32_t wb_defer, uint32_t wb_on_d2h, uint32_t inclusive, const uint64_t* part_bytes,
-                      uint32_t n_parts, const uint32_t* order, uint32_t n_order, const RefDiskOpts& dk);
+                      uint32_t n_parts, const uint32_t* order, uint32_t n_order, const RefDiskOpts& dk,
+                      const RefScoreOpts& so = RefScoreOpts{});
 
 void* refdg_open(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
                  uint32_t spare_target, uint32_t prefetch_reserve, uint32_t pf_layer, uint32_t pf_token,
@@ -162,10 +173,82 @@ void* refdg_open_disk(const uint32_t* n_units, uint32_t G, uint32_t persistent, 
                          part_bytes, n_parts, order, n_order, dk);
 }
 
+// refdg_open with scored eviction (RefScoreOpts) on the two-tier cache, or with disk flags (disk non-null) three-tier.
+void* refdg_open_scored(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
+                        uint32_t spare_target, uint32_t wb_defer, uint32_t inclusive, const uint64_t* part_bytes,
+                        uint32_t n_parts, const uint32_t* order, uint32_t n_order, uint32_t policy, uint32_t w_trans,
+                        uint32_t w_freq, uint32_t w_rec, uint32_t rows, const uint32_t* cells, uint32_t home_blocks,
+                        uint32_t disk_staging, uint32_t clean_evict, const uint8_t* disk) {
+  RefDiskOpts dk;
+  if (disk) {
+    dk.disk_tier = 1;
+    dk.home_blocks = home_blocks;
+    dk.disk_staging = disk_staging;
+    dk.clean_evict = clean_evict;
+    dk.disk = disk;
+  }
+  RefScoreOpts so;
+  so.policy = policy;
+  so.w_trans = w_trans;
+  so.w_freq = w_freq;
+  so.w_rec = w_rec;
+  so.rows = rows ? rows : 1;
+  so.cells = cells;
+  return refdg_open_impl(n_units, G, persistent, bank, blocks, spare_target, 0xFFFFFFFFu, 4, 48, wb_defer, 1, inclusive,
+                         part_bytes, n_parts, order, n_order, dk, so);
+}
+
+// The reference's model identity of a profile (dg_score_identity): per gated layer its model layer index, units, unit
+// bytes and per-unit xxh64 (hashes concatenated); the 32 raw bytes into out.
+int refdg_score_identity(uint32_t n_gated, const uint32_t* index, const uint32_t* units, const uint64_t* unit_bytes,
+                         const uint64_t* hashes, unsigned char* out) {
+  try {
+    std::vector<std::vector<uint64_t>> h(n_gated);
+    std::vector<ts::DgScoreIdLayer> v(n_gated);
+    for (uint32_t g = 0; g < n_gated; ++g) {
+      h[g].assign(hashes, hashes + units[g]);
+      hashes += units[g];
+      v[g].index = index[g];
+      v[g].units = units[g];
+      v[g].unit_bytes = unit_bytes[g];
+      v[g].hash = &h[g];
+    }
+    const std::string id = ts::dg_score_identity(v);
+    std::memcpy(out, id.data(), 32);
+    return 0;
+  } catch (const std::exception& e) {
+    return 1;
+  }
+}
+
+// The reference's TSSCPRF1 checks (dg_profile_check): 0 when the profile passes, 1 when it refuses it.
+int refdg_profile_check(const void* data, uint64_t len, const uint32_t* units, uint32_t n_gated,
+                        const unsigned char* identity) {
+  try {
+    (void)ts::dg_profile_check(data, len, std::vector<uint32_t>(units, units + n_gated),
+                               std::string(reinterpret_cast<const char*>(identity), 32));
+    return 0;
+  } catch (const std::exception& e) {
+    return 1;
+  }
+}
+
+// Between tokens: the reference's set_policy (drains, switches, resets the learning, renumbers the stamps).
+int refdg_set_policy(void* h, uint32_t policy) {
+  try {
+    static_cast<RefDg*>(h)->core->set_policy(policy);
+    return 0;
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "refdg_set_policy: %s\n", e.what());
+    return 1;
+  }
+}
+
 void* refdg_open_impl(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
                       uint32_t spare_target, uint32_t prefetch_reserve, uint32_t pf_layer, uint32_t pf_token,
                       uint32_t wb_defer, uint32_t wb_on_d2h, uint32_t inclusive, const uint64_t* part_bytes,
-                      uint32_t n_parts, const uint32_t* order, uint32_t n_order, const RefDiskOpts& dk) {
+                      uint32_t n_parts, const uint32_t* order, uint32_t n_order, const RefDiskOpts& dk,
+                      const RefScoreOpts& so) {
   try {
     auto* r = new RefDg;
     r->t = std::make_unique<Eager>(std::vector<uint64_t>(part_bytes, part_bytes + n_parts));
@@ -196,8 +279,28 @@ void* refdg_open_impl(const uint32_t* n_units, uint32_t G, uint32_t persistent, 
       for (uint32_t g = 0; g < G; ++g) keys += n_units[g];
       disk.assign(dk.disk, dk.disk + keys);
     }
+    if (so.policy) {  // as the reference context sets it up for SCORED / SCORED_AUTO
+      c.scored = true;
+      c.scored_auto = so.policy == 2;
+      c.boundary_score = true;
+      c.w_trans = so.w_trans;
+      c.w_freq = so.w_freq;
+      c.w_rec = so.w_rec;
+    }
+    r->rows = so.rows;
     r->core = std::make_unique<ts::DgCore>(c, r->t.get());
     r->core->place(std::vector<uint32_t>(order, order + n_order), dk.disk_tier ? &disk : nullptr);
+    if (so.policy && so.cells) {
+      const std::string identity(32, '\x5a');
+      std::vector<std::vector<uint32_t>> cells(G);
+      const uint32_t* p = so.cells;
+      for (uint32_t g = 0; g < G; ++g) {
+        cells[g].assign(p, p + size_t(n_units[g]) * n_units[g]);
+        p += size_t(n_units[g]) * n_units[g];
+      }
+      const std::string prof = ts::dg_profile_write(c.n_units, identity, "oracle", cells);
+      r->core->load_profile(prof.data(), prof.size(), identity);
+    }
     return r;
   } catch (const std::exception& e) {
     std::fprintf(stderr, "refdg_open: %s\n", e.what());
@@ -207,25 +310,40 @@ void* refdg_open_impl(const uint32_t* n_units, uint32_t G, uint32_t persistent, 
 
 // One token: ids [G][n] (every gated layer exported), pred [G][n_pred] (the prediction for layer g + 1 made at g;
 // n_pred = 0: none). Writes the table after the boundary (keys int32) and the counters (see refdg_counter_names).
+int refdg_token_run(void* h, const uint32_t* ids, uint32_t n, const uint32_t* pred, uint32_t n_pred,
+                    const uint8_t* run, int32_t* table_out, uint64_t* counts);
 int refdg_token(void* h, const uint32_t* ids, uint32_t n, const uint32_t* pred, uint32_t n_pred, int32_t* table_out,
                 uint64_t* counts) {
+  return refdg_token_run(h, ids, n, pred, n_pred, nullptr, table_out, counts);
+}
+
+// As refdg_token with run [G] (null: all): the gated layers the token exports, the others skipped as the reference
+// service skips them (src/dg_service.cpp:269-365).
+int refdg_token_run(void* h, const uint32_t* ids, uint32_t n, const uint32_t* pred, uint32_t n_pred,
+                    const uint8_t* run, int32_t* table_out, uint64_t* counts) {
   auto* r = static_cast<RefDg*>(h);
   try {
     ts::DgCore& c = *r->core;
     const uint32_t G = c.gated();
     ++r->seq;
-    c.begin_token(r->seq);
+    std::vector<uint8_t> rv(G, 1);
+    if (run) rv.assign(run, run + G);
+    c.begin_token(r->seq, &rv);
     for (uint32_t g = 0; g < G; ++g) {
+      if (!rv[g]) continue;
+      uint32_t nx = g + 1;
+      while (nx < G && !rv[nx]) ++nx;
       const uint32_t* x = ids + size_t(g) * n;
       uint64_t mask = 0;
       for (uint32_t i = 0; i < n; ++i)  // the export kernel: slot_of[unit_base[g] + id] < 0 at export time
         if (x[i] < c.units(g) && c.table()[c.key(g, x[i])] < 0) mask |= uint64_t(1) << i;
       c.serve_demand(g, x, n, mask);
       c.serve_use(g, x, n, mask);
-      if (n_pred && g + 1 < G) c.serve_prediction(g + 1, pred + size_t(g) * n_pred, n_pred, n, false);
-      if (c.deferred() && g + 1 < G) c.issue_writebacks(g, nullptr);
+      if (n_pred && g + 1 < G && rv[g + 1]) c.serve_prediction(g + 1, pred + size_t(g) * n_pred, n_pred, n, false);
+      if (c.deferred() && nx < G) c.issue_writebacks(g, nullptr);
+      c.score_layer(g);  // the service closes each layer after its write-back slice (nothing when not scored)
     }
-    c.end_token({}, 1);
+    c.end_token({}, r->rows);
     c.check();
     std::memcpy(table_out, c.table().data(), 4ull * c.keys());
     const ts::DgStats& s = c.stats();
@@ -236,7 +354,8 @@ int refdg_token(void* h, const uint32_t* ids, uint32_t n, const uint32_t* pred, 
                           s.wb_boundary_flushed, s.wb_issued_bytes, s.wb_cancelled_bytes, s.inclusive_kept,
                           s.inclusive_drops, uint64_t(c.free_slots()), uint64_t(c.free_blocks()),
                           uint64_t(c.on_device()), uint64_t(c.backed_units()), s.disk_reads, s.disk_drops,
-                          s.disk_discards, s.clean_drops, uint64_t(c.file_units())};
+                          s.disk_discards, s.clean_drops, uint64_t(c.file_units()), s.score_fallbacks,
+                          s.scored_victims, s.score_layers, s.score_candidates, s.score_saturated};
     std::memcpy(counts, v, sizeof v);
     return 0;
   } catch (const std::exception& e) {
@@ -249,7 +368,8 @@ const char* refdg_counter_names() {
   return "tokens lookups misses covered fetched prefetched prefetch_used pred_invalid resurrected bank_serves evicted "
          "evict_short writebacks_done predicted predicted_true miss_layers covered_waits wb_deferred wb_cancelled "
          "wb_forced wb_boundary_flushed wb_issued_bytes wb_cancelled_bytes inclusive_kept inclusive_drops free_slots "
-         "free_blocks on_device backed_units disk_reads disk_drops disk_discards clean_drops file_units";
+         "free_blocks on_device backed_units disk_reads disk_drops disk_discards clean_drops file_units "
+         "score_fallbacks scored_victims score_layers score_candidates score_saturated";
 }
 
 // The device keys in recency order, most recent first.

@@ -6,7 +6,8 @@ slot table, the counters and (three-tier) the pinned homes' recency order must b
 Configurations are drawn at random per seed: 2-6 gated layers of 4-16 units, 1-4 ids per layer (sometimes repeated,
 the batch-union case), residents, spare slots and spare blocks, clean copies (dg_inclusive_blocks), deferred or
 boundary write-backs; three-tier adds a file tier (a random share of the non-resident units), clean_evict and
-disk prefetch off. Routes are skewed (Zipf-like over a per-layer permutation) so that hits, misses, bank serves,
+disk prefetch off. Scored eviction (SCORED / SCORED_AUTO, weights, verify rows, starting counts), policy switches and
+tokens that export only some layers are drawn the same way. Routes are skewed (Zipf-like over a per-layer permutation) so that hits, misses, bank serves,
 resurrections and write-backs all occur. The reference's own CPU tests drive its core the same way
 (tests/test_dg.cpp:201)."""
 import ctypes as C
@@ -25,7 +26,8 @@ class DgCoreConfig(C.Structure):
                 ("prefetch_per_token", u32), ("wb_defer", u32), ("wb_on_d2h", u32), ("inclusive", u32),
                 ("part_bytes", C.POINTER(u64)), ("n_parts", u32), ("disk_tier", u32), ("home_blocks", u32),
                 ("disk_staging", u32), ("clean_evict", u32), ("disk_prefetch", u32),
-                ("disk", C.POINTER(C.c_uint8))]
+                ("disk", C.POINTER(C.c_uint8)), ("policy", u32), ("w_trans", u32), ("w_freq", u32), ("w_rec", u32),
+                ("rows", u32), ("score_cells", C.POINTER(u32))]
 
 
 def _lib():
@@ -40,12 +42,17 @@ def _lib():
     L.tsa_test_dgcore_host_order.restype = u32
     L.tsa_test_dgcore_close.argtypes = [C.c_void_p]
     L.tsa_test_dgcore_close.restype = None
+    L.tsa_test_dgcore_token_run.argtypes = [C.c_void_p, C.POINTER(u32), u32, C.POINTER(C.c_uint8),
+                                            C.POINTER(C.c_int32), C.POINTER(u64), u32]
+    L.tsa_test_dgcore_token_run.restype = C.c_int
+    L.tsa_test_dgcore_set_policy.argtypes = [C.c_void_p, u32]
+    L.tsa_test_dgcore_set_policy.restype = C.c_int
     return tsa, L
 
 
 class OurCore:
     def __init__(self, n_units, persistent, bank, blocks, spare_target, part_bytes, order, wb_defer, inclusive,
-                 disk=None):
+                 disk=None, score=None):
         self.tsa, self.L = _lib()
         self._keep = []
         nu = (u32 * len(n_units))(*n_units)
@@ -62,20 +69,32 @@ class OurCore:
             c.disk_tier, c.home_blocks, c.disk_staging = 1, disk["home_blocks"], disk["disk_staging"]
             c.clean_evict, c.disk_prefetch, c.disk = disk.get("clean_evict", 0), 0, fl
             self._keep.append(fl)
+        c.w_trans, c.w_freq, c.w_rec, c.rows = 700, 200, 100, 1
+        if score:
+            c.policy, c.rows = score["policy"], score.get("rows", 1)
+            c.w_trans, c.w_freq, c.w_rec = score.get("w", (700, 200, 100))
+            if score.get("cells") is not None:
+                cp = (u32 * len(score["cells"]))(*score["cells"])
+                c.score_cells = cp
+                self._keep.append(cp)
         self._keep += [nu, pb, od, c]
         self.h = C.c_void_p()
         self.tsa.check(self.L.tsa_test_dgcore_open(C.byref(c), od, len(order), C.byref(self.h)))
         self.keys = sum(n_units)
         self.names = self.L.tsa_test_dgcore_counter_names().decode().split()
 
-    def token(self, ids):
+    def token(self, ids, run=None):
         x = np.ascontiguousarray(ids, dtype=np.uint32)
         table = np.zeros(self.keys, dtype=np.int32)
         counts = np.zeros(len(self.names), dtype=np.uint64)
-        self.tsa.check(self.L.tsa_test_dgcore_token(self.h, x.ctypes.data_as(C.POINTER(u32)), x.shape[1],
-                                                    table.ctypes.data_as(C.POINTER(C.c_int32)),
-                                                    counts.ctypes.data_as(C.POINTER(u64)), len(self.names)))
+        rv = (C.c_uint8 * x.shape[0])(*run) if run is not None else None
+        self.tsa.check(self.L.tsa_test_dgcore_token_run(self.h, x.ctypes.data_as(C.POINTER(u32)), x.shape[1], rv,
+                                                        table.ctypes.data_as(C.POINTER(C.c_int32)),
+                                                        counts.ctypes.data_as(C.POINTER(u64)), len(self.names)))
         return table, {k: int(v) for k, v in zip(self.names, counts)}
+
+    def set_policy(self, policy):
+        self.tsa.check(self.L.tsa_test_dgcore_set_policy(self.h, policy))
 
     def host_order(self):
         out = np.zeros(self.keys, dtype=np.uint32)
@@ -137,20 +156,53 @@ def _case(seed, three):
                 parts=parts, order=order, wb_defer=wb_defer, inclusive=inclusive, disk=disk, routes=routes)
 
 
-def _run(seed, three):
+def _score(seed, n_units, policy=None):
+    """Scored eviction options drawn per seed: SCORED or SCORED_AUTO, default or random weights (summing to 1000),
+    1-3 verify rows per boundary (AUTO ranks only above one), and sometimes starting counts, a few cells saturated so
+    that increments are dropped."""
+    rng = np.random.default_rng(seed + 77)
+    pol = policy if policy is not None else int(rng.integers(1, 3))
+    if rng.integers(0, 2):
+        a, b = sorted(int(x) for x in rng.integers(0, 1001, size=2))
+        w = (a, b - a, 1000 - b)
+    else:
+        w = (700, 200, 100)
+    rows = int(rng.integers(1, 4))
+    cells = None
+    if rng.integers(0, 3) == 0:
+        cells = []
+        for n in n_units:
+            t = rng.integers(0, 50, size=n * n).astype(np.uint64)
+            hot = rng.random(n * n) < 0.05
+            t[hot] = 0xFFFFFFFF
+            cells += [int(v) for v in t]
+    return dict(policy=pol, w=w, rows=rows, cells=cells)
+
+
+def _run(seed, three, score=None, switch=None, partial=False):
+    """switch: (token, policy) - both cores switch policy between tokens there. partial: each token exports a random
+    nonempty subset of the gated layers (ss_begin's rows), the others keep their state."""
     if not ref.available():
         pytest.skip("oracle/_ref (the reference core) is not built")
     c = _case(seed, three)
     kw = dict(wb_defer=c["wb_defer"], inclusive=c["inclusive"])
     ours = OurCore(c["n_units"], c["persistent"], c["bank"], c["blocks"], c["spare_target"], c["parts"], c["order"],
-                   disk=c["disk"], **kw)
+                   disk=c["disk"], score=score, **kw)
     theirs = ref.RefDg(c["n_units"], c["persistent"], c["bank"], c["blocks"], c["spare_target"], c["parts"],
-                       c["order"], disk=c["disk"], **kw)
+                       c["order"], disk=c["disk"], score=score, **kw)
     seen = {}
+    rng = np.random.default_rng(seed + 5)
     try:
         for t, ids in enumerate(c["routes"]):
-            got_t, got = ours.token(ids)
-            want_t, want = theirs.token(ids)
+            if switch and t == switch[0]:
+                ours.set_policy(switch[1])
+                theirs.set_policy(switch[1])
+            run = None
+            if partial:
+                run = [int(v) for v in rng.integers(0, 2, size=ids.shape[0])]
+                run[int(rng.integers(0, ids.shape[0]))] = 1
+            got_t, got = ours.token(ids, run)
+            want_t, want = theirs.token(ids, run=run)
             assert np.array_equal(got_t, want_t), (seed, t, "table")
             for k, v in got.items():
                 assert v == want[k], (seed, t, k, v, want[k])
@@ -189,3 +241,90 @@ def test_cases_exercise_the_paths():
         assert tot2[k] > 0, k
     for k in ("disk_reads", "disk_drops", "disk_discards", "clean_drops", "writebacks_done", "bank_serves"):
         assert tot3[k] > 0, k
+
+
+@pytest.mark.parametrize("seed", range(120))
+def test_scored_two_tier_matches_reference(seed):
+    """Scored eviction (SCORED / SCORED_AUTO): victims lowest (score, demand epoch, recency stamp) first from the
+    transition counts, the 16-union window and the recency term, through the same acceptance loop as LRU."""
+    c = _case(2000 + seed, False)
+    _run(2000 + seed, False, score=_score(seed, c["n_units"]))
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_scored_three_tier_matches_reference(seed):
+    c = _case(3000 + seed, True)
+    _run(3000 + seed, True, score=_score(seed, c["n_units"]))
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_policy_switch_matches_reference(seed):
+    """ss_dg_set_policy between tokens: drained, the learning reset to the open counts, stamps renumbered in recency
+    order; placement and recency kept. Both directions and AUTO."""
+    c = _case(4000 + seed, bool(seed % 2))
+    rng = np.random.default_rng(seed)
+    sc = _score(seed, c["n_units"])
+    _run(4000 + seed, bool(seed % 2), score=sc, switch=(int(rng.integers(3, 12)), int(rng.integers(0, 3))))
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_partial_exports_match_reference(seed):
+    """Tokens that export only some gated layers (ss_begin's rows): LRU, and scored, where a layer left out scores
+    from its older history at the boundary."""
+    c = _case(6000 + seed, bool(seed % 3 == 0))
+    score = _score(seed, c["n_units"]) if seed % 2 else None
+    _run(6000 + seed, bool(seed % 3 == 0), score=score, partial=True)
+
+
+def test_lru_open_refuses_a_switch_to_scoring():
+    if not ref.available():
+        pytest.skip("oracle/_ref (the reference core) is not built")
+    c = _case(5, False)
+    ours = OurCore(c["n_units"], c["persistent"], c["bank"], c["blocks"], c["spare_target"], c["parts"], c["order"],
+                   wb_defer=1, inclusive=0)
+    theirs = ref.RefDg(c["n_units"], c["persistent"], c["bank"], c["blocks"], c["spare_target"], c["parts"],
+                       c["order"])
+    try:
+        with pytest.raises(Exception):
+            ours.set_policy(1)
+        with pytest.raises(RuntimeError):
+            theirs.set_policy(1)
+        ours.set_policy(0)  # LRU to LRU is allowed
+        theirs.set_policy(0)
+    finally:
+        ours.close()
+        theirs.close()
+
+
+def test_scored_cases_choose_other_victims_than_lru():
+    """The scored runs are not LRU in disguise: over the seeds, scored victims are taken, some transition cells
+    saturate, and for some seeds the slot tables after a token differ from the same run under LRU (with AUTO at one
+    row they never do)."""
+    if not ref.available():
+        pytest.skip("oracle/_ref (the reference core) is not built")
+    differ = victims = saturated = 0
+    for seed in range(30):
+        c = _case(2000 + seed, False)
+        sc = _score(seed, c["n_units"], policy=1)
+        kw = dict(wb_defer=c["wb_defer"], inclusive=c["inclusive"])
+        a = ref.RefDg(c["n_units"], c["persistent"], c["bank"], c["blocks"], c["spare_target"], c["parts"],
+                      c["order"], score=sc, **kw)
+        b = ref.RefDg(c["n_units"], c["persistent"], c["bank"], c["blocks"], c["spare_target"], c["parts"],
+                      c["order"], **kw)
+        auto = ref.RefDg(c["n_units"], c["persistent"], c["bank"], c["blocks"], c["spare_target"], c["parts"],
+                         c["order"], score=dict(sc, policy=2, rows=1), **kw)
+        try:
+            for ids in c["routes"]:
+                ta, ca = a.token(ids)
+                tb, _ = b.token(ids)
+                tc, cc = auto.token(ids)
+                differ += int(not np.array_equal(ta, tb))
+                assert np.array_equal(tb, tc)
+                assert cc["scored_victims"] == 0
+            victims += ca["scored_victims"]
+            saturated += ca["score_saturated"]
+        finally:
+            a.close()
+            b.close()
+            auto.close()
+    assert victims > 0 and differ > 0 and saturated > 0

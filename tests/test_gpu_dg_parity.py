@@ -5,13 +5,14 @@ token the slot table and the cache counters must be identical, and every routed 
 ss_dg_slot must checksum to the oracle's value of the file bytes. Device verify (verify_hash = 2) re-hashes every
 landed unit in HBM. Shapes: the mixtral workload at test size (reference tests/test_dg_cuda.cu:297-323 drives the
 same protocol)."""
+import ctypes
 import json
 import os
 
 import numpy as np
 import pytest
 
-from oracle import fixtures, ref
+from oracle import fixtures, ref, score_profile
 from tierstream_amd import ss
 
 pytestmark = pytest.mark.gpu
@@ -61,7 +62,29 @@ CASES = {
     # not queue behind the spinning wait kernel
     "direct-launch": dict(layers=4, units=8, parts=[64 * KiB] * 3, n_res=12, dyn=1, spares=6, n_ids=2, tokens=12,
                           graph=False),
+    # scored eviction: victims lowest score first (learned online; from a TSSCPRF1 profile bound to the descriptor's
+    # hashes, a few cells saturated; with other weights), SCORED_AUTO over two-row boundaries, and a switch of policy
+    # between tokens (ss_dg_set_policy)
+    "scored": dict(layers=4, units=16, parts=[64 * KiB] * 3, n_res=24, dyn=2, spares=12, n_ids=4, tokens=32,
+                   score=dict(policy=1)),
+    "scored-profile": dict(layers=4, units=16, parts=[64 * KiB] * 3, n_res=24, dyn=2, spares=12, n_ids=4, tokens=24,
+                           score=dict(policy=1, w=(500, 300, 200), profile=True)),
+    "scored-auto-rows": dict(layers=3, units=16, parts=[32 * KiB, 32 * KiB, 64 * KiB], n_res=16, dyn=2, spares=10,
+                             n_ids=4, tokens=24, score=dict(policy=2, rows=2)),
+    "scored-switch": dict(layers=4, units=16, parts=[64 * KiB] * 3, n_res=24, dyn=2, spares=12, n_ids=4, tokens=30,
+                          score=dict(policy=1, switch=[(10, 0), (20, 2)])),
 }
+SCORE_COUNTERS = ["score_fallbacks", "scored_victims", "score_layers", "score_candidates", "score_saturated"]
+
+
+def _profile_cells(units, layers, seed=9):
+    rng = np.random.default_rng(seed)
+    cells = []
+    for _ in range(layers):
+        t = rng.integers(0, 200, size=units * units).astype(np.uint64)
+        t[rng.random(units * units) < 0.03] = 0xFFFFFFFF
+        cells.append([int(v) for v in t])
+    return cells
 
 
 @pytest.mark.parametrize("name", list(CASES))
@@ -70,8 +93,22 @@ def test_dg_matches_reference(name, tmp_path, gpu):
     tokens = c.pop("tokens")
     zipf = c.pop("zipf", True)
     use_graph = c.pop("graph", True)
+    score = dict(c.pop("score", {}))
     m, bkw, okw = _setup(tmp_path, c["layers"], c["units"], c["parts"], c["n_res"], c["dyn"], c["spares"], c["n_ids"],
                          inclusive=c.get("inclusive", 0), wb_defer=c.get("wb_defer", 1))
+    ref_score, keep = None, []
+    if score:
+        w = score.get("w", (700, 200, 100))
+        okw.update(policy=score["policy"], dg_score_w_trans=w[0], dg_score_w_freq=w[1], dg_score_w_recency=w[2])
+        ref_score = dict(policy=score["policy"], w=w, rows=score.get("rows", 1))
+        if score.get("profile"):
+            cells = _profile_cells(c["units"], c["layers"])
+            blob = score_profile.write([c["units"]] * c["layers"], score_profile.model_identity(m), b"test fit",
+                                       cells)
+            buf = ctypes.create_string_buffer(blob, len(blob))
+            keep.append(buf)
+            okw.update(dg_score_profile=ctypes.cast(buf, ctypes.c_void_p), dg_score_profile_len=len(blob))
+            ref_score["cells"] = [v for layer in cells for v in layer]
     routes = _routes(c["layers"], c["units"], c["n_ids"], tokens, seed=5, zipf=zipf)
     d = ss.Desc(m.desc_json())
     plan = ss.Plan(d, ss.budget(**bkw))
@@ -86,34 +123,51 @@ def test_dg_matches_reference(name, tmp_path, gpu):
     D = sum(min(c["dyn"], sum(1 for u in range(c["units"]) if tiers[L][u] != 0)) for L in range(c["layers"]))
     keys = c["layers"] * c["units"]
     refdg = ref.RefDg([c["units"]] * c["layers"], R + D, c["n_ids"], P + Q, D, c["parts"],
-                      residents + list(range(keys)), wb_defer=c.get("wb_defer", 1), inclusive=c.get("inclusive", 0))
+                      residents + list(range(keys)), wb_defer=c.get("wb_defer", 1), inclusive=c.get("inclusive", 0),
+                      score=ref_score)
     ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(**okw))
     eng = ss.DgEngine(ctx, c["n_ids"], use_graph=use_graph)
+    if score.get("rows", 1) > 1:
+        eng.set_rows(score["rows"])
+    switch = dict(score.get("switch", []))
+    policy = score.get("policy", 0)
+    counters = COUNTERS + (SCORE_COUNTERS if score else [])
     expect = {(L, u): fixtures.engine_checksum(m.unit_data(L, u)) for L in range(c["layers"]) for u in range(c["units"])}
     with pytest.raises(ss.SsError):  # arms the stats snapshot: each token's boundary publishes from now on
         ctx.snapshot()
     try:
         for t in range(tokens):
+            if t in switch:
+                policy = switch[t]
+                ctx.dg_set_policy(policy)
+                refdg.set_policy(policy)
             cks, _ = eng.token(routes[t])
             want_table, want = refdg.token(routes[t].astype(np.uint32))
             got = ctx.dg_stats()
             assert np.array_equal(ctx.dg_table(), want_table), (name, t)
-            for k in COUNTERS:
+            for k in counters:
                 assert got[k] == want[k], (name, t, k, got[k], want[k])
             for L in range(c["layers"]):
                 for i, u in enumerate(routes[t, L]):
                     assert int(cks[L, i]) == expect[(L, int(u))], (name, t, L, i)
         assert got["tokens"] == tokens and got["misses"] > 0
-        _check_stats_doc(ctx, want, tokens)
+        if score and score["policy"] == 1:
+            assert got["scored_victims"] > 0 and got["score_fallbacks"] == 0
+        if score.get("profile"):
+            assert got["score_saturated"] > 0
+        _check_stats_doc(ctx, want, tokens, policy=["lru", "scored", "auto"][policy],
+                         prov="test fit" if score.get("profile") else None, publications=tokens + len(switch))
     finally:
         eng.close()
         ctx.close()
         refdg.close()
 
 
-def _check_stats_doc(ctx, want, tokens):
+def _check_stats_doc(ctx, want, tokens, policy="lru", prov=None, publications=None):
     """The exclusive counters (reference src/dg_ctx.cpp:1081-1091, since open) from the reference core's counters, the
-    stats-v1 document (reference src/dg_ctx.cpp:1359-1545) and the snapshot published at the last boundary."""
+    stats-v1 document (reference src/dg_ctx.cpp:1359-1545) and the snapshot published at the last boundary. Every
+    boundary publishes, and so does a policy switch (its drain's counters; reference src/dg_ctx.cpp:628, :1573-1584):
+    publications counts them (default: one per token)."""
     x = ctx.exclusive_stats()
     assert x["writebacks"] == want["evicted"] - want["wb_cancelled"] - want["inclusive_drops"] - want["disk_discards"]
     assert x["writeback_bytes"] == want["wb_issued_bytes"]
@@ -129,14 +183,18 @@ def _check_stats_doc(ctx, want, tokens):
             assert "three_tier" not in g or g["three_tier"][k] == st[k], k
         else:
             assert g[k] == st[k], k
-    assert g["policy"] == "lru" and g["landing_issued"] == 0 and g["pf_legacy"] == 1
+    assert g["policy"] == policy and g["landing_issued"] == 0 and g["pf_legacy"] == 1
+    assert g.get("score_profile") == prov
+    for k in SCORE_COUNTERS:
+        assert g[k] == st[k], k
     for k in ("writebacks", "writeback_bytes", "promoted", "free_blocks", "min_free_blocks"):
         assert doc["exclusive"][k] == x[k], k
     tot = ctx.stats_total()
     assert {k: v for k, v in doc["total"].items()} == tot
     assert sum(1 for _ in doc["layers"]) == len(doc["layers"]) and doc["layers"][0].keys() == tot.keys()
     stot, info = ctx.snapshot()
-    assert stot == tot and info["sequence"] == tokens and info["forwards"] == tokens and info["flags"] == 2
+    seq = tokens if publications is None else publications
+    assert stot == tot and info["sequence"] == seq and info["forwards"] == tokens and info["flags"] == 2
     assert info["exclusive_writebacks"] == x["writebacks"] and info["exclusive_blocks"] == doc["exclusive"]["blocks"]
     assert ctx.snapshot_json() == text
 

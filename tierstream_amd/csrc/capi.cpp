@@ -422,6 +422,12 @@ ss_status ss_dg_residency(ss_ctx* c, ss_dg_unit* out, uint32_t cap, uint32_t* to
 ss_status ss_dg_set_budgets(ss_ctx* c, uint32_t spare_target, uint32_t per_layer, uint32_t per_token) {
   return ctx_guard(c, [&] { dg_of(c, "ss_dg_set_budgets").set_budgets(spare_target, per_layer, per_token); });
 }
+ss_status ss_dg_end_rows(ss_ctx* c, uint32_t rows) {
+  return ctx_guard(c, [&] { dg_of(c, "ss_dg_end_rows").end(rows); });
+}
+ss_status ss_dg_set_policy(ss_ctx* c, ss_policy policy) {
+  return ctx_guard(c, [&] { dg_of(c, "ss_dg_set_policy").set_policy(policy); });
+}
 ss_status ss_stats_dg_sized(const ss_ctx* c, ss_dg_stats* out, uint32_t size) {
   return guard([&] {
     need(c && out, "ss_stats_dg: null argument");

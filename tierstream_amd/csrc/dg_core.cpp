@@ -1,6 +1,7 @@
 #include "dg_core.hpp"
 
 #include <algorithm>
+#include <chrono>
 #include <string>
 
 #include "common.hpp"
@@ -30,6 +31,7 @@ DgCore::DgCore(const DgConfig& cfg, DgTransport* t) : c_(cfg), t_(t) {
   bank_key_.assign(2u * size_t(c_.bank_slots), kNone);
   pf_layer_.assign(gated(), 0);
   layer_missed_.assign(gated(), 0);
+  run_.assign(gated(), 1);
   lc_.assign(gated(), DgLayerCounts{});
   slot_ev_.assign(slots_, nullptr);
   block_ev_.assign(c_.blocks, nullptr);
@@ -47,6 +49,27 @@ DgCore::DgCore(const DgConfig& cfg, DgTransport* t) : c_(cfg), t_(t) {
     layer_bytes_ = c_.wb_layer_bytes ? c_.wb_layer_bytes : t_->part_bytes(0);
     max_outstanding_ = c_.wb_max_outstanding ? c_.wb_max_outstanding : 2 * unit_bytes_;
     if (c_.wb_on_d2h) post_ready_ev_ = event();
+  }
+  if (c_.scored) {  // every table now: the service never allocates
+    require(c_.w_trans <= 1000 && c_.w_freq <= 1000 && c_.w_rec <= 1000 && c_.w_trans + c_.w_freq + c_.w_rec == 1000,
+            SS_E_INVALID, "device-gated: score weights must each be 0..1000 and sum to 1000");
+    require(c_.max_ids >= 1 && c_.max_ids <= 64, SS_E_INVALID, "device-gated: score unions need max ids 1..64");
+    sc_.resize(gated());
+    for (uint32_t g = 0; g < gated(); ++g) {
+      const size_t n = units(g);
+      require(n <= kScoreMaxUnits, SS_E_INVALID,
+              "device-gated: scored eviction needs at most 65536 units per gated layer (gated layer " +
+                  std::to_string(g) + " has " + std::to_string(n) + ")");
+      LayerScore& l = sc_[g];
+      l.T.assign(n * n, 0u);
+      l.rowsum.assign(n, 0);
+      l.cnt.assign(n, 0);
+      l.ring.assign(size_t(kScoreWindow) * c_.max_ids, 0u);
+      l.ring_len.assign(kScoreWindow, 0);
+      l.prev.reserve(c_.max_ids);
+      l.cur.reserve(c_.max_ids);
+    }
+    heap_.reserve(c_.persistent_slots);
   }
   victims_.reserve(c_.persistent_slots);
 }
@@ -173,6 +196,7 @@ void DgCore::place(const std::vector<uint32_t>& priority, const std::vector<uint
   free_blocks_.clear();
   for (uint32_t s = c_.persistent_slots; s-- > dev0;) free_slots_.push_back(int32_t(s));  // lowest on top
   for (int32_t b = int32_t(c_.blocks); b-- > next_block;) free_blocks_.push_back(b);
+  open_stamp_ = stamp_;
 }
 
 void DgCore::unlink(uint32_t k) {
@@ -194,6 +218,10 @@ void DgCore::push_front(uint32_t k) {
   else tail_ = k;
   head_ = k;
   x.in_list = true;
+  if (c_.scored) {  // begin_token keeps the counter below kStampLimit, so this never wraps
+    if (stamp_ == UINT64_MAX) broken("the recency stamp counter wrapped");
+    x.stamp = ++stamp_;
+  }
 }
 
 std::vector<uint32_t> DgCore::residency() const {
@@ -394,7 +422,16 @@ int32_t DgCore::take_stage() {
   return int32_t(c_.blocks + i);
 }
 
-void DgCore::begin_token(uint32_t seq) {
+void DgCore::begin_token(uint32_t seq, const std::vector<uint8_t>* run) {
+  require(!run || run->size() == gated(), SS_E_INVALID, "device-gated: the exported layers do not cover the gated layers");
+  if (c_.scored) {  // this token's epoch (the first is 1); one token pushes far fewer than 2^40 stamps
+    require(stamp_ <= kStampLimit, SS_E_BACKEND,
+            "device-gated: the scored eviction's recency stamp counter is exhausted (reopen the context)");
+    require(epoch_ < (uint64_t(1) << 63), SS_E_BACKEND, "device-gated: the scored eviction's epoch counter is exhausted");
+    ++epoch_;
+  }
+  if (run) std::copy(run->begin(), run->end(), run_.begin());
+  else std::fill(run_.begin(), run_.end(), uint8_t(1));
   seq_ = seq;
   pf_token_ = 0;
   std::fill(pf_layer_.begin(), pf_layer_.end(), 0u);
@@ -553,6 +590,7 @@ void DgCore::use(uint32_t g, uint32_t unit, bool was_miss) {
       ++st_.miss_layers;
     }
   }
+  if (c_.scored) x.demand_epoch = epoch_;  // demand uses only: prefetches and resurrections leave it
   if (x.via_prefetch && !x.used) {
     x.used = true;
     ++st_.prefetch_used;
@@ -589,6 +627,7 @@ void DgCore::serve_use(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mas
   uniq_.assign(ids, ids + n);
   std::sort(uniq_.begin(), uniq_.end());
   uniq_.erase(std::unique(uniq_.begin(), uniq_.end()), uniq_.end());
+  if (c_.scored) score_history(g);
   for (uint32_t id : uniq_) {
     bool miss = false;
     for (uint32_t i = 0; i < n; ++i)
@@ -617,7 +656,7 @@ void DgCore::serve_prediction(uint32_t g_next, const uint32_t* pred, uint32_t n)
   for (uint32_t id : pred_) fetch(g_next, id, true);
 }
 
-void DgCore::end_token() {
+void DgCore::end_token(uint32_t rows) {
   // every copy and entry write of the token has landed before anything changes home
   t_->sync(DgTransport::kDem);
   t_->sync(DgTransport::kPf);
@@ -659,52 +698,41 @@ void DgCore::end_token() {
   bank_seq_[0] = bank_seq_[1] = 0;
   bank_layer_[0] = bank_layer_[1] = kNone;
   collect();
-  // victims from the recency tail until free + pending + accepted = the spare target; the first victim without a
-  // free block stops the walk (it stays on the device)
+  // victims until free + pending + accepted = the spare target, from the recency tail or (scored) lowest score
+  // first; the first victim without a free block ends the acceptance (it stays on the device)
   size_t pending = deferred_.size();
   for (const Writeback& w : wbs_) pending += w.discard ? 0u : 1u;
   const size_t base = free_slots_.size() + pending;
   victims_.clear();
   size_t got = 0;
-  for (uint32_t k = tail_; k != kNone && base + got < c_.spare_target;) {
-    const uint32_t prev = e_[k].prev;
-    Entry& x = e_[k];
-    if (x.home == Home::Device && !x.wb_pending) {
-      // a clean copy (its block is its home again), or three-tier with no block to write into after the least
-      // recently homed pinned unit was offered (clean_evict: not even that): its file. No copy either way.
-      const bool clean = !x.backed && clean_now();
-      if (x.backed || clean || (free_blocks_.empty() && !drop_host_lru() && c_.disk_tier)) {
-        if (x.backed) ++st_.inclusive_drops;
-        else ++st_.disk_discards;
-        if (clean) {
-          ++st_.clean_drops;
-          st_.clean_drop_bytes += unit_bytes_;
-        }
-        unlink(k);
-        --on_device_;
-        free_slots_.push_back(x.slot);
-        to_lower(k);
-        table_[k] = -1;
-        ++st_.evicted;
-        ++lc_[gated_of(k)].evicted;
-        ++got;
-      } else if (free_blocks_.empty()) {
-        ++st_.evict_short;
-        break;
-      } else {
-        const int32_t b = free_blocks_.back();
-        free_blocks_.pop_back();
-        unlink(k);
-        --on_device_;
-        x.home = Home::Evicting;
-        x.block = b;
-        x.wb_pending = true;
-        table_[k] = -1;
-        victims_.push_back(k);
+  bool by_score = c_.scored && (!c_.scored_auto || rows > 1);
+  if (by_score) {  // every exported layer's union is this token's (a layer left out scores from its older history)
+    bool fresh = true;
+    for (uint32_t g = 0; g < gated(); ++g) fresh = fresh && (!run_[g] || sc_[g].served == epoch_);
+    if (!fresh) {
+      ++st_.score_fallbacks;
+      by_score = false;
+    }
+  }
+  if (by_score) {
+    const auto t0 = std::chrono::steady_clock::now();
+    select_scored(c_.spare_target > base ? c_.spare_target - base : 0);
+    for (const Cand& cd : heap_) {
+      if (!accept_victim(cd.key)) break;
+      ++got;
+      ++st_.scored_victims;
+    }
+    st_.score_ns += uint64_t(
+        std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - t0).count());
+  } else {
+    for (uint32_t k = tail_; k != kNone && base + got < c_.spare_target;) {
+      const uint32_t prev = e_[k].prev;
+      if (eligible(k)) {
+        if (!accept_victim(k)) break;
         ++got;
       }
+      k = prev;
     }
-    k = prev;
   }
   const size_t n_evict = victims_.size();
   t_->upload_table(table_.data(), keys_);  // the device table = the mirror, before any write-back is enqueued
@@ -740,6 +768,173 @@ void DgCore::end_token() {
   }
   sweep_events();
   ++st_.tokens;
+}
+
+bool DgCore::accept_victim(uint32_t k) {
+  Entry& x = e_[k];
+  // a clean copy (its block is its home again), or three-tier with no block to write into after the least recently
+  // homed pinned unit was offered (clean_evict: not even that): its file. No copy either way.
+  const bool clean = !x.backed && clean_now();
+  if (x.backed || clean || (free_blocks_.empty() && !drop_host_lru() && c_.disk_tier)) {
+    if (x.backed) ++st_.inclusive_drops;
+    else ++st_.disk_discards;
+    if (clean) {
+      ++st_.clean_drops;
+      st_.clean_drop_bytes += unit_bytes_;
+    }
+    unlink(k);
+    --on_device_;
+    free_slots_.push_back(x.slot);
+    to_lower(k);
+    table_[k] = -1;
+    ++st_.evicted;
+    ++lc_[gated_of(k)].evicted;
+    return true;
+  }
+  if (free_blocks_.empty()) {
+    ++st_.evict_short;
+    return false;
+  }
+  const int32_t b = free_blocks_.back();
+  free_blocks_.pop_back();
+  unlink(k);
+  --on_device_;
+  x.home = Home::Evicting;
+  x.block = b;
+  x.wb_pending = true;
+  table_[k] = -1;
+  victims_.push_back(k);
+  return true;
+}
+
+// Layer g's sorted unique union (uniq_) becomes this token's: every cell (r in the previous token's union, e in this
+// one) takes one saturating increment and its row sum with it; the union enters the ring of the last kScoreWindow
+// unions (the oldest leaves it, the per-unit counts follow) and becomes the previous one.
+void DgCore::score_history(uint32_t g) {
+  LayerScore& l = sc_[g];
+  const uint32_t n = units(g);
+  require(uniq_.size() <= c_.max_ids, SS_E_BACKEND, "device-gated: a score union above max ids");
+  l.cur.assign(uniq_.begin(), uniq_.end());
+  l.served = epoch_;
+  for (uint32_t r : l.prev) {
+    uint32_t* row = l.T.data() + size_t(r) * n;
+    uint64_t added = 0;
+    for (uint32_t e : l.cur) {
+      if (row[e] == UINT32_MAX) {
+        ++st_.score_saturated;
+      } else {
+        ++row[e];
+        ++added;
+      }
+    }
+    l.rowsum[r] += added;
+  }
+  if (l.ring_n == kScoreWindow) {
+    const uint32_t* old = l.ring.data() + size_t(l.ring_head) * c_.max_ids;
+    for (uint32_t i = 0; i < l.ring_len[l.ring_head]; ++i) --l.cnt[old[i]];
+    l.ring_head = (l.ring_head + 1) % kScoreWindow;
+    --l.ring_n;
+  }
+  const uint32_t at = (l.ring_head + l.ring_n) % kScoreWindow;
+  std::copy(l.cur.begin(), l.cur.end(), l.ring.begin() + ptrdiff_t(size_t(at) * c_.max_ids));
+  l.ring_len[at] = uint8_t(l.cur.size());
+  ++l.ring_n;
+  for (uint32_t e : l.cur) ++l.cnt[e];
+  l.prev.assign(l.cur.begin(), l.cur.end());
+}
+
+// Unit u of layer g, with cur = this token's union of g and denom = the sum of its rows' sums:
+//   N = sum_{r in cur} T[r][u], P = ((|cur| N) << 16) / max(1, denom), F = (cnt[u] << 16) / kScoreWindow,
+//   Rec = (1 << 16) / (1 + epoch - demand_epoch), S = w_t P + w_f F + w_r Rec
+// in unsigned integers with floor division. With at most 65536 units and 64 ids, N < 2^38 and denom < 2^54, so
+// (|cur| N) << 16 < 2^60; N <= denom bounds P by 2^22 and S below 2^33. Every term is nonnegative: when the F + Rec part alone does not order before
+// `cutoff` the transition rows are not read (the result then orders after the cutoff anyway).
+DgCore::Cand DgCore::score_of(uint32_t g, uint32_t u, uint64_t denom, const Cand* cutoff) const {
+  const LayerScore& l = sc_[g];
+  const Entry& x = e_[base_[g] + u];
+  const uint64_t F = (uint64_t(l.cnt[u]) << 16) / kScoreWindow;
+  const uint64_t R = (uint64_t(1) << 16) / (1 + (epoch_ - x.demand_epoch));
+  Cand cd{uint64_t(c_.w_freq) * F + uint64_t(c_.w_rec) * R, x.demand_epoch, x.stamp, base_[g] + u};
+  if (cutoff && !cand_less(cd, *cutoff)) return cd;
+  const uint32_t n = units(g);
+  uint64_t N = 0;
+  for (uint32_t r : l.cur) N += l.T[size_t(r) * n + u];
+  const uint64_t P = ((uint64_t(l.cur.size()) * N) << 16) / std::max<uint64_t>(1, denom);
+  cd.s += uint64_t(c_.w_trans) * P;
+  return cd;
+}
+
+// A max-heap (by the public order) of at most `need` candidates over every eligible key, then sorted ascending: the
+// victims are the `need` smallest (score, demand epoch, stamp), a total order since stamps are unique.
+void DgCore::select_scored(size_t need) {
+  heap_.clear();
+  for (uint32_t g = 0; need && g < gated(); ++g) {
+    const LayerScore& l = sc_[g];
+    uint64_t denom = 0;
+    for (uint32_t r : l.cur) denom += l.rowsum[r];
+    ++st_.score_layers;
+    for (uint32_t u = 0; u < units(g); ++u) {
+      if (!eligible(base_[g] + u)) continue;
+      ++st_.score_candidates;
+      const bool full = heap_.size() == need;
+      const Cand cd = score_of(g, u, denom, full ? &heap_.front() : nullptr);
+      if (!full) {
+        heap_.push_back(cd);
+        std::push_heap(heap_.begin(), heap_.end(), cand_less);
+      } else if (cand_less(cd, heap_.front())) {
+        std::pop_heap(heap_.begin(), heap_.end(), cand_less);
+        heap_.back() = cd;
+        std::push_heap(heap_.begin(), heap_.end(), cand_less);
+      }
+    }
+  }
+  std::sort_heap(heap_.begin(), heap_.end(), cand_less);
+}
+
+void DgCore::reset_score() {
+  for (uint32_t g = 0; g < uint32_t(sc_.size()); ++g) {
+    LayerScore& l = sc_[g];
+    const uint32_t n = units(g);
+    if (l.open_T.empty()) std::fill(l.T.begin(), l.T.end(), 0u);
+    else std::copy(l.open_T.begin(), l.open_T.end(), l.T.begin());
+    for (uint32_t r = 0; r < n; ++r) {
+      uint64_t sum = 0;
+      for (uint32_t e = 0; e < n && !l.open_T.empty(); ++e) sum += l.T[size_t(r) * n + e];
+      l.rowsum[r] = sum;
+    }
+    std::fill(l.cnt.begin(), l.cnt.end(), uint16_t(0));
+    std::fill(l.ring.begin(), l.ring.end(), 0u);
+    std::fill(l.ring_len.begin(), l.ring_len.end(), uint8_t(0));
+    l.ring_head = l.ring_n = 0;
+    l.prev.clear();
+    l.cur.clear();
+    l.served = 0;
+  }
+  epoch_ = 0;
+}
+
+void DgCore::load_counts(const unsigned char* p) {
+  require(c_.scored, SS_E_INVALID, "device-gated: starting score counts need policy SCORED or SCORED_AUTO");
+  for (uint32_t g = 0; g < gated(); ++g) {
+    LayerScore& l = sc_[g];
+    for (size_t i = 0; i < l.T.size(); ++i, p += 4)
+      l.T[i] = uint32_t(p[0]) | uint32_t(p[1]) << 8 | uint32_t(p[2]) << 16 | uint32_t(p[3]) << 24;
+    l.open_T = l.T;
+  }
+  reset_score();
+}
+
+void DgCore::set_policy(uint32_t policy) {
+  require(policy <= 2, SS_E_INVALID, "device-gated: policy must be LRU, SCORED or SCORED_AUTO");
+  require(!policy || !sc_.empty(), SS_E_INVALID, "device-gated: scoring must be provisioned at open");
+  drain();
+  collect();
+  c_.scored = policy != 0;
+  c_.scored_auto = policy == 2;
+  reset_score();
+  for (Entry& x : e_) x.demand_epoch = x.stamp = 0;
+  stamp_ = 0;
+  for (uint32_t k = tail_; k != kNone; k = e_[k].prev) e_[k].stamp = ++stamp_;  // the list's order, the head largest
 }
 
 void DgCore::drain() {
@@ -810,6 +1005,21 @@ void DgCore::check() const {
     for (uint32_t k = hhead_; k != kNone; k = e_[k].hnext)
       if (++n > keys_ || e_[k].home != Home::Host) broken("the pinned recency list");
     if (n != on_host_) broken("the pinned recency list's length");
+  }
+  if (c_.scored) {  // stamps fall strictly from the recency head; no epoch lies ahead of the token's
+    uint64_t last = UINT64_MAX;
+    for (uint32_t k = head_; k != kNone; k = e_[k].next) {
+      if (e_[k].stamp >= last || e_[k].stamp == 0 || e_[k].stamp > stamp_) broken("recency stamps");
+      last = e_[k].stamp;
+    }
+    for (uint32_t k = 0; k < keys_; ++k)
+      if (e_[k].demand_epoch > epoch_) broken("a demand epoch in the future");
+    for (const LayerScore& l : sc_) {
+      uint32_t in_ring = 0, counted = 0;
+      for (uint32_t i = 0; i < l.ring_n; ++i) in_ring += l.ring_len[(l.ring_head + i) % kScoreWindow];
+      for (uint16_t c : l.cnt) counted += c;
+      if (l.ring_n > kScoreWindow || in_ring != counted) broken("the score ring's counts");
+    }
   }
 }
 

@@ -3,7 +3,9 @@
 // resurrection, recency, the boundary's admissions, victims from the recency tail to the spare target, deferred
 // write-backs with a per-layer credit, the inclusive share of clean copies - are those of reference src/dg_core.cpp
 // (place :769-858, fetch_impl :1146-1368, serve_demand / serve_use / serve_prediction :1415-1634, end_token
-// :1636-1927, collect / write-back scheduling :961-1097) for its two-tier LRU configuration.
+// :1636-1927, collect / write-back scheduling :961-1097) for its two- and three-tier configurations, with LRU or
+// scored victims (score_history / select_scored / score_candidate :1929-2057, the boundary's one acceptance loop
+// :1775-1840, set_policy :2059-2071; the score and its order: reference docs/design.md:284-354).
 //
 // Schedule: this core asks its transport for completion (collect) only through done(), which the MI355X transport
 // answers after waiting for the event, and it never asks whether the device "ran ahead". Every decision is therefore
@@ -86,6 +88,13 @@ struct DgConfig {
   // a prefetch may read a file-homed unit.
   bool disk_tier = false, disk_prefetch = false, clean_evict = false;
   uint32_t home_blocks = 0, disk_staging = 0;
+  // Scored eviction (SS_POLICY_SCORED / SCORED_AUTO): the boundary takes its victims lowest score first instead of
+  // from the recency tail; every other decision is LRU's. Weights in thousandths (each 0..1000, sum 1000). max_ids:
+  // the ids of one export (a union's upper bound), 1..64. scored_auto: learn every token, but rank only at a boundary
+  // closing more than one verify row (end_token(rows > 1)); otherwise the recency tail.
+  bool scored = false, scored_auto = false;
+  uint32_t w_trans = 700, w_freq = 200, w_rec = 100;
+  uint32_t max_ids = 0;
 };
 
 struct DgCounts {  // the subset of ss_dg_stats this core counts
@@ -97,6 +106,11 @@ struct DgCounts {  // the subset of ss_dg_stats this core counts
   uint64_t wb_forced_wait_ns = 0, inclusive_kept = 0, inclusive_drops = 0;
   uint64_t disk_reads = 0, disk_read_bytes = 0, disk_stage_waits = 0, disk_drops = 0, disk_discards = 0;
   uint64_t clean_drops = 0, clean_drop_bytes = 0;
+  // scored eviction: boundaries that had to use the recency order (a gated layer not served this token: never expected
+  // under this core's one-export-per-layer service); victims taken in score order; layers and eligible keys the
+  // selection considered; transition increments lost to a saturated cell; selection time.
+  uint64_t score_fallbacks = 0, scored_victims = 0, score_layers = 0, score_candidates = 0, score_saturated = 0;
+  uint64_t score_ns = 0;
 };
 struct DgLayerCounts {
   uint64_t lookups = 0, misses = 0, fetched = 0, bank_serves = 0, prefetched = 0, prefetch_used = 0, evicted = 0;
@@ -140,17 +154,36 @@ class DgCore {
   const std::vector<DgLayerCounts>& layer_counts() const { return lc_; }
   std::vector<uint32_t> residency() const;  // device keys, most recent first
 
-  void begin_token(uint32_t seq);
+  // run: the gated layers this token exports (null: all); a layer left out keeps its score history unchanged
+  void begin_token(uint32_t seq, const std::vector<uint8_t>* run = nullptr);
   void serve_demand(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask);
   void serve_use(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask);
   void serve_prediction(uint32_t g_next, const uint32_t* pred, uint32_t n);
   void issue_writebacks(uint32_t g);  // the deferred write-back slice after layer g's service
-  void end_token();
+  void end_token(uint32_t rows = 1);  // rows: the verify rows the token closed (scored_auto ranks only above one)
   void drain();  // between tokens: every deferred write-back submitted, every stream synchronized
   void set_spare_target(uint32_t n);
   void set_prefetch_budget(uint32_t per_layer, uint32_t per_token);
   uint32_t spare_target() const { return c_.spare_target; }
   void check() const;  // ownership invariants (tests); throws SS_E_BACKEND naming the first broken rule
+
+  // ---- scored eviction ----
+  static constexpr uint32_t kScoreWindow = 16;       // unions in each layer's frequency ring
+  static constexpr uint32_t kScoreMaxUnits = 65536;  // units per gated layer (the integer bounds rest on it)
+  // Starting transition counts, at open (after place, before the first token): per gated layer units^2 uint32
+  // little-endian cells row-major [previous unit][unit], layers concatenated. They are also the state set_policy
+  // restores.
+  void load_counts(const unsigned char* cells);
+  // Between tokens: drains every write-back, switches LRU (0) / SCORED (1) / SCORED_AUTO (2), resets the learned
+  // state to the open counts (or zero) and every demand epoch, and renumbers the recency stamps in list order.
+  // Switching to scoring needs the tables, so an open under LRU refuses it.
+  void set_policy(uint32_t policy);
+  uint32_t policy() const { return c_.scored ? (c_.scored_auto ? 2u : 1u) : 0u; }
+  uint64_t epoch() const { return epoch_; }
+  uint64_t stamp_counter() const { return stamp_; }
+  void set_stamp_counter(uint64_t v) { stamp_ = v; }  // tests: start near the limit
+  // Past this the next token fails before it changes anything, so the stamp counter never wraps.
+  static constexpr uint64_t kStampLimit = UINT64_MAX - (uint64_t(1) << 40);
 
  private:
   static constexpr uint32_t kNone = 0xffffffffu;
@@ -162,7 +195,30 @@ class DgCore {
     void* pf_done = nullptr;
     uint32_t hprev = kNone, hnext = kNone;  // three-tier: the pinned homes' recency list
     bool in_hlist = false;
+    uint64_t demand_epoch = 0;  // scored: the token of its last demand use (0: none since open or a policy switch)
+    uint64_t stamp = 0;         // scored: its last push to the recency list (unique; larger = more recent)
   };
+  // Scored eviction, per gated layer: transition counts T[r][e] (saturating uint32, row-major) with exact row sums,
+  // the ring of the last kScoreWindow unions with per-unit counts over it, the previous and this token's union.
+  struct LayerScore {
+    std::vector<uint32_t> T, open_T;
+    std::vector<uint64_t> rowsum;
+    std::vector<uint16_t> cnt;
+    std::vector<uint32_t> ring;  // kScoreWindow rows of max_ids
+    std::vector<uint8_t> ring_len;
+    uint32_t ring_head = 0, ring_n = 0;
+    std::vector<uint32_t> prev, cur;
+    uint64_t served = 0;  // the token whose union cur holds
+  };
+  struct Cand {
+    uint64_t s, epoch, stamp;
+    uint32_t key;
+  };
+  static bool cand_less(const Cand& a, const Cand& b) {
+    if (a.s != b.s) return a.s < b.s;
+    if (a.epoch != b.epoch) return a.epoch < b.epoch;
+    return a.stamp < b.stamp;
+  }
   struct Writeback {
     uint32_t key;
     int32_t slot, block;
@@ -201,6 +257,13 @@ class DgCore {
   void attach(std::vector<void*>& where, int32_t i, void* ev);
   void detach(std::vector<void*>& where, int32_t i);
   void sweep_events();
+  void score_history(uint32_t g);  // serve_use: layer g's union into the counts, the ring and the previous union
+  // The `need` smallest eligible candidates of every gated layer, ascending, into heap_.
+  void select_scored(size_t need);
+  Cand score_of(uint32_t g, uint32_t u, uint64_t denom, const Cand* cutoff) const;
+  void reset_score();
+  bool eligible(uint32_t k) const { return e_[k].home == Home::Device && !e_[k].wb_pending; }
+  bool accept_victim(uint32_t k);  // the boundary's acceptance of one victim; false: no block for it (evict_short)
   bool on_device_or_coming(uint32_t g, uint32_t unit) const {
     const Home h = e_[key(g, unit)].home;
     return h == Home::Device || h == Home::Coming || h == Home::Bank;
@@ -227,13 +290,16 @@ class DgCore {
   void* post_ready_ev_ = nullptr;
   std::vector<uint32_t> pf_layer_;
   uint32_t pf_token_ = 0, seq_ = 0, pred_layer_ = kNone;
-  std::vector<uint8_t> layer_missed_;
+  std::vector<uint8_t> layer_missed_, run_;
   std::vector<uint32_t> pred_, uniq_, victims_;
   std::vector<void*> event_pool_, all_events_;
   std::vector<void*> slot_ev_, block_ev_;        // a write-back still copying out of the slot / into the block
   std::unordered_map<void*, int> ev_refs_;      // attachments of each such event
   DgCounts st_;
   std::vector<DgLayerCounts> lc_;
+  std::vector<LayerScore> sc_;  // scored: one per gated layer (empty under an LRU open)
+  std::vector<Cand> heap_;
+  uint64_t epoch_ = 0, stamp_ = 0, open_stamp_ = 0;
 };
 
 }  // namespace tsa

@@ -1,6 +1,7 @@
 // Test hooks over the device-gated cache state machine alone (include/tierstream_amd/tsa_test.h, tsa_test_dgcore_*):
 // this library's DgCore on an eager transport, the schedule the reference's CPU tests run its core on
 // (reference tests/test_dg.cpp:201), so placement compares with the reference core's token by token without a GPU.
+#include <algorithm>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -8,6 +9,8 @@
 
 #include "common.hpp"
 #include "dg_core.hpp"
+#include "score_profile.hpp"
+#include "sha256.hpp"
 #include "tierstream_amd/tsa_test.h"
 
 namespace tsa {
@@ -43,14 +46,15 @@ class EagerTransport final : public DgTransport {
 struct TestCore {
   std::unique_ptr<EagerTransport> t;
   std::unique_ptr<DgCore> core;
-  uint32_t seq = 0;
+  uint32_t seq = 0, rows = 1;
 };
 
 constexpr const char* kNames =
     "tokens lookups misses covered fetched prefetched prefetch_used resurrected bank_serves evicted evict_short "
     "writebacks_done miss_layers covered_waits wb_deferred wb_cancelled wb_forced wb_boundary_flushed wb_issued_bytes "
     "wb_cancelled_bytes inclusive_kept inclusive_drops free_slots free_blocks on_device backed_units disk_reads "
-    "disk_drops disk_discards clean_drops file_units";
+    "disk_drops disk_discards clean_drops file_units score_fallbacks scored_victims score_layers score_candidates "
+    "score_saturated";
 
 }  // namespace
 }  // namespace tsa
@@ -83,6 +87,14 @@ ss_status tsa_test_dgcore_open(const tsa_test_dgcore_config* cfg, const uint32_t
     c.home_blocks = cfg->home_blocks;
     c.disk_staging = cfg->disk_staging;
     c.clean_evict = cfg->clean_evict != 0;
+    require(cfg->policy <= 2, SS_E_INVALID, "tsa_test_dgcore_open: policy must be 0, 1 or 2");
+    c.scored = cfg->policy != 0;
+    c.scored_auto = cfg->policy == 2;
+    c.w_trans = cfg->w_trans;
+    c.w_freq = cfg->w_freq;
+    c.w_rec = cfg->w_rec;
+    c.max_ids = cfg->bank_slots;
+    r->rows = cfg->rows ? cfg->rows : 1;
     r->core = std::make_unique<DgCore>(c, r->t.get());
     std::vector<uint8_t> disk;
     if (c.disk_tier) {
@@ -90,6 +102,15 @@ ss_status tsa_test_dgcore_open(const tsa_test_dgcore_config* cfg, const uint32_t
       disk.assign(cfg->disk, cfg->disk + r->core->keys());
     }
     r->core->place(std::vector<uint32_t>(order, order + n_order), c.disk_tier ? &disk : nullptr);
+    if (cfg->score_cells) {
+      std::vector<unsigned char> le;
+      uint64_t cells = 0;
+      for (uint32_t g = 0; g < cfg->n_gated; ++g) cells += uint64_t(cfg->n_units[g]) * cfg->n_units[g];
+      le.resize(4 * cells);
+      for (uint64_t i = 0; i < cells; ++i)
+        for (int b = 0; b < 4; ++b) le[4 * i + b] = (unsigned char)(cfg->score_cells[i] >> (8 * b));
+      r->core->load_counts(le.data());
+    }
     r->core->check();
     *out = r.release();
   });
@@ -97,23 +118,33 @@ ss_status tsa_test_dgcore_open(const tsa_test_dgcore_config* cfg, const uint32_t
 
 ss_status tsa_test_dgcore_token(void* h, const uint32_t* ids, uint32_t n, int32_t* table_out, uint64_t* counts,
                                 uint32_t n_counts) {
+  return tsa_test_dgcore_token_run(h, ids, n, nullptr, table_out, counts, n_counts);
+}
+
+ss_status tsa_test_dgcore_token_run(void* h, const uint32_t* ids, uint32_t n, const uint8_t* run, int32_t* table_out,
+                                    uint64_t* counts, uint32_t n_counts) {
   return tsa::guard([&] {
     using namespace tsa;
     require(h && ids && n >= 1 && n <= 64, SS_E_INVALID, "tsa_test_dgcore_token: bad argument");
     auto* r = static_cast<TestCore*>(h);
     DgCore& c = *r->core;
     const uint32_t G = c.gated();
-    c.begin_token(++r->seq);
+    std::vector<uint8_t> rv(G, 1);
+    if (run) rv.assign(run, run + G);
+    c.begin_token(++r->seq, &rv);
     for (uint32_t g = 0; g < G; ++g) {
+      if (!rv[g]) continue;
       const uint32_t* x = ids + size_t(g) * n;
       uint64_t mask = 0;
       for (uint32_t i = 0; i < n; ++i)  // the export kernel: slot_of[unit_base[g] + id] < 0 at export time
         if (x[i] < c.units(g) && c.table()[c.key(g, x[i])] < 0) mask |= uint64_t(1) << i;
       c.serve_demand(g, x, n, mask);
       c.serve_use(g, x, n, mask);
-      if (c.deferred() && g + 1 < G) c.issue_writebacks(g);
+      uint32_t nx = g + 1;  // the next exported layer: no slice after the token's last one
+      while (nx < G && !rv[nx]) ++nx;
+      if (c.deferred() && nx < G) c.issue_writebacks(g);
     }
-    c.end_token();
+    c.end_token(r->rows);
     c.check();
     if (table_out) std::memcpy(table_out, c.table().data(), 4ull * c.keys());
     if (counts) {
@@ -124,7 +155,8 @@ ss_status tsa_test_dgcore_token(void* h, const uint32_t* ids, uint32_t n, int32_
                             s.wb_issued_bytes, s.wb_cancelled_bytes, s.inclusive_kept, s.inclusive_drops,
                             uint64_t(c.free_slots()), uint64_t(c.free_blocks()), uint64_t(c.on_device()),
                             uint64_t(c.backed_units()), s.disk_reads, s.disk_drops, s.disk_discards, s.clean_drops,
-                            uint64_t(c.file_units())};
+                            uint64_t(c.file_units()), s.score_fallbacks, s.scored_victims, s.score_layers,
+                            s.score_candidates, s.score_saturated};
       const uint32_t m = uint32_t(sizeof v / sizeof v[0]);
       std::memcpy(counts, v, 8ull * (n_counts < m ? n_counts : m));
     }
@@ -132,6 +164,38 @@ ss_status tsa_test_dgcore_token(void* h, const uint32_t* ids, uint32_t n, int32_
 }
 
 const char* tsa_test_dgcore_counter_names(void) { return tsa::kNames; }
+
+ss_status tsa_test_dgcore_set_policy(void* h, uint32_t policy) {
+  return tsa::guard([&] {
+    tsa::require(h != nullptr, SS_E_INVALID, "tsa_test_dgcore_set_policy: null handle");
+    auto* r = static_cast<tsa::TestCore*>(h);
+    r->core->set_policy(policy);
+    r->core->check();
+  });
+}
+
+ss_status tsa_test_sha256(const void* data, uint64_t n, unsigned char* out) {
+  return tsa::guard([&] {
+    tsa::require((data || n == 0) && out, SS_E_INVALID, "tsa_test_sha256: null argument");
+    const std::string d = tsa::sha256(data ? data : "", size_t(n));
+    std::memcpy(out, d.data(), 32);
+  });
+}
+
+ss_status tsa_test_score_profile_check(const void* data, uint64_t len, const uint32_t* units, uint32_t n_gated,
+                                       const unsigned char* identity, char* prov, uint32_t prov_cap) {
+  return tsa::guard([&] {
+    tsa::require((units || n_gated == 0) && identity, SS_E_INVALID, "tsa_test_score_profile_check: null argument");
+    const tsa::ScoreProfile v = tsa::check_score_profile(
+        data, len, std::vector<uint32_t>(units, units + n_gated),
+        std::string(reinterpret_cast<const char*>(identity), 32));
+    if (prov && prov_cap) {
+      const size_t n = std::min<size_t>(v.provenance.size(), prov_cap - 1);
+      std::memcpy(prov, v.provenance.data(), n);
+      prov[n] = '\0';
+    }
+  });
+}
 
 uint32_t tsa_test_dgcore_host_order(void* h, uint32_t* out, uint32_t cap) {
   if (!h) return 0;

@@ -19,6 +19,7 @@
 #include "dg_core.hpp"
 #include "dg_proto.hpp"
 #include "hip_rt.hpp"
+#include "score_profile.hpp"
 #include "source.hpp"
 #include "stats_json.hpp"
 #include "tsa_device.hpp"
@@ -50,6 +51,10 @@ struct Layout {
   bool disk_tier = false, disk_prefetch = false;
   uint32_t F = 0, S = 0, disk_queue = 0;
   std::vector<uint8_t> disk;
+  // scored eviction: the weights (all three 0 in the options: 700 / 200 / 100) and the profile's model identity
+  bool scored = false;
+  uint32_t w_trans = 700, w_freq = 200, w_rec = 100;
+  std::string score_identity;
 };
 
 Layout make_layout(const Desc& d, const Plan& p, const ss_options& o) {
@@ -57,9 +62,10 @@ Layout make_layout(const Desc& d, const Plan& p, const ss_options& o) {
   const ss_budget& b = p.budget;
   if (b.tier_mode != SS_TIER_MODE_EXCLUSIVE) refuse(SS_E_INVALID, "needs tier_mode EXCLUSIVE");
   if (b.pinned_backing) refuse(SS_E_INVALID, "pinned_backing is refused (each unit has one home)");
-  if (o.policy == SS_POLICY_SCORED || o.policy == SS_POLICY_SCORED_AUTO)
-    refuse(SS_E_UNSUPPORTED, "scored eviction is not part of this library's serve path (policy LRU)");
-  if (o.policy != SS_POLICY_LRU) refuse(SS_E_INVALID, "policy must be LRU or SCORED or SCORED_AUTO");
+  const bool scored = o.policy == SS_POLICY_SCORED || o.policy == SS_POLICY_SCORED_AUTO;
+  if (o.policy != SS_POLICY_LRU && !scored) refuse(SS_E_INVALID, "policy must be LRU or SCORED or SCORED_AUTO");
+  if ((o.dg_score_profile_len || o.dg_score_profile) && !scored)
+    refuse(SS_E_INVALID, "dg_score_profile needs policy SCORED");
   if (o.pin_planned) refuse(SS_E_INVALID, "needs pin_planned = 0 (planned residents are a warm start)");
   if (!o.fill_residents) refuse(SS_E_INVALID, "needs fill_residents = 1 (a resident's slot is its only copy)");
   if (o.readahead_units) refuse(SS_E_INVALID, "readahead_units must be 0 (no gated unit is read from its file)");
@@ -80,10 +86,9 @@ Layout make_layout(const Desc& d, const Plan& p, const ss_options& o) {
       o.dg_disk_queue_adapt)
     refuse(SS_E_UNSUPPORTED, "landings (dg_landing_*), dg_bank_keep and dg_disk_queue_adapt are not part of this "
                              "library's serve path");
-  if (o.dg_no_admit || o.dg_pf_revert_unused || o.dg_pf_strict_admit || o.dg_prior_len || o.dg_prior ||
-      o.dg_score_profile_len || o.dg_score_profile)
-    refuse(SS_E_UNSUPPORTED, "dg_no_admit / dg_pf_revert_unused / dg_pf_strict_admit / priors / score profiles are "
-                             "not part of this library's serve path");
+  if (o.dg_no_admit || o.dg_pf_revert_unused || o.dg_pf_strict_admit || o.dg_prior_len || o.dg_prior)
+    refuse(SS_E_UNSUPPORTED, "dg_no_admit / dg_pf_revert_unused / dg_pf_strict_admit / priors are not part of this "
+                             "library's serve path");
   if (o.dg_clean_evict > 1) refuse(SS_E_INVALID, "dg_clean_evict must be 0 or 1");
 
   Layout x;
@@ -183,6 +188,28 @@ Layout make_layout(const Desc& d, const Plan& p, const ss_options& o) {
   if (x.I && x.I >= x.Q)
     refuse(SS_E_CAPACITY, "dg_inclusive_blocks " + std::to_string(x.I) + " must stay below the spare blocks (" +
                               std::to_string(x.Q) + "): raise host_spare_units by the inclusive share");
+  // scored eviction (reference src/dg_layout.cpp:349-371): the weights, the per-layer bound, the tables' size, and
+  // every rule of the profile's format (the context loads its counts before the first token)
+  if (scored) {
+    x.scored = true;
+    if (o.dg_score_w_trans || o.dg_score_w_freq || o.dg_score_w_recency) {
+      if (o.dg_score_w_trans > 1000 || o.dg_score_w_freq > 1000 || o.dg_score_w_recency > 1000 ||
+          o.dg_score_w_trans + o.dg_score_w_freq + o.dg_score_w_recency != 1000)
+        refuse(SS_E_INVALID, "dg_score_w_trans / _freq / _recency must each be 0..1000 and sum to 1000");
+      x.w_trans = o.dg_score_w_trans;
+      x.w_freq = o.dg_score_w_freq;
+      x.w_rec = o.dg_score_w_recency;
+    }
+    std::vector<uint32_t> units;
+    for (int L : x.gated) units.push_back(uint32_t(d.layers[size_t(L)].n_units));
+    if (score_cells(units) > uint64_t(SIZE_MAX / 8)) refuse(SS_E_INVALID, "the score tables do not fit the address space");
+    if (o.dg_score_profile_len || o.dg_score_profile) {
+      if (!o.dg_score_profile || !o.dg_score_profile_len)
+        refuse(SS_E_INVALID, "dg_score_profile and dg_score_profile_len must be given together");
+      x.score_identity = score_identity(d, x.gated);
+      (void)check_score_profile(o.dg_score_profile, o.dg_score_profile_len, units, x.score_identity);
+    }
+  }
   x.persistent_slots = x.R + x.D;
   const uint64_t S = uint64_t(x.persistent_slots) + 2ull * x.B + 1;
   require(S < 0x7fffffffull, SS_E_INVALID, "device-gated: more than 2^31 - 1 slots");
@@ -983,7 +1010,7 @@ class Service {
   void serve_token(uint32_t seq) {
     const uint32_t G = core_->gated();
     std::copy(run_next_.begin(), run_next_.end(), run_.begin());
-    core_->begin_token(seq);
+    core_->begin_token(seq, &run_);
     wait_began(seq);
     auto next_run = [&](uint32_t g) {
       uint32_t h = g + 1;
@@ -1080,7 +1107,8 @@ class HipDgCtx final : public DgCtx {
     svc_->begin(seq_, run_);
   }
 
-  void end() override {
+  void end(uint32_t rows) override {
+    require(rows > 0, SS_E_INVALID, "ss_dg_end_rows: rows must be positive");
     require(in_token_, SS_E_INVALID, "ss_end: no gated token is open");
     in_token_ = false;
     const auto deadline = Clock::now() + std::chrono::milliseconds(uint64_t(o_.dg_wait_timeout_ms) + 5000);
@@ -1131,7 +1159,7 @@ class HipDgCtx final : public DgCtx {
       poisoned_ = true;
       throw;
     }
-    core_->end_token();
+    core_->end_token(rows);
     const std::vector<uint32_t> bad = tr_->collect_verify();
     tr_->profile_collect();
     if (!bad.empty()) {
@@ -1205,6 +1233,18 @@ class HipDgCtx final : public DgCtx {
     core_->set_prefetch_budget(per_layer, per_token);
   }
 
+  // Between tokens, with the device and the service done with the last one (reference src/dg_ctx.cpp:619-629).
+  void set_policy(ss_policy policy) override {
+    require(!in_token_, SS_E_INVALID, "ss_dg_set_policy: between tokens only");
+    require(!poisoned_, SS_E_BACKEND, "ss_dg_set_policy: poisoned context");
+    require(load_acquire(m_.done) == seq_ && load_acquire(m_.began) == seq_, SS_E_BACKEND,
+            "ss_dg_set_policy: device sequence desync");
+    require(!seq_ || svc_->wait_terminal(seq_, Clock::now()) == Service::kServed, SS_E_BACKEND,
+            "ss_dg_set_policy: the service does not hold the last token's terminal state");
+    core_->set_policy(uint32_t(policy));
+    fold(false);  // the drain's write-backs in the counters; no token for the hook
+  }
+
   // Counters as folded at the last successful boundary (and at open): a token whose ss_end failed never shows, and a
   // call between tokens never reads the service's live counters (reference src/dg_ctx.cpp:1547-1577).
   ss_dg_stats stats() const override {
@@ -1250,6 +1290,12 @@ class HipDgCtx final : public DgCtx {
     TSA_D(disk_discards);
     TSA_D(clean_drops);
     TSA_D(clean_drop_bytes);
+    TSA_D(score_fallbacks);
+    TSA_D(scored_victims);
+    TSA_D(score_layers);
+    TSA_D(score_candidates);
+    TSA_D(score_saturated);
+    TSA_D(score_ns);
 #undef TSA_D
     s.disk_units = fold_file_units_;
     s.disk_queue_resolved = x_.disk_tier ? x_.disk_queue : 0;
@@ -1489,6 +1535,7 @@ class HipDgCtx final : public DgCtx {
   mutable std::mutex snap_mu_;
   Published snap_;
   uint64_t verify_failures_ = 0;
+  std::string score_prov_;  // the score profile's provenance (reported in the stats document)
 
   static void add_stats(ss_layer_stats& a, const ss_layer_stats& b) {
     a.routed += b.routed;
@@ -1616,6 +1663,12 @@ void HipDgCtx::init() {
   c.home_blocks = x_.disk_tier ? x_.P : 0;
   c.disk_staging = x_.S;
   c.clean_evict = o_.dg_clean_evict != 0;
+  c.scored = x_.scored;
+  c.scored_auto = o_.policy == SS_POLICY_SCORED_AUTO;
+  c.w_trans = x_.w_trans;
+  c.w_freq = x_.w_freq;
+  c.w_rec = x_.w_rec;
+  c.max_ids = x_.B;
   core_ = std::make_unique<DgCore>(c, tr_.get());
   if (x_.disk_tier)
     tr_->enable_disk(
@@ -1645,6 +1698,15 @@ void HipDgCtx::init() {
   order.insert(order.end(), x_.residents.begin(), x_.residents.end());
   for (uint32_t k = 0; k < x_.keys; ++k) order.push_back(k);
   core_->place(order, x_.disk_tier ? &x_.disk : nullptr);
+  if (o_.dg_score_profile_len) {  // checked by the layout; its counts are read here only, before the first token
+    std::vector<uint32_t> units;
+    for (uint32_t g = 0; g < G; ++g) units.push_back(core_->units(g));
+    const ScoreProfile v = check_score_profile(o_.dg_score_profile, o_.dg_score_profile_len, units, x_.score_identity);
+    core_->load_counts(v.cells);
+    score_prov_ = v.provenance;
+  }
+  o_.dg_score_profile = nullptr;
+  o_.dg_score_profile_len = 0;
   fill();
   tr_->upload_table(core_->table().data(), x_.keys);
   core_->check();
@@ -1657,8 +1719,9 @@ void HipDgCtx::init() {
 
 // The stats-v1 document of a device-gated context (reference src/dg_ctx.cpp:1359-1545): the host contract's keys, the
 // exclusive object and the device_gated object. Counters of what this library does not serve (priors, window
-// prefetches, landings, scored victims, placement rounds, make-resident, bank keeping) are 0, as the reference writes
-// them when those are off; backend is "hip".
+// prefetches, landings, placement rounds, make-resident, bank keeping) are 0, as the reference writes them when those
+// are off; so are score_deferred and score_last_ns (this library ranks only at the boundary, where score_ns counts the
+// selection); backend is "hip".
 Json HipDgCtx::format_stats(const ss_dg_stats& s, const ss_exclusive_stats& x,
                             const std::vector<ss_layer_stats>& layers) const {
   static const std::pair<const char*, uint64_t ss_dg_stats::*> kFields[] = {
@@ -1759,9 +1822,11 @@ Json HipDgCtx::format_stats(const ss_dg_stats& s, const ss_exclusive_stats& x,
   g["landing_max_queued"] = Json::number(uint64_t(0));
   g["landing_ttl"] = Json::number(uint64_t(0));
   g["landing_failed"] = Json::number(uint64_t(0));
-  g["policy"] = Json::string("lru");
+  const uint32_t pol = core_->policy();
+  g["policy"] = Json::string(pol == 2 ? "auto" : pol == 1 ? "scored" : "lru");
   g["cuda_module_loading"] = Json::string("unknown");  // (a CUDA setting; HIP has no such mode)
   g["landing_chunk"] = Json::number(uint64_t(0));
+  if (!score_prov_.empty()) g["score_profile"] = Json::string(score_prov_);
   if (x_.disk_tier || x_.I) {  // three tiers or clean copies: only then, so the two-tier document is unchanged
     Json tt = Json::object();
     for (const auto& f : kDiskFields) tt[f.first] = Json::number(s.*f.second);

@@ -20,7 +20,8 @@ class DgCtx {
   virtual int n_sources() const = 0;
   virtual bool source_direct(int i) const = 0;
   virtual void begin(const uint32_t* rows, int n_layers) = 0;
-  virtual void end() = 0;
+  virtual void end(uint32_t rows = 1) = 0;  // rows: the verify rows the token closed (ss_dg_end_rows)
+  virtual void set_policy(ss_policy policy) = 0;
   virtual ss_dg_device_view device_view() const = 0;
   virtual int gated_index(int layer) const = 0;
   virtual void enqueue_begin(void* stream) = 0;

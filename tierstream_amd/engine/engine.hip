@@ -212,6 +212,7 @@ __attribute__((visibility("default"))) ss_status tse_host_run(ss_ctx* c, const s
 struct TseDg {
   ss_ctx* c = nullptr;
   uint32_t G = 0, n_ids = 0, max_chunks = 0;
+  uint32_t rows = 1;  // the verify rows each token closes (above one: ss_dg_end_rows instead of ss_end)
   bool checksum = true, dg = true;
   hipStream_t s = nullptr;
   int32_t* ids_dev = nullptr;               // [G][64]
@@ -306,7 +307,9 @@ __attribute__((visibility("default"))) ss_status tse_dg_token(void* h, const int
   const auto t0 = std::chrono::steady_clock::now();
   if (e->dg) TSE_CK(ss_begin(e->c, nullptr, 0));
   ss_status st = e->exec ? ck(hipGraphLaunch(e->exec, e->s)) : tse_enqueue_token(e);
-  const ss_status end_st = e->dg ? ss_end(e->c) : ck(hipStreamSynchronize(e->s));
+  const ss_status end_st = !e->dg          ? ck(hipStreamSynchronize(e->s))
+                            : e->rows > 1 ? ss_dg_end_rows(e->c, e->rows)
+                                          : ss_end(e->c);
   if (token_ms) *token_ms = ms_since(t0);
   (void)hipStreamSynchronize(e->s);
   if (st == SS_OK) st = end_st;
@@ -387,6 +390,13 @@ __attribute__((visibility("default"))) ss_status tse_slot_probe(const int32_t* s
   (void)hipFree(d_ts);
   (void)hipFree(d_words);
   return st;
+}
+
+// The verify rows each later token closes (1: ss_end; more: ss_dg_end_rows, e.g. a speculative step's rows).
+__attribute__((visibility("default"))) ss_status tse_dg_set_rows(void* h, uint32_t rows) {
+  if (!h || rows < 1) return SS_E_INVALID;
+  static_cast<TseDg*>(h)->rows = rows;
+  return SS_OK;
 }
 
 // The last token's per-layer compute-start stamps (wall clock, 100 MHz ticks), [G].

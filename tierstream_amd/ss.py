@@ -182,6 +182,10 @@ def _declare() -> C.CDLL:
         "ss_stats_snapshot_json": (st, [vp, C.POINTER(vp), C.POINTER(C.c_size_t)]),
         "ss_stats_reset": (None, [vp]),
         "ss_stats_dg_sized": (st, [vp, C.POINTER(SsDgStats), u32]),
+        "ss_dg_set_policy": (st, [vp, C.c_int]),
+        "ss_dg_end_rows": (st, [vp, u32]),
+        "tsa_test_sha256": (st, [C.c_char_p, u64, C.c_char_p]),
+        "tsa_test_score_profile_check": (st, [C.c_char_p, u64, C.POINTER(u32), u32, C.c_char_p, C.c_char_p, u32]),
         "ss_dg_get_device_view_sized": (st, [vp, C.POINTER(SsDgDeviceView), u32]),
         "ss_dg_gated_index": (C.c_int, [vp, C.c_int]),
         "ss_dg_residency": (st, [vp, vp, u32, C.POINTER(u32)]),
@@ -222,6 +226,8 @@ def engine() -> C.CDLL:
         E.tse_dg_token.argtypes = [vp, C.POINTER(i32), C.POINTER(u64), C.POINTER(C.c_double)]
         E.tse_dg_stamps.restype = C.c_int
         E.tse_dg_stamps.argtypes = [vp, C.POINTER(u64)]
+        E.tse_dg_set_rows.restype = C.c_int
+        E.tse_dg_set_rows.argtypes = [vp, u32]
         E.tse_dg_destroy.restype = None
         E.tse_dg_destroy.argtypes = [vp]
     return _engine
@@ -375,6 +381,10 @@ class Ctx:
         check(_declare().ss_stats_dg_sized(self.h, C.byref(s), C.sizeof(s)))
         return s.as_dict()
 
+    def dg_set_policy(self, policy: int):
+        """Between tokens: 0 LRU, 1 SCORED, 2 SCORED_AUTO (ss_dg_set_policy)."""
+        check(_declare().ss_dg_set_policy(self.h, policy))
+
     def dg_table(self) -> np.ndarray:
         L = _declare()
         n = u32(0)
@@ -467,6 +477,10 @@ class DgEngine:
         st = E.tse_dg_token(self.h, r.ctypes.data_as(C.POINTER(i32)),
                             cks.ctypes.data_as(C.POINTER(u64)) if want_checksums else None, C.byref(ms))
         return int(st), cks, ms.value
+
+    def set_rows(self, rows: int):
+        """The verify rows each later token closes (ss_dg_end_rows above one)."""
+        check(engine().tse_dg_set_rows(self.h, rows))
 
     def stamps(self) -> np.ndarray:
         """uint64 [G]: the last token's per-layer compute-start wall-clock ticks."""
