@@ -74,6 +74,9 @@ def parse():
                          "a drive that takes direct I/O; the other layers' file stays in --workdir)")
     ap.add_argument("--inclusive", type=int, default=0,
                     help="dg_inclusive_blocks (clean copies; 0 = spare slots + banks); spare blocks = this + 4")
+    ap.add_argument("--policy", default="lru", choices=["lru", "scored", "auto"],
+                    help="device-gated eviction policy (SS_POLICY_LRU / SCORED / SCORED_AUTO; default 700/200/100 "
+                         "weights, no profile)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the copy peaks and the library's HBM kernels alone (no serve loop: for counter runs)")
     return ap.parse_args()
@@ -390,7 +393,8 @@ def main():
         if disk_peak:
             log(f"file tier drive: {disk_peak}")
         t0 = time.time()
-        ctx = ss.Ctx(d, b, plan, ss.options(**shape.options, verify_hash=2, dg_wait_timeout_ms=20000))
+        policy = {"lru": 0, "scored": 1, "auto": 2}[a.policy]
+        ctx = ss.Ctx(d, b, plan, ss.options(**shape.options, verify_hash=2, dg_wait_timeout_ms=20000, policy=policy))
         log(f"context open (fill + hash check) in {time.time() - t0:.1f} s")
         eng = ss.DgEngine(ctx, shape.B, use_graph=True)
         G = eng.G
@@ -453,6 +457,8 @@ def main():
         if three:
             dkeys += ["disk_reads", "disk_read_bytes", "disk_read_ns", "disk_wait_ns", "disk_stage_waits",
                       "disk_drops", "disk_discards", "clean_drops"]
+        if policy:
+            dkeys += ["scored_victims", "score_layers", "score_candidates", "score_ns", "score_fallbacks"]
         dstat = {k: s1[k] - s0[k] for k in dkeys}
         if three:
             dstat["disk_max_in_flight"] = s1["disk_max_in_flight"]
@@ -491,6 +497,7 @@ def main():
                                    + ", device-gated hipGraph token, verify_hash 2"
                                    + (f"; {w.layers} of the full model's {W.WORKLOADS[w.name].layers} layers"
                                       if w.layers != W.WORKLOADS[w.name].layers else ""),
+                       "policy": a.policy,
                        "layers": w.layers, "experts": w.units, "top_k": w.top_k, "unit_bytes": w.unit_bytes,
                        "resident_units": n_res, "pinned_units": n_pin, "file_units": n_file,
                        "spare_slots": shape.D, "spare_blocks": shape.Q, "inclusive_blocks": shape.I,
@@ -554,7 +561,10 @@ def main():
                 "note": "read_GBps_wall: file-tier bytes read over the timed region's wall clock; the reads run on "
                         "reader threads while earlier copies and layers proceed (the service waits only before a "
                         "layer's ready word)"}
-        if not a.no_cpu:
+        if a.policy != "lru":  # the baseline driver runs the reference core under LRU only
+            result["cpu_baseline"] = None
+            result["cpu_baseline_note"] = "not sampled: the CPU baseline driver runs the LRU policy"
+        elif not a.no_cpu:
             est = float(np.median(lat)) / 1e3 * 20  # a first guess of the CPU's time per token
             got, why = cpu_baseline(w, shape, files, hashes, routes, warm, est, a.cpu_seconds)
             if got:
