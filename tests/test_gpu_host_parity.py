@@ -106,18 +106,23 @@ def test_host_contract_matches_reference(name, tmp_path, gpu):
     ctx.close()
 
 
-def test_device_verify_of_landed_units(tmp_path, gpu):
-    """verify_hash = 2: every landed unit re-hashed in HBM (checkpoint-parallel) against the descriptor; none fails."""
-    c = CASES["decode-lru"]
-    m = fixtures.write_model(tmp_path, c["layers"], c["units"], c["parts"], top_k=2, seed=3)
-    routes = fixtures.uniform_routes(c["layers"], c["units"], 2, 12, seed=5)
-    bkw = _budget(m, c["n_res"], c["ring"], c["dyn"])
+@pytest.mark.parametrize("name", ["decode-lru", "dense-prefix", "qwen-exclusive"])
+def test_device_verify_of_landed_units(name, tmp_path, gpu):
+    """verify_hash = 2: every landed unit re-hashed in HBM (checkpoint-parallel) against the descriptor; none fails.
+    The checks run in batches on their own stream, so a slot reused inside a forward (dense-prefix: 5 layers through a
+    2-slot ring per forward) must not take its next unit before its previous one was checked."""
+    c = CASES[name]
+    m = fixtures.write_model(tmp_path, c["layers"], c["units"], c["parts"], kind=c.get("kind", "moe"),
+                             top_k=c["top_k"], order=c.get("order", "ranked"), seed=3)
+    routes = fixtures.uniform_routes(c["layers"], c["units"], c["top_k"], 12, seed=5, tokens=c.get("tokens", 1))
+    bkw = _budget(m, c["n_res"], c["ring"], c.get("dyn", 0), **c.get("budget", {}))
     d = ss.Desc(m.desc_json())
-    ctx = ss.Ctx(d, ss.budget(**bkw), None, ss.options(pin_planned=0, verify_hash=2))
+    ctx = ss.Ctx(d, ss.budget(**bkw), None, ss.options(**c["opts"], verify_hash=2))
     try:
-        ctx.host_run(routes, 0)
+        cks, _, stats, _ = ctx.host_run(routes, c["mode"])
         import tierstream_amd as tsa
         assert tsa.ss._declare().tsa_test_verify_failures(ctx.h) == 0
+        assert sum(s["admitted"] + s["transient"] for s in stats) > 0
     finally:
         ctx.close()
 

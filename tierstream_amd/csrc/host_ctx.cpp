@@ -111,6 +111,8 @@ void HostCtx::init() {
   require(o_.verify_hash >= 0 && o_.verify_hash <= 2, SS_E_INVALID, "open: verify_hash must be 0, 1 or 2");
   dev_ = std::make_unique<HipDevice>(o_.device);
   copy_ = dev_->stream_create_dedicated();
+  copy2_ = dev_->stream_create_dedicated();
+  join_ev_ = dev_->event_create();
   if (!o_.reader_threads) o_.reader_threads = 2;
   if (!o_.staging_buffers) o_.staging_buffers = 4;
   if (!o_.staging_bytes) o_.staging_bytes = uint64_t(256) << 20;
@@ -230,6 +232,7 @@ void HostCtx::init() {
     vfail_host_ = static_cast<uint32_t*>(dev_->alloc_pinned(vcap_ * 4, "verify results"));
     vtable_dev_ = dev_->alloc_device(vcap_ * sizeof(tsa_verify_unit), "verify table");
     vfail_dev_ = static_cast<uint32_t*>(dev_->alloc_device(vcap_ * 4, "verify results"));
+    ventry_flush_.assign(vcap_, 0);
     hip_check(hipMemsetAsync(vfail_dev_, 0, vcap_ * 4, copy_), "hipMemsetAsync");
     vdone_ev_ = dev_->event_create();
     vready_ev_ = dev_->event_create();
@@ -274,6 +277,7 @@ void HostCtx::init() {
   for (const auto& j : fill)
     if (j->done_ev) ev_pool_.push_back(j->done_ev);
   stream_sync(copy_);
+  stream_sync(copy2_);
   if (dverify_) collect_verify();  // the residents' device check (one batch at open)
 }
 
@@ -316,8 +320,11 @@ void HostCtx::cleanup() noexcept {
   dev_->free_device(vfail_dev_);
   dev_->event_destroy(vdone_ev_);
   dev_->event_destroy(vready_ev_);
+  for (hipEvent_t e : vflush_ev_) dev_->event_destroy(e);
   if (vstream_) dev_->stream_destroy(vstream_);
+  dev_->event_destroy(join_ev_);
   dev_->stream_destroy(copy_);
+  dev_->stream_destroy(copy2_);
   dev_->stream_destroy(wb_);
   L_.clear();
   dev_.reset();
@@ -387,12 +394,14 @@ void HostCtx::submit(const HostJobPtr& j) {
     const uint64_t n = d_.layers[size_t(j->layer)].unit_bytes;
     try {
       std::lock_guard<std::mutex> lk(copy_mu_);
-      stream_wait(copy_, j->dst_release_ev);
-      stream_wait(copy_, j->dst_wb_ev);
-      stream_wait(copy_, j->src_wait_ev);
+      const hipStream_t cs = next_copy_stream();
+      wait_slot_check(cs, j->dst);
+      stream_wait(cs, j->dst_release_ev);
+      stream_wait(cs, j->dst_wb_ev);
+      stream_wait(cs, j->src_wait_ev);
       for (uint64_t off = 0; off < n; off += o_.copy_piece_bytes)
-        copy_h2d(at(j->dst, off), at(j->host_src, off), std::min<uint64_t>(o_.copy_piece_bytes, n - off), copy_);
-      ev_record(j->done_ev, copy_);
+        copy_h2d(at(j->dst, off), at(j->host_src, off), std::min<uint64_t>(o_.copy_piece_bytes, n - off), cs);
+      ev_record(j->done_ev, cs);
       if (dverify_) verify_landed(*j);
     } catch (const Error& e) {
       fail_job(*j, e.status(), e.what());
@@ -573,6 +582,7 @@ void HostCtx::read_unit_device(HostJob& j) {
         if (hash) h.feed(src, len);
         std::lock_guard<std::mutex> lk(copy_mu_);
         if (!waited) {
+          wait_slot_check(copy_, j.dst);
           stream_wait(copy_, j.dst_release_ev);
           stream_wait(copy_, j.dst_wb_ev);
           waited = true;
@@ -623,7 +633,22 @@ void HostCtx::verify_landed(const HostJob& j) {
   v.digest = l.hash[size_t(j.unit)];
   v.total = l.unit_bytes;
   vunits_.push_back({j.layer, j.unit});
+  vdst_[j.dst] = i;
   if (vused_ - vflushed_ >= kVerifyBatch) flush_verify();
+}
+
+void HostCtx::wait_slot_check(hipStream_t s, const void* dst) {
+  const auto it = vdst_.find(dst);
+  if (it == vdst_.end()) return;
+  const size_t i = it->second;
+  if (i >= vflushed_) flush_verify();  // (its batch was still pending: launch it now)
+  stream_wait(s, vflush_ev_[ventry_flush_[i]]);
+  vdst_.erase(it);
+}
+
+void HostCtx::join_copies() {
+  ev_record(join_ev_, copy2_);
+  stream_wait(copy_, join_ev_);
 }
 
 void HostCtx::flush_verify() {
@@ -635,12 +660,17 @@ void HostCtx::flush_verify() {
     vtable_host_[i].seg_first = segs;
     segs += count;
   }
+  join_copies();
   ev_record(vready_ev_, copy_);
   stream_wait(vstream_, vready_ev_);
   tsa_verify_unit* vd = static_cast<tsa_verify_unit*>(vtable_dev_) + vflushed_;
   copy_h2d(vd, vtable_host_ + vflushed_, n * sizeof(tsa_verify_unit), vstream_);
   hip_check(hipError_t(launch_verify(vd, uint32_t(n), segs, seg_bytes_, vfail_dev_ + vflushed_, vstream_)),
             "device verify launch");
+  if (vflushes_ == vflush_ev_.size()) vflush_ev_.push_back(dev_->event_create());
+  ev_record(vflush_ev_[vflushes_], vstream_);
+  for (size_t i = vflushed_; i < vused_; ++i) ventry_flush_[i] = vflushes_;
+  ++vflushes_;
   vflushed_ = vused_;
 }
 
@@ -663,6 +693,8 @@ void HostCtx::collect_verify() {
     std::lock_guard<std::mutex> lk(copy_mu_);
     units.swap(vunits_);
     vused_ = vflushed_ = 0;
+    vdst_.clear();  // (every launch has completed: ev_sync above)
+    vflushes_ = 0;
   }
   for (size_t i = 0; i < n; ++i)
     if (vfail_host_[i]) {
@@ -930,6 +962,7 @@ void HostCtx::seed(int layer, const int32_t* units, int n) {
   for (const auto& j : jobs)
     if (j->done_ev) ev_pool_.push_back(j->done_ev);
   stream_sync(copy_);
+  stream_sync(copy2_);
   if (excl_)
     for (int32_t u : landed) free_block(layer, u);
   if (failed != SS_OK) fail(failed, err);
@@ -1248,7 +1281,9 @@ void HostCtx::end() {
       if (!wb_evs_.empty()) {
         ev_record(wb_mark_ev_, wb_);
         stream_wait(copy_, wb_mark_ev_);
+        stream_wait(copy2_, wb_mark_ev_);
       }
+      join_copies();
       ev_record(blocks_ev_, copy_);
       wb_gate_ = true;
     }
@@ -1262,6 +1297,7 @@ void HostCtx::end() {
   }
   {
     std::lock_guard<std::mutex> lk(copy_mu_);
+    join_copies();
     for (size_t L = 0; L < L_.size(); ++L) {
       LayerState& s = L_[L];
       if (!s.rs) continue;
@@ -1306,6 +1342,7 @@ void HostCtx::check_unit(int layer, int unit) {
     ev_sync(s.job[size_t(unit)]->done_ev);
   }
   stream_sync(copy_);
+  stream_sync(copy2_);
   std::vector<char> got(size_t(l.unit_bytes));
   std::vector<char> want(size_t(round_up(l.unit_bytes, kHostAlign)) + kHostAlign);
   hip_check(hipMemcpy(got.data(), a, got.size(), hipMemcpyDeviceToHost), "hipMemcpy (check_unit)");

@@ -16,6 +16,7 @@
 #include <mutex>
 #include <string>
 #include <thread>
+#include <unordered_map>
 #include <vector>
 
 #include "hip_rt.hpp"
@@ -172,7 +173,14 @@ class HostCtx {
   Plan plan_;
   ss_options o_;
   std::unique_ptr<HipDevice> dev_;
-  hipStream_t copy_ = nullptr, wb_ = nullptr;
+  // Pinned -> HBM copies alternate between copy_ and copy2_ (two SDMA queues: one queue's per-copy gap is about 6 % of
+  // a 9 MiB unit's copy time); the other copies use copy_. join_copies() makes copy_ follow copy2_'s work so far, so
+  // an event recorded on copy_ after it stands for every copy before it.
+  hipStream_t copy_ = nullptr, copy2_ = nullptr, wb_ = nullptr;
+  hipEvent_t join_ev_ = nullptr;
+  bool copy_alt_ = false;
+  hipStream_t next_copy_stream() { return (copy_alt_ = !copy_alt_) ? copy2_ : copy_; }
+  void join_copies();  // (copy_mu_ held)
   std::vector<std::unique_ptr<SourceFile>> files_;
   std::vector<LayerState> L_;
   std::vector<RingSlot> ring_;
@@ -220,6 +228,14 @@ class HostCtx {
   hipStream_t vstream_ = nullptr;                 // the checks (copies never queue behind them)
   hipEvent_t vready_ev_ = nullptr;                // the copy stream at a flush: the batch's copies are done
   std::vector<std::pair<int, int>> vunits_;  // (layer, unit) of each verify slot this forward
+  // A landed unit's check reads its slot until the check's launch completes, so the next copy into that slot waits for
+  // it: the slot's pending entry (since the last collect), the flush that launched each entry, and per flush an event
+  // on the verify stream after its launch.
+  std::unordered_map<const void*, size_t> vdst_;
+  std::vector<uint32_t> ventry_flush_;
+  std::vector<hipEvent_t> vflush_ev_;
+  uint32_t vflushes_ = 0;
+  void wait_slot_check(hipStream_t s, const void* dst);  // (copy_mu_ held)
   hipEvent_t vdone_ev_ = nullptr;
   uint64_t verify_fail_total_ = 0;
 
