@@ -1359,7 +1359,7 @@ class HipDgCtx final : public DgCtx {
     hook_ = h;
     hook_user_ = user;
   }
-  Json stats_json() const override { return format_stats(stats(), exclusive_stats(), layers_now()); }
+  Json stats_json() const override { return format_stats(stats(), exclusive_stats(), layers_now(), core_->policy()); }
   bool snapshot(ss_layer_stats* total, ss_snapshot_info* info) const override {
     snap_armed_.store(true, std::memory_order_relaxed);
     std::lock_guard<std::mutex> lk(snap_mu_);
@@ -1391,7 +1391,7 @@ class HipDgCtx final : public DgCtx {
       if (snap_.seq == 0) return false;
       p = snap_;
     }
-    *out = format_stats(p.s, p.x, p.layers);
+    *out = format_stats(p.s, p.x, p.layers, p.policy);
     return true;
   }
   // After a successful boundary (and at open): the core's counters as the stats show them, the hook with this
@@ -1530,6 +1530,7 @@ class HipDgCtx final : public DgCtx {
     ss_dg_stats s{};
     ss_exclusive_stats x{};
     std::vector<ss_layer_stats> layers;
+    uint32_t policy = 0;
   };
   mutable std::atomic<bool> snap_armed_{false};
   mutable std::mutex snap_mu_;
@@ -1564,11 +1565,13 @@ class HipDgCtx final : public DgCtx {
     p.s = stats();
     p.x = exclusive_stats();
     p.layers = layers_now();
+    p.policy = core_->policy();  // (the engine thread's: a reader on another thread formats this copy)
     std::lock_guard<std::mutex> lk(snap_mu_);
     p.seq = snap_.seq + 1;
     std::swap(snap_, p);
   }
-  Json format_stats(const ss_dg_stats& s, const ss_exclusive_stats& x, const std::vector<ss_layer_stats>& layers) const;
+  Json format_stats(const ss_dg_stats& s, const ss_exclusive_stats& x, const std::vector<ss_layer_stats>& layers,
+                    uint32_t policy) const;
 };
 
 void HipDgCtx::init() {
@@ -1723,7 +1726,7 @@ void HipDgCtx::init() {
 // are off; so are score_deferred and score_last_ns (this library ranks only at the boundary, where score_ns counts the
 // selection); backend is "hip".
 Json HipDgCtx::format_stats(const ss_dg_stats& s, const ss_exclusive_stats& x,
-                            const std::vector<ss_layer_stats>& layers) const {
+                            const std::vector<ss_layer_stats>& layers, uint32_t pol) const {
   static const std::pair<const char*, uint64_t ss_dg_stats::*> kFields[] = {
       {"tokens", &ss_dg_stats::tokens}, {"lookups", &ss_dg_stats::lookups}, {"misses", &ss_dg_stats::misses},
       {"covered", &ss_dg_stats::covered}, {"fetched", &ss_dg_stats::fetched},
@@ -1822,7 +1825,6 @@ Json HipDgCtx::format_stats(const ss_dg_stats& s, const ss_exclusive_stats& x,
   g["landing_max_queued"] = Json::number(uint64_t(0));
   g["landing_ttl"] = Json::number(uint64_t(0));
   g["landing_failed"] = Json::number(uint64_t(0));
-  const uint32_t pol = core_->policy();
   g["policy"] = Json::string(pol == 2 ? "auto" : pol == 1 ? "scored" : "lru");
   g["cuda_module_loading"] = Json::string("unknown");  // (a CUDA setting; HIP has no such mode)
   g["landing_chunk"] = Json::number(uint64_t(0));
