@@ -84,6 +84,11 @@ SS_API const char* tsa_test_dgcore_counter_names(void);
 /* As tsa_test_dgcore_token with run [n_gated] (null: all): the gated layers the token exports (ss_begin's rows). */
 SS_API ss_status tsa_test_dgcore_token_run(void* h, const uint32_t* ids, uint32_t n, const uint8_t* run,
                                            int32_t* table_out, uint64_t* counts, uint32_t n_counts);
+/* As tsa_test_dgcore_token_run with predictions pred [n_gated][n_pred] (row g: the ids predicted at layer g for layer
+ * g + 1, served right after layer g's use when layer g + 1 exports; n_pred 0: none). */
+SS_API ss_status tsa_test_dgcore_token_pred(void* h, const uint32_t* ids, uint32_t n, const uint32_t* pred,
+                                            uint32_t n_pred, const uint8_t* run, int32_t* table_out, uint64_t* counts,
+                                            uint32_t n_counts);
 /* Between tokens: the policy switch of ss_dg_set_policy on the core alone. */
 SS_API ss_status tsa_test_dgcore_set_policy(void* h, uint32_t policy);
 /* Scored eviction's profile rules without a context: the SHA-256 of data[0..n) (32 raw bytes into out), and the

@@ -45,6 +45,9 @@ def _lib():
     L.tsa_test_dgcore_token_run.argtypes = [C.c_void_p, C.POINTER(u32), u32, C.POINTER(C.c_uint8),
                                             C.POINTER(C.c_int32), C.POINTER(u64), u32]
     L.tsa_test_dgcore_token_run.restype = C.c_int
+    L.tsa_test_dgcore_token_pred.argtypes = [C.c_void_p, C.POINTER(u32), u32, C.POINTER(u32), u32,
+                                             C.POINTER(C.c_uint8), C.POINTER(C.c_int32), C.POINTER(u64), u32]
+    L.tsa_test_dgcore_token_pred.restype = C.c_int
     L.tsa_test_dgcore_set_policy.argtypes = [C.c_void_p, u32]
     L.tsa_test_dgcore_set_policy.restype = C.c_int
     return tsa, L
@@ -67,7 +70,7 @@ class OurCore:
         if disk:
             fl = (C.c_uint8 * sum(n_units))(*disk["flags"])
             c.disk_tier, c.home_blocks, c.disk_staging = 1, disk["home_blocks"], disk["disk_staging"]
-            c.clean_evict, c.disk_prefetch, c.disk = disk.get("clean_evict", 0), 0, fl
+            c.clean_evict, c.disk_prefetch, c.disk = disk.get("clean_evict", 0), disk.get("disk_prefetch", 0), fl
             self._keep.append(fl)
         c.w_trans, c.w_freq, c.w_rec, c.rows = 700, 200, 100, 1
         if score:
@@ -83,14 +86,17 @@ class OurCore:
         self.keys = sum(n_units)
         self.names = self.L.tsa_test_dgcore_counter_names().decode().split()
 
-    def token(self, ids, run=None):
+    def token(self, ids, run=None, pred=None):
         x = np.ascontiguousarray(ids, dtype=np.uint32)
         table = np.zeros(self.keys, dtype=np.int32)
         counts = np.zeros(len(self.names), dtype=np.uint64)
         rv = (C.c_uint8 * x.shape[0])(*run) if run is not None else None
-        self.tsa.check(self.L.tsa_test_dgcore_token_run(self.h, x.ctypes.data_as(C.POINTER(u32)), x.shape[1], rv,
-                                                        table.ctypes.data_as(C.POINTER(C.c_int32)),
-                                                        counts.ctypes.data_as(C.POINTER(u64)), len(self.names)))
+        p = np.ascontiguousarray(pred, dtype=np.uint32) if pred is not None else np.zeros((1, 1), np.uint32)
+        self.tsa.check(self.L.tsa_test_dgcore_token_pred(self.h, x.ctypes.data_as(C.POINTER(u32)), x.shape[1],
+                                                         p.ctypes.data_as(C.POINTER(u32)),
+                                                         p.shape[1] if pred is not None else 0, rv,
+                                                         table.ctypes.data_as(C.POINTER(C.c_int32)),
+                                                         counts.ctypes.data_as(C.POINTER(u64)), len(self.names)))
         return table, {k: int(v) for k, v in zip(self.names, counts)}
 
     def set_policy(self, policy):
@@ -179,12 +185,33 @@ def _score(seed, n_units, policy=None):
     return dict(policy=pol, w=w, rows=rows, cells=cells)
 
 
-def _run(seed, three, score=None, switch=None, partial=False):
+def _preds(rng, routes, n_units, k):
+    """Per token [G][k]: for layer g the ids predicted for layer g + 1 - mostly its true next ids, some random, a few
+    out of range (pred_invalid); the last row is unused."""
+    T, G, _ = routes.shape
+    out = np.zeros((T, G, k), dtype=np.uint32)
+    for t in range(T):
+        for g in range(G - 1):
+            nu = n_units[g + 1]
+            for i in range(k):
+                r = rng.random()
+                if r < 0.6 and i < routes.shape[2]:
+                    out[t, g, i] = routes[t, g + 1, i]
+                elif r < 0.95:
+                    out[t, g, i] = rng.integers(0, nu)
+                else:
+                    out[t, g, i] = nu + int(rng.integers(0, 3))
+    return out
+
+
+def _run(seed, three, score=None, switch=None, partial=False, predict=0, disk_prefetch=0):
     """switch: (token, policy) - both cores switch policy between tokens there. partial: each token exports a random
     nonempty subset of the gated layers (ss_begin's rows), the others keep their state."""
     if not ref.available():
         pytest.skip("oracle/_ref (the reference core) is not built")
     c = _case(seed, three)
+    if disk_prefetch and c["disk"]:
+        c["disk"]["disk_prefetch"] = 1
     kw = dict(wb_defer=c["wb_defer"], inclusive=c["inclusive"])
     ours = OurCore(c["n_units"], c["persistent"], c["bank"], c["blocks"], c["spare_target"], c["parts"], c["order"],
                    disk=c["disk"], score=score, **kw)
@@ -192,6 +219,7 @@ def _run(seed, three, score=None, switch=None, partial=False):
                        c["order"], disk=c["disk"], score=score, **kw)
     seen = {}
     rng = np.random.default_rng(seed + 5)
+    preds = _preds(np.random.default_rng(seed + 9), c["routes"], c["n_units"], predict) if predict else None
     try:
         for t, ids in enumerate(c["routes"]):
             if switch and t == switch[0]:
@@ -201,8 +229,9 @@ def _run(seed, three, score=None, switch=None, partial=False):
             if partial:
                 run = [int(v) for v in rng.integers(0, 2, size=ids.shape[0])]
                 run[int(rng.integers(0, ids.shape[0]))] = 1
-            got_t, got = ours.token(ids, run)
-            want_t, want = theirs.token(ids, run=run)
+            pr = preds[t] if predict else None
+            got_t, got = ours.token(ids, run, pr)
+            want_t, want = theirs.token(ids, pred=pr, run=run)
             assert np.array_equal(got_t, want_t), (seed, t, "table")
             for k, v in got.items():
                 assert v == want[k], (seed, t, k, v, want[k])
@@ -239,6 +268,12 @@ def test_cases_exercise_the_paths():
             tot3[k] = tot3.get(k, 0) + v
     for k in ("misses", "bank_serves", "evicted", "writebacks_done", "resurrected", "inclusive_drops", "wb_forced"):
         assert tot2[k] > 0, k
+    tp = {}
+    for s in range(24):
+        for k, v in _run(7000 + s, s % 2 == 1, predict=int(1 + s % 4), disk_prefetch=int(s % 4 == 1)).items():
+            tp[k] = tp.get(k, 0) + v
+    for k in ("prefetched", "prefetch_used", "pred_invalid", "predicted_true", "disk_reads"):
+        assert tp[k] > 0, k
     for k in ("disk_reads", "disk_drops", "disk_discards", "clean_drops", "writebacks_done", "bank_serves"):
         assert tot3[k] > 0, k
 
@@ -274,6 +309,21 @@ def test_partial_exports_match_reference(seed):
     c = _case(6000 + seed, bool(seed % 3 == 0))
     score = _score(seed, c["n_units"]) if seed % 2 else None
     _run(6000 + seed, bool(seed % 3 == 0), score=score, partial=True)
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_prefetch_matches_reference(seed):
+    """Predictions for the next layer (serve_prediction): prefetches within the per-layer and per-token budgets and
+    the reserve, their use, resurrection from banks, invalid ids; three-tier cases read file-homed units ahead
+    (dg_disk_prefetch) in half of them; some cases export only some layers."""
+    three = seed % 2 == 1
+    _run(7000 + seed, three, predict=int(1 + seed % 4), disk_prefetch=int(seed % 4 == 1), partial=seed % 5 == 0)
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_scored_prefetch_matches_reference(seed):
+    c = _case(8000 + seed, False)
+    _run(8000 + seed, False, score=_score(seed, c["n_units"]), predict=int(1 + seed % 3))
 
 
 def test_lru_open_refuses_a_switch_to_scoring():

@@ -71,10 +71,31 @@ CASES = {
                            score=dict(policy=1, w=(500, 300, 200), profile=True)),
     "scored-auto-rows": dict(layers=3, units=16, parts=[32 * KiB, 32 * KiB, 64 * KiB], n_res=16, dyn=2, spares=10,
                              n_ids=4, tokens=24, score=dict(policy=2, rows=2)),
+    # predictions for the next layer (ss_dg_enqueue_predict): prefetches, their use and bank returns, invalid ids
+    "prefetch": dict(layers=4, units=16, parts=[64 * KiB] * 3, n_res=24, dyn=2, spares=12, n_ids=4, tokens=24,
+                     predict=3),
+    "scored-prefetch": dict(layers=4, units=16, parts=[64 * KiB] * 3, n_res=24, dyn=2, spares=12, n_ids=4, tokens=24,
+                            predict=2, score=dict(policy=1)),
     "scored-switch": dict(layers=4, units=16, parts=[64 * KiB] * 3, n_res=24, dyn=2, spares=12, n_ids=4, tokens=30,
                           score=dict(policy=1, switch=[(10, 0), (20, 2)])),
 }
 SCORE_COUNTERS = ["score_fallbacks", "scored_victims", "score_layers", "score_candidates", "score_saturated"]
+PRED_COUNTERS = ["prefetched", "prefetch_used", "pred_invalid", "predicted", "predicted_true", "wb_cancelled"]
+
+
+def _preds(routes, units, k, seed=13):
+    """[tokens][layers][k] int32: at layer g the ids predicted for layer g + 1 - its true ids first, then random ones,
+    now and then one out of range (counted as pred_invalid, never fetched)."""
+    rng = np.random.default_rng(seed)
+    T, G, n = routes.shape
+    out = np.zeros((T, G, k), dtype=np.int32)
+    for t in range(T):
+        for g in range(G - 1):
+            for i in range(k):
+                r = rng.random()
+                out[t, g, i] = routes[t, g + 1, i] if (r < 0.6 and i < n) else \
+                    (units + 1 if r > 0.95 else int(rng.integers(0, units)))
+    return out
 
 
 def _profile_cells(units, layers, seed=9):
@@ -94,6 +115,7 @@ def test_dg_matches_reference(name, tmp_path, gpu):
     zipf = c.pop("zipf", True)
     use_graph = c.pop("graph", True)
     score = dict(c.pop("score", {}))
+    predict = c.pop("predict", 0)
     m, bkw, okw = _setup(tmp_path, c["layers"], c["units"], c["parts"], c["n_res"], c["dyn"], c["spares"], c["n_ids"],
                          inclusive=c.get("inclusive", 0), wb_defer=c.get("wb_defer", 1))
     ref_score, keep = None, []
@@ -126,12 +148,13 @@ def test_dg_matches_reference(name, tmp_path, gpu):
                       residents + list(range(keys)), wb_defer=c.get("wb_defer", 1), inclusive=c.get("inclusive", 0),
                       score=ref_score)
     ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(**okw))
-    eng = ss.DgEngine(ctx, c["n_ids"], use_graph=use_graph)
+    eng = ss.DgEngine(ctx, c["n_ids"], use_graph=use_graph, n_pred=predict)
+    preds = _preds(routes, c["units"], predict) if predict else None
     if score.get("rows", 1) > 1:
         eng.set_rows(score["rows"])
     switch = dict(score.get("switch", []))
     policy = score.get("policy", 0)
-    counters = COUNTERS + (SCORE_COUNTERS if score else [])
+    counters = COUNTERS + (SCORE_COUNTERS if score else []) + (PRED_COUNTERS if predict else [])
     expect = {(L, u): fixtures.engine_checksum(m.unit_data(L, u)) for L in range(c["layers"]) for u in range(c["units"])}
     with pytest.raises(ss.SsError):  # arms the stats snapshot: each token's boundary publishes from now on
         ctx.snapshot()
@@ -141,8 +164,9 @@ def test_dg_matches_reference(name, tmp_path, gpu):
                 policy = switch[t]
                 ctx.dg_set_policy(policy)
                 refdg.set_policy(policy)
-            cks, _ = eng.token(routes[t])
-            want_table, want = refdg.token(routes[t].astype(np.uint32))
+            cks, _ = eng.token(routes[t], preds=preds[t] if predict else None)
+            want_table, want = refdg.token(routes[t].astype(np.uint32),
+                                           pred=preds[t].astype(np.uint32) if predict else None)
             got = ctx.dg_stats()
             assert np.array_equal(ctx.dg_table(), want_table), (name, t)
             for k in counters:
@@ -155,6 +179,8 @@ def test_dg_matches_reference(name, tmp_path, gpu):
             assert got["scored_victims"] > 0 and got["score_fallbacks"] == 0
         if score.get("profile"):
             assert got["score_saturated"] > 0
+        if predict:
+            assert got["prefetched"] > 0 and got["prefetch_used"] > 0 and got["pred_invalid"] > 0
         _check_stats_doc(ctx, want, tokens, policy=["lru", "scored", "auto"][policy],
                          prov="test fit" if score.get("profile") else None, publications=tokens + len(switch))
     finally:

@@ -602,7 +602,14 @@ void DgCore::use(uint32_t g, uint32_t unit, bool was_miss) {
   }
 }
 
-void DgCore::serve_demand(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask) {
+uint64_t DgCore::canonical_mask(uint32_t g, const uint32_t* ids, uint32_t n) const {
+  uint64_t m = 0;
+  for (uint32_t i = 0; i < n && i < 64; ++i)
+    if (ids[i] < units(g) && table_[key(g, ids[i])] < 0) m |= uint64_t(1) << i;
+  return m;
+}
+
+void DgCore::serve_demand(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask, uint64_t dev_mask) {
   const uint32_t nu = units(g);
   for (uint32_t i = 0; i < n; ++i)
     require(ids[i] < nu, SS_E_INVALID,
@@ -610,7 +617,12 @@ void DgCore::serve_demand(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t 
                 std::to_string(nu));
   // per masked occurrence in export order: a repeated id is fetched at its first occurrence, covered at the others
   for (uint32_t i = 0; i < n; ++i) {
-    if (!(mask >> i & 1u)) continue;
+    if (!(mask >> i & 1u)) {
+      const Entry& x = e_[key(g, ids[i])];
+      if ((dev_mask >> i & 1u) && x.home == Home::Coming && x.via_prefetch && x.pf_done)
+        t_->wait(DgTransport::kDem, x.pf_done);  // in flight when the layer exported: its readers wait for it
+      continue;
+    }
     if (on_device_or_coming(g, ids[i])) {
       cover(g, ids[i]);
       ++st_.covered;
@@ -619,7 +631,7 @@ void DgCore::serve_demand(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t 
     }
   }
   // after every fetch's landed(): a transport that checks landed units orders the ready word behind the checks
-  if (mask) t_->signal_ready(g, seq_);
+  if (mask | dev_mask) t_->signal_ready(g, seq_);
 }
 
 void DgCore::serve_use(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask) {

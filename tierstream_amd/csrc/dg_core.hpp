@@ -156,7 +156,14 @@ class DgCore {
 
   // run: the gated layers this token exports (null: all); a layer left out keeps its score history unchanged
   void begin_token(uint32_t seq, const std::vector<uint8_t>* run = nullptr);
-  void serve_demand(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask);
+  // mask: the ids whose entry the canonical schedule sees absent (the host mirror before this layer's service), which
+  // every count and fetch follows; dev_mask (default: mask): the ids the export kernel saw absent in the device table,
+  // whose readers wait for the layer's ready word. A device-only bit is an entry still in flight (a prefetch that had
+  // not landed when the layer exported): its readers wait for that copy, and nothing is counted for it.
+  void serve_demand(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask, uint64_t dev_mask);
+  void serve_demand(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask) { serve_demand(g, ids, n, mask, mask); }
+  // The canonical mask of layer g's export: the ids in range whose mirror entry is absent.
+  uint64_t canonical_mask(uint32_t g, const uint32_t* ids, uint32_t n) const;
   void serve_use(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask);
   void serve_prediction(uint32_t g_next, const uint32_t* pred, uint32_t n);
   void issue_writebacks(uint32_t g);  // the deferred write-back slice after layer g's service

@@ -54,7 +54,7 @@ constexpr const char* kNames =
     "writebacks_done miss_layers covered_waits wb_deferred wb_cancelled wb_forced wb_boundary_flushed wb_issued_bytes "
     "wb_cancelled_bytes inclusive_kept inclusive_drops free_slots free_blocks on_device backed_units disk_reads "
     "disk_drops disk_discards clean_drops file_units score_fallbacks scored_victims score_layers score_candidates "
-    "score_saturated";
+    "score_saturated pred_invalid predicted predicted_true";
 
 }  // namespace
 }  // namespace tsa
@@ -118,11 +118,16 @@ ss_status tsa_test_dgcore_open(const tsa_test_dgcore_config* cfg, const uint32_t
 
 ss_status tsa_test_dgcore_token(void* h, const uint32_t* ids, uint32_t n, int32_t* table_out, uint64_t* counts,
                                 uint32_t n_counts) {
-  return tsa_test_dgcore_token_run(h, ids, n, nullptr, table_out, counts, n_counts);
+  return tsa_test_dgcore_token_pred(h, ids, n, nullptr, 0, nullptr, table_out, counts, n_counts);
 }
 
 ss_status tsa_test_dgcore_token_run(void* h, const uint32_t* ids, uint32_t n, const uint8_t* run, int32_t* table_out,
                                     uint64_t* counts, uint32_t n_counts) {
+  return tsa_test_dgcore_token_pred(h, ids, n, nullptr, 0, run, table_out, counts, n_counts);
+}
+
+ss_status tsa_test_dgcore_token_pred(void* h, const uint32_t* ids, uint32_t n, const uint32_t* pred, uint32_t n_pred,
+                                     const uint8_t* run, int32_t* table_out, uint64_t* counts, uint32_t n_counts) {
   return tsa::guard([&] {
     using namespace tsa;
     require(h && ids && n >= 1 && n <= 64, SS_E_INVALID, "tsa_test_dgcore_token: bad argument");
@@ -140,6 +145,8 @@ ss_status tsa_test_dgcore_token_run(void* h, const uint32_t* ids, uint32_t n, co
         if (x[i] < c.units(g) && c.table()[c.key(g, x[i])] < 0) mask |= uint64_t(1) << i;
       c.serve_demand(g, x, n, mask);
       c.serve_use(g, x, n, mask);
+      // the prediction for the next layer made at this one (the service serves it when that layer exports)
+      if (pred && n_pred && g + 1 < G && rv[g + 1]) c.serve_prediction(g + 1, pred + size_t(g) * n_pred, n_pred);
       uint32_t nx = g + 1;  // the next exported layer: no slice after the token's last one
       while (nx < G && !rv[nx]) ++nx;
       if (c.deferred() && nx < G) c.issue_writebacks(g);
@@ -156,7 +163,7 @@ ss_status tsa_test_dgcore_token_run(void* h, const uint32_t* ids, uint32_t n, co
                             uint64_t(c.free_slots()), uint64_t(c.free_blocks()), uint64_t(c.on_device()),
                             uint64_t(c.backed_units()), s.disk_reads, s.disk_drops, s.disk_discards, s.clean_drops,
                             uint64_t(c.file_units()), s.score_fallbacks, s.scored_victims, s.score_layers,
-                            s.score_candidates, s.score_saturated};
+                            s.score_candidates, s.score_saturated, s.pred_invalid, s.predicted, s.predicted_true};
       const uint32_t m = uint32_t(sizeof v / sizeof v[0]);
       std::memcpy(counts, v, 8ull * (n_counts < m ? n_counts : m));
     }

@@ -1032,9 +1032,14 @@ class Service {
       require(n_pred <= kDgMaxIds && (n_pred == 0 || g + 1 < G), SS_E_BACKEND,
               "device-gated: gated layer " + std::to_string(g) + " promised " + std::to_string(n_pred) +
                   " predicted ids");
-      const uint64_t mask = uint64_t(r.mask_lo) | uint64_t(r.mask_hi) << 32;
+      const uint64_t dev_mask = uint64_t(r.mask_lo) | uint64_t(r.mask_hi) << 32;
       ids_.assign(r.ids, r.ids + n);
-      core_->serve_demand(g, ids_.data(), n, mask);
+      // the canonical schedule's mask (the mirror now, after the previous layer's prediction was served): a prefetch
+      // that had not landed when the layer exported is a hit there, as in the reference's eager schedule
+      const uint64_t mask = core_->canonical_mask(g, ids_.data(), n);
+      require((mask & ~dev_mask) == 0, SS_E_BACKEND,
+              "device-gated: gated layer " + std::to_string(g) + " exported a hit for a unit absent from the table");
+      core_->serve_demand(g, ids_.data(), n, mask, dev_mask);
       core_->serve_use(g, ids_.data(), n, mask);
       if (n_pred > 0 && run_[g + 1]) {
         wait_word(&m_.pflag[g], seq, "prediction flag", g, false, 0);

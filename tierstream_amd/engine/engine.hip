@@ -212,10 +212,12 @@ __attribute__((visibility("default"))) ss_status tse_host_run(ss_ctx* c, const s
 struct TseDg {
   ss_ctx* c = nullptr;
   uint32_t G = 0, n_ids = 0, max_chunks = 0;
+  uint32_t n_pred = 0;  // ids predicted at each layer for the next one (0: no predictions)
   uint32_t rows = 1;  // the verify rows each token closes (above one: ss_dg_end_rows instead of ss_end)
   bool checksum = true, dg = true;
   hipStream_t s = nullptr;
   int32_t* ids_dev = nullptr;               // [G][64]
+  int32_t* pred_dev = nullptr;              // [G][64]: row g predicts layer g + 1
   unsigned long long* out_dev = nullptr;    // [G][64]
   unsigned long long* start_dev = nullptr;  // [G]: wall clock at each layer's first checksum workgroup
   hipGraph_t graph = nullptr;
@@ -227,6 +229,7 @@ struct TseDg {
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
     (void)hipFree(ids_dev);
+    (void)hipFree(pred_dev);
     (void)hipFree(out_dev);
     (void)hipFree(start_dev);
     if (s) (void)hipStreamDestroy(s);
@@ -236,7 +239,9 @@ struct TseDg {
 static ss_status tse_enqueue_token(TseDg* e) {
   if (e->dg) TSE_CK(ss_dg_enqueue_begin(e->c, e->s));
   for (uint32_t g = 0; g < e->G; ++g) {
-    if (e->dg) TSE_CK(ss_dg_enqueue_export(e->c, int(g), e->ids_dev + 64 * g, int(e->n_ids), 0, e->s));
+    const int np = e->n_pred && g + 1 < e->G ? int(e->n_pred) : 0;
+    if (e->dg) TSE_CK(ss_dg_enqueue_export(e->c, int(g), e->ids_dev + 64 * g, int(e->n_ids), np, e->s));
+    if (e->dg && np) TSE_CK(ss_dg_enqueue_predict(e->c, int(g), e->pred_dev + 64 * g, np, e->s));
     if (e->dg) TSE_CK(ss_dg_enqueue_wait(e->c, int(g), e->s));
     if (e->checksum) {
       hipLaunchKernelGGL(checksum_dg, dim3(e->max_chunks, e->n_ids), dim3(kThreads), 0, e->s, e->view, g,
@@ -251,11 +256,22 @@ static ss_status tse_enqueue_token(TseDg* e) {
 // A device-gated engine: n_ids routed ids per gated layer per token, captured once into a hipGraph (use_graph = 1) or
 // enqueued per token. checksum = 0 leaves out the checksum kernels; dg = 0 leaves out the gating kernels (a baseline
 // graph for the wait overhead: the same checksum kernels, nothing gated).
+__attribute__((visibility("default"))) ss_status tse_dg_create_pred(ss_ctx* c, uint32_t n_ids, uint32_t n_pred,
+                                                                    int use_graph, int checksum, int dg, void** out);
 __attribute__((visibility("default"))) ss_status tse_dg_create(ss_ctx* c, uint32_t n_ids, int use_graph, int checksum,
                                                                int dg, void** out) {
+  return tse_dg_create_pred(c, n_ids, 0, use_graph, checksum, dg, out);
+}
+
+// As tse_dg_create, with n_pred (<= 64) ids predicted at every gated layer but the last for the next one (each token's
+// predictions come with its routes, tse_dg_token_pred).
+__attribute__((visibility("default"))) ss_status tse_dg_create_pred(ss_ctx* c, uint32_t n_ids, uint32_t n_pred,
+                                                                    int use_graph, int checksum, int dg, void** out) {
+  if (n_ids < 1 || n_ids > 64 || n_pred > 64) return SS_E_INVALID;
   auto* e = new TseDg;
   e->c = c;
   e->n_ids = n_ids;
+  e->n_pred = n_pred;
   e->checksum = checksum != 0;
   e->dg = dg != 0;
   ss_status st = ss_dg_get_device_view(c, &e->view);
@@ -268,13 +284,15 @@ __attribute__((visibility("default"))) ss_status tse_dg_create(ss_ctx* c, uint32
   for (uint32_t p = 0; p < e->view.n_parts; ++p) chunks += chunks_of(e->view.parts[p].bytes);
   e->max_chunks = chunks;
   if (hipStreamCreateWithFlags(&e->s, hipStreamNonBlocking) != hipSuccess ||
-      hipMalloc(&e->ids_dev, 4ull * 64 * e->G) != hipSuccess || hipMalloc(&e->out_dev, 8ull * 64 * e->G) != hipSuccess ||
+      hipMalloc(&e->ids_dev, 4ull * 64 * e->G) != hipSuccess || hipMalloc(&e->pred_dev, 4ull * 64 * e->G) != hipSuccess ||
+      hipMalloc(&e->out_dev, 8ull * 64 * e->G) != hipSuccess ||
       hipMalloc(&e->start_dev, 8ull * e->G) != hipSuccess) {
     delete e;
     return SS_E_NOMEM;
   }
   (void)hipMemset(e->out_dev, 0, 8ull * 64 * e->G);
   (void)hipMemset(e->ids_dev, 0, 4ull * 64 * e->G);
+  (void)hipMemset(e->pred_dev, 0, 4ull * 64 * e->G);
   (void)hipMemset(e->start_dev, 0, 8ull * e->G);
   if (use_graph) {
     st = ck(hipStreamBeginCapture(e->s, hipStreamCaptureModeThreadLocal));
@@ -295,13 +313,28 @@ __attribute__((visibility("default"))) ss_status tse_dg_create(ss_ctx* c, uint32
 
 // One token: routes (host, [G][n_ids]) uploaded, ss_begin, the graph (or the kernels), ss_end. checksums
 // ([G][n_ids]) and token_ms (begin -> end) may be NULL.
+__attribute__((visibility("default"))) ss_status tse_dg_token_pred(void* h, const int32_t* routes, const int32_t* preds,
+                                                                   uint64_t* checksums, double* token_ms);
 __attribute__((visibility("default"))) ss_status tse_dg_token(void* h, const int32_t* routes, uint64_t* checksums,
                                                               double* token_ms) {
+  return tse_dg_token_pred(h, routes, nullptr, checksums, token_ms);
+}
+
+// preds ([G][n_pred], row g for layer g + 1; the last row unused) may be NULL: zeros are predicted then.
+__attribute__((visibility("default"))) ss_status tse_dg_token_pred(void* h, const int32_t* routes, const int32_t* preds,
+                                                                   uint64_t* checksums, double* token_ms) {
   TseDg* e = static_cast<TseDg*>(h);
   std::vector<int32_t> ids(size_t(64) * e->G, 0);
   for (uint32_t g = 0; g < e->G; ++g)
     for (uint32_t i = 0; i < e->n_ids; ++i) ids[64 * g + i] = routes[size_t(g) * e->n_ids + i];
   TSE_HIP(hipMemcpyAsync(e->ids_dev, ids.data(), 4ull * ids.size(), hipMemcpyHostToDevice, e->s));
+  if (e->n_pred) {
+    std::vector<int32_t> pv(size_t(64) * e->G, 0);
+    for (uint32_t g = 0; preds && g < e->G; ++g)
+      for (uint32_t i = 0; i < e->n_pred; ++i) pv[64 * g + i] = preds[size_t(g) * e->n_pred + i];
+    TSE_HIP(hipMemcpyAsync(e->pred_dev, pv.data(), 4ull * pv.size(), hipMemcpyHostToDevice, e->s));
+    TSE_HIP(hipStreamSynchronize(e->s));  // (pv is a local)
+  }
   if (e->checksum) TSE_HIP(hipMemsetAsync(e->out_dev, 0, 8ull * 64 * e->G, e->s));
   TSE_HIP(hipStreamSynchronize(e->s));
   const auto t0 = std::chrono::steady_clock::now();

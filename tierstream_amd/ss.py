@@ -224,6 +224,10 @@ def engine() -> C.CDLL:
         E.tse_dg_create.argtypes = [vp, u32, C.c_int, C.c_int, C.c_int, C.POINTER(vp)]
         E.tse_dg_token.restype = C.c_int
         E.tse_dg_token.argtypes = [vp, C.POINTER(i32), C.POINTER(u64), C.POINTER(C.c_double)]
+        E.tse_dg_create_pred.restype = C.c_int
+        E.tse_dg_create_pred.argtypes = [vp, u32, u32, C.c_int, C.c_int, C.c_int, C.POINTER(vp)]
+        E.tse_dg_token_pred.restype = C.c_int
+        E.tse_dg_token_pred.argtypes = [vp, C.POINTER(i32), C.POINTER(i32), C.POINTER(u64), C.POINTER(C.c_double)]
         E.tse_dg_stamps.restype = C.c_int
         E.tse_dg_stamps.argtypes = [vp, C.POINTER(u64)]
         E.tse_dg_set_rows.restype = C.c_int
@@ -454,28 +458,36 @@ class Ctx:
 class DgEngine:
     """A graph-captured device-gated engine over a context (tse_dg_*)."""
 
-    def __init__(self, ctx: Ctx, n_ids: int, use_graph=True, checksum=True, gated=True):
+    def __init__(self, ctx: Ctx, n_ids: int, use_graph=True, checksum=True, gated=True, n_pred=0):
+        """n_pred: ids predicted at every gated layer but the last for the next one (ss_dg_enqueue_predict)."""
         E = engine()
         self.h = vp()
         self.G = ctx.dg_view().n_gated
         self.n_ids = n_ids
-        check(E.tse_dg_create(ctx.h, n_ids, int(use_graph), int(checksum), int(gated), C.byref(self.h)))
+        self.n_pred = n_pred
+        check(E.tse_dg_create_pred(ctx.h, n_ids, n_pred, int(use_graph), int(checksum), int(gated), C.byref(self.h)))
 
-    def token(self, routes: np.ndarray, want_checksums=True):
-        """routes int32 [G][n_ids]; returns (checksums [G][n_ids] or None, ms)."""
-        st, cks, ms = self.token_status(routes, want_checksums)
+    def token(self, routes: np.ndarray, want_checksums=True, preds=None):
+        """routes int32 [G][n_ids]; preds int32 [G][n_pred] (row g for layer g + 1); returns (checksums [G][n_ids]
+        or None, ms)."""
+        st, cks, ms = self.token_status(routes, want_checksums, preds)
         check(st)
         return cks, ms
 
-    def token_status(self, routes: np.ndarray, want_checksums=True):
+    def token_status(self, routes: np.ndarray, want_checksums=True, preds=None):
         """As token(), without raising: (status, checksums, ms); a failed token's checksums are still read back."""
         E = engine()
         r = np.ascontiguousarray(routes, dtype=np.int32)
         assert r.shape == (self.G, self.n_ids)
+        p = None
+        if preds is not None:
+            p = np.ascontiguousarray(preds, dtype=np.int32)
+            assert p.shape == (self.G, self.n_pred)
         cks = np.zeros((self.G, self.n_ids), dtype=np.uint64) if want_checksums else None
         ms = C.c_double(0)
-        st = E.tse_dg_token(self.h, r.ctypes.data_as(C.POINTER(i32)),
-                            cks.ctypes.data_as(C.POINTER(u64)) if want_checksums else None, C.byref(ms))
+        st = E.tse_dg_token_pred(self.h, r.ctypes.data_as(C.POINTER(i32)),
+                                 p.ctypes.data_as(C.POINTER(i32)) if p is not None else None,
+                                 cks.ctypes.data_as(C.POINTER(u64)) if want_checksums else None, C.byref(ms))
         return int(st), cks, ms.value
 
     def set_rows(self, rows: int):
