@@ -334,15 +334,17 @@ def test_three_tier_read_failure_fails_the_token(tmp_path, gpu, queue):
 BIG_PARTS = (8 * 1024 * KiB + 64 * KiB, 64 * KiB, 4 * 1024 * KiB)
 
 
-@pytest.mark.parametrize("clean_evict,queue,parts", [(0, 0, None), (1, 0, None), (0, 4, None), (1, 4, None),
-                                                     (0, 3, BIG_PARTS)])
-def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts):
+@pytest.mark.parametrize("clean_evict,queue,parts,predict", [(0, 0, None, 0), (1, 0, None, 0), (0, 4, None, 0),
+                                                             (1, 4, None, 0), (0, 3, BIG_PARTS, 0), (0, 4, None, 2),
+                                                             (0, 0, None, 2)])
+def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, predict):
     """Three tiers (dg_disk_tier): 12 of 32 units resident, 10 pinned, 10 read from the file on a miss through staging
     buffers. The plan's tiers are given explicitly (a planner spill to the file tier leaves no room for spare blocks,
     as in the reference). Every token the slot table and the counters (file reads, drops of the pinned LRU to the
     file, discards) must equal the reference core's, and every routed unit the engine read must checksum to the
     file's bytes; every landed unit is re-hashed in HBM (verify_hash 2). dg_disk_queue 4: the reads run on reader
-    threads and each copy out of a staging buffer awaits its read on the device; the placement is the same."""
+    threads and each copy out of a staging buffer awaits its read on the device; the placement is the same. predict:
+    the engine predicts the next layer's ids and dg_disk_prefetch lets a prefetch read a file-homed unit."""
     parts = list(parts or (64 * KiB,) * 3)
     layers, units, n_ids, staging, dyn, spares = 4, 8, 2, 4, 1, 6
     m, tiers, bkw = _three_tier(tmp_path, parts)
@@ -355,22 +357,27 @@ def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts):
     # spare slots: dyn per layer, capped by the layer's non-resident units (layer 0 is all resident here)
     D = sum(min(dyn, sum(1 for u in range(units) if tiers[L * units + u] != 0)) for L in range(layers))
     flags = [1 if t == 2 else 0 for t in tiers]
+    dpf = 1 if predict else 0
     refdg = ref.RefDg([units] * layers, 12 + D, n_ids, 10 + Q, D, parts, residents + list(range(keys)),
-                      disk=dict(flags=flags, home_blocks=10, disk_staging=staging, clean_evict=clean_evict))
+                      disk=dict(flags=flags, home_blocks=10, disk_staging=staging, clean_evict=clean_evict,
+                                disk_prefetch=dpf))
     ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(forward_mode=1, dg_max_ids=n_ids, pin_planned=0, verify_hash=2,
                                                       dg_disk_tier=1, dg_disk_staging=staging,
                                                       dg_clean_evict=clean_evict, dg_disk_queue=queue,
-                                                      dg_wait_timeout_ms=5000))
-    eng = ss.DgEngine(ctx, n_ids, use_graph=True)
+                                                      dg_disk_prefetch=dpf, dg_wait_timeout_ms=5000))
+    eng = ss.DgEngine(ctx, n_ids, use_graph=True, n_pred=predict)
     routes = _routes(layers, units, n_ids, 24, seed=9, zipf=True)
+    preds = _preds(routes, units, predict) if predict else None
     expect = {(L, u): fixtures.engine_checksum(m.unit_data(L, u)) for L in range(layers) for u in range(units)}
-    counters = COUNTERS + ["disk_reads", "disk_drops", "disk_discards", "clean_drops"]
+    counters = COUNTERS + ["disk_reads", "disk_drops", "disk_discards", "clean_drops"] + \
+        (PRED_COUNTERS if predict else [])
     with pytest.raises(ss.SsError):
         ctx.snapshot()
     try:
         for t in range(routes.shape[0]):
-            cks, _ = eng.token(routes[t])
-            want_table, want = refdg.token(routes[t].astype(np.uint32))
+            cks, _ = eng.token(routes[t], preds=preds[t] if predict else None)
+            want_table, want = refdg.token(routes[t].astype(np.uint32),
+                                           pred=preds[t].astype(np.uint32) if predict else None)
             got = ctx.dg_stats()
             assert np.array_equal(ctx.dg_table(), want_table), (t, "table")
             for k in counters:
