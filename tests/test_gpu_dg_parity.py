@@ -183,6 +183,11 @@ def test_dg_matches_reference(name, tmp_path, gpu):
             assert got["prefetched"] > 0 and got["prefetch_used"] > 0 and got["pred_invalid"] > 0
         _check_stats_doc(ctx, want, tokens, policy=["lru", "scored", "auto"][policy],
                          prov="test fit" if score.get("profile") else None, publications=tokens + len(switch))
+        with pytest.raises(ss.SsError):
+            ctx.dg_set_policy(3)  # no such policy
+        if not score:
+            with pytest.raises(ss.SsError):
+                ctx.dg_set_policy(1)  # an LRU open has no score tables
     finally:
         eng.close()
         ctx.close()
