@@ -236,6 +236,7 @@ void HostCtx::init() {
     hip_check(hipMemsetAsync(vfail_dev_, 0, vcap_ * 4, copy_), "hipMemsetAsync");
     vdone_ev_ = dev_->event_create();
     vready_ev_ = dev_->event_create();
+    vready2_ev_ = dev_->event_create();
     vstream_ = dev_->stream_create_dedicated();
     stream_sync(copy_);  // (the zeroed results before any check on the verify stream)
   }
@@ -320,6 +321,7 @@ void HostCtx::cleanup() noexcept {
   dev_->free_device(vfail_dev_);
   dev_->event_destroy(vdone_ev_);
   dev_->event_destroy(vready_ev_);
+  dev_->event_destroy(vready2_ev_);
   for (hipEvent_t e : vflush_ev_) dev_->event_destroy(e);
   if (vstream_) dev_->stream_destroy(vstream_);
   dev_->event_destroy(join_ev_);
@@ -660,9 +662,10 @@ void HostCtx::flush_verify() {
     vtable_host_[i].seg_first = segs;
     segs += count;
   }
-  join_copies();
-  ev_record(vready_ev_, copy_);
+  ev_record(vready_ev_, copy_);  // (the verify stream follows both copy streams; neither waits for the other)
+  ev_record(vready2_ev_, copy2_);
   stream_wait(vstream_, vready_ev_);
+  stream_wait(vstream_, vready2_ev_);
   tsa_verify_unit* vd = static_cast<tsa_verify_unit*>(vtable_dev_) + vflushed_;
   copy_h2d(vd, vtable_host_ + vflushed_, n * sizeof(tsa_verify_unit), vstream_);
   hip_check(hipError_t(launch_verify(vd, uint32_t(n), segs, seg_bytes_, vfail_dev_ + vflushed_, vstream_)),

@@ -226,6 +226,7 @@ class HostCtx {
   uint32_t* vfail_host_ = nullptr;
   size_t vcap_ = 0, vused_ = 0, vflushed_ = 0;  // table slots used this forward; the ones already launched
   hipStream_t vstream_ = nullptr;                 // the checks (copies never queue behind them)
+  hipEvent_t vready2_ev_ = nullptr;               // the second copy stream at a flush
   hipEvent_t vready_ev_ = nullptr;                // the copy stream at a flush: the batch's copies are done
   std::vector<std::pair<int, int>> vunits_;  // (layer, unit) of each verify slot this forward
   // A landed unit's check reads its slot until the check's launch completes, so the next copy into that slot waits for
