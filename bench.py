@@ -288,15 +288,17 @@ def measure_kernels(tsa, L, C, w, seg=8192, reps=10):
 
 
 # ---- the CPU baseline -----------------------------------------------------------------------------------------------
-def cpu_baseline(w, shape, files, hashes, routes, start, est_token_s, seconds):
-    """The reference DgCore on a memcpy transport (oracle/_ref), over tokens start.. of the same route stream. files:
-    [(path, first layer, layers)] as the descriptor's sources."""
+def cpu_baseline(w, shape, files, hashes, routes, start, est_token_s, seconds, policy=0):
+    """The reference DgCore on a memcpy transport (oracle/_ref), over tokens start.. of the same route stream, under
+    the same eviction policy (0 LRU, 1 SCORED, 2 SCORED_AUTO). files: [(path, first layer, layers)] as the
+    descriptor's sources."""
     try:
         from oracle import ref
     except Exception as e:  # noqa: BLE001
         return None, f"oracle unavailable: {e}"
     if not ref.available():
         return None, "oracle/_ref is not built"
+    ref.lib().refdg_cpu_baseline_policy(policy)
     from tierstream_amd import workloads as W
     n_tok = int(max(3, min(64, seconds / max(est_token_s, 1e-3))))
     n_tok = min(n_tok, routes.shape[0] - start)
@@ -561,12 +563,9 @@ def main():
                 "note": "read_GBps_wall: file-tier bytes read over the timed region's wall clock; the reads run on "
                         "reader threads while earlier copies and layers proceed (the service waits only before a "
                         "layer's ready word)"}
-        if a.policy != "lru":  # the baseline driver runs the reference core under LRU only
-            result["cpu_baseline"] = None
-            result["cpu_baseline_note"] = "not sampled: the CPU baseline driver runs the LRU policy"
-        elif not a.no_cpu:
+        if not a.no_cpu:
             est = float(np.median(lat)) / 1e3 * 20  # a first guess of the CPU's time per token
-            got, why = cpu_baseline(w, shape, files, hashes, routes, warm, est, a.cpu_seconds)
+            got, why = cpu_baseline(w, shape, files, hashes, routes, warm, est, a.cpu_seconds, policy=policy)
             if got:
                 ms, c, n_tok = got
                 result["cpu_baseline"] = {
@@ -577,7 +576,8 @@ def main():
                               f"placement: reference DgCore + memcpy transport + host XXH64 of each landed unit"
                               + (", file-tier units read synchronously with direct I/O into staging buffers"
                                  if three else "")
-                              + f", 1 thread; misses {c['misses']}, hash mismatches {c['hash_mismatches']}"
+                              + f", 1 thread, policy {a.policy}; misses {c['misses']}, hash mismatches "
+                                f"{c['hash_mismatches']}"
                               + (f", file reads {c['disk_reads']}" if three else ""),
                     "cpu": cpu_model(), "nproc": os.cpu_count()}
             else:

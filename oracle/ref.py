@@ -69,6 +69,7 @@ def lib() -> C.CDLL:
                                        C.POINTER(u32), u32, u32, u32, u32, u32, u32, C.POINTER(u32), u32, u32, u32,
                                        C.POINTER(C.c_uint8)]),
             "refdg_set_policy": (C.c_int, [vp, u32]),
+            "refdg_cpu_baseline_policy": (None, [u32]),
             "refdg_profile_check": (C.c_int, [C.c_char_p, u64, C.POINTER(u32), u32, C.c_char_p]),
             "refdg_score_identity": (C.c_int, [u32, C.POINTER(u32), C.POINTER(u32), C.POINTER(u64), C.POINTER(u64),
                                                C.c_char_p]),

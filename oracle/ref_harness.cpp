@@ -497,6 +497,11 @@ int refdg_cpu_baseline_disk(const uint32_t* n_units, uint32_t G, uint32_t persis
                             uint32_t n_tokens, int setup_threads, const uint8_t* disk, uint32_t home_blocks,
                             uint32_t disk_staging, uint32_t clean_evict, double* token_ms, uint64_t* out);
 
+// The eviction policy of the next refdg_cpu_baseline* runs: 0 LRU, 1 SCORED, 2 SCORED_AUTO (the weights 700 / 200 /
+// 100, no profile; each layer closed after its service as the reference service closes it).
+static uint32_t g_baseline_policy = 0;
+void refdg_cpu_baseline_policy(uint32_t policy) { g_baseline_policy = policy; }
+
 int refdg_cpu_baseline(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
                        uint32_t spare_target, uint32_t wb_defer, uint32_t inclusive, const uint64_t* part_bytes,
                        uint32_t n_parts, uint64_t host_stride, const uint32_t* order, uint32_t n_order,
@@ -564,6 +569,11 @@ int refdg_cpu_baseline_disk(const uint32_t* n_units, uint32_t G, uint32_t persis
     c.inclusive = inclusive;
     c.max_ids = bank;
     c.pf_legacy = true;
+    if (g_baseline_policy) {
+      c.scored = true;
+      c.scored_auto = g_baseline_policy == 2;
+      c.boundary_score = true;
+    }
     uint32_t n_keys = 0;
     for (uint32_t g = 0; g < G; ++g) n_keys += n_units[g];
     std::vector<uint8_t> dflags;
@@ -635,6 +645,7 @@ int refdg_cpu_baseline_disk(const uint32_t* n_units, uint32_t G, uint32_t persis
         }
         core.serve_use(g, x, n, mask);
         if (core.deferred() && g + 1 < G) core.issue_writebacks(g, nullptr);
+        core.score_layer(g);  // (nothing under LRU)
       }
       core.end_token({}, 1);
       token_ms[tok] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();

@@ -11,8 +11,8 @@ pytestmark = pytest.mark.skipif(not ref.available(), reason="oracle/_ref not bui
 KiB = 1024
 
 
-@pytest.mark.parametrize("wb_defer,inclusive", [(1, 0), (0, 0), (1, 3)])
-def test_cpu_baseline_moves_the_right_bytes(tmp_path, wb_defer, inclusive):
+@pytest.mark.parametrize("wb_defer,inclusive,policy", [(1, 0, 0), (0, 0, 0), (1, 3, 0), (1, 0, 1), (0, 3, 1)])
+def test_cpu_baseline_moves_the_right_bytes(tmp_path, wb_defer, inclusive, policy):
     layers, units, parts, n_ids = 4, 8, [16 * KiB, 16 * KiB, 32 * KiB], 2
     m = fixtures.write_model(tmp_path, layers, units, parts, top_k=n_ids, seed=7)
     keys = layers * units
@@ -25,14 +25,19 @@ def test_cpu_baseline_moves_the_right_bytes(tmp_path, wb_defer, inclusive):
     ids = np.stack([np.stack([rng.choice(units, size=n_ids, replace=False) for _ in range(layers)])
                     for _ in range(tokens)]).astype(np.uint32)
     offsets = [g * m.stride for g in range(keys)]
-    ms, got = ref.cpu_baseline([units] * layers, len(residents) + D, n_ids, P + Q, D, parts, m.stride, order, m.path,
-                               offsets, m.hashes, ids, wb_defer=wb_defer, inclusive=inclusive, setup_threads=2)
+    ref.lib().refdg_cpu_baseline_policy(policy)  # (SCORED: the benchmark's --policy scored baseline)
+    try:
+        ms, got = ref.cpu_baseline([units] * layers, len(residents) + D, n_ids, P + Q, D, parts, m.stride, order,
+                                   m.path, offsets, m.hashes, ids, wb_defer=wb_defer, inclusive=inclusive,
+                                   setup_threads=2)
+    finally:
+        ref.lib().refdg_cpu_baseline_policy(0)
     assert ms.shape == (tokens,) and np.all(ms > 0)
     assert got["hash_mismatches"] == 0
     assert got["misses"] > 0 and got["evicted"] > 0
     assert got["copied_bytes"] == got["misses"] * m.unit_bytes
     eager = ref.RefDg([units] * layers, len(residents) + D, n_ids, P + Q, D, parts, order, wb_defer=wb_defer,
-                      inclusive=inclusive)
+                      inclusive=inclusive, score=dict(policy=policy) if policy else None)
     try:
         for t in range(tokens):
             _, want = eager.token(ids[t])
@@ -40,6 +45,8 @@ def test_cpu_baseline_moves_the_right_bytes(tmp_path, wb_defer, inclusive):
         eager.close()
     for k in ("misses", "fetched", "evicted", "writebacks_done"):
         assert got[k] == want[k], k
+    if policy:
+        assert want["scored_victims"] > 0
     if inclusive == 0:
         assert got["writebacks_done"] > 0                # exclusive: evictions write units back, and they re-land intact
 
