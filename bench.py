@@ -368,6 +368,12 @@ def main():
     cold_work = tempfile.mkdtemp(prefix="tsa_bench_", dir=a.disk_dir or tempfile.gettempdir()) if three else None
     cold_path = os.path.join(cold_work, "weights-file-tier.bin") if three else None
     result = {}
+    opened = []  # handles to close in reverse order on every path out (engine, context, plan, descriptor)
+
+    def keep(h):
+        opened.append(h)
+        return h
+
     try:
         t0 = time.time()
         log(f"workload {w.name}: {w.layers} x {w.units} units of {w.unit_bytes / 2**20:.1f} MiB, writing "
@@ -380,9 +386,9 @@ def main():
             hashes += W.write_sources_gpu(w, cold_path, first_layer=cold, drop_cache=True)
             files.append((cold_path, cold, w.layers - cold))
         log(f"sources written in {time.time() - t0:.1f} s")
-        d = ss.Desc(W.desc_json(w, files, hashes))
+        d = keep(ss.Desc(W.desc_json(w, files, hashes)))
         b = ss.budget(**shape.budget)
-        plan = ss.Plan(d, b, tiers=shape.tiers) if three else ss.Plan(d, b)
+        plan = keep(ss.Plan(d, b, tiers=shape.tiers) if three else ss.Plan(d, b))
         tiers = plan.tiers()
         n_res = sum(1 for r in tiers for t in r if t == 0)
         n_pin = sum(1 for r in tiers for t in r if t == 1)
@@ -396,9 +402,10 @@ def main():
             log(f"file tier drive: {disk_peak}")
         t0 = time.time()
         policy = {"lru": 0, "scored": 1, "auto": 2}[a.policy]
-        ctx = ss.Ctx(d, b, plan, ss.options(**shape.options, verify_hash=2, dg_wait_timeout_ms=20000, policy=policy))
+        ctx = keep(ss.Ctx(d, b, plan, ss.options(**shape.options, verify_hash=2, dg_wait_timeout_ms=20000,
+                                                 policy=policy)))
         log(f"context open (fill + hash check) in {time.time() - t0:.1f} s")
-        eng = ss.DgEngine(ctx, shape.B, use_graph=True)
+        eng = keep(ss.DgEngine(ctx, shape.B, use_graph=True))
         G = eng.G
         steps, warm, probe = a.steps, a.warmup, a.probe_tokens
         routes = W.route_stream(w, warm + steps + probe)[:, :, :shape.B]
@@ -583,6 +590,8 @@ def main():
             else:
                 log(f"cpu baseline skipped: {why}")
     finally:
+        for h in reversed(opened):  # (close is idempotent: the normal path closed them already)
+            h.close()
         shutil.rmtree(work, ignore_errors=True)
         if cold_work:
             shutil.rmtree(cold_work, ignore_errors=True)
@@ -598,6 +607,7 @@ def run_host(a, w, tsa, ss, W, L, C):
     work = tempfile.mkdtemp(prefix="tsa_bench_", dir=base)
     path = os.path.join(work, "weights.bin")
     result = {}
+    opened = []  # handles to close in reverse order on every path out
     try:
         t0 = time.time()
         log(f"workload {w.name}: {w.layers} x {w.units} units of {w.unit_bytes / 2**20:.1f} MiB, writing "
@@ -606,12 +616,15 @@ def run_host(a, w, tsa, ss, W, L, C):
         log(f"sources written in {time.time() - t0:.1f} s")
         desc_json = W.desc_json(w, path, hashes)
         d = ss.Desc(desc_json)
+        opened.append(d)
         b = ss.budget(**shape.budget)
         plan = ss.Plan(d, b)
+        opened.append(plan)
         tiers = plan.tiers()
         n_res = sum(1 for r in tiers for t in r if t == 0)
         t0 = time.time()
         ctx = ss.Ctx(d, b, plan, ss.options(**shape.options))
+        opened.append(ctx)
         log(f"context open in {time.time() - t0:.1f} s: {n_res} resident units, mode {shape.mode}, budget {shape.budget}")
         steps, warm = a.steps, a.warmup
         routes = W.route_stream(w, warm + steps)
@@ -685,6 +698,8 @@ def run_host(a, w, tsa, ss, W, L, C):
             except Exception as e:  # noqa: BLE001
                 log(f"cpu baseline skipped: {e}")
     finally:
+        for h in reversed(opened):
+            h.close()
         shutil.rmtree(work, ignore_errors=True)
     print(json.dumps(result), flush=True)
 

@@ -6,11 +6,14 @@ follows, used for comparison by tests/, __graft_entry__.smoke() and bench.py's c
 
 Contents:
   xxh64_oracle.c      XXH64 and the verify checkpoint layout (liboracle.so)
-  synth.py            the synthetic byte generator (numpy) and fixture writers
-  plan_model.py       desc-v1 validation subset, unit strides, plan_make / plan_from_tiers (reference src/plan.cpp)
-  host_model.py       the host-contract forward on a CPU backend (reference src/stream_ctx.cpp, src/resident_set.cpp)
-  dg_model.py         the device-gated LRU cache state machine with an immediate transport (reference src/dg_core.cpp)
-  _ref/ (built)       the reference's own CPU library compiled from its sources (Makefile target `ref`)
+  synth.py            the synthetic byte generator (numpy): the words the product's device generator must give
+  fixtures.py         small synthetic models (source file + desc-v1 JSON), engine checksums, route streams
+  score_profile.py    TSSCPRF1 score-profile writer (hashlib SHA-256)
+  ref.py              ctypes driver of _ref/libtsref_harness.so: the reference's CPU backend through its C ABI, and its
+                      DgCore on an immediate transport (placement oracle) or a memcpy transport (the CPU baseline)
+  ref_harness.cpp     the C++ side of that driver (compiled against the reference's sources, never copied)
+  _ref/ (built)       libtsref.so and libtsref_harness.so: the reference's own CPU library compiled from its sources by
+                      the Makefile (target `ref`), and the harness linked with it
 """
 from __future__ import annotations
 
@@ -20,7 +23,6 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 LIB = HERE / "liboracle.so"
 REF_LIB = HERE / "_ref" / "libtsref.so"
-REF_DG_LIB = HERE / "_ref" / "libtsref_dg.so"
 
 _olib = None
 

@@ -30,6 +30,7 @@ class Model:
     seed: int = 99
     hashes: list = field(default_factory=list)
     tiers: str = "pinned"  # the descriptor's tier list ("pinned|disk": the planner spills to the file tier)
+    checksums: list = field(default_factory=list)  # engine_checksum of each unit, in unit order (at write time)
 
     @property
     def unit_bytes(self):
@@ -42,6 +43,10 @@ class Model:
     def unit_data(self, L: int, u: int) -> np.ndarray:
         g = L * self.units + u
         return np.concatenate([synth.uniform_bytes(self.seed, 4 * g + p, 0, pb) for p, pb in enumerate(self.parts)])
+
+    def checksum(self, L: int, u: int) -> int:
+        """engine_checksum of unit (L, u)'s bytes as written."""
+        return self.checksums[L * self.units + u]
 
     def desc_json(self) -> str:
         layers = []
@@ -72,6 +77,7 @@ def write_model(directory, layers, units, parts, kind="moe", top_k=2, order="ran
             for u in range(units):
                 b = m.unit_data(L, u)
                 m.hashes.append(xxh64(b))
+                m.checksums.append(engine_checksum(b))
                 f.write(b.tobytes())
                 f.write(b"\0" * (m.stride - m.unit_bytes))
     return m

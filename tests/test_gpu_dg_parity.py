@@ -18,6 +18,7 @@ from tierstream_amd import ss
 pytestmark = pytest.mark.gpu
 
 KiB = 1024
+MiB = 1024 * KiB
 COUNTERS = ["lookups", "misses", "covered", "fetched", "resurrected", "bank_serves", "evicted", "evict_short",
             "wb_deferred", "wb_cancelled", "wb_boundary_flushed", "inclusive_kept", "inclusive_drops"]
 
@@ -78,6 +79,23 @@ CASES = {
                             predict=2, score=dict(policy=1)),
     "scored-switch": dict(layers=4, units=16, parts=[64 * KiB] * 3, n_res=24, dyn=2, spares=12, n_ids=4, tokens=30,
                           score=dict(policy=1, switch=[(10, 0), (20, 2)])),
+    # every part at least 8 MiB, as in the Mixtral shape: a miss is one SDMA copy per part straight into its arena
+    # slot, each behind the copy out of that part of the slot's previous unit (deferred write-backs, boundary
+    # write-backs, clean copies)
+    "big-parts": dict(layers=4, units=8, parts=[8 * MiB] * 3, n_res=12, dyn=1, spares=6, n_ids=2, tokens=16),
+    "big-parts-boundary-wb": dict(layers=4, units=8, parts=[8 * MiB, 12 * MiB, 8 * MiB], n_res=10, dyn=1, spares=8,
+                                  n_ids=2, tokens=16, wb_defer=0, zipf=False),
+    "big-parts-clean": dict(layers=4, units=8, parts=[8 * MiB] * 3, n_res=12, dyn=1, spares=8, n_ids=2, tokens=16,
+                            inclusive=4),
+    # one part: one copy per miss, whatever its size
+    "single-part": dict(layers=3, units=16, parts=[256 * KiB], n_res=12, dyn=2, spares=10, n_ids=4, tokens=20,
+                        wb_defer=0, zipf=False),
+    # resident-first reads before every wait (ss_dg_slot_if_ready; reference tests/test_dg_cuda.cu:155-172,
+    # :1122-1139): a published slot's checksum must be exact; some ids are ready early and some are not
+    "early-reads": dict(layers=4, units=16, parts=[64 * KiB] * 3, n_res=24, dyn=2, spares=12, n_ids=4, tokens=24,
+                        early=True),
+    "early-reads-prefetch": dict(layers=4, units=16, parts=[64 * KiB] * 3, n_res=24, dyn=2, spares=12, n_ids=4,
+                                 tokens=24, predict=3, early=True),
 }
 SCORE_COUNTERS = ["score_fallbacks", "scored_victims", "score_layers", "score_candidates", "score_saturated"]
 PRED_COUNTERS = ["prefetched", "prefetch_used", "pred_invalid", "predicted", "predicted_true", "wb_cancelled"]
@@ -116,6 +134,7 @@ def test_dg_matches_reference(name, tmp_path, gpu):
     use_graph = c.pop("graph", True)
     score = dict(c.pop("score", {}))
     predict = c.pop("predict", 0)
+    early = c.pop("early", False)
     m, bkw, okw = _setup(tmp_path, c["layers"], c["units"], c["parts"], c["n_res"], c["dyn"], c["spares"], c["n_ids"],
                          inclusive=c.get("inclusive", 0), wb_defer=c.get("wb_defer", 1))
     ref_score, keep = None, []
@@ -148,14 +167,15 @@ def test_dg_matches_reference(name, tmp_path, gpu):
                       residents + list(range(keys)), wb_defer=c.get("wb_defer", 1), inclusive=c.get("inclusive", 0),
                       score=ref_score)
     ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(**okw))
-    eng = ss.DgEngine(ctx, c["n_ids"], use_graph=use_graph, n_pred=predict)
+    eng = ss.DgEngine(ctx, c["n_ids"], use_graph=use_graph, n_pred=predict, early=early)
     preds = _preds(routes, c["units"], predict) if predict else None
+    early_ready = early_total = 0
     if score.get("rows", 1) > 1:
         eng.set_rows(score["rows"])
     switch = dict(score.get("switch", []))
     policy = score.get("policy", 0)
     counters = COUNTERS + (SCORE_COUNTERS if score else []) + (PRED_COUNTERS if predict else [])
-    expect = {(L, u): fixtures.engine_checksum(m.unit_data(L, u)) for L in range(c["layers"]) for u in range(c["units"])}
+    expect = {(L, u): m.checksum(L, u) for L in range(c["layers"]) for u in range(c["units"])}
     with pytest.raises(ss.SsError):  # arms the stats snapshot: each token's boundary publishes from now on
         ctx.snapshot()
     try:
@@ -174,7 +194,19 @@ def test_dg_matches_reference(name, tmp_path, gpu):
             for L in range(c["layers"]):
                 for i, u in enumerate(routes[t, L]):
                     assert int(cks[L, i]) == expect[(L, int(u))], (name, t, L, i)
+            if early:
+                esum, ready = eng.early()
+                for L in range(c["layers"]):
+                    for i, u in enumerate(routes[t, L]):
+                        early_total += 1
+                        if ready[L, i]:
+                            early_ready += 1
+                            assert int(esum[L, i]) == expect[(L, int(u))], (name, t, L, i, "early read")
+                        else:
+                            assert int(esum[L, i]) == 0, (name, t, L, i)
         assert got["tokens"] == tokens and got["misses"] > 0
+        if early:
+            assert 0 < early_ready < early_total, (early_ready, early_total)
         if score and score["policy"] == 1:
             assert got["scored_victims"] > 0 and got["score_fallbacks"] == 0
         if score.get("profile"):

@@ -15,6 +15,7 @@ from tierstream_amd import ss
 pytestmark = pytest.mark.gpu
 
 KiB = 1024
+MiB = 1024 * KiB
 
 
 def _budget(m, n_res, ring_slots, dyn=0, **kw):
@@ -42,6 +43,17 @@ CASES = {
     # the SCORED policy (reference src/resident_set.cpp:52-68: 0.7 transition + 0.2 window frequency + 0.1 recency)
     "decode-scored": dict(layers=4, units=8, parts=[32 * KiB, 32 * KiB, 16 * KiB], n_res=8, ring=16, dyn=2, steps=24,
                           top_k=2, mode=0, opts=dict(pin_planned=0, policy=1, score_window=6)),
+    # the reference's CPU-runnable config at full size: 4 x 8 experts of 3 x 1 MiB, top-2 uniform, half resident
+    # (layers 0-1), the other half served from the pinned tier through an 8-slot ring, 64 steps
+    "c1-full": dict(layers=4, units=8, parts=[1 * MiB] * 3, n_res=16, ring=8, steps=64, top_k=2, mode=0, opts={}),
+    # pinned copies in several pieces (copy_piece_bytes below the unit): 256 KiB units in 64 KiB pieces, and the
+    # exclusive shape's 96 KiB units in 40 KiB pieces (a short last piece)
+    "multi-piece": dict(layers=4, units=8, parts=[96 * KiB, 96 * KiB, 64 * KiB], n_res=8, ring=16, dyn=2, steps=24,
+                        top_k=2, mode=0, opts=dict(pin_planned=0, copy_piece_bytes=64 * KiB)),
+    "multi-piece-exclusive": dict(layers=6, units=16, parts=[32 * KiB] * 3, n_res=24, ring=32, dyn=2, steps=20,
+                                  top_k=4, tokens=4, mode=2,
+                                  opts=dict(pin_planned=0, group_units=2, copy_piece_bytes=40 * KiB),
+                                  budget=dict(tier_mode=1, host_spare_units=6)),
     "qwen-exclusive-scored": dict(layers=6, units=16, parts=[32 * KiB] * 3, n_res=24, ring=32, dyn=2, steps=20,
                                   top_k=4, tokens=4, mode=2, opts=dict(pin_planned=0, group_units=2, policy=1),
                                   budget=dict(tier_mode=1, host_spare_units=6)),
@@ -72,7 +84,7 @@ def _run_case(name, tmp_path, gpu):
                 got_tab = [ctx.region_of(int(a)) if a else (0, -1, 0) for a in tabs[s, l, :c["units"]]]
                 assert got_tab == w["tables"][l], (name, s, l)
                 ids = list(range(c["units"])) if c["mode"] == 1 else [int(x) for x in routes[s, l] if x >= 0]
-                exp = [fixtures.engine_checksum(m.unit_data(l, u)) for u in ids]
+                exp = [m.checksum(l, u) for u in ids]
                 assert [int(x) for x in cks[s, l, :len(ids)]] == exp == w["checksums"][l], (name, s, l)
         return ctx, want
     except Exception:
@@ -106,7 +118,7 @@ def test_host_contract_matches_reference(name, tmp_path, gpu):
     ctx.close()
 
 
-@pytest.mark.parametrize("name", ["decode-lru", "dense-prefix", "qwen-exclusive"])
+@pytest.mark.parametrize("name", ["decode-lru", "dense-prefix", "qwen-exclusive", "c1-full", "multi-piece"])
 def test_device_verify_of_landed_units(name, tmp_path, gpu):
     """verify_hash = 2: every landed unit re-hashed in HBM (checkpoint-parallel) against the descriptor; none fails.
     The checks run in batches on their own stream, so a slot reused inside a forward (dense-prefix: 5 layers through a

@@ -4,6 +4,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <fstream>
+#include <mutex>
 #include <sstream>
 
 #include "capi_internal.hpp"
@@ -22,6 +23,43 @@ void ctx_poison(ss_ctx* c) {
 }
 
 namespace {
+
+// Contexts open now, in open order. A process that exits with one still open (an engine that failed and never called
+// ss_close) would otherwise tear the HIP runtime down under a live service thread, reader threads and streams: the
+// first ss_open registers an exit handler, and handlers registered after a library was loaded run before that
+// library's own finalizers, so the handler closes what is left while the runtime still works. A handler never throws.
+std::mutex g_open_mu;
+std::vector<ss_ctx*>* g_open = nullptr;  // allocated once and never freed: it is read by the exit handler
+
+void close_open_contexts() noexcept {
+  std::vector<ss_ctx*> left;
+  {
+    std::lock_guard<std::mutex> lk(g_open_mu);
+    if (g_open) left.swap(*g_open);
+  }
+  for (auto it = left.rbegin(); it != left.rend(); ++it) {
+    try {
+      delete *it;
+    } catch (...) {
+    }
+  }
+}
+
+void track_open(ss_ctx* c) {
+  std::lock_guard<std::mutex> lk(g_open_mu);
+  if (!g_open) {
+    g_open = new std::vector<ss_ctx*>();
+    std::atexit(close_open_contexts);
+  }
+  g_open->push_back(c);
+}
+
+void untrack(ss_ctx* c) {
+  std::lock_guard<std::mutex> lk(g_open_mu);
+  if (!g_open) return;
+  const auto it = std::find(g_open->begin(), g_open->end(), c);
+  if (it != g_open->end()) g_open->erase(it);
+}
 
 void budget_defaults(ss_budget* b) {
   std::memset(static_cast<void*>(b), 0, sizeof *b);
@@ -248,11 +286,16 @@ ss_status ss_open(const ss_desc* d, const ss_budget* budget, const ss_plan* plan
       need(o.policy == SS_POLICY_LRU || o.policy == SS_POLICY_SCORED, "ss_open: SCORED_AUTO needs device-gated mode");
       c->host = std::make_unique<HostCtx>(d->d, bb, p, o);
     }
+    track_open(c.get());
     *out = c.release();
   });
 }
 
-void ss_close(ss_ctx* c) { delete c; }
+void ss_close(ss_ctx* c) {
+  if (!c) return;
+  untrack(c);
+  delete c;
+}
 
 int ss_source_direct(const ss_ctx* c, int source) {
   if (!c) return -1;

@@ -104,6 +104,27 @@ __global__ __launch_bounds__(kThreads) void checksum_dg(ss_dg_device_view v, uin
   }
 }
 
+// Resident-first reads before layer g's wait (ss_dg_slot_if_ready): one workgroup per routed id resolves the slot
+// once; a published slot's unit is checksummed in full into out[i] and ready[i] = 1, an unpublished one leaves both 0.
+// A slot entry is published only once its unit's bytes are complete, so every ready checksum must be exact.
+__global__ __launch_bounds__(kThreads) void checksum_early_dg(ss_dg_device_view v, uint32_t g, const int32_t* ids,
+                                                              unsigned long long* out, uint32_t* ready) {
+  __shared__ int32_t slot_s;
+  if (threadIdx.x == 0) slot_s = ss_dg_slot_if_ready(&v, g, ids[blockIdx.x]);
+  __syncthreads();
+  const int32_t slot = slot_s;
+  if (slot < 0) return;
+  uint64_t word0 = 0, s = 0;
+  for (uint32_t p = 0; p < v.n_parts; ++p) {
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(static_cast<const char*>(v.parts[p].base) +
+                                                             uint64_t(slot) * v.parts[p].stride);
+    s += sum_words(base, word0, v.parts[p].bytes / 4);
+    word0 += v.parts[p].bytes / 4;
+  }
+  block_add(s, out + blockIdx.x);
+  if (threadIdx.x == 0) ready[blockIdx.x] = 1;
+}
+
 ss_status ck(hipError_t e) { return e == hipSuccess ? SS_OK : SS_E_BACKEND; }
 #define TSE_CK(x)                                          \
   do {                                                     \
@@ -215,11 +236,14 @@ struct TseDg {
   uint32_t n_pred = 0;  // ids predicted at each layer for the next one (0: no predictions)
   uint32_t rows = 1;  // the verify rows each token closes (above one: ss_dg_end_rows instead of ss_end)
   bool checksum = true, dg = true;
+  bool early = false;  // resident-first reads before every wait (checksum_early_dg)
   hipStream_t s = nullptr;
   int32_t* ids_dev = nullptr;               // [G][64]
   int32_t* pred_dev = nullptr;              // [G][64]: row g predicts layer g + 1
   unsigned long long* out_dev = nullptr;    // [G][64]
   unsigned long long* start_dev = nullptr;  // [G]: wall clock at each layer's first checksum workgroup
+  unsigned long long* early_dev = nullptr;  // [G][64]: resident-first checksums
+  uint32_t* ready_dev = nullptr;            // [G][64]: 1 where the early read found a published slot
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   ss_dg_device_view view{};
@@ -232,6 +256,8 @@ struct TseDg {
     (void)hipFree(pred_dev);
     (void)hipFree(out_dev);
     (void)hipFree(start_dev);
+    (void)hipFree(early_dev);
+    (void)hipFree(ready_dev);
     if (s) (void)hipStreamDestroy(s);
   }
 };
@@ -242,6 +268,11 @@ static ss_status tse_enqueue_token(TseDg* e) {
     const int np = e->n_pred && g + 1 < e->G ? int(e->n_pred) : 0;
     if (e->dg) TSE_CK(ss_dg_enqueue_export(e->c, int(g), e->ids_dev + 64 * g, int(e->n_ids), np, e->s));
     if (e->dg && np) TSE_CK(ss_dg_enqueue_predict(e->c, int(g), e->pred_dev + 64 * g, np, e->s));
+    if (e->early) {
+      hipLaunchKernelGGL(checksum_early_dg, dim3(e->n_ids), dim3(kThreads), 0, e->s, e->view, g, e->ids_dev + 64 * g,
+                         e->early_dev + 64 * g, e->ready_dev + 64 * g);
+      TSE_HIP(hipGetLastError());
+    }
     if (e->dg) TSE_CK(ss_dg_enqueue_wait(e->c, int(g), e->s));
     if (e->checksum) {
       hipLaunchKernelGGL(checksum_dg, dim3(e->max_chunks, e->n_ids), dim3(kThreads), 0, e->s, e->view, g,
@@ -265,8 +296,19 @@ __attribute__((visibility("default"))) ss_status tse_dg_create(ss_ctx* c, uint32
 
 // As tse_dg_create, with n_pred (<= 64) ids predicted at every gated layer but the last for the next one (each token's
 // predictions come with its routes, tse_dg_token_pred).
+__attribute__((visibility("default"))) ss_status tse_dg_create_ex(ss_ctx* c, uint32_t n_ids, uint32_t n_pred,
+                                                                  int use_graph, int checksum, int dg, int early,
+                                                                  void** out);
 __attribute__((visibility("default"))) ss_status tse_dg_create_pred(ss_ctx* c, uint32_t n_ids, uint32_t n_pred,
                                                                     int use_graph, int checksum, int dg, void** out) {
+  return tse_dg_create_ex(c, n_ids, n_pred, use_graph, checksum, dg, 0, out);
+}
+
+// As tse_dg_create_pred; early = 1 adds resident-first reads through ss_dg_slot_if_ready before every layer's wait
+// (tse_dg_early reads the last token's results back).
+__attribute__((visibility("default"))) ss_status tse_dg_create_ex(ss_ctx* c, uint32_t n_ids, uint32_t n_pred,
+                                                                  int use_graph, int checksum, int dg, int early,
+                                                                  void** out) {
   if (n_ids < 1 || n_ids > 64 || n_pred > 64) return SS_E_INVALID;
   auto* e = new TseDg;
   e->c = c;
@@ -274,6 +316,7 @@ __attribute__((visibility("default"))) ss_status tse_dg_create_pred(ss_ctx* c, u
   e->n_pred = n_pred;
   e->checksum = checksum != 0;
   e->dg = dg != 0;
+  e->early = early != 0;
   ss_status st = ss_dg_get_device_view(c, &e->view);
   if (st != SS_OK) {
     delete e;
@@ -286,7 +329,9 @@ __attribute__((visibility("default"))) ss_status tse_dg_create_pred(ss_ctx* c, u
   if (hipStreamCreateWithFlags(&e->s, hipStreamNonBlocking) != hipSuccess ||
       hipMalloc(&e->ids_dev, 4ull * 64 * e->G) != hipSuccess || hipMalloc(&e->pred_dev, 4ull * 64 * e->G) != hipSuccess ||
       hipMalloc(&e->out_dev, 8ull * 64 * e->G) != hipSuccess ||
-      hipMalloc(&e->start_dev, 8ull * e->G) != hipSuccess) {
+      hipMalloc(&e->start_dev, 8ull * e->G) != hipSuccess ||
+      (e->early && (hipMalloc(&e->early_dev, 8ull * 64 * e->G) != hipSuccess ||
+                    hipMalloc(&e->ready_dev, 4ull * 64 * e->G) != hipSuccess))) {
     delete e;
     return SS_E_NOMEM;
   }
@@ -336,6 +381,10 @@ __attribute__((visibility("default"))) ss_status tse_dg_token_pred(void* h, cons
     TSE_HIP(hipStreamSynchronize(e->s));  // (pv is a local)
   }
   if (e->checksum) TSE_HIP(hipMemsetAsync(e->out_dev, 0, 8ull * 64 * e->G, e->s));
+  if (e->early) {
+    TSE_HIP(hipMemsetAsync(e->early_dev, 0, 8ull * 64 * e->G, e->s));
+    TSE_HIP(hipMemsetAsync(e->ready_dev, 0, 4ull * 64 * e->G, e->s));
+  }
   TSE_HIP(hipStreamSynchronize(e->s));
   const auto t0 = std::chrono::steady_clock::now();
   if (e->dg) TSE_CK(ss_begin(e->c, nullptr, 0));
@@ -423,6 +472,23 @@ __attribute__((visibility("default"))) ss_status tse_slot_probe(const int32_t* s
   (void)hipFree(d_ts);
   (void)hipFree(d_words);
   return st;
+}
+
+// The last token's resident-first reads: sums[G][n_ids] and ready[G][n_ids] (an engine created with early = 1).
+__attribute__((visibility("default"))) ss_status tse_dg_early(void* h, uint64_t* sums, uint32_t* ready) {
+  TseDg* e = static_cast<TseDg*>(h);
+  if (!e || !e->early) return SS_E_INVALID;
+  std::vector<unsigned long long> s(size_t(64) * e->G);
+  std::vector<uint32_t> r(size_t(64) * e->G);
+  TSE_HIP(hipMemcpyAsync(s.data(), e->early_dev, 8ull * s.size(), hipMemcpyDeviceToHost, e->s));
+  TSE_HIP(hipMemcpyAsync(r.data(), e->ready_dev, 4ull * r.size(), hipMemcpyDeviceToHost, e->s));
+  TSE_HIP(hipStreamSynchronize(e->s));
+  for (uint32_t g = 0; g < e->G; ++g)
+    for (uint32_t i = 0; i < e->n_ids; ++i) {
+      sums[size_t(g) * e->n_ids + i] = s[64 * g + i];
+      ready[size_t(g) * e->n_ids + i] = r[64 * g + i];
+    }
+  return SS_OK;
 }
 
 // The verify rows each later token closes (1: ss_end; more: ss_dg_end_rows, e.g. a speculative step's rows).

@@ -228,6 +228,10 @@ def engine() -> C.CDLL:
         E.tse_dg_create_pred.argtypes = [vp, u32, u32, C.c_int, C.c_int, C.c_int, C.POINTER(vp)]
         E.tse_dg_token_pred.restype = C.c_int
         E.tse_dg_token_pred.argtypes = [vp, C.POINTER(i32), C.POINTER(i32), C.POINTER(u64), C.POINTER(C.c_double)]
+        E.tse_dg_create_ex.restype = C.c_int
+        E.tse_dg_create_ex.argtypes = [vp, u32, u32, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(vp)]
+        E.tse_dg_early.restype = C.c_int
+        E.tse_dg_early.argtypes = [vp, C.POINTER(u64), C.POINTER(u32)]
         E.tse_dg_stamps.restype = C.c_int
         E.tse_dg_stamps.argtypes = [vp, C.POINTER(u64)]
         E.tse_dg_set_rows.restype = C.c_int
@@ -458,14 +462,16 @@ class Ctx:
 class DgEngine:
     """A graph-captured device-gated engine over a context (tse_dg_*)."""
 
-    def __init__(self, ctx: Ctx, n_ids: int, use_graph=True, checksum=True, gated=True, n_pred=0):
-        """n_pred: ids predicted at every gated layer but the last for the next one (ss_dg_enqueue_predict)."""
+    def __init__(self, ctx: Ctx, n_ids: int, use_graph=True, checksum=True, gated=True, n_pred=0, early=False):
+        """n_pred: ids predicted at every gated layer but the last for the next one (ss_dg_enqueue_predict).
+        early: resident-first reads through ss_dg_slot_if_ready before every layer's wait (early())."""
         E = engine()
         self.h = vp()
         self.G = ctx.dg_view().n_gated
         self.n_ids = n_ids
         self.n_pred = n_pred
-        check(E.tse_dg_create_pred(ctx.h, n_ids, n_pred, int(use_graph), int(checksum), int(gated), C.byref(self.h)))
+        check(E.tse_dg_create_ex(ctx.h, n_ids, n_pred, int(use_graph), int(checksum), int(gated), int(early),
+                                 C.byref(self.h)))
 
     def token(self, routes: np.ndarray, want_checksums=True, preds=None):
         """routes int32 [G][n_ids]; preds int32 [G][n_pred] (row g for layer g + 1); returns (checksums [G][n_ids]
@@ -493,6 +499,13 @@ class DgEngine:
     def set_rows(self, rows: int):
         """The verify rows each later token closes (ss_dg_end_rows above one)."""
         check(engine().tse_dg_set_rows(self.h, rows))
+
+    def early(self):
+        """The last token's resident-first reads: (checksums uint64 [G][n_ids], ready uint32 [G][n_ids])."""
+        sums = np.zeros((self.G, self.n_ids), dtype=np.uint64)
+        ready = np.zeros((self.G, self.n_ids), dtype=np.uint32)
+        check(engine().tse_dg_early(self.h, sums.ctypes.data_as(C.POINTER(u64)), ready.ctypes.data_as(C.POINTER(u32))))
+        return sums, ready
 
     def stamps(self) -> np.ndarray:
         """uint64 [G]: the last token's per-layer compute-start wall-clock ticks."""
