@@ -252,6 +252,15 @@ typedef enum ss_prefetch_kind {
 } ss_prefetch_kind;
 SS_API ss_status ss_prefetch(ss_ctx* c, int layer, const int32_t* ids, int n, ss_prefetch_kind kind);
 SS_API ss_status ss_prefetch_layer(ss_ctx* c, int layer);
+/* Host-only read-ahead of file-backed units into host buffers, no device slot (reference ss.h:489-494,
+ * src/stream_ctx.cpp:1441-1449, src/capi.cpp:698-710). A no-op while readahead_units is 0; arguments are checked. */
+SS_API ss_status ss_host_prefetch(ss_ctx* c, int layer, const int32_t* ids, int n);
+SS_API ss_status ss_host_prefetch_layer(ss_ctx* c, int layer);
+/* Lookahead helper (reference ss.h:496-499, src/capi.cpp:577-612): rows x n_experts router scores of the next layer;
+ * per row its top_k (score descending, lower id first), the union ordered by (best rank, best score at that rank,
+ * id); up to max_out ids into out, the count into *n_out. */
+SS_API ss_status ss_lookahead_select(const float* scores, int rows, int n_experts, int top_k, int32_t* out,
+                                     int max_out, int* n_out);
 
 typedef struct ss_group {
   const int32_t* units;
@@ -375,6 +384,14 @@ SS_API ss_status ss_dg_enqueue_end(ss_ctx* c, void* stream);
 SS_API ss_status ss_dg_residency(ss_ctx* c, ss_dg_unit* out, uint32_t cap, uint32_t* total);
 SS_API ss_status ss_dg_set_budgets(ss_ctx* c, uint32_t spare_target, uint32_t prefetch_per_layer,
                                    uint32_t prefetch_per_token);
+/* Between tokens: the units of gated layer g no later boundary may evict; replaces g's previous set, n = 0 releases
+ * it (reference ss.h:683-688, src/capi.cpp:957-959, src/dg_ctx.cpp:678-689). */
+SS_API ss_status ss_dg_keep(ss_ctx* c, int g, const int32_t* ids, int n);
+/* Between tokens: dg_wb_defer and dg_flush_ready at runtime, 0 / 1 each; turning deferral off submits the deferred
+ * write-backs first. Placement and submission only: the same bytes (reference ss.h:693-699, src/capi.cpp:1021-1023,
+ * src/dg_ctx.cpp:580-592). dg_flush_ready has no effect on HIP, which submits work as it is enqueued. */
+#define SS_DG_SET_SCHED 1
+SS_API ss_status ss_dg_set_sched(ss_ctx* c, uint32_t wb_defer, uint32_t flush_ready);
 /* Scored eviction (policy SS_POLICY_SCORED or SS_POLICY_SCORED_AUTO; reference include/strix_stream/ss.h:730-746).
  * Only the boundary's choice of victims changes: the eligible units (on the device, no write-back in flight) are taken
  * lowest score first, score = w_t P + w_f F + w_r Rec in integers (P: the transition estimate from this token's union

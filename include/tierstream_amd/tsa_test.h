@@ -91,6 +91,10 @@ SS_API ss_status tsa_test_dgcore_token_pred(void* h, const uint32_t* ids, uint32
                                             uint32_t n_counts);
 /* Between tokens: the policy switch of ss_dg_set_policy on the core alone. */
 SS_API ss_status tsa_test_dgcore_set_policy(void* h, uint32_t policy);
+/* The keys every later boundary must not evict (ss_dg_keep of every gated layer; n = 0: none), and the runtime switch
+ * of write-back deferral (ss_dg_set_sched's wb_defer), on the core alone. */
+SS_API ss_status tsa_test_dgcore_set_keep(void* h, const uint32_t* keys, uint32_t n);
+SS_API ss_status tsa_test_dgcore_set_wb_defer(void* h, uint32_t on);
 /* Scored eviction's profile rules without a context: the SHA-256 of data[0..n) (32 raw bytes into out), and the
  * TSSCPRF1 checks of a profile against the gated layers' units and a 32-byte identity (SS_E_INVALID naming the first
  * broken rule; the provenance into prov, NUL-terminated, when it passes). */

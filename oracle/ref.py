@@ -69,6 +69,8 @@ def lib() -> C.CDLL:
                                        C.POINTER(u32), u32, u32, u32, u32, u32, u32, C.POINTER(u32), u32, u32, u32,
                                        C.POINTER(C.c_uint8)]),
             "refdg_set_policy": (C.c_int, [vp, u32]),
+            "refdg_set_keep": (C.c_int, [vp, C.POINTER(u32), u32]),
+            "refdg_set_wb_defer": (C.c_int, [vp, u32]),
             "refdg_cpu_baseline_policy": (None, [u32]),
             "refdg_profile_check": (C.c_int, [C.c_char_p, u64, C.POINTER(u32), u32, C.c_char_p]),
             "refdg_score_identity": (C.c_int, [u32, C.POINTER(u32), C.POINTER(u32), C.POINTER(u64), C.POINTER(u64),
@@ -281,6 +283,15 @@ class RefDg:
     def set_policy(self, policy):
         if lib().refdg_set_policy(self.h, policy) != 0:
             raise RuntimeError("refdg_set_policy failed")
+
+    def set_keep(self, keys):
+        """The keys every later boundary must not evict (ss_dg_keep of every gated layer, concatenated)."""
+        k = np.ascontiguousarray(np.asarray(keys, dtype=np.uint32))
+        lib().refdg_set_keep(self.h, k.ctypes.data_as(C.POINTER(u32)), len(k))
+
+    def set_wb_defer(self, on):
+        if lib().refdg_set_wb_defer(self.h, int(on)) != 0:
+            raise RuntimeError("refdg_set_wb_defer failed")
 
     def residency(self):
         L = lib()

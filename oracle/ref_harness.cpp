@@ -124,6 +124,7 @@ struct RefDg {
   std::unique_ptr<ts::DgCore> core;
   uint32_t seq = 0;
   uint32_t rows = 1;  // the verify rows each token's boundary closes (scored auto ranks only above one)
+  std::vector<uint32_t> keep;  // the boundary's keep list, as the reference context builds it (DgSteps::all_kept)
 };
 
 }  // namespace
@@ -343,7 +344,7 @@ int refdg_token_run(void* h, const uint32_t* ids, uint32_t n, const uint32_t* pr
       if (c.deferred() && nx < G) c.issue_writebacks(g, nullptr);
       c.score_layer(g);  // the service closes each layer after its write-back slice (nothing when not scored)
     }
-    c.end_token({}, r->rows);
+    c.end_token(r->keep, r->rows);
     c.check();
     std::memcpy(table_out, c.table().data(), 4ull * c.keys());
     const ts::DgStats& s = c.stats();
@@ -386,6 +387,24 @@ uint32_t refdg_host_order(void* h, uint32_t* out, uint32_t cap) {
   const std::vector<uint32_t> v = r->core->host_order();
   for (uint32_t i = 0; i < cap && i < v.size(); ++i) out[i] = v[i];
   return uint32_t(v.size());
+}
+
+// ss_dg_keep of every gated layer, concatenated (the reference context passes DgSteps::all_kept() to end_token).
+int refdg_set_keep(void* h, const uint32_t* keys, uint32_t n) {
+  static_cast<RefDg*>(h)->keep.assign(keys, keys + n);
+  return 0;
+}
+
+// ss_dg_set_sched's write-back deferral (the reference context calls DgCore::set_wb_defer between tokens).
+int refdg_set_wb_defer(void* h, uint32_t on) {
+  try {
+    static_cast<RefDg*>(h)->core->set_wb_defer(on != 0);
+    static_cast<RefDg*>(h)->core->check();
+    return 0;
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "refdg_set_wb_defer: %s\n", e.what());
+    return 1;
+  }
 }
 
 void refdg_close(void* h) { delete static_cast<RefDg*>(h); }

@@ -49,6 +49,61 @@ def test_library_exports_every_declared_function(header):
     assert not missing, missing
 
 
+def test_minimum_export_set_of_the_serve_path():
+    """Every function of the reference header's serve-path sections (tests/golden/min_exports.json: descriptor, plan,
+    defaults, context and forward, stats, device-gated calls) is declared in ss.h and exported, under its ss_ and its
+    ts_ name."""
+    import tierstream_amd
+    lib = tierstream_amd.lib()
+    want = json.loads((ROOT / "tests" / "golden" / "min_exports.json").read_text())["functions"]
+    ours = set(declared(ROOT / "include" / "strix_stream" / "ss.h"))
+    assert len(want) > 50
+    assert [n for n in want if n not in ours] == []
+    assert [n for n in want if not hasattr(lib, n) or not hasattr(lib, "ts_" + n[3:])] == []
+
+
+def test_lookahead_select_matches_the_reference():
+    """ss_lookahead_select against the reference's own (oracle/_ref): random score rows with ties (scores drawn from a
+    few values), every top_k, max_out below and above the union, zero rows; and the argument refusals."""
+    import numpy as np
+
+    import tierstream_amd
+    from oracle import ref
+    if not ref.available():
+        pytest.skip("oracle/_ref is not built")
+    ours, theirs = tierstream_amd.lib(), ref.lib()
+    for L in (ours, theirs):
+        L.ss_lookahead_select.restype = C.c_int
+        L.ss_lookahead_select.argtypes = [C.POINTER(C.c_float), C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int32),
+                                          C.c_int, C.POINTER(C.c_int)]
+    rng = np.random.default_rng(3)
+    fp = C.POINTER(C.c_float)
+    for case in range(400):
+        n_exp = int(rng.integers(1, 80))
+        rows = int(rng.integers(0, 9))
+        k = int(rng.integers(1, n_exp + 1))
+        levels = rng.choice([2, 5, 1000])
+        s = (rng.integers(0, levels, size=(max(rows, 1), n_exp)) / levels).astype(np.float32)
+        s = np.ascontiguousarray(s)
+        max_out = int(rng.integers(0, n_exp + 3))
+        got = []
+        for L in (ours, theirs):
+            out = np.full(n_exp + 3, -7, dtype=np.int32)
+            n = C.c_int(-1)
+            st = L.ss_lookahead_select(s.ctypes.data_as(fp), rows, n_exp, k, out.ctypes.data_as(C.POINTER(C.c_int32)),
+                                       max_out, C.byref(n))
+            got.append((st, n.value, out.tolist()))
+        assert got[0] == got[1], (case, rows, n_exp, k, max_out)
+    out = np.zeros(4, dtype=np.int32)
+    n = C.c_int(0)
+    s = np.zeros(8, dtype=np.float32)
+    for args in [(2, 4, 0), (2, 4, 5), (-1, 4, 2), (2, 0, 1)]:  # top_k 0, top_k > n_experts, rows < 0, no experts
+        for L in (ours, theirs):
+            st = L.ss_lookahead_select(s.ctypes.data_as(fp), args[0], args[1], args[2],
+                                       out.ctypes.data_as(C.POINTER(C.c_int32)), 4, C.byref(n))
+            assert st == tierstream_amd.SS_E_INVALID, (args, st)
+
+
 def test_ts_names_are_generated_from_ss_h():
     r = subprocess.run([sys.executable, "-m", "tierstream_amd.gen_ts", "--check"], cwd=ROOT, capture_output=True,
                        text=True)

@@ -50,6 +50,10 @@ def _lib():
     L.tsa_test_dgcore_token_pred.restype = C.c_int
     L.tsa_test_dgcore_set_policy.argtypes = [C.c_void_p, u32]
     L.tsa_test_dgcore_set_policy.restype = C.c_int
+    L.tsa_test_dgcore_set_keep.argtypes = [C.c_void_p, C.POINTER(u32), u32]
+    L.tsa_test_dgcore_set_keep.restype = C.c_int
+    L.tsa_test_dgcore_set_wb_defer.argtypes = [C.c_void_p, u32]
+    L.tsa_test_dgcore_set_wb_defer.restype = C.c_int
     return tsa, L
 
 
@@ -101,6 +105,13 @@ class OurCore:
 
     def set_policy(self, policy):
         self.tsa.check(self.L.tsa_test_dgcore_set_policy(self.h, policy))
+
+    def set_keep(self, keys):
+        k = np.ascontiguousarray(np.asarray(keys, dtype=np.uint32))
+        self.tsa.check(self.L.tsa_test_dgcore_set_keep(self.h, k.ctypes.data_as(C.POINTER(u32)), len(k)))
+
+    def set_wb_defer(self, on):
+        self.tsa.check(self.L.tsa_test_dgcore_set_wb_defer(self.h, int(on)))
 
     def host_order(self):
         out = np.zeros(self.keys, dtype=np.uint32)
@@ -204,9 +215,11 @@ def _preds(rng, routes, n_units, k):
     return out
 
 
-def _run(seed, three, score=None, switch=None, partial=False, predict=0, disk_prefetch=0):
+def _run(seed, three, score=None, switch=None, partial=False, predict=0, disk_prefetch=0, keep=False, sched=False):
     """switch: (token, policy) - both cores switch policy between tokens there. partial: each token exports a random
-    nonempty subset of the gated layers (ss_begin's rows), the others keep their state."""
+    nonempty subset of the gated layers (ss_begin's rows), the others keep their state. keep: now and then, between
+    tokens, a new keep list (ss_dg_keep: units no boundary may evict; sometimes empty, sometimes with keys off the
+    device). sched: now and then write-back deferral is switched (ss_dg_set_sched)."""
     if not ref.available():
         pytest.skip("oracle/_ref (the reference core) is not built")
     c = _case(seed, three)
@@ -220,11 +233,21 @@ def _run(seed, three, score=None, switch=None, partial=False, predict=0, disk_pr
     seen = {}
     rng = np.random.default_rng(seed + 5)
     preds = _preds(np.random.default_rng(seed + 9), c["routes"], c["n_units"], predict) if predict else None
+    keys = sum(c["n_units"])
+    defer = c["wb_defer"]
     try:
         for t, ids in enumerate(c["routes"]):
             if switch and t == switch[0]:
                 ours.set_policy(switch[1])
                 theirs.set_policy(switch[1])
+            if keep and rng.random() < 0.3:
+                kk = [int(k) for k in rng.choice(keys, size=int(rng.integers(0, max(2, keys // 3))), replace=False)]
+                ours.set_keep(kk)
+                theirs.set_keep(kk)
+            if sched and rng.random() < 0.25:
+                defer = 1 - defer
+                ours.set_wb_defer(defer)
+                theirs.set_wb_defer(defer)
             run = None
             if partial:
                 run = [int(v) for v in rng.integers(0, 2, size=ids.shape[0])]
@@ -324,6 +347,49 @@ def test_prefetch_matches_reference(seed):
 def test_scored_prefetch_matches_reference(seed):
     c = _case(8000 + seed, False)
     _run(8000 + seed, False, score=_score(seed, c["n_units"]), predict=int(1 + seed % 3))
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_keep_lists_match_reference(seed):
+    """ss_dg_keep: between tokens a keep list (every gated layer's set) that the next boundaries must not evict, under
+    LRU and scored victims, two and three tiers, with predictions in some cases."""
+    three = seed % 3 == 0
+    c = _case(9000 + seed, three)
+    score = _score(seed, c["n_units"]) if seed % 4 == 1 else None
+    _run(9000 + seed, three, score=score, keep=True, predict=int(seed % 5 == 2) * 2)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_wb_defer_switch_matches_reference(seed):
+    """ss_dg_set_sched's wb_defer between tokens: off submits every deferred write-back first; on again restarts the
+    per-layer credit and carry as after open."""
+    three = seed % 2 == 1
+    _run(9500 + seed, three, sched=True, keep=seed % 3 == 0)
+
+
+def test_keep_lists_protect_units():
+    """The keep cases are not vacuous: over the seeds, some boundaries would have evicted a kept unit (the tables with
+    and without the keep lists differ)."""
+    if not ref.available():
+        pytest.skip("oracle/_ref (the reference core) is not built")
+    differ = 0
+    for seed in range(20):
+        c = _case(9000 + seed, False)
+        kw = dict(wb_defer=c["wb_defer"], inclusive=c["inclusive"])
+        a = ref.RefDg(c["n_units"], c["persistent"], c["bank"], c["blocks"], c["spare_target"], c["parts"],
+                      c["order"], **kw)
+        b = ref.RefDg(c["n_units"], c["persistent"], c["bank"], c["blocks"], c["spare_target"], c["parts"],
+                      c["order"], **kw)
+        try:
+            a.set_keep(list(range(0, sum(c["n_units"]), 2)))
+            for ids in c["routes"]:
+                ta, _ = a.token(ids)
+                tb, _ = b.token(ids)
+                differ += int(not np.array_equal(ta, tb))
+        finally:
+            a.close()
+            b.close()
+    assert differ > 0
 
 
 def test_lru_open_refuses_a_switch_to_scoring():

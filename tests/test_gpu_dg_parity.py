@@ -96,6 +96,17 @@ CASES = {
                         early=True),
     "early-reads-prefetch": dict(layers=4, units=16, parts=[64 * KiB] * 3, n_res=24, dyn=2, spares=12, n_ids=4,
                                  tokens=24, predict=3, early=True),
+    # ss_dg_keep between tokens: per gated layer a set no later boundary may evict (replaced, released, sometimes
+    # holding units off the device), under LRU and scored victims
+    "keep": dict(layers=4, units=16, parts=[64 * KiB] * 3, n_res=24, dyn=2, spares=12, n_ids=4, tokens=24, keep=True),
+    "keep-scored": dict(layers=4, units=16, parts=[64 * KiB] * 3, n_res=24, dyn=2, spares=12, n_ids=4, tokens=24,
+                        keep=True, score=dict(policy=1)),
+    # ss_dg_set_sched between tokens: deferral off (the deferred write-backs submitted first) and on again, with 8 MiB
+    # parts (per-part copies behind per-part write-backs)
+    "set-sched": dict(layers=4, units=8, parts=[64 * KiB] * 3, n_res=12, dyn=1, spares=6, n_ids=2, tokens=24,
+                      sched={6: (0, 1), 12: (1, 0), 18: (0, 0)}),
+    "set-sched-big-parts": dict(layers=4, units=8, parts=[8 * MiB] * 3, n_res=12, dyn=1, spares=6, n_ids=2,
+                                tokens=16, sched={5: (0, 0), 10: (1, 1)}, keep=True),
 }
 SCORE_COUNTERS = ["score_fallbacks", "scored_victims", "score_layers", "score_candidates", "score_saturated"]
 PRED_COUNTERS = ["prefetched", "prefetch_used", "pred_invalid", "predicted", "predicted_true", "wb_cancelled"]
@@ -135,6 +146,8 @@ def test_dg_matches_reference(name, tmp_path, gpu):
     score = dict(c.pop("score", {}))
     predict = c.pop("predict", 0)
     early = c.pop("early", False)
+    keep = c.pop("keep", False)
+    sched = dict(c.pop("sched", {}))
     m, bkw, okw = _setup(tmp_path, c["layers"], c["units"], c["parts"], c["n_res"], c["dyn"], c["spares"], c["n_ids"],
                          inclusive=c.get("inclusive", 0), wb_defer=c.get("wb_defer", 1))
     ref_score, keep = None, []
@@ -178,12 +191,24 @@ def test_dg_matches_reference(name, tmp_path, gpu):
     expect = {(L, u): m.checksum(L, u) for L in range(c["layers"]) for u in range(c["units"])}
     with pytest.raises(ss.SsError):  # arms the stats snapshot: each token's boundary publishes from now on
         ctx.snapshot()
+    krng = np.random.default_rng(77)
+    kept = [[] for _ in range(c["layers"])]
     try:
         for t in range(tokens):
             if t in switch:
                 policy = switch[t]
                 ctx.dg_set_policy(policy)
                 refdg.set_policy(policy)
+            if keep and t % 3 == 1:
+                g = int(krng.integers(0, c["layers"]))
+                kept[g] = sorted(int(u) for u in krng.choice(c["units"], size=int(krng.integers(0, c["units"] // 2)),
+                                                             replace=False))
+                ctx.dg_keep(g, kept[g])
+                refdg.set_keep([g * c["units"] + u for L in range(c["layers"]) for u in kept[L] if L == g] +
+                               [L * c["units"] + u for L in range(c["layers"]) if L != g for u in kept[L]])
+            if t in sched:
+                ctx.dg_set_sched(*sched[t])
+                refdg.set_wb_defer(sched[t][0])
             cks, _ = eng.token(routes[t], preds=preds[t] if predict else None)
             want_table, want = refdg.token(routes[t].astype(np.uint32),
                                            pred=preds[t].astype(np.uint32) if predict else None)
@@ -435,3 +460,39 @@ def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, 
         eng.close()
         ctx.close()
         refdg.close()
+
+
+def test_keep_sched_and_host_calls_refuse_bad_arguments(tmp_path, gpu):
+    """ss_dg_keep: a gated layer or id out of range, a negative count; ss_dg_set_sched: a flag above 1; the host-only
+    calls on a device-gated context. Each is SS_E_INVALID and leaves the context usable (reference src/dg_ctx.cpp:
+    580-592, :678-689, src/capi.cpp:157-162)."""
+    import tierstream_amd as tsa
+    m, bkw, okw = _setup(tmp_path, 3, 8, [64 * KiB] * 3, 12, 1, 6, 2)
+    d = ss.Desc(m.desc_json())
+    plan = ss.Plan(d, ss.budget(**bkw))
+    ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(**okw))
+    eng = ss.DgEngine(ctx, 2, use_graph=True)
+    L = ss._declare()
+    try:
+        for g, ids in [(3, [0]), (-1, [0]), (0, [8]), (0, [-1])]:
+            with pytest.raises(ss.SsError) as e:
+                ctx.dg_keep(g, ids)
+            assert e.value.status == tsa.SS_E_INVALID, (g, ids)
+        assert L.ss_dg_keep(ctx.h, 0, None, -1) == tsa.SS_E_INVALID
+        for a, b in [(2, 0), (0, 2)]:
+            with pytest.raises(ss.SsError):
+                ctx.dg_set_sched(a, b)
+        assert ctx.host_prefetch(0, [1]) == tsa.SS_E_INVALID  # host-only call on a device-gated context
+        ctx.dg_keep(1, [0, 3])
+        ctx.dg_keep(1, [])
+        ctx.dg_set_sched(0, 1)
+        ctx.dg_set_sched(1, 0)
+        routes = _routes(3, 8, 2, 2, seed=3, zipf=True)
+        for t in range(2):
+            cks, _ = eng.token(routes[t])
+            for Lr in range(3):
+                for i, u in enumerate(routes[t, Lr]):
+                    assert int(cks[Lr, i]) == m.checksum(Lr, int(u))
+    finally:
+        eng.close()
+        ctx.close()

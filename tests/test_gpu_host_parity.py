@@ -172,3 +172,30 @@ def test_stats_snapshot(name, tmp_path, gpu):
         assert info["sequence"] == 3 and tot["routed"] == 0 and ctx.snapshot_json() == ctx.stats_json()
     finally:
         ctx.close()
+
+
+def test_host_prefetch_is_a_checked_no_op_without_read_ahead(tmp_path, gpu):
+    """ss_host_prefetch / ss_host_prefetch_layer with readahead_units 0 (reference src/stream_ctx.cpp:1441-1449,
+    src/capi.cpp:698-710): a no-op that still refuses a layer out of range and a negative count; the forwards after it
+    match the reference."""
+    import tierstream_amd as tsa
+    c = CASES["decode-lru"]
+    m = fixtures.write_model(tmp_path, c["layers"], c["units"], c["parts"], top_k=c["top_k"], seed=7)
+    routes = fixtures.uniform_routes(c["layers"], c["units"], c["top_k"], 4, seed=11)
+    bkw = _budget(m, c["n_res"], c["ring"], c.get("dyn", 0))
+    want = ref.host_run(m.desc_json(), ss.budget(**bkw), ss.options(**c["opts"]), routes, c["mode"])
+    d = ss.Desc(m.desc_json())
+    ctx = ss.Ctx(d, ss.budget(**bkw), None, ss.options(**c["opts"]))
+    L = ss._declare()
+    try:
+        assert ctx.host_prefetch(0, [1, 2]) == tsa.SS_OK
+        assert ctx.host_prefetch(c["layers"], [1]) == tsa.SS_E_INVALID
+        assert L.ss_host_prefetch(ctx.h, 0, None, -1) == tsa.SS_E_INVALID
+        assert L.ss_host_prefetch_layer(ctx.h, 1) == tsa.SS_OK
+        assert L.ss_host_prefetch_layer(ctx.h, -1) == tsa.SS_E_INVALID
+        _, _, stats, _ = ctx.host_run(routes, c["mode"])
+        for s in range(4):
+            assert {k: v for k, v in stats[s].items() if k != "wait_ns"} == \
+                {k: v for k, v in want[s]["stats"].items() if k != "wait_ns"}, s
+    finally:
+        ctx.close()

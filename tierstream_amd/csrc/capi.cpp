@@ -331,6 +331,16 @@ ss_status ss_prefetch(ss_ctx* c, int layer, const int32_t* ids, int n, ss_prefet
 ss_status ss_prefetch_layer(ss_ctx* c, int layer) {
   return ctx_guard(c, [&] { host_of(c, "ss_prefetch_layer").prefetch_layer(layer); });
 }
+ss_status ss_host_prefetch(ss_ctx* c, int layer, const int32_t* ids, int n) {
+  return ctx_guard(c, [&] { host_of(c, "ss_host_prefetch").host_prefetch(layer, ids, n); });
+}
+ss_status ss_host_prefetch_layer(ss_ctx* c, int layer) {
+  return ctx_guard(c, [&] { host_of(c, "ss_host_prefetch_layer").host_prefetch_layer(layer); });
+}
+ss_status ss_lookahead_select(const float* scores, int rows, int n_experts, int top_k, int32_t* out, int max_out,
+                              int* n_out) {
+  return guard([&] { lookahead_select(scores, rows, n_experts, top_k, out, max_out, n_out); });
+}
 ss_status ss_acquire(ss_ctx* c, int layer, void* stream, ss_layer_view* out) {
   return ctx_guard(c, [&] { host_of(c, "ss_acquire").acquire(layer, stream, true, out); });
 }
@@ -464,6 +474,12 @@ ss_status ss_dg_residency(ss_ctx* c, ss_dg_unit* out, uint32_t cap, uint32_t* to
 }
 ss_status ss_dg_set_budgets(ss_ctx* c, uint32_t spare_target, uint32_t per_layer, uint32_t per_token) {
   return ctx_guard(c, [&] { dg_of(c, "ss_dg_set_budgets").set_budgets(spare_target, per_layer, per_token); });
+}
+ss_status ss_dg_keep(ss_ctx* c, int g, const int32_t* ids, int n) {
+  return ctx_guard(c, [&] { dg_of(c, "ss_dg_keep").keep(g, ids, n); });
+}
+ss_status ss_dg_set_sched(ss_ctx* c, uint32_t wb_defer, uint32_t flush_ready) {
+  return ctx_guard(c, [&] { dg_of(c, "ss_dg_set_sched").set_sched(wb_defer, flush_ready); });
 }
 ss_status ss_dg_end_rows(ss_ctx* c, uint32_t rows) {
   return ctx_guard(c, [&] { dg_of(c, "ss_dg_end_rows").end(rows); });

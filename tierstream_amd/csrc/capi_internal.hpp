@@ -28,6 +28,8 @@ struct ss_ctx {
 namespace tsa {
 
 bool ctx_poisoned(const ss_ctx* c);
+void lookahead_select(const float* scores, int rows, int n_experts, int top_k, int32_t* out, int max_out,
+                      int* n_out);
 void ctx_poison(ss_ctx* c);
 
 template <class F>

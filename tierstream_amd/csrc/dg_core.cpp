@@ -44,12 +44,7 @@ DgCore::DgCore(const DgConfig& cfg, DgTransport* t) : c_(cfg), t_(t) {
   require(c_.disk_tier || (!c_.disk_prefetch && !c_.disk_staging && !c_.home_blocks && !c_.clean_evict), SS_E_INVALID,
           "device-gated: disk options without the disk tier");
   if (c_.disk_tier) stage_ev_.assign(c_.disk_staging, nullptr);
-  if (c_.wb_defer) {
-    wb_stream_ = c_.wb_on_d2h ? DgTransport::kD2h : DgTransport::kDem;
-    layer_bytes_ = c_.wb_layer_bytes ? c_.wb_layer_bytes : t_->part_bytes(0);
-    max_outstanding_ = c_.wb_max_outstanding ? c_.wb_max_outstanding : 2 * unit_bytes_;
-    if (c_.wb_on_d2h) post_ready_ev_ = event();
-  }
+  apply_wb_defer();
   if (c_.scored) {  // every table now: the service never allocates
     require(c_.w_trans <= 1000 && c_.w_freq <= 1000 && c_.w_rec <= 1000 && c_.w_trans + c_.w_freq + c_.w_rec == 1000,
             SS_E_INVALID, "device-gated: score weights must each be 0..1000 and sum to 1000");
@@ -668,7 +663,17 @@ void DgCore::serve_prediction(uint32_t g_next, const uint32_t* pred, uint32_t n)
   for (uint32_t id : pred_) fetch(g_next, id, true);
 }
 
-void DgCore::end_token(uint32_t rows) {
+void DgCore::end_token(uint32_t rows, const std::vector<uint32_t>& keep) {
+  keep_.clear();
+  if (!keep.empty()) {
+    keep_.assign(keys_, 0);
+    for (uint32_t k : keep)
+      if (k < keys_) keep_[k] = 1;
+  }
+  struct ClearKeep {
+    std::vector<uint8_t>& v;
+    ~ClearKeep() { v.clear(); }
+  } clear_keep{keep_};
   // every copy and entry write of the token has landed before anything changes home
   t_->sync(DgTransport::kDem);
   t_->sync(DgTransport::kPf);
@@ -947,6 +952,28 @@ void DgCore::set_policy(uint32_t policy) {
   for (Entry& x : e_) x.demand_epoch = x.stamp = 0;
   stamp_ = 0;
   for (uint32_t k = tail_; k != kNone; k = e_[k].prev) e_[k].stamp = ++stamp_;  // the list's order, the head largest
+}
+
+void DgCore::apply_wb_defer() {
+  if (!c_.wb_defer) {
+    wb_stream_ = DgTransport::kDem;
+    layer_bytes_ = max_outstanding_ = 0;
+    return;
+  }
+  wb_stream_ = c_.wb_on_d2h ? DgTransport::kD2h : DgTransport::kDem;
+  layer_bytes_ = c_.wb_layer_bytes ? c_.wb_layer_bytes : t_->part_bytes(0);
+  max_outstanding_ = c_.wb_max_outstanding ? c_.wb_max_outstanding : 2 * unit_bytes_;
+  if (c_.wb_on_d2h && !post_ready_ev_) post_ready_ev_ = event();
+}
+
+void DgCore::set_wb_defer(bool on) {
+  if (on == c_.wb_defer) return;
+  if (!on)
+    while (!deferred_.empty()) finish_deferred_front();  // recorded write-backs now, collected as any other
+  c_.wb_defer = on;
+  apply_wb_defer();
+  credit_ = 0;
+  prev_evict_ = 0;
 }
 
 void DgCore::drain() {

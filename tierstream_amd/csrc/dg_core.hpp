@@ -167,7 +167,13 @@ class DgCore {
   void serve_use(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask);
   void serve_prediction(uint32_t g_next, const uint32_t* pred, uint32_t n);
   void issue_writebacks(uint32_t g);  // the deferred write-back slice after layer g's service
-  void end_token(uint32_t rows = 1);  // rows: the verify rows the token closed (scored_auto ranks only above one)
+  // rows: the verify rows the token closed (scored_auto ranks only above one); keep: keys this boundary must not
+  // evict (every gated layer's ss_dg_keep set), out-of-range keys ignored
+  void end_token(uint32_t rows = 1, const std::vector<uint32_t>& keep = {});
+  // Between tokens: deferral of write-backs on or off; turning it off first submits every deferred write-back. The
+  // per-token credit and carry restart as after open. Placement and submission only: the same bytes.
+  void set_wb_defer(bool on);
+  bool wb_defer() const { return c_.wb_defer; }
   void drain();  // between tokens: every deferred write-back submitted, every stream synchronized
   void set_spare_target(uint32_t n);
   void set_prefetch_budget(uint32_t per_layer, uint32_t per_token);
@@ -269,7 +275,10 @@ class DgCore {
   void select_scored(size_t need);
   Cand score_of(uint32_t g, uint32_t u, uint64_t denom, const Cand* cutoff) const;
   void reset_score();
-  bool eligible(uint32_t k) const { return e_[k].home == Home::Device && !e_[k].wb_pending; }
+  bool eligible(uint32_t k) const {
+    return e_[k].home == Home::Device && !e_[k].wb_pending && (keep_.empty() || !keep_[k]);
+  }
+  void apply_wb_defer();  // the write-back stream, layer credit and outstanding cap of c_.wb_defer
   bool accept_victim(uint32_t k);  // the boundary's acceptance of one victim; false: no block for it (evict_short)
   bool on_device_or_coming(uint32_t g, uint32_t unit) const {
     const Home h = e_[key(g, unit)].home;
@@ -306,6 +315,7 @@ class DgCore {
   std::vector<DgLayerCounts> lc_;
   std::vector<LayerScore> sc_;  // scored: one per gated layer (empty under an LRU open)
   std::vector<Cand> heap_;
+  std::vector<uint8_t> keep_;  // during end_token: the keys its keep list protects (empty: none)
   uint64_t epoch_ = 0, stamp_ = 0, open_stamp_ = 0;
 };
 

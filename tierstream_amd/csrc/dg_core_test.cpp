@@ -47,6 +47,7 @@ struct TestCore {
   std::unique_ptr<EagerTransport> t;
   std::unique_ptr<DgCore> core;
   uint32_t seq = 0, rows = 1;
+  std::vector<uint32_t> keep;  // the boundary's keep list (ss_dg_keep of every gated layer)
 };
 
 constexpr const char* kNames =
@@ -151,7 +152,7 @@ ss_status tsa_test_dgcore_token_pred(void* h, const uint32_t* ids, uint32_t n, c
       while (nx < G && !rv[nx]) ++nx;
       if (c.deferred() && nx < G) c.issue_writebacks(g);
     }
-    c.end_token(r->rows);
+    c.end_token(r->rows, r->keep);
     c.check();
     if (table_out) std::memcpy(table_out, c.table().data(), 4ull * c.keys());
     if (counts) {
@@ -177,6 +178,22 @@ ss_status tsa_test_dgcore_set_policy(void* h, uint32_t policy) {
     tsa::require(h != nullptr, SS_E_INVALID, "tsa_test_dgcore_set_policy: null handle");
     auto* r = static_cast<tsa::TestCore*>(h);
     r->core->set_policy(policy);
+    r->core->check();
+  });
+}
+
+ss_status tsa_test_dgcore_set_keep(void* h, const uint32_t* keys, uint32_t n) {
+  return tsa::guard([&] {
+    tsa::require(h != nullptr && (keys || n == 0), SS_E_INVALID, "tsa_test_dgcore_set_keep: null argument");
+    static_cast<tsa::TestCore*>(h)->keep.assign(keys, keys + n);
+  });
+}
+
+ss_status tsa_test_dgcore_set_wb_defer(void* h, uint32_t on) {
+  return tsa::guard([&] {
+    tsa::require(h != nullptr, SS_E_INVALID, "tsa_test_dgcore_set_wb_defer: null handle");
+    auto* r = static_cast<tsa::TestCore*>(h);
+    r->core->set_wb_defer(on != 0);
     r->core->check();
   });
 }

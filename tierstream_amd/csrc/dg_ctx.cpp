@@ -1164,7 +1164,7 @@ class HipDgCtx final : public DgCtx {
       poisoned_ = true;
       throw;
     }
-    core_->end_token(rows);
+    core_->end_token(rows, all_kept());
     const std::vector<uint32_t> bad = tr_->collect_verify();
     tr_->profile_collect();
     if (!bad.empty()) {
@@ -1236,6 +1236,34 @@ class HipDgCtx final : public DgCtx {
     require(spare_target <= x_.D, SS_E_INVALID, "ss_dg_set_budgets: spare target above the billed spares");
     core_->set_spare_target(spare_target);
     core_->set_prefetch_budget(per_layer, per_token);
+  }
+
+  // ss_dg_keep (reference include/strix_stream/ss.h:683-688): a plain keep set of gated layer g, replacing the last
+  // one; the next boundaries never choose a kept unit as a victim.
+  void keep(int g, const int32_t* ids, int n) override {
+    require(!in_token_, SS_E_INVALID, "ss_dg_keep: between tokens only");
+    check_g(g, "ss_dg_keep");
+    require(n >= 0 && (n == 0 || ids), SS_E_INVALID, "ss_dg_keep: bad arguments");
+    std::vector<uint32_t> keys(static_cast<size_t>(n));
+    for (int i = 0; i < n; ++i) {
+      require(ids[i] >= 0 && uint32_t(ids[i]) < core_->units(uint32_t(g)), SS_E_INVALID, "ss_dg_keep: id out of range");
+      keys[size_t(i)] = core_->key(uint32_t(g), uint32_t(ids[i]));
+    }
+    kept_[size_t(g)] = std::move(keys);
+  }
+  // ss_dg_set_sched (reference include/strix_stream/ss.h:693-699). dg_flush_ready is accepted and kept: HIP submits
+  // every copy and value-write when it is enqueued, so there is no batched submission to flush.
+  void set_sched(uint32_t wb_defer, uint32_t flush_ready) override {
+    require(!in_token_, SS_E_INVALID, "ss_dg_set_sched: between tokens only");
+    require(wb_defer <= 1 && flush_ready <= 1, SS_E_INVALID, "ss_dg_set_sched: flags are 0 or 1");
+    core_->set_wb_defer(wb_defer != 0);
+    o_.dg_wb_defer = wb_defer;
+    o_.dg_flush_ready = flush_ready;
+  }
+  std::vector<uint32_t> all_kept() const {
+    std::vector<uint32_t> v;
+    for (const auto& k : kept_) v.insert(v.end(), k.begin(), k.end());
+    return v;
   }
 
   // Between tokens, with the device and the service done with the last one (reference src/dg_ctx.cpp:619-629).
@@ -1521,6 +1549,7 @@ class HipDgCtx final : public DgCtx {
   std::unique_ptr<DgCore> core_;
   std::unique_ptr<Service> svc_;
   std::vector<uint8_t> run_;
+  std::vector<std::vector<uint32_t>> kept_;  // per gated layer: its ss_dg_keep set (keys)
   uint32_t seq_ = 0;
   bool in_token_ = false, poisoned_ = false;
   DgCounts base_, fold_;
@@ -1719,6 +1748,7 @@ void HipDgCtx::init() {
   tr_->upload_table(core_->table().data(), x_.keys);
   core_->check();
   run_.assign(G, 1);
+  kept_.assign(G, {});
   base_l_.assign(G, DgLayerCounts{});
   fold(false);
   svc_ = std::make_unique<Service>(core_.get(), m_, x_.B, o_.dg_wait_timeout_ms, o_.device);

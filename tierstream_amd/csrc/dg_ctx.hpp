@@ -31,6 +31,10 @@ class DgCtx {
   virtual void enqueue_end(void* stream) = 0;
   virtual uint32_t residency(ss_dg_unit* out, uint32_t cap) = 0;
   virtual void set_budgets(uint32_t spare_target, uint32_t per_layer, uint32_t per_token) = 0;
+  // Between tokens: the units of gated layer g no later boundary may evict (replaces g's set; n = 0 releases it).
+  virtual void keep(int g, const int32_t* ids, int n) = 0;
+  // Between tokens: write-back deferral on / off, and dg_flush_ready (0 / 1 each).
+  virtual void set_sched(uint32_t wb_defer, uint32_t flush_ready) = 0;
   virtual ss_dg_stats stats() const = 0;
   virtual ss_layer_stats layer_stats(int layer) const = 0;
   virtual ss_layer_stats total_stats() const = 0;

@@ -895,6 +895,14 @@ void HostCtx::check_stream(void* stream, const char* what) {
           std::string(what) + ": a forward must use one engine stream (join other streams into it first)");
 }
 
+void HostCtx::host_prefetch(int layer, const int32_t* ids, int n) {
+  check_layer(layer, "host_prefetch");
+  require(n >= 0 && (ids || n == 0), SS_E_INVALID, "host_prefetch: bad ids");
+  // readahead_units is 0 in every context this library opens (a nonzero value is refused at open): nothing to read
+}
+
+void HostCtx::host_prefetch_layer(int layer) { check_layer(layer, "host_prefetch_layer"); }
+
 void HostCtx::check_layer(int layer, const char* what) const {
   require(layer >= 0 && layer < n_layers(), SS_E_INVALID, std::string(what) + ": layer out of range");
 }

@@ -63,6 +63,10 @@ class HostCtx {
   void routes_all(int layer);
   void prefetch(int layer, const int32_t* ids, int n, bool speculative);
   void prefetch_layer(int layer);
+  // Host-only read-ahead of file-backed units (ss_host_prefetch / ss_host_prefetch_layer): a no-op while
+  // readahead_units is 0; the arguments are checked either way.
+  void host_prefetch(int layer, const int32_t* ids, int n);
+  void host_prefetch_layer(int layer);
   void acquire(int layer, void* stream, bool wait_all, ss_layer_view* out);
   void group_wait(int layer, int group, void* stream);
   void release(int layer, void* stream);

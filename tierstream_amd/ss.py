@@ -184,6 +184,11 @@ def _declare() -> C.CDLL:
         "ss_stats_dg_sized": (st, [vp, C.POINTER(SsDgStats), u32]),
         "ss_dg_set_policy": (st, [vp, C.c_int]),
         "ss_dg_end_rows": (st, [vp, u32]),
+        "ss_dg_keep": (st, [vp, C.c_int, C.POINTER(i32), C.c_int]),
+        "ss_dg_set_sched": (st, [vp, u32, u32]),
+        "ss_dg_set_budgets": (st, [vp, u32, u32, u32]),
+        "ss_host_prefetch": (st, [vp, C.c_int, C.POINTER(i32), C.c_int]),
+        "ss_host_prefetch_layer": (st, [vp, C.c_int]),
         "tsa_test_sha256": (st, [C.c_char_p, u64, C.c_char_p]),
         "tsa_test_score_profile_check": (st, [C.c_char_p, u64, C.POINTER(u32), u32, C.c_char_p, C.c_char_p, u32]),
         "ss_dg_get_device_view_sized": (st, [vp, C.POINTER(SsDgDeviceView), u32]),
@@ -392,6 +397,21 @@ class Ctx:
     def dg_set_policy(self, policy: int):
         """Between tokens: 0 LRU, 1 SCORED, 2 SCORED_AUTO (ss_dg_set_policy)."""
         check(_declare().ss_dg_set_policy(self.h, policy))
+
+    def dg_keep(self, g: int, ids):
+        """Between tokens: the units of gated layer g no later boundary may evict (ss_dg_keep; empty releases)."""
+        a = np.ascontiguousarray(np.asarray(ids, dtype=np.int32))
+        check(_declare().ss_dg_keep(self.h, g, a.ctypes.data_as(C.POINTER(i32)) if len(a) else None, len(a)))
+
+    def dg_set_sched(self, wb_defer: int, flush_ready: int = 0):
+        """Between tokens: write-back deferral and dg_flush_ready (ss_dg_set_sched)."""
+        check(_declare().ss_dg_set_sched(self.h, wb_defer, flush_ready))
+
+    def host_prefetch(self, layer: int, ids) -> int:
+        """ss_host_prefetch; returns the status (no raise)."""
+        a = np.ascontiguousarray(np.asarray(ids, dtype=np.int32))
+        return int(_declare().ss_host_prefetch(self.h, layer, a.ctypes.data_as(C.POINTER(i32)) if len(a) else None,
+                                               len(a)))
 
     def dg_table(self) -> np.ndarray:
         L = _declare()
