@@ -94,6 +94,22 @@ SS_API ss_status tsa_test_dgcore_set_policy(void* h, uint32_t policy);
 /* The keys every later boundary must not evict (ss_dg_keep of every gated layer; n = 0: none), and the runtime switch
  * of write-back deferral (ss_dg_set_sched's wb_defer), on the core alone. */
 SS_API ss_status tsa_test_dgcore_set_keep(void* h, const uint32_t* keys, uint32_t n);
+/* The host contract's placement alone on the CPU (no device): a context over desc_json and the budget (plan_make,
+ * no benefit), `steps` forwards of the engine loop - ss_begin; per layer with units ss_layer_routes (mode 0, 2) or
+ * ss_layer_all (mode 1), ss_acquire (modes 0, 1) or ss_acquire_groups (mode 2); prefetch (may be NULL): the next
+ * layer's predicted ids ([steps][layers][max_ids], -1 padded), ss_prefetch of layer l + 1 after layer l's acquire,
+ * CERTAIN on even steps and SPECULATIVE on odd ones; ss_release; ss_end - every copy complete when issued. Outputs
+ * per [step][layer][unit < max_units]: the table entry's kind (0 none, 1 the layer's pool, 2 the ring) and index (pool
+ * slot or global ring slot), the unit's group (-1: none); per step the forward's total counters. */
+SS_API ss_status tsa_test_hostplace_run(const char* desc_json, size_t len, const ss_budget* budget,
+                                        const ss_options* opt, int steps, const int32_t* routes,
+                                        const int32_t* prefetch, int max_ids, int mode, int max_units,
+                                        int32_t* spot_kind, int32_t* spot_index, int32_t* group_of,
+                                        ss_layer_stats* stats);
+/* The same loop without prefetch; the exclusive-mode counters after the last forward. */
+SS_API ss_status tsa_test_hostplace_exclusive(const char* desc_json, size_t len, const ss_budget* budget,
+                                              const ss_options* opt, int steps, const int32_t* routes, int max_ids,
+                                              int mode, ss_exclusive_stats* out);
 SS_API ss_status tsa_test_dgcore_set_wb_defer(void* h, uint32_t on);
 /* Scored eviction's profile rules without a context: the SHA-256 of data[0..n) (32 raw bytes into out), and the
  * TSSCPRF1 checks of a profile against the gated layers' units and a 32-byte identity (SS_E_INVALID naming the first

@@ -48,6 +48,7 @@ def lib() -> C.CDLL:
             "ss_begin": (st, [vp, vp, C.c_int]),
             "ss_layer_routes": (st, [vp, C.c_int, C.POINTER(i32), C.c_int]),
             "ss_layer_all": (st, [vp, C.c_int]),
+            "ss_prefetch": (st, [vp, C.c_int, C.POINTER(i32), C.c_int, C.c_int]),
             "ss_acquire": (st, [vp, C.c_int, vp, C.POINTER(SsLayerView)]),
             "ss_acquire_groups": (st, [vp, C.c_int, vp, C.POINTER(SsLayerView)]),
             "ss_group_wait": (st, [vp, C.c_int, C.c_int, vp]),
@@ -152,10 +153,13 @@ def plan_json(desc_json: str, budget, benefit=None) -> dict:
         L.ss_desc_free(d)
 
 
-def host_run(desc_json: str, budget, options, routes: np.ndarray, mode: int = 0):
+def host_run(desc_json: str, budget, options, routes: np.ndarray, mode: int = 0, prefetch: np.ndarray | None = None,
+             checksums: bool = True):
     """The reference CPU backend over `routes` ([steps][layers][max_ids], -1 padded), the engine loop of the product's
     tse_host_run. Per step: {"stats": ..., "tables": [[(kind, index, offset) per unit] per layer], "groups": [...],
-    "checksums": [[...]]}; checksums are of the bytes the reference's table entries point at (host memory)."""
+    "checksums": [[...]]}; checksums are of the bytes the reference's table entries point at (host memory).
+    prefetch (same shape): after layer l's acquire, ss_prefetch of layer l + 1 with its row, CERTAIN on even steps and
+    SPECULATIVE on odd ones."""
     from tierstream_amd.ss import SsLayerStats, SsLayerView
     from .fixtures import engine_checksum
     L = lib()
@@ -191,6 +195,11 @@ def host_run(desc_json: str, budget, options, routes: np.ndarray, mode: int = 0)
                 if mode == 2:
                     for gi in range(1, v.n_groups):
                         _ck(L.ss_group_wait(ctx, l, gi, None))
+                if prefetch is not None and l + 1 < nl and L.ss_desc_layer_units(d, l + 1) > 0:
+                    q = np.ascontiguousarray(prefetch[s, l + 1], dtype=np.int32)
+                    m = int(np.sum(q >= 0))
+                    if m:
+                        _ck(L.ss_prefetch(ctx, l + 1, q.ctypes.data_as(C.POINTER(i32)), m, s % 2))
                 tab = []
                 for u in range(nu):
                     a = int(v.table_host[u])
@@ -203,7 +212,7 @@ def host_run(desc_json: str, budget, options, routes: np.ndarray, mode: int = 0)
                 ub = int(L.ss_desc_unit_bytes(d, l))
                 ids = list(range(nu)) if mode == 1 else [int(x) for x in r[:n]]
                 cks = []
-                for u in ids:
+                for u in (ids if checksums else []):
                     a = int(v.table_host[u])
                     cks.append(engine_checksum(np.frombuffer(C.string_at(a, ub), dtype=np.uint8)) if a else 0)
                 step["checksums"].append(cks)
@@ -366,6 +375,40 @@ def cpu_baseline_disk(n_units, persistent, bank, blocks, spare_target, part_byte
     names = ["misses", "fetched", "evicted", "writebacks_done", "hash_mismatches", "copied_bytes", "disk_reads",
              "disk_drops"]
     return ms, {k: int(v) for k, v in zip(names, out)}
+
+
+def host_exclusive(desc_json: str, budget, options, routes: np.ndarray) -> dict:
+    """The reference CPU backend in exclusive tier mode over `routes` (ss_layer_routes + ss_acquire per layer): its
+    ss_stats_exclusive after the last forward, as a dict."""
+    from tierstream_amd.ss import SsExclusiveStats, SsLayerView
+    L = lib()
+    L.ss_stats_exclusive_sized.restype = C.c_int
+    L.ss_stats_exclusive_sized.argtypes = [vp, C.POINTER(SsExclusiveStats), u32]
+    d, ctx = vp(), vp()
+    b = desc_json.encode()
+    _ck(L.ss_desc_from_json(b, len(b), C.byref(d)))
+    options.backend = 0  # SS_BACKEND_CPU
+    try:
+        _ck(L.ss_open(d, C.byref(budget), None, C.byref(options), C.byref(ctx)))
+        nl = L.ss_desc_n_layers(d)
+        for s in range(routes.shape[0]):
+            _ck(L.ss_begin(ctx, None, 0))
+            for l in range(nl):
+                if L.ss_desc_layer_units(d, l) <= 0:
+                    continue
+                r = np.ascontiguousarray(routes[s, l], dtype=np.int32)
+                _ck(L.ss_layer_routes(ctx, l, r.ctypes.data_as(C.POINTER(i32)), int(np.sum(r >= 0))))
+                v = SsLayerView()
+                _ck(L.ss_acquire(ctx, l, None, C.byref(v)))
+                _ck(L.ss_release(ctx, l, None))
+            _ck(L.ss_end(ctx))
+        x = SsExclusiveStats()
+        _ck(L.ss_stats_exclusive_sized(ctx, C.byref(x), C.sizeof(x)))
+        return {k: getattr(x, k) for k, _ in SsExclusiveStats._fields_ if k != "struct_size"}
+    finally:
+        if ctx:
+            L.ss_close(ctx)
+        L.ss_desc_free(d)
 
 
 def host_time(desc_json: str, budget, options, routes: np.ndarray, mode: int = 0):

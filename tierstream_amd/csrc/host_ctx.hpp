@@ -1,10 +1,14 @@
-// The host contract on one MI355X (ss_begin / ss_layer_routes / ss_layer_all / ss_acquire[_groups] / ss_group_wait /
-// ss_release / ss_end). Placement follows reference src/stream_ctx.cpp (init :69-272, jobs :433-706, forward
-// :1194-1709) decision for decision, so hit / miss / evict sequences, groups and table slots are identical; the device
-// side is this library's: slot pools and stream rings in HBM, a coarse-grained hipHostMalloc pinned tier, pinned-tier
-// misses as SDMA copies issued at once on the copy stream, file misses staged through pinned buffers by reader
-// threads, exclusive-mode write-backs on their own D2H stream, and (verify_hash = 2) every landed unit re-hashed in HBM
-// by the checkpoint-parallel XXH64 kernel.
+// The host contract on one MI355X (ss_seed / ss_begin / ss_layer_routes[_dev] / ss_layer_all / ss_prefetch /
+// ss_acquire[_groups] / ss_group_wait / ss_release / ss_end). HostPlacement decides every placement; this executor
+// carries its orders out:
+//  - layer pools and the stream ring in HBM, the pinned tier and exclusive-mode spare blocks in hipHostMalloc memory;
+//  - a copy from a pinned block is issued at once on one of two SDMA copy streams (alternating per unit);
+//  - a copy from a file is a job for the reader threads: direct-I/O reads into pinned staging, host XXH64, then the
+//    copy stream;
+//  - exclusive-mode write-backs run on their own device-to-host stream;
+//  - with verify_hash = 2 every landed unit is re-hashed in HBM (checkpoint-parallel XXH64, batched on a verify stream);
+//  - every wait the reference expresses as an event (a slot's last reader, a victim's write-back, a block's write-back,
+//    the copies of an earlier forward) is a device-side stream wait here.
 #pragma once
 
 #include <hip/hip_runtime_api.h>
@@ -20,30 +24,13 @@
 #include <vector>
 
 #include "hip_rt.hpp"
+#include "host_place.hpp"
 #include "json.hpp"
 #include "model.hpp"
-#include "residency.hpp"
 #include "source.hpp"
 #include "tierstream_amd/tsa.h"
 
 namespace tsa {
-
-struct HostJob {
-  enum State { Queued = 0, Running = 1, Done = 2, Cancelled = 3, Failed = 4 };
-  int layer = 0, unit = 0;
-  bool spec = false;
-  bool from_pinned = false;
-  bool host_dst = false;            // the pinned tier's own fill (file -> pinned host)
-  void* dst = nullptr;
-  const void* host_src = nullptr;   // pinned source
-  hipEvent_t dst_release_ev = nullptr, dst_wb_ev = nullptr, src_wait_ev = nullptr;
-  hipEvent_t done_ev = nullptr;
-  std::atomic<int> state{Queued};
-  ss_status err_status = SS_OK;
-  std::string err;
-  bool ran_as_demand = false;
-};
-using HostJobPtr = std::shared_ptr<HostJob>;
 
 // Where a table address points (test hook for parity): kind 1 = layer pool (index = layer), 2 = ring class.
 struct Region {
@@ -51,10 +38,10 @@ struct Region {
   uint64_t offset = 0;
 };
 
-class HostCtx {
+class HostCtx final : public HostWork {
  public:
   HostCtx(const Desc& d, const ss_budget& b, const Plan& p, const ss_options& o);
-  ~HostCtx();
+  ~HostCtx() override;
 
   void seed(int layer, const int32_t* units, int n);
   void begin(const uint32_t* rows, int n_layers);
@@ -73,14 +60,14 @@ class HostCtx {
   void end();
   void check_unit(int layer, int unit);
 
-  const ss_layer_stats& stats(int layer) const { return stats_[size_t(layer)]; }
+  const ss_layer_stats& stats(int layer) const { return place_.stats()[size_t(layer)]; }
   ss_layer_stats total() const;
   void stats_reset();
   void set_hook(ss_stats_hook h, void* user) {
     hook_ = h;
     hook_user_ = user;
   }
-  ss_exclusive_stats exclusive_stats() const;
+  ss_exclusive_stats exclusive_stats() const { return place_.exclusive_stats(); }
   int n_layers() const { return int(d_.layers.size()); }
   int n_sources() const { return int(files_.size()); }
   bool source_direct(int i) const { return files_[size_t(i)]->direct(); }
@@ -95,117 +82,102 @@ class HostCtx {
   bool snapshot_json(Json* out) const;
 
  private:
-  enum Loc : int8_t { None = 0, Persistent = 1, Ring = 2 };
-  struct RingSlot {
-    void* dev = nullptr;
-    uint64_t stride = 0;
-    int owner = -1;
-    HostJobPtr job;
+  // One copy onto the device (or, to_host, a pinned block's fill from the file at open).
+  struct Copy {
+    enum State : int { kQueued = 0, kRunning = 1, kDone = 2, kCancelled = 3, kFailed = 4 };
+    int32_t layer = 0, unit = 0;
+    bool speculative = false, to_host = false, demand_run = false;
+    void* dst = nullptr;
+    const void* src = nullptr;  // a pinned block, or null: the unit's file
+    hipEvent_t after[3] = {nullptr, nullptr, nullptr};  // dst's last reader, dst's victim write-back, src's write-back
+    hipEvent_t done_ev = nullptr;
+    std::atomic<int> state{kQueued};
+    ss_status status = SS_OK;
+    std::string what;
   };
-  struct RingClassState {
-    uint64_t stride;
-    size_t first, count, cursor;
-    void* base;
-  };
-  struct Staging {
-    void* host = nullptr;
-    hipEvent_t ev = nullptr;
-  };
-  struct LayerState {
-    std::unique_ptr<Residency> rs;
+  using CopyPtr = std::shared_ptr<Copy>;
+  struct LayerDev {
     void* pool = nullptr;
+    uint64_t stride = 0;
     hipEvent_t release_ev = nullptr, ready_ev = nullptr, ids_ev = nullptr;
-    bool ready_wait = false;
     void* table_dev[2] = {nullptr, nullptr};
     uint64_t* table_host[2] = {nullptr, nullptr};
     hipEvent_t table_ev[2] = {nullptr, nullptr};
     int version = 0;
-    std::vector<int8_t> loc;
-    std::vector<int32_t> slot;
-    std::vector<HostJobPtr> job;
-    std::vector<char> spec_unclaimed;
-    std::vector<int32_t> routed, pending, hits;
-    std::vector<uint32_t> count;
-    std::vector<std::vector<int32_t>> groups;
     std::vector<ss_group> group_view;
-    bool routes_given = false, acquired = false, released = false, skip = false;
-    int32_t* ids_host = nullptr;
+    int32_t* ids_host = nullptr;  // device routes copied back (ss_layer_routes_dev)
     size_t ids_cap = 0;
     int ids_n = -1;
   };
-  // verify_hash = 2: the device check of a landed unit (checkpoints of the unit, uploaded once per unit)
+  struct Staging {
+    void* host = nullptr;
+    hipEvent_t ev = nullptr;  // the last copy out of it
+  };
+  // verify_hash = 2: a unit's checkpoints in HBM (uploaded once, the first time its bytes pass the host hash)
   struct UnitCheck {
     uint64_t* states_dev = nullptr;
     uint64_t n_states = 0;
   };
 
+  // HostWork
+  void write_back(const WriteBackOrder& w) override;
+  void fetch(const FetchOrder& f) override;
+  void promote(int32_t job) override;
+  void retire(int32_t job) override;
+  bool settle(int32_t job, bool speculative) override;
+
   void init();
   void cleanup() noexcept;
-  void worker();
-  void run_job(HostJob& j);
-  void read_unit_host(int layer, int unit, void* dst, bool hash, uint64_t* digest);
-  void read_unit_device(HostJob& j);
-  void submit(const HostJobPtr& j);
-  void fail_job(HostJob& j, ss_status st, const char* msg) noexcept;
-  void promote(const HostJobPtr& j);
-  void wait_job(HostJob& j);
-  void wait_job_quiet(HostJob& j);
-  HostJobPtr make_job(int layer, int unit, void* dst, bool spec);
-  void fetch_into_persistent(int layer, int unit, int slot, bool spec, hipEvent_t dst_wb_ev = nullptr);
-  bool fetch_into_ring(int layer, int unit, bool spec);
-  void dispatch_pending();
-  void ingest_routes(int layer, const int32_t* ids, int n);
-  void ingest_dev_routes(int layer);
+  void reader_loop();
+  void read_file_unit(Copy& c);  // a reader thread: the unit's file bytes to its destination
+  void read_into_host(int layer, int unit, void* dst, bool hash, uint64_t* digest);
+  void stage_to_device(Copy& c);
+  void submit(const CopyPtr& c);
+  void finish(Copy& c, int state, ss_status st, const std::string& what) noexcept;
+  void await(Copy& c);       // until it ends; throws its error if it failed
+  void await_quiet(Copy& c);  // until it ends
+  size_t take_staging();
+  void give_staging(size_t i);
   void check_layer(int layer, const char* what) const;
   void check_stream(void* stream, const char* what);
-  void* unit_addr(int layer, int unit) const;
-  void open_forward();
-  void retire_ring(int layer);
-  hipEvent_t write_back(int layer, const Admission& a, bool speculative, size_t* n_wb);
-  void fetch_admitted(int layer, const Admission& a, bool spec);
-  uint64_t writeback_blocks(int layer, bool speculative) const;
-  int eviction_cap(int layer, bool speculative) const;
-  void free_block(int layer, int unit);
-  int block_class(int layer) const { return excl_ ? layer_class_[size_t(layer)] : -1; }
+  void ingest_dev_routes(int layer);
+  void* spot_addr(int layer, const DevSpot& s) const;
   hipEvent_t pooled_event();
-  int64_t gidx(int layer, int unit) const { return d_.unit_base[size_t(layer)] + unit; }
-  void verify_landed(const HostJob& j);  // verify_hash = 2: the unit joins the pending check batch (copy_mu_ held)
-  void flush_verify();                   // the pending batch: one launch on the verify stream behind its copies
+  int64_t gidx(int layer, int unit) const { return d_.gidx(layer, unit); }
+  hipStream_t next_copy_stream() { return (copy_alt_ = !copy_alt_) ? copy2_ : copy_; }
+  void join_copies();  // copy_ follows copy2_'s work so far (copy_mu_ held)
+  // verify_hash = 2
+  void verify_landed(const Copy& c);  // the unit joins the pending check batch (copy_mu_ held)
+  void flush_verify();                // the pending batch: one launch on the verify stream behind its copies
   void collect_verify();
+  void wait_slot_check(hipStream_t s, const void* dst);  // a slot's next copy waits for its pending check
+  void publish();
+  Json format_stats(uint64_t forwards, const ss_layer_stats* layers, const ss_exclusive_stats& x) const;
 
   Desc d_;
   Plan plan_;
   ss_options o_;
+  HostPlacement place_;
   std::unique_ptr<HipDevice> dev_;
-  // Pinned -> HBM copies alternate between copy_ and copy2_ (two SDMA queues: one queue's per-copy gap is about 6 % of
-  // a 9 MiB unit's copy time); the other copies use copy_. join_copies() makes copy_ follow copy2_'s work so far, so
-  // an event recorded on copy_ after it stands for every copy before it.
+  std::vector<std::unique_ptr<SourceFile>> files_;
+  std::vector<LayerDev> L_;
+  // Pinned -> HBM copies alternate between copy_ and copy2_ (two SDMA queues); other copies use copy_.
   hipStream_t copy_ = nullptr, copy2_ = nullptr, wb_ = nullptr;
   hipEvent_t join_ev_ = nullptr;
   bool copy_alt_ = false;
-  hipStream_t next_copy_stream() { return (copy_alt_ = !copy_alt_) ? copy2_ : copy_; }
-  void join_copies();  // (copy_mu_ held)
-  std::vector<std::unique_ptr<SourceFile>> files_;
-  std::vector<LayerState> L_;
-  std::vector<RingSlot> ring_;
-  std::vector<hipEvent_t> ring_owner_ev_;
-  std::vector<hipEvent_t> ev_pool_, all_events_;
-  std::vector<RingClassState> ring_classes_;
-  std::vector<void*> pinned_chunks_;
-  std::vector<const void*> pinned_of_;
-
-  bool excl_ = false;
-  std::vector<uint64_t> block_bytes_;
-  std::vector<int> layer_class_;
-  std::vector<std::vector<void*>> free_blocks_;
-  std::vector<void*> spare_chunks_;
-  std::vector<hipEvent_t> wb_pending_;
-  std::vector<int64_t> wb_units_;
-  std::vector<hipEvent_t> wb_evs_;
+  std::vector<void*> ring_base_;     // per ring class
+  std::vector<void*> ring_addr_;     // per ring slot
+  std::vector<void*> host_chunks_;   // the pinned tier and the spare blocks
+  std::vector<void*> block_addr_;    // per pinned block
+  uint64_t excl_blocks_ = 0;         // exclusive mode: blocks of the block classes (homes + spares)
+  std::vector<hipEvent_t> wb_ev_;    // this forward's write-back batches
   hipEvent_t blocks_ev_ = nullptr, wb_mark_ev_ = nullptr;
-  bool wb_gate_ = false;
-  std::vector<uint64_t> spares_of_;
-  ss_exclusive_stats xst_{};
+  bool wb_gate_ = false;             // the next write-back waits for blocks_ev_ (the last forward's block readers)
+  std::vector<hipEvent_t> ev_pool_, all_events_;
+  std::vector<CopyPtr> jobs_;        // this forward's, by job id
+  std::vector<CopyPtr> fills_;       // open and seed fills
+  ss_status fwd_failed_ = SS_OK;     // the first failed job of the forward (settle)
+  std::string fwd_error_;
 
   std::vector<Staging> staging_;
   std::vector<size_t> staging_free_;
@@ -213,42 +185,38 @@ class HostCtx {
   std::condition_variable staging_cv_;
   std::mutex copy_mu_;
 
+  // reader threads: demand reads first; a speculative read only while no demand waits and at most one runs
   std::mutex q_mu_;
   std::condition_variable q_cv_, done_cv_;
-  std::deque<HostJobPtr> demand_q_, spec_q_;
+  std::deque<CopyPtr> demand_q_, spec_q_;
   int demand_running_ = 0;
   bool stop_ = false;
-  std::vector<std::thread> workers_;
+  std::vector<std::thread> readers_;
 
   // verify_hash = 2
   bool dverify_ = false;
   uint64_t seg_bytes_ = 0;
   std::vector<UnitCheck> checks_;  // per global unit (with a descriptor hash)
-  void* vtable_dev_ = nullptr;     // tsa_verify_unit slots, one per possible in-flight verify
+  void* vtable_dev_ = nullptr;     // tsa_verify_unit slots, one per possible in-flight check
   uint32_t* vfail_dev_ = nullptr;
   tsa_verify_unit* vtable_host_ = nullptr;
   uint32_t* vfail_host_ = nullptr;
   size_t vcap_ = 0, vused_ = 0, vflushed_ = 0;  // table slots used this forward; the ones already launched
   hipStream_t vstream_ = nullptr;                 // the checks (copies never queue behind them)
-  hipEvent_t vready2_ev_ = nullptr;               // the second copy stream at a flush
-  hipEvent_t vready_ev_ = nullptr;                // the copy stream at a flush: the batch's copies are done
-  std::vector<std::pair<int, int>> vunits_;  // (layer, unit) of each verify slot this forward
-  // A landed unit's check reads its slot until the check's launch completes, so the next copy into that slot waits for
-  // it: the slot's pending entry (since the last collect), the flush that launched each entry, and per flush an event
-  // on the verify stream after its launch.
+  hipEvent_t vready_ev_ = nullptr, vready2_ev_ = nullptr;  // the two copy streams at a flush
+  std::vector<std::pair<int, int>> vunits_;  // (layer, unit) of each check slot this forward
+  // a landed unit's check reads its slot until its launch completes: the slot's pending entry, the flush that launched
+  // each entry, and per flush an event on the verify stream after its launch
   std::unordered_map<const void*, size_t> vdst_;
   std::vector<uint32_t> ventry_flush_;
   std::vector<hipEvent_t> vflush_ev_;
   uint32_t vflushes_ = 0;
-  void wait_slot_check(hipStream_t s, const void* dst);  // (copy_mu_ held)
   hipEvent_t vdone_ev_ = nullptr;
   uint64_t verify_fail_total_ = 0;
 
   void* fwd_stream_ = nullptr;
   bool fwd_stream_set_ = false;
-  bool poisoned_ = false, in_forward_ = false, fwd_open_ = false;
-  uint64_t forward_ = 0;
-  uint64_t n_blocks_ = 0;  // EXCLUSIVE: the pinned blocks (the homes of the pinned units and the spares)
+  bool poisoned_ = false;
   struct Published {
     uint64_t seq = 0, forwards = 0;
     std::vector<ss_layer_stats> layers;
@@ -257,10 +225,6 @@ class HostCtx {
   mutable std::atomic<bool> snap_armed_{false};
   mutable std::mutex snap_mu_;
   Published snap_;
-  void publish();
-  Json format_stats(uint64_t forwards, const ss_layer_stats* layers, const ss_exclusive_stats& x) const;
-  std::vector<HostJobPtr> fwd_jobs_;
-  std::vector<ss_layer_stats> stats_, fwd_stats_;
   ss_stats_hook hook_ = nullptr;
   void* hook_user_ = nullptr;
 };

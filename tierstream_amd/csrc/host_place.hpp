@@ -1,0 +1,195 @@
+// The host contract's placement, with no device in it: which units of a forward are hits, which are admitted into a
+// layer's pool of persistent slots (evicting whom), which stream through the ring of shared slots (and in which slot),
+// which wait for a ring slot, which pinned block each copy reads and each exclusive-mode victim is written back to,
+// how a layer's units are grouped, and every counter. It decides; a HostWork carries each decision out on a device as
+// it is made (the MI355X executor in host_ctx.cpp, or nothing at all in the CPU placement tests).
+//
+// The decisions are the reference's host contract (src/stream_ctx.cpp: ingest_routes :1303-1355, prefetch :1401-1439,
+// acquire :1459-1521, release :1572-1590, end :1600-1709; slot admission in residency.hpp), so hit / miss / evict
+// sequences, ring slots, groups and the address tables are the reference's for the same call sequence. What is this
+// library's own is the split: placement is a pure state machine driven by the ss_* calls, so its tables can be
+// compared with the reference's on the CPU, and the executor only maps orders to copies, events and reads.
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <vector>
+
+#include "model.hpp"
+#include "residency.hpp"
+
+namespace tsa {
+
+// Where a unit's bytes are on the device in this forward.
+struct DevSpot {
+  enum Kind : int8_t { kNone = 0, kPool = 1, kRing = 2 };
+  Kind kind = kNone;
+  int32_t index = -1;  // kPool: slot of the unit's layer pool; kRing: global ring slot (-1 while waiting for one)
+};
+
+// A copy of unit (layer, unit) into dst. Forward jobs are numbered from 0 in each forward; fills (open, seeds) use
+// job -1.
+struct FetchOrder {
+  int32_t job = -1;
+  int32_t layer = 0, unit = 0;
+  bool speculative = false;
+  DevSpot dst;
+  int32_t after_release = -1;    // the copy waits for this layer's last ss_release (dst's previous reader), -1: none
+  int32_t after_writeback = -1;  // dst held a victim written back by this batch of the forward, -1: none
+  int32_t src_block = -1;        // the pinned block with the unit's bytes, -1: read them from the file
+  int32_t src_writeback = -1;    // exclusive: the batch of this forward that writes src_block, -1: none
+};
+
+// Exclusive mode: victims of one admission leave their pool slots for free blocks (batch: numbered per forward).
+struct WriteBackOrder {
+  int32_t batch = 0, layer = 0;
+  std::vector<int32_t> units, slots, blocks;  // parallel
+};
+
+// A pinned block: the pinned-tier home of a unit (home >= 0, its global index) or a spare of block class `cls`.
+struct BlockHome {
+  int64_t home = -1;
+  int32_t cls = -1;
+};
+
+class HostWork {
+ public:
+  virtual ~HostWork() = default;
+  virtual void write_back(const WriteBackOrder& w) = 0;
+  virtual void fetch(const FetchOrder& f) = 0;
+  virtual void promote(int32_t job) = 0;  // a speculative job was routed: it becomes a demand
+  virtual void retire(int32_t job) = 0;   // its ring slot was released: cancel it if it never started, else wait
+  // End of forward, in job order: cancel a speculative job that never started, else wait for it; true when it ran to
+  // completion.
+  virtual bool settle(int32_t job, bool speculative) = 0;
+};
+
+class HostPlacement {
+ public:
+  HostPlacement(const Desc& d, const Plan& p, const ss_options& o);
+  void attach(HostWork* w) { w_ = w; }
+
+  // ---- the layout the executor allocates
+  bool exclusive() const { return excl_; }
+  int pool_slots(int layer) const { return L_[size_t(layer)].pool ? L_[size_t(layer)].pool->capacity() : 0; }
+  struct RingClassInfo {
+    uint64_t stride;
+    uint32_t first, count;
+  };
+  const std::vector<RingClassInfo>& ring_classes() const { return ring_cls_; }
+  uint32_t ring_slots() const { return uint32_t(ring_.size()); }
+  const std::vector<BlockHome>& blocks() const { return blocks_; }
+  const std::vector<uint64_t>& block_class_bytes() const { return class_bytes_; }
+  uint64_t block_count() const { return blocks_.size(); }
+
+  // ---- open and between forwards
+  // The planned residents' pool slots; with fill_residents, one fill copy each (job -1) through HostWork::fetch.
+  void place_residents();
+  // ss_seed: free slots only (seeds never evict); returns the units placed, each with its fill through fetch().
+  std::vector<int32_t> seed(int layer, const int32_t* units, int n);
+  void seed_landed(int layer, int32_t unit, bool ok);  // a failed fill is dropped; exclusive: a landed one's block frees
+
+  // ---- a forward
+  void begin(const uint32_t* rows, int n_layers);
+  bool forward_open() const { return fwd_open_; }
+  bool in_forward() const { return in_fwd_; }
+  bool routes_given(int layer) const { return L_[size_t(layer)].routes_in; }
+  void routes(int layer, const int32_t* ids, int n);
+  void routes_all(int layer);
+  void prefetch(int layer, const int32_t* ids, int n, bool speculative);
+  struct Acquire {
+    bool wait_ready = false;         // wait for the copies of earlier forwards into this layer's pool
+    std::vector<int32_t> wait_jobs;  // (wait_all) every fetched routed unit's job, group order
+  };
+  // ss_acquire in two steps: the units waiting for a ring slot are placed (or SS_E_CAPACITY), the groups are formed
+  // and the jobs to wait for listed; once those waits succeeded, take_table builds the layer's table and marks it
+  // acquired.
+  Acquire acquire(int layer, bool wait_all);
+  const std::vector<DevSpot>& take_table(int layer);
+  const std::vector<DevSpot>& table(int layer) const { return L_[size_t(layer)].table; }
+  const std::vector<std::vector<int32_t>>& groups(int layer) const { return L_[size_t(layer)].groups; }
+  std::vector<int32_t> group_jobs(int layer, int group) const;  // ss_group_wait's jobs (group 0: none)
+  bool acquired(int layer) const { return L_[size_t(layer)].acquired; }
+  bool released(int layer) const { return L_[size_t(layer)].released; }
+  int32_t job_of(int layer, int unit) const { return L_[size_t(layer)].job[size_t(unit)]; }
+  void release(int layer);
+  struct Ended {
+    std::vector<int> landed_layers;  // layers with a pool copy issued this forward (their next acquire waits)
+    uint32_t writeback_batches = 0;
+  };
+  Ended end();  // every job settled (HostWork::settle); residency, blocks and counters of the forward folded
+  void add_wait_ns(int layer, uint64_t ns) { fwd_[size_t(layer)].wait_ns += ns; }
+
+  // ---- counters
+  const std::vector<ss_layer_stats>& stats() const { return total_; }
+  const std::vector<ss_layer_stats>& forward_stats() const { return fwd_; }
+  void reset_stats();
+  const ss_exclusive_stats& exclusive_stats() const { return xst_; }
+  uint64_t forwards() const { return forwards_; }
+
+ private:
+  struct LayerPlace {
+    std::unique_ptr<SlotPool> pool;  // null: the layer has no units
+    int32_t cls = -1;                // exclusive: its block class
+    // this forward
+    std::vector<DevSpot> spot;
+    std::vector<int32_t> job;
+    std::vector<uint8_t> spec_open;  // fetched speculatively and not routed (yet)
+    std::vector<uint32_t> uses;      // occurrences in the routes
+    std::vector<int32_t> routed, hits, waiting;
+    std::vector<std::vector<int32_t>> groups;
+    std::vector<DevSpot> table;
+    bool routes_in = false, acquired = false, released = false, skipped = false;
+    bool ready_wait = false;  // across forwards: the next acquire waits for the pool copies of the last one
+  };
+  struct RingSlot {
+    int32_t cls = 0, owner = -1, job = -1;
+    int32_t last_reader = -1;  // the layer that released it last
+  };
+  struct Job {
+    int32_t layer, unit;
+    bool speculative, pool;
+  };
+
+  void open_forward();
+  LayerPlace& layer_with_units(int layer, const char* what);
+  int32_t new_job(int layer, int unit, bool speculative, bool pool);
+  FetchOrder order_for(int layer, int unit, bool speculative);
+  void fetch_pool(int layer, int unit, int32_t slot, bool speculative, int32_t after_writeback);
+  bool fetch_ring(int layer, int unit, bool speculative);
+  void admit(int layer, const Admission& a, bool speculative);  // write-backs, then the admitted units' copies
+  uint64_t free_for_writeback(int layer, bool speculative) const;
+  int eviction_cap(int layer, bool speculative) const;
+  void give_back_block(int layer, int unit);  // a promoted unit's block returns to its class's free list
+  void drain_waiting();
+  void take_routes(int layer, const int32_t* ids, int n);
+  uint64_t free_blocks_now() const;
+
+  const Desc& d_;
+  const Plan& p_;
+  ss_options o_;
+  HostWork* w_ = nullptr;
+  bool excl_ = false;
+  std::vector<LayerPlace> L_;
+  std::vector<RingClassInfo> ring_cls_;
+  std::vector<uint32_t> ring_cursor_;
+  std::vector<RingSlot> ring_;
+  // pinned blocks: the units' homes, then the spares; block_of_[g] the block a unit's bytes are in (-1: its file)
+  std::vector<BlockHome> blocks_;
+  std::vector<uint64_t> class_bytes_;
+  std::vector<uint64_t> class_spares_;
+  std::vector<int32_t> block_of_;
+  std::vector<std::vector<int32_t>> free_;  // per class, taken from the back
+  std::vector<int32_t> wb_batch_of_;        // per global unit: this forward's write-back batch into its block, -1
+  std::vector<int64_t> wb_touched_;
+  int32_t wb_batches_ = 0;
+  std::vector<Job> jobs_;
+  bool fwd_open_ = false, in_fwd_ = false;
+  uint64_t forwards_ = 0;
+  std::vector<ss_layer_stats> fwd_, total_;
+  ss_exclusive_stats xst_{};
+};
+
+void add_stats(ss_layer_stats& a, const ss_layer_stats& b);
+
+}  // namespace tsa

@@ -1,0 +1,117 @@
+// Test hook over the host contract's placement alone (tsa_test_hostplace_run in tsa_test.h): HostPlacement driven by
+// the engine's forward loop on a HostWork that does nothing and reports every copy as complete, so the tables, groups
+// and counters can be compared with the reference CPU backend's on the CPU (the reference's own tests drive its
+// runtime the same way: tests/test_runtime.cpp).
+#include <cstring>
+#include <vector>
+
+#include "common.hpp"
+#include "host_place.hpp"
+#include "tierstream_amd/tsa_test.h"
+
+namespace tsa {
+namespace {
+
+class NoDevice final : public HostWork {
+ public:
+  void write_back(const WriteBackOrder&) override {}
+  void fetch(const FetchOrder&) override {}
+  void promote(int32_t) override {}
+  void retire(int32_t) override {}
+  bool settle(int32_t, bool) override { return true; }
+};
+
+}  // namespace
+}  // namespace tsa
+
+extern "C" {
+
+ss_status tsa_test_hostplace_run(const char* desc_json, size_t len, const ss_budget* budget, const ss_options* opt,
+                                 int steps, const int32_t* routes, const int32_t* prefetch, int max_ids, int mode,
+                                 int max_units, int32_t* spot_kind, int32_t* spot_index, int32_t* group_of,
+                                 ss_layer_stats* stats) {
+  return tsa::guard([&] {
+    using namespace tsa;
+    require(desc_json && budget && opt && routes && steps >= 0 && max_ids > 0 && max_units > 0 && mode >= 0 &&
+                mode <= 2,
+            SS_E_INVALID, "tsa_test_hostplace_run: bad argument");
+    const Desc d = desc_from_json(json_parse(std::string(desc_json, len)));
+    const Plan p = plan_make(d, *budget, {});
+    NoDevice dev;
+    HostPlacement place(d, p, *opt);
+    place.attach(&dev);
+    place.place_residents();
+    const int L = int(d.layers.size());
+    std::vector<int32_t> ids(static_cast<size_t>(max_ids));
+    for (int s = 0; s < steps; ++s) {
+      place.begin(nullptr, 0);
+      for (int l = 0; l < L; ++l) {
+        const int nu = d.layers[size_t(l)].n_units;
+        if (nu <= 0) continue;
+        const int32_t* r = routes + (size_t(s) * L + l) * max_ids;
+        int n = 0;
+        while (n < max_ids && r[n] >= 0) ++n;
+        if (mode == 1) place.routes_all(l);
+        else place.routes(l, r, n);
+        const HostPlacement::Acquire a = place.acquire(l, mode != 2);
+        (void)a;
+        const std::vector<DevSpot>& t = place.take_table(l);
+        const size_t base = (size_t(s) * L + l) * max_units;
+        for (int u = 0; u < nu && u < max_units; ++u) {
+          spot_kind[base + u] = t[size_t(u)].kind;
+          spot_index[base + u] = t[size_t(u)].index;
+          group_of[base + u] = -1;
+        }
+        const auto& groups = place.groups(l);
+        for (size_t gi = 0; gi < groups.size(); ++gi)
+          for (int32_t u : groups[gi])
+            if (u < max_units) group_of[base + size_t(u)] = int32_t(gi);
+        // the next layer's prediction, made while this layer computes (CERTAIN on even steps, SPECULATIVE on odd)
+        if (prefetch && l + 1 < L && d.layers[size_t(l + 1)].n_units > 0) {
+          const int32_t* q = prefetch + (size_t(s) * L + l + 1) * max_ids;
+          int m = 0;
+          while (m < max_ids && q[m] >= 0) ++m;
+          if (m) place.prefetch(l + 1, q, m, s % 2 == 1);
+        }
+        place.release(l);
+      }
+      place.end();
+      stats[s] = ss_layer_stats{};
+      for (const ss_layer_stats& x : place.forward_stats()) add_stats(stats[s], x);
+    }
+  });
+}
+
+ss_status tsa_test_hostplace_exclusive(const char* desc_json, size_t len, const ss_budget* budget,
+                                       const ss_options* opt, int steps, const int32_t* routes, int max_ids, int mode,
+                                       ss_exclusive_stats* out) {
+  return tsa::guard([&] {
+    using namespace tsa;
+    require(desc_json && budget && opt && routes && out, SS_E_INVALID, "tsa_test_hostplace_exclusive: bad argument");
+    const Desc d = desc_from_json(json_parse(std::string(desc_json, len)));
+    const Plan p = plan_make(d, *budget, {});
+    NoDevice dev;
+    HostPlacement place(d, p, *opt);
+    place.attach(&dev);
+    place.place_residents();
+    const int L = int(d.layers.size());
+    for (int s = 0; s < steps; ++s) {
+      place.begin(nullptr, 0);
+      for (int l = 0; l < L; ++l) {
+        if (d.layers[size_t(l)].n_units <= 0) continue;
+        const int32_t* r = routes + (size_t(s) * L + l) * max_ids;
+        int n = 0;
+        while (n < max_ids && r[n] >= 0) ++n;
+        if (mode == 1) place.routes_all(l);
+        else place.routes(l, r, n);
+        place.acquire(l, mode != 2);
+        place.take_table(l);
+        place.release(l);
+      }
+      place.end();
+    }
+    *out = place.exclusive_stats();
+  });
+}
+
+}  // extern "C"
