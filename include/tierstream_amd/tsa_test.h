@@ -106,6 +106,13 @@ SS_API ss_status tsa_test_hostplace_run(const char* desc_json, size_t len, const
                                         const int32_t* prefetch, int max_ids, int mode, int max_units,
                                         int32_t* spot_kind, int32_t* spot_index, int32_t* group_of,
                                         ss_layer_stats* stats);
+/* The device-gated open's geometry alone (no device): the descriptor, the budget and the plan (tiers, one per unit in
+ * descriptor order; NULL: plan_make) under the options. out[0..18]: keys, gated layers, R, D, B, P, F, Q, I, staging
+ * buffers, disk queue, persistent slots, slots, guard slot, blocks, scored, w_trans, w_freq, w_rec; residents: the
+ * planned residents' keys (up to res_cap). A refused configuration returns its status. */
+SS_API ss_status tsa_test_dg_geometry(const char* desc_json, size_t len, const ss_budget* budget, const uint8_t* tiers,
+                                      size_t n_tiers, const ss_options* opt, uint32_t* out, uint32_t* residents,
+                                      uint32_t res_cap);
 /* The same loop without prefetch; the exclusive-mode counters after the last forward. */
 SS_API ss_status tsa_test_hostplace_exclusive(const char* desc_json, size_t len, const ss_budget* budget,
                                               const ss_options* opt, int steps, const int32_t* routes, int max_ids,

@@ -48,6 +48,7 @@
 #include "dg_core.hpp"
 #include "dg_score.hpp"
 #include "stream_ctx.hpp"
+#include "dg_layout.hpp"
 #include "xxh64.hpp"
 #undef private
 #undef protected
@@ -408,6 +409,34 @@ int refdg_set_wb_defer(void* h, uint32_t on) {
 }
 
 void refdg_close(void* h) { delete static_cast<RefDg*>(h); }
+
+}  // extern "C"
+
+// ---- the device-gated layout -------------------------------------------------------------------------------------------
+
+extern "C" {
+
+// The reference's dg_layout over a descriptor, a budget, the plan (tiers, one per unit; null: plan_make) and the
+// options. Returns the refusal's status (0 = laid out); out[0..18]: keys, G, R, D, B, P, F, Q, I, S, disk_queue,
+// persistent_slots, slots, guard_slot, blocks, scored, w_trans, w_freq, w_rec; residents: the tier-R keys.
+int ref_dg_layout(const char* desc_json, size_t len, const ss_budget* b, const uint8_t* tiers, size_t n_tiers,
+                  const ss_options* o, uint32_t* out, uint32_t* residents, uint32_t res_cap, char* err, size_t err_cap) {
+  try {
+    const ts::Desc d = ts::desc_from_json(ts::json_parse(std::string(desc_json, len)));
+    const ts::Plan p = tiers ? ts::plan_from_tiers(d, *b, std::vector<uint8_t>(tiers, tiers + n_tiers))
+                             : ts::plan_make(d, *b, {});
+    const ts::DgLayout x = ts::dg_layout(d, p, *o);
+    const uint32_t v[] = {x.keys, uint32_t(x.gated.size()), x.R, x.D, x.B, x.P, x.F, x.Q, x.I, x.S, x.disk_queue,
+                          x.persistent_slots, x.slots, x.guard_slot, x.blocks, uint32_t(x.scored), x.w_trans,
+                          x.w_freq, x.w_rec};
+    std::memcpy(out, v, sizeof v);
+    for (uint32_t i = 0; i < res_cap && i < x.residents.size(); ++i) residents[i] = x.residents[i];
+    return 0;
+  } catch (const ts::Error& e) {
+    std::snprintf(err, err_cap, "%s", e.what());
+    return int(e.status());
+  }
+}
 
 }  // extern "C"
 

@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "dg_core.hpp"
+#include "dg_geometry.hpp"
 #include "dg_proto.hpp"
 #include "hip_rt.hpp"
 #include "score_profile.hpp"
@@ -38,193 +39,8 @@ constexpr uint64_t kReadPiece = 8ull << 20;        // three-tier reads in flight
 
 uint64_t align64(uint64_t v) { return (v + 63) / 64 * 64; }
 
-// ---- layout: refusals and geometry (reference src/dg_layout.cpp:182-446, the two-tier subset) ---------------------
-struct Layout {
-  std::vector<int> gated, ordinal;
-  std::vector<uint32_t> unit_base;
-  std::vector<uint64_t> part_bytes, part_offset;
-  uint64_t unit_bytes = 0, host_stride = 0;
-  uint32_t keys = 0, R = 0, D = 0, B = 0, P = 0, Q = 0, I = 0;
-  uint32_t persistent_slots = 0, slots = 0, guard_slot = 0, blocks = 0;
-  std::vector<uint32_t> residents;
-  // three-tier: F file-tier units (plan tier DISK), their flags in key order, S staging buffers, reads in flight
-  bool disk_tier = false, disk_prefetch = false;
-  uint32_t F = 0, S = 0, disk_queue = 0;
-  std::vector<uint8_t> disk;
-  // scored eviction: the weights (all three 0 in the options: 700 / 200 / 100) and the profile's model identity
-  bool scored = false;
-  uint32_t w_trans = 700, w_freq = 200, w_rec = 100;
-  std::string score_identity;
-};
-
-Layout make_layout(const Desc& d, const Plan& p, const ss_options& o) {
-  auto refuse = [](ss_status st, const std::string& why) { fail(st, "device-gated: " + why); };
-  const ss_budget& b = p.budget;
-  if (b.tier_mode != SS_TIER_MODE_EXCLUSIVE) refuse(SS_E_INVALID, "needs tier_mode EXCLUSIVE");
-  if (b.pinned_backing) refuse(SS_E_INVALID, "pinned_backing is refused (each unit has one home)");
-  const bool scored = o.policy == SS_POLICY_SCORED || o.policy == SS_POLICY_SCORED_AUTO;
-  if (o.policy != SS_POLICY_LRU && !scored) refuse(SS_E_INVALID, "policy must be LRU or SCORED or SCORED_AUTO");
-  if ((o.dg_score_profile_len || o.dg_score_profile) && !scored)
-    refuse(SS_E_INVALID, "dg_score_profile needs policy SCORED");
-  if (o.pin_planned) refuse(SS_E_INVALID, "needs pin_planned = 0 (planned residents are a warm start)");
-  if (!o.fill_residents) refuse(SS_E_INVALID, "needs fill_residents = 1 (a resident's slot is its only copy)");
-  if (o.readahead_units) refuse(SS_E_INVALID, "readahead_units must be 0 (no gated unit is read from its file)");
-  if (o.spec_persistent) refuse(SS_E_INVALID, "spec_persistent is refused (prediction is the service's)");
-  if (o.dg_max_ids < 1 || o.dg_max_ids > kDgMaxIds) refuse(SS_E_INVALID, "dg_max_ids must be 1..64 (rows x top_k)");
-  if (o.dg_wait_timeout_ms < 1) refuse(SS_E_INVALID, "dg_wait_timeout_ms must be >= 1");
-  if (o.dg_wb_defer > 1) refuse(SS_E_INVALID, "dg_wb_defer must be 0 or 1");
-  if (o.dg_wb_stream > 1) refuse(SS_E_INVALID, "dg_wb_stream must be 0 or 1");
-  // the three-tier file path (reference src/dg_layout.cpp:200-225): landings, the adaptive depth and kept bank reads
-  // are not part of this library's serve path
-  if (o.dg_disk_tier > 1 || o.dg_disk_prefetch > 1) refuse(SS_E_INVALID, "dg_disk_tier / dg_disk_prefetch must be 0 or 1");
-  const bool queue_auto = o.dg_disk_queue == 0xFFFFFFFFu;
-  if (!o.dg_disk_tier && (o.dg_disk_prefetch || o.dg_disk_staging || (o.dg_disk_queue && !queue_auto)))
-    refuse(SS_E_INVALID, "dg_disk_prefetch / dg_disk_staging / dg_disk_queue need dg_disk_tier = 1");
-  if (o.dg_disk_staging > 256) refuse(SS_E_INVALID, "dg_disk_staging must be 0..256");
-  if (o.dg_disk_queue > 64 && !queue_auto) refuse(SS_E_INVALID, "dg_disk_queue must be 0..64 or SS_DG_DISK_QUEUE_AUTO");
-  if (o.dg_landing_blocks || o.dg_landing_max_queued || o.dg_landing_ttl || o.dg_landing_chunk || o.dg_bank_keep ||
-      o.dg_disk_queue_adapt)
-    refuse(SS_E_UNSUPPORTED, "landings (dg_landing_*), dg_bank_keep and dg_disk_queue_adapt are not part of this "
-                             "library's serve path");
-  if (o.dg_no_admit || o.dg_pf_revert_unused || o.dg_pf_strict_admit || o.dg_prior_len || o.dg_prior)
-    refuse(SS_E_UNSUPPORTED, "dg_no_admit / dg_pf_revert_unused / dg_pf_strict_admit / priors are not part of this "
-                             "library's serve path");
-  if (o.dg_clean_evict > 1) refuse(SS_E_INVALID, "dg_clean_evict must be 0 or 1");
-
-  Layout x;
-  x.B = o.dg_max_ids;
-  x.ordinal.assign(d.layers.size(), -1);
-  const Layer* shape = nullptr;
-  for (size_t L = 0; L < d.layers.size(); ++L) {
-    const Layer& l = d.layers[L];
-    if (l.n_units == 0) continue;
-    if (!l.streamable)
-      refuse(SS_E_UNSUPPORTED, "layer " + std::to_string(l.index) + " has non-streamable units (every unit is gated)");
-    if (!shape) {
-      shape = &l;
-      if (l.parts.size() > SS_DG_MAX_PARTS) refuse(SS_E_UNSUPPORTED, "more than 4 parts per unit");
-      uint64_t off = 0;
-      for (const Part& part : l.parts) {
-        if (part.bytes % 256 != 0)
-          refuse(SS_E_UNSUPPORTED, "part " + part.name + " is " + std::to_string(part.bytes) +
-                                       " bytes, not a multiple of 256 (the arena stride equals the part bytes)");
-        x.part_bytes.push_back(part.bytes);
-        x.part_offset.push_back(off);
-        off += part.bytes;
-      }
-      x.unit_bytes = l.unit_bytes;
-    } else {
-      bool same = l.parts.size() == shape->parts.size();
-      for (size_t i = 0; same && i < l.parts.size(); ++i) same = l.parts[i].bytes == shape->parts[i].bytes;
-      if (!same) refuse(SS_E_UNSUPPORTED, "layer " + std::to_string(l.index) + " has another part shape (one arena)");
-    }
-    x.ordinal[L] = int(x.gated.size());
-    x.gated.push_back(int(L));
-  }
-  if (x.gated.empty()) refuse(SS_E_INVALID, "the descriptor has no streamable units");
-  x.host_stride = host_stride(x.unit_bytes);
-  x.unit_base.assign(1, 0);
-  uint64_t keys = 0;
-  for (int L : x.gated) {
-    const Layer& l = d.layers[size_t(L)];
-    uint32_t planned = 0;
-    for (int u = 0; u < l.n_units; ++u) {
-      const uint8_t t = p.tier[size_t(d.unit_base[size_t(L)] + u)];
-      if (t == SS_TIER_RESIDENT) {
-        x.residents.push_back(uint32_t(keys + uint64_t(u)));
-        ++planned;
-      } else if (t == SS_TIER_PINNED) {
-        ++x.P;
-      } else if (t == SS_TIER_DISK && o.dg_disk_tier) {
-        ++x.F;
-      } else {
-        refuse(SS_E_CAPACITY, "unit (" + std::to_string(l.index) + ", " + std::to_string(u) +
-                                  ") is not resident or pinned (no gated unit is read from its file)");
-      }
-    }
-    x.D += std::min<uint32_t>(b.dynamic_slots_per_layer, uint32_t(l.n_units) - planned);
-    if (o.dg_disk_tier)
-      for (int u = 0; u < l.n_units; ++u)
-        x.disk.push_back(p.tier[size_t(d.unit_base[size_t(L)] + u)] == SS_TIER_DISK ? 1 : 0);
-    keys += uint64_t(l.n_units);
-    require(keys < 0x7fffffffull, SS_E_INVALID, "device-gated: more than 2^31 - 1 gated units");
-    x.unit_base.push_back(uint32_t(keys));
-  }
-  x.keys = uint32_t(keys);
-  x.R = uint32_t(x.residents.size());
-  x.disk_tier = o.dg_disk_tier != 0;
-  x.disk_prefetch = o.dg_disk_prefetch != 0;
-  // reads in flight (reference include/strix_stream/ss.h:318-334): 0 and 1 = one read inside its fetch; 2..64 = that
-  // many reader threads; AUTO = 4 (one read location: this library reads each source from its own file only), raised
-  // staging when dg_disk_staging is left at 0, cut to an explicit dg_disk_staging
-  if (x.disk_tier) {
-    const uint32_t q = queue_auto ? 4u : std::max<uint32_t>(o.dg_disk_queue, 1u);
-    x.S = o.dg_disk_staging ? o.dg_disk_staging : std::max<uint32_t>(8u, q);
-    x.disk_queue = std::min(q, x.S);
-  }
-  if (o.dg_spare_slots) {
-    if (o.dg_spare_slots > x.P + x.F)
-      refuse(SS_E_INVALID, "dg_spare_slots " + std::to_string(o.dg_spare_slots) + " above the non-resident units (" +
-                               std::to_string(x.P + x.F) + ")");
-    x.D = o.dg_spare_slots;
-  }
-  if (x.D < 1)
-    refuse(SS_E_INVALID, "needs dynamic_slots_per_layer > 0 or dg_spare_slots > 0 (the spare slots; the boundary keeps "
-                         "them free)");
-  const uint64_t stride = d.unit_stride(x.gated[0]);
-  uint32_t ring_slots = 0;
-  for (const RingClass& rc : p.rings)
-    if (rc.stride == stride) ring_slots = rc.slots;
-  if (uint64_t(ring_slots) < 2ull * x.B + 1)
-    refuse(SS_E_CAPACITY, "the plan bills " + std::to_string(ring_slots) + " ring slots, the banks and the guard need " +
-                              std::to_string(2 * x.B + 1) + " (set ring_slots = 2 x dg_max_ids + 1)");
-  for (const SpareClass& sc : p.spares)
-    if (sc.block_bytes == x.host_stride) x.Q = sc.blocks;
-  if (x.Q < 1)
-    refuse(SS_E_CAPACITY, "the plan granted no spare blocks (host_spare_units asked " +
-                              std::to_string(b.host_spare_units) + "): a write-back needs a free block");
-  x.blocks = x.P + x.Q;
-  x.I = o.dg_inclusive_blocks;
-  if (x.I && x.I >= x.Q)
-    refuse(SS_E_CAPACITY, "dg_inclusive_blocks " + std::to_string(x.I) + " must stay below the spare blocks (" +
-                              std::to_string(x.Q) + "): raise host_spare_units by the inclusive share");
-  // scored eviction (reference src/dg_layout.cpp:349-371): the weights, the per-layer bound, the tables' size, and
-  // every rule of the profile's format (the context loads its counts before the first token)
-  if (scored) {
-    x.scored = true;
-    if (o.dg_score_w_trans || o.dg_score_w_freq || o.dg_score_w_recency) {
-      if (o.dg_score_w_trans > 1000 || o.dg_score_w_freq > 1000 || o.dg_score_w_recency > 1000 ||
-          o.dg_score_w_trans + o.dg_score_w_freq + o.dg_score_w_recency != 1000)
-        refuse(SS_E_INVALID, "dg_score_w_trans / _freq / _recency must each be 0..1000 and sum to 1000");
-      x.w_trans = o.dg_score_w_trans;
-      x.w_freq = o.dg_score_w_freq;
-      x.w_rec = o.dg_score_w_recency;
-    }
-    std::vector<uint32_t> units;
-    for (int L : x.gated) units.push_back(uint32_t(d.layers[size_t(L)].n_units));
-    if (score_cells(units) > uint64_t(SIZE_MAX / 8)) refuse(SS_E_INVALID, "the score tables do not fit the address space");
-    if (o.dg_score_profile_len || o.dg_score_profile) {
-      if (!o.dg_score_profile || !o.dg_score_profile_len)
-        refuse(SS_E_INVALID, "dg_score_profile and dg_score_profile_len must be given together");
-      x.score_identity = score_identity(d, x.gated);
-      (void)check_score_profile(o.dg_score_profile, o.dg_score_profile_len, units, x.score_identity);
-    }
-  }
-  x.persistent_slots = x.R + x.D;
-  const uint64_t S = uint64_t(x.persistent_slots) + 2ull * x.B + 1;
-  require(S < 0x7fffffffull, SS_E_INVALID, "device-gated: more than 2^31 - 1 slots");
-  x.slots = uint32_t(S);
-  x.guard_slot = x.slots - 1;
-  // device admission: the arena, the slot table and the control words instead of what the plan billed for the slots
-  uint64_t need = S * x.unit_bytes + uint64_t(keys) * 4 + 4096;
-  const uint64_t billed = p.resident + p.dynamic + p.ring;
-  const uint64_t limit = p.cap > p.margin ? p.cap - p.margin : 0;
-  const uint64_t other = p.peak >= billed ? p.peak - billed : 0;
-  if (other + need > limit)
-    refuse(SS_E_CAPACITY, "the arena needs " + std::to_string(need) + " bytes where the plan billed " +
-                              std::to_string(billed) + "; with the rest of the plan that is above the cap - margin");
-  return x;
-}
+// The open's geometry and refusals: dg_geometry.hpp.
+using Layout = DgGeometry;
 
 // ---- fine-grained control area layout ----
 struct MappedLayout {
@@ -1073,7 +889,7 @@ class Service {
 // ---- the context ------------------------------------------------------------------------------------------------------
 class HipDgCtx final : public DgCtx {
  public:
-  HipDgCtx(const Desc& d, const Plan& p, const ss_options& o) : d_(d), o_(o), x_(make_layout(d, p, o)) {
+  HipDgCtx(const Desc& d, const Plan& p, const ss_options& o) : d_(d), o_(o), x_(dg_geometry(d, p, o)) {
     try {
       init();
     } catch (...) {

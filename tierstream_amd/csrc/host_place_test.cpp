@@ -115,3 +115,24 @@ ss_status tsa_test_hostplace_exclusive(const char* desc_json, size_t len, const 
 }
 
 }  // extern "C"
+
+// ---- the device-gated geometry alone ----------------------------------------------------------------------------------
+#include "dg_geometry.hpp"
+
+extern "C" ss_status tsa_test_dg_geometry(const char* desc_json, size_t len, const ss_budget* budget,
+                                          const uint8_t* tiers, size_t n_tiers, const ss_options* opt, uint32_t* out,
+                                          uint32_t* residents, uint32_t res_cap) {
+  return tsa::guard([&] {
+    using namespace tsa;
+    require(desc_json && budget && opt && out, SS_E_INVALID, "tsa_test_dg_geometry: null argument");
+    const Desc d = desc_from_json(json_parse(std::string(desc_json, len)));
+    const Plan p = tiers ? plan_from_tiers(d, *budget, std::vector<uint8_t>(tiers, tiers + n_tiers))
+                         : plan_make(d, *budget, {});
+    const DgGeometry x = dg_geometry(d, p, *opt);
+    const uint32_t v[] = {x.keys, uint32_t(x.gated.size()), x.R, x.D, x.B, x.P, x.F, x.Q, x.I, x.S, x.disk_queue,
+                          x.persistent_slots, x.slots, x.guard_slot, x.blocks, uint32_t(x.scored), x.w_trans,
+                          x.w_freq, x.w_rec};
+    std::memcpy(out, v, sizeof v);
+    for (uint32_t i = 0; residents && i < res_cap && i < x.residents.size(); ++i) residents[i] = x.residents[i];
+  });
+}
