@@ -1,16 +1,23 @@
-// Device-gated decode: the cache state machine, free of any device API (a transport does the copies, publications and
-// events). The decisions - homes (Host / Device / Coming / Bank / Evicting), free-slot and bank-slot choice, cover,
-// resurrection, recency, the boundary's admissions, victims from the recency tail to the spare target, deferred
-// write-backs with a per-layer credit, the inclusive share of clean copies - are those of reference src/dg_core.cpp
-// (place :769-858, fetch_impl :1146-1368, serve_demand / serve_use / serve_prediction :1415-1634, end_token
-// :1636-1927, collect / write-back scheduling :961-1097) for its two- and three-tier configurations, with LRU or
-// scored victims (score_history / select_scored / score_candidate :1929-2057, the boundary's one acceptance loop
-// :1775-1840, set_policy :2059-2071; the score and its order: reference docs/design.md:284-354).
+// Device-gated decode: where every unit of every gated layer lives, and what moves when, with no device API in it (a
+// DgTransport does the copies, table writes and events). The MI355X context drives it once per exported layer from
+// its service thread and once per token boundary; the CPU test hook drives it on a transport that completes
+// everything at once.
 //
-// Schedule: this core asks its transport for completion (collect) only through done(), which the MI355X transport
-// answers after waiting for the event, and it never asks whether the device "ran ahead". Every decision is therefore
-// the one the reference makes under its canonical (eager) schedule: placement is a function of the route stream alone,
-// which is what makes slot tables comparable bit for bit with the CPU oracle.
+// Parity: the decisions are the reference core's (src/dg_core.cpp: open placement :769-858, a miss's fetch
+// :1146-1368, a layer's service :1415-1634, the boundary :1636-1927, write-back scheduling :961-1097, scored victims
+// :1929-2071 with the score of docs/design.md:284-354), so slot tables, homes and counters compare bit for bit with the
+// reference's under its eager schedule. The structure is this library's own:
+//   - KeyOrder: one intrusive order over keys (two index arrays), used twice - the device recency order (victims come
+//     from its back) and, with the file tier, the pinned homes' order (the back one gives up its block first);
+//   - one FIFO of write-backs: a sealed prefix (event recorded, complete at the next retire) and a queued tail (parts
+//     still to submit, by a per-layer byte credit or when a slot is needed);
+//   - EventLedger: the transport's events, pooled, and the write-back events still tied to a slot or a block;
+//   - BankSlots: the two per-token banks of dg_max_ids slots that a miss borrows when no persistent slot is free;
+//   - LayerHistory: scored eviction's per-layer transition counts and window of recent unions.
+//
+// Completion: the core only learns that a write-back finished by retiring it (retire_writebacks), which the MI355X
+// transport makes true by waiting for the event; it never asks whether the device ran ahead. Placement is therefore a
+// function of the route stream alone.
 #pragma once
 
 #include <cstddef>
@@ -55,7 +62,7 @@ class DgTransport {
     if (slot_ev) wait(s, slot_ev);
     if (block_ev) wait(s, block_ev);
   }
-  // A deferred write-back (slot -> block, every part) the core has just recorded at the boundary, with write-backs on
+  // A queued write-back (slot -> block, every part) the core has just chosen at the boundary, with write-backs on
   // kD2h. It will submit it later, part by part (d2h_part on kD2h), by its credit or when it needs the slot; meanwhile
   // neither the slot nor the block is written by anything else. A transport may copy it now on kD2h and make the
   // later d2h_part calls of the same (slot, block, part) no-ops (default: nothing).
@@ -79,25 +86,24 @@ struct DgConfig {
   bool wb_defer = true, wb_on_d2h = true;
   uint64_t wb_layer_bytes = 0, wb_max_outstanding = 0;
   uint32_t inclusive = 0;  // device units that may keep their block as a clean copy
-  // Three-tier (SS_DG_DISK_TIER): keys off the device and without a pinned home live in their file (Home::File) and
-  // a miss reads them through one of disk_staging staging buffers (round robin). home_blocks: the blocks that are
-  // pinned homes at open (the plan's pinned units; the rest of `blocks` are spares). Pinned homes keep a recency list
-  // (most recently homed first); a victim that needs a block while none is free takes the least recently homed pinned
-  // unit's (that unit goes to its file, disk_drops), or with no pinned unit left goes to its file itself
-  // (disk_discards). clean_evict: such a victim goes to its file at once, no pinned unit displaced. disk_prefetch:
-  // a prefetch may read a file-homed unit.
+  // Three-tier (SS_DG_DISK_TIER): keys off the device and without a pinned home live in their file and a miss reads
+  // them through one of disk_staging staging buffers (round robin). home_blocks: the blocks that are pinned homes at
+  // open (the plan's pinned units; the rest of `blocks` are spares). A victim that needs a block while none is free
+  // takes the block of the pinned home that was homed longest ago (that unit goes to its file: disk_drops), or with no
+  // pinned home left goes to its file itself (disk_discards). clean_evict: such a victim goes to its file at once.
+  // disk_prefetch: a prefetch may read a file-homed unit.
   bool disk_tier = false, disk_prefetch = false, clean_evict = false;
   uint32_t home_blocks = 0, disk_staging = 0;
   // Scored eviction (SS_POLICY_SCORED / SCORED_AUTO): the boundary takes its victims lowest score first instead of
-  // from the recency tail; every other decision is LRU's. Weights in thousandths (each 0..1000, sum 1000). max_ids:
-  // the ids of one export (a union's upper bound), 1..64. scored_auto: learn every token, but rank only at a boundary
-  // closing more than one verify row (end_token(rows > 1)); otherwise the recency tail.
+  // from the back of the recency order; every other decision stays LRU's. Weights in thousandths (each 0..1000, sum
+  // 1000). max_ids: the ids of one export (a union's upper bound), 1..64. scored_auto: learn every token, but rank
+  // only at a boundary closing more than one verify row; otherwise the recency order.
   bool scored = false, scored_auto = false;
   uint32_t w_trans = 700, w_freq = 200, w_rec = 100;
   uint32_t max_ids = 0;
 };
 
-struct DgCounts {  // the subset of ss_dg_stats this core counts
+struct DgCounts {  // the subset of ss_dg_stats this core counts (the ABI's field names)
   uint64_t tokens = 0, lookups = 0, misses = 0, covered = 0, fetched = 0, prefetched = 0, prefetch_used = 0;
   uint64_t pred_invalid = 0, resurrected = 0, bank_serves = 0, collected_mid = 0, evicted = 0, evict_short = 0;
   uint64_t writebacks_done = 0, stalled = 0, predicted = 0, predicted_true = 0, miss_layers = 0, covered_waits = 0;
@@ -106,9 +112,9 @@ struct DgCounts {  // the subset of ss_dg_stats this core counts
   uint64_t wb_forced_wait_ns = 0, inclusive_kept = 0, inclusive_drops = 0;
   uint64_t disk_reads = 0, disk_read_bytes = 0, disk_stage_waits = 0, disk_drops = 0, disk_discards = 0;
   uint64_t clean_drops = 0, clean_drop_bytes = 0;
-  // scored eviction: boundaries that had to use the recency order (a gated layer not served this token: never expected
-  // under this core's one-export-per-layer service); victims taken in score order; layers and eligible keys the
-  // selection considered; transition increments lost to a saturated cell; selection time.
+  // scored eviction: boundaries that fell back to the recency order (an exported gated layer whose union is not this
+  // token's); victims taken in score order; layers and eligible keys the selection considered; transition increments
+  // lost to a saturated cell; selection time.
   uint64_t score_fallbacks = 0, scored_victims = 0, score_layers = 0, score_candidates = 0, score_saturated = 0;
   uint64_t score_ns = 0;
 };
@@ -116,207 +122,283 @@ struct DgLayerCounts {
   uint64_t lookups = 0, misses = 0, fetched = 0, bank_serves = 0, prefetched = 0, prefetch_used = 0, evicted = 0;
 };
 
+// An order over keys 0..n-1 (each in it at most once) with constant-time insertion at the front and removal anywhere.
+class KeyOrder {
+ public:
+  static constexpr uint32_t kEnd = 0xffffffffu;
+  void reset(uint32_t n);
+  bool has(uint32_t k) const { return member_[k] != 0; }
+  void put_front(uint32_t k);
+  void remove(uint32_t k);
+  uint32_t front() const { return front_; }
+  uint32_t back() const { return back_; }
+  uint32_t toward_back(uint32_t k) const { return link_[2 * size_t(k)]; }
+  uint32_t toward_front(uint32_t k) const { return link_[2 * size_t(k) + 1]; }
+  uint32_t size() const { return n_; }
+
+ private:
+  std::vector<uint32_t> link_;  // per key: [toward the back, toward the front]
+  std::vector<uint8_t> member_;
+  uint32_t front_ = kEnd, back_ = kEnd, n_ = 0;
+};
+
 class DgCore {
  public:
-  enum class Home : uint8_t { Host, Device, Coming, Bank, Evicting, File };
+  // Pinned: its host block is its home. Resident: a persistent slot. Landing: copied into a persistent slot this token
+  // (resident from the boundary on). InBank: copied into a bank slot for this token only. Draining: chosen at a
+  // boundary, its write-back into a block not yet retired (the slot still holds its bytes). File: three-tier only.
+  enum class Where : uint8_t { Pinned, Resident, Landing, InBank, Draining, File };
 
   DgCore(const DgConfig& cfg, DgTransport* t);
   ~DgCore();
   DgCore(const DgCore&) = delete;
   DgCore& operator=(const DgCore&) = delete;
 
-  // Open: the first persistent_slots - spare_target distinct keys of `priority` take slots 0.. (the first one most
+  // Open: the first persistent_slots - spare_target distinct keys of `priority` take slots 0.. (the first one the most
   // recent); every other key takes a block, in key order; free slots are a stack with the lowest on top. Three-tier:
   // `disk` flags the plan's file-tier keys; of the keys off the device, the plan-pinned ones and then the file-tier
-  // ones, each in `priority` order, take pinned homes up to home_blocks (blocks in key order; the recency list in
-  // priority order, the first most recent), every other key lives in its file.
-  void place(const std::vector<uint32_t>& priority, const std::vector<uint8_t>* disk = nullptr);
+  // ones, each in `priority` order, take pinned homes up to home_blocks (blocks in key order; the first by priority
+  // the most recently homed), every other key lives in its file.
+  void seat(const std::vector<uint32_t>& priority, const std::vector<uint8_t>* disk = nullptr);
   uint32_t keys() const { return keys_; }
-  uint32_t gated() const { return uint32_t(base_.size() - 1); }
-  uint32_t units(uint32_t g) const { return base_[g + 1] - base_[g]; }
-  uint32_t key(uint32_t g, uint32_t u) const { return base_[g] + u; }
+  uint32_t gated() const { return uint32_t(first_key_.size() - 1); }
+  uint32_t units(uint32_t g) const { return first_key_[g + 1] - first_key_[g]; }
+  uint32_t key(uint32_t g, uint32_t u) const { return first_key_[g] + u; }
   uint32_t gated_of(uint32_t k) const;
-  const std::vector<uint32_t>& unit_base() const { return base_; }
-  const std::vector<int32_t>& table() const { return table_; }
-  Home home(uint32_t k) const { return e_[k].home; }
-  int32_t slot_of(uint32_t k) const { return e_[k].slot; }
-  int32_t block_of(uint32_t k) const { return e_[k].block; }
-  uint32_t free_slots() const { return uint32_t(free_slots_.size()); }
-  uint32_t free_blocks() const { return uint32_t(free_blocks_.size()); }
-  const std::vector<int32_t>& free_block_ids() const { return free_blocks_; }  // the free stack, top last
-  uint32_t on_device() const { return on_device_; }
-  uint32_t file_units() const { return on_file_; }
-  std::vector<uint32_t> host_order() const;  // three-tier: the pinned homes, most recently homed first
-  uint32_t backed_units() const { return backed_; }
-  uint64_t outstanding_bytes() const { return outstanding_; }
-  uint32_t deferred() const { return uint32_t(deferred_.size()); }
-  const DgCounts& counts() const { return st_; }
-  const std::vector<DgLayerCounts>& layer_counts() const { return lc_; }
-  std::vector<uint32_t> residency() const;  // device keys, most recent first
+  const std::vector<uint32_t>& unit_base() const { return first_key_; }
+  const std::vector<int32_t>& table() const { return mirror_; }
+  Where where(uint32_t k) const { return st_[k].where; }
+  int32_t slot_of(uint32_t k) const { return st_[k].slot; }
+  int32_t block_of(uint32_t k) const { return st_[k].block; }
+  uint32_t free_slots() const { return uint32_t(free_slot_.size()); }
+  uint32_t free_blocks() const { return uint32_t(free_block_.size()); }
+  const std::vector<int32_t>& free_block_ids() const { return free_block_; }  // the free stack, top last
+  uint32_t on_device() const { return n_device_; }
+  uint32_t file_units() const { return n_file_; }
+  std::vector<uint32_t> pinned_order() const;  // three-tier: the pinned homes, most recently homed first
+  uint32_t clean_copies() const { return n_clean_; }
+  uint64_t outstanding_bytes() const { return in_flight_bytes_; }
+  uint32_t queued_writebacks() const { return uint32_t(wb_.size() - sealed_); }
+  const DgCounts& counts() const { return n_; }
+  const std::vector<DgLayerCounts>& layer_counts() const { return per_layer_; }
+  std::vector<uint32_t> device_order() const;  // device keys, most recent first
 
   // run: the gated layers this token exports (null: all); a layer left out keeps its score history unchanged
-  void begin_token(uint32_t seq, const std::vector<uint8_t>* run = nullptr);
-  // mask: the ids whose entry the canonical schedule sees absent (the host mirror before this layer's service), which
-  // every count and fetch follows; dev_mask (default: mask): the ids the export kernel saw absent in the device table,
-  // whose readers wait for the layer's ready word. A device-only bit is an entry still in flight (a prefetch that had
-  // not landed when the layer exported): its readers wait for that copy, and nothing is counted for it.
-  void serve_demand(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask, uint64_t dev_mask);
-  void serve_demand(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask) { serve_demand(g, ids, n, mask, mask); }
-  // The canonical mask of layer g's export: the ids in range whose mirror entry is absent.
-  uint64_t canonical_mask(uint32_t g, const uint32_t* ids, uint32_t n) const;
-  void serve_use(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask);
-  void serve_prediction(uint32_t g_next, const uint32_t* pred, uint32_t n);
-  void issue_writebacks(uint32_t g);  // the deferred write-back slice after layer g's service
+  void open_token(uint32_t seq, const std::vector<uint8_t>* run = nullptr);
+  // The ids of layer g's export whose mirror entry is absent (in range only): the misses the eager schedule sees.
+  uint64_t absent_mask(uint32_t g, const uint32_t* ids, uint32_t n) const;
+  // Layer g exported `ids`. mask: the misses every count and fetch follows (absent_mask before this call). dev_mask
+  // (default: mask): the ids the export kernel saw absent in the device table, whose readers wait for the layer's
+  // ready word. A device-only bit is an entry still in flight (a prefetch that had not landed when the layer
+  // exported): its readers wait for that copy, and nothing is counted for it.
+  void serve_misses(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask, uint64_t dev_mask);
+  void serve_misses(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask) { serve_misses(g, ids, n, mask, mask); }
+  // Layer g computed with `ids` (after serve_misses): lookups, misses, recency, the prediction's hits, the history.
+  void note_uses(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask);
+  // A prediction of gated layer g_next's ids, made while an earlier layer computes: prefetched in list order within
+  // the per-layer and per-token budgets.
+  void prefetch_next(uint32_t g_next, const uint32_t* pred, uint32_t n);
+  void spend_wb_credit(uint32_t g);  // the queued write-backs' slice after layer g's service
   // rows: the verify rows the token closed (scored_auto ranks only above one); keep: keys this boundary must not
-  // evict (every gated layer's ss_dg_keep set), out-of-range keys ignored
-  void end_token(uint32_t rows = 1, const std::vector<uint32_t>& keep = {});
-  // Between tokens: deferral of write-backs on or off; turning it off first submits every deferred write-back. The
+  // choose (every gated layer's ss_dg_keep set), out-of-range keys ignored
+  void close_token(uint32_t rows = 1, const std::vector<uint32_t>& keep = {});
+  // Between tokens: queueing of write-backs on or off; turning it off first submits every queued write-back. The
   // per-token credit and carry restart as after open. Placement and submission only: the same bytes.
-  void set_wb_defer(bool on);
+  void defer_writebacks(bool on);
   bool wb_defer() const { return c_.wb_defer; }
-  void drain();  // between tokens: every deferred write-back submitted, every stream synchronized
+  void quiesce();  // between tokens: every queued write-back submitted, every stream synchronized
   void set_spare_target(uint32_t n);
   void set_prefetch_budget(uint32_t per_layer, uint32_t per_token);
   uint32_t spare_target() const { return c_.spare_target; }
-  void check() const;  // ownership invariants (tests); throws SS_E_BACKEND naming the first broken rule
+  void audit() const;  // ownership invariants (tests); throws SS_E_BACKEND naming the first broken rule
 
   // ---- scored eviction ----
-  static constexpr uint32_t kScoreWindow = 16;       // unions in each layer's frequency ring
-  static constexpr uint32_t kScoreMaxUnits = 65536;  // units per gated layer (the integer bounds rest on it)
-  // Starting transition counts, at open (after place, before the first token): per gated layer units^2 uint32
-  // little-endian cells row-major [previous unit][unit], layers concatenated. They are also the state set_policy
-  // restores.
-  void load_counts(const unsigned char* cells);
-  // Between tokens: drains every write-back, switches LRU (0) / SCORED (1) / SCORED_AUTO (2), resets the learned
-  // state to the open counts (or zero) and every demand epoch, and renumbers the recency stamps in list order.
-  // Switching to scoring needs the tables, so an open under LRU refuses it.
+  static constexpr uint32_t kWindow = 16;             // unions in each layer's frequency window
+  static constexpr uint32_t kMaxScoredUnits = 65536;  // units per gated layer (the integer bounds rest on it)
+  // Starting transition counts, at open (after seat, before the first token): per gated layer units^2 uint32
+  // little-endian cells row-major [previous unit][unit], layers concatenated. A policy switch restores them.
+  void seed_transitions(const unsigned char* cells);
+  // Between tokens: quiesces, switches LRU (0) / SCORED (1) / SCORED_AUTO (2), restores the learned state to the open
+  // counts (or zero) and every demand token, and renumbers the recency stamps in the order's sequence. Switching to
+  // scoring needs the tables, so an open under LRU refuses it.
   void set_policy(uint32_t policy);
   uint32_t policy() const { return c_.scored ? (c_.scored_auto ? 2u : 1u) : 0u; }
-  uint64_t epoch() const { return epoch_; }
-  uint64_t stamp_counter() const { return stamp_; }
-  void set_stamp_counter(uint64_t v) { stamp_ = v; }  // tests: start near the limit
   // Past this the next token fails before it changes anything, so the stamp counter never wraps.
   static constexpr uint64_t kStampLimit = UINT64_MAX - (uint64_t(1) << 40);
 
  private:
-  static constexpr uint32_t kNone = 0xffffffffu;
-  struct Entry {
-    Home home = Home::Host;
+  static constexpr uint32_t kNoKey = 0xffffffffu;
+
+  struct KeyState {
+    Where where = Where::Pinned;
     int32_t slot = -1, block = -1;
-    uint32_t prev = kNone, next = kNone;
-    bool in_list = false, wb_pending = false, via_prefetch = false, used = false, backed = false;
-    void* pf_done = nullptr;
-    uint32_t hprev = kNone, hnext = kNone;  // three-tier: the pinned homes' recency list
-    bool in_hlist = false;
-    uint64_t demand_epoch = 0;  // scored: the token of its last demand use (0: none since open or a policy switch)
-    uint64_t stamp = 0;         // scored: its last push to the recency list (unique; larger = more recent)
-  };
-  // Scored eviction, per gated layer: transition counts T[r][e] (saturating uint32, row-major) with exact row sums,
-  // the ring of the last kScoreWindow unions with per-unit counts over it, the previous and this token's union.
-  struct LayerScore {
-    std::vector<uint32_t> T, open_T;
-    std::vector<uint64_t> rowsum;
-    std::vector<uint16_t> cnt;
-    std::vector<uint32_t> ring;  // kScoreWindow rows of max_ids
-    std::vector<uint8_t> ring_len;
-    uint32_t ring_head = 0, ring_n = 0;
-    std::vector<uint32_t> prev, cur;
-    uint64_t served = 0;  // the token whose union cur holds
-  };
-  struct Cand {
-    uint64_t s, epoch, stamp;
-    uint32_t key;
-  };
-  static bool cand_less(const Cand& a, const Cand& b) {
-    if (a.s != b.s) return a.s < b.s;
-    if (a.epoch != b.epoch) return a.epoch < b.epoch;
-    return a.stamp < b.stamp;
-  }
-  struct Writeback {
-    uint32_t key;
-    int32_t slot, block;
-    void* done;
-    bool discard;
-    uint64_t bytes;
-  };
-  struct Deferred {
-    uint32_t key;
-    int32_t slot, block;
-    uint32_t parts_done;
-    uint64_t bytes;
+    bool wb_open = false;    // a write-back record of this key is not retired yet
+    bool ahead = false;      // copied in by a prefetch this token
+    bool ahead_hit = false;  // ... and since used
+    bool clean = false;      // resident with its block kept as a clean copy
+    void* ahead_ev = nullptr;  // the prefetch's copy
+    uint64_t demand_token = 0;  // scored: the token of its last demand use (0: none since open or a policy switch)
   };
 
-  void unlink(uint32_t k);
-  void push_front(uint32_t k);
-  void* event();
-  uint32_t collect();
-  void submit_part(Deferred& d);
-  void* record_deferred_front(bool discard);
-  void* finish_deferred_front();
-  void force_free_slot();
-  int32_t take_bank_slot(uint32_t g);
-  void write_entry(DgTransport::Stream s, uint32_t k, int32_t v, bool landing = false);
-  bool fetch(uint32_t g, uint32_t unit, bool prefetch);
-  void cover(uint32_t g, uint32_t unit);
-  void use(uint32_t g, uint32_t unit, bool was_miss);
-  // Leaves the device (or a bank) without a write-back: its block is its home again (the recency head), else
-  // (three-tier, no block) its file.
-  void to_lower(uint32_t k);
-  void hpush(uint32_t k);    // a pinned home now (three-tier: at the recency head)
-  void hunlink(uint32_t k);  // no longer a pinned home
-  bool drop_host_lru();      // three-tier: the least recently homed pinned unit to its file, its block free
-  int32_t take_stage();      // three-tier: the next staging buffer, its last copy out of it landed
-  bool clean_now() const { return c_.clean_evict && c_.disk_tier && free_blocks_.empty(); }
-  void attach(std::vector<void*>& where, int32_t i, void* ev);
-  void detach(std::vector<void*>& where, int32_t i);
-  void sweep_events();
-  void score_history(uint32_t g);  // serve_use: layer g's union into the counts, the ring and the previous union
-  // The `need` smallest eligible candidates of every gated layer, ascending, into heap_.
-  void select_scored(size_t need);
-  Cand score_of(uint32_t g, uint32_t u, uint64_t denom, const Cand* cutoff) const;
-  void reset_score();
-  bool eligible(uint32_t k) const {
-    return e_[k].home == Home::Device && !e_[k].wb_pending && (keep_.empty() || !keep_[k]);
+  // A victim's copy into its block. Sealed: its event recorded after its last submitted part; it completes in the
+  // bookkeeping at the next retire (dropped: the key came back before it finished, so only the block returns).
+  struct WriteBack {
+    uint32_t key;
+    int32_t slot, block;
+    uint32_t parts_sent;
+    uint64_t bytes_sent;
+    void* ev;
+    bool dropped;
+  };
+
+  // The transport's events: a pool, and the write-back events still tied to a slot or a block (a copy into that slot,
+  // or out of that block, waits for them first; a tie ends when the event has completed or is replaced).
+  class EventLedger {
+   public:
+    void init(DgTransport* t, uint32_t slots, uint32_t blocks);
+    void destroy_all();
+    void* take();
+    void give(void* ev) { pool_.push_back(ev); }
+    void* on_slot(int32_t s) const { return slot_[size_t(s)]; }
+    void* on_block(int32_t b) const { return block_[size_t(b)]; }
+    void tie_slot(int32_t s, void* ev) { tie(slot_, s, ev); }
+    void tie_block(int32_t b, void* ev) { tie(block_, b, ev); }
+    void untie_slot(int32_t s) { untie(slot_, s); }
+    void untie_block(int32_t b) { untie(block_, b); }
+    void release_if_loose(void* ev);  // back to the pool unless tied somewhere
+    void sweep();                     // untie every completed event
+
+   private:
+    void tie(std::vector<void*>& at, int32_t i, void* ev);
+    void untie(std::vector<void*>& at, int32_t i);
+    DgTransport* t_ = nullptr;
+    std::vector<void*> pool_, made_, slot_, block_;
+    std::unordered_map<void*, uint32_t> ties_;
+  };
+
+  // Two banks of B slots after the persistent ones; layer g borrows from bank g & 1, which restarts for each new
+  // (token, layer) pair, so a layer's bank slots stay untouched while the next gated layer borrows from the other.
+  class BankSlots {
+   public:
+    void init(uint32_t first_slot, uint32_t per_bank);
+    // The next slot of layer g's bank in token seq (-1: the bank is used up); *held: the key last copied into it.
+    int32_t borrow(uint32_t g, uint32_t seq, uint32_t* held);
+    void hold(int32_t slot, uint32_t k) { holder_[size_t(slot) - first_] = k; }
+    void clear();
+
+   private:
+    uint32_t first_ = 0, per_ = 0;
+    uint32_t seq_[2] = {0, 0}, layer_[2] = {kNoKey, kNoKey}, used_[2] = {0, 0};
+    std::vector<uint32_t> holder_;
+  };
+
+  // Scored eviction, one per gated layer: transition counts T[r][e] (saturating uint32, row-major) with exact row sums,
+  // a window of the last kWindow unions with per-unit occurrence counts over it, and the previous and current union.
+  class LayerHistory {
+   public:
+    void init(uint32_t units, uint32_t max_ids);
+    void set_open(const unsigned char* le_cells);  // the open counts (little-endian uint32)
+    void restore();                                // the open counts, an empty window and no unions
+    // The token's sorted unique union: one saturating increment per cell (previous union x this one); returns the
+    // increments lost to saturation.
+    uint64_t learn(const std::vector<uint32_t>& uni, uint64_t token);
+    uint64_t served() const { return served_; }
+    uint64_t denominator() const;        // sum of the row sums over the current union
+    uint64_t pull(uint32_t u) const;     // sum over the current union r of T[r][u]
+    uint32_t cur_size() const { return uint32_t(cur_.size()); }
+    uint32_t seen(uint32_t u) const { return occ_[u]; }
+    bool consistent() const;
+
+   private:
+    uint32_t n_ = 0, max_ids_ = 0;
+    std::vector<uint32_t> T_, open_T_;
+    std::vector<uint64_t> row_sum_;
+    std::vector<uint16_t> occ_;
+    std::vector<uint32_t> win_;     // kWindow rows of max_ids
+    std::vector<uint8_t> win_len_;
+    uint32_t win_first_ = 0, win_n_ = 0;
+    std::vector<uint32_t> prev_, cur_;
+    uint64_t served_ = 0;  // the token whose union cur_ holds
+  };
+
+  // A victim candidate in score order: (score, demand token, stamp), a total order since stamps are unique.
+  struct Ranked {
+    uint64_t score, demand, stamp;
+    uint32_t key;
+    bool operator<(const Ranked& o) const {
+      if (score != o.score) return score < o.score;
+      if (demand != o.demand) return demand < o.demand;
+      return stamp < o.stamp;
+    }
+  };
+
+  // recency
+  void touch(uint32_t k);   // to the front of the device order (and, scored, a new stamp)
+  void make_pinned(uint32_t k);   // its block is its home now (three-tier: the most recently homed)
+  void leave_pinned(uint32_t k);  // copied in (its block stays its until the boundary)
+  // to its block, else (three-tier, none) its file; no copy
+  void fall_back(uint32_t k);
+  bool give_up_oldest_home();  // three-tier: the longest-homed pinned unit to its file, its block free
+  int32_t next_stage();        // three-tier: the next staging buffer, its last copy out of it landed
+
+  // write-backs
+  void send_part(WriteBack& w);
+  void seal_first_queued(bool dropped);
+  void finish_first_queued();
+  uint32_t retire_writebacks();
+  void free_a_slot();  // a demand miss with no free slot: submit and retire until one is free
+  void apply_wb_mode();  // the write-back stream, layer credit and in-flight cap of the current mode
+
+  // service
+  void publish(DgTransport::Stream s, uint32_t k, int32_t v, bool from_copy = false);
+  bool bring_in(uint32_t g, uint32_t u, bool ahead);
+  bool resurrect(uint32_t k);
+  bool resident_or_landing(uint32_t k) const {
+    const Where w = st_[k].where;
+    return w == Where::Resident || w == Where::Landing || w == Where::InBank;
   }
-  void apply_wb_defer();  // the write-back stream, layer credit and outstanding cap of c_.wb_defer
-  bool accept_victim(uint32_t k);  // the boundary's acceptance of one victim; false: no block for it (evict_short)
-  bool on_device_or_coming(uint32_t g, uint32_t unit) const {
-    const Home h = e_[key(g, unit)].home;
-    return h == Home::Device || h == Home::Coming || h == Home::Bank;
+
+  // boundary
+  bool choose(uint32_t k);  // one victim; false: no block to write it into (evict_short)
+  bool choosable(uint32_t k) const {
+    return st_[k].where == Where::Resident && !st_[k].wb_open && (kept_.empty() || !kept_[k]);
   }
+  void rank_by_score(size_t want);  // the `want` lowest-ranked choosable keys, ascending, into ranked_
+  Ranked rank_of(uint32_t g, uint32_t u, uint64_t denom, const Ranked* bar) const;
+  bool clean_evict_now() const { return c_.clean_evict && c_.disk_tier && free_block_.empty(); }
 
   DgConfig c_;
   DgTransport* t_;
-  std::vector<uint32_t> base_;
-  uint32_t keys_ = 0, slots_ = 0, bank_first_ = 0;
-  std::vector<Entry> e_;
-  std::vector<int32_t> table_;
-  std::vector<int32_t> free_slots_, free_blocks_;
-  uint32_t head_ = kNone, tail_ = kNone, on_device_ = 0, on_host_ = 0, backed_ = 0;
-  uint32_t hhead_ = kNone, htail_ = kNone, on_file_ = 0, stage_next_ = 0;
+  std::vector<uint32_t> first_key_;  // per gated layer, and the total last
+  uint32_t keys_ = 0, slots_ = 0;
+  std::vector<KeyState> st_;
+  std::vector<uint64_t> stamp_of_;  // scored: each key's last move to the front (unique; larger = more recent)
+  std::vector<int32_t> mirror_;     // the host copy of the device table
+  std::vector<int32_t> free_slot_, free_block_;
+  KeyOrder recent_, homed_;
+  uint32_t n_device_ = 0, n_pinned_ = 0, n_clean_ = 0, n_file_ = 0;
+  uint32_t stage_cursor_ = 0;
   std::vector<void*> stage_ev_;  // [disk_staging]: the last copy out of each staging buffer
-  std::vector<uint32_t> coming_, banked_, bank_key_;
-  uint32_t bank_seq_[2] = {0, 0}, bank_layer_[2] = {kNone, kNone}, bank_next_[2] = {0, 0};
-  std::deque<Writeback> wbs_;
-  std::deque<Deferred> deferred_;
-  uint64_t unit_bytes_ = 0, outstanding_ = 0, layer_bytes_ = 0, max_outstanding_ = 0;
+  std::vector<uint32_t> landing_, in_bank_;
+  BankSlots banks_;
+  std::deque<WriteBack> wb_;  // sealed prefix, then the queued tail
+  size_t sealed_ = 0;
+  uint64_t unit_bytes_ = 0, in_flight_bytes_ = 0, layer_grant_ = 0, in_flight_cap_ = 0;
   int64_t credit_ = 0;
-  size_t prev_evict_ = 0;
+  size_t last_chosen_ = 0;  // write-back victims of the previous boundary
   DgTransport::Stream wb_stream_ = DgTransport::kDem;
-  void* post_ready_ev_ = nullptr;
-  std::vector<uint32_t> pf_layer_;
-  uint32_t pf_token_ = 0, seq_ = 0, pred_layer_ = kNone;
-  std::vector<uint8_t> layer_missed_, run_;
-  std::vector<uint32_t> pred_, uniq_, victims_;
-  std::vector<void*> event_pool_, all_events_;
-  std::vector<void*> slot_ev_, block_ev_;        // a write-back still copying out of the slot / into the block
-  std::unordered_map<void*, int> ev_refs_;      // attachments of each such event
-  DgCounts st_;
-  std::vector<DgLayerCounts> lc_;
-  std::vector<LayerScore> sc_;  // scored: one per gated layer (empty under an LRU open)
-  std::vector<Cand> heap_;
-  std::vector<uint8_t> keep_;  // during end_token: the keys its keep list protects (empty: none)
-  uint64_t epoch_ = 0, stamp_ = 0, open_stamp_ = 0;
+  void* after_ready_ev_ = nullptr;
+  EventLedger ev_;
+  std::vector<uint32_t> ahead_in_layer_;
+  uint32_t ahead_in_token_ = 0, seq_ = 0, predicted_layer_ = kNoKey;
+  std::vector<uint8_t> layer_missed_, exported_;
+  std::vector<uint32_t> predicted_, scratch_ids_, chosen_;
+  DgCounts n_;
+  std::vector<DgLayerCounts> per_layer_;
+  std::vector<LayerHistory> hist_;  // scored: one per gated layer (empty under an LRU open)
+  std::vector<Ranked> ranked_;
+  std::vector<uint8_t> kept_;  // during close_token: the keys its keep list protects (empty: none)
+  uint64_t token_ = 0, stamp_ = 0;
 };
 
 }  // namespace tsa

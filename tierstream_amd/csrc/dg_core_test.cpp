@@ -102,7 +102,7 @@ ss_status tsa_test_dgcore_open(const tsa_test_dgcore_config* cfg, const uint32_t
       require(cfg->disk != nullptr, SS_E_INVALID, "tsa_test_dgcore_open: the disk tier needs its flags");
       disk.assign(cfg->disk, cfg->disk + r->core->keys());
     }
-    r->core->place(std::vector<uint32_t>(order, order + n_order), c.disk_tier ? &disk : nullptr);
+    r->core->seat(std::vector<uint32_t>(order, order + n_order), c.disk_tier ? &disk : nullptr);
     if (cfg->score_cells) {
       std::vector<unsigned char> le;
       uint64_t cells = 0;
@@ -110,9 +110,9 @@ ss_status tsa_test_dgcore_open(const tsa_test_dgcore_config* cfg, const uint32_t
       le.resize(4 * cells);
       for (uint64_t i = 0; i < cells; ++i)
         for (int b = 0; b < 4; ++b) le[4 * i + b] = (unsigned char)(cfg->score_cells[i] >> (8 * b));
-      r->core->load_counts(le.data());
+      r->core->seed_transitions(le.data());
     }
-    r->core->check();
+    r->core->audit();
     *out = r.release();
   });
 }
@@ -137,23 +137,23 @@ ss_status tsa_test_dgcore_token_pred(void* h, const uint32_t* ids, uint32_t n, c
     const uint32_t G = c.gated();
     std::vector<uint8_t> rv(G, 1);
     if (run) rv.assign(run, run + G);
-    c.begin_token(++r->seq, &rv);
+    c.open_token(++r->seq, &rv);
     for (uint32_t g = 0; g < G; ++g) {
       if (!rv[g]) continue;
       const uint32_t* x = ids + size_t(g) * n;
       uint64_t mask = 0;
       for (uint32_t i = 0; i < n; ++i)  // the export kernel: slot_of[unit_base[g] + id] < 0 at export time
         if (x[i] < c.units(g) && c.table()[c.key(g, x[i])] < 0) mask |= uint64_t(1) << i;
-      c.serve_demand(g, x, n, mask);
-      c.serve_use(g, x, n, mask);
+      c.serve_misses(g, x, n, mask);
+      c.note_uses(g, x, n, mask);
       // the prediction for the next layer made at this one (the service serves it when that layer exports)
-      if (pred && n_pred && g + 1 < G && rv[g + 1]) c.serve_prediction(g + 1, pred + size_t(g) * n_pred, n_pred);
+      if (pred && n_pred && g + 1 < G && rv[g + 1]) c.prefetch_next(g + 1, pred + size_t(g) * n_pred, n_pred);
       uint32_t nx = g + 1;  // the next exported layer: no slice after the token's last one
       while (nx < G && !rv[nx]) ++nx;
-      if (c.deferred() && nx < G) c.issue_writebacks(g);
+      if (c.queued_writebacks() && nx < G) c.spend_wb_credit(g);
     }
-    c.end_token(r->rows, r->keep);
-    c.check();
+    c.close_token(r->rows, r->keep);
+    c.audit();
     if (table_out) std::memcpy(table_out, c.table().data(), 4ull * c.keys());
     if (counts) {
       const DgCounts& s = c.counts();
@@ -162,7 +162,7 @@ ss_status tsa_test_dgcore_token_pred(void* h, const uint32_t* ids, uint32_t n, c
                             s.covered_waits, s.wb_deferred, s.wb_cancelled, s.wb_forced, s.wb_boundary_flushed,
                             s.wb_issued_bytes, s.wb_cancelled_bytes, s.inclusive_kept, s.inclusive_drops,
                             uint64_t(c.free_slots()), uint64_t(c.free_blocks()), uint64_t(c.on_device()),
-                            uint64_t(c.backed_units()), s.disk_reads, s.disk_drops, s.disk_discards, s.clean_drops,
+                            uint64_t(c.clean_copies()), s.disk_reads, s.disk_drops, s.disk_discards, s.clean_drops,
                             uint64_t(c.file_units()), s.score_fallbacks, s.scored_victims, s.score_layers,
                             s.score_candidates, s.score_saturated, s.pred_invalid, s.predicted, s.predicted_true};
       const uint32_t m = uint32_t(sizeof v / sizeof v[0]);
@@ -178,7 +178,7 @@ ss_status tsa_test_dgcore_set_policy(void* h, uint32_t policy) {
     tsa::require(h != nullptr, SS_E_INVALID, "tsa_test_dgcore_set_policy: null handle");
     auto* r = static_cast<tsa::TestCore*>(h);
     r->core->set_policy(policy);
-    r->core->check();
+    r->core->audit();
   });
 }
 
@@ -193,8 +193,8 @@ ss_status tsa_test_dgcore_set_wb_defer(void* h, uint32_t on) {
   return tsa::guard([&] {
     tsa::require(h != nullptr, SS_E_INVALID, "tsa_test_dgcore_set_wb_defer: null handle");
     auto* r = static_cast<tsa::TestCore*>(h);
-    r->core->set_wb_defer(on != 0);
-    r->core->check();
+    r->core->defer_writebacks(on != 0);
+    r->core->audit();
   });
 }
 
@@ -223,7 +223,7 @@ ss_status tsa_test_score_profile_check(const void* data, uint64_t len, const uin
 
 uint32_t tsa_test_dgcore_host_order(void* h, uint32_t* out, uint32_t cap) {
   if (!h) return 0;
-  const std::vector<uint32_t> v = static_cast<tsa::TestCore*>(h)->core->host_order();
+  const std::vector<uint32_t> v = static_cast<tsa::TestCore*>(h)->core->pinned_order();
   for (uint32_t i = 0; out && i < cap && i < v.size(); ++i) out[i] = v[i];
   return uint32_t(v.size());
 }

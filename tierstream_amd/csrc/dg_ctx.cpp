@@ -826,7 +826,7 @@ class Service {
   void serve_token(uint32_t seq) {
     const uint32_t G = core_->gated();
     std::copy(run_next_.begin(), run_next_.end(), run_.begin());
-    core_->begin_token(seq, &run_);
+    core_->open_token(seq, &run_);
     wait_began(seq);
     auto next_run = [&](uint32_t g) {
       uint32_t h = g + 1;
@@ -852,11 +852,11 @@ class Service {
       ids_.assign(r.ids, r.ids + n);
       // the canonical schedule's mask (the mirror now, after the previous layer's prediction was served): a prefetch
       // that had not landed when the layer exported is a hit there, as in the reference's eager schedule
-      const uint64_t mask = core_->canonical_mask(g, ids_.data(), n);
+      const uint64_t mask = core_->absent_mask(g, ids_.data(), n);
       require((mask & ~dev_mask) == 0, SS_E_BACKEND,
               "device-gated: gated layer " + std::to_string(g) + " exported a hit for a unit absent from the table");
-      core_->serve_demand(g, ids_.data(), n, mask, dev_mask);
-      core_->serve_use(g, ids_.data(), n, mask);
+      core_->serve_misses(g, ids_.data(), n, mask, dev_mask);
+      core_->note_uses(g, ids_.data(), n, mask);
       if (n_pred > 0 && run_[g + 1]) {
         wait_word(&m_.pflag[g], seq, "prediction flag", g, false, 0);
         const DgPredRecord& pr = m_.prec[g];
@@ -864,9 +864,9 @@ class Service {
                 "device-gated: gated layer " + std::to_string(g) + " predicted " + std::to_string(pr.n_pred) +
                     " ids, its export promised " + std::to_string(n_pred));
         pred_.assign(pr.pred, pr.pred + n_pred);
-        core_->serve_prediction(g + 1, pred_.data(), n_pred);
+        core_->prefetch_next(g + 1, pred_.data(), n_pred);
       }
-      if (core_->deferred() && nx < G) core_->issue_writebacks(g);
+      if (core_->queued_writebacks() && nx < G) core_->spend_wb_credit(g);
     }
   }
 
@@ -980,7 +980,7 @@ class HipDgCtx final : public DgCtx {
       poisoned_ = true;
       throw;
     }
-    core_->end_token(rows, all_kept());
+    core_->close_token(rows, all_kept());
     const std::vector<uint32_t> bad = tr_->collect_verify();
     tr_->profile_collect();
     if (!bad.empty()) {
@@ -1040,7 +1040,7 @@ class HipDgCtx final : public DgCtx {
 
   uint32_t residency(ss_dg_unit* out, uint32_t cap) override {
     require(!in_token_, SS_E_INVALID, "ss_dg_residency: between tokens only");
-    const std::vector<uint32_t> r = core_->residency();
+    const std::vector<uint32_t> r = core_->device_order();
     for (uint32_t i = 0; i < cap && i < r.size(); ++i) {
       const uint32_t g = core_->gated_of(r[i]);
       out[i] = {int32_t(g), int32_t(r[i] - core_->unit_base()[g])};
@@ -1072,7 +1072,7 @@ class HipDgCtx final : public DgCtx {
   void set_sched(uint32_t wb_defer, uint32_t flush_ready) override {
     require(!in_token_, SS_E_INVALID, "ss_dg_set_sched: between tokens only");
     require(wb_defer <= 1 && flush_ready <= 1, SS_E_INVALID, "ss_dg_set_sched: flags are 0 or 1");
-    core_->set_wb_defer(wb_defer != 0);
+    core_->defer_writebacks(wb_defer != 0);
     o_.dg_wb_defer = wb_defer;
     o_.dg_flush_ready = flush_ready;
   }
@@ -1252,7 +1252,7 @@ class HipDgCtx final : public DgCtx {
     fold_free_slots_ = core_->free_slots();
     fold_free_blocks_ = core_->free_blocks();
     fold_outstanding_ = core_->outstanding_bytes();
-    fold_backed_ = core_->backed_units();
+    fold_backed_ = core_->clean_copies();
     fold_file_units_ = core_->file_units();
     fold_read_ns_ = tr_->read_ns();
     fold_wait_ns_ = tr_->read_wait_ns();
@@ -1298,7 +1298,7 @@ class HipDgCtx final : public DgCtx {
     require(unit >= 0 && uint32_t(unit) < core_->units(uint32_t(g)), SS_E_INVALID,
             "tsa_test_dg_corrupt_block: unit out of range");
     const uint32_t k = core_->key(uint32_t(g), uint32_t(unit));
-    require(core_->home(k) == DgCore::Home::Host && core_->block_of(k) >= 0, SS_E_INVALID,
+    require(core_->where(k) == DgCore::Where::Pinned && core_->block_of(k) >= 0, SS_E_INVALID,
             "tsa_test_dg_corrupt_block: the unit is not in its pinned block");
     require(offset < x_.unit_bytes, SS_E_INVALID, "tsa_test_dg_corrupt_block: offset past the unit");
     tr_->block_ptr(core_->block_of(k))[offset] ^= char(0xff);
@@ -1550,19 +1550,19 @@ void HipDgCtx::init() {
   o_.dg_seed_n = 0;
   order.insert(order.end(), x_.residents.begin(), x_.residents.end());
   for (uint32_t k = 0; k < x_.keys; ++k) order.push_back(k);
-  core_->place(order, x_.disk_tier ? &x_.disk : nullptr);
+  core_->seat(order, x_.disk_tier ? &x_.disk : nullptr);
   if (o_.dg_score_profile_len) {  // checked by the layout; its counts are read here only, before the first token
     std::vector<uint32_t> units;
     for (uint32_t g = 0; g < G; ++g) units.push_back(core_->units(g));
     const ScoreProfile v = check_score_profile(o_.dg_score_profile, o_.dg_score_profile_len, units, x_.score_identity);
-    core_->load_counts(v.cells);
+    core_->seed_transitions(v.cells);
     score_prov_ = v.provenance;
   }
   o_.dg_score_profile = nullptr;
   o_.dg_score_profile_len = 0;
   fill();
   tr_->upload_table(core_->table().data(), x_.keys);
-  core_->check();
+  core_->audit();
   run_.assign(G, 1);
   kept_.assign(G, {});
   base_l_.assign(G, DgLayerCounts{});
@@ -1755,8 +1755,8 @@ void HipDgCtx::fill() {
   const unsigned max_threads = std::min<unsigned>(16, hw);
   std::vector<uint32_t> dev_keys, host_keys, file_keys;
   for (uint32_t k = 0; k < x_.keys; ++k) {
-    const DgCore::Home h = core_->home(k);
-    (h == DgCore::Home::Device ? dev_keys : h == DgCore::Home::File ? file_keys : host_keys).push_back(k);
+    const DgCore::Where h = core_->where(k);
+    (h == DgCore::Where::Resident ? dev_keys : h == DgCore::Where::File ? file_keys : host_keys).push_back(k);
   }
   // three-tier: the file homes stay in their files; with a hash check each is read once here, through a staging
   // buffer per worker, for its hash (and its checkpoints), never kept
@@ -1785,9 +1785,9 @@ void HipDgCtx::fill() {
         const int L = x_.gated[g];
         const int u = int(k - x_.unit_base[g]);
         const Layer& l = d_.layers[size_t(L)];
-        const DgCore::Home home = core_->home(k);
-        const bool on_dev = home == DgCore::Home::Device;
-        char* dst = home == DgCore::Home::Host ? tr_->block_ptr(core_->block_of(k)) : stage;
+        const DgCore::Where home = core_->where(k);
+        const bool on_dev = home == DgCore::Where::Resident;
+        char* dst = home == DgCore::Where::Pinned ? tr_->block_ptr(core_->block_of(k)) : stage;
         read_key(k, dst);
         if (o_.verify_hash && !l.hash.empty()) {
           tsa_unit hu{};
