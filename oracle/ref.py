@@ -42,6 +42,7 @@ def lib() -> C.CDLL:
             "ss_plan_free": (None, [vp]),
             "ss_plan_unit_tier": (C.c_int, [vp, C.c_int, C.c_int]),
             "ss_plan_to_json": (st, [vp, C.POINTER(C.c_char_p), C.POINTER(C.c_size_t)]),
+            "ss_plan_from_json": (st, [vp, C.POINTER(SsBudget), C.c_char_p, C.c_size_t, C.POINTER(vp)]),
             "ss_free": (None, [vp]),
             "ss_open": (st, [vp, C.POINTER(SsBudget), vp, C.POINTER(SsOptions), C.POINTER(vp)]),
             "ss_close": (None, [vp]),

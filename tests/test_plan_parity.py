@@ -77,3 +77,64 @@ def test_plan_matches_reference(d, kw, benefit):
         return
     got = ss.Plan(desc_, ss.budget(**kw), benefit)
     assert got.json() == ref.plan_json(d, ss.budget(**kw), benefit)
+
+
+def _from_json(L, desc_text: str, budget, plan_text: bytes):
+    """Status and canonical plan JSON of ss_plan_from_json over `plan_text` (None when refused)."""
+    import ctypes as C
+    vp = C.c_void_p
+    L.ss_plan_from_json.restype = C.c_int
+    L.ss_plan_from_json.argtypes = [vp, C.POINTER(ss.SsBudget), C.c_char_p, C.c_size_t, C.POINTER(vp)]
+    d, p = vp(), vp()
+    b = desc_text.encode()
+    assert L.ss_desc_from_json(b, len(b), C.byref(d)) == 0
+    try:
+        st = L.ss_plan_from_json(d, C.byref(budget), plan_text, len(plan_text), C.byref(p))
+        if st != 0:
+            return st, None
+        s, n = C.c_char_p(), C.c_size_t()
+        assert L.ss_plan_to_json(p, C.byref(s), C.byref(n)) == 0
+        out = C.string_at(s, n.value)
+        L.ss_free(s)
+        L.ss_plan_free(p)
+        return 0, out
+    finally:
+        L.ss_desc_free(d)
+
+
+def _tier_edits(tiers, rng):
+    """The reference's plan tiers, and broken or re-lettered copies of them."""
+    yield "same", tiers
+    L = int(rng.integers(len(tiers)))
+    yield "missing", None
+    yield "short-list", tiers[:-1]
+    if tiers[L]:
+        yield "short-layer", tiers[:L] + [tiers[L][:-1]] + tiers[L + 1:]
+        for letter in "RPDXBZr\x00":
+            yield f"letter-{letter!r}", tiers[:L] + [letter + tiers[L][1:]] + tiers[L + 1:]
+        yield "all-pinned", [("P" * len(t)) for t in tiers]
+        yield "all-resident", [("R" * len(t)) for t in tiers]
+        yield "all-backed", [("B" * len(t)) for t in tiers]
+        yield "all-disk", [("D" * len(t)) for t in tiers]
+    yield "number", tiers[:L] + [7] + tiers[L + 1:]
+
+
+@pytest.mark.parametrize("d,kw,benefit", list(cases(40)))
+def test_plan_from_json_matches_reference(d, kw, benefit):
+    """ss_plan_from_json on the reference's own plan document and on edited copies of its tier letters (other tiers,
+    a letter outside R P D X B, a NUL, wrong lengths, a missing or mistyped list): the same status and, when accepted,
+    the same canonical plan (reference src/plan.cpp:460-477, src/capi.cpp:384-391)."""
+    if ref.plan_status(d, ss.budget(**kw), benefit) != 0:
+        pytest.skip("the reference makes no plan for this budget")
+    want = ref.plan_json(d, ss.budget(**kw), benefit)
+    rng = np.random.default_rng(len(d))
+    for name, tiers in _tier_edits(want["tiers"], rng):
+        doc = dict(want)
+        if tiers is None:
+            doc.pop("tiers")
+        else:
+            doc["tiers"] = tiers
+        text = json.dumps(doc).encode()
+        got_o = _from_json(ss._declare(), d, ss.budget(**kw), text)
+        got_t = _from_json(ref.lib(), d, ss.budget(**kw), text)
+        assert got_o == got_t, (name, got_o[0], got_t[0])

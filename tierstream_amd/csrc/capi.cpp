@@ -230,8 +230,9 @@ ss_status ss_plan_from_tiers(const ss_desc* d, const ss_budget* b, const uint8_t
 ss_status ss_plan_from_json(const ss_desc* d, const ss_budget* b, const char* text, size_t len, ss_plan** out) {
   return guard([&] {
     need(d && b && text && out, "ss_plan_from_json: null argument");
+    const std::vector<uint8_t> tiers = tiers_from_json(d->d, json_parse(std::string(text, len)));  // before the budget
     const ss_budget bb = versioned(b, budget_defaults, "ss_plan_from_json budget");
-    *out = new ss_plan{plan_from_tiers(d->d, bb, tiers_from_json(d->d, json_parse(std::string(text, len)))), d};
+    *out = new ss_plan{plan_from_tiers(d->d, bb, tiers), d};
   });
 }
 void ss_plan_free(ss_plan* p) { delete p; }

@@ -1,6 +1,5 @@
 #include "json.hpp"
 
-#include <cerrno>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -10,287 +9,327 @@
 namespace tsa {
 namespace {
 
-constexpr int kMaxDepth = 64;
+constexpr size_t kNestLimit = 64;                  // containers below the top value
+constexpr size_t kTextLimit = size_t(256) << 20;   // bytes of text
 
-struct Parser {
-  const std::string& s;
-  size_t i = 0;
+bool digit(char c) { return c >= '0' && c <= '9'; }
 
-  [[noreturn]] void bad(const std::string& what) const {
-    fail(SS_E_DESC, "json: " + what + " at offset " + std::to_string(i));
+int hex_value(char c) {
+  if (digit(c)) return c - '0';
+  if (c >= 'a' && c <= 'f') return c - 'a' + 10;
+  if (c >= 'A' && c <= 'F') return c - 'A' + 10;
+  return -1;
+}
+
+// Appends code point cp (at most 0x10FFFF) as UTF-8: the lead byte carries the length, continuation bytes 6 bits each.
+void append_utf8(std::string& out, uint32_t cp) {
+  if (cp < 0x80) {
+    out.push_back(char(cp));
+    return;
   }
-  void ws() {
-    while (i < s.size() && (s[i] == ' ' || s[i] == '\t' || s[i] == '\n' || s[i] == '\r')) ++i;
+  const int n = cp < 0x800 ? 2 : cp < 0x10000 ? 3 : 4;
+  static const unsigned char lead[5] = {0, 0, 0xC0, 0xE0, 0xF0};
+  char buf[4];
+  for (int k = n - 1; k > 0; --k, cp >>= 6) buf[k] = char(0x80 | (cp & 0x3F));
+  buf[0] = char(lead[n] | cp);
+  out.append(buf, size_t(n));
+}
+
+// The text and a read position, and the pieces of the grammar that do not nest.
+class Reader {
+ public:
+  explicit Reader(const std::string& t) : t_(t) {}
+
+  [[noreturn]] void reject(const std::string& why) const {
+    fail(SS_E_DESC, "json: " + why + " (byte " + std::to_string(pos_) + ")");
   }
-  bool eat(char c) {
-    ws();
-    if (i < s.size() && s[i] == c) {
-      ++i;
-      return true;
+  void space() {
+    while (pos_ < t_.size()) {
+      const char c = t_[pos_];
+      if (c != ' ' && c != '\t' && c != '\n' && c != '\r') return;
+      ++pos_;
     }
-    return false;
   }
-  void expect(char c) {
-    if (!eat(c)) bad(std::string("expected '") + c + "'");
+  bool done() const { return pos_ >= t_.size(); }
+  char peek() const { return t_[pos_]; }
+  bool skip(char c) {  // after whitespace
+    space();
+    if (done() || peek() != c) return false;
+    ++pos_;
+    return true;
   }
-  static void put_utf8(std::string& out, uint32_t cp) {
-    if (cp < 0x80) {
-      out += char(cp);
-    } else if (cp < 0x800) {
-      out += char(0xC0 | (cp >> 6));
-      out += char(0x80 | (cp & 0x3F));
-    } else if (cp < 0x10000) {
-      out += char(0xE0 | (cp >> 12));
-      out += char(0x80 | ((cp >> 6) & 0x3F));
-      out += char(0x80 | (cp & 0x3F));
-    } else {
-      out += char(0xF0 | (cp >> 18));
-      out += char(0x80 | ((cp >> 12) & 0x3F));
-      out += char(0x80 | ((cp >> 6) & 0x3F));
-      out += char(0x80 | (cp & 0x3F));
+  size_t pos() const { return pos_; }
+
+  std::string string_body() {  // at the opening quote
+    if (done() || peek() != '"') reject("a string must start here");
+    ++pos_;
+    std::string out;
+    for (;;) {
+      if (done()) reject("the string never ends");
+      const char c = t_[pos_++];
+      if (c == '"') return out;
+      if (static_cast<unsigned char>(c) < 0x20) reject("a raw control byte inside a string");
+      if (c != '\\') {
+        out.push_back(c);
+        continue;
+      }
+      if (done()) reject("the string ends inside an escape");
+      const char e = t_[pos_++];
+      switch (e) {
+        case '"': case '\\': case '/': out.push_back(e); break;
+        case 'b': out.push_back('\b'); break;
+        case 'f': out.push_back('\f'); break;
+        case 'n': out.push_back('\n'); break;
+        case 'r': out.push_back('\r'); break;
+        case 't': out.push_back('\t'); break;
+        case 'u': append_utf8(out, code_point()); break;
+        default: reject(std::string("unknown escape \\") + e);
+      }
     }
   }
-  uint32_t hex4() {
-    if (i + 4 > s.size()) bad("short \\u escape");
+
+  Json scalar() {  // at a non-container value
+    const char c = peek();
+    if (c == '"') return Json::string(string_body());
+    if (word("true")) return Json::boolean(true);
+    if (word("false")) return Json::boolean(false);
+    if (word("null")) return Json{};
+    return number();
+  }
+
+ private:
+  uint32_t hex_quad() {
+    if (t_.size() - pos_ < 4) reject("a \\u escape needs four hex digits");
     uint32_t v = 0;
     for (int k = 0; k < 4; ++k) {
-      const char c = s[i++];
-      v <<= 4;
-      if (c >= '0' && c <= '9') v |= uint32_t(c - '0');
-      else if (c >= 'a' && c <= 'f') v |= uint32_t(c - 'a' + 10);
-      else if (c >= 'A' && c <= 'F') v |= uint32_t(c - 'A' + 10);
-      else bad("bad \\u escape");
+      const int h = hex_value(t_[pos_++]);
+      if (h < 0) reject("a \\u escape needs four hex digits");
+      v = v << 4 | uint32_t(h);
     }
     return v;
   }
-  std::string str() {
-    ws();
-    if (i >= s.size() || s[i] != '"') bad("expected a string");
-    ++i;
-    std::string out;
-    while (true) {
-      if (i >= s.size()) bad("unterminated string");
-      const char c = s[i++];
-      if (c == '"') break;
-      if (static_cast<unsigned char>(c) < 0x20) bad("control character in a string");
-      if (c != '\\') {
-        out += c;
-        continue;
-      }
-      if (i >= s.size()) bad("unterminated escape");
-      const char e = s[i++];
-      switch (e) {
-        case '"': out += '"'; break;
-        case '\\': out += '\\'; break;
-        case '/': out += '/'; break;
-        case 'b': out += '\b'; break;
-        case 'f': out += '\f'; break;
-        case 'n': out += '\n'; break;
-        case 'r': out += '\r'; break;
-        case 't': out += '\t'; break;
-        case 'u': {
-          uint32_t cp = hex4();
-          if (cp >= 0xD800 && cp < 0xDC00) {
-            if (i + 2 > s.size() || s[i] != '\\' || s[i + 1] != 'u') bad("lone surrogate");
-            i += 2;
-            const uint32_t lo = hex4();
-            if (lo < 0xDC00 || lo >= 0xE000) bad("bad surrogate pair");
-            cp = 0x10000 + ((cp - 0xD800) << 10) + (lo - 0xDC00);
-          }
-          put_utf8(out, cp);
-          break;
-        }
-        default: bad("bad escape");
-      }
-    }
-    return out;
+  // After "\u": one code point; a high surrogate must be followed at once by an escaped low one.
+  uint32_t code_point() {
+    const uint32_t u = hex_quad();
+    if (u >= 0xDC00 && u <= 0xDFFF) reject("a low surrogate with no high one before it");
+    if (u < 0xD800 || u > 0xDBFF) return u;
+    if (t_.size() - pos_ < 2 || t_[pos_] != '\\' || t_[pos_ + 1] != 'u') reject("a high surrogate with no low one");
+    pos_ += 2;
+    const uint32_t lo = hex_quad();
+    if (lo < 0xDC00 || lo > 0xDFFF) reject("a high surrogate followed by a non-low escape");
+    return 0x10000 + ((u - 0xD800) << 10 | (lo - 0xDC00));
   }
-  Json value(int depth) {
-    if (depth > kMaxDepth) bad("nesting too deep");
-    ws();
-    if (i >= s.size()) bad("unexpected end");
-    const char c = s[i];
-    if (c == '{') {
-      ++i;
-      Json o = Json::object();
-      if (eat('}')) return o;
-      do {
-        std::string k = str();
-        expect(':');
-        if (o.obj.count(k)) bad("duplicate key \"" + k + "\"");
-        o.obj.emplace(std::move(k), value(depth + 1));
-      } while (eat(','));
-      expect('}');
-      return o;
-    }
-    if (c == '[') {
-      ++i;
-      Json a = Json::array();
-      if (eat(']')) return a;
-      do a.arr.push_back(value(depth + 1));
-      while (eat(','));
-      expect(']');
-      return a;
-    }
-    if (c == '"') return Json::string(str());
-    if (s.compare(i, 4, "true") == 0) {
-      i += 4;
-      return Json::boolean(true);
-    }
-    if (s.compare(i, 5, "false") == 0) {
-      i += 5;
-      return Json::boolean(false);
-    }
-    if (s.compare(i, 4, "null") == 0) {
-      i += 4;
-      return Json{};
-    }
-    // number: -?(0|[1-9][0-9]*)(\.[0-9]+)?([eE][+-]?[0-9]+)?
-    const size_t start = i;
-    if (s[i] == '-') ++i;
-    if (i >= s.size() || !isdigit(static_cast<unsigned char>(s[i]))) bad("bad value");
-    if (s[i] == '0') ++i;
-    else
-      while (i < s.size() && isdigit(static_cast<unsigned char>(s[i]))) ++i;
-    if (i < s.size() && s[i] == '.') {
-      ++i;
-      if (i >= s.size() || !isdigit(static_cast<unsigned char>(s[i]))) bad("bad number");
-      while (i < s.size() && isdigit(static_cast<unsigned char>(s[i]))) ++i;
-    }
-    if (i < s.size() && (s[i] == 'e' || s[i] == 'E')) {
-      ++i;
-      if (i < s.size() && (s[i] == '+' || s[i] == '-')) ++i;
-      if (i >= s.size() || !isdigit(static_cast<unsigned char>(s[i]))) bad("bad exponent");
-      while (i < s.size() && isdigit(static_cast<unsigned char>(s[i]))) ++i;
-    }
-    Json n;
-    n.kind = Json::Number;
-    n.text = s.substr(start, i - start);
-    return n;
+  bool word(const char* w) {
+    size_t n = 0;
+    while (w[n]) ++n;
+    if (t_.compare(pos_, n, w) != 0) return false;
+    pos_ += n;
+    return true;
   }
+  void digits() {
+    while (!done() && digit(peek())) ++pos_;
+  }
+  // -?(0|[1-9][0-9]*)(.[0-9]+)?([eE][+-]?[0-9]+)?, kept as text
+  Json number() {
+    const size_t from = pos_;
+    if (peek() == '-') ++pos_;
+    if (done() || !digit(peek())) reject("not a value");
+    if (peek() == '0') ++pos_;
+    else digits();
+    if (!done() && peek() == '.') {
+      ++pos_;
+      if (done() || !digit(peek())) reject("a fraction needs digits");
+      digits();
+    }
+    if (!done() && (peek() == 'e' || peek() == 'E')) {
+      ++pos_;
+      if (!done() && (peek() == '+' || peek() == '-')) ++pos_;
+      if (done() || !digit(peek())) reject("an exponent needs digits");
+      digits();
+    }
+    Json j;
+    j.kind = Json::Number;
+    j.text = t_.substr(from, pos_ - from);
+    return j;
+  }
+
+  const std::string& t_;
+  size_t pos_ = 0;
 };
 
-void dump_string(std::string& out, const std::string& v) {
-  out += '"';
-  for (unsigned char c : v) {
-    switch (c) {
-      case '"': out += "\\\""; break;
-      case '\\': out += "\\\\"; break;
-      case '\n': out += "\\n"; break;
-      case '\r': out += "\\r"; break;
-      case '\t': out += "\\t"; break;
-      case '\b': out += "\\b"; break;
-      case '\f': out += "\\f"; break;
-      default:
-        if (c < 0x20) {
-          char buf[8];
-          std::snprintf(buf, sizeof buf, "\\u%04x", c);
-          out += buf;
-        } else {
-          out += char(c);
-        }
-    }
-  }
-  out += '"';
+// The next object key and its colon; *slot becomes the key's (new) value.
+Json* open_member(Reader& r, Json& o) {
+  r.space();
+  if (r.done()) r.reject("the text ends inside an object");
+  std::string key = r.string_body();
+  if (!r.skip(':')) r.reject("a key needs a ':'");
+  if (o.obj.count(key)) r.reject("key \"" + key + "\" appears twice");
+  return &o.obj[key];
 }
 
-void dump(std::string& out, const Json& j) {
-  switch (j.kind) {
-    case Json::Null: out += "null"; break;
-    case Json::Bool: out += j.b ? "true" : "false"; break;
-    case Json::Number: out += j.text; break;
-    case Json::String: dump_string(out, j.text); break;
-    case Json::Array: {
-      out += '[';
-      for (size_t k = 0; k < j.arr.size(); ++k) {
-        if (k) out += ',';
-        dump(out, j.arr[k]);
+// Iterative: `open` holds the containers being filled (never more than kNestLimit + 1), so deep text cannot exhaust
+// the native stack. A pointer to an open container stays valid: its parent is not touched while it is open.
+Json parse_text(Reader& r) {
+  Json root;
+  std::vector<Json*> open;
+  Json* slot = &root;  // where the next value goes
+  for (;;) {
+    if (open.size() > kNestLimit) r.reject("containers nested more than 64 deep");
+    r.space();
+    if (r.done()) r.reject("the text ends where a value should start");
+    const char c = r.peek();
+    bool filled = true;
+    if (c == '{' || c == '[') {
+      r.skip(c);
+      *slot = c == '{' ? Json::object() : Json::array();
+      open.push_back(slot);
+      if (r.skip(c == '{' ? '}' : ']')) {
+        open.pop_back();
+      } else {
+        slot = c == '{' ? open_member(r, *slot) : (slot->arr.emplace_back(), &slot->arr.back());
+        filled = false;
       }
-      out += ']';
-      break;
+    } else {
+      *slot = r.scalar();
+    }
+    // after a complete value: a separator opens the next one, a bracket closes the innermost container
+    while (filled && !open.empty()) {
+      Json& top = *open.back();
+      if (r.skip(',')) {
+        slot = top.is_object() ? open_member(r, top) : (top.arr.emplace_back(), &top.arr.back());
+        filled = false;
+      } else if (r.skip(top.is_object() ? '}' : ']')) {
+        open.pop_back();
+      } else {
+        r.reject(top.is_object() ? "expected ',' or '}'" : "expected ',' or ']'");
+      }
+    }
+    if (filled) return root;
+  }
+}
+
+void write_string(std::string& out, const std::string& v) {
+  static const char hex[] = "0123456789abcdef";
+  out.push_back('"');
+  for (const char ch : v) {
+    const unsigned char c = static_cast<unsigned char>(ch);
+    const char* named = c == '"' ? "\\\"" : c == '\\' ? "\\\\" : c == '\n' ? "\\n" : c == '\r' ? "\\r" : c == '\t' ? "\\t" : nullptr;
+    if (named) {
+      out += named;
+    } else if (c < 0x20) {
+      out += "\\u00";
+      out.push_back(hex[c >> 4]);
+      out.push_back(hex[c & 15]);
+    } else {
+      out.push_back(ch);
+    }
+  }
+  out.push_back('"');
+}
+
+void write_value(std::string& out, const Json& j) {
+  switch (j.kind) {
+    case Json::Null: out += "null"; return;
+    case Json::Bool: out += j.b ? "true" : "false"; return;
+    case Json::Number: out += j.text; return;
+    case Json::String: write_string(out, j.text); return;
+    case Json::Array: {
+      out.push_back('[');
+      const char* sep = "";
+      for (const Json& e : j.arr) {
+        out += sep;
+        write_value(out, e);
+        sep = ",";
+      }
+      out.push_back(']');
+      return;
     }
     case Json::Object: {
-      out += '{';
-      bool first = true;
+      out.push_back('{');
+      const char* sep = "";
       for (const auto& kv : j.obj) {
-        if (!first) out += ',';
-        first = false;
-        dump_string(out, kv.first);
-        out += ':';
-        dump(out, kv.second);
+        out += sep;
+        write_string(out, kv.first);
+        out.push_back(':');
+        write_value(out, kv.second);
+        sep = ",";
       }
-      out += '}';
-      break;
+      out.push_back('}');
+      return;
     }
   }
 }
 
-bool is_integer_literal(const std::string& t) {
-  size_t i = t[0] == '-' ? 1 : 0;
-  if (i >= t.size()) return false;
-  for (; i < t.size(); ++i)
-    if (!isdigit(static_cast<unsigned char>(t[i]))) return false;
+// The magnitude of an all-digit literal of at most 20 digits; false when it is not one or does not fit 64 bits.
+bool magnitude(const std::string& t, size_t from, uint64_t* out) {
+  if (from >= t.size() || t.size() - from > 20) return false;
+  uint64_t v = 0;
+  for (size_t i = from; i < t.size(); ++i) {
+    if (!digit(t[i])) return false;
+    const uint64_t d = uint64_t(t[i] - '0');
+    if (v > (UINT64_MAX - d) / 10) return false;
+    v = v * 10 + d;
+  }
+  *out = v;
   return true;
 }
 
 }  // namespace
 
 Json Json::number_f(double v) {
-  Json j;
-  j.kind = Number;
   char buf[40];
   std::snprintf(buf, sizeof buf, "%.17g", v);
+  Json j = of(Number);
   j.text = buf;
   return j;
 }
 
 Json json_parse(const std::string& text) {
-  Parser p{text};
-  Json v = p.value(0);
-  p.ws();
-  if (p.i != text.size()) p.bad("trailing characters");
+  require(text.size() <= kTextLimit, SS_E_DESC, "json: more than 256 MiB of text");
+  Reader r(text);
+  Json v = parse_text(r);
+  r.space();
+  if (!r.done()) r.reject("text after the value");
   return v;
 }
 
 std::string json_dump(const Json& j) {
   std::string out;
-  dump(out, j);
+  write_value(out, j);
   return out;
 }
 
 uint64_t json_u64(const Json& j, const std::string& where) {
-  require(j.kind == Json::Number && is_integer_literal(j.text) && j.text[0] != '-', SS_E_DESC,
-          where + ": expected a non-negative integer");
-  errno = 0;
-  char* end = nullptr;
-  const unsigned long long v = std::strtoull(j.text.c_str(), &end, 10);
-  require(errno == 0 && end && *end == '\0', SS_E_DESC, where + ": integer out of range");
-  return uint64_t(v);
+  uint64_t v = 0;
+  require(j.kind == Json::Number, SS_E_DESC, where + ": not a number");
+  require(magnitude(j.text, 0, &v), SS_E_DESC, where + ": " + j.text + " is not an integer in 0..2^64-1");
+  return v;
 }
 
 int64_t json_i64(const Json& j, const std::string& where) {
-  require(j.kind == Json::Number && is_integer_literal(j.text), SS_E_DESC, where + ": expected an integer");
-  errno = 0;
-  char* end = nullptr;
-  const long long v = std::strtoll(j.text.c_str(), &end, 10);
-  require(errno == 0 && end && *end == '\0', SS_E_DESC, where + ": integer out of range");
-  return int64_t(v);
+  require(j.kind == Json::Number, SS_E_DESC, where + ": not a number");
+  const bool minus = !j.text.empty() && j.text[0] == '-';
+  uint64_t v = 0;
+  require(magnitude(j.text, minus ? 1 : 0, &v) && v <= uint64_t(INT64_MAX), SS_E_DESC,
+          where + ": " + j.text + " is not an integer of magnitude below 2^63");
+  return minus ? -int64_t(v) : int64_t(v);
 }
 
 double json_f64(const Json& j, const std::string& where) {
-  require(j.kind == Json::Number, SS_E_DESC, where + ": expected a number");
-  const double v = std::strtod(j.text.c_str(), nullptr);
-  require(std::isfinite(v), SS_E_DESC, where + ": number out of range");
+  require(j.kind == Json::Number, SS_E_DESC, where + ": not a number");
+  char* end = nullptr;
+  const double v = std::strtod(j.text.c_str(), &end);
+  require(end && *end == '\0' && std::isfinite(v), SS_E_DESC, where + ": " + j.text + " is not a finite double");
   return v;
 }
 
 const std::string& json_str(const Json& j, const std::string& where) {
-  require(j.kind == Json::String, SS_E_DESC, where + ": expected a string");
+  require(j.kind == Json::String, SS_E_DESC, where + ": not a string");
   return j.text;
 }
 
 bool json_bool(const Json& j, const std::string& where) {
-  require(j.kind == Json::Bool, SS_E_DESC, where + ": expected true or false");
+  require(j.kind == Json::Bool, SS_E_DESC, where + ": not true or false");
   return j.b;
 }
 

@@ -1,5 +1,7 @@
-// desc-v1 and plan-v1: parsing, validation, the planner. The rules (and so every tier decision) are those of reference
-// src/desc.cpp:128-413 and src/plan.cpp:317-477; the code is this library's own.
+// desc-v1 and plan-v1. The document formats, the refusal rules and the planner's decisions are the reference's
+// (src/desc.cpp:128-413, src/plan.cpp:36-477), checked document by document against it; the structure is this
+// library's: a key-tracking object reader for the descriptor, overflow-checked arithmetic through the compiler's
+// builtins, and a planner whose prefix search prices every split in one backward pass.
 #include "model.hpp"
 
 #include <algorithm>
@@ -15,109 +17,223 @@ namespace tsa {
 namespace {
 
 constexpr const char* kDescSchema = "strix-stream/desc-v1";
-constexpr int kMaxLayers = 4096;
-constexpr int kMaxUnits = 1 << 16;
+constexpr size_t kLayerLimit = 4096;
+constexpr uint64_t kUnitLimit = 65536;
+constexpr uint64_t kDescByteLimit = uint64_t(1) << 56;
 
-// "strix-stream/<x>" also accepts the renamed "tierstream/<x>".
-bool schema_ok(const std::string& got, const std::string& emitted) {
-  if (got == emitted) return true;
-  const std::string old = "strix-stream/";
-  return emitted.rfind(old, 0) == 0 && got == "tierstream/" + emitted.substr(old.size());
+std::string num(uint64_t v) { return std::to_string(v); }
+
+// ---- checked sizes ----------------------------------------------------------------------------------------------------
+uint64_t plus(uint64_t a, uint64_t b, const std::string& where, ss_status st = SS_E_DESC) {
+  uint64_t r = 0;
+  require(!__builtin_add_overflow(a, b, &r), st, where + ": a byte count overflows 64 bits");
+  return r;
+}
+uint64_t times(uint64_t a, uint64_t b, const std::string& where, ss_status st = SS_E_DESC) {
+  uint64_t r = 0;
+  require(!__builtin_mul_overflow(a, b, &r), st, where + ": a byte count overflows 64 bits");
+  return r;
+}
+bool pow2(uint64_t v) { return v != 0 && (v & (v - 1)) == 0; }
+
+// ---- reading -----------------------------------------------------------------------------------------------------------
+// One JSON object being read into the descriptor. Each key the reader asks for is noted; finish() refuses every other
+// key, except the "x-" notes an adapter may leave.
+class Fields {
+ public:
+  Fields(const Json& j, std::string path) : j_(j), path_(std::move(path)) {
+    require(j.is_object(), SS_E_DESC, path_ + ": not an object");
+  }
+  std::string where(const char* k) const { return path_ + "." + k; }
+  const Json* get(const char* k) {
+    asked_.insert(k);
+    return j_.find(k);
+  }
+  const Json& need(const char* k) {
+    const Json* v = get(k);
+    require(v != nullptr, SS_E_DESC, path_ + ": \"" + k + "\" is required");
+    return *v;
+  }
+  uint64_t count(const char* k, uint64_t absent, uint64_t limit = UINT64_MAX) {
+    const Json* v = get(k);
+    const uint64_t x = v ? json_u64(*v, where(k)) : absent;
+    require(x <= limit, SS_E_DESC, where(k) + ": " + num(x) + " exceeds " + num(limit));
+    return x;
+  }
+  uint64_t count_needed(const char* k) { return json_u64(need(k), where(k)); }
+  std::string text(const char* k, const std::string& absent = "") {
+    const Json* v = get(k);
+    return v ? json_str(*v, where(k)) : absent;
+  }
+  std::string text_needed(const char* k) { return json_str(need(k), where(k)); }
+  const std::vector<Json>* list(const char* k) {
+    const Json* v = get(k);
+    if (!v) return nullptr;
+    require(v->is_array(), SS_E_DESC, where(k) + ": not an array");
+    return &v->arr;
+  }
+  void finish() const {
+    for (const auto& kv : j_.obj)
+      require(asked_.count(kv.first) || kv.first.compare(0, 2, "x-") == 0, SS_E_DESC,
+              path_ + ": unknown key \"" + kv.first + "\"");
+  }
+
+ private:
+  const Json& j_;
+  std::string path_;
+  std::set<std::string> asked_;
+};
+
+std::string item(const std::string& path, size_t i) { return path + "[" + num(i) + "]"; }
+
+// The element formats a part may declare (the reference's list), or any "x-" private format.
+bool format_known(const std::string& f) {
+  static const std::set<std::string> kFormats = {
+      "F32",   "F16",    "BF16",   "FP8_E4M3", "FP8_E5M2", "EXL3",   "MXFP4",  "NVFP4", "Q2_K",    "Q3_K",  "Q4_K",
+      "Q5_K",  "Q6_K",   "Q8_0",   "Q4_0",     "Q4_1",     "Q5_0",   "Q5_1",   "IQ1_S", "IQ1_M",   "IQ2_XXS", "IQ2_XS",
+      "IQ2_S", "IQ3_XXS", "IQ3_S", "IQ4_NL",   "IQ4_XS",   "TQ1_0",  "TQ2_0",  "I8",    "U8",      "mixed"};
+  return kFormats.count(f) || f.compare(0, 2, "x-") == 0;
 }
 
-std::string idx(const std::string& base, size_t i) { return base + "[" + std::to_string(i) + "]"; }
-
-uint64_t add_ck(uint64_t a, uint64_t b, const std::string& w) {
-  require(a <= UINT64_MAX - b, SS_E_DESC, w + ": byte arithmetic overflows 64 bits");
-  return a + b;
-}
-uint64_t mul_ck(uint64_t a, uint64_t b, const std::string& w) {
-  require(a == 0 || b <= UINT64_MAX / a, SS_E_DESC, w + ": byte arithmetic overflows 64 bits");
-  return a * b;
-}
-uint64_t capped(uint64_t v, uint64_t max, const std::string& w) {
-  require(v <= max, SS_E_DESC, w + ": " + std::to_string(v) + " is above the limit " + std::to_string(max));
+// A 16-digit lowercase hex xxh64.
+uint64_t hash_of(const std::string& s, const std::string& where) {
+  require(s.size() == 16, SS_E_DESC, where + ": an xxh64 is 16 lowercase hex digits");
+  uint64_t v = 0;
+  for (const char c : s) {
+    const bool dec = c >= '0' && c <= '9', hex = c >= 'a' && c <= 'f';
+    require(dec || hex, SS_E_DESC, where + ": an xxh64 is 16 lowercase hex digits");
+    v = v << 4 | uint64_t(dec ? c - '0' : c - 'a' + 10);
+  }
   return v;
 }
-
-const Json& need(const Json& o, const char* k, const std::string& w) {
-  const Json* v = o.find(k);
-  require(v != nullptr, SS_E_DESC, w + ": missing \"" + k + "\"");
-  return *v;
-}
-uint64_t u64_or(const Json& o, const char* k, const std::string& w, uint64_t d) {
-  const Json* v = o.find(k);
-  return v ? json_u64(*v, w + "." + k) : d;
-}
-std::string str_or(const Json& o, const char* k, const std::string& w, const std::string& d = "") {
-  const Json* v = o.find(k);
-  return v ? json_str(*v, w + "." + k) : d;
-}
-
-void only_keys(const Json& o, const std::string& w, std::initializer_list<const char*> keys) {
-  require(o.is_object(), SS_E_DESC, w + ": expected an object");
-  for (const auto& kv : o.obj) {
-    if (kv.first.rfind("x-", 0) == 0) continue;  // adapter notes
-    bool ok = false;
-    for (const char* k : keys) ok = ok || kv.first == k;
-    require(ok, SS_E_DESC, w + ": unknown key \"" + kv.first + "\"");
-  }
-}
-
-std::vector<NamedBytes> named(const Json* v, const std::string& w) {
-  std::vector<NamedBytes> out;
-  if (!v) return out;
-  require(v->is_array(), SS_E_DESC, w + ": expected an array");
-  for (size_t i = 0; i < v->arr.size(); ++i) {
-    const Json& e = v->arr[i];
-    const std::string ew = idx(w, i);
-    only_keys(e, ew, {"name", "bytes"});
-    out.push_back({json_str(need(e, "name", ew), ew + ".name"), json_u64(need(e, "bytes", ew), ew + ".bytes")});
-  }
-  return out;
-}
-
-bool known_format(const std::string& f) {
-  static const char* known[] = {"F32",   "F16",    "BF16",    "FP8_E4M3", "FP8_E5M2", "EXL3",   "MXFP4",  "NVFP4",
-                                "Q2_K",  "Q3_K",   "Q4_K",    "Q5_K",     "Q6_K",     "Q8_0",   "Q4_0",   "Q4_1",
-                                "Q5_0",  "Q5_1",   "IQ1_S",   "IQ1_M",    "IQ2_XXS",  "IQ2_XS", "IQ2_S",  "IQ3_XXS",
-                                "IQ3_S", "IQ4_NL", "IQ4_XS",  "TQ1_0",    "TQ2_0",    "I8",     "U8",     "mixed"};
-  for (const char* k : known)
-    if (f == k) return true;
-  return f.rfind("x-", 0) == 0;
-}
-
-std::string hex16(uint64_t v) {
+std::string hash_text(uint64_t v) {
   char b[17];
   std::snprintf(b, sizeof b, "%016llx", static_cast<unsigned long long>(v));
   return b;
 }
-uint64_t parse_hex16(const std::string& s, const std::string& w) {
-  require(s.size() == 16, SS_E_DESC, w + ": expected 16 hex digits");
-  uint64_t v = 0;
-  for (char c : s) {
-    v <<= 4;
-    if (c >= '0' && c <= '9') v |= uint64_t(c - '0');
-    else if (c >= 'a' && c <= 'f') v |= uint64_t(c - 'a' + 10);
-    else fail(SS_E_DESC, w + ": expected lowercase hex digits");
+
+template <class E>
+E pick(const std::string& got, const std::initializer_list<std::pair<const char*, E>>& names, const std::string& where) {
+  std::string all;
+  for (const auto& n : names) {
+    if (got == n.first) return n.second;
+    all += (all.empty() ? "" : " | ") + std::string(n.first);
   }
-  return v;
+  fail(SS_E_DESC, where + ": \"" + got + "\" is not one of " + all);
 }
 
-const char* tiers_text(Tiers t) {
-  switch (t) {
-    case Tiers::Pinned: return "pinned";
-    case Tiers::Disk: return "disk";
-    case Tiers::PinnedDisk: return "pinned|disk";
-    case Tiers::Pair: return "pair";
-  }
+const std::initializer_list<std::pair<const char*, Order>> kOrders = {{"prefix", Order::Prefix}, {"ranked", Order::Ranked}};
+const std::initializer_list<std::pair<const char*, Tiers>> kTierSets = {
+    {"pinned", Tiers::Pinned}, {"disk", Tiers::Disk}, {"pinned|disk", Tiers::PinnedDisk}, {"pair", Tiers::Pair}};
+const std::initializer_list<std::pair<const char*, LayerKind>> kKinds = {
+    {"dense", LayerKind::Dense}, {"moe", LayerKind::Moe}, {"blob", LayerKind::Blob}};
+
+template <class E>
+const char* name_of(E v, const std::initializer_list<std::pair<const char*, E>>& names) {
+  for (const auto& n : names)
+    if (n.second == v) return n.first;
   return "?";
 }
 
-std::string gib(uint64_t n) {
-  char b[32];
-  std::snprintf(b, sizeof b, "%.3f", double(n) / double(kGiB));
-  return b;
+std::vector<NamedBytes> read_named(Fields& f, const char* k) {
+  std::vector<NamedBytes> out;
+  const std::vector<Json>* v = f.list(k);
+  for (size_t i = 0; v && i < v->size(); ++i) {
+    Fields e((*v)[i], item(f.where(k), i));
+    out.push_back({e.text_needed("name"), e.count_needed("bytes")});
+    e.finish();
+  }
+  return out;
+}
+
+Part read_part(const Json& j, const std::string& path) {
+  Fields f(j, path);
+  Part p;
+  p.name = f.text("name");
+  p.format = f.text_needed("format");
+  p.source = int(f.count("source", 0, 1024));
+  p.offset = f.count_needed("offset");
+  p.bytes = f.count_needed("bytes");
+  p.stride = f.count("stride", p.bytes);
+  f.finish();
+  return p;
+}
+
+Layer read_layer(const Json& j, const std::string& path) {
+  Fields f(j, path);
+  Layer l;
+  const int64_t index = json_i64(f.need("index"), f.where("index"));
+  require(index >= 0 && index < int64_t(kLayerLimit), SS_E_DESC, f.where("index") + ": outside 0..4095");
+  l.index = int(index);
+  l.kind = pick(f.text_needed("kind"), kKinds, f.where("kind"));
+  l.fixed_bytes = f.count("fixed_bytes", 0);
+  l.n_units = int(f.count("n_units", l.kind == LayerKind::Blob ? 1 : 0, kUnitLimit));
+  l.top_k = int(f.count("top_k", 0, kUnitLimit));
+  l.n_shared = int(f.count("n_shared", 0, kUnitLimit));
+  l.unit_bytes = f.count("unit_bytes", 0);
+  if (const Json* s = f.get("streamable")) l.streamable = json_bool(*s, f.where("streamable"));
+  if (const std::vector<Json>* parts = f.list("parts"))
+    for (size_t p = 0; p < parts->size(); ++p) l.parts.push_back(read_part((*parts)[p], item(f.where("parts"), p)));
+  if (const Json* r = f.get("router")) {
+    Fields rf(*r, f.where("router"));
+    l.has_router = true;
+    l.router.tensor = rf.text_needed("tensor");
+    l.router.bias = rf.text("bias");
+    l.router.format = rf.text("format", "F32");
+    l.router.score = rf.text("score", "softmax");
+    l.router.rows = uint32_t(rf.count("rows", 0, kUnitLimit));
+    l.router.cols = uint32_t(rf.count("cols", 0, uint64_t(1) << 24));
+    rf.finish();
+  }
+  if (const Json* h = f.get("hash")) {
+    require(h->is_array(), SS_E_DESC, f.where("hash") + ": not an array of xxh64 strings");
+    for (size_t k = 0; k < h->arr.size(); ++k)
+      l.hash.push_back(hash_of(json_str(h->arr[k], item(f.where("hash"), k)), item(f.where("hash"), k)));
+  }
+  if (const std::vector<Json>* b = f.list("benefit"))
+    for (size_t k = 0; k < b->size(); ++k) l.benefit.push_back(json_f64((*b)[k], item(f.where("benefit"), k)));
+  f.finish();
+  return l;
+}
+
+// ---- rules across fields ------------------------------------------------------------------------------------------------
+void check_units(const Desc& d, Layer& l, const std::string& lw) {
+  require(!l.parts.empty(), SS_E_DESC, lw + ": units need at least one part");
+  uint64_t sum = 0;
+  for (size_t p = 0; p < l.parts.size(); ++p) {
+    const Part& part = l.parts[p];
+    const std::string pw = item(lw + ".parts", p);
+    require(part.bytes > 0, SS_E_DESC, pw + ".bytes: zero");
+    require(format_known(part.format), SS_E_DESC, pw + ".format: \"" + part.format + "\" is not a known format");
+    require(part.source >= 0 && size_t(part.source) < d.sources.size(), SS_E_DESC,
+            pw + ".source: " + num(uint64_t(part.source)) + " names no source");
+    require(l.n_units == 1 || part.stride >= part.bytes, SS_E_DESC, pw + ".stride: below bytes, so units overlap");
+    sum = plus(sum, part.bytes, pw);
+    plus(plus(part.offset, times(uint64_t(l.n_units - 1), part.stride, pw), pw), part.bytes, pw);  // the last byte
+  }
+  if (l.unit_bytes == 0) l.unit_bytes = sum;
+  require(l.unit_bytes == sum, SS_E_DESC,
+          lw + ".unit_bytes: " + num(l.unit_bytes) + " but the parts add up to " + num(sum));
+  times(plus(l.unit_bytes, d.unit_align, lw), uint64_t(l.n_units), lw);
+  require(l.hash.empty() || l.hash.size() == size_t(l.n_units), SS_E_DESC, lw + ".hash: not one per unit");
+  require(l.benefit.empty() || l.benefit.size() == size_t(l.n_units), SS_E_DESC, lw + ".benefit: not one per unit");
+  require(!l.has_router || l.router.rows == 0 || l.router.rows == uint32_t(l.n_units), SS_E_DESC,
+          lw + ".router.rows: not n_units");
+}
+
+void check_kind(const Layer& l, const std::string& lw) {
+  switch (l.kind) {
+    case LayerKind::Dense:
+      require(l.n_units == 0 && l.parts.empty(), SS_E_DESC, lw + ": a dense layer has fixed bytes only, no units");
+      break;
+    case LayerKind::Blob:
+      require(l.n_units == 1, SS_E_DESC, lw + ": a blob layer is one unit");
+      break;
+    case LayerKind::Moe:
+      require(l.n_units >= 1, SS_E_DESC, lw + ": a moe layer needs units");
+      require(l.top_k >= 1 && l.top_k <= l.n_units, SS_E_DESC, lw + ".top_k: outside 1..n_units");
+      break;
+  }
 }
 
 }  // namespace
@@ -129,182 +245,79 @@ uint64_t Desc::unit_stride(int layer) const {
 
 uint64_t Desc::fixed_total() const {
   uint64_t t = 0;
-  for (const auto& n : fixed_device) t += n.bytes;
-  for (size_t L = 0; L < layers.size(); ++L) {
-    t += layers[L].fixed_bytes;
-    if (!layers[L].streamable) t += uint64_t(layers[L].n_units) * unit_stride(int(L));
-  }
+  for (const NamedBytes& n : fixed_device) t += n.bytes;
+  for (size_t L = 0; L < layers.size(); ++L)
+    t += layers[L].fixed_bytes + (layers[L].streamable ? 0 : uint64_t(layers[L].n_units) * unit_stride(int(L)));
   return t;
 }
 
 Desc desc_from_json(const Json& j) {
-  const std::string w = "desc";
-  only_keys(j, w,
-            {"schema", "model", "engine", "fixed_device", "host_fixed", "state_bytes_per_position",
-             "workspace_bytes_per_row", "unit_align", "sources", "order", "tiers", "ring_slots", "routes", "layers",
-             "lookup_tables"});
-  require(schema_ok(json_str(need(j, "schema", w), "desc.schema"), kDescSchema), SS_E_DESC,
-          std::string("desc.schema: expected \"") + kDescSchema + "\"");
+  Fields f(j, "desc");
+  const std::string schema = f.text_needed("schema");
+  // the renamed project's "tierstream/" prefix reads as the same format
+  require(schema == kDescSchema || schema == "tierstream/desc-v1", SS_E_DESC,
+          "desc.schema: \"" + schema + "\" is not " + kDescSchema);
   Desc d;
-  d.model = str_or(j, "model", w);
-  d.engine = str_or(j, "engine", w);
-  d.fixed_device = named(j.find("fixed_device"), "desc.fixed_device");
-  d.host_fixed = named(j.find("host_fixed"), "desc.host_fixed");
-  d.state_bytes_per_position = u64_or(j, "state_bytes_per_position", w, 0);
-  d.workspace_bytes_per_row = u64_or(j, "workspace_bytes_per_row", w, 0);
-  d.unit_align = u64_or(j, "unit_align", w, 256);
-  d.ring_slots = uint32_t(capped(u64_or(j, "ring_slots", w, 0), 1u << 20, "desc.ring_slots"));
-  d.routes = str_or(j, "routes", w);
-  const std::string order = str_or(j, "order", w, "ranked");
-  if (order == "prefix") d.order = Order::Prefix;
-  else if (order == "ranked") d.order = Order::Ranked;
-  else fail(SS_E_DESC, "desc.order: expected prefix | ranked");
-  const std::string tiers = str_or(j, "tiers", w, "pinned|disk");
-  if (tiers == "pinned") d.tiers = Tiers::Pinned;
-  else if (tiers == "disk") d.tiers = Tiers::Disk;
-  else if (tiers == "pinned|disk") d.tiers = Tiers::PinnedDisk;
-  else if (tiers == "pair") d.tiers = Tiers::Pair;
-  else fail(SS_E_DESC, "desc.tiers: expected pinned | disk | pinned|disk | pair");
-
-  if (const Json* s = j.find("sources")) {
-    require(s->is_array(), SS_E_DESC, "desc.sources: expected an array");
-    for (size_t i = 0; i < s->arr.size(); ++i) {
-      const std::string sw = idx("desc.sources", i);
-      only_keys(s->arr[i], sw, {"name", "path", "align"});
+  d.model = f.text("model");
+  d.engine = f.text("engine");
+  d.fixed_device = read_named(f, "fixed_device");
+  d.host_fixed = read_named(f, "host_fixed");
+  d.state_bytes_per_position = f.count("state_bytes_per_position", 0);
+  d.workspace_bytes_per_row = f.count("workspace_bytes_per_row", 0);
+  d.unit_align = f.count("unit_align", 256);
+  d.ring_slots = uint32_t(f.count("ring_slots", 0, uint64_t(1) << 20));
+  d.routes = f.text("routes");
+  d.order = pick(f.text("order", "ranked"), kOrders, "desc.order");
+  d.tiers = pick(f.text("tiers", "pinned|disk"), kTierSets, "desc.tiers");
+  if (const std::vector<Json>* s = f.list("sources"))
+    for (size_t i = 0; i < s->size(); ++i) {
+      Fields sf((*s)[i], item("desc.sources", i));
       Source src;
-      src.name = str_or(s->arr[i], "name", sw);
-      src.path = json_str(need(s->arr[i], "path", sw), sw + ".path");
-      src.align = u64_or(s->arr[i], "align", sw, 4096);
+      src.name = sf.text("name");
+      src.path = sf.text_needed("path");
+      src.align = sf.count("align", 4096);
+      sf.finish();
       d.sources.push_back(src);
     }
-  }
-  const Json& layers = need(j, "layers", w);
-  require(layers.is_array(), SS_E_DESC, "desc.layers: expected an array");
-  for (size_t i = 0; i < layers.arr.size(); ++i) {
-    const Json& lj = layers.arr[i];
-    const std::string lw = idx("desc.layers", i);
-    only_keys(lj, lw,
-              {"index", "kind", "fixed_bytes", "n_units", "top_k", "n_shared", "unit_bytes", "parts", "router", "hash",
-               "benefit", "streamable"});
-    Layer l;
-    const int64_t index = json_i64(need(lj, "index", lw), lw + ".index");
-    require(index >= 0 && index < kMaxLayers, SS_E_DESC, lw + ".index: 0..4095");
-    l.index = int(index);
-    const std::string kind = json_str(need(lj, "kind", lw), lw + ".kind");
-    if (kind == "dense") l.kind = LayerKind::Dense;
-    else if (kind == "moe") l.kind = LayerKind::Moe;
-    else if (kind == "blob") l.kind = LayerKind::Blob;
-    else fail(SS_E_DESC, lw + ".kind: expected dense | moe | blob");
-    l.fixed_bytes = u64_or(lj, "fixed_bytes", lw, 0);
-    l.n_units = int(capped(u64_or(lj, "n_units", lw, l.kind == LayerKind::Blob ? 1 : 0), kMaxUnits, lw + ".n_units"));
-    l.top_k = int(capped(u64_or(lj, "top_k", lw, 0), kMaxUnits, lw + ".top_k"));
-    l.n_shared = int(capped(u64_or(lj, "n_shared", lw, 0), kMaxUnits, lw + ".n_shared"));
-    l.unit_bytes = u64_or(lj, "unit_bytes", lw, 0);
-    if (const Json* st = lj.find("streamable")) l.streamable = json_bool(*st, lw + ".streamable");
-    if (const Json* parts = lj.find("parts")) {
-      require(parts->is_array(), SS_E_DESC, lw + ".parts: expected an array");
-      for (size_t p = 0; p < parts->arr.size(); ++p) {
-        const Json& pj = parts->arr[p];
-        const std::string pw = idx(lw + ".parts", p);
-        only_keys(pj, pw, {"name", "format", "source", "offset", "stride", "bytes"});
-        Part part;
-        part.name = str_or(pj, "name", pw);
-        part.format = json_str(need(pj, "format", pw), pw + ".format");
-        part.source = int(capped(u64_or(pj, "source", pw, 0), 1024, pw + ".source"));
-        part.offset = json_u64(need(pj, "offset", pw), pw + ".offset");
-        part.bytes = json_u64(need(pj, "bytes", pw), pw + ".bytes");
-        part.stride = u64_or(pj, "stride", pw, part.bytes);
-        l.parts.push_back(part);
-      }
-    }
-    if (const Json* r = lj.find("router")) {
-      const std::string rw = lw + ".router";
-      only_keys(*r, rw, {"tensor", "bias", "format", "score", "rows", "cols"});
-      l.has_router = true;
-      l.router.tensor = json_str(need(*r, "tensor", rw), rw + ".tensor");
-      l.router.bias = str_or(*r, "bias", rw);
-      l.router.format = str_or(*r, "format", rw, "F32");
-      l.router.score = str_or(*r, "score", rw, "softmax");
-      l.router.rows = uint32_t(capped(u64_or(*r, "rows", rw, 0), kMaxUnits, rw + ".rows"));
-      l.router.cols = uint32_t(capped(u64_or(*r, "cols", rw, 0), 1u << 24, rw + ".cols"));
-    }
-    if (const Json* h = lj.find("hash")) {
-      require(h->is_array(), SS_E_DESC, lw + ".hash: expected an array of xxh64 hex strings");
-      for (size_t k = 0; k < h->arr.size(); ++k)
-        l.hash.push_back(parse_hex16(json_str(h->arr[k], idx(lw + ".hash", k)), idx(lw + ".hash", k)));
-    }
-    if (const Json* b = lj.find("benefit")) {
-      require(b->is_array(), SS_E_DESC, lw + ".benefit: expected an array");
-      for (size_t k = 0; k < b->arr.size(); ++k) l.benefit.push_back(json_f64(b->arr[k], idx(lw + ".benefit", k)));
-    }
-    d.layers.push_back(std::move(l));
-  }
-  if (const Json* t = j.find("lookup_tables")) {
-    require(t->is_array(), SS_E_DESC, "desc.lookup_tables: expected an array");
-    for (size_t i = 0; i < t->arr.size(); ++i) {
-      const std::string tw = idx("desc.lookup_tables", i);
-      only_keys(t->arr[i], tw, {"name", "source", "offset", "rows", "row_bytes", "placement"});
+  const Json& layers = f.need("layers");
+  require(layers.is_array(), SS_E_DESC, "desc.layers: not an array");
+  for (size_t i = 0; i < layers.arr.size(); ++i) d.layers.push_back(read_layer(layers.arr[i], item("desc.layers", i)));
+  if (const std::vector<Json>* t = f.list("lookup_tables"))
+    for (size_t i = 0; i < t->size(); ++i) {
+      Fields tf((*t)[i], item("desc.lookup_tables", i));
       LookupTable lt;
-      lt.name = json_str(need(t->arr[i], "name", tw), tw + ".name");
-      lt.source = int(capped(u64_or(t->arr[i], "source", tw, 0), 1024, tw + ".source"));
-      lt.offset = u64_or(t->arr[i], "offset", tw, 0);
-      lt.rows = json_u64(need(t->arr[i], "rows", tw), tw + ".rows");
-      lt.row_bytes = json_u64(need(t->arr[i], "row_bytes", tw), tw + ".row_bytes");
-      lt.placement = str_or(t->arr[i], "placement", tw, "file");
+      lt.name = tf.text_needed("name");
+      lt.source = int(tf.count("source", 0, 1024));
+      lt.offset = tf.count("offset", 0);
+      lt.rows = tf.count_needed("rows");
+      lt.row_bytes = tf.count_needed("row_bytes");
+      lt.placement = tf.text("placement", "file");
+      tf.finish();
       d.lookup_tables.push_back(lt);
     }
-  }
+  f.finish();
   desc_validate(d);
   return d;
 }
 
 void desc_validate(Desc& d) {
-  require(!d.layers.empty() && d.layers.size() <= size_t(kMaxLayers), SS_E_DESC, "desc.layers: 1..4096 layers");
-  require(d.unit_align >= 1 && (d.unit_align & (d.unit_align - 1)) == 0, SS_E_DESC, "desc.unit_align: power of two");
-  for (size_t s = 0; s < d.sources.size(); ++s) {
-    const uint64_t a = d.sources[s].align;
-    require(a >= 1 && (a & (a - 1)) == 0 && a <= (1u << 20), SS_E_DESC,
-            idx("desc.sources", s) + ".align: power of two <= 1 MiB");
-  }
+  require(!d.layers.empty() && d.layers.size() <= kLayerLimit, SS_E_DESC, "desc.layers: needs 1..4096 layers");
+  require(pow2(d.unit_align), SS_E_DESC, "desc.unit_align: not a power of two");
+  for (size_t s = 0; s < d.sources.size(); ++s)
+    require(pow2(d.sources[s].align) && d.sources[s].align <= (uint64_t(1) << 20), SS_E_DESC,
+            item("desc.sources", s) + ".align: not a power of two up to 1 MiB");
   d.unit_base.assign(d.layers.size(), 0);
   d.total_units = 0;
   d.max_unit_bytes = 0;
   d.max_units_per_layer = 0;
   for (size_t i = 0; i < d.layers.size(); ++i) {
     Layer& l = d.layers[i];
-    const std::string lw = idx("desc.layers", i);
-    require(l.index == int(i), SS_E_DESC, lw + ".index: layers must be listed in order 0..n-1");
-    require(l.n_units >= 0 && l.n_units <= kMaxUnits, SS_E_DESC, lw + ".n_units: 0..65536");
-    if (l.kind == LayerKind::Dense)
-      require(l.n_units == 0 && l.parts.empty(), SS_E_DESC, lw + ": a dense layer has no units (use fixed_bytes)");
-    else if (l.kind == LayerKind::Blob)
-      require(l.n_units == 1, SS_E_DESC, lw + ": a blob layer has exactly one unit");
-    else {
-      require(l.n_units >= 1, SS_E_DESC, lw + ": a moe layer needs n_units >= 1");
-      require(l.top_k >= 1 && l.top_k <= l.n_units, SS_E_DESC, lw + ".top_k: 1..n_units");
-    }
+    const std::string lw = item("desc.layers", i);
+    require(l.index == int(i), SS_E_DESC, lw + ".index: layers are listed 0, 1, ... in order");
+    require(l.n_units >= 0 && uint64_t(l.n_units) <= kUnitLimit, SS_E_DESC, lw + ".n_units: outside 0..65536");
+    check_kind(l, lw);
     if (l.n_units > 0) {
-      require(!l.parts.empty(), SS_E_DESC, lw + ".parts: a layer with units needs parts");
-      uint64_t sum = 0;
-      for (size_t p = 0; p < l.parts.size(); ++p) {
-        const Part& part = l.parts[p];
-        const std::string pw = idx(lw + ".parts", p);
-        require(part.bytes > 0, SS_E_DESC, pw + ".bytes: > 0");
-        require(known_format(part.format), SS_E_DESC, pw + ".format: unknown format " + part.format);
-        require(part.source >= 0 && size_t(part.source) < d.sources.size(), SS_E_DESC, pw + ".source: no such source");
-        require(l.n_units == 1 || part.stride >= part.bytes, SS_E_DESC, pw + ".stride: >= bytes (units overlap)");
-        sum = add_ck(sum, part.bytes, pw);
-        add_ck(add_ck(part.offset, mul_ck(uint64_t(l.n_units - 1), part.stride, pw), pw), part.bytes, pw);
-      }
-      if (l.unit_bytes == 0) l.unit_bytes = sum;
-      require(l.unit_bytes == sum, SS_E_DESC,
-              lw + ".unit_bytes: " + std::to_string(l.unit_bytes) + " != sum of parts " + std::to_string(sum));
-      mul_ck(add_ck(l.unit_bytes, d.unit_align, lw), uint64_t(l.n_units), lw);
-      require(l.hash.empty() || l.hash.size() == size_t(l.n_units), SS_E_DESC, lw + ".hash: one per unit");
-      require(l.benefit.empty() || l.benefit.size() == size_t(l.n_units), SS_E_DESC, lw + ".benefit: one per unit");
-      if (l.has_router)
-        require(l.router.rows == 0 || l.router.rows == uint32_t(l.n_units), SS_E_DESC,
-                lw + ".router.rows: must equal n_units");
+      check_units(d, l, lw);
       if (l.streamable) {
         d.max_unit_bytes = std::max(d.max_unit_bytes, l.unit_bytes);
         d.max_units_per_layer = std::max(d.max_units_per_layer, l.n_units);
@@ -313,278 +326,216 @@ void desc_validate(Desc& d) {
     d.unit_base[i] = d.total_units;
     d.total_units += l.n_units;
   }
-  uint64_t dev = 0, host = 0;
-  for (const auto& n : d.fixed_device) dev = add_ck(dev, n.bytes, "desc.fixed_device");
-  for (const auto& n : d.host_fixed) host = add_ck(host, n.bytes, "desc.host_fixed");
-  uint64_t all = add_ck(dev, host, "desc");
+  // everything the model could occupy, each unit at its host stride: below 2^56 bytes
+  uint64_t device = 0, host = 0;
+  for (const NamedBytes& n : d.fixed_device) device = plus(device, n.bytes, "desc.fixed_device");
+  for (const NamedBytes& n : d.host_fixed) host = plus(host, n.bytes, "desc.host_fixed");
+  uint64_t everything = plus(device, host, "desc");
   for (size_t L = 0; L < d.layers.size(); ++L) {
-    const uint64_t st = add_ck(d.layers[L].unit_bytes, 4096, idx("desc.layers", L));
-    all = add_ck(all, mul_ck(uint64_t(d.layers[L].n_units), st, idx("desc.layers", L)), idx("desc.layers", L));
+    const std::string lw = item("desc.layers", L);
+    everything = plus(everything, times(uint64_t(d.layers[L].n_units), plus(d.layers[L].unit_bytes, 4096, lw), lw), lw);
   }
-  require(all < (uint64_t(1) << 56), SS_E_DESC, "desc: total bytes above 2^56 (64 PiB)");
-  for (size_t L = 0; L < d.layers.size(); ++L) {
-    dev = add_ck(dev, d.layers[L].fixed_bytes, idx("desc.layers", L) + ".fixed_bytes");
+  require(everything < kDescByteLimit, SS_E_DESC, "desc: the model's bytes reach 2^56");
+  for (size_t L = 0; L < d.layers.size(); ++L) {  // the fixed device total must fit 64 bits too
+    const std::string lw = item("desc.layers", L);
+    device = plus(device, d.layers[L].fixed_bytes, lw + ".fixed_bytes");
     if (!d.layers[L].streamable)
-      dev = add_ck(dev, mul_ck(uint64_t(d.layers[L].n_units), d.unit_stride(int(L)), idx("desc.layers", L)),
-                   idx("desc.layers", L));
+      device = plus(device, times(uint64_t(d.layers[L].n_units), d.unit_stride(int(L)), lw), lw);
   }
   for (size_t i = 0; i < d.lookup_tables.size(); ++i) {
     const LookupTable& t = d.lookup_tables[i];
-    const std::string tw = idx("desc.lookup_tables", i);
-    require(t.source >= 0 && size_t(t.source) < d.sources.size(), SS_E_DESC, tw + ".source: no such source");
+    const std::string tw = item("desc.lookup_tables", i);
+    require(t.source >= 0 && size_t(t.source) < d.sources.size(), SS_E_DESC, tw + ".source: names no source");
     require(t.placement == "file" || t.placement == "pinned" || t.placement == "device", SS_E_DESC,
-            tw + ".placement: file | pinned | device");
+            tw + ".placement: \"" + t.placement + "\" is not file | pinned | device");
   }
 }
 
 Json desc_to_json(const Desc& d) {
-  Json j = Json::object();
-  j["schema"] = Json::string(kDescSchema);
-  if (!d.model.empty()) j["model"] = Json::string(d.model);
-  if (!d.engine.empty()) j["engine"] = Json::string(d.engine);
-  auto list = [](const std::vector<NamedBytes>& v) {
+  const auto str = [](const std::string& s) { return Json::string(s); };
+  const auto u = [](uint64_t v) { return Json::number(v); };
+  const auto i = [](int64_t v) { return Json::number_i(v); };
+  const auto named = [&](const std::vector<NamedBytes>& v) {
     Json a = Json::array();
-    for (const auto& n : v) {
+    for (const NamedBytes& n : v) {
       Json e = Json::object();
-      e["name"] = Json::string(n.name);
-      e["bytes"] = Json::number(n.bytes);
+      e["name"] = str(n.name);
+      e["bytes"] = u(n.bytes);
       a.push(e);
     }
     return a;
   };
-  j["fixed_device"] = list(d.fixed_device);
-  j["host_fixed"] = list(d.host_fixed);
-  j["state_bytes_per_position"] = Json::number(d.state_bytes_per_position);
-  j["workspace_bytes_per_row"] = Json::number(d.workspace_bytes_per_row);
-  j["unit_align"] = Json::number(d.unit_align);
-  j["order"] = Json::string(d.order == Order::Prefix ? "prefix" : "ranked");
-  j["tiers"] = Json::string(tiers_text(d.tiers));
-  j["ring_slots"] = Json::number(uint64_t(d.ring_slots));
-  if (!d.routes.empty()) j["routes"] = Json::string(d.routes);
-  Json srcs = Json::array();
-  for (const auto& s : d.sources) {
+  Json j = Json::object();
+  j["schema"] = str(kDescSchema);
+  if (!d.model.empty()) j["model"] = str(d.model);
+  if (!d.engine.empty()) j["engine"] = str(d.engine);
+  if (!d.routes.empty()) j["routes"] = str(d.routes);
+  j["fixed_device"] = named(d.fixed_device);
+  j["host_fixed"] = named(d.host_fixed);
+  j["state_bytes_per_position"] = u(d.state_bytes_per_position);
+  j["workspace_bytes_per_row"] = u(d.workspace_bytes_per_row);
+  j["unit_align"] = u(d.unit_align);
+  j["order"] = str(name_of(d.order, kOrders));
+  j["tiers"] = str(name_of(d.tiers, kTierSets));
+  j["ring_slots"] = u(d.ring_slots);
+  j["sources"] = Json::array();
+  for (const Source& s : d.sources) {
     Json e = Json::object();
-    if (!s.name.empty()) e["name"] = Json::string(s.name);
-    e["path"] = Json::string(s.path);
-    e["align"] = Json::number(s.align);
-    srcs.push(e);
+    if (!s.name.empty()) e["name"] = str(s.name);
+    e["path"] = str(s.path);
+    e["align"] = u(s.align);
+    j["sources"].push(e);
   }
-  j["sources"] = srcs;
-  Json layers = Json::array();
-  for (const auto& l : d.layers) {
+  j["layers"] = Json::array();
+  for (const Layer& l : d.layers) {
     Json e = Json::object();
-    e["index"] = Json::number_i(l.index);
-    e["kind"] = Json::string(l.kind == LayerKind::Dense ? "dense" : l.kind == LayerKind::Moe ? "moe" : "blob");
-    e["fixed_bytes"] = Json::number(l.fixed_bytes);
+    e["index"] = i(l.index);
+    e["kind"] = str(name_of(l.kind, kKinds));
+    e["fixed_bytes"] = u(l.fixed_bytes);
+    if (l.top_k) e["top_k"] = i(l.top_k);
+    if (l.n_shared) e["n_shared"] = i(l.n_shared);
     if (l.n_units > 0) {
-      e["n_units"] = Json::number_i(l.n_units);
-      e["unit_bytes"] = Json::number(l.unit_bytes);
+      e["n_units"] = i(l.n_units);
+      e["unit_bytes"] = u(l.unit_bytes);
       e["streamable"] = Json::boolean(l.streamable);
-      Json parts = Json::array();
-      for (const auto& p : l.parts) {
+      e["parts"] = Json::array();
+      for (const Part& p : l.parts) {
         Json pj = Json::object();
-        if (!p.name.empty()) pj["name"] = Json::string(p.name);
-        pj["format"] = Json::string(p.format);
-        pj["source"] = Json::number_i(p.source);
-        pj["offset"] = Json::number(p.offset);
-        pj["stride"] = Json::number(p.stride);
-        pj["bytes"] = Json::number(p.bytes);
-        parts.push(pj);
+        if (!p.name.empty()) pj["name"] = str(p.name);
+        pj["format"] = str(p.format);
+        pj["source"] = i(p.source);
+        pj["offset"] = u(p.offset);
+        pj["stride"] = u(p.stride);
+        pj["bytes"] = u(p.bytes);
+        e["parts"].push(pj);
       }
-      e["parts"] = parts;
       if (!l.hash.empty()) {
-        Json h = Json::array();
-        for (uint64_t v : l.hash) h.push(Json::string(hex16(v)));
-        e["hash"] = h;
+        e["hash"] = Json::array();
+        for (uint64_t h : l.hash) e["hash"].push(str(hash_text(h)));
       }
       if (!l.benefit.empty()) {
-        Json b = Json::array();
-        for (double v : l.benefit) b.push(Json::number_f(v));
-        e["benefit"] = b;
+        e["benefit"] = Json::array();
+        for (double b : l.benefit) e["benefit"].push(Json::number_f(b));
       }
     }
-    if (l.top_k) e["top_k"] = Json::number_i(l.top_k);
-    if (l.n_shared) e["n_shared"] = Json::number_i(l.n_shared);
     if (l.has_router) {
       Json r = Json::object();
-      r["tensor"] = Json::string(l.router.tensor);
-      if (!l.router.bias.empty()) r["bias"] = Json::string(l.router.bias);
-      r["format"] = Json::string(l.router.format);
-      r["score"] = Json::string(l.router.score);
-      r["rows"] = Json::number(uint64_t(l.router.rows));
-      r["cols"] = Json::number(uint64_t(l.router.cols));
+      r["tensor"] = str(l.router.tensor);
+      if (!l.router.bias.empty()) r["bias"] = str(l.router.bias);
+      r["format"] = str(l.router.format);
+      r["score"] = str(l.router.score);
+      r["rows"] = u(l.router.rows);
+      r["cols"] = u(l.router.cols);
       e["router"] = r;
     }
-    layers.push(e);
+    j["layers"].push(e);
   }
-  j["layers"] = layers;
-  Json tables = Json::array();
-  for (const auto& t : d.lookup_tables) {
+  j["lookup_tables"] = Json::array();
+  for (const LookupTable& t : d.lookup_tables) {
     Json e = Json::object();
-    e["name"] = Json::string(t.name);
-    e["source"] = Json::number_i(t.source);
-    e["offset"] = Json::number(t.offset);
-    e["rows"] = Json::number(t.rows);
-    e["row_bytes"] = Json::number(t.row_bytes);
-    e["placement"] = Json::string(t.placement);
-    tables.push(e);
+    e["name"] = str(t.name);
+    e["source"] = i(t.source);
+    e["offset"] = u(t.offset);
+    e["rows"] = u(t.rows);
+    e["row_bytes"] = u(t.row_bytes);
+    e["placement"] = str(t.placement);
+    j["lookup_tables"].push(e);
   }
-  j["lookup_tables"] = tables;
   return j;
 }
 
-// ---------------------------------------------------------------------------------------------------------------------
-// Planner. Units are streamable (layer, unit) pairs in model order; "bytes" is the device slot (unit stride).
+// ---- the planner ----------------------------------------------------------------------------------------------------------
 namespace {
 
-struct Cand {
-  int64_t g;
+std::string gib(uint64_t n) {
+  char b[32];
+  std::snprintf(b, sizeof b, "%.3f", double(n) / double(kGiB));
+  return b;
+}
+
+bool exclusive(const ss_budget& b) { return b.tier_mode == SS_TIER_MODE_EXCLUSIVE; }
+bool has_pinned_copy(uint8_t t) { return t == SS_TIER_PINNED || t == SS_TIER_RESIDENT_BACKED; }
+bool on_device(uint8_t t) { return t == SS_TIER_RESIDENT || t == SS_TIER_RESIDENT_BACKED; }
+
+// A streamable unit as the planner ranks it: model key, layer, device slot bytes, benefit.
+struct Streamed {
+  int64_t key;
   int layer;
-  uint64_t bytes;
-  double benefit;
+  uint64_t slot;
+  double value;
 };
 
-double per_byte(const Cand& c) {
-  return c.bytes ? c.benefit / double(c.bytes) : std::numeric_limits<double>::infinity();
-}
-// Higher benefit per byte first; model order breaks ties.
-bool before(const Cand& a, const Cand& b) {
-  const double x = per_byte(a), y = per_byte(b);
-  if (x != y) return x > y;
-  return a.g < b.g;
+// Denser (benefit per slot byte) first; model order among equals. A total order on distinct keys.
+bool denser(const Streamed& a, const Streamed& b) {
+  const double inf = std::numeric_limits<double>::infinity();
+  const double x = a.slot ? a.value / double(a.slot) : inf, y = b.slot ? b.value / double(b.slot) : inf;
+  return x != y ? x > y : a.key < b.key;
 }
 
-std::vector<Cand> candidates(const Desc& d, const std::vector<double>& benefit) {
-  std::vector<Cand> v;
+// Every streamable unit in model order, valued by the caller's benefit, else the descriptor's, else 1.
+std::vector<Streamed> streamable_units(const Desc& d, const std::vector<double>& benefit) {
+  std::vector<Streamed> v;
   for (size_t L = 0; L < d.layers.size(); ++L) {
     const Layer& l = d.layers[L];
     if (!l.streamable) continue;
     for (int u = 0; u < l.n_units; ++u) {
-      const int64_t g = d.unit_base[L] + u;
-      const double b = !benefit.empty() ? benefit[size_t(g)] : !l.benefit.empty() ? l.benefit[size_t(u)] : 1.0;
-      require(std::isfinite(b) && b >= 0, SS_E_INVALID, "plan: benefit must be finite and >= 0");
-      v.push_back({g, int(L), d.unit_stride(int(L)), b});
+      const int64_t key = d.unit_base[L] + u;
+      const double b = !benefit.empty() ? benefit[size_t(key)] : !l.benefit.empty() ? l.benefit[size_t(u)] : 1.0;
+      require(std::isfinite(b) && b >= 0, SS_E_INVALID, "plan: a benefit is negative or not finite");
+      v.push_back({key, int(L), d.unit_stride(int(L)), b});
     }
   }
   return v;
 }
 
-uint64_t dynamic_upper(const Desc& d, const ss_budget& b) {
-  if (!b.dynamic_slots_per_layer) return 0;
-  uint64_t t = 0;
-  for (size_t L = 0; L < d.layers.size(); ++L) {
-    const Layer& l = d.layers[L];
-    if (l.streamable && l.n_units > 0)
-      t += uint64_t(std::min<uint32_t>(b.dynamic_slots_per_layer, uint32_t(l.n_units))) * d.unit_stride(int(L));
-  }
-  return t;
+// Ring slots for a slot size: the budget's, else the descriptor's, else twice the most units of any streamable layer
+// with that slot size.
+uint32_t ring_slots_for(const Desc& d, const ss_budget& b, uint64_t stride) {
+  if (b.ring_slots) return b.ring_slots;
+  if (d.ring_slots) return d.ring_slots;
+  uint32_t n = 0;
+  for (size_t L = 0; L < d.layers.size(); ++L)
+    if (d.layers[L].streamable && d.layers[L].n_units && d.unit_stride(int(L)) == stride)
+      n = std::max(n, uint32_t(2 * d.layers[L].n_units));
+  return n;
 }
 
-// One ring per distinct slot size among the streamed units; slots: the budget's, else the descriptor's, else twice the
-// most units of any layer with that slot size. Sorted by slot size.
-std::vector<RingClass> rings_of(const Desc& d, const ss_budget& b, const std::vector<Cand>& streamed) {
+// One ring per distinct nonzero slot size among `slots`, by size (none with the pair tier set).
+std::vector<RingClass> rings_for(const Desc& d, const ss_budget& b, const std::vector<uint64_t>& slots) {
   std::vector<RingClass> out;
   if (d.tiers == Tiers::Pair) return out;
-  for (const Cand& c : streamed) {
-    if (!c.bytes) continue;
-    bool seen = false;
-    for (const RingClass& r : out) seen = seen || r.stride == c.bytes;
-    if (seen) continue;
-    uint32_t slots = b.ring_slots ? b.ring_slots : d.ring_slots;
-    if (!slots)
-      for (size_t L = 0; L < d.layers.size(); ++L)
-        if (d.layers[L].streamable && d.layers[L].n_units && d.unit_stride(int(L)) == c.bytes)
-          slots = std::max(slots, uint32_t(2 * d.layers[L].n_units));
-    out.push_back({c.bytes, slots});
-  }
-  std::sort(out.begin(), out.end(), [](const RingClass& x, const RingClass& y) { return x.stride < y.stride; });
+  std::set<uint64_t> sizes(slots.begin(), slots.end());
+  sizes.erase(0);
+  for (uint64_t s : sizes) out.push_back({s, ring_slots_for(d, b, s)});
   return out;
 }
 
-uint64_t ring_total(const std::vector<RingClass>& r) {
+uint64_t ring_bytes(const std::vector<RingClass>& r) {
   uint64_t t = 0;
   for (const RingClass& c : r) t += c.stride * c.slots;
   return t;
 }
 
-bool excl(const ss_budget& b) { return b.tier_mode == SS_TIER_MODE_EXCLUSIVE; }
-bool pinned_copy(uint8_t t) { return t == SS_TIER_PINNED || t == SS_TIER_RESIDENT_BACKED; }
-
-uint64_t spare_total(const std::vector<SpareClass>& s) {
+// The device bytes the dynamic slots take at most (before any unit is placed).
+uint64_t dynamic_ceiling(const Desc& d, const ss_budget& b) {
   uint64_t t = 0;
-  for (const SpareClass& c : s) {
-    require(c.blocks == 0 || c.block_bytes <= (UINT64_MAX - t) / c.blocks, SS_E_INVALID,
-            "plan: spare block bytes overflow");
-    t += c.block_bytes * c.blocks;
-  }
+  for (size_t L = 0; b.dynamic_slots_per_layer && L < d.layers.size(); ++L)
+    if (d.layers[L].streamable && d.layers[L].n_units > 0)
+      t += uint64_t(std::min<uint32_t>(b.dynamic_slots_per_layer, uint32_t(d.layers[L].n_units))) *
+           d.unit_stride(int(L));
   return t;
 }
 
-// The totals every consumer bills, from the tiers alone.
-void totals(const Desc& d, const ss_budget& b, Plan& p) {
-  std::vector<Cand> streamed;
-  p.resident = p.pinned = p.disk = p.dynamic = 0;
-  p.n_resident = p.n_pinned = p.n_disk = p.n_pair = p.n_backed = 0;
-  for (size_t L = 0; L < d.layers.size(); ++L) {
-    const Layer& l = d.layers[L];
-    int planned = 0;
-    for (int u = 0; u < l.n_units; ++u) {
-      const int64_t g = d.unit_base[L] + u;
-      const uint8_t t = p.tier[size_t(g)];
-      require(t <= SS_TIER_RESIDENT_BACKED, SS_E_INVALID, "plan: bad tier value");
-      if (!l.streamable) {
-        require(t == SS_TIER_RESIDENT, SS_E_INVALID, "plan: a non-streamable layer's units must be resident");
-        continue;
-      }
-      require(!(excl(b) && t == SS_TIER_RESIDENT_BACKED), SS_E_INVALID,
-              "plan: tier B (resident with a pinned copy) is the second copy the exclusive tier mode removes");
-      if (t == SS_TIER_RESIDENT || t == SS_TIER_RESIDENT_BACKED) {
-        p.resident += d.unit_stride(int(L));
-        ++p.n_resident;
-        ++planned;
-        if (t == SS_TIER_RESIDENT_BACKED) ++p.n_backed;
-        continue;
-      }
-      if (t != SS_TIER_PAIR) streamed.push_back({g, int(L), d.unit_stride(int(L)), 0.0});
-      if (t == SS_TIER_PINNED) {
-        ++p.n_pinned;
-      } else if (t == SS_TIER_DISK) {
-        p.disk += l.unit_bytes;
-        ++p.n_disk;
-      } else {
-        ++p.n_pair;
-      }
-    }
-    if (l.streamable && l.n_units > 0 && b.dynamic_slots_per_layer)
-      p.dynamic += uint64_t(std::min<uint32_t>(b.dynamic_slots_per_layer, uint32_t(l.n_units - planned))) *
-                   d.unit_stride(int(L));
-  }
-  const uint64_t layout = pinned_layout(d, p.tier).total;
-  p.pinned = layout;
-  for (const auto& n : d.host_fixed) p.pinned += n.bytes;
-  require(p.pinned >= layout, SS_E_INVALID, "plan: host byte total overflows");
-  p.spares = spare_classes(d, b, b.host_pinned_bytes > p.pinned ? b.host_pinned_bytes - p.pinned : 0);
-  p.pinned += spare_total(p.spares);
-  p.rings = rings_of(d, b, streamed);
-  p.ring = ring_total(p.rings);
-  require(p.pinned <= b.host_pinned_bytes, SS_E_CAPACITY,
-          d.engine + ": " + gib(p.pinned) + " GiB must be pinned on the host, above the host budget " +
-              gib(b.host_pinned_bytes) + " GiB; raise the cap or the host budget");
-  p.peak = p.fixed + p.dynamic + p.ring + p.resident;
-  require(p.peak + p.margin <= p.cap, SS_E_CAPACITY,
-          d.engine + ": predicted peak " + gib(p.peak) + " GiB above the cap " + gib(p.cap) + " GiB - margin " +
-              gib(p.margin) + " GiB");
-}
-
-Plan start_plan(const Desc& d, const ss_budget& b) {
-  require(b.device_bytes > 0, SS_E_INVALID, "plan: device budget must be > 0");
+// The budget's own rules and the fixed bill, before any unit is placed.
+Plan open_plan(const Desc& d, const ss_budget& b) {
+  require(b.device_bytes > 0, SS_E_INVALID, "plan: no device budget");
   require(b.tier_mode == SS_TIER_MODE_INCLUSIVE || b.tier_mode == SS_TIER_MODE_EXCLUSIVE, SS_E_INVALID,
-          "plan: tier_mode must be SS_TIER_MODE_INCLUSIVE or SS_TIER_MODE_EXCLUSIVE");
-  if (excl(b)) {
+          "plan: tier_mode is neither inclusive nor exclusive");
+  if (exclusive(b)) {
     require(!b.pinned_backing, SS_E_INVALID,
-            "plan: pinned_backing keeps a second pinned copy of residents, which the exclusive tier mode removes");
+            "plan: pinned_backing asks for the second pinned copy of residents that the exclusive mode gives up");
     require(d.tiers == Tiers::Pinned || d.tiers == Tiers::PinnedDisk, SS_E_INVALID,
-            d.engine + ": the exclusive tier mode needs a descriptor whose tiers allow pinned");
+            d.engine + ": the exclusive mode needs a pinned tier, and the descriptor's tiers have none");
   }
   Plan p;
   p.budget = b;
@@ -593,42 +544,160 @@ Plan start_plan(const Desc& d, const ss_budget& b) {
   p.tier.assign(size_t(d.total_units), SS_TIER_RESIDENT);
   p.dynamic_slots_per_layer = b.dynamic_slots_per_layer;
   p.fixed = d.fixed_total() + b.workspace_bytes;
-  p.dynamic = dynamic_upper(d, b);
+  p.dynamic = dynamic_ceiling(d, b);
   require(p.cap >= p.margin + p.fixed + p.dynamic, SS_E_CAPACITY,
-          d.engine + ": fixed device memory " + gib(p.fixed) + " GiB + dynamic slots " + gib(p.dynamic) +
-              " GiB + margin " + gib(p.margin) + " GiB exceeds the " + gib(p.cap) + " GiB cap");
+          d.engine + ": the " + gib(p.cap) + " GiB cap holds neither fixed " + gib(p.fixed) + " GiB + dynamic " +
+              gib(p.dynamic) + " GiB + margin " + gib(p.margin) + " GiB");
   return p;
 }
 
-// RESIDENT -> RESIDENT_BACKED while the host budget left after host_fixed and the pinned tier lasts, lowest benefit
-// per byte first, stopping at the first that does not fit.
-void give_backing(const Desc& d, const ss_budget& b, const std::vector<double>& benefit, std::vector<uint8_t>& tier) {
+// Which units stay on the device. Prefix order: the longest model-order prefix that fits with the rings of the rest
+// (each split priced in one backward pass). Ranked: everything if it fits, else the rings of everything first and then
+// the densest units that still fit, skipping any that does not.
+std::vector<char> choose_residents(const Desc& d, const ss_budget& b, const std::vector<Streamed>& units, uint64_t room,
+                                   bool* ok) {
+  const size_t n = units.size();
+  std::vector<char> keep(n, 0);
+  uint64_t all = 0;
+  for (const Streamed& s : units) all += s.slot;
+  *ok = true;
+  if (d.order == Order::Prefix) {
+    // ring[k]: the rings of units[k..n); prefix[k]: the slots of units[0..k)
+    std::vector<uint64_t> ring(n + 1, 0);
+    std::set<uint64_t> seen;
+    for (size_t k = n; k-- > 0;) {
+      ring[k] = ring[k + 1];
+      if (d.tiers != Tiers::Pair && units[k].slot && seen.insert(units[k].slot).second)
+        ring[k] += units[k].slot * ring_slots_for(d, b, units[k].slot);
+    }
+    uint64_t prefix = all;
+    for (size_t k = n + 1; k-- > 0;) {
+      if (prefix + ring[k] <= room) {
+        std::fill(keep.begin(), keep.begin() + std::ptrdiff_t(k), char(1));
+        return keep;
+      }
+      if (k) prefix -= units[k - 1].slot;
+    }
+    *ok = false;
+    return keep;
+  }
+  if (all <= room) {
+    std::fill(keep.begin(), keep.end(), char(1));
+    return keep;
+  }
+  std::vector<uint64_t> slots;
+  for (const Streamed& s : units) slots.push_back(s.slot);
+  const uint64_t rings = ring_bytes(rings_for(d, b, slots));
+  if (rings > room) {
+    *ok = false;
+    return keep;
+  }
+  std::vector<size_t> by_density(n);
+  for (size_t i = 0; i < n; ++i) by_density[i] = i;
+  std::sort(by_density.begin(), by_density.end(), [&](size_t a, size_t c) { return denser(units[a], units[c]); });
+  uint64_t left = room - rings;
+  for (size_t i : by_density)
+    if (units[i].slot <= left) {
+      keep[i] = 1;
+      left -= units[i].slot;
+    }
+  return keep;
+}
+
+uint64_t host_budget_after_fixed(const Desc& d, const ss_budget& b) {
   uint64_t left = b.host_pinned_bytes;
-  for (const auto& n : d.host_fixed) left = left > n.bytes ? left - n.bytes : 0;
-  std::vector<Cand> res;
-  for (const Cand& c : candidates(d, benefit)) {
-    const uint8_t t = tier[size_t(c.g)];
-    if (t == SS_TIER_PINNED) {
-      const uint64_t hb = host_stride(d.layers[size_t(c.layer)].unit_bytes);
+  for (const NamedBytes& n : d.host_fixed) left = left > n.bytes ? left - n.bytes : 0;
+  return left;
+}
+
+// pinned_backing: residents take a pinned copy, least dense first, while the host budget left after host_fixed and
+// the pinned tier lasts; the first that does not fit ends it.
+void back_residents(const Desc& d, const ss_budget& b, const std::vector<Streamed>& units, std::vector<uint8_t>& tier) {
+  uint64_t left = host_budget_after_fixed(d, b);
+  std::vector<Streamed> res;
+  for (const Streamed& s : units) {
+    if (tier[size_t(s.key)] == SS_TIER_PINNED) {
+      const uint64_t hb = host_stride(d.layers[size_t(s.layer)].unit_bytes);
       left = left > hb ? left - hb : 0;
-    } else if (t == SS_TIER_RESIDENT) {
-      res.push_back(c);
+    } else if (tier[size_t(s.key)] == SS_TIER_RESIDENT) {
+      res.push_back(s);
     }
   }
-  std::stable_sort(res.begin(), res.end(), [](const Cand& x, const Cand& y) { return before(y, x); });
-  for (const Cand& c : res) {
-    const uint64_t hb = host_stride(d.layers[size_t(c.layer)].unit_bytes);
-    if (hb > left) break;
-    tier[size_t(c.g)] = SS_TIER_RESIDENT_BACKED;
+  std::sort(res.begin(), res.end(), [](const Streamed& x, const Streamed& y) { return denser(y, x); });
+  for (const Streamed& s : res) {
+    const uint64_t hb = host_stride(d.layers[size_t(s.layer)].unit_bytes);
+    if (hb > left) return;
+    tier[size_t(s.key)] = SS_TIER_RESIDENT_BACKED;
     left -= hb;
   }
+}
+
+// The bill of a complete tier assignment (made here or handed in): every tier checked, the device and host totals,
+// the rings of the streamed units, the spare blocks; then both budgets.
+void bill(const Desc& d, const ss_budget& b, Plan& p) {
+  std::vector<uint64_t> streamed_slots;
+  p.resident = p.pinned = p.disk = p.dynamic = 0;
+  p.n_resident = p.n_pinned = p.n_disk = p.n_pair = p.n_backed = 0;
+  for (size_t L = 0; L < d.layers.size(); ++L) {
+    const Layer& l = d.layers[L];
+    const uint64_t stride = d.unit_stride(int(L));
+    int on_dev = 0;
+    for (int u = 0; u < l.n_units; ++u) {
+      const uint8_t t = p.tier[size_t(d.unit_base[L] + u)];
+      require(t <= SS_TIER_RESIDENT_BACKED, SS_E_INVALID, "plan: tier value " + num(t) + " is not a tier");
+      if (!l.streamable) {
+        require(t == SS_TIER_RESIDENT, SS_E_INVALID, "plan: a layer that cannot stream keeps its units resident");
+        continue;
+      }
+      require(!(exclusive(b) && t == SS_TIER_RESIDENT_BACKED), SS_E_INVALID,
+              "plan: tier B keeps a second pinned copy, which the exclusive mode gives up");
+      switch (t) {
+        case SS_TIER_RESIDENT_BACKED: ++p.n_backed; [[fallthrough]];
+        case SS_TIER_RESIDENT:
+          p.resident += stride;
+          ++p.n_resident;
+          ++on_dev;
+          break;
+        case SS_TIER_PINNED:
+          ++p.n_pinned;
+          streamed_slots.push_back(stride);
+          break;
+        case SS_TIER_DISK:
+          ++p.n_disk;
+          p.disk += l.unit_bytes;
+          streamed_slots.push_back(stride);
+          break;
+        default: ++p.n_pair; break;
+      }
+    }
+    if (l.streamable && l.n_units > 0 && b.dynamic_slots_per_layer)
+      p.dynamic += uint64_t(std::min<uint32_t>(b.dynamic_slots_per_layer, uint32_t(l.n_units - on_dev))) * stride;
+  }
+  const uint64_t layout = pinned_layout(d, p.tier).total;
+  p.pinned = layout;
+  for (const NamedBytes& n : d.host_fixed) p.pinned += n.bytes;
+  require(p.pinned >= layout, SS_E_INVALID, "plan: the host total overflows 64 bits");
+  p.spares = spare_classes(d, b, b.host_pinned_bytes > p.pinned ? b.host_pinned_bytes - p.pinned : 0);
+  for (const SpareClass& c : p.spares) {
+    const uint64_t blocks = times(c.block_bytes, c.blocks, "plan: spare blocks", SS_E_INVALID);
+    p.pinned = plus(p.pinned, blocks, "plan: spare blocks", SS_E_INVALID);
+  }
+  p.rings = rings_for(d, b, streamed_slots);
+  p.ring = ring_bytes(p.rings);
+  require(p.pinned <= b.host_pinned_bytes, SS_E_CAPACITY,
+          d.engine + ": " + gib(p.pinned) + " GiB must be pinned but the host budget is " + gib(b.host_pinned_bytes) +
+              " GiB");
+  p.peak = p.fixed + p.dynamic + p.ring + p.resident;
+  require(p.peak + p.margin <= p.cap, SS_E_CAPACITY,
+          d.engine + ": the predicted peak " + gib(p.peak) + " GiB + margin " + gib(p.margin) + " GiB is above the " +
+              gib(p.cap) + " GiB cap");
 }
 
 }  // namespace
 
 uint64_t host_stride(uint64_t bytes) {
-  require(bytes <= UINT64_MAX - (kHostStride - 1), SS_E_INVALID, "plan: unit bytes overflow the host stride");
-  return (bytes + kHostStride - 1) / kHostStride * kHostStride;
+  require(bytes <= UINT64_MAX - (kHostStride - 1), SS_E_INVALID, "plan: a unit's host stride overflows 64 bits");
+  return (bytes + kHostStride - 1) & ~(kHostStride - 1);
 }
 
 uint64_t plan_margin(const ss_budget& b) {
@@ -643,212 +712,153 @@ bool same_budget(const ss_budget& a, const ss_budget& b) {
          a.host_spare_units == b.host_spare_units;
 }
 
+// Units with a pinned copy, in model order at 4 KiB host strides, packed into chunks of at most 1 GiB (a unit larger
+// than that alone in its chunk).
 PinnedLayout pinned_layout(const Desc& d, const std::vector<uint8_t>& tier) {
-  // model order, 4 KiB strides, chunks of at most 1 GiB (a larger unit alone in its chunk)
   PinnedLayout pl;
   pl.chunk_of.assign(size_t(d.total_units), -1);
   pl.offset_of.assign(size_t(d.total_units), 0);
-  uint64_t used = 0;
-  bool open = false;
   for (size_t L = 0; L < d.layers.size(); ++L) {
     const uint64_t st = host_stride(d.layers[L].unit_bytes);
     for (int u = 0; u < d.layers[L].n_units; ++u) {
-      const int64_t g = d.unit_base[L] + u;
-      if (!pinned_copy(tier[size_t(g)])) continue;
-      if (!open || (used > 0 && used + st > kPinnedChunk)) {
-        if (open) pl.chunk_bytes.push_back(used);
-        used = 0;
-        open = true;
-      }
-      pl.chunk_of[size_t(g)] = int32_t(pl.chunk_bytes.size());
-      pl.offset_of[size_t(g)] = used;
-      used += st;
+      const size_t key = size_t(d.unit_base[L] + u);
+      if (!has_pinned_copy(tier[key])) continue;
+      if (pl.chunk_bytes.empty() || pl.chunk_bytes.back() + st > kPinnedChunk) pl.chunk_bytes.push_back(0);
+      pl.chunk_of[key] = int32_t(pl.chunk_bytes.size() - 1);
+      pl.offset_of[key] = pl.chunk_bytes.back();
+      pl.chunk_bytes.back() += st;
     }
   }
-  if (open) pl.chunk_bytes.push_back(used);
-  for (uint64_t c : pl.chunk_bytes) {
-    require(pl.total <= UINT64_MAX - c, SS_E_INVALID, "plan: pinned layout overflows");
-    pl.total += c;
-  }
+  for (uint64_t c : pl.chunk_bytes) pl.total = plus(pl.total, c, "plan: pinned layout", SS_E_INVALID);
   return pl;
 }
 
+// Exclusive mode: per distinct host stride of the streamable units, up to host_spare_units (default 64, at most the
+// units of that stride) spare blocks, granted smallest blocks first from what is left of the host budget.
 std::vector<SpareClass> spare_classes(const Desc& d, const ss_budget& b, uint64_t host_left) {
   std::vector<SpareClass> out;
-  if (!excl(b)) return out;
-  std::vector<std::pair<uint64_t, uint64_t>> per;  // host stride -> streamable units of that stride
-  for (const Layer& l : d.layers) {
-    if (!l.streamable || !l.n_units) continue;
-    const uint64_t hs = host_stride(l.unit_bytes);
-    bool found = false;
-    for (auto& x : per)
-      if (x.first == hs) {
-        x.second += uint64_t(l.n_units);
-        found = true;
-      }
-    if (!found) per.push_back({hs, uint64_t(l.n_units)});
-  }
-  for (const auto& x : per) {
-    const uint64_t want = b.host_spare_units ? b.host_spare_units : 64;
-    out.push_back({x.first, uint32_t(std::min<uint64_t>(want, x.second)), 0});
-  }
-  std::sort(out.begin(), out.end(), [](const SpareClass& x, const SpareClass& y) { return x.block_bytes < y.block_bytes; });
-  for (SpareClass& c : out) {  // smallest blocks first
+  if (!exclusive(b)) return out;
+  std::map<uint64_t, uint64_t> units_of;  // host stride -> streamable units
+  for (const Layer& l : d.layers)
+    if (l.streamable && l.n_units) units_of[host_stride(l.unit_bytes)] += uint64_t(l.n_units);
+  const uint64_t want = b.host_spare_units ? b.host_spare_units : 64;
+  for (const auto& kv : units_of) {  // by block size
+    SpareClass c{kv.first, uint32_t(std::min(want, kv.second)), 0};
     c.blocks = uint32_t(std::min<uint64_t>(c.asked, host_left / c.block_bytes));
     host_left -= uint64_t(c.blocks) * c.block_bytes;
+    out.push_back(c);
   }
   return out;
 }
 
 Plan plan_make(const Desc& d, const ss_budget& b, const std::vector<double>& benefit) {
   require(benefit.empty() || int64_t(benefit.size()) == d.total_units, SS_E_INVALID,
-          "plan: benefit needs one value per unit (ss_desc_total_units)");
-  Plan p = start_plan(d, b);
-  const std::vector<Cand> units = candidates(d, benefit);
-  uint64_t room = p.cap - p.margin - p.fixed - p.dynamic;
-  std::vector<char> chosen(units.size(), 0);
-  uint64_t total = 0;
-  for (const Cand& c : units) total += c.bytes;
-  bool ok = false;
-  if (d.order == Order::Prefix) {
-    // the longest prefix that fits together with the rings of what is left
-    std::vector<Cand> rest;
-    for (size_t k = units.size() + 1; k-- > 0;) {
-      rest.assign(units.begin() + std::ptrdiff_t(k), units.end());
-      if (total + ring_total(rings_of(d, b, rest)) <= room) {
-        for (size_t i = 0; i < k; ++i) chosen[i] = 1;
-        ok = true;
-        break;
-      }
-      if (k) total -= units[k - 1].bytes;
-    }
-  } else if (total <= room) {
-    std::fill(chosen.begin(), chosen.end(), char(1));
-    ok = true;
-  } else {
-    const uint64_t ring = ring_total(rings_of(d, b, units));
-    if (ring <= room) {
-      room -= ring;
-      std::vector<size_t> order(units.size());
-      for (size_t i = 0; i < order.size(); ++i) order[i] = i;
-      std::stable_sort(order.begin(), order.end(), [&](size_t a, size_t c) { return before(units[a], units[c]); });
-      uint64_t used = 0;
-      for (size_t i : order)
-        if (used + units[i].bytes <= room) {
-          chosen[i] = 1;
-          used += units[i].bytes;
-        }
-      ok = true;
-    }
-  }
-  require(ok, SS_E_CAPACITY,
-          d.engine + ": nothing fits under the " + gib(p.cap) + " GiB cap: fixed " + gib(p.fixed) + " GiB + margin " +
-              gib(p.margin) + " GiB + the stream rings exceed it");
-  uint64_t host_left = b.host_pinned_bytes;
-  for (const auto& n : d.host_fixed) host_left = host_left > n.bytes ? host_left - n.bytes : 0;
-  std::vector<Cand> spill;
+          "plan: the benefit list needs one value per unit (ss_desc_total_units)");
+  Plan p = open_plan(d, b);
+  const std::vector<Streamed> units = streamable_units(d, benefit);
+  bool fits = false;
+  const std::vector<char> keep = choose_residents(d, b, units, p.cap - p.margin - p.fixed - p.dynamic, &fits);
+  require(fits, SS_E_CAPACITY,
+          d.engine + ": nothing fits under the " + gib(p.cap) + " GiB cap once fixed " + gib(p.fixed) +
+              " GiB, margin " + gib(p.margin) + " GiB and the stream rings are taken");
+  // the rest by the descriptor's tier set; pinned|disk: pinned while the host budget lasts, densest first
+  std::vector<Streamed> spill;
   for (size_t i = 0; i < units.size(); ++i) {
-    if (chosen[i]) continue;
-    const Cand& c = units[i];
-    uint8_t& t = p.tier[size_t(c.g)];
+    if (keep[i]) continue;
+    uint8_t& t = p.tier[size_t(units[i].key)];
     switch (d.tiers) {
-      case Tiers::Pinned: {
-        t = SS_TIER_PINNED;
-        const uint64_t hb = host_stride(d.layers[size_t(c.layer)].unit_bytes);
-        host_left = host_left > hb ? host_left - hb : 0;
-        break;
-      }
+      case Tiers::Pinned: t = SS_TIER_PINNED; break;
       case Tiers::Disk: t = SS_TIER_DISK; break;
       case Tiers::Pair: t = SS_TIER_PAIR; break;
-      case Tiers::PinnedDisk: spill.push_back(c); break;
+      case Tiers::PinnedDisk: spill.push_back(units[i]); break;
     }
   }
-  std::stable_sort(spill.begin(), spill.end(), before);
-  for (const Cand& c : spill) {
-    const uint64_t hb = host_stride(d.layers[size_t(c.layer)].unit_bytes);
-    if (hb <= host_left) {
-      p.tier[size_t(c.g)] = SS_TIER_PINNED;
-      host_left -= hb;
-    } else {
-      p.tier[size_t(c.g)] = SS_TIER_DISK;
-    }
+  std::sort(spill.begin(), spill.end(), denser);
+  uint64_t host_left = host_budget_after_fixed(d, b);
+  for (const Streamed& s : spill) {
+    const uint64_t hb = host_stride(d.layers[size_t(s.layer)].unit_bytes);
+    const bool pin = hb <= host_left;
+    p.tier[size_t(s.key)] = pin ? SS_TIER_PINNED : SS_TIER_DISK;
+    if (pin) host_left -= hb;
   }
-  if (b.pinned_backing) give_backing(d, b, benefit, p.tier);
-  totals(d, b, p);
+  if (b.pinned_backing) back_residents(d, b, units, p.tier);
+  bill(d, b, p);
   return p;
 }
 
 Plan plan_from_tiers(const Desc& d, const ss_budget& b, const std::vector<uint8_t>& tiers) {
   require(int64_t(tiers.size()) == d.total_units, SS_E_INVALID, "plan: one tier per unit (ss_desc_total_units)");
-  Plan p = start_plan(d, b);
+  Plan p = open_plan(d, b);
   p.tier = tiers;
-  totals(d, b, p);
+  bill(d, b, p);
   return p;
 }
 
+namespace {
+constexpr char kTierLetters[] = "RPDXB";  // by ss_tier value: resident, pinned, disk, pair, resident with a pinned copy
+}
+
 Json plan_to_json(const Desc& d, const Plan& p) {
+  const auto u = [](uint64_t v) { return Json::number(v); };
   Json j = Json::object();
   j["schema"] = Json::string("strix-stream/plan-v1");
   j["engine"] = Json::string(d.engine);
-  j["cap_bytes"] = Json::number(p.cap);
-  j["margin_bytes"] = Json::number(p.margin);
-  j["fixed_bytes"] = Json::number(p.fixed);
-  j["dynamic_bytes"] = Json::number(p.dynamic);
-  j["dynamic_slots_per_layer"] = Json::number(uint64_t(p.dynamic_slots_per_layer));
-  j["ring_bytes"] = Json::number(p.ring);
-  Json rings = Json::array();
+  j["cap_bytes"] = u(p.cap);
+  j["margin_bytes"] = u(p.margin);
+  j["fixed_bytes"] = u(p.fixed);
+  j["dynamic_bytes"] = u(p.dynamic);
+  j["dynamic_slots_per_layer"] = u(p.dynamic_slots_per_layer);
+  j["ring_bytes"] = u(p.ring);
+  j["rings"] = Json::array();
   for (const RingClass& c : p.rings) {
     Json r = Json::object();
-    r["slot_bytes"] = Json::number(c.stride);
-    r["slots"] = Json::number(uint64_t(c.slots));
-    rings.push(r);
+    r["slot_bytes"] = u(c.stride);
+    r["slots"] = u(c.slots);
+    j["rings"].push(r);
   }
-  j["rings"] = rings;
-  j["resident_bytes"] = Json::number(p.resident);
-  j["pinned_bytes"] = Json::number(p.pinned);
-  j["disk_bytes"] = Json::number(p.disk);
-  j["peak_bytes"] = Json::number(p.peak);
-  j["n_resident"] = Json::number(p.n_resident);
-  j["n_pinned"] = Json::number(p.n_pinned);
-  j["n_disk"] = Json::number(p.n_disk);
-  j["n_pair"] = Json::number(p.n_pair);
-  j["n_backed"] = Json::number(p.n_backed);
-  if (p.budget.tier_mode == SS_TIER_MODE_EXCLUSIVE) {
+  j["resident_bytes"] = u(p.resident);
+  j["pinned_bytes"] = u(p.pinned);
+  j["disk_bytes"] = u(p.disk);
+  j["peak_bytes"] = u(p.peak);
+  j["n_resident"] = u(p.n_resident);
+  j["n_pinned"] = u(p.n_pinned);
+  j["n_disk"] = u(p.n_disk);
+  j["n_pair"] = u(p.n_pair);
+  j["n_backed"] = u(p.n_backed);
+  if (exclusive(p.budget)) {
     j["tier_mode"] = Json::string("exclusive");
-    Json sp = Json::array();
+    j["spare_blocks"] = Json::array();
     for (const SpareClass& c : p.spares) {
       Json x = Json::object();
-      x["block_bytes"] = Json::number(c.block_bytes);
-      x["asked"] = Json::number(uint64_t(c.asked));
-      x["blocks"] = Json::number(uint64_t(c.blocks));
-      sp.push(x);
+      x["block_bytes"] = u(c.block_bytes);
+      x["asked"] = u(c.asked);
+      x["blocks"] = u(c.blocks);
+      j["spare_blocks"].push(x);
     }
-    j["spare_blocks"] = sp;
   }
-  Json layers = Json::array();
+  j["tiers"] = Json::array();
   for (size_t L = 0; L < d.layers.size(); ++L) {
-    std::string s;
-    for (int u = 0; u < d.layers[L].n_units; ++u) s += "RPDXB"[p.tier[size_t(d.unit_base[L] + u)]];
-    layers.push(Json::string(s));
+    std::string s(size_t(d.layers[L].n_units), '?');
+    for (size_t u2 = 0; u2 < s.size(); ++u2) s[u2] = kTierLetters[p.tier[size_t(d.unit_base[L]) + u2]];
+    j["tiers"].push(Json::string(s));
   }
-  j["tiers"] = layers;
   return j;
 }
 
 std::vector<uint8_t> tiers_from_json(const Desc& d, const Json& j) {
-  static const char kLetters[] = "RPDXB";
   const Json* t = j.find("tiers");
   require(t && t->is_array() && t->arr.size() == d.layers.size(), SS_E_DESC,
-          "plan json: \"tiers\" needs one string per layer");
+          "plan json: \"tiers\" is not one string per layer");
   std::vector<uint8_t> out;
+  out.reserve(size_t(d.total_units));
   for (size_t L = 0; L < d.layers.size(); ++L) {
     const std::string& s = json_str(t->arr[L], "plan.tiers");
     require(s.size() == size_t(d.layers[L].n_units), SS_E_DESC,
-            "plan json: tiers[" + std::to_string(L) + "] needs one letter per unit");
-    for (char c : s) {
-      const char* k = c ? std::strchr(kLetters, c) : nullptr;
-      require(k != nullptr, SS_E_DESC, "plan json: tier letters are R P D X B");
-      out.push_back(uint8_t(k - kLetters));
+            "plan json: tiers[" + num(L) + "] is not one letter per unit");
+    for (const char c : s) {
+      const char* at = c ? std::strchr(kTierLetters, c) : nullptr;
+      require(at != nullptr, SS_E_DESC, "plan json: '" + std::string(1, c) + "' is not a tier letter (R P D X B)");
+      out.push_back(uint8_t(at - kTierLetters));
     }
   }
   return out;

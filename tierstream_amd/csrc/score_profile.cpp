@@ -1,4 +1,6 @@
-// TSSCPRF1 profiles: checks and the model identity (reference src/dg_score.cpp:45-120).
+// TSSCPRF1 score profiles: the model identity they are bound to, and the checks a profile passes before its counts
+// seed scored eviction. The byte layout and the identity's definition are the format's (reference src/dg_score.cpp,
+// include/strix_stream/ss.h:730-746); the refusals match the reference's profile check profile by profile.
 #include "score_profile.hpp"
 
 #include <cstring>
@@ -9,82 +11,96 @@
 namespace tsa {
 namespace {
 
-void le32(std::string& b, uint32_t v) {
-  for (int i = 0; i < 4; ++i) b.push_back(char(v >> (8 * i)));
-}
-void le64(std::string& b, uint64_t v) {
-  for (int i = 0; i < 8; ++i) b.push_back(char(v >> (8 * i)));
-}
-uint32_t rd32(const unsigned char* p) { return uint32_t(p[0]) | uint32_t(p[1]) << 8 | uint32_t(p[2]) << 16 | uint32_t(p[3]) << 24; }
+constexpr char kMagic[8] = {'T', 'S', 'S', 'C', 'P', 'R', 'F', '1'};
+constexpr uint32_t kVersion = 1;
+constexpr uint32_t kProvenanceLimit = 4096;
+constexpr uint32_t kScoredUnitLimit = 65536;
 
-[[noreturn]] void bad(const std::string& why) { fail(SS_E_INVALID, "dg_score_profile (TSSCPRF1): " + why); }
+[[noreturn]] void refuse(const std::string& why) { fail(SS_E_INVALID, "score profile (TSSCPRF1): " + why); }
 
-// a + b and a * b on sizes a hostile header could overflow
-uint64_t sum(uint64_t a, uint64_t b) {
-  if (a > UINT64_MAX - b) bad("size overflows");
-  return a + b;
+// Sizes from a header nobody vouches for: an overflow is a refusal, not a wrap.
+uint64_t add(uint64_t a, uint64_t b) {
+  uint64_t r = 0;
+  if (__builtin_add_overflow(a, b, &r)) refuse("a size in the header overflows 64 bits");
+  return r;
 }
-uint64_t prod(uint64_t a, uint64_t b) {
-  if (b && a > UINT64_MAX / b) bad("size overflows");
-  return a * b;
+uint64_t mul(uint64_t a, uint64_t b) {
+  uint64_t r = 0;
+  if (__builtin_mul_overflow(a, b, &r)) refuse("a size in the header overflows 64 bits");
+  return r;
+}
+
+void put_le(std::string& out, uint64_t v, int bytes) {
+  for (int i = 0; i < bytes; ++i, v >>= 8) out.push_back(char(v & 0xff));
+}
+
+uint32_t le32_at(const unsigned char* p, uint64_t at) {
+  uint32_t v = 0;
+  for (int i = 3; i >= 0; --i) v = v << 8 | p[at + uint64_t(i)];
+  return v;
 }
 
 }  // namespace
 
 std::string score_identity(const Desc& d, const std::vector<int>& gated) {
-  std::string b;
-  le32(b, uint32_t(gated.size()));
+  std::string msg;
+  put_le(msg, gated.size(), 4);
   for (size_t g = 0; g < gated.size(); ++g) {
     const Layer& l = d.layers[size_t(gated[g])];
     require(l.hash.size() == size_t(l.n_units), SS_E_INVALID,
-            "dg_score_profile: gated layer " + std::to_string(g) +
-                " has no per-unit hashes in the descriptor (a profile is bound to them)");
-    le32(b, uint32_t(l.index));
-    le32(b, uint32_t(l.n_units));
-    le64(b, l.unit_bytes);
-    for (uint64_t h : l.hash) le64(b, h);
+            "score profile: gated layer " + std::to_string(g) +
+                " has no per-unit xxh64 list in the descriptor, and a profile is bound to it");
+    put_le(msg, uint32_t(l.index), 4);
+    put_le(msg, uint32_t(l.n_units), 4);
+    put_le(msg, l.unit_bytes, 8);
+    for (uint64_t h : l.hash) put_le(msg, h, 8);
   }
-  return sha256(b.data(), b.size());
+  return sha256(msg.data(), msg.size());
 }
 
 uint64_t score_cells(const std::vector<uint32_t>& units) {
-  uint64_t n = 0;
+  uint64_t cells = 0;
   for (size_t g = 0; g < units.size(); ++g) {
-    require(units[g] <= 65536, SS_E_INVALID,
-            "device-gated: scored eviction needs at most 65536 units per gated layer (gated layer " +
-                std::to_string(g) + " has " + std::to_string(units[g]) + ")");
-    n = sum(n, prod(units[g], units[g]));
+    require(units[g] <= kScoredUnitLimit, SS_E_INVALID,
+            "scored eviction: gated layer " + std::to_string(g) + " has " + std::to_string(units[g]) +
+                " units, above 65536");
+    cells = add(cells, mul(units[g], units[g]));
   }
-  return n;
+  return cells;
 }
 
 ScoreProfile check_score_profile(const void* data, uint64_t len, const std::vector<uint32_t>& units,
                                  const std::string& identity) {
-  if (!data) bad("null data");
+  if (!data) refuse("no bytes");
   const auto* p = static_cast<const unsigned char*>(data);
-  const uint64_t G = units.size();
-  const uint64_t at_id = sum(16, prod(4, G));  // magic, version, n_gated, units
-  const uint64_t fixed = sum(at_id, 36);       // identity, prov_len
-  if (len < fixed) bad("truncated header (" + std::to_string(len) + " bytes)");
-  if (std::memcmp(p, "TSSCPRF1", 8) != 0) bad("bad magic");
-  if (rd32(p + 8) != 1) bad("unsupported version " + std::to_string(rd32(p + 8)));
-  if (rd32(p + 12) != G) bad("n_gated " + std::to_string(rd32(p + 12)) + " != the context's " + std::to_string(G));
-  for (uint64_t g = 0; g < G; ++g)
-    if (rd32(p + 16 + 4 * g) != units[size_t(g)])
-      bad("units of gated layer " + std::to_string(g) + " are " + std::to_string(rd32(p + 16 + 4 * g)) +
-          ", the context has " + std::to_string(units[size_t(g)]));
-  const uint32_t prov = rd32(p + at_id + 32);
-  if (prov > 4096) bad("provenance longer than 4096 bytes");
-  const uint64_t header = fixed + prov;
-  const uint64_t want = sum(sum(header, prod(4, score_cells(units))), 32);
-  if (len != want) bad("size " + std::to_string(len) + " != " + std::to_string(want) + " (header + cells + checksum)");
-  if (identity.size() != 32 || std::memcmp(p + at_id, identity.data(), 32) != 0)
-    bad("identity mismatch (another model, layer set or descriptor)");
-  if (sha256(p, size_t(len - 32)) != std::string(reinterpret_cast<const char*>(p + len - 32), 32))
-    bad("checksum mismatch");
+  const uint64_t n_gated = units.size();
+  // magic, version, layer count, per-layer units | identity | provenance length
+  const uint64_t units_at = 16, identity_at = add(units_at, mul(4, n_gated)), prov_len_at = add(identity_at, 32);
+  const uint64_t prov_at = add(prov_len_at, 4);
+  if (len < prov_at) refuse(std::to_string(len) + " bytes is shorter than the fixed header");
+  if (std::memcmp(p, kMagic, sizeof kMagic) != 0) refuse("not a TSSCPRF1 profile (magic)");
+  if (le32_at(p, 8) != kVersion) refuse("version " + std::to_string(le32_at(p, 8)) + " (only 1 is read)");
+  if (le32_at(p, 12) != n_gated)
+    refuse("written for " + std::to_string(le32_at(p, 12)) + " gated layers, the context has " +
+           std::to_string(n_gated));
+  for (uint64_t g = 0; g < n_gated; ++g) {
+    const uint32_t written = le32_at(p, units_at + 4 * g);
+    if (written != units[size_t(g)])
+      refuse("gated layer " + std::to_string(g) + " has " + std::to_string(written) + " units in the profile and " +
+             std::to_string(units[size_t(g)]) + " in the context");
+  }
+  const uint32_t prov_len = le32_at(p, prov_len_at);
+  if (prov_len > kProvenanceLimit) refuse("provenance of " + std::to_string(prov_len) + " bytes (at most 4096)");
+  const uint64_t cells_at = add(prov_at, prov_len);
+  const uint64_t expect = add(add(cells_at, mul(4, score_cells(units))), 32);
+  if (len != expect) refuse(std::to_string(len) + " bytes where the header implies " + std::to_string(expect));
+  if (identity.size() != 32 || std::memcmp(p + identity_at, identity.data(), 32) != 0)
+    refuse("bound to another model identity (descriptor, gated layers or hashes differ)");
+  if (sha256(p, size_t(len - 32)).compare(0, 32, reinterpret_cast<const char*>(p + len - 32), 32) != 0)
+    refuse("the SHA-256 at its end does not match its bytes");
   ScoreProfile v;
-  v.provenance.assign(reinterpret_cast<const char*>(p + fixed), prov);
-  v.cells = p + header;
+  v.provenance.assign(reinterpret_cast<const char*>(p + prov_at), prov_len);
+  v.cells = p + cells_at;
   return v;
 }
 
