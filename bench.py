@@ -51,6 +51,11 @@ TICK_NS = 10.0  # wall_clock64 runs at 100 MHz on gfx950
 # counter's reading for a copy kernel of known size (FETCH 2.0, WRITE 1.0): 347,205 KiB fetched, nothing written
 # (profiles/dg_verify_kernel_mixtral_unit_pmc.md).
 VERIFY_TRAFFIC_PER_UNIT = {352321536: 347205 * 1024}
+# The host contract's verify_kernel: HBM bytes fetched per algorithmic byte hashed, keyed by unit bytes, from
+# rocprofv3 --pmc FETCH_SIZE over the bench's own timed steps (scaled as above): a full batch of 32 units fetches
+# 148,799.25 KiB x 2.0 = 304,740,864 B for 301,989,888 B of units, nothing written
+# (profiles/verify_kernel_qwen3_host_pmc.md).
+HOST_VERIFY_TRAFFIC_RATIO: dict[int, float] = {9437184: 304740864 / 301989888}
 
 
 def log(*a):
@@ -289,18 +294,18 @@ def measure_kernels(tsa, L, C, w, seg=8192, reps=10):
 
 # ---- the CPU baseline -----------------------------------------------------------------------------------------------
 def cpu_baseline(w, shape, files, hashes, routes, start, est_token_s, seconds, policy=0):
-    """The reference DgCore on a memcpy transport (oracle/_ref), over tokens start.. of the same route stream, under
-    the same eviction policy (0 LRU, 1 SCORED, 2 SCORED_AUTO). files: [(path, first layer, layers)] as the
-    descriptor's sources."""
+    """The reference DgCore on a memcpy transport (oracle/_ref), under the same eviction policy (0 LRU, 1 SCORED,
+    2 SCORED_AUTO): tokens 0..start-1 of the same route stream replayed untimed (the warmup: the timed tokens start
+    from the placement the device's timed tokens start from), then tokens start.. timed. files: [(path, first layer,
+    layers)] as the descriptor's sources."""
     try:
         from oracle import ref
     except Exception as e:  # noqa: BLE001
         return None, f"oracle unavailable: {e}"
     if not ref.available():
         return None, "oracle/_ref is not built"
-    ref.lib().refdg_cpu_baseline_policy(policy)
     from tierstream_amd import workloads as W
-    n_tok = int(max(3, min(64, seconds / max(est_token_s, 1e-3))))
+    n_tok = int(max(16, min(256, seconds / max(est_token_s, 1e-3))))
     n_tok = min(n_tok, routes.shape[0] - start)
     keys = w.n_units
     residents = list(range(shape.R))
@@ -311,19 +316,21 @@ def cpu_baseline(w, shape, files, hashes, routes, start, est_token_s, seconds, p
             for u in range(w.units):
                 path_of.append(i)
                 offsets.append(W.unit_offset(w, L, u, first))
-    ids = routes[start:start + n_tok].astype(np.uint32)
+    ids = routes[:start + n_tok].astype(np.uint32)
     hs = (w.unit_bytes + 4095) // 4096 * 4096
     t0 = time.time()
     if shape.F:
         flags = [1 if t == 2 else 0 for t in shape.tiers]
         ms, c = ref.cpu_baseline_disk([w.units] * w.layers, shape.R + shape.D, shape.B, shape.P + shape.Q, shape.D,
                                       w.parts, hs, order, [f[0] for f in files], path_of, offsets, hashes, ids, flags,
-                                      shape.P, 8, clean_evict=w.clean_evict, setup_threads=16)
+                                      shape.P, 8, clean_evict=w.clean_evict, setup_threads=16, warm=start,
+                                      policy=policy)
     else:
         ms, c = ref.cpu_baseline([w.units] * w.layers, shape.R + shape.D, shape.B, shape.P + shape.Q, shape.D, w.parts,
                                  hs, order, files[0][0], offsets, hashes, ids, wb_defer=1, inclusive=shape.I,
-                                 setup_threads=16)
-    log(f"cpu baseline: {n_tok} tokens in {time.time() - t0:.1f} s (setup included), counters {c}")
+                                 setup_threads=16, warm=start, policy=policy)
+    log(f"cpu baseline: {start} warmup + {n_tok} timed tokens in {time.time() - t0:.1f} s (setup included), "
+        f"counters {c}")
     return (ms, c, n_tok), None
 
 
@@ -507,6 +514,9 @@ def main():
                                    + (f"; {w.layers} of the full model's {W.WORKLOADS[w.name].layers} layers"
                                       if w.layers != W.WORKLOADS[w.name].layers else ""),
                        "policy": a.policy,
+                       "residency": f"{n_res} of {w.n_units} units resident ({100 * n_res / w.n_units:.0f} %); device "
+                                    f"arena {shape.R + shape.D + 2 * shape.B + 1} of {w.n_units} unit slots (residents "
+                                    f"R {shape.R} + spares D {shape.D} + two banks of {shape.B} + the guard slot)",
                        "layers": w.layers, "experts": w.units, "top_k": w.top_k, "unit_bytes": w.unit_bytes,
                        "resident_units": n_res, "pinned_units": n_pin, "file_units": n_file,
                        "spare_slots": shape.D, "spare_blocks": shape.Q, "inclusive_blocks": shape.I,
@@ -579,8 +589,10 @@ def main():
                     "value": round(pct(ms, 50), 3), "unit": "ms", "cores": 1, "kind": "reference",
                     "p99_ms": round(pct(ms, 99), 3), "mean_ms": round(float(np.mean(ms)), 3),
                     "copy_GBps": round(c["copied_bytes"] / (float(np.sum(ms)) / 1e3) / 1e9, 2),
-                    "sample": f"tokens {warm}..{warm + n_tok - 1} of the same route stream from the open-time "
-                              f"placement: reference DgCore + memcpy transport + host XXH64 of each landed unit"
+                    "sample": f"tokens {warm}..{warm + n_tok - 1} of the same route stream, after tokens 0..{warm - 1} "
+                              f"replayed untimed from the open-time placement (so the timed tokens start from the "
+                              f"placement the GPU's timed tokens start from): reference DgCore + memcpy transport + "
+                              f"host XXH64 of each landed unit"
                               + (", file-tier units read synchronously with direct I/O into staging buffers"
                                  if three else "")
                               + f", 1 thread, policy {a.policy}; misses {c['misses']}, hash mismatches "
@@ -633,11 +645,13 @@ def run_host(a, w, tsa, ss, W, L, C):
         ctx.host_run(routes[:warm], shape.mode, want_tables=False)
         s0 = ctx.stats_total()
         x0 = ctx.exclusive_stats() if w.tier_mode == 1 else None
+        ctx.profile_enable(ctx.PROF_VERIFY)  # each check launch bracketed by its dispatch's own begin and end stamps
         tsa.check(L.tsa_device_sync())
         t_start = time.perf_counter()
         cks, _, stats, lat = ctx.host_run(routes[warm:warm + steps], shape.mode, want_tables=False)
         tsa.check(L.tsa_device_sync())
         wall = time.perf_counter() - t_start
+        prof = ctx.profile_read(wait=True)
         s1 = ctx.stats_total()
         x1 = ctx.exclusive_stats() if w.tier_mode == 1 else None
         seen, bad = {}, 0
@@ -673,7 +687,7 @@ def run_host(a, w, tsa, ss, W, L, C):
             "h2d": {"bytes_per_step": h2d_bytes // steps, "wall_GBps": round(h2d_bytes / wall / 1e9, 2),
                     "pinned_peak_GBps": round(peaks["h2d_pinned_GBps"], 2),
                     "frac_of_pinned_peak_wall": round(h2d_bytes / wall / 1e9 / peaks["h2d_pinned_GBps"], 3)},
-            "roofline": None,
+            "roofline": host_roofline(prof, w),
             "kernels": kern,
             "stats": dst,
             "exclusive": {k: x1[k] - x0[k] for k in x1} if x1 else None,
@@ -702,6 +716,23 @@ def run_host(a, w, tsa, ss, W, L, C):
             h.close()
         shutil.rmtree(work, ignore_errors=True)
     print(json.dumps(result), flush=True)
+
+
+def host_roofline(prof, w):
+    """The host contract's dominant kernel: verify_kernel, the device XXH64 of each batch of landed units (up to 32 per
+    launch), live over the timed steps."""
+    if not prof["verifies"] or not prof["verify_ns"]:
+        return None
+    gbps = prof["verify_bytes"] / prof["verify_ns"]
+    per_launch = prof["verify_bytes"] / prof["verifies"]
+    ratio = HOST_VERIFY_TRAFFIC_RATIO.get(w.unit_bytes)
+    return {"bound": "hbm", "kernel": "verify_kernel (device XXH64 of each batch of landed units)",
+            "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "traffic": int(ratio * per_launch) if ratio else None,
+            "launches": prof["verifies"], "units": prof["verify_units"], "bytes_per_launch": int(per_launch),
+            "mean_launch_us": round(prof["verify_ns"] / prof["verifies"] / 1e3, 2),
+            "note": "live: each launch checks a batch of landed units behind both copy streams while the engine reads "
+                    "resident and landed units; bracketed by the dispatch's own begin and end stamps"}
 
 
 def cpu_model():

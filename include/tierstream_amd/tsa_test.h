@@ -39,7 +39,8 @@ typedef struct tsa_test_profile {
 } tsa_test_profile;
 /* on: a mask of what is bracketed, TSA_TEST_PROF_COPY | _WRITEBACK | _VERIFY (0: nothing); 1 keeps its older meaning
  * of everything. The verify launches take the dispatch's own begin and end stamps (no extra stream work); a copy
- * bracket records two events on the copy's stream. */
+ * bracket records two events on the copy's stream. A host-contract context brackets its check launches only
+ * (TSA_TEST_PROF_VERIFY; between forwards); a device-gated one every kind (between tokens). */
 #define TSA_TEST_PROF_COPY 0x2
 #define TSA_TEST_PROF_WRITEBACK 0x4
 #define TSA_TEST_PROF_VERIFY 0x8

@@ -73,7 +73,6 @@ def lib() -> C.CDLL:
             "refdg_set_policy": (C.c_int, [vp, u32]),
             "refdg_set_keep": (C.c_int, [vp, C.POINTER(u32), u32]),
             "refdg_set_wb_defer": (C.c_int, [vp, u32]),
-            "refdg_cpu_baseline_policy": (None, [u32]),
             "refdg_profile_check": (C.c_int, [C.c_char_p, u64, C.POINTER(u32), u32, C.c_char_p]),
             "refdg_score_identity": (C.c_int, [u32, C.POINTER(u32), C.POINTER(u32), C.POINTER(u64), C.POINTER(u64),
                                                C.c_char_p]),
@@ -82,12 +81,12 @@ def lib() -> C.CDLL:
             "refdg_cpu_baseline": (C.c_int, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, C.POINTER(u64), u32,
                                               u64, C.POINTER(u32), u32, C.c_char_p, C.POINTER(u64), C.POINTER(u64),
                                               C.POINTER(u32), u32, u32, C.c_int, C.POINTER(C.c_double),
-                                              C.POINTER(u64)]),
+                                              C.POINTER(u64), u32, u32]),
             "refdg_cpu_baseline_disk": (C.c_int, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, C.POINTER(u64),
                                                    u32, u64, C.POINTER(u32), u32, C.POINTER(C.c_char_p), u32,
                                                    C.POINTER(u32), C.POINTER(u64), C.POINTER(u64), C.POINTER(u32), u32,
                                                    u32, C.c_int, C.POINTER(C.c_uint8), u32, u32, u32,
-                                                   C.POINTER(C.c_double), C.POINTER(u64)]),
+                                                   C.POINTER(C.c_double), C.POINTER(u64), u32, u32]),
         }
         for name, (res, args) in sigs.items():
             f = getattr(L, name)
@@ -322,9 +321,10 @@ class RefDg:
 
 
 def cpu_baseline(n_units, persistent, bank, blocks, spare_target, part_bytes, host_stride, order, path, unit_offsets,
-                 hashes, ids: np.ndarray, wb_defer=1, inclusive=0, setup_threads=16):
+                 hashes, ids: np.ndarray, wb_defer=1, inclusive=0, setup_threads=16, warm=0, policy=0):
     """The reference DgCore on a synchronous memcpy transport over host memory (refdg_cpu_baseline), timed per token
-    on the calling thread. ids uint32 [tokens][G][n]. Returns (token_ms [tokens], counters dict)."""
+    on the calling thread. ids uint32 [warm + tokens][G][n]: the first `warm` tokens run untimed. policy: 0 LRU,
+    1 SCORED, 2 SCORED_AUTO. Returns (token_ms [tokens], counters dict over the timed tokens)."""
     L = lib()
     x = np.ascontiguousarray(ids, dtype=np.uint32)
     tokens, G, n = x.shape
@@ -333,22 +333,27 @@ def cpu_baseline(n_units, persistent, bank, blocks, spare_target, part_bytes, ho
     od = (u32 * len(order))(*order)
     offs = np.ascontiguousarray(unit_offsets, dtype=np.uint64)
     hs = np.ascontiguousarray(hashes, dtype=np.uint64)
-    ms = np.zeros(tokens, dtype=np.float64)
-    out = np.zeros(6, dtype=np.uint64)
+    assert 0 <= warm < tokens, "refdg_cpu_baseline: needs at least one timed token after the warmup"
+    ms = np.zeros(tokens - warm, dtype=np.float64)
+    out = np.zeros(len(BASELINE_COUNTERS), dtype=np.uint64)
     st = L.refdg_cpu_baseline(nu, G, persistent, bank, blocks, spare_target, wb_defer, inclusive, pb, len(part_bytes),
                               host_stride, od, len(order), str(path).encode(), offs.ctypes.data_as(C.POINTER(u64)),
-                              hs.ctypes.data_as(C.POINTER(u64)), x.ctypes.data_as(C.POINTER(u32)), n, tokens,
+                              hs.ctypes.data_as(C.POINTER(u64)), x.ctypes.data_as(C.POINTER(u32)), n, tokens - warm,
                               setup_threads, ms.ctypes.data_as(C.POINTER(C.c_double)),
-                              out.ctypes.data_as(C.POINTER(u64)))
+                              out.ctypes.data_as(C.POINTER(u64)), warm, policy)
     if st != 0:
         raise RuntimeError("refdg_cpu_baseline failed")
-    names = ["misses", "fetched", "evicted", "writebacks_done", "hash_mismatches", "copied_bytes"]
-    return ms, {k: int(v) for k, v in zip(names, out)}
+    return ms, {k: int(v) for k, v in zip(BASELINE_COUNTERS, out)}
+
+
+# The counters refdg_cpu_baseline* report over their timed tokens, in order.
+BASELINE_COUNTERS = ["misses", "fetched", "evicted", "writebacks_done", "hash_mismatches", "copied_bytes", "disk_reads",
+                     "disk_drops", "score_layers", "score_candidates"]
 
 
 def cpu_baseline_disk(n_units, persistent, bank, blocks, spare_target, part_bytes, host_stride, order, paths, path_of,
                       unit_offsets, hashes, ids: np.ndarray, disk_flags, home_blocks, disk_staging, clean_evict=0,
-                      wb_defer=1, setup_threads=16):
+                      wb_defer=1, setup_threads=16, warm=0, policy=0):
     """Three tiers (refdg_cpu_baseline_disk): key k's bytes in paths[path_of[k]] at unit_offsets[k]; the file-tier keys
     (disk_flags) are read synchronously into a staging buffer on a miss (direct I/O where the file system allows it).
     Returns (token_ms [tokens], counters dict)."""
@@ -363,19 +368,19 @@ def cpu_baseline_disk(n_units, persistent, bank, blocks, spare_target, part_byte
     offs = np.ascontiguousarray(unit_offsets, dtype=np.uint64)
     hs = np.ascontiguousarray(hashes, dtype=np.uint64)
     fl = np.ascontiguousarray(disk_flags, dtype=np.uint8)
-    ms = np.zeros(tokens, dtype=np.float64)
-    out = np.zeros(8, dtype=np.uint64)
+    assert 0 <= warm < tokens, "refdg_cpu_baseline_disk: needs at least one timed token after the warmup"
+    ms = np.zeros(tokens - warm, dtype=np.float64)
+    out = np.zeros(len(BASELINE_COUNTERS), dtype=np.uint64)
     st = L.refdg_cpu_baseline_disk(nu, G, persistent, bank, blocks, spare_target, wb_defer, 0, pb, len(part_bytes),
                                    host_stride, od, len(order), pa, len(paths), po.ctypes.data_as(C.POINTER(u32)),
                                    offs.ctypes.data_as(C.POINTER(u64)), hs.ctypes.data_as(C.POINTER(u64)),
-                                   x.ctypes.data_as(C.POINTER(u32)), n, tokens, setup_threads,
+                                   x.ctypes.data_as(C.POINTER(u32)), n, tokens - warm, setup_threads,
                                    fl.ctypes.data_as(C.POINTER(C.c_uint8)), home_blocks, disk_staging, clean_evict,
-                                   ms.ctypes.data_as(C.POINTER(C.c_double)), out.ctypes.data_as(C.POINTER(u64)))
+                                   ms.ctypes.data_as(C.POINTER(C.c_double)), out.ctypes.data_as(C.POINTER(u64)), warm,
+                                   policy)
     if st != 0:
         raise RuntimeError("refdg_cpu_baseline_disk failed")
-    names = ["misses", "fetched", "evicted", "writebacks_done", "hash_mismatches", "copied_bytes", "disk_reads",
-             "disk_drops"]
-    return ms, {k: int(v) for k, v in zip(names, out)}
+    return ms, {k: int(v) for k, v in zip(BASELINE_COUNTERS, out)}
 
 
 def host_exclusive(desc_json: str, budget, options, routes: np.ndarray) -> dict:

@@ -529,38 +529,39 @@ void parallel_for(uint32_t n, int threads, F work) {
 
 extern "C" {
 
-// The CPU baseline over `n_tokens` tokens of ids [n_tokens][G][n]: the same placement as refdg_open, then per token
-// begin_token, per gated layer the export mask, serve_demand (synchronous memcpy of every miss), a host XXH64 of every
-// landed unit against hashes[key], serve_use, issue_writebacks, and end_token, on the calling thread. The source file
-// holds unit `key` at unit_offset[key] (unit bytes contiguous). token_ms[t] = the token's wall time; out[] = misses,
-// fetched, evicted, writebacks_done, hash mismatches, bytes copied into slots (sums over the timed tokens).
+// The CPU baseline over n_warm + n_tokens tokens of ids [n_warm + n_tokens][G][n]: the same placement as refdg_open,
+// then per token begin_token, per gated layer the export mask, serve_demand (synchronous memcpy of every miss), a host
+// XXH64 of every landed unit against hashes[key], serve_use, issue_writebacks and score_layer (the reference service's
+// close of each exported layer, the last one included), and end_token, on the calling thread. The first n_warm tokens
+// run untimed (the placement the timed tokens start from is the one after warmup, as on the device); token_ms[t] = the
+// wall time of timed token t. policy: 0 LRU, 1 SCORED, 2 SCORED_AUTO (weights 700 / 200 / 100, no profile). The
+// source file holds unit `key` at unit_offset[key] (unit bytes contiguous). out[10], sums over the timed tokens:
+// misses, fetched, evicted, writebacks_done, hash mismatches, bytes copied into slots, file reads, drops of pinned
+// units to their file, score_layers, score_candidates.
 // Three-tier variant: n_paths source files, key k in paths[path_of[k]] at unit_offset[k]; disk[k] = 1 for the
 // file-tier keys, home_blocks = the pinned homes, disk_staging buffers; reads are synchronous (one at a time inside
-// their fetch: dg_disk_queue 1). out[6] = file reads, out[7] = drops of pinned units to their file.
+// their fetch: dg_disk_queue 1).
 int refdg_cpu_baseline_disk(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
                             uint32_t spare_target, uint32_t wb_defer, uint32_t inclusive, const uint64_t* part_bytes,
                             uint32_t n_parts, uint64_t host_stride, const uint32_t* order, uint32_t n_order,
                             const char* const* paths, uint32_t n_paths, const uint32_t* path_of,
                             const uint64_t* unit_offset, const uint64_t* hashes, const uint32_t* ids, uint32_t n,
                             uint32_t n_tokens, int setup_threads, const uint8_t* disk, uint32_t home_blocks,
-                            uint32_t disk_staging, uint32_t clean_evict, double* token_ms, uint64_t* out);
-
-// The eviction policy of the next refdg_cpu_baseline* runs: 0 LRU, 1 SCORED, 2 SCORED_AUTO (the weights 700 / 200 /
-// 100, no profile; each layer closed after its service as the reference service closes it).
-static uint32_t g_baseline_policy = 0;
-void refdg_cpu_baseline_policy(uint32_t policy) { g_baseline_policy = policy; }
+                            uint32_t disk_staging, uint32_t clean_evict, double* token_ms, uint64_t* out,
+                            uint32_t n_warm, uint32_t policy);
 
 int refdg_cpu_baseline(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
                        uint32_t spare_target, uint32_t wb_defer, uint32_t inclusive, const uint64_t* part_bytes,
                        uint32_t n_parts, uint64_t host_stride, const uint32_t* order, uint32_t n_order,
                        const char* path, const uint64_t* unit_offset, const uint64_t* hashes, const uint32_t* ids,
-                       uint32_t n, uint32_t n_tokens, int setup_threads, double* token_ms, uint64_t* out) {
+                       uint32_t n, uint32_t n_tokens, int setup_threads, double* token_ms, uint64_t* out,
+                       uint32_t n_warm, uint32_t policy) {
   uint32_t keys = 0;
   for (uint32_t g = 0; g < G; ++g) keys += n_units[g];
   const std::vector<uint32_t> path_of(keys, 0);
   return refdg_cpu_baseline_disk(n_units, G, persistent, bank, blocks, spare_target, wb_defer, inclusive, part_bytes,
                                  n_parts, host_stride, order, n_order, &path, 1, path_of.data(), unit_offset, hashes,
-                                 ids, n, n_tokens, setup_threads, nullptr, 0, 0, 0, token_ms, out);
+                                 ids, n, n_tokens, setup_threads, nullptr, 0, 0, 0, token_ms, out, n_warm, policy);
 }
 
 int refdg_cpu_baseline_disk(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
@@ -569,7 +570,8 @@ int refdg_cpu_baseline_disk(const uint32_t* n_units, uint32_t G, uint32_t persis
                             const char* const* paths, uint32_t n_paths, const uint32_t* path_of,
                             const uint64_t* unit_offset, const uint64_t* hashes, const uint32_t* ids, uint32_t n,
                             uint32_t n_tokens, int setup_threads, const uint8_t* disk, uint32_t home_blocks,
-                            uint32_t disk_staging, uint32_t clean_evict, double* token_ms, uint64_t* out) {
+                            uint32_t disk_staging, uint32_t clean_evict, double* token_ms, uint64_t* out,
+                            uint32_t n_warm, uint32_t policy) {
   std::vector<int> fds, dfds;
   auto close_all = [&] {
     for (int f : fds) ::close(f);
@@ -617,9 +619,9 @@ int refdg_cpu_baseline_disk(const uint32_t* n_units, uint32_t G, uint32_t persis
     c.inclusive = inclusive;
     c.max_ids = bank;
     c.pf_legacy = true;
-    if (g_baseline_policy) {
+    if (policy) {
       c.scored = true;
-      c.scored_auto = g_baseline_policy == 2;
+      c.scored_auto = policy == 2;
       c.boundary_score = true;
     }
     uint32_t n_keys = 0;
@@ -670,10 +672,14 @@ int refdg_cpu_baseline_disk(const uint32_t* n_units, uint32_t G, uint32_t persis
     parallel_for(all_blocks + 1, setup_threads, [&](uint32_t b) {
       if (!used_block[b]) std::memset(t.block(int32_t(b) - 1), 0, host_stride);
     });
-    // the timed tokens
-    const ts::DgStats s0 = core.stats();
+    // the warmup tokens (untimed), then the timed ones
+    ts::DgStats s0 = core.stats();
     uint64_t bad = 0, copied = 0;
-    for (uint32_t tok = 0; tok < n_tokens; ++tok) {
+    for (uint32_t tok = 0; tok < n_warm + n_tokens; ++tok) {
+      if (tok == n_warm) {
+        s0 = core.stats();
+        bad = copied = 0;
+      }
       const auto t0 = std::chrono::steady_clock::now();
       core.begin_token(tok + 1);
       for (uint32_t g = 0; g < G; ++g) {
@@ -696,7 +702,8 @@ int refdg_cpu_baseline_disk(const uint32_t* n_units, uint32_t G, uint32_t persis
         core.score_layer(g);  // (nothing under LRU)
       }
       core.end_token({}, 1);
-      token_ms[tok] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+      if (tok >= n_warm)
+        token_ms[tok - n_warm] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     }
     const ts::DgStats& s1 = core.stats();
     out[0] = s1.misses - s0.misses;
@@ -705,10 +712,10 @@ int refdg_cpu_baseline_disk(const uint32_t* n_units, uint32_t G, uint32_t persis
     out[3] = s1.writebacks_done - s0.writebacks_done;
     out[4] = bad;
     out[5] = copied;
-    if (disk) {
-      out[6] = s1.disk_reads - s0.disk_reads;
-      out[7] = s1.disk_drops - s0.disk_drops;
-    }
+    out[6] = s1.disk_reads - s0.disk_reads;
+    out[7] = s1.disk_drops - s0.disk_drops;
+    out[8] = s1.score_layers - s0.score_layers;
+    out[9] = s1.score_candidates - s0.score_candidates;
     close_all();
     return 0;
   } catch (const std::exception& e) {

@@ -25,14 +25,11 @@ def test_cpu_baseline_moves_the_right_bytes(tmp_path, wb_defer, inclusive, polic
     ids = np.stack([np.stack([rng.choice(units, size=n_ids, replace=False) for _ in range(layers)])
                     for _ in range(tokens)]).astype(np.uint32)
     offsets = [g * m.stride for g in range(keys)]
-    ref.lib().refdg_cpu_baseline_policy(policy)  # (SCORED: the benchmark's --policy scored baseline)
-    try:
-        ms, got = ref.cpu_baseline([units] * layers, len(residents) + D, n_ids, P + Q, D, parts, m.stride, order,
-                                   m.path, offsets, m.hashes, ids, wb_defer=wb_defer, inclusive=inclusive,
-                                   setup_threads=2)
-    finally:
-        ref.lib().refdg_cpu_baseline_policy(0)
-    assert ms.shape == (tokens,) and np.all(ms > 0)
+    warm = 5  # replayed untimed: the timed tokens start from the placement after them
+    ms, got = ref.cpu_baseline([units] * layers, len(residents) + D, n_ids, P + Q, D, parts, m.stride, order, m.path,
+                               offsets, m.hashes, ids, wb_defer=wb_defer, inclusive=inclusive, setup_threads=2,
+                               warm=warm, policy=policy)
+    assert ms.shape == (tokens - warm,) and np.all(ms > 0)
     assert got["hash_mismatches"] == 0
     assert got["misses"] > 0 and got["evicted"] > 0
     assert got["copied_bytes"] == got["misses"] * m.unit_bytes
@@ -41,12 +38,15 @@ def test_cpu_baseline_moves_the_right_bytes(tmp_path, wb_defer, inclusive, polic
     try:
         for t in range(tokens):
             _, want = eager.token(ids[t])
+            if t == warm - 1:
+                before = dict(want)
     finally:
         eager.close()
-    for k in ("misses", "fetched", "evicted", "writebacks_done"):
-        assert got[k] == want[k], k
+    # the eager core's counters over the same timed tokens (after the same warmup)
+    for k in ("misses", "fetched", "evicted", "writebacks_done", "score_layers", "score_candidates"):
+        assert got[k] == want[k] - before[k], k
     if policy:
-        assert want["scored_victims"] > 0
+        assert want["scored_victims"] > 0 and got["score_layers"] > 0 and got["score_candidates"] > 0
     if inclusive == 0:
         assert got["writebacks_done"] > 0                # exclusive: evictions write units back, and they re-land intact
 

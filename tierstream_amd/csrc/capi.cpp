@@ -523,13 +523,14 @@ ss_status tsa_test_profile_enable(ss_ctx* c, int on) {
     need(c != nullptr, "tsa_test_profile_enable: null context");
     need(on >= 0 && on <= (TSA_TEST_PROF_COPY | TSA_TEST_PROF_WRITEBACK | TSA_TEST_PROF_VERIFY),
          "tsa_test_profile_enable: on is 0, 1 or a mask of TSA_TEST_PROF_*");
-    dg_of(c, "tsa_test_profile_enable").profile_enable(on);
+    if (c->dg) c->dg->profile_enable(on);
+    else c->host->profile_enable(on);
   });
 }
 ss_status tsa_test_profile_read(ss_ctx* c, int wait, tsa_test_profile* out) {
   return guard([&] {
     need(c && out, "tsa_test_profile_read: null argument");
-    *out = dg_of(c, "tsa_test_profile_read").profile_read(wait != 0);
+    *out = c->dg ? c->dg->profile_read(wait != 0) : c->host->profile_read(wait != 0);
   });
 }
 ss_status tsa_test_dg_stamps(const ss_ctx* c, uint64_t* out, uint32_t cap, uint32_t* n) {

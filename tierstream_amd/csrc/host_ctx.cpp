@@ -253,6 +253,7 @@ void HostCtx::cleanup() noexcept {
   dev_->event_destroy(vready_ev_);
   dev_->event_destroy(vready2_ev_);
   for (hipEvent_t e : vflush_ev_) dev_->event_destroy(e);
+  for (hipEvent_t e : prof_made_) dev_->event_destroy(e);
   dev_->stream_destroy(vstream_);
   dev_->event_destroy(join_ev_);
   dev_->stream_destroy(copy_);
@@ -628,13 +629,58 @@ void HostCtx::flush_verify() {
   stream_wait(vstream_, vready2_ev_);
   tsa_verify_unit* vd = static_cast<tsa_verify_unit*>(vtable_dev_) + vflushed_;
   copy_h2d(vd, vtable_host_ + vflushed_, n * sizeof(tsa_verify_unit), vstream_);
-  hip_check(hipError_t(launch_verify(vd, uint32_t(n), segs, seg_bytes_, vfail_dev_ + vflushed_, vstream_)),
+  TimedCheck t{nullptr, nullptr, 0, uint32_t(n)};
+  if (prof_verify_) {
+    for (hipEvent_t* e : {&t.start, &t.stop}) {
+      if (prof_free_.empty()) prof_made_.push_back(*e = dev_->event_create_timed());
+      else *e = prof_free_.back(), prof_free_.pop_back();
+    }
+    for (size_t i = vflushed_; i < vused_; ++i) t.bytes += vtable_host_[i].total;
+  }
+  hip_check(hipError_t(launch_verify(vd, uint32_t(n), segs, seg_bytes_, vfail_dev_ + vflushed_, vstream_, t.start,
+                                     t.stop)),
             "device check launch");
+  if (t.start) prof_pending_.push_back(t);
   if (vflushes_ == vflush_ev_.size()) vflush_ev_.push_back(dev_->event_create());
   ev_record(vflush_ev_[vflushes_], vstream_);
   for (size_t i = vflushed_; i < vused_; ++i) ventry_flush_[i] = vflushes_;
   ++vflushes_;
   vflushed_ = vused_;
+}
+
+void HostCtx::prof_drain(bool wait) {
+  size_t kept = 0;
+  for (const TimedCheck& t : prof_pending_) {
+    if (wait) hip_check(hipEventSynchronize(t.stop), "hipEventSynchronize (check timing)");
+    else if (hipEventQuery(t.stop) != hipSuccess) {
+      prof_pending_[kept++] = t;
+      continue;
+    }
+    float ms = 0;
+    hip_check(hipEventElapsedTime(&ms, t.start, t.stop), "hipEventElapsedTime (check timing)");
+    ++prof_sum_.verifies;
+    prof_sum_.verify_units += t.units;
+    prof_sum_.verify_bytes += t.bytes;
+    prof_sum_.verify_ns += uint64_t(double(ms) * 1e6);
+    prof_free_.push_back(t.start);
+    prof_free_.push_back(t.stop);
+  }
+  prof_pending_.resize(kept);
+}
+
+void HostCtx::profile_enable(int on) {
+  std::lock_guard<std::mutex> lk(copy_mu_);
+  prof_drain(true);
+  prof_verify_ = (on == 1) || (on & TSA_TEST_PROF_VERIFY);
+  prof_sum_ = tsa_test_profile{};
+}
+
+tsa_test_profile HostCtx::profile_read(bool wait) {
+  std::lock_guard<std::mutex> lk(copy_mu_);
+  prof_drain(wait);
+  tsa_test_profile out = prof_sum_;
+  out.pending = prof_pending_.size();
+  return out;
 }
 
 void HostCtx::collect_verify() {

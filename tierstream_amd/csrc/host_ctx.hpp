@@ -29,6 +29,7 @@
 #include "model.hpp"
 #include "source.hpp"
 #include "tierstream_amd/tsa.h"
+#include "tierstream_amd/tsa_test.h"
 
 namespace tsa {
 
@@ -75,6 +76,10 @@ class HostCtx final : public HostWork {
   bool poisoned() const { return poisoned_; }
   Region region_of(uint64_t addr) const;
   uint64_t verify_failures() const { return verify_fail_total_; }
+  // Timing (a test hook, between forwards): each device-check launch bracketed by its dispatch's own begin and end
+  // stamps when on & TSA_TEST_PROF_VERIFY (this context brackets nothing else); read sums the completed brackets.
+  void profile_enable(int on);
+  tsa_test_profile profile_read(bool wait);
   // The stats-v1 document of the counters now; the snapshot publication (armed by the first snapshot call, published
   // at each ss_end that folds a forward and each reset between forwards; any thread).
   Json stats_json() const;
@@ -213,6 +218,17 @@ class HostCtx final : public HostWork {
   uint32_t vflushes_ = 0;
   hipEvent_t vdone_ev_ = nullptr;
   uint64_t verify_fail_total_ = 0;
+  // check launch timing (profile_enable): brackets in flight, recycled events, the sums so far (copy_mu_)
+  struct TimedCheck {
+    hipEvent_t start, stop;
+    uint64_t bytes;
+    uint32_t units;
+  };
+  bool prof_verify_ = false;
+  std::vector<TimedCheck> prof_pending_;
+  std::vector<hipEvent_t> prof_free_, prof_made_;
+  tsa_test_profile prof_sum_{};
+  void prof_drain(bool wait);  // copy_mu_ held
 
   void* fwd_stream_ = nullptr;
   bool fwd_stream_set_ = false;

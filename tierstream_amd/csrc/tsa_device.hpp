@@ -82,8 +82,9 @@ inline bool set_dg_verify_shape(DgVerifyLaunch& l, const void* const* arena, con
 
 // Each returns a hipError_t as an int (0 = launched); none synchronizes or allocates.
 int launch_digest(const TsaUnit* units_dev, uint32_t n, uint64_t* out_dev, hipStream_t stream);
+// start / stop (timing events, or null): recorded with the kernel's own begin and end (hipExtLaunchKernelGGL).
 int launch_verify(const TsaVerifyUnit* units_dev, uint32_t n_units, uint64_t n_segments, uint64_t seg_bytes,
-                  uint32_t* fail_dev, hipStream_t stream);
+                  uint32_t* fail_dev, hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 // start / stop (timing events, or null): recorded with the kernel's own begin and end (hipExtLaunchKernelGGL).
 int launch_dg_verify(const DgVerifyLaunch& a, hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 int launch_scatter(const TsaScatterJob* jobs_dev, uint32_t n_jobs, uint64_t n_blocks, hipStream_t stream);

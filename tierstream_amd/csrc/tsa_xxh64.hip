@@ -299,13 +299,17 @@ int launch_dg_verify(const DgVerifyLaunch& a, hipStream_t stream, hipEvent_t sta
 }
 
 int launch_verify(const TsaVerifyUnit* units_dev, uint32_t n_units, uint64_t n_segments, uint64_t seg_bytes,
-                  uint32_t* fail_dev, hipStream_t stream) {
+                  uint32_t* fail_dev, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   if (n_units == 0 || n_segments == 0) return 0;
   const uint32_t threads = 256;
   const uint64_t blocks = (n_segments * 4 + threads - 1) / threads;
   if (blocks > 0x7fffffffull) return int(hipErrorInvalidValue);
-  hipLaunchKernelGGL(dev::verify_kernel, dim3(uint32_t(blocks)), dim3(threads), 0, stream, units_dev, n_units,
-                     n_segments, seg_bytes, fail_dev);
+  if (start && stop)  // the events take the dispatch's own begin and end timestamps
+    hipExtLaunchKernelGGL(dev::verify_kernel, dim3(uint32_t(blocks)), dim3(threads), 0, stream, start, stop, 0,
+                          units_dev, n_units, n_segments, seg_bytes, fail_dev);
+  else
+    hipLaunchKernelGGL(dev::verify_kernel, dim3(uint32_t(blocks)), dim3(threads), 0, stream, units_dev, n_units,
+                       n_segments, seg_bytes, fail_dev);
   return int(hipGetLastError());
 }
 
