@@ -75,6 +75,8 @@ typedef struct tsa_test_dgcore_config {
    * row-major [previous unit][unit], layers concatenated; null = an empty table). The union width is bank_slots. */
   uint32_t policy, w_trans, w_freq, w_rec, rows;
   const uint32_t* score_cells;
+  /* appended: dg_bank_keep (0, 1, 2; three-tier only) */
+  uint32_t bank_keep;
 } tsa_test_dgcore_config;
 SS_API ss_status tsa_test_dgcore_open(const tsa_test_dgcore_config* cfg, const uint32_t* order, uint32_t n_order,
                                       void** out);

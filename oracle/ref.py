@@ -67,6 +67,8 @@ def lib() -> C.CDLL:
             "refdg_residency": (u32, [vp, C.POINTER(u32), u32]),
             "refdg_open_disk": (vp, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, C.POINTER(u64), u32,
                                      C.POINTER(u32), u32, u32, u32, u32, u32, C.POINTER(C.c_uint8)]),
+            "refdg_open_disk_keep": (vp, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, C.POINTER(u64), u32,
+                                          C.POINTER(u32), u32, u32, u32, u32, u32, C.POINTER(C.c_uint8), u32]),
             "refdg_open_scored": (vp, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, C.POINTER(u64), u32,
                                        C.POINTER(u32), u32, u32, u32, u32, u32, u32, C.POINTER(u32), u32, u32, u32,
                                        C.POINTER(C.c_uint8)]),
@@ -240,7 +242,7 @@ class RefDg:
     def __init__(self, n_units, persistent, bank, blocks, spare_target, part_bytes, order, prefetch_reserve=0xFFFFFFFF,
                  pf_layer=4, pf_token=48, wb_defer=1, wb_on_d2h=1, inclusive=0, disk=None, score=None):
         """disk (three-tier): dict(flags=[keys] 0/1 file-tier, home_blocks=P, disk_staging=S, clean_evict=0,
-        disk_prefetch=0); the prefetch budgets then take their defaults. score (scored eviction): dict(policy=1 SCORED
+        disk_prefetch=0, bank_keep=0); the prefetch budgets then take their defaults. score (scored eviction): dict(policy=1 SCORED
         or 2 SCORED_AUTO, w=(w_trans, w_freq, w_rec), rows=verify rows per boundary, cells=None or the starting
         transition counts, per gated layer units^2 row-major, concatenated); the prefetch budgets take their defaults
         and disk prefetch stays off."""
@@ -263,9 +265,10 @@ class RefDg:
                                   pf_token, wb_defer, wb_on_d2h, inclusive, pb, len(part_bytes), od, len(order))
         else:
             fl = (C.c_uint8 * sum(n_units))(*disk["flags"])
-            self.h = L.refdg_open_disk(nu, len(n_units), persistent, bank, blocks, spare_target, wb_defer, inclusive,
-                                       pb, len(part_bytes), od, len(order), disk["home_blocks"], disk["disk_staging"],
-                                       disk.get("clean_evict", 0), disk.get("disk_prefetch", 0), fl)
+            self.h = L.refdg_open_disk_keep(nu, len(n_units), persistent, bank, blocks, spare_target, wb_defer,
+                                            inclusive, pb, len(part_bytes), od, len(order), disk["home_blocks"],
+                                            disk["disk_staging"], disk.get("clean_evict", 0),
+                                            disk.get("disk_prefetch", 0), fl, disk.get("bank_keep", 0))
         if not self.h:
             raise RuntimeError("refdg_open failed")
         self.keys = sum(n_units)

@@ -135,7 +135,7 @@ extern "C" {
 // Three-tier options of refdg_open (disk_tier 0: none of the others is read): home_blocks = the plan's pinned units,
 // disk_staging buffers, the file-tier flags of the keys (keys entries, key order), clean_evict, disk_prefetch.
 struct RefDiskOpts {
-  uint32_t disk_tier = 0, home_blocks = 0, disk_staging = 0, clean_evict = 0, disk_prefetch = 0;
+  uint32_t disk_tier = 0, home_blocks = 0, disk_staging = 0, clean_evict = 0, disk_prefetch = 0, bank_keep = 0;
   const uint8_t* disk = nullptr;
 };
 // Scored eviction options of refdg_open (policy 0 = LRU: none of the others is read): policy 1 SCORED / 2 SCORED_AUTO,
@@ -171,6 +171,24 @@ void* refdg_open_disk(const uint32_t* n_units, uint32_t G, uint32_t persistent, 
   dk.clean_evict = clean_evict;
   dk.disk_prefetch = disk_prefetch;
   dk.disk = disk;
+  return refdg_open_impl(n_units, G, persistent, bank, blocks, spare_target, 0xFFFFFFFFu, 4, 48, wb_defer, 1, inclusive,
+                         part_bytes, n_parts, order, n_order, dk);
+}
+
+// refdg_open_disk with dg_bank_keep (0, 1, 2).
+void* refdg_open_disk_keep(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
+                           uint32_t spare_target, uint32_t wb_defer, uint32_t inclusive, const uint64_t* part_bytes,
+                           uint32_t n_parts, const uint32_t* order, uint32_t n_order, uint32_t home_blocks,
+                           uint32_t disk_staging, uint32_t clean_evict, uint32_t disk_prefetch, const uint8_t* disk,
+                           uint32_t bank_keep) {
+  RefDiskOpts dk;
+  dk.disk_tier = 1;
+  dk.home_blocks = home_blocks;
+  dk.disk_staging = disk_staging;
+  dk.clean_evict = clean_evict;
+  dk.disk_prefetch = disk_prefetch;
+  dk.disk = disk;
+  dk.bank_keep = bank_keep;
   return refdg_open_impl(n_units, G, persistent, bank, blocks, spare_target, 0xFFFFFFFFu, 4, 48, wb_defer, 1, inclusive,
                          part_bytes, n_parts, order, n_order, dk);
 }
@@ -277,6 +295,7 @@ void* refdg_open_impl(const uint32_t* n_units, uint32_t G, uint32_t persistent, 
       c.disk_staging = dk.disk_staging;
       c.disk_queue = 1;
       c.clean_evict = dk.clean_evict != 0;
+      c.bank_keep = dk.bank_keep;
       uint32_t keys = 0;
       for (uint32_t g = 0; g < G; ++g) keys += n_units[g];
       disk.assign(dk.disk, dk.disk + keys);
@@ -357,7 +376,8 @@ int refdg_token_run(void* h, const uint32_t* ids, uint32_t n, const uint32_t* pr
                           s.inclusive_drops, uint64_t(c.free_slots()), uint64_t(c.free_blocks()),
                           uint64_t(c.on_device()), uint64_t(c.backed_units()), s.disk_reads, s.disk_drops,
                           s.disk_discards, s.clean_drops, uint64_t(c.file_units()), s.score_fallbacks,
-                          s.scored_victims, s.score_layers, s.score_candidates, s.score_saturated};
+                          s.scored_victims, s.score_layers, s.score_candidates, s.score_saturated, s.bank_kept,
+                          s.bank_keep_drops, s.bank_keep_rereads};
     std::memcpy(counts, v, sizeof v);
     return 0;
   } catch (const std::exception& e) {
@@ -371,7 +391,8 @@ const char* refdg_counter_names() {
          "evict_short writebacks_done predicted predicted_true miss_layers covered_waits wb_deferred wb_cancelled "
          "wb_forced wb_boundary_flushed wb_issued_bytes wb_cancelled_bytes inclusive_kept inclusive_drops free_slots "
          "free_blocks on_device backed_units disk_reads disk_drops disk_discards clean_drops file_units "
-         "score_fallbacks scored_victims score_layers score_candidates score_saturated";
+         "score_fallbacks scored_victims score_layers score_candidates score_saturated bank_kept bank_keep_drops "
+         "bank_keep_rereads";
 }
 
 // The device keys in recency order, most recent first.

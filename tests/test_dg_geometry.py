@@ -7,8 +7,8 @@ in flight, slot counts, guard slot, blocks and score weights.
 Configurations are drawn per seed around valid ones: layers and units, one to five parts (now and then not a multiple
 of 256, or five), the planner's tiers or explicit ones (with file homes), dynamic and explicit spare slots, ring slots
 around 2 x dg_max_ids + 1, spare blocks, clean copies, the file tier's options, the policy and its weights, and a broken
-option now and then. Options the reference accepts but this library does not serve (landings, kept bank reads, the
-adaptive read depth, no-admit, prefetch revert, strict admission) must be refused with SS_E_UNSUPPORTED."""
+option now and then (dg_bank_keep among them). Options the reference accepts but this library does not serve (landings,
+the adaptive read depth, no-admit, prefetch revert, strict admission) must be refused with SS_E_UNSUPPORTED."""
 import ctypes as C
 
 import numpy as np
@@ -21,8 +21,7 @@ KiB = 1024
 u32 = C.c_uint32
 FIELDS = ["keys", "G", "R", "D", "B", "P", "F", "Q", "I", "S", "disk_queue", "persistent_slots", "slots", "guard_slot",
           "blocks", "scored", "w_trans", "w_freq", "w_rec"]
-UNSERVED = ["dg_landing_blocks", "dg_bank_keep", "dg_disk_queue_adapt", "dg_no_admit", "dg_pf_revert_unused",
-            "dg_pf_strict_admit"]
+UNSERVED = ["dg_landing_blocks", "dg_disk_queue_adapt", "dg_no_admit", "dg_pf_revert_unused", "dg_pf_strict_admit"]
 
 
 def _case(seed, tmp_path):
@@ -69,6 +68,8 @@ def _case(seed, tmp_path):
         if rng.random() < 0.5:
             a, b = sorted(int(x) for x in rng.integers(0, 1001, size=2))
             okw.update(dg_score_w_trans=a, dg_score_w_freq=b - a, dg_score_w_recency=1000 - b + int(rng.random() < 0.1))
+    if rng.random() < 0.15:
+        okw.update(dg_bank_keep=int(rng.choice([0, 1, 2, 3])))
     if rng.random() < 0.02:
         okw.update(dg_wb_defer=2)
     if rng.random() < 0.02:

@@ -27,7 +27,7 @@ class DgCoreConfig(C.Structure):
                 ("part_bytes", C.POINTER(u64)), ("n_parts", u32), ("disk_tier", u32), ("home_blocks", u32),
                 ("disk_staging", u32), ("clean_evict", u32), ("disk_prefetch", u32),
                 ("disk", C.POINTER(C.c_uint8)), ("policy", u32), ("w_trans", u32), ("w_freq", u32), ("w_rec", u32),
-                ("rows", u32), ("score_cells", C.POINTER(u32))]
+                ("rows", u32), ("score_cells", C.POINTER(u32)), ("bank_keep", u32)]
 
 
 def _lib():
@@ -75,6 +75,7 @@ class OurCore:
             fl = (C.c_uint8 * sum(n_units))(*disk["flags"])
             c.disk_tier, c.home_blocks, c.disk_staging = 1, disk["home_blocks"], disk["disk_staging"]
             c.clean_evict, c.disk_prefetch, c.disk = disk.get("clean_evict", 0), disk.get("disk_prefetch", 0), fl
+            c.bank_keep = disk.get("bank_keep", 0)
             self._keep.append(fl)
         c.w_trans, c.w_freq, c.w_rec, c.rows = 700, 200, 100, 1
         if score:
@@ -215,7 +216,8 @@ def _preds(rng, routes, n_units, k):
     return out
 
 
-def _run(seed, three, score=None, switch=None, partial=False, predict=0, disk_prefetch=0, keep=False, sched=False):
+def _run(seed, three, score=None, switch=None, partial=False, predict=0, disk_prefetch=0, keep=False, sched=False,
+         bank_keep=0):
     """switch: (token, policy) - both cores switch policy between tokens there. partial: each token exports a random
     nonempty subset of the gated layers (ss_begin's rows), the others keep their state. keep: now and then, between
     tokens, a new keep list (ss_dg_keep: units no boundary may evict; sometimes empty, sometimes with keys off the
@@ -225,6 +227,8 @@ def _run(seed, three, score=None, switch=None, partial=False, predict=0, disk_pr
     c = _case(seed, three)
     if disk_prefetch and c["disk"]:
         c["disk"]["disk_prefetch"] = 1
+    if bank_keep and c["disk"]:
+        c["disk"]["bank_keep"] = bank_keep
     kw = dict(wb_defer=c["wb_defer"], inclusive=c["inclusive"])
     ours = OurCore(c["n_units"], c["persistent"], c["bank"], c["blocks"], c["spare_target"], c["parts"], c["order"],
                    disk=c["disk"], score=score, **kw)
@@ -444,3 +448,24 @@ def test_scored_cases_choose_other_victims_than_lru():
             b.close()
             auto.close()
     assert victims > 0 and differ > 0 and saturated > 0
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("seed", range(60))
+def test_bank_keep_matches_reference(seed, mode):
+    """dg_bank_keep: a bank-served demand file miss read into a pinned block (a free one, else the longest-homed
+    unit's), which becomes its home at the bank's release - at the front of the pinned order (1) or behind its front
+    half (2); tables, counters (bank_kept, bank_keep_drops, bank_keep_rereads) and the pinned order every token
+    (reference src/dg_core.cpp keep_block / hpush_mid, docs/design.md 3.16)."""
+    _run(3000 + seed, True, bank_keep=mode, predict=int(seed % 3), disk_prefetch=int(seed % 4 == 1))
+
+
+def test_bank_keep_cases_exercise_the_paths():
+    if not ref.available():
+        pytest.skip("oracle/_ref (the reference core) is not built")
+    tot = {}
+    for s in range(30):
+        for k, v in _run(3000 + s, True, bank_keep=1 + s % 2).items():
+            tot[k] = tot.get(k, 0) + v
+    for k in ("bank_kept", "bank_keep_drops", "bank_keep_rereads", "bank_serves", "disk_drops"):
+        assert tot[k] > 0, k

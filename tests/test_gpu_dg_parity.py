@@ -396,17 +396,20 @@ def test_three_tier_read_failure_fails_the_token(tmp_path, gpu, queue):
 BIG_PARTS = (8 * 1024 * KiB + 64 * KiB, 64 * KiB, 4 * 1024 * KiB)
 
 
-@pytest.mark.parametrize("clean_evict,queue,parts,predict", [(0, 0, None, 0), (1, 0, None, 0), (0, 4, None, 0),
-                                                             (1, 4, None, 0), (0, 3, BIG_PARTS, 0), (0, 4, None, 2),
-                                                             (0, 0, None, 2)])
-def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, predict):
+@pytest.mark.parametrize("clean_evict,queue,parts,predict,bank_keep",
+                         [(0, 0, None, 0, 0), (1, 0, None, 0, 0), (0, 4, None, 0, 0), (1, 4, None, 0, 0),
+                          (0, 3, BIG_PARTS, 0, 0), (0, 4, None, 2, 0), (0, 0, None, 2, 0), (0, 0, None, 0, 1),
+                          (0, 4, None, 0, 2), (0, 3, BIG_PARTS, 0, 1), (0, 4, None, 2, 1)])
+def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, predict, bank_keep):
     """Three tiers (dg_disk_tier): 12 of 32 units resident, 10 pinned, 10 read from the file on a miss through staging
     buffers. The plan's tiers are given explicitly (a planner spill to the file tier leaves no room for spare blocks,
     as in the reference). Every token the slot table and the counters (file reads, drops of the pinned LRU to the
     file, discards) must equal the reference core's, and every routed unit the engine read must checksum to the
     file's bytes; every landed unit is re-hashed in HBM (verify_hash 2). dg_disk_queue 4: the reads run on reader
     threads and each copy out of a staging buffer awaits its read on the device; the placement is the same. predict:
-    the engine predicts the next layer's ids and dg_disk_prefetch lets a prefetch read a file-homed unit."""
+    the engine predicts the next layer's ids and dg_disk_prefetch lets a prefetch read a file-homed unit. bank_keep
+    (dg_bank_keep 1 / 2): a bank-served file miss is read into a pinned block, which becomes its home (its
+    counters compared too)."""
     parts = list(parts or (64 * KiB,) * 3)
     layers, units, n_ids, staging, dyn, spares = 4, 8, 2, 4, 1, 6
     m, tiers, bkw = _three_tier(tmp_path, parts)
@@ -422,16 +425,17 @@ def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, 
     dpf = 1 if predict else 0
     refdg = ref.RefDg([units] * layers, 12 + D, n_ids, 10 + Q, D, parts, residents + list(range(keys)),
                       disk=dict(flags=flags, home_blocks=10, disk_staging=staging, clean_evict=clean_evict,
-                                disk_prefetch=dpf))
+                                disk_prefetch=dpf, bank_keep=bank_keep))
     ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(forward_mode=1, dg_max_ids=n_ids, pin_planned=0, verify_hash=2,
                                                       dg_disk_tier=1, dg_disk_staging=staging,
                                                       dg_clean_evict=clean_evict, dg_disk_queue=queue,
-                                                      dg_disk_prefetch=dpf, dg_wait_timeout_ms=5000))
+                                                      dg_disk_prefetch=dpf, dg_bank_keep=bank_keep,
+                                                      dg_wait_timeout_ms=5000))
     eng = ss.DgEngine(ctx, n_ids, use_graph=True, n_pred=predict)
     routes = _routes(layers, units, n_ids, 24, seed=9, zipf=True)
     preds = _preds(routes, units, predict) if predict else None
     expect = {(L, u): fixtures.engine_checksum(m.unit_data(L, u)) for L in range(layers) for u in range(units)}
-    counters = COUNTERS + ["disk_reads", "disk_drops", "disk_discards", "clean_drops"] + \
+    counters = COUNTERS + ["disk_reads", "disk_drops", "disk_discards", "clean_drops", "bank_kept"] + \
         (PRED_COUNTERS if predict else [])
     with pytest.raises(ss.SsError):
         ctx.snapshot()
@@ -448,14 +452,18 @@ def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, 
                 for i, u in enumerate(routes[t, L]):
                     assert int(cks[L, i]) == expect[(L, int(u))], (t, L, i)
         assert got["disk_reads"] > 0 and (got["disk_drops"] + got["disk_discards"]) > 0, got
+        if bank_keep:
+            assert got["bank_kept"] > 0, got
         assert got["disk_queue_resolved"] == max(queue, 1) and 1 <= got["disk_max_in_flight"] <= max(queue, 1), got
         assert got["disk_read_ns"] > 0 and got["disk_wait_ns"] > 0, got
         assert ctx.verify_failures() == 0
         _check_stats_doc(ctx, want, routes.shape[0])
         tt = json.loads(ctx.stats_json())["device_gated"]["three_tier"]
-        for k in ("disk_reads", "disk_drops", "disk_discards", "clean_drops"):
+        for k in ("disk_reads", "disk_drops", "disk_discards", "clean_drops", "bank_kept"):
             assert tt[k] == got[k], k
         assert tt["disk_queue_resolved"] == max(queue, 1) and tt["staging"] == staging
+        assert tt["bank_keep"] == bank_keep and tt["bank_keep_drops"] == want["bank_keep_drops"]
+        assert tt["bank_keep_rereads"] == want["bank_keep_rereads"]
     finally:
         eng.close()
         ctx.close()

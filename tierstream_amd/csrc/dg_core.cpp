@@ -12,7 +12,7 @@ namespace {
 std::string str(uint64_t v) { return std::to_string(v); }
 }  // namespace
 
-void DgTransport::read_unit(uint32_t, int32_t) {
+void DgTransport::read_unit(uint32_t, int32_t, int32_t) {
   fail(SS_E_UNSUPPORTED, "device-gated: this transport has no file tier");
 }
 
@@ -20,21 +20,39 @@ void DgTransport::read_unit(uint32_t, int32_t) {
 void KeyOrder::reset(uint32_t n) {
   link_.assign(2 * size_t(n), kEnd);
   member_.assign(n, 0);
-  front_ = back_ = kEnd;
-  n_ = 0;
+  front_ = back_ = half_last_ = kEnd;
+  n_ = half_n_ = 0;
 }
 
-void KeyOrder::put_front(uint32_t k) {
-  link_[2 * size_t(k)] = front_;
-  link_[2 * size_t(k) + 1] = kEnd;
-  if (front_ == kEnd) back_ = k;
-  else link_[2 * size_t(front_) + 1] = k;
-  front_ = k;
-  member_[k] = 1;
+void KeyOrder::link_after(uint32_t k, uint32_t prev) {
+  const uint32_t next = prev == kEnd ? front_ : link_[2 * size_t(prev)];
+  link_[2 * size_t(k)] = next;
+  link_[2 * size_t(k) + 1] = prev;
+  if (prev == kEnd) front_ = k;
+  else link_[2 * size_t(prev)] = k;
+  if (next == kEnd) back_ = k;
+  else link_[2 * size_t(next) + 1] = k;
   ++n_;
 }
 
+void KeyOrder::put_front(uint32_t k) {
+  link_after(k, kEnd);
+  member_[k] = 2;  // ahead of every key: the front half grows by it
+  if (half_n_++ == 0) half_last_ = k;
+  rebalance();
+}
+
+void KeyOrder::put_middle(uint32_t k) {
+  link_after(k, half_last_);
+  member_[k] = 1;
+  rebalance();
+}
+
 void KeyOrder::remove(uint32_t k) {
+  if (member_[k] == 2) {
+    --half_n_;
+    if (half_last_ == k) half_last_ = toward_front(k);
+  }
   const uint32_t behind = link_[2 * size_t(k)], ahead = link_[2 * size_t(k) + 1];
   if (ahead == kEnd) front_ = behind;
   else link_[2 * size_t(ahead)] = behind;
@@ -43,6 +61,29 @@ void KeyOrder::remove(uint32_t k) {
   link_[2 * size_t(k)] = link_[2 * size_t(k) + 1] = kEnd;
   member_[k] = 0;
   --n_;
+  rebalance();
+}
+
+// Each insertion or removal moves the half's boundary by one key at most.
+void KeyOrder::rebalance() {
+  const uint32_t want = n_ / 2;
+  for (; half_n_ > want; --half_n_) {
+    member_[half_last_] = 1;
+    half_last_ = toward_front(half_last_);
+  }
+  for (; half_n_ < want; ++half_n_) {
+    half_last_ = half_last_ == kEnd ? front_ : toward_back(half_last_);
+    member_[half_last_] = 2;
+  }
+}
+
+bool KeyOrder::half_consistent() const {
+  uint32_t i = 0, last = kEnd;
+  for (uint32_t k = front_; k != kEnd; k = toward_back(k), ++i) {
+    if (member_[k] != (i < n_ / 2 ? 2 : 1)) return false;
+    if (i + 1 == n_ / 2) last = k;
+  }
+  return i == n_ && half_n_ == n_ / 2 && half_last_ == last;
 }
 
 // ---- EventLedger ------------------------------------------------------------------------------------------------------
@@ -246,6 +287,7 @@ DgCore::DgCore(const DgConfig& cfg, DgTransport* t) : c_(cfg), t_(t) {
     require(!c_.disk_prefetch && c_.disk_staging == 0 && c_.home_blocks == 0 && !c_.clean_evict, SS_E_INVALID,
             "device-gated: file-tier options given without the file tier");
   }
+  require(c_.bank_keep <= 2, SS_E_INVALID, "device-gated: dg_bank_keep is 0, 1 or 2");
   if (c_.prefetch_reserve_auto) c_.prefetch_reserve = std::min<uint32_t>(24, c_.spare_target / 4);
 
   st_.assign(keys_, KeyState{});
@@ -401,11 +443,31 @@ void DgCore::fall_back(uint32_t k) {
     return;
   }
   x.where = Where::Pinned;
-  make_pinned(k);
+  if (x.home_middle && c_.disk_tier) {  // (dg_bank_keep 2: a one-off read does not displace the recently homed)
+    ++n_pinned_;
+    homed_.put_middle(k);
+  } else {
+    make_pinned(k);
+  }
+  x.home_middle = false;
 }
 
 // The pinned unit homed longest ago goes to its file (its bytes are there already) and gives up its block, which no
 // copy is using (a pinned home is only ever read, by a fetch that has since landed or not yet started).
+// dg_bank_keep: the block a bank-served demand file miss is read into, its pinned home once the bank releases it.
+int32_t DgCore::block_to_keep() {
+  if (!c_.bank_keep || !c_.disk_tier) return -1;
+  if (free_block_.empty()) {
+    const uint32_t oldest = homed_.back();
+    if (!give_up_oldest_home()) return -1;
+    st_[oldest].dropped_for_keep = n_.tokens + 1;
+    ++n_.bank_keep_drops;
+  }
+  const int32_t b = free_block_.back();
+  free_block_.pop_back();
+  return b;
+}
+
 bool DgCore::give_up_oldest_home() {
   if (!c_.disk_tier || homed_.size() == 0) return false;
   const uint32_t k = homed_.back();
@@ -646,18 +708,40 @@ bool DgCore::bring_in(uint32_t g, uint32_t u, bool ahead) {
   }
 
   const DgTransport::Stream s = ahead ? DgTransport::kPf : DgTransport::kDem;
-  if (x.where == Where::File) {  // read into a staging buffer, then copied in from there like a pinned home
-    const int32_t stage = next_stage();
-    t_->read_unit(k, stage);
+  if (x.where == Where::File) {  // read into a staging buffer (or a kept block), then copied in from there
+    const int32_t kept = banked ? block_to_keep() : -1;
+    const int32_t src = kept >= 0 ? kept : next_stage();
+    if (kept >= 0) {
+      if (void* wb = ev_.on_block(kept)) t_->event_sync(wb);  // a write-back may still be copying into it
+      try {
+        t_->read_unit(k, src, slot);
+      } catch (...) {  // nothing begun for the key: the block is free again
+        free_block_.push_back(kept);
+        throw;
+      }
+    } else {
+      t_->read_unit(k, src, slot);
+    }
     ++n_.disk_reads;
     n_.disk_read_bytes += unit_bytes_;
-    t_->wait_copy_in(s, slot, stage, ev_.on_slot(slot), nullptr);  // (write-backs never touch staging buffers)
+    t_->wait_copy_in(s, slot, src, ev_.on_slot(slot), nullptr);  // (the block's own write-back ended above)
     ev_.untie_slot(slot);
-    t_->h2d(s, slot, stage);
-    void*& last = stage_ev_[size_t(stage) - c_.blocks];
-    if (!last) last = ev_.take();
-    t_->record(last, s);
+    if (kept >= 0) ev_.untie_block(kept);
+    t_->h2d(s, slot, src);
+    if (kept >= 0) {  // the block is the key's: its pinned home when the bank releases it
+      x.block = kept;
+      x.home_middle = c_.bank_keep == 2;
+      ++n_.bank_kept;
+    } else {
+      void*& last = stage_ev_[size_t(src) - c_.blocks];
+      if (!last) last = ev_.take();
+      t_->record(last, s);
+    }
     --n_file_;
+    if (x.dropped_for_keep) {  // dropped for a kept read, and read back from its file
+      if (n_.tokens + 1 - x.dropped_for_keep <= 8) ++n_.bank_keep_rereads;
+      x.dropped_for_keep = 0;
+    }
   } else {  // after the slot's last write-back and any write-back still copying into this block
     t_->wait_copy_in(s, slot, x.block, ev_.on_slot(slot), ev_.on_block(x.block));
     ev_.untie_slot(slot);
@@ -1107,6 +1191,7 @@ void DgCore::audit() const {
   if (n_clean != n_clean_) broken("clean-copy count");
   if (recent_.size() != n_device_) broken("recency order length");
   if (c_.disk_tier && homed_.size() != n_pinned_) broken("homes' order length");
+  if (c_.disk_tier && !homed_.half_consistent()) broken("the homes' order's front half");
   if (c_.scored) {  // stamps fall strictly from the front; no demand token ahead of the current one
     uint64_t above = UINT64_MAX;
     for (uint32_t k = recent_.front(); k != KeyOrder::kEnd; k = recent_.toward_back(k)) {

@@ -53,7 +53,8 @@ class DgTransport {
   virtual void upload_table(const int32_t* table, uint32_t n) = 0;  // the whole table on kDem, then sync
   // Three-tier: the unit's bytes from its file into staging block `block` (blocks .. blocks + disk_staging - 1: the
   // host layout of a unit), synchronously; the core then copies it in from that block as from a pinned home.
-  virtual void read_unit(uint32_t key, int32_t block);
+  // slot: where the copy that follows puts it (a bank slot when the read went into a kept pinned block).
+  virtual void read_unit(uint32_t key, int32_t block, int32_t slot);
   // Before h2d(s, slot, block): slot_ev / block_ev (either may be null) are the write-backs that may still read the
   // slot or write the block. The default makes s wait for both; a transport that tracks its copies per part may let
   // each part of the next h2d wait only for the same part of those write-backs.
@@ -94,6 +95,10 @@ struct DgConfig {
   // disk_prefetch: a prefetch may read a file-homed unit.
   bool disk_tier = false, disk_prefetch = false, clean_evict = false;
   uint32_t home_blocks = 0, disk_staging = 0;
+  // dg_bank_keep (three-tier): a demand file miss served through a bank slot is read into a pinned block - a free one,
+  // else the longest-homed pinned unit's (that unit to its file) - which becomes its pinned home when the bank releases
+  // it: at the front of the homes' order (1) or behind its front half (2). 0: read through a staging buffer.
+  uint32_t bank_keep = 0;
   // Scored eviction (SS_POLICY_SCORED / SCORED_AUTO): the boundary takes its victims lowest score first instead of
   // from the back of the recency order; every other decision stays LRU's. Weights in thousandths (each 0..1000, sum
   // 1000). max_ids: the ids of one export (a union's upper bound), 1..64. scored_auto: learn every token, but rank
@@ -112,6 +117,9 @@ struct DgCounts {  // the subset of ss_dg_stats this core counts (the ABI's fiel
   uint64_t wb_forced_wait_ns = 0, inclusive_kept = 0, inclusive_drops = 0;
   uint64_t disk_reads = 0, disk_read_bytes = 0, disk_stage_waits = 0, disk_drops = 0, disk_discards = 0;
   uint64_t clean_drops = 0, clean_drop_bytes = 0;
+  // dg_bank_keep: reads kept in a pinned block; pinned units dropped to their file for one; such a dropped unit read
+  // from its file again within 8 tokens
+  uint64_t bank_kept = 0, bank_keep_drops = 0, bank_keep_rereads = 0;
   // scored eviction: boundaries that fell back to the recency order (an exported gated layer whose union is not this
   // token's); victims taken in score order; layers and eligible keys the selection considered; transition increments
   // lost to a saturated cell; selection time.
@@ -122,24 +130,30 @@ struct DgLayerCounts {
   uint64_t lookups = 0, misses = 0, fetched = 0, bank_serves = 0, prefetched = 0, prefetch_used = 0, evicted = 0;
 };
 
-// An order over keys 0..n-1 (each in it at most once) with constant-time insertion at the front and removal anywhere.
+// An order over keys 0..n-1 (each in it at most once) with constant-time insertion and removal. It also keeps the
+// boundary after its first size() / 2 keys (the front half), so a key can go in at the middle in constant time.
 class KeyOrder {
  public:
   static constexpr uint32_t kEnd = 0xffffffffu;
   void reset(uint32_t n);
   bool has(uint32_t k) const { return member_[k] != 0; }
   void put_front(uint32_t k);
+  void put_middle(uint32_t k);  // right behind the front half (as it was before k joined)
   void remove(uint32_t k);
   uint32_t front() const { return front_; }
   uint32_t back() const { return back_; }
   uint32_t toward_back(uint32_t k) const { return link_[2 * size_t(k)]; }
   uint32_t toward_front(uint32_t k) const { return link_[2 * size_t(k) + 1]; }
   uint32_t size() const { return n_; }
+  bool half_consistent() const;  // the front half is exactly the first size() / 2 keys (tests)
 
  private:
+  void link_after(uint32_t k, uint32_t prev);  // prev kEnd: at the front
+  void rebalance();
   std::vector<uint32_t> link_;  // per key: [toward the back, toward the front]
-  std::vector<uint8_t> member_;
+  std::vector<uint8_t> member_;  // 0: out; 1: in the back half; 2: in the front half
   uint32_t front_ = kEnd, back_ = kEnd, n_ = 0;
+  uint32_t half_last_ = kEnd, half_n_ = 0;  // the front half's last key and its size
 };
 
 class DgCore {
@@ -236,8 +250,10 @@ class DgCore {
     bool ahead = false;      // copied in by a prefetch this token
     bool ahead_hit = false;  // ... and since used
     bool clean = false;      // resident with its block kept as a clean copy
+    bool home_middle = false;  // dg_bank_keep 2: its kept block becomes its home behind the front half of the order
     void* ahead_ev = nullptr;  // the prefetch's copy
     uint64_t demand_token = 0;  // scored: the token of its last demand use (0: none since open or a policy switch)
+    uint64_t dropped_for_keep = 0;  // dg_bank_keep: 1 + the tokens closed when a kept read took its block (0: none)
   };
 
   // A victim's copy into its block. Sealed: its event recorded after its last submitted part; it completes in the
@@ -339,6 +355,7 @@ class DgCore {
   // to its block, else (three-tier, none) its file; no copy
   void fall_back(uint32_t k);
   bool give_up_oldest_home();  // three-tier: the longest-homed pinned unit to its file, its block free
+  int32_t block_to_keep();     // dg_bank_keep: a free block, else the longest-homed unit's; -1: none (stage it)
   int32_t next_stage();        // three-tier: the next staging buffer, its last copy out of it landed
 
   // write-backs

@@ -37,7 +37,7 @@ class EagerTransport final : public DgTransport {
   void event_sync(void*) override {}
   void sync(Stream) override {}
   void upload_table(const int32_t*, uint32_t) override {}
-  void read_unit(uint32_t, int32_t) override {}
+  void read_unit(uint32_t, int32_t, int32_t) override {}
 
  private:
   std::vector<uint64_t> parts_;
@@ -55,7 +55,7 @@ constexpr const char* kNames =
     "writebacks_done miss_layers covered_waits wb_deferred wb_cancelled wb_forced wb_boundary_flushed wb_issued_bytes "
     "wb_cancelled_bytes inclusive_kept inclusive_drops free_slots free_blocks on_device backed_units disk_reads "
     "disk_drops disk_discards clean_drops file_units score_fallbacks scored_victims score_layers score_candidates "
-    "score_saturated pred_invalid predicted predicted_true";
+    "score_saturated pred_invalid predicted predicted_true bank_kept bank_keep_drops bank_keep_rereads";
 
 }  // namespace
 }  // namespace tsa
@@ -88,6 +88,7 @@ ss_status tsa_test_dgcore_open(const tsa_test_dgcore_config* cfg, const uint32_t
     c.home_blocks = cfg->home_blocks;
     c.disk_staging = cfg->disk_staging;
     c.clean_evict = cfg->clean_evict != 0;
+    c.bank_keep = cfg->bank_keep;
     require(cfg->policy <= 2, SS_E_INVALID, "tsa_test_dgcore_open: policy must be 0, 1 or 2");
     c.scored = cfg->policy != 0;
     c.scored_auto = cfg->policy == 2;
@@ -164,7 +165,8 @@ ss_status tsa_test_dgcore_token_pred(void* h, const uint32_t* ids, uint32_t n, c
                             uint64_t(c.free_slots()), uint64_t(c.free_blocks()), uint64_t(c.on_device()),
                             uint64_t(c.clean_copies()), s.disk_reads, s.disk_drops, s.disk_discards, s.clean_drops,
                             uint64_t(c.file_units()), s.score_fallbacks, s.scored_victims, s.score_layers,
-                            s.score_candidates, s.score_saturated, s.pred_invalid, s.predicted, s.predicted_true};
+                            s.score_candidates, s.score_saturated, s.pred_invalid, s.predicted, s.predicted_true,
+                            s.bank_kept, s.bank_keep_drops, s.bank_keep_rereads};
       const uint32_t m = uint32_t(sizeof v / sizeof v[0]);
       std::memcpy(counts, v, 8ull * (n_counts < m ? n_counts : m));
     }

@@ -250,11 +250,13 @@ class HipTransport final : public DgTransport {
     for (uint32_t i = 0; i < x_.S; ++i)
       stage_.push_back(static_cast<char*>(dev_->alloc_pinned(x_.host_stride, "disk staging buffer")));
     if (x_.disk_queue > 1) {
-      rword_host_ = static_cast<uint32_t*>(dev_->alloc_mapped(4ull * x_.S, &rword_dev_, "read words"));
-      std::memset(rword_host_, 0, 4ull * x_.S);
-      rgen_.assign(x_.S, 0);
-      rpending_.assign(x_.S, 0);
-      raux_.assign(x_.S, 0);
+      // one word per staging buffer, then (dg_bank_keep) one per bank slot for reads kept in a pinned block
+      const uint32_t words = x_.S + (x_.bank_keep ? 2 * x_.B : 0);
+      rword_host_ = static_cast<uint32_t*>(dev_->alloc_mapped(4ull * words, &rword_dev_, "read words"));
+      std::memset(rword_host_, 0, 4ull * words);
+      rgen_.assign(words, 0);
+      rpending_.assign(words, 0);
+      raux_.assign(words, 0);
       dw_ = dw;
       std::vector<ReadPool::Piece> pieces;  // 8 MiB slices of each part (4 KiB-aligned; the last one the rest)
       for (uint32_t p = 0; p < x_.part_bytes.size(); ++p)
@@ -264,9 +266,15 @@ class HipTransport final : public DgTransport {
                                          std::move(finisher));
     }
   }
-  // A file read into staging buffer `block`: synchronous, or queued to the pool (its copies then await its word).
-  void read_unit(uint32_t key, int32_t block) override {
-    require(reader_ && uint32_t(block) >= x_.blocks, SS_E_BACKEND, "device-gated: a file read outside the staging buffers");
+  // A file read into staging buffer `block`, or (dg_bank_keep) into pinned block `block` for bank slot `slot`:
+  // synchronous, or queued to the pool (the copy out of the block then awaits the read's word: a staging buffer's, or
+  // the bank slot's, which is reused only once the copy that awaited it last has run).
+  void read_unit(uint32_t key, int32_t block, int32_t slot) override {
+    const bool staged = uint32_t(block) >= x_.blocks;
+    const bool kept = !staged && x_.bank_keep && slot >= int32_t(x_.persistent_slots) &&
+                      uint32_t(slot) < x_.persistent_slots + 2 * x_.B;
+    require(reader_ && (staged || kept), SS_E_BACKEND,
+            "device-gated: a file read into neither a staging buffer nor a kept block");
     if (!pool_) {
       const auto t0 = Clock::now();
       reader_(key, block_ptr(block));
@@ -275,11 +283,12 @@ class HipTransport final : public DgTransport {
       read_wait_ns_ += ns;
       return;
     }
-    const uint32_t i = uint32_t(block) - x_.blocks;
+    const uint32_t i = staged ? uint32_t(block) - x_.blocks : x_.S + (uint32_t(slot) - x_.persistent_slots);
     if (++rgen_[i] == 0) rgen_[i] = 1;  // (0 is the word's initial value)
     rpending_[i] = rgen_[i];
     raux_[i] = uint32_t(std::upper_bound(x_.unit_base.begin(), x_.unit_base.end(), key) - x_.unit_base.begin()) - 1;
-    pool_->submit(key, stage_[i], rword_host_ + i, rgen_[i]);
+    if (!staged) kept_word_[block] = i;
+    pool_->submit(key, block_ptr(block), rword_host_ + i, rgen_[i]);
   }
   // Every read submitted so far has returned; rethrows the first failed read (the token fails before the layer whose
   // copies read it is signalled ready, so its bytes never reach an engine).
@@ -314,9 +323,18 @@ class HipTransport final : public DgTransport {
   }
   void h2d_unit(Stream s, int32_t slot, int32_t block) {
     const char* src = block_ptr(block);
-    if (pool_ && uint32_t(block) >= x_.blocks) {  // its read may still run: the stream waits for the read's word
-      const uint32_t i = uint32_t(block) - x_.blocks;
-      if (rpending_[i]) {
+    if (pool_) {  // a read into this block may still run: the stream waits for the read's word
+      uint32_t i = UINT32_MAX;
+      if (uint32_t(block) >= x_.blocks) {
+        i = uint32_t(block) - x_.blocks;
+      } else if (!kept_word_.empty()) {
+        const auto it = kept_word_.find(block);
+        if (it != kept_word_.end()) {
+          i = it->second;
+          kept_word_.erase(it);
+        }
+      }
+      if (i != UINT32_MAX && rpending_[i]) {
         const uint32_t* w = static_cast<const uint32_t*>(rword_dev_) + i;
         hip_check(hipError_t(dg_launch_await(dw_, w, rpending_[i], raux_[i], s_[s])), "await of a file read");
         rpending_[i] = 0;
@@ -695,7 +713,8 @@ class HipTransport final : public DgTransport {
   std::unique_ptr<ReadPool> pool_;                    // reads in flight (dg_disk_queue > 1)
   uint32_t* rword_host_ = nullptr;                    // per staging buffer: the generation of its last finished read
   void* rword_dev_ = nullptr;
-  std::vector<uint32_t> rgen_, rpending_, raux_;      // per staging buffer: last generation, one to await, its layer
+  std::vector<uint32_t> rgen_, rpending_, raux_;      // per read word: last generation, one to await, its layer
+  std::unordered_map<int32_t, uint32_t> kept_word_;   // dg_bank_keep: a pinned block read into -> its read's word
   DgDevWords dw_;                                     // the await kernel's abort words and deadline
   uint64_t read_ns_ = 0, read_wait_ns_ = 0;
   std::function<void(uint32_t, char*)> reader_;       // three-tier: a key's bytes from its file, host block layout
@@ -1139,6 +1158,7 @@ class HipDgCtx final : public DgCtx {
     TSA_D(disk_discards);
     TSA_D(clean_drops);
     TSA_D(clean_drop_bytes);
+    TSA_D(bank_kept);
     TSA_D(score_fallbacks);
     TSA_D(scored_victims);
     TSA_D(score_layers);
@@ -1208,7 +1228,10 @@ class HipDgCtx final : public DgCtx {
     hook_ = h;
     hook_user_ = user;
   }
-  Json stats_json() const override { return format_stats(stats(), exclusive_stats(), layers_now(), core_->policy()); }
+  Json stats_json() const override {
+    return format_stats(stats(), exclusive_stats(), layers_now(), core_->policy(),
+                        fold_.bank_keep_drops - base_.bank_keep_drops, fold_.bank_keep_rereads - base_.bank_keep_rereads);
+  }
   bool snapshot(ss_layer_stats* total, ss_snapshot_info* info) const override {
     snap_armed_.store(true, std::memory_order_relaxed);
     std::lock_guard<std::mutex> lk(snap_mu_);
@@ -1240,7 +1263,7 @@ class HipDgCtx final : public DgCtx {
       if (snap_.seq == 0) return false;
       p = snap_;
     }
-    *out = format_stats(p.s, p.x, p.layers, p.policy);
+    *out = format_stats(p.s, p.x, p.layers, p.policy, p.keep_drops, p.keep_rereads);
     return true;
   }
   // After a successful boundary (and at open): the core's counters as the stats show them, the hook with this
@@ -1381,6 +1404,7 @@ class HipDgCtx final : public DgCtx {
     ss_exclusive_stats x{};
     std::vector<ss_layer_stats> layers;
     uint32_t policy = 0;
+    uint64_t keep_drops = 0, keep_rereads = 0;  // (dg_bank_keep counters outside ss_dg_stats)
   };
   mutable std::atomic<bool> snap_armed_{false};
   mutable std::mutex snap_mu_;
@@ -1416,12 +1440,14 @@ class HipDgCtx final : public DgCtx {
     p.x = exclusive_stats();
     p.layers = layers_now();
     p.policy = core_->policy();  // (the engine thread's: a reader on another thread formats this copy)
+    p.keep_drops = fold_.bank_keep_drops - base_.bank_keep_drops;
+    p.keep_rereads = fold_.bank_keep_rereads - base_.bank_keep_rereads;
     std::lock_guard<std::mutex> lk(snap_mu_);
     p.seq = snap_.seq + 1;
     std::swap(snap_, p);
   }
   Json format_stats(const ss_dg_stats& s, const ss_exclusive_stats& x, const std::vector<ss_layer_stats>& layers,
-                    uint32_t policy) const;
+                    uint32_t policy, uint64_t s_keep_drops, uint64_t s_keep_rereads) const;
 };
 
 void HipDgCtx::init() {
@@ -1516,6 +1542,7 @@ void HipDgCtx::init() {
   c.home_blocks = x_.disk_tier ? x_.P : 0;
   c.disk_staging = x_.S;
   c.clean_evict = o_.dg_clean_evict != 0;
+  c.bank_keep = x_.bank_keep;
   c.scored = x_.scored;
   c.scored_auto = o_.policy == SS_POLICY_SCORED_AUTO;
   c.w_trans = x_.w_trans;
@@ -1577,7 +1604,8 @@ void HipDgCtx::init() {
 // are off; so are score_deferred and score_last_ns (this library ranks only at the boundary, where score_ns counts the
 // selection); backend is "hip".
 Json HipDgCtx::format_stats(const ss_dg_stats& s, const ss_exclusive_stats& x,
-                            const std::vector<ss_layer_stats>& layers, uint32_t pol) const {
+                            const std::vector<ss_layer_stats>& layers, uint32_t pol, uint64_t s_keep_drops,
+                            uint64_t s_keep_rereads) const {
   static const std::pair<const char*, uint64_t ss_dg_stats::*> kFields[] = {
       {"tokens", &ss_dg_stats::tokens}, {"lookups", &ss_dg_stats::lookups}, {"misses", &ss_dg_stats::misses},
       {"covered", &ss_dg_stats::covered}, {"fetched", &ss_dg_stats::fetched},
@@ -1685,9 +1713,9 @@ Json HipDgCtx::format_stats(const ss_dg_stats& s, const ss_exclusive_stats& x,
     for (const auto& f : kDiskFields) tt[f.first] = Json::number(s.*f.second);
     tt["unit_subread_bytes"] = Json::number(uint64_t(0));
     tt["clean_evict"] = Json::number(uint64_t(uint64_t(o_.dg_clean_evict != 0)));
-    tt["bank_keep"] = Json::number(uint64_t(0));
-    tt["bank_keep_drops"] = Json::number(uint64_t(0));
-    tt["bank_keep_rereads"] = Json::number(uint64_t(0));
+    tt["bank_keep"] = Json::number(uint64_t(o_.dg_bank_keep));
+    tt["bank_keep_drops"] = Json::number(s_keep_drops);
+    tt["bank_keep_rereads"] = Json::number(s_keep_rereads);
     tt["disk_queue"] = Json::number(uint64_t(uint64_t(x_.disk_queue)));
     tt["disk_queue_resolved"] = Json::number(uint64_t(uint64_t(x_.disk_queue)));
     tt["disk_locations"] = Json::number(uint64_t(uint64_t(x_.disk_tier ? 1 : 0)));

@@ -65,8 +65,8 @@ void check_options(const ss_options& o, const ss_budget& b) {
       {o.dg_landing_blocks && o.dg_disk_queue <= 1, SS_E_INVALID,
        "dg_landing_blocks needs dg_disk_queue > 1 (landing reads run on the reader threads)"},
       // valid for the reference, not served by this library
-      {o.dg_landing_blocks || o.dg_bank_keep || o.dg_disk_queue_adapt, SS_E_UNSUPPORTED,
-       "landings (dg_landing_*), dg_bank_keep and dg_disk_queue_adapt are not served by this library"},
+      {o.dg_landing_blocks || o.dg_disk_queue_adapt, SS_E_UNSUPPORTED,
+       "landings (dg_landing_*) and dg_disk_queue_adapt are not served by this library"},
       {o.dg_no_admit || o.dg_pf_revert_unused || o.dg_pf_strict_admit || o.dg_prior_len || o.dg_prior,
        SS_E_UNSUPPORTED, "dg_no_admit, dg_pf_revert_unused, dg_pf_strict_admit and priors are not served by this library"},
   };
@@ -153,6 +153,7 @@ void place_homes(const Desc& d, const Plan& p, const ss_options& o, DgGeometry& 
 void size_disk_tier(const ss_options& o, DgGeometry& x) {
   x.disk_tier = o.dg_disk_tier != 0;
   x.disk_prefetch = o.dg_disk_prefetch != 0;
+  x.bank_keep = x.disk_tier ? o.dg_bank_keep : 0;  // (no effect without the file tier)
   if (!x.disk_tier) return;
   if (o.dg_disk_queue == kQueueAuto) {
     constexpr uint32_t kLocations = 1;

@@ -5,8 +5,8 @@
 //
 // The rules are the reference's (src/dg_layout.cpp:159-180 and :182-393): the geometry is part of what an engine sees
 // (slot counts, the guard slot) and the refusals are part of the ABI. This library serves a subset of the reference's
-// options (landings, kept bank reads, the adaptive read depth, no-admit, prefetch revert, strict admission and priors
-// are refused with SS_E_UNSUPPORTED), and it does not re-check the host budget for its own control memory (an
+// options (landings, the adaptive read depth, no-admit, prefetch revert, strict admission and priors are refused
+// with SS_E_UNSUPPORTED), and it does not re-check the host budget for its own control memory (an
 // allocation that does not fit fails the open with SS_E_NOMEM).
 #pragma once
 
@@ -41,6 +41,7 @@ struct DgGeometry {
   uint32_t blocks = 0;           // P + Q
   std::vector<uint32_t> residents;  // keys of the planned residents, in key order
   bool disk_tier = false, disk_prefetch = false;
+  uint32_t bank_keep = 0;     // dg_bank_keep with the file tier (0 without it)
   std::vector<uint8_t> disk;  // per key: a file home (three tiers only)
   bool scored = false;
   uint32_t w_trans = 700, w_freq = 200, w_rec = 100;
