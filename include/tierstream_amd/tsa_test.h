@@ -84,6 +84,14 @@ SS_API ss_status tsa_test_dgcore_open(const tsa_test_dgcore_config* cfg, const u
 SS_API ss_status tsa_test_dgcore_token(void* h, const uint32_t* ids, uint32_t n, int32_t* table_out, uint64_t* counts,
                                        uint32_t n_counts);
 SS_API const char* tsa_test_dgcore_counter_names(void);
+/* dg_disk_queue_adapt's read-depth controller alone (no pool, no clock): n busy periods (reads[i], bytes[i], ns[i])
+ * fed in order; depth[i] = the depth after period i; counters[13] = changes, calibrations, windows, verdicts,
+ * reads_1, bytes_1, ns_1, reads_u, bytes_u, ns_u, depth, bound, calibrating; recent[16 * 7] = the last verdicts (seq,
+ * reads, from, to, GB/s at U, GB/s at 1, why: 0 start, 1 keep U, 2 keep 1, 3 split, 4 recheck, 5 drift); *n_recent
+ * their count. */
+SS_API ss_status tsa_test_depth_ctl(uint32_t bound, uint32_t n, const uint64_t* reads, const uint64_t* bytes,
+                                    const uint64_t* ns, uint32_t* depth, uint64_t* counters, double* recent,
+                                    uint32_t* n_recent);
 /* As tsa_test_dgcore_token with run [n_gated] (null: all): the gated layers the token exports (ss_begin's rows). */
 SS_API ss_status tsa_test_dgcore_token_run(void* h, const uint32_t* ids, uint32_t n, const uint8_t* run,
                                            int32_t* table_out, uint64_t* counts, uint32_t n_counts);

@@ -47,6 +47,7 @@
 #define protected public
 #include "dg_core.hpp"
 #include "dg_score.hpp"
+#include "dg_load.hpp"
 #include "stream_ctx.hpp"
 #include "dg_layout.hpp"
 #include "xxh64.hpp"
@@ -747,3 +748,27 @@ int refdg_cpu_baseline_disk(const uint32_t* n_units, uint32_t G, uint32_t persis
 }
 
 }  // extern "C"
+
+// The reference's read-depth controller (DgDepthCtl) fed n busy periods; outputs as tsa_test_depth_ctl.
+extern "C" int refdg_depth_ctl(uint32_t bound, uint32_t n, const uint64_t* reads, const uint64_t* bytes,
+                               const uint64_t* ns, uint32_t* depth, uint64_t* counters, double* recent,
+                               uint32_t* n_recent) {
+  try {
+    ts::DgDepthCtl c(bound);
+    for (uint32_t i = 0; i < n; ++i) depth[i] = c.on_busy(reads[i], bytes[i], ns[i]);
+    const uint64_t v[] = {c.changes, c.calibrations, c.windows, c.decisions(), c.reads1, c.bytes1, c.ns1,
+                          c.readsu, c.bytesu, c.nsu, c.depth(), c.bound(), uint64_t(c.calibrating())};
+    std::memcpy(counters, v, sizeof v);
+    uint32_t k = 0;
+    for (const ts::DgDepthCtl::Decision& d : c.ring()) {
+      const double r[] = {double(d.seq), double(d.reads), double(d.from), double(d.to), d.rate_u, d.rate_1,
+                          double(int(d.reason))};
+      std::memcpy(recent + 7 * k++, r, sizeof r);
+    }
+    *n_recent = k;
+    return 0;
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "refdg_depth_ctl: %s\n", e.what());
+    return 1;
+  }
+}

@@ -7,8 +7,8 @@ in flight, slot counts, guard slot, blocks and score weights.
 Configurations are drawn per seed around valid ones: layers and units, one to five parts (now and then not a multiple
 of 256, or five), the planner's tiers or explicit ones (with file homes), dynamic and explicit spare slots, ring slots
 around 2 x dg_max_ids + 1, spare blocks, clean copies, the file tier's options, the policy and its weights, and a broken
-option now and then (dg_bank_keep among them). Options the reference accepts but this library does not serve (landings,
-the adaptive read depth, no-admit, prefetch revert, strict admission) must be refused with SS_E_UNSUPPORTED."""
+option now and then (dg_bank_keep and dg_disk_queue_adapt among them). Options the reference accepts but this library does not serve
+(landings, no-admit, prefetch revert, strict admission) must be refused with SS_E_UNSUPPORTED."""
 import ctypes as C
 
 import numpy as np
@@ -21,7 +21,7 @@ KiB = 1024
 u32 = C.c_uint32
 FIELDS = ["keys", "G", "R", "D", "B", "P", "F", "Q", "I", "S", "disk_queue", "persistent_slots", "slots", "guard_slot",
           "blocks", "scored", "w_trans", "w_freq", "w_rec"]
-UNSERVED = ["dg_landing_blocks", "dg_disk_queue_adapt", "dg_no_admit", "dg_pf_revert_unused", "dg_pf_strict_admit"]
+UNSERVED = ["dg_landing_blocks", "dg_no_admit", "dg_pf_revert_unused", "dg_pf_strict_admit"]
 
 
 def _case(seed, tmp_path):
@@ -70,6 +70,10 @@ def _case(seed, tmp_path):
             okw.update(dg_score_w_trans=a, dg_score_w_freq=b - a, dg_score_w_recency=1000 - b + int(rng.random() < 0.1))
     if rng.random() < 0.15:
         okw.update(dg_bank_keep=int(rng.choice([0, 1, 2, 3])))
+    if rng.random() < 0.1:  # (valid with the file tier at the AUTO queue only)
+        okw.update(dg_disk_queue_adapt=int(rng.choice([1, 1, 2])))
+        if disk and rng.random() < 0.7:
+            okw.update(dg_disk_queue=0xFFFFFFFF)
     if rng.random() < 0.02:
         okw.update(dg_wb_defer=2)
     if rng.random() < 0.02:
@@ -78,8 +82,6 @@ def _case(seed, tmp_path):
     if rng.random() < 0.08:
         unserved = str(rng.choice(UNSERVED))
         okw[unserved] = 1
-        if unserved == "dg_disk_queue_adapt":
-            okw.update(dg_disk_tier=1, dg_disk_queue=0xFFFFFFFF)
         if unserved == "dg_landing_blocks":
             okw.update(dg_disk_tier=1, dg_disk_queue=4)
     return m, bkw, okw, tiers, unserved

@@ -396,11 +396,15 @@ def test_three_tier_read_failure_fails_the_token(tmp_path, gpu, queue):
 BIG_PARTS = (8 * 1024 * KiB + 64 * KiB, 64 * KiB, 4 * 1024 * KiB)
 
 
-@pytest.mark.parametrize("clean_evict,queue,parts,predict,bank_keep",
-                         [(0, 0, None, 0, 0), (1, 0, None, 0, 0), (0, 4, None, 0, 0), (1, 4, None, 0, 0),
-                          (0, 3, BIG_PARTS, 0, 0), (0, 4, None, 2, 0), (0, 0, None, 2, 0), (0, 0, None, 0, 1),
-                          (0, 4, None, 0, 2), (0, 3, BIG_PARTS, 0, 1), (0, 4, None, 2, 1)])
-def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, predict, bank_keep):
+AUTO = 0xFFFFFFFF  # SS_DG_DISK_QUEUE_AUTO: one read location resolves to 4 reads in flight
+
+
+@pytest.mark.parametrize("clean_evict,queue,parts,predict,bank_keep,adapt",
+                         [(0, 0, None, 0, 0, 0), (1, 0, None, 0, 0, 0), (0, 4, None, 0, 0, 0), (1, 4, None, 0, 0, 0),
+                          (0, 3, BIG_PARTS, 0, 0, 0), (0, 4, None, 2, 0, 0), (0, 0, None, 2, 0, 0),
+                          (0, 0, None, 0, 1, 0), (0, 4, None, 0, 2, 0), (0, 3, BIG_PARTS, 0, 1, 0),
+                          (0, 4, None, 2, 1, 0), (0, AUTO, BIG_PARTS, 0, 1, 1), (0, AUTO, None, 2, 0, 1)])
+def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, predict, bank_keep, adapt):
     """Three tiers (dg_disk_tier): 12 of 32 units resident, 10 pinned, 10 read from the file on a miss through staging
     buffers. The plan's tiers are given explicitly (a planner spill to the file tier leaves no room for spare blocks,
     as in the reference). Every token the slot table and the counters (file reads, drops of the pinned LRU to the
@@ -409,7 +413,8 @@ def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, 
     threads and each copy out of a staging buffer awaits its read on the device; the placement is the same. predict:
     the engine predicts the next layer's ids and dg_disk_prefetch lets a prefetch read a file-homed unit. bank_keep
     (dg_bank_keep 1 / 2): a bank-served file miss is read into a pinned block, which becomes its home (its
-    counters compared too)."""
+    counters compared too). adapt (dg_disk_queue_adapt at SS_DG_DISK_QUEUE_AUTO): the pool's depth follows its
+    measured throughput - the placement is the same; with file prefetches the open declines it."""
     parts = list(parts or (64 * KiB,) * 3)
     layers, units, n_ids, staging, dyn, spares = 4, 8, 2, 4, 1, 6
     m, tiers, bkw = _three_tier(tmp_path, parts)
@@ -430,7 +435,7 @@ def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, 
                                                       dg_disk_tier=1, dg_disk_staging=staging,
                                                       dg_clean_evict=clean_evict, dg_disk_queue=queue,
                                                       dg_disk_prefetch=dpf, dg_bank_keep=bank_keep,
-                                                      dg_wait_timeout_ms=5000))
+                                                      dg_disk_queue_adapt=adapt, dg_wait_timeout_ms=5000))
     eng = ss.DgEngine(ctx, n_ids, use_graph=True, n_pred=predict)
     routes = _routes(layers, units, n_ids, 24, seed=9, zipf=True)
     preds = _preds(routes, units, predict) if predict else None
@@ -454,14 +459,21 @@ def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, 
         assert got["disk_reads"] > 0 and (got["disk_drops"] + got["disk_discards"]) > 0, got
         if bank_keep:
             assert got["bank_kept"] > 0, got
-        assert got["disk_queue_resolved"] == max(queue, 1) and 1 <= got["disk_max_in_flight"] <= max(queue, 1), got
+        resolved = 4 if queue == AUTO else max(queue, 1)
+        assert got["disk_queue_resolved"] == resolved and 1 <= got["disk_max_in_flight"] <= resolved, got
+        assert got["disk_depth_adapt"] == (0 if not adapt else 2 if predict else 1), got
+        assert 1 <= got["disk_depth_active"] <= resolved, got
         assert got["disk_read_ns"] > 0 and got["disk_wait_ns"] > 0, got
         assert ctx.verify_failures() == 0
         _check_stats_doc(ctx, want, routes.shape[0])
         tt = json.loads(ctx.stats_json())["device_gated"]["three_tier"]
         for k in ("disk_reads", "disk_drops", "disk_discards", "clean_drops", "bank_kept"):
             assert tt[k] == got[k], k
-        assert tt["disk_queue_resolved"] == max(queue, 1) and tt["staging"] == staging
+        assert tt["disk_queue_resolved"] == resolved and tt["staging"] == staging
+        assert tt["disk_queue_adapt"] == ("off" if not adapt else "declined: file prefetches" if predict else "on")
+        if adapt and not predict:
+            dd = tt["disk_depth"]
+            assert dd["bound"] == 4 and dd["calibrations"] >= 1 and 1 <= dd["depth"] <= 4, dd
         assert tt["bank_keep"] == bank_keep and tt["bank_keep_drops"] == want["bank_keep_drops"]
         assert tt["bank_keep_rereads"] == want["bank_keep_rereads"]
     finally:

@@ -9,6 +9,7 @@
 
 #include "common.hpp"
 #include "dg_core.hpp"
+#include "depth_ctl.hpp"
 #include "score_profile.hpp"
 #include "sha256.hpp"
 #include "tierstream_amd/tsa_test.h"
@@ -233,3 +234,28 @@ uint32_t tsa_test_dgcore_host_order(void* h, uint32_t* out, uint32_t cap) {
 void tsa_test_dgcore_close(void* h) { delete static_cast<tsa::TestCore*>(h); }
 
 }  // extern "C"
+
+// ---- the read-depth controller alone ----------------------------------------------------------------------------------
+// n busy periods (reads[i], bytes[i], ns[i]) fed in order: depth[i] = the depth after period i; counters[13] =
+// changes, calibrations, windows, verdicts, reads_1, bytes_1, ns_1, reads_u, bytes_u, ns_u, depth, bound, calibrating;
+// recent[16 * 7] = the last verdicts (seq, reads, from, to, gbps_u, gbps_1, why) as doubles; *n_recent their count.
+extern "C" ss_status tsa_test_depth_ctl(uint32_t bound, uint32_t n, const uint64_t* reads, const uint64_t* bytes,
+                                        const uint64_t* ns, uint32_t* depth, uint64_t* counters, double* recent,
+                                        uint32_t* n_recent) {
+  return tsa::guard([&] {
+    tsa::require((n == 0 || (reads && bytes && ns && depth)) && counters && recent && n_recent, SS_E_INVALID,
+                 "tsa_test_depth_ctl: null argument");
+    tsa::ReadDepthController c(bound);
+    for (uint32_t i = 0; i < n; ++i) depth[i] = c.feed(reads[i], bytes[i], ns[i]);
+    const uint64_t v[] = {c.changes, c.calibrations, c.windows, c.verdicts(), c.reads_1, c.bytes_1, c.ns_1,
+                          c.reads_u, c.bytes_u, c.ns_u, c.depth(), c.bound(), uint64_t(c.calibrating())};
+    std::memcpy(counters, v, sizeof v);
+    uint32_t k = 0;
+    for (const tsa::ReadDepthController::Verdict& d : c.recent()) {
+      const double r[] = {double(d.seq), double(d.reads), double(d.from), double(d.to), d.gbps_u, d.gbps_1,
+                          double(int(d.why))};
+      std::memcpy(recent + 7 * k++, r, sizeof r);
+    }
+    *n_recent = k;
+  });
+}

@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "dg_core.hpp"
+#include "depth_ctl.hpp"
 #include "dg_geometry.hpp"
 #include "dg_proto.hpp"
 #include "hip_rt.hpp"
@@ -74,8 +75,22 @@ class ReadPool {
   using PieceReader = std::function<void(uint32_t key, uint32_t part, uint64_t off, uint64_t bytes, char* dst)>;
   using Finisher = std::function<void(uint32_t key, const char* block)>;
   ReadPool(uint32_t threads, std::vector<Piece> pieces, PieceReader read, Finisher finish)
-      : pieces_(std::move(pieces)), read_(std::move(read)), finish_(std::move(finish)) {
+      : pieces_(std::move(pieces)), read_(std::move(read)), finish_(std::move(finish)), threads_(threads),
+        limit_(threads) {
+    for (const Piece& pc : pieces_) unit_bytes_ += pc.bytes;
     for (uint32_t i = 0; i < threads; ++i) th_.emplace_back([this] { run(); });
+  }
+  // dg_disk_queue_adapt: pieces run at most depth() at a time, the depth chosen by a controller fed each busy period
+  // (from the first piece taken while idle to no piece queued or running: its whole units and their bytes).
+  void adapt() {
+    std::lock_guard<std::mutex> l(m_);
+    ctl_ = std::make_unique<ReadDepthController>(threads_);
+    limit_ = ctl_->depth();
+  }
+  // f(controller) under the pool's lock (no-op when not adapting)
+  void with_controller(const std::function<void(const ReadDepthController&)>& f) {
+    std::lock_guard<std::mutex> l(m_);
+    if (ctl_) f(*ctl_);
   }
   ~ReadPool() { stop(); }
   // The queued reads finish first; no piece is dropped.
@@ -137,11 +152,16 @@ class ReadPool {
       Job j;
       {
         std::unique_lock<std::mutex> l(m_);
-        cv_.wait(l, [this] { return stop_ || !q_.empty(); });
+        cv_.wait(l, [this] { return (stop_ && q_.empty()) || (!q_.empty() && running_ < limit_); });
         if (q_.empty()) return;  // stopping, nothing queued
         j = q_.front();
         q_.pop_front();
         max_running_ = std::max<uint64_t>(max_running_, ++running_);
+        if (ctl_ && !busy_) {  // a busy period begins
+          busy_ = true;
+          busy_t0_ = Clock::now();
+          busy_units_ = 0;
+        }
       }
       Unit& u = *j.unit;
       std::exception_ptr e;
@@ -159,6 +179,16 @@ class ReadPool {
         --running_;
         if (e && !err_) err_ = e;
         last = --u.left == 0;
+        if (ctl_ && busy_) {
+          busy_units_ += last;
+          if (running_ == 0 && q_.empty()) {  // idle again: the period's throughput picks the next depth
+            busy_ = false;
+            const uint64_t ns =
+                uint64_t(std::chrono::duration_cast<std::chrono::nanoseconds>(Clock::now() - busy_t0_).count());
+            limit_ = std::min(std::max<uint32_t>(ctl_->feed(busy_units_, busy_units_ * unit_bytes_, ns), 1), threads_);
+          }
+        }
+        if (ctl_) cv_.notify_all();  // (a piece slot is free under the depth limit)
       }
       if (!last) continue;
       try {  // every piece of the unit landed (or failed): the finisher, then the word
@@ -180,6 +210,12 @@ class ReadPool {
   std::deque<Job> q_;
   std::deque<Unit> units_;  // (stable addresses: jobs point at their unit)
   std::vector<std::thread> th_;
+  uint32_t threads_ = 0, limit_ = 0;  // readers; pieces that may run at once
+  uint64_t unit_bytes_ = 0;
+  std::unique_ptr<ReadDepthController> ctl_;  // dg_disk_queue_adapt
+  bool busy_ = false;
+  Clock::time_point busy_t0_{};
+  uint64_t busy_units_ = 0;
   uint64_t inflight_ = 0, running_ = 0, max_running_ = 0;
   std::atomic<uint64_t> read_ns_{0};
   std::exception_ptr err_;
@@ -294,6 +330,12 @@ class HipTransport final : public DgTransport {
   // copies read it is signalled ready, so its bytes never reach an engine).
   void drain_reads() {
     if (pool_) read_wait_ns_ += pool_->drain();
+  }
+  void adapt_reads() {
+    if (pool_) pool_->adapt();
+  }
+  void read_controller(const std::function<void(const ReadDepthController&)>& f) const {
+    if (pool_) pool_->with_controller(f);
   }
   void stop_reads() {
     if (pool_) pool_->stop();
@@ -1168,6 +1210,14 @@ class HipDgCtx final : public DgCtx {
 #undef TSA_D
     s.disk_units = fold_file_units_;
     s.disk_queue_resolved = x_.disk_tier ? x_.disk_queue : 0;
+    s.disk_depth_adapt = adapt_;
+    s.disk_depth_active = x_.disk_tier ? x_.disk_queue : 0;
+    if (adapt_ == 1)
+      tr_->read_controller([&](const ReadDepthController& c) {
+        s.disk_depth_active = c.depth();
+        s.disk_depth_changes = c.changes;
+        s.disk_depth_calibrations = c.calibrations;
+      });
     s.disk_locations = x_.disk_tier ? 1 : 0;
     s.disk_read_ns = fold_read_ns_ - base_read_ns_;
     s.disk_wait_ns = fold_wait_ns_ - base_wait_ns_;
@@ -1411,6 +1461,8 @@ class HipDgCtx final : public DgCtx {
   Published snap_;
   uint64_t verify_failures_ = 0;
   std::string score_prov_;  // the score profile's provenance (reported in the stats document)
+  uint32_t adapt_ = 0;      // dg_disk_queue_adapt: 0 off, 1 adapting, 2 declined (adapt_why_)
+  std::string adapt_why_;
 
   static void add_stats(ss_layer_stats& a, const ss_layer_stats& b) {
     a.routed += b.routed;
@@ -1563,6 +1615,14 @@ void HipDgCtx::init() {
           if (o_.verify_hash == 1) check_key(k, block);
         },
         dw_);
+  // dg_disk_queue_adapt (the open accepted it only with the file tier at SS_DG_DISK_QUEUE_AUTO): the pool's depth
+  // from its measured throughput, unless one reader or file prefetches make it moot (reference src/dg_ctx.cpp:1897)
+  if (o_.dg_disk_queue_adapt) {
+    adapt_ = 2;
+    if (x_.disk_queue <= 1) adapt_why_ = "one reader";
+    else if (x_.disk_prefetch) adapt_why_ = "file prefetches";
+    else adapt_ = 1, tr_->adapt_reads();
+  }
   // priority: the seed (validated), the plan's residents, then key order
   std::vector<uint32_t> order;
   for (uint32_t i = 0; i < o_.dg_seed_n; ++i) {
@@ -1722,7 +1782,31 @@ Json HipDgCtx::format_stats(const ss_dg_stats& s, const ss_exclusive_stats& x,
     tt["disk_units_open"] = Json::number(uint64_t(uint64_t(x_.F)));
     tt["staging"] = Json::number(uint64_t(uint64_t(x_.S)));
     tt["inclusive_blocks"] = Json::number(uint64_t(uint64_t(x_.I)));
-    tt["disk_queue_adapt"] = Json::string("off");
+    tt["disk_queue_adapt"] = Json::string(adapt_ == 1 ? "on" : adapt_ == 2 ? "declined: " + adapt_why_ : "off");
+    if (adapt_ == 1)
+      tr_->read_controller([&](const ReadDepthController& c) {
+        Json a = Json::object();
+        const std::pair<const char*, uint64_t> nums[] = {
+            {"depth", c.depth()}, {"bound", c.bound()}, {"calibrating", c.calibrating()}, {"changes", c.changes},
+            {"calibrations", c.calibrations}, {"windows", c.windows}, {"decisions", c.verdicts()},
+            {"reads_1", c.reads_1}, {"bytes_1", c.bytes_1}, {"busy_ns_1", c.ns_1}, {"reads_u", c.reads_u},
+            {"bytes_u", c.bytes_u}, {"busy_ns_u", c.ns_u}};
+        for (const auto& f : nums) a[f.first] = Json::number(f.second);
+        static const char* const why[] = {"start", "keep_u", "keep_1", "split", "recheck", "drift"};
+        a["ring"] = Json::array();
+        for (const ReadDepthController::Verdict& v : c.recent()) {
+          Json e = Json::object();
+          e["seq"] = Json::number(v.seq);
+          e["reads"] = Json::number(v.reads);
+          e["from"] = Json::number(uint64_t(v.from));
+          e["to"] = Json::number(uint64_t(v.to));
+          e["gbps_u"] = Json::number_f(v.gbps_u);  // (bytes / ns = GB/s)
+          e["gbps_1"] = Json::number_f(v.gbps_1);
+          e["reason"] = Json::string(why[int(v.why)]);
+          a["ring"].push(e);
+        }
+        tt["disk_depth"] = a;
+      });
     g["three_tier"] = tt;
   }
   j["device_gated"] = g;

@@ -65,8 +65,7 @@ void check_options(const ss_options& o, const ss_budget& b) {
       {o.dg_landing_blocks && o.dg_disk_queue <= 1, SS_E_INVALID,
        "dg_landing_blocks needs dg_disk_queue > 1 (landing reads run on the reader threads)"},
       // valid for the reference, not served by this library
-      {o.dg_landing_blocks || o.dg_disk_queue_adapt, SS_E_UNSUPPORTED,
-       "landings (dg_landing_*) and dg_disk_queue_adapt are not served by this library"},
+      {o.dg_landing_blocks != 0, SS_E_UNSUPPORTED, "landings (dg_landing_*) are not served by this library"},
       {o.dg_no_admit || o.dg_pf_revert_unused || o.dg_pf_strict_admit || o.dg_prior_len || o.dg_prior,
        SS_E_UNSUPPORTED, "dg_no_admit, dg_pf_revert_unused, dg_pf_strict_admit and priors are not served by this library"},
   };

@@ -5,8 +5,7 @@
 //
 // The rules are the reference's (src/dg_layout.cpp:159-180 and :182-393): the geometry is part of what an engine sees
 // (slot counts, the guard slot) and the refusals are part of the ABI. This library serves a subset of the reference's
-// options (landings, the adaptive read depth, no-admit, prefetch revert, strict admission and priors are refused
-// with SS_E_UNSUPPORTED), and it does not re-check the host budget for its own control memory (an
+// options (landings, no-admit, prefetch revert, strict admission and priors are refused with SS_E_UNSUPPORTED), and it does not re-check the host budget for its own control memory (an
 // allocation that does not fit fails the open with SS_E_NOMEM).
 #pragma once
 
