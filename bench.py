@@ -82,6 +82,12 @@ def parse():
     ap.add_argument("--policy", default="lru", choices=["lru", "scored", "auto"],
                     help="device-gated eviction policy (SS_POLICY_LRU / SCORED / SCORED_AUTO; default 700/200/100 "
                          "weights, no profile)")
+    ap.add_argument("--bank-keep", type=int, default=0, choices=[0, 1, 2],
+                    help="three tiers: dg_bank_keep (bank-served file misses kept in a pinned block)")
+    ap.add_argument("--disk-queue", type=int, default=-1,
+                    help="three tiers: dg_disk_queue (file reads in flight; -1: the workload's)")
+    ap.add_argument("--disk-adapt", action="store_true",
+                    help="three tiers: dg_disk_queue SS_DG_DISK_QUEUE_AUTO with dg_disk_queue_adapt")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the copy peaks and the library's HBM kernels alone (no serve loop: for counter runs)")
     return ap.parse_args()
@@ -209,12 +215,22 @@ def measure_disk(path, w, n_layers, threads=4, seconds=4.0):
     return out
 
 
-def measure_kernels(tsa, L, C, w, seg=8192, reps=10):
+def verify_seg_bytes(unit_bytes):
+    """The device check's checkpoint segment a context uses for this unit size: 8 KiB, halved down to 2 KiB while a
+    unit has fewer than 16,384 segments (the library's rule, tierstream_amd/csrc/dg_ctx.cpp verify_seg_bytes)."""
+    seg = 8192
+    while seg > 2048 and unit_bytes // seg < 16384:
+        seg //= 2
+    return seg
+
+
+def measure_kernels(tsa, L, C, w, seg=None, reps=10):
     """The library's HBM kernels alone at the workload's unit shape: the device XXH64 verify of one unit (checkpoints
     every `seg` bytes, computed on the host) and the unit scatter used as a plain copy of known size (one part of
     256 MiB: read 256 MiB, write 256 MiB), whose counters calibrate the traffic counters of the others."""
     parts = w.parts
     ub = w.unit_bytes
+    seg = seg or verify_seg_bytes(ub)
     bufs = []
     out = {}
     s, e0, e1 = C.c_void_p(), C.c_void_p(), C.c_void_p()
@@ -409,8 +425,15 @@ def main():
             log(f"file tier drive: {disk_peak}")
         t0 = time.time()
         policy = {"lru": 0, "scored": 1, "auto": 2}[a.policy]
-        ctx = keep(ss.Ctx(d, b, plan, ss.options(**shape.options, verify_hash=2, dg_wait_timeout_ms=20000,
-                                                 policy=policy)))
+        extra = {}
+        if three and a.bank_keep:
+            extra["dg_bank_keep"] = a.bank_keep
+        if three and a.disk_queue >= 0:
+            extra["dg_disk_queue"] = a.disk_queue
+        if three and a.disk_adapt:
+            extra.update(dg_disk_queue=0xFFFFFFFF, dg_disk_queue_adapt=1)
+        opts = {**shape.options, **extra}
+        ctx = keep(ss.Ctx(d, b, plan, ss.options(**opts, verify_hash=2, dg_wait_timeout_ms=20000, policy=policy)))
         log(f"context open (fill + hash check) in {time.time() - t0:.1f} s")
         eng = keep(ss.DgEngine(ctx, shape.B, use_graph=True))
         G = eng.G
@@ -472,13 +495,17 @@ def main():
                  "inclusive_kept", "inclusive_drops", "miss_layers", "wb_forced", "collected_mid", "stalled"]
         if three:
             dkeys += ["disk_reads", "disk_read_bytes", "disk_read_ns", "disk_wait_ns", "disk_stage_waits",
-                      "disk_drops", "disk_discards", "clean_drops"]
+                      "disk_drops", "disk_discards", "clean_drops", "bank_kept"]
         if policy:
             dkeys += ["scored_victims", "score_layers", "score_candidates", "score_ns", "score_fallbacks"]
         dstat = {k: s1[k] - s0[k] for k in dkeys}
         if three:
             dstat["disk_max_in_flight"] = s1["disk_max_in_flight"]
             dstat["disk_queue_resolved"] = s1["disk_queue_resolved"]
+            dstat["disk_depth_adapt"] = s1["disk_depth_adapt"]
+            dstat["disk_depth_active"] = s1["disk_depth_active"]
+            dstat["disk_depth_changes"] = s1["disk_depth_changes"]
+            dstat["disk_depth_calibrations"] = s1["disk_depth_calibrations"]
         failures = ctx.verify_failures()
         eng.close()
         ctx.close()
@@ -514,6 +541,7 @@ def main():
                                    + (f"; {w.layers} of the full model's {W.WORKLOADS[w.name].layers} layers"
                                       if w.layers != W.WORKLOADS[w.name].layers else ""),
                        "policy": a.policy,
+                       "options": {k: v for k, v in extra.items()},
                        "residency": f"{n_res} of {w.n_units} units resident ({100 * n_res / w.n_units:.0f} %); device "
                                     f"arena {shape.R + shape.D + 2 * shape.B + 1} of {w.n_units} unit slots (residents "
                                     f"R {shape.R} + spares D {shape.D} + two banks of {shape.B} + the guard slot)",

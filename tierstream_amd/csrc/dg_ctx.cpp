@@ -34,7 +34,14 @@ using Clock = std::chrono::steady_clock;
 // device-verify checkpoint spacing: 8 KiB gives one 336 MiB unit 43,008 independent segments, one lane-quad each
 // (2,688 wavefronts), enough to keep every SIMD of the chip busy in one launch; the checkpoints cost 32 bytes per
 // segment (0.4 % of the unit) in HBM
-constexpr uint64_t kSegBytes = 8 * 1024;
+// The device check's checkpoint segment: 8 KiB, halved (down to 2 KiB) while one unit has fewer than 16,384
+// segments - a quad of lanes per segment, so that one unit's check is at least 4 waves per CU of a 256-CU chip
+// (checkpoints cost 32 B per segment: 0.4 % of the unit's bytes at 8 KiB, 1.6 % at 2 KiB).
+uint64_t verify_seg_bytes(uint64_t unit_bytes) {
+  uint64_t seg = 8 * 1024;
+  while (seg > 2 * 1024 && unit_bytes / seg < 16384) seg /= 2;
+  return seg;
+}
 constexpr uint64_t kScatterBelow = 8ull << 20;     // parts smaller than this land staged + scattered
 constexpr uint64_t kReadPiece = 8ull << 20;        // three-tier reads in flight: the largest piece one reader reads
 
@@ -519,7 +526,8 @@ class HipTransport final : public DgTransport {
     hip_check(hipMemset(vfail_dev_, 0, 4ull * vcap_), "hipMemset");
     vs_ = dev_->stream_create_dedicated();
     DgVerifyLaunch& a = vlaunch_;
-    require(set_dg_verify_shape(a, arena_.data(), x_.part_bytes.data(), uint32_t(x_.part_bytes.size()), kSegBytes) &&
+    require(set_dg_verify_shape(a, arena_.data(), x_.part_bytes.data(), uint32_t(x_.part_bytes.size()),
+                                verify_seg_bytes(x_.unit_bytes)) &&
                 a.unit_segs == n_ckpt && a.unit_bytes == x_.unit_bytes,
             SS_E_BACKEND, "device verify: the parts' segments disagree with the checkpoint count");
     a.ckpt = ckpt_dev;
@@ -1859,7 +1867,7 @@ void HipDgCtx::fill() {
   uint64_t n_ckpt = 0;
   std::vector<uint64_t> ckpt_host;
   if (dverify) {
-    n_ckpt = tsa_checkpoint_count(x_.part_bytes.data(), uint32_t(x_.part_bytes.size()), kSegBytes);
+    n_ckpt = tsa_checkpoint_count(x_.part_bytes.data(), uint32_t(x_.part_bytes.size()), verify_seg_bytes(x_.unit_bytes));
     ckpt_dev_ = static_cast<uint64_t*>(dev_->alloc_device(uint64_t(x_.keys) * n_ckpt * 32, "verify checkpoints"));
     ckpt_host.assign(size_t(uint64_t(x_.keys) * n_ckpt * 4), 0);
   }
@@ -1910,7 +1918,8 @@ void HipDgCtx::fill() {
           hu.n_ext = uint32_t(x_.part_bytes.size());
           uint64_t dig = 0;
           if (dverify) {
-            const ss_status s = tsa_xxh64_checkpoints(&hu, kSegBytes, ckpt_host.data() + uint64_t(k) * n_ckpt * 4,
+            const ss_status s = tsa_xxh64_checkpoints(&hu, verify_seg_bytes(x_.unit_bytes),
+                                                      ckpt_host.data() + uint64_t(k) * n_ckpt * 4,
                                                       n_ckpt, &dig);
             require(s == SS_OK, s, "device-gated: checkpoints of a unit");
           } else {
