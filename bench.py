@@ -88,6 +88,12 @@ def parse():
                     help="three tiers: dg_disk_queue (file reads in flight; -1: the workload's)")
     ap.add_argument("--disk-adapt", action="store_true",
                     help="three tiers: dg_disk_queue SS_DG_DISK_QUEUE_AUTO with dg_disk_queue_adapt")
+    ap.add_argument("--predict", type=float, default=0.0,
+                    help="device-gated: the engine predicts the next layer's ids (ss_dg_enqueue_predict), each of the "
+                         "true ids with this probability and a random unit otherwise (0: no predictions)")
+    ap.add_argument("--landing-blocks", type=int, default=0,
+                    help="three tiers: dg_landing_blocks (predicted file-homed units read ahead into landing blocks)")
+    ap.add_argument("--landing-ttl", type=int, default=0, help="three tiers: dg_landing_ttl")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the copy peaks and the library's HBM kernels alone (no serve loop: for counter runs)")
     return ap.parse_args()
@@ -410,6 +416,8 @@ def main():
             files.append((cold_path, cold, w.layers - cold))
         log(f"sources written in {time.time() - t0:.1f} s")
         d = keep(ss.Desc(W.desc_json(w, files, hashes)))
+        if three and a.landing_blocks:  # the landing blocks are pinned on top of the plan
+            shape.budget["host_pinned_bytes"] += a.landing_blocks * ((w.unit_bytes + 4095) // 4096 * 4096)
         b = ss.budget(**shape.budget)
         plan = keep(ss.Plan(d, b, tiers=shape.tiers) if three else ss.Plan(d, b))
         tiers = plan.tiers()
@@ -432,13 +440,24 @@ def main():
             extra["dg_disk_queue"] = a.disk_queue
         if three and a.disk_adapt:
             extra.update(dg_disk_queue=0xFFFFFFFF, dg_disk_queue_adapt=1)
+        if three and a.landing_blocks:
+            extra.update(dg_landing_blocks=a.landing_blocks, dg_landing_ttl=a.landing_ttl)
         opts = {**shape.options, **extra}
         ctx = keep(ss.Ctx(d, b, plan, ss.options(**opts, verify_hash=2, dg_wait_timeout_ms=20000, policy=policy)))
         log(f"context open (fill + hash check) in {time.time() - t0:.1f} s")
-        eng = keep(ss.DgEngine(ctx, shape.B, use_graph=True))
+        n_pred = shape.B if a.predict > 0 else 0
+        eng = keep(ss.DgEngine(ctx, shape.B, use_graph=True, n_pred=n_pred))
         G = eng.G
         steps, warm, probe = a.steps, a.warmup, a.probe_tokens
         routes = W.route_stream(w, warm + steps + probe)[:, :, :shape.B]
+        preds = None
+        if n_pred:  # row g: layer g + 1's ids, each kept with probability --predict, else a random unit
+            prng = np.random.default_rng(w.seed + 17)
+            preds = np.zeros((routes.shape[0], G, n_pred), dtype=np.int32)
+            preds[:, :-1] = routes[:, 1:, :n_pred]
+            miss = prng.random(preds.shape) >= a.predict
+            preds[miss] = prng.integers(0, w.units, size=int(miss.sum()))
+            preds[:, -1] = 0
         ck_seen, ck_bad = {}, 0
 
         def check_cks(t, cks):
@@ -450,8 +469,11 @@ def main():
                     if ck_seen.setdefault(k, v) != v:
                         ck_bad += 1
 
+        def pred_of(t):
+            return preds[t] if preds is not None else None
+
         for t in range(warm):
-            cks, _ = eng.token(routes[t])
+            cks, _ = eng.token(routes[t], preds=pred_of(t))
             check_cks(t, cks)
         # the timed region brackets only the verify launches (their own dispatch stamps: no extra stream work); the
         # copies and write-backs are bracketed in the probe tokens after it
@@ -461,7 +483,7 @@ def main():
         lat = np.zeros(steps)
         t_start = time.perf_counter()
         for i in range(steps):
-            cks, lat[i] = eng.token(routes[warm + i])
+            cks, lat[i] = eng.token(routes[warm + i], preds=pred_of(warm + i))
             check_cks(warm + i, cks)
         tsa.check(L.tsa_device_sync())
         wall = time.perf_counter() - t_start
@@ -476,7 +498,7 @@ def main():
         ctx.profile_enable(ctx.PROF_COPY | ctx.PROF_WRITEBACK)
         for i in range(probe):
             t = warm + steps + i
-            cks, _ = eng.token(routes[t])
+            cks, _ = eng.token(routes[t], preds=pred_of(t))
             check_cks(t, cks)
             st = ctx.dg_stamps().astype(np.int64)
             start = eng.stamps().astype(np.int64)
@@ -498,6 +520,12 @@ def main():
                       "disk_drops", "disk_discards", "clean_drops", "bank_kept"]
         if policy:
             dkeys += ["scored_victims", "score_layers", "score_candidates", "score_ns", "score_fallbacks"]
+        if n_pred:
+            dkeys += ["predicted", "predicted_true", "prefetched", "prefetch_used"]
+        if three and a.landing_blocks:
+            dkeys += ["landing_issued", "landing_promoted", "landing_late", "landing_expired", "landing_expired_layer",
+                      "landing_dropped_full", "landing_read_bytes", "landing_cancelled", "landing_yields",
+                      "landing_aborted_bytes", "landing_wait_ns"]
         dstat = {k: s1[k] - s0[k] for k in dkeys}
         if three:
             dstat["disk_max_in_flight"] = s1["disk_max_in_flight"]
@@ -542,6 +570,7 @@ def main():
                                       if w.layers != W.WORKLOADS[w.name].layers else ""),
                        "policy": a.policy,
                        "options": {k: v for k, v in extra.items()},
+                       "predict": a.predict,
                        "residency": f"{n_res} of {w.n_units} units resident ({100 * n_res / w.n_units:.0f} %); device "
                                     f"arena {shape.R + shape.D + 2 * shape.B + 1} of {w.n_units} unit slots (residents "
                                     f"R {shape.R} + spares D {shape.D} + two banks of {shape.B} + the guard slot)",

@@ -77,6 +77,8 @@ typedef struct tsa_test_dgcore_config {
   const uint32_t* score_cells;
   /* appended: dg_bank_keep (0, 1, 2; three-tier only) */
   uint32_t bank_keep;
+  /* appended: dg_landing_blocks and dg_landing_ttl (three-tier only; 0 blocks: no landing) */
+  uint32_t landing_blocks, landing_ttl;
 } tsa_test_dgcore_config;
 SS_API ss_status tsa_test_dgcore_open(const tsa_test_dgcore_config* cfg, const uint32_t* order, uint32_t n_order,
                                       void** out);
@@ -92,6 +94,11 @@ SS_API const char* tsa_test_dgcore_counter_names(void);
 SS_API ss_status tsa_test_depth_ctl(uint32_t bound, uint32_t n, const uint64_t* reads, const uint64_t* bytes,
                                     const uint64_t* ns, uint32_t* depth, uint64_t* counters, double* recent,
                                     uint32_t* n_recent);
+/* The three-tier read pool alone (no device, no file): scenario 0..9 on a pool whose reader blocks each unit's pieces
+ * behind a gate the scenario opens - demand reads before landing reads, the landing cap, the reader kept free of
+ * landing reads, a drop (cancelled, cut short), a claim, failures, a yield, whole landing reads, stop, one read per
+ * word. SS_OK when the scenario's checks hold, else SS_E_BACKEND with the failed check in msg. */
+SS_API ss_status tsa_test_read_pool(uint32_t scenario, char* msg, uint32_t cap);
 /* As tsa_test_dgcore_token with run [n_gated] (null: all): the gated layers the token exports (ss_begin's rows). */
 SS_API ss_status tsa_test_dgcore_token_run(void* h, const uint32_t* ids, uint32_t n, const uint8_t* run,
                                            int32_t* table_out, uint64_t* counts, uint32_t n_counts);
@@ -118,9 +125,10 @@ SS_API ss_status tsa_test_hostplace_run(const char* desc_json, size_t len, const
                                         int32_t* spot_kind, int32_t* spot_index, int32_t* group_of,
                                         ss_layer_stats* stats);
 /* The device-gated open's geometry alone (no device): the descriptor, the budget and the plan (tiers, one per unit in
- * descriptor order; NULL: plan_make) under the options. out[0..18]: keys, gated layers, R, D, B, P, F, Q, I, staging
- * buffers, disk queue, persistent slots, slots, guard slot, blocks, scored, w_trans, w_freq, w_rec; residents: the
- * planned residents' keys (up to res_cap). A refused configuration returns its status. */
+ * descriptor order; NULL: plan_make) under the options. out[0..22]: keys, gated layers, R, D, B, P, F, Q, I, staging
+ * buffers, disk queue, persistent slots, slots, guard slot, blocks, scored, w_trans, w_freq, w_rec, landing blocks,
+ * landing pieces running at most, landing TTL, landing piece bytes (0: one per part); residents: the planned
+ * residents' keys (up to res_cap). A refused configuration returns its status. */
 SS_API ss_status tsa_test_dg_geometry(const char* desc_json, size_t len, const ss_budget* budget, const uint8_t* tiers,
                                       size_t n_tiers, const ss_options* opt, uint32_t* out, uint32_t* residents,
                                       uint32_t res_cap);
@@ -137,6 +145,8 @@ SS_API ss_status tsa_test_score_profile_check(const void* data, uint64_t len, co
                                               const unsigned char* identity, char* prov, uint32_t prov_cap);
 /* Three-tier: the pinned homes, most recently homed first; the return is the count. */
 SS_API uint32_t tsa_test_dgcore_host_order(void* h, uint32_t* out, uint32_t cap);
+/* Landings: per landing block the key it holds (0xFFFFFFFF: none); the return is the landing blocks. */
+SS_API uint32_t tsa_test_dgcore_land_owner(void* h, uint32_t* out, uint32_t cap);
 SS_API void tsa_test_dgcore_close(void* h);
 
 #ifdef __cplusplus

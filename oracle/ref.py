@@ -69,6 +69,10 @@ def lib() -> C.CDLL:
                                      C.POINTER(u32), u32, u32, u32, u32, u32, C.POINTER(C.c_uint8)]),
             "refdg_open_disk_keep": (vp, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, C.POINTER(u64), u32,
                                           C.POINTER(u32), u32, u32, u32, u32, u32, C.POINTER(C.c_uint8), u32]),
+            "refdg_open_disk_land": (vp, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, C.POINTER(u64), u32,
+                                          C.POINTER(u32), u32, u32, u32, u32, u32, C.POINTER(C.c_uint8), u32, u32,
+                                          u32]),
+            "refdg_land_owner": (u32, [vp, C.POINTER(u32), u32]),
             "refdg_open_scored": (vp, [C.POINTER(u32), u32, u32, u32, u32, u32, u32, u32, C.POINTER(u64), u32,
                                        C.POINTER(u32), u32, u32, u32, u32, u32, u32, C.POINTER(u32), u32, u32, u32,
                                        C.POINTER(C.c_uint8)]),
@@ -242,7 +246,7 @@ class RefDg:
     def __init__(self, n_units, persistent, bank, blocks, spare_target, part_bytes, order, prefetch_reserve=0xFFFFFFFF,
                  pf_layer=4, pf_token=48, wb_defer=1, wb_on_d2h=1, inclusive=0, disk=None, score=None):
         """disk (three-tier): dict(flags=[keys] 0/1 file-tier, home_blocks=P, disk_staging=S, clean_evict=0,
-        disk_prefetch=0, bank_keep=0); the prefetch budgets then take their defaults. score (scored eviction): dict(policy=1 SCORED
+        disk_prefetch=0, bank_keep=0, landing_blocks=0, landing_ttl=0); the prefetch budgets then take their defaults. score (scored eviction): dict(policy=1 SCORED
         or 2 SCORED_AUTO, w=(w_trans, w_freq, w_rec), rows=verify rows per boundary, cells=None or the starting
         transition counts, per gated layer units^2 row-major, concatenated); the prefetch budgets take their defaults
         and disk prefetch stays off."""
@@ -265,10 +269,11 @@ class RefDg:
                                   pf_token, wb_defer, wb_on_d2h, inclusive, pb, len(part_bytes), od, len(order))
         else:
             fl = (C.c_uint8 * sum(n_units))(*disk["flags"])
-            self.h = L.refdg_open_disk_keep(nu, len(n_units), persistent, bank, blocks, spare_target, wb_defer,
+            self.h = L.refdg_open_disk_land(nu, len(n_units), persistent, bank, blocks, spare_target, wb_defer,
                                             inclusive, pb, len(part_bytes), od, len(order), disk["home_blocks"],
                                             disk["disk_staging"], disk.get("clean_evict", 0),
-                                            disk.get("disk_prefetch", 0), fl, disk.get("bank_keep", 0))
+                                            disk.get("disk_prefetch", 0), fl, disk.get("bank_keep", 0),
+                                            disk.get("landing_blocks", 0), disk.get("landing_ttl", 0))
         if not self.h:
             raise RuntimeError("refdg_open failed")
         self.keys = sum(n_units)
@@ -315,6 +320,12 @@ class RefDg:
         """Three-tier: the pinned homes, most recently homed first."""
         out = np.zeros(self.keys, dtype=np.uint32)
         n = lib().refdg_host_order(self.h, out.ctypes.data_as(C.POINTER(u32)), self.keys)
+        return [int(x) for x in out[:n]]
+
+    def land_owner(self):
+        """Landings: per landing block the key it holds (0xFFFFFFFF: none)."""
+        out = np.zeros(4096, dtype=np.uint32)
+        n = lib().refdg_land_owner(self.h, out.ctypes.data_as(C.POINTER(u32)), 4096)
         return [int(x) for x in out[:n]]
 
     def close(self):

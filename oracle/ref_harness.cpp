@@ -137,6 +137,7 @@ extern "C" {
 // disk_staging buffers, the file-tier flags of the keys (keys entries, key order), clean_evict, disk_prefetch.
 struct RefDiskOpts {
   uint32_t disk_tier = 0, home_blocks = 0, disk_staging = 0, clean_evict = 0, disk_prefetch = 0, bank_keep = 0;
+  uint32_t landing_blocks = 0, landing_ttl = 0;
   const uint8_t* disk = nullptr;
 };
 // Scored eviction options of refdg_open (policy 0 = LRU: none of the others is read): policy 1 SCORED / 2 SCORED_AUTO,
@@ -172,6 +173,26 @@ void* refdg_open_disk(const uint32_t* n_units, uint32_t G, uint32_t persistent, 
   dk.clean_evict = clean_evict;
   dk.disk_prefetch = disk_prefetch;
   dk.disk = disk;
+  return refdg_open_impl(n_units, G, persistent, bank, blocks, spare_target, 0xFFFFFFFFu, 4, 48, wb_defer, 1, inclusive,
+                         part_bytes, n_parts, order, n_order, dk);
+}
+
+// refdg_open_disk with dg_bank_keep (0, 1, 2) and landings (landing_blocks 0: none; landing_ttl).
+void* refdg_open_disk_land(const uint32_t* n_units, uint32_t G, uint32_t persistent, uint32_t bank, uint32_t blocks,
+                           uint32_t spare_target, uint32_t wb_defer, uint32_t inclusive, const uint64_t* part_bytes,
+                           uint32_t n_parts, const uint32_t* order, uint32_t n_order, uint32_t home_blocks,
+                           uint32_t disk_staging, uint32_t clean_evict, uint32_t disk_prefetch, const uint8_t* disk,
+                           uint32_t bank_keep, uint32_t landing_blocks, uint32_t landing_ttl) {
+  RefDiskOpts dk;
+  dk.disk_tier = 1;
+  dk.home_blocks = home_blocks;
+  dk.disk_staging = disk_staging;
+  dk.clean_evict = clean_evict;
+  dk.disk_prefetch = disk_prefetch;
+  dk.disk = disk;
+  dk.bank_keep = bank_keep;
+  dk.landing_blocks = landing_blocks;
+  dk.landing_ttl = landing_ttl;
   return refdg_open_impl(n_units, G, persistent, bank, blocks, spare_target, 0xFFFFFFFFu, 4, 48, wb_defer, 1, inclusive,
                          part_bytes, n_parts, order, n_order, dk);
 }
@@ -297,6 +318,8 @@ void* refdg_open_impl(const uint32_t* n_units, uint32_t G, uint32_t persistent, 
       c.disk_queue = 1;
       c.clean_evict = dk.clean_evict != 0;
       c.bank_keep = dk.bank_keep;
+      c.landing_blocks = dk.landing_blocks;
+      c.landing_ttl = dk.landing_ttl;
       uint32_t keys = 0;
       for (uint32_t g = 0; g < G; ++g) keys += n_units[g];
       disk.assign(dk.disk, dk.disk + keys);
@@ -378,7 +401,10 @@ int refdg_token_run(void* h, const uint32_t* ids, uint32_t n, const uint32_t* pr
                           uint64_t(c.on_device()), uint64_t(c.backed_units()), s.disk_reads, s.disk_drops,
                           s.disk_discards, s.clean_drops, uint64_t(c.file_units()), s.score_fallbacks,
                           s.scored_victims, s.score_layers, s.score_candidates, s.score_saturated, s.bank_kept,
-                          s.bank_keep_drops, s.bank_keep_rereads};
+                          s.bank_keep_drops, s.bank_keep_rereads, s.landing_issued, s.landing_promoted,
+                          s.landing_expired, s.landing_expired_layer, s.landing_dropped_full,
+                          s.landing_skipped_passed, s.landing_read_bytes, uint64_t(c.landing_units()),
+                          uint64_t(c.landing_free()), s.landing_late, s.landing_cancelled, s.landing_failed};
     std::memcpy(counts, v, sizeof v);
     return 0;
   } catch (const std::exception& e) {
@@ -393,13 +419,22 @@ const char* refdg_counter_names() {
          "wb_forced wb_boundary_flushed wb_issued_bytes wb_cancelled_bytes inclusive_kept inclusive_drops free_slots "
          "free_blocks on_device backed_units disk_reads disk_drops disk_discards clean_drops file_units "
          "score_fallbacks scored_victims score_layers score_candidates score_saturated bank_kept bank_keep_drops "
-         "bank_keep_rereads";
+         "bank_keep_rereads landing_issued landing_promoted landing_expired landing_expired_layer "
+         "landing_dropped_full landing_skipped_passed landing_read_bytes landing_units landing_free landing_late "
+         "landing_cancelled landing_failed";
 }
 
 // The device keys in recency order, most recent first.
 uint32_t refdg_residency(void* h, uint32_t* out, uint32_t cap) {
   auto* r = static_cast<RefDg*>(h);
   const std::vector<uint32_t> v = r->core->residency();
+  for (uint32_t i = 0; i < cap && i < v.size(); ++i) out[i] = v[i];
+  return uint32_t(v.size());
+}
+
+// Landings: per landing block the key it holds (0xFFFFFFFF: none).
+uint32_t refdg_land_owner(void* h, uint32_t* out, uint32_t cap) {
+  const auto& v = static_cast<RefDg*>(h)->core->land_owner_;
   for (uint32_t i = 0; i < cap && i < v.size(); ++i) out[i] = v[i];
   return uint32_t(v.size());
 }
@@ -439,8 +474,9 @@ void refdg_close(void* h) { delete static_cast<RefDg*>(h); }
 extern "C" {
 
 // The reference's dg_layout over a descriptor, a budget, the plan (tiers, one per unit; null: plan_make) and the
-// options. Returns the refusal's status (0 = laid out); out[0..18]: keys, G, R, D, B, P, F, Q, I, S, disk_queue,
-// persistent_slots, slots, guard_slot, blocks, scored, w_trans, w_freq, w_rec; residents: the tier-R keys.
+// options. Returns the refusal's status (0 = laid out); out[0..22]: keys, G, R, D, B, P, F, Q, I, S, disk_queue,
+// persistent_slots, slots, guard_slot, blocks, scored, w_trans, w_freq, w_rec, L, landing_queued, landing_ttl,
+// landing_chunk; residents: the tier-R keys.
 int ref_dg_layout(const char* desc_json, size_t len, const ss_budget* b, const uint8_t* tiers, size_t n_tiers,
                   const ss_options* o, uint32_t* out, uint32_t* residents, uint32_t res_cap, char* err, size_t err_cap) {
   try {
@@ -450,7 +486,7 @@ int ref_dg_layout(const char* desc_json, size_t len, const ss_budget* b, const u
     const ts::DgLayout x = ts::dg_layout(d, p, *o);
     const uint32_t v[] = {x.keys, uint32_t(x.gated.size()), x.R, x.D, x.B, x.P, x.F, x.Q, x.I, x.S, x.disk_queue,
                           x.persistent_slots, x.slots, x.guard_slot, x.blocks, uint32_t(x.scored), x.w_trans,
-                          x.w_freq, x.w_rec};
+                          x.w_freq, x.w_rec, x.L, x.landing_queued, x.landing_ttl, x.landing_chunk};
     std::memcpy(out, v, sizeof v);
     for (uint32_t i = 0; i < res_cap && i < x.residents.size(); ++i) residents[i] = x.residents[i];
     return 0;

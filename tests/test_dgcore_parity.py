@@ -27,7 +27,8 @@ class DgCoreConfig(C.Structure):
                 ("part_bytes", C.POINTER(u64)), ("n_parts", u32), ("disk_tier", u32), ("home_blocks", u32),
                 ("disk_staging", u32), ("clean_evict", u32), ("disk_prefetch", u32),
                 ("disk", C.POINTER(C.c_uint8)), ("policy", u32), ("w_trans", u32), ("w_freq", u32), ("w_rec", u32),
-                ("rows", u32), ("score_cells", C.POINTER(u32)), ("bank_keep", u32)]
+                ("rows", u32), ("score_cells", C.POINTER(u32)), ("bank_keep", u32), ("landing_blocks", u32),
+                ("landing_ttl", u32)]
 
 
 def _lib():
@@ -40,6 +41,8 @@ def _lib():
     L.tsa_test_dgcore_counter_names.restype = C.c_char_p
     L.tsa_test_dgcore_host_order.argtypes = [C.c_void_p, C.POINTER(u32), u32]
     L.tsa_test_dgcore_host_order.restype = u32
+    L.tsa_test_dgcore_land_owner.argtypes = [C.c_void_p, C.POINTER(u32), u32]
+    L.tsa_test_dgcore_land_owner.restype = u32
     L.tsa_test_dgcore_close.argtypes = [C.c_void_p]
     L.tsa_test_dgcore_close.restype = None
     L.tsa_test_dgcore_token_run.argtypes = [C.c_void_p, C.POINTER(u32), u32, C.POINTER(C.c_uint8),
@@ -76,6 +79,7 @@ class OurCore:
             c.disk_tier, c.home_blocks, c.disk_staging = 1, disk["home_blocks"], disk["disk_staging"]
             c.clean_evict, c.disk_prefetch, c.disk = disk.get("clean_evict", 0), disk.get("disk_prefetch", 0), fl
             c.bank_keep = disk.get("bank_keep", 0)
+            c.landing_blocks, c.landing_ttl = disk.get("landing_blocks", 0), disk.get("landing_ttl", 0)
             self._keep.append(fl)
         c.w_trans, c.w_freq, c.w_rec, c.rows = 700, 200, 100, 1
         if score:
@@ -117,6 +121,11 @@ class OurCore:
     def host_order(self):
         out = np.zeros(self.keys, dtype=np.uint32)
         n = self.L.tsa_test_dgcore_host_order(self.h, out.ctypes.data_as(C.POINTER(u32)), self.keys)
+        return [int(v) for v in out[:n]]
+
+    def land_owner(self):
+        out = np.zeros(4096, dtype=np.uint32)
+        n = self.L.tsa_test_dgcore_land_owner(self.h, out.ctypes.data_as(C.POINTER(u32)), 4096)
         return [int(v) for v in out[:n]]
 
     def close(self):
@@ -217,7 +226,7 @@ def _preds(rng, routes, n_units, k):
 
 
 def _run(seed, three, score=None, switch=None, partial=False, predict=0, disk_prefetch=0, keep=False, sched=False,
-         bank_keep=0):
+         bank_keep=0, landing=None):
     """switch: (token, policy) - both cores switch policy between tokens there. partial: each token exports a random
     nonempty subset of the gated layers (ss_begin's rows), the others keep their state. keep: now and then, between
     tokens, a new keep list (ss_dg_keep: units no boundary may evict; sometimes empty, sometimes with keys off the
@@ -229,6 +238,8 @@ def _run(seed, three, score=None, switch=None, partial=False, predict=0, disk_pr
         c["disk"]["disk_prefetch"] = 1
     if bank_keep and c["disk"]:
         c["disk"]["bank_keep"] = bank_keep
+    if landing and c["disk"]:
+        c["disk"]["landing_blocks"], c["disk"]["landing_ttl"] = landing
     kw = dict(wb_defer=c["wb_defer"], inclusive=c["inclusive"])
     ours = OurCore(c["n_units"], c["persistent"], c["bank"], c["blocks"], c["spare_target"], c["parts"], c["order"],
                    disk=c["disk"], score=score, **kw)
@@ -264,6 +275,8 @@ def _run(seed, three, score=None, switch=None, partial=False, predict=0, disk_pr
                 assert v == want[k], (seed, t, k, v, want[k])
             if three:
                 assert ours.host_order() == theirs.host_order(), (seed, t, "pinned recency order")
+            if landing:
+                assert ours.land_owner() == theirs.land_owner(), (seed, t, "landing blocks")
             for k in got:
                 seen[k] = seen.get(k, 0) + got[k]
         return seen
@@ -468,4 +481,31 @@ def test_bank_keep_cases_exercise_the_paths():
         for k, v in _run(3000 + s, True, bank_keep=1 + s % 2).items():
             tot[k] = tot.get(k, 0) + v
     for k in ("bank_kept", "bank_keep_drops", "bank_keep_rereads", "bank_serves", "disk_drops"):
+        assert tot[k] > 0, k
+
+
+@pytest.mark.parametrize("ttl", [0, 1, 3])
+@pytest.mark.parametrize("seed", range(40))
+def test_landings_match_reference(seed, ttl):
+    """dg_landing_blocks: a prediction of a file-homed unit reads it into a landing block (no slot, outside the
+    prefetch budgets; none free: dropped), a demand copies it from there into the slot a file miss would have taken,
+    and a landing goes back to its file after its target layer (TTL 0) or after TTL boundaries undemanded; tables,
+    counters (landing_issued / promoted / expired / expired_layer / dropped_full / read_bytes, the landed units and
+    free blocks) and every landing block's key every token (reference src/dg_core.cpp:501-610, :1146-1330, :1650-1663,
+    docs/design.md 3.15)."""
+    blocks = 1 + seed % 6
+    _run(5000 + seed, True, predict=1 + seed % 4, disk_prefetch=int(seed % 5 == 2), bank_keep=int(seed % 7 == 3),
+         landing=(blocks, ttl), keep=seed % 4 == 1, sched=seed % 6 == 5)
+
+
+def test_landing_cases_exercise_the_paths():
+    if not ref.available():
+        pytest.skip("oracle/_ref (the reference core) is not built")
+    tot = {}
+    for s in range(24):
+        for ttl in (0, 2):
+            for k, v in _run(5000 + s, True, predict=1 + s % 4, landing=(1 + s % 6, ttl)).items():
+                tot[k] = tot.get(k, 0) + v
+    for k in ("landing_issued", "landing_promoted", "landing_expired", "landing_expired_layer", "landing_dropped_full",
+              "disk_reads"):
         assert tot[k] > 0, k

@@ -29,7 +29,8 @@ def _setup(tmp_path, layers, units, parts, n_res, dyn, spares, n_ids, inclusive=
     hs = (m.unit_bytes + 4095) // 4096 * 4096
     ring = 2 * n_ids + 1
     dev = n_res * st + ring * st + dyn * layers * st + st // 2
-    host = (layers * units - n_res + spares) * hs + hs // 2 + (1 << 20)
+    # the open's own: a staging unit, its control area and bounce buffer, and four units of startup headroom
+    host = (layers * units - n_res + spares + 5) * hs + (64 << 20)
     bkw = dict(device_bytes=dev, host_pinned_bytes=host, dynamic_slots_per_layer=dyn, ring_slots=ring, tier_mode=1,
                host_spare_units=spares)
     okw = dict(forward_mode=1, dg_max_ids=n_ids, pin_planned=0, verify_hash=2, dg_inclusive_blocks=inclusive,
@@ -346,7 +347,10 @@ def test_device_check_gates_a_corrupted_unit(tmp_path, gpu):
         ctx.close()
 
 
-def _three_tier(tmp_path, parts=(64 * KiB,) * 3):
+def _three_tier(tmp_path, parts=(64 * KiB,) * 3, extra_blocks=4):
+    """extra_blocks: the open's own pinned buffers on top of the plan's (staging buffers, landing blocks), which the
+    host budget must hold as well (plus its staging unit, four units of startup headroom and a margin for the control
+    area and a bounce buffer per reader)."""
     layers, units, parts, n_ids = 4, 8, list(parts), 2
     m = fixtures.write_model(tmp_path, layers, units, parts, top_k=n_ids, seed=31, tiers="pinned|disk")
     tiers = [0] * 12 + [1] * 10 + [2] * 10
@@ -354,8 +358,8 @@ def _three_tier(tmp_path, parts=(64 * KiB,) * 3):
     hs = (m.unit_bytes + 4095) // 4096 * 4096
     ring, dyn, spares = 2 * n_ids + 1, 1, 6
     bkw = dict(device_bytes=12 * st + ring * st + dyn * layers * st + st // 2,
-               host_pinned_bytes=(10 + spares) * hs + hs // 2, dynamic_slots_per_layer=dyn, ring_slots=ring,
-               tier_mode=1, host_spare_units=spares)
+               host_pinned_bytes=(10 + spares + extra_blocks + 5) * hs + (128 << 20), dynamic_slots_per_layer=dyn,
+               ring_slots=ring, tier_mode=1, host_spare_units=spares)
     return m, tiers, bkw
 
 
@@ -397,14 +401,24 @@ BIG_PARTS = (8 * 1024 * KiB + 64 * KiB, 64 * KiB, 4 * 1024 * KiB)
 
 
 AUTO = 0xFFFFFFFF  # SS_DG_DISK_QUEUE_AUTO: one read location resolves to 4 reads in flight
+LANDING_COUNTERS = ["landing_issued", "landing_promoted", "landing_expired", "landing_expired_layer",
+                    "landing_dropped_full", "landing_skipped_passed"]
 
 
-@pytest.mark.parametrize("clean_evict,queue,parts,predict,bank_keep,adapt",
-                         [(0, 0, None, 0, 0, 0), (1, 0, None, 0, 0, 0), (0, 4, None, 0, 0, 0), (1, 4, None, 0, 0, 0),
-                          (0, 3, BIG_PARTS, 0, 0, 0), (0, 4, None, 2, 0, 0), (0, 0, None, 2, 0, 0),
-                          (0, 0, None, 0, 1, 0), (0, 4, None, 0, 2, 0), (0, 3, BIG_PARTS, 0, 1, 0),
-                          (0, 4, None, 2, 1, 0), (0, AUTO, BIG_PARTS, 0, 1, 1), (0, AUTO, None, 2, 0, 1)])
-def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, predict, bank_keep, adapt):
+def _landing_failed(ctx):
+    return json.loads(ctx.stats_json())["device_gated"]["landing_failed"]
+
+
+# landings: (dg_landing_blocks, dg_landing_ttl, dg_landing_chunk, dg_landing_max_queued)
+@pytest.mark.parametrize("clean_evict,queue,parts,predict,bank_keep,adapt,landing",
+                         [(0, 0, None, 0, 0, 0, None), (1, 0, None, 0, 0, 0, None), (0, 4, None, 0, 0, 0, None),
+                          (1, 4, None, 0, 0, 0, None), (0, 3, BIG_PARTS, 0, 0, 0, None), (0, 4, None, 2, 0, 0, None),
+                          (0, 0, None, 2, 0, 0, None), (0, 0, None, 0, 1, 0, None), (0, 4, None, 0, 2, 0, None),
+                          (0, 3, BIG_PARTS, 0, 1, 0, None), (0, 4, None, 2, 1, 0, None),
+                          (0, AUTO, BIG_PARTS, 0, 1, 1, None), (0, AUTO, None, 2, 0, 1, None),
+                          (0, 4, None, 2, 0, 0, (4, 0, 0, 0)), (1, 3, BIG_PARTS, 2, 0, 0, (2, 2, 1 << 20, 2)),
+                          (0, AUTO, None, 2, 1, 0, (3, 1, 0xFFFFFFFF, 1)), (0, 4, None, 3, 2, 0, (1, 3, 4096, 4))])
+def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, predict, bank_keep, adapt, landing):
     """Three tiers (dg_disk_tier): 12 of 32 units resident, 10 pinned, 10 read from the file on a miss through staging
     buffers. The plan's tiers are given explicitly (a planner spill to the file tier leaves no room for spare blocks,
     as in the reference). Every token the slot table and the counters (file reads, drops of the pinned LRU to the
@@ -414,10 +428,15 @@ def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, 
     the engine predicts the next layer's ids and dg_disk_prefetch lets a prefetch read a file-homed unit. bank_keep
     (dg_bank_keep 1 / 2): a bank-served file miss is read into a pinned block, which becomes its home (its
     counters compared too). adapt (dg_disk_queue_adapt at SS_DG_DISK_QUEUE_AUTO): the pool's depth follows its
-    measured throughput - the placement is the same; with file prefetches the open declines it."""
+    measured throughput - the placement is the same; with file prefetches the open declines it. landing
+    (dg_landing_blocks, _ttl, _chunk, _max_queued): a prediction of a file-homed unit reads it into a landing block on
+    the read pool's landing queue, and its demand copies it from there after the read's word on the device; the
+    landings' placement counters equal the reference's, and the bytes landed are the reads issued less those the pool
+    dropped (cancelled, cut short or failed)."""
     parts = list(parts or (64 * KiB,) * 3)
     layers, units, n_ids, staging, dyn, spares = 4, 8, 2, 4, 1, 6
-    m, tiers, bkw = _three_tier(tmp_path, parts)
+    n_land, ttl, chunk, max_queued = landing or (0, 0, 0, 0)
+    m, tiers, bkw = _three_tier(tmp_path, parts, extra_blocks=staging + n_land)
     keys = layers * units
     d = ss.Desc(m.desc_json())
     plan = ss.Plan(d, ss.budget(**bkw), tiers=tiers)
@@ -430,18 +449,20 @@ def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, 
     dpf = 1 if predict else 0
     refdg = ref.RefDg([units] * layers, 12 + D, n_ids, 10 + Q, D, parts, residents + list(range(keys)),
                       disk=dict(flags=flags, home_blocks=10, disk_staging=staging, clean_evict=clean_evict,
-                                disk_prefetch=dpf, bank_keep=bank_keep))
+                                disk_prefetch=dpf, bank_keep=bank_keep, landing_blocks=n_land, landing_ttl=ttl))
+    lopt = dict(dg_landing_blocks=n_land, dg_landing_ttl=ttl, dg_landing_chunk=chunk, dg_landing_max_queued=max_queued) \
+        if n_land else {}
     ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(forward_mode=1, dg_max_ids=n_ids, pin_planned=0, verify_hash=2,
                                                       dg_disk_tier=1, dg_disk_staging=staging,
                                                       dg_clean_evict=clean_evict, dg_disk_queue=queue,
                                                       dg_disk_prefetch=dpf, dg_bank_keep=bank_keep,
-                                                      dg_disk_queue_adapt=adapt, dg_wait_timeout_ms=5000))
+                                                      dg_disk_queue_adapt=adapt, dg_wait_timeout_ms=5000, **lopt))
     eng = ss.DgEngine(ctx, n_ids, use_graph=True, n_pred=predict)
     routes = _routes(layers, units, n_ids, 24, seed=9, zipf=True)
     preds = _preds(routes, units, predict) if predict else None
     expect = {(L, u): fixtures.engine_checksum(m.unit_data(L, u)) for L in range(layers) for u in range(units)}
     counters = COUNTERS + ["disk_reads", "disk_drops", "disk_discards", "clean_drops", "bank_kept"] + \
-        (PRED_COUNTERS if predict else [])
+        (PRED_COUNTERS if predict else []) + (LANDING_COUNTERS if n_land else [])
     with pytest.raises(ss.SsError):
         ctx.snapshot()
     try:
@@ -453,10 +474,20 @@ def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, 
             assert np.array_equal(ctx.dg_table(), want_table), (t, "table")
             for k in counters:
                 assert got[k] == want[k], (t, k, got[k], want[k])
-            for L in range(layers):
-                for i, u in enumerate(routes[t, L]):
-                    assert int(cks[L, i]) == expect[(L, int(u))], (t, L, i)
+            for g in range(layers):
+                for i, u in enumerate(routes[t, g]):
+                    assert int(cks[g, i]) == expect[(g, int(u))], (t, g, i)
+            if n_land:
+                unread = got["landing_aborted_bytes"] + \
+                    (got["landing_cancelled"] + _landing_failed(ctx)) * m.unit_bytes
+                assert got["landing_read_bytes"] + unread == want["landing_read_bytes"], (t, got, want)
         assert got["disk_reads"] > 0 and (got["disk_drops"] + got["disk_discards"]) > 0, got
+        if n_land:
+            assert got["landing_issued"] > 0 and got["landing_promoted"] > 0, got
+            dg = json.loads(ctx.stats_json())["device_gated"]
+            assert dg["landing_blocks"] == n_land and dg["landing_ttl"] == ttl
+            assert dg["landing_max_queued"] == (max_queued or 1)
+            assert dg["landing_chunk"] == ("whole" if chunk == 0xFFFFFFFF else chunk or 4 << 20)
         if bank_keep:
             assert got["bank_kept"] > 0, got
         resolved = 4 if queue == AUTO else max(queue, 1)

@@ -31,7 +31,7 @@ CHILD = textwrap.dedent("""
     hs = (m.unit_bytes + 4095) // 4096 * 4096
     d = ss.Desc(m.desc_json())
     if mode == "dg":
-        bkw = dict(device_bytes=(12 + 5 + 3) * st + st // 2, host_pinned_bytes=(24 - 12 + 6) * hs + hs // 2,
+        bkw = dict(device_bytes=(12 + 5 + 3) * st + st // 2, host_pinned_bytes=(24 - 12 + 6 + 5) * hs + (64 << 20),
                    dynamic_slots_per_layer=1, ring_slots=5, tier_mode=1, host_spare_units=6)
         ctx = ss.Ctx(d, ss.budget(**bkw), ss.Plan(d, ss.budget(**bkw)),
                      ss.options(forward_mode=1, dg_max_ids=2, pin_planned=0, verify_hash=2, dg_wait_timeout_ms=5000))

@@ -288,6 +288,9 @@ DgCore::DgCore(const DgConfig& cfg, DgTransport* t) : c_(cfg), t_(t) {
             "device-gated: file-tier options given without the file tier");
   }
   require(c_.bank_keep <= 2, SS_E_INVALID, "device-gated: dg_bank_keep is 0, 1 or 2");
+  require(c_.disk_tier || !c_.landing_blocks, SS_E_INVALID, "device-gated: landing blocks without the file tier");
+  require(uint64_t(c_.blocks) + c_.disk_staging + c_.landing_blocks < 0x7fffffffull, SS_E_INVALID,
+          "device-gated: 2^31 - 1 host blocks or more");
   if (c_.prefetch_reserve_auto) c_.prefetch_reserve = std::min<uint32_t>(24, c_.spare_target / 4);
 
   st_.assign(keys_, KeyState{});
@@ -301,6 +304,10 @@ DgCore::DgCore(const DgConfig& cfg, DgTransport* t) : c_(cfg), t_(t) {
   exported_.assign(gated(), 1);
   per_layer_.assign(gated(), DgLayerCounts{});
   if (c_.disk_tier) stage_ev_.assign(c_.disk_staging, nullptr);
+  served_.assign(gated(), 0);
+  free_land_.reserve(c_.landing_blocks);
+  land_busy_.reserve(c_.landing_blocks);
+  land_owner_.assign(c_.landing_blocks, kNoKey);
   chosen_.reserve(c_.persistent_slots);
   apply_wb_mode();
   if (c_.scored) {  // every table now, so the service never allocates
@@ -374,6 +381,11 @@ void DgCore::seat(const std::vector<uint32_t>& priority, const std::vector<uint8
 
   std::fill(st_.begin(), st_.end(), KeyState{});
   std::fill(mirror_.begin(), mirror_.end(), -1);
+  free_land_.clear();
+  for (uint32_t l = c_.landing_blocks; l-- > 0;) free_land_.push_back(int32_t(l));  // block 0 taken first
+  land_busy_.clear();
+  std::fill(land_owner_.begin(), land_owner_.end(), kNoKey);
+  n_land_ = 0;
   recent_.reset(keys_);
   homed_.reset(keys_);
   n_device_ = n_pinned_ = n_clean_ = n_file_ = 0;
@@ -623,6 +635,7 @@ void DgCore::open_token(uint32_t seq, const std::vector<uint8_t>* run) {
   ahead_in_token_ = 0;
   std::fill(ahead_in_layer_.begin(), ahead_in_layer_.end(), 0u);
   std::fill(layer_missed_.begin(), layer_missed_.end(), uint8_t(0));
+  std::fill(served_.begin(), served_.end(), uint8_t(0));
   predicted_.clear();
   predicted_layer_ = kNoKey;
 }
@@ -674,8 +687,9 @@ bool DgCore::bring_in(uint32_t g, uint32_t u, bool ahead) {
   const uint32_t k = key(g, u);
   KeyState& x = st_[k];
   if (ahead && (ahead_in_layer_[g] >= c_.prefetch_per_layer || ahead_in_token_ >= c_.prefetch_per_token)) return false;
-  if (resident_or_landing(k)) return false;
+  if (on_device_or_arriving(k)) return false;
   if (x.where == Where::Draining) return resurrect(k);
+  if (x.where == Where::Landed && ahead) return false;  // a landing is copied in by a demand only
   if (x.where == Where::File && ahead && !c_.disk_prefetch) return false;
 
   // a persistent slot above the prefetch reserve, else (a demand) a bank slot
@@ -742,6 +756,18 @@ bool DgCore::bring_in(uint32_t g, uint32_t u, bool ahead) {
       if (n_.tokens + 1 - x.dropped_for_keep <= 8) ++n_.bank_keep_rereads;
       x.dropped_for_keep = 0;
     }
+  } else if (x.where == Where::Landed) {  // from its landing block, as from a pinned block
+    const int32_t lb = land_block(x.land);
+    t_->wait_copy_in(s, slot, lb, ev_.on_slot(slot), nullptr);
+    ev_.untie_slot(slot);
+    t_->h2d(s, slot, lb);
+    land_busy_.push_back(x.land);  // free at the next landing or boundary (the transport orders the reuse)
+    land_owner_[size_t(x.land)] = kNoKey;
+    x.land = -1;
+    x.land_age = 0;
+    --n_land_;
+    --n_file_;
+    ++n_.landing_promoted;
   } else {  // after the slot's last write-back and any write-back still copying into this block
     t_->wait_copy_in(s, slot, x.block, ev_.on_slot(slot), ev_.on_block(x.block));
     ev_.untie_slot(slot);
@@ -765,8 +791,8 @@ bool DgCore::bring_in(uint32_t g, uint32_t u, bool ahead) {
     ++n_.bank_serves;
     ++lc.bank_serves;
   } else {
-    x.where = Where::Landing;
-    landing_.push_back(k);
+    x.where = Where::Arriving;
+    arriving_.push_back(k);
     touch(k);
     ++n_device_;
   }
@@ -791,12 +817,12 @@ void DgCore::serve_misses(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t 
   for (uint32_t i = 0; i < n; ++i) {  // a repeated id: fetched at its first miss, covered at the next
     const uint32_t k = key(g, ids[i]);
     const KeyState& x = st_[k];
-    const bool prefetch_in_flight = x.where == Where::Landing && x.ahead && x.ahead_ev;
+    const bool prefetch_in_flight = x.where == Where::Arriving && x.ahead && x.ahead_ev;
     if (!(mask >> i & 1u)) {
       if ((dev_mask >> i & 1u) && prefetch_in_flight) t_->wait(DgTransport::kDem, x.ahead_ev);
       continue;
     }
-    if (!resident_or_landing(k)) {
+    if (!on_device_or_arriving(k)) {
       bring_in(g, ids[i], false);
       continue;
     }
@@ -805,6 +831,10 @@ void DgCore::serve_misses(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t 
       ++n_.covered_waits;
     }
     ++n_.covered;
+  }
+  if (c_.landing_blocks && c_.landing_ttl == 0) {  // nothing demands layer g again this token
+    served_[g] = 1;
+    expire_layer_landings(g, ids, n);
   }
   if (mask | dev_mask) t_->signal_ready(g, seq_);  // after every fetch's landed()
 }
@@ -856,7 +886,75 @@ void DgCore::prefetch_next(uint32_t g_next, const uint32_t* pred, uint32_t n) {
   }
   n_.predicted += predicted_.size();
   predicted_layer_ = g_next;
-  for (uint32_t id : predicted_) bring_in(g_next, id, true);
+  for (uint32_t id : predicted_)
+    if (!advise_land(g_next, id)) bring_in(g_next, id, true);  // (landings on: a file-homed unit lands instead)
+}
+
+// ---- landings (dg_landing_blocks) -------------------------------------------------------------------------------------
+// A prediction of a file-homed unit reads it into a landing block of its own pool: no slot is taken and nothing is
+// evicted or written back for it, outside the prefetch budgets. It stays file-homed (Landed: no slot, block or entry)
+// until a demand copies it from its landing block into the slot a file miss would have taken; no free landing block
+// drops the advice, and a landing is never displaced. In this schedule a landing read has landed when its layer is
+// served: the transport orders every copy out of a landing block after its read on the device.
+bool DgCore::advise_land(uint32_t g, uint32_t u) {
+  if (!c_.landing_blocks) return false;
+  const uint32_t k = key(g, u);
+  const Where w = st_[k].where;
+  if (w == Where::Landed) return true;  // (already landing: left as it is)
+  if (w != Where::File) return false;
+  if (c_.landing_ttl == 0 && served_[g]) {  // its layer's demand has passed: it could never be used
+    ++n_.landing_skipped_passed;
+    return true;
+  }
+  land(k);
+  return true;
+}
+
+void DgCore::land(uint32_t k) {
+  reclaim_lands();
+  if (free_land_.empty()) {
+    ++n_.landing_dropped_full;
+    return;
+  }
+  const int32_t l = free_land_.back();
+  t_->read_landing(k, land_block(l));
+  free_land_.pop_back();
+  KeyState& x = st_[k];
+  land_owner_[size_t(l)] = k;
+  x.where = Where::Landed;
+  x.land = l;
+  x.land_age = 0;
+  ++n_land_;
+  ++n_.landing_issued;
+  n_.landing_read_bytes += unit_bytes_;
+}
+
+void DgCore::unland(uint32_t k) {
+  KeyState& x = st_[k];
+  const int32_t l = x.land;
+  free_land_.push_back(l);
+  land_owner_[size_t(l)] = kNoKey;
+  x.land = -1;
+  x.land_age = 0;
+  x.where = Where::File;
+  --n_land_;
+  t_->drop_landing(land_block(l));
+}
+
+void DgCore::reclaim_lands() {
+  free_land_.insert(free_land_.end(), land_busy_.begin(), land_busy_.end());
+  land_busy_.clear();
+}
+
+// landing_ttl 0, after layer g's demand: its landings it did not route go back to their file (in block order).
+void DgCore::expire_layer_landings(uint32_t g, const uint32_t* ids, uint32_t n) {
+  for (uint32_t l = 0; l < c_.landing_blocks; ++l) {
+    const uint32_t k = land_owner_[l];
+    if (k == kNoKey || k < first_key_[g] || k >= first_key_[g + 1]) continue;
+    if (std::find(ids, ids + n, k - first_key_[g]) != ids + n) continue;
+    unland(k);
+    ++n_.landing_expired_layer;
+  }
 }
 
 // ---- the boundary -----------------------------------------------------------------------------------------------------
@@ -872,9 +970,18 @@ void DgCore::close_token(uint32_t rows, const std::vector<uint32_t>& keep) {
   } unkeep{kept_};
   t_->sync(DgTransport::kDem);  // every copy and table write of the token landed before homes change
   t_->sync(DgTransport::kPf);
-  for (uint32_t k : landing_) {  // resident now; the block it came from is free, or kept as a clean copy
+  if (c_.landing_blocks) {  // the blocks copied out of are free; a landing not demanded for landing_ttl boundaries (TTL
+    reclaim_lands();        // 0: this one) goes back to its file, no copy (the file holds its bytes)
+    for (uint32_t l = 0; l < c_.landing_blocks; ++l) {
+      const uint32_t k = land_owner_[l];
+      if (k == kNoKey || ++st_[k].land_age < std::max<uint32_t>(c_.landing_ttl, 1)) continue;
+      unland(k);
+      ++n_.landing_expired;
+    }
+  }
+  for (uint32_t k : arriving_) {  // resident now; the block it came from is free, or kept as a clean copy
     KeyState& x = st_[k];
-    if (x.where != Where::Landing) continue;
+    if (x.where != Where::Arriving) continue;
     x.where = Where::Resident;
     x.ahead = false;
     if (x.ahead_ev) ev_.give(x.ahead_ev);
@@ -889,7 +996,7 @@ void DgCore::close_token(uint32_t rows, const std::vector<uint32_t>& keep) {
       x.block = -1;
     }
   }
-  landing_.clear();
+  arriving_.clear();
   for (uint32_t k : in_bank_) {  // borrowed for the token: back to the block (or the file) it came from
     KeyState& x = st_[k];
     if (x.where == Where::InBank) {
@@ -1130,11 +1237,11 @@ void DgCore::audit() const {
     owner[size_t(i)] = who;
   };
   constexpr uint32_t kFree = 0xfffffffeu;
-  uint32_t n_dev = 0, n_pin = 0, n_file = 0, n_clean = 0;
+  uint32_t n_dev = 0, n_pin = 0, n_file = 0, n_clean = 0, n_land = 0;
   for (uint32_t k = 0; k < keys_; ++k) {
     const KeyState& x = st_[k];
     const std::string who = "key " + str(k);
-    const bool has_slot = x.where == Where::Resident || x.where == Where::Landing || x.where == Where::InBank ||
+    const bool has_slot = x.where == Where::Resident || x.where == Where::Arriving || x.where == Where::InBank ||
                           x.where == Where::Draining;
     if (has_slot) own(slot_owner, x.slot, k, "slot");
     else if (x.slot != -1) broken(who + " holds a slot off the device");
@@ -1147,8 +1254,8 @@ void DgCore::audit() const {
         if (x.clean != (x.block >= 0)) broken(who + " clean flag and block disagree");
         ++n_dev;
         break;
-      case Where::Landing:
-        if (!recent_.has(k)) broken(who + " landing but not in the recency order");
+      case Where::Arriving:
+        if (!recent_.has(k)) broken(who + " arriving but not in the recency order");
         ++n_dev;
         break;
       case Where::InBank:
@@ -1166,9 +1273,17 @@ void DgCore::audit() const {
         if (!c_.disk_tier || x.block >= 0 || mirror_[k] >= 0) broken(who + " in its file with a block or an entry");
         ++n_file;
         break;
+      case Where::Landed:
+        if (x.block >= 0 || mirror_[k] >= 0 || x.land < 0 || uint32_t(x.land) >= c_.landing_blocks ||
+            land_owner_[size_t(x.land)] != k)
+          broken(who + " landed with a block or an entry, or not owning its landing block");
+        ++n_file;
+        ++n_land;
+        break;
     }
+    if (x.where != Where::Landed && x.land >= 0) broken(who + " holds a landing block off the landing state");
     if (x.where != Where::Pinned && homed_.has(k)) broken(who + " in the homes' order but not pinned");
-    if (recent_.has(k) && x.where != Where::Resident && x.where != Where::Landing)
+    if (recent_.has(k) && x.where != Where::Resident && x.where != Where::Arriving)
       broken(who + " in the recency order off the device");
   }
   for (int32_t s : free_slot_) own(slot_owner, s, kFree, "free slot");
@@ -1188,6 +1303,19 @@ void DgCore::audit() const {
   if (n_dev != n_device_) broken("device count");
   if (n_pin != n_pinned_) broken("pinned count");
   if (n_file != n_file_) broken("file count");
+  if (n_land != n_land_) broken("landing count");
+  {  // every landing block once: owned, free or copied out of since the last reclaim
+    std::vector<uint8_t> seen(c_.landing_blocks, 0);
+    uint32_t owned = 0;
+    for (uint32_t l = 0; l < c_.landing_blocks; ++l) owned += land_owner_[l] != kNoKey;
+    for (const std::vector<int32_t>* v : {&free_land_, &land_busy_})
+      for (int32_t l : *v) {
+        if (l < 0 || uint32_t(l) >= c_.landing_blocks || seen[size_t(l)]++ || land_owner_[size_t(l)] != kNoKey)
+          broken("landing block " + str(uint64_t(int64_t(l))) + " free twice, out of range or owned");
+      }
+    if (owned != n_land_ || owned + free_land_.size() + land_busy_.size() != c_.landing_blocks)
+      broken("landing blocks lost");
+  }
   if (n_clean != n_clean_) broken("clean-copy count");
   if (recent_.size() != n_device_) broken("recency order length");
   if (c_.disk_tier && homed_.size() != n_pinned_) broken("homes' order length");

@@ -55,6 +55,14 @@ class DgTransport {
   // host layout of a unit), synchronously; the core then copies it in from that block as from a pinned home.
   // slot: where the copy that follows puts it (a bank slot when the read went into a kept pinned block).
   virtual void read_unit(uint32_t key, int32_t block, int32_t slot);
+  // Landings (dg_landing_blocks): the unit's file read into landing block `block` (blocks + disk_staging + l), queued
+  // behind the demand reads. The core may copy out of the block (h2d) right after this call: the transport orders
+  // that copy after the read, and this read after the block's previous read and its last copy out. Default:
+  // read_unit.
+  virtual void read_landing(uint32_t key, int32_t block) { read_unit(key, block, -1); }
+  // The landing in `block` will never be copied out (it expired): a read not started yet may be dropped (default:
+  // nothing).
+  virtual void drop_landing(int32_t block) { (void)block; }
   // Before h2d(s, slot, block): slot_ev / block_ev (either may be null) are the write-backs that may still read the
   // slot or write the block. The default makes s wait for both; a transport that tracks its copies per part may let
   // each part of the next h2d wait only for the same part of those write-backs.
@@ -99,6 +107,11 @@ struct DgConfig {
   // else the longest-homed pinned unit's (that unit to its file) - which becomes its pinned home when the bank releases
   // it: at the front of the homes' order (1) or behind its front half (2). 0: read through a staging buffer.
   uint32_t bank_keep = 0;
+  // dg_landing_blocks (three-tier): a prediction of a file-homed unit reads it into one of landing_blocks landing
+  // blocks (never a slot): a demand then copies it from there, as from a pinned block. landing_ttl 0: a landing its
+  // target layer did not demand goes back to its file right after that layer's demand (and a prediction for a layer
+  // already served this token lands nothing); N >= 1: one not demanded for N boundaries goes back to its file.
+  uint32_t landing_blocks = 0, landing_ttl = 0;
   // Scored eviction (SS_POLICY_SCORED / SCORED_AUTO): the boundary takes its victims lowest score first instead of
   // from the back of the recency order; every other decision stays LRU's. Weights in thousandths (each 0..1000, sum
   // 1000). max_ids: the ids of one export (a union's upper bound), 1..64. scored_auto: learn every token, but rank
@@ -120,6 +133,16 @@ struct DgCounts {  // the subset of ss_dg_stats this core counts (the ABI's fiel
   // dg_bank_keep: reads kept in a pinned block; pinned units dropped to their file for one; such a dropped unit read
   // from its file again within 8 tokens
   uint64_t bank_kept = 0, bank_keep_drops = 0, bank_keep_rereads = 0;
+  // dg_landing_blocks: landing reads issued; demands served from a landing block; landings back to their file at a
+  // boundary (TTL) and right after their target layer (TTL 0); advice dropped with no free landing block; predictions
+  // for a layer already served (TTL 0); the bytes of the reads issued
+  uint64_t landing_issued = 0, landing_promoted = 0, landing_expired = 0, landing_expired_layer = 0;
+  uint64_t landing_dropped_full = 0, landing_skipped_passed = 0, landing_read_bytes = 0;
+  // the physical side of landings, which the core never sees (the context adds its transport's): demands of a landing
+  // whose read still ran, host waits for a landing block's reuse, reads dropped before they started, demand reads a
+  // part-way landing read gave its readers to, bytes not read of reads dropped part-way, failed landing reads
+  uint64_t landing_late = 0, landing_wait_ns = 0, landing_cancelled = 0, landing_yields = 0;
+  uint64_t landing_aborted_bytes = 0, landing_failed = 0;
   // scored eviction: boundaries that fell back to the recency order (an exported gated layer whose union is not this
   // token's); victims taken in score order; layers and eligible keys the selection considered; transition increments
   // lost to a saturated cell; selection time.
@@ -158,10 +181,12 @@ class KeyOrder {
 
 class DgCore {
  public:
-  // Pinned: its host block is its home. Resident: a persistent slot. Landing: copied into a persistent slot this token
-  // (resident from the boundary on). InBank: copied into a bank slot for this token only. Draining: chosen at a
+  // Pinned: its host block is its home. Resident: a persistent slot. Arriving: copied into a persistent slot this
+  // token (resident from the boundary on). InBank: copied into a bank slot for this token only. Draining: chosen at a
   // boundary, its write-back into a block not yet retired (the slot still holds its bytes). File: three-tier only.
-  enum class Where : uint8_t { Pinned, Resident, Landing, InBank, Draining, File };
+  // Landed: its home is still its file, and its read into a landing block was issued (no slot, block or entry); a
+  // demand copies it from there.
+  enum class Where : uint8_t { Pinned, Resident, Arriving, InBank, Draining, File, Landed };
 
   DgCore(const DgConfig& cfg, DgTransport* t);
   ~DgCore();
@@ -188,7 +213,10 @@ class DgCore {
   uint32_t free_blocks() const { return uint32_t(free_block_.size()); }
   const std::vector<int32_t>& free_block_ids() const { return free_block_; }  // the free stack, top last
   uint32_t on_device() const { return n_device_; }
-  uint32_t file_units() const { return n_file_; }
+  uint32_t file_units() const { return n_file_; }  // three-tier: file-homed keys (landings included)
+  uint32_t landing_units() const { return n_land_; }
+  uint32_t landing_free() const { return uint32_t(free_land_.size() + land_busy_.size()); }
+  const std::vector<uint32_t>& landing_owners() const { return land_owner_; }  // per landing block: its key, or ~0
   std::vector<uint32_t> pinned_order() const;  // three-tier: the pinned homes, most recently homed first
   uint32_t clean_copies() const { return n_clean_; }
   uint64_t outstanding_bytes() const { return in_flight_bytes_; }
@@ -254,6 +282,8 @@ class DgCore {
     void* ahead_ev = nullptr;  // the prefetch's copy
     uint64_t demand_token = 0;  // scored: the token of its last demand use (0: none since open or a policy switch)
     uint64_t dropped_for_keep = 0;  // dg_bank_keep: 1 + the tokens closed when a kept read took its block (0: none)
+    int32_t land = -1;              // Landed: its landing block (0 .. landing_blocks - 1)
+    uint32_t land_age = 0;          // Landed: boundaries since it landed
   };
 
   // A victim's copy into its block. Sealed: its event recorded after its last submitted part; it completes in the
@@ -370,10 +400,18 @@ class DgCore {
   void publish(DgTransport::Stream s, uint32_t k, int32_t v, bool from_copy = false);
   bool bring_in(uint32_t g, uint32_t u, bool ahead);
   bool resurrect(uint32_t k);
-  bool resident_or_landing(uint32_t k) const {
+  bool on_device_or_arriving(uint32_t k) const {
     const Where w = st_[k].where;
-    return w == Where::Resident || w == Where::Landing || w == Where::InBank;
+    return w == Where::Resident || w == Where::Arriving || w == Where::InBank;
   }
+
+  // landings
+  int32_t land_block(int32_t l) const { return int32_t(c_.blocks + c_.disk_staging) + l; }
+  bool advise_land(uint32_t g, uint32_t u);  // true: the landing path took the prediction (a bring_in must not)
+  void land(uint32_t k);
+  void unland(uint32_t k);       // back to its file, its landing block free
+  void reclaim_lands();          // landing blocks copied out of since the last reclaim: free
+  void expire_layer_landings(uint32_t g, const uint32_t* ids, uint32_t n);
 
   // boundary
   bool choose(uint32_t k);  // one victim; false: no block to write it into (evict_short)
@@ -396,7 +434,11 @@ class DgCore {
   uint32_t n_device_ = 0, n_pinned_ = 0, n_clean_ = 0, n_file_ = 0;
   uint32_t stage_cursor_ = 0;
   std::vector<void*> stage_ev_;  // [disk_staging]: the last copy out of each staging buffer
-  std::vector<uint32_t> landing_, in_bank_;
+  std::vector<uint32_t> arriving_, in_bank_;
+  std::vector<int32_t> free_land_, land_busy_;  // free landing blocks (a stack, block 0 on top at open); copied out of
+  std::vector<uint32_t> land_owner_;            // per landing block: its key (kNoKey: free)
+  uint32_t n_land_ = 0;
+  std::vector<uint8_t> served_;                 // landing_ttl 0: the gated layers whose demand this token served
   BankSlots banks_;
   std::deque<WriteBack> wb_;  // sealed prefix, then the queued tail
   size_t sealed_ = 0;

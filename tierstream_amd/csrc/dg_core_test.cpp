@@ -56,7 +56,9 @@ constexpr const char* kNames =
     "writebacks_done miss_layers covered_waits wb_deferred wb_cancelled wb_forced wb_boundary_flushed wb_issued_bytes "
     "wb_cancelled_bytes inclusive_kept inclusive_drops free_slots free_blocks on_device backed_units disk_reads "
     "disk_drops disk_discards clean_drops file_units score_fallbacks scored_victims score_layers score_candidates "
-    "score_saturated pred_invalid predicted predicted_true bank_kept bank_keep_drops bank_keep_rereads";
+    "score_saturated pred_invalid predicted predicted_true bank_kept bank_keep_drops bank_keep_rereads "
+    "landing_issued landing_promoted landing_expired landing_expired_layer landing_dropped_full "
+    "landing_skipped_passed landing_read_bytes landing_units landing_free";
 
 }  // namespace
 }  // namespace tsa
@@ -90,6 +92,8 @@ ss_status tsa_test_dgcore_open(const tsa_test_dgcore_config* cfg, const uint32_t
     c.disk_staging = cfg->disk_staging;
     c.clean_evict = cfg->clean_evict != 0;
     c.bank_keep = cfg->bank_keep;
+    c.landing_blocks = cfg->landing_blocks;
+    c.landing_ttl = cfg->landing_ttl;
     require(cfg->policy <= 2, SS_E_INVALID, "tsa_test_dgcore_open: policy must be 0, 1 or 2");
     c.scored = cfg->policy != 0;
     c.scored_auto = cfg->policy == 2;
@@ -167,7 +171,10 @@ ss_status tsa_test_dgcore_token_pred(void* h, const uint32_t* ids, uint32_t n, c
                             uint64_t(c.clean_copies()), s.disk_reads, s.disk_drops, s.disk_discards, s.clean_drops,
                             uint64_t(c.file_units()), s.score_fallbacks, s.scored_victims, s.score_layers,
                             s.score_candidates, s.score_saturated, s.pred_invalid, s.predicted, s.predicted_true,
-                            s.bank_kept, s.bank_keep_drops, s.bank_keep_rereads};
+                            s.bank_kept, s.bank_keep_drops, s.bank_keep_rereads, s.landing_issued,
+                            s.landing_promoted, s.landing_expired, s.landing_expired_layer, s.landing_dropped_full,
+                            s.landing_skipped_passed, s.landing_read_bytes, uint64_t(c.landing_units()),
+                            uint64_t(c.landing_free())};
       const uint32_t m = uint32_t(sizeof v / sizeof v[0]);
       std::memcpy(counts, v, 8ull * (n_counts < m ? n_counts : m));
     }
@@ -227,6 +234,13 @@ ss_status tsa_test_score_profile_check(const void* data, uint64_t len, const uin
 uint32_t tsa_test_dgcore_host_order(void* h, uint32_t* out, uint32_t cap) {
   if (!h) return 0;
   const std::vector<uint32_t> v = static_cast<tsa::TestCore*>(h)->core->pinned_order();
+  for (uint32_t i = 0; out && i < cap && i < v.size(); ++i) out[i] = v[i];
+  return uint32_t(v.size());
+}
+
+uint32_t tsa_test_dgcore_land_owner(void* h, uint32_t* out, uint32_t cap) {
+  if (!h) return 0;
+  const std::vector<uint32_t>& v = static_cast<tsa::TestCore*>(h)->core->landing_owners();
   for (uint32_t i = 0; out && i < cap && i < v.size(); ++i) out[i] = v[i];
   return uint32_t(v.size());
 }

@@ -21,6 +21,7 @@
 #include "dg_geometry.hpp"
 #include "dg_proto.hpp"
 #include "hip_rt.hpp"
+#include "read_pool.hpp"
 #include "score_profile.hpp"
 #include "source.hpp"
 #include "stats_json.hpp"
@@ -31,9 +32,6 @@ namespace tsa {
 namespace {
 
 using Clock = std::chrono::steady_clock;
-// device-verify checkpoint spacing: 8 KiB gives one 336 MiB unit 43,008 independent segments, one lane-quad each
-// (2,688 wavefronts), enough to keep every SIMD of the chip busy in one launch; the checkpoints cost 32 bytes per
-// segment (0.4 % of the unit) in HBM
 // The device check's checkpoint segment: 8 KiB, halved (down to 2 KiB) while one unit has fewer than 16,384
 // segments - a quad of lanes per segment, so that one unit's check is at least 4 waves per CU of a 256-CU chip
 // (checkpoints cost 32 B per segment: 0.4 % of the unit's bytes at 8 KiB, 1.6 % at 2 KiB).
@@ -64,170 +62,6 @@ MappedLayout mapped_layout(uint32_t G) {
   m.total = align64(m.words + 8 * 4);
   return m;
 }
-
-// ---- three-tier reads in flight ------------------------------------------------------------------------------------
-// dg_disk_queue > 1: reader threads read file-tier units into staging buffers in pieces of at most 8 MiB (a part, or a
-// 4 KiB-aligned slice of one), so one unit's read runs on every reader at once. The piece that completes a unit runs
-// the unit's finisher (the host hash check with verify_hash 1), then stores the read's generation into the staging
-// buffer's word in fine-grained host memory, which the stream that copies out of the buffer polls first (an await
-// kernel): the service thread only decides and enqueues, and the reads of a layer's misses overlap one another and
-// the copies of the units read before them. The word is stored on every path (a failed piece records its error
-// first), so every await ends.
-class ReadPool {
- public:
-  struct Piece {
-    uint32_t part;
-    uint64_t off, bytes, dst_off;  // offset inside the part, bytes, offset inside the host block
-  };
-  using PieceReader = std::function<void(uint32_t key, uint32_t part, uint64_t off, uint64_t bytes, char* dst)>;
-  using Finisher = std::function<void(uint32_t key, const char* block)>;
-  ReadPool(uint32_t threads, std::vector<Piece> pieces, PieceReader read, Finisher finish)
-      : pieces_(std::move(pieces)), read_(std::move(read)), finish_(std::move(finish)), threads_(threads),
-        limit_(threads) {
-    for (const Piece& pc : pieces_) unit_bytes_ += pc.bytes;
-    for (uint32_t i = 0; i < threads; ++i) th_.emplace_back([this] { run(); });
-  }
-  // dg_disk_queue_adapt: pieces run at most depth() at a time, the depth chosen by a controller fed each busy period
-  // (from the first piece taken while idle to no piece queued or running: its whole units and their bytes).
-  void adapt() {
-    std::lock_guard<std::mutex> l(m_);
-    ctl_ = std::make_unique<ReadDepthController>(threads_);
-    limit_ = ctl_->depth();
-  }
-  // f(controller) under the pool's lock (no-op when not adapting)
-  void with_controller(const std::function<void(const ReadDepthController&)>& f) {
-    std::lock_guard<std::mutex> l(m_);
-    if (ctl_) f(*ctl_);
-  }
-  ~ReadPool() { stop(); }
-  // The queued reads finish first; no piece is dropped.
-  void stop() {
-    {
-      std::lock_guard<std::mutex> l(m_);
-      stop_ = true;
-    }
-    cv_.notify_all();
-    for (auto& t : th_)
-      if (t.joinable()) t.join();
-  }
-  void submit(uint32_t key, char* block, uint32_t* word, uint32_t gen) {
-    {
-      std::lock_guard<std::mutex> l(m_);
-      units_.push_back(Unit{key, block, word, gen, uint32_t(pieces_.size())});
-      Unit* u = &units_.back();
-      for (const Piece& pc : pieces_) q_.push_back(Job{u, &pc});
-      ++inflight_;
-    }
-    cv_.notify_all();
-  }
-  // Waits for every submitted read (returns the wait in ns); rethrows the first read failure not yet reported.
-  uint64_t drain() {
-    std::unique_lock<std::mutex> l(m_);
-    uint64_t ns = 0;
-    if (inflight_) {
-      const auto t0 = Clock::now();
-      idle_.wait(l, [this] { return inflight_ == 0; });
-      ns = uint64_t(std::chrono::duration_cast<std::chrono::nanoseconds>(Clock::now() - t0).count());
-    }
-    units_.clear();  // (every unit finished: no job points into the list)
-    if (err_) {
-      std::exception_ptr e = err_;
-      err_ = nullptr;
-      std::rethrow_exception(e);
-    }
-    return ns;
-  }
-  uint64_t read_ns() const { return read_ns_.load(std::memory_order_relaxed); }
-  uint64_t max_running() {
-    std::lock_guard<std::mutex> l(m_);
-    return max_running_;
-  }
-
- private:
-  struct Unit {
-    uint32_t key;
-    char* block;
-    uint32_t* word;
-    uint32_t gen, left;  // pieces not yet read
-  };
-  struct Job {
-    Unit* unit;
-    const Piece* piece;
-  };
-  void run() {
-    for (;;) {
-      Job j;
-      {
-        std::unique_lock<std::mutex> l(m_);
-        cv_.wait(l, [this] { return (stop_ && q_.empty()) || (!q_.empty() && running_ < limit_); });
-        if (q_.empty()) return;  // stopping, nothing queued
-        j = q_.front();
-        q_.pop_front();
-        max_running_ = std::max<uint64_t>(max_running_, ++running_);
-        if (ctl_ && !busy_) {  // a busy period begins
-          busy_ = true;
-          busy_t0_ = Clock::now();
-          busy_units_ = 0;
-        }
-      }
-      Unit& u = *j.unit;
-      std::exception_ptr e;
-      const auto t0 = Clock::now();
-      try {
-        read_(u.key, j.piece->part, j.piece->off, j.piece->bytes, u.block + j.piece->dst_off);
-      } catch (...) {
-        e = std::current_exception();
-      }
-      read_ns_.fetch_add(uint64_t(std::chrono::duration_cast<std::chrono::nanoseconds>(Clock::now() - t0).count()),
-                         std::memory_order_relaxed);
-      bool last;
-      {
-        std::lock_guard<std::mutex> l(m_);
-        --running_;
-        if (e && !err_) err_ = e;
-        last = --u.left == 0;
-        if (ctl_ && busy_) {
-          busy_units_ += last;
-          if (running_ == 0 && q_.empty()) {  // idle again: the period's throughput picks the next depth
-            busy_ = false;
-            const uint64_t ns =
-                uint64_t(std::chrono::duration_cast<std::chrono::nanoseconds>(Clock::now() - busy_t0_).count());
-            limit_ = std::min(std::max<uint32_t>(ctl_->feed(busy_units_, busy_units_ * unit_bytes_, ns), 1), threads_);
-          }
-        }
-        if (ctl_) cv_.notify_all();  // (a piece slot is free under the depth limit)
-      }
-      if (!last) continue;
-      try {  // every piece of the unit landed (or failed): the finisher, then the word
-        finish_(u.key, u.block);
-      } catch (...) {
-        std::lock_guard<std::mutex> l(m_);
-        if (!err_) err_ = std::current_exception();
-      }
-      std::lock_guard<std::mutex> l(m_);
-      __atomic_store_n(u.word, u.gen, __ATOMIC_RELEASE);  // the buffer's bytes (or the failure) before the word
-      if (--inflight_ == 0) idle_.notify_all();
-    }
-  }
-  std::vector<Piece> pieces_;
-  PieceReader read_;
-  Finisher finish_;
-  std::mutex m_;
-  std::condition_variable cv_, idle_;
-  std::deque<Job> q_;
-  std::deque<Unit> units_;  // (stable addresses: jobs point at their unit)
-  std::vector<std::thread> th_;
-  uint32_t threads_ = 0, limit_ = 0;  // readers; pieces that may run at once
-  uint64_t unit_bytes_ = 0;
-  std::unique_ptr<ReadDepthController> ctl_;  // dg_disk_queue_adapt
-  bool busy_ = false;
-  Clock::time_point busy_t0_{};
-  uint64_t busy_units_ = 0;
-  uint64_t inflight_ = 0, running_ = 0, max_running_ = 0;
-  std::atomic<uint64_t> read_ns_{0};
-  std::exception_ptr err_;
-  bool stop_ = false;
-};
 
 // ---- the HIP transport ----------------------------------------------------------------------------------------------
 class HipTransport final : public DgTransport {
@@ -275,45 +109,73 @@ class HipTransport final : public DgTransport {
     dev_->free_device(vfail_dev_);
     for (hipEvent_t e : prof_events_) dev_->event_destroy(e);
     for (char* b : stage_) dev_->free_pinned(b);
+    for (void* c : land_chunks_) dev_->free_pinned(c);
+    for (hipEvent_t e : land_copy_ev_) dev_->event_destroy(e);
     dev_->free_pinned(rword_host_);
   }
 
   hipStream_t stream(Stream s) const { return s_[s]; }
-  // blocks 0 .. blocks - 1: the pinned homes and spares (in chunks); blocks .. blocks + S - 1: the staging buffers
+  // blocks 0 .. blocks - 1: the pinned homes and spares (in chunks); blocks .. blocks + S - 1: the staging buffers;
+  // blocks + S .. blocks + S + L - 1: the landing blocks (in chunks)
   char* block_ptr(int32_t b) const {
+    if (uint32_t(b) >= x_.blocks + x_.S) {
+      const uint64_t l = uint32_t(b) - x_.blocks - x_.S;
+      return static_cast<char*>(land_chunks_[size_t(l / land_per_chunk_)]) + (l % land_per_chunk_) * x_.host_stride;
+    }
     if (uint32_t(b) >= x_.blocks) return stage_[size_t(uint32_t(b) - x_.blocks)];
     return static_cast<char*>(chunks_[size_t(uint64_t(b) / per_chunk_)]) + (uint64_t(b) % per_chunk_) * x_.host_stride;
   }
+  bool landing_block(int32_t b) const { return uint32_t(b) >= x_.blocks + x_.S; }
   // Three-tier: the staging buffers (pinned, one host stride each) and the context's readers of a key's file bytes
-  // (the whole unit; a piece of a part) and its finisher; with x_.disk_queue > 1 a read pool and one word per
-  // staging buffer in fine-grained host memory.
+  // (the whole unit; a piece of a part) and its finisher; with x_.disk_queue > 1 a read pool, one word per staging
+  // buffer in fine-grained host memory (then one per bank slot with dg_bank_keep, then one per landing block) and the
+  // landing blocks (pinned, in chunks of at most 1 GiB).
   void enable_disk(std::function<void(uint32_t, char*)> reader, ReadPool::PieceReader piece_reader,
                    ReadPool::Finisher finisher, const DgDevWords& dw) {
     reader_ = std::move(reader);
     for (uint32_t i = 0; i < x_.S; ++i)
       stage_.push_back(static_cast<char*>(dev_->alloc_pinned(x_.host_stride, "disk staging buffer")));
     if (x_.disk_queue > 1) {
-      // one word per staging buffer, then (dg_bank_keep) one per bank slot for reads kept in a pinned block
-      const uint32_t words = x_.S + (x_.bank_keep ? 2 * x_.B : 0);
+      land_word0_ = x_.S + (x_.bank_keep ? 2 * x_.B : 0);
+      const uint32_t words = land_word0_ + x_.L;
       rword_host_ = static_cast<uint32_t*>(dev_->alloc_mapped(4ull * words, &rword_dev_, "read words"));
       std::memset(rword_host_, 0, 4ull * words);
       rgen_.assign(words, 0);
       rpending_.assign(words, 0);
       raux_.assign(words, 0);
       dw_ = dw;
-      std::vector<ReadPool::Piece> pieces;  // 8 MiB slices of each part (4 KiB-aligned; the last one the rest)
-      for (uint32_t p = 0; p < x_.part_bytes.size(); ++p)
-        for (uint64_t o = 0; o < x_.part_bytes[p]; o += kReadPiece)
-          pieces.push_back(ReadPool::Piece{p, o, std::min(kReadPiece, x_.part_bytes[p] - o), x_.part_offset[p] + o});
-      pool_ = std::make_unique<ReadPool>(x_.disk_queue, std::move(pieces), std::move(piece_reader),
-                                         std::move(finisher));
+      const auto slices = [&](uint64_t piece) {  // slices of each part (4 KiB-aligned; the last one the rest)
+        std::vector<ReadPool::Piece> v;
+        for (uint32_t p = 0; p < x_.part_bytes.size(); ++p) {
+          const uint64_t step = piece ? piece : x_.part_bytes[p];
+          for (uint64_t o = 0; o < x_.part_bytes[p]; o += step)
+            v.push_back(ReadPool::Piece{p, o, std::min(step, x_.part_bytes[p] - o), x_.part_offset[p] + o});
+        }
+        return v;
+      };
+      ReadPool::LandingRule lr;
+      if (x_.L) {
+        land_per_chunk_ = std::max<uint64_t>(1, kPinnedChunk / x_.host_stride);
+        for (uint64_t left = x_.L; left > 0;) {
+          const uint64_t n = std::min(land_per_chunk_, left);
+          land_chunks_.push_back(dev_->alloc_pinned(n * x_.host_stride, "landing blocks"));
+          left -= n;
+        }
+        land_copy_ev_.assign(x_.L, nullptr);
+        land_key_.assign(x_.L, 0);
+        lr.pieces = slices(x_.landing_chunk);
+        lr.cap = x_.landing_queued;
+        lr.reserve = x_.landing_chunk != 0;  // (whole reads: at most `cap` reads of any kind, as before chunks)
+      }
+      pool_ = std::make_unique<ReadPool>(x_.disk_queue, words, slices(kReadPiece), std::move(lr),
+                                         std::move(piece_reader), std::move(finisher));
     }
   }
   // A file read into staging buffer `block`, or (dg_bank_keep) into pinned block `block` for bank slot `slot`:
   // synchronous, or queued to the pool (the copy out of the block then awaits the read's word: a staging buffer's, or
   // the bank slot's, which is reused only once the copy that awaited it last has run).
   void read_unit(uint32_t key, int32_t block, int32_t slot) override {
-    const bool staged = uint32_t(block) >= x_.blocks;
+    const bool staged = uint32_t(block) >= x_.blocks && uint32_t(block) < x_.blocks + x_.S;
     const bool kept = !staged && x_.bank_keep && slot >= int32_t(x_.persistent_slots) &&
                       uint32_t(slot) < x_.persistent_slots + 2 * x_.B;
     require(reader_ && (staged || kept), SS_E_BACKEND,
@@ -329,10 +191,38 @@ class HipTransport final : public DgTransport {
     const uint32_t i = staged ? uint32_t(block) - x_.blocks : x_.S + (uint32_t(slot) - x_.persistent_slots);
     if (++rgen_[i] == 0) rgen_[i] = 1;  // (0 is the word's initial value)
     rpending_[i] = rgen_[i];
-    raux_[i] = uint32_t(std::upper_bound(x_.unit_base.begin(), x_.unit_base.end(), key) - x_.unit_base.begin()) - 1;
+    raux_[i] = gated_of(key);
     if (!staged) kept_word_[block] = i;
-    pool_->submit(key, block_ptr(block), rword_host_ + i, rgen_[i]);
+    pool_->submit(i, key, block_ptr(block), rword_host_ + i, rgen_[i]);
   }
+  uint32_t gated_of(uint32_t key) const {
+    return uint32_t(std::upper_bound(x_.unit_base.begin(), x_.unit_base.end(), key) - x_.unit_base.begin()) - 1;
+  }
+  // A landing read into landing block `block`, on the pool's landing queue. The block's previous read (a landing
+  // dropped while it ran) and its last copy out (a promotion's) end first: waited for here, on the host.
+  void read_landing(uint32_t key, int32_t block) override {
+    require(pool_ && landing_block(block), SS_E_BACKEND, "device-gated: a landing read without landing blocks");
+    const uint32_t l = uint32_t(block) - x_.blocks - x_.S, i = land_word0_ + l;
+    const auto t0 = Clock::now();
+    bool waited = pool_->wait_idle(i) > 0;
+    if (hipEvent_t e = land_copy_ev_[l]; e && !ev_done(e)) {
+      ev_sync(e);
+      waited = true;
+    }
+    if (waited)
+      land_wait_ns_ += uint64_t(std::chrono::duration_cast<std::chrono::nanoseconds>(Clock::now() - t0).count());
+    if (++rgen_[i] == 0) rgen_[i] = 1;
+    rpending_[i] = rgen_[i];
+    raux_[i] = gated_of(key);
+    land_key_[l] = key;
+    pool_->submit_landing(i, key, block_ptr(block), rword_host_ + i, rgen_[i]);
+  }
+  void drop_landing(int32_t block) override {
+    if (pool_ && landing_block(block)) pool_->drop(land_word0_ + (uint32_t(block) - x_.blocks - x_.S));
+  }
+  // The physical side of landings: ns the service waited on a landing block's reuse, and the pool's counts.
+  uint64_t landing_wait_ns() const { return land_wait_ns_; }
+  ReadPool::LandingCounts landing_counts() const { return pool_ ? pool_->landing_counts() : ReadPool::LandingCounts{}; }
   // Every read submitted so far has returned; rethrows the first failed read (the token fails before the layer whose
   // copies read it is signalled ready, so its bytes never reach an engine).
   void drain_reads() {
@@ -365,6 +255,11 @@ class HipTransport final : public DgTransport {
   void h2d(Stream s, int32_t slot, int32_t block) override {
     h2d_unit(s, slot, block);
     wait_slot_ = wait_block_ = -1;
+    if (landing_block(block)) {  // the block's next landing read waits for this copy
+      hipEvent_t& e = land_copy_ev_[size_t(uint32_t(block) - x_.blocks - x_.S)];
+      if (!e) e = dev_->event_create();
+      ev_record(e, s_[s]);
+    }
   }
   void part_wait(Stream s, int32_t slot, int32_t block, uint32_t p) {
     if (slot >= 0 && slot == wait_slot_) stream_wait(s_[s], part_ev_[part_ev_index(false, slot, p)]);
@@ -372,9 +267,23 @@ class HipTransport final : public DgTransport {
   }
   void h2d_unit(Stream s, int32_t slot, int32_t block) {
     const char* src = block_ptr(block);
+    const bool landing = landing_block(block);
+    if (landing) {  // a promotion: its landing read becomes a demand read if it still runs; one that failed reads again
+      const uint32_t l = uint32_t(block) - x_.blocks - x_.S, i = land_word0_ + l;
+      const ReadPool::Claim c = pool_->claim(i);
+      if (c == ReadPool::Claim::Landed) {
+        rpending_[i] = 0;  // (its word is stored: nothing to await)
+      } else if (c == ReadPool::Claim::Failed) {
+        if (++rgen_[i] == 0) rgen_[i] = 1;
+        rpending_[i] = rgen_[i];
+        pool_->submit(i, land_key_[l], block_ptr(block), rword_host_ + i, rgen_[i]);
+      }
+    }
     if (pool_) {  // a read into this block may still run: the stream waits for the read's word
       uint32_t i = UINT32_MAX;
-      if (uint32_t(block) >= x_.blocks) {
+      if (landing) {
+        i = land_word0_ + (uint32_t(block) - x_.blocks - x_.S);
+      } else if (uint32_t(block) >= x_.blocks) {
         i = uint32_t(block) - x_.blocks;
       } else if (!kept_word_.empty()) {
         const auto it = kept_word_.find(block);
@@ -765,6 +674,12 @@ class HipTransport final : public DgTransport {
   void* rword_dev_ = nullptr;
   std::vector<uint32_t> rgen_, rpending_, raux_;      // per read word: last generation, one to await, its layer
   std::unordered_map<int32_t, uint32_t> kept_word_;   // dg_bank_keep: a pinned block read into -> its read's word
+  std::vector<void*> land_chunks_;                    // the landing blocks (pinned chunks)
+  uint64_t land_per_chunk_ = 1;
+  uint32_t land_word0_ = 0;                           // the first landing block's read word
+  std::vector<hipEvent_t> land_copy_ev_;              // per landing block: its last copy out (lazily made)
+  std::vector<uint32_t> land_key_;                    // per landing block: the key of its last landing read
+  uint64_t land_wait_ns_ = 0;
   DgDevWords dw_;                                     // the await kernel's abort words and deadline
   uint64_t read_ns_ = 0, read_wait_ns_ = 0;
   std::function<void(uint32_t, char*)> reader_;       // three-tier: a key's bytes from its file, host block layout
@@ -1209,6 +1124,18 @@ class HipDgCtx final : public DgCtx {
     TSA_D(clean_drops);
     TSA_D(clean_drop_bytes);
     TSA_D(bank_kept);
+    TSA_D(landing_issued);
+    TSA_D(landing_promoted);
+    TSA_D(landing_late);
+    TSA_D(landing_wait_ns);
+    TSA_D(landing_expired);
+    TSA_D(landing_dropped_full);
+    TSA_D(landing_read_bytes);
+    TSA_D(landing_cancelled);
+    TSA_D(landing_expired_layer);
+    TSA_D(landing_skipped_passed);
+    TSA_D(landing_yields);
+    TSA_D(landing_aborted_bytes);
     TSA_D(score_fallbacks);
     TSA_D(scored_victims);
     TSA_D(score_layers);
@@ -1287,8 +1214,7 @@ class HipDgCtx final : public DgCtx {
     hook_user_ = user;
   }
   Json stats_json() const override {
-    return format_stats(stats(), exclusive_stats(), layers_now(), core_->policy(),
-                        fold_.bank_keep_drops - base_.bank_keep_drops, fold_.bank_keep_rereads - base_.bank_keep_rereads);
+    return format_stats(stats(), exclusive_stats(), layers_now(), core_->policy(), extras());
   }
   bool snapshot(ss_layer_stats* total, ss_snapshot_info* info) const override {
     snap_armed_.store(true, std::memory_order_relaxed);
@@ -1321,7 +1247,7 @@ class HipDgCtx final : public DgCtx {
       if (snap_.seq == 0) return false;
       p = snap_;
     }
-    *out = format_stats(p.s, p.x, p.layers, p.policy, p.keep_drops, p.keep_rereads);
+    *out = format_stats(p.s, p.x, p.layers, p.policy, p.extra);
     return true;
   }
   // After a successful boundary (and at open): the core's counters as the stats show them, the hook with this
@@ -1329,6 +1255,16 @@ class HipDgCtx final : public DgCtx {
   void fold(bool call_hook) {
     prev_l_ = fold_l_;
     fold_ = core_->counts();
+    if (x_.L) {  // the landings' physical side; the bytes landed are the reads issued less those never read
+      const ReadPool::LandingCounts lc = tr_->landing_counts();
+      fold_.landing_late = lc.late;
+      fold_.landing_wait_ns = tr_->landing_wait_ns();
+      fold_.landing_cancelled = lc.cancelled;
+      fold_.landing_yields = lc.yields;
+      fold_.landing_aborted_bytes = lc.aborted_bytes;
+      fold_.landing_failed = lc.failed;
+      fold_.landing_read_bytes -= std::min(fold_.landing_read_bytes, lc.unread_bytes);
+    }
     fold_l_ = core_->layer_counts();
     fold_free_slots_ = core_->free_slots();
     fold_free_blocks_ = core_->free_blocks();
@@ -1456,13 +1392,20 @@ class HipDgCtx final : public DgCtx {
   uint64_t fold_read_ns_ = 0, fold_wait_ns_ = 0, fold_max_in_flight_ = 0, base_read_ns_ = 0, base_wait_ns_ = 0;
   ss_stats_hook hook_ = nullptr;
   void* hook_user_ = nullptr;
+  struct Extras {  // counters the stats document shows outside ss_dg_stats (since the last reset)
+    uint64_t keep_drops = 0, keep_rereads = 0, landing_failed = 0;
+  };
+  Extras extras() const {
+    return Extras{fold_.bank_keep_drops - base_.bank_keep_drops, fold_.bank_keep_rereads - base_.bank_keep_rereads,
+                  fold_.landing_failed - base_.landing_failed};
+  }
   struct Published {
     uint64_t seq = 0;
     ss_dg_stats s{};
     ss_exclusive_stats x{};
     std::vector<ss_layer_stats> layers;
     uint32_t policy = 0;
-    uint64_t keep_drops = 0, keep_rereads = 0;  // (dg_bank_keep counters outside ss_dg_stats)
+    Extras extra;
   };
   mutable std::atomic<bool> snap_armed_{false};
   mutable std::mutex snap_mu_;
@@ -1500,14 +1443,13 @@ class HipDgCtx final : public DgCtx {
     p.x = exclusive_stats();
     p.layers = layers_now();
     p.policy = core_->policy();  // (the engine thread's: a reader on another thread formats this copy)
-    p.keep_drops = fold_.bank_keep_drops - base_.bank_keep_drops;
-    p.keep_rereads = fold_.bank_keep_rereads - base_.bank_keep_rereads;
+    p.extra = extras();
     std::lock_guard<std::mutex> lk(snap_mu_);
     p.seq = snap_.seq + 1;
     std::swap(snap_, p);
   }
   Json format_stats(const ss_dg_stats& s, const ss_exclusive_stats& x, const std::vector<ss_layer_stats>& layers,
-                    uint32_t policy, uint64_t s_keep_drops, uint64_t s_keep_rereads) const;
+                    uint32_t policy, const Extras& extra) const;
 };
 
 void HipDgCtx::init() {
@@ -1603,6 +1545,8 @@ void HipDgCtx::init() {
   c.disk_staging = x_.S;
   c.clean_evict = o_.dg_clean_evict != 0;
   c.bank_keep = x_.bank_keep;
+  c.landing_blocks = x_.L;
+  c.landing_ttl = x_.landing_ttl;
   c.scored = x_.scored;
   c.scored_auto = o_.policy == SS_POLICY_SCORED_AUTO;
   c.w_trans = x_.w_trans;
@@ -1668,12 +1612,11 @@ void HipDgCtx::init() {
 
 // The stats-v1 document of a device-gated context (reference src/dg_ctx.cpp:1359-1545): the host contract's keys, the
 // exclusive object and the device_gated object. Counters of what this library does not serve (priors, window
-// prefetches, landings, placement rounds, make-resident, bank keeping) are 0, as the reference writes them when those
-// are off; so are score_deferred and score_last_ns (this library ranks only at the boundary, where score_ns counts the
+// prefetches, placement rounds, make-resident, layer tokens) are 0, as the reference writes them when those are off;
+// so are score_deferred and score_last_ns (this library ranks only at the boundary, where score_ns counts the
 // selection); backend is "hip".
 Json HipDgCtx::format_stats(const ss_dg_stats& s, const ss_exclusive_stats& x,
-                            const std::vector<ss_layer_stats>& layers, uint32_t pol, uint64_t s_keep_drops,
-                            uint64_t s_keep_rereads) const {
+                            const std::vector<ss_layer_stats>& layers, uint32_t pol, const Extras& extra) const {
   static const std::pair<const char*, uint64_t ss_dg_stats::*> kFields[] = {
       {"tokens", &ss_dg_stats::tokens}, {"lookups", &ss_dg_stats::lookups}, {"misses", &ss_dg_stats::misses},
       {"covered", &ss_dg_stats::covered}, {"fetched", &ss_dg_stats::fetched},
@@ -1768,13 +1711,14 @@ Json HipDgCtx::format_stats(const ss_dg_stats& s, const ss_exclusive_stats& x,
   g["pf_revert_unused"] = Json::number(uint64_t(0));
   g["pf_strict_admit"] = Json::number(uint64_t(0));
   g["pf_legacy"] = Json::number(uint64_t(1));
-  g["landing_blocks"] = Json::number(uint64_t(0));
-  g["landing_max_queued"] = Json::number(uint64_t(0));
-  g["landing_ttl"] = Json::number(uint64_t(0));
-  g["landing_failed"] = Json::number(uint64_t(0));
+  g["landing_blocks"] = Json::number(uint64_t(x_.L));
+  g["landing_max_queued"] = Json::number(uint64_t(x_.L ? x_.landing_queued : 0));
+  g["landing_ttl"] = Json::number(uint64_t(x_.landing_ttl));
+  g["landing_failed"] = Json::number(extra.landing_failed);
   g["policy"] = Json::string(pol == 2 ? "auto" : pol == 1 ? "scored" : "lru");
   g["cuda_module_loading"] = Json::string("unknown");  // (a CUDA setting; HIP has no such mode)
-  g["landing_chunk"] = Json::number(uint64_t(0));
+  if (x_.L && !x_.landing_chunk) g["landing_chunk"] = Json::string("whole");
+  else g["landing_chunk"] = Json::number(uint64_t(x_.L ? x_.landing_chunk : 0));
   if (!score_prov_.empty()) g["score_profile"] = Json::string(score_prov_);
   if (x_.disk_tier || x_.I) {  // three tiers or clean copies: only then, so the two-tier document is unchanged
     Json tt = Json::object();
@@ -1782,8 +1726,8 @@ Json HipDgCtx::format_stats(const ss_dg_stats& s, const ss_exclusive_stats& x,
     tt["unit_subread_bytes"] = Json::number(uint64_t(0));
     tt["clean_evict"] = Json::number(uint64_t(uint64_t(o_.dg_clean_evict != 0)));
     tt["bank_keep"] = Json::number(uint64_t(o_.dg_bank_keep));
-    tt["bank_keep_drops"] = Json::number(s_keep_drops);
-    tt["bank_keep_rereads"] = Json::number(s_keep_rereads);
+    tt["bank_keep_drops"] = Json::number(extra.keep_drops);
+    tt["bank_keep_rereads"] = Json::number(extra.keep_rereads);
     tt["disk_queue"] = Json::number(uint64_t(uint64_t(x_.disk_queue)));
     tt["disk_queue_resolved"] = Json::number(uint64_t(uint64_t(x_.disk_queue)));
     tt["disk_locations"] = Json::number(uint64_t(uint64_t(x_.disk_tier ? 1 : 0)));

@@ -65,7 +65,6 @@ void check_options(const ss_options& o, const ss_budget& b) {
       {o.dg_landing_blocks && o.dg_disk_queue <= 1, SS_E_INVALID,
        "dg_landing_blocks needs dg_disk_queue > 1 (landing reads run on the reader threads)"},
       // valid for the reference, not served by this library
-      {o.dg_landing_blocks != 0, SS_E_UNSUPPORTED, "landings (dg_landing_*) are not served by this library"},
       {o.dg_no_admit || o.dg_pf_revert_unused || o.dg_pf_strict_admit || o.dg_prior_len || o.dg_prior,
        SS_E_UNSUPPORTED, "dg_no_admit, dg_pf_revert_unused, dg_pf_strict_admit and priors are not served by this library"},
   };
@@ -154,6 +153,10 @@ void size_disk_tier(const ss_options& o, DgGeometry& x) {
   x.disk_prefetch = o.dg_disk_prefetch != 0;
   x.bank_keep = x.disk_tier ? o.dg_bank_keep : 0;  // (no effect without the file tier)
   if (!x.disk_tier) return;
+  x.L = x.F ? o.dg_landing_blocks : 0u;  // (nothing to land without file homes)
+  x.landing_queued = o.dg_landing_max_queued ? o.dg_landing_max_queued : 1u;
+  x.landing_ttl = o.dg_landing_ttl;
+  x.landing_chunk = o.dg_landing_chunk == 0xFFFFFFFFu ? 0u : o.dg_landing_chunk ? o.dg_landing_chunk : 4ull << 20;
   if (o.dg_disk_queue == kQueueAuto) {
     constexpr uint32_t kLocations = 1;
     x.disk_queue = std::min<uint32_t>(std::max<uint32_t>(3 * kLocations, 4), 8);
@@ -185,6 +188,45 @@ void size_scoring(const Desc& d, const ss_options& o, DgGeometry& x) {
     x.score_identity = score_identity(d, x.gated);
     (void)check_score_profile(o.dg_score_profile, o.dg_score_profile_len, units, x.score_identity);
   }
+}
+
+// Host admission: the pinned bytes an open adds to the plan's (reference src/dg_layout.cpp:96-125 and :393-420, whose
+// sum decides which budgets admit an open, so it is kept as it is): the control area as laid out for 64-id records
+// (a 288-byte export record and a 272-byte prediction record per gated layer, three word arrays of the gated layers,
+// seven words, and 32 layer-token part records with two part word arrays), a bounce buffer per reader (the context's
+// and each file reader's, min(staging_bytes, 16 MiB) rounded up to the sources' alignment, at least 4 alignments; with
+// file readers cut to the largest part plus two alignments), one unit of staging (4 KiB rounded), and the file
+// tier's staging buffers and landing blocks of one host stride each.
+struct HostExtra {
+  uint64_t mapped = 0, bounce = 0, staging = 0, disk_staging = 0, landing = 0, total = 0;
+};
+HostExtra host_extra(const Desc& d, const ss_options& o, const DgGeometry& x) {
+  constexpr uint64_t kRecord = 288, kPredRecord = 272, kParts = 32;
+  const auto a64 = [](uint64_t v) { return (v + 63) / 64 * 64; };
+  const uint64_t G = x.gated.size();
+  HostExtra h;
+  h.mapped = a64(G * kRecord) + a64(G * kPredRecord) + 3 * a64(G * 4) + a64(7 * 4) + a64(kParts * kRecord) +
+             2 * a64(kParts * 4);
+  uint64_t align = 4096, part_max = 0;
+  for (const Source& src : d.sources) align = std::max(align, src.align);
+  for (uint64_t pb : x.part_bytes) part_max = std::max(part_max, pb);
+  const auto up = [align](uint64_t v) {
+    uint64_t r = 0;
+    if (__builtin_add_overflow(v, align - 1, &r)) refuse(SS_E_INVALID, "the bounce buffer overflows");
+    return r / align * align;
+  };
+  const uint64_t want = std::min<uint64_t>(o.staging_bytes ? o.staging_bytes : 16ull << 20, 16ull << 20);
+  uint64_t bounce = std::max(up(want), 4 * align);
+  const uint64_t readers = 1 + (x.disk_queue > 1 ? x.disk_queue : 0);
+  if (readers > 1) bounce = std::max(std::min(bounce, up(part_max + 2 * align)), 4 * align);
+  h.bounce = bounce * readers;
+  h.staging = (x.unit_bytes + 4095) / 4096 * 4096;
+  h.disk_staging = uint64_t(x.S) * x.host_stride;
+  h.landing = uint64_t(x.L) * x.host_stride;
+  const uint64_t parts[] = {h.mapped, h.bounce, h.staging, h.disk_staging, h.landing};
+  for (uint64_t v : parts)
+    if (__builtin_add_overflow(h.total, v, &h.total)) refuse(SS_E_INVALID, "the host extras overflow");
+  return h;
 }
 
 }  // namespace
@@ -239,6 +281,23 @@ DgGeometry dg_geometry(const Desc& d, const Plan& p, const ss_options& o) {
   if (rest + x.arena_need > limit)
     refuse(SS_E_CAPACITY, "the arena needs " + std::to_string(x.arena_need) + " bytes of HBM where the plan billed " +
                               std::to_string(billed) + "; with the rest of the plan that exceeds the cap less margin");
+  const HostExtra h = host_extra(d, o, x);
+  uint64_t host_total = 0;
+  if (__builtin_add_overflow(p.pinned, h.total, &host_total)) refuse(SS_E_INVALID, "the host bytes overflow");
+  if (host_total > p.budget.host_pinned_bytes)
+    refuse(SS_E_CAPACITY, "the plan's pinned bytes (" + std::to_string(p.pinned) + ") plus the control area (" +
+                              std::to_string(h.mapped) + "), the bounce buffers (" + std::to_string(h.bounce) +
+                              "), the staging unit (" + std::to_string(h.staging) + "), the file tier's staging "
+                              "buffers (" + std::to_string(h.disk_staging) + ") and the landing blocks (" +
+                              std::to_string(h.landing) + ") exceed the host budget (" +
+                              std::to_string(p.budget.host_pinned_bytes) + ")");
+  // ... and headroom for four units beyond that: the reference's open streams its startup through a ring of four
+  // buffers of at least a unit each (reference src/dg_layout.cpp:425-444, its defaults). This open stages its startup
+  // through the spare blocks instead, but admits the same budgets.
+  const uint64_t headroom = p.budget.host_pinned_bytes - host_total;
+  if (headroom / 4 / 4096 * 4096 < x.unit_bytes)
+    refuse(SS_E_CAPACITY, "the host budget leaves " + std::to_string(headroom) + " bytes beyond the open's pinned "
+                              "bytes; the startup needs four units (" + std::to_string(4 * x.unit_bytes) + ")");
   return x;
 }
 

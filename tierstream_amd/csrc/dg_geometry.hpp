@@ -5,8 +5,9 @@
 //
 // The rules are the reference's (src/dg_layout.cpp:159-180 and :182-393): the geometry is part of what an engine sees
 // (slot counts, the guard slot) and the refusals are part of the ABI. This library serves a subset of the reference's
-// options (landings, no-admit, prefetch revert, strict admission and priors are refused with SS_E_UNSUPPORTED), and it does not re-check the host budget for its own control memory (an
-// allocation that does not fit fails the open with SS_E_NOMEM).
+// options (no-admit, prefetch revert, strict admission and priors are refused with SS_E_UNSUPPORTED), and it does not
+// re-check the host budget for its own control memory (an allocation that does not fit fails the open with
+// SS_E_NOMEM).
 #pragma once
 
 #include <cstdint>
@@ -41,6 +42,11 @@ struct DgGeometry {
   std::vector<uint32_t> residents;  // keys of the planned residents, in key order
   bool disk_tier = false, disk_prefetch = false;
   uint32_t bank_keep = 0;     // dg_bank_keep with the file tier (0 without it)
+  // landings (dg_landing_blocks, only with file homes in the plan): L landing blocks (block indices blocks + S ..);
+  // landing pieces running at most; the TTL in boundaries (0: expiry after the target layer); a landing read's piece
+  // bytes (0: one piece per part, dg_landing_chunk 0xFFFFFFFF)
+  uint32_t L = 0, landing_queued = 1, landing_ttl = 0;
+  uint64_t landing_chunk = 4ull << 20;
   std::vector<uint8_t> disk;  // per key: a file home (three tiers only)
   bool scored = false;
   uint32_t w_trans = 700, w_freq = 200, w_rec = 100;

@@ -131,7 +131,7 @@ extern "C" ss_status tsa_test_dg_geometry(const char* desc_json, size_t len, con
     const DgGeometry x = dg_geometry(d, p, *opt);
     const uint32_t v[] = {x.keys, uint32_t(x.gated.size()), x.R, x.D, x.B, x.P, x.F, x.Q, x.I, x.S, x.disk_queue,
                           x.persistent_slots, x.slots, x.guard_slot, x.blocks, uint32_t(x.scored), x.w_trans,
-                          x.w_freq, x.w_rec};
+                          x.w_freq, x.w_rec, x.L, x.landing_queued, x.landing_ttl, uint32_t(x.landing_chunk)};
     std::memcpy(out, v, sizeof v);
     for (uint32_t i = 0; residents && i < res_cap && i < x.residents.size(); ++i) residents[i] = x.residents[i];
   });

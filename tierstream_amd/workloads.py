@@ -291,7 +291,9 @@ def dg_shape(w: Workload) -> DgShape:
     # the planner reserves min(dynamic slots, units) for every layer before it places residents (reference
     # src/plan.cpp:60-64); the spare slots it bills afterwards (D) are what the residents leave
     reserve = w.layers * min(dyn, w.units)
-    budget = dict(device_bytes=(R + reserve + ring) * st + st // 2, host_pinned_bytes=(P + Q) * hs + hs // 2,
+    # the open pins a staging unit, a bounce buffer and its control area on top of the plan's blocks, and admits a
+    # budget with four units of startup headroom beyond them
+    budget = dict(device_bytes=(R + reserve + ring) * st + st // 2, host_pinned_bytes=(P + Q + 5) * hs + (64 << 20),
                   dynamic_slots_per_layer=dyn, ring_slots=ring, tier_mode=1, host_spare_units=Q)
     options = dict(forward_mode=1, dg_max_ids=B, pin_planned=0, dg_inclusive_blocks=I, dg_wb_defer=1)
     return DgShape(R, D, B, P, Q, I, budget, options)
@@ -313,7 +315,11 @@ def _dg_shape_three_tier(w: Workload, R: int, B: int, st: int, hs: int) -> DgSha
     if P < 1 or F < 1:
         raise ValueError(f"{w.name}: three tiers need pinned and file units (R {R}, P {P}, F {F})")
     reserve = w.layers * min(dyn, w.units)
-    budget = dict(device_bytes=(R + reserve + ring) * st + st // 2, host_pinned_bytes=(P + Q) * hs + hs // 2,
+    # the open's own pinned buffers come on top of the plan's: a staging unit, the 8 staging buffers of the file tier,
+    # a margin for its control area and a bounce buffer per reader, and four units of startup headroom (landing
+    # blocks, when asked for, are added by the caller)
+    budget = dict(device_bytes=(R + reserve + ring) * st + st // 2,
+                  host_pinned_bytes=(P + Q + 13) * hs + (160 << 20),
                   dynamic_slots_per_layer=dyn, ring_slots=ring, tier_mode=1, host_spare_units=Q)
     options = dict(forward_mode=1, dg_max_ids=B, pin_planned=0, dg_wb_defer=1, dg_disk_tier=1,
                    dg_disk_queue=w.disk_queue, dg_clean_evict=w.clean_evict)
