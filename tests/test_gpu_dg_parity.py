@@ -272,7 +272,10 @@ def _check_stats_doc(ctx, want, tokens, policy="lru", prov=None, publications=No
             assert "three_tier" not in g or g["three_tier"][k] == st[k], k
         else:
             assert g[k] == st[k], k
-    assert g["policy"] == policy and g["landing_issued"] == 0 and g["pf_legacy"] == 1
+    assert g["policy"] == policy and g["pf_legacy"] == 1
+    for k in LANDING_COUNTERS + ["landing_read_bytes", "landing_cancelled", "landing_late", "landing_yields",
+                                 "landing_aborted_bytes"]:
+        assert g[k] == st[k], k
     assert g.get("score_profile") == prov
     for k in SCORE_COUNTERS:
         assert g[k] == st[k], k
