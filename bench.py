@@ -94,6 +94,8 @@ def parse():
     ap.add_argument("--landing-blocks", type=int, default=0,
                     help="three tiers: dg_landing_blocks (predicted file-homed units read ahead into landing blocks)")
     ap.add_argument("--landing-ttl", type=int, default=0, help="three tiers: dg_landing_ttl")
+    ap.add_argument("--landing-max-queued", type=int, default=0, help="three tiers: dg_landing_max_queued")
+    ap.add_argument("--landing-chunk", type=int, default=0, help="three tiers: dg_landing_chunk")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the copy peaks and the library's HBM kernels alone (no serve loop: for counter runs)")
     return ap.parse_args()
@@ -441,7 +443,8 @@ def main():
         if three and a.disk_adapt:
             extra.update(dg_disk_queue=0xFFFFFFFF, dg_disk_queue_adapt=1)
         if three and a.landing_blocks:
-            extra.update(dg_landing_blocks=a.landing_blocks, dg_landing_ttl=a.landing_ttl)
+            extra.update(dg_landing_blocks=a.landing_blocks, dg_landing_ttl=a.landing_ttl,
+                         dg_landing_max_queued=a.landing_max_queued, dg_landing_chunk=a.landing_chunk)
         opts = {**shape.options, **extra}
         ctx = keep(ss.Ctx(d, b, plan, ss.options(**opts, verify_hash=2, dg_wait_timeout_ms=20000, policy=policy)))
         log(f"context open (fill + hash check) in {time.time() - t0:.1f} s")
