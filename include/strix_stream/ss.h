@@ -392,6 +392,33 @@ SS_API ss_status ss_dg_keep(ss_ctx* c, int g, const int32_t* ids, int n);
  * src/dg_ctx.cpp:580-592). dg_flush_ready has no effect on HIP, which submits work as it is enqueued. */
 #define SS_DG_SET_SCHED 1
 SS_API ss_status ss_dg_set_sched(ss_ctx* c, uint32_t wb_defer, uint32_t flush_ready);
+/* dg_diag = 1: gated layer g's row of the last completed token, between tokens (reference ss.h:702-729). Host
+ * microseconds: seen_us = from the previous layer's service end (layer 0: the previous token's) to its export flag
+ * seen; demand_us = flag seen -> its misses' copies and ready enqueued; pred_wait_us = -> its prediction's flag seen;
+ * prefetch_us = -> the prediction served; serve_us = flag seen -> the layer's service done (write-back slice included).
+ * Counts as the stats count them, for this layer: ids (unique), misses, covered, fetched, prefetched (for the next
+ * layer), predicted_true, covered_waits. Device: dma_ms = the demand stream's time from before the layer's first copy
+ * to its ready word (-1: no miss); dma_first_ms = to the first fetched unit's copies (-1: no fetch); wb_left_ms = how
+ * long the previous boundary's write-backs still ran after the layer's copies began (0: done before; -2: still running
+ * at this boundary; -1: none or no miss); gpu_wait_us / gpu_export_ready_us = the wait kernel's entry / the export
+ * flag -> ready seen, on the device clock (-1: no miss). A failed token's rows keep their host fields, device ones -1. */
+typedef struct ss_dg_layer_timeline {
+  uint32_t struct_size, layer;
+  double seen_us, demand_us, pred_wait_us, prefetch_us, serve_us;
+  uint32_t ids, misses, covered, fetched, prefetched, reserved0;
+  double dma_ms;
+  uint32_t predicted_true, covered_waits;
+  double gpu_wait_us, gpu_export_ready_us, wb_left_ms, dma_first_ms;
+} ss_dg_layer_timeline;
+SS_API ss_status ss_dg_timeline_sized(const ss_ctx* c, int g, ss_dg_layer_timeline* out, uint32_t size);
+/* dg_diag = 1: the last successful boundary's host microseconds: sync = the copy streams' synchronize, select =
+ * admissions, retired write-backs and the victims, upload = the table upload, issue = enqueueing the write-backs;
+ * writebacks = the victims written back. */
+typedef struct ss_dg_boundary_timeline {
+  uint32_t struct_size, writebacks;
+  double sync_us, select_us, upload_us, issue_us;
+} ss_dg_boundary_timeline;
+SS_API ss_status ss_dg_boundary_timeline_sized(const ss_ctx* c, ss_dg_boundary_timeline* out, uint32_t size);
 /* Scored eviction (policy SS_POLICY_SCORED or SS_POLICY_SCORED_AUTO; reference include/strix_stream/ss.h:730-746).
  * Only the boundary's choice of victims changes: the eligible units (on the device, no write-back in flight) are taken
  * lowest score first, score = w_t P + w_f F + w_r Rec in integers (P: the transition estimate from this token's union

@@ -550,3 +550,85 @@ def test_keep_sched_and_host_calls_refuse_bad_arguments(tmp_path, gpu):
     finally:
         eng.close()
         ctx.close()
+
+
+def test_dg_timeline(tmp_path, gpu):
+    """dg_diag = 1 (ss_dg_timeline_sized, ss_dg_boundary_timeline_sized; reference ss.h:702-729): after every token each
+    gated layer's row holds its counts - their sums are the token's ss_dg_stats deltas, which equal the reference
+    core's - host times that add up (demand, prediction wait and prefetch inside the layer's service), and device
+    measurements only where the layer had a miss (its copies' time, the first fetch's copies within it, the wait
+    kernel's stall within the export-to-ready time); the boundary's row counts the token's write-back victims. The
+    calls refuse a context without dg_diag, a gated layer out of range and a host context."""
+    c = dict(CASES["prefetch"])
+    m, bkw, okw = _setup(tmp_path, c["layers"], c["units"], c["parts"], c["n_res"], c["dyn"], c["spares"], c["n_ids"])
+    okw.update(dg_diag=1)
+    d = ss.Desc(m.desc_json())
+    plan = ss.Plan(d, ss.budget(**bkw))
+    tiers = plan.tiers()
+    G, U = c["layers"], c["units"]
+    residents = [L * U + u for L in range(G) for u in range(U) if tiers[L][u] == 0]
+    P = sum(1 for L in range(G) for u in range(U) if tiers[L][u] == 1)
+    Q = plan.json()["spare_blocks"][0]["blocks"]
+    D = sum(min(c["dyn"], sum(1 for u in range(U) if tiers[L][u] != 0)) for L in range(G))
+    refdg = ref.RefDg([U] * G, len(residents) + D, c["n_ids"], P + Q, D, c["parts"], residents + list(range(G * U)))
+    ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(**okw))
+    eng = ss.DgEngine(ctx, c["n_ids"], use_graph=True, n_pred=3)
+    routes = _routes(G, U, c["n_ids"], 16, seed=5, zipf=True)
+    preds = _preds(routes, U, 3)
+    keys = {"ids": "lookups", "misses": "misses", "covered": "covered", "fetched": "fetched",
+            "prefetched": "prefetched", "predicted_true": "predicted_true", "covered_waits": "covered_waits"}
+    try:
+        with pytest.raises(ss.SsError):
+            ctx.dg_timeline(0)  # no token yet
+        with pytest.raises(ss.SsError):
+            ctx.dg_boundary_timeline()
+        prev, prev_ref = ctx.dg_stats(), {sk: 0 for sk in keys.values()}
+        measured = wb_rows = 0
+        for t in range(routes.shape[0]):
+            eng.token(routes[t], preds=preds[t])
+            _, want = refdg.token(routes[t].astype(np.uint32), pred=preds[t].astype(np.uint32))
+            got = ctx.dg_stats()
+            rows = [ctx.dg_timeline(g) for g in range(G)]
+            for k, sk in keys.items():
+                delta = got[sk] - prev[sk]
+                assert sum(r[k] for r in rows) == delta, (t, k)
+                assert delta == want[sk] - prev_ref[sk], (t, k)
+            for g, r in enumerate(rows):
+                assert r["layer"] == g
+                for k in ("seen_us", "demand_us", "pred_wait_us", "prefetch_us", "serve_us"):
+                    assert r[k] >= 0, (t, g, k)
+                assert r["demand_us"] + r["pred_wait_us"] + r["prefetch_us"] <= r["serve_us"] + 1e-3, (t, g, r)
+                if r["misses"]:
+                    assert r["dma_ms"] >= 0 and r["gpu_wait_us"] >= 0, (t, g, r)
+                    assert r["gpu_export_ready_us"] >= r["gpu_wait_us"], (t, g, r)
+                    measured += 1
+                if r["dma_ms"] < 0:
+                    assert r["misses"] == 0 and r["dma_first_ms"] == -1 and r["wb_left_ms"] == -1, (t, g, r)
+                if r["fetched"]:
+                    assert 0 <= r["dma_first_ms"] <= r["dma_ms"] + 1e-3, (t, g, r)
+                assert r["wb_left_ms"] in (-1, -2) or r["wb_left_ms"] >= 0, (t, g, r)
+                wb_rows += r["wb_left_ms"] >= 0
+            b = ctx.dg_boundary_timeline()
+            assert b["writebacks"] == got["wb_deferred"] - prev["wb_deferred"], (t, b)
+            assert min(b["sync_us"], b["select_us"], b["upload_us"], b["issue_us"]) >= 0, (t, b)
+            prev, prev_ref = got, want
+        assert measured > 0 and wb_rows > 0, (measured, wb_rows)
+        with pytest.raises(ss.SsError):
+            ctx.dg_timeline(G)
+    finally:
+        eng.close()
+        ctx.close()
+        refdg.close()
+    okw.update(dg_diag=0)
+    d2 = ss.Desc(m.desc_json())
+    ctx2 = ss.Ctx(d2, ss.budget(**bkw), ss.Plan(d2, ss.budget(**bkw)), ss.options(**okw))
+    eng2 = ss.DgEngine(ctx2, c["n_ids"], use_graph=True)
+    try:
+        eng2.token(routes[0])
+        with pytest.raises(ss.SsError):
+            ctx2.dg_timeline(0)  # opened without dg_diag
+        with pytest.raises(ss.SsError):
+            ctx2.dg_boundary_timeline()
+    finally:
+        eng2.close()
+        ctx2.close()

@@ -482,6 +482,24 @@ ss_status ss_dg_keep(ss_ctx* c, int g, const int32_t* ids, int n) {
 ss_status ss_dg_set_sched(ss_ctx* c, uint32_t wb_defer, uint32_t flush_ready) {
   return ctx_guard(c, [&] { dg_of(c, "ss_dg_set_sched").set_sched(wb_defer, flush_ready); });
 }
+ss_status ss_dg_timeline_sized(const ss_ctx* c, int g, ss_dg_layer_timeline* out, uint32_t size) {
+  return guard([&] {
+    need(c && out && size >= sizeof(uint32_t), "ss_dg_timeline: bad argument");
+    ss_dg_layer_timeline t;
+    dg_of(c, "ss_dg_timeline").timeline(g, &t);
+    t.struct_size = std::min<uint32_t>(size, uint32_t(sizeof t));
+    std::memcpy(static_cast<void*>(out), &t, t.struct_size);
+  });
+}
+ss_status ss_dg_boundary_timeline_sized(const ss_ctx* c, ss_dg_boundary_timeline* out, uint32_t size) {
+  return guard([&] {
+    need(c && out && size >= sizeof(uint32_t), "ss_dg_boundary_timeline: bad argument");
+    ss_dg_boundary_timeline t;
+    dg_of(c, "ss_dg_boundary_timeline").boundary_timeline(&t);
+    t.struct_size = std::min<uint32_t>(size, uint32_t(sizeof t));
+    std::memcpy(static_cast<void*>(out), &t, t.struct_size);
+  });
+}
 ss_status ss_dg_end_rows(ss_ctx* c, uint32_t rows) {
   return ctx_guard(c, [&] { dg_of(c, "ss_dg_end_rows").end(rows); });
 }

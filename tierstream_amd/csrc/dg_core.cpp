@@ -814,6 +814,9 @@ void DgCore::serve_misses(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t 
   for (uint32_t i = 0; i < n; ++i)
     require(ids[i] < nu, SS_E_INVALID,
             "device-gated: gated layer " + str(g) + " exported unit " + str(ids[i]) + " (it has " + str(nu) + ")");
+  const bool any = (mask | dev_mask) != 0;
+  if (any) t_->diag_mark(g, 0);
+  bool first_miss = true;
   for (uint32_t i = 0; i < n; ++i) {  // a repeated id: fetched at its first miss, covered at the next
     const uint32_t k = key(g, ids[i]);
     const KeyState& x = st_[k];
@@ -824,6 +827,8 @@ void DgCore::serve_misses(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t 
     }
     if (!on_device_or_arriving(k)) {
       bring_in(g, ids[i], false);
+      if (first_miss) t_->diag_mark(g, 2);
+      first_miss = false;
       continue;
     }
     if (prefetch_in_flight) {  // the layer's readers wait for the prefetch's copy
@@ -836,7 +841,10 @@ void DgCore::serve_misses(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t 
     served_[g] = 1;
     expire_layer_landings(g, ids, n);
   }
-  if (mask | dev_mask) t_->signal_ready(g, seq_);  // after every fetch's landed()
+  if (any) {
+    t_->signal_ready(g, seq_);  // after every fetch's landed()
+    t_->diag_mark(g, 1);
+  }
 }
 
 void DgCore::note_uses(uint32_t g, const uint32_t* ids, uint32_t n, uint64_t mask) {
@@ -968,8 +976,17 @@ void DgCore::close_token(uint32_t rows, const std::vector<uint32_t>& keep) {
     std::vector<uint8_t>& v;
     ~Unkeep() { v.clear(); }
   } unkeep{kept_};
+  using Clock = std::chrono::steady_clock;
+  const auto us = [](Clock::time_point a, Clock::time_point b) {
+    return double(std::chrono::duration_cast<std::chrono::nanoseconds>(b - a).count()) / 1e3;
+  };
+  DgBoundaryTimes bt = bt_;
+  const auto t_sync = Clock::now();
+  t_->diag_boundary();
   t_->sync(DgTransport::kDem);  // every copy and table write of the token landed before homes change
   t_->sync(DgTransport::kPf);
+  const auto t_select = Clock::now();
+  bt.sync_us = us(t_sync, t_select);
   if (c_.landing_blocks) {  // the blocks copied out of are free; a landing not demanded for landing_ttl boundaries (TTL
     reclaim_lands();        // 0: this one) goes back to its file, no copy (the file holds its bytes)
     for (uint32_t l = 0; l < c_.landing_blocks; ++l) {
@@ -1042,7 +1059,11 @@ void DgCore::close_token(uint32_t rows, const std::vector<uint32_t>& keep) {
       k = next;
     }
   }
+  const auto t_upload = Clock::now();
+  bt.select_us = us(t_select, t_upload);
   t_->upload_table(mirror_.data(), keys_);  // the device table equals the mirror before any write-back is enqueued
+  const auto t_issue = Clock::now();
+  bt.upload_us = us(t_upload, t_issue);
 
   // Queued write-backs older than this boundary and the one before it are submitted now (the carry); this boundary's
   // victims are queued (or, without queueing, copied whole on kD2h).
@@ -1079,7 +1100,12 @@ void DgCore::close_token(uint32_t rows, const std::vector<uint32_t>& keep) {
       ++per_layer_[gated_of(k)].evicted;
     }
   }
+  if (!chosen_.empty()) t_->diag_writebacks_issued();
   ev_.sweep();
+  bt.issue_us = us(t_issue, Clock::now());
+  bt.writebacks = uint32_t(chosen_.size());
+  ++bt.boundaries;
+  bt_ = bt;  // (published whole: a boundary that throws leaves the last complete one)
   ++n_.tokens;
 }
 

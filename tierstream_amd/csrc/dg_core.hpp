@@ -81,6 +81,17 @@ class DgTransport {
   virtual void landed(Stream s, uint32_t g, const uint32_t* keys, const int32_t* slots, uint32_t n) {
     (void)s, (void)g, (void)keys, (void)slots, (void)n;
   }
+  // dg_diag timing marks (default: nothing): which 0 = before layer g's first copy, 2 = after its first miss's copies,
+  // 1 = after its ready word; the boundary begins; the boundary has issued its write-backs.
+  virtual void diag_mark(uint32_t g, int which) { (void)g, (void)which; }
+  virtual void diag_boundary() {}
+  virtual void diag_writebacks_issued() {}
+};
+
+struct DgBoundaryTimes {  // the last boundary's host microseconds by phase, its write-back victims, boundaries so far
+  uint64_t boundaries = 0;
+  uint32_t writebacks = 0;
+  double sync_us = 0, select_us = 0, upload_us = 0, issue_us = 0;
 };
 
 struct DgConfig {
@@ -222,6 +233,7 @@ class DgCore {
   uint64_t outstanding_bytes() const { return in_flight_bytes_; }
   uint32_t queued_writebacks() const { return uint32_t(wb_.size() - sealed_); }
   const DgCounts& counts() const { return n_; }
+  const DgBoundaryTimes& boundary_times() const { return bt_; }
   const std::vector<DgLayerCounts>& layer_counts() const { return per_layer_; }
   std::vector<uint32_t> device_order() const;  // device keys, most recent first
 
@@ -458,6 +470,7 @@ class DgCore {
   std::vector<Ranked> ranked_;
   std::vector<uint8_t> kept_;  // during close_token: the keys its keep list protects (empty: none)
   uint64_t token_ = 0, stamp_ = 0;
+  DgBoundaryTimes bt_;
 };
 
 }  // namespace tsa

@@ -111,6 +111,9 @@ class HipTransport final : public DgTransport {
     for (char* b : stage_) dev_->free_pinned(b);
     for (void* c : land_chunks_) dev_->free_pinned(c);
     for (hipEvent_t e : land_copy_ev_) dev_->event_destroy(e);
+    for (auto* v : {&dma_a_, &dma_b_, &dma_f_})
+      for (hipEvent_t e : *v) dev_->event_destroy(e);
+    for (hipEvent_t e : wb_end_) dev_->event_destroy(e);
     dev_->free_pinned(rword_host_);
   }
 
@@ -220,6 +223,74 @@ class HipTransport final : public DgTransport {
   void drop_landing(int32_t block) override {
     if (pool_ && landing_block(block)) pool_->drop(land_word0_ + (uint32_t(block) - x_.blocks - x_.S));
   }
+  // dg_diag: per gated layer three timed events (before its first copy on the demand stream, after its first miss's
+  // copies there, after its ready word on the stream that writes it) and the boundary's write-back end, alternating
+  // between two events so that a token is compared with the boundary before it.
+  void enable_diag(uint32_t G) {
+    for (auto* v : {&dma_a_, &dma_b_, &dma_f_})
+      for (uint32_t g = 0; g < G; ++g) v->push_back(dev_->event_create_timed());
+    dma_used_.assign(G, 0);
+    for (hipEvent_t& e : wb_end_) e = dev_->event_create_timed();
+    diag_ = true;
+  }
+  void diag_mark(uint32_t g, int which) override {
+    if (!diag_ || g >= dma_used_.size()) return;
+    if (which == 0) {
+      ev_record(dma_a_[g], s_[kDem]);
+      dma_used_[g] = 1;
+    } else if (which == 2) {
+      ev_record(dma_f_[g], s_[kDem]);
+      dma_used_[g] = 2;
+    } else {
+      ev_record(dma_b_[g], verify_ ? vs_ : s_[kDem]);
+    }
+  }
+  void diag_boundary() override {
+    if (!diag_) return;
+    wb_prev_ = wb_cur_;
+    wb_prev_valid_ = wb_cur_valid_;
+    wb_cur_ ^= 1;
+    wb_cur_valid_ = false;
+  }
+  void diag_writebacks_issued() override {
+    if (!diag_) return;
+    ev_record(wb_end_[wb_cur_], s_[kD2h]);
+    wb_cur_valid_ = true;
+  }
+  struct LayerDma {
+    double dma_ms = -1, dma_first_ms = -1, wb_left_ms = -1;
+  };
+  // After the boundary: per marked layer the times between its marks, and how long the previous boundary's
+  // write-backs ran past its first mark (-2: still running now). Never throws (a timing error gives -1).
+  std::vector<LayerDma> diag_collect() {
+    std::vector<LayerDma> out(dma_used_.size());
+    if (!diag_) return out;
+    int wb = 0;
+    if (wb_prev_valid_) {
+      const hipError_t q = hipEventQuery(wb_end_[wb_prev_]);
+      wb = q == hipSuccess ? 1 : q == hipErrorNotReady ? -2 : 0;
+    }
+    const auto elapsed = [](hipEvent_t a, hipEvent_t b) {
+      float ms = 0;
+      if (hipEventSynchronize(b) != hipSuccess) return -1.0;
+      return hipEventElapsedTime(&ms, a, b) == hipSuccess ? double(ms) : -1.0;
+    };
+    for (size_t g = 0; g < dma_used_.size(); ++g) {
+      if (!dma_used_[g]) continue;
+      LayerDma& d = out[g];
+      d.dma_ms = elapsed(dma_a_[g], dma_b_[g]);
+      if (dma_used_[g] == 2) d.dma_first_ms = elapsed(dma_a_[g], dma_f_[g]);
+      dma_used_[g] = 0;
+      if (wb == 1) {
+        const double ms = elapsed(dma_a_[g], wb_end_[wb_prev_]);
+        d.wb_left_ms = ms == -1.0 ? -1.0 : ms > 0 ? ms : 0.0;
+      } else if (wb == -2) {
+        d.wb_left_ms = -2;
+      }
+    }
+    return out;
+  }
+  void diag_forget() { std::fill(dma_used_.begin(), dma_used_.end(), uint8_t(0)); }
   // The physical side of landings: ns the service waited on a landing block's reuse, and the pool's counts.
   uint64_t landing_wait_ns() const { return land_wait_ns_; }
   ReadPool::LandingCounts landing_counts() const { return pool_ ? pool_->landing_counts() : ReadPool::LandingCounts{}; }
@@ -680,6 +751,12 @@ class HipTransport final : public DgTransport {
   std::vector<hipEvent_t> land_copy_ev_;              // per landing block: its last copy out (lazily made)
   std::vector<uint32_t> land_key_;                    // per landing block: the key of its last landing read
   uint64_t land_wait_ns_ = 0;
+  bool diag_ = false;                                 // dg_diag: the timeline's device marks
+  std::vector<hipEvent_t> dma_a_, dma_b_, dma_f_;
+  std::vector<uint8_t> dma_used_;                     // per layer: 0 unmarked, 1 marked, 2 with its first miss
+  hipEvent_t wb_end_[2] = {nullptr, nullptr};
+  int wb_cur_ = 0, wb_prev_ = 1;
+  bool wb_cur_valid_ = false, wb_prev_valid_ = false;
   DgDevWords dw_;                                     // the await kernel's abort words and deadline
   uint64_t read_ns_ = 0, read_wait_ns_ = 0;
   std::function<void(uint32_t, char*)> reader_;       // three-tier: a key's bytes from its file, host block layout
@@ -703,8 +780,20 @@ class Service {
     pred_.reserve(kDgMaxIds);
   }
   ~Service() { stop_join(); }
+  // dg_diag: one gated layer's row of the last token served (host times in microseconds; the counters' deltas)
+  struct Row {
+    double seen_us = 0, demand_us = 0, pred_wait_us = 0, prefetch_us = 0, serve_us = 0;
+    uint32_t ids = 0, misses = 0, covered = 0, fetched = 0, prefetched = 0, predicted_true = 0, covered_waits = 0;
+  };
+  void enable_timeline() {
+    diag_ = true;
+    rows_.assign(core_->gated(), Row{});
+  }
+  // Between tokens only (after the token's terminal word, which orders the rows' writes before it).
+  const std::vector<Row>& timeline() const { return rows_; }
   void start() {
     const uint32_t seen = host_seq_.load(std::memory_order_acquire);
+    t_served_ = Clock::now();  // the first token's seen_us of its first layer counts from here
     th_ = std::thread([this, seen] { run(seen); });
   }
   void begin(uint32_t seq, const std::vector<uint8_t>& run) {
@@ -807,11 +896,16 @@ class Service {
       publish(kServed, seq);
     }
   }
+  static double us_between(Clock::time_point a, Clock::time_point b) {
+    return double(std::chrono::duration_cast<std::chrono::nanoseconds>(b - a).count()) / 1e3;
+  }
   void serve_token(uint32_t seq) {
     const uint32_t G = core_->gated();
     std::copy(run_next_.begin(), run_next_.end(), run_.begin());
+    if (diag_) std::fill(rows_.begin(), rows_.end(), Row{});  // (a failed token leaves the layers it reached)
     core_->open_token(seq, &run_);
     wait_began(seq);
+    Clock::time_point t_prev = t_served_;
     auto next_run = [&](uint32_t g) {
       uint32_t h = g + 1;
       while (h < G && !run_[h]) ++h;
@@ -822,6 +916,10 @@ class Service {
       const uint32_t nx = next_run(g);
       wait_word(&m_.flag[g], seq, "export flag", g, true, last_flag_[g]);
       last_flag_[g] = seq;
+      const Clock::time_point t_seen = Clock::now();
+      Row row;
+      row.seen_us = us_between(t_prev, t_seen);
+      if (diag_) before_ = core_->counts();
       const DgRecord& r = m_.rec[g];
       require(r.seq == seq, SS_E_BACKEND,
               "device-gated: sequence desync: the record of gated layer " + std::to_string(g) + " is for token " +
@@ -840,18 +938,38 @@ class Service {
       require((mask & ~dev_mask) == 0, SS_E_BACKEND,
               "device-gated: gated layer " + std::to_string(g) + " exported a hit for a unit absent from the table");
       core_->serve_misses(g, ids_.data(), n, mask, dev_mask);
+      const Clock::time_point t_demand = Clock::now();
+      row.demand_us = us_between(t_seen, t_demand);
       core_->note_uses(g, ids_.data(), n, mask);
       if (n_pred > 0 && run_[g + 1]) {
         wait_word(&m_.pflag[g], seq, "prediction flag", g, false, 0);
+        const Clock::time_point t_pw = Clock::now();
+        row.pred_wait_us = us_between(t_demand, t_pw);
         const DgPredRecord& pr = m_.prec[g];
         require(pr.n_pred == n_pred, SS_E_BACKEND,
                 "device-gated: gated layer " + std::to_string(g) + " predicted " + std::to_string(pr.n_pred) +
                     " ids, its export promised " + std::to_string(n_pred));
         pred_.assign(pr.pred, pr.pred + n_pred);
         core_->prefetch_next(g + 1, pred_.data(), n_pred);
+        row.prefetch_us = us_between(t_pw, Clock::now());
       }
       if (core_->queued_writebacks() && nx < G) core_->spend_wb_credit(g);
+      const Clock::time_point t_end = Clock::now();
+      row.serve_us = us_between(t_seen, t_end);
+      if (diag_) {
+        const DgCounts& a = core_->counts();
+        row.ids = uint32_t(a.lookups - before_.lookups);  // (one lookup per unique id)
+        row.misses = uint32_t(a.misses - before_.misses);
+        row.covered = uint32_t(a.covered - before_.covered);
+        row.fetched = uint32_t(a.fetched - before_.fetched);
+        row.prefetched = uint32_t(a.prefetched - before_.prefetched);
+        row.predicted_true = uint32_t(a.predicted_true - before_.predicted_true);
+        row.covered_waits = uint32_t(a.covered_waits - before_.covered_waits);
+        rows_[g] = row;
+      }
+      t_prev = t_end;
     }
+    t_served_ = Clock::now();  // the next token's first seen_us counts from here
   }
 
   DgCore* core_;
@@ -862,6 +980,10 @@ class Service {
   std::vector<uint8_t> run_, run_next_;
   std::vector<uint32_t> last_flag_;
   std::vector<uint32_t> ids_, pred_;
+  bool diag_ = false;
+  std::vector<Row> rows_;
+  DgCounts before_;
+  Clock::time_point t_served_{};
   std::atomic<uint32_t> host_seq_{0};
   std::atomic<uint64_t> term_{0};
   std::atomic<bool> stop_{false};
@@ -916,6 +1038,13 @@ class HipDgCtx final : public DgCtx {
     require(rows > 0, SS_E_INVALID, "ss_dg_end_rows: rows must be positive");
     require(in_token_, SS_E_INVALID, "ss_end: no gated token is open");
     in_token_ = false;
+    struct FailedRows {  // dg_diag: a failed token's host rows stay readable, its device measurements -1
+      HipDgCtx* c;
+      bool ok = false;
+      ~FailedRows() {
+        if (!ok) c->failed_timeline();
+      }
+    } rows_guard{this};
     const auto deadline = Clock::now() + std::chrono::milliseconds(uint64_t(o_.dg_wait_timeout_ms) + 5000);
     // 1. the completion edge: the end kernel ran after every reader of the token
     bool at = false;
@@ -979,7 +1108,78 @@ class HipDgCtx final : public DgCtx {
       poisoned_ = true;
       fail(SS_E_BACKEND, token_failure(dev, "no device check result names the unit"));
     }
+    if (o_.dg_diag) collect_timeline();
+    rows_guard.ok = true;
     fold(true);
+  }
+
+  // dg_diag, after a successful boundary: the device side of each exported layer's row - the transport's marks and the
+  // device stamps (export end, wait entry, ready seen; 100 ticks per microsecond).
+  void collect_timeline() {
+    const std::vector<HipTransport::LayerDma> dma = tr_->diag_collect();
+    std::vector<uint64_t> st(4 * x_.gated.size(), 0);
+    tr_->read_device(st.data(), dw_.stamps, 8 * st.size());
+    for (size_t g = 0; g < diag_rows_.size(); ++g) {
+      LayerDiag& d = diag_rows_[g];
+      d = LayerDiag{};
+      if (!run_[g]) continue;  // (its stamps are an older token's)
+      d.dma_ms = dma[g].dma_ms;
+      d.dma_first_ms = dma[g].dma_first_ms;
+      d.wb_left_ms = dma[g].wb_left_ms;
+      const uint64_t ex = st[4 * g], in = st[4 * g + 1], rd = st[4 * g + 2];
+      if (ex && in && rd && rd >= in && rd >= ex) {
+        d.gpu_wait_us = double(rd - in) / 100.0;
+        d.gpu_export_ready_us = double(rd - ex) / 100.0;
+      }
+    }
+    timeline_valid_ = true;
+  }
+  void failed_timeline() noexcept {
+    if (!o_.dg_diag) return;
+    std::fill(diag_rows_.begin(), diag_rows_.end(), LayerDiag{});
+    tr_->diag_forget();
+    timeline_valid_ = true;
+  }
+  void timeline(int g, ss_dg_layer_timeline* out) const override {
+    require(!in_token_, SS_E_INVALID, "ss_dg_timeline: between tokens only");
+    require(o_.dg_diag != 0, SS_E_INVALID, "ss_dg_timeline: open the context with dg_diag = 1");
+    check_g(g, "ss_dg_timeline");
+    require(timeline_valid_, SS_E_INVALID, "ss_dg_timeline: no token has completed");
+    const Service::Row& t = svc_->timeline()[size_t(g)];
+    const LayerDiag& d = diag_rows_[size_t(g)];
+    std::memset(out, 0, sizeof *out);
+    out->struct_size = uint32_t(sizeof *out);
+    out->layer = uint32_t(x_.gated[size_t(g)]);
+    out->seen_us = t.seen_us;
+    out->demand_us = t.demand_us;
+    out->pred_wait_us = t.pred_wait_us;
+    out->prefetch_us = t.prefetch_us;
+    out->serve_us = t.serve_us;
+    out->ids = t.ids;
+    out->misses = t.misses;
+    out->covered = t.covered;
+    out->fetched = t.fetched;
+    out->prefetched = t.prefetched;
+    out->predicted_true = t.predicted_true;
+    out->covered_waits = t.covered_waits;
+    out->dma_ms = d.dma_ms;
+    out->dma_first_ms = d.dma_first_ms;
+    out->wb_left_ms = d.wb_left_ms;
+    out->gpu_wait_us = d.gpu_wait_us;
+    out->gpu_export_ready_us = d.gpu_export_ready_us;
+  }
+  void boundary_timeline(ss_dg_boundary_timeline* out) const override {
+    require(!in_token_, SS_E_INVALID, "ss_dg_boundary_timeline: between tokens only");
+    require(o_.dg_diag != 0, SS_E_INVALID, "ss_dg_boundary_timeline: open the context with dg_diag = 1");
+    const DgBoundaryTimes& b = core_->boundary_times();
+    require(b.boundaries > 0, SS_E_INVALID, "ss_dg_boundary_timeline: no token has completed");
+    std::memset(out, 0, sizeof *out);
+    out->struct_size = uint32_t(sizeof *out);
+    out->writebacks = b.writebacks;
+    out->sync_us = b.sync_us;
+    out->select_us = b.select_us;
+    out->upload_us = b.upload_us;
+    out->issue_us = b.issue_us;
   }
 
   ss_dg_device_view device_view() const override {
@@ -1413,6 +1613,11 @@ class HipDgCtx final : public DgCtx {
   uint64_t verify_failures_ = 0;
   std::string score_prov_;  // the score profile's provenance (reported in the stats document)
   uint32_t adapt_ = 0;      // dg_disk_queue_adapt: 0 off, 1 adapting, 2 declined (adapt_why_)
+  struct LayerDiag {        // dg_diag: a layer's device measurements of the last token (-1: none)
+    double dma_ms = -1, dma_first_ms = -1, wb_left_ms = -1, gpu_wait_us = -1, gpu_export_ready_us = -1;
+  };
+  std::vector<LayerDiag> diag_rows_;
+  bool timeline_valid_ = false;
   std::string adapt_why_;
 
   static void add_stats(ss_layer_stats& a, const ss_layer_stats& b) {
@@ -1607,6 +1812,11 @@ void HipDgCtx::init() {
   base_l_.assign(G, DgLayerCounts{});
   fold(false);
   svc_ = std::make_unique<Service>(core_.get(), m_, x_.B, o_.dg_wait_timeout_ms, o_.device);
+  if (o_.dg_diag) {
+    tr_->enable_diag(G);
+    svc_->enable_timeline();
+    diag_rows_.assign(G, LayerDiag{});
+  }
   svc_->start();
 }
 

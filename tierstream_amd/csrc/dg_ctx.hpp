@@ -51,6 +51,8 @@ class DgCtx {
   virtual void profile_enable(int on) = 0;
   virtual tsa_test_profile profile_read(bool wait) = 0;
   virtual uint32_t stamps(uint64_t* out, uint32_t cap) const = 0;
+  virtual void timeline(int g, ss_dg_layer_timeline* out) const = 0;  // dg_diag (ss_dg_timeline_sized)
+  virtual void boundary_timeline(ss_dg_boundary_timeline* out) const = 0;
   virtual void corrupt_block(int g, int unit, uint64_t offset) = 0;
 };
 

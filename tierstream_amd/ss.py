@@ -136,6 +136,25 @@ class SsDgStats(C.Structure):
         return {n: int(getattr(self, n)) for n, _ in self._fields_ if not n.startswith("reserved")}
 
 
+class SsDgLayerTimeline(C.Structure):
+    _fields_ = [("struct_size", u32), ("layer", u32)] + [(n, C.c_double) for n in (
+        "seen_us", "demand_us", "pred_wait_us", "prefetch_us", "serve_us")] + [(n, u32) for n in (
+            "ids", "misses", "covered", "fetched", "prefetched", "reserved0")] + [("dma_ms", C.c_double)] + \
+        [("predicted_true", u32), ("covered_waits", u32)] + [(n, C.c_double) for n in (
+            "gpu_wait_us", "gpu_export_ready_us", "wb_left_ms", "dma_first_ms")]
+
+    def as_dict(self):
+        return {n: getattr(self, n) for n, _ in self._fields_ if not n.startswith("reserved") and n != "struct_size"}
+
+
+class SsDgBoundaryTimeline(C.Structure):
+    _fields_ = [("struct_size", u32), ("writebacks", u32)] + [(n, C.c_double) for n in (
+        "sync_us", "select_us", "upload_us", "issue_us")]
+
+    def as_dict(self):
+        return {n: getattr(self, n) for n, _ in self._fields_ if n != "struct_size"}
+
+
 _declared = False
 
 
@@ -182,6 +201,8 @@ def _declare() -> C.CDLL:
         "ss_stats_snapshot_json": (st, [vp, C.POINTER(vp), C.POINTER(C.c_size_t)]),
         "ss_stats_reset": (None, [vp]),
         "ss_stats_dg_sized": (st, [vp, C.POINTER(SsDgStats), u32]),
+        "ss_dg_timeline_sized": (st, [vp, C.c_int, C.POINTER(SsDgLayerTimeline), u32]),
+        "ss_dg_boundary_timeline_sized": (st, [vp, C.POINTER(SsDgBoundaryTimeline), u32]),
         "ss_dg_set_policy": (st, [vp, C.c_int]),
         "ss_dg_end_rows": (st, [vp, u32]),
         "ss_dg_keep": (st, [vp, C.c_int, C.POINTER(i32), C.c_int]),
@@ -393,6 +414,18 @@ class Ctx:
         s = SsDgStats()
         check(_declare().ss_stats_dg_sized(self.h, C.byref(s), C.sizeof(s)))
         return s.as_dict()
+
+    def dg_timeline(self, g: int) -> dict:
+        """dg_diag = 1, between tokens: gated layer g's row of the last completed token (ss_dg_timeline_sized)."""
+        t = SsDgLayerTimeline()
+        check(_declare().ss_dg_timeline_sized(self.h, g, C.byref(t), C.sizeof(t)))
+        return t.as_dict()
+
+    def dg_boundary_timeline(self) -> dict:
+        """dg_diag = 1, between tokens: the last boundary's phases (ss_dg_boundary_timeline_sized)."""
+        t = SsDgBoundaryTimeline()
+        check(_declare().ss_dg_boundary_timeline_sized(self.h, C.byref(t), C.sizeof(t)))
+        return t.as_dict()
 
     def dg_set_policy(self, policy: int):
         """Between tokens: 0 LRU, 1 SCORED, 2 SCORED_AUTO (ss_dg_set_policy)."""
