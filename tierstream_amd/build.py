@@ -3,6 +3,8 @@
 libtierstream_amd.so  the product: the ss_* / ts_* / tsa_* C ABI, host runtime and HIP kernels (csrc/).
 libtsa_engine.so      the synthetic engine the tests and the benchmark drive the library with (engine/): graph-captured
                       device-gated tokens, checksum kernels that read units through the tables. Not part of the product.
+libtierstream.a       the product's objects as a static archive, under the reference's archive name, and an identical
+libstrix_stream.a     copy under its older name (engines link either by name; they add -lamdhip64 -lstdc++ -lpthread).
 
 Every call recompiles every source (objects under _build/, compiled in parallel).
 """
@@ -29,6 +31,7 @@ CXX_FLAGS = ["-x", "c++"]
 LINK = ["-shared", "-fPIC", f"--offload-arch={ARCH}", "-Wl,-rpath,/opt/rocm/lib", "-L/opt/rocm/lib", "-lamdhip64",
         "-lpthread"]
 
+ARCHIVES = ["libtierstream.a", "libstrix_stream.a"]
 LIBS = {
     "libtierstream_amd.so": {"dir": PKG / "csrc", "extra_link": []},
     "libtsa_engine.so": {"dir": PKG / "engine", "extra_link": [f"-L{PKG}", "-ltierstream_amd",
@@ -71,6 +74,15 @@ def build(verbose: bool = False, jobs: int | None = None) -> list[Path]:
             raise RuntimeError(f"link of {name} failed:\n{p.stdout}{p.stderr}")
         os.replace(tmp, target)
         out.append(target)
+        if name == "libtierstream_amd.so":  # the static archives of the same objects
+            for a in ARCHIVES:
+                tmp = PKG / (a + ".tmp")
+                tmp.unlink(missing_ok=True)
+                p = subprocess.run(["ar", "rcs", str(tmp), *[str(o) for o in objs]], capture_output=True, text=True)
+                if p.returncode != 0:
+                    raise RuntimeError(f"ar of {a} failed:\n{p.stdout}{p.stderr}")
+                os.replace(tmp, PKG / a)
+                out.append(PKG / a)
     return out
 
 
