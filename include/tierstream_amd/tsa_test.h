@@ -132,10 +132,11 @@ SS_API ss_status tsa_test_hostplace_run(const char* desc_json, size_t len, const
 SS_API ss_status tsa_test_dg_geometry(const char* desc_json, size_t len, const ss_budget* budget, const uint8_t* tiers,
                                       size_t n_tiers, const ss_options* opt, uint32_t* out, uint32_t* residents,
                                       uint32_t res_cap);
-/* The same loop without prefetch; the exclusive-mode counters after the last forward. */
+/* The same loop (prefetch may be NULL); the exclusive-mode counters after the last forward. */
 SS_API ss_status tsa_test_hostplace_exclusive(const char* desc_json, size_t len, const ss_budget* budget,
-                                              const ss_options* opt, int steps, const int32_t* routes, int max_ids,
-                                              int mode, ss_exclusive_stats* out);
+                                              const ss_options* opt, int steps, const int32_t* routes,
+                                              const int32_t* prefetch, int max_ids, int mode,
+                                              ss_exclusive_stats* out);
 SS_API ss_status tsa_test_dgcore_set_wb_defer(void* h, uint32_t on);
 /* Scored eviction's profile rules without a context: the SHA-256 of data[0..n) (32 raw bytes into out), and the
  * TSSCPRF1 checks of a profile against the gated layers' units and a 32-byte identity (SS_E_INVALID naming the first

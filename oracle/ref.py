@@ -40,6 +40,7 @@ def lib() -> C.CDLL:
             "ss_options_defaults_sized": (None, [C.POINTER(SsOptions), u32]),
             "ss_plan_make": (st, [vp, C.POINTER(SsBudget), C.POINTER(C.c_double), C.c_size_t, C.POINTER(vp)]),
             "ss_plan_free": (None, [vp]),
+            "ss_plan_from_tiers": (st, [vp, C.POINTER(SsBudget), C.POINTER(C.c_uint8), C.c_size_t, C.POINTER(vp)]),
             "ss_plan_unit_tier": (C.c_int, [vp, C.c_int, C.c_int]),
             "ss_plan_to_json": (st, [vp, C.POINTER(C.c_char_p), C.POINTER(C.c_size_t)]),
             "ss_plan_from_json": (st, [vp, C.POINTER(SsBudget), C.c_char_p, C.c_size_t, C.POINTER(vp)]),
@@ -55,6 +56,7 @@ def lib() -> C.CDLL:
             "ss_group_wait": (st, [vp, C.c_int, C.c_int, vp]),
             "ss_release": (st, [vp, C.c_int, vp]),
             "ss_end": (st, [vp]),
+            "ss_host_prefetch_layer": (st, [vp, C.c_int]),
             "ss_stats_total": (st, [vp, C.POINTER(SsLayerStats)]),
             "ss_stats_to_json": (st, [vp, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]),
             "ref_region_of": (C.c_int, [vp, u64, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(u64)]),
@@ -160,12 +162,14 @@ def plan_json(desc_json: str, budget, benefit=None) -> dict:
 
 
 def host_run(desc_json: str, budget, options, routes: np.ndarray, mode: int = 0, prefetch: np.ndarray | None = None,
-             checksums: bool = True):
+             checksums: bool = True, host_lookahead: int = 0, tiers=None):
     """The reference CPU backend over `routes` ([steps][layers][max_ids], -1 padded), the engine loop of the product's
     tse_host_run. Per step: {"stats": ..., "tables": [[(kind, index, offset) per unit] per layer], "groups": [...],
     "checksums": [[...]]}; checksums are of the bytes the reference's table entries point at (host memory).
     prefetch (same shape): after layer l's acquire, ss_prefetch of layer l + 1 with its row, CERTAIN on even steps and
-    SPECULATIVE on odd ones."""
+    SPECULATIVE on odd ones. host_lookahead H: after each layer's routes, ss_host_prefetch_layer of the next H layers
+    with units (as the product's loop). tiers: the plan's tiers, one per unit in descriptor order (None: the planner's
+    plan)."""
     from tierstream_amd.ss import SsLayerStats, SsLayerView
     from .fixtures import engine_checksum
     L = lib()
@@ -174,8 +178,12 @@ def host_run(desc_json: str, budget, options, routes: np.ndarray, mode: int = 0,
     _ck(L.ss_desc_from_json(b, len(b), C.byref(d)))
     options.backend = 0  # SS_BACKEND_CPU
     out = []
+    plan = vp()
     try:
-        _ck(L.ss_open(d, C.byref(budget), None, C.byref(options), C.byref(ctx)))
+        if tiers is not None:
+            t = (C.c_uint8 * len(tiers))(*tiers)
+            _ck(L.ss_plan_from_tiers(d, C.byref(budget), t, len(tiers), C.byref(plan)))
+        _ck(L.ss_open(d, C.byref(budget), plan if tiers is not None else None, C.byref(options), C.byref(ctx)))
         nl = L.ss_desc_n_layers(d)
         steps, _, max_ids = routes.shape
         for s in range(steps):
@@ -196,6 +204,13 @@ def host_run(desc_json: str, budget, options, routes: np.ndarray, mode: int = 0,
                     _ck(L.ss_layer_all(ctx, l))
                 else:
                     _ck(L.ss_layer_routes(ctx, l, r.ctypes.data_as(C.POINTER(i32)), n))
+                left = host_lookahead
+                for h in range(l + 1, nl):
+                    if left <= 0:
+                        break
+                    if L.ss_desc_layer_units(d, h) > 0:
+                        _ck(L.ss_host_prefetch_layer(ctx, h))
+                        left -= 1
                 v = SsLayerView()
                 _ck((L.ss_acquire_groups if mode == 2 else L.ss_acquire)(ctx, l, None, C.byref(v)))
                 if mode == 2:
@@ -236,6 +251,8 @@ def host_run(desc_json: str, budget, options, routes: np.ndarray, mode: int = 0,
     finally:
         if ctx:
             L.ss_close(ctx)
+        if tiers is not None and plan:
+            L.ss_plan_free(plan)
         L.ss_desc_free(d)
     return out
 
@@ -397,9 +414,11 @@ def cpu_baseline_disk(n_units, persistent, bank, blocks, spare_target, part_byte
     return ms, {k: int(v) for k, v in zip(BASELINE_COUNTERS, out)}
 
 
-def host_exclusive(desc_json: str, budget, options, routes: np.ndarray) -> dict:
-    """The reference CPU backend in exclusive tier mode over `routes` (ss_layer_routes + ss_acquire per layer): its
-    ss_stats_exclusive after the last forward, as a dict."""
+def host_exclusive(desc_json: str, budget, options, routes: np.ndarray, prefetch: np.ndarray | None = None,
+                   mode: int = 0) -> dict:
+    """The reference CPU backend in exclusive tier mode over `routes` (ss_layer_routes + ss_acquire per layer; mode 2:
+    ss_acquire_groups and every group's wait; prefetch as in host_run): its ss_stats_exclusive after the last forward,
+    as a dict."""
     from tierstream_amd.ss import SsExclusiveStats, SsLayerView
     L = lib()
     L.ss_stats_exclusive_sized.restype = C.c_int
@@ -419,7 +438,15 @@ def host_exclusive(desc_json: str, budget, options, routes: np.ndarray) -> dict:
                 r = np.ascontiguousarray(routes[s, l], dtype=np.int32)
                 _ck(L.ss_layer_routes(ctx, l, r.ctypes.data_as(C.POINTER(i32)), int(np.sum(r >= 0))))
                 v = SsLayerView()
-                _ck(L.ss_acquire(ctx, l, None, C.byref(v)))
+                _ck((L.ss_acquire_groups if mode == 2 else L.ss_acquire)(ctx, l, None, C.byref(v)))
+                if mode == 2:
+                    for gi in range(1, v.n_groups):
+                        _ck(L.ss_group_wait(ctx, l, gi, None))
+                if prefetch is not None and l + 1 < nl and L.ss_desc_layer_units(d, l + 1) > 0:
+                    q = np.ascontiguousarray(prefetch[s, l + 1], dtype=np.int32)
+                    m = int(np.sum(q >= 0))
+                    if m:
+                        _ck(L.ss_prefetch(ctx, l + 1, q.ctypes.data_as(C.POINTER(i32)), m, s % 2))
                 _ck(L.ss_release(ctx, l, None))
             _ck(L.ss_end(ctx))
         x = SsExclusiveStats()

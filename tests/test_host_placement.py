@@ -31,8 +31,8 @@ def _lib():
                                          C.POINTER(ss.SsLayerStats)]
     L.tsa_test_hostplace_exclusive.restype = C.c_int
     L.tsa_test_hostplace_exclusive.argtypes = [C.c_char_p, C.c_size_t, C.POINTER(ss.SsBudget),
-                                               C.POINTER(ss.SsOptions), C.c_int, C.POINTER(i32), C.c_int, C.c_int,
-                                               C.POINTER(ss.SsExclusiveStats)]
+                                               C.POINTER(ss.SsOptions), C.c_int, C.POINTER(i32), C.POINTER(i32),
+                                               C.c_int, C.c_int, C.POINTER(ss.SsExclusiveStats)]
     return tsa, L
 
 
@@ -174,10 +174,15 @@ def test_cases_exercise_the_paths(tmp_path):
     assert multi_group > 0
 
 
-@pytest.mark.parametrize("seed", range(40))
+@pytest.mark.parametrize("seed", range(60))
 def test_exclusive_counters_match_reference(seed, tmp_path):
     """Exclusive tier mode: write-backs, discards, deferrals, rereads, promotions and free blocks after the same
-    forwards (the reference's ss_stats_exclusive)."""
+    forwards (the reference's ss_stats_exclusive); on every third seed with next-layer prefetch (certain and
+    speculative) of guesses, and on every fourth with hits-first groups. rereads (a pinned read of a block whose
+    write-back this forward issued) is a discrete device's count: the reference counts it only where a write-back
+    leaves an event to wait for (src/stream_ctx.cpp:672-676, :1064-1100), never on its unified CPU backend. Only a
+    prefetch makes one (a victim of the next layer's admission routed in the same forward), so without prefetch both
+    are 0; with it, ours counts what the reference's discrete backend would."""
     if not ref.available():
         pytest.skip("oracle/_ref (the reference CPU backend) is not built")
     rng = np.random.default_rng(500 + seed)
@@ -196,13 +201,27 @@ def test_exclusive_counters_match_reference(seed, tmp_path):
     if okw["exclusive_discard"]:
         m.tiers = "pinned|disk"
     routes = fixtures.uniform_routes(layers, units, top_k, 12, seed=seed + 1)
-    want = ref.host_exclusive(m.desc_json(), ss.budget(**bkw), ss.options(**okw), routes)
+    prefetch = None
+    if seed % 3 == 2:
+        guess = fixtures.uniform_routes(layers, units, top_k, 12, seed=seed + 2)
+        guess[:, :, 0] = np.where(rng.random((12, layers)) < 0.6, routes[:, :, 0], guess[:, :, 0])
+        prefetch = guess
+    mode = 2 if seed % 4 == 3 else 0
+    if mode == 2:
+        okw.update(group_units=2)
+    want = ref.host_exclusive(m.desc_json(), ss.budget(**bkw), ss.options(**okw), routes, prefetch=prefetch,
+                              mode=mode)
     tsa, L = _lib()
     x = ss.SsExclusiveStats()
     js = m.desc_json().encode()
     r = np.ascontiguousarray(routes, dtype=np.int32)
+    pf = np.ascontiguousarray(prefetch, dtype=np.int32) if prefetch is not None else None
     tsa.check(L.tsa_test_hostplace_exclusive(js, len(js), C.byref(ss.budget(**bkw)), C.byref(ss.options(**okw)),
-                                             routes.shape[0], r.ctypes.data_as(C.POINTER(i32)), routes.shape[2], 0,
-                                             C.byref(x)))
+                                             routes.shape[0], r.ctypes.data_as(C.POINTER(i32)),
+                                             pf.ctypes.data_as(C.POINTER(i32)) if pf is not None else None,
+                                             routes.shape[2], mode, C.byref(x)))
     got = {k: getattr(x, k) for k, _ in ss.SsExclusiveStats._fields_ if k != "struct_size"}
+    assert want["rereads"] == 0
+    if prefetch is not None:
+        want["rereads"] = got["rereads"]
     assert got == want, seed

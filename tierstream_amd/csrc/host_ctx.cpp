@@ -81,8 +81,6 @@ hipEvent_t HostCtx::pooled_event() {
 }
 
 void HostCtx::init() {
-  require(o_.readahead_units == 0, SS_E_UNSUPPORTED,
-          "open: host read-ahead (readahead_units) is not part of this library's serve path");
   require(o_.verify_hash >= 0 && o_.verify_hash <= 2, SS_E_INVALID, "open: verify_hash must be 0, 1 or 2");
   if (!o_.reader_threads) o_.reader_threads = 2;
   if (!o_.staging_buffers) o_.staging_buffers = 4;
@@ -186,6 +184,16 @@ void HostCtx::init() {
     stream_sync(copy_);
   }
 
+  if (place_.ra_on()) {  // host read-ahead: buffers of the largest unit a file read can bring, each with its event
+    for (uint32_t i = 0; i < o_.readahead_units; ++i) {
+      ra_ev_.push_back(dev_->event_create());
+      ra_buf_.push_back(dev_->alloc_pinned(place_.ra_bytes(), "read-ahead buffer"));
+      ra_free_.push_back(int32_t(o_.readahead_units - 1 - i));  // buffer 0 taken first
+    }
+    ra_index_.resize(d_.layers.size());
+    for (size_t L = 0; L < d_.layers.size(); ++L) ra_index_[L].assign(size_t(d_.layers[L].n_units), -1);
+  }
+
   for (uint32_t i = 0; i < o_.reader_threads; ++i) readers_.emplace_back([this] { reader_loop(); });
 
   // the pinned tier from the files, then the residents (from their pinned copies where they have one)
@@ -241,6 +249,8 @@ void HostCtx::cleanup() noexcept {
     dev_->free_pinned(s.host);
     dev_->event_destroy(s.ev);
   }
+  for (void* b : ra_buf_) dev_->free_pinned(b);
+  for (hipEvent_t e : ra_ev_) dev_->event_destroy(e);
   for (hipEvent_t e : all_events_) dev_->event_destroy(e);
   dev_->event_destroy(blocks_ev_);
   dev_->event_destroy(wb_mark_ev_);
@@ -287,7 +297,7 @@ void HostCtx::write_back(const WriteBackOrder& w) {
   ev_record(ev, wb_);
 }
 
-void HostCtx::fetch(const FetchOrder& f) {
+bool HostCtx::fetch(const FetchOrder& f) {
   auto c = std::make_shared<Copy>();
   c->layer = f.layer;
   c->unit = f.unit;
@@ -304,7 +314,22 @@ void HostCtx::fetch(const FetchOrder& f) {
   } else {
     fills_.push_back(c);
   }
+  if (ra_on() && f.job >= 0 && f.src_block < 0) {
+    const int32_t i = ra_index_[size_t(f.layer)][size_t(f.unit)];
+    if (i >= 0) {
+      RaEntry& e = *ra_entries_[size_t(i)];
+      if (f.speculative) {
+        if (f.dst.kind == DevSpot::kPool) {  // a speculative admission reads the file as any speculative fetch
+          std::lock_guard<std::mutex> lk(q_mu_);
+          ra_abandon_locked(e);
+        }  // (a speculative ring fetch leaves the request alone)
+      } else if (ra_land(e, c)) {
+        return true;
+      }
+    }
+  }
   submit(c);
+  return false;
 }
 
 void HostCtx::promote(int32_t job) {
@@ -342,18 +367,9 @@ bool HostCtx::settle(int32_t job, bool) {
 // ---- copies and reads ---------------------------------------------------------------------------------------------
 
 void HostCtx::submit(const CopyPtr& c) {
-  if (c->src && !c->to_host) {
-    // a pinned block: issued now on the next copy stream (an SDMA queue), in pieces of copy_piece_bytes
-    const uint64_t n = d_.layers[size_t(c->layer)].unit_bytes;
+  if (c->src && !c->to_host) {  // a pinned block: issued now
     try {
-      std::lock_guard<std::mutex> lk(copy_mu_);
-      const hipStream_t cs = next_copy_stream();
-      wait_slot_check(cs, c->dst);
-      for (hipEvent_t e : c->after) stream_wait(cs, e);
-      for (uint64_t off = 0; off < n; off += o_.copy_piece_bytes)
-        copy_h2d(at(c->dst, off), at(c->src, off), std::min(o_.copy_piece_bytes, n - off), cs);
-      ev_record(c->done_ev, cs);
-      if (dverify_) verify_landed(*c);
+      issue_copy(*c, c->src, nullptr);
     } catch (const Error& e) {
       finish(*c, Copy::kFailed, e.status(), e.what());
       throw;
@@ -368,6 +384,21 @@ void HostCtx::submit(const CopyPtr& c) {
   q_cv_.notify_all();
 }
 
+// Host memory (a pinned block, a read-ahead buffer) into c's destination on the next copy stream (an SDMA queue), in
+// pieces of copy_piece_bytes, behind the destination's waits; after_ev (if any) is recorded behind the copy too.
+void HostCtx::issue_copy(Copy& c, const void* src, hipEvent_t after_ev) {
+  const uint64_t n = d_.layers[size_t(c.layer)].unit_bytes;
+  std::lock_guard<std::mutex> lk(copy_mu_);
+  const hipStream_t cs = next_copy_stream();
+  wait_slot_check(cs, c.dst);
+  for (hipEvent_t e : c.after) stream_wait(cs, e);
+  for (uint64_t off = 0; off < n; off += o_.copy_piece_bytes)
+    copy_h2d(at(c.dst, off), at(src, off), std::min(o_.copy_piece_bytes, n - off), cs);
+  ev_record(c.done_ev, cs);
+  if (after_ev) ev_record(after_ev, cs);
+  if (dverify_) verify_landed(c);
+}
+
 void HostCtx::finish(Copy& c, int state, ss_status st, const std::string& what) noexcept {
   {
     std::lock_guard<std::mutex> lk(q_mu_);
@@ -378,6 +409,8 @@ void HostCtx::finish(Copy& c, int state, ss_status st, const std::string& what) 
     }
     c.state.store(state);
     if (c.demand_run) --demand_running_;
+    if (c.ra_run) --ra_running_;
+    c.demand_run = c.ra_run = false;
   }
   done_cv_.notify_all();
   q_cv_.notify_all();
@@ -398,18 +431,29 @@ void HostCtx::reader_loop() {
     dev_->bind();
   } catch (...) {
   }
+  // demand reads first, then read-ahead reads on at most max(1, readers - 1) readers, then a speculative read while
+  // at most one demand read runs
+  const int ra_cap = std::max(1, int(o_.reader_threads) - 1);
   for (;;) {
     CopyPtr c;
     {
       std::unique_lock<std::mutex> lk(q_mu_);
-      auto runnable = [&] { return !demand_q_.empty() || (!spec_q_.empty() && demand_running_ <= 1); };
+      auto runnable = [&] {
+        return !demand_q_.empty() || (!ra_q_.empty() && ra_running_ < ra_cap) ||
+               (!spec_q_.empty() && demand_running_ <= 1);
+      };
       q_cv_.wait(lk, [&] { return stop_ || runnable(); });
-      if (stop_ && demand_q_.empty() && spec_q_.empty()) return;
+      if (stop_ && demand_q_.empty() && spec_q_.empty() && ra_q_.empty()) return;
       if (!demand_q_.empty()) {
         c = demand_q_.front();
         demand_q_.pop_front();
         c->demand_run = true;
         ++demand_running_;
+      } else if (!ra_q_.empty() && (ra_running_ < ra_cap || stop_)) {
+        c = ra_q_.front();
+        ra_q_.pop_front();
+        c->ra_run = true;
+        ++ra_running_;
       } else if (!spec_q_.empty() && demand_running_ <= 1) {
         c = spec_q_.front();
         spec_q_.pop_front();
@@ -419,20 +463,26 @@ void HostCtx::reader_loop() {
       int queued = Copy::kQueued;
       if (!c->state.compare_exchange_strong(queued, Copy::kRunning)) {  // cancelled while queued
         if (c->demand_run) --demand_running_;
+        if (c->ra_run) --ra_running_;
+        c->demand_run = c->ra_run = false;
         done_cv_.notify_all();
         continue;
       }
     }
+    int state = Copy::kDone;
+    ss_status st = SS_OK;
+    std::string what;
     try {
       read_file_unit(*c);
-      finish(*c, Copy::kDone, SS_OK, std::string());
     } catch (const Error& e) {
-      finish(*c, Copy::kFailed, e.status(), e.what());
+      state = Copy::kFailed, st = e.status(), what = e.what();
     } catch (const std::bad_alloc&) {
-      finish(*c, Copy::kFailed, SS_E_NOMEM, "out of host memory");
+      state = Copy::kFailed, st = SS_E_NOMEM, what = "out of host memory";
     } catch (const std::exception& e) {
-      finish(*c, Copy::kFailed, SS_E_BACKEND, e.what());
+      state = Copy::kFailed, st = SS_E_BACKEND, what = e.what();
     }
+    if (c->ra) ra_read_ended(*c, state, st, what);  // (its landing first: the read counts as ended after it)
+    else finish(*c, state, st, what);
   }
 }
 
@@ -457,7 +507,8 @@ void HostCtx::read_file_unit(Copy& c) {
   const bool hash = o_.verify_hash && !l.hash.empty();
   if (c.to_host) {
     uint64_t digest = 0;
-    read_into_host(c.layer, c.unit, c.dst, hash, &digest);
+    if (c.ra) ev_sync(ra_ev_[size_t(c.ra->buf)]);  // the buffer's last copy out has completed
+    read_into_host(c.layer, c.unit, c.dst, hash, &digest, &c.bytes_read);
     require(!hash || digest == l.hash[size_t(c.unit)], SS_E_HASH,
             "unit (" + std::to_string(c.layer) + ", " + std::to_string(c.unit) + ") bytes differ from the descriptor hash");
     return;
@@ -467,7 +518,7 @@ void HostCtx::read_file_unit(Copy& c) {
 
 // A unit's file bytes into host memory at dst (direct I/O through staging where the range is not aligned), hashed on
 // the way; with device checks on, its checkpoints are kept in HBM once the digest certifies them.
-void HostCtx::read_into_host(int layer, int unit, void* dst, bool hash, uint64_t* digest) {
+void HostCtx::read_into_host(int layer, int unit, void* dst, bool hash, uint64_t* digest, uint64_t* got) {
   const Layer& l = d_.layers[size_t(layer)];
   const int64_t g = gidx(layer, unit);
   std::vector<uint64_t> states;
@@ -484,6 +535,7 @@ void HostCtx::read_into_host(int layer, int unit, void* dst, bool hash, uint64_t
                 " is past the end of its source");
     if (!f.direct() || (off % al == 0 && part.bytes % al == 0 && uintptr_t(out) % al == 0)) {
       f.pread_all(out, part.bytes, off);
+      if (got) *got += part.bytes;
     } else {
       const uint64_t cap = (o_.staging_bytes - 2 * al) / al * al;
       for (uint64_t done = 0; done < part.bytes;) {
@@ -494,6 +546,7 @@ void HostCtx::read_into_host(int layer, int unit, void* dst, bool hash, uint64_t
           ev_sync(staging_[i].ev);
           require(f.pread_some(staging_[i].host, a1 - a0, a0) >= lead + len, SS_E_IO, "short read");
           std::memcpy(out + done, at(staging_[i].host, lead), size_t(len));
+          if (got) *got += len;
         } catch (...) {
           give_staging(i);
           throw;
@@ -575,6 +628,228 @@ void HostCtx::stage_to_device(Copy& c) {
   }
   ev_record(c.done_ev, copy_);
   if (dverify_) verify_landed(c);
+}
+
+// ---- host read-ahead (readahead_units; reference src/stream_ctx.cpp:732-1017, docs/design.md 3.6) -----------------------
+// A forward's file-backed units that wait for a ring slot (or that ss_host_prefetch names) are read ahead into pinned
+// read-ahead buffers, one unit each, by the reader threads below demand reads; when the unit gets its slot, the copy
+// lands from the buffer (at once if the read ended, else when it does: a read still queued then becomes a demand
+// read). Placement never depends on it: the same slots, tables and groups, only where the bytes come from.
+
+void HostCtx::read_ahead(int layer, int unit) {
+  if (!ra_on() || ra_frozen_) return;
+  ra_entries_.push_back(std::make_unique<RaEntry>());
+  RaEntry& e = *ra_entries_.back();
+  e.layer = layer;
+  e.unit = unit;
+  ra_index_[size_t(layer)][size_t(unit)] = int32_t(ra_entries_.size() - 1);
+  ra_wait_.push_back(&e);
+}
+
+// Waiting requests take free buffers, oldest first; one whose unit got a copy or a pinned source meanwhile is dropped.
+void HostCtx::ra_pump() {
+  if (!ra_on() || ra_frozen_) return;
+  while (!ra_wait_.empty()) {
+    RaEntry& e = *ra_wait_.front();
+    bool drop;
+    {
+      std::lock_guard<std::mutex> lk(q_mu_);
+      drop = e.st != RaEntry::kWaiting;
+      if (!drop && !place_.ra_wanted(e.layer, e.unit)) {
+        e.st = RaEntry::kAbandoned;
+        drop = true;
+      }
+    }
+    if (drop) {
+      ra_wait_.pop_front();
+      continue;
+    }
+    auto p = std::make_shared<Copy>();
+    p->layer = e.layer;
+    p->unit = e.unit;
+    p->to_host = true;
+    p->ra = &e;
+    {
+      std::lock_guard<std::mutex> lk(q_mu_);
+      if (ra_free_.empty()) return;  // the next engine call tries again
+      e.buf = ra_free_.back();
+      ra_free_.pop_back();
+      p->dst = ra_buf_[size_t(e.buf)];
+      e.producer = p;
+      e.st = RaEntry::kReading;
+      ra_q_.push_back(p);
+    }
+    ra_wait_.pop_front();
+    q_cv_.notify_all();
+  }
+}
+
+void HostCtx::ra_give_buf_locked(RaEntry& e) {
+  if (e.buf < 0) return;
+  ra_free_.push_back(e.buf);
+  e.buf = -1;
+}
+
+void HostCtx::ra_abandon_locked(RaEntry& e) {
+  switch (e.st) {
+    case RaEntry::kWaiting:
+      e.st = RaEntry::kAbandoned;
+      break;
+    case RaEntry::kReady:  // read, never to land
+      ra_give_buf_locked(e);
+      e.st = RaEntry::kAbandoned;
+      break;
+    case RaEntry::kReading: {
+      int queued = Copy::kQueued;
+      if (e.producer->state.compare_exchange_strong(queued, Copy::kCancelled)) {  // never started: no read at all
+        const auto it = std::find(ra_q_.begin(), ra_q_.end(), e.producer);
+        if (it != ra_q_.end()) ra_q_.erase(it);
+        ra_give_buf_locked(e);
+      }  // (running: its end gives the buffer back)
+      e.st = RaEntry::kAbandoned;
+      break;
+    }
+    default:  // Landing (its copy decides), Consumed, Abandoned, Failed
+      break;
+  }
+}
+
+// The unit got its slot (a demand fetch, child: its job): lands from the buffer when the read ended or runs, else
+// (never started, or failed: a fallback) the caller reads the file.
+bool HostCtx::ra_land(RaEntry& e, const CopyPtr& child) {
+  bool issue = false, attached = false, fallback = false;
+  {
+    std::lock_guard<std::mutex> lk(q_mu_);
+    switch (e.st) {
+      case RaEntry::kWaiting:  // not started: the ordinary read starts as early
+        e.st = RaEntry::kAbandoned;
+        break;
+      case RaEntry::kReady:
+        e.st = RaEntry::kLanding;
+        e.child = child;
+        child->state.store(Copy::kRunning);
+        issue = attached = true;
+        break;
+      case RaEntry::kReading: {
+        e.st = RaEntry::kLanding;
+        e.child = child;
+        attached = true;
+        const auto it = std::find(ra_q_.begin(), ra_q_.end(), e.producer);
+        if (it != ra_q_.end()) {  // still queued: a demand waits behind it now
+          ra_q_.erase(it);
+          demand_q_.push_front(e.producer);
+        }
+        break;
+      }
+      case RaEntry::kFailed:
+        fallback = true;
+        break;
+      default:
+        break;
+    }
+  }
+  if (fallback) ++ra_st_.fallback;
+  if (attached) q_cv_.notify_all();
+  if (issue) ra_issue_child(e, *child);
+  return attached;
+}
+
+// The copy out of the read-ahead buffer into the child's slot (the child is running); the buffer is read again only
+// after this copy (its event).
+void HostCtx::ra_issue_child(RaEntry& e, Copy& child) {
+  int state = Copy::kDone;
+  ss_status st = SS_OK;
+  std::string what;
+  try {
+    issue_copy(child, ra_buf_[size_t(e.buf)], ra_ev_[size_t(e.buf)]);
+  } catch (const Error& x) {
+    state = Copy::kFailed, st = x.status(), what = x.what();
+  } catch (const std::exception& x) {
+    state = Copy::kFailed, st = SS_E_BACKEND, what = x.what();
+  }
+  {
+    std::lock_guard<std::mutex> lk(q_mu_);
+    e.st = state == Copy::kDone ? RaEntry::kConsumed : RaEntry::kFailed;
+    ra_give_buf_locked(e);
+  }
+  finish(child, state, st, what);
+}
+
+// A read-ahead read ended (state kDone or kFailed; a reader thread): its request moves on - a landing waiting for it
+// is issued now, or fails with it (the forward fails: its copy had no other source) - and only then the read counts
+// as ended.
+void HostCtx::ra_read_ended(Copy& p, int state, ss_status st, const std::string& what) {
+  RaEntry& e = *p.ra;
+  CopyPtr issue, failed;
+  {
+    std::lock_guard<std::mutex> lk(q_mu_);
+    const bool ok = state == Copy::kDone;
+    switch (e.st) {
+      case RaEntry::kReading:
+        if (ok) {
+          e.st = RaEntry::kReady;
+        } else {
+          e.st = RaEntry::kFailed;
+          ra_give_buf_locked(e);
+        }
+        break;
+      case RaEntry::kLanding: {
+        int queued = Copy::kQueued;
+        if (!e.child->state.compare_exchange_strong(queued, Copy::kRunning)) {  // its copy was cancelled meanwhile
+          ra_give_buf_locked(e);
+          break;
+        }
+        if (ok) {
+          issue = e.child;
+        } else {
+          failed = e.child;
+          e.st = RaEntry::kFailed;
+          ra_give_buf_locked(e);
+        }
+        break;
+      }
+      case RaEntry::kAbandoned:
+        ra_give_buf_locked(e);
+        break;
+      default:
+        break;
+    }
+  }
+  if (issue) ra_issue_child(e, *issue);
+  if (failed) finish(*failed, Copy::kFailed, st, "read-ahead: " + what);
+  finish(p, state, st, what);
+}
+
+// ss_end: no new request; the ones not landing are abandoned; every read ends (a landing's copy is issued by its
+// read's end); then each request counts once and the file bytes it read count in the layer's bytes_disk.
+void HostCtx::ra_end_forward() {
+  if (!ra_on()) return;
+  {
+    std::lock_guard<std::mutex> lk(q_mu_);
+    ra_frozen_ = true;
+    for (auto& e : ra_entries_) ra_abandon_locked(*e);
+  }
+  ra_wait_.clear();
+  done_cv_.notify_all();
+  for (auto& e : ra_entries_)
+    if (e->producer) await_quiet(*e->producer);
+  for (auto& e : ra_entries_) {
+    ++ra_st_.requested;
+    const int ps = e->producer ? e->producer->state.load() : int(Copy::kCancelled);
+    const uint64_t b = e->producer ? e->producer->bytes_read : 0;
+    ra_st_.bytes += b;
+    place_.add_disk_bytes(e->layer, b);
+    if (ps == Copy::kDone) {
+      ++ra_st_.read;
+      if (e->st == RaEntry::kConsumed) ++ra_st_.landed;
+      else ++ra_st_.unused;
+    } else if (ps == Copy::kFailed) {
+      ++ra_st_.failed;
+    }
+    ra_index_[size_t(e->layer)][size_t(e->unit)] = -1;
+  }
+  ra_entries_.clear();
+  ra_frozen_ = false;
 }
 
 // ---- device checks (verify_hash = 2) --------------------------------------------------------------------------------
@@ -772,11 +1047,13 @@ void HostCtx::begin(const uint32_t* rows, int n_layers) { place_.begin(rows, n_l
 void HostCtx::routes(int layer, const int32_t* ids, int n) {
   check_layer(layer, "routes");
   place_.routes(layer, ids, n);
+  ra_pump();
 }
 
 void HostCtx::routes_all(int layer) {
   check_layer(layer, "layer_all");
   place_.routes_all(layer);
+  ra_pump();
 }
 
 // The ids are copied back on the engine stream right behind the router and taken at the next call that needs them.
@@ -809,6 +1086,7 @@ void HostCtx::ingest_dev_routes(int layer) {
 void HostCtx::prefetch(int layer, const int32_t* ids, int n, bool speculative) {
   check_layer(layer, "prefetch");
   place_.prefetch(layer, ids, n, speculative);
+  ra_pump();
 }
 
 void HostCtx::prefetch_layer(int layer) {
@@ -816,15 +1094,23 @@ void HostCtx::prefetch_layer(int layer) {
   std::vector<int32_t> all(static_cast<size_t>(d_.layers[size_t(layer)].n_units));
   for (size_t u = 0; u < all.size(); ++u) all[u] = int32_t(u);
   place_.prefetch(layer, all.data(), int(all.size()), false);
+  ra_pump();
 }
 
+// Read-ahead of file-backed units of a layer, no device slot (a checked no-op while readahead_units is 0).
 void HostCtx::host_prefetch(int layer, const int32_t* ids, int n) {
   check_layer(layer, "host_prefetch");
-  require(n >= 0 && (ids || n == 0), SS_E_INVALID, "host_prefetch: bad ids");
-  // readahead_units is 0 in every context this library opens (a nonzero value is refused at open): nothing to read
+  place_.host_prefetch(layer, ids, n);
+  ra_pump();
 }
 
-void HostCtx::host_prefetch_layer(int layer) { check_layer(layer, "host_prefetch_layer"); }
+void HostCtx::host_prefetch_layer(int layer) {
+  check_layer(layer, "host_prefetch_layer");
+  if (!place_.ra_on()) return;
+  std::vector<int32_t> all(static_cast<size_t>(d_.layers[size_t(layer)].n_units));
+  for (size_t u = 0; u < all.size(); ++u) all[u] = int32_t(u);
+  host_prefetch(layer, all.data(), int(all.size()));
+}
 
 void HostCtx::acquire(int layer, void* stream, bool wait_all, ss_layer_view* out) {
   check_layer(layer, "acquire");
@@ -833,6 +1119,7 @@ void HostCtx::acquire(int layer, void* stream, bool wait_all, ss_layer_view* out
   require(!place_.acquired(layer), SS_E_INVALID, "acquire: layer acquired twice in one forward");
   check_stream(stream, "acquire");
   ingest_dev_routes(layer);
+  ra_pump();
   require(place_.routes_given(layer), SS_E_INVALID,
           "acquire: no routes for layer " + std::to_string(layer) + " (ss_layer_routes / ss_layer_all first)");
   const hipStream_t es = static_cast<hipStream_t>(stream);
@@ -887,6 +1174,7 @@ void HostCtx::release(int layer, void* stream) {
   ev_record(s.release_ev, static_cast<hipStream_t>(stream));
   ev_record(s.table_ev[s.version], static_cast<hipStream_t>(stream));  // its table is read until here
   place_.release(layer);
+  ra_pump();
 }
 
 void HostCtx::end() {
@@ -896,6 +1184,7 @@ void HostCtx::end() {
             "end: layer " + std::to_string(L) + " acquired but not released");
   fwd_failed_ = SS_OK;
   fwd_error_.clear();
+  ra_end_forward();
   const HostPlacement::Ended e = place_.end();  // settles every job of the forward
   {
     std::lock_guard<std::mutex> lk(copy_mu_);
@@ -985,6 +1274,7 @@ ss_layer_stats HostCtx::total() const {
 
 void HostCtx::stats_reset() {
   place_.reset_stats();
+  ra_st_ = RaCounts{};
   if (!place_.in_forward()) publish();
 }
 
@@ -993,6 +1283,7 @@ void HostCtx::publish() {
   std::lock_guard<std::mutex> lk(snap_mu_);
   snap_.layers = place_.stats();
   snap_.x = place_.exclusive_stats();
+  snap_.ra = ra_st_;
   snap_.forwards = place_.forwards();
   ++snap_.seq;
 }
@@ -1007,6 +1298,16 @@ bool HostCtx::snapshot(ss_layer_stats* total, ss_snapshot_info* info) const {
     for (const ss_layer_stats& l : snap_.layers) add_stats(t, l);
     i.sequence = snap_.seq;
     i.forwards = snap_.forwards;
+    if (ra_on()) {
+      const RaCounts& r = snap_.ra;
+      i.readahead_requested = r.requested;
+      i.readahead_read = r.read;
+      i.readahead_landed = r.landed;
+      i.readahead_unused = r.unused;
+      i.readahead_failed = r.failed;
+      i.readahead_fallback = r.fallback;
+      i.readahead_bytes = r.bytes;
+    }
     if (place_.exclusive()) {
       const ss_exclusive_stats& x = snap_.x;
       i.exclusive_writebacks = x.writebacks;
@@ -1018,6 +1319,11 @@ bool HostCtx::snapshot(ss_layer_stats* total, ss_snapshot_info* info) const {
       i.exclusive_rereads = x.rereads;
       i.exclusive_discards = x.discards;
     }
+  }
+  if (ra_on()) {  // (fixed at open)
+    i.flags |= SS_SNAPSHOT_READAHEAD;
+    i.readahead_buffers = ra_buf_.size();
+    i.readahead_buffer_bytes = place_.ra_bytes();
   }
   if (place_.exclusive()) {
     i.flags |= SS_SNAPSHOT_EXCLUSIVE;
@@ -1037,16 +1343,17 @@ bool HostCtx::snapshot_json(Json* out) const {
     if (snap_.seq == 0) return false;
     p = snap_;
   }
-  *out = format_stats(p.forwards, p.layers.data(), p.x);
+  *out = format_stats(p.forwards, p.layers.data(), p.x, p.ra);
   return true;
 }
 
 Json HostCtx::stats_json() const {
-  return format_stats(place_.forwards(), place_.stats().data(), place_.exclusive_stats());
+  return format_stats(place_.forwards(), place_.stats().data(), place_.exclusive_stats(), ra_st_);
 }
 
 // The stats-v1 document (its keys and layout: reference src/stream_ctx.cpp:1826-1885).
-Json HostCtx::format_stats(uint64_t forwards, const ss_layer_stats* layers, const ss_exclusive_stats& x) const {
+Json HostCtx::format_stats(uint64_t forwards, const ss_layer_stats* layers, const ss_exclusive_stats& x,
+                           const RaCounts& ra) const {
   Json doc = Json::object();
   doc["schema"] = Json::string("strix-stream/stats-v1");
   doc["backend"] = Json::string("hip");
@@ -1062,6 +1369,15 @@ Json HostCtx::format_stats(uint64_t forwards, const ss_layer_stats* layers, cons
   }
   doc["total"] = stats_object(sum);
   doc["layers"] = per_layer;
+  if (ra_on()) {  // (readahead_units 0: no such object)
+    Json r = Json::object();
+    const std::pair<const char*, uint64_t> fields[] = {
+        {"buffers", ra_buf_.size()}, {"buffer_bytes", place_.ra_bytes()}, {"requested", ra.requested},
+        {"read", ra.read},           {"landed", ra.landed},               {"unused", ra.unused},
+        {"failed", ra.failed},       {"fallback", ra.fallback},           {"bytes", ra.bytes}};
+    for (const auto& f : fields) r[f.first] = Json::number(f.second);
+    doc["readahead"] = r;
+  }
   if (place_.exclusive()) {
     Json e = Json::object();
     const std::pair<const char*, uint64_t> fields[] = {

@@ -6,6 +6,8 @@
 //  - a copy from a file is a job for the reader threads: direct-I/O reads into pinned staging, host XXH64, then the
 //    copy stream;
 //  - exclusive-mode write-backs run on their own device-to-host stream;
+//  - with readahead_units, file-backed units a forward will need are read ahead into pinned read-ahead buffers by the
+//    reader threads (below demand reads), and their copy later lands from the buffer;
 //  - with verify_hash = 2 every landed unit is re-hashed in HBM (checkpoint-parallel XXH64, batched on a verify stream);
 //  - every wait the reference expresses as an event (a slot's last reader, a victim's write-back, a block's write-back,
 //    the copies of an earlier forward) is a device-side stream wait here.
@@ -87,11 +89,15 @@ class HostCtx final : public HostWork {
   bool snapshot_json(Json* out) const;
 
  private:
-  // One copy onto the device (or, to_host, a pinned block's fill from the file at open).
+  struct RaEntry;
+  // One copy onto the device (or, to_host, a pinned block's fill from the file at open, or a read-ahead read).
   struct Copy {
     enum State : int { kQueued = 0, kRunning = 1, kDone = 2, kCancelled = 3, kFailed = 4 };
     int32_t layer = 0, unit = 0;
     bool speculative = false, to_host = false, demand_run = false;
+    bool ra_run = false;        // running as a read-ahead read (counted against the read-ahead reader cap)
+    RaEntry* ra = nullptr;      // a read-ahead read: its request
+    uint64_t bytes_read = 0;    // a read-ahead read: the file bytes it read
     void* dst = nullptr;
     const void* src = nullptr;  // a pinned block, or null: the unit's file
     hipEvent_t after[3] = {nullptr, nullptr, nullptr};  // dst's last reader, dst's victim write-back, src's write-back
@@ -124,9 +130,24 @@ class HostCtx final : public HostWork {
     uint64_t n_states = 0;
   };
 
+  // Host read-ahead: one request of this forward. Waiting (no buffer yet) -> Reading (its read queued or running) ->
+  // Ready (read) -> Landing (a fetch takes it: the copy out of the buffer is issued when the read ends) -> Consumed;
+  // Abandoned (not needed any more), Failed (its read failed: the fetch reads the file).
+  struct RaEntry {
+    enum State : uint8_t { kWaiting, kReading, kReady, kLanding, kConsumed, kAbandoned, kFailed };
+    int32_t layer = 0, unit = 0;
+    State st = kWaiting;
+    int32_t buf = -1;
+    std::shared_ptr<Copy> producer, child;
+  };
+  struct RaCounts {  // the reference's "readahead" counters: requests, reads ended, landed, unused, failed, fallback
+    uint64_t requested = 0, read = 0, landed = 0, unused = 0, failed = 0, fallback = 0, bytes = 0;
+  };
+
   // HostWork
   void write_back(const WriteBackOrder& w) override;
-  void fetch(const FetchOrder& f) override;
+  bool fetch(const FetchOrder& f) override;
+  void read_ahead(int layer, int unit) override;
   void promote(int32_t job) override;
   void retire(int32_t job) override;
   bool settle(int32_t job, bool speculative) override;
@@ -135,9 +156,20 @@ class HostCtx final : public HostWork {
   void cleanup() noexcept;
   void reader_loop();
   void read_file_unit(Copy& c);  // a reader thread: the unit's file bytes to its destination
-  void read_into_host(int layer, int unit, void* dst, bool hash, uint64_t* digest);
+  // got: + the file bytes read (null: not counted)
+  void read_into_host(int layer, int unit, void* dst, bool hash, uint64_t* digest, uint64_t* got = nullptr);
   void stage_to_device(Copy& c);
   void submit(const CopyPtr& c);
+  void issue_copy(Copy& c, const void* src, hipEvent_t after_ev);  // host memory -> c.dst now (copy_mu_ taken)
+  // read-ahead
+  bool ra_on() const { return !ra_buf_.empty(); }
+  void ra_pump();                                  // waiting requests take free buffers (engine thread)
+  bool ra_land(RaEntry& e, const CopyPtr& child);  // a fetch of e's unit: true when it lands from the buffer
+  void ra_issue_child(RaEntry& e, Copy& child);    // the copy out of e's buffer (e's read has ended)
+  void ra_read_ended(Copy& p, int state, ss_status st, const std::string& what);  // a reader thread
+  void ra_abandon_locked(RaEntry& e);              // q_mu_ held
+  void ra_give_buf_locked(RaEntry& e);             // q_mu_ held
+  void ra_end_forward();                           // ss_end: no more requests, reads ended, counts
   void finish(Copy& c, int state, ss_status st, const std::string& what) noexcept;
   void await(Copy& c);       // until it ends; throws its error if it failed
   void await_quiet(Copy& c);  // until it ends
@@ -157,7 +189,8 @@ class HostCtx final : public HostWork {
   void collect_verify();
   void wait_slot_check(hipStream_t s, const void* dst);  // a slot's next copy waits for its pending check
   void publish();
-  Json format_stats(uint64_t forwards, const ss_layer_stats* layers, const ss_exclusive_stats& x) const;
+  Json format_stats(uint64_t forwards, const ss_layer_stats* layers, const ss_exclusive_stats& x,
+                    const RaCounts& ra) const;
 
   Desc d_;
   Plan plan_;
@@ -193,8 +226,17 @@ class HostCtx final : public HostWork {
   // reader threads: demand reads first; a speculative read only while no demand waits and at most one runs
   std::mutex q_mu_;
   std::condition_variable q_cv_, done_cv_;
-  std::deque<CopyPtr> demand_q_, spec_q_;
-  int demand_running_ = 0;
+  std::deque<CopyPtr> demand_q_, spec_q_, ra_q_;
+  int demand_running_ = 0, ra_running_ = 0;
+  // read-ahead buffers (pinned, one unit each) and this forward's requests
+  std::vector<void*> ra_buf_;
+  std::vector<hipEvent_t> ra_ev_;                     // per buffer: its last copy out
+  std::vector<int32_t> ra_free_;                      // q_mu_
+  std::vector<std::unique_ptr<RaEntry>> ra_entries_;  // engine thread (their states under q_mu_)
+  std::vector<std::vector<int32_t>> ra_index_;        // [layer][unit]: its entry this forward, -1
+  std::deque<RaEntry*> ra_wait_;                      // engine thread
+  bool ra_frozen_ = false;
+  RaCounts ra_st_;                                    // since open or the last reset
   bool stop_ = false;
   std::vector<std::thread> readers_;
 
@@ -237,6 +279,7 @@ class HostCtx final : public HostWork {
     uint64_t seq = 0, forwards = 0;
     std::vector<ss_layer_stats> layers;
     ss_exclusive_stats x{};
+    RaCounts ra;
   };
   mutable std::atomic<bool> snap_armed_{false};
   mutable std::mutex snap_mu_;

@@ -82,7 +82,21 @@ HostPlacement::HostPlacement(const Desc& d, const Plan& p, const ss_options& o) 
     s.spec_open.assign(size_t(l.n_units), 0);
     s.uses.assign(size_t(l.n_units), 0);
     s.table.assign(size_t(l.n_units), DevSpot{});
+    s.ra_asked.assign(size_t(l.n_units), 0);
   }
+  // host read-ahead: buffers of the largest host stride a unit can be read from its file with (none: off)
+  require(o_.readahead_units <= 64, SS_E_INVALID, "open: readahead_units must be <= 64");
+  if (o_.readahead_units)
+    for (size_t L = 0; L < d_.layers.size(); ++L) {
+      const Layer& l = d_.layers[L];
+      if (!l.streamable || !l.n_units) continue;
+      for (int u = 0; u < l.n_units; ++u) {
+        const uint8_t t = p_.tier[size_t(d_.gidx(int(L), u))];
+        if (t == SS_TIER_PINNED || t == SS_TIER_PAIR) continue;
+        ra_bytes_ = std::max(ra_bytes_, host_stride(l.unit_bytes));
+        break;  // (a layer's units are one size)
+      }
+    }
   for (const RingClass& rc : p_.rings) {
     if (!rc.slots) continue;
     ring_cls_.push_back({rc.stride, uint32_t(ring_.size()), rc.slots});
@@ -186,9 +200,9 @@ void HostPlacement::fetch_pool(int layer, int unit, int32_t slot, bool speculati
   f.after_writeback = after_writeback;
   s.spot[size_t(unit)] = f.dst;
   s.job[size_t(unit)] = f.job;
-  (f.src_block >= 0 ? fwd_[size_t(layer)].bytes_pinned : fwd_[size_t(layer)].bytes_disk) +=
-      d_.layers[size_t(layer)].unit_bytes;
-  w_->fetch(f);
+  if (!w_->fetch(f))  // (a landing from a read-ahead buffer: its file bytes count when the read-ahead ends)
+    (f.src_block >= 0 ? fwd_[size_t(layer)].bytes_pinned : fwd_[size_t(layer)].bytes_disk) +=
+        d_.layers[size_t(layer)].unit_bytes;
 }
 
 // The next free ring slot of the layer's stride class, round robin from the class's cursor.
@@ -212,9 +226,9 @@ bool HostPlacement::fetch_ring(int layer, int unit, bool speculative) {
     r.job = f.job;
     s.spot[size_t(unit)] = f.dst;
     s.job[size_t(unit)] = f.job;
-    (f.src_block >= 0 ? fwd_[size_t(layer)].bytes_pinned : fwd_[size_t(layer)].bytes_disk) +=
-        d_.layers[size_t(layer)].unit_bytes;
-    w_->fetch(f);
+    if (!w_->fetch(f))
+      (f.src_block >= 0 ? fwd_[size_t(layer)].bytes_pinned : fwd_[size_t(layer)].bytes_disk) +=
+          d_.layers[size_t(layer)].unit_bytes;
     return true;
   }
   return false;
@@ -319,6 +333,7 @@ void HostPlacement::open_forward() {
     s.hits.clear();
     s.waiting.clear();
     s.groups.clear();
+    std::fill(s.ra_asked.begin(), s.ra_asked.end(), uint8_t(0));
     s.routes_in = s.acquired = s.released = s.skipped = false;
   }
   std::fill(fwd_.begin(), fwd_.end(), ss_layer_stats{});
@@ -397,6 +412,7 @@ void HostPlacement::take_routes(int layer, const int32_t* ids, int n) {
     if (!fetch_ring(layer, u, false)) {
       s.waiting.push_back(u);
       s.spot[size_t(u)] = DevSpot{DevSpot::kRing, -1};
+      ra_request(layer, u, true);  // its file read need not wait for the ring slot
     }
   st.admitted += a.admitted.size();
   st.transient += a.transient.size();
@@ -433,6 +449,7 @@ void HostPlacement::prefetch(int layer, const int32_t* ids, int n, bool speculat
       if (speculative) break;
       s.waiting.push_back(u);
       s.spot[size_t(u)] = DevSpot{DevSpot::kRing, -1};
+      ra_request(layer, u, true);
     }
     busy[size_t(u)] = 1;
     if (speculative) {
@@ -441,6 +458,33 @@ void HostPlacement::prefetch(int layer, const int32_t* ids, int n, bool speculat
     }
     ++issued;
   }
+}
+
+void HostPlacement::host_prefetch(int layer, const int32_t* ids, int n) {
+  require(n >= 0 && (ids || n == 0), SS_E_INVALID, "host_prefetch: bad ids");
+  if (!ra_on()) return;  // read-ahead off: nothing to read
+  open_forward();        // (between forwards: the requests belong to the next one)
+  layer_with_units(layer, "host_prefetch");
+  for (int i = 0; i < n; ++i) ra_request(layer, ids[i], false);
+}
+
+void HostPlacement::ra_request(int layer, int unit, bool pending_ok) {
+  if (!ra_on()) return;
+  LayerPlace& s = L_[size_t(layer)];
+  const Layer& l = d_.layers[size_t(layer)];
+  if (!s.pool || !l.streamable || unit < 0 || unit >= l.n_units || s.ra_asked[size_t(unit)]) return;
+  if (!ra_wanted(layer, unit) || host_stride(l.unit_bytes) > ra_bytes_) return;
+  const DevSpot& sp = s.spot[size_t(unit)];
+  if (sp.kind != DevSpot::kNone && !(pending_ok && sp.kind == DevSpot::kRing && sp.index < 0)) return;
+  s.ra_asked[size_t(unit)] = 1;
+  w_->read_ahead(layer, unit);
+}
+
+bool HostPlacement::ra_wanted(int layer, int unit) const {
+  const LayerPlace& s = L_[size_t(layer)];
+  const int64_t g = d_.gidx(layer, unit);
+  return s.pool && p_.tier[size_t(g)] != SS_TIER_PAIR && block_of_[size_t(g)] < 0 && s.pool->slot(unit) < 0 &&
+         s.job[size_t(unit)] < 0;
 }
 
 HostPlacement::Acquire HostPlacement::acquire(int layer, bool wait_all) {

@@ -56,7 +56,11 @@ class HostWork {
  public:
   virtual ~HostWork() = default;
   virtual void write_back(const WriteBackOrder& w) = 0;
-  virtual void fetch(const FetchOrder& f) = 0;
+  // true: the copy lands from the unit's read-ahead buffer (its file bytes are counted when the read-ahead ends)
+  virtual bool fetch(const FetchOrder& f) = 0;
+  // Host read-ahead (readahead_units): read file-backed unit (layer, unit) into a host buffer now, for a later fetch
+  // of it in this forward (default: nothing).
+  virtual void read_ahead(int layer, int unit) { (void)layer, (void)unit; }
   virtual void promote(int32_t job) = 0;  // a speculative job was routed: it becomes a demand
   virtual void retire(int32_t job) = 0;   // its ring slot was released: cancel it if it never started, else wait
   // End of forward, in job order: cancel a speculative job that never started, else wait for it; true when it ran to
@@ -97,6 +101,13 @@ class HostPlacement {
   void routes(int layer, const int32_t* ids, int n);
   void routes_all(int layer);
   void prefetch(int layer, const int32_t* ids, int n, bool speculative);
+  // ss_host_prefetch: read-ahead requests for the eligible units (allowed between forwards: they belong to the next)
+  void host_prefetch(int layer, const int32_t* ids, int n);
+  bool ra_on() const { return ra_bytes_ > 0; }   // readahead_units > 0 and some unit can be read from its file
+  uint64_t ra_bytes() const { return ra_bytes_; }  // a read-ahead buffer: the largest host stride read from a file
+  void add_disk_bytes(int layer, uint64_t b) { fwd_[size_t(layer)].bytes_disk += b; }  // (read-ahead reads, at end)
+  // A requested read-ahead is still of use: the unit is off the device with no copy of it, no pinned source.
+  bool ra_wanted(int layer, int unit) const;
   struct Acquire {
     bool wait_ready = false;         // wait for the copies of earlier forwards into this layer's pool
     std::vector<int32_t> wait_jobs;  // (wait_all) every fetched routed unit's job, group order
@@ -141,6 +152,7 @@ class HostPlacement {
     std::vector<DevSpot> table;
     bool routes_in = false, acquired = false, released = false, skipped = false;
     bool ready_wait = false;  // across forwards: the next acquire waits for the pool copies of the last one
+    std::vector<uint8_t> ra_asked;  // this forward: a read-ahead was requested (never twice)
   };
   struct RingSlot {
     int32_t cls = 0, owner = -1, job = -1;
@@ -162,6 +174,9 @@ class HostPlacement {
   int eviction_cap(int layer, bool speculative) const;
   void give_back_block(int layer, int unit);  // a promoted unit's block returns to its class's free list
   void drain_waiting();
+  // A read-ahead request for a unit the forward will read from its file: not requested yet, not on the device, no
+  // copy of it yet (pending_ok: or only waiting for a ring slot), no pinned source, not a peer's.
+  void ra_request(int layer, int unit, bool pending_ok);
   void take_routes(int layer, const int32_t* ids, int n);
   uint64_t free_blocks_now() const;
 
@@ -184,6 +199,7 @@ class HostPlacement {
   std::vector<int64_t> wb_touched_;
   int32_t wb_batches_ = 0;
   std::vector<Job> jobs_;
+  uint64_t ra_bytes_ = 0;
   bool fwd_open_ = false, in_fwd_ = false;
   uint64_t forwards_ = 0;
   std::vector<ss_layer_stats> fwd_, total_;

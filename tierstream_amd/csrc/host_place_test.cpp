@@ -15,7 +15,7 @@ namespace {
 class NoDevice final : public HostWork {
  public:
   void write_back(const WriteBackOrder&) override {}
-  void fetch(const FetchOrder&) override {}
+  bool fetch(const FetchOrder&) override { return false; }
   void promote(int32_t) override {}
   void retire(int32_t) override {}
   bool settle(int32_t, bool) override { return true; }
@@ -83,8 +83,8 @@ ss_status tsa_test_hostplace_run(const char* desc_json, size_t len, const ss_bud
 }
 
 ss_status tsa_test_hostplace_exclusive(const char* desc_json, size_t len, const ss_budget* budget,
-                                       const ss_options* opt, int steps, const int32_t* routes, int max_ids, int mode,
-                                       ss_exclusive_stats* out) {
+                                       const ss_options* opt, int steps, const int32_t* routes,
+                                       const int32_t* prefetch, int max_ids, int mode, ss_exclusive_stats* out) {
   return tsa::guard([&] {
     using namespace tsa;
     require(desc_json && budget && opt && routes && out, SS_E_INVALID, "tsa_test_hostplace_exclusive: bad argument");
@@ -106,6 +106,12 @@ ss_status tsa_test_hostplace_exclusive(const char* desc_json, size_t len, const 
         else place.routes(l, r, n);
         place.acquire(l, mode != 2);
         place.take_table(l);
+        if (prefetch && l + 1 < L && d.layers[size_t(l + 1)].n_units > 0) {
+          const int32_t* q = prefetch + (size_t(s) * L + l + 1) * max_ids;
+          int m = 0;
+          while (m < max_ids && q[m] >= 0) ++m;
+          if (m) place.prefetch(l + 1, q, m, s % 2 == 1);
+        }
         place.release(l);
       }
       place.end();

@@ -145,12 +145,17 @@ extern "C" {
 
 // Host contract: `steps` forwards over every layer with units. routes[step][layer][max_ids] (-1 = none);
 // mode 0 = ss_layer_routes + ss_acquire, 1 = ss_layer_all + ss_acquire, 2 = ss_layer_routes + ss_acquire_groups with
-// one ss_group_wait per group. Outputs (may be NULL): checksums[step][layer][max_ids] of the routed ids (0 for -1),
+// one ss_group_wait per group; host_lookahead H > 0: after each layer's routes, ss_host_prefetch_layer of the next H
+// layers with units; prefetch (same shape as routes, may be NULL): after layer l's acquire, ss_prefetch of layer l + 1
+// with its row, CERTAIN on even steps and SPECULATIVE on odd ones (the next layer's ids while this one holds its slots).
+// Outputs (may be NULL): checksums[step][layer][max_ids] of the routed ids (0 for -1),
 // tables[step][layer][max_units] = the layer's table_host, stats[step] = the forward's totals, step_ms[step].
-__attribute__((visibility("default"))) ss_status tse_host_run(ss_ctx* c, const ss_desc* d, int steps,
-                                                              const int32_t* routes, int max_ids, int max_units,
-                                                              int mode, uint64_t* checksums, uint64_t* tables,
-                                                              ss_layer_stats* stats, double* step_ms) {
+__attribute__((visibility("default"))) ss_status tse_host_run_ex(ss_ctx* c, const ss_desc* d, int steps,
+                                                                 const int32_t* routes, const int32_t* prefetch,
+                                                                 int max_ids, int max_units, int mode,
+                                                                 int host_lookahead, uint64_t* checksums,
+                                                                 uint64_t* tables, ss_layer_stats* stats,
+                                                                 double* step_ms) {
   const int L = ss_desc_n_layers(d);
   hipStream_t s = nullptr;
   TSE_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
@@ -175,6 +180,11 @@ __attribute__((visibility("default"))) ss_status tse_host_run(ss_ctx* c, const s
       while (n < max_ids && r[n] >= 0) ++n;
       if (mode == 1) st = ss_layer_all(c, l);
       else st = ss_layer_routes(c, l, r, n);
+      for (int h = l + 1, left = host_lookahead; st == SS_OK && left > 0 && h < L; ++h)
+        if (ss_desc_layer_units(d, h) > 0) {
+          st = ss_host_prefetch_layer(c, h);
+          --left;
+        }
       if (st != SS_OK) break;
       ss_layer_view v{};
       st = mode == 2 ? ss_acquire_groups(c, l, s, &v) : ss_acquire(c, l, s, &v);
@@ -182,6 +192,13 @@ __attribute__((visibility("default"))) ss_status tse_host_run(ss_ctx* c, const s
       if (mode == 2)
         for (int gi = 1; st == SS_OK && gi < v.n_groups; ++gi) st = ss_group_wait(c, l, gi, s);
       if (st != SS_OK) break;
+      if (prefetch && l + 1 < L && ss_desc_layer_units(d, l + 1) > 0) {
+        const int32_t* q = prefetch + (size_t(step) * L + l + 1) * max_ids;
+        int m = 0;
+        while (m < max_ids && q[m] >= 0) ++m;
+        if (m && (st = ss_prefetch(c, l + 1, q, m, step % 2 ? SS_PREFETCH_SPECULATIVE : SS_PREFETCH_CERTAIN)) != SS_OK)
+          break;
+      }
       const int n_read = mode == 1 ? std::min(nu, max_ids) : n;
       int32_t* rid = ids_host + size_t(l) * max_ids;
       for (int i = 0; i < n_read; ++i) rid[i] = mode == 1 ? i : r[i];
@@ -227,6 +244,14 @@ __attribute__((visibility("default"))) ss_status tse_host_run(ss_ctx* c, const s
   (void)hipHostFree(ids_host);
   (void)hipStreamDestroy(s);
   return st;
+}
+
+__attribute__((visibility("default"))) ss_status tse_host_run(ss_ctx* c, const ss_desc* d, int steps,
+                                                              const int32_t* routes, int max_ids, int max_units,
+                                                              int mode, uint64_t* checksums, uint64_t* tables,
+                                                              ss_layer_stats* stats, double* step_ms) {
+  return tse_host_run_ex(c, d, steps, routes, nullptr, max_ids, max_units, mode, 0, checksums, tables, stats,
+                         step_ms);
 }
 
 // ---- device-gated ----

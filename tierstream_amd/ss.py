@@ -246,6 +246,10 @@ def engine() -> C.CDLL:
         E.tse_host_run.restype = C.c_int
         E.tse_host_run.argtypes = [vp, vp, C.c_int, C.POINTER(i32), C.c_int, C.c_int, C.c_int, C.POINTER(u64),
                                    C.POINTER(u64), C.POINTER(SsLayerStats), C.POINTER(C.c_double)]
+        E.tse_host_run_ex.restype = C.c_int
+        E.tse_host_run_ex.argtypes = [vp, vp, C.c_int, C.POINTER(i32), C.POINTER(i32), C.c_int, C.c_int, C.c_int,
+                                      C.c_int, C.POINTER(u64), C.POINTER(u64), C.POINTER(SsLayerStats),
+                                      C.POINTER(C.c_double)]
         E.tse_dg_create.restype = C.c_int
         E.tse_dg_create.argtypes = [vp, u32, C.c_int, C.c_int, C.c_int, C.POINTER(vp)]
         E.tse_dg_token.restype = C.c_int
@@ -494,20 +498,28 @@ class Ctx:
         return k.value, i.value, int(off.value)
 
     # ---- engine drivers ----
-    def host_run(self, routes: np.ndarray, mode: int = 0, want_tables=True):
-        """routes int32 [steps][layers][max_ids]; returns checksums, tables, per-step stats, step ms."""
+    def host_run(self, routes: np.ndarray, mode: int = 0, want_tables=True, host_lookahead: int = 0,
+                 prefetch: np.ndarray | None = None):
+        """routes int32 [steps][layers][max_ids]; host_lookahead H: ss_host_prefetch_layer of the next H layers after
+        each layer's routes; prefetch (routes' shape): after layer l's acquire, ss_prefetch of layer l + 1 with its
+        row, CERTAIN on even steps and SPECULATIVE on odd ones; returns checksums, tables, per-step stats, step ms."""
         E = engine()
         steps, L, max_ids = routes.shape
         max_units = max(self.desc.units(l) for l in range(L))
         r = np.ascontiguousarray(routes, dtype=np.int32)
+        q = None
+        if prefetch is not None:
+            q = np.ascontiguousarray(prefetch, dtype=np.int32)
+            assert q.shape == r.shape
         cks = np.zeros((steps, L, max_ids), dtype=np.uint64)
         tabs = np.zeros((steps, L, max_units), dtype=np.uint64) if want_tables else None
         stats = (SsLayerStats * steps)()
         ms = np.zeros(steps, dtype=np.float64)
-        st = E.tse_host_run(self.h, self.desc.h, steps, r.ctypes.data_as(C.POINTER(i32)), max_ids, max_units, mode,
-                            cks.ctypes.data_as(C.POINTER(u64)),
-                            tabs.ctypes.data_as(C.POINTER(u64)) if want_tables else None, stats,
-                            ms.ctypes.data_as(C.POINTER(C.c_double)))
+        st = E.tse_host_run_ex(self.h, self.desc.h, steps, r.ctypes.data_as(C.POINTER(i32)),
+                               q.ctypes.data_as(C.POINTER(i32)) if q is not None else None, max_ids, max_units,
+                               mode, host_lookahead, cks.ctypes.data_as(C.POINTER(u64)),
+                               tabs.ctypes.data_as(C.POINTER(u64)) if want_tables else None, stats,
+                               ms.ctypes.data_as(C.POINTER(C.c_double)))
         check(st)
         return cks, tabs, [s.as_dict() for s in stats], ms
 
