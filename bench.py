@@ -447,7 +447,8 @@ def main():
                          dg_landing_max_queued=a.landing_max_queued, dg_landing_chunk=a.landing_chunk)
         opts = {**shape.options, **extra}
         ctx = keep(ss.Ctx(d, b, plan, ss.options(**opts, verify_hash=2, dg_wait_timeout_ms=20000, policy=policy)))
-        log(f"context open (fill + hash check) in {time.time() - t0:.1f} s")
+        open_s = time.time() - t0
+        log(f"context open (fill + hash check) in {open_s:.1f} s")
         n_pred = shape.B if a.predict > 0 else 0
         eng = keep(ss.DgEngine(ctx, shape.B, use_graph=True, n_pred=n_pred))
         G = eng.G
@@ -622,6 +623,14 @@ def main():
                           "busy_GBps": round(pprof["writeback_bytes"] / pprof["writeback_ns"], 2)
                           if pprof["writeback_ns"] else None,
                           "sample": f"the {probe} probe tokens (part copies to host, issued at each boundary)"},
+            "open": {"seconds": round(open_s, 2),
+                     "device_bytes": n_res * w.unit_bytes, "pinned_bytes": n_pin * w.unit_bytes,
+                     "hashed_bytes": (n_res + n_pin + n_file) * w.unit_bytes,
+                     "hashed_GBps": round((n_res + n_pin + n_file) * w.unit_bytes / open_s / 1e9, 2),
+                     "device_GBps": round(n_res * w.unit_bytes / open_s / 1e9, 2),
+                     "note": "ss_open's fill: every unit read from the source once and hashed on the host (checkpoints "
+                             "for the device check), the residents copied into HBM through pinned staging blocks, the "
+                             "pinned homes kept in their blocks; 16 worker threads"},
             "stats": dstat,
             "checks": {"verify_failures": failures, "checksum_mismatches": ck_bad,
                        "units_seen": len(ck_seen)},
