@@ -93,8 +93,15 @@ void HostCtx::init() {
 
   dev_ = std::make_unique<HipDevice>(o_.device);
   copy_ = dev_->stream_create_dedicated();
-  copy2_ = dev_->stream_create_dedicated();
-  join_ev_ = dev_->event_create();
+  uint64_t largest = 0;
+  for (const Layer& l : d_.layers)
+    if (l.n_units) largest = std::max(largest, l.unit_bytes);
+  const int copy_streams = largest <= kSmallUnit ? 3 : 2;
+  for (int i = 1; i < copy_streams; ++i) {
+    copyx_.push_back(dev_->stream_create_dedicated());
+    joinx_ev_.push_back(dev_->event_create());
+    vreadyx_ev_.push_back(dev_->event_create());
+  }
   for (const auto& s : d_.sources) files_.push_back(std::make_unique<SourceFile>(s.path, o_.direct_io != 0));
   for (uint32_t i = 0; i < o_.staging_buffers; ++i) {
     staging_.push_back(Staging{dev_->alloc_pinned(o_.staging_bytes, "staging buffer"), nullptr});
@@ -179,7 +186,6 @@ void HostCtx::init() {
     hip_check(hipMemsetAsync(vfail_dev_, 0, vcap_ * 4, copy_), "hipMemsetAsync");
     vdone_ev_ = dev_->event_create();
     vready_ev_ = dev_->event_create();
-    vready2_ev_ = dev_->event_create();
     vstream_ = dev_->stream_create_dedicated();
     stream_sync(copy_);
   }
@@ -216,8 +222,7 @@ void HostCtx::init() {
   for (const CopyPtr& c : fills_)
     if (c->done_ev) ev_pool_.push_back(c->done_ev);
   fills_.clear();
-  stream_sync(copy_);
-  stream_sync(copy2_);
+  sync_copies();
   if (dverify_) collect_verify();  // the residents' device check, one batch at open
 }
 
@@ -261,13 +266,13 @@ void HostCtx::cleanup() noexcept {
   dev_->free_device(vfail_dev_);
   dev_->event_destroy(vdone_ev_);
   dev_->event_destroy(vready_ev_);
-  dev_->event_destroy(vready2_ev_);
   for (hipEvent_t e : vflush_ev_) dev_->event_destroy(e);
   for (hipEvent_t e : prof_made_) dev_->event_destroy(e);
   dev_->stream_destroy(vstream_);
-  dev_->event_destroy(join_ev_);
+  for (hipEvent_t e : joinx_ev_) dev_->event_destroy(e);
+  for (hipEvent_t e : vreadyx_ev_) dev_->event_destroy(e);
   dev_->stream_destroy(copy_);
-  dev_->stream_destroy(copy2_);
+  for (hipStream_t x : copyx_) dev_->stream_destroy(x);
   dev_->stream_destroy(wb_);
   L_.clear();
   dev_.reset();
@@ -885,8 +890,15 @@ void HostCtx::wait_slot_check(hipStream_t s, const void* dst) {
 }
 
 void HostCtx::join_copies() {
-  ev_record(join_ev_, copy2_);
-  stream_wait(copy_, join_ev_);
+  for (size_t i = 0; i < copyx_.size(); ++i) {
+    ev_record(joinx_ev_[i], copyx_[i]);
+    stream_wait(copy_, joinx_ev_[i]);
+  }
+}
+
+void HostCtx::sync_copies() {
+  stream_sync(copy_);
+  for (hipStream_t x : copyx_) stream_sync(x);
 }
 
 void HostCtx::flush_verify() {
@@ -899,9 +911,11 @@ void HostCtx::flush_verify() {
     segs += count;
   }
   ev_record(vready_ev_, copy_);
-  ev_record(vready2_ev_, copy2_);
   stream_wait(vstream_, vready_ev_);
-  stream_wait(vstream_, vready2_ev_);
+  for (size_t i = 0; i < copyx_.size(); ++i) {
+    ev_record(vreadyx_ev_[i], copyx_[i]);
+    stream_wait(vstream_, vreadyx_ev_[i]);
+  }
   tsa_verify_unit* vd = static_cast<tsa_verify_unit*>(vtable_dev_) + vflushed_;
   copy_h2d(vd, vtable_host_ + vflushed_, n * sizeof(tsa_verify_unit), vstream_);
   TimedCheck t{nullptr, nullptr, 0, uint32_t(n)};
@@ -1028,8 +1042,7 @@ void HostCtx::seed(int layer, const int32_t* units, int n) {
   fills_.clear();
   bool synced = true;
   try {
-    stream_sync(copy_);
-    stream_sync(copy2_);
+    sync_copies();
   } catch (const Error& e) {
     synced = false;
     if (failed == SS_OK) {
@@ -1232,8 +1245,7 @@ void HostCtx::check_unit(int layer, int unit) {
     await(*jobs_[size_t(j)]);
     ev_sync(jobs_[size_t(j)]->done_ev);
   }
-  stream_sync(copy_);
-  stream_sync(copy2_);
+  sync_copies();
   std::vector<char> got(size_t(l.unit_bytes));
   std::vector<char> want(size_t(round_up(l.unit_bytes, kHostAlign)) + kHostAlign);
   hip_check(hipMemcpy(got.data(), a, got.size(), hipMemcpyDeviceToHost), "hipMemcpy (check_unit)");

@@ -2,7 +2,7 @@
 // ss_acquire[_groups] / ss_group_wait / ss_release / ss_end). HostPlacement decides every placement; this executor
 // carries its orders out:
 //  - layer pools and the stream ring in HBM, the pinned tier and exclusive-mode spare blocks in hipHostMalloc memory;
-//  - a copy from a pinned block is issued at once on one of two SDMA copy streams (alternating per unit);
+//  - a copy from a pinned block is issued at once on one of two or three SDMA copy streams (rotating per unit);
 //  - a copy from a file is a job for the reader threads: direct-I/O reads into pinned staging, host XXH64, then the
 //    copy stream;
 //  - exclusive-mode write-backs run on their own device-to-host stream;
@@ -181,8 +181,12 @@ class HostCtx final : public HostWork {
   void* spot_addr(int layer, const DevSpot& s) const;
   hipEvent_t pooled_event();
   int64_t gidx(int layer, int unit) const { return d_.gidx(layer, unit); }
-  hipStream_t next_copy_stream() { return (copy_alt_ = !copy_alt_) ? copy2_ : copy_; }
-  void join_copies();  // copy_ follows copy2_'s work so far (copy_mu_ held)
+  hipStream_t next_copy_stream() {
+    copy_next_ = (copy_next_ + 1) % int(copyx_.size() + 1);
+    return copy_next_ ? copyx_[size_t(copy_next_ - 1)] : copy_;
+  }
+  void join_copies();  // copy_ follows the other copy streams' work so far (copy_mu_ held)
+  void sync_copies();  // every copy stream drained
   // verify_hash = 2
   void verify_landed(const Copy& c);  // the unit joins the pending check batch (copy_mu_ held)
   void flush_verify();                // the pending batch: one launch on the verify stream behind its copies
@@ -199,10 +203,14 @@ class HostCtx final : public HostWork {
   std::unique_ptr<HipDevice> dev_;
   std::vector<std::unique_ptr<SourceFile>> files_;
   std::vector<LayerDev> L_;
-  // Pinned -> HBM copies alternate between copy_ and copy2_ (two SDMA queues); other copies use copy_.
-  hipStream_t copy_ = nullptr, copy2_ = nullptr, wb_ = nullptr;
-  hipEvent_t join_ev_ = nullptr;
-  bool copy_alt_ = false;
+  // Pinned -> HBM copies rotate over copy_ and copyx_ (SDMA queues); other copies use copy_. Units of at most
+  // kSmallUnit bytes rotate over three queues, larger ones over two (measured: 9 MiB units 2 % faster per step on three
+  // than on two, 224 MiB units 2 % slower).
+  static constexpr uint64_t kSmallUnit = uint64_t(64) << 20;
+  hipStream_t copy_ = nullptr, wb_ = nullptr;
+  std::vector<hipStream_t> copyx_;  // the other copy streams
+  std::vector<hipEvent_t> joinx_ev_, vreadyx_ev_;  // per other copy stream: its mark at a join / at a check flush
+  int copy_next_ = 0;
   std::vector<void*> ring_base_;     // per ring class
   std::vector<void*> ring_addr_;     // per ring slot
   std::vector<void*> host_chunks_;   // the pinned tier and the spare blocks
@@ -250,7 +258,7 @@ class HostCtx final : public HostWork {
   uint32_t* vfail_host_ = nullptr;
   size_t vcap_ = 0, vused_ = 0, vflushed_ = 0;  // table slots used this forward; the ones already launched
   hipStream_t vstream_ = nullptr;                 // the checks (copies never queue behind them)
-  hipEvent_t vready_ev_ = nullptr, vready2_ev_ = nullptr;  // the two copy streams at a flush
+  hipEvent_t vready_ev_ = nullptr;  // copy_ at a flush (the other copy streams: vreadyx_ev_)
   std::vector<std::pair<int, int>> vunits_;  // (layer, unit) of each check slot this forward
   // a landed unit's check reads its slot until its launch completes: the slot's pending entry, the flush that launched
   // each entry, and per flush an event on the verify stream after its launch
