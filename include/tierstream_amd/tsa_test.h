@@ -20,6 +20,9 @@ SS_API ss_status tsa_test_region_of(const ss_ctx* c, uint64_t addr, int* kind, i
 SS_API ss_status tsa_test_dg_table(const ss_ctx* c, int32_t* out, uint32_t cap, uint32_t* n);
 /* verify_hash = 2: landed units whose device check failed, since open. */
 SS_API uint64_t tsa_test_verify_failures(const ss_ctx* c);
+/* Host contract: unit copies from pinned blocks since open, and the host-to-device copies they were issued as (a run
+ * of neighbouring units is one copy). SS_E_INVALID on a device-gated context. */
+SS_API ss_status tsa_test_host_copies(const ss_ctx* c, uint64_t* units, uint64_t* copies);
 
 /* Device-gated timing (measurement only; the cache state is untouched). While enabled the library brackets every unit
  * copy host -> HBM, every write-back HBM -> host and every device verify launch with timed events on the stream that
@@ -132,6 +135,12 @@ SS_API ss_status tsa_test_hostplace_run(const char* desc_json, size_t len, const
 SS_API ss_status tsa_test_dg_geometry(const char* desc_json, size_t len, const ss_budget* budget, const uint8_t* tiers,
                                       size_t n_tiers, const ss_options* opt, uint32_t* out, uint32_t* residents,
                                       uint32_t res_cap);
+/* The host contract's copy runs alone (no device): orders k = 0 .. n-1 with their layer, source and destination
+ * allocations (-1 source: not a pinned block) and addresses; run_of[k] = the index of the copy that carries order k
+ * (neighbouring units in both allocations, one slot apart, at most cap bytes per copy). */
+SS_API ss_status tsa_test_copy_runs(const int32_t* layer, const int32_t* src_alloc, const int32_t* dst_alloc,
+                                    const uint64_t* src, const uint64_t* dst, size_t n, uint64_t unit_bytes,
+                                    uint64_t cap, uint32_t* run_of);
 /* The same loop (prefetch may be NULL); the exclusive-mode counters after the last forward. */
 SS_API ss_status tsa_test_hostplace_exclusive(const char* desc_json, size_t len, const ss_budget* budget,
                                               const ss_options* opt, int steps, const int32_t* routes,

@@ -141,6 +141,14 @@ def test_host_contract_matches_reference(name, tmp_path, gpu):
     if name == "qwen-exclusive":
         x = ctx.exclusive_stats()
         assert x["writebacks"] > 0  # the shape exercises write-backs
+    # pinned-block copies of neighbouring units into neighbouring slots go as one copy (checked above: every table
+    # entry's bytes); pieces below the unit size keep one copy per unit
+    units, copies = ctx.host_copies()
+    assert 0 < copies <= units, (units, copies)
+    if "copy_piece_bytes" in CASES[name]["opts"]:
+        assert copies == units
+    if name in ("qwen-exclusive", "qwen-exclusive-scored", "qwen-exclusive-prefetch"):
+        assert copies < units, (units, copies)
     if CASES[name].get("prefetch"):  # the shape exercises certain prefetches and used and dropped speculative ones
         assert tot["prefetched"] > 0 and tot["spec_used"] > 0 and tot["spec_dropped"] > 0, tot
     ctx.close()

@@ -536,6 +536,13 @@ uint64_t tsa_test_verify_failures(const ss_ctx* c) {
   if (!c) return 0;
   return c->dg ? c->dg->verify_failures() : c->host->verify_failures();
 }
+ss_status tsa_test_host_copies(const ss_ctx* c, uint64_t* units, uint64_t* copies) {
+  return guard([&] {
+    need(c && units && copies, "tsa_test_host_copies: null argument");
+    need(c->host != nullptr, "tsa_test_host_copies: a host-contract context");
+    c->host->copy_counts(units, copies);
+  });
+}
 ss_status tsa_test_profile_enable(ss_ctx* c, int on) {
   return guard([&] {
     need(c != nullptr, "tsa_test_profile_enable: null context");

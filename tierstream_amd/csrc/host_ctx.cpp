@@ -4,6 +4,7 @@
 #include <chrono>
 #include <cstring>
 
+#include "copy_runs.hpp"
 #include "stats_json.hpp"
 #include "tsa_device.hpp"
 
@@ -117,6 +118,7 @@ void HostCtx::init() {
     const auto& blocks = place_.blocks();
     const auto& cls_bytes = place_.block_class_bytes();
     block_addr_.assign(blocks.size(), nullptr);
+    block_alloc_.assign(blocks.size(), -1);
     std::vector<uint64_t> left(cls_bytes.size(), 0);
     for (const BlockHome& b : blocks)
       if (b.home < 0) ++left[size_t(b.cls)];
@@ -129,6 +131,7 @@ void HostCtx::init() {
       if (b.home >= 0) {
         block_addr_[i] = at(host_chunks_[first_chunk + size_t(pl.chunk_of[size_t(b.home)])],
                             pl.offset_of[size_t(b.home)]);
+        block_alloc_[i] = int32_t(first_chunk + size_t(pl.chunk_of[size_t(b.home)]));
         continue;
       }
       const uint64_t bytes = cls_bytes[size_t(b.cls)];
@@ -140,6 +143,7 @@ void HostCtx::init() {
         cursor_cls = b.cls;
       }
       block_addr_[i] = cursor;
+      block_alloc_[i] = int32_t(host_chunks_.size() - 1);
       cursor += bytes;
       --in_chunk;
       --left[size_t(b.cls)];
@@ -170,7 +174,10 @@ void HostCtx::init() {
   }
   for (const auto& rc : place_.ring_classes()) {
     ring_base_.push_back(dev_->alloc_device(rc.stride * rc.count, "stream ring"));
-    for (uint32_t i = 0; i < rc.count; ++i) ring_addr_.push_back(at(ring_base_.back(), rc.stride * i));
+    for (uint32_t i = 0; i < rc.count; ++i) {
+      ring_addr_.push_back(at(ring_base_.back(), rc.stride * i));
+      ring_alloc_.push_back(int32_t(ring_base_.size() - 1));
+    }
   }
 
   if (o_.verify_hash == 2) {  // the device check of every landed unit: checkpoint tables and the launch slots
@@ -217,10 +224,13 @@ void HostCtx::init() {
   }
   for (const CopyPtr& c : fills_) await(*c);
   fills_.clear();
-  place_.place_residents();
+  {
+    PendGuard g{this};
+    place_.place_residents();
+    flush_copies();
+  }
   for (const CopyPtr& c : fills_) await(*c);
-  for (const CopyPtr& c : fills_)
-    if (c->done_ev) ev_pool_.push_back(c->done_ev);
+  for (const CopyPtr& c : fills_) release_event(*c);
   fills_.clear();
   sync_copies();
   if (dverify_) collect_verify();  // the residents' device check, one batch at open
@@ -309,6 +319,8 @@ bool HostCtx::fetch(const FetchOrder& f) {
   c->speculative = f.speculative;
   c->dst = spot_addr(f.layer, f.dst);
   c->src = f.src_block >= 0 ? block_addr_[size_t(f.src_block)] : nullptr;
+  c->src_alloc = f.src_block >= 0 ? block_alloc_[size_t(f.src_block)] : -1;
+  c->dst_alloc = f.dst.kind == DevSpot::kRing ? ring_alloc_[size_t(f.dst.index)] : -2 - f.layer;
   c->after[0] = f.after_release >= 0 ? L_[size_t(f.after_release)].release_ev : nullptr;
   c->after[1] = f.after_writeback >= 0 ? wb_ev_[size_t(f.after_writeback)] : nullptr;
   c->after[2] = f.src_writeback >= 0 ? wb_ev_[size_t(f.src_writeback)] : nullptr;
@@ -372,13 +384,8 @@ bool HostCtx::settle(int32_t job, bool) {
 // ---- copies and reads ---------------------------------------------------------------------------------------------
 
 void HostCtx::submit(const CopyPtr& c) {
-  if (c->src && !c->to_host) {  // a pinned block: issued now
-    try {
-      issue_copy(*c, c->src, nullptr);
-    } catch (const Error& e) {
-      finish(*c, Copy::kFailed, e.status(), e.what());
-      throw;
-    }
+  if (c->src && !c->to_host) {  // a pinned block: issued when the engine call returns (flush_copies)
+    pend_.push_back(c);
     c->state.store(Copy::kDone);
     return;
   }
@@ -392,8 +399,12 @@ void HostCtx::submit(const CopyPtr& c) {
 // Host memory (a pinned block, a read-ahead buffer) into c's destination on the next copy stream (an SDMA queue), in
 // pieces of copy_piece_bytes, behind the destination's waits; after_ev (if any) is recorded behind the copy too.
 void HostCtx::issue_copy(Copy& c, const void* src, hipEvent_t after_ev) {
-  const uint64_t n = d_.layers[size_t(c.layer)].unit_bytes;
   std::lock_guard<std::mutex> lk(copy_mu_);
+  issue_copy_locked(c, src, after_ev);
+}
+
+void HostCtx::issue_copy_locked(Copy& c, const void* src, hipEvent_t after_ev) {
+  const uint64_t n = d_.layers[size_t(c.layer)].unit_bytes;
   const hipStream_t cs = next_copy_stream();
   wait_slot_check(cs, c.dst);
   for (hipEvent_t e : c.after) stream_wait(cs, e);
@@ -402,6 +413,81 @@ void HostCtx::issue_copy(Copy& c, const void* src, hipEvent_t after_ev) {
   ev_record(c.done_ev, cs);
   if (after_ev) ev_record(after_ev, cs);
   if (dverify_) verify_landed(c);
+}
+
+void HostCtx::flush_copies() {
+  if (pend_.empty()) return;
+  std::lock_guard<std::mutex> lk(copy_mu_);
+  std::vector<CopyRunItem> items(pend_.size());
+  for (size_t k = 0; k < pend_.size(); ++k) {
+    const Copy& c = *pend_[k];
+    items[k] = CopyRunItem{c.layer, c.src_alloc, c.dst_alloc, uint64_t(reinterpret_cast<uintptr_t>(c.src)),
+                           uint64_t(reinterpret_cast<uintptr_t>(c.dst))};
+  }
+  size_t i = 0;
+  try {
+    while (i < pend_.size()) {
+      const uint64_t n = d_.layers[size_t(pend_[i]->layer)].unit_bytes;
+      const uint64_t cap = std::max(o_.copy_piece_bytes, n);  // a run of small units stays one piece
+      const size_t j = copy_run_end(items.data(), items.size(), i, n, cap);
+      issue_run(i, j, j > i + 1 ? (items[j - 1].dst - items[i].dst) + n : n);
+      i = j;
+    }
+  } catch (...) {
+    for (; i < pend_.size(); ++i) {  // never issued: their waits would see nothing
+      pend_[i]->state.store(Copy::kFailed);
+      pend_[i]->status = SS_E_BACKEND;
+    }
+    pend_.clear();
+    throw;
+  }
+  pend_.clear();
+}
+
+void HostCtx::issue_run(size_t first, size_t end, uint64_t span) {
+  Copy& lead = *pend_[first];
+  pinned_units_ += end - first;
+  ++pinned_copies_;
+  if (end == first + 1) {
+    issue_copy_locked(lead, lead.src, nullptr);
+    return;
+  }
+  const hipStream_t cs = next_copy_stream();
+  hipEvent_t waited[16];
+  size_t n_waited = 0;
+  for (size_t k = first; k < end; ++k) {
+    Copy& c = *pend_[k];
+    wait_slot_check(cs, c.dst);
+    for (hipEvent_t e : c.after) {
+      if (!e || std::find(waited, waited + n_waited, e) != waited + n_waited) continue;
+      stream_wait(cs, e);
+      if (n_waited < 16) waited[n_waited++] = e;
+    }
+  }
+  for (uint64_t off = 0; off < span; off += o_.copy_piece_bytes)
+    copy_h2d(at(lead.dst, off), at(lead.src, off), std::min(o_.copy_piece_bytes, span - off), cs);
+  ev_record(lead.done_ev, cs);
+  for (size_t k = first; k < end; ++k) {
+    Copy& c = *pend_[k];
+    if (k != first) {
+      ev_pool_.push_back(c.done_ev);
+      c.done_ev = lead.done_ev;
+      c.owns_ev = false;
+    }
+    if (dverify_) verify_landed(c);
+  }
+}
+
+// Engine-stream waits for jobs' copies: each distinct event once (the units of one run share theirs).
+void HostCtx::wait_jobs(const std::vector<int32_t>& jobs, hipStream_t es) {
+  std::vector<hipEvent_t> seen;
+  for (int32_t j : jobs) {
+    Copy& c = *jobs_[size_t(j)];
+    await(c);
+    if (!c.done_ev || std::find(seen.begin(), seen.end(), c.done_ev) != seen.end()) continue;
+    stream_wait(es, c.done_ev);
+    seen.push_back(c.done_ev);
+  }
 }
 
 void HostCtx::finish(Copy& c, int state, ss_status st, const std::string& what) noexcept {
@@ -1022,7 +1108,12 @@ void HostCtx::check_stream(void* stream, const char* what) {
 void HostCtx::seed(int layer, const int32_t* units, int n) {
   check_layer(layer, "seed");
   fills_.clear();
-  const std::vector<int32_t> placed = place_.seed(layer, units, n);
+  std::vector<int32_t> placed;
+  {
+    PendGuard g{this};
+    placed = place_.seed(layer, units, n);
+    flush_copies();
+  }
   ss_status failed = SS_OK;
   std::string error;
   std::vector<char> ok(placed.size(), 0);
@@ -1038,7 +1129,7 @@ void HostCtx::seed(int layer, const int32_t* units, int n) {
       }
     }
   }
-  for (const CopyPtr& c : fills_) ev_pool_.push_back(c->done_ev);
+  for (const CopyPtr& c : fills_) release_event(*c);
   fills_.clear();
   bool synced = true;
   try {
@@ -1059,13 +1150,17 @@ void HostCtx::begin(const uint32_t* rows, int n_layers) { place_.begin(rows, n_l
 
 void HostCtx::routes(int layer, const int32_t* ids, int n) {
   check_layer(layer, "routes");
+  PendGuard g{this};
   place_.routes(layer, ids, n);
+  flush_copies();
   ra_pump();
 }
 
 void HostCtx::routes_all(int layer) {
   check_layer(layer, "layer_all");
+  PendGuard g{this};
   place_.routes_all(layer);
+  flush_copies();
   ra_pump();
 }
 
@@ -1093,12 +1188,16 @@ void HostCtx::ingest_dev_routes(int layer) {
   ev_sync(s.ids_ev);
   const int n = s.ids_n;
   s.ids_n = -1;
+  PendGuard g{this};
   place_.routes(layer, s.ids_host, n);
+  flush_copies();
 }
 
 void HostCtx::prefetch(int layer, const int32_t* ids, int n, bool speculative) {
   check_layer(layer, "prefetch");
+  PendGuard g{this};
   place_.prefetch(layer, ids, n, speculative);
+  flush_copies();
   ra_pump();
 }
 
@@ -1106,7 +1205,9 @@ void HostCtx::prefetch_layer(int layer) {
   check_layer(layer, "prefetch_layer");
   std::vector<int32_t> all(static_cast<size_t>(d_.layers[size_t(layer)].n_units));
   for (size_t u = 0; u < all.size(); ++u) all[u] = int32_t(u);
+  PendGuard g{this};
   place_.prefetch(layer, all.data(), int(all.size()), false);
+  flush_copies();
   ra_pump();
 }
 
@@ -1137,14 +1238,13 @@ void HostCtx::acquire(int layer, void* stream, bool wait_all, ss_layer_view* out
           "acquire: no routes for layer " + std::to_string(layer) + " (ss_layer_routes / ss_layer_all first)");
   const hipStream_t es = static_cast<hipStream_t>(stream);
   LayerDev& s = L_[size_t(layer)];
+  PendGuard g{this};
   const HostPlacement::Acquire a = place_.acquire(layer, wait_all);
+  flush_copies();
   if (a.wait_ready) stream_wait(es, s.ready_ev);  // the copies an earlier forward issued into this layer's pool
   if (!a.wait_jobs.empty()) {
     const uint64_t t0 = now_ns();
-    for (int32_t j : a.wait_jobs) {
-      await(*jobs_[size_t(j)]);
-      stream_wait(es, jobs_[size_t(j)]->done_ev);
-    }
+    wait_jobs(a.wait_jobs, es);
     place_.add_wait_ns(layer, now_ns() - t0);
   }
   const std::vector<DevSpot>& t = place_.take_table(layer);
@@ -1171,10 +1271,7 @@ void HostCtx::group_wait(int layer, int group, void* stream) {
   const std::vector<int32_t> jobs = place_.group_jobs(layer, group);
   if (jobs.empty()) return;
   const uint64_t t0 = now_ns();
-  for (int32_t j : jobs) {
-    await(*jobs_[size_t(j)]);
-    stream_wait(static_cast<hipStream_t>(stream), jobs_[size_t(j)]->done_ev);
-  }
+  wait_jobs(jobs, static_cast<hipStream_t>(stream));
   place_.add_wait_ns(layer, now_ns() - t0);
 }
 
@@ -1186,7 +1283,9 @@ void HostCtx::release(int layer, void* stream) {
   LayerDev& s = L_[size_t(layer)];
   ev_record(s.release_ev, static_cast<hipStream_t>(stream));
   ev_record(s.table_ev[s.version], static_cast<hipStream_t>(stream));  // its table is read until here
+  PendGuard g{this};
   place_.release(layer);
+  flush_copies();
   ra_pump();
 }
 
@@ -1198,7 +1297,9 @@ void HostCtx::end() {
   fwd_failed_ = SS_OK;
   fwd_error_.clear();
   ra_end_forward();
+  flush_copies();
   const HostPlacement::Ended e = place_.end();  // settles every job of the forward
+  flush_copies();
   {
     std::lock_guard<std::mutex> lk(copy_mu_);
     join_copies();  // the once-per-forward marks below stand for the copies on both streams
@@ -1218,7 +1319,7 @@ void HostCtx::end() {
   for (hipEvent_t ev : wb_ev_) ev_pool_.push_back(ev);
   wb_ev_.clear();
   for (const CopyPtr& c : jobs_)
-    if (c) ev_pool_.push_back(c->done_ev);
+    if (c) release_event(*c);
   jobs_.clear();
   fwd_stream_set_ = false;
   fwd_stream_ = nullptr;

@@ -78,6 +78,11 @@ class HostCtx final : public HostWork {
   bool poisoned() const { return poisoned_; }
   Region region_of(uint64_t addr) const;
   uint64_t verify_failures() const { return verify_fail_total_; }
+  void copy_counts(uint64_t* units, uint64_t* copies) const {
+    std::lock_guard<std::mutex> lk(copy_mu_);
+    *units = pinned_units_;
+    *copies = pinned_copies_;
+  }
   // Timing (a test hook, between forwards): each device-check launch bracketed by its dispatch's own begin and end
   // stamps when on & TSA_TEST_PROF_VERIFY (this context brackets nothing else); read sums the completed brackets.
   void profile_enable(int on);
@@ -102,6 +107,9 @@ class HostCtx final : public HostWork {
     const void* src = nullptr;  // a pinned block, or null: the unit's file
     hipEvent_t after[3] = {nullptr, nullptr, nullptr};  // dst's last reader, dst's victim write-back, src's write-back
     hipEvent_t done_ev = nullptr;
+    bool owns_ev = true;      // false: done_ev is the event of the run it was copied in (its first copy owns it)
+    int32_t src_alloc = -1;   // a pinned block's allocation (-1: not a pinned block)
+    int32_t dst_alloc = -1;   // the destination's allocation (a ring class, or a layer's pool)
     std::atomic<int> state{kQueued};
     ss_status status = SS_OK;
     std::string what;
@@ -161,6 +169,26 @@ class HostCtx final : public HostWork {
   void stage_to_device(Copy& c);
   void submit(const CopyPtr& c);
   void issue_copy(Copy& c, const void* src, hipEvent_t after_ev);  // host memory -> c.dst now (copy_mu_ taken)
+  void issue_copy_locked(Copy& c, const void* src, hipEvent_t after_ev);  // the same, copy_mu_ held
+  // Copies from pinned blocks are held until the engine call that ordered them returns, then issued: a run of them
+  // whose sources and destinations advance by the same stride inside one allocation each goes as one copy (the units
+  // of a layer's misses are fetched in id order, so neighbours in a pinned layout often take neighbouring ring slots).
+  void flush_copies();
+  void issue_run(size_t first, size_t end, uint64_t span);  // pend_[first, end) as one copy of span bytes (copy_mu_)
+  struct PendGuard {  // an engine call that throws part-way still issues what it ordered
+    HostCtx* h;
+    ~PendGuard() {
+      if (h->pend_.empty()) return;
+      try {
+        h->flush_copies();
+      } catch (...) {
+      }
+    }
+  };
+  void wait_jobs(const std::vector<int32_t>& jobs, hipStream_t es);
+  void release_event(const Copy& c) {
+    if (c.done_ev && c.owns_ev) ev_pool_.push_back(c.done_ev);
+  }
   // read-ahead
   bool ra_on() const { return !ra_buf_.empty(); }
   void ra_pump();                                  // waiting requests take free buffers (engine thread)
@@ -222,6 +250,10 @@ class HostCtx final : public HostWork {
   std::vector<hipEvent_t> ev_pool_, all_events_;
   std::vector<CopyPtr> jobs_;        // this forward's, by job id
   std::vector<CopyPtr> fills_;       // open and seed fills
+  std::vector<CopyPtr> pend_;        // pinned-block copies ordered by the current engine call, not issued yet
+  uint64_t pinned_units_ = 0, pinned_copies_ = 0;  // since open (copy_mu_)
+  std::vector<int32_t> block_alloc_;  // per pinned block: its allocation (an index into host_chunks_)
+  std::vector<int32_t> ring_alloc_;   // per ring slot: its ring class
   ss_status fwd_failed_ = SS_OK;     // the first failed job of the forward (settle)
   std::string fwd_error_;
 
@@ -229,7 +261,7 @@ class HostCtx final : public HostWork {
   std::vector<size_t> staging_free_;
   std::mutex staging_mu_;
   std::condition_variable staging_cv_;
-  std::mutex copy_mu_;
+  mutable std::mutex copy_mu_;
 
   // reader threads: demand reads first; a speculative read only while no demand waits and at most one runs
   std::mutex q_mu_;

@@ -6,6 +6,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "copy_runs.hpp"
 #include "host_place.hpp"
 #include "tierstream_amd/tsa_test.h"
 
@@ -78,6 +79,25 @@ ss_status tsa_test_hostplace_run(const char* desc_json, size_t len, const ss_bud
       place.end();
       stats[s] = ss_layer_stats{};
       for (const ss_layer_stats& x : place.forward_stats()) add_stats(stats[s], x);
+    }
+  });
+}
+
+ss_status tsa_test_copy_runs(const int32_t* layer, const int32_t* src_alloc, const int32_t* dst_alloc,
+                             const uint64_t* src, const uint64_t* dst, size_t n, uint64_t unit_bytes, uint64_t cap,
+                             uint32_t* run_of) {
+  return tsa::guard([&] {
+    using namespace tsa;
+    require(n == 0 || (layer && src_alloc && dst_alloc && src && dst && run_of), SS_E_INVALID,
+            "tsa_test_copy_runs: null argument");
+    require(unit_bytes > 0, SS_E_INVALID, "tsa_test_copy_runs: unit_bytes is 0");
+    std::vector<CopyRunItem> items(n);
+    for (size_t k = 0; k < n; ++k) items[k] = CopyRunItem{layer[k], src_alloc[k], dst_alloc[k], src[k], dst[k]};
+    uint32_t run = 0;
+    for (size_t i = 0; i < n; ++run) {
+      const size_t j = copy_run_end(items.data(), n, i, unit_bytes, std::max(cap, unit_bytes));
+      for (size_t k = i; k < j; ++k) run_of[k] = run;
+      i = j;
     }
   });
 }

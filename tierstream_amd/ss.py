@@ -218,6 +218,7 @@ def _declare() -> C.CDLL:
         "tsa_test_region_of": (st, [vp, u64, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(u64)]),
         "tsa_test_dg_table": (st, [vp, C.POINTER(i32), u32, C.POINTER(u32)]),
         "tsa_test_verify_failures": (u64, [vp]),
+        "tsa_test_host_copies": (st, [vp, C.POINTER(u64), C.POINTER(u64)]),
         "tsa_test_profile_enable": (st, [vp, C.c_int]),
         "tsa_test_profile_read": (st, [vp, C.c_int, C.POINTER(TsaTestProfile)]),
         "tsa_test_dg_stamps": (st, [vp, C.POINTER(u64), u32, C.POINTER(u32)]),
@@ -465,6 +466,12 @@ class Ctx:
 
     def verify_failures(self) -> int:
         return int(_declare().tsa_test_verify_failures(self.h))
+
+    def host_copies(self) -> tuple[int, int]:
+        """Host contract: (unit copies from pinned blocks since open, the copies they were issued as)."""
+        units, copies = u64(), u64()
+        check(_declare().tsa_test_host_copies(self.h, C.byref(units), C.byref(copies)))
+        return int(units.value), int(copies.value)
 
     PROF_COPY, PROF_WRITEBACK, PROF_VERIFY = 0x2, 0x4, 0x8
 
