@@ -94,11 +94,7 @@ void HostCtx::init() {
 
   dev_ = std::make_unique<HipDevice>(o_.device);
   copy_ = dev_->stream_create_dedicated();
-  uint64_t largest = 0;
-  for (const Layer& l : d_.layers)
-    if (l.n_units) largest = std::max(largest, l.unit_bytes);
-  const int copy_streams = largest <= kSmallUnit ? 3 : 2;
-  for (int i = 1; i < copy_streams; ++i) {
+  for (int i = 1; i < kCopyStreams; ++i) {
     copyx_.push_back(dev_->stream_create_dedicated());
     joinx_ev_.push_back(dev_->event_create());
     vreadyx_ev_.push_back(dev_->event_create());

@@ -2,7 +2,8 @@
 // ss_acquire[_groups] / ss_group_wait / ss_release / ss_end). HostPlacement decides every placement; this executor
 // carries its orders out:
 //  - layer pools and the stream ring in HBM, the pinned tier and exclusive-mode spare blocks in hipHostMalloc memory;
-//  - a copy from a pinned block is issued at once on one of two or three SDMA copy streams (rotating per unit);
+//  - copies from pinned blocks are issued when the engine call that ordered them returns, on two SDMA copy streams
+//    (alternating per copy; neighbouring units into neighbouring slots go as one copy);
 //  - a copy from a file is a job for the reader threads: direct-I/O reads into pinned staging, host XXH64, then the
 //    copy stream;
 //  - exclusive-mode write-backs run on their own device-to-host stream;
@@ -231,10 +232,10 @@ class HostCtx final : public HostWork {
   std::unique_ptr<HipDevice> dev_;
   std::vector<std::unique_ptr<SourceFile>> files_;
   std::vector<LayerDev> L_;
-  // Pinned -> HBM copies rotate over copy_ and copyx_ (SDMA queues); other copies use copy_. Units of at most
-  // kSmallUnit bytes rotate over three queues, larger ones over two (measured: 9 MiB units 2 % faster per step on three
-  // than on two, 224 MiB units 2 % slower).
-  static constexpr uint64_t kSmallUnit = uint64_t(64) << 20;
+  // Pinned -> HBM copies rotate over copy_ and copyx_ (kCopyStreams SDMA queues); other copies use copy_. Measured
+  // with neighbouring units merged: three queues gain under 1 % on 9 MiB units and cost 2 % on 224 MiB blobs, and every
+  // extra queue slows the device checks beside it.
+  static constexpr int kCopyStreams = 2;
   hipStream_t copy_ = nullptr, wb_ = nullptr;
   std::vector<hipStream_t> copyx_;  // the other copy streams
   std::vector<hipEvent_t> joinx_ev_, vreadyx_ev_;  // per other copy stream: its mark at a join / at a check flush
