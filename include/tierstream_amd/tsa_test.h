@@ -20,6 +20,11 @@ SS_API ss_status tsa_test_region_of(const ss_ctx* c, uint64_t addr, int* kind, i
 SS_API ss_status tsa_test_dg_table(const ss_ctx* c, int32_t* out, uint32_t cap, uint32_t* n);
 /* verify_hash = 2: landed units whose device check failed, since open. */
 SS_API uint64_t tsa_test_verify_failures(const ss_ctx* c);
+/* Host contract test hooks under the reference's names (its src/capi.cpp:721-734; its tests declare them by hand):
+ * reader threads take no job while held (closing the context still ends them); wait until every read-ahead read of
+ * the open forward has ended (readers not held). */
+SS_API ss_status ss_test_hold_readers(ss_ctx* c, int hold);
+SS_API ss_status ss_test_ra_quiesce(ss_ctx* c);
 /* Host contract: unit copies from pinned blocks since open, and the host-to-device copies they were issued as (a run
  * of neighbouring units is one copy). SS_E_INVALID on a device-gated context. */
 SS_API ss_status tsa_test_host_copies(const ss_ctx* c, uint64_t* units, uint64_t* copies);

@@ -1,9 +1,10 @@
-"""Host contract error paths on the MI355X, against the reference CPU backend driven by the same calls (reference
-tests/test_runtime.cpp:216-256): a unit whose file bytes differ from the descriptor hash fails the acquire that needs it
-with SS_E_HASH (verify_hash = 1), the forward's end reports it again, and the next forward serves the healthy units; a
-stream ring too small for a layer's transient units is SS_E_CAPACITY naming the ring, not a hang, and the forward still
-ends cleanly. Both libraries see the same descriptor, plan tiers, budget and options; every status must be the
-reference's."""
+"""Host contract error paths and read-ahead states on the MI355X, against the reference CPU backend driven by the same
+calls (reference tests/test_runtime.cpp:216-256, tests/test_readahead.cpp:387-476): a unit whose file bytes differ from
+the descriptor hash fails the acquire that needs it with SS_E_HASH (verify_hash = 1), the forward's end reports it
+again, and the next forward serves the healthy units; a stream ring too small for a layer's transient units is
+SS_E_CAPACITY naming the ring, not a hang, and the forward still ends cleanly; read-ahead landings from reads that have
+ended and from reads held back (the reference's ss_test_hold_readers / ss_test_ra_quiesce hooks); a close with reads in
+flight. Both libraries see the same descriptor, plan tiers, budget and options; every status must be the reference's."""
 import ctypes as C
 import json
 
@@ -121,3 +122,125 @@ def test_ring_too_small_is_an_error_not_a_hang(tmp_path, gpu):
     ours, theirs = seen["ours"], seen["reference"]
     assert ours[0] == theirs[0] == [OK, OK, E_CAPACITY, OK], (ours, theirs)
     assert "ring" in ours[1] and "ring" in theirs[1], (ours[1], theirs[1])
+
+
+def _declare_hooks(L):
+    for name, args in (("ss_test_hold_readers", [vp, C.c_int]), ("ss_test_ra_quiesce", [vp]),
+                       ("ss_host_prefetch", [vp, C.c_int, C.POINTER(i32), C.c_int]), ("ss_check_unit", [vp, C.c_int, C.c_int]),
+                       ("ss_stats_reset", [vp])):
+        f = getattr(L, name)
+        f.restype = C.c_int
+        f.argtypes = args
+    L.ss_stats_exclusive_sized.restype = C.c_int
+    L.ss_stats_exclusive_sized.argtypes = [vp, C.POINTER(ss.SsExclusiveStats), C.c_uint32]
+    L.ss_stats_total.restype = C.c_int
+    L.ss_stats_total.argtypes = [vp, C.POINTER(ss.SsLayerStats)]
+    L.ss_stats_to_json.restype = C.c_int
+    L.ss_stats_to_json.argtypes = [vp, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]
+    L.ss_free.argtypes = [C.c_void_p]
+
+
+def _doc(L, c):
+    txt, n = C.c_void_p(), C.c_size_t()
+    assert L.ss_stats_to_json(c, C.byref(txt), C.byref(n)) == OK
+    out = json.loads(C.string_at(txt, n.value).decode())
+    L.ss_free(txt)
+    return out
+
+
+@pytest.mark.parametrize("excl", [1, 0])
+@pytest.mark.parametrize("reading", [0, 1])
+def test_read_ahead_lands_in_admitted_slots(excl, reading, tmp_path, gpu):
+    """Reference tests/test_readahead.cpp:410-476: two file-backed units asked for by ss_host_prefetch, then routed and
+    admitted into the layer's pool (evicting two residents), land from their read-ahead buffers, whether the reads
+    have ended (ss_test_ra_quiesce: Ready) or are still held back (ss_test_hold_readers: the landing waits for the
+    read). Exclusive: the landings go into the victims' slots after their write-backs; inclusive: the victims just
+    leave. Each unit's file bytes count once (its read), the landing copy nowhere; the evicted residents then come
+    back from their blocks (exclusive) or their file. Statuses, stats, the read-ahead object and the exclusive
+    counters must be the reference's."""
+    m = fixtures.write_model(tmp_path, 3, 8, [4 * KiB, 4 * KiB], top_k=2, seed=23, tiers="pinned|disk")
+    desc = m.desc_json()
+    tiers = [1] * 8 + [0, 0, 0, 0, 2, 2, 2, 2] + [1] * 8
+    bkw = dict(device_bytes=256 << 20, host_pinned_bytes=4 << 20, ring_slots=16, tier_mode=excl)
+    okw = dict(verify_hash=1, pin_planned=0, staging_bytes=64 * KiB, readahead_units=2)
+    seen = {}
+    for name, L, backend in _libs():
+        _declare_hooks(L)
+        r = _Run(L, backend, desc, tiers, bkw, okw)
+        try:
+            assert r.open_status == OK, (name, L.ss_last_error())
+            L.ss_stats_reset(r.c)
+            ids = np.array([5, 6], dtype=np.int32)
+            out = [L.ss_begin(r.c, None, 0)]
+            if reading:
+                out.append(L.ss_test_hold_readers(r.c, 1))
+            out.append(L.ss_host_prefetch(r.c, 1, ids.ctypes.data_as(C.POINTER(i32)), 2))
+            if not reading:
+                out.append(L.ss_test_ra_quiesce(r.c))
+            out.append(r.routes(1, [5, 6]))
+            if reading:
+                out.append(L.ss_test_hold_readers(r.c, 0))
+            a, v = r.acquire(1)
+            out += [a, L.ss_check_unit(r.c, 1, 5), L.ss_check_unit(r.c, 1, 6), L.ss_release(r.c, 1, None),
+                    L.ss_end(r.c)]
+            doc = _doc(L, r.c)
+            t = ss.SsLayerStats()
+            L.ss_stats_total(r.c, C.byref(t))
+            x = ss.SsExclusiveStats()
+            L.ss_stats_exclusive_sized(r.c, C.byref(x), C.sizeof(x))
+            first = (doc["readahead"], t.as_dict(), x.writebacks)
+            # 5 and 6 are resident now; the evicted residents come back
+            out += [L.ss_begin(r.c, None, 0), r.routes(1, [0, 1, 5, 6])]
+            a, v = r.acquire(1)
+            out += [a] + [L.ss_check_unit(r.c, 1, u) for u in (0, 1, 5, 6)] + [L.ss_release(r.c, 1, None),
+                                                                               L.ss_end(r.c)]
+            L.ss_stats_total(r.c, C.byref(t))
+            seen[name] = (out, first, t.as_dict())
+        finally:
+            r.close()
+    ours, theirs = seen["ours"], seen["reference"]
+    assert all(s == OK for s in ours[0]), ours[0]
+    assert ours[0] == theirs[0]
+    ra, tot1, wb = ours[1]
+    ub = m.unit_bytes
+    assert ra["landed"] == 2 and ra["unused"] == 0 and ra["bytes"] == 2 * ub, ra
+    assert tot1["bytes_disk"] == 2 * ub and tot1["admitted"] == 2 and tot1["bytes_pinned"] == 0, tot1
+    assert wb == (2 if excl else 0)
+    assert ours[2]["hits"] == 2 and ours[2]["bytes_disk"] == (2 if excl else 4) * ub, ours[2]
+    drop = ("wait_ns",)
+    assert {k: v for k, v in tot1.items() if k not in drop} == {k: v for k, v in theirs[1][1].items() if k not in drop}
+    assert ra == theirs[1][0] and wb == theirs[1][2]
+    assert {k: v for k, v in ours[2].items() if k not in drop} == {k: v for k, v in theirs[2].items() if k not in drop}
+
+
+def test_close_with_reads_in_flight(tmp_path, gpu):
+    """Reference tests/test_readahead.cpp:387-408: a context closed with read-ahead reads queued behind held readers
+    (no ss_end) closes cleanly; a new context on the same files then serves."""
+    m = fixtures.write_model(tmp_path, 4, 16, [4 * KiB, 4 * KiB], top_k=2, seed=29, tiers="pinned|disk")
+    desc = m.desc_json()
+    tiers = [1] * 16 + [2] * 48
+    bkw = dict(device_bytes=256 << 20, host_pinned_bytes=8 << 20, ring_slots=16)
+    okw = dict(verify_hash=1, staging_bytes=64 * KiB, readahead_units=2)
+    L = ss._declare()
+    _declare_hooks(L)
+    r = _Run(L, None, desc, tiers, bkw, okw)
+    try:
+        assert r.open_status == OK, L.ss_last_error()
+        assert L.ss_test_hold_readers(r.c, 1) == OK
+        assert L.ss_begin(r.c, None, 0) == OK
+        L.ss_host_prefetch_layer.restype = C.c_int
+        L.ss_host_prefetch_layer.argtypes = [vp, C.c_int]
+        assert L.ss_host_prefetch_layer(r.c, 3) == OK
+        assert L.ss_layer_all(r.c, 3) == OK
+        assert L.ss_test_hold_readers(r.c, 0) == OK
+    finally:
+        r.close()  # (the forward never ended)
+    r = _Run(L, None, desc, tiers, bkw, okw)
+    try:
+        assert r.open_status == OK
+        assert L.ss_begin(r.c, None, 0) == OK and r.routes(2, [1, 2]) == OK
+        a, _ = r.acquire(2)
+        assert a == OK and L.ss_check_unit(r.c, 2, 1) == OK and L.ss_check_unit(r.c, 2, 2) == OK
+        assert L.ss_release(r.c, 2, None) == OK and L.ss_end(r.c) == OK
+    finally:
+        r.close()

@@ -543,6 +543,18 @@ ss_status tsa_test_host_copies(const ss_ctx* c, uint64_t* units, uint64_t* copie
     c->host->copy_counts(units, copies);
   });
 }
+ss_status ss_test_hold_readers(ss_ctx* c, int hold) {
+  return guard([&] {
+    need(c != nullptr && c->host != nullptr, "ss_test_hold_readers: a host-contract context");
+    c->host->test_hold_readers(hold != 0);
+  });
+}
+ss_status ss_test_ra_quiesce(ss_ctx* c) {
+  return guard([&] {
+    need(c != nullptr && c->host != nullptr, "ss_test_ra_quiesce: a host-contract context");
+    c->host->test_ra_quiesce();
+  });
+}
 ss_status tsa_test_profile_enable(ss_ctx* c, int on) {
   return guard([&] {
     need(c != nullptr, "tsa_test_profile_enable: null context");

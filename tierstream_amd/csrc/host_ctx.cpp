@@ -529,7 +529,7 @@ void HostCtx::reader_loop() {
         return !demand_q_.empty() || (!ra_q_.empty() && ra_running_ < ra_cap) ||
                (!spec_q_.empty() && demand_running_ <= 1);
       };
-      q_cv_.wait(lk, [&] { return stop_ || runnable(); });
+      q_cv_.wait(lk, [&] { return stop_ || (!hold_ && runnable()); });
       if (stop_ && demand_q_.empty() && spec_q_.empty() && ra_q_.empty()) return;
       if (!demand_q_.empty()) {
         c = demand_q_.front();
@@ -571,6 +571,19 @@ void HostCtx::reader_loop() {
     if (c->ra) ra_read_ended(*c, state, st, what);  // (its landing first: the read counts as ended after it)
     else finish(*c, state, st, what);
   }
+}
+
+void HostCtx::test_hold_readers(bool hold) {
+  {
+    std::lock_guard<std::mutex> lk(q_mu_);
+    hold_ = hold;
+  }
+  q_cv_.notify_all();
+}
+
+void HostCtx::test_ra_quiesce() {
+  for (auto& e : ra_entries_)
+    if (e->producer) await_quiet(*e->producer);
 }
 
 size_t HostCtx::take_staging() {

@@ -79,6 +79,10 @@ class HostCtx final : public HostWork {
   bool poisoned() const { return poisoned_; }
   Region region_of(uint64_t addr) const;
   uint64_t verify_failures() const { return verify_fail_total_; }
+  // Test hooks: reader threads take no job while held (a stop still ends them); wait until every read-ahead read of
+  // the forward has ended (readers not held).
+  void test_hold_readers(bool hold);
+  void test_ra_quiesce();
   void copy_counts(uint64_t* units, uint64_t* copies) const {
     std::lock_guard<std::mutex> lk(copy_mu_);
     *units = pinned_units_;
@@ -279,6 +283,7 @@ class HostCtx final : public HostWork {
   bool ra_frozen_ = false;
   RaCounts ra_st_;                                    // since open or the last reset
   bool stop_ = false;
+  bool hold_ = false;  // test hook: readers take no job
   std::vector<std::thread> readers_;
 
   // verify_hash = 2
