@@ -244,3 +244,131 @@ def test_close_with_reads_in_flight(tmp_path, gpu):
         assert L.ss_release(r.c, 2, None) == OK and L.ss_end(r.c) == OK
     finally:
         r.close()
+
+
+def _declare_more(L):
+    for name, res, args in (("ss_seed", C.c_int, [vp, C.c_int, C.POINTER(i32), C.c_int]),
+                            ("ss_stats_layer", C.c_int, [vp, C.c_int, C.POINTER(ss.SsLayerStats)]),
+                            ("ss_prefetch", C.c_int, [vp, C.c_int, C.POINTER(i32), C.c_int, C.c_int]),
+                            ("ss_layer_all", C.c_int, [vp, C.c_int]),
+                            ("ss_release", C.c_int, [vp, C.c_int, vp])):
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+
+
+def _ids(*xs):
+    a = np.array(xs, dtype=np.int32)
+    return a, a.ctypes.data_as(C.POINTER(i32))
+
+
+def _streams():
+    import tierstream_amd as tsa
+    out = []
+    for _ in range(2):
+        s = C.c_void_p()
+        tsa.check(tsa.lib().tsa_stream_create(C.byref(s)))
+        out.append(s)
+    return out
+
+
+def test_call_order_errors(tmp_path, gpu):
+    """Reference tests/test_runtime.cpp:291-311: calls out of order are SS_E_INVALID and leave the context usable."""
+    m = fixtures.write_model(tmp_path, 3, 8, [4 * KiB, 4 * KiB], top_k=2, seed=31, tiers="pinned|disk")
+    tiers = [2] * 24
+    bkw = dict(device_bytes=256 << 20, host_pinned_bytes=0, ring_slots=8)
+    seen = {}
+    for name, L, backend in _libs():
+        _declare_more(L)
+        r = _Run(L, backend, m.desc_json(), tiers, bkw, dict(staging_bytes=64 * KiB))
+        try:
+            assert r.open_status == OK, (name, L.ss_last_error())
+            bad, p = _ids(99)
+            out = [r.acquire(1)[0], L.ss_begin(r.c, None, 0), L.ss_begin(r.c, None, 0), r.acquire(1)[0],
+                   L.ss_layer_routes(r.c, 1, p, 1), L.ss_layer_all(r.c, 2), r.acquire(2)[0], L.ss_end(r.c),
+                   L.ss_release(r.c, 2, None), L.ss_end(r.c), L.ss_release(r.c, 2, None)]
+            seen[name] = out
+        finally:
+            r.close()
+    E = 1  # SS_E_INVALID
+    assert seen["ours"] == seen["reference"] == [E, OK, E, E, E, OK, OK, E, OK, OK, E], seen
+
+
+def test_one_stream_per_forward_and_seed_rollback(tmp_path, gpu):
+    """Reference tests/test_runtime.cpp:313-357: a seed with an invalid id is refused whole; a seed whose unit fails
+    its hash is rolled back (SS_E_HASH) while the healthy one stays; a forward uses one engine stream (another one is
+    SS_E_INVALID), the next forward may use another; the rolled-back unit is read again and fails again, not served
+    as a hit on garbage."""
+    m, desc = _model(tmp_path, corrupt=(1, 3))
+    st = (m.unit_bytes + 255) // 256 * 256
+    tiers = [2] * 24
+    bkw = dict(device_bytes=256 << 20, host_pinned_bytes=0, ring_slots=4, dynamic_slots_per_layer=4)
+    okw = dict(verify_hash=1, pin_planned=0, staging_buffers=2, staging_bytes=1 << 20)
+    s1, s2 = _streams()
+    seen = {}
+    for name, L, backend in _libs():
+        _declare_more(L)
+        r = _Run(L, backend, desc, tiers, bkw, okw)
+        try:
+            assert r.open_status == OK, (name, L.ss_last_error())
+            mixed, pm = _ids(2, 99)
+            seed, ps = _ids(2, 3)
+            two, p2 = _ids(2)
+            three, p3 = _ids(3)
+            out = [L.ss_seed(r.c, 1, pm, 2), L.ss_seed(r.c, 1, ps, 2), L.ss_begin(r.c, None, 0),
+                   L.ss_layer_routes(r.c, 1, p2, 1)]
+            v = SsLayerView()
+            out.append(L.ss_acquire(r.c, 1, s1, C.byref(v)))
+            out.append(L.ss_check_unit(r.c, 1, 2) if name == "ours" else OK)
+            out += [L.ss_release(r.c, 1, s2), L.ss_release(r.c, 1, s1), L.ss_end(r.c), L.ss_begin(r.c, None, 0),
+                    L.ss_layer_routes(r.c, 1, p3, 1), L.ss_acquire(r.c, 1, s2, C.byref(v)), int(L.ss_end(r.c) != OK)]
+            s = ss.SsLayerStats()
+            L.ss_stats_layer(r.c, 1, C.byref(s))
+            seen[name] = (out, s.hits)
+        finally:
+            r.close()
+    import tierstream_amd as tsa
+    for x in (s1, s2):
+        tsa.lib().tsa_stream_destroy(x)
+    E = 1
+    assert seen["ours"] == seen["reference"], seen
+    assert seen["ours"] == ([E, E_HASH, OK, OK, OK, OK, E, OK, OK, OK, OK, E_HASH, 1], 1), seen
+
+
+def test_seed_and_prefetch_between_forwards(tmp_path, gpu):
+    """Reference tests/test_runtime.cpp:258-289: units seeded between forwards are hits (one group of two, both
+    resident before the forward); an idle CERTAIN prefetch of the next forward's layer 2 lands before its routes."""
+    m = fixtures.write_model(tmp_path, 3, 16, [4 * KiB, 4 * KiB], top_k=2, seed=37, tiers="pinned|disk")
+    tiers = [2] * 48
+    bkw = dict(device_bytes=256 << 20, host_pinned_bytes=0, ring_slots=4, dynamic_slots_per_layer=4)
+    okw = dict(pin_planned=0, staging_bytes=64 * KiB)
+    seen = {}
+    for name, L, backend in _libs():
+        _declare_more(L)
+        r = _Run(L, backend, m.desc_json(), tiers, bkw, okw)
+        try:
+            assert r.open_status == OK, (name, L.ss_last_error())
+            seed, ps = _ids(5, 9, 9)
+            nxt, pn = _ids(1, 6)
+            r1, p1 = _ids(5, 9)
+            out = [L.ss_seed(r.c, 1, ps, 3), L.ss_prefetch(r.c, 2, pn, 2, 0), L.ss_begin(r.c, None, 0),
+                   L.ss_layer_routes(r.c, 1, p1, 2)]
+            v = SsLayerView()
+            out.append(L.ss_acquire(r.c, 1, None, C.byref(v)))
+            out.append(v.groups[0].n_units)
+            out += [L.ss_release(r.c, 1, None), L.ss_layer_routes(r.c, 2, pn, 2), L.ss_acquire(r.c, 2, None, C.byref(v))]
+            if name == "ours":
+                out += [L.ss_check_unit(r.c, 2, 1), L.ss_check_unit(r.c, 2, 6)]
+            else:
+                out += [OK, OK]
+            out += [L.ss_release(r.c, 2, None), L.ss_end(r.c)]
+            stats = []
+            for layer in (1, 2):
+                s = ss.SsLayerStats()
+                L.ss_stats_layer(r.c, layer, C.byref(s))
+                stats.append({k: x for k, x in s.as_dict().items() if k != "wait_ns"})
+            seen[name] = (out, stats)
+        finally:
+            r.close()
+    assert seen["ours"] == seen["reference"], seen
+    assert seen["ours"][0] == [OK, OK, OK, OK, OK, 2, OK, OK, OK, OK, OK, OK, OK] and seen["ours"][1][0]["hits"] == 2
