@@ -372,3 +372,40 @@ def test_seed_and_prefetch_between_forwards(tmp_path, gpu):
             r.close()
     assert seen["ours"] == seen["reference"], seen
     assert seen["ours"][0] == [OK, OK, OK, OK, OK, 2, OK, OK, OK, OK, OK, OK, OK] and seen["ours"][1][0]["hits"] == 2
+
+
+def test_exclusive_evicted_then_routed_same_forward(tmp_path, gpu):
+    """Reference tests/test_exclusive.cpp:610-633: a CERTAIN prefetch of layer 1 evicts resident 0 (LRU, lowest id)
+    into a free block; the layer's routes then route 0, which is read back from the block its write-back of this same
+    forward targets - the copy must wait for that write-back (ss_check_unit: the device bytes equal the file's). Two
+    write-backs, no file bytes. rereads counts the read-back on this discrete device; the reference's unified CPU
+    backend never counts it."""
+    m = fixtures.write_model(tmp_path, 3, 8, [4 * KiB, 4 * KiB], top_k=2, seed=41, tiers="pinned|disk")
+    tiers = [1] * 8 + [0, 0, 0, 0, 1, 1, 1, 1] + [1] * 8
+    bkw = dict(device_bytes=256 << 20, host_pinned_bytes=4 << 20, ring_slots=4, tier_mode=1, host_spare_units=2)
+    okw = dict(verify_hash=1, pin_planned=0, staging_bytes=64 * KiB)
+    seen = {}
+    for name, L, backend in _libs():
+        _declare_more(L)
+        _declare_hooks(L)
+        r = _Run(L, backend, m.desc_json(), tiers, bkw, okw)
+        try:
+            assert r.open_status == OK, (name, L.ss_last_error())
+            pre, pp = _ids(5)
+            ids, pi = _ids(0, 5)
+            out = [L.ss_begin(r.c, None, 0), L.ss_prefetch(r.c, 1, pp, 1, 0), L.ss_layer_routes(r.c, 1, pi, 2)]
+            v = SsLayerView()
+            out.append(L.ss_acquire(r.c, 1, None, C.byref(v)))
+            out += [L.ss_check_unit(r.c, 1, 0), L.ss_check_unit(r.c, 1, 5), L.ss_release(r.c, 1, None), L.ss_end(r.c)]
+            x = ss.SsExclusiveStats()
+            L.ss_stats_exclusive_sized(r.c, C.byref(x), C.sizeof(x))
+            t = ss.SsLayerStats()
+            L.ss_stats_total(r.c, C.byref(t))
+            seen[name] = (out, x.writebacks, x.rereads, t.bytes_disk,
+                          {k: v for k, v in t.as_dict().items() if k != "wait_ns"})
+        finally:
+            r.close()
+    ours, theirs = seen["ours"], seen["reference"]
+    assert ours[0] == theirs[0] == [OK] * 8, (ours, theirs)
+    assert ours[1] == theirs[1] == 2 and ours[3] == theirs[3] == 0 and ours[4] == theirs[4], (ours, theirs)
+    assert theirs[2] == 0 and ours[2] == 1, (ours, theirs)
