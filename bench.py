@@ -48,14 +48,14 @@ HBM_PEAK_GBPS = 8000.0
 TICK_NS = 10.0  # wall_clock64 runs at 100 MHz on gfx950
 # HBM bytes one verify launch moves per unit it checks, keyed by unit bytes: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
 # on a launch of one unit of this shape (dg_verify_kernel through tsa_xxh64_verify_slots), each scaled by the
-# counter's reading for a copy kernel of known size (FETCH 2.0, WRITE 1.0): 347,205 KiB fetched, nothing written
-# (profiles/dg_verify_kernel_mixtral_unit_pmc.md).
-VERIFY_TRAFFIC_PER_UNIT = {352321536: 347205 * 1024}
+# counter's reading for a copy kernel of known size (FETCH 2.0, WRITE 1.0), 2 KiB checkpoint segments: 355,269.75 KiB
+# fetched, nothing written (profiles/dg_verify_kernel_mixtral_unit_pmc.md).
+VERIFY_TRAFFIC_PER_UNIT = {352321536: 363796224}
 # The host contract's verify_kernel: HBM bytes fetched per algorithmic byte hashed, keyed by unit bytes, from
 # rocprofv3 --pmc FETCH_SIZE over the bench's own timed steps (scaled as above): a full batch of 32 units fetches
-# 148,799.25 KiB x 2.0 = 304,740,864 B for 301,989,888 B of units, nothing written
+# 152,527.41 KiB x 2.0 = 312,376,128 B for 301,989,888 B of units (2 KiB checkpoint segments), nothing written
 # (profiles/verify_kernel_qwen3_host_pmc.md).
-HOST_VERIFY_TRAFFIC_RATIO: dict[int, float] = {9437184: 304740864 / 301989888}
+HOST_VERIFY_TRAFFIC_RATIO: dict[int, float] = {9437184: 312376128 / 301989888}
 
 
 def log(*a):
@@ -224,12 +224,9 @@ def measure_disk(path, w, n_layers, threads=4, seconds=4.0):
 
 
 def verify_seg_bytes(unit_bytes):
-    """The device check's checkpoint segment a context uses for this unit size: 8 KiB, halved down to 2 KiB while a
-    unit has fewer than 16,384 segments (the library's rule, tierstream_amd/csrc/dg_ctx.cpp verify_seg_bytes)."""
-    seg = 8192
-    while seg > 2048 and unit_bytes // seg < 16384:
-        seg //= 2
-    return seg
+    """The device check's checkpoint segment a context uses (the library's rule, tierstream_amd/csrc/dg_ctx.cpp
+    verify_seg_bytes): 2 KiB for every unit size."""
+    return 2048
 
 
 def measure_kernels(tsa, L, C, w, seg=None, reps=10):

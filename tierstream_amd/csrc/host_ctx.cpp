@@ -12,7 +12,7 @@ namespace tsa {
 namespace {
 
 constexpr uint64_t kHostAlign = 4096;
-constexpr uint64_t kSegBytes = 8 * 1024;  // device check checkpoints: 32 B per 8 KiB segment (0.4 % of a unit)
+constexpr uint64_t kSegBytes = 2 * 1024;  // device check checkpoints: 32 B per 2 KiB segment (1.6 % of a unit)
 constexpr size_t kCheckBatch = 32;         // landed units per device check launch
 
 uint64_t now_ns() {
