@@ -109,6 +109,33 @@ CASES = {
     "set-sched-big-parts": dict(layers=4, units=8, parts=[8 * MiB] * 3, n_res=12, dyn=1, spares=6, n_ids=2,
                                 tokens=16, sched={5: (0, 0), 10: (1, 1)}, keep=True),
 }
+
+
+def _random_case(seed):
+    """A device-gated configuration drawn around the cases above: layers, units, parts (small ones staged and
+    scattered, one part copied straight), batch size, residents, spare slots and blocks, clean copies, deferral,
+    routes, predictions and scored victims."""
+    rng = np.random.default_rng(900 + seed)
+    layers = int(rng.integers(2, 6))
+    units = int(rng.choice([8, 12, 16]))
+    parts = [[64 * KiB] * 3, [32 * KiB, 32 * KiB, 64 * KiB], [256 * KiB], [128 * KiB, 64 * KiB]][int(rng.integers(0, 4))]
+    n_ids = int(rng.integers(1, min(4, units // 2) + 1))
+    n_res = int(rng.integers(units // 2, layers * units // 2 + 1))
+    spares = 2 * n_ids + int(rng.integers(2, 9))
+    c = dict(layers=layers, units=units, parts=parts, n_res=n_res, dyn=int(rng.integers(1, 3)), spares=spares,
+             n_ids=n_ids, tokens=int(rng.integers(12, 21)), wb_defer=int(rng.integers(0, 2)),
+             zipf=bool(rng.integers(0, 2)), random=True)
+    if rng.integers(0, 3) == 0:
+        c["inclusive"] = spares // 2
+    if rng.integers(0, 3) == 0:
+        c["predict"] = int(rng.integers(1, 3))
+    if rng.integers(0, 4) == 0:
+        c["score"] = dict(policy=1)
+    return c
+
+
+for _s in range(48):
+    CASES[f"random-{_s}"] = _random_case(_s)
 SCORE_COUNTERS = ["score_fallbacks", "scored_victims", "score_layers", "score_candidates", "score_saturated"]
 PRED_COUNTERS = ["prefetched", "prefetch_used", "pred_invalid", "predicted", "predicted_true", "wb_cancelled"]
 
@@ -141,6 +168,7 @@ def _profile_cells(units, layers, seed=9):
 @pytest.mark.parametrize("name", list(CASES))
 def test_dg_matches_reference(name, tmp_path, gpu):
     c = dict(CASES[name])
+    rand = c.pop("random", False)  # (a drawn configuration: the coverage checks below need not hold)
     tokens = c.pop("tokens")
     zipf = c.pop("zipf", True)
     use_graph = c.pop("graph", True)
@@ -230,14 +258,14 @@ def test_dg_matches_reference(name, tmp_path, gpu):
                             assert int(esum[L, i]) == expect[(L, int(u))], (name, t, L, i, "early read")
                         else:
                             assert int(esum[L, i]) == 0, (name, t, L, i)
-        assert got["tokens"] == tokens and got["misses"] > 0
-        if early:
+        assert got["tokens"] == tokens and (rand or got["misses"] > 0)
+        if early and not rand:
             assert 0 < early_ready < early_total, (early_ready, early_total)
-        if score and score["policy"] == 1:
+        if score and score["policy"] == 1 and not rand:
             assert got["scored_victims"] > 0 and got["score_fallbacks"] == 0
         if score.get("profile"):
             assert got["score_saturated"] > 0
-        if predict:
+        if predict and not rand:
             assert got["prefetched"] > 0 and got["prefetch_used"] > 0 and got["pred_invalid"] > 0
         _check_stats_doc(ctx, want, tokens, policy=["lru", "scored", "auto"][policy],
                          prov="test fit" if score.get("profile") else None, publications=tokens + len(switch))
