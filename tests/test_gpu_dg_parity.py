@@ -440,6 +440,16 @@ def _landing_failed(ctx):
     return json.loads(ctx.stats_json())["device_gated"]["landing_failed"]
 
 
+# drawn combinations of the options below (every one opens in both libraries; the coverage checks at the end of the
+# test need not hold for them)
+RANDOM_THREE_TIER = [
+    (0, AUTO, None, 3, 0, 0, (1, 3, 4096, 0)), (0, 0, BIG_PARTS, 3, 0, 0, None), (1, 4, None, 3, 0, 0, None),
+    (1, AUTO, None, 2, 1, 1, None), (1, AUTO, None, 2, 2, 0, (4, 0, 4096, 4)), (1, 4, BIG_PARTS, 2, 1, 0, None),
+    (1, AUTO, None, 3, 0, 0, (4, 1, 1 << 20, 2)), (0, 4, None, 0, 0, 0, None), (0, 3, BIG_PARTS, 3, 2, 0, (3, 1, 1 << 20, 0)),
+    (1, 3, None, 3, 0, 0, (3, 1, 0, 0)), (0, 4, BIG_PARTS, 3, 0, 0, None), (1, 3, None, 2, 1, 0, (2, 2, 0xFFFFFFFF, 4)),
+    (1, 0, None, 2, 0, 0, None), (1, 4, BIG_PARTS, 3, 0, 0, (1, 0, 0, 1)), (0, 4, BIG_PARTS, 0, 0, 0, None)]
+
+
 # landings: (dg_landing_blocks, dg_landing_ttl, dg_landing_chunk, dg_landing_max_queued)
 @pytest.mark.parametrize("clean_evict,queue,parts,predict,bank_keep,adapt,landing",
                          [(0, 0, None, 0, 0, 0, None), (1, 0, None, 0, 0, 0, None), (0, 4, None, 0, 0, 0, None),
@@ -448,7 +458,8 @@ def _landing_failed(ctx):
                           (0, 3, BIG_PARTS, 0, 1, 0, None), (0, 4, None, 2, 1, 0, None),
                           (0, AUTO, BIG_PARTS, 0, 1, 1, None), (0, AUTO, None, 2, 0, 1, None),
                           (0, 4, None, 2, 0, 0, (4, 0, 0, 0)), (1, 3, BIG_PARTS, 2, 0, 0, (2, 2, 1 << 20, 2)),
-                          (0, AUTO, None, 2, 1, 0, (3, 1, 0xFFFFFFFF, 1)), (0, 4, None, 3, 2, 0, (1, 3, 4096, 4))])
+                          (0, AUTO, None, 2, 1, 0, (3, 1, 0xFFFFFFFF, 1)), (0, 4, None, 3, 2, 0, (1, 3, 4096, 4))]
+                         + RANDOM_THREE_TIER)
 def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, predict, bank_keep, adapt, landing):
     """Three tiers (dg_disk_tier): 12 of 32 units resident, 10 pinned, 10 read from the file on a miss through staging
     buffers. The plan's tiers are given explicitly (a planner spill to the file tier leaves no room for spare blocks,
@@ -464,6 +475,7 @@ def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, 
     the read pool's landing queue, and its demand copies it from there after the read's word on the device; the
     landings' placement counters equal the reference's, and the bytes landed are the reads issued less those the pool
     dropped (cancelled, cut short or failed)."""
+    rand = (clean_evict, queue, parts, predict, bank_keep, adapt, landing) in RANDOM_THREE_TIER
     parts = list(parts or (64 * KiB,) * 3)
     layers, units, n_ids, staging, dyn, spares = 4, 8, 2, 4, 1, 6
     n_land, ttl, chunk, max_queued = landing or (0, 0, 0, 0)
@@ -512,14 +524,14 @@ def test_three_tier_matches_reference(tmp_path, gpu, clean_evict, queue, parts, 
                 unread = got["landing_aborted_bytes"] + \
                     (got["landing_cancelled"] + _landing_failed(ctx)) * m.unit_bytes
                 assert got["landing_read_bytes"] + unread == want["landing_read_bytes"], (t, got, want)
-        assert got["disk_reads"] > 0 and (got["disk_drops"] + got["disk_discards"]) > 0, got
+        assert got["disk_reads"] > 0 and (rand or (got["disk_drops"] + got["disk_discards"]) > 0), got
         if n_land:
-            assert got["landing_issued"] > 0 and got["landing_promoted"] > 0, got
+            assert rand or (got["landing_issued"] > 0 and got["landing_promoted"] > 0), got
             dg = json.loads(ctx.stats_json())["device_gated"]
             assert dg["landing_blocks"] == n_land and dg["landing_ttl"] == ttl
             assert dg["landing_max_queued"] == (max_queued or 1)
             assert dg["landing_chunk"] == ("whole" if chunk == 0xFFFFFFFF else chunk or 4 << 20)
-        if bank_keep:
+        if bank_keep and not rand:
             assert got["bank_kept"] > 0, got
         resolved = 4 if queue == AUTO else max(queue, 1)
         assert got["disk_queue_resolved"] == resolved and 1 <= got["disk_max_in_flight"] <= resolved, got
