@@ -48,7 +48,6 @@ HostPlacement::HostPlacement(const Desc& d, const Plan& p, const ss_options& o) 
   L_.resize(d_.layers.size());
   if (excl_) {
     for (const SpareClass& c : p_.spares) class_bytes_.push_back(c.block_bytes);
-    free_.resize(class_bytes_.size());
     for (size_t L = 0; L < d_.layers.size(); ++L) {
       const Layer& l = d_.layers[L];
       if (!l.streamable || !l.n_units) continue;
@@ -60,10 +59,8 @@ HostPlacement::HostPlacement(const Desc& d, const Plan& p, const ss_options& o) 
             L_[L].cls;
     }
     for (size_t k = 0; k < p_.spares.size(); ++k) {
-      const int32_t first = int32_t(blocks_.size());
-      for (uint32_t i = 0; i < p_.spares[k].blocks; ++i) blocks_.push_back(BlockHome{-1, int32_t(k)});
-      for (int32_t b = int32_t(blocks_.size()); b-- > first;) free_[k].push_back(b);  // lowest on top
-      class_spares_.push_back(p_.spares[k].blocks);
+      spare_.add_class(int32_t(blocks_.size()), p_.spares[k].blocks);
+      blocks_.resize(blocks_.size() + p_.spares[k].blocks, BlockHome{-1, int32_t(k)});
       xst_.free_blocks += p_.spares[k].blocks;
     }
     xst_.min_free_blocks = xst_.free_blocks;
@@ -97,20 +94,13 @@ HostPlacement::HostPlacement(const Desc& d, const Plan& p, const ss_options& o) 
         break;  // (a layer's units are one size)
       }
     }
-  for (const RingClass& rc : p_.rings) {
-    if (!rc.slots) continue;
-    ring_cls_.push_back({rc.stride, uint32_t(ring_.size()), rc.slots});
-    ring_cursor_.push_back(0);
-    for (uint32_t i = 0; i < rc.slots; ++i) ring_.push_back(RingSlot{int32_t(ring_cls_.size() - 1)});
-  }
+  for (const RingClass& rc : p_.rings)
+    if (rc.slots) {
+      ring_cls_.push_back({rc.stride, ring_.size(), rc.slots});
+      ring_.add_class(rc.stride, rc.slots);
+    }
   fwd_.assign(d_.layers.size(), ss_layer_stats{});
   total_.assign(d_.layers.size(), ss_layer_stats{});
-}
-
-uint64_t HostPlacement::free_blocks_now() const {
-  uint64_t f = 0;
-  for (const auto& v : free_) f += v.size();
-  return f;
 }
 
 // ---- open and seeds -------------------------------------------------------------------------------------------------
@@ -191,130 +181,120 @@ FetchOrder HostPlacement::order_for(int layer, int unit, bool speculative) {
   return f;
 }
 
-void HostPlacement::fetch_pool(int layer, int unit, int32_t slot, bool speculative, int32_t after_writeback) {
-  LayerPlace& s = L_[size_t(layer)];
+// Every forward copy goes out through here: the unit's spot and job for this forward, the executor's copy, and its
+// bytes (a copy that lands from a read-ahead buffer has its file bytes counted when the read-ahead ends).
+void HostPlacement::issue(const FetchOrder& f) {
+  LayerPlace& s = L_[size_t(f.layer)];
+  s.spot[size_t(f.unit)] = f.dst;
+  s.job[size_t(f.unit)] = f.job;
+  if (w_->fetch(f)) return;
+  ss_layer_stats& st = fwd_[size_t(f.layer)];
+  (f.src_block >= 0 ? st.bytes_pinned : st.bytes_disk) += d_.layers[size_t(f.layer)].unit_bytes;
+}
+
+bool HostPlacement::stream(int layer, int unit, bool speculative) {
+  const int cls = ring_.class_for(d_.unit_stride(layer));
+  if (!ring_.has_free(cls)) return false;
   FetchOrder f = order_for(layer, unit, speculative);
-  f.job = new_job(layer, unit, speculative, true);
-  f.dst = DevSpot{DevSpot::kPool, slot};
-  f.after_release = layer;  // the pool slot's last reader is this layer in an earlier forward
-  f.after_writeback = after_writeback;
-  s.spot[size_t(unit)] = f.dst;
-  s.job[size_t(unit)] = f.job;
-  if (!w_->fetch(f))  // (a landing from a read-ahead buffer: its file bytes count when the read-ahead ends)
-    (f.src_block >= 0 ? fwd_[size_t(layer)].bytes_pinned : fwd_[size_t(layer)].bytes_disk) +=
-        d_.layers[size_t(layer)].unit_bytes;
+  f.job = new_job(layer, unit, speculative, false);
+  const RingPool::Grant g = ring_.grant(cls, layer, f.job);
+  f.dst = DevSpot{DevSpot::kRing, g.slot};
+  f.after_release = g.prev_reader;
+  issue(f);
+  return true;
 }
 
-// The next free ring slot of the layer's stride class, round robin from the class's cursor.
-bool HostPlacement::fetch_ring(int layer, int unit, bool speculative) {
-  const uint64_t stride = d_.unit_stride(layer);
-  size_t c = 0;
-  while (c < ring_cls_.size() && ring_cls_[c].stride != stride) ++c;
-  if (c == ring_cls_.size()) return false;
-  const RingClassInfo& rc = ring_cls_[c];
-  for (uint32_t k = 0; k < rc.count; ++k) {
-    const uint32_t pos = (ring_cursor_[c] + k) % rc.count;
-    RingSlot& r = ring_[rc.first + pos];
-    if (r.owner >= 0) continue;
-    ring_cursor_[c] = (pos + 1) % rc.count;
-    LayerPlace& s = L_[size_t(layer)];
-    FetchOrder f = order_for(layer, unit, speculative);
-    f.job = new_job(layer, unit, speculative, false);
-    f.dst = DevSpot{DevSpot::kRing, int32_t(rc.first + pos)};
-    f.after_release = r.last_reader;
-    r.owner = layer;
-    r.job = f.job;
-    s.spot[size_t(unit)] = f.dst;
-    s.job[size_t(unit)] = f.job;
-    if (!w_->fetch(f))
-      (f.src_block >= 0 ? fwd_[size_t(layer)].bytes_pinned : fwd_[size_t(layer)].bytes_disk) +=
-          d_.layers[size_t(layer)].unit_bytes;
-    return true;
-  }
-  return false;
+// No ring slot for now: the unit queues for one (kRing without a slot marks it placed), and its file read, if it has
+// one to make, need not wait for the slot.
+void HostPlacement::wait_for_ring(int layer, int unit) {
+  L_[size_t(layer)].spot[size_t(unit)] = DevSpot{DevSpot::kRing, -1};
+  line_.join(layer, unit);
+  ra_request(layer, unit, true);
 }
 
-// Units waiting for a ring slot, in layer order: a later layer never takes a slot before an earlier one's waiters.
-void HostPlacement::drain_waiting() {
-  for (size_t L = 0; L < L_.size(); ++L) {
-    std::vector<int32_t>& q = L_[L].waiting;
-    size_t k = 0;
-    while (k < q.size() && fetch_ring(int(L), q[k], false)) ++k;
-    q.erase(q.begin(), q.begin() + std::ptrdiff_t(k));
-    if (!q.empty()) return;
-  }
+void HostPlacement::serve_wait_line() {
+  line_.serve([this](int32_t layer, int32_t unit) { return stream(layer, unit, false); });
 }
 
-uint64_t HostPlacement::free_for_writeback(int layer, bool speculative) const {
+HostPlacement::VictimBudget HostPlacement::victim_budget(int layer, bool speculative) const {
+  VictimBudget b;
+  if (!excl_) return b;  // inclusive: a victim simply leaves its slot
   const int32_t cls = L_[size_t(layer)].cls;
-  if (cls < 0) return 0;
-  uint64_t f = free_[size_t(cls)].size();
-  if (speculative) {  // a guess leaves half of the class's spares to demands
-    const uint64_t reserve = (class_spares_[size_t(cls)] + 1) / 2;
-    f = f > reserve ? f - reserve : 0;
+  if (cls >= 0) {
+    // a speculative admission leaves half of the class's spares (rounded up) to demand admissions
+    const uint64_t keep = speculative ? (uint64_t(spare_.spares(cls)) + 1) / 2 : 0;
+    const uint64_t have = spare_.free(cls);
+    b.blocks = have > keep ? have - keep : 0;
   }
-  return f;
+  // one block per victim, except that a demand admission with exclusive_discard evicts as it needs (its victims past
+  // the blocks are dropped to their files); a layer without a block class evicts nothing
+  b.cap = cls < 0 ? 0 : (o_.exclusive_discard && !speculative) ? -1 : int(std::min<uint64_t>(b.blocks, INT32_MAX));
+  return b;
 }
 
-// Exclusive mode: one free block per victim; a demand admission with exclusive_discard is uncapped (victims past the
-// free blocks go to their files).
-int HostPlacement::eviction_cap(int layer, bool speculative) const {
-  if (!excl_) return -1;
-  if (L_[size_t(layer)].cls < 0) return 0;
-  if (o_.exclusive_discard && !speculative) return -1;
-  return int(std::min<uint64_t>(free_for_writeback(layer, speculative), uint64_t(INT32_MAX)));
+// Exclusive mode: the first victims (while the budget's blocks last) are written back into free blocks as one batch;
+// the rest are discarded to their files. Every victim was a resident, which owns no block.
+int32_t HostPlacement::write_back_victims(int layer, const Admission& a, const VictimBudget& b) {
+  const int32_t cls = L_[size_t(layer)].cls;
+  const size_t n = a.evicted.size();
+  if (cls < 0 || (n > b.blocks && !o_.exclusive_discard))
+    fail(SS_E_BACKEND, "exclusive: admission evicted past its victim budget (internal)");
+  for (int32_t u : a.evicted)
+    if (block_of_[size_t(d_.gidx(layer, u))] >= 0) fail(SS_E_BACKEND, "exclusive: a resident victim had a pinned block (internal)");
+  const size_t kept = size_t(std::min<uint64_t>(b.blocks, n));
+  xst_.discards += n - kept;
+  if (!kept) return -1;
+  WriteBackOrder w;
+  w.batch = wb_batches_++;
+  w.layer = layer;
+  w.units.assign(a.evicted.begin(), a.evicted.begin() + std::ptrdiff_t(kept));
+  w.slots.assign(a.evicted_slot.begin(), a.evicted_slot.begin() + std::ptrdiff_t(kept));
+  for (int32_t u : w.units) {
+    const size_t g = size_t(d_.gidx(layer, u));
+    const int32_t blk = spare_.take(cls);
+    block_of_[g] = blk;
+    w.blocks.push_back(blk);
+  }
+  xst_.writebacks += kept;
+  xst_.writeback_bytes += kept * d_.layers[size_t(layer)].unit_bytes;
+  w_->write_back(w);
+  // published after the order: a read of one of these blocks later in the forward waits for the batch
+  for (int32_t u : w.units) {
+    const int64_t g = d_.gidx(layer, u);
+    wb_batch_of_[size_t(g)] = w.batch;
+    wb_touched_.push_back(g);
+  }
+  return w.batch;
 }
 
-void HostPlacement::admit(int layer, const Admission& a, bool speculative) {
-  int32_t batch = -1;
-  size_t written = 0;
-  if (excl_ && !a.evicted.empty()) {
-    const int32_t cls = L_[size_t(layer)].cls;
-    const uint64_t room = free_for_writeback(layer, speculative);
-    if (cls < 0 || (!o_.exclusive_discard && room < a.evicted.size()))
-      fail(SS_E_BACKEND, "exclusive: more victims than free blocks (internal)");
-    written = size_t(std::min<uint64_t>(room, a.evicted.size()));
-    for (int32_t u : a.evicted)
-      if (block_of_[size_t(d_.gidx(layer, u))] >= 0)
-        fail(SS_E_BACKEND, "exclusive: a victim still owns a pinned block (internal)");
-    xst_.discards += a.evicted.size() - written;  // past the free blocks: its file is its only home now
-    if (written) {
-      WriteBackOrder w;
-      w.batch = batch = wb_batches_++;
-      w.layer = layer;
-      const uint64_t ub = d_.layers[size_t(layer)].unit_bytes;
-      for (size_t i = 0; i < written; ++i) {
-        const int64_t g = d_.gidx(layer, a.evicted[i]);
-        const int32_t b = free_[size_t(cls)].back();
-        free_[size_t(cls)].pop_back();
-        block_of_[size_t(g)] = b;
-        w.units.push_back(a.evicted[i]);
-        w.slots.push_back(a.evicted_slot[i]);
-        w.blocks.push_back(b);
-        ++xst_.writebacks;
-        xst_.writeback_bytes += ub;
-      }
-      w_->write_back(w);
-      for (size_t i = 0; i < written; ++i) {
-        const int64_t g = d_.gidx(layer, a.evicted[i]);
-        wb_batch_of_[size_t(g)] = batch;
-        wb_touched_.push_back(g);
-      }
-    }
+Admission HostPlacement::admit_units(int layer, const std::vector<int32_t>& units, const std::vector<char>& held,
+                                     bool speculative) {
+  const VictimBudget b = victim_budget(layer, speculative);
+  Admission a = L_[size_t(layer)].pool->admit(units, held, true, b.cap);
+  xst_.deferred += uint64_t(a.deferred);
+  const int32_t batch = excl_ && !a.evicted.empty() ? write_back_victims(layer, a, b) : -1;
+  // a copy into a slot whose victim went out in the batch waits for it; the written victims are the first ones
+  std::vector<int32_t> wb_slots;
+  if (batch >= 0) {
+    const size_t kept = size_t(std::min<uint64_t>(b.blocks, a.evicted.size()));
+    wb_slots.assign(a.evicted_slot.begin(), a.evicted_slot.begin() + std::ptrdiff_t(kept));
   }
   for (size_t k = 0; k < a.admitted.size(); ++k) {
-    int32_t after = -1;  // only a copy into a written-back victim's slot waits for the batch
-    for (size_t i = 0; batch >= 0 && i < written && after < 0; ++i)
-      if (a.evicted_slot[i] == a.admitted_slot[k]) after = batch;
-    fetch_pool(layer, a.admitted[k], a.admitted_slot[k], speculative, after);
+    FetchOrder f = order_for(layer, a.admitted[k], speculative);
+    f.job = new_job(layer, a.admitted[k], speculative, true);
+    f.dst = DevSpot{DevSpot::kPool, a.admitted_slot[k]};
+    f.after_release = layer;  // a pool slot's last reader is this layer, in an earlier forward
+    if (std::find(wb_slots.begin(), wb_slots.end(), a.admitted_slot[k]) != wb_slots.end()) f.after_writeback = batch;
+    issue(f);
   }
+  return a;
 }
 
 void HostPlacement::give_back_block(int layer, int unit) {
   const int64_t g = d_.gidx(layer, unit);
   const int32_t b = block_of_[size_t(g)];
   if (b < 0) return;
-  free_[size_t(L_[size_t(layer)].cls)].push_back(b);
+  spare_.give(L_[size_t(layer)].cls, b);
   block_of_[size_t(g)] = -1;
   ++xst_.promoted;
 }
@@ -329,13 +309,13 @@ void HostPlacement::open_forward() {
     std::fill(s.job.begin(), s.job.end(), -1);
     std::fill(s.spec_open.begin(), s.spec_open.end(), uint8_t(0));
     std::fill(s.uses.begin(), s.uses.end(), 0u);
+    std::fill(s.ra_asked.begin(), s.ra_asked.end(), uint8_t(0));
     s.routed.clear();
     s.hits.clear();
-    s.waiting.clear();
     s.groups.clear();
-    std::fill(s.ra_asked.begin(), s.ra_asked.end(), uint8_t(0));
     s.routes_in = s.acquired = s.released = s.skipped = false;
   }
+  line_.clear();
   std::fill(fwd_.begin(), fwd_.end(), ss_layer_stats{});
   fwd_open_ = true;
 }
@@ -344,9 +324,10 @@ void HostPlacement::begin(const uint32_t* rows, int n_layers) {
   require(!in_fwd_, SS_E_INVALID, "begin: the previous forward has not ended");
   require(!rows || n_layers == int(L_.size()), SS_E_INVALID, "begin: rows_per_layer needs one entry per layer");
   open_forward();
-  for (size_t L = 0; rows && L < L_.size(); ++L) L_[L].skipped = rows[L] == 0;
+  if (rows)
+    for (size_t L = 0; L < L_.size(); ++L) L_[L].skipped = rows[L] == 0;
   if (excl_) {
-    xst_.free_blocks = free_blocks_now();
+    xst_.free_blocks = spare_.total_free();
     xst_.min_free_blocks = std::min(xst_.min_free_blocks, xst_.free_blocks);
   }
   in_fwd_ = true;
@@ -365,98 +346,99 @@ void HostPlacement::routes_all(int layer) {
   take_routes(layer, all.data(), int(all.size()));
 }
 
-// One layer's routes: hits stay, units fetched earlier in the forward are claimed, the other misses ask the pool
-// for slots (evicting as it decides, write-backs first in exclusive mode) and the rest stream through the ring or
-// wait for a ring slot.
+HostPlacement::RouteSort HostPlacement::sort_routes(int layer) const {
+  const LayerPlace& s = L_[size_t(layer)];
+  const int n = d_.layers[size_t(layer)].n_units;
+  RouteSort r;
+  r.held.assign(size_t(n), 0);
+  for (int u = 0; u < n; ++u) {
+    const bool placed = s.spot[size_t(u)].kind != DevSpot::kNone;
+    const bool routed = s.uses[size_t(u)] && p_.tier[size_t(d_.gidx(layer, u))] != SS_TIER_PAIR;
+    r.held[size_t(u)] = char(placed || routed);
+    if (!routed) continue;
+    if (placed) r.claims.push_back(u);
+    else if (s.pool->slot(u) >= 0) r.hits.push_back(u);
+    else r.asks.push_back(u);
+  }
+  return r;
+}
+
+// One layer's routes: hits stay, units placed earlier in the forward are claimed, the others ask the pool for slots
+// (victims written back first in exclusive mode) and whatever the pool does not take streams through the ring or
+// waits for a ring slot.
 void HostPlacement::take_routes(int layer, const int32_t* ids, int n) {
   LayerPlace& s = layer_with_units(layer, "routes");
-  const Layer& l = d_.layers[size_t(layer)];
+  const int nu = d_.layers[size_t(layer)].n_units;
   require(!s.routes_in, SS_E_INVALID, "routes: already given for layer " + std::to_string(layer) + " in this forward");
   require(!s.skipped, SS_E_INVALID, "routes: layer " + std::to_string(layer) + " is skipped in this forward");
-  for (int i = 0; i < n; ++i)
-    require(ids[i] < l.n_units, SS_E_INVALID, "routes: unit id " + std::to_string(ids[i]) + " out of range");
+  const int32_t* bad = std::find_if(ids, ids + n, [nu](int32_t id) { return id >= nu; });
+  require(bad == ids + n, SS_E_INVALID, "routes: unit id " + std::to_string(bad == ids + n ? 0 : *bad) +
+                                            " out of range");
   s.routes_in = true;
   for (int i = 0; i < n; ++i)
-    if (ids[i] >= 0) ++s.uses[size_t(ids[i])];
+    if (ids[i] >= 0) ++s.uses[size_t(ids[i])];  // (negative ids are empty route entries)
+
+  RouteSort r = sort_routes(layer);
   ss_layer_stats& st = fwd_[size_t(layer)];
-  std::vector<char> busy(size_t(l.n_units), 0);
-  std::vector<int32_t> misses, ask;
-  for (int u = 0; u < l.n_units; ++u) {
-    const bool placed = s.spot[size_t(u)].kind != DevSpot::kNone;
-    busy[size_t(u)] = placed;
-    if (!s.uses[size_t(u)] || p_.tier[size_t(d_.gidx(layer, u))] == SS_TIER_PAIR) continue;
-    busy[size_t(u)] = 1;  // routed: never a victim of this layer's own misses
-    s.routed.push_back(u);
-    if (placed) {  // fetched earlier in this forward (a prefetch)
-      if (s.spec_open[size_t(u)]) {
-        s.spec_open[size_t(u)] = 0;
-        ++st.spec_used;
-        if (s.job[size_t(u)] >= 0) w_->promote(s.job[size_t(u)]);
-      } else {
-        ++st.prefetched;
-      }
-      misses.push_back(u);
-    } else if (s.pool->slot(u) >= 0) {
-      s.hits.push_back(u);
-    } else {
-      ask.push_back(u);
-      misses.push_back(u);
+  for (int32_t u : r.claims) {
+    if (!s.spec_open[size_t(u)]) {
+      ++st.prefetched;
+      continue;
     }
+    s.spec_open[size_t(u)] = 0;  // a guess that came true: its job turns into a demand
+    ++st.spec_used;
+    if (s.job[size_t(u)] >= 0) w_->promote(s.job[size_t(u)]);
   }
+  std::vector<int32_t> misses(r.claims.size() + r.asks.size());
+  std::merge(r.claims.begin(), r.claims.end(), r.asks.begin(), r.asks.end(), misses.begin());
+  s.hits = std::move(r.hits);
+  std::merge(misses.begin(), misses.end(), s.hits.begin(), s.hits.end(), std::back_inserter(s.routed));
   st.routed += s.routed.size();
   st.hits += s.hits.size();
-  const Admission a = s.pool->admit(ask, busy, true, eviction_cap(layer, false));
-  xst_.deferred += uint64_t(a.deferred);
-  admit(layer, a, false);
+
+  const Admission a = admit_units(layer, r.asks, r.held, false);
   for (int32_t u : a.transient)
-    if (!fetch_ring(layer, u, false)) {
-      s.waiting.push_back(u);
-      s.spot[size_t(u)] = DevSpot{DevSpot::kRing, -1};
-      ra_request(layer, u, true);  // its file read need not wait for the ring slot
-    }
+    if (!stream(layer, u, false)) wait_for_ring(layer, u);
   st.admitted += a.admitted.size();
   st.transient += a.transient.size();
   st.evicted += a.evicted.size();
   s.pool->observe(s.routed, misses);
 }
 
-// Prefetch before the layer's routes: CERTAIN admits like a demand; SPECULATIVE (at most lookahead_budget units) uses
-// the ring only (unless spec_persistent) and never waits for a ring slot.
+// Prefetch before the layer's routes, in the order asked: CERTAIN places a unit as a demand would (admission, else the
+// ring, else the wait line); SPECULATIVE places at most lookahead_budget units, in the ring only unless spec_persistent
+// (a guess never evicts otherwise), and stops at the first unit the ring cannot take (a guess never waits).
 void HostPlacement::prefetch(int layer, const int32_t* ids, int n, bool speculative) {
   require(ids || n <= 0, SS_E_INVALID, "prefetch: bad ids");
   open_forward();
   LayerPlace& s = layer_with_units(layer, "prefetch");
   if (s.routes_in || s.acquired) return;  // too late to help
-  const Layer& l = d_.layers[size_t(layer)];
+  const int nu = d_.layers[size_t(layer)].n_units;
   ss_layer_stats& st = fwd_[size_t(layer)];
-  std::vector<char> busy(size_t(l.n_units), 0);
-  for (int u = 0; u < l.n_units; ++u) busy[size_t(u)] = s.spot[size_t(u)].kind != DevSpot::kNone;
-  uint32_t issued = 0;
-  for (int i = 0; i < n; ++i) {
-    if (speculative && issued >= o_.lookahead_budget) break;
+  std::vector<char> held(static_cast<size_t>(nu), 0);
+  for (int u = 0; u < nu; ++u) held[size_t(u)] = char(s.spot[size_t(u)].kind != DevSpot::kNone);
+  const bool admits = !speculative || o_.spec_persistent;
+  const uint32_t budget = speculative ? o_.lookahead_budget : UINT32_MAX;
+  uint32_t placed = 0;
+  for (int i = 0; i < n && placed < budget; ++i) {
     const int32_t u = ids[i];
-    if (u < 0 || u >= l.n_units || busy[size_t(u)] || s.pool->slot(u) >= 0 ||
-        p_.tier[size_t(d_.gidx(layer, u))] == SS_TIER_PAIR)
-      continue;
-    const Admission a = speculative && !o_.spec_persistent
-                            ? Admission{}
-                            : s.pool->admit({u}, busy, true, eviction_cap(layer, speculative));
-    xst_.deferred += uint64_t(a.deferred);
+    const bool wanted = u >= 0 && u < nu && !held[size_t(u)] && s.pool->slot(u) < 0 &&
+                        p_.tier[size_t(d_.gidx(layer, u))] != SS_TIER_PAIR;
+    if (!wanted) continue;
+    // the admission's deferrals count even when it admitted nothing
+    const Admission a = admits ? admit_units(layer, {u}, held, speculative) : Admission{};
     if (!a.admitted.empty()) {
-      admit(layer, a, speculative);
       st.evicted += a.evicted.size();
-    } else if (!fetch_ring(layer, u, speculative)) {
-      if (speculative) break;
-      s.waiting.push_back(u);
-      s.spot[size_t(u)] = DevSpot{DevSpot::kRing, -1};
-      ra_request(layer, u, true);
+    } else if (!stream(layer, u, speculative)) {
+      if (speculative) return;
+      wait_for_ring(layer, u);
     }
-    busy[size_t(u)] = 1;
+    held[size_t(u)] = 1;
+    ++placed;
     if (speculative) {
       s.spec_open[size_t(u)] = 1;
       ++st.spec_issued;
     }
-    ++issued;
   }
 }
 
@@ -468,64 +450,76 @@ void HostPlacement::host_prefetch(int layer, const int32_t* ids, int n) {
   for (int i = 0; i < n; ++i) ra_request(layer, ids[i], false);
 }
 
-void HostPlacement::ra_request(int layer, int unit, bool pending_ok) {
-  if (!ra_on()) return;
+// kDevice: resident, or a copy of it already ordered this forward; kPinned: it has a pinned block; kPeer: a PAIR unit
+// (never fetched); kFile: only its file holds it.
+HostPlacement::Source HostPlacement::source_now(int layer, int unit) const {
+  const LayerPlace& s = L_[size_t(layer)];
+  const size_t g = size_t(d_.gidx(layer, unit));
+  if (p_.tier[g] == SS_TIER_PAIR) return Source::kPeer;
+  if (s.pool->slot(unit) >= 0 || s.job[size_t(unit)] >= 0) return Source::kDevice;
+  return block_of_[g] >= 0 ? Source::kPinned : Source::kFile;
+}
+
+bool HostPlacement::ra_wanted(int layer, int unit) const {
+  return L_[size_t(layer)].pool && source_now(layer, unit) == Source::kFile;
+}
+
+// Read-ahead is asked for at most once per unit and forward, for a streamable unit its file alone holds whose bytes
+// fit a buffer, and which is not placed this forward (or, waiting_ok, only waits for a ring slot).
+void HostPlacement::ra_request(int layer, int unit, bool waiting_ok) {
+  if (!ra_on() || layer < 0 || size_t(layer) >= L_.size()) return;
   LayerPlace& s = L_[size_t(layer)];
   const Layer& l = d_.layers[size_t(layer)];
   if (!s.pool || !l.streamable || unit < 0 || unit >= l.n_units || s.ra_asked[size_t(unit)]) return;
-  if (!ra_wanted(layer, unit) || host_stride(l.unit_bytes) > ra_bytes_) return;
-  const DevSpot& sp = s.spot[size_t(unit)];
-  if (sp.kind != DevSpot::kNone && !(pending_ok && sp.kind == DevSpot::kRing && sp.index < 0)) return;
+  const DevSpot& at = s.spot[size_t(unit)];
+  const bool free_to_read = at.kind == DevSpot::kNone || (waiting_ok && at.kind == DevSpot::kRing && at.index < 0);
+  if (!free_to_read || host_stride(l.unit_bytes) > ra_bytes_ || source_now(layer, unit) != Source::kFile) return;
   s.ra_asked[size_t(unit)] = 1;
   w_->read_ahead(layer, unit);
 }
 
-bool HostPlacement::ra_wanted(int layer, int unit) const {
-  const LayerPlace& s = L_[size_t(layer)];
-  const int64_t g = d_.gidx(layer, unit);
-  return s.pool && p_.tier[size_t(g)] != SS_TIER_PAIR && block_of_[size_t(g)] < 0 && s.pool->slot(unit) < 0 &&
-         s.job[size_t(unit)] < 0;
-}
-
 HostPlacement::Acquire HostPlacement::acquire(int layer, bool wait_all) {
   LayerPlace& s = layer_with_units(layer, "acquire");
-  drain_waiting();
-  require(s.waiting.empty(), SS_E_CAPACITY,
-          "acquire: the stream ring cannot take layer " + std::to_string(layer) + "'s " +
-              std::to_string(s.waiting.size()) + " remaining transient units (release earlier layers or plan more "
-              "ring slots)");
+  serve_wait_line();
+  const uint32_t left = line_.waiting(layer);
+  require(left == 0, SS_E_CAPACITY,
+          "acquire: the stream ring cannot take layer " + std::to_string(layer) + "'s " + std::to_string(left) +
+              " remaining transient units (release earlier layers or plan more ring slots)");
   Acquire r;
   r.wait_ready = s.ready_wait;
   s.ready_wait = false;
-  // groups: 0 = resident before this forward; then the fetched units, most routed first (route order on ties),
-  // group_units at a time, each group ascending
+  // group 0: the units resident before this forward; then the units fetched for it, most-routed first (lower id
+  // first among equals), group_units to a group (all in one without it), each group in id order
   std::vector<int32_t> fetched;
-  for (int32_t u : s.routed)
-    if (s.job[size_t(u)] >= 0) fetched.push_back(u);
-  std::stable_sort(fetched.begin(), fetched.end(),
-                   [&](int32_t a, int32_t b) { return s.uses[size_t(a)] > s.uses[size_t(b)]; });
+  std::copy_if(s.routed.begin(), s.routed.end(), std::back_inserter(fetched),
+               [&s](int32_t u) { return s.job[size_t(u)] >= 0; });
+  std::sort(fetched.begin(), fetched.end(), [&s](int32_t a, int32_t b) {
+    return s.uses[size_t(a)] != s.uses[size_t(b)] ? s.uses[size_t(a)] > s.uses[size_t(b)] : a < b;
+  });
   s.groups.assign(1, s.hits);
-  const size_t per = o_.group_units ? size_t(o_.group_units) : std::max<size_t>(fetched.size(), 1);
-  for (size_t k = 0; k < fetched.size(); k += per) {
-    std::vector<int32_t> g(fetched.begin() + std::ptrdiff_t(k),
-                           fetched.begin() + std::ptrdiff_t(std::min(fetched.size(), k + per)));
-    std::sort(g.begin(), g.end());
-    s.groups.push_back(std::move(g));
+  const size_t per = o_.group_units ? size_t(o_.group_units) : fetched.size();
+  for (auto it = fetched.begin(); it != fetched.end();) {
+    const auto stop = per && size_t(fetched.end() - it) > per ? it + std::ptrdiff_t(per) : fetched.end();
+    s.groups.emplace_back(it, stop);
+    std::sort(s.groups.back().begin(), s.groups.back().end());
+    it = stop;
   }
   if (wait_all)
     for (int32_t u : fetched) r.wait_jobs.push_back(s.job[size_t(u)]);
   return r;
 }
 
+// The layer's table: a unit fetched this forward appears where its copy went, if it was routed; any other unit
+// appears in its pool slot if it is resident.
 const std::vector<DevSpot>& HostPlacement::take_table(int layer) {
   LayerPlace& s = L_[size_t(layer)];
-  // every routed unit, and every resident not fetched this forward
   for (size_t u = 0; u < s.table.size(); ++u) {
-    DevSpot& t = s.table[u];
-    const bool present = s.job[u] >= 0 ? s.uses[u] != 0 : s.pool->slot(int(u)) >= 0;
-    if (!present) t = DevSpot{};
-    else if (s.spot[u].kind == DevSpot::kRing) t = s.spot[u];
-    else t = DevSpot{DevSpot::kPool, s.pool->slot(int(u))};
+    if (s.job[u] >= 0) {
+      s.table[u] = s.uses[u] ? s.spot[u] : DevSpot{};
+      continue;
+    }
+    const int slot = s.pool->slot(int(u));
+    s.table[u] = slot >= 0 ? DevSpot{DevSpot::kPool, slot} : DevSpot{};
   }
   s.acquired = true;
   return s.table;
@@ -542,18 +536,11 @@ std::vector<int32_t> HostPlacement::group_jobs(int layer, int group) const {
 void HostPlacement::release(int layer) {
   LayerPlace& s = L_[size_t(layer)];
   s.released = true;
-  for (size_t u = 0; u < s.spec_open.size(); ++u)
-    if (s.spec_open[u]) {
-      s.spec_open[u] = 0;
-      ++fwd_[size_t(layer)].spec_dropped;
-    }
-  for (RingSlot& r : ring_) {
-    if (r.owner != layer) continue;
-    w_->retire(r.job);
-    r.last_reader = layer;
-    r.owner = r.job = -1;
-  }
-  drain_waiting();
+  const auto open = std::count(s.spec_open.begin(), s.spec_open.end(), uint8_t(1));
+  fwd_[size_t(layer)].spec_dropped += uint64_t(open);  // guesses never routed
+  std::fill(s.spec_open.begin(), s.spec_open.end(), uint8_t(0));
+  ring_.release(layer, [this](int32_t job) { w_->retire(job); });
+  serve_wait_line();
 }
 
 HostPlacement::Ended HostPlacement::end() {
@@ -579,11 +566,12 @@ HostPlacement::Ended HostPlacement::end() {
       e.landed_layers.push_back(int(L));
     }
   }
-  for (RingSlot& r : ring_) r.owner = r.job = -1;
+  ring_.reset_holders();
+  line_.clear();
   if (excl_) {
     for (int64_t g : wb_touched_) wb_batch_of_[size_t(g)] = -1;
     wb_touched_.clear();
-    xst_.free_blocks = free_blocks_now();
+    xst_.free_blocks = spare_.total_free();
   }
   e.writeback_batches = uint32_t(wb_batches_);
   wb_batches_ = 0;

@@ -4,17 +4,20 @@
 // how a layer's units are grouped, and every counter. It decides; a HostWork carries each decision out on a device as
 // it is made (the MI355X executor in host_ctx.cpp, or nothing at all in the CPU placement tests).
 //
-// The decisions are the reference's host contract (src/stream_ctx.cpp: ingest_routes :1303-1355, prefetch :1401-1439,
-// acquire :1459-1521, release :1572-1590, end :1600-1709; slot admission in residency.hpp), so hit / miss / evict
-// sequences, ring slots, groups and the address tables are the reference's for the same call sequence. What is this
-// library's own is the split: placement is a pure state machine driven by the ss_* calls, so its tables can be
-// compared with the reference's on the CPU, and the executor only maps orders to copies, events and reads.
+// The rules are the reference's host contract (src/stream_ctx.cpp: routes :1303-1355, prefetch :1401-1439, acquire
+// :1459-1521, release :1572-1590, end :1600-1709; slot admission in residency.hpp), so hit / miss / evict sequences,
+// ring slots, groups and the address tables equal the reference's for the same call sequence. The structure is this
+// library's: placement is a pure state machine driven by the ss_* calls; a layer's routes are sorted into hits, claims
+// and asks in one pass; the ring, its wait line and the spare blocks are objects of their own (host_slots.hpp); each
+// admission computes its victim budget once and carries it through; and the read-ahead rules ask one question, where
+// a unit's bytes would come from now.
 #pragma once
 
 #include <cstdint>
 #include <memory>
 #include <vector>
 
+#include "host_slots.hpp"
 #include "model.hpp"
 #include "residency.hpp"
 
@@ -81,7 +84,7 @@ class HostPlacement {
     uint32_t first, count;
   };
   const std::vector<RingClassInfo>& ring_classes() const { return ring_cls_; }
-  uint32_t ring_slots() const { return uint32_t(ring_.size()); }
+  uint32_t ring_slots() const { return ring_.size(); }
   const std::vector<BlockHome>& blocks() const { return blocks_; }
   const std::vector<uint64_t>& block_class_bytes() const { return class_bytes_; }
   uint64_t block_count() const { return blocks_.size(); }
@@ -147,38 +150,50 @@ class HostPlacement {
     std::vector<int32_t> job;
     std::vector<uint8_t> spec_open;  // fetched speculatively and not routed (yet)
     std::vector<uint32_t> uses;      // occurrences in the routes
-    std::vector<int32_t> routed, hits, waiting;
+    std::vector<int32_t> routed, hits;  // this forward's routed units and its hits, ascending
     std::vector<std::vector<int32_t>> groups;
     std::vector<DevSpot> table;
     bool routes_in = false, acquired = false, released = false, skipped = false;
     bool ready_wait = false;  // across forwards: the next acquire waits for the pool copies of the last one
     std::vector<uint8_t> ra_asked;  // this forward: a read-ahead was requested (never twice)
   };
-  struct RingSlot {
-    int32_t cls = 0, owner = -1, job = -1;
-    int32_t last_reader = -1;  // the layer that released it last
-  };
   struct Job {
     int32_t layer, unit;
     bool speculative, pool;
   };
+  // A layer's routed units sorted in one pass: hits were resident before this forward, claims were placed earlier in
+  // it (a prefetch), asks need admission; held marks the units an admission must not evict (routed, or placed).
+  struct RouteSort {
+    std::vector<int32_t> hits, claims, asks;
+    std::vector<char> held;
+  };
+  // What one admission may evict: cap for SlotPool::admit (-1: none) and the blocks its victims may be written to.
+  struct VictimBudget {
+    int cap = -1;
+    uint64_t blocks = 0;
+  };
+  // Where a unit's bytes would come from if it were fetched now.
+  enum class Source { kDevice, kPinned, kFile, kPeer };
 
   void open_forward();
   LayerPlace& layer_with_units(int layer, const char* what);
   int32_t new_job(int layer, int unit, bool speculative, bool pool);
   FetchOrder order_for(int layer, int unit, bool speculative);
-  void fetch_pool(int layer, int unit, int32_t slot, bool speculative, int32_t after_writeback);
-  bool fetch_ring(int layer, int unit, bool speculative);
-  void admit(int layer, const Admission& a, bool speculative);  // write-backs, then the admitted units' copies
-  uint64_t free_for_writeback(int layer, bool speculative) const;
-  int eviction_cap(int layer, bool speculative) const;
+  void issue(const FetchOrder& f);  // records the copy's spot and job, hands it to the executor, counts its bytes
+  RouteSort sort_routes(int layer) const;
+  VictimBudget victim_budget(int layer, bool speculative) const;
+  // Admission of `units` into the layer's pool: victims leave for blocks (exclusive), the admitted units are copied.
+  Admission admit_units(int layer, const std::vector<int32_t>& units, const std::vector<char>& held, bool speculative);
+  int32_t write_back_victims(int layer, const Admission& a, const VictimBudget& b);  // its batch, -1: none
+  bool stream(int layer, int unit, bool speculative);  // a ring slot now (false: none free)
+  void wait_for_ring(int layer, int unit);
+  void serve_wait_line();
   void give_back_block(int layer, int unit);  // a promoted unit's block returns to its class's free list
-  void drain_waiting();
-  // A read-ahead request for a unit the forward will read from its file: not requested yet, not on the device, no
-  // copy of it yet (pending_ok: or only waiting for a ring slot), no pinned source, not a peer's.
-  void ra_request(int layer, int unit, bool pending_ok);
+  Source source_now(int layer, int unit) const;
+  // A read-ahead request for a unit the forward will read from its file (see ra_wanted); waiting_ok: also while it
+  // waits for a ring slot.
+  void ra_request(int layer, int unit, bool waiting_ok);
   void take_routes(int layer, const int32_t* ids, int n);
-  uint64_t free_blocks_now() const;
 
   const Desc& d_;
   const Plan& p_;
@@ -187,15 +202,14 @@ class HostPlacement {
   bool excl_ = false;
   std::vector<LayerPlace> L_;
   std::vector<RingClassInfo> ring_cls_;
-  std::vector<uint32_t> ring_cursor_;
-  std::vector<RingSlot> ring_;
+  RingPool ring_;
+  WaitLine line_;
   // pinned blocks: the units' homes, then the spares; block_of_[g] the block a unit's bytes are in (-1: its file)
   std::vector<BlockHome> blocks_;
   std::vector<uint64_t> class_bytes_;
-  std::vector<uint64_t> class_spares_;
   std::vector<int32_t> block_of_;
-  std::vector<std::vector<int32_t>> free_;  // per class, taken from the back
-  std::vector<int32_t> wb_batch_of_;        // per global unit: this forward's write-back batch into its block, -1
+  SpareBlocks spare_;
+  std::vector<int32_t> wb_batch_of_;  // per global unit: this forward's write-back batch into its block, -1
   std::vector<int64_t> wb_touched_;
   int32_t wb_batches_ = 0;
   std::vector<Job> jobs_;
