@@ -203,6 +203,7 @@ void HostCtx::init() {
     for (size_t L = 0; L < d_.layers.size(); ++L) ra_index_[L].assign(size_t(d_.layers[L].n_units), -1);
   }
 
+  reads_.set_readers(int(o_.reader_threads));
   for (uint32_t i = 0; i < o_.reader_threads; ++i) readers_.emplace_back([this] { reader_loop(); });
 
   // the pinned tier from the files, then the residents (from their pinned copies where they have one)
@@ -235,9 +236,8 @@ void HostCtx::init() {
 void HostCtx::cleanup() noexcept {
   {
     std::lock_guard<std::mutex> lk(q_mu_);
-    stop_ = true;
+    reads_.stop();
   }
-  q_cv_.notify_all();
   for (auto& t : readers_) t.join();
   readers_.clear();
   if (!dev_) return;
@@ -349,12 +349,7 @@ void HostCtx::promote(int32_t job) {
   const CopyPtr& c = jobs_[size_t(job)];
   std::lock_guard<std::mutex> lk(q_mu_);
   if (c->state.load() != Copy::kQueued || !c->speculative) return;
-  const auto it = std::find(spec_q_.begin(), spec_q_.end(), c);
-  if (it == spec_q_.end()) return;
-  spec_q_.erase(it);
-  demand_q_.push_front(c);  // a demand now: ahead of every other queued read
-  c->speculative = false;
-  q_cv_.notify_one();
+  if (reads_.raise(ReadClass::kGuess, c)) c->speculative = false;  // a demand now: ahead of every other queued read
 }
 
 void HostCtx::retire(int32_t job) {
@@ -385,11 +380,8 @@ void HostCtx::submit(const CopyPtr& c) {
     c->state.store(Copy::kDone);
     return;
   }
-  {
-    std::lock_guard<std::mutex> lk(q_mu_);
-    (c->speculative ? spec_q_ : demand_q_).push_back(c);
-  }
-  q_cv_.notify_all();
+  std::lock_guard<std::mutex> lk(q_mu_);
+  reads_.push(c->speculative ? ReadClass::kGuess : ReadClass::kDemand, c);
 }
 
 // Host memory (a pinned block, a read-ahead buffer) into c's destination on the next copy stream (an SDMA queue), in
@@ -495,12 +487,10 @@ void HostCtx::finish(Copy& c, int state, ss_status st, const std::string& what) 
     } catch (...) {
     }
     c.state.store(state);
-    if (c.demand_run) --demand_running_;
-    if (c.ra_run) --ra_running_;
-    c.demand_run = c.ra_run = false;
+    if (c.reading) reads_.ended(c.ran_as);
+    c.reading = false;
   }
   done_cv_.notify_all();
-  q_cv_.notify_all();
 }
 
 void HostCtx::await_quiet(Copy& c) {
@@ -513,72 +503,46 @@ void HostCtx::await(Copy& c) {
   if (c.state.load() == Copy::kFailed) fail(c.status, c.what);
 }
 
+// One reader thread: it starts whatever read the scheduler gives it, runs it outside the lock, and reports the
+// outcome (a read-ahead read through its request, which may have a landing waiting for it).
 void HostCtx::reader_loop() {
   try {
     dev_->bind();
-  } catch (...) {
+  } catch (...) {  // (a device that cannot be bound fails the first copy this thread issues)
   }
-  // demand reads first, then read-ahead reads on at most max(1, readers - 1) readers, then a speculative read while
-  // at most one demand read runs
-  const int ra_cap = std::max(1, int(o_.reader_threads) - 1);
   for (;;) {
     CopyPtr c;
     {
       std::unique_lock<std::mutex> lk(q_mu_);
-      auto runnable = [&] {
-        return !demand_q_.empty() || (!ra_q_.empty() && ra_running_ < ra_cap) ||
-               (!spec_q_.empty() && demand_running_ <= 1);
-      };
-      q_cv_.wait(lk, [&] { return stop_ || (!hold_ && runnable()); });
-      if (stop_ && demand_q_.empty() && spec_q_.empty() && ra_q_.empty()) return;
-      if (!demand_q_.empty()) {
-        c = demand_q_.front();
-        demand_q_.pop_front();
-        c->demand_run = true;
-        ++demand_running_;
-      } else if (!ra_q_.empty() && (ra_running_ < ra_cap || stop_)) {
-        c = ra_q_.front();
-        ra_q_.pop_front();
-        c->ra_run = true;
-        ++ra_running_;
-      } else if (!spec_q_.empty() && demand_running_ <= 1) {
-        c = spec_q_.front();
-        spec_q_.pop_front();
-      } else {
-        continue;
-      }
+      ReadClass cls;
+      if (!reads_.wait_next(lk, &c, &cls)) return;
       int queued = Copy::kQueued;
-      if (!c->state.compare_exchange_strong(queued, Copy::kRunning)) {  // cancelled while queued
-        if (c->demand_run) --demand_running_;
-        if (c->ra_run) --ra_running_;
-        c->demand_run = c->ra_run = false;
+      if (!c->state.compare_exchange_strong(queued, Copy::kRunning)) {  // cancelled while it queued: never read
+        reads_.ended(cls);
         done_cv_.notify_all();
         continue;
       }
+      c->reading = true;
+      c->ran_as = cls;
     }
-    int state = Copy::kDone;
-    ss_status st = SS_OK;
-    std::string what;
+    ReadOutcome r;
     try {
       read_file_unit(*c);
     } catch (const Error& e) {
-      state = Copy::kFailed, st = e.status(), what = e.what();
+      r = ReadOutcome{Copy::kFailed, e.status(), e.what()};
     } catch (const std::bad_alloc&) {
-      state = Copy::kFailed, st = SS_E_NOMEM, what = "out of host memory";
+      r = ReadOutcome{Copy::kFailed, SS_E_NOMEM, "out of host memory"};
     } catch (const std::exception& e) {
-      state = Copy::kFailed, st = SS_E_BACKEND, what = e.what();
+      r = ReadOutcome{Copy::kFailed, SS_E_BACKEND, e.what()};
     }
-    if (c->ra) ra_read_ended(*c, state, st, what);  // (its landing first: the read counts as ended after it)
-    else finish(*c, state, st, what);
+    if (c->ra) ra_read_ended(*c, r.state, r.status, r.what);  // (its landing first: the read counts as ended after)
+    else finish(*c, r.state, r.status, r.what);
   }
 }
 
 void HostCtx::test_hold_readers(bool hold) {
-  {
-    std::lock_guard<std::mutex> lk(q_mu_);
-    hold_ = hold;
-  }
-  q_cv_.notify_all();
+  std::lock_guard<std::mutex> lk(q_mu_);
+  reads_.hold(hold);
 }
 
 void HostCtx::test_ra_quiesce() {
@@ -616,58 +580,76 @@ void HostCtx::read_file_unit(Copy& c) {
   stage_to_device(c);
 }
 
-// A unit's file bytes into host memory at dst (direct I/O through staging where the range is not aligned), hashed on
-// the way; with device checks on, its checkpoints are kept in HBM once the digest certifies them.
+// The checkpoint states a host hash of (layer, unit) records for the device check: one set of four accumulators per
+// check segment, or none when device checks are off or the unit has no descriptor hash.
+std::vector<uint64_t> HostCtx::checkpoint_buffer(const Layer& l, bool hash) const {
+  if (!dverify_ || !hash) return {};
+  const uint64_t span = l.unit_bytes / 32 * 32;
+  return std::vector<uint64_t>(4 * std::max<uint64_t>(1, (span + seg_bytes_ - 1) / seg_bytes_), 0);
+}
+
+// Keeps a unit's checkpoints in HBM (the first time a host hash certified them; copy_mu_ held).
+void HostCtx::keep_checkpoints_locked(int64_t g, const std::vector<uint64_t>& states) {
+  if (checks_[size_t(g)].states_dev) return;
+  UnitCheck k;
+  k.n_states = states.size() / 4;
+  k.states_dev = static_cast<uint64_t*>(dev_->alloc_device(states.size() * 8, "check checkpoints"));
+  hip_check(hipMemcpy(k.states_dev, states.data(), states.size() * 8, hipMemcpyHostToDevice), "hipMemcpy");
+  checks_[size_t(g)] = k;
+}
+
+const SourceFile& HostCtx::part_source(int layer, int unit, const Part& part, uint64_t* off) const {
+  const SourceFile& f = *files_[size_t(part.source)];
+  *off = part.offset + uint64_t(unit) * part.stride;
+  require(*off + part.bytes <= f.size(), SS_E_IO,
+          "unit (" + std::to_string(layer) + ", " + std::to_string(unit) + ") part " + part.name +
+              " is past the end of its source");
+  return f;
+}
+
+// A unit's file bytes into host memory at dst, part after part. A part whose offset, length and destination suit the
+// file's alignment is read straight into dst and hashed there; any other part goes window by window through a staging
+// buffer (an aligned covering read), each window's piece hashed in the staging buffer while it is still in cache, then
+// copied out to dst. got (if given) counts the bytes read so far, also when a read fails part-way. With device checks
+// on, the checkpoints the hash recorded are kept in HBM once its digest matches the descriptor.
 void HostCtx::read_into_host(int layer, int unit, void* dst, bool hash, uint64_t* digest, uint64_t* got) {
   const Layer& l = d_.layers[size_t(layer)];
-  const int64_t g = gidx(layer, unit);
-  std::vector<uint64_t> states;
-  if (dverify_ && hash) states.assign(4 * std::max<uint64_t>(1, (l.unit_bytes / 32 * 32 + seg_bytes_ - 1) / seg_bytes_), 0);
+  std::vector<uint64_t> states = checkpoint_buffer(l, hash);
   CheckpointHasher h(l.unit_bytes, seg_bytes_, states.empty() ? nullptr : states.data());
   uint64_t pos = 0;
   for (const Part& part : l.parts) {
-    const SourceFile& f = *files_[size_t(part.source)];
+    uint64_t off = 0;
+    const SourceFile& f = part_source(layer, unit, part, &off);
     const uint64_t al = std::max<uint64_t>(d_.sources[size_t(part.source)].align, 512);
-    const uint64_t off = part.offset + uint64_t(unit) * part.stride;
     char* out = at(dst, pos);
-    require(off + part.bytes <= f.size(), SS_E_IO,
-            "unit (" + std::to_string(layer) + ", " + std::to_string(unit) + ") part " + part.name +
-                " is past the end of its source");
-    if (!f.direct() || (off % al == 0 && part.bytes % al == 0 && uintptr_t(out) % al == 0)) {
+    const bool straight = !f.direct() || (off % al == 0 && part.bytes % al == 0 && uintptr_t(out) % al == 0);
+    if (straight) {
       f.pread_all(out, part.bytes, off);
       if (got) *got += part.bytes;
+      if (hash) h.feed(out, part.bytes);
     } else {
       const uint64_t cap = (o_.staging_bytes - 2 * al) / al * al;
-      for (uint64_t done = 0; done < part.bytes;) {
-        const uint64_t len = std::min(cap, part.bytes - done);
-        const uint64_t a0 = (off + done) / al * al, lead = off + done - a0, a1 = round_up(off + done + len, al);
-        const size_t i = take_staging();
-        try {
-          ev_sync(staging_[i].ev);
-          require(f.pread_some(staging_[i].host, a1 - a0, a0) >= lead + len, SS_E_IO, "short read");
-          std::memcpy(out + done, at(staging_[i].host, lead), size_t(len));
-          if (got) *got += len;
-        } catch (...) {
-          give_staging(i);
-          throw;
-        }
-        give_staging(i);
-        done += len;
-      }
+      for_each_cover_window(off, part.bytes, al, cap, [&](const CoverWindow& w) {
+        struct Lease {  // the staging buffer goes back however the window ends
+          HostCtx& x;
+          size_t i;
+          ~Lease() { x.give_staging(i); }
+        } lease{*this, take_staging()};
+        char* buf = static_cast<char*>(staging_[lease.i].host);
+        ev_sync(staging_[lease.i].ev);  // its last copy out has completed
+        require(f.pread_some(buf, w.span, w.a0) >= w.lead + w.len, SS_E_IO,
+                "short read of " + f.path() + " at " + std::to_string(w.a0));
+        if (hash) h.feed(buf + w.lead, w.len);
+        std::memcpy(out + w.at, buf + w.lead, size_t(w.len));
+        if (got) *got += w.len;
+      });
     }
-    if (hash) h.feed(out, part.bytes);
     pos += part.bytes;
   }
   if (digest) *digest = h.digest();
   if (!states.empty() && h.digest() == l.hash[size_t(unit)]) {
     std::lock_guard<std::mutex> lk(copy_mu_);
-    if (!checks_[size_t(g)].states_dev) {
-      UnitCheck k;
-      k.n_states = states.size() / 4;
-      k.states_dev = static_cast<uint64_t*>(dev_->alloc_device(states.size() * 8, "check checkpoints"));
-      hip_check(hipMemcpy(k.states_dev, states.data(), states.size() * 8, hipMemcpyHostToDevice), "hipMemcpy");
-      checks_[size_t(g)] = k;
-    }
+    keep_checkpoints_locked(gidx(layer, unit), states);
   }
 }
 
@@ -676,56 +658,42 @@ void HostCtx::read_into_host(int layer, int unit, void* dst, bool hash, uint64_t
 void HostCtx::stage_to_device(Copy& c) {
   const Layer& l = d_.layers[size_t(c.layer)];
   const bool hash = o_.verify_hash && !l.hash.empty();
-  const int64_t g = gidx(c.layer, c.unit);
-  std::vector<uint64_t> states;
-  if (dverify_ && hash) states.assign(4 * std::max<uint64_t>(1, (l.unit_bytes / 32 * 32 + seg_bytes_ - 1) / seg_bytes_), 0);
+  std::vector<uint64_t> states = checkpoint_buffer(l, hash);
   CheckpointHasher h(l.unit_bytes, seg_bytes_, states.empty() ? nullptr : states.data());
   uint64_t pos = 0;
-  bool ordered = false;
+  bool ordered = false;  // the destination's waits go before its first piece
   for (const Part& part : l.parts) {
-    const SourceFile& f = *files_[size_t(part.source)];
+    uint64_t off = 0;
+    const SourceFile& f = part_source(c.layer, c.unit, part, &off);
     const uint64_t al = f.direct() ? std::max<uint64_t>(d_.sources[size_t(part.source)].align, 512) : 1;
-    const uint64_t off = part.offset + uint64_t(c.unit) * part.stride;
-    require(off + part.bytes <= f.size(), SS_E_IO,
-            "unit (" + std::to_string(c.layer) + ", " + std::to_string(c.unit) + ") part " + part.name +
-                " is past the end of its source");
     const uint64_t cap = (o_.staging_bytes - 2 * std::max<uint64_t>(al, kHostAlign)) / kHostAlign * kHostAlign;
-    for (uint64_t done = 0; done < part.bytes;) {
-      const uint64_t len = std::min(cap, part.bytes - done);
-      const uint64_t a0 = (off + done) / al * al, lead = off + done - a0, a1 = round_up(off + done + len, al);
-      const size_t i = take_staging();
-      try {
-        ev_sync(staging_[i].ev);  // its previous copy out has completed
-        require(f.pread_some(staging_[i].host, a1 - a0, a0) >= lead + len, SS_E_IO, "short read");
-        const char* src = at(staging_[i].host, lead);
-        if (hash) h.feed(src, len);
-        std::lock_guard<std::mutex> lk(copy_mu_);
-        if (!ordered) {
-          wait_slot_check(copy_, c.dst);
-          for (hipEvent_t e : c.after) stream_wait(copy_, e);
-          ordered = true;
-        }
-        copy_h2d(at(c.dst, pos + done), src, len, copy_);
-        ev_record(staging_[i].ev, copy_);
-      } catch (...) {
-        give_staging(i);
-        throw;
+    for_each_cover_window(off, part.bytes, al, cap, [&](const CoverWindow& w) {
+      struct Lease {  // the staging buffer goes back however the window ends
+        HostCtx& x;
+        size_t i;
+        ~Lease() { x.give_staging(i); }
+      } lease{*this, take_staging()};
+      Staging& st = staging_[lease.i];
+      ev_sync(st.ev);  // its last copy out has completed
+      require(f.pread_some(st.host, w.span, w.a0) >= w.lead + w.len, SS_E_IO,
+              "short read of " + f.path() + " at " + std::to_string(w.a0));
+      const char* piece = at(st.host, w.lead);
+      if (hash) h.feed(piece, w.len);
+      std::lock_guard<std::mutex> lk(copy_mu_);
+      if (!ordered) {
+        wait_slot_check(copy_, c.dst);
+        for (hipEvent_t e : c.after) stream_wait(copy_, e);
+        ordered = true;
       }
-      give_staging(i);
-      done += len;
-    }
+      copy_h2d(at(c.dst, pos + w.at), piece, w.len, copy_);
+      ev_record(st.ev, copy_);
+    });
     pos += part.bytes;
   }
   require(!hash || h.digest() == l.hash[size_t(c.unit)], SS_E_HASH,
           "unit (" + std::to_string(c.layer) + ", " + std::to_string(c.unit) + ") bytes differ from the descriptor hash");
   std::lock_guard<std::mutex> lk(copy_mu_);
-  if (!states.empty() && !checks_[size_t(g)].states_dev) {
-    UnitCheck k;
-    k.n_states = states.size() / 4;
-    k.states_dev = static_cast<uint64_t*>(dev_->alloc_device(states.size() * 8, "check checkpoints"));
-    hip_check(hipMemcpy(k.states_dev, states.data(), states.size() * 8, hipMemcpyHostToDevice), "hipMemcpy");
-    checks_[size_t(g)] = k;
-  }
+  if (!states.empty()) keep_checkpoints_locked(gidx(c.layer, c.unit), states);
   ev_record(c.done_ev, copy_);
   if (dverify_) verify_landed(c);
 }
@@ -777,10 +745,9 @@ void HostCtx::ra_pump() {
       p->dst = ra_buf_[size_t(e.buf)];
       e.producer = p;
       e.st = RaEntry::kReading;
-      ra_q_.push_back(p);
+      reads_.push(ReadClass::kAhead, p);
     }
     ra_wait_.pop_front();
-    q_cv_.notify_all();
   }
 }
 
@@ -802,8 +769,7 @@ void HostCtx::ra_abandon_locked(RaEntry& e) {
     case RaEntry::kReading: {
       int queued = Copy::kQueued;
       if (e.producer->state.compare_exchange_strong(queued, Copy::kCancelled)) {  // never started: no read at all
-        const auto it = std::find(ra_q_.begin(), ra_q_.end(), e.producer);
-        if (it != ra_q_.end()) ra_q_.erase(it);
+        reads_.remove(ReadClass::kAhead, e.producer);
         ra_give_buf_locked(e);
       }  // (running: its end gives the buffer back)
       e.st = RaEntry::kAbandoned;
@@ -834,11 +800,7 @@ bool HostCtx::ra_land(RaEntry& e, const CopyPtr& child) {
         e.st = RaEntry::kLanding;
         e.child = child;
         attached = true;
-        const auto it = std::find(ra_q_.begin(), ra_q_.end(), e.producer);
-        if (it != ra_q_.end()) {  // still queued: a demand waits behind it now
-          ra_q_.erase(it);
-          demand_q_.push_front(e.producer);
-        }
+        reads_.raise(ReadClass::kAhead, e.producer);  // still queued: a demand waits behind it now
         break;
       }
       case RaEntry::kFailed:
@@ -849,7 +811,6 @@ bool HostCtx::ra_land(RaEntry& e, const CopyPtr& child) {
     }
   }
   if (fallback) ++ra_st_.fallback;
-  if (attached) q_cv_.notify_all();
   if (issue) ra_issue_child(e, *child);
   return attached;
 }
@@ -1342,31 +1303,42 @@ void HostCtx::end() {
   if (fwd_failed_ != SS_OK) fail(fwd_failed_, fwd_error_);
 }
 
+// ss_check_unit (a test hook): the unit's bytes where this forward's table puts them must equal its file bytes and
+// hash to the descriptor's digest. The device bytes come back a part at a time and are compared as they arrive, so a
+// mismatch names the part and its first differing byte.
 void HostCtx::check_unit(int layer, int unit) {
   check_layer(layer, "check_unit");
   const Layer& l = d_.layers[size_t(layer)];
   require(place_.acquired(layer) && !place_.released(layer), SS_E_INVALID, "check_unit: layer not acquired");
   require(unit >= 0 && unit < l.n_units, SS_E_INVALID, "check_unit: unit out of range");
   const LayerDev& s = L_[size_t(layer)];
-  void* a = reinterpret_cast<void*>(uintptr_t(s.table_host[s.version][unit]));
-  require(a != nullptr, SS_E_INVALID, "check_unit: unit not available in this forward");
-  const int32_t j = place_.job_of(layer, unit);
-  if (j >= 0) {
+  const char* dev = reinterpret_cast<const char*>(uintptr_t(s.table_host[s.version][unit]));
+  require(dev != nullptr, SS_E_INVALID, "check_unit: unit not available in this forward");
+  if (const int32_t j = place_.job_of(layer, unit); j >= 0) {  // its copy, if this forward made one, has landed
     await(*jobs_[size_t(j)]);
     ev_sync(jobs_[size_t(j)]->done_ev);
   }
   sync_copies();
-  std::vector<char> got(size_t(l.unit_bytes));
-  std::vector<char> want(size_t(round_up(l.unit_bytes, kHostAlign)) + kHostAlign);
-  hip_check(hipMemcpy(got.data(), a, got.size(), hipMemcpyDeviceToHost), "hipMemcpy (check_unit)");
-  char* w = reinterpret_cast<char*>(round_up(uint64_t(reinterpret_cast<uintptr_t>(want.data())), kHostAlign));
-  read_into_host(layer, unit, w, false, nullptr);
-  require(std::memcmp(got.data(), w, got.size()) == 0, SS_E_HASH,
-          "check_unit: landed bytes of (" + std::to_string(layer) + ", " + std::to_string(unit) +
-              ") differ from the source");
-  require(l.hash.empty() || xxh64(got.data(), got.size()) == l.hash[size_t(unit)], SS_E_HASH,
-          "check_unit: landed bytes of (" + std::to_string(layer) + ", " + std::to_string(unit) +
-              ") differ from the descriptor hash");
+  std::vector<char> file_buf(size_t(round_up(l.unit_bytes, kHostAlign) + kHostAlign));
+  char* file = reinterpret_cast<char*>(round_up(uint64_t(uintptr_t(file_buf.data())), kHostAlign));
+  read_into_host(layer, unit, file, false, nullptr);
+  const std::string who = "(" + std::to_string(layer) + ", " + std::to_string(unit) + ")";
+  uint64_t biggest = 0;
+  for (const Part& part : l.parts) biggest = std::max(biggest, part.bytes);
+  std::vector<char> landed(static_cast<size_t>(biggest));
+  Xxh64 h;
+  uint64_t pos = 0;
+  for (const Part& part : l.parts) {
+    hip_check(hipMemcpy(landed.data(), dev + pos, size_t(part.bytes), hipMemcpyDeviceToHost), "hipMemcpy (check_unit)");
+    const auto diff = std::mismatch(landed.begin(), landed.begin() + std::ptrdiff_t(part.bytes), file + pos);
+    require(diff.first == landed.begin() + std::ptrdiff_t(part.bytes), SS_E_HASH,
+            "check_unit: landed bytes of " + who + " differ from the source (part " + part.name + ", byte " +
+                std::to_string(diff.first - landed.begin()) + ")");
+    h.update(landed.data(), size_t(part.bytes));
+    pos += part.bytes;
+  }
+  require(l.hash.empty() || h.digest() == l.hash[size_t(unit)], SS_E_HASH,
+          "check_unit: landed bytes of " + who + " differ from the descriptor hash");
 }
 
 Region HostCtx::region_of(uint64_t addr) const {

@@ -30,6 +30,7 @@
 #include "host_place.hpp"
 #include "json.hpp"
 #include "model.hpp"
+#include "read_sched.hpp"
 #include "source.hpp"
 #include "tierstream_amd/tsa.h"
 #include "tierstream_amd/tsa_test.h"
@@ -104,8 +105,9 @@ class HostCtx final : public HostWork {
   struct Copy {
     enum State : int { kQueued = 0, kRunning = 1, kDone = 2, kCancelled = 3, kFailed = 4 };
     int32_t layer = 0, unit = 0;
-    bool speculative = false, to_host = false, demand_run = false;
-    bool ra_run = false;        // running as a read-ahead read (counted against the read-ahead reader cap)
+    bool speculative = false, to_host = false;
+    bool reading = false;                   // a reader started it (its class counts it running until it ends)
+    ReadClass ran_as = ReadClass::kDemand;  // (reading) the class it was started from
     RaEntry* ra = nullptr;      // a read-ahead read: its request
     uint64_t bytes_read = 0;    // a read-ahead read: the file bytes it read
     void* dst = nullptr;
@@ -120,6 +122,11 @@ class HostCtx final : public HostWork {
     std::string what;
   };
   using CopyPtr = std::shared_ptr<Copy>;
+  struct ReadOutcome {
+    int state = Copy::kDone;
+    ss_status status = SS_OK;
+    std::string what;
+  };
   struct LayerDev {
     void* pool = nullptr;
     uint64_t stride = 0;
@@ -171,6 +178,9 @@ class HostCtx final : public HostWork {
   void read_file_unit(Copy& c);  // a reader thread: the unit's file bytes to its destination
   // got: + the file bytes read (null: not counted)
   void read_into_host(int layer, int unit, void* dst, bool hash, uint64_t* digest, uint64_t* got = nullptr);
+  std::vector<uint64_t> checkpoint_buffer(const Layer& l, bool hash) const;
+  void keep_checkpoints_locked(int64_t g, const std::vector<uint64_t>& states);
+  const SourceFile& part_source(int layer, int unit, const Part& part, uint64_t* off) const;
   void stage_to_device(Copy& c);
   void submit(const CopyPtr& c);
   void issue_copy(Copy& c, const void* src, hipEvent_t after_ev);  // host memory -> c.dst now (copy_mu_ taken)
@@ -268,11 +278,11 @@ class HostCtx final : public HostWork {
   std::condition_variable staging_cv_;
   mutable std::mutex copy_mu_;
 
-  // reader threads: demand reads first; a speculative read only while no demand waits and at most one runs
+  // reader threads and the reads they start (read_sched.hpp); q_mu_ guards the scheduler, copy states and read-ahead
+  // request states together
   std::mutex q_mu_;
-  std::condition_variable q_cv_, done_cv_;
-  std::deque<CopyPtr> demand_q_, spec_q_, ra_q_;
-  int demand_running_ = 0, ra_running_ = 0;
+  std::condition_variable done_cv_;
+  ReadScheduler<CopyPtr> reads_;
   // read-ahead buffers (pinned, one unit each) and this forward's requests
   std::vector<void*> ra_buf_;
   std::vector<hipEvent_t> ra_ev_;                     // per buffer: its last copy out
@@ -282,8 +292,6 @@ class HostCtx final : public HostWork {
   std::deque<RaEntry*> ra_wait_;                      // engine thread
   bool ra_frozen_ = false;
   RaCounts ra_st_;                                    // since open or the last reset
-  bool stop_ = false;
-  bool hold_ = false;  // test hook: readers take no job
   std::vector<std::thread> readers_;
 
   // verify_hash = 2
