@@ -146,6 +146,15 @@ SS_API ss_status tsa_test_dg_geometry(const char* desc_json, size_t len, const s
 SS_API ss_status tsa_test_copy_runs(const int32_t* layer, const int32_t* src_alloc, const int32_t* dst_alloc,
                                     const uint64_t* src, const uint64_t* dst, size_t n, uint64_t unit_bytes,
                                     uint64_t cap, uint32_t* run_of);
+/* The host contract's read scheduler alone, single-threaded: ops[3k .. 3k+2] = (op, class, id) with op 0 push,
+ * 1 raise (from class to the head of demand), 2 remove, 3 take (a reader asks for a read: taken[2j] = its id or -1,
+ * taken[2j+1] = its class or -1), 4 end (a read of class ended), 5 hold (id != 0) or release, 6 stop; classes
+ * 0 demand, 1 read-ahead, 2 speculative. *n_taken = the takes. No reference counterpart: it pins the executor's rule. */
+SS_API ss_status tsa_test_read_sched(const int32_t* ops, size_t n_ops, int readers, int32_t* taken, size_t* n_taken);
+/* The aligned windows covering [off, off + n) with reads aligned to al, at most cap bytes of the range each:
+ * windows[5k .. 5k+4] = (at, len, a0, span, lead). No reference counterpart. */
+SS_API ss_status tsa_test_cover_windows(uint64_t off, uint64_t n, uint64_t al, uint64_t cap, uint64_t* windows,
+                                        size_t max_w, size_t* n_w);
 /* The same loop (prefetch may be NULL); the exclusive-mode counters after the last forward. */
 SS_API ss_status tsa_test_hostplace_exclusive(const char* desc_json, size_t len, const ss_budget* budget,
                                               const ss_options* opt, int steps, const int32_t* routes,

@@ -7,6 +7,7 @@
 
 #include "common.hpp"
 #include "copy_runs.hpp"
+#include "read_sched.hpp"
 #include "host_place.hpp"
 #include "tierstream_amd/tsa_test.h"
 
@@ -99,6 +100,55 @@ ss_status tsa_test_copy_runs(const int32_t* layer, const int32_t* src_alloc, con
       for (size_t k = i; k < j; ++k) run_of[k] = run;
       i = j;
     }
+  });
+}
+
+ss_status tsa_test_read_sched(const int32_t* ops, size_t n_ops, int readers, int32_t* taken, size_t* n_taken) {
+  return tsa::guard([&] {
+    using namespace tsa;
+    require((n_ops == 0 || ops) && taken && n_taken, SS_E_INVALID, "tsa_test_read_sched: null argument");
+    ReadScheduler<int32_t> q;
+    q.set_readers(readers);
+    size_t out = 0;
+    for (size_t k = 0; k < n_ops; ++k) {
+      const int32_t op = ops[3 * k], cls = ops[3 * k + 1], id = ops[3 * k + 2];
+      require(cls >= 0 && cls < 3, SS_E_INVALID, "tsa_test_read_sched: class out of range");
+      const ReadClass c = ReadClass(cls);
+      switch (op) {
+        case 0: q.push(c, id); break;
+        case 1: q.raise(c, id); break;
+        case 2: q.remove(c, id); break;
+        case 3: {
+          int32_t got = -1;
+          ReadClass gc = ReadClass::kDemand;
+          const bool ok = q.try_next(&got, &gc);
+          taken[2 * out] = ok ? got : -1;
+          taken[2 * out + 1] = ok ? int32_t(gc) : -1;
+          ++out;
+          break;
+        }
+        case 4: q.ended(c); break;
+        case 5: q.hold(id != 0); break;
+        case 6: q.stop(); break;
+        default: fail(SS_E_INVALID, "tsa_test_read_sched: unknown op");
+      }
+    }
+    *n_taken = out;
+  });
+}
+
+ss_status tsa_test_cover_windows(uint64_t off, uint64_t n, uint64_t al, uint64_t cap, uint64_t* windows, size_t max_w,
+                                 size_t* n_w) {
+  return tsa::guard([&] {
+    using namespace tsa;
+    require(windows && n_w && al > 0 && cap >= al && cap % al == 0, SS_E_INVALID, "tsa_test_cover_windows: bad argument");
+    size_t k = 0;
+    for_each_cover_window(off, n, al, cap, [&](const CoverWindow& w) {
+      require(k < max_w, SS_E_CAPACITY, "tsa_test_cover_windows: too many windows");
+      uint64_t* o = windows + 5 * k++;
+      o[0] = w.at, o[1] = w.len, o[2] = w.a0, o[3] = w.span, o[4] = w.lead;
+    });
+    *n_w = k;
   });
 }
 

@@ -52,11 +52,12 @@ class ReadScheduler {
   // Blocks on lk (the queue mutex) until this reader may start a read, takes it and counts it running; false when the
   // scheduler is stopped and nothing is left to read.
   bool wait_next(std::unique_lock<std::mutex>& lk, T* out, ReadClass* cls) {
-    int c = -1;
-    cv_.wait(lk, [&] {
-      c = pick();
-      return c >= 0 || (stop_ && idle());
-    });
+    cv_.wait(lk, [&] { return pick() >= 0 || (stop_ && idle()); });
+    return try_next(out, cls);
+  }
+  // The read a reader may start now, if any (taken and counted running).
+  bool try_next(T* out, ReadClass* cls) {
+    const int c = pick();
     if (c < 0) return false;
     *out = std::move(q_[c].front());
     q_[c].pop_front();
