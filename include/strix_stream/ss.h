@@ -392,6 +392,11 @@ SS_API ss_status ss_dg_keep(ss_ctx* c, int g, const int32_t* ids, int n);
  * src/dg_ctx.cpp:580-592). dg_flush_ready has no effect on HIP, which submits work as it is enqueued. */
 #define SS_DG_SET_SCHED 1
 SS_API ss_status ss_dg_set_sched(ss_ctx* c, uint32_t wb_defer, uint32_t flush_ready);
+/* Three-tier clean eviction (ss_options.dg_clean_evict) between tokens: on = 0 or 1, from the next boundary's victims
+ * on; refused inside a token (SS_E_INVALID). Placement only: the same bytes (reference ss.h:1756-1760,
+ * src/capi.cpp:1024-1025). */
+#define SS_DG_CLEAN_EVICT 1
+SS_API ss_status ss_dg_set_clean_evict(ss_ctx* c, uint32_t on);
 /* dg_diag = 1: gated layer g's row of the last completed token, between tokens (reference ss.h:702-729). Host
  * microseconds: seen_us = from the previous layer's service end (layer 0: the previous token's) to its export flag
  * seen; demand_us = flag seen -> its misses' copies and ready enqueued; pred_wait_us = -> its prediction's flag seen;

@@ -25,6 +25,20 @@ SS_API uint64_t tsa_test_verify_failures(const ss_ctx* c);
  * the open forward has ended (readers not held). */
 SS_API ss_status ss_test_hold_readers(ss_ctx* c, int hold);
 SS_API ss_status ss_test_ra_quiesce(ss_ctx* c);
+/* One-shot fault injection in the host read-ahead path (reference src/capi.cpp:717-719, src/stream_ctx.cpp:508-1015):
+ * 1 queueing a read fails, 2 queueing a landing fails, 3 a landing's copy fails before it starts, 4 after its first
+ * piece (the buffer is quarantined), 5 a read fails, 8 a read fails after a part, 9 a read's bytes fail the hash.
+ * The reference's copy mutations 6, 7 and 10 (a copy that skips a wait) are refused with SS_E_UNSUPPORTED. */
+SS_API ss_status ss_test_inject(ss_ctx* c, int what);
+/* Exclusive tier mode, between forwards: every pinned block held exactly once (a unit off the device, or a free list),
+ * no write-back pending (reference src/capi.cpp:691-696, src/stream_ctx.cpp:1914-1938). SS_E_INVALID names the first
+ * broken rule; the context is not poisoned. */
+SS_API ss_status ss_test_check_exclusive(ss_ctx* c);
+/* Device-gated, for a context opened with dg_test_hooks = 1 (reference include/strix_stream/ss_test.h:19, :30,
+ * src/capi.cpp:898-921): the cache core's ownership invariants between tokens (SS_E_BACKEND names the first broken
+ * one, nothing is poisoned); stop the service thread (the next token fails closed and poisons the context). */
+SS_API ss_status ss_test_dg_check(ss_ctx* c);
+SS_API ss_status ss_test_dg_stop_service(ss_ctx* c);
 /* Host contract: unit copies from pinned blocks since open, and the host-to-device copies they were issued as (a run
  * of neighbouring units is one copy). SS_E_INVALID on a device-gated context. */
 SS_API ss_status tsa_test_host_copies(const ss_ctx* c, uint64_t* units, uint64_t* copies);

@@ -81,6 +81,9 @@ def lib() -> C.CDLL:
             "refdg_set_policy": (C.c_int, [vp, u32]),
             "refdg_set_keep": (C.c_int, [vp, C.POINTER(u32), u32]),
             "refdg_set_wb_defer": (C.c_int, [vp, u32]),
+            "refdg_table": (u32, [vp, C.POINTER(i32), u32]),
+            "refdg_set_budgets": (C.c_int, [vp, u32, u32, u32]),
+            "refdg_set_clean_evict": (C.c_int, [vp, u32]),
             "refdg_profile_check": (C.c_int, [C.c_char_p, u64, C.POINTER(u32), u32, C.c_char_p]),
             "refdg_score_identity": (C.c_int, [u32, C.POINTER(u32), C.POINTER(u32), C.POINTER(u64), C.POINTER(u64),
                                                C.c_char_p]),
@@ -326,6 +329,20 @@ class RefDg:
     def set_wb_defer(self, on):
         if lib().refdg_set_wb_defer(self.h, int(on)) != 0:
             raise RuntimeError("refdg_set_wb_defer failed")
+
+    def table(self) -> np.ndarray:
+        """The slot table now (after open: the seeded placement)."""
+        out = np.zeros(self.keys, dtype=np.int32)
+        lib().refdg_table(self.h, out.ctypes.data_as(C.POINTER(i32)), self.keys)
+        return out
+
+    def set_budgets(self, spare_target, per_layer, per_token):
+        if lib().refdg_set_budgets(self.h, spare_target, per_layer, per_token) != 0:
+            raise RuntimeError("refdg_set_budgets failed")
+
+    def set_clean_evict(self, on):
+        if lib().refdg_set_clean_evict(self.h, int(on)) != 0:
+            raise RuntimeError("refdg_set_clean_evict failed")
 
     def residency(self):
         L = lib()

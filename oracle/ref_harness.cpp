@@ -465,6 +465,37 @@ int refdg_set_wb_defer(void* h, uint32_t on) {
   }
 }
 
+// The slot table now (after open: the seeded placement, before any token).
+uint32_t refdg_table(void* h, int32_t* out, uint32_t cap) {
+  const auto& t = static_cast<RefDg*>(h)->core->table();
+  for (uint32_t i = 0; i < cap && i < t.size(); ++i) out[i] = t[i];
+  return uint32_t(t.size());
+}
+
+// ss_dg_set_budgets between tokens (the reference context: src/dg_ctx.cpp:892-899).
+int refdg_set_budgets(void* h, uint32_t spare_target, uint32_t per_layer, uint32_t per_token) {
+  try {
+    ts::DgCore& c = *static_cast<RefDg*>(h)->core;
+    c.set_spare_target(spare_target);
+    c.set_prefetch_budget(per_layer, per_token);
+    return 0;
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "refdg_set_budgets: %s\n", e.what());
+    return 1;
+  }
+}
+
+// ss_dg_set_clean_evict between tokens (the reference context: src/dg_ctx.cpp:595-605).
+int refdg_set_clean_evict(void* h, uint32_t on) {
+  try {
+    static_cast<RefDg*>(h)->core->set_clean_evict(on != 0);
+    return 0;
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "refdg_set_clean_evict: %s\n", e.what());
+    return 1;
+  }
+}
+
 void refdg_close(void* h) { delete static_cast<RefDg*>(h); }
 
 }  // extern "C"

@@ -49,6 +49,20 @@ def test_library_exports_every_declared_function(header):
     assert not missing, missing
 
 
+def test_reference_test_hooks_and_clean_evict_are_exported():
+    """The host and device-gated test hooks the reference's own tests link by name (reference
+    include/strix_stream/ss_test.h:14-28, src/capi.cpp:691-737, :898-921), and ss_dg_set_clean_evict (reference
+    include/strix_stream/ss.h:1760) with its ts_ name."""
+    import tierstream_amd
+    lib = tierstream_amd.lib()
+    names = ["ss_test_inject", "ss_test_check_exclusive", "ss_test_hold_readers", "ss_test_ra_quiesce",
+             "ss_test_dg_check", "ss_test_dg_stop_service", "ss_dg_set_clean_evict", "ts_dg_set_clean_evict"]
+    assert [n for n in names if not hasattr(lib, n)] == []
+    test_h = set(declared(ROOT / "include" / "tierstream_amd" / "tsa_test.h"))
+    assert {n for n in names[:6]} <= test_h
+    assert "ss_dg_set_clean_evict" in set(declared(ROOT / "include" / "strix_stream" / "ss.h"))
+
+
 def test_minimum_export_set_of_the_serve_path():
     """Every function of the reference header's serve-path sections (tests/golden/min_exports.json: descriptor, plan,
     defaults, context and forward, stats, device-gated calls) is declared in ss.h and exported, under its ss_ and its

@@ -482,6 +482,9 @@ ss_status ss_dg_keep(ss_ctx* c, int g, const int32_t* ids, int n) {
 ss_status ss_dg_set_sched(ss_ctx* c, uint32_t wb_defer, uint32_t flush_ready) {
   return ctx_guard(c, [&] { dg_of(c, "ss_dg_set_sched").set_sched(wb_defer, flush_ready); });
 }
+ss_status ss_dg_set_clean_evict(ss_ctx* c, uint32_t on) {
+  return ctx_guard(c, [&] { dg_of(c, "ss_dg_set_clean_evict").set_clean_evict(on); });
+}
 ss_status ss_dg_timeline_sized(const ss_ctx* c, int g, ss_dg_layer_timeline* out, uint32_t size) {
   return guard([&] {
     need(c && out && size >= sizeof(uint32_t), "ss_dg_timeline: bad argument");
@@ -554,6 +557,24 @@ ss_status ss_test_ra_quiesce(ss_ctx* c) {
     need(c != nullptr && c->host != nullptr, "ss_test_ra_quiesce: a host-contract context");
     c->host->test_ra_quiesce();
   });
+}
+ss_status ss_test_inject(ss_ctx* c, int what) {
+  return ctx_guard(c, [&] { host_of(c, "ss_test_inject").test_inject(what); });
+}
+ss_status ss_test_check_exclusive(ss_ctx* c) {
+  return guard([&] {  // a broken rule is reported (SS_E_INVALID) and poisons nothing
+    need(c != nullptr, "ss_test_check_exclusive: null context");
+    host_of(c, "ss_test_check_exclusive").check_exclusive();
+  });
+}
+ss_status ss_test_dg_check(ss_ctx* c) {
+  return guard([&] {  // a broken invariant is reported (SS_E_BACKEND) and poisons nothing
+    need(c != nullptr, "ss_test_dg_check: null context");
+    dg_of(c, "ss_test_dg_check").test_check();
+  });
+}
+ss_status ss_test_dg_stop_service(ss_ctx* c) {
+  return ctx_guard(c, [&] { dg_of(c, "ss_test_dg_stop_service").test_stop_service(); });
 }
 ss_status tsa_test_profile_enable(ss_ctx* c, int on) {
   return guard([&] {

@@ -262,6 +262,7 @@ class DgCore {
   bool wb_defer() const { return c_.wb_defer; }
   void quiesce();  // between tokens: every queued write-back submitted, every stream synchronized
   void set_spare_target(uint32_t n);
+  void set_clean_evict(bool on) { c_.clean_evict = on; }  // (only a file tier has a victim to drop to its file)
   void set_prefetch_budget(uint32_t per_layer, uint32_t per_token);
   uint32_t spare_target() const { return c_.spare_target; }
   void audit() const;  // ownership invariants (tests); throws SS_E_BACKEND naming the first broken rule

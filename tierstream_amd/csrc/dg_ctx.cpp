@@ -20,6 +20,7 @@
 #include "depth_ctl.hpp"
 #include "dg_geometry.hpp"
 #include "dg_proto.hpp"
+#include "dg_service.hpp"
 #include "hip_rt.hpp"
 #include "read_pool.hpp"
 #include "score_profile.hpp"
@@ -762,233 +763,6 @@ class HipTransport final : public DgTransport {
   size_t vev_used_ = 0;
 };
 
-// ---- the service thread ----------------------------------------------------------------------------------------------
-struct ServiceStop {};
-
-class Service {
- public:
-  enum State : uint32_t { kIdle = 0, kServed = 1, kFailed = 2, kStopped = 3 };
-  Service(DgCore* core, const DgMappedHost& m, uint32_t max_ids, uint32_t timeout_ms, int device)
-      : core_(core), m_(m), max_ids_(max_ids), timeout_(std::chrono::milliseconds(timeout_ms)), device_(device) {
-    run_.assign(core_->gated(), 1);
-    run_next_.assign(core_->gated(), 1);
-    last_flag_.assign(core_->gated(), 0);
-    ids_.reserve(kDgMaxIds);
-    pred_.reserve(kDgMaxIds);
-  }
-  ~Service() { stop_join(); }
-  // dg_diag: one gated layer's row of the last token served (host times in microseconds; the counters' deltas)
-  struct Row {
-    double seen_us = 0, demand_us = 0, pred_wait_us = 0, prefetch_us = 0, serve_us = 0;
-    uint32_t ids = 0, misses = 0, covered = 0, fetched = 0, prefetched = 0, predicted_true = 0, covered_waits = 0;
-  };
-  void enable_timeline() {
-    diag_ = true;
-    rows_.assign(core_->gated(), Row{});
-  }
-  // Between tokens only (after the token's terminal word, which orders the rows' writes before it).
-  const std::vector<Row>& timeline() const { return rows_; }
-  void start() {
-    const uint32_t seen = host_seq_.load(std::memory_order_acquire);
-    t_served_ = Clock::now();  // the first token's seen_us of its first layer counts from here
-    th_ = std::thread([this, seen] { run(seen); });
-  }
-  void begin(uint32_t seq, const std::vector<uint8_t>& run) {
-    std::copy(run.begin(), run.end(), run_next_.begin());
-    host_seq_.store(seq, std::memory_order_release);
-  }
-  State wait_terminal(uint32_t seq, Clock::time_point deadline) {
-    for (uint32_t spins = 0;; ++spins) {
-      const uint64_t t = term_.load(std::memory_order_acquire);
-      const State s = State(t >> 32);
-      if (s == kFailed || s == kStopped) return s;
-      if (s == kServed && uint32_t(t) == seq) return kServed;
-      if ((spins & 1023u) == 0 && Clock::now() > deadline) return kIdle;
-      _mm_pause();
-    }
-  }
-  void stop_join() {
-    stop_.store(true, std::memory_order_release);
-    if (m_.host_abort) store_release(m_.host_abort, 1);
-    if (th_.joinable()) th_.join();
-  }
-  std::string error() const {
-    std::lock_guard<std::mutex> lk(mu_);
-    return err_;
-  }
-
- private:
-  void publish(State s, uint32_t seq) { term_.store(uint64_t(s) << 32 | seq, std::memory_order_release); }
-  void fail_with(const std::string& msg) {
-    {
-      std::lock_guard<std::mutex> lk(mu_);
-      if (err_.empty()) err_ = msg;
-    }
-    if (m_.host_abort) store_release(m_.host_abort, 1);  // every later wait of the token sees it
-  }
-  void wait_word(const uint32_t* w, uint32_t seq, const char* what, uint32_t g, bool strict, uint32_t last) {
-    const auto start = Clock::now();
-    for (uint32_t spins = 0;; ++spins) {
-      const uint32_t v = load_acquire(w);
-      if (v == seq) return;
-      if (strict && v != last)
-        fail(SS_E_BACKEND, std::string("device-gated: sequence desync: ") + what + " of gated layer " +
-                               std::to_string(g) + " holds " + std::to_string(v) + " while serving token " +
-                               std::to_string(seq));
-      if ((spins & 4095u) == 0) {
-        if (stop_.load(std::memory_order_acquire)) throw ServiceStop{};
-        if (Clock::now() - start > timeout_)
-          fail(SS_E_BACKEND, std::string("device-gated: ") + what + " of gated layer " + std::to_string(g) +
-                                 " never came (token " + std::to_string(seq) + ")");
-      }
-      _mm_pause();
-    }
-  }
-  void wait_began(uint32_t seq) {
-    for (uint32_t spins = 0;; ++spins) {
-      const uint32_t v = load_acquire(m_.began);
-      if (v == seq) return;
-      if (int32_t(v - seq) > 0)
-        fail(SS_E_BACKEND, "device-gated: sequence desync: a gated step began with seq " + std::to_string(v) +
-                               " while serving token " + std::to_string(seq) + " (a step ran outside ss_begin / ss_end)");
-      if ((spins & 1023u) == 0) {
-        if (stop_.load(std::memory_order_acquire)) throw ServiceStop{};
-        if (load_acquire(m_.host_abort)) throw ServiceStop{};
-      }
-      if (spins < 20000) _mm_pause();
-      else std::this_thread::yield();
-    }
-  }
-  void run(uint32_t seen) {
-    try {
-      hip_check(hipSetDevice(device_), "hipSetDevice (service)");
-    } catch (const std::exception& e) {
-      fail_with(e.what());
-      publish(kFailed, 0);
-      return;
-    }
-    for (;;) {
-      uint32_t seq = 0;
-      for (uint32_t spins = 0;; ++spins) {
-        seq = host_seq_.load(std::memory_order_acquire);
-        if (seq != seen) break;
-        if (stop_.load(std::memory_order_acquire)) {
-          publish(kStopped, seen);
-          return;
-        }
-        if (spins < 20000) _mm_pause();
-        else std::this_thread::yield();
-      }
-      seen = seq;
-      try {
-        serve_token(seq);
-      } catch (const ServiceStop&) {
-        publish(kStopped, seq);
-        return;
-      } catch (const std::exception& e) {
-        fail_with(e.what());
-        publish(kFailed, seq);
-        return;
-      }
-      publish(kServed, seq);
-    }
-  }
-  static double us_between(Clock::time_point a, Clock::time_point b) {
-    return double(std::chrono::duration_cast<std::chrono::nanoseconds>(b - a).count()) / 1e3;
-  }
-  void serve_token(uint32_t seq) {
-    const uint32_t G = core_->gated();
-    std::copy(run_next_.begin(), run_next_.end(), run_.begin());
-    if (diag_) std::fill(rows_.begin(), rows_.end(), Row{});  // (a failed token leaves the layers it reached)
-    core_->open_token(seq, &run_);
-    wait_began(seq);
-    Clock::time_point t_prev = t_served_;
-    auto next_run = [&](uint32_t g) {
-      uint32_t h = g + 1;
-      while (h < G && !run_[h]) ++h;
-      return h;
-    };
-    for (uint32_t g = 0; g < G; ++g) {
-      if (!run_[g]) continue;
-      const uint32_t nx = next_run(g);
-      wait_word(&m_.flag[g], seq, "export flag", g, true, last_flag_[g]);
-      last_flag_[g] = seq;
-      const Clock::time_point t_seen = Clock::now();
-      Row row;
-      row.seen_us = us_between(t_prev, t_seen);
-      if (diag_) before_ = core_->counts();
-      const DgRecord& r = m_.rec[g];
-      require(r.seq == seq, SS_E_BACKEND,
-              "device-gated: sequence desync: the record of gated layer " + std::to_string(g) + " is for token " +
-                  std::to_string(r.seq) + ", serving " + std::to_string(seq));
-      const uint32_t n = r.n_ids, n_pred = r.n_pred_promised;
-      require(n >= 1 && n <= max_ids_, SS_E_BACKEND,
-              "device-gated: gated layer " + std::to_string(g) + " exported " + std::to_string(n) + " ids");
-      require(n_pred <= kDgMaxIds && (n_pred == 0 || g + 1 < G), SS_E_BACKEND,
-              "device-gated: gated layer " + std::to_string(g) + " promised " + std::to_string(n_pred) +
-                  " predicted ids");
-      const uint64_t dev_mask = uint64_t(r.mask_lo) | uint64_t(r.mask_hi) << 32;
-      ids_.assign(r.ids, r.ids + n);
-      // the canonical schedule's mask (the mirror now, after the previous layer's prediction was served): a prefetch
-      // that had not landed when the layer exported is a hit there, as in the reference's eager schedule
-      const uint64_t mask = core_->absent_mask(g, ids_.data(), n);
-      require((mask & ~dev_mask) == 0, SS_E_BACKEND,
-              "device-gated: gated layer " + std::to_string(g) + " exported a hit for a unit absent from the table");
-      core_->serve_misses(g, ids_.data(), n, mask, dev_mask);
-      const Clock::time_point t_demand = Clock::now();
-      row.demand_us = us_between(t_seen, t_demand);
-      core_->note_uses(g, ids_.data(), n, mask);
-      if (n_pred > 0 && run_[g + 1]) {
-        wait_word(&m_.pflag[g], seq, "prediction flag", g, false, 0);
-        const Clock::time_point t_pw = Clock::now();
-        row.pred_wait_us = us_between(t_demand, t_pw);
-        const DgPredRecord& pr = m_.prec[g];
-        require(pr.n_pred == n_pred, SS_E_BACKEND,
-                "device-gated: gated layer " + std::to_string(g) + " predicted " + std::to_string(pr.n_pred) +
-                    " ids, its export promised " + std::to_string(n_pred));
-        pred_.assign(pr.pred, pr.pred + n_pred);
-        core_->prefetch_next(g + 1, pred_.data(), n_pred);
-        row.prefetch_us = us_between(t_pw, Clock::now());
-      }
-      if (core_->queued_writebacks() && nx < G) core_->spend_wb_credit(g);
-      const Clock::time_point t_end = Clock::now();
-      row.serve_us = us_between(t_seen, t_end);
-      if (diag_) {
-        const DgCounts& a = core_->counts();
-        row.ids = uint32_t(a.lookups - before_.lookups);  // (one lookup per unique id)
-        row.misses = uint32_t(a.misses - before_.misses);
-        row.covered = uint32_t(a.covered - before_.covered);
-        row.fetched = uint32_t(a.fetched - before_.fetched);
-        row.prefetched = uint32_t(a.prefetched - before_.prefetched);
-        row.predicted_true = uint32_t(a.predicted_true - before_.predicted_true);
-        row.covered_waits = uint32_t(a.covered_waits - before_.covered_waits);
-        rows_[g] = row;
-      }
-      t_prev = t_end;
-    }
-    t_served_ = Clock::now();  // the next token's first seen_us counts from here
-  }
-
-  DgCore* core_;
-  DgMappedHost m_;
-  uint32_t max_ids_;
-  std::chrono::milliseconds timeout_;
-  int device_;
-  std::vector<uint8_t> run_, run_next_;
-  std::vector<uint32_t> last_flag_;
-  std::vector<uint32_t> ids_, pred_;
-  bool diag_ = false;
-  std::vector<Row> rows_;
-  DgCounts before_;
-  Clock::time_point t_served_{};
-  std::atomic<uint32_t> host_seq_{0};
-  std::atomic<uint64_t> term_{0};
-  std::atomic<bool> stop_{false};
-  mutable std::mutex mu_;
-  std::string err_;
-  std::thread th_;
-};
-
 // ---- the context ------------------------------------------------------------------------------------------------------
 class HipDgCtx final : public DgCtx {
  public:
@@ -1007,30 +781,67 @@ class HipDgCtx final : public DgCtx {
   int n_sources() const override { return int(files_.size()); }
   bool source_direct(int i) const override { return files_[size_t(i)]->direct(); }
 
+  // The device's words after the last token, as ss_begin and ss_end need them.
+  struct SeqWords {
+    uint32_t done = 0, began = 0;
+    bool flags_behind = true;  // no export or prediction flag is past the last token
+  };
+  SeqWords seq_words() const {
+    SeqWords w;
+    w.done = load_acquire(m_.done);
+    w.began = load_acquire(m_.began);
+    for (size_t g = 0; g < x_.gated.size() && w.flags_behind; ++g)
+      w.flags_behind = int32_t(load_acquire(m_.flag + g) - seq_) <= 0 && int32_t(load_acquire(m_.pflag + g) - seq_) <= 0;
+    return w;
+  }
+  // A token that cannot be trusted ends the context: the device's waits end on host_abort, the service stops, and
+  // every later call but close and stats is refused.
+  [[noreturn]] void fail_closed(const std::string& why) {
+    const std::string dev = device_error();
+    store_release(m_.host_abort, 1);
+    svc_->stop_join();
+    poisoned_ = true;
+    fail(SS_E_BACKEND, token_failure(dev, why));
+  }
+
+  // ss_begin: a new token may open only where the last one closed - the device's done and began words hold its
+  // sequence and no flag is ahead of it (anything else is a step that ran outside ss_begin / ss_end).
   void begin(const uint32_t* rows, int n_layers) override {
     require(!in_token_, SS_E_INVALID, "ss_begin: a gated token is already open (call ss_end)");
-    if (rows)
-      require(n_layers == int(d_.layers.size()), SS_E_INVALID, "ss_begin: rows_per_layer must cover every layer");
-    for (size_t g = 0; g < x_.gated.size(); ++g) run_[g] = !rows || rows[size_t(x_.gated[g])] != 0;
-    // no step ran outside a pair: every word still holds the last token's sequence
-    bool clean = load_acquire(m_.done) == seq_ && load_acquire(m_.began) == seq_;
-    for (size_t g = 0; clean && g < x_.gated.size(); ++g)
-      clean = int32_t(load_acquire(m_.flag + g) - seq_) <= 0 && int32_t(load_acquire(m_.pflag + g) - seq_) <= 0;
-    if (!clean) {
+    require(!rows || n_layers == int(d_.layers.size()), SS_E_INVALID, "ss_begin: rows_per_layer must cover every layer");
+    const SeqWords w = seq_words();
+    if (w.done != seq_ || w.began != seq_ || !w.flags_behind) {
       store_release(m_.host_abort, 1);
       svc_->stop_join();
       poisoned_ = true;
-      fail(SS_E_BACKEND, "device-gated: sequence desync at ss_begin: a gated step ran outside ss_begin / ss_end (done " +
-                             std::to_string(load_acquire(m_.done)) + ", began " +
-                             std::to_string(load_acquire(m_.began)) + ", last token " + std::to_string(seq_) +
-                             "; the context is poisoned)");
+      fail(SS_E_BACKEND, "device-gated: ss_begin found a step that ran outside ss_begin / ss_end (device done " +
+                             std::to_string(w.done) + ", began " + std::to_string(w.began) + ", last token " +
+                             std::to_string(seq_) + (w.flags_behind ? "" : ", a flag ahead of it") +
+                             "); the context is poisoned");
     }
+    for (size_t g = 0; g < x_.gated.size(); ++g) run_[g] = !rows || rows[size_t(x_.gated[g])] != 0;
     ++seq_;
     in_token_ = true;
     store_release(m_.host_seq, seq_);  // the begin kernel authorizes exactly this sequence
     svc_->begin(seq_, run_);
   }
 
+  // Waits for the device's done word to reach this token (the end kernel ran after every reader of the token); the
+  // reason it cannot be trusted, or empty.
+  std::string completion_problem(Clock::time_point deadline) const {
+    for (uint32_t polls = 0;; ++polls) {
+      const uint32_t v = load_acquire(m_.done);
+      if (v == seq_) break;
+      if (int32_t(v - seq_) > 0) return "sequence desync at ss_end: the device finished token " + std::to_string(v);
+      if ((polls & 1023u) == 0 && Clock::now() > deadline) return "the device did not finish it (no end kernel)";
+      if (polls < 100000) _mm_pause();
+      else std::this_thread::yield();
+    }
+    return load_acquire(m_.began) == seq_ ? std::string() : "sequence desync at ss_end: another gated step ran in it";
+  }
+
+  // ss_end: the token must be complete on the device and served in full; then the boundary runs and the device checks
+  // of the token's landed units report. A device error or a failed check poisons the context.
   void end(uint32_t rows) override {
     require(rows > 0, SS_E_INVALID, "ss_dg_end_rows: rows must be positive");
     require(in_token_, SS_E_INVALID, "ss_end: no gated token is open");
@@ -1043,55 +854,28 @@ class HipDgCtx final : public DgCtx {
       }
     } rows_guard{this};
     const auto deadline = Clock::now() + std::chrono::milliseconds(uint64_t(o_.dg_wait_timeout_ms) + 5000);
-    // 1. the completion edge: the end kernel ran after every reader of the token
-    bool at = false;
-    for (uint32_t spins = 0;; ++spins) {
-      const uint32_t v = load_acquire(m_.done);
-      if (v == seq_) {
-        at = true;
-        break;
-      }
-      if (int32_t(v - seq_) > 0) break;
-      if ((spins & 1023u) == 0 && Clock::now() > deadline) break;
-      if (spins < 100000) _mm_pause();
-      else std::this_thread::yield();
-    }
-    const uint32_t began = load_acquire(m_.began);
-    if (!at || began != seq_) {
-      const std::string dev = device_error();
-      store_release(m_.host_abort, 1);
-      svc_->stop_join();
-      poisoned_ = true;
-      fail(SS_E_BACKEND, token_failure(dev, at ? "sequence desync at ss_end: another gated step ran in it"
-                                               : "the device did not finish it (no end kernel)"));
-    }
-    // 2. the service's terminal word for this token
-    if (svc_->wait_terminal(seq_, deadline) != Service::kServed) {
-      const std::string dev = device_error();
-      store_release(m_.host_abort, 1);
-      svc_->stop_join();
-      poisoned_ = true;
+    if (const std::string why = completion_problem(deadline); !why.empty()) fail_closed(why);
+    if (svc_->wait_outcome(seq_, deadline) != DgService::Outcome::kServed) {
       const std::string why = svc_->error();
-      fail(SS_E_BACKEND, token_failure(dev, "the service: " + (why.empty() ? std::string("it did not finish") : why)));
+      fail_closed("the service: " + (why.empty() ? std::string("it did not finish") : why));
     }
-    // 3. the device's error word (a failed device check is reported with its units below)
     const std::string dev = device_error();
-    const bool hash_abort = load_acquire(m_.err_code) == kDgHash;
+    const bool hash_abort = load_acquire(m_.err_code) == kDgHash;  // a failed device check: named with its units below
     if (!dev.empty() && !hash_abort) {
       poisoned_ = true;
       fail(SS_E_BACKEND, token_failure(dev, ""));
     }
-    // 4. the boundary, then the device check of this token's landed units (a check of a prefetch may end after the
-    // end kernel: its failure is only in the check's result words)
-    tr_->verify_sync();  // the boundary may hand a landed slot to a write-back or a new copy
+    // the boundary: every check of the token has ended (it may hand a landed slot to a write-back or a new copy) and
+    // every read has returned (a prefetch's read may still use a staging buffer the boundary reuses)
+    tr_->verify_sync();
     try {
-      tr_->drain_reads();  // (a prefetch's read may still run: the boundary may reuse its staging buffer)
+      tr_->drain_reads();
     } catch (...) {
       poisoned_ = true;
       throw;
     }
     core_->close_token(rows, all_kept());
-    const std::vector<uint32_t> bad = tr_->collect_verify();
+    const std::vector<uint32_t> bad = tr_->collect_verify();  // (a prefetch's check may end after the end kernel)
     tr_->profile_collect();
     if (!bad.empty()) {
       verify_failures_ += bad.size();
@@ -1142,7 +926,7 @@ class HipDgCtx final : public DgCtx {
     require(o_.dg_diag != 0, SS_E_INVALID, "ss_dg_timeline: open the context with dg_diag = 1");
     check_g(g, "ss_dg_timeline");
     require(timeline_valid_, SS_E_INVALID, "ss_dg_timeline: no token has completed");
-    const Service::Row& t = svc_->timeline()[size_t(g)];
+    const DgService::Row& t = svc_->timeline()[size_t(g)];
     const LayerDiag& d = diag_rows_[size_t(g)];
     std::memset(out, 0, sizeof *out);
     out->struct_size = uint32_t(sizeof *out);
@@ -1257,6 +1041,28 @@ class HipDgCtx final : public DgCtx {
     o_.dg_wb_defer = wb_defer;
     o_.dg_flush_ready = flush_ready;
   }
+  // ss_dg_set_clean_evict (reference include/strix_stream/ss.h:1756-1760): from the next boundary's victims on.
+  void set_clean_evict(uint32_t on) override {
+    require(!in_token_, SS_E_INVALID, "ss_dg_set_clean_evict: between tokens only");
+    require(!poisoned_, SS_E_BACKEND, "ss_dg_set_clean_evict: poisoned context");
+    require(on <= 1, SS_E_INVALID, "ss_dg_set_clean_evict: on is 0 or 1");
+    core_->set_clean_evict(on != 0);
+    o_.dg_clean_evict = on;
+  }
+  // Test hooks under the reference's names (its include/strix_stream/ss_test.h:19, :30), for a context opened with
+  // dg_test_hooks = 1.
+  void test_hooks_on(const char* what) const {
+    require(o_.dg_test_hooks != 0, SS_E_INVALID, std::string(what) + ": open the context with dg_test_hooks = 1");
+  }
+  void test_check() override {
+    test_hooks_on("ss_test_dg_check");
+    require(!in_token_, SS_E_INVALID, "ss_test_dg_check: between tokens only");
+    core_->audit();
+  }
+  void test_stop_service() override {
+    test_hooks_on("ss_test_dg_stop_service");
+    svc_->stop_join();
+  }
   std::vector<uint32_t> all_kept() const {
     std::vector<uint32_t> v;
     for (const auto& k : kept_) v.insert(v.end(), k.begin(), k.end());
@@ -1269,7 +1075,7 @@ class HipDgCtx final : public DgCtx {
     require(!poisoned_, SS_E_BACKEND, "ss_dg_set_policy: poisoned context");
     require(load_acquire(m_.done) == seq_ && load_acquire(m_.began) == seq_, SS_E_BACKEND,
             "ss_dg_set_policy: device sequence desync");
-    require(!seq_ || svc_->wait_terminal(seq_, Clock::now()) == Service::kServed, SS_E_BACKEND,
+    require(!seq_ || svc_->wait_outcome(seq_, Clock::now()) == DgService::Outcome::kServed, SS_E_BACKEND,
             "ss_dg_set_policy: the service does not hold the last token's terminal state");
     core_->set_policy(uint32_t(policy));
     fold(false);  // the drain's write-backs in the counters; no token for the hook
@@ -1577,7 +1383,7 @@ class HipDgCtx final : public DgCtx {
   DgMappedHost m_;
   std::unique_ptr<HipTransport> tr_;
   std::unique_ptr<DgCore> core_;
-  std::unique_ptr<Service> svc_;
+  std::unique_ptr<DgService> svc_;
   std::vector<uint8_t> run_;
   std::vector<std::vector<uint32_t>> kept_;  // per gated layer: its ss_dg_keep set (keys)
   uint32_t seq_ = 0;
@@ -1808,7 +1614,7 @@ void HipDgCtx::init() {
   kept_.assign(G, {});
   base_l_.assign(G, DgLayerCounts{});
   fold(false);
-  svc_ = std::make_unique<Service>(core_.get(), m_, x_.B, o_.dg_wait_timeout_ms, o_.device);
+  svc_ = std::make_unique<DgService>(core_.get(), m_, x_.B, o_.dg_wait_timeout_ms, o_.device);
   if (o_.dg_diag) {
     tr_->enable_diag(G);
     svc_->enable_timeline();

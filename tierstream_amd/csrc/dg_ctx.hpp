@@ -35,6 +35,12 @@ class DgCtx {
   virtual void keep(int g, const int32_t* ids, int n) = 0;
   // Between tokens: write-back deferral on / off, and dg_flush_ready (0 / 1 each).
   virtual void set_sched(uint32_t wb_defer, uint32_t flush_ready) = 0;
+  // Between tokens: dg_clean_evict on / off from the next victim on (ss_dg_set_clean_evict).
+  virtual void set_clean_evict(uint32_t on) = 0;
+  // Test hooks (opened with dg_test_hooks = 1): the core's ownership invariants, between tokens; stop the service
+  // thread (the next token fails closed).
+  virtual void test_check() = 0;
+  virtual void test_stop_service() = 0;
   virtual ss_dg_stats stats() const = 0;
   virtual ss_layer_stats layer_stats(int layer) const = 0;
   virtual ss_layer_stats total_stats() const = 0;

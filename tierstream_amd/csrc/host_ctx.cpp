@@ -545,6 +545,21 @@ void HostCtx::test_hold_readers(bool hold) {
   reads_.hold(hold);
 }
 
+// ss_test_inject (the reference's one-shot fault injections, src/stream_ctx.cpp:508-1015): 1 queueing a read-ahead
+// read fails, 2 queueing a landing fails, 3 a landing's copy fails before it starts, 4 after its first piece (its buffer
+// is quarantined), 5 a read-ahead read fails, 8 fails after a part, 9 reads bytes that fail the hash. The
+// synchronization mutations 6, 7 and 10 (a copy skipping a wait) are not offered. Any other value arms nothing.
+void HostCtx::test_inject(int what) {
+  require(what != 6 && what != 7 && what != 10, SS_E_UNSUPPORTED,
+          "ss_test_inject: mutations that skip a copy's wait (6, 7, 10) are not offered by this library");
+  inject_.store(what);
+}
+
+bool HostCtx::take_inject(int what) {
+  int armed = what;
+  return inject_.load() == what && inject_.compare_exchange_strong(armed, 0);
+}
+
 void HostCtx::test_ra_quiesce() {
   for (auto& e : ra_entries_)
     if (e->producer) await_quiet(*e->producer);
@@ -572,7 +587,9 @@ void HostCtx::read_file_unit(Copy& c) {
   if (c.to_host) {
     uint64_t digest = 0;
     if (c.ra) ev_sync(ra_ev_[size_t(c.ra->buf)]);  // the buffer's last copy out has completed
+    if (c.ra && take_inject(5)) fail(SS_E_IO, "read-ahead: injected read failure");
     read_into_host(c.layer, c.unit, c.dst, hash, &digest, &c.bytes_read);
+    if (c.ra && take_inject(9)) digest = ~digest;
     require(!hash || digest == l.hash[size_t(c.unit)], SS_E_HASH,
             "unit (" + std::to_string(c.layer) + ", " + std::to_string(c.unit) + ") bytes differ from the descriptor hash");
     return;
@@ -645,6 +662,7 @@ void HostCtx::read_into_host(int layer, int unit, void* dst, bool hash, uint64_t
       });
     }
     pos += part.bytes;
+    if (got && take_inject(8)) fail(SS_E_IO, "read-ahead: injected failure after a part");
   }
   if (digest) *digest = h.digest();
   if (!states.empty() && h.digest() == l.hash[size_t(unit)]) {
@@ -744,8 +762,16 @@ void HostCtx::ra_pump() {
       ra_free_.pop_back();
       p->dst = ra_buf_[size_t(e.buf)];
       e.producer = p;
-      e.st = RaEntry::kReading;
-      reads_.push(ReadClass::kAhead, p);
+      if (take_inject(1)) {  // queueing the read failed: it ends at once, and the unit's fetch reads its file
+        p->status = SS_E_NOMEM;
+        p->what = "read-ahead: queueing a read failed";
+        p->state.store(Copy::kFailed);
+        ra_give_buf_locked(e);
+        e.st = RaEntry::kFailed;
+      } else {
+        e.st = RaEntry::kReading;
+        reads_.push(ReadClass::kAhead, p);
+      }
     }
     ra_wait_.pop_front();
   }
@@ -783,7 +809,7 @@ void HostCtx::ra_abandon_locked(RaEntry& e) {
 // The unit got its slot (a demand fetch, child: its job): lands from the buffer when the read ended or runs, else
 // (never started, or failed: a fallback) the caller reads the file.
 bool HostCtx::ra_land(RaEntry& e, const CopyPtr& child) {
-  bool issue = false, attached = false, fallback = false;
+  bool issue = false, attached = false, fallback = false, lost = false;
   {
     std::lock_guard<std::mutex> lk(q_mu_);
     switch (e.st) {
@@ -791,10 +817,17 @@ bool HostCtx::ra_land(RaEntry& e, const CopyPtr& child) {
         e.st = RaEntry::kAbandoned;
         break;
       case RaEntry::kReady:
-        e.st = RaEntry::kLanding;
         e.child = child;
         child->state.store(Copy::kRunning);
-        issue = attached = true;
+        attached = true;
+        if (take_inject(2)) {  // the landing fails for good (no fallback that depends on timing)
+          e.st = RaEntry::kFailed;
+          ra_give_buf_locked(e);
+          lost = true;
+        } else {
+          e.st = RaEntry::kLanding;
+          issue = true;
+        }
         break;
       case RaEntry::kReading: {
         e.st = RaEntry::kLanding;
@@ -811,6 +844,7 @@ bool HostCtx::ra_land(RaEntry& e, const CopyPtr& child) {
     }
   }
   if (fallback) ++ra_st_.fallback;
+  if (lost) finish(*child, Copy::kFailed, SS_E_NOMEM, "read-ahead: queueing a landing failed");
   if (issue) ra_issue_child(e, *child);
   return attached;
 }
@@ -821,7 +855,14 @@ void HostCtx::ra_issue_child(RaEntry& e, Copy& child) {
   int state = Copy::kDone;
   ss_status st = SS_OK;
   std::string what;
+  bool quarantine = false;  // a copy out of the buffer may still run: it is never read into again
   try {
+    if (take_inject(3)) fail(SS_E_IO, "read-ahead: injected copy failure");
+    if (take_inject(4)) {
+      quarantine = true;
+      issue_first_piece(child, ra_buf_[size_t(e.buf)]);
+      fail(SS_E_IO, "read-ahead: injected copy failure after its first piece");
+    }
     issue_copy(child, ra_buf_[size_t(e.buf)], ra_ev_[size_t(e.buf)]);
   } catch (const Error& x) {
     state = Copy::kFailed, st = x.status(), what = x.what();
@@ -831,9 +872,19 @@ void HostCtx::ra_issue_child(RaEntry& e, Copy& child) {
   {
     std::lock_guard<std::mutex> lk(q_mu_);
     e.st = state == Copy::kDone ? RaEntry::kConsumed : RaEntry::kFailed;
-    ra_give_buf_locked(e);
+    if (quarantine) e.buf = -1;
+    else ra_give_buf_locked(e);
   }
   finish(child, state, st, what);
+}
+
+// (ss_test_inject 4) only the first piece of a landing's copy, behind the destination's waits.
+void HostCtx::issue_first_piece(Copy& c, const void* src) {
+  std::lock_guard<std::mutex> lk(copy_mu_);
+  const hipStream_t cs = next_copy_stream();
+  wait_slot_check(cs, c.dst);
+  for (hipEvent_t e : c.after) stream_wait(cs, e);
+  copy_h2d(c.dst, src, std::min(o_.copy_piece_bytes, d_.layers[size_t(c.layer)].unit_bytes), cs);
 }
 
 // A read-ahead read ended (state kDone or kFailed; a reader thread): its request moves on - a landing waiting for it
@@ -841,7 +892,7 @@ void HostCtx::ra_issue_child(RaEntry& e, Copy& child) {
 // as ended.
 void HostCtx::ra_read_ended(Copy& p, int state, ss_status st, const std::string& what) {
   RaEntry& e = *p.ra;
-  CopyPtr issue, failed;
+  CopyPtr issue, failed, lost;
   {
     std::lock_guard<std::mutex> lk(q_mu_);
     const bool ok = state == Copy::kDone;
@@ -860,10 +911,10 @@ void HostCtx::ra_read_ended(Copy& p, int state, ss_status st, const std::string&
           ra_give_buf_locked(e);
           break;
         }
-        if (ok) {
+        if (ok && !take_inject(2)) {
           issue = e.child;
         } else {
-          failed = e.child;
+          (ok ? lost : failed) = e.child;  // (ok: its landing could not be queued)
           e.st = RaEntry::kFailed;
           ra_give_buf_locked(e);
         }
@@ -878,6 +929,7 @@ void HostCtx::ra_read_ended(Copy& p, int state, ss_status st, const std::string&
   }
   if (issue) ra_issue_child(e, *issue);
   if (failed) finish(*failed, Copy::kFailed, st, "read-ahead: " + what);
+  if (lost) finish(*lost, Copy::kFailed, SS_E_NOMEM, "read-ahead: queueing a landing failed");
   finish(p, state, st, what);
 }
 

@@ -84,6 +84,8 @@ class HostCtx final : public HostWork {
   // the forward has ended (readers not held).
   void test_hold_readers(bool hold);
   void test_ra_quiesce();
+  void test_inject(int what);
+  void check_exclusive() const { place_.check_blocks(); }
   void copy_counts(uint64_t* units, uint64_t* copies) const {
     std::lock_guard<std::mutex> lk(copy_mu_);
     *units = pinned_units_;
@@ -178,6 +180,8 @@ class HostCtx final : public HostWork {
   void read_file_unit(Copy& c);  // a reader thread: the unit's file bytes to its destination
   // got: + the file bytes read (null: not counted)
   void read_into_host(int layer, int unit, void* dst, bool hash, uint64_t* digest, uint64_t* got = nullptr);
+  bool take_inject(int what);  // (one shot) the armed injection is `what`: disarm it and report true
+  void issue_first_piece(Copy& c, const void* src);
   std::vector<uint64_t> checkpoint_buffer(const Layer& l, bool hash) const;
   void keep_checkpoints_locked(int64_t g, const std::vector<uint64_t>& states);
   const SourceFile& part_source(int layer, int unit, const Part& part, uint64_t* off) const;
@@ -293,6 +297,7 @@ class HostCtx final : public HostWork {
   bool ra_frozen_ = false;
   RaCounts ra_st_;                                    // since open or the last reset
   std::vector<std::thread> readers_;
+  std::atomic<int> inject_{0};  // ss_test_inject
 
   // verify_hash = 2
   bool dverify_ = false;

@@ -582,6 +582,32 @@ HostPlacement::Ended HostPlacement::end() {
   return e;
 }
 
+void HostPlacement::check_blocks() const {
+  require(excl_, SS_E_INVALID, "check_exclusive: the context is not in the exclusive tier mode");
+  require(!in_fwd_ && !fwd_open_, SS_E_INVALID, "check_exclusive: only between forwards");
+  std::vector<uint32_t> holders(blocks_.size(), 0);
+  for (size_t L = 0; L < L_.size(); ++L) {
+    if (!L_[L].pool) continue;
+    const Layer& l = d_.layers[L];
+    for (int u = 0; u < l.n_units; ++u) {
+      const size_t g = size_t(d_.gidx(int(L), u));
+      if (p_.tier[g] == SS_TIER_PAIR) continue;  // another device's unit
+      require(wb_batch_of_[g] < 0, SS_E_INVALID, "check_exclusive: a write-back is still pending at a boundary");
+      const int32_t b = block_of_[g];
+      if (b < 0) continue;
+      const std::string who = "unit (" + std::to_string(L) + ", " + std::to_string(u) + ")";
+      require(l.streamable, SS_E_INVALID, "check_exclusive: " + who + " is not streamable and owns a block");
+      require(L_[L].pool->slot(u) < 0, SS_E_INVALID, "check_exclusive: " + who + " is in a slot and a block");
+      ++holders[size_t(b)];
+    }
+  }
+  for (size_t k = 0; k < spare_.classes(); ++k)
+    for (int32_t b : spare_.free_list(int(k))) ++holders[size_t(b)];
+  for (size_t b = 0; b < holders.size(); ++b)
+    require(holders[b] == 1, SS_E_INVALID,
+            "check_exclusive: block " + std::to_string(b) + (holders[b] ? " is held twice" : " is held by no one"));
+}
+
 void HostPlacement::reset_stats() { std::fill(total_.begin(), total_.end(), ss_layer_stats{}); }
 
 }  // namespace tsa

@@ -139,6 +139,9 @@ class HostPlacement {
   const std::vector<ss_layer_stats>& forward_stats() const { return fwd_; }
   void reset_stats();
   const ss_exclusive_stats& exclusive_stats() const { return xst_; }
+  // Exclusive mode, between forwards: each pinned block belongs to exactly one unit off the device or to a free list,
+  // and no write-back is pending (ss_test_check_exclusive; SS_E_INVALID naming the first rule broken).
+  void check_blocks() const;
   uint64_t forwards() const { return forwards_; }
 
  private:

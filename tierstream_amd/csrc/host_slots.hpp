@@ -165,6 +165,7 @@ class SpareBlocks {
     return b;
   }
   void give(int cls, int32_t b) { stack_[size_t(cls)].push_back(b); }
+  const std::vector<int32_t>& free_list(int cls) const { return stack_[size_t(cls)]; }
 
  private:
   std::vector<std::vector<int32_t>> stack_;

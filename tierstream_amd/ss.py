@@ -87,6 +87,17 @@ class SsPlanTotals(C.Structure):
                                    "n_disk"]]
 
 
+class SsDgUnit(C.Structure):
+    _fields_ = [("gated", C.c_int32), ("unit", C.c_int32)]
+
+
+def dg_seed(units) -> tuple:
+    """(array, count) for ss_options.dg_seed / dg_seed_n from (gated layer, unit) pairs; keep the array alive while the
+    context opens."""
+    arr = (SsDgUnit * max(len(units), 1))(*[SsDgUnit(int(g), int(u)) for g, u in units])
+    return arr, len(units)
+
+
 class SsDgPart(C.Structure):
     _fields_ = [("base", vp), ("stride", u64), ("bytes", u64)]
 
@@ -215,6 +226,10 @@ def _declare() -> C.CDLL:
         "ss_dg_get_device_view_sized": (st, [vp, C.POINTER(SsDgDeviceView), u32]),
         "ss_dg_gated_index": (C.c_int, [vp, C.c_int]),
         "ss_dg_residency": (st, [vp, vp, u32, C.POINTER(u32)]),
+        "ss_dg_set_clean_evict": (st, [vp, u32]),
+        "ss_source_direct": (C.c_int, [vp, C.c_int]),
+        "ss_test_dg_check": (st, [vp]),
+        "ss_test_dg_stop_service": (st, [vp]),
         "tsa_test_region_of": (st, [vp, u64, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(u64)]),
         "tsa_test_dg_table": (st, [vp, C.POINTER(i32), u32, C.POINTER(u32)]),
         "tsa_test_verify_failures": (u64, [vp]),
@@ -444,6 +459,38 @@ class Ctx:
     def dg_set_sched(self, wb_defer: int, flush_ready: int = 0):
         """Between tokens: write-back deferral and dg_flush_ready (ss_dg_set_sched)."""
         check(_declare().ss_dg_set_sched(self.h, wb_defer, flush_ready))
+
+    def dg_set_clean_evict(self, on: int):
+        """Between tokens: dg_clean_evict on / off (ss_dg_set_clean_evict)."""
+        check(_declare().ss_dg_set_clean_evict(self.h, on))
+
+    def dg_set_budgets(self, spare_target: int, per_layer: int, per_token: int):
+        """Between tokens: the spare target and the prefetch budgets (ss_dg_set_budgets)."""
+        check(_declare().ss_dg_set_budgets(self.h, spare_target, per_layer, per_token))
+
+    def dg_gated_index(self, layer: int) -> int:
+        """The gated ordinal of a descriptor layer, -1 for a layer without units or out of range."""
+        return int(_declare().ss_dg_gated_index(self.h, layer))
+
+    def dg_residency(self) -> list[tuple[int, int]]:
+        """Between tokens: the units on the device, most recently used first, as (gated layer, unit)."""
+        L = _declare()
+        n = u32(0)
+        check(L.ss_dg_residency(self.h, None, 0, C.byref(n)))
+        arr = (SsDgUnit * max(n.value, 1))()
+        check(L.ss_dg_residency(self.h, C.cast(arr, vp), n.value, C.byref(n)))
+        return [(int(arr[i].gated), int(arr[i].unit)) for i in range(n.value)]
+
+    def source_direct(self, source: int = 0) -> int:
+        """1: the source is read with O_DIRECT; 0: buffered (its file system refused O_DIRECT); < 0: an error."""
+        return int(_declare().ss_source_direct(self.h, source))
+
+    def test_dg_check(self) -> int:
+        """ss_test_dg_check: the status (no raise)."""
+        return int(_declare().ss_test_dg_check(self.h))
+
+    def test_dg_stop_service(self) -> int:
+        return int(_declare().ss_test_dg_stop_service(self.h))
 
     def host_prefetch(self, layer: int, ids) -> int:
         """ss_host_prefetch; returns the status (no raise)."""
