@@ -20,6 +20,10 @@ SS_API ss_status tsa_test_region_of(const ss_ctx* c, uint64_t addr, int* kind, i
 SS_API ss_status tsa_test_dg_table(const ss_ctx* c, int32_t* out, uint32_t cap, uint32_t* n);
 /* verify_hash = 2: landed units whose device check failed, since open. */
 SS_API uint64_t tsa_test_verify_failures(const ss_ctx* c);
+/* Device-gated: 1 when the context's unit copies go through the HSA runtime's copy engines (each with a completion
+ * signal), 0 when they go through HIP streams (the file tier, parts small enough to be staged and scattered, or
+ * TSA_DG_COPIES=hip at open). */
+SS_API int tsa_test_dg_hsa_copies(const ss_ctx* c);
 /* Host contract test hooks under the reference's names (its src/capi.cpp:721-734; its tests declare them by hand):
  * reader threads take no job while held (closing the context still ends them); wait until every read-ahead read of
  * the open forward has ended (readers not held). */

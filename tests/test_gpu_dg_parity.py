@@ -108,6 +108,19 @@ CASES = {
                       sched={6: (0, 1), 12: (1, 0), 18: (0, 0)}),
     "set-sched-big-parts": dict(layers=4, units=8, parts=[8 * MiB] * 3, n_res=12, dyn=1, spares=6, n_ids=2,
                                 tokens=16, sched={5: (0, 0), 10: (1, 1)}, keep=True),
+    # parts copied whole go through the HSA runtime's copy engines (a completion signal per copy, later copies and the
+    # host-launched value writes behind them); the same cases with the HIP streams' copies (TSA_DG_COPIES=hip), and
+    # without device verify (ready words and slot entries then follow the copies through the same host queue)
+    "big-parts-hip-copies": dict(layers=4, units=8, parts=[8 * MiB] * 3, n_res=12, dyn=1, spares=6, n_ids=2,
+                                 tokens=16, hip_copies=True),
+    "single-part-prefetch-hip-copies": dict(layers=4, units=16, parts=[256 * KiB], n_res=24, dyn=2, spares=12,
+                                            n_ids=4, tokens=20, predict=3, hip_copies=True),
+    "single-part-prefetch": dict(layers=4, units=16, parts=[256 * KiB], n_res=24, dyn=2, spares=12, n_ids=4,
+                                 tokens=20, predict=3),
+    "big-parts-no-verify": dict(layers=4, units=8, parts=[8 * MiB] * 3, n_res=12, dyn=1, spares=6, n_ids=2, tokens=16,
+                                verify=0),
+    "single-part-prefetch-no-verify": dict(layers=4, units=16, parts=[256 * KiB], n_res=24, dyn=2, spares=12, n_ids=4,
+                                           tokens=20, predict=3, verify=0, early=True),
 }
 
 
@@ -165,6 +178,19 @@ def _profile_cells(units, layers, seed=9):
     return cells
 
 
+def _open(d, bkw, plan, okw, hip_copies=False):
+    """A device-gated context; hip_copies: its unit copies on HIP streams (TSA_DG_COPIES=hip while it opens)."""
+    old = os.environ.pop("TSA_DG_COPIES", None)
+    if hip_copies:
+        os.environ["TSA_DG_COPIES"] = "hip"
+    try:
+        return ss.Ctx(d, ss.budget(**bkw), plan, ss.options(**okw))
+    finally:
+        os.environ.pop("TSA_DG_COPIES", None)
+        if old is not None:
+            os.environ["TSA_DG_COPIES"] = old
+
+
 @pytest.mark.parametrize("name", list(CASES))
 def test_dg_matches_reference(name, tmp_path, gpu):
     c = dict(CASES[name])
@@ -177,8 +203,10 @@ def test_dg_matches_reference(name, tmp_path, gpu):
     early = c.pop("early", False)
     keep = c.pop("keep", False)
     sched = dict(c.pop("sched", {}))
+    hip_copies = c.pop("hip_copies", False)
     m, bkw, okw = _setup(tmp_path, c["layers"], c["units"], c["parts"], c["n_res"], c["dyn"], c["spares"], c["n_ids"],
                          inclusive=c.get("inclusive", 0), wb_defer=c.get("wb_defer", 1))
+    okw["verify_hash"] = c.pop("verify", 2)
     ref_score, keep = None, []
     if score:
         w = score.get("w", (700, 200, 100))
@@ -208,7 +236,9 @@ def test_dg_matches_reference(name, tmp_path, gpu):
     refdg = ref.RefDg([c["units"]] * c["layers"], R + D, c["n_ids"], P + Q, D, c["parts"],
                       residents + list(range(keys)), wb_defer=c.get("wb_defer", 1), inclusive=c.get("inclusive", 0),
                       score=ref_score)
-    ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(**okw))
+    ctx = _open(d, bkw, plan, okw, hip_copies)
+    staged = len(c["parts"]) > 1 and min(c["parts"]) < 8 * MiB
+    assert ctx.hsa_copies() == (not staged and not hip_copies), name
     eng = ss.DgEngine(ctx, c["n_ids"], use_graph=use_graph, n_pred=predict, early=early)
     preds = _preds(routes, c["units"], predict) if predict else None
     early_ready = early_total = 0
@@ -592,14 +622,15 @@ def test_keep_sched_and_host_calls_refuse_bad_arguments(tmp_path, gpu):
         ctx.close()
 
 
-def test_dg_timeline(tmp_path, gpu):
+@pytest.mark.parametrize("copies", ["staged", "hsa", "hip"])
+def test_dg_timeline(tmp_path, gpu, copies):
     """dg_diag = 1 (ss_dg_timeline_sized, ss_dg_boundary_timeline_sized; reference ss.h:702-729): after every token each
     gated layer's row holds its counts - their sums are the token's ss_dg_stats deltas, which equal the reference
     core's - host times that add up (demand, prediction wait and prefetch inside the layer's service), and device
     measurements only where the layer had a miss (its copies' time, the first fetch's copies within it, the wait
     kernel's stall within the export-to-ready time); the boundary's row counts the token's write-back victims. The
     calls refuse a context without dg_diag, a gated layer out of range and a host context."""
-    c = dict(CASES["prefetch"])
+    c = dict(CASES["prefetch"] if copies == "staged" else CASES["single-part-prefetch"])
     m, bkw, okw = _setup(tmp_path, c["layers"], c["units"], c["parts"], c["n_res"], c["dyn"], c["spares"], c["n_ids"])
     okw.update(dg_diag=1)
     d = ss.Desc(m.desc_json())
@@ -611,7 +642,8 @@ def test_dg_timeline(tmp_path, gpu):
     Q = plan.json()["spare_blocks"][0]["blocks"]
     D = sum(min(c["dyn"], sum(1 for u in range(U) if tiers[L][u] != 0)) for L in range(G))
     refdg = ref.RefDg([U] * G, len(residents) + D, c["n_ids"], P + Q, D, c["parts"], residents + list(range(G * U)))
-    ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(**okw))
+    ctx = _open(d, bkw, plan, okw, copies == "hip")
+    assert ctx.hsa_copies() == (copies == "hsa")
     eng = ss.DgEngine(ctx, c["n_ids"], use_graph=True, n_pred=3)
     routes = _routes(G, U, c["n_ids"], 16, seed=5, zipf=True)
     preds = _preds(routes, U, 3)

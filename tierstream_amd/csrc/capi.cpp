@@ -539,6 +539,7 @@ uint64_t tsa_test_verify_failures(const ss_ctx* c) {
   if (!c) return 0;
   return c->dg ? c->dg->verify_failures() : c->host->verify_failures();
 }
+int tsa_test_dg_hsa_copies(const ss_ctx* c) { return c && c->dg && c->dg->hsa_copies() ? 1 : 0; }
 ss_status tsa_test_host_copies(const ss_ctx* c, uint64_t* units, uint64_t* copies) {
   return guard([&] {
     need(c && units && copies, "tsa_test_host_copies: null argument");

@@ -7,10 +7,12 @@
 #include <atomic>
 #include <chrono>
 #include <condition_variable>
+#include <cstdlib>
 #include <cstring>
 #include <deque>
 #include <exception>
 #include <functional>
+#include <memory>
 #include <mutex>
 #include <thread>
 #include <unordered_map>
@@ -22,6 +24,7 @@
 #include "dg_proto.hpp"
 #include "dg_service.hpp"
 #include "hip_rt.hpp"
+#include "hsa_copy.hpp"
 #include "read_pool.hpp"
 #include "score_profile.hpp"
 #include "source.hpp"
@@ -86,6 +89,7 @@ class HipTransport final : public DgTransport {
     }
   }
   ~HipTransport() override {
+    if (hsa_) hsa_->wait_all();  // every copy out of and into the context's memory has ended
     if (pool_) pool_->stop();  // every read's word stored: no await left waiting on the streams below
     if (vs_) (void)hipStreamSynchronize(vs_);
     for (auto& s : s_) {
@@ -116,6 +120,21 @@ class HipTransport final : public DgTransport {
   }
 
   hipStream_t stream(Stream s) const { return s_[s]; }
+
+  // Unit copies through the HSA runtime (HsaCopier) instead of the HIP streams, possible where every part is copied
+  // whole (no scatter) and no file tier reads into the blocks (its reads order the copies behind device waits).
+  // Decided before the core makes its first event. Each library stream is then a lane: `tail_` holds the copies
+  // (signals, one reference each) its next operation waits for - its last copy and what wait() added since - and the
+  // core's events are Marks, the tail of the lane they were recorded on. A lane's value writes (slot entries, ready
+  // words) and timing marks go through the host-launched queue of checks, behind the copies they follow, on one HIP
+  // stream; no HIP stream carries a unit copy.
+  bool enable_hsa_copies(int device) {
+    if (scatter_ || reader_) return false;
+    hsa_ = std::make_unique<HsaCopier>(device);
+    part_sig_.assign(part_ev_.size(), 0);
+    return true;
+  }
+  bool hsa_copies() const { return hsa_ != nullptr; }
   // blocks 0 .. blocks - 1: the pinned homes and spares (in chunks); blocks .. blocks + S - 1: the staging buffers;
   // blocks + S .. blocks + S + L - 1: the landing blocks (in chunks)
   char* block_ptr(int32_t b) const {
@@ -133,6 +152,7 @@ class HipTransport final : public DgTransport {
   // landing blocks (pinned, in chunks of at most 1 GiB).
   void enable_disk(std::function<void(uint32_t, char*)> reader, ReadPool::PieceReader piece_reader,
                    ReadPool::Finisher finisher, const DgDevWords& dw) {
+    require(!hsa_, SS_E_BACKEND, "device-gated: the file tier with copies through the HSA runtime");
     reader_ = std::move(reader);
     for (uint32_t i = 0; i < x_.S; ++i)
       stage_.push_back(static_cast<char*>(dev_->alloc_pinned(x_.host_stride, "disk staging buffer")));
@@ -237,10 +257,22 @@ class HipTransport final : public DgTransport {
       ev_record(dma_a_[g], s_[kDem]);
       dma_used_[g] = 1;
     } else if (which == 2) {
-      ev_record(dma_f_[g], s_[kDem]);
       dma_used_[g] = 2;
+      if (!hsa_) return ev_record(dma_f_[g], s_[kDem]);
+      Check c;  // (with HSA copies: once the layer's copies so far have ended)
+      c.kind = Check::kMark;
+      c.mark = dma_f_[g];
+      hold(c.sigs, tail_[kDem]);
+      checks_.push_back(std::move(c));
+      poll_checks();
+    } else if (verify_ || hsa_) {  // after the layer's ready word, in the order of the checks
+      Check c;
+      c.kind = Check::kMark;
+      c.mark = dma_b_[g];
+      checks_.push_back(std::move(c));
+      poll_checks();
     } else {
-      ev_record(dma_b_[g], verify_ ? vs_ : s_[kDem]);
+      ev_record(dma_b_[g], s_[kDem]);
     }
   }
   void diag_boundary() override {
@@ -252,8 +284,21 @@ class HipTransport final : public DgTransport {
   }
   void diag_writebacks_issued() override {
     if (!diag_) return;
-    ev_record(wb_end_[wb_cur_], s_[kD2h]);
     wb_cur_valid_ = true;
+    if (!hsa_) return ev_record(wb_end_[wb_cur_], s_[kD2h]);
+    drop(wb_sigs_[wb_cur_]);  // (with HSA copies: recorded when a poll of the queue sees the write-backs ended)
+    hold(wb_sigs_[wb_cur_], tail_[kD2h]);
+    wb_seen_[wb_cur_] = false;
+    poll_wb_marks();
+  }
+  void poll_wb_marks() {
+    if (!diag_ || !hsa_) return;
+    for (int i = 0; i < 2; ++i)
+      if (!wb_seen_[i] && all_done(wb_sigs_[i])) {
+        ev_record(wb_end_[i], s_[kD2h]);
+        drop(wb_sigs_[i]);
+        wb_seen_[i] = true;
+      }
   }
   struct LayerDma {
     double dma_ms = -1, dma_first_ms = -1, wb_left_ms = -1;
@@ -264,7 +309,10 @@ class HipTransport final : public DgTransport {
     std::vector<LayerDma> out(dma_used_.size());
     if (!diag_) return out;
     int wb = 0;
-    if (wb_prev_valid_) {
+    poll_wb_marks();
+    if (wb_prev_valid_ && hsa_ && !wb_seen_[wb_prev_]) {
+      wb = -2;
+    } else if (wb_prev_valid_) {
       const hipError_t q = hipEventQuery(wb_end_[wb_prev_]);
       wb = q == hipSuccess ? 1 : q == hipErrorNotReady ? -2 : 0;
     }
@@ -331,11 +379,48 @@ class HipTransport final : public DgTransport {
     }
   }
   void part_wait(Stream s, int32_t slot, int32_t block, uint32_t p) {
-    if (slot >= 0 && slot == wait_slot_) stream_wait(s_[s], part_ev_[part_ev_index(false, slot, p)]);
-    if (block >= 0 && block == wait_block_) stream_wait(s_[s], part_ev_[part_ev_index(true, block, p)]);
+    if (slot >= 0 && slot == wait_slot_) gate(s, part_ev_[part_ev_index(false, slot, p)]);
+    if (block >= 0 && block == wait_block_) gate(s, part_ev_[part_ev_index(true, block, p)]);
   }
+  // Waits on the library's queues. A device barrier (hipStreamWaitEvent) parked on one CU-masked queue while its event
+  // is still running slows every kernel dispatched from the other CU-masked queues, the device check among them
+  // (measured on one MI355X: one 336 MiB check 57 us with no such barrier, about 90 us beside two). So a wait reaches
+  // the device only when it must: an event that has completed is no wait at all; on the demand stream the service
+  // thread waits on the host (the stream is in order: nothing behind the copy could start earlier), launching the
+  // checks whose copies land meanwhile; the D2H stream's waits are kept until its next copy (one followed by nothing
+  // is dropped); anything else is a device barrier.
+  void gate(Stream s, hipEvent_t ev) {
+    if (!ev || ev_done(ev)) return;
+    if (s == kDem && std::this_thread::get_id() == service_thread_) {
+      while (!ev_done(ev)) {
+        poll_checks();
+        _mm_pause();
+      }
+      return;
+    }
+    if (s == kD2h) {
+      d2h_waits_.push_back(ev);
+      return;
+    }
+    stream_wait(s_[s], ev);
+  }
+  void d2h_ready() {  // before an operation on the D2H stream: its kept waits
+    for (hipEvent_t e : d2h_waits_)
+      if (!ev_done(e)) stream_wait(s_[kD2h], e);
+    d2h_waits_.clear();
+  }
+  void set_service_thread(std::thread::id id) { service_thread_ = id; }
   void h2d_unit(Stream s, int32_t slot, int32_t block) {
     const char* src = block_ptr(block);
+    if (hsa_) {  // part by part on the lane, each after the same part of the write-backs named by wait_copy_in
+      for (uint32_t p = 0; p < uint32_t(x_.part_bytes.size()); ++p) {
+        const uint32_t ws = slot >= 0 && slot == wait_slot_ ? part_sig_[part_ev_index(false, slot, p)] : 0;
+        const uint32_t wb = block >= 0 && block == wait_block_ ? part_sig_[part_ev_index(true, block, p)] : 0;
+        const uint32_t sig = lane_copy(s, slot_ptr(p, slot), src + x_.part_offset[p], x_.part_bytes[p], false, ws, wb);
+        prof_copy(kProfCopy, sig, x_.part_bytes[p], p == 0 ? 1 : 0);
+      }
+      return;
+    }
     const bool landing = landing_block(block);
     if (landing) {  // a promotion: its landing read becomes a demand read if it still runs; one that failed reads again
       const uint32_t l = uint32_t(block) - x_.blocks - x_.S, i = land_word0_ + l;
@@ -398,6 +483,11 @@ class HipTransport final : public DgTransport {
     prof_end(t, s_[s]);
   }
   void d2h(int32_t slot, int32_t block) override {
+    if (hsa_) {
+      for (uint32_t p = 0; p < parts(); ++p) hsa_d2h_part(kD2h, slot, block, p, p == 0 ? 1 : 0);
+      return;
+    }
+    d2h_ready();
     Timed t = prof_start(kProfWb, x_.unit_bytes, 1, s_[kD2h]);
     char* dst = block_ptr(block);
     for (uint32_t p = 0; p < x_.part_bytes.size(); ++p) {
@@ -413,13 +503,28 @@ class HipTransport final : public DgTransport {
   // those submissions find the part copied and only the part's events matter (recorded at the copy).
   void prestage(int32_t slot, int32_t block) override {
     const uint32_t P = uint32_t(x_.part_bytes.size());
-    for (uint32_t p = 0; p < P; ++p) {
-      Timed t = prof_start(kProfWb, x_.part_bytes[p], 1, s_[kD2h]);
-      copy_d2h(block_ptr(block) + x_.part_offset[p], slot_ptr(p, slot), x_.part_bytes[p], s_[kD2h]);
-      mark_part(kD2h, slot, block, p);
-      prof_end(t, s_[kD2h]);
+    if (hsa_) {
+      for (uint32_t p = 0; p < P; ++p) hsa_d2h_part(kD2h, slot, block, p, 1);
+    } else {
+      d2h_ready();
+      for (uint32_t p = 0; p < P; ++p) {
+        Timed t = prof_start(kProfWb, x_.part_bytes[p], 1, s_[kD2h]);
+        copy_d2h(block_ptr(block) + x_.part_offset[p], slot_ptr(p, slot), x_.part_bytes[p], s_[kD2h]);
+        mark_part(kD2h, slot, block, p);
+        prof_end(t, s_[kD2h]);
+      }
     }
     prestaged_[slot] = {block, (1u << P) - 1u};
+  }
+  // One part of a write-back on lane s (HSA copies): the part's signal becomes the slot's and the block's.
+  void hsa_d2h_part(Stream s, int32_t slot, int32_t block, uint32_t p, uint32_t count) {
+    const uint32_t sig = lane_copy(s, block_ptr(block) + x_.part_offset[p], slot_ptr(p, slot), x_.part_bytes[p], true);
+    for (size_t i : {part_ev_index(false, slot, p), part_ev_index(true, block, p)}) {
+      hsa_->ref(sig);
+      hsa_->unref(part_sig_[i]);
+      part_sig_[i] = sig;
+    }
+    prof_copy(kProfWb, sig, x_.part_bytes[p], count);
   }
   void d2h_part(Stream s, int32_t slot, int32_t block, uint32_t p) override {
     auto it = prestaged_.find(slot);
@@ -428,6 +533,8 @@ class HipTransport final : public DgTransport {
       if (!it->second.parts) prestaged_.erase(it);
       return;
     }
+    if (hsa_) return hsa_d2h_part(s, slot, block, p, 1);
+    if (s == kD2h) d2h_ready();
     Timed t = prof_start(kProfWb, x_.part_bytes[p], 1, s_[s]);
     copy_d2h(block_ptr(block) + x_.part_offset[p], slot_ptr(p, slot), x_.part_bytes[p], s_[s]);
     mark_part(s, slot, block, p);
@@ -447,19 +554,33 @@ class HipTransport final : public DgTransport {
   uint32_t parts() const override { return uint32_t(x_.part_bytes.size()); }
   uint64_t part_bytes(uint32_t p) const override { return x_.part_bytes[p]; }
   void write_entry(Stream s, uint32_t key, int32_t v) override {
+    if (hsa_) {  // behind the lane's copies (a fetched unit's entry after its bytes), in the queue's order
+      Check c;
+      c.kind = Check::kEntry;
+      hold(c.sigs, tail_[s]);
+      c.key = key;
+      c.v = v;
+      checks_.push_back(std::move(c));
+      poll_checks();
+      return;
+    }
     hip_check(hipStreamWriteValue32(s_[s], slot_of_ + key, uint32_t(v), 0), "hipStreamWriteValue32 (slot entry)");
   }
   // ready[g] = seq after the layer's demand copies (and cover waits) on kDem; with device verify on the verify stream,
   // behind the checks of every unit landed so far in the token (its stream order).
   void signal_ready(uint32_t g, uint32_t seq) override {
     drain_reads();
-    if (!verify_) {
+    if (!verify_ && !hsa_) {
       hip_check(hipStreamWriteValue32(s_[kDem], ready_ + g, seq, 0), "hipStreamWriteValue32 (ready)");
       return;
     }
-    hipEvent_t ev = next_vev();  // the layer's cover waits and copies, all on kDem
-    ev_record(ev, s_[kDem]);
-    stream_wait(vs_, ev);
+    if (hsa_) {  // the layer's cover waits and copies, all on kDem's lane
+      hold(vsigs_, tail_[kDem]);
+    } else {
+      hipEvent_t ev = next_vev();
+      ev_record(ev, s_[kDem]);
+      vafter_.push_back(ev);
+    }
     if (vpending_) {  // the layer's last check writes the ready word when it has published its units
       vlaunch_.ready = ready_;
       vlaunch_.ready_g = g;
@@ -467,21 +588,111 @@ class HipTransport final : public DgTransport {
       flush_verify();
       vlaunch_.ready = nullptr;
     } else {
-      hip_check(hipStreamWriteValue32(vs_, ready_ + g, seq, 0), "hipStreamWriteValue32 (ready)");
+      Check c;
+      c.kind = Check::kReady;
+      c.after.swap(vafter_);
+      c.sigs.swap(vsigs_);
+      c.g = g;
+      c.seq = seq;
+      checks_.push_back(std::move(c));
+      poll_checks();
     }
   }
-  void* event_create() override { return dev_->event_create(); }
-  void event_destroy(void* ev) override { dev_->event_destroy(static_cast<hipEvent_t>(ev)); }
-  void record(void* ev, Stream s) override { ev_record(static_cast<hipEvent_t>(ev), s_[s]); }
-  void wait(Stream s, void* ev) override { stream_wait(s_[s], static_cast<hipEvent_t>(ev)); }
+  struct Mark {
+    std::vector<uint32_t> sigs;
+  };
+  void* event_create() override { return hsa_ ? static_cast<void*>(new Mark) : dev_->event_create(); }
+  void event_destroy(void* ev) override {
+    if (!hsa_) return dev_->event_destroy(static_cast<hipEvent_t>(ev));
+    if (Mark* m = static_cast<Mark*>(ev)) {
+      drop(m->sigs);
+      delete m;
+    }
+  }
+  void record(void* ev, Stream s) override {
+    if (hsa_) {
+      Mark* m = static_cast<Mark*>(ev);
+      drop(m->sigs);
+      hold(m->sigs, tail_[s]);
+      return;
+    }
+    if (s == kD2h) d2h_ready();
+    ev_record(static_cast<hipEvent_t>(ev), s_[s]);
+  }
+  void wait(Stream s, void* ev) override {
+    if (hsa_) return hold(tail_[s], static_cast<Mark*>(ev)->sigs);
+    gate(s, static_cast<hipEvent_t>(ev));
+  }
   bool done(void* ev) override {  // the canonical schedule: a completion query waits for the completion
-    ev_sync(static_cast<hipEvent_t>(ev));
+    event_sync(ev);
     return true;
   }
-  bool query(void* ev) override { return ev_done(static_cast<hipEvent_t>(ev)); }
-  void event_sync(void* ev) override { ev_sync(static_cast<hipEvent_t>(ev)); }
-  void sync(Stream s) override { stream_sync(s_[s]); }
+  bool query(void* ev) override {
+    return hsa_ ? all_done(static_cast<Mark*>(ev)->sigs) : ev_done(static_cast<hipEvent_t>(ev));
+  }
+  void event_sync(void* ev) override {
+    if (hsa_) return host_wait(static_cast<Mark*>(ev)->sigs);
+    ev_sync(static_cast<hipEvent_t>(ev));
+  }
+  void sync(Stream s) override {
+    if (hsa_) {  // the lane's copies, then (a copy-in lane) the queued value writes behind them
+      host_wait(tail_[s]);
+      if (s != kD2h) {
+        drain_checks();
+        stream_sync(queue_stream());
+      }
+      return;
+    }
+    if (s == kD2h) d2h_ready();
+    stream_sync(s_[s]);
+  }
+  // ---- lanes (HSA copies) ----
+  // Adds the signals of `sigs` still running to `into`, with a reference each.
+  void hold(std::vector<uint32_t>& into, const std::vector<uint32_t>& sigs) {
+    for (uint32_t g : sigs)
+      if (!hsa_->done(g)) {
+        hsa_->ref(g);
+        into.push_back(g);
+      }
+  }
+  void drop(std::vector<uint32_t>& sigs) {
+    for (uint32_t g : sigs) hsa_->unref(g);
+    sigs.clear();
+  }
+  bool all_done(const std::vector<uint32_t>& sigs) const {
+    for (uint32_t g : sigs)
+      if (!hsa_->done(g)) return false;
+    return true;
+  }
+  // One copy on lane s after the lane's tail and up to two more signals; it becomes the lane's tail.
+  uint32_t lane_copy(Stream s, void* dst, const void* src, uint64_t bytes, bool to_host, uint32_t also = 0,
+                     uint32_t also2 = 0) {
+    std::vector<uint32_t>& t = tail_[s];
+    deps_.assign(t.begin(), t.end());
+    if (also) deps_.push_back(also);
+    if (also2) deps_.push_back(also2);
+    const uint32_t sig = hsa_->copy(dst, src, bytes, to_host, deps_.data(), uint32_t(deps_.size()));
+    drop(t);
+    t.push_back(sig);  // (the copy's own reference)
+    return sig;
+  }
+  // On the host until every signal has ended; the service thread launches the checks whose copies land meanwhile.
+  void host_wait(const std::vector<uint32_t>& sigs) {
+    const bool svc = std::this_thread::get_id() == service_thread_;
+    for (uint32_t spins = 0; !all_done(sigs); ++spins) {
+      if (svc) poll_checks();
+      if (svc || spins < 4096) _mm_pause();
+      else std::this_thread::yield();
+    }
+  }
+  // The HIP stream of the queue's value writes and launches: the verify stream, else (HSA copies without device
+  // verify) the demand stream's, which then carries no copy.
+  hipStream_t queue_stream() const { return vs_ ? vs_ : s_[kDem]; }
   void upload_table(const int32_t* table, uint32_t n) override {
+    if (hsa_) {  // no queued entry write may land after the table
+      drain_checks();
+      stream_sync(queue_stream());
+    }
     std::memcpy(stage_host_, table, 4ull * n);
     copy_h2d(slot_of_, stage_host_, 4ull * n, s_[kDem]);
     stream_sync(s_[kDem]);
@@ -530,9 +741,13 @@ class HipTransport final : public DgTransport {
     if (!verify_ || n == 0) return;
     require(vused_ + n <= vcap_, SS_E_BACKEND, "device verify: more landed units in a token than the table holds");
     flush_verify();
-    hipEvent_t landed_ev = next_vev();
-    ev_record(landed_ev, s_[s]);
-    stream_wait(vs_, landed_ev);
+    if (hsa_) {
+      hold(vsigs_, tail_[s]);
+    } else {
+      hipEvent_t landed_ev = next_vev();
+      ev_record(landed_ev, s_[s]);
+      vafter_.push_back(landed_ev);
+    }
     for (uint32_t i0 = 0; i0 < n; i0 += kDgVerifyMax) {
       if (i0) flush_verify();
       DgVerifyLaunch& a = vlaunch_;
@@ -550,14 +765,61 @@ class HipTransport final : public DgTransport {
     }
     if (s != kDem) flush_verify();  // a prefetch's check carries no ready word
   }
+  // The check of the units gathered in vlaunch_ joins the queue of checks, behind the events of their copies.
   void flush_verify() {
     if (!vpending_) return;
     vpending_ = false;
-    const DgVerifyLaunch& a = vlaunch_;
-    // timed by the launch's own start / stop events (the kernel's begin and end, not the queue around it)
-    Timed t = prof_take(kProfVerify, uint64_t(a.n) * x_.unit_bytes, a.n);
-    hip_check(hipError_t(launch_dg_verify(a, vs_, t.a, t.b)), "device verify launch");
-    prof_put(t);
+    Check c;
+    c.after.swap(vafter_);
+    c.sigs.swap(vsigs_);
+    c.launch = vlaunch_;
+    checks_.push_back(std::move(c));
+    poll_checks();
+  }
+  // The queue of checks, launched in order from the host: the head goes once every event and copy signal it waits for
+  // has completed, so its stream never holds a device barrier. A ready word without a check of its own is a value
+  // write in the same order, as is (HSA copies) a slot entry; a timing mark is an event record. Called by the service
+  // thread (while it waits, and before a token is marked served) and at the boundary.
+  struct Check {
+    enum Kind { kLaunch, kReady, kMark, kEntry } kind = kLaunch;
+    std::vector<hipEvent_t> after;
+    std::vector<uint32_t> sigs;  // (HSA copies) with a reference each
+    DgVerifyLaunch launch;
+    uint32_t g = 0, seq = 0;
+    hipEvent_t mark = nullptr;
+    uint32_t key = 0;
+    int32_t v = 0;
+  };
+  bool poll_checks() {
+    poll_wb_marks();
+    while (!checks_.empty()) {
+      Check& c = checks_.front();
+      while (!c.after.empty() && ev_done(c.after.back())) c.after.pop_back();
+      if (!c.after.empty()) return false;
+      while (!c.sigs.empty() && hsa_->done(c.sigs.back())) {
+        hsa_->unref(c.sigs.back());
+        c.sigs.pop_back();
+      }
+      if (!c.sigs.empty()) return false;
+      const hipStream_t q = queue_stream();
+      if (c.kind == Check::kLaunch) {
+        // timed by the launch's own start / stop events (the kernel's begin and end, not the queue around it)
+        Timed t = prof_take(kProfVerify, uint64_t(c.launch.n) * x_.unit_bytes, c.launch.n);
+        hip_check(hipError_t(launch_dg_verify(c.launch, vs_, t.a, t.b)), "device verify launch");
+        prof_put(t);
+      } else if (c.kind == Check::kReady) {
+        hip_check(hipStreamWriteValue32(q, ready_ + c.g, c.seq, 0), "hipStreamWriteValue32 (ready)");
+      } else if (c.kind == Check::kEntry) {
+        hip_check(hipStreamWriteValue32(q, slot_of_ + c.key, uint32_t(c.v), 0), "hipStreamWriteValue32 (slot entry)");
+      } else {
+        ev_record(c.mark, q);
+      }
+      checks_.pop_front();
+    }
+    return true;
+  }
+  void drain_checks() {
+    while (!poll_checks()) _mm_pause();
   }
   // A small device-to-host read on the demand stream (between tokens), not on the null stream.
   void read_device(void* dst, const void* src, uint64_t bytes) {
@@ -567,6 +829,7 @@ class HipTransport final : public DgTransport {
   // Before the boundary may reuse a slot: every check of this token has read its bytes.
   void verify_sync() {
     flush_verify();  // (every demand landing is followed by its layer's signal_ready: nothing should be pending)
+    drain_checks();
     if (vs_) stream_sync(vs_);
   }
   // At the boundary: the keys whose landed bytes differ from their descriptor hash.
@@ -595,6 +858,8 @@ class HipTransport final : public DgTransport {
     drain_locked(true);
     prof_mask_ = on == 1 ? (TSA_TEST_PROF_COPY | TSA_TEST_PROF_WRITEBACK | TSA_TEST_PROF_VERIFY) : uint32_t(on);
     prof_tot_ = tsa_test_profile{};
+    // HSA copies are timed by the copy engine's own timestamps (start to end of each part)
+    if (hsa_) hsa_->profiling((prof_mask_ & (TSA_TEST_PROF_COPY | TSA_TEST_PROF_WRITEBACK)) != 0);
   }
   tsa_test_profile profile_read(bool wait) {
     std::lock_guard<std::mutex> lk(prof_mu_);
@@ -612,10 +877,22 @@ class HipTransport final : public DgTransport {
   enum ProfKind : uint32_t { kProfCopy, kProfWb, kProfVerify };
   struct Timed {
     hipEvent_t a = nullptr, b = nullptr;
+    uint32_t sig = 0;  // (HSA copies) the copy's signal, referenced, instead of the events
     ProfKind kind = kProfCopy;
     uint64_t bytes = 0;
     uint32_t units = 0;
   };
+  void prof_copy(ProfKind k, uint32_t sig, uint64_t bytes, uint32_t units) {
+    std::lock_guard<std::mutex> lk(prof_mu_);
+    if (!(prof_mask_ & prof_bit(k))) return;
+    Timed t;
+    t.sig = sig;
+    t.kind = k;
+    t.bytes = bytes;
+    t.units = units;
+    hsa_->ref(sig);
+    pending_.push_back(t);
+  }
   hipEvent_t take_event_locked() {
     if (prof_free_.empty()) {
       prof_events_.push_back(dev_->event_create_timed());
@@ -666,14 +943,25 @@ class HipTransport final : public DgTransport {
   void drain_locked(bool wait) {
     size_t keep = 0;
     for (const Timed& t : pending_) {
-      if (wait) ev_sync(t.b);
-      else if (!ev_done(t.b)) {
-        pending_[keep++] = t;
-        continue;
+      uint64_t ns = 0;
+      if (t.sig) {
+        if (!wait && !hsa_->done(t.sig)) {
+          pending_[keep++] = t;
+          continue;
+        }
+        while (!hsa_->done(t.sig)) std::this_thread::yield();
+        (void)hsa_->copy_ns(t.sig, &ns);
+        hsa_->unref(t.sig);
+      } else {
+        if (wait) ev_sync(t.b);
+        else if (!ev_done(t.b)) {
+          pending_[keep++] = t;
+          continue;
+        }
+        float ms = 0.0f;
+        hip_check(hipEventElapsedTime(&ms, t.a, t.b), "hipEventElapsedTime");
+        ns = uint64_t(double(ms) * 1e6 + 0.5);
       }
-      float ms = 0.0f;
-      hip_check(hipEventElapsedTime(&ms, t.a, t.b), "hipEventElapsedTime");
-      const uint64_t ns = uint64_t(double(ms) * 1e6 + 0.5);
       switch (t.kind) {
         case kProfCopy:
           prof_tot_.copies += t.units;  // a unit's first part counts the unit
@@ -681,7 +969,7 @@ class HipTransport final : public DgTransport {
           prof_tot_.copy_ns += ns;
           break;
         case kProfWb:
-          ++prof_tot_.writebacks;
+          prof_tot_.writebacks += t.units;  // (a unit copied out whole counts once, at its first part)
           prof_tot_.writeback_bytes += t.bytes;
           prof_tot_.writeback_ns += ns;
           break;
@@ -692,8 +980,10 @@ class HipTransport final : public DgTransport {
           prof_tot_.verify_ns += ns;
           break;
       }
-      prof_free_.push_back(t.a);
-      prof_free_.push_back(t.b);
+      if (t.a) {
+        prof_free_.push_back(t.a);
+        prof_free_.push_back(t.b);
+      }
     }
     pending_.resize(keep);
   }
@@ -723,6 +1013,17 @@ class HipTransport final : public DgTransport {
   bool verify_ = false;
   DgVerifyLaunch vlaunch_;            // the next launch (arena, shape, checkpoints, gate and publication words fixed)
   bool vpending_ = false;             // vlaunch_ holds units whose check is not launched yet
+  std::vector<hipEvent_t> vafter_;    // the copies the next queued check (or ready word) waits for
+  std::deque<Check> checks_;          // queued checks, ready words and marks, in verify-stream order
+  std::vector<hipEvent_t> d2h_waits_; // waits of the D2H stream kept until its next operation
+  std::unique_ptr<HsaCopier> hsa_;    // unit copies through the HSA runtime (null: on the HIP streams)
+  std::vector<uint32_t> tail_[3];     // (HSA copies) per lane: what its next operation waits for
+  std::vector<uint32_t> deps_;        // (HSA copies) a copy's dependencies, reused
+  std::vector<uint32_t> vsigs_;       // (HSA copies) the copies the next queued check (or ready word) waits for
+  std::vector<uint32_t> part_sig_;    // (HSA copies) as part_ev_: the last write-back copy of each part (0: none)
+  std::vector<uint32_t> wb_sigs_[2];  // (HSA copies, dg_diag) the boundary's write-backs, until seen ended
+  bool wb_seen_[2] = {true, true};
+  std::thread::id service_thread_;
   uint32_t* vcount_dev_ = nullptr;    // the launches' publication counter
   uint64_t* digests_dev_ = nullptr;   // [keys]: the descriptor hashes
   uint32_t vcap_ = 0, vused_ = 0;
@@ -1295,6 +1596,7 @@ class HipDgCtx final : public DgCtx {
     return uint32_t(t.size());
   }
   uint64_t verify_failures() const override { return verify_failures_; }
+  bool hsa_copies() const override { return tr_ && tr_->hsa_copies(); }
 
   void profile_enable(int on) override {
     require(!in_token_, SS_E_INVALID, "tsa_test_profile_enable: between tokens only");
@@ -1529,6 +1831,10 @@ void HipDgCtx::init() {
   }
   tr_ = std::make_unique<HipTransport>(dev_.get(), x_, arena_, slot_of_dev_, dw_.ready, block_chunks_, per_chunk_,
                                        G * x_.B + o_.dg_prefetch_per_token + x_.D);
+  // unit copies through the HSA runtime, except with the file tier or small parts (staged and scattered) and unless
+  // TSA_DG_COPIES=hip asks for the HIP streams' copies
+  const char* copies = std::getenv("TSA_DG_COPIES");
+  if (!x_.disk_tier && !(copies && std::strcmp(copies, "hip") == 0)) tr_->enable_hsa_copies(o_.device);
   DgConfig c;
   for (int L : x_.gated) c.n_units.push_back(uint32_t(d_.layers[size_t(L)].n_units));
   c.persistent_slots = x_.persistent_slots;
@@ -1620,7 +1926,9 @@ void HipDgCtx::init() {
     svc_->enable_timeline();
     diag_rows_.assign(G, LayerDiag{});
   }
+  svc_->set_hooks({[this] { tr_->poll_checks(); }, [this] { tr_->drain_checks(); }});
   svc_->start();
+  tr_->set_service_thread(svc_->thread_id());
 }
 
 // The stats-v1 document of a device-gated context (reference src/dg_ctx.cpp:1359-1545): the host contract's keys, the

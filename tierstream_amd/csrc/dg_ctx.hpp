@@ -53,6 +53,7 @@ class DgCtx {
   virtual bool snapshot_json(Json* out) const = 0;
   virtual uint32_t host_table(int32_t* out, uint32_t cap) const = 0;
   virtual uint64_t verify_failures() const = 0;
+  virtual bool hsa_copies() const = 0;  // unit copies through the HSA runtime (else the HIP streams)
   // measurement hooks (tsa_test.h)
   virtual void profile_enable(int on) = 0;
   virtual tsa_test_profile profile_read(bool wait) = 0;

@@ -135,6 +135,7 @@ void DgService::await_flag(const uint32_t* w, uint32_t seq, uint32_t g, const ch
   for (;;) {
     const uint32_t v = load_acquire(w);
     if (v == seq) return;
+    if (hooks_.while_waiting) hooks_.while_waiting();
     if (last && v != *last)
       fail(SS_E_BACKEND, "device-gated: sequence desync: the " + std::string(what) + " of " + layer_name(g) +
                              " reads " + std::to_string(v) + ", neither token " + std::to_string(seq) +
@@ -189,6 +190,7 @@ void DgService::serve(uint32_t seq) {
   core_->open_token(seq, &run_);
   await_began(seq);  // every flag's deadline starts once the step has begun
   for (size_t i = 0; i < plan_.size(); ++i) serve_layer(seq, plan_[i], i + 1 < plan_.size() ? plan_[i + 1] : G_);
+  if (hooks_.before_served) hooks_.before_served();
   last_end_ = Clock::now();
 }
 

@@ -15,6 +15,7 @@
 #include <atomic>
 #include <chrono>
 #include <cstdint>
+#include <functional>
 #include <mutex>
 #include <string>
 #include <thread>
@@ -40,6 +41,14 @@ class DgService {
   DgService(const DgService&) = delete;
   DgService& operator=(const DgService&) = delete;
 
+  // The transport's work on the service thread: between two polls of a mapped word (queued device checks whose copies
+  // have landed are launched), and after a token's last layer, before it counts as served (every queued check
+  // launched: each layer's ready word depends on one).
+  struct Hooks {
+    std::function<void()> while_waiting, before_served;
+  };
+  std::thread::id thread_id() const { return th_.get_id(); }
+  void set_hooks(Hooks h) { hooks_ = std::move(h); }
   void enable_timeline();
   const std::vector<Row>& timeline() const { return rows_; }  // between tokens only (ordered by the outcome word)
   void start();
@@ -69,6 +78,7 @@ class DgService {
   void await_began(uint32_t seq);
 
   DgCore* core_;
+  Hooks hooks_;
   DgMappedHost m_;
   uint32_t max_ids_;
   std::chrono::milliseconds timeout_;

@@ -140,8 +140,14 @@ __global__ __launch_bounds__(256) void digest_kernel(const TsaUnit* __restrict__
   if (live && q == 0) out[u] = xfinal(all, total, tail, tail_len);
 }
 
+// Both verify kernels are held to 8 waves per SIMD (at most 64 VGPRs): unbounded, the compiler spends registers on
+// scheduling (83-86 VGPRs, 5 waves per SIMD) and the kernel has 5/8 of the loads in flight it could; bounded it needs
+// 52-58 with no spill, and one 336 MiB unit's check (3 parts, 2 KiB segments, timed alone in a fresh process) ran
+// 67 -> 62 us.
+#define TSA_VERIFY_BOUNDS __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8)))
+
 // One (unit, segment) per quad. seg_first is the prefix sum of segments over the launch's units (ascending).
-__global__ __launch_bounds__(256) void verify_kernel(const TsaVerifyUnit* __restrict__ units, uint32_t n_units,
+__global__ TSA_VERIFY_BOUNDS void verify_kernel(const TsaVerifyUnit* __restrict__ units, uint32_t n_units,
                                                      uint64_t n_segments, uint64_t seg_bytes,
                                                      uint32_t* __restrict__ fail) {
   const uint64_t gid = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -211,7 +217,7 @@ __global__ __launch_bounds__(256) void verify_kernel(const TsaVerifyUnit* __rest
 }
 
 // Device-gated verify: one quad per (unit, segment) of the launch's units, all of the arena's part shape.
-__global__ __launch_bounds__(256) void dg_verify_kernel(const DgVerifyLaunch a) {
+__global__ TSA_VERIFY_BOUNDS void dg_verify_kernel(const DgVerifyLaunch a) {
   const uint64_t gid = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const uint64_t s = gid >> 2;
   const uint32_t q = uint32_t(gid & 3u);

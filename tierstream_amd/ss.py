@@ -233,6 +233,7 @@ def _declare() -> C.CDLL:
         "tsa_test_region_of": (st, [vp, u64, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(u64)]),
         "tsa_test_dg_table": (st, [vp, C.POINTER(i32), u32, C.POINTER(u32)]),
         "tsa_test_verify_failures": (u64, [vp]),
+        "tsa_test_dg_hsa_copies": (C.c_int, [vp]),
         "tsa_test_host_copies": (st, [vp, C.POINTER(u64), C.POINTER(u64)]),
         "tsa_test_profile_enable": (st, [vp, C.c_int]),
         "tsa_test_profile_read": (st, [vp, C.c_int, C.POINTER(TsaTestProfile)]),
@@ -513,6 +514,10 @@ class Ctx:
 
     def verify_failures(self) -> int:
         return int(_declare().tsa_test_verify_failures(self.h))
+
+    def hsa_copies(self) -> bool:
+        """Device-gated: whether unit copies go through the HSA runtime's copy engines (else HIP streams)."""
+        return bool(_declare().tsa_test_dg_hsa_copies(self.h))
 
     def host_copies(self) -> tuple[int, int]:
         """Host contract: (unit copies from pinned blocks since open, the copies they were issued as)."""
