@@ -96,6 +96,9 @@ def parse():
     ap.add_argument("--landing-ttl", type=int, default=0, help="three tiers: dg_landing_ttl")
     ap.add_argument("--landing-max-queued", type=int, default=0, help="three tiers: dg_landing_max_queued")
     ap.add_argument("--landing-chunk", type=int, default=0, help="three tiers: dg_landing_chunk")
+    ap.add_argument("--copies", default="hsa", choices=["hsa", "hip"],
+                    help="device-gated unit copies: through the HSA runtime's copy engines (the library's default "
+                         "where parts are copied whole) or on HIP streams (TSA_DG_COPIES=hip)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the copy peaks and the library's HBM kernels alone (no serve loop: for counter runs)")
     return ap.parse_args()
@@ -443,7 +446,10 @@ def main():
             extra.update(dg_landing_blocks=a.landing_blocks, dg_landing_ttl=a.landing_ttl,
                          dg_landing_max_queued=a.landing_max_queued, dg_landing_chunk=a.landing_chunk)
         opts = {**shape.options, **extra}
+        os.environ["TSA_DG_COPIES"] = a.copies  # (read by the open)
         ctx = keep(ss.Ctx(d, b, plan, ss.options(**opts, verify_hash=2, dg_wait_timeout_ms=20000, policy=policy)))
+        os.environ.pop("TSA_DG_COPIES", None)
+        copies = "hsa" if ctx.hsa_copies() else "hip"
         open_s = time.time() - t0
         log(f"context open (fill + hash check) in {open_s:.1f} s")
         n_pred = shape.B if a.predict > 0 else 0
@@ -570,6 +576,7 @@ def main():
                                    + (f"; {w.layers} of the full model's {W.WORKLOADS[w.name].layers} layers"
                                       if w.layers != W.WORKLOADS[w.name].layers else ""),
                        "policy": a.policy,
+                       "copies": copies,
                        "options": {k: v for k, v in extra.items()},
                        "predict": a.predict,
                        "residency": f"{n_res} of {w.n_units} units resident ({100 * n_res / w.n_units:.0f} %); device "
