@@ -373,15 +373,19 @@ def test_zero_miss_token_needs_no_copy(tmp_path, gpu):
         ctx.close()
 
 
-def test_device_check_gates_a_corrupted_unit(tmp_path, gpu):
+@pytest.mark.parametrize("path", ["staged", "hsa", "hip"])
+def test_device_check_gates_a_corrupted_unit(tmp_path, gpu, path):
     """verify_hash = 2 gates what the engine reads: a unit whose pinned copy was corrupted lands, its device check
     fails, and the check raises the token's abort before the layer's ready word. Every read of the token from then on
     resolves to the zeroed guard slot (checksum 0), the layers before it read their true bytes, the token fails with
-    SS_E_HASH naming the unit, and the context is poisoned."""
-    m, bkw, okw = _setup(tmp_path, 4, 8, [64 * KiB] * 3, 12, 1, 6, 2)
+    SS_E_HASH naming the unit, and the context is poisoned. staged: small parts, checked inside their scatter; hsa /
+    hip: one part copied whole through the HSA runtime / a HIP stream and checked on the verify stream."""
+    parts = [64 * KiB] * 3 if path == "staged" else [256 * KiB]
+    m, bkw, okw = _setup(tmp_path, 4, 8, parts, 12, 1, 6, 2)
     d = ss.Desc(m.desc_json())
     plan = ss.Plan(d, ss.budget(**bkw))
-    ctx = ss.Ctx(d, ss.budget(**bkw), plan, ss.options(**okw))
+    ctx = _open(d, bkw, plan, okw, path == "hip")
+    assert ctx.hsa_copies() == (path == "hsa")
     eng = ss.DgEngine(ctx, 2, use_graph=True)
     try:
         table = ctx.dg_table().reshape(4, 8)

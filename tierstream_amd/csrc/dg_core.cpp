@@ -741,7 +741,7 @@ bool DgCore::bring_in(uint32_t g, uint32_t u, bool ahead) {
     t_->wait_copy_in(s, slot, src, ev_.on_slot(slot), nullptr);  // (the block's own write-back ended above)
     ev_.untie_slot(slot);
     if (kept >= 0) ev_.untie_block(kept);
-    t_->h2d(s, slot, src);
+    t_->h2d(s, slot, src, k);
     if (kept >= 0) {  // the block is the key's: its pinned home when the bank releases it
       x.block = kept;
       x.home_middle = c_.bank_keep == 2;
@@ -760,7 +760,7 @@ bool DgCore::bring_in(uint32_t g, uint32_t u, bool ahead) {
     const int32_t lb = land_block(x.land);
     t_->wait_copy_in(s, slot, lb, ev_.on_slot(slot), nullptr);
     ev_.untie_slot(slot);
-    t_->h2d(s, slot, lb);
+    t_->h2d(s, slot, lb, k);
     land_busy_.push_back(x.land);  // free at the next landing or boundary (the transport orders the reuse)
     land_owner_[size_t(x.land)] = kNoKey;
     x.land = -1;
@@ -772,7 +772,7 @@ bool DgCore::bring_in(uint32_t g, uint32_t u, bool ahead) {
     t_->wait_copy_in(s, slot, x.block, ev_.on_slot(slot), ev_.on_block(x.block));
     ev_.untie_slot(slot);
     ev_.untie_block(x.block);
-    t_->h2d(s, slot, x.block);
+    t_->h2d(s, slot, x.block, k);
     leave_pinned(k);
   }
   publish(s, k, slot, true);

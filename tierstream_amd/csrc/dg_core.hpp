@@ -32,7 +32,7 @@ class DgTransport {
  public:
   enum Stream { kDem = 0, kPf = 1, kD2h = 2 };
   virtual ~DgTransport() = default;
-  virtual void h2d(Stream s, int32_t slot, int32_t block) = 0;  // every part, host block -> slot
+  virtual void h2d(Stream s, int32_t slot, int32_t block, uint32_t key) = 0;  // every part of key's unit, block -> slot
   virtual void d2h(int32_t slot, int32_t block) = 0;            // every part, slot -> block, on kD2h
   virtual void d2h_part(Stream s, int32_t slot, int32_t block, uint32_t part) = 0;
   virtual uint32_t parts() const = 0;

@@ -22,7 +22,7 @@ class EagerTransport final : public DgTransport {
  public:
   explicit EagerTransport(std::vector<uint64_t> parts) : parts_(std::move(parts)) {}
   ~EagerTransport() override = default;
-  void h2d(Stream, int32_t, int32_t) override {}
+  void h2d(Stream, int32_t, int32_t, uint32_t) override {}
   void d2h(int32_t, int32_t) override {}
   void d2h_part(Stream, int32_t, int32_t, uint32_t) override {}
   uint32_t parts() const override { return uint32_t(parts_.size()); }

@@ -265,7 +265,7 @@ class HipTransport final : public DgTransport {
       hold(c.sigs, tail_[kDem]);
       checks_.push_back(std::move(c));
       poll_checks();
-    } else if (verify_ || hsa_) {  // after the layer's ready word, in the order of the checks
+    } else if ((verify_ && !fused()) || hsa_) {  // after the layer's ready word, in the order of the checks
       Check c;
       c.kind = Check::kMark;
       c.mark = dma_b_[g];
@@ -369,8 +369,8 @@ class HipTransport final : public DgTransport {
     wait_slot_ = slot_ev ? slot : -1;
     wait_block_ = block_ev ? block : -1;
   }
-  void h2d(Stream s, int32_t slot, int32_t block) override {
-    h2d_unit(s, slot, block);
+  void h2d(Stream s, int32_t slot, int32_t block, uint32_t key) override {
+    h2d_unit(s, slot, block, key);
     wait_slot_ = wait_block_ = -1;
     if (landing_block(block)) {  // the block's next landing read waits for this copy
       hipEvent_t& e = land_copy_ev_[size_t(uint32_t(block) - x_.blocks - x_.S)];
@@ -410,7 +410,7 @@ class HipTransport final : public DgTransport {
     d2h_waits_.clear();
   }
   void set_service_thread(std::thread::id id) { service_thread_ = id; }
-  void h2d_unit(Stream s, int32_t slot, int32_t block) {
+  void h2d_unit(Stream s, int32_t slot, int32_t block, uint32_t key) {
     const char* src = block_ptr(block);
     if (hsa_) {  // part by part on the lane, each after the same part of the write-backs named by wait_copy_in
       for (uint32_t p = 0; p < uint32_t(x_.part_bytes.size()); ++p) {
@@ -468,6 +468,11 @@ class HipTransport final : public DgTransport {
     Timed t = prof_start(kProfCopy, x_.unit_bytes, 1, s_[s]);
     copy_h2d(stage_dev_[k], src, x_.unit_bytes, s_[s]);
     for (uint32_t p = 0; p < P; ++p) part_wait(s, slot, -1, p);   // the scatter writes every part of the slot
+    if (fused()) {  // with device verify, the scatter is the check: the staged bytes cross HBM once each way
+      scatter_check(s, k, slot, key);
+      prof_end(t, s_[s]);
+      return;
+    }
     const uint32_t j = job_next_[k]++ % kJobRing;
     tsa_scatter_job& job = jobs_host_[k][j];
     std::memset(&job, 0, sizeof job);
@@ -482,6 +487,26 @@ class HipTransport final : public DgTransport {
     hip_check(hipError_t(launch_scatter(jobs_dev_[k] + j, 1, scatter_blocks_, s_[s])), "scatter launch");
     prof_end(t, s_[s]);
   }
+  // The staged unit in staging buffer k into `slot`, hashed on the way against its checkpoints and digest, on the
+  // copy's stream: a mismatch raises the token's abort; the last workgroup publishes the unit's slot entry.
+  void scatter_check(Stream s, int k, int32_t slot, uint32_t key) {
+    require(vused_ + 1 <= vcap_, SS_E_BACKEND, "device verify: more landed units in a token than the table holds");
+    DgVerifyLaunch a = vlaunch_;  // (the shape, checkpoints, digests and abort words)
+    a.n = 1;
+    a.keys[0] = key;
+    a.slots[0] = slot;
+    a.fail = vfail_dev_ + vused_;
+    a.aux = gated_of(key);
+    a.ready = nullptr;
+    a.done_count = vcount_dev_ + 1 + k;  // (the launches of one stream share a count)
+    Timed t = prof_take(kProfVerify, x_.unit_bytes, 1);
+    hip_check(hipError_t(launch_dg_scatter_verify(a, stage_dev_[k], s_[s], t.a, t.b)), "scatter check launch");
+    prof_put(t);
+    vkeys_.push_back(key);
+    ++vused_;
+  }
+  // Device verify of staged units happens in their scatter (no launch on the verify stream).
+  bool fused() const { return scatter_ && verify_; }
   void d2h(int32_t slot, int32_t block) override {
     if (hsa_) {
       for (uint32_t p = 0; p < parts(); ++p) hsa_d2h_part(kD2h, slot, block, p, p == 0 ? 1 : 0);
@@ -570,7 +595,9 @@ class HipTransport final : public DgTransport {
   // behind the checks of every unit landed so far in the token (its stream order).
   void signal_ready(uint32_t g, uint32_t seq) override {
     drain_reads();
-    if (!verify_ && !hsa_) {
+    // (fused checks: every check of the layer ran on the demand stream before this, or on the prefetch stream before
+    // an event the demand stream waited for)
+    if ((!verify_ || fused()) && !hsa_) {
       hip_check(hipStreamWriteValue32(s_[kDem], ready_ + g, seq, 0), "hipStreamWriteValue32 (ready)");
       return;
     }
@@ -738,7 +765,7 @@ class HipTransport final : public DgTransport {
   // A landed unit's check is launched once the next landed() or the layer's signal_ready() comes (the service issues
   // them back to back), so the layer's last check can carry the ready word; each waits for its own unit's copies.
   void landed(Stream s, uint32_t g, const uint32_t* keys, const int32_t* slots, uint32_t n) override {
-    if (!verify_ || n == 0) return;
+    if (!verify_ || n == 0 || fused()) return;  // (fused: checked and published by the unit's scatter)
     require(vused_ + n <= vcap_, SS_E_BACKEND, "device verify: more landed units in a token than the table holds");
     flush_verify();
     if (hsa_) {
@@ -831,6 +858,10 @@ class HipTransport final : public DgTransport {
     flush_verify();  // (every demand landing is followed by its layer's signal_ready: nothing should be pending)
     drain_checks();
     if (vs_) stream_sync(vs_);
+    if (fused()) {  // the checks ran on the copy streams
+      stream_sync(s_[kDem]);
+      stream_sync(s_[kPf]);
+    }
   }
   // At the boundary: the keys whose landed bytes differ from their descriptor hash.
   std::vector<uint32_t> collect_verify() {

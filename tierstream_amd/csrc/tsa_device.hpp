@@ -87,6 +87,10 @@ int launch_verify(const TsaVerifyUnit* units_dev, uint32_t n_units, uint64_t n_s
                   uint32_t* fail_dev, hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 // start / stop (timing events, or null): recorded with the kernel's own begin and end (hipExtLaunchKernelGGL).
 int launch_dg_verify(const DgVerifyLaunch& a, hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+// The staged units' fused scatter and check: unit i's parts lie back to back at src + i x unit_bytes (HBM staging);
+// each is written to its arena slot while it is hashed, with the same checks and publication as launch_dg_verify.
+int launch_dg_scatter_verify(const DgVerifyLaunch& a, const void* src, hipStream_t stream, hipEvent_t start = nullptr,
+                             hipEvent_t stop = nullptr);
 int launch_scatter(const TsaScatterJob* jobs_dev, uint32_t n_jobs, uint64_t n_blocks, hipStream_t stream);
 int launch_synth(void* dst, uint64_t bytes, uint64_t seed, uint64_t stream_id, uint64_t offset, uint32_t kind,
                  float sigma, hipStream_t stream);

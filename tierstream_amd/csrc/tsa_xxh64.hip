@@ -85,19 +85,36 @@ __device__ uint64_t xfinal(const uint64_t v[4], uint64_t total, const unsigned c
 // (coalesced 16-byte loads into LDS, chains run from LDS) beat it.
 constexpr int kBlock = 16;
 typedef __attribute__((address_space(1))) const uint64_t gword_t;
+typedef __attribute__((address_space(1))) uint64_t gout_t;
 
-__device__ __forceinline__ uint64_t chain(uint64_t v, const unsigned char* p, uint64_t n, uint32_t q) {
+// kCopy: each word read is also stored at the same offset from d (the staged unit's bytes into their arena slot while
+// they are hashed: the bytes cross HBM once each way).
+template <bool kCopy>
+__device__ __forceinline__ uint64_t chain_t(uint64_t v, const unsigned char* p, unsigned char* d, uint64_t n,
+                                            uint32_t q) {
   gword_t* w = reinterpret_cast<gword_t*>(reinterpret_cast<uintptr_t>(p)) + q;
+  gout_t* o = reinterpret_cast<gout_t*>(reinterpret_cast<uintptr_t>(d)) + q;
   uint64_t s = 0;
   for (; s + kBlock <= n; s += kBlock) {
     uint64_t buf[kBlock];
 #pragma unroll
     for (int k = 0; k < kBlock; ++k) buf[k] = w[4 * (s + k)];
+    if (kCopy) {
+#pragma unroll
+      for (int k = 0; k < kBlock; ++k) o[4 * (s + k)] = buf[k];
+    }
 #pragma unroll
     for (int k = 0; k < kBlock; ++k) v = xround(v, buf[k]);
   }
-  for (; s < n; ++s) v = xround(v, w[4 * s]);
+  for (; s < n; ++s) {
+    const uint64_t x = w[4 * s];
+    if (kCopy) o[4 * s] = x;
+    v = xround(v, x);
+  }
   return v;
+}
+__device__ __forceinline__ uint64_t chain(uint64_t v, const unsigned char* p, uint64_t n, uint32_t q) {
+  return chain_t<false>(v, p, nullptr, n, q);
 }
 
 __device__ __forceinline__ void init_acc(uint64_t v[4]) {
@@ -216,8 +233,11 @@ __global__ TSA_VERIFY_BOUNDS void verify_kernel(const TsaVerifyUnit* __restrict_
   }
 }
 
-// Device-gated verify: one quad per (unit, segment) of the launch's units, all of the arena's part shape.
-__global__ TSA_VERIFY_BOUNDS void dg_verify_kernel(const DgVerifyLaunch a) {
+// Device-gated verify: one quad per (unit, segment) of the launch's units, all of the arena's part shape. kCopy (the
+// staged units' fused scatter): unit u's bytes are read from src + u x unit_bytes, where its parts lie back to back,
+// and written to their arena slot as they are hashed; the last segment's lane 0 also moves the unit's tail.
+template <bool kCopy>
+__device__ __forceinline__ void dg_verify_body(const DgVerifyLaunch& a, const unsigned char* src) {
   const uint64_t gid = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const uint64_t s = gid >> 2;
   const uint32_t q = uint32_t(gid & 3u);
@@ -232,20 +252,27 @@ __global__ TSA_VERIFY_BOUNDS void dg_verify_kernel(const DgVerifyLaunch a) {
     local = s - uint64_t(u) * a.unit_segs;
     uint64_t k = local;
     uint32_t p = 0;
-    while (p + 1 < a.n_parts && k >= a.part_segs[p]) k -= a.part_segs[p++];
+    uint64_t src_off = uint64_t(u) * a.unit_bytes;  // (kCopy) the part's first byte in src
+    while (p + 1 < a.n_parts && k >= a.part_segs[p]) {
+      k -= a.part_segs[p];
+      src_off += a.part_bytes[p++];
+    }
     const bool last_part = p + 1 == a.n_parts;
     const uint64_t span = last_part ? a.part_bytes[p] / 32 * 32 : a.part_bytes[p];
     const uint64_t off = k * a.seg_bytes;
     const uint64_t end = off + a.seg_bytes < span ? off + a.seg_bytes : span;
     const unsigned char* base = a.arena[p] + uint64_t(a.slots[u]) * a.part_bytes[p];
+    const unsigned char* from = kCopy ? src + src_off : base;
     last = last_part && k + 1 == a.part_segs[p];
     if (last) {
-      tail = base + span;
+      tail = from + span;
       tail_len = uint32_t(a.part_bytes[p] - span);
+      if (kCopy && q == 0)
+        for (uint32_t i = 0; i < tail_len; ++i) const_cast<unsigned char*>(base)[span + i] = tail[i];
     }
     key = a.keys[u];
     v = a.ckpt[(key * a.unit_segs + local) * 4 + q];
-    v = chain(v, base + off, end > off ? (end - off) / 32 : 0, q);
+    v = chain_t<kCopy>(v, from + off, const_cast<unsigned char*>(base) + off, end > off ? (end - off) / 32 : 0, q);
   }
   uint64_t all[4];
   const uint32_t base4 = threadIdx.x & ~3u;
@@ -280,6 +307,11 @@ __global__ TSA_VERIFY_BOUNDS void dg_verify_kernel(const DgVerifyLaunch a) {
   }
 }
 
+__global__ TSA_VERIFY_BOUNDS void dg_verify_kernel(const DgVerifyLaunch a) { dg_verify_body<false>(a, nullptr); }
+__global__ TSA_VERIFY_BOUNDS void dg_scatter_verify_kernel(const DgVerifyLaunch a, const unsigned char* src) {
+  dg_verify_body<true>(a, src);
+}
+
 }  // namespace dev
 
 int launch_digest(const TsaUnit* units_dev, uint32_t n, uint64_t* out_dev, hipStream_t stream) {
@@ -301,6 +333,22 @@ int launch_dg_verify(const DgVerifyLaunch& a, hipStream_t stream, hipEvent_t sta
     hipExtLaunchKernelGGL(dev::dg_verify_kernel, dim3(uint32_t(blocks)), dim3(threads), 0, stream, start, stop, 0, a);
   else
     hipLaunchKernelGGL(dev::dg_verify_kernel, dim3(uint32_t(blocks)), dim3(threads), 0, stream, a);
+  return int(hipGetLastError());
+}
+
+int launch_dg_scatter_verify(const DgVerifyLaunch& a, const void* src, hipStream_t stream, hipEvent_t start,
+                             hipEvent_t stop) {
+  if (a.n == 0 || a.unit_segs == 0) return 0;
+  if (a.n > kDgVerifyMax || a.n_parts == 0 || a.n_parts > 4 || !src) return int(hipErrorInvalidValue);
+  const uint32_t threads = 256;
+  const uint64_t blocks = (uint64_t(a.n) * a.unit_segs * 4 + threads - 1) / threads;
+  if (blocks > 0x7fffffffull) return int(hipErrorInvalidValue);
+  const unsigned char* s = static_cast<const unsigned char*>(src);
+  if (start && stop)
+    hipExtLaunchKernelGGL(dev::dg_scatter_verify_kernel, dim3(uint32_t(blocks)), dim3(threads), 0, stream, start, stop,
+                          0, a, s);
+  else
+    hipLaunchKernelGGL(dev::dg_scatter_verify_kernel, dim3(uint32_t(blocks)), dim3(threads), 0, stream, a, s);
   return int(hipGetLastError());
 }
 
