@@ -138,6 +138,10 @@ SS_API ss_status tsa_test_dgcore_set_policy(void* h, uint32_t policy);
 /* The keys every later boundary must not evict (ss_dg_keep of every gated layer; n = 0: none), and the runtime switch
  * of write-back deferral (ss_dg_set_sched's wb_defer), on the core alone. */
 SS_API ss_status tsa_test_dgcore_set_keep(void* h, const uint32_t* keys, uint32_t n);
+/* Copy-order checking on the core's CPU transport: the copies kept as a device would run them (each stream in order,
+ * streams ordered only by the waits the core asks for); a later token call fails at the first file read, copy in or
+ * copy out whose memory a copy not ordered before it may still use. */
+SS_API ss_status tsa_test_dgcore_check_order(void* h, int on);
 /* The host contract's placement alone on the CPU (no device): a context over desc_json and the budget (plan_make,
  * no benefit), `steps` forwards of the engine loop - ss_begin; per layer with units ss_layer_routes (mode 0, 2) or
  * ss_layer_all (mode 1), ss_acquire (modes 0, 1) or ss_acquire_groups (mode 2); prefetch (may be NULL): the next

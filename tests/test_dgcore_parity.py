@@ -57,6 +57,8 @@ def _lib():
     L.tsa_test_dgcore_set_keep.restype = C.c_int
     L.tsa_test_dgcore_set_wb_defer.argtypes = [C.c_void_p, u32]
     L.tsa_test_dgcore_set_wb_defer.restype = C.c_int
+    L.tsa_test_dgcore_check_order.argtypes = [C.c_void_p, C.c_int]
+    L.tsa_test_dgcore_check_order.restype = C.c_int
     return tsa, L
 
 
@@ -92,6 +94,8 @@ class OurCore:
         self._keep += [nu, pb, od, c]
         self.h = C.c_void_p()
         self.tsa.check(self.L.tsa_test_dgcore_open(C.byref(c), od, len(order), C.byref(self.h)))
+        # every token also checks the copies' order (tsa_test_dgcore_check_order, tests/test_dgcore_order.py)
+        self.tsa.check(self.L.tsa_test_dgcore_check_order(self.h, 1))
         self.keys = sum(n_units)
         self.names = self.L.tsa_test_dgcore_counter_names().decode().split()
 

@@ -568,8 +568,9 @@ uint32_t DgCore::retire_writebacks() {
     wb_.pop_front();
     KeyState& x = st_[w.key];
     x.wb_open = false;
-    if (w.dropped) {
+    if (w.dropped) {  // (its unit is resident again in the slot, which a copy in must not overwrite before w ends)
       free_block_.push_back(w.block);
+      ev_.tie_slot(w.slot, w.ev);
       ev_.tie_block(w.block, w.ev);
     } else {
       x.where = Where::Pinned;
@@ -658,6 +659,12 @@ bool DgCore::resurrect(uint32_t k) {
     if (wb_[i].key != k) continue;
     found = true;
     if (wb_[i].parts_sent == 0) {
+      // (a transport may have copied it already, at the boundary: the slot and the block wait for that copy)
+      t_->unqueue(wb_[i].slot, wb_[i].block);
+      void* ev = ev_.take();
+      t_->record(ev, wb_stream_);
+      ev_.tie_slot(wb_[i].slot, ev);
+      ev_.tie_block(wb_[i].block, ev);
       free_block_.push_back(wb_[i].block);
       wb_.erase(wb_.begin() + ptrdiff_t(i));
       x.wb_open = false;

@@ -76,6 +76,11 @@ class DgTransport {
   // neither the slot nor the block is written by anything else. A transport may copy it now on kD2h and make the
   // later d2h_part calls of the same (slot, block, part) no-ops (default: nothing).
   virtual void prestage(int32_t slot, int32_t block) { (void)slot, (void)block; }
+  // The core dropped a queued write-back (slot -> block) before submitting any part of it (its unit came back). A
+  // transport that prestaged it forgets it; its copy may still run: the core then ties the slot and the block to an
+  // event recorded on the write-back stream, so that the block's next user (a file read, a copy into the slot) waits
+  // for it (default: nothing).
+  virtual void unqueue(int32_t slot, int32_t block) { (void)slot, (void)block; }
   // Units just copied in (key, slot) on stream s: one call per fetch, right after its copies (a demand's before the
   // layer's signal_ready). A transport that verifies landed bytes enqueues the check here (default: nothing).
   virtual void landed(Stream s, uint32_t g, const uint32_t* keys, const int32_t* slots, uint32_t n) {

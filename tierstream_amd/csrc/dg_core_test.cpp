@@ -4,7 +4,9 @@
 #include <algorithm>
 #include <cstring>
 #include <memory>
+#include <set>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "common.hpp"
@@ -17,31 +19,119 @@
 namespace tsa {
 namespace {
 
-// Every copy, entry write, event and file read completes when issued.
+// Every copy, entry write, event and file read completes when issued. With check_order on, the transport also keeps
+// the copies as a device would run them - each stream in order, streams ordered only by the waits the core asks for and
+// by the protocol (a layer's export is served only after the engine passed the previous ready word, which followed that
+// layer's copies on the demand stream) - and fails the token at the first call whose memory could still be in use by a
+// copy not ordered before it: a file read
+// into a block (the host writes it at once) while any copy reads or writes that block and the host has not waited for
+// it; a copy in (block -> slot) while a copy still writes the block or reads or writes the slot; a copy out (slot ->
+// block, at once or prestaged) while a copy still writes the slot or reads or writes the block.
 class EagerTransport final : public DgTransport {
  public:
   explicit EagerTransport(std::vector<uint64_t> parts) : parts_(std::move(parts)) {}
   ~EagerTransport() override = default;
-  void h2d(Stream, int32_t, int32_t, uint32_t) override {}
-  void d2h(int32_t, int32_t) override {}
-  void d2h_part(Stream, int32_t, int32_t, uint32_t) override {}
+  void h2d(Stream s, int32_t slot, int32_t block, uint32_t) override { copy(s, block, -1 - slot, "copy in"); }
+  void d2h(int32_t slot, int32_t block) override { copy(kD2h, -1 - slot, block, "write-back"); }
+  void d2h_part(Stream s, int32_t slot, int32_t block, uint32_t) override {
+    if (staged_.count({slot, block})) return;  // (copied at the boundary already)
+    copy(s, -1 - slot, block, "write-back part");
+  }
+  void prestage(int32_t slot, int32_t block) override {
+    copy(kD2h, -1 - slot, block, "prestaged write-back");
+    staged_.insert({slot, block});
+  }
+  void unqueue(int32_t slot, int32_t block) override { staged_.erase({slot, block}); }
   uint32_t parts() const override { return uint32_t(parts_.size()); }
   uint64_t part_bytes(uint32_t p) const override { return parts_[p]; }
   void write_entry(Stream, uint32_t, int32_t) override {}
-  void signal_ready(uint32_t, uint32_t) override {}
-  void* event_create() override { return new int(0); }
-  void event_destroy(void* ev) override { delete static_cast<int*>(ev); }
-  void record(void*, Stream) override {}
-  void wait(Stream, void*) override {}
-  bool done(void*) override { return true; }
-  bool query(void*) override { return true; }
-  void event_sync(void*) override {}
-  void sync(Stream) override {}
+  void signal_ready(uint32_t, uint32_t) override {
+    for (int t = 0; t < 3; ++t) ready_cover_[t] = t == kDem ? last_[kDem] : seen_[kDem][t];
+  }
+  // A layer's export is served: the engine passed every earlier ready word, so their copies have ended.
+  void layer_begins() {
+    for (int t = 0; t < 3; ++t) host_[t] = std::max(host_[t], ready_cover_[t]);
+  }
+  void* event_create() override { return new Ev(); }
+  void event_destroy(void* ev) override { delete static_cast<Ev*>(ev); }
+  void record(void* ev, Stream s) override {
+    Ev& e = *static_cast<Ev*>(ev);
+    for (int t = 0; t < 3; ++t) e.cover[t] = t == s ? last_[s] : seen_[s][t];
+  }
+  void wait(Stream s, void* ev) override { after(s, *static_cast<Ev*>(ev)); }
+  bool done(void* ev) override {
+    host(*static_cast<Ev*>(ev));
+    return true;
+  }
+  bool query(void* ev) override { return done(ev); }
+  void event_sync(void* ev) override { host(*static_cast<Ev*>(ev)); }
+  void sync(Stream s) override {
+    host_[s] = last_[s];
+    for (int t = 0; t < 3; ++t) host_[t] = std::max(host_[t], seen_[s][t]);
+  }
   void upload_table(const int32_t*, uint32_t) override {}
-  void read_unit(uint32_t, int32_t, int32_t) override {}
+  void read_unit(uint32_t key, int32_t block, int32_t) override {
+    if (!check_) return;
+    for (const Copy& c : copies_)
+      if ((c.from == block || c.to == block) && host_[c.s] < c.id)
+        fail("a file read of key " + std::to_string(key) + " into block " + std::to_string(block) + " while " +
+             c.what + " " + std::to_string(c.id) + " (" + where(c.from) + " -> " + where(c.to) + ", stream " +
+             std::to_string(c.s) + ") may still use it");
+  }
+  // As the MI355X transport: a landing read first waits on the host for the block's last copy out.
+  void read_landing(uint32_t key, int32_t block) override {
+    for (const Copy& c : copies_)
+      if (c.from == block) host_[c.s] = std::max(host_[c.s], c.id);
+    read_unit(key, block, -1);
+  }
+  void wait_copy_in(Stream s, int32_t, int32_t, void* slot_ev, void* block_ev) override {
+    if (slot_ev) wait(s, slot_ev);
+    if (block_ev) wait(s, block_ev);
+  }
+  void check_order(bool on) { check_ = on; }
+  const std::string& violation() const { return violation_; }
 
  private:
+  // A copy: from / to as block b (>= 0) or slot s (encoded -1 - s), on stream s, id in issue order.
+  struct Copy {
+    int s;
+    int32_t from, to;
+    uint64_t id;
+    std::string what;
+  };
+  struct Ev {
+    uint64_t cover[3] = {0, 0, 0};  // per stream: the last copy id the event's completion implies
+  };
+  bool before(const Copy& c, int s) const { return c.s == s || seen_[s][c.s] >= c.id || host_[c.s] >= c.id; }
+  void after(int s, const Ev& e) {
+    for (int t = 0; t < 3; ++t) seen_[s][t] = std::max(seen_[s][t], e.cover[t]);
+  }
+  void host(const Ev& e) {
+    for (int t = 0; t < 3; ++t) host_[t] = std::max(host_[t], e.cover[t]);
+  }
+  void copy(int s, int32_t from, int32_t to, const char* what) {
+    if (check_)
+      for (const Copy& c : copies_) {
+        const bool clash = c.to == to || c.to == from || c.from == to;  // (two reads of one place do not clash)
+        if (clash && !before(c, s))
+          fail(std::string(what) + " (" + where(from) + " -> " + where(to) + ") on stream " + std::to_string(s) +
+               " while " + c.what + " " + std::to_string(c.id) + " (" + where(c.from) + " -> " + where(c.to) +
+               ", stream " + std::to_string(c.s) + ") may still run");
+      }
+    copies_.push_back(Copy{s, from, to, ++next_, what});
+    last_[s] = next_;
+  }
+  static std::string where(int32_t x) { return x >= 0 ? "block " + std::to_string(x) : "slot " + std::to_string(-1 - x); }
+  void fail(const std::string& why) {
+    if (violation_.empty()) violation_ = why;
+  }
+
   std::vector<uint64_t> parts_;
+  bool check_ = false;
+  std::string violation_;
+  std::vector<Copy> copies_;
+  std::set<std::pair<int32_t, int32_t>> staged_;
+  uint64_t next_ = 0, last_[3] = {0, 0, 0}, host_[3] = {0, 0, 0}, seen_[3][3] = {}, ready_cover_[3] = {0, 0, 0};
 };
 
 struct TestCore {
@@ -150,6 +240,7 @@ ss_status tsa_test_dgcore_token_pred(void* h, const uint32_t* ids, uint32_t n, c
       uint64_t mask = 0;
       for (uint32_t i = 0; i < n; ++i)  // the export kernel: slot_of[unit_base[g] + id] < 0 at export time
         if (x[i] < c.units(g) && c.table()[c.key(g, x[i])] < 0) mask |= uint64_t(1) << i;
+      r->t->layer_begins();
       c.serve_misses(g, x, n, mask);
       c.note_uses(g, x, n, mask);
       // the prediction for the next layer made at this one (the service serves it when that layer exports)
@@ -160,6 +251,7 @@ ss_status tsa_test_dgcore_token_pred(void* h, const uint32_t* ids, uint32_t n, c
     }
     c.close_token(r->rows, r->keep);
     c.audit();
+    require(r->t->violation().empty(), SS_E_BACKEND, "copy order: " + r->t->violation());
     if (table_out) std::memcpy(table_out, c.table().data(), 4ull * c.keys());
     if (counts) {
       const DgCounts& s = c.counts();
@@ -189,6 +281,13 @@ ss_status tsa_test_dgcore_set_policy(void* h, uint32_t policy) {
     auto* r = static_cast<tsa::TestCore*>(h);
     r->core->set_policy(policy);
     r->core->audit();
+  });
+}
+
+ss_status tsa_test_dgcore_check_order(void* h, int on) {
+  return tsa::guard([&] {
+    tsa::require(h != nullptr, SS_E_INVALID, "tsa_test_dgcore_check_order: null handle");
+    static_cast<tsa::TestCore*>(h)->t->check_order(on != 0);
   });
 }
 

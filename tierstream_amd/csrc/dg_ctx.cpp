@@ -541,6 +541,10 @@ class HipTransport final : public DgTransport {
     }
     prestaged_[slot] = {block, (1u << P) - 1u};
   }
+  void unqueue(int32_t slot, int32_t block) override {  // (its copies, if any, stay in the stream's order)
+    const auto it = prestaged_.find(slot);
+    if (it != prestaged_.end() && it->second.block == block) prestaged_.erase(it);
+  }
   // One part of a write-back on lane s (HSA copies): the part's signal becomes the slot's and the block's.
   void hsa_d2h_part(Stream s, int32_t slot, int32_t block, uint32_t p, uint32_t count) {
     const uint32_t sig = lane_copy(s, block_ptr(block) + x_.part_offset[p], slot_ptr(p, slot), x_.part_bytes[p], true);
