@@ -5,14 +5,15 @@ order; at most dg_landing_max_queued landing pieces run and one reader stays fre
 before it starts is cancelled with nothing read, one dropped part-way loses its queued pieces (aborted bytes) and is
 never finished (no hash check); a claimed landing read runs as a demand read ahead of the landing queue and drain waits
 for it; a landing read's failure is kept until a claim finds it Failed, a claimed one's is reported; a landing read
-part-way yields its reader to a demand read; whole landing reads (dg_landing_chunk 0xFFFFFFFF) start only while fewer
+part-way yields its reader to a demand read when more demand pieces wait than idle readers could take, and not when
+idle readers take them (src/dg_load.cpp:746-750); whole landing reads (dg_landing_chunk 0xFFFFFFFF) start only while fewer
 than the cap pieces of any kind run; stop drops unclaimed landing reads; a word's second read waits for its first."""
 import ctypes as C
 
 import pytest
 
 SCENARIOS = ["demand_first", "cap", "reserve", "drop", "claim", "failures", "yields", "whole", "stop_drops",
-             "word_order"]
+             "word_order", "no_yield_with_idle_readers"]
 
 
 @pytest.mark.parametrize("i", range(len(SCENARIOS)), ids=SCENARIOS)

@@ -59,10 +59,7 @@ void ReadPool::enqueue(uint32_t w, uint32_t key, char* dst, uint32_t* word, uint
     u->left = uint32_t(ps.size());
     for (const Piece& p : ps) (landing ? lq_ : q_).push_back(Job{u.get(), &p});
     failed_[w] = 0;
-    if (!landing) {
-      ++demand_inflight_;
-      lc_.yields += partway_.size();  // each landing read part-way gives its readers to this one
-    }
+    if (!landing) ++demand_inflight_;
     at_[w] = std::move(u);
   }
   cv_.notify_all();
@@ -145,6 +142,10 @@ void ReadPool::run() {
         if (!u.err) u.err = e;
       }
       const bool last = --u.left == 0;
+      // a landing read part-way yields this reader when more demand pieces wait than the other readers idle could
+      // take (reference src/dg_load.cpp:746-750, per piece here): the reader takes a demand piece next
+      if (from_landing && u.landing && !u.dropped && !e && u.left > u.running && q_.size() + running_ + 1 > threads_)
+        ++lc_.yields;
       if (ctl_ && busy_) {
         busy_units_ += last;
         if (running_ == 0 && q_.empty() && lq_.empty()) {  // idle again: the period's throughput picks the depth

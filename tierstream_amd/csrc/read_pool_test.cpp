@@ -247,6 +247,22 @@ void yields() {
   CHECK(p->landing_counts().yields == 1);
 }
 
+// 10: no yield while idle readers take the demand read: five readers, one running a landing read's first piece, the
+// four others take the demand read's four pieces at once; the landing read then runs to its end.
+void no_yield_with_idle_readers() {
+  Rig r;
+  auto p = make(r, 5, 1);
+  landing(*p, r, 0, kLandingKey);
+  spin_until([&] { return r.started() == 1; });
+  demand(*p, r, 1, 1);
+  spin_until([&] { return r.started() == 5; });
+  r.open_all();
+  p->drain();
+  p->wait_idle(0);
+  CHECK(r.order() == repeat({{kLandingKey, 1}, {1, 4}, {kLandingKey, 3}}));
+  CHECK(p->landing_counts().yields == 0);
+}
+
 // 7: whole landing reads (no chunks, no reserve): a landing read starts only while fewer than `cap` pieces of any kind
 // run, in one piece.
 void whole() {
@@ -322,6 +338,7 @@ extern "C" ss_status tsa_test_read_pool(uint32_t scenario, char* msg, uint32_t c
       case 7: whole(); break;
       case 8: stop_drops(); break;
       case 9: word_order(); break;
+      case 10: no_yield_with_idle_readers(); break;
       default: return SS_E_INVALID;
     }
     return SS_OK;

@@ -390,10 +390,8 @@ __attribute__((visibility("default"))) ss_status tse_dg_token(void* h, const int
   return tse_dg_token_pred(h, routes, nullptr, checksums, token_ms);
 }
 
-// preds ([G][n_pred], row g for layer g + 1; the last row unused) may be NULL: zeros are predicted then.
-__attribute__((visibility("default"))) ss_status tse_dg_token_pred(void* h, const int32_t* routes, const int32_t* preds,
-                                                                   uint64_t* checksums, double* token_ms) {
-  TseDg* e = static_cast<TseDg*>(h);
+// The token's routes (and predictions) on the device and its output words cleared, before ss_begin.
+static ss_status stage_token(TseDg* e, const int32_t* routes, const int32_t* preds) {
   std::vector<int32_t> ids(size_t(64) * e->G, 0);
   for (uint32_t g = 0; g < e->G; ++g)
     for (uint32_t i = 0; i < e->n_ids; ++i) ids[64 * g + i] = routes[size_t(g) * e->n_ids + i];
@@ -411,6 +409,22 @@ __attribute__((visibility("default"))) ss_status tse_dg_token_pred(void* h, cons
     TSE_HIP(hipMemsetAsync(e->ready_dev, 0, 4ull * 64 * e->G, e->s));
   }
   TSE_HIP(hipStreamSynchronize(e->s));
+  return SS_OK;
+}
+
+// ss_begin and the token's kernels enqueued, nothing more: the token stays open (an engine that fails mid-token).
+__attribute__((visibility("default"))) ss_status tse_dg_token_open(void* h, const int32_t* routes) {
+  TseDg* e = static_cast<TseDg*>(h);
+  TSE_CK(stage_token(e, routes, nullptr));
+  if (e->dg) TSE_CK(ss_begin(e->c, nullptr, 0));
+  return e->exec ? ck(hipGraphLaunch(e->exec, e->s)) : tse_enqueue_token(e);
+}
+
+// preds ([G][n_pred], row g for layer g + 1; the last row unused) may be NULL: zeros are predicted then.
+__attribute__((visibility("default"))) ss_status tse_dg_token_pred(void* h, const int32_t* routes, const int32_t* preds,
+                                                                   uint64_t* checksums, double* token_ms) {
+  TseDg* e = static_cast<TseDg*>(h);
+  TSE_CK(stage_token(e, routes, preds));
   const auto t0 = std::chrono::steady_clock::now();
   if (e->dg) TSE_CK(ss_begin(e->c, nullptr, 0));
   ss_status st = e->exec ? ck(hipGraphLaunch(e->exec, e->s)) : tse_enqueue_token(e);

@@ -277,6 +277,8 @@ def engine() -> C.CDLL:
         E.tse_dg_token_pred.argtypes = [vp, C.POINTER(i32), C.POINTER(i32), C.POINTER(u64), C.POINTER(C.c_double)]
         E.tse_dg_create_ex.restype = C.c_int
         E.tse_dg_create_ex.argtypes = [vp, u32, u32, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(vp)]
+        E.tse_dg_token_open.restype = C.c_int
+        E.tse_dg_token_open.argtypes = [vp, C.POINTER(i32)]
         E.tse_dg_early.restype = C.c_int
         E.tse_dg_early.argtypes = [vp, C.POINTER(u64), C.POINTER(u32)]
         E.tse_dg_stamps.restype = C.c_int
@@ -619,6 +621,12 @@ class DgEngine:
                                  p.ctypes.data_as(C.POINTER(i32)) if p is not None else None,
                                  cks.ctypes.data_as(C.POINTER(u64)) if want_checksums else None, C.byref(ms))
         return int(st), cks, ms.value
+
+    def token_open(self, routes: np.ndarray):
+        """ss_begin and the token's kernels enqueued, without ss_end: the token stays open (a failing engine)."""
+        r = np.ascontiguousarray(routes, dtype=np.int32)
+        assert r.shape == (self.G, self.n_ids)
+        check(engine().tse_dg_token_open(self.h, r.ctypes.data_as(C.POINTER(i32))))
 
     def set_rows(self, rows: int):
         """The verify rows each later token closes (ss_dg_end_rows above one)."""
