@@ -99,6 +99,10 @@ def parse():
     ap.add_argument("--copies", default="hsa", choices=["hsa", "hip"],
                     help="device-gated unit copies: through the HSA runtime's copy engines (the library's default "
                          "where parts are copied whole) or on HIP streams (TSA_DG_COPIES=hip)")
+    ap.add_argument("--timeline", default="",
+                    help="device-gated: open with dg_diag and write every timed token's per-layer timeline rows "
+                         "(ss_dg_timeline_sized) and device stamps to this JSON file (read between tokens: each "
+                         "token's latency excludes them, the timed region's wall clock does not)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the copy peaks and the library's HBM kernels alone (no serve loop: for counter runs)")
     return ap.parse_args()
@@ -447,7 +451,9 @@ def main():
                          dg_landing_max_queued=a.landing_max_queued, dg_landing_chunk=a.landing_chunk)
         opts = {**shape.options, **extra}
         os.environ["TSA_DG_COPIES"] = a.copies  # (read by the open)
-        ctx = keep(ss.Ctx(d, b, plan, ss.options(**opts, verify_hash=2, dg_wait_timeout_ms=20000, policy=policy)))
+        diag = {"dg_diag": 1} if a.timeline else {}
+        ctx = keep(ss.Ctx(d, b, plan, ss.options(**opts, verify_hash=2, dg_wait_timeout_ms=20000, policy=policy,
+                                                  **diag)))
         os.environ.pop("TSA_DG_COPIES", None)
         copies = "hsa" if ctx.hsa_copies() else "hip"
         open_s = time.time() - t0
@@ -489,9 +495,17 @@ def main():
         tsa.check(L.tsa_device_sync())
         lat = np.zeros(steps)
         t_start = time.perf_counter()
+        rows = []
         for i in range(steps):
             cks, lat[i] = eng.token(routes[warm + i], preds=pred_of(warm + i))
             check_cks(warm + i, cks)
+            if a.timeline:  # (between tokens: outside the token's own latency)
+                rows.append({"token": i, "lat_ms": float(lat[i]), "rows": [ctx.dg_timeline(g) for g in range(G)],
+                             "stamps": ctx.dg_stamps().astype(np.int64).tolist(),
+                             "boundary": ctx.dg_boundary_timeline()})
+        if a.timeline:
+            with open(a.timeline, "w") as f:
+                json.dump(rows, f)
         tsa.check(L.tsa_device_sync())
         wall = time.perf_counter() - t_start
         s1 = ctx.dg_stats()
