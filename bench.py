@@ -51,11 +51,21 @@ TICK_NS = 10.0  # wall_clock64 runs at 100 MHz on gfx950
 # counter's reading for a copy kernel of known size (FETCH 2.0, WRITE 1.0), 2 KiB checkpoint segments: 355,269.75 KiB
 # fetched, nothing written (profiles/dg_verify_kernel_mixtral_unit_pmc.md).
 VERIFY_TRAFFIC_PER_UNIT = {352321536: 363796224}
+# The staged units' fused scatter and check (dg_scatter_verify_kernel), keyed by unit bytes: FETCH_SIZE x 2.0 +
+# WRITE_SIZE x 1.0 on one launch of one unit of this shape through tsa_xxh64_scatter_verify_slots, 2 KiB segments
+# (profiles/dg_scatter_verify_kernel_deepseek_unit_pmc.md).
+SCATTER_VERIFY_TRAFFIC_PER_UNIT = {24772608: 50441780}
+TRAFFIC_SOURCE = {("verify", 352321536): "profiles/dg_verify_kernel_mixtral_unit_pmc.md",
+                  ("fused", 24772608): "profiles/dg_scatter_verify_kernel_deepseek_unit_pmc.md"}
 # The host contract's verify_kernel: HBM bytes fetched per algorithmic byte hashed, keyed by unit bytes, from
 # rocprofv3 --pmc FETCH_SIZE over the bench's own timed steps (scaled as above): a full batch of 32 units fetches
 # 152,527.41 KiB x 2.0 = 312,376,128 B for 301,989,888 B of units (2 KiB checkpoint segments), nothing written
 # (profiles/verify_kernel_qwen3_host_pmc.md).
-HOST_VERIFY_TRAFFIC_RATIO: dict[int, float] = {9437184: 312376128 / 301989888}
+# dense-prefix: a batch of 2 blobs (469,762,048 B) fetches 237,586.2 KiB x 2.0 = 486,576,553 B
+# (profiles/verify_kernel_dense_prefix_host_pmc.md).
+HOST_VERIFY_TRAFFIC_RATIO: dict[int, float] = {9437184: 312376128 / 301989888, 234881024: 486576553 / 469762048}
+HOST_TRAFFIC_SOURCE = {9437184: "profiles/verify_kernel_qwen3_host_pmc.md",
+                       234881024: "profiles/verify_kernel_dense_prefix_host_pmc.md"}
 
 
 def log(*a):
@@ -295,6 +305,19 @@ def measure_kernels(tsa, L, C, w, seg=None, reps=10):
         out["verify"] = {"kernel": "dg_verify_kernel", "unit_bytes": ub, "seg_bytes": seg, "segments": n_ck,
                          "us": round(t * 1e6, 1), "GBps": round(ub / t / 1e9, 1),
                          "frac_of_hbm_peak": round(ub / t / 1e9 / HBM_PEAK_GBPS, 4), "fail_word": bad}
+        if len(parts) > 1 and min(parts) < (8 << 20):  # staged: the scatter and the check in one kernel
+            staged = dev_alloc(ub)
+            for p, (b, pb) in enumerate(zip(pbufs, parts)):
+                tsa.check(L.tsa_memcpy(C.c_void_p(staged.ptr + sum(parts[:p])), C.c_void_p(b.ptr), pb, 2, s))
+            tsa.check(L.tsa_stream_sync(s))
+            fail.upload(np.zeros(16, dtype=np.uint32))
+            t2 = timed(lambda: tsa.check(L.tsa_xxh64_scatter_verify_slots(C.byref(av), keys, slots, 1,
+                                                                          C.c_void_p(staged.ptr),
+                                                                          C.c_void_p(fail.ptr), s)))
+            out["scatter_verify"] = {"kernel": "dg_scatter_verify_kernel", "unit_bytes": ub, "bytes_moved": 2 * ub,
+                                     "us": round(t2 * 1e6, 1), "GBps": round(2 * ub / t2 / 1e9, 1),
+                                     "frac_of_hbm_peak": round(2 * ub / t2 / 1e9 / HBM_PEAK_GBPS, 4),
+                                     "fail_word": int(fail.download(4, dtype=np.uint32)[0])}
         # the scatter kernel as a plain copy: one part of 256 MiB
         n = 256 << 20
         src, dst = dev_alloc(n), dev_alloc(n)
@@ -570,6 +593,7 @@ def main():
         # (dg_scatter_verify_kernel): each landed unit is read from HBM staging and written to its slot once
         fused = len(w.parts) > 1 and min(w.parts) < (8 << 20)
         ver_bytes = prof["verify_bytes"] * (2 if fused else 1)
+        traffic_unit = (SCATTER_VERIFY_TRAFFIC_PER_UNIT if fused else VERIFY_TRAFFIC_PER_UNIT).get(w.unit_bytes)
         ver_gbps = ver_bytes / prof["verify_ns"] if prof["verify_ns"] else None
         miss_bytes = dstat["fetched"] * w.unit_bytes
         result = {
@@ -622,8 +646,9 @@ def main():
                          if fused else "dg_verify_kernel (device XXH64 of every landed unit)",
                          "achieved": round(ver_gbps, 1) if ver_gbps else None, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(ver_gbps / HBM_PEAK_GBPS, 4) if ver_gbps else None,
-                         "traffic": int(VERIFY_TRAFFIC_PER_UNIT[w.unit_bytes] * prof["verify_units"] /
-                                        max(prof["verifies"], 1)) if w.unit_bytes in VERIFY_TRAFFIC_PER_UNIT else None,
+                         "traffic": int(traffic_unit * prof["verify_units"] / max(prof["verifies"], 1))
+                         if traffic_unit else None,
+                         "traffic_source": TRAFFIC_SOURCE.get(("fused" if fused else "verify", w.unit_bytes)),
                          "launches": prof["verifies"], "units": prof["verify_units"],
                          "bytes_per_launch": ver_bytes // max(prof["verifies"], 1),
                          "mean_launch_us": round(prof["verify_ns"] / max(prof["verifies"], 1) / 1e3, 2),
@@ -822,6 +847,7 @@ def host_roofline(prof, w):
     return {"bound": "hbm", "kernel": "verify_kernel (device XXH64 of each batch of landed units)",
             "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
             "traffic": int(ratio * per_launch) if ratio else None,
+            "traffic_source": HOST_TRAFFIC_SOURCE.get(w.unit_bytes),
             "launches": prof["verifies"], "units": prof["verify_units"], "bytes_per_launch": int(per_launch),
             "mean_launch_us": round(prof["verify_ns"] / prof["verifies"] / 1e3, 2),
             "note": "live: each launch checks a batch of landed units behind both copy streams while the engine reads "

@@ -87,6 +87,12 @@ typedef struct tsa_arena_verify {
  * arrays of n entries (any n: launches of up to 64 units each). The caller zeroes fail_dev. */
 SS_API ss_status tsa_xxh64_verify_slots(const tsa_arena_verify* a, const uint32_t* keys, const int32_t* slots, uint32_t n,
                                         uint32_t* fail_dev, void* stream);
+/* The same check fused with the staged units' scatter (a device-gated context with verify_hash = 2 and parts under
+ * 8 MiB): unit i's bytes lie back to back at src_dev + i x (its parts' bytes), 8-byte aligned; each is written to
+ * (keys[i], slots[i])'s arena slot while it is hashed, so its bytes cross HBM once each way. Replaces the reference's
+ * per-part copies (src/dg_ctx.cpp:163-168) followed by a separate check. */
+SS_API ss_status tsa_xxh64_scatter_verify_slots(const tsa_arena_verify* a, const uint32_t* keys, const int32_t* slots,
+                                                uint32_t n, const void* src_dev, uint32_t* fail_dev, void* stream);
 
 /* One staged unit: src_dev holds the unit's bytes back to back; part p goes to dst[p] (parts[p] bytes). Every pointer
  * 16-byte aligned, every part a multiple of 16 bytes. block_first: prefix sum of the jobs' 16 KiB blocks. */

@@ -122,6 +122,63 @@ def test_verify_checkpoint_parallel(gpu, oracle, seg):
     assert [int(x != 0) for x in res] == [1, 1, 0, 0, 0, 0]
 
 
+@pytest.mark.parametrize("parts,seg", [([64 * 1024] * 3, 2048), ([2048, 4096 + 32, 1000], 1024), ([96], 1024),
+                                       ([8454144, 64 * 1024, 4 * 1024 * 1024], 2048)])
+def test_scatter_verify_slots_arena(gpu, oracle, parts, seg):
+    """tsa_xxh64_scatter_verify_slots (the staged units' scatter fused with their check): units back to back in HBM
+    staging go to their arena slots byte for byte (a last part's tail under 32 bytes included) and pass; a flipped
+    staged byte - a part's first, the unit's last (in the tail) - fails only its unit, whose slot then holds the
+    flipped bytes as staged."""
+    rng = np.random.default_rng(len(parts) * seg + parts[0] + 7)
+    ub = sum(parts)
+    slots_n, keys_n = 6, 5
+    arena = [gpu.DeviceBuffer(slots_n * pb) for pb in parts]
+    data = {k: [rng.integers(0, 256, pb, dtype=np.uint8) for pb in parts] for k in range(keys_n)}
+    placed = {0: 3, 2: 0, 4: 5, 1: 1}  # key -> slot, in the order the units are staged
+    n_ck = len(oracle.checkpoints(data[0], seg)[0]) // 4
+    states = np.zeros((keys_n, n_ck, 4), dtype=np.uint64)
+    digests = np.zeros(keys_n, dtype=np.uint64)
+    for k in range(keys_n):
+        st, dg = oracle.checkpoints(data[k], seg)
+        states[k] = st.reshape(n_ck, 4)
+        digests[k] = dg
+    st_dev = gpu.DeviceBuffer(states.nbytes)
+    st_dev.upload(states)
+    dg_dev = gpu.DeviceBuffer(digests.nbytes)
+    dg_dev.upload(digests)
+    staged = np.concatenate([np.concatenate(data[k]) for k in placed])
+    src = gpu.DeviceBuffer(staged.nbytes)
+    a = gpu.TsaArenaVerify()
+    for p, (buf, pb) in enumerate(zip(arena, parts)):
+        a.arena[p] = buf.ptr
+        a.part_bytes[p] = pb
+    a.n_parts, a.seg_bytes, a.states_dev, a.digests_dev = len(parts), seg, st_dev.ptr, dg_dev.ptr
+    keys = (C.c_uint32 * len(placed))(*placed.keys())
+    slots = (C.c_int32 * len(placed))(*placed.values())
+    fail = gpu.DeviceBuffer(4 * len(placed))
+
+    def run(bytes_):
+        src.upload(bytes_)
+        fail.upload(np.zeros(len(placed), dtype=np.uint32))
+        gpu.check(gpu.lib().tsa_xxh64_scatter_verify_slots(C.byref(a), keys, slots, len(placed), C.c_void_p(src.ptr),
+                                                           C.c_void_p(fail.ptr), None))
+        gpu.check(gpu.lib().tsa_stream_sync(None))
+        return list(fail.download(4 * len(placed)).view(np.uint32))
+
+    def slot_bytes(sl):
+        return np.concatenate([buf.download(pb, sl * pb) for buf, pb in zip(arena, parts)])
+
+    assert run(staged) == [0] * len(placed)
+    for i, (k, sl) in enumerate(placed.items()):
+        assert np.array_equal(slot_bytes(sl), staged[i * ub:(i + 1) * ub]), (k, sl)
+    bad = staged.copy()
+    bad[2 * ub - 1] ^= 0xFF           # unit 1 (key 2): its last byte
+    bad[3 * ub + (parts[0] if len(parts) > 1 else 1)] ^= 0x01  # unit 3 (key 1): its second part's first byte
+    got = run(bad)
+    assert got[0] == 0 and got[1] != 0 and got[2] == 0 and got[3] != 0, got
+    assert np.array_equal(slot_bytes(placed[2]), bad[ub:2 * ub])  # (written as staged, and flagged)
+
+
 @pytest.mark.parametrize("parts,seg", [([64 * 1024] * 3, 8192), ([2048, 4096 + 32, 1000], 1024), ([96], 1024)])
 def test_verify_slots_arena(gpu, oracle, parts, seg):
     """tsa_xxh64_verify_slots (the device-gated check): keys in arena slots, by value; against the oracle's

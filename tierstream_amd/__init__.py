@@ -86,6 +86,7 @@ def _declare(L: C.CDLL) -> None:
         "tsa_xxh64_checkpoints": (st, [C.POINTER(TsaUnit), u64, C.POINTER(u64), u64, C.POINTER(u64)]),
         "tsa_xxh64_verify": (st, [vp, u32, u64, u64, vp, vp]),
         "tsa_xxh64_verify_slots": (st, [vp, C.POINTER(u32), C.POINTER(i32), u32, vp, vp]),
+        "tsa_xxh64_scatter_verify_slots": (st, [vp, C.POINTER(u32), C.POINTER(i32), u32, vp, vp, vp]),
         "tsa_scatter_blocks": (u64, [C.POINTER(u64), u32]),
         "tsa_scatter": (st, [vp, u32, u64, vp]),
         "tsa_synth": (st, [vp, u64, u64, u64, u64, u32, C.c_float, vp]),

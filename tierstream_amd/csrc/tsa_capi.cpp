@@ -122,33 +122,52 @@ ss_status tsa_xxh64_verify(const tsa_verify_unit* units_dev, uint32_t n_units, u
   });
 }
 
+// The checks of n arena units in launches of up to kDgVerifyMax; src_dev (the fused scatter): the units' bytes back
+// to back, unit i at src_dev + i x unit_bytes, written to their slots while they are hashed.
+static void arena_checks(const char* what, const tsa_arena_verify* a, const uint32_t* keys, const int32_t* slots,
+                         uint32_t n, const void* src_dev, uint32_t* fail_dev, void* stream) {
+  const std::string w(what);
+  require(a != nullptr, SS_E_INVALID, w + ": null arena");
+  require(n == 0 || (keys && slots && fail_dev), SS_E_INVALID, w + ": null argument");
+  require(a->n_parts >= 1 && a->n_parts <= TSA_MAX_EXTENTS, SS_E_INVALID, w + ": 1..4 parts");
+  require(a->seg_bytes > 0 && a->seg_bytes % 32 == 0, SS_E_INVALID, w + ": seg_bytes must be a multiple of 32");
+  require(n == 0 || (a->states_dev && a->digests_dev), SS_E_INVALID, w + ": null states or digests");
+  for (uint32_t p = 0; p < a->n_parts; ++p)
+    require(a->arena[p] != nullptr && reinterpret_cast<uintptr_t>(a->arena[p]) % 8 == 0 && a->part_bytes[p] % 8 == 0,
+            SS_E_INVALID, w + ": every arena part 8-byte aligned with a multiple of 8 bytes");
+  DgVerifyLaunch l;
+  require(set_dg_verify_shape(l, a->arena, a->part_bytes, a->n_parts, a->seg_bytes), SS_E_INVALID,
+          w + ": a part but the last is not a multiple of 32");
+  require(n == 0 || !src_dev || reinterpret_cast<uintptr_t>(src_dev) % 8 == 0, SS_E_INVALID,
+          w + ": the staged bytes must be 8-byte aligned");
+  l.ckpt = a->states_dev;
+  l.digests = a->digests_dev;
+  for (uint32_t i0 = 0; i0 < n; i0 += kDgVerifyMax) {
+    l.n = std::min(kDgVerifyMax, n - i0);
+    l.fail = fail_dev + i0;
+    for (uint32_t i = 0; i < l.n; ++i) {
+      require(slots[i0 + i] >= 0, SS_E_INVALID, w + ": negative slot");
+      l.keys[i] = keys[i0 + i];
+      l.slots[i] = slots[i0 + i];
+    }
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (src_dev)
+      launch_ck(launch_dg_scatter_verify(l, static_cast<const char*>(src_dev) + uint64_t(i0) * l.unit_bytes, s), what);
+    else
+      launch_ck(launch_dg_verify(l, s), what);
+  }
+}
+
 ss_status tsa_xxh64_verify_slots(const tsa_arena_verify* a, const uint32_t* keys, const int32_t* slots, uint32_t n,
                                  uint32_t* fail_dev, void* stream) {
+  return guard([&] { arena_checks("tsa_xxh64_verify_slots", a, keys, slots, n, nullptr, fail_dev, stream); });
+}
+
+ss_status tsa_xxh64_scatter_verify_slots(const tsa_arena_verify* a, const uint32_t* keys, const int32_t* slots,
+                                         uint32_t n, const void* src_dev, uint32_t* fail_dev, void* stream) {
   return guard([&] {
-    require(a != nullptr, SS_E_INVALID, "tsa_xxh64_verify_slots: null arena");
-    require(n == 0 || (keys && slots && fail_dev), SS_E_INVALID, "tsa_xxh64_verify_slots: null argument");
-    require(a->n_parts >= 1 && a->n_parts <= TSA_MAX_EXTENTS, SS_E_INVALID, "tsa_xxh64_verify_slots: 1..4 parts");
-    require(a->seg_bytes > 0 && a->seg_bytes % 32 == 0, SS_E_INVALID,
-            "tsa_xxh64_verify_slots: seg_bytes must be a multiple of 32");
-    require(n == 0 || (a->states_dev && a->digests_dev), SS_E_INVALID, "tsa_xxh64_verify_slots: null states or digests");
-    for (uint32_t p = 0; p < a->n_parts; ++p)
-      require(a->arena[p] != nullptr && reinterpret_cast<uintptr_t>(a->arena[p]) % 8 == 0 && a->part_bytes[p] % 8 == 0,
-              SS_E_INVALID, "tsa_xxh64_verify_slots: every arena part 8-byte aligned with a multiple of 8 bytes");
-    DgVerifyLaunch l;
-    require(set_dg_verify_shape(l, a->arena, a->part_bytes, a->n_parts, a->seg_bytes), SS_E_INVALID,
-            "tsa_xxh64_verify_slots: a part but the last is not a multiple of 32");
-    l.ckpt = a->states_dev;
-    l.digests = a->digests_dev;
-    for (uint32_t i0 = 0; i0 < n; i0 += kDgVerifyMax) {
-      l.n = std::min(kDgVerifyMax, n - i0);
-      l.fail = fail_dev + i0;
-      for (uint32_t i = 0; i < l.n; ++i) {
-        require(slots[i0 + i] >= 0, SS_E_INVALID, "tsa_xxh64_verify_slots: negative slot");
-        l.keys[i] = keys[i0 + i];
-        l.slots[i] = slots[i0 + i];
-      }
-      launch_ck(launch_dg_verify(l, static_cast<hipStream_t>(stream)), "tsa_xxh64_verify_slots");
-    }
+    require(n == 0 || src_dev, SS_E_INVALID, "tsa_xxh64_scatter_verify_slots: null staged bytes");
+    arena_checks("tsa_xxh64_scatter_verify_slots", a, keys, slots, n, src_dev, fail_dev, stream);
   });
 }
 
