@@ -125,6 +125,15 @@ SS_API ss_status tsa_test_depth_ctl(uint32_t bound, uint32_t n, const uint64_t* 
  * landing reads, a drop (cancelled, cut short), a claim, failures, a yield, whole landing reads, stop, one read per
  * word. SS_OK when the scenario's checks hold, else SS_E_BACKEND with the failed check in msg. */
 SS_API ss_status tsa_test_read_pool(uint32_t scenario, char* msg, uint32_t cap);
+/* The host contract's cross-stream wait bookkeeping alone (no device): n_ops random event records, waits and stream
+ * replacements over n_streams (1..16) streams, checked against vector clocks that apply every wait. counts[0] = 0 when
+ * every stream's clock stays equal to the reference's, else the first step (1-based) at which one differs; counts[1] =
+ * the waits skipped as implied. mode 0: the library's bookkeeping; 1 and 2: planted mistakes the check must catch (an
+ * earlier wait counted whatever its mark; a replaced stream keeping its predecessor's waits). */
+SS_API ss_status tsa_test_stream_order(uint32_t seed, uint32_t n_ops, uint32_t n_streams, int mode, uint64_t* counts);
+/* Host contract: cross-stream waits given to the runtime since open, and those skipped as implied by an earlier wait of
+ * the same stream. SS_E_INVALID on a device-gated context. */
+SS_API ss_status tsa_test_host_waits(const ss_ctx* c, uint64_t* issued, uint64_t* skipped);
 /* As tsa_test_dgcore_token with run [n_gated] (null: all): the gated layers the token exports (ss_begin's rows). */
 SS_API ss_status tsa_test_dgcore_token_run(void* h, const uint32_t* ids, uint32_t n, const uint8_t* run,
                                            int32_t* table_out, uint64_t* counts, uint32_t n_counts);

@@ -149,6 +149,12 @@ def test_host_contract_matches_reference(name, tmp_path, gpu):
         assert copies == units
     if name in ("qwen-exclusive", "qwen-exclusive-scored", "qwen-exclusive-prefetch"):
         assert copies < units, (units, copies)
+    # cross-stream waits implied by an earlier wait of the same stream are not given (the results above are the
+    # reference's all the same)
+    issued, skipped = ctx.host_waits()
+    assert issued > 0, (issued, skipped)
+    if name.startswith("qwen"):  # many copies per layer behind the same releases and checks
+        assert skipped > 0, (issued, skipped)
     if CASES[name].get("prefetch"):  # the shape exercises certain prefetches and used and dropped speculative ones
         assert tot["prefetched"] > 0 and tot["spec_used"] > 0 and tot["spec_dropped"] > 0, tot
     ctx.close()

@@ -547,6 +547,13 @@ ss_status tsa_test_host_copies(const ss_ctx* c, uint64_t* units, uint64_t* copie
     c->host->copy_counts(units, copies);
   });
 }
+ss_status tsa_test_host_waits(const ss_ctx* c, uint64_t* issued, uint64_t* skipped) {
+  return guard([&] {
+    need(c && issued && skipped, "tsa_test_host_waits: null argument");
+    need(c->host != nullptr, "tsa_test_host_waits: a host-contract context");
+    c->host->wait_counts(issued, skipped);
+  });
+}
 ss_status ss_test_hold_readers(ss_ctx* c, int hold) {
   return guard([&] {
     need(c != nullptr && c->host != nullptr, "ss_test_hold_readers: a host-contract context");

@@ -296,7 +296,7 @@ void* HostCtx::spot_addr(int layer, const DevSpot& s) const {
 // written only after that forward's copies out of them (blocks_ev_, recorded at its end on the copy stream).
 void HostCtx::write_back(const WriteBackOrder& w) {
   if (wb_gate_) {
-    stream_wait(wb_, blocks_ev_);
+    ord_.wait(wb_, blocks_ev_);
     wb_gate_ = false;
   }
   hipEvent_t ev = pooled_event();
@@ -305,7 +305,7 @@ void HostCtx::write_back(const WriteBackOrder& w) {
   const uint64_t ub = d_.layers[size_t(w.layer)].unit_bytes;
   for (size_t i = 0; i < w.slots.size(); ++i)
     copy_d2h(block_addr_[size_t(w.blocks[i])], spot_addr(w.layer, DevSpot{DevSpot::kPool, w.slots[i]}), ub, wb_);
-  ev_record(ev, wb_);
+  ord_.record(ev, wb_);
 }
 
 bool HostCtx::fetch(const FetchOrder& f) {
@@ -395,11 +395,11 @@ void HostCtx::issue_copy_locked(Copy& c, const void* src, hipEvent_t after_ev) {
   const uint64_t n = d_.layers[size_t(c.layer)].unit_bytes;
   const hipStream_t cs = next_copy_stream();
   wait_slot_check(cs, c.dst);
-  for (hipEvent_t e : c.after) stream_wait(cs, e);
+  for (hipEvent_t e : c.after) ord_.wait(cs, e);
   for (uint64_t off = 0; off < n; off += o_.copy_piece_bytes)
     copy_h2d(at(c.dst, off), at(src, off), std::min(o_.copy_piece_bytes, n - off), cs);
-  ev_record(c.done_ev, cs);
-  if (after_ev) ev_record(after_ev, cs);
+  ord_.record(c.done_ev, cs);
+  if (after_ev) ord_.record(after_ev, cs);
   if (dverify_) verify_landed(c);
 }
 
@@ -448,13 +448,13 @@ void HostCtx::issue_run(size_t first, size_t end, uint64_t span) {
     wait_slot_check(cs, c.dst);
     for (hipEvent_t e : c.after) {
       if (!e || std::find(waited, waited + n_waited, e) != waited + n_waited) continue;
-      stream_wait(cs, e);
+      ord_.wait(cs, e);
       if (n_waited < 16) waited[n_waited++] = e;
     }
   }
   for (uint64_t off = 0; off < span; off += o_.copy_piece_bytes)
     copy_h2d(at(lead.dst, off), at(lead.src, off), std::min(o_.copy_piece_bytes, span - off), cs);
-  ev_record(lead.done_ev, cs);
+  ord_.record(lead.done_ev, cs);
   for (size_t k = first; k < end; ++k) {
     Copy& c = *pend_[k];
     if (k != first) {
@@ -473,7 +473,7 @@ void HostCtx::wait_jobs(const std::vector<int32_t>& jobs, hipStream_t es) {
     Copy& c = *jobs_[size_t(j)];
     await(c);
     if (!c.done_ev || std::find(seen.begin(), seen.end(), c.done_ev) != seen.end()) continue;
-    stream_wait(es, c.done_ev);
+    ord_.wait(es, c.done_ev);
     seen.push_back(c.done_ev);
   }
 }
@@ -700,11 +700,11 @@ void HostCtx::stage_to_device(Copy& c) {
       std::lock_guard<std::mutex> lk(copy_mu_);
       if (!ordered) {
         wait_slot_check(copy_, c.dst);
-        for (hipEvent_t e : c.after) stream_wait(copy_, e);
+        for (hipEvent_t e : c.after) ord_.wait(copy_, e);
         ordered = true;
       }
       copy_h2d(at(c.dst, pos + w.at), piece, w.len, copy_);
-      ev_record(st.ev, copy_);
+      ord_.record(st.ev, copy_);
     });
     pos += part.bytes;
   }
@@ -712,7 +712,7 @@ void HostCtx::stage_to_device(Copy& c) {
           "unit (" + std::to_string(c.layer) + ", " + std::to_string(c.unit) + ") bytes differ from the descriptor hash");
   std::lock_guard<std::mutex> lk(copy_mu_);
   if (!states.empty()) keep_checkpoints_locked(gidx(c.layer, c.unit), states);
-  ev_record(c.done_ev, copy_);
+  ord_.record(c.done_ev, copy_);
   if (dverify_) verify_landed(c);
 }
 
@@ -883,7 +883,7 @@ void HostCtx::issue_first_piece(Copy& c, const void* src) {
   std::lock_guard<std::mutex> lk(copy_mu_);
   const hipStream_t cs = next_copy_stream();
   wait_slot_check(cs, c.dst);
-  for (hipEvent_t e : c.after) stream_wait(cs, e);
+  for (hipEvent_t e : c.after) ord_.wait(cs, e);
   copy_h2d(c.dst, src, std::min(o_.copy_piece_bytes, d_.layers[size_t(c.layer)].unit_bytes), cs);
 }
 
@@ -993,14 +993,14 @@ void HostCtx::wait_slot_check(hipStream_t s, const void* dst) {
   const auto it = vdst_.find(dst);
   if (it == vdst_.end()) return;
   if (it->second >= vflushed_) flush_verify();
-  stream_wait(s, vflush_ev_[ventry_flush_[it->second]]);
+  ord_.wait(s, vflush_ev_[ventry_flush_[it->second]]);
   vdst_.erase(it);
 }
 
 void HostCtx::join_copies() {
   for (size_t i = 0; i < copyx_.size(); ++i) {
-    ev_record(joinx_ev_[i], copyx_[i]);
-    stream_wait(copy_, joinx_ev_[i]);
+    ord_.record(joinx_ev_[i], copyx_[i]);
+    ord_.wait(copy_, joinx_ev_[i]);
   }
 }
 
@@ -1018,11 +1018,11 @@ void HostCtx::flush_verify() {
     vtable_host_[i].seg_first = segs;
     segs += count;
   }
-  ev_record(vready_ev_, copy_);
-  stream_wait(vstream_, vready_ev_);
+  ord_.record(vready_ev_, copy_);
+  ord_.wait(vstream_, vready_ev_);
   for (size_t i = 0; i < copyx_.size(); ++i) {
-    ev_record(vreadyx_ev_[i], copyx_[i]);
-    stream_wait(vstream_, vreadyx_ev_[i]);
+    ord_.record(vreadyx_ev_[i], copyx_[i]);
+    ord_.wait(vstream_, vreadyx_ev_[i]);
   }
   tsa_verify_unit* vd = static_cast<tsa_verify_unit*>(vtable_dev_) + vflushed_;
   copy_h2d(vd, vtable_host_ + vflushed_, n * sizeof(tsa_verify_unit), vstream_);
@@ -1039,7 +1039,7 @@ void HostCtx::flush_verify() {
             "device check launch");
   if (t.start) prof_pending_.push_back(t);
   if (vflushes_ == vflush_ev_.size()) vflush_ev_.push_back(dev_->event_create());
-  ev_record(vflush_ev_[vflushes_], vstream_);
+  ord_.record(vflush_ev_[vflushes_], vstream_);
   for (size_t i = vflushed_; i < vused_; ++i) ventry_flush_[i] = vflushes_;
   ++vflushes_;
   vflushed_ = vused_;
@@ -1089,7 +1089,7 @@ void HostCtx::collect_verify() {
     flush_verify();
     copy_d2h(vfail_host_, vfail_dev_, 4 * n, vstream_);
     hip_check(hipMemsetAsync(vfail_dev_, 0, 4 * n, vstream_), "hipMemsetAsync");
-    ev_record(vdone_ev_, vstream_);
+    ord_.record(vdone_ev_, vstream_);
   }
   ev_sync(vdone_ev_);
   std::vector<std::pair<int, int>> units;
@@ -1121,6 +1121,7 @@ void HostCtx::check_stream(void* stream, const char* what) {
   if (!fwd_stream_set_) {
     fwd_stream_ = stream;
     fwd_stream_set_ = true;
+    ord_.forget(static_cast<hipStream_t>(stream));  // (a new stream may reuse an earlier forward's handle)
     return;
   }
   require(stream == fwd_stream_, SS_E_INVALID,
@@ -1200,7 +1201,7 @@ void HostCtx::routes_dev(int layer, const int32_t* ids_dev, int n, void* stream)
   }
   check_stream(stream, "routes_dev");
   copy_d2h(s.ids_host, ids_dev, 4 * uint64_t(n), static_cast<hipStream_t>(stream));
-  ev_record(s.ids_ev, static_cast<hipStream_t>(stream));
+  ord_.record(s.ids_ev, static_cast<hipStream_t>(stream));
   s.ids_n = n;
 }
 
@@ -1263,7 +1264,7 @@ void HostCtx::acquire(int layer, void* stream, bool wait_all, ss_layer_view* out
   PendGuard g{this};
   const HostPlacement::Acquire a = place_.acquire(layer, wait_all);
   flush_copies();
-  if (a.wait_ready) stream_wait(es, s.ready_ev);  // the copies an earlier forward issued into this layer's pool
+  if (a.wait_ready) ord_.wait(es, s.ready_ev);  // the copies an earlier forward issued into this layer's pool
   if (!a.wait_jobs.empty()) {
     const uint64_t t0 = now_ns();
     wait_jobs(a.wait_jobs, es);
@@ -1303,8 +1304,8 @@ void HostCtx::release(int layer, void* stream) {
           "release: layer not acquired or already released");
   check_stream(stream, "release");
   LayerDev& s = L_[size_t(layer)];
-  ev_record(s.release_ev, static_cast<hipStream_t>(stream));
-  ev_record(s.table_ev[s.version], static_cast<hipStream_t>(stream));  // its table is read until here
+  ord_.record(s.release_ev, static_cast<hipStream_t>(stream));
+  ord_.record(s.table_ev[s.version], static_cast<hipStream_t>(stream));  // its table is read until here
   PendGuard g{this};
   place_.release(layer);
   flush_copies();
@@ -1329,14 +1330,14 @@ void HostCtx::end() {
       // the next forward's write-backs reuse blocks this one freed: they wait for blocks_ev_ (every copy out of them);
       // a later read of a block written back in this forward follows its write-back
       if (e.writeback_batches) {
-        ev_record(wb_mark_ev_, wb_);
-        stream_wait(copy_, wb_mark_ev_);
+        ord_.record(wb_mark_ev_, wb_);
+        ord_.wait(copy_, wb_mark_ev_);
       }
-      ev_record(blocks_ev_, copy_);
+      ord_.record(blocks_ev_, copy_);
       wb_gate_ = true;
     }
     // this forward's pool copies are issued but may still be in flight: the next acquire of those layers waits
-    for (int L : e.landed_layers) ev_record(L_[size_t(L)].ready_ev, copy_);
+    for (int L : e.landed_layers) ord_.record(L_[size_t(L)].ready_ev, copy_);
   }
   for (hipEvent_t ev : wb_ev_) ev_pool_.push_back(ev);
   wb_ev_.clear();

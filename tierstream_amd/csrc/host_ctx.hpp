@@ -32,6 +32,7 @@
 #include "model.hpp"
 #include "read_sched.hpp"
 #include "source.hpp"
+#include "stream_order.hpp"
 #include "tierstream_amd/tsa.h"
 #include "tierstream_amd/tsa_test.h"
 
@@ -91,6 +92,8 @@ class HostCtx final : public HostWork {
     *units = pinned_units_;
     *copies = pinned_copies_;
   }
+  // Cross-stream waits given to the runtime and those skipped as implied by an earlier wait of the same stream.
+  void wait_counts(uint64_t* issued, uint64_t* skipped) { ord_.counts(issued, skipped); }
   // Timing (a test hook, between forwards): each device-check launch bracketed by its dispatch's own begin and end
   // stamps when on & TSA_TEST_PROF_VERIFY (this context brackets nothing else); read sums the completed brackets.
   void profile_enable(int on);
@@ -281,6 +284,7 @@ class HostCtx final : public HostWork {
   std::mutex staging_mu_;
   std::condition_variable staging_cv_;
   mutable std::mutex copy_mu_;
+  StreamOrder ord_;  // every event record and cross-stream wait of this context
 
   // reader threads and the reads they start (read_sched.hpp); q_mu_ guards the scheduler, copy states and read-ahead
   // request states together

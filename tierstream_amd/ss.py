@@ -235,6 +235,8 @@ def _declare() -> C.CDLL:
         "tsa_test_verify_failures": (u64, [vp]),
         "tsa_test_dg_hsa_copies": (C.c_int, [vp]),
         "tsa_test_host_copies": (st, [vp, C.POINTER(u64), C.POINTER(u64)]),
+        "tsa_test_host_waits": (st, [vp, C.POINTER(u64), C.POINTER(u64)]),
+        "tsa_test_stream_order": (st, [u32, u32, u32, C.c_int, C.POINTER(u64)]),
         "tsa_test_profile_enable": (st, [vp, C.c_int]),
         "tsa_test_profile_read": (st, [vp, C.c_int, C.POINTER(TsaTestProfile)]),
         "tsa_test_dg_stamps": (st, [vp, C.POINTER(u64), u32, C.POINTER(u32)]),
@@ -526,6 +528,12 @@ class Ctx:
         units, copies = u64(), u64()
         check(_declare().tsa_test_host_copies(self.h, C.byref(units), C.byref(copies)))
         return int(units.value), int(copies.value)
+
+    def host_waits(self) -> tuple[int, int]:
+        """Host contract: (cross-stream waits given to the runtime since open, waits skipped as implied)."""
+        issued, skipped = u64(), u64()
+        check(_declare().tsa_test_host_waits(self.h, C.byref(issued), C.byref(skipped)))
+        return int(issued.value), int(skipped.value)
 
     PROF_COPY, PROF_WRITEBACK, PROF_VERIFY = 0x2, 0x4, 0x8
 
