@@ -406,6 +406,10 @@ void HostCtx::issue_copy_locked(Copy& c, const void* src, hipEvent_t after_ev) {
 void HostCtx::flush_copies() {
   if (pend_.empty()) return;
   std::lock_guard<std::mutex> lk(copy_mu_);
+  // Copies behind a write-back of this forward (into a victim's slot, or out of a block being written) go after the
+  // others the engine call ordered: the write-back, a device-to-host copy on its own stream, runs while the copy
+  // streams move the rest instead of holding the stream it waits on.
+  std::stable_partition(pend_.begin(), pend_.end(), [](const CopyPtr& c) { return !c->after[1] && !c->after[2]; });
   std::vector<CopyRunItem> items(pend_.size());
   for (size_t k = 0; k < pend_.size(); ++k) {
     const Copy& c = *pend_[k];
