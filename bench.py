@@ -115,6 +115,9 @@ def parse():
                          "token's latency excludes them, the timed region's wall clock does not)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the copy peaks and the library's HBM kernels alone (no serve loop: for counter runs)")
+    ap.add_argument("--beside", default="none", choices=["none", "h2d", "d2h"],
+                    help="with --kernels-only: time the unit check while pinned copies of this direction run on "
+                         "another stream (a landing or a write-back beside a check, as in the serve loop)")
     return ap.parse_args()
 
 
@@ -246,7 +249,29 @@ def verify_seg_bytes(unit_bytes):
     return 2048
 
 
-def measure_kernels(tsa, L, C, w, seg=None, reps=10):
+def start_copies(tsa, L, C, direction, n=1 << 30, count=24):
+    """Queue `count` pinned copies of n bytes in one direction on a stream of their own (about 0.45 s of PCIe work at
+    the pinned peak); returns the function that waits for them and frees their buffers."""
+    host, dev, s = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    tsa.check(L.tsa_host_alloc(C.byref(host), n))
+    tsa.check(L.tsa_malloc(C.byref(dev), n))
+    tsa.check(L.tsa_stream_create(C.byref(s)))
+    C.memset(host, 1, n)
+    for _ in range(count):
+        if direction == "h2d":
+            tsa.check(L.tsa_memcpy(dev, host, n, 0, s))
+        else:
+            tsa.check(L.tsa_memcpy(host, dev, n, 1, s))
+
+    def done():
+        tsa.check(L.tsa_stream_sync(s))
+        L.tsa_stream_destroy(s)
+        L.tsa_free(dev)
+        L.tsa_host_free(host)
+    return done
+
+
+def measure_kernels(tsa, L, C, w, seg=None, reps=10, beside="none"):
     """The library's HBM kernels alone at the workload's unit shape: the device XXH64 verify of one unit (checkpoints
     every `seg` bytes, computed on the host) and the unit scatter used as a plain copy of known size (one part of
     256 MiB: read 256 MiB, write 256 MiB), whose counters calibrate the traffic counters of the others."""
@@ -300,11 +325,18 @@ def measure_kernels(tsa, L, C, w, seg=None, reps=10):
         keys, slots = (C.c_uint32 * 1)(0), (C.c_int32 * 1)(0)
         fail = dev_alloc(64)
         fail.upload(np.zeros(16, dtype=np.uint32))
-        t = timed(lambda: tsa.check(L.tsa_xxh64_verify_slots(C.byref(av), keys, slots, 1, C.c_void_p(fail.ptr), s)))
+        busy = start_copies(tsa, L, C, beside) if beside != "none" else None
+        try:
+            t = timed(lambda: tsa.check(L.tsa_xxh64_verify_slots(C.byref(av), keys, slots, 1, C.c_void_p(fail.ptr),
+                                                                 s)))
+        finally:
+            if busy:
+                busy()
         bad = int(fail.download(4, dtype=np.uint32)[0])
         out["verify"] = {"kernel": "dg_verify_kernel", "unit_bytes": ub, "seg_bytes": seg, "segments": n_ck,
                          "us": round(t * 1e6, 1), "GBps": round(ub / t / 1e9, 1),
-                         "frac_of_hbm_peak": round(ub / t / 1e9 / HBM_PEAK_GBPS, 4), "fail_word": bad}
+                         "frac_of_hbm_peak": round(ub / t / 1e9 / HBM_PEAK_GBPS, 4), "fail_word": bad,
+                         "beside": beside}
         if len(parts) > 1 and min(parts) < (8 << 20):  # staged: the scatter and the check in one kernel
             staged = dev_alloc(ub)
             for p, (b, pb) in enumerate(zip(pbufs, parts)):
@@ -413,7 +445,7 @@ def main():
         w = W.scaled(w, inclusive_blocks=a.inclusive, spare_units=a.inclusive + 4)
     shape = W.dg_shape(w)
     if a.kernels_only:
-        kern = measure_kernels(tsa, L, C, w)
+        kern = measure_kernels(tsa, L, C, w, beside=a.beside)
         log(f"kernels {kern}")
         peaks = measure_peaks(tsa, L, C)
         print(json.dumps({"kernels_only": True, "workload": w.name, "kernels": kern, "peaks": peaks}), flush=True)
