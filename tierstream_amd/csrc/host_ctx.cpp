@@ -498,6 +498,7 @@ void HostCtx::finish(Copy& c, int state, ss_status st, const std::string& what) 
 }
 
 void HostCtx::await_quiet(Copy& c) {
+  if (c.state.load() >= Copy::kDone) return;  // (an ended copy never changes state again: no lock needed)
   std::unique_lock<std::mutex> lk(q_mu_);
   done_cv_.wait(lk, [&] { return c.state.load() >= Copy::kDone; });
 }
