@@ -54,6 +54,13 @@ CASES = {
                                   top_k=4, tokens=4, mode=2,
                                   opts=dict(pin_planned=0, group_units=2, copy_piece_bytes=40 * KiB),
                                   budget=dict(tier_mode=1, host_spare_units=6)),
+    # an engine that takes a new stream for every forward (the last one destroyed; a new stream may reuse its handle):
+    # the library's record of what each stream already waits for starts afresh for the new engine stream
+    "qwen-exclusive-fresh-streams": dict(layers=6, units=16, parts=[32 * KiB] * 3, n_res=24, ring=32, dyn=2, steps=20,
+                                         top_k=4, tokens=4, mode=2, fresh=True, opts=dict(pin_planned=0, group_units=2),
+                                         budget=dict(tier_mode=1, host_spare_units=6)),
+    "decode-lru-fresh-streams": dict(layers=4, units=8, parts=[32 * KiB, 32 * KiB, 16 * KiB], n_res=8, ring=16, dyn=2,
+                                     steps=24, top_k=2, mode=0, fresh=True, opts=dict(pin_planned=0)),
     "qwen-exclusive-scored": dict(layers=6, units=16, parts=[32 * KiB] * 3, n_res=24, ring=32, dyn=2, steps=20,
                                   top_k=4, tokens=4, mode=2, opts=dict(pin_planned=0, group_units=2, policy=1),
                                   budget=dict(tier_mode=1, host_spare_units=6)),
@@ -93,7 +100,7 @@ def _run_case(name, tmp_path, gpu):
     d = ss.Desc(desc_json)
     ctx = ss.Ctx(d, ss.budget(**bkw), None, ss.options(**c["opts"]))
     try:
-        cks, tabs, stats, _ = ctx.host_run(routes, c["mode"], prefetch=prefetch)
+        cks, tabs, stats, _ = ctx.host_run(routes, c["mode"] | (0x10 if c.get("fresh") else 0), prefetch=prefetch)
         for s in range(c["steps"]):
             w = want[s]
             got_stats = {k: v for k, v in stats[s].items() if k != "wait_ns"}

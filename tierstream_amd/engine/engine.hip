@@ -145,7 +145,8 @@ extern "C" {
 
 // Host contract: `steps` forwards over every layer with units. routes[step][layer][max_ids] (-1 = none);
 // mode 0 = ss_layer_routes + ss_acquire, 1 = ss_layer_all + ss_acquire, 2 = ss_layer_routes + ss_acquire_groups with
-// one ss_group_wait per group; host_lookahead H > 0: after each layer's routes, ss_host_prefetch_layer of the next H
+// one ss_group_wait per group; mode | 0x10: a new engine stream for every forward, the last one destroyed after its
+// forward (an engine that does not keep one stream; a new stream may reuse the old handle); host_lookahead H > 0: after each layer's routes, ss_host_prefetch_layer of the next H
 // layers with units; prefetch (same shape as routes, may be NULL): after layer l's acquire, ss_prefetch of layer l + 1
 // with its row, CERTAIN on even steps and SPECULATIVE on odd ones (the next layer's ids while this one holds its slots).
 // Outputs (may be NULL): checksums[step][layer][max_ids] of the routed ids (0 for -1),
@@ -157,6 +158,8 @@ __attribute__((visibility("default"))) ss_status tse_host_run_ex(ss_ctx* c, cons
                                                                  uint64_t* tables, ss_layer_stats* stats,
                                                                  double* step_ms) {
   const int L = ss_desc_n_layers(d);
+  const bool fresh_streams = (mode & 0x10) != 0;
+  mode &= 0xF;
   hipStream_t s = nullptr;
   TSE_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
   int32_t* ids_dev = nullptr;
@@ -167,6 +170,11 @@ __attribute__((visibility("default"))) ss_status tse_host_run_ex(ss_ctx* c, cons
       hipHostMalloc(&ids_host, 4ull * max_ids * L, hipHostMallocDefault) != hipSuccess)
     st = SS_E_NOMEM;
   for (int step = 0; st == SS_OK && step < steps; ++step) {
+    if (fresh_streams && step > 0) {  // (the last forward's work on s has completed: it was synchronized)
+      (void)hipStreamDestroy(s);
+      s = nullptr;
+      if ((st = ck(hipStreamCreateWithFlags(&s, hipStreamNonBlocking))) != SS_OK) break;
+    }
     const auto t0 = std::chrono::steady_clock::now();
     ss_layer_stats before{};
     ss_stats_total(c, &before);
