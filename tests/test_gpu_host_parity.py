@@ -59,6 +59,11 @@ CASES = {
     "qwen-exclusive-fresh-streams": dict(layers=6, units=16, parts=[32 * KiB] * 3, n_res=24, ring=32, dyn=2, steps=20,
                                          top_k=4, tokens=4, mode=2, fresh=True, opts=dict(pin_planned=0, group_units=2),
                                          budget=dict(tier_mode=1, host_spare_units=6)),
+    # the null stream as the engine stream (nullptr to every ss_* call; the engine's own work on the null stream too)
+    "qwen-exclusive-null-stream": dict(layers=6, units=16, parts=[32 * KiB] * 3, n_res=24, ring=32, dyn=2, steps=12,
+                                       top_k=4, tokens=4, mode=2, null_stream=True,
+                                       opts=dict(pin_planned=0, group_units=2),
+                                       budget=dict(tier_mode=1, host_spare_units=6)),
     "decode-lru-fresh-streams": dict(layers=4, units=8, parts=[32 * KiB, 32 * KiB, 16 * KiB], n_res=8, ring=16, dyn=2,
                                      steps=24, top_k=2, mode=0, fresh=True, opts=dict(pin_planned=0)),
     "qwen-exclusive-scored": dict(layers=6, units=16, parts=[32 * KiB] * 3, n_res=24, ring=32, dyn=2, steps=20,
@@ -100,7 +105,8 @@ def _run_case(name, tmp_path, gpu):
     d = ss.Desc(desc_json)
     ctx = ss.Ctx(d, ss.budget(**bkw), None, ss.options(**c["opts"]))
     try:
-        cks, tabs, stats, _ = ctx.host_run(routes, c["mode"] | (0x10 if c.get("fresh") else 0), prefetch=prefetch)
+        flags = (0x10 if c.get("fresh") else 0) | (0x20 if c.get("null_stream") else 0)
+        cks, tabs, stats, _ = ctx.host_run(routes, c["mode"] | flags, prefetch=prefetch)
         for s in range(c["steps"]):
             w = want[s]
             got_stats = {k: v for k, v in stats[s].items() if k != "wait_ns"}

@@ -146,7 +146,8 @@ extern "C" {
 // Host contract: `steps` forwards over every layer with units. routes[step][layer][max_ids] (-1 = none);
 // mode 0 = ss_layer_routes + ss_acquire, 1 = ss_layer_all + ss_acquire, 2 = ss_layer_routes + ss_acquire_groups with
 // one ss_group_wait per group; mode | 0x10: a new engine stream for every forward, the last one destroyed after its
-// forward (an engine that does not keep one stream; a new stream may reuse the old handle); host_lookahead H > 0: after each layer's routes, ss_host_prefetch_layer of the next H
+// forward (an engine that does not keep one stream; a new stream may reuse the old handle); mode | 0x20: the null
+// stream, for the ss_* calls (nullptr) and the engine's own work; host_lookahead H > 0: after each layer's routes, ss_host_prefetch_layer of the next H
 // layers with units; prefetch (same shape as routes, may be NULL): after layer l's acquire, ss_prefetch of layer l + 1
 // with its row, CERTAIN on even steps and SPECULATIVE on odd ones (the next layer's ids while this one holds its slots).
 // Outputs (may be NULL): checksums[step][layer][max_ids] of the routed ids (0 for -1),
@@ -158,10 +159,11 @@ __attribute__((visibility("default"))) ss_status tse_host_run_ex(ss_ctx* c, cons
                                                                  uint64_t* tables, ss_layer_stats* stats,
                                                                  double* step_ms) {
   const int L = ss_desc_n_layers(d);
-  const bool fresh_streams = (mode & 0x10) != 0;
+  const bool null_stream = (mode & 0x20) != 0;
+  const bool fresh_streams = (mode & 0x10) != 0 && !null_stream;
   mode &= 0xF;
   hipStream_t s = nullptr;
-  TSE_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  if (!null_stream) TSE_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
   int32_t* ids_dev = nullptr;
   int32_t* ids_host = nullptr;  // pinned: a layer's id copy needs no host wait (the step's end waits for them all)
   unsigned long long* out_dev = nullptr;
@@ -250,7 +252,7 @@ __attribute__((visibility("default"))) ss_status tse_host_run_ex(ss_ctx* c, cons
   (void)hipFree(ids_dev);
   (void)hipFree(out_dev);
   (void)hipHostFree(ids_host);
-  (void)hipStreamDestroy(s);
+  if (s) (void)hipStreamDestroy(s);
   return st;
 }
 
