@@ -307,3 +307,50 @@ def test_three_tier_direct_io(queue, gpu):
             refdg.close()
     finally:
         shutil.rmtree(d0, ignore_errors=True)
+
+
+def test_legacy_null_stream_is_refused(tmp_path, gpu):
+    """The library's streams are CU-masked (a hardware queue each), which the HIP runtime creates as blocking
+    streams: work on the legacy null stream and theirs wait for each other, so a layer's wait kernel there would hold
+    the checks and ready words it waits for until dg_wait_timeout_ms. Every ss_dg_enqueue_* call refuses that stream
+    (nullptr and hipStreamLegacy) with SS_E_INVALID, launches nothing and leaves the context usable: the tokens that
+    follow on the engine's own stream match the reference core. (The reference's streams are non-blocking and take
+    the null stream, src/dg_ctx.cpp:71-73.)"""
+    import ctypes as C
+    import tierstream_amd as tsa
+    _need_ref()
+    s = _Shape(tmp_path)
+    routes = base._routes(s.layers, s.units, s.n_ids, 6, seed=9, zipf=True)
+    ctx, refdg = s.ctx(), s.refdg()
+    L = tsa.lib()
+    vp, i32 = C.c_void_p, C.c_int
+    for name, types in [("ss_dg_enqueue_begin", [vp, vp]), ("ss_dg_enqueue_end", [vp, vp]),
+                        ("ss_dg_enqueue_wait", [vp, i32, vp]), ("ss_dg_enqueue_predict", [vp, i32, vp, i32, vp]),
+                        ("ss_dg_enqueue_export", [vp, i32, vp, i32, i32, vp])]:
+        getattr(L, name).argtypes = types
+        getattr(L, name).restype = i32
+    ids = tsa.DeviceBuffer(4 * 64)
+    ids.upload(np.zeros(64, dtype=np.int32))
+    calls = {
+        "ss_dg_enqueue_begin": lambda st: L.ss_dg_enqueue_begin(ctx.h, st),
+        "ss_dg_enqueue_export": lambda st: L.ss_dg_enqueue_export(ctx.h, 0, ids.ptr, 1, 0, st),
+        "ss_dg_enqueue_predict": lambda st: L.ss_dg_enqueue_predict(ctx.h, 0, ids.ptr, 1, st),
+        "ss_dg_enqueue_wait": lambda st: L.ss_dg_enqueue_wait(ctx.h, 0, st),
+        "ss_dg_enqueue_end": lambda st: L.ss_dg_enqueue_end(ctx.h, st),
+    }
+    try:
+        for name, call in calls.items():
+            for st in (None, 1):  # nullptr, hipStreamLegacy
+                assert call(st) == E_INVALID, (name, st)
+                msg = L.ss_last_error().decode()
+                assert name in msg and "legacy null stream" in msg, msg
+        eng = ss.DgEngine(ctx, s.n_ids)
+        try:
+            for t in range(6):
+                s.check(ctx, refdg, eng, routes[t], tag=("after refusals", t))
+        finally:
+            eng.close()
+    finally:
+        ids.close()
+        ctx.close()
+        refdg.close()

@@ -1320,8 +1320,20 @@ class HipDgCtx final : public DgCtx {
   void check_g(int g, const char* fn) const {
     require(g >= 0 && size_t(g) < x_.gated.size(), SS_E_INVALID, std::string(fn) + ": gated layer out of range");
   }
-  void enqueue_begin(void* stream) override { launch_ck(dg_launch_begin(dw_, stream), "ss_dg_enqueue_begin"); }
+  // Any engine stream but the legacy null stream. The library's streams are CU-masked (a hardware queue each), which
+  // the HIP runtime creates as blocking streams: work on the legacy null stream and theirs wait for each other, so a
+  // layer's wait kernel there would hold the checks and ready words it waits for until dg_wait_timeout_ms.
+  static void check_engine_stream(void* stream, const char* fn) {
+    require(stream != nullptr && stream != static_cast<void*>(hipStreamLegacy), SS_E_INVALID,
+            std::string(fn) + ": the engine stream cannot be the legacy null stream (the library's streams wait for "
+                              "it); use a stream created with hipStreamNonBlocking");
+  }
+  void enqueue_begin(void* stream) override {
+    check_engine_stream(stream, "ss_dg_enqueue_begin");
+    launch_ck(dg_launch_begin(dw_, stream), "ss_dg_enqueue_begin");
+  }
   void enqueue_export(int g, const int32_t* ids_dev, int n, int n_pred, void* stream) override {
+    check_engine_stream(stream, "ss_dg_enqueue_export");
     check_g(g, "ss_dg_enqueue_export");
     require(ids_dev && n >= 1 && uint32_t(n) <= x_.B, SS_E_INVALID, "ss_dg_enqueue_export: 1..dg_max_ids ids");
     require(n_pred >= 0 && n_pred <= int(kDgMaxIds), SS_E_INVALID, "ss_dg_enqueue_export: n_pred 0..64");
@@ -1329,15 +1341,20 @@ class HipDgCtx final : public DgCtx {
               "ss_dg_enqueue_export");
   }
   void enqueue_predict(int g, const int32_t* ids_dev, int n, void* stream) override {
+    check_engine_stream(stream, "ss_dg_enqueue_predict");
     check_g(g, "ss_dg_enqueue_predict");
     require(ids_dev && n >= 1 && n <= int(kDgMaxIds), SS_E_INVALID, "ss_dg_enqueue_predict: 1..64 ids");
     launch_ck(dg_launch_predict(dw_, uint32_t(g), ids_dev, uint32_t(n), stream), "ss_dg_enqueue_predict");
   }
   void enqueue_wait(int g, void* stream) override {
+    check_engine_stream(stream, "ss_dg_enqueue_wait");
     check_g(g, "ss_dg_enqueue_wait");
     launch_ck(dg_launch_wait(dw_, uint32_t(g), stream), "ss_dg_enqueue_wait");
   }
-  void enqueue_end(void* stream) override { launch_ck(dg_launch_end(dw_, stream), "ss_dg_enqueue_end"); }
+  void enqueue_end(void* stream) override {
+    check_engine_stream(stream, "ss_dg_enqueue_end");
+    launch_ck(dg_launch_end(dw_, stream), "ss_dg_enqueue_end");
+  }
 
   uint32_t residency(ss_dg_unit* out, uint32_t cap) override {
     require(!in_token_, SS_E_INVALID, "ss_dg_residency: between tokens only");
