@@ -179,7 +179,15 @@ def test_scatter_verify_slots_arena(gpu, oracle, parts, seg):
     assert np.array_equal(slot_bytes(placed[2]), bad[ub:2 * ub])  # (written as staged, and flagged)
 
 
-@pytest.mark.parametrize("parts,seg", [([64 * 1024] * 3, 8192), ([2048, 4096 + 32, 1000], 1024), ([96], 1024)])
+@pytest.mark.parametrize("parts,seg", [([64 * 1024] * 3, 8192), ([2048, 4096 + 32, 1000], 1024), ([96], 1024),
+                                       # 2 KiB segments and 16-byte aligned parts: the LDS-streamed kernel (whole
+                                       # segments; short last segments and a 16-byte tail; one- and two-stripe
+                                       # segments; many workgroups with a partly dead last wave)
+                                       ([64 * 1024] * 3, 2048), ([2048, 4096 + 32, 1008], 2048), ([96], 2048),
+                                       ([64, 80], 2048), ([8454144, 64 * 1024 + 32, 4 * 1024 * 1024 + 16], 2048),
+                                       # 2 KiB segments, a last part of 1000 bytes: slots 1 and 5 are not 16-byte
+                                       # aligned, so the launch takes the chain kernel
+                                       ([2048, 4096 + 32, 1000], 2048)])
 def test_verify_slots_arena(gpu, oracle, parts, seg):
     """tsa_xxh64_verify_slots (the device-gated check): keys in arena slots, by value; against the oracle's
     checkpoints and XXH64; then one flipped byte fails only its unit."""

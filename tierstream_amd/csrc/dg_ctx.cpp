@@ -103,7 +103,6 @@ class HipTransport final : public DgTransport {
       dev_->free_device(jobs_dev_[k]);
     }
     dev_->free_device(digests_dev_);
-    dev_->free_device(vcount_dev_);
     dev_->stream_destroy(vs_);
     for (hipEvent_t e : vev_) dev_->event_destroy(e);
     for (hipEvent_t e : part_ev_) dev_->event_destroy(e);
@@ -488,7 +487,7 @@ class HipTransport final : public DgTransport {
     prof_end(t, s_[s]);
   }
   // The staged unit in staging buffer k into `slot`, hashed on the way against its checkpoints and digest, on the
-  // copy's stream: a mismatch raises the token's abort; the last workgroup publishes the unit's slot entry.
+  // copy's stream: a mismatch raises the token's abort; a one-wave kernel behind it publishes the unit's slot entry.
   void scatter_check(Stream s, int k, int32_t slot, uint32_t key) {
     require(vused_ + 1 <= vcap_, SS_E_BACKEND, "device verify: more landed units in a token than the table holds");
     DgVerifyLaunch a = vlaunch_;  // (the shape, checkpoints, digests and abort words)
@@ -498,7 +497,6 @@ class HipTransport final : public DgTransport {
     a.fail = vfail_dev_ + vused_;
     a.aux = gated_of(key);
     a.ready = nullptr;
-    a.done_count = vcount_dev_ + 1 + k;  // (the launches of one stream share a count)
     Timed t = prof_take(kProfVerify, x_.unit_bytes, 1);
     hip_check(hipError_t(launch_dg_scatter_verify(a, stage_dev_[k], s_[s], t.a, t.b)), "scatter check launch");
     prof_put(t);
@@ -756,9 +754,7 @@ class HipTransport final : public DgTransport {
     a.err_code = dw.err_code;
     a.err_aux = dw.err_aux;
     a.err = kDgHash;
-    vcount_dev_ = static_cast<uint32_t*>(dev_->alloc_device(64, "verify publication counter"));
-    hip_check(hipMemset(vcount_dev_, 0, 64), "hipMemset");
-    a.done_count = vcount_dev_;
+    a.publish = 1;
     a.slot_of = slot_of_;
   }
   bool publishes_landed() const override { return verify_; }
@@ -1059,7 +1055,6 @@ class HipTransport final : public DgTransport {
   std::vector<uint32_t> wb_sigs_[2];  // (HSA copies, dg_diag) the boundary's write-backs, until seen ended
   bool wb_seen_[2] = {true, true};
   std::thread::id service_thread_;
-  uint32_t* vcount_dev_ = nullptr;    // the launches' publication counter
   uint64_t* digests_dev_ = nullptr;   // [keys]: the descriptor hashes
   uint32_t vcap_ = 0, vused_ = 0;
   uint32_t* vfail_host_ = nullptr;

@@ -46,10 +46,9 @@ struct DgVerifyLaunch {
   uint32_t* err_code = nullptr;
   uint32_t* err_aux = nullptr;
   uint32_t err = 0, aux = 0;
-  // Publication by the launch's last workgroup (done_count null: none): every unit's entry slot_of[key] = slot (when
-  // slot_of is set), then ready[ready_g] = seq (when ready is set). done_count is a zeroed device word the launches of
-  // one stream share (the last workgroup zeroes it again).
-  uint32_t* done_count = nullptr;
+  // Publication (publish 0: none): once the check has ended, a one-wave kernel on the same stream writes every unit's
+  // entry slot_of[key] = slot (when slot_of is set), then ready[ready_g] = seq (when ready is set).
+  uint32_t publish = 0;
   int32_t* slot_of = nullptr;
   uint32_t* ready = nullptr;
   uint32_t ready_g = 0, seq = 0;

@@ -236,80 +236,229 @@ __global__ TSA_VERIFY_BOUNDS void verify_kernel(const TsaVerifyUnit* __restrict_
 // Device-gated verify: one quad per (unit, segment) of the launch's units, all of the arena's part shape. kCopy (the
 // staged units' fused scatter): unit u's bytes are read from src + u x unit_bytes, where its parts lie back to back,
 // and written to their arena slot as they are hashed; the last segment's lane 0 also moves the unit's tail.
-template <bool kCopy>
-__device__ __forceinline__ void dg_verify_body(const DgVerifyLaunch& a, const unsigned char* src) {
-  const uint64_t gid = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  const uint64_t s = gid >> 2;
-  const uint32_t q = uint32_t(gid & 3u);
-  const bool live = s < uint64_t(a.n) * a.unit_segs;
+struct DgSeg {
   uint64_t v = 0, local = 0, key = 0;
-  uint32_t u = 0;
-  bool last = false;
+  uint32_t u = 0, stripes = 0, tail_len = 0;
+  bool live = false, last = false;
+  const unsigned char* from = nullptr;  // the segment's first byte (where it is read)
+  unsigned char* to = nullptr;          // (kCopy) where it is written
   const unsigned char* tail = nullptr;
-  uint32_t tail_len = 0;
-  if (live) {
-    u = uint32_t(s / a.unit_segs);
-    local = s - uint64_t(u) * a.unit_segs;
-    uint64_t k = local;
-    uint32_t p = 0;
-    uint64_t src_off = uint64_t(u) * a.unit_bytes;  // (kCopy) the part's first byte in src
-    while (p + 1 < a.n_parts && k >= a.part_segs[p]) {
-      k -= a.part_segs[p];
-      src_off += a.part_bytes[p++];
-    }
-    const bool last_part = p + 1 == a.n_parts;
-    const uint64_t span = last_part ? a.part_bytes[p] / 32 * 32 : a.part_bytes[p];
-    const uint64_t off = k * a.seg_bytes;
-    const uint64_t end = off + a.seg_bytes < span ? off + a.seg_bytes : span;
-    const unsigned char* base = a.arena[p] + uint64_t(a.slots[u]) * a.part_bytes[p];
-    const unsigned char* from = kCopy ? src + src_off : base;
-    last = last_part && k + 1 == a.part_segs[p];
-    if (last) {
-      tail = from + span;
-      tail_len = uint32_t(a.part_bytes[p] - span);
-      if (kCopy && q == 0)
-        for (uint32_t i = 0; i < tail_len; ++i) const_cast<unsigned char*>(base)[span + i] = tail[i];
-    }
-    key = a.keys[u];
-    v = a.ckpt[(key * a.unit_segs + local) * 4 + q];
-    v = chain_t<kCopy>(v, from + off, const_cast<unsigned char*>(base) + off, end > off ? (end - off) / 32 : 0, q);
+};
+
+// The launch's tables (keys, slots, the parts' arrays) are kernel arguments. Indexed by a per-lane value they become
+// per-lane loads from the argument segment; so the wave reads its first lane's unit with scalar loads (per-lane
+// loads only run in a wave that straddles two units) and the part's fields are carried along the walk over the parts
+// with constant indices, which keeps every other read of the arguments a scalar load.
+
+template <bool kCopy>
+__device__ __forceinline__ DgSeg dg_segment(const DgVerifyLaunch& a, const unsigned char* src, uint64_t s, uint32_t q) {
+  DgSeg g;
+  g.live = s < uint64_t(a.n) * a.unit_segs;
+  const uint32_t u_lane = g.live ? uint32_t(s / a.unit_segs) : a.n - 1;  // (a dead lane sides with the last unit)
+  const uint32_t u0 = __builtin_amdgcn_readfirstlane(u_lane);
+  uint32_t key = a.keys[u0];  // scalar loads
+  int32_t slot = a.slots[u0];
+  if (u_lane != u0) {  // only in a wave that straddles two units
+    key = a.keys[u_lane];
+    slot = a.slots[u_lane];
   }
+  if (!g.live) return g;
+  g.u = u_lane;
+  g.local = s - uint64_t(g.u) * a.unit_segs;
+  uint64_t k = g.local;
+  uint32_t p = 0;
+  uint64_t src_off = uint64_t(g.u) * a.unit_bytes;  // (kCopy) the part's first byte in src
+  uint64_t pbytes = a.part_bytes[0], psegs = a.part_segs[0];
+  const unsigned char* parena = a.arena[0];
+#pragma unroll
+  for (uint32_t i = 0; i + 1 < 4; ++i) {
+    if (p == i && i + 1 < a.n_parts && k >= a.part_segs[i]) {
+      k -= a.part_segs[i];
+      src_off += a.part_bytes[i];
+      p = i + 1;
+      pbytes = a.part_bytes[i + 1];
+      psegs = a.part_segs[i + 1];
+      parena = a.arena[i + 1];
+    }
+  }
+  const bool last_part = p + 1 == a.n_parts;
+  const uint64_t span = last_part ? pbytes / 32 * 32 : pbytes;
+  const uint64_t off = k * a.seg_bytes;
+  const uint64_t end = off + a.seg_bytes < span ? off + a.seg_bytes : span;
+  unsigned char* base = const_cast<unsigned char*>(parena) + uint64_t(slot) * pbytes;
+  const unsigned char* from = kCopy ? src + src_off : base;
+  g.last = last_part && k + 1 == psegs;
+  if (g.last) {
+    g.tail = from + span;
+    g.tail_len = uint32_t(pbytes - span);
+    if (kCopy && q == 0)
+      for (uint32_t i = 0; i < g.tail_len; ++i) base[span + i] = g.tail[i];
+  }
+  g.key = key;
+  g.v = a.ckpt[(g.key * a.unit_segs + g.local) * 4 + q];
+  g.from = from + off;
+  g.to = base + off;
+  g.stripes = end > off ? uint32_t((end - off) / 32) : 0;
+  return g;
+}
+
+// The segment's check (the next checkpoint, or for the unit's last segment the digest) and the gate.
+__device__ __forceinline__ void dg_finish(const DgVerifyLaunch& a, const DgSeg& g, uint64_t v, uint32_t q) {
   uint64_t all[4];
   const uint32_t base4 = threadIdx.x & ~3u;
 #pragma unroll
   for (int k = 0; k < 4; ++k) all[k] = __shfl(v, int(base4 + k), 64);
   bool bad = false;
-  if (live) {
-    if (!last) bad = v != a.ckpt[(key * a.unit_segs + local + 1) * 4 + q];
-    else if (q == 0) bad = xfinal(all, a.unit_bytes, tail, tail_len) != a.digests[key];
+  if (g.live) {
+    if (!g.last) bad = v != a.ckpt[(g.key * a.unit_segs + g.local + 1) * 4 + q];
+    else if (q == 0) bad = xfinal(all, a.unit_bytes, g.tail, g.tail_len) != a.digests[g.key];
   }
   if (bad) {
-    atomicOr(a.fail + u, 1u);
+    atomicOr(a.fail + g.u, 1u);
     if (a.abort) {  // the gate: the token fails before the layer's ready word is written
       if (atomicCAS(a.err_code, 0u, a.err) == 0u) atomicExch(a.err_aux, a.aux);
       atomicExch(a.abort, 1u);
     }
-    __threadfence();  // performed before this thread reaches the barrier below (and so before its group counts)
   }
-  if (!a.done_count) return;
-  // publication by the last workgroup to finish. Only a failing thread has words to release, and it did so above;
-  // the count itself is relaxed (a release fence per workgroup is an L2 write-back each on this chip).
-  __syncthreads();
+}
+
+// Publication after a check, launched behind it on its stream (so it starts once every workgroup of the check has
+// ended and its writes, a failing one's abort among them, are visible): the landed units' slot entries, then the
+// layer's ready word. Counting the check's workgroups in the check itself instead (an agent-scope atomic per
+// workgroup, the last one publishing) cost 8 us per 336 MiB check on this chip: each atomic waits in the memory
+// queues behind the check's own reads and holds its workgroup's slot.
+__global__ __launch_bounds__(64) void dg_publish_kernel(const DgVerifyLaunch a) {
   if (threadIdx.x != 0) return;
-  if (__hip_atomic_fetch_add(a.done_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != gridDim.x - 1u) return;
   if (a.slot_of)
     for (uint32_t i = 0; i < a.n; ++i)
       __hip_atomic_store(a.slot_of + a.keys[i], a.slots[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(a.done_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (a.ready) {
     __threadfence_system();
     __hip_atomic_store(a.ready + a.ready_g, a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 
+template <bool kCopy>
+__device__ __forceinline__ void dg_verify_body(const DgVerifyLaunch& a, const unsigned char* src) {
+  const uint64_t gid = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const uint32_t q = uint32_t(gid & 3u);
+  const DgSeg g = dg_segment<kCopy>(a, src, gid >> 2, q);
+  uint64_t v = 0;
+  if (g.live) v = chain_t<kCopy>(g.v, g.from, g.to, g.stripes, q);
+  dg_finish(a, g, v, q);
+}
+
 __global__ TSA_VERIFY_BOUNDS void dg_verify_kernel(const DgVerifyLaunch a) { dg_verify_body<false>(a, nullptr); }
 __global__ TSA_VERIFY_BOUNDS void dg_scatter_verify_kernel(const DgVerifyLaunch a, const unsigned char* src) {
   dg_verify_body<true>(a, src);
+}
+
+// ---- The LDS-streamed check (2 KiB segments, 16-byte aligned parts) ----
+//
+// The chain loop above reads 8 bytes per lane at a 32-byte stride: every load instruction of a wave touches 16 lines
+// (one per quad) and relies on the CU cache to keep each line for the next three. Here every wave streams its 16
+// segments through LDS instead, with direct-to-LDS 16-byte loads (global_load_lds_dwordx4): 64 lanes fill 1 KiB of
+// LDS per instruction, eight whole 128-byte lines, with the non-temporal hint (the bytes are read once). The quads
+// then run their chains from LDS. Measured on one 336 MiB unit: 52-53 us against 58 us for the chain loop, the same
+// as a plain coalesced 16-byte streaming read of the unit.
+//
+// Per wave: a chunk is 256 bytes (8 stripes) of each of its 16 segments, 4 KiB, four loads: load k carries segments
+// 4k..4k+3, lanes 16i..16i+15 the 16 pieces of segment 4k+i. A segment's stripes are rotated by (its quad index mod 8)
+// inside its 256 bytes, so that the wave's ds_read_b64 of one stripe of all 16 segments spreads over the LDS banks.
+// Two chunk buffers per wave: the loads of chunk c+2 are issued when chunk c has been hashed. The loads are inline
+// assembly, so the compiler neither waits for them nor knows them; each chunk waits for its own loads with an explicit
+// vmcnt (loads complete in order) and the buffer is reused only after its LDS reads have completed (lgkmcnt 0).
+// Lanes whose piece lies past their segment's stripes load the segment's first bytes instead (never out of bounds),
+// and every wave issues the same number of loads, which the vmcnt counts rely on.
+constexpr uint32_t kLdsSegBytes = 2048;  // 8 chunks of 256 bytes per segment
+constexpr uint32_t kLdsChunks = kLdsSegBytes / 256;
+constexpr uint32_t kLdsWaveBytes = 2 * 4096;  // two chunk buffers
+
+__device__ __forceinline__ void lds_load16(const unsigned char* g, uint32_t lds_addr) {
+  uint32_t save;  // M0 (the LDS destination) is restored for the compiler; s_nop: an M0 write before an LDS load
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off nt\n\t"
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0"
+      : "=&s"(save)
+      : "v"(g), "s"(lds_addr)
+      : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_loads() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// The wave's 16 quads (lane = 4 j + q) each hash `stripes` (<= 64) stripes from `from` (16-byte aligned) starting at
+// state v; all 64 lanes must call it. lds: the wave's kLdsWaveBytes of LDS (its address and its 32-bit LDS offset).
+__device__ __forceinline__ uint64_t lds_chain(uint64_t v, const unsigned char* from, uint32_t stripes,
+                                              const unsigned char* lds, uint32_t lds_off) {
+  const uint32_t lane = threadIdx.x & 63u, q = lane & 3u, j = lane >> 2;
+  const uint32_t i = lane >> 4, m = lane & 15u;
+  const unsigned char* src[4];
+  uint32_t n[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {  // the lane loads for segment 4k + i (quad 4k + i's lane 0 holds its source)
+    const int owner = int((4 * k + i) * 4);
+    src[k] = reinterpret_cast<const unsigned char*>(
+        __shfl(static_cast<unsigned long long>(reinterpret_cast<uintptr_t>(from)), owner, 64));
+    n[k] = uint32_t(__shfl(int(stripes), owner, 64));
+  }
+  auto issue = [&](uint32_t c) {
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) {
+      const uint32_t rot = (4 * k + i) & 7u;
+      const uint32_t g = (((m >> 1) - rot) & 7u) + 8 * c;  // the global stripe this lane's LDS piece holds
+      const unsigned char* at = g < n[k] ? src[k] + g * 32 + (m & 1u) * 16 : src[k];
+      lds_load16(at, lds_off + (c & 1u) * 4096 + k * 1024);
+    }
+  };
+  issue(0);
+  issue(1);
+  // v (the segment's checkpoint) arrives here: the compiler's wait for it (a vmcnt(0), which also covers the two
+  // chunks just issued) then sits before the loop, not inside it at every use of the loop-carried state
+  asm volatile("" : "+v"(v));
+  const uint32_t rot = j & 7u;
+  const unsigned char* rd = lds + (j >> 2) * 1024 + (j & 3u) * 256 + q * 8;
+  auto hash = [&](uint32_t c) {
+    const unsigned char* b = rd + (c & 1u) * 4096;
+#pragma unroll
+    for (uint32_t t = 0; t < 8; ++t) {
+      const uint64_t x = *reinterpret_cast<const uint64_t*>(b + ((t + rot) & 7u) * 32);
+      const uint64_t r = xround(v, x);
+      v = 8 * c + t < stripes ? r : v;
+    }
+  };
+  // chunks 0 .. kLdsChunks - 3: the next chunk's four loads may still be in flight; then this buffer is refilled
+#pragma unroll 2
+  for (uint32_t c = 0; c + 2 < kLdsChunks; ++c) {
+    wait_loads<4>();
+    hash(c);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this buffer's LDS reads are done before it is refilled
+    issue(c + 2);
+  }
+  wait_loads<4>();
+  hash(kLdsChunks - 2);
+  wait_loads<0>();
+  hash(kLdsChunks - 1);
+  return v;
+}
+
+__global__ __launch_bounds__(256) void dg_verify_lds_kernel(const DgVerifyLaunch a) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[4 * kLdsWaveBytes];
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  unsigned char* mine = lds + wave * kLdsWaveBytes;
+  const uint32_t mine_off = uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)(mine)));
+  const uint64_t gid = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const uint32_t q = uint32_t(gid & 3u);
+  const DgSeg g = dg_segment<false>(a, nullptr, gid >> 2, q);
+  // a dead quad (past the launch's segments) streams unit 0's first bytes and hashes none of them
+  const unsigned char* from = g.live ? g.from : a.arena[0] + uint64_t(a.slots[0]) * a.part_bytes[0];
+  const uint64_t v = lds_chain(g.v, from, g.live ? g.stripes : 0u, mine, mine_off);
+  dg_finish(a, g, v, q);
 }
 
 }  // namespace dev
@@ -323,17 +472,38 @@ int launch_digest(const TsaUnit* units_dev, uint32_t n, uint64_t* out_dev, hipSt
   return int(hipGetLastError());
 }
 
+// The LDS-streamed kernel needs 2 KiB segments and every part of every unit of the launch 16-byte aligned and at
+// least 16 bytes long (a lane with nothing to load reads its segment's first 16 bytes).
+static bool dg_lds_shape(const DgVerifyLaunch& a) {
+  if (a.seg_bytes != dev::kLdsSegBytes) return false;
+  for (uint32_t p = 0; p < a.n_parts; ++p) {
+    if (reinterpret_cast<uintptr_t>(a.arena[p]) % 16 != 0 || a.part_bytes[p] < 16) return false;
+    if (a.part_bytes[p] % 16 == 0) continue;
+    for (uint32_t u = 0; u < a.n; ++u)
+      if (uint64_t(a.slots[u]) * a.part_bytes[p] % 16 != 0) return false;
+  }
+  return true;
+}
+
+static int launch_publish(const DgVerifyLaunch& a, hipStream_t stream) {
+  if (!a.publish || (!a.slot_of && !a.ready)) return 0;
+  hipLaunchKernelGGL(dev::dg_publish_kernel, dim3(1), dim3(64), 0, stream, a);
+  return int(hipGetLastError());
+}
+
 int launch_dg_verify(const DgVerifyLaunch& a, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   if (a.n == 0 || a.unit_segs == 0) return 0;
   if (a.n > kDgVerifyMax || a.n_parts == 0 || a.n_parts > 4) return int(hipErrorInvalidValue);
   const uint32_t threads = 256;
   const uint64_t blocks = (uint64_t(a.n) * a.unit_segs * 4 + threads - 1) / threads;
   if (blocks > 0x7fffffffull) return int(hipErrorInvalidValue);
+  auto* k = dg_lds_shape(a) ? dev::dg_verify_lds_kernel : dev::dg_verify_kernel;
   if (start && stop)  // the events take the dispatch's own begin and end timestamps
-    hipExtLaunchKernelGGL(dev::dg_verify_kernel, dim3(uint32_t(blocks)), dim3(threads), 0, stream, start, stop, 0, a);
+    hipExtLaunchKernelGGL(k, dim3(uint32_t(blocks)), dim3(threads), 0, stream, start, stop, 0, a);
   else
-    hipLaunchKernelGGL(dev::dg_verify_kernel, dim3(uint32_t(blocks)), dim3(threads), 0, stream, a);
-  return int(hipGetLastError());
+    hipLaunchKernelGGL(k, dim3(uint32_t(blocks)), dim3(threads), 0, stream, a);
+  const int e = int(hipGetLastError());
+  return e ? e : launch_publish(a, stream);
 }
 
 int launch_dg_scatter_verify(const DgVerifyLaunch& a, const void* src, hipStream_t stream, hipEvent_t start,
@@ -349,7 +519,8 @@ int launch_dg_scatter_verify(const DgVerifyLaunch& a, const void* src, hipStream
                           0, a, s);
   else
     hipLaunchKernelGGL(dev::dg_scatter_verify_kernel, dim3(uint32_t(blocks)), dim3(threads), 0, stream, a, s);
-  return int(hipGetLastError());
+  const int e = int(hipGetLastError());
+  return e ? e : launch_publish(a, stream);
 }
 
 int launch_verify(const TsaVerifyUnit* units_dev, uint32_t n_units, uint64_t n_segments, uint64_t seg_bytes,
