@@ -90,13 +90,16 @@ def _verify(gpu, ext_groups, states_list, digests, seg):
     return fail.download(4 * len(units)).view(np.uint32)
 
 
-@pytest.mark.parametrize("seg", [1024, 1536, 8192, 65536])
-def test_verify_checkpoint_parallel(gpu, oracle, seg):
+@pytest.mark.parametrize("seg,align", [(1024, 256), (1536, 256), (8192, 256), (65536, 256),
+                                       # 2 KiB segments: waves of whole 16-byte aligned segments stream through LDS,
+                                       # the rest (the 31-byte and empty units, 8-byte aligned extents) run the chain
+                                       (2048, 256), (2048, 8)])
+def test_verify_checkpoint_parallel(gpu, oracle, seg, align):
     rng = np.random.default_rng(seg)
     shapes = [[1 << 20] * 3, [(1 << 18) + 32 * 5, 4096, 1000], [31], [0], [32 * 3 + 5], [1 << 16, 1 << 16]]
     groups = [[rng.integers(0, 256, s, dtype=np.uint8) for s in sh] for sh in shapes]
     flat = [a for g in groups for a in g]
-    buf, ext = _pack(gpu, flat)
+    buf, ext = _pack(gpu, flat, align)
     ext_groups, k = [], 0
     for g in groups:
         ext_groups.append(ext[k:k + len(g)])

@@ -157,20 +157,145 @@ __global__ __launch_bounds__(256) void digest_kernel(const TsaUnit* __restrict__
   if (live && q == 0) out[u] = xfinal(all, total, tail, tail_len);
 }
 
-// Both verify kernels are held to 8 waves per SIMD (at most 64 VGPRs): unbounded, the compiler spends registers on
-// scheduling (83-86 VGPRs, 5 waves per SIMD) and the kernel has 5/8 of the loads in flight it could; bounded it needs
-// 52-58 with no spill, and one 336 MiB unit's check (3 parts, 2 KiB segments, timed alone in a fresh process) ran
-// 67 -> 62 us.
+// ---- The LDS-streamed check (2 KiB segments in 16-byte aligned memory) ----
+//
+// The chain loop above reads 8 bytes per lane at a 32-byte stride: every load instruction of a wave touches 16 lines
+// (one per quad) and relies on the CU cache to keep each line for the next three. Here every wave streams its 16
+// segments through LDS instead, with direct-to-LDS 16-byte loads (global_load_lds_dwordx4): 64 lanes fill 1 KiB of
+// LDS per instruction, eight whole 128-byte lines, with the non-temporal hint (the bytes are read once). The quads
+// then run their chains from LDS. Measured on one 336 MiB unit: 52-53 us against 58 us for the chain loop, the same
+// as a plain coalesced 16-byte streaming read of the unit.
+//
+// Per wave: a chunk is 256 bytes (8 stripes) of each of its 16 segments, 4 KiB, four loads: load k carries segments
+// 4k..4k+3, lanes 16i..16i+15 the 16 pieces of segment 4k+i. A segment's stripes are rotated by (its quad index mod 8)
+// inside its 256 bytes, so that the wave's ds_read_b64 of one stripe of all 16 segments spreads over the LDS banks.
+// Two chunk buffers per wave: the loads of chunk c+2 are issued when chunk c has been hashed. The loads are inline
+// assembly, so the compiler neither waits for them nor knows them; each chunk waits for its own loads with an explicit
+// vmcnt (loads complete in order) and the buffer is reused only after its LDS reads have completed (lgkmcnt 0).
+// Lanes whose piece lies past their segment's stripes load the segment's first bytes instead (never out of bounds),
+// and every wave issues the same number of loads, which the vmcnt counts rely on.
+constexpr uint32_t kLdsSegBytes = 2048;  // 8 chunks of 256 bytes per segment
+constexpr uint32_t kLdsChunks = kLdsSegBytes / 256;
+constexpr uint32_t kLdsWaveBytes = 2 * 4096;  // two chunk buffers
+
+__device__ __forceinline__ void lds_load16(const unsigned char* g, uint32_t lds_addr) {
+  uint32_t save;  // M0 (the LDS destination) is restored for the compiler; s_nop: an M0 write before an LDS load
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off nt\n\t"
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0"
+      : "=&s"(save)
+      : "v"(g), "s"(lds_addr)
+      : "memory");
+}
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) u32x4 gu32x4_t;
+
+template <int N>
+__device__ __forceinline__ void wait_loads() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// The wave's 16 quads (lane = 4 j + q) each hash `stripes` (<= 64) stripes from `from` (16-byte aligned) starting at
+// state v; all 64 lanes must call it. lds: the wave's kLdsWaveBytes of LDS (its address and its 32-bit LDS offset).
+// kCopy: every stripe is also written to the same offset from `to` (16-byte aligned), each lane storing the 16-byte
+// pieces it loaded, from LDS, once they have landed.
+template <bool kCopy>
+__device__ __forceinline__ uint64_t lds_chain_t(uint64_t v, const unsigned char* from, unsigned char* to,
+                                                uint32_t stripes, const unsigned char* lds, uint32_t lds_off) {
+  const uint32_t lane = threadIdx.x & 63u, q = lane & 3u, j = lane >> 2;
+  const uint32_t i = lane >> 4, m = lane & 15u;
+  const unsigned char* src[4];
+  unsigned char* dst[4];
+  uint32_t n[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {  // the lane loads for segment 4k + i (quad 4k + i's lane 0 holds its source)
+    const int owner = int((4 * k + i) * 4);
+    src[k] = reinterpret_cast<const unsigned char*>(
+        __shfl(static_cast<unsigned long long>(reinterpret_cast<uintptr_t>(from)), owner, 64));
+    if (kCopy)
+      dst[k] = reinterpret_cast<unsigned char*>(
+          __shfl(static_cast<unsigned long long>(reinterpret_cast<uintptr_t>(to)), owner, 64));
+    n[k] = uint32_t(__shfl(int(stripes), owner, 64));
+  }
+  auto piece = [&](uint32_t c, uint32_t k) {  // the global stripe this lane's piece of load k of chunk c holds
+    return (((m >> 1) - ((4 * k + i) & 7u)) & 7u) + 8 * c;
+  };
+  auto issue = [&](uint32_t c) {
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) {
+      const uint32_t g = piece(c, k);
+      const unsigned char* at = g < n[k] ? src[k] + g * 32 + (m & 1u) * 16 : src[k];
+      lds_load16(at, lds_off + (c & 1u) * 4096 + k * 1024);
+    }
+  };
+  issue(0);
+  issue(1);
+  // v (the segment's checkpoint) arrives here: the compiler's wait for it (a vmcnt(0), which also covers the two
+  // chunks just issued) then sits before the loop, not inside it at every use of the loop-carried state
+  asm volatile("" : "+v"(v));
+  const uint32_t rot = j & 7u;
+  const unsigned char* rd = lds + (j >> 2) * 1024 + (j & 3u) * 256 + q * 8;
+  auto hash = [&](uint32_t c) {
+    if (kCopy) {  // the lane's own four pieces, as they landed in LDS
+#pragma unroll
+      for (uint32_t k = 0; k < 4; ++k) {
+        const uint32_t g = piece(c, k);
+        const u32x4 x = *reinterpret_cast<const u32x4*>(lds + (c & 1u) * 4096 + k * 1024 + lane * 16);
+        if (g < n[k])  // (a global store: a generic one would also count on the LDS counter waited on below)
+          *reinterpret_cast<gu32x4_t*>(reinterpret_cast<uintptr_t>(dst[k] + g * 32 + (m & 1u) * 16)) = x;
+      }
+    }
+    const unsigned char* b = rd + (c & 1u) * 4096;
+#pragma unroll
+    for (uint32_t t = 0; t < 8; ++t) {
+      const uint64_t x = *reinterpret_cast<const uint64_t*>(b + ((t + rot) & 7u) * 32);
+      const uint64_t r = xround(v, x);
+      v = 8 * c + t < stripes ? r : v;
+    }
+  };
+  // chunks 0 .. kLdsChunks - 3: the next chunk's four loads may still be in flight (vmcnt 4 also holds with the copy's
+  // stores among them: loads complete in order among themselves); then this buffer is refilled
+#pragma unroll 2
+  for (uint32_t c = 0; c + 2 < kLdsChunks; ++c) {
+    wait_loads<4>();
+    hash(c);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this buffer's LDS reads are done before it is refilled
+    issue(c + 2);
+  }
+  wait_loads<4>();
+  hash(kLdsChunks - 2);
+  wait_loads<0>();
+  hash(kLdsChunks - 1);
+  return v;
+}
+__device__ __forceinline__ uint64_t lds_chain(uint64_t v, const unsigned char* from, uint32_t stripes,
+                                              const unsigned char* lds, uint32_t lds_off) {
+  return lds_chain_t<false>(v, from, nullptr, stripes, lds, lds_off);
+}
+
+// The chain-loop kernels (dg_verify_kernel, dg_scatter_verify_kernel) are held to 8 waves per SIMD (at most 64
+// VGPRs): unbounded, the compiler spends registers on scheduling (83-86 VGPRs, 5 waves per SIMD) and the kernel has
+// 5/8 of the loads in flight it could; bounded it needs 52-58 with no spill, and one 336 MiB unit's check (3 parts,
+// 2 KiB segments, timed alone in a fresh process) ran 67 -> 62 us. The LDS-streamed kernels keep their loads in LDS,
+// not in registers, and run 5 waves per SIMD (their 32 KiB of LDS per workgroup).
 #define TSA_VERIFY_BOUNDS __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8)))
 
-// One (unit, segment) per quad. seg_first is the prefix sum of segments over the launch's units (ascending).
-__global__ TSA_VERIFY_BOUNDS void verify_kernel(const TsaVerifyUnit* __restrict__ units, uint32_t n_units,
+// One (unit, segment) per quad. seg_first is the prefix sum of segments over the launch's units (ascending). A wave
+// whose segments are all 2 KiB pieces of 16-byte aligned extents, each of at least one stripe, streams them through
+// LDS (lds_chain); any other wave (other segment sizes, unaligned extents, a last extent under 32 bytes) runs the
+// chain loop. The choice is the wave's: all its lanes take one path.
+__global__ __launch_bounds__(256) void verify_kernel(const TsaVerifyUnit* __restrict__ units, uint32_t n_units,
                                                      uint64_t n_segments, uint64_t seg_bytes,
                                                      uint32_t* __restrict__ fail) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[4 * kLdsWaveBytes];
   const uint64_t gid = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const uint64_t s = gid >> 2;
   const uint32_t q = uint32_t(gid & 3u);
-  const bool live = s < n_segments;
+  bool live = s < n_segments;
   uint32_t ui = 0;
   if (live) {  // the unit holding global segment s (units sorted by seg_first)
     uint32_t lo = 0, hi = n_units;
@@ -182,8 +307,9 @@ __global__ TSA_VERIFY_BOUNDS void verify_kernel(const TsaVerifyUnit* __restrict_
     ui = lo;
   }
   uint64_t v = 0;
-  bool last = false, check_state = false;
-  uint64_t local = 0, total = 0;
+  bool last = false;
+  uint64_t local = 0, total = 0, stripes = 0;
+  const unsigned char* from = nullptr;
   const unsigned char* tail = nullptr;
   uint32_t tail_len = 0;
   const TsaVerifyUnit* un = units + ui;
@@ -192,7 +318,6 @@ __global__ TSA_VERIFY_BOUNDS void verify_kernel(const TsaVerifyUnit* __restrict_
     // the extent and the segment inside it
     uint64_t k = local;
     uint32_t e = 0;
-    uint64_t off = 0, stripes = 0;
     for (; e < un->n_ext; ++e) {
       const uint64_t b = un->ext[e].bytes;
       const bool last_ext = e + 1 == un->n_ext;
@@ -200,9 +325,10 @@ __global__ TSA_VERIFY_BOUNDS void verify_kernel(const TsaVerifyUnit* __restrict_
       uint64_t nseg = (span + seg_bytes - 1) / seg_bytes;
       if (last_ext && nseg == 0) nseg = 1;
       if (k < nseg) {
-        off = k * seg_bytes;
+        const uint64_t off = k * seg_bytes;
         const uint64_t end = off + seg_bytes < span ? off + seg_bytes : span;
         stripes = (end - off) / 32;
+        from = static_cast<const unsigned char*>(un->ext[e].ptr) + off;
         last = last_ext && k + 1 == nseg;
         if (last) {
           tail = static_cast<const unsigned char*>(un->ext[e].ptr) + span;
@@ -212,21 +338,36 @@ __global__ TSA_VERIFY_BOUNDS void verify_kernel(const TsaVerifyUnit* __restrict_
       }
       k -= nseg;
     }
-    if (e == un->n_ext) {  // the launch's prefix sums disagree with the extents: reported, nothing read
+    if (e == un->n_ext) {  // the launch's prefix sums disagree with the extents: reported, nothing read or checked
       if (q == 0) atomicOr(fail + ui, 2u);
-      return;  // (the whole quad: its lanes share s)
+      live = false;
+    } else {
+      v = un->states[4 * local + q];
+      total = un->total;
     }
-    v = un->states[4 * local + q];
-    v = chain(v, static_cast<const unsigned char*>(un->ext[e].ptr) + off, stripes, q);
-    total = un->total;
-    check_state = !last;
+  }
+  const uint64_t lanes_live = __ballot(live);
+  if (lanes_live == 0) return;  // (the whole wave)
+  const bool lds_path = seg_bytes == kLdsSegBytes &&
+                        __all(!live || ((reinterpret_cast<uintptr_t>(from) & 15u) == 0 && stripes >= 1));
+  if (lds_path) {
+    // a dead lane streams a live lane's segment (in bounds) and hashes none of it
+    const unsigned char* any = reinterpret_cast<const unsigned char*>(__shfl(
+        static_cast<unsigned long long>(reinterpret_cast<uintptr_t>(from)), __ffsll((long long)lanes_live) - 1, 64));
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    unsigned char* mine = lds + wave * kLdsWaveBytes;
+    const uint32_t mine_off =
+        uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)(mine)));
+    v = lds_chain(v, live ? from : any, live ? uint32_t(stripes) : 0u, mine, mine_off);
+  } else if (live) {
+    v = chain(v, from, stripes, q);
   }
   uint64_t all[4];
   const uint32_t base = threadIdx.x & ~3u;
 #pragma unroll
   for (int k = 0; k < 4; ++k) all[k] = __shfl(v, int(base + k), 64);
   if (!live) return;
-  if (check_state) {
+  if (!last) {
     if (v != un->states[4 * (local + 1) + q]) atomicOr(fail + ui, 1u);
   } else if (q == 0) {
     if (xfinal(all, total, tail, tail_len) != un->digest) atomicOr(fail + ui, 1u);
@@ -256,9 +397,10 @@ __device__ __forceinline__ DgSeg dg_segment(const DgVerifyLaunch& a, const unsig
   g.live = s < uint64_t(a.n) * a.unit_segs;
   const uint32_t u_lane = g.live ? uint32_t(s / a.unit_segs) : a.n - 1;  // (a dead lane sides with the last unit)
   const uint32_t u0 = __builtin_amdgcn_readfirstlane(u_lane);
-  uint32_t key = a.keys[u0];  // scalar loads
+  uint32_t key = a.keys[u0];  // scalar loads, here (the empty asm takes them as scalars before any branch)
   int32_t slot = a.slots[u0];
-  if (u_lane != u0) {  // only in a wave that straddles two units
+  asm volatile("" ::"s"(key), "s"(slot));
+  if (!__all(u_lane == u0)) {  // only in a wave that straddles two units
     key = a.keys[u_lane];
     slot = a.slots[u_lane];
   }
@@ -353,112 +495,23 @@ __global__ TSA_VERIFY_BOUNDS void dg_scatter_verify_kernel(const DgVerifyLaunch 
   dg_verify_body<true>(a, src);
 }
 
-// ---- The LDS-streamed check (2 KiB segments, 16-byte aligned parts) ----
-//
-// The chain loop above reads 8 bytes per lane at a 32-byte stride: every load instruction of a wave touches 16 lines
-// (one per quad) and relies on the CU cache to keep each line for the next three. Here every wave streams its 16
-// segments through LDS instead, with direct-to-LDS 16-byte loads (global_load_lds_dwordx4): 64 lanes fill 1 KiB of
-// LDS per instruction, eight whole 128-byte lines, with the non-temporal hint (the bytes are read once). The quads
-// then run their chains from LDS. Measured on one 336 MiB unit: 52-53 us against 58 us for the chain loop, the same
-// as a plain coalesced 16-byte streaming read of the unit.
-//
-// Per wave: a chunk is 256 bytes (8 stripes) of each of its 16 segments, 4 KiB, four loads: load k carries segments
-// 4k..4k+3, lanes 16i..16i+15 the 16 pieces of segment 4k+i. A segment's stripes are rotated by (its quad index mod 8)
-// inside its 256 bytes, so that the wave's ds_read_b64 of one stripe of all 16 segments spreads over the LDS banks.
-// Two chunk buffers per wave: the loads of chunk c+2 are issued when chunk c has been hashed. The loads are inline
-// assembly, so the compiler neither waits for them nor knows them; each chunk waits for its own loads with an explicit
-// vmcnt (loads complete in order) and the buffer is reused only after its LDS reads have completed (lgkmcnt 0).
-// Lanes whose piece lies past their segment's stripes load the segment's first bytes instead (never out of bounds),
-// and every wave issues the same number of loads, which the vmcnt counts rely on.
-constexpr uint32_t kLdsSegBytes = 2048;  // 8 chunks of 256 bytes per segment
-constexpr uint32_t kLdsChunks = kLdsSegBytes / 256;
-constexpr uint32_t kLdsWaveBytes = 2 * 4096;  // two chunk buffers
-
-__device__ __forceinline__ void lds_load16(const unsigned char* g, uint32_t lds_addr) {
-  uint32_t save;  // M0 (the LDS destination) is restored for the compiler; s_nop: an M0 write before an LDS load
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %2\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, off nt\n\t"
-      "s_mov_b32 m0, %0\n\t"
-      "s_nop 0"
-      : "=&s"(save)
-      : "v"(g), "s"(lds_addr)
-      : "memory");
-}
-template <int N>
-__device__ __forceinline__ void wait_loads() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// The wave's 16 quads (lane = 4 j + q) each hash `stripes` (<= 64) stripes from `from` (16-byte aligned) starting at
-// state v; all 64 lanes must call it. lds: the wave's kLdsWaveBytes of LDS (its address and its 32-bit LDS offset).
-__device__ __forceinline__ uint64_t lds_chain(uint64_t v, const unsigned char* from, uint32_t stripes,
-                                              const unsigned char* lds, uint32_t lds_off) {
-  const uint32_t lane = threadIdx.x & 63u, q = lane & 3u, j = lane >> 2;
-  const uint32_t i = lane >> 4, m = lane & 15u;
-  const unsigned char* src[4];
-  uint32_t n[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {  // the lane loads for segment 4k + i (quad 4k + i's lane 0 holds its source)
-    const int owner = int((4 * k + i) * 4);
-    src[k] = reinterpret_cast<const unsigned char*>(
-        __shfl(static_cast<unsigned long long>(reinterpret_cast<uintptr_t>(from)), owner, 64));
-    n[k] = uint32_t(__shfl(int(stripes), owner, 64));
-  }
-  auto issue = [&](uint32_t c) {
-#pragma unroll
-    for (uint32_t k = 0; k < 4; ++k) {
-      const uint32_t rot = (4 * k + i) & 7u;
-      const uint32_t g = (((m >> 1) - rot) & 7u) + 8 * c;  // the global stripe this lane's LDS piece holds
-      const unsigned char* at = g < n[k] ? src[k] + g * 32 + (m & 1u) * 16 : src[k];
-      lds_load16(at, lds_off + (c & 1u) * 4096 + k * 1024);
-    }
-  };
-  issue(0);
-  issue(1);
-  // v (the segment's checkpoint) arrives here: the compiler's wait for it (a vmcnt(0), which also covers the two
-  // chunks just issued) then sits before the loop, not inside it at every use of the loop-carried state
-  asm volatile("" : "+v"(v));
-  const uint32_t rot = j & 7u;
-  const unsigned char* rd = lds + (j >> 2) * 1024 + (j & 3u) * 256 + q * 8;
-  auto hash = [&](uint32_t c) {
-    const unsigned char* b = rd + (c & 1u) * 4096;
-#pragma unroll
-    for (uint32_t t = 0; t < 8; ++t) {
-      const uint64_t x = *reinterpret_cast<const uint64_t*>(b + ((t + rot) & 7u) * 32);
-      const uint64_t r = xround(v, x);
-      v = 8 * c + t < stripes ? r : v;
-    }
-  };
-  // chunks 0 .. kLdsChunks - 3: the next chunk's four loads may still be in flight; then this buffer is refilled
-#pragma unroll 2
-  for (uint32_t c = 0; c + 2 < kLdsChunks; ++c) {
-    wait_loads<4>();
-    hash(c);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this buffer's LDS reads are done before it is refilled
-    issue(c + 2);
-  }
-  wait_loads<4>();
-  hash(kLdsChunks - 2);
-  wait_loads<0>();
-  hash(kLdsChunks - 1);
-  return v;
-}
-
-__global__ __launch_bounds__(256) void dg_verify_lds_kernel(const DgVerifyLaunch a) {
+template <bool kCopy>
+__device__ __forceinline__ void dg_verify_lds_body(const DgVerifyLaunch& a, const unsigned char* src) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[4 * kLdsWaveBytes];
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   unsigned char* mine = lds + wave * kLdsWaveBytes;
   const uint32_t mine_off = uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)(mine)));
   const uint64_t gid = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const uint32_t q = uint32_t(gid & 3u);
-  const DgSeg g = dg_segment<false>(a, nullptr, gid >> 2, q);
-  // a dead quad (past the launch's segments) streams unit 0's first bytes and hashes none of them
-  const unsigned char* from = g.live ? g.from : a.arena[0] + uint64_t(a.slots[0]) * a.part_bytes[0];
-  const uint64_t v = lds_chain(g.v, from, g.live ? g.stripes : 0u, mine, mine_off);
+  const DgSeg g = dg_segment<kCopy>(a, src, gid >> 2, q);
+  // a dead quad (past the launch's segments) streams unit 0's first bytes and hashes (and writes) none of them
+  const unsigned char* from = g.live ? g.from : kCopy ? src : a.arena[0] + uint64_t(a.slots[0]) * a.part_bytes[0];
+  const uint64_t v = lds_chain_t<kCopy>(g.v, from, g.to, g.live ? g.stripes : 0u, mine, mine_off);
   dg_finish(a, g, v, q);
+}
+__global__ __launch_bounds__(256) void dg_verify_lds_kernel(const DgVerifyLaunch a) { dg_verify_lds_body<false>(a, nullptr); }
+__global__ __launch_bounds__(256) void dg_scatter_verify_lds_kernel(const DgVerifyLaunch a, const unsigned char* src) {
+  dg_verify_lds_body<true>(a, src);
 }
 
 }  // namespace dev
@@ -506,6 +559,14 @@ int launch_dg_verify(const DgVerifyLaunch& a, hipStream_t stream, hipEvent_t sta
   return e ? e : launch_publish(a, stream);
 }
 
+// The fused kernel's LDS form also needs the staged bytes 16-byte aligned: src and every part of every staged unit.
+static bool dg_scatter_lds_shape(const DgVerifyLaunch& a, const void* src) {
+  if (!dg_lds_shape(a) || reinterpret_cast<uintptr_t>(src) % 16 != 0) return false;
+  for (uint32_t p = 0; p < a.n_parts; ++p)
+    if (a.part_bytes[p] % 16 != 0) return false;
+  return true;
+}
+
 int launch_dg_scatter_verify(const DgVerifyLaunch& a, const void* src, hipStream_t stream, hipEvent_t start,
                              hipEvent_t stop) {
   if (a.n == 0 || a.unit_segs == 0) return 0;
@@ -514,11 +575,11 @@ int launch_dg_scatter_verify(const DgVerifyLaunch& a, const void* src, hipStream
   const uint64_t blocks = (uint64_t(a.n) * a.unit_segs * 4 + threads - 1) / threads;
   if (blocks > 0x7fffffffull) return int(hipErrorInvalidValue);
   const unsigned char* s = static_cast<const unsigned char*>(src);
+  auto* k = dg_scatter_lds_shape(a, src) ? dev::dg_scatter_verify_lds_kernel : dev::dg_scatter_verify_kernel;
   if (start && stop)
-    hipExtLaunchKernelGGL(dev::dg_scatter_verify_kernel, dim3(uint32_t(blocks)), dim3(threads), 0, stream, start, stop,
-                          0, a, s);
+    hipExtLaunchKernelGGL(k, dim3(uint32_t(blocks)), dim3(threads), 0, stream, start, stop, 0, a, s);
   else
-    hipLaunchKernelGGL(dev::dg_scatter_verify_kernel, dim3(uint32_t(blocks)), dim3(threads), 0, stream, a, s);
+    hipLaunchKernelGGL(k, dim3(uint32_t(blocks)), dim3(threads), 0, stream, a, s);
   const int e = int(hipGetLastError());
   return e ? e : launch_publish(a, stream);
 }
