@@ -47,25 +47,36 @@ METRIC = "decode-step serve latency p50/p99; miss H2D GB/s and HBM GB/s vs roofl
 HBM_PEAK_GBPS = 8000.0
 TICK_NS = 10.0  # wall_clock64 runs at 100 MHz on gfx950
 # HBM bytes one verify launch moves per unit it checks, keyed by unit bytes: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
-# on a launch of one unit of this shape (dg_verify_kernel through tsa_xxh64_verify_slots), each scaled by the
-# counter's reading for a copy kernel of known size (FETCH 2.0, WRITE 1.0), 2 KiB checkpoint segments: 355,269.75 KiB
-# fetched, nothing written (profiles/dg_verify_kernel_mixtral_unit_pmc.md).
-VERIFY_TRAFFIC_PER_UNIT = {352321536: 363796224}
-# The staged units' fused scatter and check (dg_scatter_verify_kernel), keyed by unit bytes: FETCH_SIZE x 2.0 +
+# on a launch of one unit of this shape (dg_verify_lds_kernel through tsa_xxh64_verify_slots), each scaled by the
+# counter's reading for a copy kernel of known size (FETCH 2.0, WRITE 1.0), 2 KiB checkpoint segments: 349,927.25 KiB
+# fetched, nothing written (profiles/dg_verify_lds_kernel_mixtral_unit_pmc.md).
+VERIFY_TRAFFIC_PER_UNIT = {352321536: 358325504, 24772608: 25338624}
+# The staged units' fused scatter and check (dg_scatter_verify_lds_kernel), keyed by unit bytes: FETCH_SIZE x 2.0 +
 # WRITE_SIZE x 1.0 on one launch of one unit of this shape through tsa_xxh64_scatter_verify_slots, 2 KiB segments
-# (profiles/dg_scatter_verify_kernel_deepseek_unit_pmc.md).
-SCATTER_VERIFY_TRAFFIC_PER_UNIT = {24772608: 50441780}
-TRAFFIC_SOURCE = {("verify", 352321536): "profiles/dg_verify_kernel_mixtral_unit_pmc.md",
-                  ("fused", 24772608): "profiles/dg_scatter_verify_kernel_deepseek_unit_pmc.md"}
+# (profiles/dg_scatter_verify_lds_kernel_deepseek_unit_pmc.md).
+SCATTER_VERIFY_TRAFFIC_PER_UNIT = {24772608: 50273920}
+TRAFFIC_SOURCE = {("verify", 352321536): "profiles/dg_verify_lds_kernel_mixtral_unit_pmc.md",
+                  ("verify", 24772608): "profiles/dg_scatter_verify_lds_kernel_deepseek_unit_pmc.md",
+                  ("fused", 24772608): "profiles/dg_scatter_verify_lds_kernel_deepseek_unit_pmc.md"}
 # The host contract's verify_kernel: HBM bytes fetched per algorithmic byte hashed, keyed by unit bytes, from
 # rocprofv3 --pmc FETCH_SIZE over the bench's own timed steps (scaled as above): a full batch of 32 units fetches
-# 152,527.41 KiB x 2.0 = 312,376,128 B for 301,989,888 B of units (2 KiB checkpoint segments), nothing written
+# 149,987.63 KiB x 2.0 = 307,174,656 B for 301,989,888 B of units (2 KiB checkpoint segments), nothing written
 # (profiles/verify_kernel_qwen3_host_pmc.md).
-# dense-prefix: a batch of 2 blobs (469,762,048 B) fetches 237,586.2 KiB x 2.0 = 486,576,553 B
+# dense-prefix: a batch of 2 blobs (469,762,048 B) fetches 232,268.63 KiB x 2.0 = 475,686,144 B
 # (profiles/verify_kernel_dense_prefix_host_pmc.md).
-HOST_VERIFY_TRAFFIC_RATIO: dict[int, float] = {9437184: 312376128 / 301989888, 234881024: 486576553 / 469762048}
+HOST_VERIFY_TRAFFIC_RATIO: dict[int, float] = {9437184: 307174656 / 301989888, 234881024: 475686144 / 469762048}
 HOST_TRAFFIC_SOURCE = {9437184: "profiles/verify_kernel_qwen3_host_pmc.md",
                        234881024: "profiles/verify_kernel_dense_prefix_host_pmc.md"}
+
+
+def dg_check_kernel(parts, seg, fused):
+    """The kernel the library launches for a device-gated check of this arena shape: the LDS-streamed one for 2 KiB
+    segments and 16-byte aligned parts of at least 16 bytes (the arena's parts are separate allocations), the chain
+    loop otherwise."""
+    lds = seg == 2048 and all(pb % 16 == 0 and pb >= 16 for pb in parts)
+    if fused:
+        return "dg_scatter_verify_lds_kernel" if lds else "dg_scatter_verify_kernel"
+    return "dg_verify_lds_kernel" if lds else "dg_verify_kernel"
 
 
 def log(*a):
@@ -333,7 +344,8 @@ def measure_kernels(tsa, L, C, w, seg=None, reps=10, beside="none"):
             if busy:
                 busy()
         bad = int(fail.download(4, dtype=np.uint32)[0])
-        out["verify"] = {"kernel": "dg_verify_kernel", "unit_bytes": ub, "seg_bytes": seg, "segments": n_ck,
+        out["verify"] = {"kernel": dg_check_kernel(parts, seg, False), "unit_bytes": ub, "seg_bytes": seg,
+                         "segments": n_ck,
                          "us": round(t * 1e6, 1), "GBps": round(ub / t / 1e9, 1),
                          "frac_of_hbm_peak": round(ub / t / 1e9 / HBM_PEAK_GBPS, 4), "fail_word": bad,
                          "beside": beside}
@@ -346,7 +358,8 @@ def measure_kernels(tsa, L, C, w, seg=None, reps=10, beside="none"):
             t2 = timed(lambda: tsa.check(L.tsa_xxh64_scatter_verify_slots(C.byref(av), keys, slots, 1,
                                                                           C.c_void_p(staged.ptr),
                                                                           C.c_void_p(fail.ptr), s)))
-            out["scatter_verify"] = {"kernel": "dg_scatter_verify_kernel", "unit_bytes": ub, "bytes_moved": 2 * ub,
+            out["scatter_verify"] = {"kernel": dg_check_kernel(parts, seg, True), "unit_bytes": ub,
+                                     "bytes_moved": 2 * ub,
                                      "us": round(t2 * 1e6, 1), "GBps": round(2 * ub / t2 / 1e9, 1),
                                      "frac_of_hbm_peak": round(2 * ub / t2 / 1e9 / HBM_PEAK_GBPS, 4),
                                      "fail_word": int(fail.download(4, dtype=np.uint32)[0])}
@@ -674,8 +687,9 @@ def main():
                     "frac_of_pinned_peak": round(copy_gbps / peaks["h2d_pinned_GBps"], 3) if copy_gbps else None,
                     "frac_of_pcie_gen5_x16": round(copy_gbps / 64.0, 3) if copy_gbps else None},
             "roofline": {"bound": "hbm",
-                         "kernel": "dg_scatter_verify_kernel (each staged unit into its slot, XXH64-checked on the way)"
-                         if fused else "dg_verify_kernel (device XXH64 of every landed unit)",
+                         "kernel": dg_check_kernel(w.parts, verify_seg_bytes(w.unit_bytes), fused)
+                         + (" (each staged unit into its slot, XXH64-checked on the way)" if fused
+                            else " (device XXH64 of every landed unit)"),
                          "achieved": round(ver_gbps, 1) if ver_gbps else None, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(ver_gbps / HBM_PEAK_GBPS, 4) if ver_gbps else None,
                          "traffic": int(traffic_unit * prof["verify_units"] / max(prof["verifies"], 1))
@@ -685,7 +699,8 @@ def main():
                          "bytes_per_launch": ver_bytes // max(prof["verifies"], 1),
                          "mean_launch_us": round(prof["verify_ns"] / max(prof["verifies"], 1) / 1e3, 2),
                          "note": "live: each launch checks the units a layer's copies landed, before the layer's ready word "
-                                 "(the engine's compute of the layer waits for it); standalone figure under "
+                                 "(a one-wave dg_publish_kernel behind it writes the slot entries and the ready word; "
+                                 "the engine's compute of the layer waits for it); standalone figure under "
                                  "kernels.verify"},
             "kernels": kern,
             "pcie": {k: round(peaks[k], 2) for k in ("h2d_pinned_GBps", "d2h_pinned_GBps", "bidir_h2d_GBps",
