@@ -495,10 +495,10 @@ __global__ TSA_VERIFY_BOUNDS void dg_scatter_verify_kernel(const DgVerifyLaunch 
   dg_verify_body<true>(a, src);
 }
 
-template <bool kCopy, int kWaves>
+template <bool kCopy>
 __device__ __forceinline__ void dg_verify_lds_body(const DgVerifyLaunch& a, const unsigned char* src) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kWaves * kLdsWaveBytes];
-  const uint32_t wave = kWaves == 1 ? 0u : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  __shared__ __attribute__((aligned(16))) unsigned char lds[4 * kLdsWaveBytes];
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   unsigned char* mine = lds + wave * kLdsWaveBytes;
   const uint32_t mine_off = uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)(mine)));
   const uint64_t gid = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -509,16 +509,9 @@ __device__ __forceinline__ void dg_verify_lds_body(const DgVerifyLaunch& a, cons
   const uint64_t v = lds_chain_t<kCopy>(g.v, from, g.to, g.live ? g.stripes : 0u, mine, mine_off);
   dg_finish(a, g, v, q);
 }
-// Workgroups of kWaves waves: four for large launches; one for a launch of few segments (a 24.8 MB unit is 756 waves),
-// which then spreads over every CU instead of leaving a quarter of them idle.
-template <int kWaves>
-__global__ __launch_bounds__(64 * kWaves) void dg_verify_lds_kernel(const DgVerifyLaunch a) {
-  dg_verify_lds_body<false, kWaves>(a, nullptr);
-}
-template <int kWaves>
-__global__ __launch_bounds__(64 * kWaves) void dg_scatter_verify_lds_kernel(const DgVerifyLaunch a,
-                                                                            const unsigned char* src) {
-  dg_verify_lds_body<true, kWaves>(a, src);
+__global__ __launch_bounds__(256) void dg_verify_lds_kernel(const DgVerifyLaunch a) { dg_verify_lds_body<false>(a, nullptr); }
+__global__ __launch_bounds__(256) void dg_scatter_verify_lds_kernel(const DgVerifyLaunch a, const unsigned char* src) {
+  dg_verify_lds_body<true>(a, src);
 }
 
 }  // namespace dev
@@ -551,32 +544,13 @@ static int launch_publish(const DgVerifyLaunch& a, hipStream_t stream) {
   return int(hipGetLastError());
 }
 
-// Waves per workgroup of an LDS-streamed check: 4, unless that leaves fewer than two workgroups per CU of the chip
-// (256 CUs on MI355X; the count is read once per process).
-static int lds_waves(uint64_t waves) {
-  static const uint64_t cus = [] {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      return uint64_t(256);
-    return uint64_t(n);
-  }();
-  return waves >= 4 * 2 * cus ? 4 : 1;
-}
-
 int launch_dg_verify(const DgVerifyLaunch& a, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   if (a.n == 0 || a.unit_segs == 0) return 0;
   if (a.n > kDgVerifyMax || a.n_parts == 0 || a.n_parts > 4) return int(hipErrorInvalidValue);
-  const uint64_t quads = uint64_t(a.n) * a.unit_segs;
-  uint32_t threads = 256;
-  void (*k)(DgVerifyLaunch) = dev::dg_verify_kernel;
-  if (dg_lds_shape(a)) {
-    const int w = lds_waves((quads + 15) / 16);
-    threads = 64u * uint32_t(w);
-    k = w == 4 ? dev::dg_verify_lds_kernel<4> : dev::dg_verify_lds_kernel<1>;
-  }
-  const uint64_t blocks = (quads * 4 + threads - 1) / threads;
+  const uint32_t threads = 256;
+  const uint64_t blocks = (uint64_t(a.n) * a.unit_segs * 4 + threads - 1) / threads;
   if (blocks > 0x7fffffffull) return int(hipErrorInvalidValue);
+  auto* k = dg_lds_shape(a) ? dev::dg_verify_lds_kernel : dev::dg_verify_kernel;
   if (start && stop)  // the events take the dispatch's own begin and end timestamps
     hipExtLaunchKernelGGL(k, dim3(uint32_t(blocks)), dim3(threads), 0, stream, start, stop, 0, a);
   else
@@ -597,17 +571,11 @@ int launch_dg_scatter_verify(const DgVerifyLaunch& a, const void* src, hipStream
                              hipEvent_t stop) {
   if (a.n == 0 || a.unit_segs == 0) return 0;
   if (a.n > kDgVerifyMax || a.n_parts == 0 || a.n_parts > 4 || !src) return int(hipErrorInvalidValue);
-  const uint64_t quads = uint64_t(a.n) * a.unit_segs;
-  uint32_t threads = 256;
-  void (*k)(DgVerifyLaunch, const unsigned char*) = dev::dg_scatter_verify_kernel;
-  if (dg_scatter_lds_shape(a, src)) {
-    const int w = lds_waves((quads + 15) / 16);
-    threads = 64u * uint32_t(w);
-    k = w == 4 ? dev::dg_scatter_verify_lds_kernel<4> : dev::dg_scatter_verify_lds_kernel<1>;
-  }
-  const uint64_t blocks = (quads * 4 + threads - 1) / threads;
+  const uint32_t threads = 256;
+  const uint64_t blocks = (uint64_t(a.n) * a.unit_segs * 4 + threads - 1) / threads;
   if (blocks > 0x7fffffffull) return int(hipErrorInvalidValue);
   const unsigned char* s = static_cast<const unsigned char*>(src);
+  auto* k = dg_scatter_lds_shape(a, src) ? dev::dg_scatter_verify_lds_kernel : dev::dg_scatter_verify_kernel;
   if (start && stop)
     hipExtLaunchKernelGGL(k, dim3(uint32_t(blocks)), dim3(threads), 0, stream, start, stop, 0, a, s);
   else
